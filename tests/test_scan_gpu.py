@@ -1,0 +1,250 @@
+"""Parity of the HIP scan kernels with the CPU oracle (GPU tests).
+
+Mirrors the reference's scan tests (tests/test_scan_chunk.py:55-138, 236-301,
+484-548): every retention form against the sequential oracle, ragged tiles,
+multi-segment decomposition, exact causality by perturbation, gradients
+(q, k, v and the retention) against float64 autograd through the oracle, and
+the multi-view / key-mass variants.  Tolerances: rel 1e-3 for fp32 and rel
+2e-2 for bf16 (max-abs error / max-abs oracle).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import scans as oracle
+from tests.conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-3, torch.bfloat16: 2e-2}
+
+
+def _streams(B, H, T, Dk, Dv, seed=20260725, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, T, Dk, generator=g, dtype=dtype)
+    k = torch.randn(B, H, T, Dk, generator=g, dtype=dtype)
+    v = torch.randn(B, H, T, Dv, generator=g, dtype=dtype)
+    return q, k, v
+
+
+def _rounded(x, dtype):
+    """Round to the kernel dtype and back, so the oracle sees the same inputs."""
+    return x.to(dtype).to(torch.float64)
+
+
+def _retention(kind, B, H, T, seed=11):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "none":
+        return None
+    if kind == "static":
+        return torch.log(torch.rand(H, generator=g, dtype=torch.float64) * 0.099 + 0.9)
+    return -torch.rand(B, H, T, 1, generator=g, dtype=torch.float64) * 0.2
+
+
+def _oracle_decay(ret, like):
+    if ret is None:
+        return None
+    return oracle.as_stream(ret, like) if ret.ndim == 1 else ret
+
+
+SHAPES = [
+    (2, 3, 37, 5, 4),      # the reference's _streams fixture shape
+    (1, 2, 64, 64, 64),    # exactly one tile
+    (2, 2, 300, 64, 64),   # ragged, several tiles
+    (1, 2, 260, 128, 64),  # wide keys
+    (1, 1, 130, 64, 128),  # wide values
+    (1, 1, 1, 8, 8),       # a single token
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_forward_matches_naive(cuda, dtype, kind, shape):
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dk, Dv = shape
+    q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, Dk, Dv))
+    ret = _retention(kind, B, H, T)
+    expected = oracle.linattn_naive(q, k, v, _oracle_decay(ret, q))
+    r_dev = None if ret is None else ret.to(cuda, torch.float32)
+    actual = scan_hip.linattn_views(q.to(cuda, dtype), k.to(cuda, dtype), v.to(cuda, dtype), (r_dev,), 64)[0]
+    assert actual.dtype == dtype and actual.shape == expected.shape
+    assert rel_err(actual, expected) < TOL[dtype], (shape, kind, dtype)
+
+
+@pytest.mark.parametrize("seg_chunks", [1, 2, 3, 7])
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+def test_segmented_decomposition_is_exact(cuda, seg_chunks, kind):
+    """Any segmentation of the tile axis gives the same scan (fp32)."""
+    from thetascan_amd._core.ops import scan_hip
+    from thetascan_amd import _lib
+
+    B, H, T, Dk, Dv = 2, 2, 450, 64, 64
+    q, k, v = _streams(B, H, T, Dk, Dv, dtype=torch.float32)
+    ret = _retention(kind, B, H, T)
+    expected = oracle.linattn_naive(q.double(), k.double(), v.double(), _oracle_decay(ret, q.double()))
+    kw = {"retention": {"none": _lib.RET_NONE, "static": _lib.RET_STATIC, "stream": _lib.RET_STREAM}[kind]}
+    if kind == "static":
+        kw["log_alpha"] = ret.to(cuda, torch.float32)
+    if kind == "stream":
+        kw["decay"] = ret.to(cuda, torch.float32)
+    out, _, _ = scan_hip.scan_launch(q.to(cuda), k.to(cuda), v.to(cuda), seg_chunks=seg_chunks, **kw)
+    assert rel_err(out, expected) < 1e-4
+
+
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+def test_reverse_scan_is_the_time_reversed_scan(cuda, kind):
+    """The anti-causal mode used by the backward equals flipping time."""
+    from thetascan_amd._core.ops import scan_hip
+    from thetascan_amd import _lib
+
+    B, H, T, D = 1, 2, 200, 32
+    q, k, v = _streams(B, H, T, D, D, dtype=torch.float32)
+    ret = _retention(kind, B, H, T)
+    # out_i = sum_{t>=i} w(t,i) <q_i, k_t> v_t  with w(t,i) = prod_{i<j<=t} a_j
+    decay = _oracle_decay(ret, q.double())
+    if decay is None:
+        rdecay = None
+    else:
+        # reversed logical position s uses the decay of physical T - s (0 at s = 0)
+        flipped = decay.flip(2)
+        rdecay = torch.cat([torch.zeros_like(flipped[:, :, :1]), flipped[:, :, :-1]], dim=2)
+    expected = oracle.linattn_naive(q.double().flip(2), k.double().flip(2), v.double().flip(2), rdecay).flip(2)
+    kw = {"retention": {"none": _lib.RET_NONE, "static": _lib.RET_STATIC, "stream": _lib.RET_STREAM}[kind]}
+    if kind == "static":
+        kw["log_alpha"] = ret.to(cuda, torch.float32)
+    if kind == "stream":
+        kw["decay"] = ret.to(cuda, torch.float32)
+    out, _, _ = scan_hip.scan_launch(q.to(cuda), k.to(cuda), v.to(cuda), reverse=True, seg_chunks=1, **kw)
+    assert rel_err(out, expected) < 1e-4
+
+
+def test_exact_causality_by_perturbation(cuda):
+    """Adding to k, v at t >= cut leaves every output before cut bitwise unchanged
+    (tests/test_scan_chunk.py:236-268)."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, D = 2, 2, 333, 64
+    q, k, v = (x.to(cuda, torch.bfloat16) for x in _streams(B, H, T, D, D, dtype=torch.float32))
+    la = torch.log(torch.tensor([0.9, 0.99], device=cuda))
+    for cut in (1, 63, 64, 65, 200):
+        k2, v2 = k.clone(), v.clone()
+        k2[:, :, cut:] += 2.0
+        v2[:, :, cut:] += 2.0
+        for ret in (None, la):
+            a = scan_hip.linattn_views(q, k, v, (ret,), 64)[0]
+            b = scan_hip.linattn_views(q, k2, v2, (ret,), 64)[0]
+            assert torch.equal(a[:, :, :cut], b[:, :, :cut]), cut
+
+
+def test_deterministic_replay(cuda):
+    from thetascan_amd._core.ops import scan_hip
+
+    q, k, v = (x.to(cuda, torch.bfloat16) for x in _streams(2, 4, 1000, 64, 64, dtype=torch.float32))
+    a = scan_hip.linattn_views(q, k, v, (None,), 64)[0]
+    b = scan_hip.linattn_views(q, k, v, (None,), 64)[0]
+    assert torch.equal(a, b)
+
+
+def test_multi_view_matches_separate_views(cuda):
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, D = 2, 3, 150, 32
+    q, k, v = (_rounded(x, torch.float32) for x in _streams(B, H, T, D, D))
+    la = torch.log(torch.tensor([0.9, 0.5, 0.99], dtype=torch.float64))
+    stream = _retention("stream", B, H, T)
+    rets = (None, la, stream)
+    outs = scan_hip.linattn_views(q.to(cuda, torch.float32), k.to(cuda, torch.float32),
+                                  v.to(cuda, torch.float32), tuple(None if r is None else r.to(cuda, torch.float32) for r in rets))
+    for out, ret in zip(outs, rets):
+        assert rel_err(out, oracle.linattn_naive(q, k, v, _oracle_decay(ret, q))) < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mass_column_matches_unit_value_column(cuda, dtype):
+    """linattn_views_mass == scan against cat([v, 1]) (engine.py:430-442)."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dk, Dv = 2, 2, 200, 64, 64
+    q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, Dk, Dv))
+    q, k = q.abs(), k.abs()
+    la = torch.log(torch.tensor([0.9, 0.99], dtype=torch.float64))
+    unit = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1)
+    for ret in (None, la):
+        expected = oracle.linattn_naive(q, k, unit, _oracle_decay(ret, q))
+        r_dev = None if ret is None else ret.to(cuda, torch.float32)
+        (num, mass), = scan_hip.linattn_views_mass(q.to(cuda, dtype), k.to(cuda, dtype), v.to(cuda, dtype), (r_dev,))
+        assert rel_err(num, expected[..., :-1]) < TOL[dtype]
+        assert rel_err(mass, expected[..., -1]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+def test_final_state_matches_recurrence(cuda, kind):
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dk, Dv = 2, 2, 299, 64, 64
+    q, k, v = _streams(B, H, T, Dk, Dv, dtype=torch.float32)
+    ret = _retention(kind, B, H, T)
+    expected = oracle.final_state_naive(k.double(), v.double(), _oracle_decay(ret, q.double()))
+    r_dev = None if ret is None else ret.to(cuda, torch.float32)
+    state = scan_hip.final_state(q.to(cuda), k.to(cuda), v.to(cuda), r_dev, with_mass=True)
+    assert rel_err(state[..., :Dv], expected) < 1e-4
+    mass = oracle.final_state_naive(k.double(), torch.ones_like(v[..., :1]).double(), _oracle_decay(ret, q.double()))
+    assert rel_err(state[..., Dv:], mass) < 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+@pytest.mark.parametrize("with_mass", [False, True])
+def test_gradients_match_float64_autograd(cuda, dtype, kind, with_mass):
+    """q, k, v and retention gradients (tests/test_scan_chunk.py:271-301)."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dk, Dv = 2, 2, 150, 32, 32
+    q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, Dk, Dv))
+    ret = _retention(kind, B, H, T)
+    g = torch.Generator().manual_seed(5)
+    dO = _rounded(torch.randn(B, H, T, Dv, generator=g, dtype=torch.float64), dtype)
+    dm = torch.randn(B, H, T, generator=g, dtype=torch.float64) * 0.1
+
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    r_ref = None if ret is None else ret.clone().requires_grad_(True)
+    if with_mass:
+        unit = torch.cat([leaves[2], torch.ones_like(v[..., :1])], dim=-1)
+        full = oracle.linattn_quad(leaves[0], leaves[1], unit, _oracle_decay(r_ref, q))
+        loss = (full[..., :-1] * dO).sum() + (full[..., -1] * dm).sum()
+    else:
+        full = oracle.linattn_quad(leaves[0], leaves[1], leaves[2], _oracle_decay(r_ref, q))
+        loss = (full * dO).sum()
+    loss.backward()
+
+    dev = [t.to(cuda, dtype).requires_grad_(True) for t in (q, k, v)]
+    r_dev = None if ret is None else ret.to(cuda, torch.float32).requires_grad_(True)
+    if with_mass:
+        (num, mass), = scan_hip.linattn_views_mass(*dev, (r_dev,))
+        loss_dev = (num.float() * dO.to(cuda, torch.float32)).sum() + (mass * dm.to(cuda, torch.float32)).sum()
+    else:
+        out = scan_hip.linattn_views(*dev, (r_dev,))[0]
+        loss_dev = (out.float() * dO.to(cuda, torch.float32)).sum()
+    loss_dev.backward()
+    tol = TOL[dtype] * (2 if dtype == torch.bfloat16 else 1)
+    for a, e, name in zip(dev, leaves, "qkv"):
+        assert rel_err(a.grad, e.grad) < tol, name
+    if ret is not None:
+        assert rel_err(r_dev.grad, r_ref.grad) < (5e-3 if dtype == torch.float32 else 5e-2), "retention"
+
+
+def test_errors_match_the_reference(cuda):
+    from thetascan_amd._core.ops import scan_hip
+
+    q, k, v = (x.to(cuda) for x in _streams(1, 2, 10, 8, 8, dtype=torch.float32))
+    with pytest.raises(ValueError, match="chunk must be >= 1"):
+        scan_hip.linattn(q, k, v, chunk=0)
+    with pytest.raises(NotImplementedError, match="scalar decay only"):
+        scan_hip.linattn(q, k, v, decay=torch.zeros(1, 2, 10, 8, device=cuda))
+    with pytest.raises(ValueError, match="one entry per head"):
+        scan_hip.linattn(q, k, v, log_alpha=torch.zeros(3, device=cuda))
+    with pytest.raises(RuntimeError, match="GPU"):
+        scan_hip.linattn(q.cpu(), k.cpu(), v.cpu())

@@ -1,0 +1,383 @@
+"""The ``hip`` scan backend: chunked linear-attention scans on MI355X.
+
+Same contract as the reference chunk backend
+(``src/thetascan/_core/ops/scan_chunk.py:246-358``):
+
+* :func:`linattn_views` ``(q, k, v, retentions, chunk) -> tuple`` scans one
+  stream set through several temporal views.  ``None`` is the plain causal
+  sum, a ``[H]`` tensor a static per-head log-retention, a ``[B,H,T,1]``
+  tensor a per-token log-retention stream.
+* :func:`linattn` is the one-view wrapper with the reference's ``decay`` /
+  ``log_alpha`` keywords.
+
+Inputs are ``[B,H,T,D]`` (any strides with a contiguous feature axis),
+outputs are new tensors in the query dtype.  Everything is differentiable in
+``q``, ``k``, ``v`` and the retention.  The arithmetic runs in the HIP kernels
+of ``libthetascan_hip.so``; there is no CPU path -- CPU tensors raise.
+
+Chunk semantics.  ``chunk`` is validated exactly like the reference
+(``ValueError`` below 1).  The scan is exact for any tiling, so the kernel
+always works in its own 64-token tiles; ``chunk`` therefore only changes the
+reference's rounding, never the mathematical result.  Retention phases are
+formed in fp32 per tile and the carried state is fp32, as the reference's
+precision policy requires (``scan_chunk.py:89-99, 301``).
+
+Backward.  The gradients of a causal scan are scans of the same form:
+
+* ``dq = scan(dO, v, k)`` (causal),
+* ``dk = scan(v, dO, q)`` and ``dv = scan(k, q, dO)`` (anti-causal),
+
+all with the forward retention.  The key-mass column of the normalized read
+(``engine.py:419-442``) rides along as ext columns (ones in ``v``, its
+gradient in ``dO``).  Retention gradients follow from
+``dL_t = q_t.dq_t - k_t.dk_t`` (gradient with respect to the cumulative log
+at t): ``dlog_alpha = sum_t t dL_t`` for a static head retention and the
+reverse cumulative sum of ``dL`` for a per-token stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ... import _lib
+
+DEFAULT_CHUNK = 512   # reference default (scan_chunk.DEFAULT_CHUNK); validated only
+TILE = 64             # the kernel's tile
+
+
+# ------------------------------------------------------------------ launching
+
+def _vec(dtype: torch.dtype) -> int:
+    return 8 if dtype == torch.bfloat16 else 4
+
+
+def _kernel_view(x: torch.Tensor, width: int | None = None) -> torch.Tensor:
+    """Return ``x`` as a kernel-legal [B,H,T,F] view (padding/copying if needed)."""
+    vec = _vec(x.dtype)
+    feat = x.shape[-1]
+    target = -(-feat // vec) * vec if width is None else width
+    ok = (
+        target == feat
+        and x.stride(-1) == 1
+        and all(s % vec == 0 for s in x.stride()[:3])
+        and x.data_ptr() % 16 == 0
+    )
+    if ok:
+        return x
+    out = x.new_zeros(*x.shape[:3], target)
+    out[..., :feat] = x
+    return out
+
+
+def _ext_arg(ext):
+    """(mode, tensor) for an ext column: None, 'ones' or an fp32 [B,H,T] tensor."""
+    if ext is None:
+        return _lib.EXT_NONE, None
+    if isinstance(ext, str):
+        assert ext == "ones"
+        return _lib.EXT_ONES, None
+    return _lib.EXT_ARRAY, ext.to(torch.float32)
+
+
+def scan_launch(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    retention: int = _lib.RET_NONE,
+    log_alpha: torch.Tensor | None = None,
+    decay: torch.Tensor | None = None,
+    reverse: bool = False,
+    q_ext=None,
+    k_ext=None,
+    v_ext=None,
+    out: torch.Tensor | None = None,
+    out_mode: int = _lib.OUT_STORE,
+    out_scale: float = 1.0,
+    want_ext_out: bool = False,
+    ext_out: torch.Tensor | None = None,
+    want_final: bool = False,
+    seg_chunks: int = 0,
+):
+    """One kernel scan.  Returns ``(out, ext_out, final_state)``.
+
+    ``out`` is ``[B,H,T,dv]``; ``ext_out`` (fp32 ``[B,H,T]``) is the result
+    column of the ``v`` ext column; ``final_state`` is the fp32
+    ``[B,H,dk(+1),dv(+1)]`` state after the last token (ext rows/columns
+    included when present).
+    """
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    lib = _lib.load()
+    dtype = q.dtype
+    code = _lib.dtype_code(dtype)
+    if k.dtype != dtype:
+        k = k.to(dtype)
+    if v.dtype != dtype:
+        v = v.to(dtype)
+    B, H, T, dk = q.shape
+    dv = v.shape[-1]
+    if k.shape[:3] != (B, H, T) or v.shape[:3] != (B, H, T) or k.shape[-1] != dk:
+        raise ValueError(f"hip scan: incompatible shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    vec = _vec(dtype)
+    dkw = -(-dk // vec) * vec
+    dvw = -(-dv // vec) * vec
+    qk = _kernel_view(q, dkw)
+    kk = _kernel_view(k, dkw)
+    vk = _kernel_view(v, dvw)
+    qe_mode, qe = _ext_arg(q_ext)
+    ke_mode, ke = _ext_arg(k_ext)
+    ve_mode, ve = _ext_arg(v_ext)
+
+    desc = _lib.ScanDesc(
+        B, H, T, dkw, dvw, code, retention, int(reverse), qe_mode, ke_mode, ve_mode,
+        out_mode, float(out_scale), int(seg_chunks), int(want_final),
+    )
+    c_dkp, c_dvp, c_nseg = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(lib.ts_scan_layout(ctypes.byref(desc), ctypes.byref(c_dkp), ctypes.byref(c_dvp),
+                                  ctypes.byref(c_nseg)), "scan layout")
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(ws_bytes)), "scan workspace")
+
+    out_dtype = dtype if out_mode == _lib.OUT_STORE else torch.float32
+    if out is None:
+        if out_mode == _lib.OUT_ACCUM_F32:
+            raise ValueError("accumulating scan needs an output tensor")
+        out_buf = torch.empty(B, H, T, dvw, dtype=out_dtype, device=q.device)
+    else:
+        if out.dtype != out_dtype or out.shape[-1] != dvw or out.stride(-1) != 1:
+            raise ValueError("hip scan: output buffer does not match the scan")
+        out_buf = out
+    if want_ext_out and ext_out is None:
+        if out_mode == _lib.OUT_ACCUM_F32:
+            raise ValueError("accumulating scan needs an ext output tensor")
+        ext_out = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
+    final = None
+    if want_final:
+        final = torch.empty(B * H, c_dkp.value, c_dvp.value, dtype=torch.float32, device=q.device)
+    workspace = None
+    if ws_bytes.value:
+        workspace = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
+
+    la = None
+    if retention == _lib.RET_STATIC:
+        la = log_alpha.detach().to(device=q.device, dtype=torch.float32).reshape(H).contiguous()
+    dec = None
+    if retention == _lib.RET_STREAM:
+        dec = decay.detach().to(dtype=torch.float32).reshape(B, H, T)
+
+    io = _lib.ScanIO(
+        _lib.strided(qk), _lib.strided(kk), _lib.strided(vk),
+        _lib.strided(qe), _lib.strided(ke), _lib.strided(ve),
+        la.data_ptr() if la is not None else None,
+        _lib.strided(dec),
+        _lib.strided(out_buf),
+        _lib.strided(ext_out if want_ext_out else None),
+        final.data_ptr() if final is not None else None,
+    )
+    status = lib.ts_scan_fwd(
+        ctypes.byref(desc), ctypes.byref(io),
+        workspace.data_ptr() if workspace is not None else None,
+        ws_bytes.value, _lib.stream_handle(q.device),
+    )
+    _lib.check(status, "ts_scan_fwd")
+    result = out_buf if out is not None else out_buf[..., :dv]
+    if final is not None:
+        final = final.view(B, H, c_dkp.value, c_dvp.value)
+    return result, ext_out, final
+
+
+# ------------------------------------------------------------------ retentions
+
+def _classify(retention, q: torch.Tensor):
+    """Validate one retention exactly like the reference (scan_chunk.py:277-291)."""
+    heads = q.shape[1]
+    if retention is None:
+        return _lib.RET_NONE
+    if retention.ndim == 4:
+        if retention.shape[-1] != 1:
+            raise NotImplementedError("chunk backend: scalar decay only (v1)")
+        return _lib.RET_STREAM
+    if retention.numel() != heads:
+        raise ValueError(
+            "chunk backend: a static retention needs one entry per head, "
+            f"got {tuple(retention.shape)} for q {tuple(q.shape)}"
+        )
+    return _lib.RET_STATIC
+
+
+def _ret_kwargs(kind: int, retention):
+    if kind == _lib.RET_STATIC:
+        return {"retention": kind, "log_alpha": retention}
+    if kind == _lib.RET_STREAM:
+        return {"retention": kind, "decay": retention}
+    return {"retention": kind}
+
+
+def _retention_grad(kind: int, retention: torch.Tensor, dL: torch.Tensor) -> torch.Tensor:
+    """Gradient of a retention from dL[B,H,T] = q.dq - k.dk (per view)."""
+    if kind == _lib.RET_STATIC:
+        t = torch.arange(dL.shape[2], device=dL.device, dtype=torch.float32)
+        grad = (dL * t).sum(dim=(0, 2))
+        return grad.to(retention.dtype).view_as(retention)
+    # d a_j = sum_{t>=j} dL_t for j >= 1; position 0 never multiplies a stored term.
+    grad = dL.flip(-1).cumsum(-1).flip(-1)
+    grad[..., 0] = 0.0
+    return grad.unsqueeze(-1).to(retention.dtype)
+
+
+# ------------------------------------------------------------------ autograd
+
+class _ScanViews(torch.autograd.Function):
+    """Forward: one kernel scan per retention.  Backward: three scans per view."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, with_mass, *retentions):
+        kinds = [_classify(r, q) for r in retentions]
+        outs, masses = [], []
+        for kind, r in zip(kinds, retentions):
+            out, mass, _ = scan_launch(
+                q, k, v, **_ret_kwargs(kind, r),
+                v_ext="ones" if with_mass else None, want_ext_out=with_mass,
+            )
+            outs.append(out)
+            if with_mass:
+                masses.append(mass)
+        ctx.kinds = kinds
+        ctx.with_mass = with_mass
+        ctx.n_views = len(retentions)
+        ctx.save_for_backward(q, k, v, *[r if r is not None else None for r in retentions])
+        return (*outs, *masses)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        q, k, v, *retentions = ctx.saved_tensors
+        n = ctx.n_views
+        d_outs = grads[:n]
+        d_mass = grads[n:] if ctx.with_mass else [None] * n
+        need_q, need_k, need_v = ctx.needs_input_grad[0:3]
+        need_r = ctx.needs_input_grad[4:]
+        B, H, T, dk = q.shape
+        dv = v.shape[-1]
+        dq = torch.zeros(B, H, T, -(-dk // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+        dkk = torch.zeros_like(dq)
+        dvv = torch.zeros(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+        r_grads = []
+        for j in range(n):
+            kind, r = ctx.kinds[j], retentions[j]
+            dO = d_outs[j]
+            dm = d_mass[j]
+            if dO is None and dm is None:
+                r_grads.append(None)
+                continue
+            if dO is None:
+                dO = torch.zeros(B, H, T, dv, dtype=q.dtype, device=q.device)
+            dO = dO.to(q.dtype)
+            rk = _ret_kwargs(kind, r)
+            mass_ext = dm is not None
+            q_ext = dm.to(torch.float32) if mass_ext else None
+            want_r = r is not None and need_r[j]
+            if want_r:
+                dq_j, _, _ = scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
+                                         out_mode=_lib.OUT_STORE_F32)
+                dk_j, _, _ = scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
+                                         k_ext=q_ext, out_mode=_lib.OUT_STORE_F32)
+                dL = (q.float() * dq_j[..., :dk]).sum(-1) - (k.float() * dk_j[..., :dk]).sum(-1)
+                r_grads.append(_retention_grad(kind, r, dL))
+                dq[..., : dq_j.shape[-1]] += dq_j
+                dkk[..., : dk_j.shape[-1]] += dk_j
+            else:
+                r_grads.append(None)
+                if need_q:
+                    scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
+                                out=dq, out_mode=_lib.OUT_ACCUM_F32)
+                if need_k:
+                    scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
+                                k_ext=q_ext, out=dkk, out_mode=_lib.OUT_ACCUM_F32)
+            if need_v and dO is not None:
+                scan_launch(k, q, dO, **rk, reverse=True, out=dvv, out_mode=_lib.OUT_ACCUM_F32)
+        gq = dq[..., :dk].to(q.dtype) if need_q else None
+        gk = dkk[..., :dk].to(k.dtype) if need_k else None
+        gv = dvv[..., :dv].to(v.dtype) if need_v else None
+        return (gq, gk, gv, None, *r_grads)
+
+
+def _run_views(q, k, v, retentions, chunk, with_mass):
+    if chunk < 1:
+        raise ValueError("chunk backend: chunk must be >= 1")
+    if not retentions:
+        return ()
+    for r in retentions:
+        _classify(r, q)
+    return _ScanViews.apply(q, k, v, with_mass, *retentions)
+
+
+def linattn_views(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    retentions: tuple,
+    chunk: int = DEFAULT_CHUNK,
+) -> tuple:
+    """Scan one stream set through several temporal views (scan_chunk.py:246-339)."""
+    return tuple(_run_views(q, k, v, tuple(retentions), chunk, False))
+
+
+def linattn_views_mass(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    retentions: tuple,
+    chunk: int = DEFAULT_CHUNK,
+) -> tuple:
+    """Like :func:`linattn_views` with an implicit unit value column.
+
+    Returns ``((num_0, mass_0), (num_1, mass_1), ...)`` where ``mass`` is the
+    fp32 ``[B,H,T]`` result of the unit column -- the same numbers the
+    reference obtains from ``cat([v, ones])`` (``engine.py:430``), without
+    materialising the augmented tensor.
+    """
+    res = _run_views(q, k, v, tuple(retentions), chunk, True)
+    n = len(retentions)
+    return tuple((res[j], res[n + j]) for j in range(n))
+
+
+def linattn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    decay: torch.Tensor | None = None,
+    chunk: int = DEFAULT_CHUNK,
+    log_alpha: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Inclusive causal scan (scan_chunk.py:342-358); ``log_alpha`` wins over ``decay``."""
+    retention = log_alpha if log_alpha is not None else decay
+    return linattn_views(q, k, v, (retention,), chunk)[0]
+
+
+def final_state(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    retention=None,
+    with_mass: bool = False,
+) -> torch.Tensor:
+    """fp32 state after the last token: ``N_T = sum_i w(T-1,i) k_i v_i^T``.
+
+    With ``with_mass`` the last column is the key mass ``D_T = sum_i w k_i``.
+    Shape ``[B,H,dk,dv(+1)]``.  Not differentiable (a streaming-decode cache).
+    """
+    kind = _classify(retention, q)
+    _, _, fin = scan_launch(
+        q.detach(), k.detach(), v.detach(), **_ret_kwargs(kind, retention),
+        v_ext="ones" if with_mass else None, want_final=True,
+    )
+    dk = k.shape[-1]
+    dv = v.shape[-1]
+    vec = _vec(q.dtype)
+    dvw = -(-dv // vec) * vec
+    state = fin[:, :, :dk, :dv]
+    if with_mass:
+        state = torch.cat([state, fin[:, :, :dk, dvw:dvw + 1]], dim=-1)
+    return state

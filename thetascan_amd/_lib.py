@@ -1,0 +1,169 @@
+"""ctypes binding of ``libthetascan_hip.so`` (C ABI in ``include/thetascan_hip.h``).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already mapped (both carry the ``libamdhip64.so.7`` soname).  Nothing here
+falls back to a CPU path: a missing library or a non-GPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+from ._build import LIB_PATH
+
+TS_OK = 0
+TS_ERR_VALUE = 1
+TS_ERR_NOT_IMPLEMENTED = 2
+TS_ERR_RUNTIME = 3
+
+TS_BF16 = 0
+TS_F32 = 1
+
+RET_NONE = 0
+RET_STATIC = 1
+RET_STREAM = 2
+
+EXT_NONE = 0
+EXT_ONES = 1
+EXT_ARRAY = 2
+
+OUT_STORE = 0
+OUT_STORE_F32 = 1
+OUT_ACCUM_F32 = 2
+
+
+class Strided(ctypes.Structure):
+    _fields_ = [
+        ("ptr", ctypes.c_void_p),
+        ("sb", ctypes.c_int64),
+        ("sh", ctypes.c_int64),
+        ("st", ctypes.c_int64),
+    ]
+
+
+class ScanDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("dk", ctypes.c_int32),
+        ("dv", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("retention", ctypes.c_int32),
+        ("reverse", ctypes.c_int32),
+        ("q_ext", ctypes.c_int32),
+        ("k_ext", ctypes.c_int32),
+        ("v_ext", ctypes.c_int32),
+        ("out_mode", ctypes.c_int32),
+        ("out_scale", ctypes.c_float),
+        ("seg_chunks", ctypes.c_int32),
+        ("want_final", ctypes.c_int32),
+    ]
+
+
+class ScanIO(ctypes.Structure):
+    _fields_ = [
+        ("q", Strided),
+        ("k", Strided),
+        ("v", Strided),
+        ("q_ext", Strided),
+        ("k_ext", Strided),
+        ("v_ext", Strided),
+        ("log_alpha", ctypes.c_void_p),
+        ("decay", Strided),
+        ("out", Strided),
+        ("out_ext", Strided),
+        ("final_state", ctypes.c_void_p),
+    ]
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+# Every symbol include/thetascan_hip.h declares.
+EXPORTS = (
+    "ts_abi_version",
+    "ts_last_error",
+    "ts_scan_layout",
+    "ts_scan_workspace_bytes",
+    "ts_scan_fwd",
+    "ts_feature_fwd",
+    "ts_feature_bwd",
+    "ts_read_fwd",
+    "ts_read_bwd",
+    "ts_wcumsum",
+)
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library (raises if it was never built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m thetascan_amd._build` "
+                "(or __graft_entry__.build()); the hip backend has no fallback"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_LOCAL)
+        lib.ts_abi_version.restype = ctypes.c_int
+        lib.ts_last_error.restype = ctypes.c_char_p
+        lib.ts_scan_layout.argtypes = [
+            ctypes.POINTER(ScanDesc),
+            ctypes.POINTER(ctypes.c_int32),
+            ctypes.POINTER(ctypes.c_int32),
+            ctypes.POINTER(ctypes.c_int32),
+        ]
+        lib.ts_scan_workspace_bytes.argtypes = [ctypes.POINTER(ScanDesc), ctypes.POINTER(ctypes.c_size_t)]
+        lib.ts_scan_fwd.argtypes = [
+            ctypes.POINTER(ScanDesc),
+            ctypes.POINTER(ScanIO),
+            ctypes.c_void_p,
+            ctypes.c_size_t,
+            ctypes.c_void_p,
+        ]
+        if lib.ts_abi_version() != 1:
+            raise RuntimeError("libthetascan_hip.so ABI version mismatch")
+        _lib = lib
+        return lib
+
+
+def check(status: int, what: str) -> None:
+    if status == TS_OK:
+        return
+    message = (load().ts_last_error() or b"").decode(errors="replace") or what
+    if status == TS_ERR_VALUE:
+        raise ValueError(message)
+    if status == TS_ERR_NOT_IMPLEMENTED:
+        raise NotImplementedError(message)
+    raise RuntimeError(message)
+
+
+def strided(t: torch.Tensor | None) -> Strided:
+    """Describe a [B,H,T,(F)] tensor (or None) for the C ABI."""
+    if t is None:
+        return Strided(None, 0, 0, 0)
+    s = t.stride()
+    return Strided(t.data_ptr(), s[0], s[1], s[2])
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return TS_BF16
+    if dtype == torch.float32:
+        return TS_F32
+    raise NotImplementedError(f"hip backend computes in bfloat16 or float32, got {dtype}")

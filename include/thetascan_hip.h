@@ -113,6 +113,122 @@ int ts_scan_workspace_bytes(const ts_scan_desc* desc, size_t* bytes);
 int ts_scan_fwd(const ts_scan_desc* desc, const ts_scan_io* io,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+
+/* ------------------------------------------------------------------ write */
+
+enum ts_feature_kind { TS_FEAT_RELU2 = 0, TS_FEAT_SOFTMAX = 1 };
+
+typedef struct ts_feature_desc {
+  int32_t B, H, T;
+  int32_t d;            /* head width (16..128, multiple of 16)                */
+  int32_t m;            /* feature width (16..256, multiple of 16)             */
+  int32_t dtype;        /* ts_dtype of x, weights and bf16/fp32 outputs        */
+  int32_t kind;         /* ts_feature_kind                                      */
+  int32_t in_rot;       /* input-RoPE rotated channels of x (0 = none)         */
+  int32_t feat_rot;     /* feature-RoPE rotated channels of phi (0 = none)     */
+  int32_t has_tau;      /* relu2: subtract the per-head threshold tau[H]       */
+  float gain;           /* softmax: logit gain                                 */
+  float resid_scale;    /* s = 1/sqrt(depth) of the residual read              */
+  float eps;            /* 1e-6 in the reference                               */
+} ts_feature_desc;
+
+typedef struct ts_feature_io {
+  ts_strided x;                    /* [B,H,T,d] raw keys or queries            */
+  const void* w1;                  /* [H,m,d] effective W1                     */
+  const void* w2;                  /* [H,d,m] effective W2 (resid only)        */
+  const float* tau;                /* [H]                                      */
+  const float* in_cos;             /* [T, in_rot/2]                            */
+  const float* in_sin;
+  const float* f_cos;              /* [T, feat_rot/2]                          */
+  const float* f_sin;
+  ts_strided phi;                  /* out [B,H,T,m]: rotated features          */
+  ts_strided resid;                /* out [B,H,T,d]: xn + s*W2 h  (or NULL)    */
+} ts_feature_io;
+
+/* Fused write-side feature map for one stream (keys, or queries):
+ *   xn  = l2norm(rope_in(x));  a = W1 xn;  pre = rmsnorm(a) - tau
+ *   h   = relu2_ridge(pre) | softmax(gain * pre);  phi = rope_feat(h)
+ *   resid = xn + s * W2 h   (queries only)
+ * Replaces block.py:595-618 (input RoPE, L2 norm, feature-RoPE table),
+ * engine.py:117-158 (_block_forward), kernel_features.py:73-135 (feature
+ * maps), engine.py:74-86 (_hrot_stream) and the base term of
+ * engine.py:522-528. */
+int ts_feature_fwd(const ts_feature_desc* desc, const ts_feature_io* io, hipStream_t stream);
+
+typedef struct ts_feature_bwd_io {
+  ts_strided x;                    /* [B,H,T,d] forward input                  */
+  const void* w1;                  /* [H,m,d]                                  */
+  const void* w1t;                 /* [H,d,m] (W1 transposed)                  */
+  const void* w2t;                 /* [H,m,d] (W2 transposed; resid only)      */
+  const float* tau;
+  const float* in_cos;
+  const float* in_sin;
+  const float* f_cos;
+  const float* f_sin;
+  ts_strided dphi;                 /* fp32 [B,H,T,m]: grad of phi              */
+  ts_strided dresid;               /* fp32 [B,H,T,d]: grad of resid (or NULL)  */
+  ts_strided dx;                   /* out [B,H,T,d]: grad of x                 */
+  ts_strided da;                   /* out [B,H,T,m]: grad of a = W1 xn (NULL ok) */
+  ts_strided xn;                   /* out [B,H,T,d]: xn (NULL ok)              */
+  ts_strided h;                    /* out [B,H,T,m]: unrotated h (NULL ok)     */
+  ts_strided dtau;                 /* out fp32 [B,H,T]: -sum_j dpre_j (NULL ok) */
+} ts_feature_bwd_io;
+
+/* Backward of ts_feature_fwd (recomputes the forward tile in registers/LDS).
+ * Weight gradients are then plain GEMMs of the returned da/xn/h tiles. */
+int ts_feature_bwd(const ts_feature_desc* desc, const ts_feature_bwd_io* io, hipStream_t stream);
+
+/* ------------------------------------------------------------------- read */
+
+typedef struct ts_read_desc {
+  int32_t B, H, T, d;
+  int32_t dtype;        /* of num, resid, gate and y                           */
+  int32_t normalize;    /* 1: mem = num / (mass + eps)                         */
+  int32_t gate;         /* 1: y *= silu(g)                                     */
+  float scale;          /* s = 1/sqrt(depth)                                   */
+  float eps;
+} ts_read_desc;
+
+typedef struct ts_read_io {
+  ts_strided num;                  /* [B,H,T,d] scan numerator                 */
+  ts_strided mass;                 /* fp32 [B,H,T] key mass (normalize)        */
+  ts_strided resid;                /* [B,H,T,d] xn + s*W2 h                    */
+  ts_strided g;                    /* gate pre-activation, [B,H,T,d] view      */
+  ts_strided y;                    /* out [B,H,T,d] view (e.g. of [B,T,H*d])   */
+} ts_read_io;
+
+/* Normalized read epilogue:  y = (resid + s * num / (mass + eps)) * silu(g).
+ * Replaces engine.py:440-442, 526-528 and the output gate of
+ * block.py:721-722 (gates.py:34-40). */
+int ts_read_fwd(const ts_read_desc* desc, const ts_read_io* io, hipStream_t stream);
+
+typedef struct ts_read_bwd_io {
+  ts_strided num, mass, resid, g;  /* forward inputs                           */
+  ts_strided dy;                   /* grad of y                                */
+  ts_strided dnum;                 /* out [B,H,T,d] (desc dtype)               */
+  ts_strided dmass;                /* out fp32 [B,H,T] (normalize)             */
+  ts_strided dresid;               /* out fp32 [B,H,T,d]                       */
+  ts_strided dg;                   /* out [B,H,T,d] (gate)                     */
+} ts_read_bwd_io;
+
+int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t stream);
+
+/* --------------------------------------------------------------- prefixes */
+
+/* Decayed prefix sum along T of an fp32 [B,H,T,F] stream:
+ *   z_t = a_t z_{t-1} + x_t   (a = exp(log_alpha[h]) static, or exp(decay[b,h,t]),
+ *   or 1 for the plain prefix), optionally anti-causal (reverse).
+ * Replaces interface.ema_cumsum / causal_prefix_sum / Accumulator.mass_cum
+ * (src/thetascan/_core/ops/interface.py:58-107, 216-230). */
+typedef struct ts_wcumsum_desc {
+  int32_t B, H, T, F;
+  int32_t retention;    /* ts_retention                                        */
+  int32_t reverse;
+} ts_wcumsum_desc;
+
+int ts_wcumsum(const ts_wcumsum_desc* desc, ts_strided x, ts_strided out, const float* log_alpha,
+               ts_strided decay, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,158 @@
+"""Mixer parity on the GPU (hip backend) against the reference.
+
+* Every golden case (written from the reference, float64) is loaded into the
+  MI355X module by state dict and run in fp32 on the GPU: outputs and every
+  parameter gradient must match the reference within rel 1e-3 (fp32 bar).
+* The fused three-kernel path and the composed path agree with each other.
+* bf16 runs at benchmark-like widths match the float64 CPU oracle within rel
+  2e-2 (the bf16 bar), forward and backward.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mixer as oracle_mixer
+from tests.conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+CASES = json.loads((GOLDEN / "mixer_cases.json").read_text())
+
+
+def build_module(pub: dict, device, dtype=torch.float32):
+    import thetascan_amd as ts
+
+    pub = json.loads(json.dumps(pub))
+    pub["runtime"]["backend"] = "hip"
+    return ts.ThetaScan(ts.ThetaScanConfig.from_dict(pub)).to(device=device, dtype=dtype)
+
+
+def load_golden(name):
+    data = np.load(GOLDEN / f"mixer_{name}.npz", allow_pickle=False)
+    state = {k[len("param:"):]: torch.from_numpy(data[k]) for k in data.files if k.startswith("param:")}
+    for k in data.files:
+        if k.startswith("buffer:"):
+            state[k[len("buffer:"):]] = torch.from_numpy(data[k])
+    grads = {k[len("grad:"):]: torch.from_numpy(data[k]) for k in data.files
+             if k.startswith("grad:") and k != "grad:x"}
+    return state, grads, {k: torch.from_numpy(data[k]) for k in ("x", "dy", "y", "grad:x")}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_mixer_matches_reference_golden(cuda, name):
+    state, grads, arr = load_golden(name)
+    module = build_module(CASES[name]["config"], cuda)
+    module.load_state_dict({k: v.to(torch.float32) if v.is_floating_point() else v for k, v in state.items()},
+                           strict=True)
+    x = arr["x"].to(cuda, torch.float32).requires_grad_(True)
+    y = module(x)
+    print(f"{name}: path={module._core.last_path}", flush=True)
+    assert rel_err(y, arr["y"]) < 1e-3, name
+    (y * arr["dy"].to(cuda, torch.float32)).sum().backward()
+    assert rel_err(x.grad, arr["grad:x"]) < 2e-3, name
+    params = dict(module.named_parameters())
+    for pname, g in grads.items():
+        assert params[pname].grad is not None, (name, pname)
+        assert rel_err(params[pname].grad, g) < 5e-3, (name, pname)
+
+
+def _headline_config(placement: str, normalization: str, feature_map="relu2_ridge", d_model=512, heads=8,
+                     mult=1):
+    return {
+        "d_model": d_model, "n_heads": heads, "head_dim": None, "memory_multiplier": mult,
+        "feature_expansion": 1, "expansion_key": "thetascan", "depth": 1, "share_key_query": False,
+        "key_value_heads": None, "output_gate": True, "family": "kernel",
+        "gn": {"nonlinearity": "relu2", "jacobian_steps": 1, "read_normalization": "none"},
+        "kernel": {"feature_map": feature_map, "value_representation": "raw", "value_anchors": 8,
+                   "value_mlp_multiplier": 1.0, "kernel_sharpness": 8.0, "kernel_sharpness_mode": "fixed",
+                   "score_bias": False, "relu2_threshold_mode": "none", "sparsity": "none",
+                   "sparse_blend_init": 0.0, "relative_threshold_init": 0.01, "threshold_temperature": 0.25,
+                   "bspline_basis_count": 8, "bspline_degree": 3, "bspline_bound": 3.0, "bspline_scale": 1.0,
+                   "bspline_scale_mode": "fixed", "feature_parameters_trainable": True,
+                   "read_normalization": normalization},
+        "rope": {"mode": "partial", "fraction": 0.5, "base": 10000.0, "placement": placement},
+        "temporal": {"mode": "sum", "bank_mode": "fast", "retention_init": 0.9, "recency_branches": 1,
+                     "retention_inits": None, "half_life_inits": None, "blend_mode": "free"},
+        "regularization": {"feature_weight": 0.0, "head_weight": 0.0, "value_mlp_weight": 0.0},
+        "runtime": {"backend": "hip", "scan_chunk": 64},
+    }
+
+
+def _seeded(module, seed=0, w2_std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in sorted(module.named_parameters()):
+            if name.endswith("W2.0"):
+                p.copy_(torch.randn(p.shape, generator=g) * w2_std)
+            elif name.endswith("ogate.g.lin.weight"):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+
+
+@pytest.mark.parametrize("variant", [("feature", "none"), ("input", "key_mass"), ("input", "none")])
+@pytest.mark.parametrize("feature_map", ["relu2_ridge", "softmax_partition"])
+def test_fused_and_composed_paths_agree(cuda, variant, feature_map):
+    placement, normalization = variant
+    pub = _headline_config(placement, normalization, feature_map, d_model=256, heads=4)
+    module = build_module(pub, cuda)
+    _seeded(module, 1)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 200, 256, generator=g).to(cuda)
+    dy = torch.randn(2, 200, 256, generator=g).to(cuda)
+    outs, grads = [], []
+    for force_composed in (False, True):
+        module.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        if force_composed:
+            module._core.fused_eligible = lambda _x: False
+        y = module(xi)
+        assert module._core.last_path == ("composed" if force_composed else "fused")
+        (y * dy).sum().backward()
+        outs.append(y.detach())
+        grads.append([xi.grad] + [p.grad.clone() for p in module.parameters()])
+    assert rel_err(outs[0], outs[1]) < 1e-4
+    for a, b in zip(grads[0], grads[1]):
+        assert rel_err(a, b) < 1e-3
+
+
+@pytest.mark.parametrize("variant", [("feature", "none"), ("input", "key_mass")])
+def test_headline_bf16_matches_float64_oracle(cuda, variant):
+    """The benchmark mixer (kernel, ReLU^2 ridge, m=d=64, H=8, d_model=512) in
+    bf16 on the GPU against the float64 oracle, at T=256 (rel 2e-2)."""
+    placement, normalization = variant
+    pub = _headline_config(placement, normalization)
+    module = build_module(pub, cuda, torch.float32)
+    _seeded(module, 3)
+    core = oracle_mixer.core_config(pub)
+    params64 = {k: v.detach().double().cpu().clone().requires_grad_(True) for k, v in module._core.named_parameters()}
+    g = torch.Generator().manual_seed(4)
+    B, T = 2, 256
+    x = torch.randn(B, T, 512, generator=g, dtype=torch.float64)
+    dy = torch.randn(B, T, 512, generator=g, dtype=torch.float64) * 0.1
+    x64 = x.clone().requires_grad_(True)
+    y64 = oracle_mixer.forward(core, params64, x64)
+    (y64 * dy).sum().backward()
+
+    module = module.to(torch.bfloat16)
+    xb = x.to(cuda, torch.bfloat16).requires_grad_(True)
+    yb = module(xb)
+    assert module._core.last_path == "fused"
+    (yb.float() * dy.to(cuda, torch.float32)).sum().backward()
+    assert rel_err(yb, y64) < 2e-2
+    assert rel_err(xb.grad, x64.grad) < 2e-2
+    for name, p in module._core.named_parameters():
+        if params64[name].grad is not None and params64[name].grad.abs().max() > 0:
+            assert rel_err(p.grad, params64[name].grad) < 3e-2, name
+
+
+def test_cpu_input_raises_instead_of_falling_back(cuda):
+    import thetascan_amd as ts
+
+    module = ts.ThetaScan(ts.ThetaScanConfig(d_model=64, n_heads=2, family="kernel"))
+    with pytest.raises(RuntimeError, match="GPU"):
+        module(torch.randn(1, 8, 64))

@@ -1,0 +1,465 @@
+"""The ThetaScan token mixer on the hip backend.
+
+Parameters, buffers, names, shapes and initialisation follow the reference
+module (src/thetascan/_core/modules/block.py:136-406), so state dicts move
+between the two unchanged (including the 40-byte expansion fingerprint and
+its strict-load check).  ``forward`` (block.py:573-724) runs in one of two
+ways, both on the GPU:
+
+* the fused hot path (``fused.kernel_memory``) for a depth-1 kernel memory
+  with a ReLU^2-ridge or fixed-gain softmax-partition map, raw values, plain
+  or key-mass read and the plain temporal sum: three HIP kernels (write,
+  scan, read) between the two projection GEMMs;
+* the composed path (``engine``) for everything else, where every scan and
+  key mass still runs in the HIP kernels.
+"""
+from __future__ import annotations
+
+import hashlib
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ..config import ThetaScanConfig
+from ..ops import engine, fused
+from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
+from .gates import DecayGate, OutGate
+from .norms import l2norm
+from .rope import apply_rope, rope_cache, rotated_width
+
+_EXPANSION_MAP_DOMAIN = "thetascan-expansion-v1"
+_EXPANSION_FINGERPRINT_MAGIC = b"TSXF"
+_EXPANSION_FINGERPRINT_SCHEMA_VERSION = 1
+
+FUSED_HEAD_DIMS = (16, 32, 48, 64, 96, 128)
+
+
+def _inverse_softplus(value: float) -> float:
+    return value + math.log(-math.expm1(-value))
+
+
+def _row_correlation_penalty(weight: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
+    rows = weight / weight.norm(dim=-1, keepdim=True).clamp_min(eps)
+    gram = rows @ rows.t()
+    count = gram.shape[0]
+    if count < 2:
+        return weight.new_zeros(())
+    off = gram * (1.0 - torch.eye(count, dtype=gram.dtype, device=gram.device))
+    return off.square().sum() / (count * (count - 1))
+
+
+def _sign_domain(shape, *, key: str, role: str) -> bytes:
+    """Versioned SHAKE256 domain of one fixed sign stream (block.py:67-74)."""
+    return f"{_EXPANSION_MAP_DOMAIN}\0{key}\0{role}\0{','.join(str(v) for v in shape)}".encode("utf-8")
+
+
+def _fixed_rademacher(shape, *, key: str, role: str) -> torch.Tensor:
+    """Low bit of each SHAKE256 byte -> +-1 (block.py:49-64)."""
+    count = math.prod(shape)
+    raw = hashlib.shake_256(_sign_domain(shape, key=key, role=role)).digest(count)
+    bits = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(torch.int64) & 1
+    return (bits.to(torch.float32) * 2.0 - 1.0).reshape(shape)
+
+
+def _fixed_row_map(shape, *, key: str, role: str, row_norm: float = 1.0, center_rows: bool = True):
+    """Deterministic rows of prescribed L2 norm (block.py:117-133)."""
+    matrix = _fixed_rademacher(shape, key=key, role=role)
+    if center_rows:
+        matrix = matrix - matrix.mean(dim=-1, keepdim=True)
+    fallback = _fixed_rademacher(shape, key=key, role=f"{role}-fallback")
+    norm = matrix.norm(dim=-1, keepdim=True)
+    matrix = torch.where(norm > 0.0, matrix, fallback)
+    return matrix * (float(row_norm) / matrix.norm(dim=-1, keepdim=True))
+
+
+def _expansion_fingerprint(*, key: str, effective_hidden: int, feature_expansion: int, depth: int):
+    """``TSXF || u32 schema || sha256`` identity of the expansion maps (block.py:77-114)."""
+    if feature_expansion <= 1:
+        raise ValueError("an expansion fingerprint requires feature_expansion > 1")
+    base_hidden = effective_hidden // feature_expansion
+    digest = hashlib.sha256()
+    digest.update(b"thetascan-expansion-checkpoint\0")
+    digest.update(_EXPANSION_MAP_DOMAIN.encode("ascii"))
+    for layer in range(depth):
+        for desc in (
+            _sign_domain((1, effective_hidden, base_hidden), key=key, role=f"w1-expand-layer-{layer}"),
+            _sign_domain((1, base_hidden, effective_hidden), key=key, role=f"w2-expand-layer-{layer}"),
+        ):
+            digest.update(len(desc).to_bytes(8, "big"))
+            digest.update(desc)
+    encoded = _EXPANSION_FINGERPRINT_MAGIC + _EXPANSION_FINGERPRINT_SCHEMA_VERSION.to_bytes(4, "big") + digest.digest()
+    return torch.tensor(tuple(encoded), dtype=torch.uint8)
+
+
+class ThetaScan(nn.Module):
+    """Drop-in token mixer x[B,T,D] -> y[B,T,D] on MI355X."""
+
+    def __init__(self, cfg: ThetaScanConfig):
+        super().__init__()
+        self.cfg = cfg
+        D, H, d, m, L = cfg.d_model, cfg.n_heads, cfg.head_dim, cfg.mem_hidden, cfg.depth
+        if cfg.softmax_gain_mode == "learned_per_head":
+            self.kernel_sharpness_raw = nn.Parameter(torch.full((H,), _inverse_softplus(float(cfg.softmax_gain))))
+        elif cfg.softmax_gain_mode == "learned_per_feature":
+            self.kernel_sharpness_raw = nn.Parameter(torch.full((H, m), _inverse_softplus(float(cfg.softmax_gain))))
+        else:
+            self.register_parameter("kernel_sharpness_raw", None)
+        if cfg.kernel_score_bias:
+            self.kernel_score_bias = nn.Parameter(torch.zeros(H, m))
+        else:
+            self.register_parameter("kernel_score_bias", None)
+        if cfg.kernel_relu2_threshold_mode == "learned_per_head":
+            self.kernel_relu2_threshold = nn.Parameter(torch.zeros(H))
+        else:
+            self.register_parameter("kernel_relu2_threshold", None)
+        if cfg.kernel_sparsity != "none":
+            rho0 = float(cfg.kernel_relative_threshold_init)
+            self.kernel_relative_threshold_raw = nn.Parameter(torch.full((H,), math.log(rho0 / (1.0 - rho0))))
+        else:
+            self.register_parameter("kernel_relative_threshold_raw", None)
+        if cfg.kernel_sparsity == "relative_st_blend":
+            self.kernel_sparse_blend_raw = nn.Parameter(torch.full((H,), float(cfg.kernel_sparse_blend_init)))
+        else:
+            self.register_parameter("kernel_sparse_blend_raw", None)
+        if cfg.bspline_scale_mode == "learned_per_head":
+            self.bspline_scale_raw = nn.Parameter(torch.full((H,), _inverse_softplus(float(cfg.bspline_scale))))
+        else:
+            self.register_parameter("bspline_scale_raw", None)
+
+        if cfg.key_value_heads is not None:
+            G = cfg.key_value_heads
+            self.proj_qkv = None
+            self.proj_q = nn.Linear(D, H * d, bias=False)
+            self.proj_k = nn.Linear(D, G * d, bias=False)
+            self.proj_v = nn.Linear(D, G * d, bias=False)
+        elif cfg.share_kq:
+            self.proj_qkv = None
+            self.proj_q1 = nn.Linear(D, d, bias=False)
+            self.proj_k1 = nn.Linear(D, d, bias=False)
+            self.proj_v = nn.Linear(D, H * d, bias=False)
+            self.kq_bias = nn.Parameter(torch.zeros(2, H, d))
+        else:
+            self.proj_qkv = nn.Linear(D, 3 * H * d, bias=False)
+        self.proj_out = nn.Linear(H * d, D, bias=False)
+
+        def w(*shape, fan):
+            return nn.Parameter(torch.randn(*shape) / math.sqrt(fan))
+
+        width = m // cfg.feature_expansion
+        proj_rows = width // cfg.bspline_basis_count if cfg.kernel_kind == "projected_bspline" else width
+        self.W1 = nn.ParameterList([w(H, proj_rows, d, fan=d) for _ in range(L)])
+        self.W2 = nn.ParameterList([nn.Parameter(torch.zeros(H, d, width)) for _ in range(L)])
+        if cfg.nonlin == "swiglu":
+            self.Wg = nn.ParameterList([w(H, m, d, fan=d) for _ in range(L)])
+        elif cfg.learn_thresh:
+            self.Wg = nn.ParameterList([nn.Parameter(torch.zeros(H, m, 1)) for _ in range(L)])
+        elif cfg.value_centers:
+            self.Wg = nn.ParameterList([w(1, cfg.value_centers, d, fan=d) for _ in range(L)])
+        else:
+            self.Wg = None
+
+        self._w1_expansion_buffer_names: tuple = ()
+        self._w2_expansion_buffer_names: tuple = ()
+        self.register_buffer("_expansion_fingerprint", None)
+        if cfg.feature_expansion > 1:
+            w1_names, w2_names = [], []
+            for layer in range(L):
+                w1_name, w2_name = f"_expand_w1_{layer}", f"_expand_w2_{layer}"
+                self.register_buffer(w1_name, _fixed_row_map((1, m, width), key=cfg.expansion_key,
+                                                             role=f"w1-expand-layer-{layer}", center_rows=False),
+                                     persistent=False)
+                self.register_buffer(w2_name, _fixed_row_map((1, width, m), key=cfg.expansion_key,
+                                                             role=f"w2-expand-layer-{layer}", center_rows=False),
+                                     persistent=False)
+                w1_names.append(w1_name)
+                w2_names.append(w2_name)
+            self._w1_expansion_buffer_names = tuple(w1_names)
+            self._w2_expansion_buffer_names = tuple(w2_names)
+            self._expansion_fingerprint = _expansion_fingerprint(
+                key=cfg.expansion_key, effective_hidden=m, feature_expansion=cfg.feature_expansion, depth=L)
+
+        self.decay = DecayGate(D, H) if cfg.decay_gate != "off" else None
+        self.vmlp_in = self.vmlp_out = None
+        if cfg.value_mlp_mult > 0:
+            vh = max(1, int(cfg.value_mlp_mult * d))
+            self.vmlp_in = nn.Linear(d, vh)
+            self.vmlp_out = nn.Linear(vh, d)
+            nn.init.zeros_(self.vmlp_out.weight)
+            nn.init.zeros_(self.vmlp_out.bias)
+        self.ogate = OutGate(D, H, d) if cfg.out_gate else None
+        if cfg.read_fade:
+            alphas = cfg.resolved_fade_alphas
+            if cfg.fade_branches == 1:
+                self.fade_alpha = nn.Parameter(torch.full((H,), math.log(alphas[0] / (1.0 - alphas[0]))))
+                self.fade_eta = nn.Parameter(torch.zeros(H))
+            else:
+                raw = [math.log(a / (1.0 - a)) for a in alphas]
+                self.fade_alpha = nn.Parameter(torch.tensor(raw).view(-1, 1).expand(-1, H).clone())
+                self.fade_eta = nn.Parameter(torch.zeros(cfg.fade_branches, H))
+        else:
+            self.fade_alpha = None
+            self.fade_eta = None
+        self._backend = None
+        self.last_path = None
+
+    # ------------------------------------------------------------ checkpoints
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs) -> None:
+        """Reject a checkpoint whose expansion fingerprint does not match (block.py:335-406)."""
+        fingerprint = self._expansion_fingerprint
+        key = prefix + "_expansion_fingerprint"
+        if fingerprint is not None and key in state_dict:
+            loaded = state_dict[key]
+            loaded_bytes = None
+            if (torch.is_tensor(loaded) and loaded.dtype == torch.uint8 and loaded.ndim == 1
+                    and loaded.numel() == fingerprint.numel()):
+                loaded_bytes = bytes(loaded.detach().cpu().tolist())
+            expected = bytes(fingerprint.detach().cpu().tolist())
+            if loaded_bytes != expected:
+                if loaded_bytes is None:
+                    reason = "malformed compact fingerprint"
+                elif loaded_bytes[:4] != _EXPANSION_FINGERPRINT_MAGIC:
+                    reason = "unknown compact fingerprint encoding"
+                elif int.from_bytes(loaded_bytes[4:8], "big") != _EXPANSION_FINGERPRINT_SCHEMA_VERSION:
+                    reason = (f"unsupported fingerprint schema version {int.from_bytes(loaded_bytes[4:8], 'big')} "
+                              f"(expected {_EXPANSION_FINGERPRINT_SCHEMA_VERSION})")
+                else:
+                    reason = "fingerprint mismatch (different expansion_key, map shapes, or map derivation)"
+                error_msgs.append(f"{key}: cannot load random feature expansion: {reason}")
+                raise RuntimeError(error_msgs[-1])
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+
+    # ------------------------------------------------------------ controls
+
+    def kernel_sharpness(self):
+        if self.kernel_sharpness_raw is None:
+            return None
+        value = F.softplus(self.kernel_sharpness_raw)
+        return value.clamp_min(torch.finfo(value.dtype).tiny)
+
+    def kernel_relative_threshold(self):
+        if self.kernel_relative_threshold_raw is None:
+            return None
+        return torch.sigmoid(self.kernel_relative_threshold_raw)
+
+    def kernel_sparse_blend_alpha(self):
+        if self.kernel_sparse_blend_raw is None:
+            return None
+        bounded = self.kernel_sparse_blend_raw.clamp(0.0, 1.0)
+        surrogate = torch.sigmoid(self.kernel_sparse_blend_raw)
+        return bounded.detach() + surrogate - surrogate.detach()
+
+    def bspline_scale(self):
+        if self.bspline_scale_raw is None:
+            return None
+        value = F.softplus(self.bspline_scale_raw)
+        return value.clamp_min(torch.finfo(value.dtype).tiny)
+
+    def kernel_controls(self) -> dict:
+        return {
+            "spline_scale": self.bspline_scale(),
+            "score_bias": self.kernel_score_bias,
+            "relu2_threshold": self.kernel_relu2_threshold,
+            "relative_threshold": self.kernel_relative_threshold(),
+            "sparse_blend_alpha": self.kernel_sparse_blend_alpha(),
+        }
+
+    def key_query_feature_parameters(self):
+        seen = set()
+        for parameter in self.W1:
+            if id(parameter) not in seen:
+                seen.add(id(parameter))
+                yield parameter
+        for name in ("kernel_sharpness_raw", "kernel_score_bias", "kernel_relu2_threshold",
+                     "kernel_relative_threshold_raw", "kernel_sparse_blend_raw", "bspline_scale_raw"):
+            parameter = getattr(self, name, None)
+            if parameter is not None and id(parameter) not in seen:
+                seen.add(id(parameter))
+                yield parameter
+
+    def fade_blends(self):
+        if self.fade_eta is None:
+            return None
+        return torch.tanh(self.fade_eta) if self.cfg.fade_blend_mode == "tanh" else self.fade_eta
+
+    def ortho_loss(self) -> torch.Tensor:
+        """Cosine decorrelation of theta0 rows and heads (block.py:496-544)."""
+        cfg = self.cfg
+        out = torch.zeros((), device=self.W2[0].device, dtype=self.W2[0].dtype)
+        if cfg.ortho_intra == 0.0 and cfg.ortho_inter == 0.0 and cfg.value_mlp_ortho == 0.0:
+            return out
+        lists = [self.W1, self.W2] + ([] if cfg.learn_thresh else [self.Wg])
+        mats = [W for lst in lists if lst is not None for W in lst]
+        if cfg.ortho_intra:
+            eligible = [W for W in mats if W.shape[-2] > 1]
+            acc = 0.0
+            for W in eligible:
+                Wn = W / W.norm(dim=-1, keepdim=True).clamp_min(cfg.eps)
+                G = Wn @ Wn.transpose(-1, -2)
+                r = G.shape[-1]
+                off = G * (1.0 - torch.eye(r, device=G.device, dtype=G.dtype))
+                acc = acc + off.square().sum() / (G.shape[0] * r * (r - 1))
+            if eligible:
+                out = out + cfg.ortho_intra * acc / len(eligible)
+        if cfg.ortho_inter and cfg.n_heads > 1:
+            eligible = [W for W in mats if W.shape[0] > 1]
+            acc = 0.0
+            for W in eligible:
+                V = W.flatten(1)
+                Vn = V / V.norm(dim=-1, keepdim=True).clamp_min(cfg.eps)
+                Gh = Vn @ Vn.t()
+                Hh = Gh.shape[0]
+                off = Gh * (1.0 - torch.eye(Hh, device=Gh.device, dtype=Gh.dtype))
+                acc = acc + off.square().sum() / (Hh * (Hh - 1))
+            if eligible:
+                out = out + cfg.ortho_inter * acc / len(eligible)
+        if cfg.value_mlp_ortho and self.vmlp_in is not None:
+            out = out + cfg.value_mlp_ortho * (_row_correlation_penalty(self.vmlp_in.weight, cfg.eps)
+                                               + _row_correlation_penalty(self.vmlp_out.weight, cfg.eps)) / 2.0
+        return out
+
+    def _weights(self):
+        """Effective (expanded) memory weights per depth level (block.py:546-567)."""
+        out = []
+        for l in range(self.cfg.depth):
+            W1, W2 = self.W1[l], self.W2[l]
+            if self.cfg.feature_expansion > 1:
+                W1 = torch.matmul(getattr(self, self._w1_expansion_buffer_names[l]).to(W1.dtype), W1)
+                W2 = torch.matmul(W2, getattr(self, self._w2_expansion_buffer_names[l]).to(W2.dtype))
+            out.append((W1, W2, self.Wg[l] if self.Wg is not None else None))
+        return out
+
+    # ------------------------------------------------------------ forward
+
+    def fused_eligible(self, x: torch.Tensor) -> bool:
+        """Whether the three-kernel hot path covers this configuration and input."""
+        cfg = self.cfg
+        if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
+            return False
+        if cfg.write_rule != "kernel" or cfg.depth != 1 or cfg.value_centers or cfg.value_mlp_mult > 0:
+            return False
+        if cfg.read_fade or cfg.accumulation != "sum" or cfg.share_kq or cfg.key_value_heads is not None:
+            return False
+        if cfg.read_norm and cfg.read_norm_mode != "key_mass":
+            return False
+        if cfg.head_dim not in FUSED_HEAD_DIMS or cfg.mem_hidden % 16 or cfg.mem_hidden > 256:
+            return False
+        if cfg.kernel_kind == "relu2_ridge":
+            return self.kernel_score_bias is None
+        if cfg.kernel_kind == "softmax_partition":
+            return (cfg.softmax_gain_mode == "fixed" and cfg.kernel_sparsity == "none"
+                    and self.kernel_score_bias is None)
+        return False
+
+    def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        B, T, _ = x.shape
+        H, d, m = cfg.n_heads, cfg.head_dim, cfg.mem_hidden
+        qkv = F.linear(x, self.proj_qkv.weight).view(B, T, 3, H, d)
+        in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
+        feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
+        kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
+        spec = fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot, cfg.rope_base,
+                                 1.0 / math.sqrt(cfg.depth), cfg.eps)
+        (W1, W2, _), = self._weights()
+        g = self.ogate.preactivation(x) if self.ogate is not None else None
+        y = fused.kernel_memory(qkv, W1, W2, self.kernel_relu2_threshold, g, spec, cfg.read_norm)
+        return F.linear(y, self.proj_out.weight)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        self._backend = resolve_backend(cfg.backend, cfg.decay_gate, cfg.accumulation, device=x.device,
+                                        require_scalar_decay=cfg.read_fade)
+        if not x.is_cuda:
+            raise RuntimeError("the hip backend runs on the GPU only (no CPU fallback)")
+        if self.fused_eligible(x):
+            self.last_path = "fused"
+            return self._forward_fused(x)
+        self.last_path = "composed"
+        return self._forward_composed(x)
+
+    def _project(self, x):
+        cfg = self.cfg
+        B, T, _ = x.shape
+        H, d = cfg.n_heads, cfg.head_dim
+        if cfg.key_value_heads is not None:
+            G = cfg.key_value_heads
+            q = F.linear(x, self.proj_q.weight).view(B, T, H, d).transpose(1, 2)
+            k = F.linear(x, self.proj_k.weight).view(B, T, G, d).transpose(1, 2)
+            v = F.linear(x, self.proj_v.weight).view(B, T, G, d).transpose(1, 2)
+            return q, k.repeat_interleave(H // G, dim=1), v.repeat_interleave(H // G, dim=1)
+        if cfg.share_kq:
+            kqb = self.kq_bias.to(dtype=x.dtype)
+            q = F.linear(x, self.proj_q1.weight).unsqueeze(1) + kqb[0][None, :, None, :]
+            k = F.linear(x, self.proj_k1.weight).unsqueeze(1) + kqb[1][None, :, None, :]
+            v = F.linear(x, self.proj_v.weight).view(B, T, H, d).transpose(1, 2)
+            return q, k, v
+        q, k, v = F.linear(x, self.proj_qkv.weight).view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
+        return q, k, v
+
+    def _forward_composed(self, x: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        B, T, _ = x.shape
+        H, d = cfg.n_heads, cfg.head_dim
+        q, k, v = self._project(x)
+        if cfg.rope_placement == "input":
+            q = apply_rope(q, cfg.rope, cfg.rope_frac, cfg.rope_base)
+            k = apply_rope(k, cfg.rope, cfg.rope_frac, cfg.rope_base)
+        if cfg.qk_norm:
+            q, k = l2norm(q, cfg.eps), l2norm(k, cfg.eps)
+        v_w = v
+        if self.vmlp_in is not None:
+            v_w = v_w + self.vmlp_out(F.silu(self.vmlp_in(v_w)))
+        hrot = None
+        if cfg.rope_placement == "feature" and cfg.rope != "none":
+            rot = rotated_width(cfg.mem_hidden, cfg.rope, cfg.rope_frac)
+            if rot:
+                hcos, hsin = rope_cache(T, rot, cfg.rope_base, x.device, x.dtype)
+                hrot = (hcos, hsin, rot)
+        decay_d = decay_m = None
+        if self.decay is not None:
+            decay_d, decay_m = self.decay(x)
+        acc = Accumulator(self._backend, decay_d=decay_d, decay_m=decay_m, eps=cfg.eps, chunk=cfg.scan_chunk)
+        weights = self._weights()
+        sharp = self.kernel_sharpness()
+        controls = self.kernel_controls()
+        streams, _, _ = engine.write_streams(weights, cfg, k, v_w, hrot=hrot, softmax_gain=sharp,
+                                             kernel_controls=controls)
+        views = [acc]
+        etas = []
+        if cfg.read_fade:
+            alpha_raw = self.fade_alpha
+            eta = self.fade_blends()
+            if alpha_raw.ndim == 1:
+                alpha_raw, eta = alpha_raw.unsqueeze(0), eta.unsqueeze(0)
+            for branch in range(cfg.fade_branches):
+                log_alpha = (-F.softplus(-alpha_raw[branch])).to(dtype=x.dtype)
+                la_s = log_alpha.view(1, H, 1, 1).expand(B, H, T, 1)
+                fast = Accumulator(self._backend, decay_d=la_s, decay_m=la_s, eps=cfg.eps, chunk=cfg.scan_chunk,
+                                   static_log_alpha=log_alpha)
+                if cfg.read_fade_mode == "fast":
+                    views.append(FadeFast(fast, log_alpha, chunk=cfg.scan_chunk))
+                else:
+                    views.append(FadeStale(acc, fast, log_alpha, cfg.scan_chunk))
+                etas.append(eta[branch].view(1, -1, 1, 1))
+            if cfg.read_fade_mode == "stale":
+                views.append(NullAccumulator())
+        reads = engine.dual_read_views(weights, cfg, q, streams, tuple(views), hrot=hrot, softmax_gain=sharp,
+                                       kernel_controls=controls)
+        y = reads[0]
+        if cfg.read_fade:
+            if cfg.read_fade_mode == "fast":
+                for out_fast, eta in zip(reads[1:], etas):
+                    y = y + eta.to(y.dtype) * (out_fast - reads[0])
+            else:
+                base = reads[-1]
+                for out_stale, eta in zip(reads[1:-1], etas):
+                    y = y - eta.to(y.dtype) * (out_stale - base)
+        if self.ogate is not None:
+            y = y * self.ogate(x)
+        y = y.transpose(1, 2).reshape(B, T, H * d)
+        return F.linear(y, self.proj_out.weight)

@@ -1,0 +1,250 @@
+"""Fused HIP hot path of the kernel-family mixer (write -> scan -> read).
+
+``kernel_memory`` is one autograd node covering everything between the qkv
+projection and the output projection of a kernel-memory mixer:
+
+    phi_k = feature(k)                 ts_feature_fwd   (keys)
+    phi_q, resid = feature(q)          ts_feature_fwd   (queries, + W2 base)
+    num, mass = scan(phi_q, phi_k, v)  ts_scan_fwd      (key-mass column)
+    y = (resid + s*num/(mass+eps)) * silu(g)            ts_read_fwd
+
+and its backward (ts_read_bwd -> three scans -> ts_feature_bwd, then plain
+GEMMs for the W1/W2 gradients).  Reference chain:
+src/thetascan/_core/modules/block.py:593-724 and
+src/thetascan/_core/ops/engine.py:260-544 for a depth-1 kernel memory.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from ... import _lib
+from . import scan_hip
+
+
+def _rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos/sin [T, rot/2] (rope.py:7-38 phases, kept in fp32)."""
+    inv = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
+    f = torch.outer(torch.arange(T, device=device, dtype=torch.float32), inv)
+    return f.cos().contiguous(), f.sin().contiguous()
+
+
+_TABLES: dict = {}
+
+
+def rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    key = (T, rot, float(base), str(device))
+    hit = _TABLES.get(key)
+    if hit is None:
+        if len(_TABLES) > 64:
+            _TABLES.clear()
+        hit = _TABLES[key] = _rope_tables(T, rot, base, device)
+    return hit
+
+
+class FeatureSpec:
+    """Static description of one fused feature map."""
+
+    def __init__(self, kind: int, m: int, gain: float, in_rot: int, feat_rot: int, rope_base: float,
+                 resid_scale: float, eps: float = 1e-6):
+        self.kind, self.m, self.gain = kind, m, gain
+        self.in_rot, self.feat_rot, self.rope_base = in_rot, feat_rot, rope_base
+        self.resid_scale, self.eps = resid_scale, eps
+
+    def desc(self, x: torch.Tensor, has_tau: bool) -> _lib.FeatureDesc:
+        B, H, T, d = x.shape
+        return _lib.FeatureDesc(B, H, T, d, self.m, _lib.dtype_code(x.dtype), self.kind, self.in_rot,
+                                self.feat_rot, int(has_tau), float(self.gain), float(self.resid_scale),
+                                float(self.eps))
+
+    def tables(self, T: int, device):
+        ic = is_ = fc = fs = None
+        if self.in_rot:
+            ic, is_ = rope_tables(T, self.in_rot, self.rope_base, device)
+        if self.feat_rot:
+            fc, fs = rope_tables(T, self.feat_rot, self.rope_base, device)
+        return ic, is_, fc, fs
+
+
+def feature_fwd(spec: FeatureSpec, x, w1, w2, tau, want_resid: bool):
+    lib = _lib.load()
+    B, H, T, d = x.shape
+    phi = torch.empty(B, H, T, spec.m, dtype=x.dtype, device=x.device)
+    resid = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device) if want_resid else None
+    ic, is_, fc, fs = spec.tables(T, x.device)
+    io = _lib.FeatureIO(_lib.strided(x), _lib.ptr(w1), _lib.ptr(w2), _lib.ptr(tau), _lib.ptr(ic),
+                        _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(phi), _lib.strided(resid))
+    desc = spec.desc(x, tau is not None)
+    _lib.check(lib.ts_feature_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device)),
+               "ts_feature_fwd")
+    return phi, resid
+
+
+def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_weights=True):
+    """Returns (da, xn, h, dtau_tok); dx is written in place."""
+    lib = _lib.load()
+    B, H, T, d = x.shape
+    m = spec.m
+    w1t = w1.transpose(1, 2).contiguous()
+    w2t = w2.transpose(1, 2).contiguous() if (dresid is not None) else None
+    da = torch.empty(B, H, T, m, dtype=x.dtype, device=x.device) if want_weights else None
+    xn = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device) if want_weights else None
+    h = torch.empty(B, H, T, m, dtype=x.dtype, device=x.device) if (want_weights and dresid is not None) else None
+    dtau = torch.empty(B, H, T, dtype=torch.float32, device=x.device) if tau is not None else None
+    ic, is_, fc, fs = spec.tables(T, x.device)
+    io = _lib.FeatureBwdIO(
+        _lib.strided(x), _lib.ptr(w1), _lib.ptr(w1t), _lib.ptr(w2t), _lib.ptr(tau), _lib.ptr(ic),
+        _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(dphi), _lib.strided(dresid),
+        _lib.strided(dx), _lib.strided(da), _lib.strided(xn), _lib.strided(h), _lib.strided(dtau),
+    )
+    desc = spec.desc(x, tau is not None)
+    _lib.check(lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device)),
+               "ts_feature_bwd")
+    return da, xn, h, dtau
+
+
+def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6):
+    lib = _lib.load()
+    B, H, T, d = num.shape
+    desc = _lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None), int(g is not None),
+                         float(scale), float(eps))
+    io = _lib.ReadIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
+                     _lib.strided(y))
+    _lib.check(lib.ts_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device)),
+               "ts_read_fwd")
+    return y
+
+
+def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6):
+    lib = _lib.load()
+    B, H, T, d = num.shape
+    dnum = torch.empty_like(num)
+    dmass = torch.empty(B, H, T, dtype=torch.float32, device=num.device) if mass is not None else None
+    dresid = torch.empty(B, H, T, d, dtype=torch.float32, device=num.device)
+    dg = torch.empty(B, T, H, d, dtype=num.dtype, device=num.device).transpose(1, 2) if g is not None else None
+    desc = _lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None), int(g is not None),
+                         float(scale), float(eps))
+    io = _lib.ReadBwdIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
+                        _lib.strided(dy), _lib.strided(dnum), _lib.strided(dmass), _lib.strided(dresid),
+                        _lib.strided(dg))
+    _lib.check(lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device)),
+               "ts_read_bwd")
+    return dnum, dmass, dresid, dg
+
+
+def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Tensor:
+    """Decayed prefix sum along T of a [B,H,T,F] stream (fp32 result).
+
+    ``retention`` is None (plain prefix), a static [H] log-retention or a
+    [B,H,T,1] per-token log-retention stream.
+    """
+    if not x.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    lib = _lib.load()
+    xf = x.to(torch.float32)
+    if xf.stride(-1) != 1:
+        xf = xf.contiguous()
+    B, H, T, F = xf.shape
+    out = torch.empty(B, H, T, F, dtype=torch.float32, device=x.device)
+    kind, la, dec = _lib.RET_NONE, None, None
+    if retention is not None:
+        if retention.ndim == 4:
+            kind = _lib.RET_STREAM
+            dec = retention.detach().to(torch.float32).reshape(B, H, T)
+        else:
+            kind = _lib.RET_STATIC
+            la = retention.detach().to(torch.float32).reshape(H).contiguous()
+    desc = _lib.WcumsumDesc(B, H, T, F, kind, int(reverse))
+    _lib.check(lib.ts_wcumsum(ctypes.byref(desc), _lib.strided(xf), _lib.strided(out), _lib.ptr(la),
+                              _lib.strided(dec), _lib.stream_handle(x.device)), "ts_wcumsum")
+    return out
+
+
+def _weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """sum_{b,t} a[b,h,t,:]^T b[b,h,t,:] -> [H, A, B] (a plain batched GEMM)."""
+    B, H, T, A = a.shape
+    Bw = b.shape[-1]
+    a2 = a.permute(1, 3, 0, 2).reshape(H, A, B * T)
+    b2 = b.permute(1, 0, 2, 3).reshape(H, B * T, Bw)
+    return torch.bmm(a2.float(), b2.float())
+
+
+class _KernelMemory(torch.autograd.Function):
+    """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g) for a depth-1 kernel memory."""
+
+    @staticmethod
+    def forward(ctx, qkv, w1, w2, tau, g, spec: FeatureSpec, normalize: bool, seg_chunks: int):
+        B, T, three, H, d = qkv.shape
+        q = qkv[:, :, 0].transpose(1, 2)
+        k = qkv[:, :, 1].transpose(1, 2)
+        v = qkv[:, :, 2].transpose(1, 2)
+        dt = qkv.dtype
+        w1c = w1.to(dt).contiguous()
+        w2c = w2.to(dt).contiguous()
+        tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
+        phi_k, _ = feature_fwd(spec, k, w1c, None, tauf, False)
+        phi_q, resid = feature_fwd(spec, q, w1c, w2c, tauf, True)
+        num, mass, _ = scan_hip.scan_launch(
+            phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
+            seg_chunks=seg_chunks,
+        )
+        gv = None if g is None else g.view(B, T, H, d).transpose(1, 2)
+        y = torch.empty(B, T, H, d, dtype=dt, device=qkv.device)
+        read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps)
+        ctx.spec, ctx.normalize, ctx.seg_chunks = spec, normalize, seg_chunks
+        ctx.has_tau, ctx.has_g = tau is not None, g is not None
+        ctx.tau_dtype = None if tau is None else tau.dtype
+        ctx.w_dtypes = (w1.dtype, w2.dtype)
+        ctx.save_for_backward(qkv, w1c, w2c, tauf, g, phi_q, phi_k, num, mass, resid)
+        return y.view(B, T, H * d)
+
+    @staticmethod
+    def backward(ctx, dy):
+        qkv, w1c, w2c, tauf, g, phi_q, phi_k, num, mass, resid = ctx.saved_tensors
+        spec = ctx.spec
+        B, T, three, H, d = qkv.shape
+        dt = qkv.dtype
+        q = qkv[:, :, 0].transpose(1, 2)
+        k = qkv[:, :, 1].transpose(1, 2)
+        v = qkv[:, :, 2].transpose(1, 2)
+        dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
+        gv = None if g is None else g.view(B, T, H, d).transpose(1, 2)
+        dnum, dmass, dresid, dg = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps)
+        norm = ctx.normalize
+        q_ext = dmass if norm else None
+        dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
+                                            out_mode=_lib.OUT_STORE_F32, seg_chunks=ctx.seg_chunks)
+        dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
+                                            k_ext=q_ext, out_mode=_lib.OUT_STORE_F32, seg_chunks=ctx.seg_chunks)
+        dqkv = torch.empty_like(qkv)
+        dq = dqkv[:, :, 0].transpose(1, 2)
+        dk = dqkv[:, :, 1].transpose(1, 2)
+        dv = dqkv[:, :, 2].transpose(1, 2)
+        scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=ctx.seg_chunks)
+        need_w1 = ctx.needs_input_grad[1]
+        need_w2 = ctx.needs_input_grad[2]
+        da_k, xn_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=need_w1)
+        da_q, xn_q, h_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c,
+                                              want_weights=need_w1 or need_w2)
+        dw1 = dw2 = dtau = None
+        if need_w1:
+            dw1 = (_weight_grad(da_k, xn_k) + _weight_grad(da_q, xn_q)).to(ctx.w_dtypes[0])
+        if need_w2:
+            dw2 = (_weight_grad(dresid, h_q) * spec.resid_scale).to(ctx.w_dtypes[1])
+        if ctx.has_tau and ctx.needs_input_grad[3]:
+            dtau = (dtau_k.sum(dim=(0, 2)) + dtau_q.sum(dim=(0, 2))).to(ctx.tau_dtype)
+        dgo = None
+        if ctx.has_g:
+            dgo = dg.transpose(1, 2).reshape(B, T, H * d)
+        return dqkv, dw1, dw2, dtau, dgo, None, None, None
+
+
+def kernel_memory(qkv, w1, w2, tau, g, spec: FeatureSpec, normalize: bool, seg_chunks: int = 0):
+    """Fused kernel-memory read; qkv is the [B,T,3,H,d] projection output."""
+    if not qkv.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    if not qkv.is_contiguous():
+        qkv = qkv.contiguous()
+    return _KernelMemory.apply(qkv, w1, w2, tau, g, spec, normalize, seg_chunks)

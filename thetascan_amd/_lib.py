@@ -80,22 +80,109 @@ class ScanIO(ctypes.Structure):
     ]
 
 
+class FeatureDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("m", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("kind", ctypes.c_int32),
+        ("in_rot", ctypes.c_int32),
+        ("feat_rot", ctypes.c_int32),
+        ("has_tau", ctypes.c_int32),
+        ("gain", ctypes.c_float),
+        ("resid_scale", ctypes.c_float),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class FeatureIO(ctypes.Structure):
+    _fields_ = [
+        ("x", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("in_cos", ctypes.c_void_p),
+        ("in_sin", ctypes.c_void_p),
+        ("f_cos", ctypes.c_void_p),
+        ("f_sin", ctypes.c_void_p),
+        ("phi", Strided),
+        ("resid", Strided),
+    ]
+
+
+class FeatureBwdIO(ctypes.Structure):
+    _fields_ = [
+        ("x", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w1t", ctypes.c_void_p),
+        ("w2t", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("in_cos", ctypes.c_void_p),
+        ("in_sin", ctypes.c_void_p),
+        ("f_cos", ctypes.c_void_p),
+        ("f_sin", ctypes.c_void_p),
+        ("dphi", Strided),
+        ("dresid", Strided),
+        ("dx", Strided),
+        ("da", Strided),
+        ("xn", Strided),
+        ("h", Strided),
+        ("dtau", Strided),
+    ]
+
+
+class ReadDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("normalize", ctypes.c_int32),
+        ("gate", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class ReadIO(ctypes.Structure):
+    _fields_ = [("num", Strided), ("mass", Strided), ("resid", Strided), ("g", Strided), ("y", Strided)]
+
+
+class ReadBwdIO(ctypes.Structure):
+    _fields_ = [
+        ("num", Strided),
+        ("mass", Strided),
+        ("resid", Strided),
+        ("g", Strided),
+        ("dy", Strided),
+        ("dnum", Strided),
+        ("dmass", Strided),
+        ("dresid", Strided),
+        ("dg", Strided),
+    ]
+
+
+class WcumsumDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("F", ctypes.c_int32),
+        ("retention", ctypes.c_int32),
+        ("reverse", ctypes.c_int32),
+    ]
+
+
+FEAT_RELU2 = 0
+FEAT_SOFTMAX = 1
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
-# Every symbol include/thetascan_hip.h declares.
-EXPORTS = (
-    "ts_abi_version",
-    "ts_last_error",
-    "ts_scan_layout",
-    "ts_scan_workspace_bytes",
-    "ts_scan_fwd",
-    "ts_feature_fwd",
-    "ts_feature_bwd",
-    "ts_read_fwd",
-    "ts_read_bwd",
-    "ts_wcumsum",
-)
 
 
 def library_path() -> Path:
@@ -132,6 +219,12 @@ def load() -> ctypes.CDLL:
             ctypes.c_size_t,
             ctypes.c_void_p,
         ]
+        P = ctypes.POINTER
+        lib.ts_feature_fwd.argtypes = [P(FeatureDesc), P(FeatureIO), ctypes.c_void_p]
+        lib.ts_feature_bwd.argtypes = [P(FeatureDesc), P(FeatureBwdIO), ctypes.c_void_p]
+        lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
+        lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
+        lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
         if lib.ts_abi_version() != 1:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
@@ -155,6 +248,10 @@ def strided(t: torch.Tensor | None) -> Strided:
         return Strided(None, 0, 0, 0)
     s = t.stride()
     return Strided(t.data_ptr(), s[0], s[1], s[2])
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
 
 
 def stream_handle(device: torch.device) -> int:

@@ -6,6 +6,9 @@
 
 namespace ts {
 
+// Record a message for ts_last_error() and return `code` (host side).
+int fail(int code, const char* fmt, ...);
+
 typedef __bf16 bf16;
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -60,6 +63,61 @@ template <typename E> struct Vec16 {
     uint4 raw;
     E e[16 / sizeof(E)];
   };
+};
+
+// Fragment loads/stores for MFMA operands (LDS or global, 16-byte aligned).
+template <typename E> struct LdsIO;
+template <> struct LdsIO<bf16> {
+  static __device__ __forceinline__ bf16x8 ld8(const bf16* p) {
+    uint4 r = *(const uint4*)p;
+    return __builtin_bit_cast(bf16x8, r);
+  }
+  static __device__ __forceinline__ bf16x4 ld4(const bf16* p) {
+    uint2 r = *(const uint2*)p;
+    return __builtin_bit_cast(bf16x4, r);
+  }
+  static __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  static __device__ __forceinline__ bf16x8 from_acc(floatx4 a, floatx4 b) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r[i] = (bf16)a[i];
+      r[4 + i] = (bf16)b[i];
+    }
+    return r;
+  }
+  static __device__ __forceinline__ bf16x4 from_acc4(floatx4 a) {
+    bf16x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (bf16)a[i];
+    return r;
+  }
+  static __device__ __forceinline__ void st4(bf16* p, float a0, float a1, float a2, float a3) {
+    bf16x4 r;
+    r[0] = (bf16)a0; r[1] = (bf16)a1; r[2] = (bf16)a2; r[3] = (bf16)a3;
+    *(uint2*)p = __builtin_bit_cast(uint2, r);
+  }
+};
+template <> struct LdsIO<float> {
+  static __device__ __forceinline__ floatx8 ld8(const float* p) {
+    floatx4 a = *(const floatx4*)p;
+    floatx4 b = *(const floatx4*)(p + 4);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  static __device__ __forceinline__ floatx4 ld4(const float* p) { return *(const floatx4*)p; }
+  static __device__ __forceinline__ floatx8 cat(floatx4 a, floatx4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  static __device__ __forceinline__ floatx8 from_acc(floatx4 a, floatx4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  static __device__ __forceinline__ floatx4 from_acc4(floatx4 a) { return a; }
+  static __device__ __forceinline__ void st4(float* p, float a0, float a1, float a2, float a3) {
+    floatx4 r = {a0, a1, a2, a3};
+    *(floatx4*)p = r;
+  }
 };
 
 }  // namespace ts

@@ -1,0 +1,235 @@
+// Read epilogue (normalised read + residual + output gate) and decayed
+// prefix sums for gfx950.  Both are HBM-bound streaming kernels: one thread
+// owns one (batch, head, token) row and walks it in 16-byte vectors.
+
+#include "ts_common.h"
+#include "thetascan_hip.h"
+
+#include <string.h>
+
+namespace ts {
+
+struct ReadP {
+  int B, H, T, d, normalize, gate;
+  float s, eps;
+  ts_strided num, mass, resid, g, y, dy, dnum, dmass, dresid, dg;
+};
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float dsilu(float x) {
+  const float sg = 1.0f / (1.0f + expf(-x));
+  return sg * (1.0f + x * (1.0f - sg));
+}
+
+template <typename E>
+__device__ __forceinline__ const E* rowp(const ts_strided& s, int b, int h, int t) {
+  return (const E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
+}
+template <typename E>
+__device__ __forceinline__ E* rowp_w(const ts_strided& s, int b, int h, int t) {
+  return (E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
+}
+
+template <typename E>
+__device__ __forceinline__ void ld_vec(const E* p, float* out) {
+  Vec16<E> v;
+  v.raw = *(const uint4*)p;
+#pragma unroll
+  for (int e = 0; e < Vec16<E>::N; ++e) out[e] = tof(v.e[e]);
+}
+template <typename E>
+__device__ __forceinline__ void st_vec(E* p, const float* in) {
+  Vec16<E> v;
+#pragma unroll
+  for (int e = 0; e < Vec16<E>::N; ++e) v.e[e] = cvt<E>(in[e]);
+  *(uint4*)p = v.raw;
+}
+
+// y = (resid + s * num / (mass + eps)) * silu(g)     (engine.py:440-442, 526-528; gates.py:34-40)
+template <typename E>
+__global__ __launch_bounds__(256) void read_fwd_kernel(ReadP p) {
+  constexpr int N = Vec16<E>::N;
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nrows = (int64_t)p.B * p.H * p.T;
+  if (row >= nrows) return;
+  const int t = (int)(row % p.T);
+  const int h = (int)((row / p.T) % p.H);
+  const int b = (int)(row / ((int64_t)p.T * p.H));
+  float scale = p.s;
+  if (p.normalize) scale = p.s / (rowp<float>(p.mass, b, h, t)[0] + p.eps);
+  const E* num = rowp<E>(p.num, b, h, t);
+  const E* res = p.resid.ptr ? rowp<E>(p.resid, b, h, t) : nullptr;
+  const E* gg = p.gate ? rowp<E>(p.g, b, h, t) : nullptr;
+  E* y = rowp_w<E>(p.y, b, h, t);
+  for (int c = 0; c < p.d; c += N) {
+    float nv[N], rv[N], gv[N], out[N];
+    ld_vec<E>(num + c, nv);
+    if (res) ld_vec<E>(res + c, rv);
+    if (gg) ld_vec<E>(gg + c, gv);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      float v = (res ? rv[e] : 0.0f) + scale * nv[e];
+      out[e] = gg ? v * silu(gv[e]) : v;
+    }
+    st_vec<E>(y + c, out);
+  }
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p) {
+  constexpr int N = Vec16<E>::N;
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nrows = (int64_t)p.B * p.H * p.T;
+  if (row >= nrows) return;
+  const int t = (int)(row % p.T);
+  const int h = (int)((row / p.T) % p.H);
+  const int b = (int)(row / ((int64_t)p.T * p.H));
+  float denom = 1.0f;
+  if (p.normalize) denom = rowp<float>(p.mass, b, h, t)[0] + p.eps;
+  const float scale = p.s / denom;
+  const E* num = rowp<E>(p.num, b, h, t);
+  const E* res = p.resid.ptr ? rowp<E>(p.resid, b, h, t) : nullptr;
+  const E* gg = p.gate ? rowp<E>(p.g, b, h, t) : nullptr;
+  const E* dy = rowp<E>(p.dy, b, h, t);
+  E* dnum = rowp_w<E>(p.dnum, b, h, t);
+  float* dres = p.dresid.ptr ? rowp_w<float>(p.dresid, b, h, t) : nullptr;
+  E* dg = p.gate ? rowp_w<E>(p.dg, b, h, t) : nullptr;
+  float dot = 0.0f;
+  for (int c = 0; c < p.d; c += N) {
+    float nv[N], rv[N], gv[N], dv[N], o_dnum[N], o_dg[N];
+    ld_vec<E>(num + c, nv);
+    ld_vec<E>(dy + c, dv);
+    if (res) ld_vec<E>(res + c, rv);
+    if (gg) ld_vec<E>(gg + c, gv);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      float dpre = dv[e];
+      if (gg) {
+        const float ypre = (res ? rv[e] : 0.0f) + scale * nv[e];
+        o_dg[e] = dv[e] * ypre * dsilu(gv[e]);
+        dpre = dv[e] * silu(gv[e]);
+      }
+      o_dnum[e] = scale * dpre;
+      dot += dpre * nv[e];
+      if (dres) dres[c + e] = dpre;
+    }
+    st_vec<E>(dnum + c, o_dnum);
+    if (dg) st_vec<E>(dg + c, o_dg);
+  }
+  if (p.normalize) rowp_w<float>(p.dmass, b, h, t)[0] = -p.s * dot / (denom * denom);
+}
+
+// z_t = a_t z_{t-1} + x_t  over T for every (b, h, feature).
+__global__ __launch_bounds__(256) void wcumsum_kernel(int B, int H, int T, int F, int ret, int reverse,
+                                                      ts_strided x, ts_strided out, const float* log_alpha,
+                                                      ts_strided decay) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)B * H * F) return;
+  const int f = (int)(idx % F);
+  const int h = (int)((idx / F) % H);
+  const int b = (int)(idx / ((int64_t)F * H));
+  const float* xb = (const float*)x.ptr + (int64_t)b * x.sb + (int64_t)h * x.sh + f;
+  float* ob = (float*)out.ptr + (int64_t)b * out.sb + (int64_t)h * out.sh + f;
+  const float a_static = ret == TS_RET_STATIC ? expf(log_alpha[h]) : 1.0f;
+  const float* db = ret == TS_RET_STREAM
+                        ? (const float*)decay.ptr + (int64_t)b * decay.sb + (int64_t)h * decay.sh
+                        : nullptr;
+  float z = 0.0f;
+  for (int s = 0; s < T; ++s) {
+    const int tp = reverse ? T - 1 - s : s;
+    float a = a_static;
+    if (db) {
+      // a_t multiplies the state when stepping into t; anti-causal scans
+      // step from t+1 into t and use the decay of t+1.
+      const int src = reverse ? tp + 1 : tp;
+      a = src < T ? expf(db[(int64_t)src * decay.st]) : 1.0f;
+    }
+    z = (s == 0 ? 0.0f : a * z) + xb[(int64_t)tp * x.st];
+    ob[(int64_t)tp * out.st] = z;
+  }
+}
+
+}  // namespace ts
+
+namespace {
+
+using ts::fail;
+
+int check_read(const ts_read_desc* d) {
+  if (!d) return fail(TS_ERR_VALUE, "read: null descriptor");
+  if (d->B < 1 || d->H < 1 || d->T < 0 || d->d < 1) return fail(TS_ERR_VALUE, "read: bad shape");
+  if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "read: unknown dtype");
+  const int vec = d->dtype == TS_BF16 ? 8 : 4;
+  if (d->d % vec) return fail(TS_ERR_VALUE, "read: width %d is not a multiple of 16 bytes", d->d);
+  return TS_OK;
+}
+
+void fill_read(const ts_read_desc* d, ts::ReadP& p) {
+  memset(&p, 0, sizeof(p));
+  p.B = d->B; p.H = d->H; p.T = d->T; p.d = d->d;
+  p.normalize = d->normalize; p.gate = d->gate; p.s = d->scale; p.eps = d->eps;
+}
+
+int finish(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ts_read_fwd(const ts_read_desc* d, const ts_read_io* io, hipStream_t stream) {
+  int rc = check_read(d);
+  if (rc) return rc;
+  if (!io || !io->num.ptr || !io->y.ptr) return fail(TS_ERR_VALUE, "read: missing tensors");
+  if (d->normalize && !io->mass.ptr) return fail(TS_ERR_VALUE, "read: missing mass");
+  if (d->gate && !io->g.ptr) return fail(TS_ERR_VALUE, "read: missing gate");
+  const int64_t rows = (int64_t)d->B * d->H * d->T;
+  if (rows == 0) return TS_OK;
+  ts::ReadP p;
+  fill_read(d, p);
+  p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.y = io->y;
+  const dim3 grid((unsigned)((rows + 255) / 256));
+  if (d->dtype == TS_BF16)
+    hipLaunchKernelGGL(ts::read_fwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(ts::read_fwd_kernel<float>, grid, dim3(256), 0, stream, p);
+  return finish("read");
+}
+
+int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t stream) {
+  int rc = check_read(d);
+  if (rc) return rc;
+  if (!io || !io->num.ptr || !io->dy.ptr || !io->dnum.ptr) return fail(TS_ERR_VALUE, "read bwd: missing tensors");
+  if (d->normalize && (!io->mass.ptr || !io->dmass.ptr)) return fail(TS_ERR_VALUE, "read bwd: missing mass");
+  if (d->gate && (!io->g.ptr || !io->dg.ptr)) return fail(TS_ERR_VALUE, "read bwd: missing gate");
+  const int64_t rows = (int64_t)d->B * d->H * d->T;
+  if (rows == 0) return TS_OK;
+  ts::ReadP p;
+  fill_read(d, p);
+  p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.dy = io->dy;
+  p.dnum = io->dnum; p.dmass = io->dmass; p.dresid = io->dresid; p.dg = io->dg;
+  const dim3 grid((unsigned)((rows + 255) / 256));
+  if (d->dtype == TS_BF16)
+    hipLaunchKernelGGL(ts::read_bwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(ts::read_bwd_kernel<float>, grid, dim3(256), 0, stream, p);
+  return finish("read bwd");
+}
+
+int ts_wcumsum(const ts_wcumsum_desc* d, ts_strided x, ts_strided out, const float* log_alpha,
+               ts_strided decay, hipStream_t stream) {
+  if (!d || d->B < 1 || d->H < 1 || d->T < 0 || d->F < 1) return fail(TS_ERR_VALUE, "wcumsum: bad shape");
+  if (!x.ptr || !out.ptr) return fail(TS_ERR_VALUE, "wcumsum: missing tensors");
+  if (d->retention == TS_RET_STATIC && !log_alpha) return fail(TS_ERR_VALUE, "wcumsum: missing log_alpha");
+  if (d->retention == TS_RET_STREAM && !decay.ptr) return fail(TS_ERR_VALUE, "wcumsum: missing decay");
+  const int64_t n = (int64_t)d->B * d->H * d->F;
+  if (d->T == 0) return TS_OK;
+  hipLaunchKernelGGL(ts::wcumsum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, d->B, d->H, d->T,
+                     d->F, d->retention, d->reverse, x, out, log_alpha, decay);
+  return finish("wcumsum");
+}
+
+}  // extern "C"

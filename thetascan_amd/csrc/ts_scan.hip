@@ -62,61 +62,6 @@ struct ScanP {
   int nsum;       // segments that run the summary kernel
 };
 
-// ---------------------------------------------------------------- LDS loads
-template <typename E> struct LdsIO;
-template <> struct LdsIO<bf16> {
-  static __device__ __forceinline__ bf16x8 ld8(const bf16* p) {
-    uint4 r = *(const uint4*)p;
-    return __builtin_bit_cast(bf16x8, r);
-  }
-  static __device__ __forceinline__ bf16x4 ld4(const bf16* p) {
-    uint2 r = *(const uint2*)p;
-    return __builtin_bit_cast(bf16x4, r);
-  }
-  static __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
-  static __device__ __forceinline__ bf16x8 from_acc(floatx4 a, floatx4 b) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      r[i] = (bf16)a[i];
-      r[4 + i] = (bf16)b[i];
-    }
-    return r;
-  }
-  static __device__ __forceinline__ bf16x4 from_acc4(floatx4 a) {
-    bf16x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = (bf16)a[i];
-    return r;
-  }
-  static __device__ __forceinline__ void st4(bf16* p, float a0, float a1, float a2, float a3) {
-    bf16x4 r;
-    r[0] = (bf16)a0; r[1] = (bf16)a1; r[2] = (bf16)a2; r[3] = (bf16)a3;
-    *(uint2*)p = __builtin_bit_cast(uint2, r);
-  }
-};
-template <> struct LdsIO<float> {
-  static __device__ __forceinline__ floatx8 ld8(const float* p) {
-    floatx4 a = *(const floatx4*)p;
-    floatx4 b = *(const floatx4*)(p + 4);
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
-  static __device__ __forceinline__ floatx4 ld4(const float* p) { return *(const floatx4*)p; }
-  static __device__ __forceinline__ floatx8 cat(floatx4 a, floatx4 b) {
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
-  static __device__ __forceinline__ floatx8 from_acc(floatx4 a, floatx4 b) {
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
-  static __device__ __forceinline__ floatx4 from_acc4(floatx4 a) { return a; }
-  static __device__ __forceinline__ void st4(float* p, float a0, float a1, float a2, float a3) {
-    floatx4 r = {a0, a1, a2, a3};
-    *(floatx4*)p = r;
-  }
-};
-
 __device__ __forceinline__ int phys_t(const ScanP& p, int t) { return p.reverse ? p.T - 1 - t : t; }
 
 // Load a [C, wpad] tile of rows t0..t0+63 (zero padded past T and past
@@ -417,7 +362,7 @@ __global__ void scan_prefix_kernel(float* seg, const float* segdec, float* final
 }  // namespace ts
 
 // ============================================================== host side
-namespace {
+namespace ts {
 
 thread_local char g_err[512] = "";
 
@@ -428,6 +373,12 @@ int fail(int code, const char* fmt, ...) {
   va_end(ap);
   return code;
 }
+
+}  // namespace ts
+
+namespace {
+
+using ts::fail;
 
 const int kDkPads[] = {32, 64, 80, 128, 144};
 
@@ -531,7 +482,7 @@ extern "C" {
 
 int ts_abi_version(void) { return TS_ABI_VERSION; }
 
-const char* ts_last_error(void) { return g_err; }
+const char* ts_last_error(void) { return ts::g_err; }
 
 int ts_scan_layout(const ts_scan_desc* desc, int32_t* dk_pad, int32_t* dv_pad, int32_t* n_segments) {
   Layout L;

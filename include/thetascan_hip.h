@@ -124,8 +124,8 @@ typedef struct ts_feature_desc {
   int32_t m;            /* feature width (16..256, multiple of 16)             */
   int32_t dtype;        /* ts_dtype of x, weights and bf16/fp32 outputs        */
   int32_t kind;         /* ts_feature_kind                                      */
-  int32_t in_rot;       /* input-RoPE rotated channels of x (0 = none)         */
-  int32_t feat_rot;     /* feature-RoPE rotated channels of phi (0 = none)     */
+  int32_t in_rot;       /* input-RoPE rotated channels of x (0 or 4k <= d)     */
+  int32_t feat_rot;     /* feature-RoPE rotated channels of phi (0 or 4k <= m) */
   int32_t has_tau;      /* relu2: subtract the per-head threshold tau[H]       */
   float gain;           /* softmax: logit gain                                 */
   float resid_scale;    /* s = 1/sqrt(depth) of the residual read              */
@@ -165,8 +165,8 @@ typedef struct ts_feature_bwd_io {
   const float* in_sin;
   const float* f_cos;
   const float* f_sin;
-  ts_strided dphi;                 /* fp32 [B,H,T,m]: grad of phi              */
-  ts_strided dresid;               /* fp32 [B,H,T,d]: grad of resid (or NULL)  */
+  ts_strided dphi;                 /* [B,H,T,m]: grad of phi                   */
+  ts_strided dresid;               /* [B,H,T,d]: grad of resid (or NULL)       */
   ts_strided dx;                   /* out [B,H,T,d]: grad of x                 */
   ts_strided da;                   /* out [B,H,T,m]: grad of a = W1 xn (NULL ok) */
   ts_strided xn;                   /* out [B,H,T,d]: xn (NULL ok)              */
@@ -207,7 +207,7 @@ typedef struct ts_read_bwd_io {
   ts_strided dy;                   /* grad of y                                */
   ts_strided dnum;                 /* out [B,H,T,d] (desc dtype)               */
   ts_strided dmass;                /* out fp32 [B,H,T] (normalize)             */
-  ts_strided dresid;               /* out fp32 [B,H,T,d]                       */
+  ts_strided dresid;               /* out [B,H,T,d] (desc dtype; NULL ok)      */
   ts_strided dg;                   /* out [B,H,T,d] (gate)                     */
 } ts_read_bwd_io;
 

@@ -256,8 +256,9 @@ class View:
     "stale" (plain - fast), "null" (zero memory).  interface.py:198-327.
     """
 
-    def __init__(self, kind, decay=None, log_alpha=None):
+    def __init__(self, kind, decay=None, log_alpha=None, scan=scans.linattn_naive):
         self.kind, self.decay, self.log_alpha = kind, decay, log_alpha
+        self.linattn = scan
 
     def terms(self):
         if self.kind == "null":
@@ -274,7 +275,7 @@ class View:
         for coef, ret in self.terms():
             if ret is not None and ret.ndim == 1:
                 ret = scans.as_stream(ret, q)
-            out = out + coef * scans.linattn_naive(q, k, v, ret)
+            out = out + coef * self.linattn(q, k, v, ret)
         return out
 
     def mass_cum(self, keys):
@@ -528,8 +529,16 @@ def project(c, params, x):
     return q, k, v
 
 
-def forward(c, params, x):
-    """ThetaScan forward x[B,T,D] -> y[B,T,D] (block.py:573-724), scans via the naive loop."""
+SCANS = {"naive": scans.linattn_naive, "quad": scans.linattn_quad, "cumsum": scans.linattn_cumsum}
+
+
+def forward(c, params, x, backend: str = "naive"):
+    """ThetaScan forward x[B,T,D] -> y[B,T,D] (block.py:573-724).
+
+    ``backend`` picks the oracle scan: the naive loop (parity target), the
+    quadratic form, or the prefix-sum form (the CPU baseline algorithm).
+    """
+    scan = SCANS[backend]
     B, T, _ = x.shape
     H, d = c["n_heads"], c["head_dim"]
     q, k, v = project(c, params, x)
@@ -557,7 +566,7 @@ def forward(c, params, x):
     def read(view):
         return read_view(weights, c, q, streams, view, hrot, ctl)
 
-    y = read(View("plain", decay=decay))
+    y = read(View("plain", decay=decay, scan=scan))
     if c["read_fade"]:
         raw = params["fade_alpha"]
         eta = params["fade_eta"]
@@ -570,14 +579,14 @@ def forward(c, params, x):
             out = base
             for j in range(c["fade_branches"]):
                 la = -F.softplus(-raw[j])
-                out = out + eta[j].view(1, -1, 1, 1) * (read(View("fast", log_alpha=la)) - base)
+                out = out + eta[j].view(1, -1, 1, 1) * (read(View("fast", log_alpha=la, scan=scan)) - base)
             y = out
         else:
-            null = read(View("null"))
+            null = read(View("null", scan=scan))
             out = base
             for j in range(c["fade_branches"]):
                 la = -F.softplus(-raw[j])
-                stale = read(View("stale", decay=None, log_alpha=la))
+                stale = read(View("stale", decay=None, log_alpha=la, scan=scan))
                 out = out - eta[j].view(1, -1, 1, 1) * (stale - null)
             y = out
     if c["out_gate"]:

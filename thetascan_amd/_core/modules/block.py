@@ -24,6 +24,7 @@ import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
 from ..ops import engine, fused
+from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
 from .norms import l2norm
@@ -348,6 +349,10 @@ class ThetaScan(nn.Module):
             return False
         if cfg.head_dim not in FUSED_HEAD_DIMS or cfg.mem_hidden % 16 or cfg.mem_hidden > 256:
             return False
+        rot_in = rotated_width(cfg.head_dim, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
+        rot_feat = rotated_width(cfg.mem_hidden, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
+        if rot_in % 4 or rot_feat % 4:
+            return False
         if cfg.kernel_kind == "relu2_ridge":
             return self.kernel_score_bias is None
         if cfg.kernel_kind == "softmax_partition":
@@ -359,16 +364,18 @@ class ThetaScan(nn.Module):
         cfg = self.cfg
         B, T, _ = x.shape
         H, d, m = cfg.n_heads, cfg.head_dim, cfg.mem_hidden
-        qkv = F.linear(x, self.proj_qkv.weight).view(B, T, 3, H, d)
+        qkv = linear(x, self.proj_qkv.weight).view(B, T, 3, H, d)
         in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
         feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
         kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
         spec = fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot, cfg.rope_base,
                                  1.0 / math.sqrt(cfg.depth), cfg.eps)
         (W1, W2, _), = self._weights()
-        g = self.ogate.preactivation(x) if self.ogate is not None else None
+        g = None
+        if self.ogate is not None:
+            g = linear(x, self.ogate.g.lin.weight, self.ogate.g.lin.bias)
         y = fused.kernel_memory(qkv, W1, W2, self.kernel_relu2_threshold, g, spec, cfg.read_norm)
-        return F.linear(y, self.proj_out.weight)
+        return linear(y, self.proj_out.weight)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         cfg = self.cfg

@@ -22,6 +22,7 @@ import torch
 
 from ... import _lib
 from . import scan_hip
+from .linear import split_k_outer
 
 
 def _rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -82,22 +83,35 @@ def feature_fwd(spec: FeatureSpec, x, w1, w2, tau, want_resid: bool):
     return phi, resid
 
 
+def _head_major(B, H, T, w, dtype, device):
+    """[B,H,T,w] view of a head-major [H,B*T,w] buffer (GEMM-ready for weight grads)."""
+    buf = torch.empty(H, B, T, w, dtype=dtype, device=device)
+    return buf.transpose(0, 1), buf.view(H, B * T, w)
+
+
 def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_weights=True):
-    """Returns (da, xn, h, dtau_tok); dx is written in place."""
+    """Backward of one stream; dx is written in place.
+
+    Returns head-major ``[H, B*T, .]`` tiles ``(da, xn, h)`` for the weight
+    gradients (None when not wanted) and the per-token threshold gradient.
+    """
     lib = _lib.load()
     B, H, T, d = x.shape
     m = spec.m
     w1t = w1.transpose(1, 2).contiguous()
     w2t = w2.transpose(1, 2).contiguous() if (dresid is not None) else None
-    da = torch.empty(B, H, T, m, dtype=x.dtype, device=x.device) if want_weights else None
-    xn = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device) if want_weights else None
-    h = torch.empty(B, H, T, m, dtype=x.dtype, device=x.device) if (want_weights and dresid is not None) else None
+    da = xn = h = da_v = xn_v = h_v = None
+    if want_weights:
+        da_v, da = _head_major(B, H, T, m, x.dtype, x.device)
+        xn_v, xn = _head_major(B, H, T, d, x.dtype, x.device)
+        if dresid is not None:
+            h_v, h = _head_major(B, H, T, m, x.dtype, x.device)
     dtau = torch.empty(B, H, T, dtype=torch.float32, device=x.device) if tau is not None else None
     ic, is_, fc, fs = spec.tables(T, x.device)
     io = _lib.FeatureBwdIO(
         _lib.strided(x), _lib.ptr(w1), _lib.ptr(w1t), _lib.ptr(w2t), _lib.ptr(tau), _lib.ptr(ic),
         _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(dphi), _lib.strided(dresid),
-        _lib.strided(dx), _lib.strided(da), _lib.strided(xn), _lib.strided(h), _lib.strided(dtau),
+        _lib.strided(dx), _lib.strided(da_v), _lib.strided(xn_v), _lib.strided(h_v), _lib.strided(dtau),
     )
     desc = spec.desc(x, tau is not None)
     _lib.check(lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device)),
@@ -122,7 +136,7 @@ def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6):
     B, H, T, d = num.shape
     dnum = torch.empty_like(num)
     dmass = torch.empty(B, H, T, dtype=torch.float32, device=num.device) if mass is not None else None
-    dresid = torch.empty(B, H, T, d, dtype=torch.float32, device=num.device)
+    dresid, dresid_hm = _head_major(B, H, T, d, num.dtype, num.device)
     dg = torch.empty(B, T, H, d, dtype=num.dtype, device=num.device).transpose(1, 2) if g is not None else None
     desc = _lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None), int(g is not None),
                          float(scale), float(eps))
@@ -131,7 +145,7 @@ def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6):
                         _lib.strided(dg))
     _lib.check(lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device)),
                "ts_read_bwd")
-    return dnum, dmass, dresid, dg
+    return dnum, dmass, (dresid, dresid_hm), dg
 
 
 def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Tensor:
@@ -163,12 +177,8 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
 
 
 def _weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """sum_{b,t} a[b,h,t,:]^T b[b,h,t,:] -> [H, A, B] (a plain batched GEMM)."""
-    B, H, T, A = a.shape
-    Bw = b.shape[-1]
-    a2 = a.permute(1, 3, 0, 2).reshape(H, A, B * T)
-    b2 = b.permute(1, 0, 2, 3).reshape(H, B * T, Bw)
-    return torch.bmm(a2.float(), b2.float())
+    """sum_n a[h,n,:]^T b[h,n,:] -> fp32 [H, A, B] for head-major tiles (split-K GEMM)."""
+    return split_k_outer(a, b)
 
 
 class _KernelMemory(torch.autograd.Function):
@@ -211,13 +221,13 @@ class _KernelMemory(torch.autograd.Function):
         v = qkv[:, :, 2].transpose(1, 2)
         dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
         gv = None if g is None else g.view(B, T, H, d).transpose(1, 2)
-        dnum, dmass, dresid, dg = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps)
+        dnum, dmass, (dresid, dresid_hm), dg = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps)
         norm = ctx.normalize
         q_ext = dmass if norm else None
         dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
-                                            out_mode=_lib.OUT_STORE_F32, seg_chunks=ctx.seg_chunks)
+                                            seg_chunks=ctx.seg_chunks)
         dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
-                                            k_ext=q_ext, out_mode=_lib.OUT_STORE_F32, seg_chunks=ctx.seg_chunks)
+                                            k_ext=q_ext, seg_chunks=ctx.seg_chunks)
         dqkv = torch.empty_like(qkv)
         dq = dqkv[:, :, 0].transpose(1, 2)
         dk = dqkv[:, :, 1].transpose(1, 2)
@@ -232,7 +242,7 @@ class _KernelMemory(torch.autograd.Function):
         if need_w1:
             dw1 = (_weight_grad(da_k, xn_k) + _weight_grad(da_q, xn_q)).to(ctx.w_dtypes[0])
         if need_w2:
-            dw2 = (_weight_grad(dresid, h_q) * spec.resid_scale).to(ctx.w_dtypes[1])
+            dw2 = (_weight_grad(dresid_hm, h_q) * spec.resid_scale).to(ctx.w_dtypes[1])
         if ctx.has_tau and ctx.needs_input_grad[3]:
             dtau = (dtau_k.sum(dim=(0, 2)) + dtau_q.sum(dim=(0, 2))).to(ctx.tau_dtype)
         dgo = None

@@ -1,6 +1,5 @@
 // Read epilogue (normalised read + residual + output gate) and decayed
-// prefix sums for gfx950.  Both are HBM-bound streaming kernels: one thread
-// owns one (batch, head, token) row and walks it in 16-byte vectors.
+// prefix sums for gfx950.  Both are HBM-bound streaming kernels.
 
 #include "ts_common.h"
 #include "thetascan_hip.h"
@@ -45,78 +44,96 @@ __device__ __forceinline__ void st_vec(E* p, const float* in) {
   *(uint4*)p = v.raw;
 }
 
+// Work mapping of the read kernels: a row (one (b, h, t)) is split into
+// 16-byte chunks; `p2` consecutive lanes (a power of two >= chunks per row)
+// own one row, so every load and store instruction covers whole contiguous
+// row segments, and a row reduction is a log2(p2)-step butterfly.
+struct RowMap {
+  int64_t row;
+  int chunk;
+  bool active;
+};
+
+__device__ __forceinline__ RowMap row_map(int64_t nrows, int nchunk, int p2) {
+  const int64_t gtid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  RowMap r;
+  r.row = gtid / p2;
+  r.chunk = (int)(gtid % p2);
+  r.active = r.row < nrows && r.chunk < nchunk;
+  return r;
+}
+
+__device__ __forceinline__ float row_sum(float v, int p2) {
+  for (int o = 1; o < p2; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 // y = (resid + s * num / (mass + eps)) * silu(g)     (engine.py:440-442, 526-528; gates.py:34-40)
 template <typename E>
-__global__ __launch_bounds__(256) void read_fwd_kernel(ReadP p) {
+__global__ __launch_bounds__(256) void read_fwd_kernel(ReadP p, int p2) {
   constexpr int N = Vec16<E>::N;
-  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t nrows = (int64_t)p.B * p.H * p.T;
-  if (row >= nrows) return;
-  const int t = (int)(row % p.T);
-  const int h = (int)((row / p.T) % p.H);
-  const int b = (int)(row / ((int64_t)p.T * p.H));
+  const RowMap rm = row_map(nrows, p.d / N, p2);
+  if (!rm.active) return;
+  const int t = (int)(rm.row % p.T);
+  const int h = (int)((rm.row / p.T) % p.H);
+  const int b = (int)(rm.row / ((int64_t)p.T * p.H));
+  const int c = rm.chunk * N;
   float scale = p.s;
   if (p.normalize) scale = p.s / (rowp<float>(p.mass, b, h, t)[0] + p.eps);
-  const E* num = rowp<E>(p.num, b, h, t);
-  const E* res = p.resid.ptr ? rowp<E>(p.resid, b, h, t) : nullptr;
-  const E* gg = p.gate ? rowp<E>(p.g, b, h, t) : nullptr;
-  E* y = rowp_w<E>(p.y, b, h, t);
-  for (int c = 0; c < p.d; c += N) {
-    float nv[N], rv[N], gv[N], out[N];
-    ld_vec<E>(num + c, nv);
-    if (res) ld_vec<E>(res + c, rv);
-    if (gg) ld_vec<E>(gg + c, gv);
+  float nv[N], rv[N], gv[N], out[N];
+  ld_vec<E>(rowp<E>(p.num, b, h, t) + c, nv);
+  if (p.resid.ptr) ld_vec<E>(rowp<E>(p.resid, b, h, t) + c, rv);
+  if (p.gate) ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-      float v = (res ? rv[e] : 0.0f) + scale * nv[e];
-      out[e] = gg ? v * silu(gv[e]) : v;
-    }
-    st_vec<E>(y + c, out);
+  for (int e = 0; e < N; ++e) {
+    const float v = (p.resid.ptr ? rv[e] : 0.0f) + scale * nv[e];
+    out[e] = p.gate ? v * silu(gv[e]) : v;
   }
+  st_vec<E>(rowp_w<E>(p.y, b, h, t) + c, out);
 }
 
 template <typename E>
-__global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p) {
+__global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p, int p2) {
   constexpr int N = Vec16<E>::N;
-  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t nrows = (int64_t)p.B * p.H * p.T;
-  if (row >= nrows) return;
+  const RowMap rm = row_map(nrows, p.d / N, p2);
+  // inactive lanes still take part in the row butterfly with zeros
+  const int64_t row = rm.row < nrows ? rm.row : nrows - 1;
   const int t = (int)(row % p.T);
   const int h = (int)((row / p.T) % p.H);
   const int b = (int)(row / ((int64_t)p.T * p.H));
+  const int c = rm.chunk * N;
   float denom = 1.0f;
   if (p.normalize) denom = rowp<float>(p.mass, b, h, t)[0] + p.eps;
   const float scale = p.s / denom;
-  const E* num = rowp<E>(p.num, b, h, t);
-  const E* res = p.resid.ptr ? rowp<E>(p.resid, b, h, t) : nullptr;
-  const E* gg = p.gate ? rowp<E>(p.g, b, h, t) : nullptr;
-  const E* dy = rowp<E>(p.dy, b, h, t);
-  E* dnum = rowp_w<E>(p.dnum, b, h, t);
-  float* dres = p.dresid.ptr ? rowp_w<float>(p.dresid, b, h, t) : nullptr;
-  E* dg = p.gate ? rowp_w<E>(p.dg, b, h, t) : nullptr;
   float dot = 0.0f;
-  for (int c = 0; c < p.d; c += N) {
-    float nv[N], rv[N], gv[N], dv[N], o_dnum[N], o_dg[N];
-    ld_vec<E>(num + c, nv);
-    ld_vec<E>(dy + c, dv);
-    if (res) ld_vec<E>(res + c, rv);
-    if (gg) ld_vec<E>(gg + c, gv);
+  if (rm.active) {
+    float nv[N], rv[N], gv[N], dv[N], o_dnum[N], o_dg[N], o_dres[N];
+    ld_vec<E>(rowp<E>(p.num, b, h, t) + c, nv);
+    ld_vec<E>(rowp<E>(p.dy, b, h, t) + c, dv);
+    if (p.resid.ptr) ld_vec<E>(rowp<E>(p.resid, b, h, t) + c, rv);
+    if (p.gate) ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
 #pragma unroll
     for (int e = 0; e < N; ++e) {
       float dpre = dv[e];
-      if (gg) {
-        const float ypre = (res ? rv[e] : 0.0f) + scale * nv[e];
+      if (p.gate) {
+        const float ypre = (p.resid.ptr ? rv[e] : 0.0f) + scale * nv[e];
         o_dg[e] = dv[e] * ypre * dsilu(gv[e]);
         dpre = dv[e] * silu(gv[e]);
       }
       o_dnum[e] = scale * dpre;
+      o_dres[e] = dpre;
       dot += dpre * nv[e];
-      if (dres) dres[c + e] = dpre;
     }
-    st_vec<E>(dnum + c, o_dnum);
-    if (dg) st_vec<E>(dg + c, o_dg);
+    st_vec<E>(rowp_w<E>(p.dnum, b, h, t) + c, o_dnum);
+    if (p.dresid.ptr) st_vec<E>(rowp_w<E>(p.dresid, b, h, t) + c, o_dres);
+    if (p.gate) st_vec<E>(rowp_w<E>(p.dg, b, h, t) + c, o_dg);
   }
-  if (p.normalize) rowp_w<float>(p.dmass, b, h, t)[0] = -p.s * dot / (denom * denom);
+  if (p.normalize) {
+    dot = row_sum(dot, p2);
+    if (rm.active && rm.chunk == 0) rowp_w<float>(p.dmass, b, h, t)[0] = -p.s * dot / (denom * denom);
+  }
 }
 
 // z_t = a_t z_{t-1} + x_t  over T for every (b, h, feature).
@@ -161,7 +178,16 @@ int check_read(const ts_read_desc* d) {
   if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "read: unknown dtype");
   const int vec = d->dtype == TS_BF16 ? 8 : 4;
   if (d->d % vec) return fail(TS_ERR_VALUE, "read: width %d is not a multiple of 16 bytes", d->d);
+  if (d->d / vec > 64) return fail(TS_ERR_NOT_IMPLEMENTED, "read: width %d is too wide", d->d);
   return TS_OK;
+}
+
+// Lanes per row: chunks of 16 bytes rounded up to a power of two (<= 64).
+int lanes_per_row(const ts_read_desc* d) {
+  const int chunks = d->d / (d->dtype == TS_BF16 ? 8 : 4);
+  int p2 = 1;
+  while (p2 < chunks) p2 <<= 1;
+  return p2;
 }
 
 void fill_read(const ts_read_desc* d, ts::ReadP& p) {
@@ -191,11 +217,12 @@ int ts_read_fwd(const ts_read_desc* d, const ts_read_io* io, hipStream_t stream)
   ts::ReadP p;
   fill_read(d, p);
   p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.y = io->y;
-  const dim3 grid((unsigned)((rows + 255) / 256));
+  const int p2 = lanes_per_row(d);
+  const dim3 grid((unsigned)((rows * p2 + 255) / 256));
   if (d->dtype == TS_BF16)
-    hipLaunchKernelGGL(ts::read_fwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(ts::read_fwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p, p2);
   else
-    hipLaunchKernelGGL(ts::read_fwd_kernel<float>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(ts::read_fwd_kernel<float>, grid, dim3(256), 0, stream, p, p2);
   return finish("read");
 }
 
@@ -211,11 +238,12 @@ int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t str
   fill_read(d, p);
   p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.dy = io->dy;
   p.dnum = io->dnum; p.dmass = io->dmass; p.dresid = io->dresid; p.dg = io->dg;
-  const dim3 grid((unsigned)((rows + 255) / 256));
+  const int p2 = lanes_per_row(d);
+  const dim3 grid((unsigned)((rows * p2 + 255) / 256));
   if (d->dtype == TS_BF16)
-    hipLaunchKernelGGL(ts::read_bwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(ts::read_bwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p, p2);
   else
-    hipLaunchKernelGGL(ts::read_bwd_kernel<float>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(ts::read_bwd_kernel<float>, grid, dim3(256), 0, stream, p, p2);
   return finish("read bwd");
 }
 

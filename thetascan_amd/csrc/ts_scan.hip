@@ -64,42 +64,6 @@ struct ScanP {
 
 __device__ __forceinline__ int phys_t(const ScanP& p, int t) { return p.reverse ? p.T - 1 - t : t; }
 
-// Load a [C, wpad] tile of rows t0..t0+63 (zero padded past T and past
-// `width`; column `width` carries the optional ext column) into LDS, row-major
-// at `rowdst` and/or transposed at `tdst`.
-template <typename E>
-__device__ __forceinline__ void load_tile(const ScanP& p, const ts_strided& src, int ext_mode,
-                                          const ts_strided& ext, int width, int wpad, int b,
-                                          int h, int t0, E* rowdst, int rpitch, E* tdst,
-                                          int tpitch, int tid, int nthreads) {
-  constexpr int VEC = 16 / (int)sizeof(E);
-  const int nvec = wpad / VEC;
-  const E* base = (const E*)src.ptr + (int64_t)b * src.sb + (int64_t)h * src.sh;
-  for (int idx = tid; idx < C * nvec; idx += nthreads) {
-    const int r = idx / nvec;
-    const int c0 = (idx - r * nvec) * VEC;
-    const int t = t0 + r;
-    Vec16<E> val;
-    val.raw = make_uint4(0u, 0u, 0u, 0u);
-    if (t < p.T) {
-      const int tp = phys_t(p, t);
-      if (c0 < width) {
-        val.raw = *(const uint4*)(base + (int64_t)tp * src.st + c0);
-      } else if (c0 == width && ext_mode != TS_EXT_NONE) {
-        float x = 1.0f;
-        if (ext_mode == TS_EXT_ARRAY)
-          x = ((const float*)ext.ptr)[(int64_t)b * ext.sb + (int64_t)h * ext.sh + (int64_t)tp * ext.st];
-        val.e[0] = cvt<E>(x);
-      }
-    }
-    if (rowdst) *(uint4*)(rowdst + r * rpitch + c0) = val.raw;
-    if (tdst) {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) tdst[(c0 + e) * tpitch + r] = val.e[e];
-    }
-  }
-}
-
 // Per-tile retention tables (wave 0).  Matches scan_chunk._static_weights
 // (scan_chunk.py:102-119) and _tile_weights (scan_chunk.py:122-155): phases
 // are formed in fp32, exponents of the intra-tile weight are clamped to <= 0.
@@ -143,21 +107,164 @@ __device__ __forceinline__ void tile_decay(const ScanP& p, int b, int h, int t0,
   }
 }
 
-template <typename E, int DKP, bool MAIN>
-__global__ __launch_bounds__(1024) void scan_kernel(ScanP p) {
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
+
+// Staging of the K / V tiles and access to their transposed fragments.
+//
+// bf16: tiles stay row-major in LDS ([token][feature], 16-byte writes) and
+// the token-contiguous fragments that the key-axis contractions need are read
+// with the gfx950 LDS transpose read (ds_read_b64_tr_b16).  Within each group
+// of 16 lanes, lane j addresses row key0 + j/4, column c0 + 4*(j%4); lane i
+// then receives M[key0 .. key0+3][c0 + i], i.e. one column and four
+// consecutive tokens -- an MFMA operand fragment.  Two such reads give the
+// eight tokens of a 32-deep contraction.
+//
+// fp32 (the parity path): K and V are additionally stored transposed.
+template <typename E> struct Tiles;
+
+template <> struct Tiles<bf16> {
+  static constexpr bool kTransposedCopy = false;
+  // lane: column c0 + (lane & 15), tokens 32kp + 8*(lane >> 4) + 0..7
+  static __device__ __forceinline__ bf16x8 tcol8(const bf16* rows, int pitch, int c0, int kp, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const bf16* a = rows + (32 * kp + 8 * g + (j >> 2)) * pitch + c0 + 4 * (j & 3);
+    shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)a);
+    shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(a + 4 * pitch));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
+template <> struct Tiles<float> {
+  static constexpr bool kTransposedCopy = true;
+  // rows here is the transposed copy [feature][token]
+  static __device__ __forceinline__ floatx8 tcol8(const float* cols, int pitch, int c0, int kp, int lane) {
+    const int g = lane >> 4, l16 = lane & 15;
+    return LdsIO<float>::ld8(cols + (c0 + l16) * pitch + 32 * kp + 8 * g);
+  }
+};
+
+// Register-staged tile loader.  Each thread owns MAXV 16-byte vectors of the
+// next tile (Q rows for MAIN, then K rows, then V rows).  Vector counts per
+// tensor are multiples of 64, so the tensor a vector belongs to is uniform
+// across a wave; everything that does not change from tile to tile (tensor,
+// row, column, ext role, base pointer) is resolved once before the tile loop,
+// and a tile only adds its time offset.  The fetch for tile c+1 is issued
+// before tile c is computed, so its latency hides behind the MFMA work.
+struct LoadSlot {
+  const char* base;   // (b, h) row 0 of the tensor, plus the column offset
+  const float* ext;   // (b, h) base of the ext column array (or null)
+  int64_t st;         // row stride in bytes
+  int ext_st;         // row stride of the ext array (elements)
+  int row;            // row inside the tile
+  int kind;           // 0 data, 1 ext column (ones), 2 ext column (array), 3 zero padding
+  int tensor;         // 0 Q, 1 K, 2 V, -1 idle
+  int off;            // element offset of the vector inside its LDS row
+};
+
+template <typename E, int DKP, bool MAIN, int MAXV>
+struct Loader {
+  static constexpr int VEC = 16 / (int)sizeof(E);
+  uint4 r[MAXV];
+  LoadSlot sl[MAXV];
+
+  __device__ __forceinline__ void setup(const ScanP& p, int b, int h, int dvp, int tid, int nt) {
+    const int nq = MAIN ? C * (DKP / VEC) : 0;
+    const int nk = C * (DKP / VEC);
+    const int nv = C * (dvp / VEC);
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      LoadSlot& L = sl[i];
+      int idx = tid + i * nt;
+      int per_row, width, ext_mode;
+      const ts_strided* src;
+      const ts_strided* ext;
+      if (idx < nq) {
+        L.tensor = 0; per_row = DKP / VEC; width = p.dk; ext_mode = p.q_ext; src = &p.q; ext = &p.qe;
+      } else if ((idx -= nq) < nk) {
+        L.tensor = 1; per_row = DKP / VEC; width = p.dk; ext_mode = p.k_ext; src = &p.k; ext = &p.ke;
+      } else if ((idx -= nk) < nv) {
+        L.tensor = 2; per_row = dvp / VEC; width = p.dv; ext_mode = p.v_ext; src = &p.v; ext = &p.ve;
+      } else {
+        L.tensor = -1; per_row = 1; width = 0; ext_mode = 0; src = &p.v; ext = &p.ve;
+      }
+      L.row = idx / per_row;
+      const int c0 = (idx - L.row * per_row) * VEC;
+      L.off = c0;
+      L.kind = c0 < width ? 0 : (c0 == width && ext_mode != TS_EXT_NONE ? ext_mode : 3);
+      L.base = (const char*)src->ptr + ((int64_t)b * src->sb + (int64_t)h * src->sh + c0) * (int64_t)sizeof(E);
+      L.st = src->st * (int64_t)sizeof(E);
+      L.ext = ext->ptr ? (const float*)ext->ptr + (int64_t)b * ext->sb + (int64_t)h * ext->sh : nullptr;
+      L.ext_st = (int)ext->st;
+    }
+  }
+
+  __device__ __forceinline__ void fetch(const ScanP& p, int t0) {
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      const LoadSlot& L = sl[i];
+      const int t = t0 + L.row;
+      const int tp = p.reverse ? p.T - 1 - t : t;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (L.tensor >= 0 && t < p.T) {
+        if (L.kind == 0) {
+          v = *(const uint4*)(L.base + (int64_t)tp * L.st);
+        } else if (L.kind != 3) {
+          Vec16<E> e;
+          e.raw = v;
+          e.e[0] = cvt<E>(L.kind == TS_EXT_ARRAY ? L.ext[(int64_t)tp * L.ext_st] : 1.0f);
+          v = e.raw;
+        }
+      }
+      r[i] = v;
+    }
+  }
+
+  __device__ __forceinline__ void store(E* Qs, E* Ks, E* Vs, E* KTs, E* VTs, int qp, int vp, int tp) {
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      const LoadSlot& L = sl[i];
+      Vec16<E> val;
+      val.raw = r[i];
+      if (L.tensor == 0) {
+        *(uint4*)(Qs + L.row * qp + L.off) = val.raw;
+      } else if (L.tensor == 1) {
+        *(uint4*)(Ks + L.row * qp + L.off) = val.raw;
+        if (Tiles<E>::kTransposedCopy) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) KTs[(L.off + e) * tp + L.row] = val.e[e];
+        }
+      } else if (L.tensor == 2) {
+        if (Tiles<E>::kTransposedCopy) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) VTs[(L.off + e) * tp + L.row] = val.e[e];
+        } else {
+          *(uint4*)(Vs + L.row * vp + L.off) = val.raw;
+        }
+      }
+    }
+  }
+};
+
+template <typename E, int DKP, bool MAIN, bool WIDE>
+__global__ __launch_bounds__(WIDE ? 576 : 256) void scan_kernel(ScanP p) {
   typedef typename Frag<E>::f8 F8;
-  typedef typename Frag<E>::f4 F4;
   typedef LdsIO<E> IO;
+  typedef Tiles<E> TL;
   constexpr int VEC = 16 / (int)sizeof(E);
   constexpr int QP = DKP + VEC;  // row pitch of Qs / Ks (elements)
-  constexpr int TP = C + VEC;    // row pitch of KTs / VTs / Ps
+  constexpr int TP = C + VEC;    // row pitch of Ps and of transposed copies
   constexpr int NKB = DKP / 16;  // 16-row key-feature blocks of the state
   constexpr int NK32 = DKP / 32; // full 32-wide contraction blocks over dk
   constexpr bool KTAIL = (DKP % 32) != 0;
+  // Worst case of (Q + K + V vectors) / threads with NT = max(256, 4*dvp):
+  // ((MAIN ? 2 : 1) * 64 * DKP + 64 * 64) / VEC / 256.
+  constexpr int MAXV = ((MAIN ? 2 : 1) * DKP + 64 + 4 * VEC - 1) / (4 * VEC);
 
   const int dvp = p.dvp;
-  const int NW = dvp / 16;
-  const int NT = NW * 64;
+  const int NWV = dvp / 16;              // waves that own a value block
+  const int NT = blockDim.x;
+  const int VP = dvp + VEC;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
@@ -167,56 +274,61 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanP p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
+  const bool owner = w < NWV;
+  const int64_t obase = (int64_t)b * p.out.sb + (int64_t)h * p.out.sh;
+  const int64_t oebase = (int64_t)b * p.oe.sb + (int64_t)h * p.oe.sh;
 
   extern __shared__ __align__(16) unsigned char smem[];
   E* Qs = (E*)smem;
   E* Ks = Qs + (MAIN ? C * QP : 0);
-  E* KTs = Ks + (MAIN ? C * QP : 0);
-  E* VTs = KTs + DKP * TP;
-  E* Ps = VTs + dvp * TP;
+  E* Vs = Ks + C * QP;                                   // row-major V (bf16)
+  E* KTs = Vs + (TL::kTransposedCopy ? 0 : C * VP);      // transposed copies (fp32)
+  E* VTs = KTs + (TL::kTransposedCopy ? DKP * TP : 0);
+  E* Ps = VTs + (TL::kTransposedCopy ? dvp * TP : 0);
   float* s_carry = (float*)(Ps + (MAIN ? C * TP : 0));
   float* s_wk = s_carry + C;
   float* s_pw = s_wk + C;
   float* s_lloc = s_pw + C;
   float* s_misc = s_lloc + C;
+  const E* Kt_src = TL::kTransposedCopy ? KTs : Ks;
+  const E* Vt_src = TL::kTransposedCopy ? VTs : Vs;
+  const int kt_pitch = TL::kTransposedCopy ? TP : QP;
+  const int vt_pitch = TL::kTransposedCopy ? TP : VP;
 
   floatx4 S[NKB];
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) S[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
   bool state_zero = true;
-  if (MAIN && seg > 0) {
+  if (MAIN && seg > 0 && owner) {
     const float* src = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)(DKP * dvp);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) S[kb][i] = src[(kb * 16 + 4 * g + i) * dvp + w * 16 + l16];
-    state_zero = false;
   }
+  if (MAIN && seg > 0) state_zero = false;
 
   const int c_begin = seg * p.seg_chunks;
   const int c_end = min(c_begin + p.seg_chunks, p.nchunks);
   float seg_log = 0.0f;
+  Loader<E, DKP, MAIN, MAXV> ld;
+  ld.setup(p, b, h, dvp, tid, NT);
+  ld.fetch(p, c_begin * C);
 
   for (int c = c_begin; c < c_end; ++c) {
     const int t0 = c * C;
     const int len = min(C, p.T - t0);
     __syncthreads();  // LDS of the previous tile is no longer read
+    ld.store(Qs, Ks, Vs, KTs, VTs, QP, VP, TP);
     if (p.ret != TS_RET_NONE && w == 0)
       tile_decay(p, b, h, t0, len, lane, s_carry, s_wk, s_pw, s_lloc, s_misc);
-    if (MAIN) {
-      load_tile<E>(p, p.q, p.q_ext, p.qe, p.dk, DKP, b, h, t0, Qs, QP, nullptr, 0, tid, NT);
-      load_tile<E>(p, p.k, p.k_ext, p.ke, p.dk, DKP, b, h, t0, Ks, QP, KTs, TP, tid, NT);
-    } else {
-      load_tile<E>(p, p.k, p.k_ext, p.ke, p.dk, DKP, b, h, t0, nullptr, 0, KTs, TP, tid, NT);
-    }
-    load_tile<E>(p, p.v, p.v_ext, p.ve, p.dv, dvp, b, h, t0, nullptr, 0, VTs, TP, tid, NT);
     __syncthreads();
+    if (c + 1 < c_end) ld.fetch(p, t0 + C);  // next tile in flight
 
     if (MAIN) {
       // ---- causal score tile P[query][key] = w(q,k) <q, k>, shared via LDS.
-      // 10 lower-triangular 16x16 blocks plus the two upper blocks that the
-      // 32-key contraction of query blocks 0 and 2 reads (written as zero).
-      for (int bi = w; bi < kScoreBlocks; bi += NW) {
+      const int nw_all = NT >> 6;
+      for (int bi = w; bi < kScoreBlocks; bi += nw_all) {
         const int qb = (kBlockQ >> (2 * bi)) & 3;
         const int kb = (kBlockK >> (2 * bi)) & 3;
         const int query = qb * 16 + l16;
@@ -247,97 +359,100 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanP p) {
       __syncthreads();
     }
 
-    // ---- value block of this wave
-    F8 av[2];
+    if (owner) {
+      // ---- value block of this wave
+      F8 av[2];
 #pragma unroll
-    for (int kp = 0; kp < 2; ++kp) av[kp] = IO::ld8(VTs + (w * 16 + l16) * TP + kp * 32 + 8 * g);
+      for (int kp = 0; kp < 2; ++kp) av[kp] = TL::tcol8(Vt_src, vt_pitch, w * 16, kp, lane);
 
-    if (MAIN) {
+      if (MAIN) {
 #pragma unroll
-      for (int qb = 0; qb < 4; ++qb) {
-        const int query = qb * 16 + l16;
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (!state_zero) {
-          const E* qrow = Qs + query * QP;
+        for (int qb = 0; qb < 4; ++qb) {
+          const int query = qb * 16 + l16;
+          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+          if (!state_zero) {
+            const E* qrow = Qs + query * QP;
 #pragma unroll
-          for (int j = 0; j < NK32; ++j)
-            acc = mma32(IO::from_acc(S[2 * j], S[2 * j + 1]),
-                        IO::cat(IO::ld4(qrow + 32 * j + 4 * g), IO::ld4(qrow + 32 * j + 16 + 4 * g)),
-                        acc);
-          if (KTAIL) acc = mma16(IO::from_acc4(S[NKB - 1]), IO::ld4(qrow + NK32 * 32 + 4 * g), acc);
-          if (p.ret != TS_RET_NONE) {
-            const float cw = s_carry[query];
+            for (int j = 0; j < NK32; ++j)
+              acc = mma32(IO::from_acc(S[2 * j], S[2 * j + 1]),
+                          IO::cat(IO::ld4(qrow + 32 * j + 4 * g), IO::ld4(qrow + 32 * j + 16 + 4 * g)), acc);
+            if (KTAIL) acc = mma16(IO::from_acc4(S[NKB - 1]), IO::ld4(qrow + NK32 * 32 + 4 * g), acc);
+            if (p.ret != TS_RET_NONE) {
+              const float cw = s_carry[query];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] *= cw;
-          }
-        }
-#pragma unroll
-        for (int kp = 0; kp <= qb / 2; ++kp)
-          acc = mma32(av[kp], IO::ld8(Ps + query * TP + kp * 32 + 8 * g), acc);
-
-        const int t = t0 + query;
-        if (t < p.T) {
-          const int tp = phys_t(p, t);
-          const int dvb = w * 16 + 4 * g;
-          const int64_t ooff = (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + (int64_t)tp * p.out.st;
-          if (p.out_mode == TS_OUT_STORE) {
-            E* o = (E*)p.out.ptr + ooff + dvb;
-            if (dvb + 4 <= p.dv) {
-              IO::st4(o, acc[0], acc[1], acc[2], acc[3]);
-            } else {
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                if (dvb + i < p.dv) o[i] = cvt<E>(acc[i]);
+              for (int i = 0; i < 4; ++i) acc[i] *= cw;
             }
-          } else {
-            float* o = (float*)p.out.ptr + ooff + dvb;
+          }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              if (dvb + i < p.dv) {
-                const float val = p.out_scale * acc[i];
-                o[i] = p.out_mode == TS_OUT_ACCUM_F32 ? o[i] + val : val;
+          for (int kp = 0; kp <= qb / 2; ++kp)
+            acc = mma32(av[kp], IO::ld8(Ps + query * TP + kp * 32 + 8 * g), acc);
+
+          const int t = t0 + query;
+          if (t < p.T) {
+            const int tp = phys_t(p, t);
+            const int dvb = w * 16 + 4 * g;
+            const int64_t ooff = obase + (int64_t)tp * p.out.st;
+            if (p.out_mode == TS_OUT_STORE) {
+              E* o = (E*)p.out.ptr + ooff + dvb;
+              if (dvb + 4 <= p.dv) {
+                IO::st4(o, acc[0], acc[1], acc[2], acc[3]);
+              } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                  if (dvb + i < p.dv) o[i] = cvt<E>(acc[i]);
+              }
+            } else {
+              float* o = (float*)p.out.ptr + ooff + dvb;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                if (dvb + i < p.dv) {
+                  const float val = p.out_scale * acc[i];
+                  o[i] = p.out_mode == TS_OUT_ACCUM_F32 ? o[i] + val : val;
+                }
               }
             }
-          }
-          if (p.oe.ptr && dvb <= p.dv && p.dv < dvb + 4) {
-            float* oe = (float*)p.oe.ptr + (int64_t)b * p.oe.sb + (int64_t)h * p.oe.sh + (int64_t)tp * p.oe.st;
-            const float val = (p.out_mode == TS_OUT_STORE ? 1.0f : p.out_scale) * acc[p.dv - dvb];
-            *oe = p.out_mode == TS_OUT_ACCUM_F32 ? *oe + val : val;
+            if (p.oe.ptr && dvb <= p.dv && p.dv < dvb + 4) {
+              float* oe = (float*)p.oe.ptr + oebase + (int64_t)tp * p.oe.st;
+              const float val = (p.out_mode == TS_OUT_STORE ? 1.0f : p.out_scale) * acc[p.dv - dvb];
+              *oe = p.out_mode == TS_OUT_ACCUM_F32 ? *oe + val : val;
+            }
           }
         }
       }
-    }
 
-    // ---- state update: S = decay(tile) * S + K_w^T V
-    if (p.ret != TS_RET_NONE) {
-      const float cdec = expf(s_misc[0]);
+      // ---- state update: S = decay(tile) * S + K_w^T V
+      if (p.ret != TS_RET_NONE) {
+        const float cdec = expf(s_misc[0]);
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S[kb][i] *= cdec;
-      if (tid == 0) seg_log += s_misc[0];
-    }
+          for (int i = 0; i < 4; ++i) S[kb][i] *= cdec;
+      }
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
+      for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-      for (int kp = 0; kp < 2; ++kp) {
-        F8 ak = IO::ld8(KTs + (kb * 16 + l16) * TP + kp * 32 + 8 * g);
-        if (p.ret != TS_RET_NONE) {
+        for (int kp = 0; kp < 2; ++kp) {
+          F8 ak = TL::tcol8(Kt_src, kt_pitch, kb * 16, kp, lane);
+          if (p.ret != TS_RET_NONE) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ak[e] = cvt<E>(tof(ak[e]) * s_wk[kp * 32 + 8 * g + e]);
+            for (int e = 0; e < 8; ++e) ak[e] = cvt<E>(tof(ak[e]) * s_wk[kp * 32 + 8 * g + e]);
+          }
+          S[kb] = mma32(ak, av[kp], S[kb]);
         }
-        S[kb] = mma32(ak, av[kp], S[kb]);
       }
     }
+    if (p.ret != TS_RET_NONE && tid == 0) seg_log += s_misc[0];
     state_zero = false;
   }
 
   if (!MAIN) {
-    float* dst = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)(DKP * dvp);
+    if (owner) {
+      float* dst = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)(DKP * dvp);
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * dvp + w * 16 + l16] = S[kb][i];
+        for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * dvp + w * 16 + l16] = S[kb][i];
+    }
     if (tid == 0) p.segdec[(size_t)bh * p.nseg + seg] = seg_log;
   }
 }
@@ -408,14 +523,14 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   L->dkp = pick_dkp(dk_eff);
   if (L->dkp < 0) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: key width %d exceeds 144", dk_eff);
   L->dvp = ((d->dv + (d->v_ext != TS_EXT_NONE ? 1 : 0)) + 15) / 16 * 16;
-  if (L->dvp > 256) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: value width %d exceeds 256", L->dvp);
+  if (L->dvp > 144) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: value width %d exceeds 144", L->dvp);
   L->nchunks = (d->T + ts::C - 1) / ts::C;
   const int bh = d->B * d->H;
   if (d->seg_chunks > 0) {
     L->seg_chunks = d->seg_chunks;
   } else {
-    // Enough workgroups to fill 256 CUs a few times over.
-    int want = 768 / (bh > 0 ? bh : 1);
+    // Two resident workgroups per CU on 256 CUs.
+    int want = 512 / (bh > 0 ? bh : 1);
     if (want < 1) want = 1;
     L->seg_chunks = (L->nchunks + want - 1) / want;
     if (L->seg_chunks < 1) L->seg_chunks = 1;
@@ -431,20 +546,29 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
 
 size_t lds_bytes(int esize, int dkp, int dvp, bool main_kernel) {
   const int vec = 16 / esize;
-  const int qp = dkp + vec, tp = ts::C + vec;
-  size_t elems = (size_t)dkp * tp + (size_t)dvp * tp;
-  if (main_kernel) elems += 2 * (size_t)ts::C * qp + (size_t)ts::C * tp;
+  const int qp = dkp + vec, tp = ts::C + vec, vp = dvp + vec;
+  size_t elems = (size_t)ts::C * qp;                       // K rows
+  if (main_kernel) elems += (size_t)ts::C * qp + (size_t)ts::C * tp;  // Q rows, P
+  if (esize == 2)
+    elems += (size_t)ts::C * vp;                           // V rows
+  else
+    elems += (size_t)dkp * tp + (size_t)dvp * tp;          // K^T, V^T copies
   return elems * esize + 5 * ts::C * sizeof(float);
+}
+
+int block_threads(int dvp) {
+  const int t = dvp / 16 * 64;
+  return t < 256 ? 256 : t;
 }
 
 typedef void (*KernelFn)(ts::ScanP);
 
-template <typename E>
-KernelFn pick_kernel(int dkp, bool main_kernel) {
+template <typename E, bool WIDE>
+KernelFn pick_kernel_w(int dkp, bool main_kernel) {
   switch (dkp) {
-#define TS_CASE(D)                                                                           \
-  case D:                                                                                    \
-    return main_kernel ? (KernelFn)ts::scan_kernel<E, D, true> : (KernelFn)ts::scan_kernel<E, D, false>;
+#define TS_CASE(D)                                                                                   \
+  case D:                                                                                            \
+    return main_kernel ? (KernelFn)ts::scan_kernel<E, D, true, WIDE> : (KernelFn)ts::scan_kernel<E, D, false, WIDE>;
     TS_CASE(32)
     TS_CASE(64)
     TS_CASE(80)
@@ -453,6 +577,11 @@ KernelFn pick_kernel(int dkp, bool main_kernel) {
 #undef TS_CASE
   }
   return nullptr;
+}
+
+template <typename E>
+KernelFn pick_kernel(int dkp, int dvp, bool main_kernel) {
+  return dvp > 64 ? pick_kernel_w<E, true>(dkp, main_kernel) : pick_kernel_w<E, false>(dkp, main_kernel);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -545,9 +674,11 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   }
 
   const int bh = d->B * d->H;
-  const dim3 block(L.dvp / 16 * 64);
-  KernelFn fsum = d->dtype == TS_BF16 ? pick_kernel<ts::bf16>(L.dkp, false) : pick_kernel<float>(L.dkp, false);
-  KernelFn fmain = d->dtype == TS_BF16 ? pick_kernel<ts::bf16>(L.dkp, true) : pick_kernel<float>(L.dkp, true);
+  const dim3 block(block_threads(L.dvp));
+  KernelFn fsum = d->dtype == TS_BF16 ? pick_kernel<ts::bf16>(L.dkp, L.dvp, false)
+                                      : pick_kernel<float>(L.dkp, L.dvp, false);
+  KernelFn fmain = d->dtype == TS_BF16 ? pick_kernel<ts::bf16>(L.dkp, L.dvp, true)
+                                       : pick_kernel<float>(L.dkp, L.dvp, true);
   const size_t lds_sum = lds_bytes(esize, L.dkp, L.dvp, false);
   const size_t lds_main = lds_bytes(esize, L.dkp, L.dvp, true);
   if (lds_main > 160 * 1024)

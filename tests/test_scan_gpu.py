@@ -54,6 +54,8 @@ SHAPES = [
     (2, 2, 300, 64, 64),   # ragged, several tiles
     (1, 2, 260, 128, 64),  # wide keys
     (1, 1, 130, 64, 128),  # wide values
+    (1, 2, 200, 72, 64),   # keys padded to 80: a 16-wide contraction tail
+    (1, 1, 150, 136, 48),  # keys padded to 144, values narrower than a tile
     (1, 1, 1, 8, 8),       # a single token
 ]
 
@@ -180,6 +182,49 @@ def test_mass_column_matches_unit_value_column(cuda, dtype):
         assert rel_err(mass, expected[..., -1]) < TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dk", [32, 64])
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("kind", ["none", "static"])
+def test_ext_columns_match_concatenated_features(cuda, dtype, dk, reverse, kind):
+    """A q ext column (array) and a k ext column (ones) equal one more feature
+    of q and k; used by the key-mass backward (engine.py:430-442)."""
+    from thetascan_amd._core.ops import scan_hip
+    from thetascan_amd import _lib
+
+    B, H, T, Dv = 2, 2, 170, 64
+    q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, dk, Dv, seed=3))
+    g = torch.Generator().manual_seed(8)
+    qe = torch.randn(B, H, T, generator=g, dtype=torch.float64)
+    qe = qe.to(torch.float32).double()
+    ret = _retention(kind, B, H, T)
+    qc = torch.cat([q, qe[..., None]], dim=-1)
+    kc = torch.cat([k, torch.ones_like(k[..., :1])], dim=-1)
+    decay = _oracle_decay(ret, q)
+    if reverse:
+        rdecay = None
+        if decay is not None:
+            flipped = decay.flip(2)
+            rdecay = torch.cat([torch.zeros_like(flipped[:, :, :1]), flipped[:, :, :-1]], dim=2)
+        expected = oracle.linattn_naive(qc.flip(2), kc.flip(2), v.flip(2), rdecay).flip(2)
+    else:
+        expected = oracle.linattn_naive(qc, kc, v, decay)
+    kw = {"retention": _lib.RET_STATIC if kind == "static" else _lib.RET_NONE}
+    if kind == "static":
+        kw["log_alpha"] = ret.to(cuda, torch.float32)
+    out, _, _ = scan_hip.scan_launch(q.to(cuda, dtype), k.to(cuda, dtype), v.to(cuda, dtype), reverse=reverse,
+                                     q_ext=qe.to(cuda, torch.float32), k_ext="ones", seg_chunks=2, **kw)
+    assert rel_err(out, expected) < TOL[dtype], (dk, reverse, kind)
+    # the same columns the other way round (k ext array, q ext ones)
+    out2, _, _ = scan_hip.scan_launch(k.to(cuda, dtype), q.to(cuda, dtype), v.to(cuda, dtype), reverse=reverse,
+                                      q_ext="ones", k_ext=qe.to(cuda, torch.float32), seg_chunks=2, **kw)
+    if reverse:
+        expected2 = oracle.linattn_naive(kc.flip(2), qc.flip(2), v.flip(2), rdecay).flip(2)
+    else:
+        expected2 = oracle.linattn_naive(kc, qc, v, decay)
+    assert rel_err(out2, expected2) < TOL[dtype], (dk, reverse, kind, "swapped")
+
+
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
 def test_final_state_matches_recurrence(cuda, kind):
     from thetascan_amd._core.ops import scan_hip
@@ -198,11 +243,12 @@ def test_final_state_matches_recurrence(cuda, kind):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
 @pytest.mark.parametrize("with_mass", [False, True])
-def test_gradients_match_float64_autograd(cuda, dtype, kind, with_mass):
+@pytest.mark.parametrize("width", [32, 64])
+def test_gradients_match_float64_autograd(cuda, dtype, kind, with_mass, width):
     """q, k, v and retention gradients (tests/test_scan_chunk.py:271-301)."""
     from thetascan_amd._core.ops import scan_hip
 
-    B, H, T, Dk, Dv = 2, 2, 150, 32, 32
+    B, H, T, Dk, Dv = 2, 2, 150, width, width
     q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, Dk, Dv))
     ret = _retention(kind, B, H, T)
     g = torch.Generator().manual_seed(5)

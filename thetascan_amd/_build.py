@@ -10,6 +10,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -27,10 +29,10 @@ HIPCC_FLAGS = (
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # Never let the compiler form packed-fp32 VALU ops on this target.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 )
+NOISE = "is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -40,23 +42,31 @@ def hipcc() -> str:
     return found
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into ``thetascan_amd/libthetascan_hip.so``."""
-    sources = [str(CSRC / name) for name in SOURCES if (CSRC / name).exists()]
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *sources, "-o", str(tmp)]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    errors = "\n".join(
-        line for line in (proc.stdout + proc.stderr).splitlines() if noise not in line
-    )
+    messages = "\n".join(line for line in (proc.stdout + proc.stderr).splitlines() if NOISE not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{errors}")
-    if verbose and errors.strip():
-        print(errors, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{messages}")
+    if verbose and messages.strip():
+        print(messages, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source (in parallel) and link ``thetascan_amd/libthetascan_hip.so``."""
+    sources = [CSRC / name for name in SOURCES if (CSRC / name).exists()]
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="thetascan_build_") as tmpdir:
+        objects = [Path(tmpdir) / (src.stem + ".o") for src in sources]
+        cmds = [[cc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+                for src, obj in zip(sources, objects)]
+        with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+            for fut in [pool.submit(_run, cmd, verbose) for cmd in cmds]:
+                fut.result()
+        tmp = LIB_PATH.with_suffix(".so.tmp")
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)], verbose)
+        os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
 

@@ -40,8 +40,14 @@ __device__ __forceinline__ floatx4 mma32(floatx8 a, floatx8 b, floatx4 c) {
   return c;
 }
 // D += A * B over a 16-wide contraction block (four k-values per lane).
+// Issued as the 32-deep MFMA with the upper four k-values zero: a dependent
+// accumulation chain then uses one MFMA opcode throughout.  Mixing the
+// 16x16x16 and 16x16x32 bf16 opcodes back to back on one accumulator read a
+// stale accumulator on gfx950 (compiler-inserted wait states were missing).
 __device__ __forceinline__ floatx4 mma16(bf16x4 a, bf16x4 b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  const bf16x4 z = {(bf16)0.0f, (bf16)0.0f, (bf16)0.0f, (bf16)0.0f};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(a, z, 0, 1, 2, 3, 4, 5, 6, 7),
+                                                 __builtin_shufflevector(b, z, 0, 1, 2, 3, 4, 5, 6, 7), c, 0, 0, 0);
 }
 __device__ __forceinline__ floatx4 mma16(floatx4 a, floatx4 b, floatx4 c) {
 #pragma unroll

@@ -14,8 +14,14 @@ The timed region brackets exactly ``--steps`` steps with a device
 synchronisation on both sides, inputs already resident in HBM.
 
 Extra objects on the JSON line:
-  roofline      -- the dominant kernel (the forward scan) against HBM peak:
-                   algorithmic bytes per launch / mean launch time (HIP events)
+  roofline      -- the HIP entry point with the most time per step against
+                   HBM peak: algorithmic bytes per launch / mean launch time,
+                   from events bracketing each launch on its own stream during
+                   real fwd+bwd steps (an instrumented replay after the
+                   clean timed region); ``traffic`` is the HBM bytes per launch
+                   measured with rocprofv3 PMC counters when recorded
+  passes        -- the same figures for every HIP entry point of the step
+  scan_mfma     -- the scan's tile contractions against the dense bf16 MFMA peak
   cpu_baseline  -- the CPU oracle's prefix-sum (``cumsum``) mixer, fp32,
                    fwd+bwd on a bounded sample, on this host's cores
 """
@@ -34,6 +40,7 @@ if REPO not in sys.path:
 
 METRIC = "mixer tokens/s fwd+bwd (B8 T4096 H8 d64 bf16); % of MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 B, T, H, D_HEAD, D_MODEL = 8, 4096, 8, 64, 512
 
 
@@ -92,51 +99,103 @@ def time_steps(module, x, dy, steps: int, warmup: int):
     return start.elapsed_time(stop) / steps
 
 
-def scan_roofline(module, x, reps: int = 20):
-    """Mean duration of the forward scan kernel chain on the step's real inputs."""
+def scan_flops(B_, H_, T_, dk, dv, tile=64):
+    """Algorithmic MFMA work of one forward scan over full 64-token tiles:
+    per token and head C*dk (scores) + C*dv (P.V) + dk*dv (carried-state read)
+    + dk*dv (state update) multiply-adds."""
+    return 2 * B_ * H_ * T_ * (tile * dk + tile * dv + 2 * dk * dv)
+
+
+def pass_profile(module, x, dy, steps: int = 5):
+    """Per-entry-point timing inside real fwd+bwd steps.
+
+    Every HIP entry point called during ``steps`` steps is bracketed by events
+    on the stream it launches on (``_lib.record_launches``).  Returns, per entry
+    point, launches per step, mean duration per launch and achieved GB/s of its
+    algorithmic bytes (inputs read once, outputs written once).
+    """
     import torch
-    from thetascan_amd._core.ops import fused, scan_hip
+    from thetascan_amd import _lib
 
-    core = module._core
-    cfg = core.cfg
-    with torch.no_grad():
-        qkv = torch.nn.functional.linear(x, core.proj_qkv.weight).view(B, T, 3, H, D_HEAD)
-        (W1, W2, _), = core._weights()
-        feat_rot = 32 if cfg.rope_placement == "feature" else 0
-        in_rot = 32 if cfg.rope_placement == "input" else 0
-        spec = fused.FeatureSpec(fused._lib.FEAT_RELU2, 64, 1.0, in_rot, feat_rot, 10000.0, 1.0)
-        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-        phi_k, _ = fused.feature_fwd(spec, k, W1.contiguous(), None, None, False)
-        phi_q, _ = fused.feature_fwd(spec, q, W1.contiguous(), W2.contiguous(), None, True)
-        mass = cfg.read_norm
+    def step():
+        module.zero_grad(set_to_none=True)
+        module(x).backward(dy)
 
-        def run():
-            scan_hip.scan_launch(phi_q, phi_k, v, v_ext="ones" if mass else None, want_ext_out=mass)
-
-        for _ in range(3):
-            run()
+    step()
+    torch.cuda.synchronize()
+    with _lib.record_launches() as recs:
+        for _ in range(steps):
+            step()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            run()
-        e1.record()
-        torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    n = B * H * T
-    # algorithmic bytes: read phi_q, phi_k (m = 64), v (d = 64) in bf16; write num (bf16) [+ fp32 mass]
-    per_token = 3 * 64 * 2 + 64 * 2 + (4 if mass else 0)
-    algo = n * per_token
-    achieved = algo / (ms * 1e-3) / 1e9
-    return {
-        "kernel": "forward scan (ts_scan_fwd: summary + prefix + main kernels)",
-        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "ms_per_launch": round(ms, 4), "algorithmic_bytes": algo, "bytes_per_token_head": per_token,
+        rows = [(name, a.elapsed_time(b), nb) for name, a, b, nb in recs]
+    table = {}
+    for name, ms, nb in rows:
+        t = table.setdefault(name, {"launches": 0, "ms": 0.0, "bytes": 0})
+        t["launches"] += 1
+        t["ms"] += ms
+        t["bytes"] += nb
+    out = {}
+    for name, t in sorted(table.items(), key=lambda kv: -kv[1]["ms"]):
+        gbs = t["bytes"] / (t["ms"] * 1e-3) / 1e9
+        out[name] = {
+            "launches_per_step": t["launches"] / steps,
+            "ms_per_step": round(t["ms"] / steps, 4),
+            "ms_per_launch": round(t["ms"] / t["launches"], 4),
+            "bytes_per_launch": t["bytes"] // t["launches"],
+            "achieved_GBs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        }
+    return out
+
+
+def roofline_of(passes: dict, traffic: dict) -> dict:
+    """The dominant entry point (most time per step) against the HBM roofline."""
+    name, p = next(iter(passes.items()))
+    entry = {
+        "kernel": name, "bound": "hbm", "achieved": p["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": p["hbm_frac"], "traffic": traffic.get(name), "ms_per_launch": p["ms_per_launch"],
+        "bytes_per_launch": p["bytes_per_launch"], "launches_per_step": p["launches_per_step"],
     }
+    return entry
 
 
-def cpu_baseline(budget_s: float = 20.0):
+def load_traffic() -> dict:
+    """HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE +
+    WRITE_SIZE, scaled by the same counters on a plain copy), keyed by entry
+    point; empty when no measurement is recorded."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    return {k: v["bytes_per_launch"] for k, v in data.get("entry_points", {}).items() if "bytes_per_launch" in v}
+
+
+def copy_calibration(n_mib: int = 256, reps: int = 3):
+    """A plain device copy of a known size (for scaling PMC byte counters)."""
+    import torch
+
+    src = torch.ones(n_mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes_each_way": src.numel() * 4, "reps": reps}
+
+
+def scan_mfma(passes: dict) -> dict | None:
+    """Intra-chunk MFMA work of the forward scan against the dense bf16 peak."""
+    p = passes.get("ts_scan_fwd")
+    if p is None:
+        return None
+    flops = scan_flops(B, H, T, 64, 64)
+    achieved = flops / (p["ms_per_launch"] * 1e-3) / 1e12
+    return {"kernel": "ts_scan_fwd", "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "flops_per_launch": flops}
+
+
+def cpu_baseline(budget_s: float = 12.0):
     """fp32 fwd+bwd of the oracle mixer with the reference's prefix-sum scan on the host CPU."""
     import torch
     from oracle import mixer as oracle_mixer
@@ -161,7 +220,7 @@ def cpu_baseline(budget_s: float = 20.0):
         return time.perf_counter() - t0
 
     first = run()
-    reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
+    reps = max(3, min(25, int(budget_s / max(first, 1e-3))))
     times = [run() for _ in range(reps)]
     t = statistics.median(times)
     model = ""
@@ -186,6 +245,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-variant", action="store_true", help="skip the key-mass variant")
     ap.add_argument("--steps-only", action="store_true", help="time the steps only (for profilers)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 256 MiB device copy (reference for PMC byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -206,6 +267,8 @@ def main() -> int:
     module = seeded_module(headline_config("feature_rope"), 0).to(dev, torch.bfloat16)
     ms = time_steps(module, x, dy, args.steps, args.warmup)
     assert module._core.last_path == "fused"
+    if args.calibrate_copy:
+        copy_calibration()
     if args.steps_only:
         print(json.dumps({"ms_per_step": ms}), flush=True)
         return 0
@@ -220,13 +283,18 @@ def main() -> int:
                    "batch": B, "seq_len": T, "heads": H, "head_dim": D_HEAD, "d_model": D_MODEL,
                    "parallelism": "single GPU"},
     }
-    out["roofline"] = scan_roofline(module, x)
+    traffic = load_traffic()
+    passes = pass_profile(module, x, dy)
+    out["roofline"] = roofline_of(passes, traffic)
+    out["passes"] = passes
+    out["scan_mfma"] = scan_mfma(passes)
     if not args.no_variant:
         module_b = seeded_module(headline_config("key_mass"), 0).to(dev, torch.bfloat16)
         ms_b = time_steps(module_b, x, dy, args.steps, args.warmup)
+        passes_b = pass_profile(module_b, x, dy)
         out["variants"] = {
             "input_rope_key_mass": {"value": round(tokens / (ms_b * 1e-3), 1), "ms_per_step": round(ms_b, 4),
-                                    "roofline": scan_roofline(module_b, x)},
+                                    "roofline": roofline_of(passes_b, {}), "passes": passes_b},
         }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

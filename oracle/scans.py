@@ -1,6 +1,6 @@
 """CPU restatements of the reference scan backends (test infrastructure only).
 
-Pinning (see tests/test_oracle_scans.py):
+Pinning (tests/test_oracle_golden.py, tests/test_oracle_closed_forms.py):
 * ``naive``  -- golden vectors written from the reference (tests/golden),
   the constant-stream closed form (1 - a^(t+1)) / (1 - a), a hand-computed
   3-token case, and agreement with the independent ``quad`` formulation.

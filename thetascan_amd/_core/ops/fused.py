@@ -78,8 +78,9 @@ def feature_fwd(spec: FeatureSpec, x, w1, w2, tau, want_resid: bool):
     io = _lib.FeatureIO(_lib.strided(x), _lib.ptr(w1), _lib.ptr(w2), _lib.ptr(tau), _lib.ptr(ic),
                         _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(phi), _lib.strided(resid))
     desc = spec.desc(x, tau is not None)
-    _lib.check(lib.ts_feature_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device)),
-               "ts_feature_fwd")
+    with _lib.timed("ts_feature_fwd", _lib.nbytes(x, phi, resid)):
+        status = lib.ts_feature_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
+    _lib.check(status, "ts_feature_fwd")
     return phi, resid
 
 
@@ -114,8 +115,9 @@ def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_w
         _lib.strided(dx), _lib.strided(da_v), _lib.strided(xn_v), _lib.strided(h_v), _lib.strided(dtau),
     )
     desc = spec.desc(x, tau is not None)
-    _lib.check(lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device)),
-               "ts_feature_bwd")
+    with _lib.timed("ts_feature_bwd", _lib.nbytes(x, dphi, dresid, dx, da, xn, h, dtau)):
+        status = lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
+    _lib.check(status, "ts_feature_bwd")
     return da, xn, h, dtau
 
 
@@ -126,8 +128,9 @@ def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6):
                          float(scale), float(eps))
     io = _lib.ReadIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
                      _lib.strided(y))
-    _lib.check(lib.ts_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device)),
-               "ts_read_fwd")
+    with _lib.timed("ts_read_fwd", _lib.nbytes(num, mass, resid, g, y)):
+        status = lib.ts_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
+    _lib.check(status, "ts_read_fwd")
     return y
 
 
@@ -143,8 +146,9 @@ def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6):
     io = _lib.ReadBwdIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
                         _lib.strided(dy), _lib.strided(dnum), _lib.strided(dmass), _lib.strided(dresid),
                         _lib.strided(dg))
-    _lib.check(lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device)),
-               "ts_read_bwd")
+    with _lib.timed("ts_read_bwd", _lib.nbytes(num, mass, resid, g, dy, dnum, dmass, dresid, dg)):
+        status = lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
+    _lib.check(status, "ts_read_bwd")
     return dnum, dmass, (dresid, dresid_hm), dg
 
 
@@ -171,8 +175,10 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
             kind = _lib.RET_STATIC
             la = retention.detach().to(torch.float32).reshape(H).contiguous()
     desc = _lib.WcumsumDesc(B, H, T, F, kind, int(reverse))
-    _lib.check(lib.ts_wcumsum(ctypes.byref(desc), _lib.strided(xf), _lib.strided(out), _lib.ptr(la),
-                              _lib.strided(dec), _lib.stream_handle(x.device)), "ts_wcumsum")
+    with _lib.timed("ts_wcumsum", _lib.nbytes(xf, out, dec)):
+        status = lib.ts_wcumsum(ctypes.byref(desc), _lib.strided(xf), _lib.strided(out), _lib.ptr(la),
+                                _lib.strided(dec), _lib.stream_handle(x.device))
+    _lib.check(status, "ts_wcumsum")
     return out
 
 

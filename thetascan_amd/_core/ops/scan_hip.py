@@ -176,11 +176,15 @@ def scan_launch(
         _lib.strided(ext_out if want_ext_out else None),
         final.data_ptr() if final is not None else None,
     )
-    status = lib.ts_scan_fwd(
-        ctypes.byref(desc), ctypes.byref(io),
-        workspace.data_ptr() if workspace is not None else None,
-        ws_bytes.value, _lib.stream_handle(q.device),
-    )
+    out_bytes = B * H * T * dv * out_buf.element_size() * (2 if out_mode == _lib.OUT_ACCUM_F32 else 1)
+    traffic = (_lib.nbytes(q, k, v, qe, ke, ve, dec) + out_bytes
+               + (_lib.nbytes(ext_out) * (2 if out_mode == _lib.OUT_ACCUM_F32 else 1) if want_ext_out else 0))
+    with _lib.timed("ts_scan_fwd", traffic):
+        status = lib.ts_scan_fwd(
+            ctypes.byref(desc), ctypes.byref(io),
+            workspace.data_ptr() if workspace is not None else None,
+            ws_bytes.value, _lib.stream_handle(q.device),
+        )
     _lib.check(status, "ts_scan_fwd")
     result = out_buf if out is not None else out_buf[..., :dv]
     if final is not None:

@@ -6,6 +6,7 @@ falls back to a CPU path: a missing library or a non-GPU tensor raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
 from pathlib import Path
@@ -256,6 +257,43 @@ def ptr(t: torch.Tensor | None):
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+# ------------------------------------------------------------ launch timing
+
+_RECORDS: list | None = None
+
+
+@contextlib.contextmanager
+def record_launches():
+    """Collect ``(name, start_event, end_event, bytes)`` for every entry-point
+    call made inside the block.  The events bracket the C call on the stream
+    it launches on; ``bytes`` is the call's algorithmic traffic (every input
+    element read once, every output element written once)."""
+    global _RECORDS
+    previous, _RECORDS = _RECORDS, []
+    try:
+        yield _RECORDS
+    finally:
+        _RECORDS = previous
+
+
+@contextlib.contextmanager
+def timed(name: str, nbytes: int):
+    """Bracket one entry-point call with events when launches are recorded."""
+    if _RECORDS is None:
+        yield
+        return
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    yield
+    end.record()
+    _RECORDS.append((name, start, end, int(nbytes)))
+
+
+def nbytes(*tensors) -> int:
+    """Bytes of the given tensors (None entries count zero)."""
+    return sum(t.numel() * t.element_size() for t in tensors if t is not None)
 
 
 def dtype_code(dtype: torch.dtype) -> int:

@@ -120,8 +120,8 @@ enum ts_feature_kind { TS_FEAT_RELU2 = 0, TS_FEAT_SOFTMAX = 1 };
 
 typedef struct ts_feature_desc {
   int32_t B, H, T;
-  int32_t d;            /* head width (16..128, multiple of 16)                */
-  int32_t m;            /* feature width (16..256, multiple of 16)             */
+  int32_t d;            /* head width: 16, 32, 64 or 128                        */
+  int32_t m;            /* feature width: 16, 32, 64, 128 or 256                */
   int32_t dtype;        /* ts_dtype of x, weights and bf16/fp32 outputs        */
   int32_t kind;         /* ts_feature_kind                                      */
   int32_t in_rot;       /* input-RoPE rotated channels of x (0 or 4k <= d)     */
@@ -172,11 +172,26 @@ typedef struct ts_feature_bwd_io {
   ts_strided xn;                   /* out [B,H,T,d]: xn (NULL ok)              */
   ts_strided h;                    /* out [B,H,T,m]: unrotated h (NULL ok)     */
   ts_strided dtau;                 /* out fp32 [B,H,T]: -sum_j dpre_j (NULL ok) */
+  float* dw1_part;                 /* out fp32 [P,H,m,d]: partial sums of da^T xn        */
+  float* dw2_part;                 /* out fp32 [P,H,d,m]: partial sums of s dresid^T h   */
+  float* dtau_part;                /* out fp32 [P,H]: partial sums of -sum_j dpre_j      */
 } ts_feature_bwd_io;
 
 /* Backward of ts_feature_fwd (recomputes the forward tile in registers/LDS).
- * Weight gradients are then plain GEMMs of the returned da/xn/h tiles. */
+ * Two ways to obtain the weight gradients of W1, W2 and tau:
+ *   fused    -- dw1_part != NULL: every workgroup contracts its tokens'
+ *               da^T xn (and s dresid^T h, and the tau gradient) into one of
+ *               P partial slots, P from ts_feature_bwd_parts(); the caller
+ *               sums the slots.  da/xn/h/dtau are then ignored.
+ *   per-token -- dw1_part == NULL: da, xn, h, dtau are written per token
+ *               (any may be NULL) for the caller's own GEMMs.
+ * Replaces the autograd backward of the chain ts_feature_fwd replaces. */
 int ts_feature_bwd(const ts_feature_desc* desc, const ts_feature_bwd_io* io, hipStream_t stream);
+
+/* Number P of partial weight-gradient slots ts_feature_bwd fills for `desc`
+ * (with or without a dresid input), or 0 when no fused weight-gradient kernel
+ * covers the shape (the per-token outputs must be used). */
+int ts_feature_bwd_parts(const ts_feature_desc* desc, int32_t has_dresid, int32_t* parts);
 
 /* ------------------------------------------------------------------- read */
 

@@ -34,7 +34,8 @@ _EXPANSION_MAP_DOMAIN = "thetascan-expansion-v1"
 _EXPANSION_FINGERPRINT_MAGIC = b"TSXF"
 _EXPANSION_FINGERPRINT_SCHEMA_VERSION = 1
 
-FUSED_HEAD_DIMS = (16, 32, 48, 64, 96, 128)
+FUSED_HEAD_DIMS = (16, 32, 64, 128)
+FUSED_FEATURE_WIDTHS = (16, 32, 64, 128, 256)
 
 
 def _inverse_softplus(value: float) -> float:
@@ -347,7 +348,7 @@ class ThetaScan(nn.Module):
             return False
         if cfg.read_norm and cfg.read_norm_mode != "key_mass":
             return False
-        if cfg.head_dim not in FUSED_HEAD_DIMS or cfg.mem_hidden % 16 or cfg.mem_hidden > 256:
+        if cfg.head_dim not in FUSED_HEAD_DIMS or cfg.mem_hidden not in FUSED_FEATURE_WIDTHS:
             return False
         rot_in = rotated_width(cfg.head_dim, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
         rot_feat = rotated_width(cfg.mem_hidden, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0

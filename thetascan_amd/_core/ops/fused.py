@@ -93,32 +93,68 @@ def _head_major(B, H, T, w, dtype, device):
 def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_weights=True):
     """Backward of one stream; dx is written in place.
 
-    Returns head-major ``[H, B*T, .]`` tiles ``(da, xn, h)`` for the weight
-    gradients (None when not wanted) and the per-token threshold gradient.
+    Returns fp32 ``(dw1 [H,m,d], dw2 [H,d,m], dtau [H])`` -- this stream's
+    contributions to the gradients of W1, W2 (queries only) and the threshold
+    tau (None where not applicable or not wanted).  The weight gradients are
+    contracted inside the kernel into per-workgroup partial slots and summed
+    here; shapes without a fused kernel fall back to per-token tiles and
+    split-K GEMMs.
     """
     lib = _lib.load()
     B, H, T, d = x.shape
     m = spec.m
+    dev = x.device
     w1t = w1.transpose(1, 2).contiguous()
     w2t = w2.transpose(1, 2).contiguous() if (dresid is not None) else None
-    da = xn = h = da_v = xn_v = h_v = None
+    desc = spec.desc(x, tau is not None)
+    parts = ctypes.c_int32(0)
     if want_weights:
-        da_v, da = _head_major(B, H, T, m, x.dtype, x.device)
-        xn_v, xn = _head_major(B, H, T, d, x.dtype, x.device)
+        _lib.check(lib.ts_feature_bwd_parts(ctypes.byref(desc), int(dresid is not None), ctypes.byref(parts)),
+                   "ts_feature_bwd_parts")
+    P = parts.value
+    da = xn = h = da_v = xn_v = h_v = dtau_tok = None
+    dw1p = dw2p = dtaup = None
+    if want_weights and P > 0:
+        dw1p = torch.empty(P, H, m, d, dtype=torch.float32, device=dev)
         if dresid is not None:
-            h_v, h = _head_major(B, H, T, m, x.dtype, x.device)
-    dtau = torch.empty(B, H, T, dtype=torch.float32, device=x.device) if tau is not None else None
-    ic, is_, fc, fs = spec.tables(T, x.device)
+            dw2p = torch.empty(P, H, d, m, dtype=torch.float32, device=dev)
+        if tau is not None:
+            dtaup = torch.empty(P, H, dtype=torch.float32, device=dev)
+    elif want_weights:
+        da_v, da = _head_major(B, H, T, m, x.dtype, dev)
+        xn_v, xn = _head_major(B, H, T, d, x.dtype, dev)
+        if dresid is not None:
+            h_v, h = _head_major(B, H, T, m, x.dtype, dev)
+        if tau is not None:
+            dtau_tok = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    ic, is_, fc, fs = spec.tables(T, dev)
     io = _lib.FeatureBwdIO(
         _lib.strided(x), _lib.ptr(w1), _lib.ptr(w1t), _lib.ptr(w2t), _lib.ptr(tau), _lib.ptr(ic),
         _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(dphi), _lib.strided(dresid),
-        _lib.strided(dx), _lib.strided(da_v), _lib.strided(xn_v), _lib.strided(h_v), _lib.strided(dtau),
+        _lib.strided(dx), _lib.strided(da_v), _lib.strided(xn_v), _lib.strided(h_v), _lib.strided(dtau_tok),
+        _lib.ptr(dw1p), _lib.ptr(dw2p), _lib.ptr(dtaup),
     )
-    desc = spec.desc(x, tau is not None)
-    with _lib.timed("ts_feature_bwd", _lib.nbytes(x, dphi, dresid, dx, da, xn, h, dtau)):
-        status = lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
+    traffic = _lib.nbytes(x, dphi, dresid, dx, da, xn, h, dtau_tok, dw1p, dw2p, dtaup)
+    with _lib.timed("ts_feature_bwd", traffic):
+        status = lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(dev))
     _lib.check(status, "ts_feature_bwd")
-    return da, xn, h, dtau
+    if not want_weights:
+        return None, None, None
+    if P > 0:
+        return (dw1p.sum(0), None if dw2p is None else dw2p.sum(0), None if dtaup is None else dtaup.sum(0))
+    dw1 = split_k_outer(da, xn)
+    dw2 = None if h is None else split_k_outer(_head_major_of(dresid), h) * spec.resid_scale
+    dtau = None if dtau_tok is None else dtau_tok.sum(dim=(0, 2))
+    return dw1, dw2, dtau
+
+
+def _head_major_of(t: torch.Tensor) -> torch.Tensor:
+    """[H, B*T, w] view (or copy) of a [B,H,T,w] tensor."""
+    B, H, T, w = t.shape
+    hm = t.transpose(0, 1)
+    if not hm.is_contiguous():
+        hm = hm.contiguous()
+    return hm.view(H, B * T, w)
 
 
 def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6):
@@ -182,11 +218,6 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
     return out
 
 
-def _weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """sum_n a[h,n,:]^T b[h,n,:] -> fp32 [H, A, B] for head-major tiles (split-K GEMM)."""
-    return split_k_outer(a, b)
-
-
 class _KernelMemory(torch.autograd.Function):
     """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g) for a depth-1 kernel memory."""
 
@@ -241,16 +272,18 @@ class _KernelMemory(torch.autograd.Function):
         scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=ctx.seg_chunks)
         need_w1 = ctx.needs_input_grad[1]
         need_w2 = ctx.needs_input_grad[2]
-        da_k, xn_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=need_w1)
-        da_q, xn_q, h_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c,
-                                              want_weights=need_w1 or need_w2)
+        need_tau = ctx.has_tau and ctx.needs_input_grad[3]
+        want_k = need_w1 or need_tau
+        want_q = need_w1 or need_w2 or need_tau
+        dw1_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=want_k)
+        dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c, want_weights=want_q)
         dw1 = dw2 = dtau = None
         if need_w1:
-            dw1 = (_weight_grad(da_k, xn_k) + _weight_grad(da_q, xn_q)).to(ctx.w_dtypes[0])
+            dw1 = (dw1_k + dw1_q).to(ctx.w_dtypes[0])
         if need_w2:
-            dw2 = (_weight_grad(dresid_hm, h_q) * spec.resid_scale).to(ctx.w_dtypes[1])
-        if ctx.has_tau and ctx.needs_input_grad[3]:
-            dtau = (dtau_k.sum(dim=(0, 2)) + dtau_q.sum(dim=(0, 2))).to(ctx.tau_dtype)
+            dw2 = dw2_q.to(ctx.w_dtypes[1])
+        if need_tau:
+            dtau = (dtau_k + dtau_q).to(ctx.tau_dtype)
         dgo = None
         if ctx.has_g:
             dgo = dg.transpose(1, 2).reshape(B, T, H * d)

@@ -132,6 +132,9 @@ class FeatureBwdIO(ctypes.Structure):
         ("xn", Strided),
         ("h", Strided),
         ("dtau", Strided),
+        ("dw1_part", ctypes.c_void_p),
+        ("dw2_part", ctypes.c_void_p),
+        ("dtau_part", ctypes.c_void_p),
     ]
 
 
@@ -223,6 +226,7 @@ def load() -> ctypes.CDLL:
         P = ctypes.POINTER
         lib.ts_feature_fwd.argtypes = [P(FeatureDesc), P(FeatureIO), ctypes.c_void_p]
         lib.ts_feature_bwd.argtypes = [P(FeatureDesc), P(FeatureBwdIO), ctypes.c_void_p]
+        lib.ts_feature_bwd_parts.argtypes = [P(FeatureDesc), ctypes.c_int32, P(ctypes.c_int32)]
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]

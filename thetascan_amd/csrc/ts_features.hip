@@ -1,14 +1,22 @@
 // Fused write-side feature map for gfx950 (forward and backward).
 //
-// One workgroup = 4 waves = 64 tokens of one (batch, head); each wave owns 16
-// tokens end to end.  The tile is computed transposed, a^T = W1 xn^T, so the
-// MFMA accumulator already holds, per lane, one token and four consecutive
-// features of every 16-feature block.  Every per-token reduction (RMSNorm,
-// feature mass, softmax max/sum, L2-norm dot products) is then a lane-local
-// sum plus two cross-lane steps, feature-RoPE pairs are lane-local, and the
-// accumulator feeds the next MFMA (W2 h^T, W1^T da^T) directly as an operand
-// with the contraction index permuted consistently in both operands.  Only
-// the L2-normalised inputs are staged in LDS (as the B operand of a^T).
+// A workgroup (4 waves) walks `groups` consecutive 64-token groups of one
+// (batch, head).  Each group's input rows are fetched with coalesced 16-byte
+// loads into registers one group ahead of their use, stored to LDS, and
+// consumed from there; outputs are assembled as LDS rows and written back
+// with 16-byte stores.  Wave w computes tokens 16w..16w+15 of a group.
+//
+// The tile is computed transposed, a^T = W1 xn^T, so the MFMA accumulator
+// holds, per lane, one token and four consecutive features of every
+// 16-feature block.  Per-token reductions (RMSNorm, feature mass, softmax
+// max/sum, L2-norm dot products) are then lane-local sums plus two cross-lane
+// steps, feature-RoPE pairs are lane-local, and the accumulator feeds the next
+// MFMA (W2 h^T, W1^T da^T) directly as an operand with the contraction index
+// permuted consistently in both operands.
+//
+// The backward also contracts each group's da^T xn and dresid^T h over its
+// 64 tokens (MFMA on token-major LDS rows read transposed) into per-workgroup
+// partial weight gradients, so dW1 and dW2 never need per-token tiles in HBM.
 //
 // Reference chain replaced: block.py:595-618 (input RoPE, L2 norm),
 // engine.py:117-158 (_block_forward: W1, RMSNorm, threshold, feature map,
@@ -22,10 +30,18 @@
 
 namespace ts {
 
+// A [B,H,T,width] stream: base pointer, element strides of batch and head and
+// a 32-bit element stride of time (the host checks (T + 64) * st fits).
+struct Str {
+  void* ptr;
+  int64_t sb, sh;
+  int st;
+};
+
 struct FeatP {
-  int B, H, T, m, in_rot, feat_rot, has_tau, kind;
-  float gain, s, eps;
-  ts_strided x, phi, resid;
+  int B, H, T, m, in_rot, feat_rot, has_tau, kind, groups;
+  float gain, s, eps, inv_m;
+  Str x, phi, resid, dphi, dresid, dx, da, xn, h, dtau;
   const void* w1;
   const void* w2;
   const void* w1t;
@@ -35,12 +51,26 @@ struct FeatP {
   const float* in_sin;
   const float* f_cos;
   const float* f_sin;
-  ts_strided dphi, dresid, dx, da, xn, h, dtau;
-  int groups;  // 64-token groups per workgroup
-  int w_lds;   // weights staged in LDS
+  float* dw1_part;   // [parts, H, m, D] (fused weight gradients)
+  float* dw2_part;   // [parts, H, D, m]
+  float* dtau_part;  // [parts, H]
 };
 
-constexpr int TT = 64;  // tokens per workgroup (16 per wave)
+constexpr int TT = 64;  // tokens per group (16 per wave)
+
+// Rows of one (batch, head) slice.
+template <typename E>
+struct Rows {
+  E* base;
+  int st;
+  __device__ __forceinline__ E* at(int t) const { return base + t * st; }
+};
+template <typename E>
+__device__ __forceinline__ Rows<E> rows_of(const Str& s, int b, int h) {
+  return Rows<E>{(E*)s.ptr + b * s.sb + h * s.sh, s.st};
+}
+
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 __device__ __forceinline__ float sum_g(float v) {  // over the 4 lane groups of a token
   v += __shfl_xor(v, 16, 64);
@@ -51,11 +81,6 @@ __device__ __forceinline__ float max_g(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, 64));
   v = fmaxf(v, __shfl_xor(v, 32, 64));
   return v;
-}
-
-template <typename E>
-__device__ __forceinline__ E* at(const ts_strided& s, int b, int h, int t) {
-  return (E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
 }
 
 // Four consecutive elements <-> floats.
@@ -70,67 +95,110 @@ __device__ __forceinline__ void st4f(E* p, const float* v) {
   LdsIO<E>::st4(p, v[0], v[1], v[2], v[3]);
 }
 
-// Rotate pairs (c, c+1), (c+2, c+3) of a four-feature group starting at even c.
-__device__ __forceinline__ void rot4(float* v, int c, int rot, const float* cs_tab, const float* sn_tab,
-                                     int64_t row, bool inverse) {
+// RoPE of the four-feature group starting at c (a multiple of 4) of token t:
+// pairs (c, c+1) and (c+2, c+3) rotate when `on` (c < rot and t < T).
+// Branch-free: other lanes read table entry 0 and rotate by the identity.
+__device__ __forceinline__ void rope4(float* v, int c, int rot, const float* cs_tab, const float* sn_tab, int t,
+                                      bool on, bool inverse) {
+  const int idx = on ? t * (rot >> 1) + (c >> 1) : 0;
+  float2 cs = *(const float2*)(cs_tab + idx);
+  float2 sn = *(const float2*)(sn_tab + idx);
+  if (!on) {
+    cs = make_float2(1.f, 1.f);
+    sn = make_float2(0.f, 0.f);
+  }
+  if (inverse) {
+    sn.x = -sn.x;
+    sn.y = -sn.y;
+  }
+  const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3];
+  v[0] = a0 * cs.x - b0 * sn.x;
+  v[1] = a0 * sn.x + b0 * cs.x;
+  v[2] = a1 * cs.y - b1 * sn.y;
+  v[3] = a1 * sn.y + b1 * cs.y;
+}
+
+// Register-staged copy of one [64 x width] token tile: 16-byte vectors,
+// row-major, vector idx = tid + i * 256.  Rows at or past T load as zero.
+template <typename E, int MAXW>
+struct RowTile {
+  static constexpr int VEC = 16 / (int)sizeof(E);
+  static constexpr int SLOTS = (TT * MAXW / VEC + 255) / 256;
+  uint4 r[SLOTS];
+  int rc[SLOTS];  // row | column << 8, or -1 for an unused slot
+
+  __device__ __forceinline__ void init(int width, int tid) {
+    const int per_row = width / VEC;
 #pragma unroll
-  for (int e = 0; e < 4; e += 2) {
-    if (c + e < rot) {
-      const float cs = cs_tab[row + (c + e) / 2];
-      const float sn = inverse ? -sn_tab[row + (c + e) / 2] : sn_tab[row + (c + e) / 2];
-      const float a = v[e], b = v[e + 1];
-      v[e] = a * cs - b * sn;
-      v[e + 1] = a * sn + b * cs;
+    for (int i = 0; i < SLOTS; ++i) {
+      const int idx = tid + i * 256;
+      const int row = idx / per_row;
+      rc[i] = idx < TT * per_row ? row | (((idx - row * per_row) * VEC) << 8) : -1;
     }
+  }
+  __device__ __forceinline__ void fetch(const Rows<E>& src, int t0, int T) {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+      r[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (rc[i] >= 0 && t0 + (rc[i] & 255) < T) r[i] = *(const uint4*)(src.at(t0 + (rc[i] & 255)) + (rc[i] >> 8));
+    }
+  }
+  __device__ __forceinline__ void store(E* dst, int pitch) const {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i)
+      if (rc[i] >= 0) *(uint4*)(dst + (rc[i] & 255) * pitch + (rc[i] >> 8)) = r[i];
+  }
+};
+
+// LDS rows of a [64 x width] tile -> global rows t0.. (rows past T dropped).
+template <typename E>
+__device__ __forceinline__ void write_rows(const E* src, int pitch, const Rows<E>& dst, int t0, int T, int width,
+                                           int tid) {
+  constexpr int VEC = 16 / (int)sizeof(E);
+  const int per_row = width / VEC;
+  for (int idx = tid; idx < TT * per_row; idx += 256) {
+    const int row = idx / per_row;
+    const int c = (idx - row * per_row) * VEC;
+    if (t0 + row < T) *(uint4*)(dst.at(t0 + row) + c) = *(const uint4*)(src + row * pitch + c);
   }
 }
 
-// Row pass over x (four lanes per token, d/4 contiguous dims each): input
-// RoPE, L2 norm; writes xn to the wave's LDS rows and returns ||x_rot||.
+// One token row of x from LDS in the accumulator layout (dims 16db+4g+i):
+// input RoPE, L2 norm.  Keeps the rotated x in xr, writes xn over the row,
+// returns ||x_rot||.
 template <typename E, int D>
-__device__ __forceinline__ float stage_xn(const FeatP& p, int b, int h, int t, int g, E* xs_row) {
-  constexpr int CH = D / 4;
-  const bool valid = t < p.T;
-  float xv[CH];
-  const E* src = at<E>(p.x, b, h, valid ? t : 0) + g * CH;
-#pragma unroll
-  for (int i = 0; i < CH; i += 4) {
-    if (valid) {
-      ld4f<E>(src + i, xv + i);
-    } else {
-      xv[i] = xv[i + 1] = xv[i + 2] = xv[i + 3] = 0.f;
-    }
-  }
-  if (p.in_rot > 0 && valid) {
-    const int64_t row = (int64_t)t * (p.in_rot / 2);
-#pragma unroll
-    for (int i = 0; i < CH; i += 4) rot4(xv + i, g * CH + i, p.in_rot, p.in_cos, p.in_sin, row, false);
-  }
+__device__ __forceinline__ float load_xn(const FeatP& p, int t, bool valid, int g, E* xrow, float (*xr)[4]) {
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < CH; ++i) ss += xv[i] * xv[i];
-  const float nrm = sqrtf(sum_g(ss));
-  const float inv = 1.0f / fmaxf(nrm, p.eps);
+  for (int db = 0; db < D / 16; ++db) {
+    ld4f<E>(xrow + db * 16 + 4 * g, xr[db]);
+    if (p.in_rot > 0)
+      rope4(xr[db], db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, false);
 #pragma unroll
-  for (int i = 0; i < CH; i += 4) {
-    float o[4] = {xv[i] * inv, xv[i + 1] * inv, xv[i + 2] * inv, xv[i + 3] * inv};
-    st4f<E>(xs_row + g * CH + i, o);
+    for (int i = 0; i < 4; ++i) ss += xr[db][i] * xr[db][i];
+  }
+  const float nrm = sqrtf(sum_g(ss));
+  const float inv = rcp(fmaxf(nrm, p.eps));
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    float o[4] = {xr[db][0] * inv, xr[db][1] * inv, xr[db][2] * inv, xr[db][3] * inv};
+    st4f<E>(xrow + db * 16 + 4 * g, o);
   }
   return nrm;
 }
 
 // acc[fb] = (W1 xn^T) block fb: lane holds token l16, features 16fb+4g+i.
-// W1 rows (length D) start every `wp` elements (LDS or global).
+// W1 rows (length D) start every `wp` elements.
 template <typename E, int D, int MB>
-__device__ __forceinline__ void gemm_a(const E* w1, int wp, const E* xs, int l16, int g, int nfb, floatx4* acc) {
+__device__ __forceinline__ void gemm_a(const E* w1, int wp, const E* xs, int xp, int l16, int g, int nfb,
+                                       floatx4* acc) {
   typedef LdsIO<E> IO;
-  constexpr int XP = D + 16 / (int)sizeof(E);
-  const E* xrow = xs + l16 * XP;
+  const E* xrow = xs + l16 * xp;
 #pragma unroll
   for (int fb = 0; fb < MB; ++fb) {
     acc[fb] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (fb < nfb) {
-      const E* wrow = w1 + (size_t)(fb * 16 + l16) * wp;
+      const E* wrow = w1 + (fb * 16 + l16) * wp;
 #pragma unroll
       for (int kk = 0; kk < D / 32; ++kk)
         acc[fb] = mma32(IO::ld8(wrow + kk * 32 + 8 * g), IO::ld8(xrow + kk * 32 + 8 * g), acc[fb]);
@@ -150,7 +218,7 @@ __device__ __forceinline__ void gemm_back(const E* wt, int wp, const floatx4* re
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
     out[db] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const E* wrow = wt + (size_t)(db * 16 + l16) * wp;
+    const E* wrow = wt + (db * 16 + l16) * wp;
 #pragma unroll
     for (int j = 0; j < MB / 2; ++j) {
       if (2 * j + 1 < nfb)
@@ -166,6 +234,36 @@ __device__ __forceinline__ void gemm_back(const E* wt, int wp, const floatx4* re
   }
 }
 
+// Token-axis MFMA fragment of a token-major LDS tile: column c0 + (lane & 15),
+// tokens {32kp+4g..+3} and {32kp+16+4g..+3} for lane group g.  bf16 uses the
+// gfx950 transposing LDS read (ds_read_b64_tr_b16: within each 16-lane
+// group, lane j addresses row r0 + j/4, column c0 + 4*(j%4); lane i receives
+// rows r0..r0+3 of column c0 + i).
+template <typename E> struct TokFrag;
+template <> struct TokFrag<bf16> {
+  typedef short shortx4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
+  static __device__ __forceinline__ bf16x8 get(const bf16* rows, int pitch, int c0, int kp, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const bf16* a = rows + (32 * kp + 4 * g + (j >> 2)) * pitch + c0 + 4 * (j & 3);
+    shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)a);
+    shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(a + 16 * pitch));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+template <> struct TokFrag<float> {
+  static __device__ __forceinline__ floatx8 get(const float* rows, int pitch, int c0, int kp, int lane) {
+    const int g = lane >> 4, l16 = lane & 15;
+    floatx8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = 32 * kp + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4);
+      v[e] = rows[tok * pitch + c0 + l16];
+    }
+    return v;
+  }
+};
+
 // Copy a [rows x cols] row-major global matrix into LDS rows of pitch `pitch`.
 template <typename E>
 __device__ __forceinline__ void stage_matrix(const E* src, int rows, int cols, E* dst, int pitch, int tid) {
@@ -173,7 +271,7 @@ __device__ __forceinline__ void stage_matrix(const E* src, int rows, int cols, E
   const int per_row = cols / VEC;
   for (int idx = tid; idx < rows * per_row; idx += 256) {
     const int r = idx / per_row, c = (idx - r * per_row) * VEC;
-    *(uint4*)(dst + r * pitch + c) = *(const uint4*)(src + (size_t)r * cols + c);
+    *(uint4*)(dst + r * pitch + c) = *(const uint4*)(src + r * cols + c);
   }
 }
 
@@ -181,15 +279,14 @@ __device__ __forceinline__ void stage_matrix(const E* src, int rows, int cols, E
 // the statistics the backward needs.
 template <int MB>
 __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const floatx4* a, int nfb, floatx4* hv,
-                                            float& rinv, float& mass, float& mx) {
+                                            float& rinv, float& mass) {
   float ss = 0.f;
 #pragma unroll
   for (int fb = 0; fb < MB; ++fb)
     if (fb < nfb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) ss += a[fb][i] * a[fb][i];
-  rinv = rsqrtf(sum_g(ss) / (float)p.m + p.eps);
-  mx = 0.f;
+  rinv = rsqrtf(sum_g(ss) * p.inv_m + p.eps);
   if (p.kind == TS_FEAT_RELU2) {
     float sf = 0.f;
 #pragma unroll
@@ -203,8 +300,8 @@ __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const flo
       }
     mass = sum_g(sf);
     const bool ok = mass > p.eps;
-    const float inv = ok ? 1.0f / mass : 0.f;
-    const float uni = 1.0f / (float)p.m;
+    const float inv = ok ? rcp(mass) : 0.f;
+    const float uni = p.inv_m;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
@@ -216,18 +313,18 @@ __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const flo
       if (fb < nfb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) m_ = fmaxf(m_, p.gain * (a[fb][i] * rinv - tau));
-    mx = max_g(m_);
+    const float mx = max_g(m_);
     float se = 0.f;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = fb < nfb ? expf(p.gain * (a[fb][i] * rinv - tau) - mx) : 0.f;
+        const float e = fb < nfb ? __expf(p.gain * (a[fb][i] * rinv - tau) - mx) : 0.f;
         hv[fb][i] = e;
         se += e;
       }
     mass = sum_g(se);
-    const float inv = 1.0f / mass;
+    const float inv = rcp(mass);
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
@@ -235,250 +332,412 @@ __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const flo
   }
 }
 
-// Weights live in LDS when p.w_lds (staged once per workgroup, shared by its
-// 4 waves x NG token groups); otherwise they are read from global memory.
+// LDS carve-up shared by the kernels and the host (element offsets of each
+// tile; pitches are the tile width plus one 16-byte vector).
+struct FeatLayout {
+  int xp, mp;                    // row pitches of d-wide and m-wide tiles
+  int xs, ps, rs, hs, os;        // tiles: x/xn(/resid), phi|dphi/da, dresid, h, dx
+  int w1, w1t, w2;               // weights: W1 [m][xp], W1^T [d][mp], W2 [d][mp] or W2^T [m][xp]
+  int end;                       // total elements
+};
+
+__host__ __device__ constexpr FeatLayout feat_layout(int esize, int d, int m, bool fwd, bool resid, bool wgrad,
+                                                     bool w_lds) {
+  const int vec = 16 / esize;
+  FeatLayout L{};
+  L.xp = d + vec;
+  L.mp = m + vec;
+  int off = 0;
+  L.xs = off; off += TT * L.xp;
+  L.ps = off; off += TT * L.mp;
+  L.rs = L.hs = L.os = -1;
+  if (!fwd) {
+    if (resid) { L.rs = off; off += TT * L.xp; }
+    if (wgrad && resid) { L.hs = off; off += TT * L.mp; }
+    L.os = off; off += TT * L.xp;
+  }
+  L.w1 = L.w1t = L.w2 = -1;
+  if (w_lds) {
+    L.w1 = off; off += m * L.xp;
+    if (fwd) {
+      if (resid) { L.w2 = off; off += d * L.mp; }
+    } else {
+      L.w1t = off; off += d * L.mp;
+      if (resid) { L.w2 = off; off += m * L.xp; }
+    }
+  }
+  L.end = off;
+  return L;
+}
+
+constexpr int kLdsMax = 160 * 1024;
+
+// Weights are staged in LDS exactly when the largest layout a kernel
+// instantiation serves (full width MB*16, with W2) fits.
+template <typename E, int D, int MB, bool FWD, bool WG>
+constexpr bool weights_in_lds() {
+  return feat_layout((int)sizeof(E), D, MB * 16, FWD, true, WG, true).end * (int)sizeof(E) + 64 <= kLdsMax;
+}
+
 template <typename E, int D, int MB>
 __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
-  constexpr int VEC = 16 / (int)sizeof(E);
-  constexpr int XP = D + VEC;
+  constexpr bool WL = weights_in_lds<E, D, MB, true, false>();
   const int b = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
-  const int m = p.m, nfb = m / 16;
+  constexpr int nfb = MB;
+  const int m = MB * 16;
   const bool want_resid = p.resid.ptr != nullptr;
+  const FeatLayout L = feat_layout((int)sizeof(E), D, m, true, want_resid, false, WL);
   extern __shared__ __align__(16) unsigned char smem[];
-  E* xs = (E*)smem + w * 16 * XP;
-  const E* w1 = (const E*)p.w1 + (size_t)h * m * D;
-  const E* w2 = want_resid ? (const E*)p.w2 + (size_t)h * D * m : nullptr;
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* ps = base + L.ps;
+  const E* w1 = (const E*)p.w1 + h * m * D;
+  const E* w2 = (const E*)p.w2 + h * D * m;
   int wp1 = D, wp2 = m;
-  if (p.w_lds) {
-    E* ws1 = (E*)smem + TT * XP;
-    E* ws2 = ws1 + m * (D + VEC);
-    stage_matrix<E>(w1, m, D, ws1, D + VEC, tid);
-    if (want_resid) stage_matrix<E>(w2, D, m, ws2, m + VEC, tid);
-    w1 = ws1;
-    w2 = ws2;
-    wp1 = D + VEC;
-    wp2 = m + VEC;
+  if constexpr (WL) {
+    stage_matrix<E>(w1, m, D, base + L.w1, L.xp, tid);
+    if (want_resid) stage_matrix<E>(w2, D, m, base + L.w2, L.mp, tid);
+    w1 = base + L.w1;
+    w2 = base + L.w2;
+    wp1 = L.xp;
+    wp2 = L.mp;
   }
   const float tau = p.has_tau ? p.tau[h] : 0.f;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
 
+  RowTile<E, D> ldx;
+  ldx.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
   for (int grp = 0; grp < p.groups; ++grp) {
-    const int t = (blockIdx.x * p.groups + grp) * TT + w * 16 + l16;
-    const bool valid = t < p.T;
-    __syncthreads();  // weights staged / previous group done with xs
-    stage_xn<E, D>(p, b, h, t, g, xs + l16 * XP);
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();       // weights staged; previous group's rows written out
+    ldx.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldx.fetch(xsrc, t0 + TT, p.T);
     __syncthreads();
 
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    E* xrow = xs + row * L.xp;
+    float xr[D / 16][4];
+    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
+    __syncthreads();  // xn rows complete before they feed the MFMA
+
     floatx4 a[MB], hv[MB];
-    gemm_a<E, D, MB>(w1, wp1, xs, l16, g, nfb, a);
-    float rinv, mass, mx;
-    feature_map<MB>(p, tau, a, nfb, hv, rinv, mass, mx);
-    if (valid) {
-      E* dst = at<E>(p.phi, b, h, t);
-      const int64_t frow = (int64_t)t * (p.feat_rot / 2);
+    gemm_a<E, D, MB>(w1, wp1, xs + w * 16 * L.xp, L.xp, l16, g, nfb, a);
+    float rinv, mass;
+    feature_map<MB>(p, tau, a, nfb, hv, rinv, mass);
+    {
+      E* prow = ps + row * L.mp;
 #pragma unroll
       for (int fb = 0; fb < MB; ++fb) {
         if (fb < nfb) {
           float v[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
-          if (p.feat_rot > 0) rot4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, frow, false);
-          st4f<E>(dst + fb * 16 + 4 * g, v);
+          if (p.feat_rot > 0)
+            rope4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, t, valid && fb * 16 + 4 * g < p.feat_rot,
+                  false);
+          st4f<E>(prow + fb * 16 + 4 * g, v);
         }
       }
     }
     if (want_resid) {
-      floatx4 base[D / 16];
-      gemm_back<E, D, MB>(w2, wp2, hv, l16, g, nfb, base);
-      if (valid) {
-        E* dst = at<E>(p.resid, b, h, t);
+      floatx4 base_[D / 16];
+      gemm_back<E, D, MB>(w2, wp2, hv, l16, g, nfb, base_);
+      const float inv = rcp(fmaxf(nrm, p.eps));
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) {
-          float xn[4];
-          ld4f<E>(xs + l16 * XP + db * 16 + 4 * g, xn);
-          float v[4];
+      for (int db = 0; db < D / 16; ++db) {
+        float v[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = xn[i] + p.s * base[db][i];
-          st4f<E>(dst + db * 16 + 4 * g, v);
-        }
+        for (int i = 0; i < 4; ++i) v[i] = xr[db][i] * inv + p.s * base_[db][i];
+        st4f<E>(xrow + db * 16 + 4 * g, v);  // resid over this lane's own xn entries
       }
     }
+    __syncthreads();
+    write_rows<E>(ps, L.mp, rows_of<E>(p.phi, b, h), t0, p.T, m, tid);
+    if (want_resid) write_rows<E>(xs, L.xp, rows_of<E>(p.resid, b, h), t0, p.T, D, tid);
   }
 }
 
-template <typename E, int D, int MB>
+// Weight-gradient blocks per wave of the fused backward: wave w owns the
+// feature blocks fb = w, w + 4, ... of dW1 (and of dW2), each across all D/16
+// head-dim blocks.
+template <int D, int MB>
+constexpr int wgrad_blocks() { return ((MB + 3) / 4) * (D / 16); }
+
+template <typename E, int D, int MB, bool WG>
 __global__ __launch_bounds__(256) void feature_bwd_kernel(FeatP p) {
   typedef LdsIO<E> IO;
-  constexpr int VEC = 16 / (int)sizeof(E);
-  constexpr int XP = D + VEC;
+  typedef TokFrag<E> TF;
+  constexpr bool WL = weights_in_lds<E, D, MB, false, WG>();
+  constexpr int NB = WG ? wgrad_blocks<D, MB>() : 1;
   const int b = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
-  const int m = p.m, nfb = m / 16;
+  constexpr int nfb = MB;
+  const int m = MB * 16;
   const bool has_resid = p.dresid.ptr != nullptr;
+  const FeatLayout L = feat_layout((int)sizeof(E), D, m, false, has_resid, WG, WL);
   extern __shared__ __align__(16) unsigned char smem[];
-  E* xs = (E*)smem + w * 16 * XP;
-  const E* w1 = (const E*)p.w1 + (size_t)h * m * D;
-  const E* w1t = (const E*)p.w1t + (size_t)h * D * m;
-  const E* w2t = has_resid ? (const E*)p.w2t + (size_t)h * m * D : nullptr;
+  E* base = (E*)smem;
+  E* xs = base + L.xs;  // x, then xn
+  E* ps = base + L.ps;  // dphi, then da
+  E* rs = base + L.rs;  // dresid
+  E* hs = base + L.hs;  // h
+  E* os = base + L.os;  // dx
+  float* red = (float*)(base + L.end);  // [4] wave partial sums
+
+  const E* w1 = (const E*)p.w1 + h * m * D;
+  const E* w1t = (const E*)p.w1t + h * D * m;
+  const E* w2t = (const E*)p.w2t + h * m * D;
   int wpa = D, wpt = m;
-  if (p.w_lds) {
-    E* ws1 = (E*)smem + TT * XP;
-    E* ws1t = ws1 + m * (D + VEC);
-    E* ws2t = ws1t + D * (m + VEC);
-    stage_matrix<E>(w1, m, D, ws1, D + VEC, tid);
-    stage_matrix<E>(w1t, D, m, ws1t, m + VEC, tid);
-    if (has_resid) stage_matrix<E>(w2t, m, D, ws2t, D + VEC, tid);
-    w1 = ws1;
-    w1t = ws1t;
-    w2t = ws2t;
-    wpa = D + VEC;
-    wpt = m + VEC;
+  if constexpr (WL) {
+    stage_matrix<E>(w1, m, D, base + L.w1, L.xp, tid);
+    stage_matrix<E>(w1t, D, m, base + L.w1t, L.mp, tid);
+    if (has_resid) stage_matrix<E>(w2t, m, D, base + L.w2, L.xp, tid);
+    w1 = base + L.w1;
+    w1t = base + L.w1t;
+    w2t = base + L.w2;
+    wpa = L.xp;
+    wpt = L.mp;
   }
   const float tau = p.has_tau ? p.tau[h] : 0.f;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  const Rows<E> psrc = rows_of<E>(p.dphi, b, h);
+  const Rows<E> rsrc = rows_of<E>(p.dresid, b, h);
+
+  floatx4 acc1[NB], acc2[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) acc1[k] = acc2[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float dtau_acc = 0.f;
+
+  RowTile<E, D> ldx, ldr;
+  RowTile<E, MB * 16> ldp;
+  ldx.init(D, tid);
+  ldr.init(has_resid ? D : 0, tid);
+  ldp.init(m, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  ldp.fetch(psrc, g0 * TT, p.T);
+  if (has_resid) ldr.fetch(rsrc, g0 * TT, p.T);
 
   for (int grp = 0; grp < p.groups; ++grp) {
-  const int t = (blockIdx.x * p.groups + grp) * TT + w * 16 + l16;
-  const bool valid = t < p.T;
-  const int tc = valid ? t : 0;
-  __syncthreads();  // weights staged / previous group done with xs
-  const float nrm = stage_xn<E, D>(p, b, h, t, g, xs + l16 * XP);
-  __syncthreads();
-  if (valid && p.xn.ptr) {
-    constexpr int CH = D / 4;
-    E* dst = at<E>(p.xn, b, h, t) + g * CH;
-#pragma unroll
-    for (int i = 0; i < CH; i += 4) {
-      float v[4];
-      ld4f<E>(xs + l16 * XP + g * CH + i, v);
-      st4f<E>(dst + i, v);
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();       // weights staged; previous group fully consumed
+    ldx.store(xs, L.xp);
+    ldp.store(ps, L.mp);
+    if (has_resid) ldr.store(rs, L.xp);
+    if (grp + 1 < p.groups) {
+      ldx.fetch(xsrc, t0 + TT, p.T);
+      ldp.fetch(psrc, t0 + TT, p.T);
+      if (has_resid) ldr.fetch(rsrc, t0 + TT, p.T);
     }
-  }
+    __syncthreads();
 
-  floatx4 a[MB], hv[MB];
-  gemm_a<E, D, MB>(w1, wpa, xs, l16, g, nfb, a);
-  float rinv, mass, mx;
-  feature_map<MB>(p, tau, a, nfb, hv, rinv, mass, mx);
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    E* xrow = xs + row * L.xp;
+    float xr[D / 16][4];
+    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
+    __syncthreads();  // xn rows complete before they feed the MFMA
 
-  // dh = rotate^T(dphi) (+ s W2^T dresid)
-  floatx4 dh[MB];
-  if (has_resid) {
-    const E* drow = at<E>(p.dresid, b, h, tc);
+    floatx4 a[MB], hv[MB];
+    gemm_a<E, D, MB>(w1, wpa, xs + w * 16 * L.xp, L.xp, l16, g, nfb, a);
+    float rinv, mass;
+    feature_map<MB>(p, tau, a, nfb, hv, rinv, mass);
+
+    // dh = rotate^T(dphi) (+ s W2^T dresid); rows past T are zero in LDS
+    floatx4 dh[MB];
+    const E* rrow = rs + row * L.xp;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb) {
       dh[fb] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (fb < nfb) {
-        const E* wrow = w2t + (size_t)(fb * 16 + l16) * wpa;
+      if (has_resid && fb < nfb) {
+        const E* wrow = w2t + (fb * 16 + l16) * wpa;
 #pragma unroll
         for (int kk = 0; kk < D / 32; ++kk)
-          dh[fb] = mma32(IO::ld8(wrow + kk * 32 + 8 * g), IO::ld8(drow + kk * 32 + 8 * g), dh[fb]);
+          dh[fb] = mma32(IO::ld8(wrow + kk * 32 + 8 * g), IO::ld8(rrow + kk * 32 + 8 * g), dh[fb]);
         if (D % 32)
-          dh[fb] = mma16(IO::ld4(wrow + (D / 32) * 32 + 4 * g), IO::ld4(drow + (D / 32) * 32 + 4 * g), dh[fb]);
+          dh[fb] = mma16(IO::ld4(wrow + (D / 32) * 32 + 4 * g), IO::ld4(rrow + (D / 32) * 32 + 4 * g), dh[fb]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dh[fb][i] = valid ? dh[fb][i] * p.s : 0.f;
+        for (int i = 0; i < 4; ++i) dh[fb][i] *= p.s;
       }
     }
-  } else {
+    float sdh = 0.f;
+    {
+      const E* prow = ps + row * L.mp;
 #pragma unroll
-    for (int fb = 0; fb < MB; ++fb) dh[fb] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-  float sdh = 0.f;
-  if (valid) {
-    const E* src = at<E>(p.dphi, b, h, t);
-    const int64_t frow = (int64_t)t * (p.feat_rot / 2);
+      for (int fb = 0; fb < MB; ++fb) {
+        if (fb < nfb) {
+          float v[4];
+          ld4f<E>(prow + fb * 16 + 4 * g, v);
+          if (p.feat_rot > 0)
+            rope4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, t, valid && fb * 16 + 4 * g < p.feat_rot, true);
 #pragma unroll
-    for (int fb = 0; fb < MB; ++fb) {
-      if (fb < nfb) {
-        float v[4];
-        ld4f<E>(src + fb * 16 + 4 * g, v);
-        if (p.feat_rot > 0) rot4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, frow, true);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dh[fb][i] += v[i];
-          sdh += dh[fb][i] * hv[fb][i];
+          for (int i = 0; i < 4; ++i) {
+            dh[fb][i] += v[i];
+            sdh += dh[fb][i] * hv[fb][i];
+          }
         }
       }
     }
-  }
-  sdh = sum_g(sdh);
-  // dpre -> da (RMSNorm backward); reuse dh as da
-  const bool ok = p.kind != TS_FEAT_RELU2 || mass > p.eps;
-  const float minv = 1.0f / mass;
-  float sdp = 0.f, sda = 0.f;
-#pragma unroll
-  for (int fb = 0; fb < MB; ++fb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float dp = 0.f;
-      if (fb < nfb) {
-        if (p.kind == TS_FEAT_RELU2) {
-          const float pre = a[fb][i] * rinv - tau;
-          dp = ok ? (dh[fb][i] - sdh) * minv * 2.0f * fmaxf(pre, 0.f) : 0.f;
-        } else {
-          dp = p.gain * hv[fb][i] * (dh[fb][i] - sdh);
-        }
-      }
-      dh[fb][i] = dp;
-      sdp += dp;
-      sda += dp * a[fb][i];
-    }
-  }
-  sdp = sum_g(sdp);
-  sda = sum_g(sda);
-  if (p.dtau.ptr && g == 0 && valid) *at<float>(p.dtau, b, h, t) = -sdp;
-  const float c3 = rinv * rinv * rinv * sda / (float)p.m;
-#pragma unroll
-  for (int fb = 0; fb < MB; ++fb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dh[fb][i] = rinv * dh[fb][i] - c3 * a[fb][i];
-  if (valid) {
-    E* da_out = p.da.ptr ? at<E>(p.da, b, h, t) : nullptr;
-    E* h_out = p.h.ptr ? at<E>(p.h, b, h, t) : nullptr;
+    sdh = sum_g(sdh);
+    // dpre -> da (RMSNorm backward); dh becomes da
+    const bool ok = p.kind != TS_FEAT_RELU2 || mass > p.eps;
+    const float minv = rcp(mass);
+    float sdp = 0.f, sda = 0.f;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb) {
-      if (fb < nfb) {
-        float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
-        if (da_out) st4f<E>(da_out + fb * 16 + 4 * g, v);
-        float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
-        if (h_out) st4f<E>(h_out + fb * 16 + 4 * g, u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float dp = 0.f;
+        if (fb < nfb) {
+          if (p.kind == TS_FEAT_RELU2) {
+            const float pre = a[fb][i] * rinv - tau;
+            dp = ok ? (dh[fb][i] - sdh) * minv * 2.0f * fmaxf(pre, 0.f) : 0.f;
+          } else {
+            dp = p.gain * hv[fb][i] * (dh[fb][i] - sdh);
+          }
+        }
+        dh[fb][i] = dp;
+        sdp += dp;
+        sda += dp * a[fb][i];
       }
     }
-  }
+    sdp = sum_g(sdp);
+    sda = sum_g(sda);
+    if (g == 0 && valid) {
+      if (WG) dtau_acc -= sdp;
+      else if (p.dtau.ptr) *rows_of<float>(p.dtau, b, h).at(t) = -sdp;
+    }
+    const float c3 = rinv * rinv * rinv * sda * p.inv_m;
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dh[fb][i] = rinv * dh[fb][i] - c3 * a[fb][i];
 
-  // dxn^T = W1^T da^T  (W1^T given as [D x m])
-  floatx4 dxn[D / 16];
-  gemm_back<E, D, MB>(w1t, wpt, dh, l16, g, nfb, dxn);
-  // residual path, L2-norm backward, input-RoPE backward at dims 16db+4g+i
-  const E* xsrc = at<E>(p.x, b, h, tc);
-  const E* drow = has_resid ? at<E>(p.dresid, b, h, tc) : nullptr;
-  const float inv = 1.0f / fmaxf(nrm, p.eps);
-  const int64_t irow = (int64_t)tc * (p.in_rot / 2);
-  float xr[D / 16][4];
-  float dot = 0.f;
+    if constexpr (WG) {
+      // da over this lane's dphi entries; h for the dW2 contraction
+      E* prow = ps + row * L.mp;
+      E* hrow = hs + row * L.mp;
 #pragma unroll
-  for (int db = 0; db < D / 16; ++db) {
-    ld4f<E>(xsrc + db * 16 + 4 * g, xr[db]);
-    if (p.in_rot > 0) rot4(xr[db], db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, irow, false);
-    if (drow) {
-      float r[4];
-      ld4f<E>(drow + db * 16 + 4 * g, r);
+      for (int fb = 0; fb < MB; ++fb) {
+        if (fb < nfb) {
+          float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
+          st4f<E>(prow + fb * 16 + 4 * g, v);
+          if (has_resid) {
+            float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
+            st4f<E>(hrow + fb * 16 + 4 * g, u);
+          }
+        }
+      }
+    } else if (valid) {
+      E* da_out = p.da.ptr ? rows_of<E>(p.da, b, h).at(t) : nullptr;
+      E* h_out = p.h.ptr ? rows_of<E>(p.h, b, h).at(t) : nullptr;
+      E* xn_out = p.xn.ptr ? rows_of<E>(p.xn, b, h).at(t) : nullptr;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dxn[db][i] += r[i];
+      for (int fb = 0; fb < MB; ++fb) {
+        if (fb < nfb) {
+          float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
+          if (da_out) st4f<E>(da_out + fb * 16 + 4 * g, v);
+          float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
+          if (h_out) st4f<E>(h_out + fb * 16 + 4 * g, u);
+        }
+      }
+      if (xn_out) {
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+          float v[4];
+          ld4f<E>(xrow + db * 16 + 4 * g, v);
+          st4f<E>(xn_out + db * 16 + 4 * g, v);
+        }
+      }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dot += dxn[db][i] * xr[db][i] * inv;
-  }
-  dot = sum_g(dot);
-  if (valid) {
-    E* dst = at<E>(p.dx, b, h, t);
+
+    // dxn^T = W1^T da^T  (W1^T given as [D x m])
+    floatx4 dxn[D / 16];
+    gemm_back<E, D, MB>(w1t, wpt, dh, l16, g, nfb, dxn);
+    // residual path, L2-norm backward, input-RoPE backward at dims 16db+4g+i
+    const float inv = rcp(fmaxf(nrm, p.eps));
+    float dot = 0.f;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-      float v[4];
+      if (has_resid) {
+        float r[4];
+        ld4f<E>(rrow + db * 16 + 4 * g, r);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[i] = nrm > p.eps ? (dxn[db][i] - xr[db][i] * inv * dot) / nrm : dxn[db][i] / p.eps;
-      if (p.in_rot > 0) rot4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, irow, true);
-      st4f<E>(dst + db * 16 + 4 * g, v);
+        for (int i = 0; i < 4; ++i) dxn[db][i] += r[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dot += dxn[db][i] * xr[db][i];
+    }
+    dot = sum_g(dot) * inv * inv;
+    {
+      const bool big = nrm > p.eps;
+      const float scale = big ? rcp(nrm) : rcp(p.eps);
+      E* orow = os + row * L.xp;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (big ? dxn[db][i] - xr[db][i] * dot : dxn[db][i]) * scale;
+        if (p.in_rot > 0)
+          rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, true);
+        st4f<E>(orow + db * 16 + 4 * g, v);
+      }
+    }
+    __syncthreads();  // da, h, xn, dx rows of all four waves complete
+    write_rows<E>(os, L.xp, rows_of<E>(p.dx, b, h), t0, p.T, D, tid);
+
+    if constexpr (WG) {
+      // dW1[f][e] += sum_t da[t][f] xn[t][e];  dW2[e][f] += sum_t dresid[t][e] h[t][f]
+#pragma unroll
+      for (int j = 0; j < (MB + 3) / 4; ++j) {
+        const int fb = w + 4 * j;
+        if (fb < nfb) {
+#pragma unroll
+          for (int kp = 0; kp < 2; ++kp) {
+            const auto fa = TF::get(ps, L.mp, fb * 16, kp, lane);
+            const auto fh = has_resid ? TF::get(hs, L.mp, fb * 16, kp, lane) : fa;
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) {
+              const int k = j * (D / 16) + db;
+              acc1[k] = mma32(fa, TF::get(xs, L.xp, db * 16, kp, lane), acc1[k]);
+              if (has_resid) acc2[k] = mma32(TF::get(rs, L.xp, db * 16, kp, lane), fh, acc2[k]);
+            }
+          }
+        }
+      }
+    }
+  }  // token groups
+
+  if constexpr (WG) {
+    const int part = b * gridDim.x + blockIdx.x;
+    float* d1 = p.dw1_part + ((size_t)part * p.H + h) * (size_t)m * D;
+    float* d2 = p.dw2_part + ((size_t)part * p.H + h) * (size_t)D * m;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int fb = w + 4 * (k / (D / 16)), db = k % (D / 16);
+      if (fb < nfb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          d1[(fb * 16 + 4 * g + i) * D + db * 16 + l16] = acc1[k][i];
+          if (has_resid) d2[(db * 16 + 4 * g + i) * m + fb * 16 + l16] = p.s * acc2[k][i];
+        }
+      }
+    }
+    if (p.dtau_part) {
+      float v = dtau_acc;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      if (lane == 0) red[w] = v;
+      __syncthreads();
+      if (tid == 0) p.dtau_part[(size_t)part * p.H + h] = red[0] + red[1] + red[2] + red[3];
     }
   }
-  }  // token groups
 }
 
 }  // namespace ts
@@ -490,24 +749,45 @@ using ts::fail;
 
 typedef void (*FeatFn)(ts::FeatP);
 
+template <typename E, int D, int MB>
+FeatFn pick3(bool fwd, bool wgrad) {
+  if (fwd) return (FeatFn)ts::feature_fwd_kernel<E, D, MB>;
+  if (wgrad) {
+    if constexpr (ts::wgrad_blocks<D, MB>() <= 8) return (FeatFn)ts::feature_bwd_kernel<E, D, MB, true>;
+    return nullptr;
+  }
+  return (FeatFn)ts::feature_bwd_kernel<E, D, MB, false>;
+}
+
+// Kernels exist for head widths d in {16, 32, 64, 128} and feature widths
+// m in {16, 32, 64, 128, 256} (the feature-block count is a compile-time
+// constant, so no per-block predicates remain in the kernels).
 template <typename E, int D>
-FeatFn pick_mb(int m, bool fwd) {
-  if (m <= 64) return fwd ? (FeatFn)ts::feature_fwd_kernel<E, D, 4> : (FeatFn)ts::feature_bwd_kernel<E, D, 4>;
-  if (m <= 128) return fwd ? (FeatFn)ts::feature_fwd_kernel<E, D, 8> : (FeatFn)ts::feature_bwd_kernel<E, D, 8>;
-  return fwd ? (FeatFn)ts::feature_fwd_kernel<E, D, 16> : (FeatFn)ts::feature_bwd_kernel<E, D, 16>;
+FeatFn pick_mb(int m, bool fwd, bool wgrad) {
+  switch (m) {
+    case 16: return pick3<E, D, 1>(fwd, wgrad);
+    case 32: return pick3<E, D, 2>(fwd, wgrad);
+    case 64: return pick3<E, D, 4>(fwd, wgrad);
+    case 128: return pick3<E, D, 8>(fwd, wgrad);
+    case 256: return pick3<E, D, 16>(fwd, wgrad);
+  }
+  return nullptr;
 }
 
 template <typename E>
-FeatFn pick_feature(int d, int m, bool fwd) {
+FeatFn pick_feature(int d, int m, bool fwd, bool wgrad) {
   switch (d) {
-    case 16: return pick_mb<E, 16>(m, fwd);
-    case 32: return pick_mb<E, 32>(m, fwd);
-    case 48: return pick_mb<E, 48>(m, fwd);
-    case 64: return pick_mb<E, 64>(m, fwd);
-    case 96: return pick_mb<E, 96>(m, fwd);
-    case 128: return pick_mb<E, 128>(m, fwd);
+    case 16: return pick_mb<E, 16>(m, fwd, wgrad);
+    case 32: return pick_mb<E, 32>(m, fwd, wgrad);
+    case 64: return pick_mb<E, 64>(m, fwd, wgrad);
+    case 128: return pick_mb<E, 128>(m, fwd, wgrad);
   }
   return nullptr;
+}
+
+FeatFn pick(const ts_feature_desc* d, bool fwd, bool wgrad) {
+  return d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, fwd, wgrad)
+                             : pick_feature<float>(d->d, d->m, fwd, wgrad);
 }
 
 int check_feature_desc(const ts_feature_desc* d) {
@@ -516,37 +796,82 @@ int check_feature_desc(const ts_feature_desc* d) {
   if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "feature: unknown dtype");
   if (d->kind != TS_FEAT_RELU2 && d->kind != TS_FEAT_SOFTMAX)
     return fail(TS_ERR_NOT_IMPLEMENTED, "feature: kind %d has no fused kernel", d->kind);
-  if (d->m < 16 || d->m > 256 || d->m % 16)
-    return fail(TS_ERR_NOT_IMPLEMENTED, "feature: width m=%d outside 16..256 (multiple of 16)", d->m);
+  if (d->m != 16 && d->m != 32 && d->m != 64 && d->m != 128 && d->m != 256)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature: no fused kernel for feature width m=%d", d->m);
   if (d->in_rot < 0 || d->in_rot > d->d || d->in_rot % 4)
     return fail(TS_ERR_VALUE, "feature: input rotation must be a multiple of 4 within d");
   if (d->feat_rot < 0 || d->feat_rot > d->m || d->feat_rot % 4)
     return fail(TS_ERR_VALUE, "feature: feature rotation must be a multiple of 4 within m");
+  if (!pick(d, true, false)) return fail(TS_ERR_NOT_IMPLEMENTED, "feature: no fused kernel for head width d=%d", d->d);
   return TS_OK;
 }
 
-int launch_feature(FeatFn fn, const ts_feature_desc* d, bool fwd, bool resid, hipStream_t stream, ts::FeatP& p) {
-  if (!fn) return fail(TS_ERR_NOT_IMPLEMENTED, "feature: head width d=%d has no fused kernel", d->d);
+// Stream descriptor for the kernels: 16-byte aligned rows and a time stride
+// whose offsets up to T + 64 rows fit in 32 bits.
+int to_str(const char* name, const ts_strided& s, int esize, int T, ts::Str* out) {
+  *out = ts::Str{const_cast<void*>(s.ptr), s.sb, s.sh, 0};
+  if (!s.ptr) return TS_OK;
+  const int vec = 16 / esize;
+  if (((uintptr_t)s.ptr & 15u) || s.sb % vec || s.sh % vec || s.st % vec || s.st < 0)
+    return fail(TS_ERR_VALUE, "feature: rows of %s must be 16-byte aligned", name);
+  if ((int64_t)(T + ts::TT) * s.st >= ((int64_t)1 << 31))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature: time stride of %s too large", name);
+  out->st = (int)s.st;
+  return TS_OK;
+}
+
+// Per-token fp32 scalar stream (dtau): no alignment requirement.
+int to_str_scalar(const ts_strided& s, int T, ts::Str* out) {
+  *out = ts::Str{const_cast<void*>(s.ptr), s.sb, s.sh, (int)s.st};
+  if (s.ptr && (int64_t)(T + ts::TT) * s.st >= ((int64_t)1 << 31))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature: time stride of dtau too large");
+  return TS_OK;
+}
+
+constexpr size_t kLdsTwoPerCu = 80 * 1024;
+
+struct Plan {
+  bool wgrad;
+  size_t lds;
+  int groups;
+  dim3 grid;
+};
+
+// Weights in LDS: the same compile-time rule as weights_in_lds().
+bool kernel_wl(int es, int d, int m, bool fwd, bool wgrad) {
+  return (size_t)ts::feat_layout(es, d, m, fwd, true, wgrad, true).end * es + 64 <= (size_t)ts::kLdsMax;
+}
+
+size_t lds_bytes(int es, int d, int m, bool fwd, bool resid, bool wgrad) {
+  const bool wl = kernel_wl(es, d, m, fwd, wgrad);
+  return (size_t)ts::feat_layout(es, d, m, fwd, resid, wgrad, wl).end * es + 4 * sizeof(float);
+}
+
+// Launch plan of one call: fused weight gradients when a kernel exists for
+// the shape and its tiles fit in LDS; enough 64-token groups per workgroup
+// to leave about two (backward) or four (forward) resident workgroups per CU.
+int plan_feature(const ts_feature_desc* d, bool fwd, bool resid, bool want_wgrad, Plan* P) {
   const int es = d->dtype == TS_BF16 ? 2 : 4;
-  const int vec = 16 / es;
-  const size_t xs_bytes = (size_t)ts::TT * (d->d + vec) * es;
-  size_t w_bytes = (size_t)d->m * (d->d + vec) * es;              // W1 rows
-  if (fwd) {
-    if (resid) w_bytes += (size_t)d->d * (d->m + vec) * es;       // W2 rows
-  } else {
-    w_bytes += (size_t)d->d * (d->m + vec) * es;                  // W1^T rows
-    if (resid) w_bytes += (size_t)d->m * (d->d + vec) * es;       // W2^T rows
-  }
-  p.w_lds = xs_bytes + w_bytes <= 64 * 1024;
-  const size_t lds = xs_bytes + (p.w_lds ? w_bytes : 0);
-  // Enough token groups per workgroup to amortise the weight staging while
-  // keeping >= 4 workgroups per CU at long sequences.
+  P->wgrad = !fwd && want_wgrad && pick(d, false, true) != nullptr &&
+             lds_bytes(es, d->d, d->m, fwd, resid, true) <= (size_t)ts::kLdsMax;
+  P->lds = lds_bytes(es, d->d, d->m, fwd, resid, P->wgrad);
+  if (P->lds > (size_t)ts::kLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "feature: tiles need %zu bytes of LDS", P->lds);
   const int tiles = (d->T + ts::TT - 1) / ts::TT;
+  const long target = fwd ? 1024 : 512;
   int groups = 1;
-  while (groups < 4 && (long)((tiles + 2 * groups - 1) / (2 * groups)) * d->H * d->B >= 1024) groups *= 2;
-  p.groups = groups;
-  dim3 grid((tiles + groups - 1) / groups, d->H, d->B);
-  hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, p);
+  while (groups < 16 && (long)((tiles + 2 * groups - 1) / (2 * groups)) * d->H * d->B >= target) groups *= 2;
+  P->groups = groups;
+  P->grid = dim3((tiles + groups - 1) / groups, d->H, d->B);
+  return TS_OK;
+}
+
+int launch_feature(FeatFn fn, const Plan& P, hipStream_t stream, ts::FeatP& p) {
+  p.groups = P.groups;
+  if (P.lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)P.lds);
+    if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "feature: LDS request failed: %s", hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(fn, P.grid, dim3(256), P.lds, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "feature: launch failed: %s", hipGetErrorString(e));
   return TS_OK;
@@ -556,7 +881,7 @@ void fill_common(const ts_feature_desc* d, ts::FeatP& p) {
   memset(&p, 0, sizeof(p));
   p.B = d->B; p.H = d->H; p.T = d->T; p.m = d->m;
   p.in_rot = d->in_rot; p.feat_rot = d->feat_rot; p.has_tau = d->has_tau; p.kind = d->kind;
-  p.gain = d->gain; p.s = d->resid_scale; p.eps = d->eps;
+  p.gain = d->gain; p.s = d->resid_scale; p.eps = d->eps; p.inv_m = 1.0f / (float)d->m;
 }
 
 }  // namespace
@@ -571,14 +896,27 @@ int ts_feature_fwd(const ts_feature_desc* d, const ts_feature_io* io, hipStream_
   if (d->has_tau && !io->tau) return fail(TS_ERR_VALUE, "feature: missing tau");
   if ((d->in_rot && (!io->in_cos || !io->in_sin)) || (d->feat_rot && (!io->f_cos || !io->f_sin)))
     return fail(TS_ERR_VALUE, "feature: missing rope tables");
-  if (d->T == 0) return TS_OK;
+  const int es = d->dtype == TS_BF16 ? 2 : 4;
   ts::FeatP p;
   fill_common(d, p);
-  p.x = io->x; p.phi = io->phi; p.resid = io->resid;
+  if ((rc = to_str("x", io->x, es, d->T, &p.x)) || (rc = to_str("phi", io->phi, es, d->T, &p.phi)) ||
+      (rc = to_str("resid", io->resid, es, d->T, &p.resid)))
+    return rc;
+  if (d->T == 0) return TS_OK;
   p.w1 = io->w1; p.w2 = io->w2; p.tau = io->tau;
   p.in_cos = io->in_cos; p.in_sin = io->in_sin; p.f_cos = io->f_cos; p.f_sin = io->f_sin;
-  FeatFn fn = d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, true) : pick_feature<float>(d->d, d->m, true);
-  return launch_feature(fn, d, true, io->resid.ptr != nullptr, stream, p);
+  Plan P;
+  if ((rc = plan_feature(d, true, io->resid.ptr != nullptr, false, &P))) return rc;
+  return launch_feature(pick(d, true, false), P, stream, p);
+}
+
+int ts_feature_bwd_parts(const ts_feature_desc* d, int32_t has_dresid, int32_t* parts) {
+  int rc = check_feature_desc(d);
+  if (rc) return rc;
+  Plan P;
+  if ((rc = plan_feature(d, false, has_dresid != 0, true, &P))) return rc;
+  if (parts) *parts = P.wgrad ? (int32_t)(P.grid.x * P.grid.z) : 0;
+  return TS_OK;
 }
 
 int ts_feature_bwd(const ts_feature_desc* d, const ts_feature_bwd_io* io, hipStream_t stream) {
@@ -590,15 +928,33 @@ int ts_feature_bwd(const ts_feature_desc* d, const ts_feature_bwd_io* io, hipStr
   if (d->has_tau && !io->tau) return fail(TS_ERR_VALUE, "feature bwd: missing tau");
   if ((d->in_rot && (!io->in_cos || !io->in_sin)) || (d->feat_rot && (!io->f_cos || !io->f_sin)))
     return fail(TS_ERR_VALUE, "feature bwd: missing rope tables");
-  if (d->T == 0) return TS_OK;
+  const int es = d->dtype == TS_BF16 ? 2 : 4;
   ts::FeatP p;
   fill_common(d, p);
-  p.x = io->x; p.w1 = io->w1; p.w1t = io->w1t; p.w2t = io->w2t; p.tau = io->tau;
+  if ((rc = to_str("x", io->x, es, d->T, &p.x)) || (rc = to_str("dphi", io->dphi, es, d->T, &p.dphi)) ||
+      (rc = to_str("dx", io->dx, es, d->T, &p.dx)) || (rc = to_str("dresid", io->dresid, es, d->T, &p.dresid)))
+    return rc;
+  const bool want_wgrad = io->dw1_part != nullptr;
+  if (!want_wgrad) {
+    if ((rc = to_str("da", io->da, es, d->T, &p.da)) || (rc = to_str("xn", io->xn, es, d->T, &p.xn)) ||
+        (rc = to_str("h", io->h, es, d->T, &p.h)) || (rc = to_str_scalar(io->dtau, d->T, &p.dtau)))
+      return rc;
+  }
+  Plan P;
+  if ((rc = plan_feature(d, false, io->dresid.ptr != nullptr, want_wgrad, &P))) return rc;
+  if (want_wgrad && !P.wgrad)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature bwd: no fused weight-gradient kernel for d=%d m=%d", d->d, d->m);
+  if (want_wgrad && io->dresid.ptr && !io->dw2_part)
+    return fail(TS_ERR_VALUE, "feature bwd: fused weight gradients with dresid need dw2_part");
+  if (want_wgrad && d->has_tau && !io->dtau_part)
+    return fail(TS_ERR_VALUE, "feature bwd: fused weight gradients with tau need dtau_part");
+  if (d->T == 0) return TS_OK;
+  p.w1 = io->w1; p.w1t = io->w1t; p.w2t = io->w2t; p.tau = io->tau;
   p.in_cos = io->in_cos; p.in_sin = io->in_sin; p.f_cos = io->f_cos; p.f_sin = io->f_sin;
-  p.dphi = io->dphi; p.dresid = io->dresid; p.dx = io->dx; p.da = io->da; p.xn = io->xn; p.h = io->h;
-  p.dtau = io->dtau;
-  FeatFn fn = d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, false) : pick_feature<float>(d->d, d->m, false);
-  return launch_feature(fn, d, false, io->dresid.ptr != nullptr, stream, p);
+  if (want_wgrad) {
+    p.dw1_part = io->dw1_part; p.dw2_part = io->dw2_part; p.dtau_part = io->dtau_part;
+  }
+  return launch_feature(pick(d, false, P.wgrad), P, stream, p);
 }
 
 }  // extern "C"

@@ -80,6 +80,9 @@ def _ext_arg(ext):
     return _lib.EXT_ARRAY, ext.to(torch.float32)
 
 
+MAX_WIDTH = 128  # widest key / value width one kernel launch handles
+
+
 def scan_launch(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -100,7 +103,80 @@ def scan_launch(
     want_final: bool = False,
     seg_chunks: int = 0,
 ):
-    """One kernel scan.  Returns ``(out, ext_out, final_state)``.
+    """One scan (several kernel launches when a width exceeds ``MAX_WIDTH``).
+
+    Returns ``(out, ext_out, final_state)`` as :func:`_scan_once`.  The scan
+    is linear in each operand, so wide values split into independent value
+    chunks and wide keys into key chunks whose results add up.
+    """
+    dk, dv = q.shape[-1], v.shape[-1]
+    if dk <= MAX_WIDTH and dv <= MAX_WIDTH:
+        return _scan_once(q, k, v, retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse,
+                          q_ext=q_ext, k_ext=k_ext, v_ext=v_ext, out=out, out_mode=out_mode, out_scale=out_scale,
+                          want_ext_out=want_ext_out, ext_out=ext_out, want_final=want_final,
+                          seg_chunks=seg_chunks)
+    if want_final:
+        raise NotImplementedError(f"hip scan: final state of widths dk={dk} dv={dv} above {MAX_WIDTH}")
+    kw = dict(retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse, seg_chunks=seg_chunks)
+    B, H, T = q.shape[:3]
+    if dv > MAX_WIDTH:
+        pieces, ext_res = [], ext_out
+        for i, c0 in enumerate(range(0, dv, MAX_WIDTH)):
+            vs = v[..., c0:c0 + MAX_WIDTH]
+            o_i = None if out is None else out[..., c0:c0 + vs.shape[-1]]
+            r, e, _ = scan_launch(q, k, vs, q_ext=q_ext, k_ext=k_ext, v_ext=v_ext if i == 0 else None,
+                                  out=o_i, out_mode=out_mode, out_scale=out_scale,
+                                  want_ext_out=want_ext_out and i == 0, ext_out=ext_out if i == 0 else None, **kw)
+            pieces.append(r)
+            if i == 0:
+                ext_res = e
+        result = out if out is not None else torch.cat(pieces, dim=-1)
+        return result, ext_res, None
+    # dk > MAX_WIDTH: accumulate fp32 partial scans over key chunks
+    acc = None if out_mode == _lib.OUT_ACCUM_F32 else torch.zeros(B, H, T, dv, dtype=torch.float32,
+                                                                  device=q.device)
+    target = out if out_mode == _lib.OUT_ACCUM_F32 else acc
+    eacc = None
+    if want_ext_out:
+        eacc = ext_out if out_mode == _lib.OUT_ACCUM_F32 else torch.zeros(B, H, T, dtype=torch.float32,
+                                                                           device=q.device)
+    scale = out_scale if out_mode != _lib.OUT_STORE else 1.0
+    for i, c0 in enumerate(range(0, dk, MAX_WIDTH)):
+        first = i == 0
+        _scan_once(q[..., c0:c0 + MAX_WIDTH], k[..., c0:c0 + MAX_WIDTH], v,
+                   q_ext=q_ext if first else None, k_ext=k_ext if first else None, v_ext=v_ext,
+                   out=target, out_mode=_lib.OUT_ACCUM_F32, out_scale=scale,
+                   want_ext_out=want_ext_out, ext_out=eacc, **kw)
+    if out_mode == _lib.OUT_ACCUM_F32:
+        return out, ext_out, None
+    if out_mode == _lib.OUT_STORE_F32:
+        result = acc if out is None else out.copy_(acc)
+    else:
+        result = acc.to(q.dtype) if out is None else out.copy_(acc)
+    return result, eacc, None
+
+
+def _scan_once(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    retention: int = _lib.RET_NONE,
+    log_alpha: torch.Tensor | None = None,
+    decay: torch.Tensor | None = None,
+    reverse: bool = False,
+    q_ext=None,
+    k_ext=None,
+    v_ext=None,
+    out: torch.Tensor | None = None,
+    out_mode: int = _lib.OUT_STORE,
+    out_scale: float = 1.0,
+    want_ext_out: bool = False,
+    ext_out: torch.Tensor | None = None,
+    want_final: bool = False,
+    seg_chunks: int = 0,
+):
+    """One kernel launch.  Returns ``(out, ext_out, final_state)``.
 
     ``out`` is ``[B,H,T,dv]``; ``ext_out`` (fp32 ``[B,H,T]``) is the result
     column of the ``v`` ext column; ``final_state`` is the fp32
@@ -155,7 +231,7 @@ def scan_launch(
         ext_out = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
     final = None
     if want_final:
-        final = torch.empty(B * H, c_dkp.value, c_dvp.value, dtype=torch.float32, device=q.device)
+        final = torch.zeros(B * H, c_dkp.value, c_dvp.value, dtype=torch.float32, device=q.device)
     workspace = None
     if ws_bytes.value:
         workspace = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)

@@ -467,7 +467,7 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
 template <int D, int MB>
 constexpr int wgrad_blocks() { return ((MB + 3) / 4) * (D / 16); }
 
-template <typename E, int D, int MB, bool WG>
+template <typename E, int D, int MB, bool WG, bool RESID>
 __global__ __launch_bounds__(256) void feature_bwd_kernel(FeatP p) {
   typedef LdsIO<E> IO;
   typedef TokFrag<E> TF;
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256) void feature_bwd_kernel(FeatP p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
   constexpr int nfb = MB;
   const int m = MB * 16;
-  const bool has_resid = p.dresid.ptr != nullptr;
+  constexpr bool has_resid = RESID;
   const FeatLayout L = feat_layout((int)sizeof(E), D, m, false, has_resid, WG, WL);
   extern __shared__ __align__(16) unsigned char smem[];
   E* base = (E*)smem;
@@ -750,44 +750,47 @@ using ts::fail;
 typedef void (*FeatFn)(ts::FeatP);
 
 template <typename E, int D, int MB>
-FeatFn pick3(bool fwd, bool wgrad) {
+FeatFn pick3(bool fwd, bool wgrad, bool resid) {
   if (fwd) return (FeatFn)ts::feature_fwd_kernel<E, D, MB>;
   if (wgrad) {
-    if constexpr (ts::wgrad_blocks<D, MB>() <= 8) return (FeatFn)ts::feature_bwd_kernel<E, D, MB, true>;
+    if constexpr (ts::wgrad_blocks<D, MB>() <= 8)
+      return resid ? (FeatFn)ts::feature_bwd_kernel<E, D, MB, true, true>
+                   : (FeatFn)ts::feature_bwd_kernel<E, D, MB, true, false>;
     return nullptr;
   }
-  return (FeatFn)ts::feature_bwd_kernel<E, D, MB, false>;
+  return resid ? (FeatFn)ts::feature_bwd_kernel<E, D, MB, false, true>
+               : (FeatFn)ts::feature_bwd_kernel<E, D, MB, false, false>;
 }
 
 // Kernels exist for head widths d in {16, 32, 64, 128} and feature widths
 // m in {16, 32, 64, 128, 256} (the feature-block count is a compile-time
 // constant, so no per-block predicates remain in the kernels).
 template <typename E, int D>
-FeatFn pick_mb(int m, bool fwd, bool wgrad) {
+FeatFn pick_mb(int m, bool fwd, bool wgrad, bool resid) {
   switch (m) {
-    case 16: return pick3<E, D, 1>(fwd, wgrad);
-    case 32: return pick3<E, D, 2>(fwd, wgrad);
-    case 64: return pick3<E, D, 4>(fwd, wgrad);
-    case 128: return pick3<E, D, 8>(fwd, wgrad);
-    case 256: return pick3<E, D, 16>(fwd, wgrad);
+    case 16: return pick3<E, D, 1>(fwd, wgrad, resid);
+    case 32: return pick3<E, D, 2>(fwd, wgrad, resid);
+    case 64: return pick3<E, D, 4>(fwd, wgrad, resid);
+    case 128: return pick3<E, D, 8>(fwd, wgrad, resid);
+    case 256: return pick3<E, D, 16>(fwd, wgrad, resid);
   }
   return nullptr;
 }
 
 template <typename E>
-FeatFn pick_feature(int d, int m, bool fwd, bool wgrad) {
+FeatFn pick_feature(int d, int m, bool fwd, bool wgrad, bool resid) {
   switch (d) {
-    case 16: return pick_mb<E, 16>(m, fwd, wgrad);
-    case 32: return pick_mb<E, 32>(m, fwd, wgrad);
-    case 64: return pick_mb<E, 64>(m, fwd, wgrad);
-    case 128: return pick_mb<E, 128>(m, fwd, wgrad);
+    case 16: return pick_mb<E, 16>(m, fwd, wgrad, resid);
+    case 32: return pick_mb<E, 32>(m, fwd, wgrad, resid);
+    case 64: return pick_mb<E, 64>(m, fwd, wgrad, resid);
+    case 128: return pick_mb<E, 128>(m, fwd, wgrad, resid);
   }
   return nullptr;
 }
 
-FeatFn pick(const ts_feature_desc* d, bool fwd, bool wgrad) {
-  return d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, fwd, wgrad)
-                             : pick_feature<float>(d->d, d->m, fwd, wgrad);
+FeatFn pick(const ts_feature_desc* d, bool fwd, bool wgrad, bool resid = false) {
+  return d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, fwd, wgrad, resid)
+                             : pick_feature<float>(d->d, d->m, fwd, wgrad, resid);
 }
 
 int check_feature_desc(const ts_feature_desc* d) {
@@ -954,7 +957,7 @@ int ts_feature_bwd(const ts_feature_desc* d, const ts_feature_bwd_io* io, hipStr
   if (want_wgrad) {
     p.dw1_part = io->dw1_part; p.dw2_part = io->dw2_part; p.dtau_part = io->dtau_part;
   }
-  return launch_feature(pick(d, false, P.wgrad), P, stream, p);
+  return launch_feature(pick(d, false, P.wgrad, io->dresid.ptr != nullptr), P, stream, p);
 }
 
 }  // extern "C"

@@ -2,26 +2,35 @@
 //
 // One view of the reference's chunk backend
 // (src/thetascan/_core/ops/scan_chunk.py:246-339): the sequence is cut into
-// 64-token tiles; inside a tile the causal score block is a bf16 (or fp32)
-// MFMA contraction with fp32 accumulation, and across tiles an fp32
+// 64-token tiles; inside a tile the causal score block is an MFMA contraction
+// (bf16 or fp32 operands, fp32 accumulation), and across tiles an fp32
 // [dk, dv] state carries everything already written.
 //
-// Work decomposition (one workgroup per (batch*head, segment)):
+// Work decomposition (one workgroup of four waves per (batch*head, segment)):
 //   1. summary kernel : each segment of `seg_chunks` tiles folds its own
 //                       writes into a local state U_p (no queries needed);
-//   2. prefix kernel  : exclusive scan of U_p over segments with the decay
-//                       of each segment -> the state entering every segment;
+//   2. prefix kernel  : exclusive scan of U_p over segments with the decay of
+//                       each segment -> the state entering every segment;
 //   3. main kernel    : each segment re-walks its tiles from that incoming
 //                       state and writes the outputs.
 // This turns B*H sequential scans (64 at the benchmark shape) into B*H*nseg
 // independent workgroups so the whole chip is busy.
 //
-// Inside a workgroup wave w owns value block w (16 value columns): it holds
-// the state S[:, 16w:16w+16] in registers (MFMA accumulator layout) and
-// produces out[:, 16w:16w+16].  The score tile is computed once and shared
-// through LDS.  Orientation (O^T = S^T Q^T + V^T P^T, S += K_w^T V) is chosen
-// so the register state feeds the next MFMA directly as an operand, with the
-// contraction index permuted consistently in both operands.
+// Inside a tile, wave w owns query block w (16 queries) and value block(s)
+// w (+4): it computes the causal scores of its own queries only (no score is
+// computed twice), keeps them in MFMA accumulator registers and feeds them
+// straight into the P.V contraction for every value block; the carried state
+// enters through a bf16 copy of the state that each wave publishes in LDS for
+// its own value block.  The fp32 state itself never leaves the owning wave's
+// registers.  One barrier per tile.
+//
+// Extra "ext" columns (the key-mass unit column of the normalized read and
+// its gradient) are rank-1 terms and never widen an MFMA tile:
+//   key-side ext  (q_ext x k_ext): score += qe_t ke_i; the state gains a row
+//                 u = sum_i w ke_i v_i (a [dv] vector), read as qe_t u;
+//   value-side ext (v_ext):        out_ext_t = sum_i w s_ti ve_i + <q_t, D>,
+//                 D = sum_i w ve_i k_i (a [dk] vector).
+// Both vector states are MFMA contractions against a broadcast ext row.
 
 #include "ts_common.h"
 #include "thetascan_hip.h"
@@ -69,7 +78,7 @@ __device__ __forceinline__ void bstf(rsrc_t r, uint32_t off, float v) {
 
 struct ScanP {
   int B, H, T, dk, dv, dvp;
-  int nchunks, seg_chunks, nseg, nsum;
+  int nchunks, seg_chunks, nseg, nsum, nelem;
   int ret, reverse;
   int q_ext, k_ext, v_ext;
   int out_mode;
@@ -78,7 +87,7 @@ struct ScanP {
   // bytes spanned by one (batch, head) slice of each tensor
   uint32_t q_rec, k_rec, v_rec, qe_rec, ke_rec, ve_rec, dec_rec, out_rec, oe_rec;
   const float* log_alpha;
-  float* seg;     // [BH][nseg][DKP][dvp]
+  float* seg;     // [BH][nseg][nelem]: S [DK][dvp], u [dvp], D [DK]
   float* segdec;  // [BH][nseg]
 };
 
@@ -97,24 +106,17 @@ __device__ __forceinline__ uint32_t row_off(const ScanP& p, int t0, int row, int
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
-// Token-axis operand fragments.  Contractions over the 64 tokens of a tile
-// are split into two 32-token halves kp; within a half, lane group g = lane/16
-// supplies the tokens {4g..4g+3} and {16+4g..16+4g+3} (offset 32kp).  This is
-// exactly the token set that the accumulator fragment of a 16x16 score block
-// holds per lane (rows 4g..4g+3 of key blocks 2kp and 2kp+1), so score
-// fragments feed the P.V contraction without a shuffle.
-//
-// bf16: tiles stay row-major in LDS and the fragment is read with the gfx950
-// LDS transpose read (ds_read_b64_tr_b16): within each 16-lane group, lane j
-// addresses row r0 + j/4, column c0 + 4*(j%4), and lane i receives
-// M[r0 .. r0+3][c0 + i].
-// fp32: tiles are additionally stored transposed ([feature][token]).
-template <typename E> struct Tiles;
-
-template <> struct Tiles<bf16> {
-  static constexpr bool kTransposedCopy = false;
-  // lane: column c0 + (lane & 15), the eight tokens of half kp for group lane >> 4
-  static __device__ __forceinline__ bf16x8 tcol8(const bf16* rows, int pitch, int c0, int kp, int lane) {
+// Token-axis operand fragment of a token-major LDS tile: column c0 + (lane & 15),
+// tokens {32kp+4g..+3} and {32kp+16+4g..+3} for lane group g = lane >> 4.
+// This is exactly the token set the accumulator fragments of two 16x16
+// score blocks 2kp, 2kp+1 hold per lane, so score fragments feed the P.V
+// contraction without a shuffle.  bf16 uses the gfx950 transposing LDS read
+// (ds_read_b64_tr_b16: within each 16-lane group, lane j addresses row
+// r0 + j/4, column c0 + 4*(j%4), and lane i receives rows r0..r0+3 of
+// column c0 + i); fp32 gathers.
+template <typename E> struct Tok;
+template <> struct Tok<bf16> {
+  static __device__ __forceinline__ bf16x8 col8(const bf16* rows, int pitch, int c0, int kp, int lane) {
     const int g = lane >> 4, j = lane & 15;
     const bf16* a = rows + (32 * kp + 4 * g + (j >> 2)) * pitch + c0 + 4 * (j & 3);
     shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)a);
@@ -122,19 +124,19 @@ template <> struct Tiles<bf16> {
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
 };
-
-template <> struct Tiles<float> {
-  static constexpr bool kTransposedCopy = true;
-  static __device__ __forceinline__ floatx8 tcol8(const float* cols, int pitch, int c0, int kp, int lane) {
+template <> struct Tok<float> {
+  static __device__ __forceinline__ floatx8 col8(const float* rows, int pitch, int c0, int kp, int lane) {
     const int g = lane >> 4, l16 = lane & 15;
-    const float* a = cols + (c0 + l16) * pitch + 32 * kp + 4 * g;
-    return LdsIO<float>::cat(LdsIO<float>::ld4(a), LdsIO<float>::ld4(a + 16));
+    floatx8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = rows[(32 * kp + (e < 4 ? 4 * g + e : 12 + 4 * g + e)) * pitch + c0 + l16];
+    return v;
   }
 };
 
 // Feature-axis fragment of row `row` for contraction block j (32 features):
-// features {32j+4g..+3} and {32j+16+4g..+3}, the order in which the state's
-// accumulator fragments S[2j], S[2j+1] hold them.
+// features {32j+4g..+3} and {32j+16+4g..+3}.  Queries are loaded in the same
+// order, and the state's accumulator fragments hold their rows that way.
 template <typename E>
 __device__ __forceinline__ typename Frag<E>::f8 frow8(const E* rows, int pitch, int row, int j, int g) {
   const E* a = rows + row * pitch + 32 * j + 4 * g;
@@ -145,114 +147,122 @@ __device__ __forceinline__ typename Frag<E>::f4 frow4(const E* rows, int pitch, 
   return LdsIO<E>::ld4(rows + row * pitch + 32 * j + 4 * g);
 }
 
-// Register-staged loader (bf16) of one tile section (Q, K or V rows): each
-// thread owns SLOTS 16-byte vectors, vector idx = tid + i * NT, row-major over
-// the section's padded width.  Section sizes are multiples of 64 vectors, so
-// whether slot i is in range is uniform per wave.  Per slot only the row and
-// column (meta) and the byte offset of that row in tile 0 are kept; a tile
-// adds a uniform offset.
-template <typename E, int SLOTS>
-struct SecLoader {
-  static constexpr int VEC = 16 / (int)sizeof(E);
-  uint32_t off0[SLOTS];  // data (or ext column) byte offset at tile t = 0
-  int meta[SLOTS];       // row | c0 << 8 | kind << 16 ; kind 0 data, 1 ext ones, 2 ext array, 3 pad
-  uint4 r[SLOTS];
-  float ev[SLOTS];
+// A broadcast operand: eight fp32 LDS values (the same two runs of four a
+// frow8 / col8 fragment covers), identical for every lane of the group.
+template <typename E>
+__device__ __forceinline__ typename Frag<E>::f8 bcast8(const float* vec, int base, int g, float scale = 1.0f) {
+  typename Frag<E>::f8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = cvt<E>(scale * vec[base + (e < 4 ? 4 * g + e : 12 + 4 * g + e)]);
+  return r;
+}
+template <typename E>
+__device__ __forceinline__ typename Frag<E>::f4 bcast4(const float* vec, int base, int g) {
+  typename Frag<E>::f4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = cvt<E>(vec[base + 4 * g + e]);
+  return r;
+}
 
-  __device__ __forceinline__ static int kind_of(int c0, int width, int ext_mode) {
-    return c0 < width ? 0 : (c0 == width && ext_mode != TS_EXT_NONE ? ext_mode : 3);
-  }
-  __device__ __forceinline__ void setup(const ScanP& p, int n, int per_row, int width, int ext_mode, int st_b,
-                                        int est_b, int tid, int NT) {
+// Register-staged loader of one [64 x width] tile section: each thread owns
+// SLOTS 16-byte vectors (vector idx = tid + i * 256, row-major over the padded
+// width).  Sections are multiples of 64 vectors, so whether a slot is in range
+// is uniform per wave.  Per slot the byte offset at tile 0 and the LDS offset
+// are kept; a tile adds a uniform byte offset.
+template <typename E, int SLOTS>
+struct TileLoader {
+  static constexpr int VEC = 16 / (int)sizeof(E);
+  uint32_t off0[SLOTS];
+  int lds[SLOTS];
+  uint4 r[SLOTS];
+
+  __device__ __forceinline__ void setup(const ScanP& p, int per_row, int width, int pitch, int st_b, int tid) {
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
-      const int idx = tid + i * NT;
+      const int idx = tid + i * 256;
       const int row = idx / per_row;
       const int c0 = (idx - row * per_row) * VEC;
-      const int kind = idx < n ? kind_of(c0, width, ext_mode) : 3;
-      meta[i] = (row & 255) | (c0 << 8) | (kind << 16);
-      off0[i] = kind == 0 ? row_off(p, 0, row, st_b) + (uint32_t)(c0 * sizeof(E))
-                          : (kind == TS_EXT_ARRAY ? row_off(p, 0, row, est_b) : kOOB);
+      lds[i] = idx < C * per_row ? row * pitch + c0 : -1;
+      off0[i] = c0 < width ? row_off(p, 0, row, st_b) + (uint32_t)(c0 * (int)sizeof(E)) : kOOB;
     }
   }
-  // Registers <- rows of the tile starting at t0.
-  __device__ __forceinline__ void fetch(const ScanP& p, rsrc_t data, rsrc_t ext, int ext_mode, int n, int st_b,
-                                        int est_b, int t0, int sgn, int wave_first, int NT) {
+  __device__ __forceinline__ void fetch(rsrc_t data, int t0, int sgn, int st_b, int wave_first, int n) {
     const uint32_t delta = (uint32_t)(sgn * t0 * st_b);
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
-      if (wave_first + i * NT >= n) break;  // uniform
-      const int kind = meta[i] >> 16;
-      r[i] = bld16(data, kind == 0 ? off0[i] + delta : kOOB);
-      if (ext_mode == TS_EXT_ARRAY) {
-        const uint32_t edelta = (uint32_t)(sgn * t0 * est_b);
-        ev[i] = bldf(ext, kind == TS_EXT_ARRAY ? off0[i] + edelta : kOOB);
-      } else if (ext_mode == TS_EXT_ONES) {
-        ev[i] = (t0 + (meta[i] & 255) < p.T) ? 1.0f : 0.0f;
-      }
+      if (wave_first + i * 256 >= n) break;  // uniform
+      r[i] = bld16(data, off0[i] == kOOB ? kOOB : off0[i] + delta);
     }
   }
-  // LDS rows (pitch in elements) <- registers.
-  __device__ __forceinline__ void store(E* dst, int pitch, int ext_mode, int n, int wave_first, int NT) {
+  __device__ __forceinline__ void store(E* dst, int wave_first, int n) const {
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) {
-      if (wave_first + i * NT >= n) break;  // uniform
-      const int m = meta[i];
-      const int row = m & 255, c0 = (m >> 8) & 255, kind = m >> 16;
-      Vec16<E> val;
-      val.raw = r[i];
-      if (ext_mode != TS_EXT_NONE && (kind == TS_EXT_ONES || kind == TS_EXT_ARRAY)) val.e[0] = cvt<E>(ev[i]);
-      *(uint4*)(dst + row * pitch + c0) = val.raw;
+      if (wave_first + i * 256 >= n) break;  // uniform
+      *(uint4*)(dst + lds[i]) = r[i];
     }
   }
 };
 
-// Slots per thread for a section of `width` padded columns when the kernel
-// runs `nt_min` or more threads.
-constexpr int sec_slots(int width, int vec, int nt_min) { return (C * width / vec + nt_min - 1) / nt_min; }
-constexpr int nt_min_of(int maxw) { return maxw == 4 ? 256 : (maxw == 5 ? 320 : 384); }
-// V-section slots: the largest over the value widths a kernel with `maxw`
-// waves serves (one wave per 16 value columns, at least four waves).
-constexpr int v_slots(int maxw, int vec) {
-  int best = 1;
-  for (int dvp = maxw == 4 ? 16 : (maxw == 5 ? 80 : 96); dvp <= maxw * 16; dvp += 16) {
-    const int nt = (dvp / 16 < 4 ? 4 : dvp / 16) * 64;
-    const int s = (C * dvp / vec + nt - 1) / nt;
-    if (s > best) best = s;
-  }
-  return best;
+// LDS carve-up (elements of E unless noted), shared with the host.
+struct ScanLayout {
+  int kp, vp;        // row pitches of K / V / state tiles
+  int stage;         // elements per stage: K [C][kp], V [C][vp]
+  int stages;
+  int st;            // state copy [dvp][kp] (MAIN), `nst` buffers
+  int nst;
+  int fbase;         // float offset (in floats, from the byte end of the E part)
+  int bytes;
+};
+
+__host__ __device__ constexpr int scan_stages(int esize) { return esize == 2 ? 2 : 1; }
+
+// Float region after the E tiles (per stage: ke[C], ve[C]; then u[2][dvp],
+// D[2][DK], pw[68], lloc[4][C]).
+__host__ __device__ inline ScanLayout scan_layout(int esize, int DK, int dvp, bool main_kernel) {
+  const int vec = 16 / esize;
+  ScanLayout L{};
+  L.kp = DK + vec;
+  L.vp = dvp + vec;
+  L.stage = C * L.kp + C * L.vp;
+  L.stages = scan_stages(esize);
+  L.nst = main_kernel ? (esize == 2 ? 2 : 1) : 0;
+  L.st = dvp * L.kp;
+  const int e_elems = L.stages * L.stage + L.nst * L.st;
+  const int e_bytes = (e_elems * esize + 15) / 16 * 16;
+  L.fbase = e_bytes / 4;
+  const int floats = L.stages * 2 * C + 2 * dvp + 2 * DK + 68 + 4 * C;
+  L.bytes = e_bytes + floats * 4;
+  return L;
 }
 
 // GEN = false compiles the common case only: no retention, no ext columns,
-// plain stores, no ext output (the host picks it whenever a call allows).
-template <typename E, int DKP, bool MAIN, int MAXW, bool GEN>
-__global__ __launch_bounds__(MAXW * 64) void scan_kernel(ScanP p) {
+// plain stores (the host picks it whenever a call allows).
+template <typename E, int DK, int NVW, bool MAIN, bool GEN>
+__global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   typedef typename Frag<E>::f8 F8;
   typedef typename Frag<E>::f4 F4;
   typedef LdsIO<E> IO;
-  typedef Tiles<E> TL;
+  typedef Tok<E> TK;
   constexpr int ES = (int)sizeof(E);
   constexpr int VEC = 16 / ES;
-  constexpr bool QREG = MAIN && ES == 2 && DKP <= 80;  // Q fragments straight from HBM to registers
-  constexpr bool QLDS = MAIN && !QREG;                 // Q staged through LDS
-  constexpr int STAGES = ES == 2 ? 2 : 1;
-  constexpr int KP = DKP + VEC;  // row pitch of Q / K tiles (elements)
-  constexpr int TP = C + VEC;    // row pitch of transposed copies (fp32)
-  constexpr int NK32 = DKP / 32;
-  constexpr bool KTAIL = (DKP % 32) != 0;
-  constexpr int NKB = DKP / 16;
-  constexpr int SLOTS_K = sec_slots(DKP, VEC, nt_min_of(MAXW));
-  constexpr int SLOTS_V = v_slots(MAXW, VEC);
+  constexpr int NK32 = DK / 32;
+  constexpr bool KTAIL = (DK % 32) != 0;
+  constexpr int NKB = DK / 16;
+  constexpr int NKO = (NKB + 3) / 4;         // key blocks of D owned per wave
+  constexpr int STAGES = scan_stages(ES);
+  constexpr int SLOTS_K = (C * DK / VEC + 255) / 256;
+  constexpr int SLOTS_V = (C * 64 * NVW / VEC + 255) / 256;
 
   const int ret = GEN ? p.ret : TS_RET_NONE;
   const int q_ext = GEN ? p.q_ext : TS_EXT_NONE;
   const int k_ext = GEN ? p.k_ext : TS_EXT_NONE;
   const int v_ext = GEN ? p.v_ext : TS_EXT_NONE;
+  const bool kx = q_ext != TS_EXT_NONE && k_ext != TS_EXT_NONE;  // key-side rank-1 term
+  const bool vx = v_ext != TS_EXT_NONE;
   const int out_mode = GEN ? p.out_mode : TS_OUT_STORE;
   const bool has_oe = GEN && p.oe.ptr != nullptr;
 
   const int tid = threadIdx.x;
-  const int NT = blockDim.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int g = lane >> 4;
@@ -262,52 +272,34 @@ __global__ __launch_bounds__(MAXW * 64) void scan_kernel(ScanP p) {
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int dvp = p.dvp;
-  const int NWV = dvp >> 4;
-  const bool owner = w < NWV;
-  const int VP = dvp + VEC;  // row pitch of V tiles (bf16)
+  const int nvb = dvp >> 4;
   const int sgn = p.reverse ? -1 : 1;
+  const int wave_first = __builtin_amdgcn_readfirstlane(tid & ~63);
 
   // ---- LDS carve-up
+  const ScanLayout L = scan_layout(ES, DK, dvp, MAIN);
   extern __shared__ __align__(16) unsigned char smem[];
-  const int q_elems = QLDS ? C * KP : 0;
-  const int k_elems = C * KP;
-  const int kt_elems = TL::kTransposedCopy ? DKP * TP : 0;
-  const int v_elems = TL::kTransposedCopy ? dvp * TP : C * VP;
-  const int stage_elems = q_elems + k_elems + kt_elems + v_elems;
-  E* stage0 = (E*)smem;
-  float* s_pw = (float*)(stage0 + STAGES * stage_elems);  // alpha^d, d = 0..64 (static)
-  float* s_lloc = s_pw + 68;                              // per-wave tile log-decay (stream)
-  float* my_lloc = s_lloc + w * C;
+  E* ebase = (E*)smem;
+  E* st_base = ebase + STAGES * L.stage;
+  float* fb = (float*)smem + L.fbase;
+  float* s_ext = fb;                              // [stage][ke C | ve C]
+  float* s_u = s_ext + STAGES * 2 * C;            // [2][dvp]
+  float* s_d = s_u + 2 * dvp;                     // [2][DK]
+  float* s_pw = s_d + 2 * DK;                     // alpha^d, d = 0..64 (static)
+  float* my_lloc = s_pw + 68 + w * C;             // per-wave tile log-decay (stream)
 
-  // ---- per-(b, h) addressing.  Section 0 is Q, 1 is K, 2 is V.
-  auto sec_stream = [&](int sec) -> const ts_strided& { return sec == 0 ? p.q : (sec == 1 ? p.k : p.v); };
-  const int nq_vec = QLDS ? C * (DKP / VEC) : 0;
-  const int nk_vec = C * (DKP / VEC);
-  const int nv_vec = C * (dvp / VEC);
-  const int n_vec = nq_vec + nk_vec + nv_vec;
+  // ---- per-(b, h) addressing
   const int64_t bh_q = (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
   const int64_t bh_k = (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
   const int64_t bh_v = (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
-  // Buffer resources are rebuilt where used from these scalars, so they do
-  // not stay live in scalar registers across the tile loop.
-  auto data_rsrc = [&](int sec) -> rsrc_t {
-    if (sec == 0) return make_rsrc((const E*)p.q.ptr + bh_q, p.q_rec);
-    if (sec == 1) return make_rsrc((const E*)p.k.ptr + bh_k, p.k_rec);
-    return make_rsrc((const E*)p.v.ptr + bh_v, p.v_rec);
-  };
-  auto ext_rsrc = [&](int sec) -> rsrc_t {
-    const ts_strided& e = sec == 0 ? p.qe : (sec == 1 ? p.ke : p.ve);
-    const uint32_t rec = sec == 0 ? p.qe_rec : (sec == 1 ? p.ke_rec : p.ve_rec);
-    return make_rsrc(bh_base(e, b, h, 4), rec);
-  };
-  auto ext_mode_of = [&](int sec) -> int { return sec == 0 ? q_ext : (sec == 1 ? k_ext : v_ext); };
-  auto st_bytes = [&](int sec) -> int { return (int)sec_stream(sec).st * ES; };
-  auto est_bytes = [&](int sec) -> int { return (int)(sec == 0 ? p.qe.st : (sec == 1 ? p.ke.st : p.ve.st)) * 4; };
-  auto width_of = [&](int sec) -> int { return sec == 2 ? p.dv : p.dk; };
-  auto per_row_of = [&](int sec) -> int { return sec == 2 ? dvp / VEC : DKP / VEC; };
-
-  // ---- retention addressing
+  const int q_st_b = (int)p.q.st * ES;
+  const int k_st_b = (int)p.k.st * ES;
+  const int v_st_b = (int)p.v.st * ES;
   const int dec_st_b = (int)p.decay.st * 4;
+  auto k_rsrc = [&]() { return make_rsrc((const E*)p.k.ptr + bh_k, p.k_rec); };
+  auto v_rsrc = [&]() { return make_rsrc((const E*)p.v.ptr + bh_v, p.v_rec); };
+  auto q_rsrc = [&]() { return make_rsrc((const E*)p.q.ptr + bh_q, p.q_rec); };
+
   // a(s), the decay applied when stepping into logical position s: a reversed
   // scan steps from physical s+1 down to s and uses the decay of the physical
   // successor (logical s = 0 has none).
@@ -317,22 +309,25 @@ __global__ __launch_bounds__(MAXW * 64) void scan_kernel(ScanP p) {
     const uint32_t off = (s < p.T && src < p.T) ? (uint32_t)(src * dec_st_b) : kOOB;
     return bldf(make_rsrc(bh_base(p.decay, b, h, 4), p.dec_rec), off);
   };
+  // ext value of token t0 + row for an ext column (ones or fp32 array)
+  auto ext_of = [&](int mode, const ts_strided& e, uint32_t rec, int t0, int row) -> float {
+    if (mode == TS_EXT_ONES) return t0 + row < p.T ? 1.0f : 0.0f;
+    return bldf(make_rsrc(bh_base(e, b, h, 4), rec), row_off(p, t0, row, (int)e.st * 4));
+  };
 
-  // ---- state
-  floatx4 S[NKB];
+  // ---- state: value blocks vb = w + 4r owned by this wave
+  floatx4 S[NVW][NKB];
+  floatx4 us[NVW];   // u for the owned value blocks (every row the same)
+  floatx4 dst_[NKO]; // D for the owned key blocks kb = w + 4r (every row the same)
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) S[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
-  bool state_zero = true;
-  if (MAIN && seg > 0) {
-    state_zero = false;
-    if (owner) {
-      const float* src = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)(DKP * dvp);
+  for (int r = 0; r < NVW; ++r) {
+    us[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) S[kb][i] = src[(kb * 16 + 4 * g + i) * dvp + w * 16 + l16];
-    }
+    for (int kb = 0; kb < NKB; ++kb) S[r][kb] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
+#pragma unroll
+  for (int r = 0; r < NKO; ++r) dst_[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+
   const float la = ret == TS_RET_STATIC ? p.log_alpha[h] : 0.0f;
   if (ret == TS_RET_STATIC && w == 0) {
     s_pw[lane] = expf(la * (float)lane);
@@ -342,84 +337,95 @@ __global__ __launch_bounds__(MAXW * 64) void scan_kernel(ScanP p) {
   const int c_begin = seg * p.seg_chunks;
   const int c_end = min(c_begin + p.seg_chunks, p.nchunks);
   float seg_log = 0.0f;
+  bool state_zero = true;
 
-  // ---- tile loading --------------------------------------------------------
-  const int wave_first = __builtin_amdgcn_readfirstlane(tid & ~63);
-  SecLoader<E, QLDS ? SLOTS_K : 1> ldq;
-  SecLoader<E, SLOTS_K> ldk;
-  SecLoader<E, SLOTS_V> ldv;
-  if constexpr (STAGES == 2) {
-    if constexpr (QLDS)
-      ldq.setup(p, nq_vec, DKP / VEC, p.dk, q_ext, st_bytes(0), est_bytes(0), tid, NT);
-    ldk.setup(p, nk_vec, DKP / VEC, p.dk, k_ext, st_bytes(1), est_bytes(1), tid, NT);
-    ldv.setup(p, nv_vec, dvp / VEC, p.dv, v_ext, st_bytes(2), est_bytes(2), tid, NT);
-  }
-  // Registers <- tile starting at t0.
-  auto fetch = [&](int t0) {
-    if constexpr (QLDS)
-      ldq.fetch(p, data_rsrc(0), ext_rsrc(0), q_ext, nq_vec, st_bytes(0), est_bytes(0), t0, sgn, wave_first, NT);
-    ldk.fetch(p, data_rsrc(1), ext_rsrc(1), k_ext, nk_vec, st_bytes(1), est_bytes(1), t0, sgn, wave_first, NT);
-    ldv.fetch(p, data_rsrc(2), ext_rsrc(2), v_ext, nv_vec, st_bytes(2), est_bytes(2), t0, sgn, wave_first, NT);
-  };
-  // Stage `st` <- registers.
-  auto store = [&](int st) {
-    E* base = stage0 + st * stage_elems;
-    if constexpr (QLDS) ldq.store(base, KP, q_ext, nq_vec, wave_first, NT);
-    ldk.store(base + q_elems, KP, k_ext, nk_vec, wave_first, NT);
-    ldv.store(base + q_elems + k_elems + kt_elems, VP, v_ext, nv_vec, wave_first, NT);
-  };
-  // fp32: synchronous load of tile t0 into the single stage (row-major Q, K;
-  // transposed K^T, V^T).
-  auto load_sync = [&](int t0) {
-    E* Qs = stage0;
-    E* Ks = Qs + q_elems;
-    E* KTs = Ks + k_elems;
-    E* VTs = KTs + kt_elems;
-    for (int idx = tid; idx < n_vec; idx += NT) {
-      const int sec = idx < nq_vec ? 0 : (idx < nq_vec + nk_vec ? 1 : 2);
-      const int j = idx - (sec == 2 ? nq_vec + nk_vec : (sec == 1 ? nq_vec : 0));
-      const int per_row = per_row_of(sec);
-      const int row = j / per_row;
-      const int c0 = (j - row * per_row) * VEC;
-      const int kind = SecLoader<E, 1>::kind_of(c0, width_of(sec), ext_mode_of(sec));
-      Vec16<E> val;
-      val.raw = bld16(data_rsrc(sec), kind == 0 ? row_off(p, t0, row, st_bytes(sec)) + (uint32_t)(c0 * ES) : kOOB);
-      if (kind == TS_EXT_ARRAY) val.e[0] = cvt<E>(bldf(ext_rsrc(sec), row_off(p, t0, row, est_bytes(sec))));
-      if (kind == TS_EXT_ONES) val.e[0] = cvt<E>(t0 + row < p.T ? 1.0f : 0.0f);
-      if (sec == 0) {
-        *(uint4*)(Qs + row * KP + c0) = val.raw;
-      } else if (sec == 1) {
-        *(uint4*)(Ks + row * KP + c0) = val.raw;
+  // publish the state entering a tile (bf16 / fp32 copy, u, D) into buffer `bi`
+  auto publish = [&](int bi) {
+    E* st = st_base + bi * L.st;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) KTs[(c0 + e) * TP + row] = val.e[e];
-      } else {
+    for (int r = 0; r < NVW; ++r) {
+      const int vb = w + 4 * r;
+      if (vb < nvb) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) VTs[(c0 + e) * TP + row] = val.e[e];
+        for (int kb = 0; kb < NKB; ++kb)
+          IO::st4(st + (vb * 16 + l16) * L.kp + kb * 16 + 4 * g, S[r][kb][0], S[r][kb][1], S[r][kb][2], S[r][kb][3]);
+        if (kx && g == 0) s_u[bi * dvp + vb * 16 + l16] = us[r][0];
+      }
+    }
+    if (vx && g == 0) {
+#pragma unroll
+      for (int r = 0; r < NKO; ++r) {
+        const int kb = w + 4 * r;
+        if (kb < NKB) s_d[bi * DK + kb * 16 + l16] = dst_[r][0];
       }
     }
   };
 
-  // ---- Q fragments in registers (bf16, narrow keys)
-  constexpr int NQJ = QREG ? NK32 : 1;
-  F8 qr[4][NQJ];
-  F4 qt[4];
-  const int q_st_b = (int)p.q.st * ES;
-  auto qload = [&](int t0, int qb) {
-    if constexpr (QREG) {
-      const uint32_t ro = row_off(p, t0, qb * 16 + l16, q_st_b);
-      float qev = 0.0f;
-      if (q_ext == TS_EXT_ARRAY) qev = bldf(ext_rsrc(0), row_off(p, t0, qb * 16 + l16, est_bytes(0)));
-      else if (q_ext == TS_EXT_ONES) qev = t0 + qb * 16 + l16 < p.T ? 1.0f : 0.0f;
-      auto part = [&](int c) -> bf16x4 {
-        uint2 raw = bld8(data_rsrc(0), c < p.dk ? ro + (uint32_t)(c * ES) : kOOB);
-        bf16x4 v = __builtin_bit_cast(bf16x4, raw);
-        if (q_ext != TS_EXT_NONE && c == p.dk) v[0] = (bf16)qev;
-        return v;
-      };
+  if (MAIN && seg > 0) {
+    state_zero = false;
+    const float* src = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)p.nelem;
 #pragma unroll
-      for (int j = 0; j < NK32; ++j) qr[qb][j] = IO::cat(part(32 * j + 4 * g), part(32 * j + 16 + 4 * g));
-      if (KTAIL) qt[qb] = part(32 * NK32 + 4 * g);
+    for (int r = 0; r < NVW; ++r) {
+      const int vb = w + 4 * r;
+      if (vb < nvb) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S[r][kb][i] = src[(kb * 16 + 4 * g + i) * dvp + vb * 16 + l16];
+        const float u = src[DK * dvp + vb * 16 + l16];
+        us[r] = floatx4{u, u, u, u};
+      }
     }
+#pragma unroll
+    for (int r = 0; r < NKO; ++r) {
+      const int kb = w + 4 * r;
+      if (kb < NKB) {
+        const float d = src[DK * dvp + dvp + kb * 16 + l16];
+        dst_[r] = floatx4{d, d, d, d};
+      }
+    }
+  }
+
+  // ---- tile loading
+  const int nk_vec = C * (DK / VEC);
+  const int nv_vec = C * (dvp / VEC);
+  TileLoader<E, SLOTS_K> ldk;
+  TileLoader<E, SLOTS_V> ldv;
+  ldk.setup(p, DK / VEC, p.dk, L.kp, k_st_b, tid);
+  ldv.setup(p, dvp / VEC, p.dv, L.vp, v_st_b, tid);
+  float ext_r = 0.0f;  // this thread's ke (wave 0) / ve (wave 1) of the fetched tile
+  auto fetch = [&](int t0) {
+    ldk.fetch(k_rsrc(), t0, sgn, k_st_b, wave_first, nk_vec);
+    ldv.fetch(v_rsrc(), t0, sgn, v_st_b, wave_first, nv_vec);
+    if (w == 0 && kx) ext_r = ext_of(k_ext, p.ke, p.ke_rec, t0, lane);
+    if (w == 1 && vx) ext_r = ext_of(v_ext, p.ve, p.ve_rec, t0, lane);
+  };
+  auto store = [&](int stg) {
+    E* base = ebase + stg * L.stage;
+    ldk.store(base, wave_first, nk_vec);
+    ldv.store(base + C * L.kp, wave_first, nv_vec);
+    if (w < 2) s_ext[stg * 2 * C + w * C + lane] = ext_r;
+  };
+
+  // ---- queries of this wave's block (registers)
+  F8 qr[NK32 > 0 ? NK32 : 1];
+  F4 qt;
+  float qe = 0.0f;
+  auto qload = [&](int t0) {
+    const int row = w * 16 + l16;
+    const uint32_t ro = row_off(p, t0, row, q_st_b);
+    auto part = [&](int c) -> F4 {
+      const uint32_t off = c < p.dk ? ro + (uint32_t)(c * ES) : kOOB;
+      if constexpr (ES == 2) {
+        return __builtin_bit_cast(F4, bld8(q_rsrc(), off));
+      } else {
+        return __builtin_bit_cast(F4, bld16(q_rsrc(), off));
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < NK32; ++j) qr[j] = IO::cat(part(32 * j + 4 * g), part(32 * j + 16 + 4 * g));
+    if (KTAIL) qt = part(32 * NK32 + 4 * g);
+    if (kx) qe = ext_of(q_ext, p.qe, p.qe_rec, t0, row);
   };
 
   // ---- output addressing
@@ -427,56 +433,53 @@ __global__ __launch_bounds__(MAXW * 64) void scan_kernel(ScanP p) {
   const void* out_base = bh_base(p.out, b, h, osz);
   const int out_st_b = (int)p.out.st * osz;
   const int oe_st_b = (int)p.oe.st * 4;
-  const int ocol = w * 16 + 4 * g;  // first of this lane's 4 value columns
-  const uint32_t ocol_off = ocol < p.dv ? (uint32_t)(ocol * osz) : kOOB;
-  const int oext_r = p.dv - ocol;   // 0..3 if this lane holds the ext column
 
   // ---- prologue
   float dcur = 0.0f, dnext = 0.0f;
   if constexpr (STAGES == 2) {
     fetch(c_begin * C);
-    if constexpr (QREG) {
-#pragma unroll
-      for (int qb = 0; qb < 4; ++qb) qload(c_begin * C, qb);
-    }
-    if (ret == TS_RET_STREAM && owner) dnext = decay_of(c_begin * C);
+    if (ret == TS_RET_STREAM) dnext = decay_of(c_begin * C);
     store(c_begin & 1);
     if (c_begin + 1 < c_end) fetch((c_begin + 1) * C);
-    __syncthreads();
   }
+  if (MAIN) {
+    qload(c_begin * C);
+    if (!state_zero) publish(c_begin & (L.nst - 1));
+  }
+  if constexpr (STAGES == 2) __syncthreads();
 
   for (int c = c_begin; c < c_end; ++c) {
     const int t0 = c * C;
     const int len = min(C, p.T - t0);
-    const E* base;
+    const E* Ks;
+    const float* ext_s;
     if constexpr (STAGES == 2) {
       if (c + 1 < c_end) store((c + 1) & 1);
       if (c + 2 < c_end) fetch(t0 + 2 * C);
-      base = stage0 + (c & 1) * stage_elems;
-      if (ret == TS_RET_STREAM && owner) {
+      Ks = ebase + (c & 1) * L.stage;
+      ext_s = s_ext + (c & 1) * 2 * C;
+      if (ret == TS_RET_STREAM) {
         dcur = dnext;
         if (c + 1 < c_end) dnext = decay_of(t0 + C);
       }
     } else {
       __syncthreads();  // the previous tile is no longer read
-      load_sync(t0);
-      if (ret == TS_RET_STREAM && owner) dcur = decay_of(t0);
+      fetch(t0);
+      store(0);
+      if (ret == TS_RET_STREAM) dcur = decay_of(t0);
       __syncthreads();
-      base = stage0;
+      Ks = ebase;
+      ext_s = s_ext;
     }
-    const E* Qs = base;
-    const E* Ks = base + q_elems;
-    const E* KTs = Ks + k_elems;
-    const E* Vs = KTs + kt_elems;
-    const E* Kt_src = TL::kTransposedCopy ? KTs : Ks;
-    const int kt_pitch = TL::kTransposedCopy ? TP : KP;
-    const int vt_pitch = TL::kTransposedCopy ? TP : VP;
+    const E* Vs = Ks + C * L.kp;
+    const float* ke_s = ext_s;
+    const float* ve_s = ext_s + C;
 
     // ---- retention of this tile (per wave)
     float tile_log = 0.0f;
     if (ret == TS_RET_STATIC) {
       tile_log = la * (float)len;
-    } else if (ret == TS_RET_STREAM && owner) {
+    } else if (ret == TS_RET_STREAM) {
       float x = dcur;
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {
@@ -488,159 +491,224 @@ __global__ __launch_bounds__(MAXW * 64) void scan_kernel(ScanP p) {
     }
     seg_log += tile_log;
 
-    if (owner) {
-      // value fragments of this wave's 16 columns, both token halves
-      F8 av[2];
+    if constexpr (MAIN) {
+      const int query = w * 16 + l16;
+      const float lq = ret == TS_RET_STREAM ? my_lloc[query] : 0.0f;
+      const float cw = ret == TS_RET_STATIC ? s_pw[query + 1] : (ret == TS_RET_STREAM ? expf(lq) : 1.0f);
+      // ---- causal scores of this query block: sc[kb] = D[key][query], kb <= w
+      floatx4 sc[4];
 #pragma unroll
-      for (int kp = 0; kp < 2; ++kp) av[kp] = TL::tcol8(Vs, vt_pitch, w * 16, kp, lane);
-
-      if constexpr (MAIN) {
-        F8 sA[NK32 > 0 ? NK32 : 1];
-        F4 sT;
-        if (!state_zero) {
+      for (int kb = 0; kb < 4; ++kb) {
+        sc[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (kb > w) continue;
+        const int krow = kb * 16 + l16;
 #pragma unroll
-          for (int j = 0; j < NK32; ++j) sA[j] = IO::from_acc(S[2 * j], S[2 * j + 1]);
-          if (KTAIL) sT = IO::from_acc4(S[NKB - 1]);
+        for (int j = 0; j < NK32; ++j) sc[kb] = mma32(frow8<E>(Ks, L.kp, krow, j, g), qr[j], sc[kb]);
+        if (KTAIL) sc[kb] = mma16(frow4<E>(Ks, L.kp, krow, NK32, g), qt, sc[kb]);
+        floatx4 lk;
+        if (ret == TS_RET_STREAM) lk = *(const floatx4*)(my_lloc + kb * 16 + 4 * g);
+        floatx4 kev;
+        if (kx) kev = *(const floatx4*)(ke_s + kb * 16 + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb * 16 + 4 * g + i;
+          float s = sc[kb][i];
+          if (kx) s += qe * kev[i];
+          float wt = 1.0f;
+          if (ret == TS_RET_STATIC) wt = s_pw[max(query - key, 0)];
+          else if (ret == TS_RET_STREAM) wt = expf(fminf(lq - lk[i], 0.0f));
+          sc[kb][i] = (kb < w || key <= query) ? s * wt : 0.0f;
         }
-#pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
-          const int query = qb * 16 + l16;
-          auto qfrag = [&](int j) -> F8 {
-            if constexpr (QREG) return qr[qb][j];
-            else return frow8<E>(Qs, KP, query, j, g);
-          };
-          auto qtail = [&]() -> F4 {
-            if constexpr (QREG) return qt[qb];
-            else return frow4<E>(Qs, KP, query, NK32, g);
-          };
-          float lq = 0.0f;
-          if (ret == TS_RET_STREAM) lq = my_lloc[query];
-          // causal score blocks (key block kb <= qb): D[key][query]
-          floatx4 sc[4];
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            sc[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
-            if (kb > qb) continue;
-            const int krow = kb * 16 + l16;
-#pragma unroll
-            for (int j = 0; j < NK32; ++j) sc[kb] = mma32(frow8<E>(Ks, KP, krow, j, g), qfrag(j), sc[kb]);
-            if (KTAIL) sc[kb] = mma16(frow4<E>(Ks, KP, krow, NK32, g), qtail(), sc[kb]);
-            floatx4 lk;
-            if (ret == TS_RET_STREAM) lk = *(const floatx4*)(my_lloc + kb * 16 + 4 * g);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = kb * 16 + 4 * g + i;
-              float wt = 1.0f;
-              if (ret == TS_RET_STATIC) wt = s_pw[max(query - key, 0)];
-              else if (ret == TS_RET_STREAM) wt = expf(fminf(lq - lk[i], 0.0f));
-              sc[kb][i] = (kb < qb || key <= query) ? sc[kb][i] * wt : 0.0f;
-            }
-          }
-          // O^T = carry * S^T Q^T + V^T P^T
-          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-          if (!state_zero) {
-#pragma unroll
-            for (int j = 0; j < NK32; ++j) acc = mma32(sA[j], qfrag(j), acc);
-            if (KTAIL) acc = mma16(sT, qtail(), acc);
-            if (ret != TS_RET_NONE) {
-              const float cw = ret == TS_RET_STATIC ? s_pw[query + 1] : expf(lq);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) acc[i] *= cw;
-            }
-          }
-          acc = mma32(av[0], IO::from_acc(sc[0], sc[1]), acc);
-          if (qb >= 2) acc = mma32(av[1], IO::from_acc(sc[2], sc[3]), acc);
-          if constexpr (QREG) {
-            if (c + 1 < c_end) qload(t0 + C, qb);  // next tile's queries of this block
-          }
+      }
+      const F8 p0 = IO::from_acc(sc[0], sc[1]);
+      const F8 p1 = IO::from_acc(sc[2], sc[3]);
+      const E* st = st_base + (c & (L.nst - 1)) * L.st;
+      const float* u_in = s_u + (c & (L.nst - 1)) * dvp;
+      const float* d_in = s_d + (c & (L.nst - 1)) * DK;
 
-          // ---- output rows
-          const uint32_t ro = row_off(p, t0, query, out_st_b);
-          if (out_mode == TS_OUT_STORE) {
-            if constexpr (ES == 2) {
-              bf16x4 o;
+      // ---- outputs O^T[v][query] = cw (S^T Q^T)[v] + (V^T P^T)[v], every value block
+      const uint32_t ro = row_off(p, t0, query, out_st_b);
+      const rsrc_t out_rs = make_rsrc(out_base, p.out_rec);
 #pragma unroll
-              for (int i = 0; i < 4; ++i) o[i] = (bf16)acc[i];
-              bst8(make_rsrc(out_base, p.out_rec), ro + ocol_off, __builtin_bit_cast(uint2, o));
-            } else {
-              bst16(make_rsrc(out_base, p.out_rec), ro + ocol_off, __builtin_bit_cast(uint4, acc));
-            }
+      for (int vb = 0; vb < 4 * NVW; ++vb) {
+        if (vb >= nvb) break;
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (!state_zero) {
+          const int vrow = vb * 16 + l16;
+#pragma unroll
+          for (int j = 0; j < NK32; ++j) acc = mma32(frow8<E>(st, L.kp, vrow, j, g), qr[j], acc);
+          if (KTAIL) acc = mma16(frow4<E>(st, L.kp, vrow, NK32, g), qt, acc);
+          if (kx) {
+            const floatx4 u4 = *(const floatx4*)(u_in + vb * 16 + 4 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += qe * u4[i];
+          }
+          if (ret != TS_RET_NONE) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] *= cw;
+          }
+        }
+        acc = mma32(TK::col8(Vs, L.vp, vb * 16, 0, lane), p0, acc);
+        if (w >= 2) acc = mma32(TK::col8(Vs, L.vp, vb * 16, 1, lane), p1, acc);
+
+        const int ocol = vb * 16 + 4 * g;
+        const uint32_t ooff = ocol < p.dv ? ro + (uint32_t)(ocol * osz) : kOOB;
+        if (out_mode == TS_OUT_STORE) {
+          if constexpr (ES == 2) {
+            bf16x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (bf16)acc[i];
+            bst8(out_rs, ooff, __builtin_bit_cast(uint2, o));
           } else {
-            floatx4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = p.out_scale * acc[i];
-            if (out_mode == TS_OUT_ACCUM_F32) {
-              const floatx4 prev = __builtin_bit_cast(floatx4, bld16(make_rsrc(out_base, p.out_rec), ro + ocol_off));
-#pragma unroll
-              for (int i = 0; i < 4; ++i) o[i] += prev[i];
-            }
-            bst16(make_rsrc(out_base, p.out_rec), ro + ocol_off, __builtin_bit_cast(uint4, o));
+            bst16(out_rs, ooff, __builtin_bit_cast(uint4, acc));
           }
-          if (has_oe && oext_r >= 0 && oext_r < 4) {
-            float val = acc[0];
-            if (oext_r == 1) val = acc[1];
-            if (oext_r == 2) val = acc[2];
-            if (oext_r == 3) val = acc[3];
-            if (out_mode != TS_OUT_STORE) val *= p.out_scale;
-            const uint32_t eo = row_off(p, t0, query, oe_st_b);
-            const rsrc_t oe_rs = make_rsrc(bh_base(p.oe, b, h, 4), p.oe_rec);
-            if (out_mode == TS_OUT_ACCUM_F32) val += bldf(oe_rs, eo);
-            bstf(oe_rs, eo, val);
+        } else {
+          floatx4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = p.out_scale * acc[i];
+          if (out_mode == TS_OUT_ACCUM_F32) {
+            const floatx4 prev = __builtin_bit_cast(floatx4, bld16(out_rs, ooff));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] += prev[i];
           }
+          bst16(out_rs, ooff, __builtin_bit_cast(uint4, o));
         }
       }
 
-      // ---- state update: S = decay(tile) * S + K^T diag(wk) V
-      F8 avw[2] = {av[0], av[1]};
-      if (ret != TS_RET_NONE) {
-        const float cdec = ret == TS_RET_STATIC ? s_pw[len] : expf(tile_log);
+      // ---- value-side ext column: out_ext = cw <q, D> + sum_keys P ve
+      if (vx) {
+        floatx4 oacc = {0.f, 0.f, 0.f, 0.f};
+        if (!state_zero) {
+#pragma unroll
+          for (int j = 0; j < NK32; ++j) oacc = mma32(bcast8<E>(d_in, 32 * j, g), qr[j], oacc);
+          if (KTAIL) oacc = mma16(bcast4<E>(d_in, 32 * NK32, g), qt, oacc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[i] *= cw;
+        }
+        oacc = mma32(bcast8<E>(ve_s, 0, g), p0, oacc);
+        if (w >= 2) oacc = mma32(bcast8<E>(ve_s, 32, g), p1, oacc);
+        if (has_oe && g == 0) {
+          float val = oacc[0];
+          if (out_mode != TS_OUT_STORE) val *= p.out_scale;
+          const uint32_t eo = row_off(p, t0, query, oe_st_b);
+          const rsrc_t oe_rs = make_rsrc(bh_base(p.oe, b, h, 4), p.oe_rec);
+          if (out_mode == TS_OUT_ACCUM_F32) val += bldf(oe_rs, eo);
+          bstf(oe_rs, eo, val);
+        }
+      }
+      if (c + 1 < c_end) qload(t0 + C);  // next tile's queries of this block
+    }
+
+    // ---- state update: S = decay(tile) * S + K^T diag(wk) V (owned value blocks)
+    const float cdec = ret == TS_RET_STATIC ? s_pw[len] : (ret == TS_RET_STREAM ? expf(tile_log) : 1.0f);
+    floatx4 wk4[2][2];  // per-key weights of this lane's keys {32kp+4g+i, 32kp+16+4g+i}
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = 32 * kp + 16 * hf + 4 * g + i;
+          float wk = 1.0f;
+          if (ret == TS_RET_STATIC) wk = key < len ? s_pw[len - 1 - key] : 0.0f;
+          else if (ret == TS_RET_STREAM) wk = key < len ? expf(tile_log - my_lloc[key]) : 0.0f;
+          wk4[kp][hf][i] = wk;
+        }
+#pragma unroll
+    for (int r = 0; r < NVW; ++r) {
+      const int vb = w + 4 * r;
+      if (vb >= nvb) break;
+      F8 avw[2];
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        avw[kp] = TK::col8(Vs, L.vp, vb * 16, kp, lane);
+        if (ret != TS_RET_NONE) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) avw[kp][e] = cvt<E>(tof(avw[kp][e]) * wk4[kp][e >> 2][e & 3]);
+        }
+      }
+      if (ret != TS_RET_NONE && !(MAIN && state_zero)) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) S[kb][i] *= cdec;
+          for (int i = 0; i < 4; ++i) S[r][kb][i] *= cdec;
 #pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-          floatx4 l0, l1;
-          if (ret == TS_RET_STREAM) {
-            l0 = *(const floatx4*)(my_lloc + 32 * kp + 4 * g);
-            l1 = *(const floatx4*)(my_lloc + 32 * kp + 16 + 4 * g);
-          }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int key = 32 * kp + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4);
-            float wk = 0.0f;
-            if (key < len) {
-              if (ret == TS_RET_STATIC) wk = s_pw[len - 1 - key];
-              else wk = expf(tile_log - (e < 4 ? l0[e] : l1[e - 4]));
-            }
-            avw[kp][e] = cvt<E>(tof(av[kp][e]) * wk);
-          }
-        }
+        for (int i = 0; i < 4; ++i) us[r][i] *= cdec;
       }
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int kp = 0; kp < 2; ++kp) S[kb] = mma32(TL::tcol8(Kt_src, kt_pitch, kb * 16, kp, lane), avw[kp], S[kb]);
+        for (int kp = 0; kp < 2; ++kp) S[r][kb] = mma32(TK::col8(Ks, L.kp, kb * 16, kp, lane), avw[kp], S[r][kb]);
+      if (kx) {
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) us[r] = mma32(bcast8<E>(ke_s, 32 * kp, g), avw[kp], us[r]);
+      }
+    }
+    if (vx) {
+      // D = decay * D + K^T (wk ve): a broadcast (wk ve) row against K columns
+#pragma unroll
+      for (int r = 0; r < NKO; ++r) {
+        const int kb = w + 4 * r;
+        if (kb >= NKB) break;
+        if (ret != TS_RET_NONE) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst_[r][i] *= cdec;
+        }
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+          F8 a;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int key = 32 * kp + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+            a[e] = cvt<E>(ve_s[key] * wk4[kp][e >> 2][e & 3]);
+          }
+          dst_[r] = mma32(a, TK::col8(Ks, L.kp, kb * 16, kp, lane), dst_[r]);
+        }
+      }
     }
     state_zero = false;
+    if constexpr (MAIN) {
+      if (c + 1 < c_end) {
+        if constexpr (STAGES == 1) __syncthreads();  // single state copy: readers of this tile are done
+        publish((c + 1) & (L.nst - 1));
+      }
+    }
     if constexpr (STAGES == 2) __syncthreads();
   }
 
   if constexpr (!MAIN) {
-    if (owner) {
-      float* dst = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)(DKP * dvp);
+    float* dst = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)p.nelem;
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
+    for (int r = 0; r < NVW; ++r) {
+      const int vb = w + 4 * r;
+      if (vb < nvb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * dvp + w * 16 + l16] = S[kb][i];
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * dvp + vb * 16 + l16] = S[r][kb][i];
+        if (g == 0) dst[DK * dvp + vb * 16 + l16] = us[r][0];
+      }
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int r = 0; r < NKO; ++r) {
+        const int kb = w + 4 * r;
+        if (kb < NKB) dst[DK * dvp + dvp + kb * 16 + l16] = dst_[r][0];
+      }
     }
     if (tid == 0) p.segdec[(size_t)bh * p.nseg + seg] = seg_log;
   }
 }
 
 // Exclusive scan of the segment summaries:  seg[p] <- state entering segment p.
-__global__ void scan_prefix_kernel(float* seg, const float* segdec, float* final_state, int nseg,
-                                   int nsum, int nelem) {
+// With `fin`, the state after the last token is also written in the exact
+// [dk + kx][dv + vx] layout (ext row / column last).
+struct FinalP {
+  float* fin;
+  int DK, dvp, dk, dv, kx, vx;
+};
+
+__global__ void scan_prefix_kernel(float* seg, const float* segdec, FinalP F, int nseg, int nsum, int nelem) {
   const int bh = blockIdx.y;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= nelem) return;
@@ -652,7 +720,21 @@ __global__ void scan_prefix_kernel(float* seg, const float* segdec, float* final
     base[(size_t)s * nelem] = carry;
     if (s < nsum) carry = expf(segdec[(size_t)bh * nseg + s]) * carry + u;
   }
-  if (final_state) final_state[(size_t)bh * nelem + e] = carry;
+  if (F.fin) {
+    const int rows = F.dk + F.kx, cols = F.dv + F.vx;
+    float* out = F.fin + (size_t)bh * rows * cols;
+    const int ns = F.DK * F.dvp;
+    if (e < ns) {
+      const int f = e / F.dvp, v = e - f * F.dvp;
+      if (f < F.dk && v < F.dv) out[f * cols + v] = carry;
+    } else if (e < ns + F.dvp) {
+      const int v = e - ns;
+      if (F.kx && v < F.dv) out[F.dk * cols + v] = carry;
+    } else {
+      const int f = e - ns - F.dvp;
+      if (F.vx && f < F.dk) out[f * cols + F.dv] = carry;
+    }
+  }
 }
 
 }  // namespace ts
@@ -676,7 +758,7 @@ namespace {
 
 using ts::fail;
 
-const int kDkPads[] = {32, 64, 80, 128, 144};
+const int kDkPads[] = {16, 32, 64, 128};
 
 int pick_dkp(int need) {
   for (int v : kDkPads)
@@ -685,7 +767,8 @@ int pick_dkp(int need) {
 }
 
 struct Layout {
-  int dkp, dvp, nchunks, seg_chunks, nseg, nsum;
+  int dkp, dvp, nvw, nchunks, seg_chunks, nseg, nsum, nelem;
+  bool kx, vx;
   size_t ws_bytes;
 };
 
@@ -696,15 +779,21 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "scan: unknown dtype");
   if (d->retention < TS_RET_NONE || d->retention > TS_RET_STREAM)
     return fail(TS_ERR_VALUE, "scan: unknown retention kind");
+  for (int e : {d->q_ext, d->k_ext, d->v_ext})
+    if (e < TS_EXT_NONE || e > TS_EXT_ARRAY) return fail(TS_ERR_VALUE, "scan: unknown ext column kind");
   const int vec = d->dtype == TS_BF16 ? 8 : 4;
   if (d->dk % vec || d->dv % vec)
     return fail(TS_ERR_VALUE, "scan: feature widths must be multiples of 16 bytes (dk=%d dv=%d)",
                 d->dk, d->dv);
-  const int dk_eff = d->dk + ((d->q_ext != TS_EXT_NONE || d->k_ext != TS_EXT_NONE) ? 1 : 0);
-  L->dkp = pick_dkp(dk_eff);
-  if (L->dkp < 0) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: key width %d exceeds 144", dk_eff);
-  L->dvp = ((d->dv + (d->v_ext != TS_EXT_NONE ? 1 : 0)) + 15) / 16 * 16;
-  if (L->dvp > 144) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: value width %d exceeds 144", L->dvp);
+  L->kx = d->q_ext != TS_EXT_NONE && d->k_ext != TS_EXT_NONE;
+  L->vx = d->v_ext != TS_EXT_NONE;
+  if (L->kx && L->vx)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: key-side and value-side ext columns together");
+  L->dkp = pick_dkp(d->dk);
+  if (L->dkp < 0) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: key width %d exceeds 128", d->dk);
+  L->dvp = (d->dv + 15) / 16 * 16;
+  if (L->dvp > 128) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: value width %d exceeds 128", d->dv);
+  L->nvw = L->dvp <= 64 ? 1 : 2;
   L->nchunks = (d->T + ts::C - 1) / ts::C;
   const int bh = d->B * d->H;
   if (d->seg_chunks > 0) {
@@ -718,76 +807,45 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   }
   L->nseg = L->nchunks > 0 ? (L->nchunks + L->seg_chunks - 1) / L->seg_chunks : 0;
   L->nsum = d->want_final ? L->nseg : (L->nseg > 0 ? L->nseg - 1 : 0);
+  L->nelem = L->dkp * L->dvp + L->dvp + L->dkp;
   L->ws_bytes = 0;
   if (L->nsum > 0)
-    L->ws_bytes = (size_t)bh * L->nseg * (size_t)L->dkp * L->dvp * sizeof(float) +
-                  (size_t)bh * L->nseg * sizeof(float) + 256;
+    L->ws_bytes = (size_t)bh * L->nseg * (size_t)L->nelem * sizeof(float) + (size_t)bh * L->nseg * sizeof(float) + 256;
   return TS_OK;
-}
-
-int max_waves(int dvp) {
-  const int nw = dvp / 16;
-  return nw <= 4 ? 4 : (nw <= 5 ? 5 : 9);
-}
-
-int block_threads(int dvp) {
-  const int nw = dvp / 16;
-  return (nw < 4 ? 4 : nw) * 64;
-}
-
-// Dynamic LDS of one workgroup; mirrors the carve-up at the top of scan_kernel.
-size_t lds_bytes(int esize, int dkp, int dvp, bool main_kernel) {
-  const int vec = 16 / esize;
-  const bool qreg = main_kernel && esize == 2 && dkp <= 80;
-  const bool qlds = main_kernel && !qreg;
-  const int stages = esize == 2 ? 2 : 1;
-  const int kp = dkp + vec, tp = ts::C + vec, vp = dvp + vec;
-  size_t elems = (qlds ? (size_t)ts::C * kp : 0) + (size_t)ts::C * kp;
-  if (esize == 2)
-    elems += (size_t)ts::C * vp;
-  else
-    elems += (size_t)dkp * tp + (size_t)dvp * tp;
-  const int nw = block_threads(dvp) / 64;
-  return stages * elems * esize + (68 + (size_t)nw * ts::C) * sizeof(float);
 }
 
 typedef void (*KernelFn)(ts::ScanP);
 
-template <typename E, int MAXW, bool GEN>
-KernelFn pick_kernel_w(int dkp, bool main_kernel) {
+template <typename E, int NVW, bool GEN>
+KernelFn pick_kernel_v(int dkp, bool main_kernel) {
   switch (dkp) {
-#define TS_CASE(D)                                                                      \
-  case D:                                                                               \
-    return main_kernel ? (KernelFn)ts::scan_kernel<E, D, true, MAXW, GEN>               \
-                       : (KernelFn)ts::scan_kernel<E, D, false, MAXW, GEN>;
+#define TS_CASE(D)                                                                    \
+  case D:                                                                             \
+    return main_kernel ? (KernelFn)ts::scan_kernel<E, D, NVW, true, GEN>              \
+                       : (KernelFn)ts::scan_kernel<E, D, NVW, false, GEN>;
+    TS_CASE(16)
     TS_CASE(32)
     TS_CASE(64)
-    TS_CASE(80)
     TS_CASE(128)
-    TS_CASE(144)
 #undef TS_CASE
   }
   return nullptr;
 }
 
-// bf16 kernels are specialised by wave count (register budget per launch
-// size) and, up to five waves, by whether the call needs the general
-// features; the fp32 parity kernels use one general 9-wave build.
-KernelFn pick_kernel(bool bf16, int dkp, int dvp, bool main_kernel, bool general) {
-  if (!bf16) return pick_kernel_w<float, 9, true>(dkp, main_kernel);
-  switch (max_waves(dvp)) {
-    case 4:
-      return general ? pick_kernel_w<ts::bf16, 4, true>(dkp, main_kernel)
-                     : pick_kernel_w<ts::bf16, 4, false>(dkp, main_kernel);
-    case 5:
-      return general ? pick_kernel_w<ts::bf16, 5, true>(dkp, main_kernel)
-                     : pick_kernel_w<ts::bf16, 5, false>(dkp, main_kernel);
-    default: return pick_kernel_w<ts::bf16, 9, true>(dkp, main_kernel);
-  }
+// bf16 kernels are specialised by whether the call needs the general features
+// (retention, ext columns, fp32 outputs); the fp32 parity kernels are general.
+KernelFn pick_kernel(bool bf16, int dkp, int nvw, bool main_kernel, bool general) {
+  if (!bf16)
+    return nvw == 1 ? pick_kernel_v<float, 1, true>(dkp, main_kernel) : pick_kernel_v<float, 2, true>(dkp, main_kernel);
+  if (nvw == 1)
+    return general ? pick_kernel_v<ts::bf16, 1, true>(dkp, main_kernel)
+                   : pick_kernel_v<ts::bf16, 1, false>(dkp, main_kernel);
+  return general ? pick_kernel_v<ts::bf16, 2, true>(dkp, main_kernel)
+                 : pick_kernel_v<ts::bf16, 2, false>(dkp, main_kernel);
 }
 
 // Bytes spanned by one (batch, head) slice of a [.., T, width] stream, or an
-// error if rows up to T + one tile could not be addressed with 31-bit offsets.
+// error if rows up to T + two tiles could not be addressed with 31-bit offsets.
 int slice_bytes(const char* name, const ts_strided& s, int T, int width, int esize, uint32_t* out) {
   *out = 0;
   if (!s.ptr) return TS_OK;
@@ -810,12 +868,13 @@ int check_stream(const char* name, const ts_strided& s, int vec, bool required) 
   return TS_OK;
 }
 
-int launch(KernelFn fn, dim3 grid, dim3 block, size_t lds, hipStream_t stream, const ts::ScanP& p) {
+int launch(KernelFn fn, dim3 grid, size_t lds, hipStream_t stream, const ts::ScanP& p) {
+  if (!fn) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: no kernel for this shape");
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: LDS request failed: %s", hipGetErrorString(e));
   }
-  hipLaunchKernelGGL(fn, grid, block, lds, stream, p);
+  hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: launch failed: %s", hipGetErrorString(e));
   return TS_OK;
@@ -833,8 +892,8 @@ int ts_scan_layout(const ts_scan_desc* desc, int32_t* dk_pad, int32_t* dv_pad, i
   Layout L;
   int rc = compute_layout(desc, &L);
   if (rc) return rc;
-  if (dk_pad) *dk_pad = L.dkp;
-  if (dv_pad) *dv_pad = L.dvp;
+  if (dk_pad) *dk_pad = desc->dk + (L.kx ? 1 : 0);
+  if (dv_pad) *dv_pad = desc->dv + (L.vx ? 1 : 0);
   if (n_segments) *n_segments = L.nseg;
   return TS_OK;
 }
@@ -877,9 +936,11 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   ts::ScanP p;
   memset(&p, 0, sizeof(p));
   p.B = d->B; p.H = d->H; p.T = d->T; p.dk = d->dk; p.dv = d->dv; p.dvp = L.dvp;
-  p.nchunks = L.nchunks; p.seg_chunks = L.seg_chunks; p.nseg = L.nseg; p.nsum = L.nsum;
+  p.nchunks = L.nchunks; p.seg_chunks = L.seg_chunks; p.nseg = L.nseg; p.nsum = L.nsum; p.nelem = L.nelem;
   p.ret = d->retention; p.reverse = d->reverse;
-  p.q_ext = d->q_ext; p.k_ext = d->k_ext; p.v_ext = d->v_ext;
+  p.q_ext = L.kx ? d->q_ext : TS_EXT_NONE;
+  p.k_ext = L.kx ? d->k_ext : TS_EXT_NONE;
+  p.v_ext = d->v_ext;
   p.out_mode = d->out_mode; p.out_scale = d->out_scale;
   p.q = io->q; p.k = io->k; p.v = io->v;
   p.qe = io->q_ext; p.ke = io->k_ext; p.ve = io->v_ext;
@@ -897,30 +958,30 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   if ((rc = slice_bytes("out_ext", p.oe, d->T, 1, 4, &p.oe_rec))) return rc;
   if (L.ws_bytes > 0) {
     p.seg = (float*)workspace;
-    p.segdec = p.seg + (size_t)d->B * d->H * L.nseg * (size_t)L.dkp * L.dvp;
+    p.segdec = p.seg + (size_t)d->B * d->H * L.nseg * (size_t)L.nelem;
   }
 
   const int bh = d->B * d->H;
-  const dim3 block(block_threads(L.dvp));
-  const bool general = d->retention != TS_RET_NONE || d->q_ext != TS_EXT_NONE || d->k_ext != TS_EXT_NONE ||
-                       d->v_ext != TS_EXT_NONE || d->out_mode != TS_OUT_STORE || io->out_ext.ptr != nullptr;
-  KernelFn fsum = pick_kernel(d->dtype == TS_BF16, L.dkp, L.dvp, false, general);
-  KernelFn fmain = pick_kernel(d->dtype == TS_BF16, L.dkp, L.dvp, true, general);
-  const size_t lds_sum = lds_bytes(esize, L.dkp, L.dvp, false);
-  const size_t lds_main = lds_bytes(esize, L.dkp, L.dvp, true);
+  const bool general = d->retention != TS_RET_NONE || L.kx || L.vx || d->out_mode != TS_OUT_STORE ||
+                       io->out_ext.ptr != nullptr;
+  KernelFn fsum = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, false, general);
+  KernelFn fmain = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, true, general);
+  const size_t lds_sum = (size_t)ts::scan_layout(esize, L.dkp, L.dvp, false).bytes;
+  const size_t lds_main = (size_t)ts::scan_layout(esize, L.dkp, L.dvp, true).bytes;
   if (lds_main > 160 * 1024)
-    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: tile of %lld bytes exceeds LDS (dk_pad=%d)",
-                (long long)lds_main, L.dkp);
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: tile of %lld bytes exceeds LDS (dk_pad=%d dv_pad=%d)",
+                (long long)lds_main, L.dkp, L.dvp);
 
   if (L.nsum > 0) {
-    if ((rc = launch(fsum, dim3(L.nsum, bh), block, lds_sum, stream, p))) return rc;
-    const int nelem = L.dkp * L.dvp;
-    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
-                       p.segdec, d->want_final ? io->final_state : nullptr, L.nseg, L.nsum, nelem);
+    if ((rc = launch(fsum, dim3(L.nsum, bh), lds_sum, stream, p))) return rc;
+    ts::FinalP F{d->want_final ? io->final_state : nullptr, L.dkp, L.dvp, d->dk, d->dv, L.kx ? 1 : 0,
+                 L.vx ? 1 : 0};
+    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
+                       p.segdec, F, L.nseg, L.nsum, L.nelem);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: prefix launch failed: %s", hipGetErrorString(e));
   }
-  return launch(fmain, dim3(L.nseg, bh), block, lds_main, stream, p);
+  return launch(fmain, dim3(L.nseg, bh), lds_main, stream, p);
 }
 
 }  // extern "C"

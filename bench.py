@@ -79,12 +79,19 @@ def seeded_module(config, seed: int):
     return module
 
 
-def time_steps(module, x, dy, steps: int, warmup: int):
+def time_steps(module, x, dy, steps: int, warmup: int, graphed=None):
+    """Mean ms per fwd+bwd step over exactly ``steps`` steps after ``warmup``.
+
+    With ``graphed`` (a ``torch.cuda.make_graphed_callables`` wrapper of the
+    module) each step replays the captured forward and backward graphs: the
+    same kernels on the same data, without the host launch overhead."""
     import torch
+
+    fwd = module if graphed is None else graphed
 
     def step():
         module.zero_grad(set_to_none=True)
-        y = module(x)
+        y = fwd(x)
         y.backward(dy)
 
     for _ in range(warmup):
@@ -104,6 +111,18 @@ def scan_flops(B_, H_, T_, dk, dv, tile=64):
     per token and head C*dk (scores) + C*dv (P.V) + dk*dv (carried-state read)
     + dk*dv (state update) multiply-adds."""
     return 2 * B_ * H_ * T_ * (tile * dk + tile * dv + 2 * dk * dv)
+
+
+def graphed_step_ms(module, x, dy, steps: int, warmup: int):
+    """Step time of graph replays of a copy of ``module`` (capture replaces the
+    copy's forward; the original stays eager for the per-kernel timing)."""
+    import copy
+
+    import torch
+
+    twin = copy.deepcopy(module)
+    graphed = torch.cuda.make_graphed_callables(twin, (x,), num_warmup_iters=3)
+    return time_steps(twin, x, dy, steps, warmup, graphed)
 
 
 def pass_profile(module, x, dy, steps: int = 5):
@@ -243,6 +262,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", choices=("eager", "graph"), default="eager",
+                    help="time eager execution (default) or graph replays of the captured step")
     ap.add_argument("--no-variant", action="store_true", help="skip the key-mass variant")
     ap.add_argument("--steps-only", action="store_true", help="time the steps only (for profilers)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -265,8 +286,16 @@ def main() -> int:
     dy = (torch.randn(B, T, D_MODEL, generator=g) * 1e-2).to(dev, torch.bfloat16)
 
     module = seeded_module(headline_config("feature_rope"), 0).to(dev, torch.bfloat16)
-    ms = time_steps(module, x, dy, args.steps, args.warmup)
+    ms_eager = time_steps(module, x, dy, args.steps, args.warmup)
     assert module._core.last_path == "fused"
+    execution = "eager"
+    ms = ms_eager
+    if args.mode == "graph":
+        try:
+            ms = graphed_step_ms(module, x, dy, args.steps, args.warmup)
+            execution = "graph"
+        except Exception as exc:  # capture unsupported here: report eager, say why
+            print(f"graph capture failed ({exc!r}); reporting eager execution", file=sys.stderr)
     if args.calibrate_copy:
         copy_calibration()
     if args.steps_only:
@@ -278,6 +307,10 @@ def main() -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (x ~ N(0,1), dy ~ N(0,1e-4), seeded weights)",
+        "execution": ("hip-graph replay of the captured fwd+bwd step (torch.cuda.make_graphed_callables)"
+                      if execution == "graph" else "eager"),
+        "eager": {"value": round(tokens / (ms_eager * 1e-3), 1), "ms_per_step": round(ms_eager, 4)}
+        if execution == "graph" else None,
         "config": {"workload": "ThetaScan-Kernel mixer fwd+bwd, ReLU^2 ridge, m=64, chunk 64, feature RoPE, "
                                "unnormalized read",
                    "batch": B, "seq_len": T, "heads": H, "head_dim": D_HEAD, "d_model": D_MODEL,
@@ -290,10 +323,15 @@ def main() -> int:
     out["scan_mfma"] = scan_mfma(passes)
     if not args.no_variant:
         module_b = seeded_module(headline_config("key_mass"), 0).to(dev, torch.bfloat16)
-        ms_b = time_steps(module_b, x, dy, args.steps, args.warmup)
+        ms_b_eager = time_steps(module_b, x, dy, args.steps, args.warmup)
+        ms_b = ms_b_eager
+        if execution == "graph":
+            ms_b = graphed_step_ms(module_b, x, dy, args.steps, args.warmup)
         passes_b = pass_profile(module_b, x, dy)
         out["variants"] = {
             "input_rope_key_mass": {"value": round(tokens / (ms_b * 1e-3), 1), "ms_per_step": round(ms_b, 4),
+                                    "eager": {"value": round(tokens / (ms_b_eager * 1e-3), 1),
+                                              "ms_per_step": round(ms_b_eager, 4)} if execution == "graph" else None,
                                     "roofline": roofline_of(passes_b, {}), "passes": passes_b},
         }
     if not args.no_cpu_baseline:

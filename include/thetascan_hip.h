@@ -244,6 +244,22 @@ typedef struct ts_wcumsum_desc {
 int ts_wcumsum(const ts_wcumsum_desc* desc, ts_strided x, ts_strided out, const float* log_alpha,
                ts_strided decay, hipStream_t stream);
 
+/* out[i] = scale * (sum_{s<na} a[s*n + i] + sum_{s<nb} b[s*n + i]) for i < n,
+ * written as ts_dtype out_dtype: sums the partial weight-gradient slots of
+ * one or two ts_feature_bwd calls (keys and queries) into the gradient of W1,
+ * W2 or tau.  With ts_feature_bwd it replaces the autograd reductions of the
+ * weight gradients of engine.py:117-158 (summed over every token). */
+int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t n, void* out,
+                 int32_t out_dtype, float scale, hipStream_t stream);
+
+/* parts[s][c] = sum of x[r * row_stride + c] over the rows r of slice s
+ * (rows split into `slices` equal runs), for a [rows, cols] matrix of
+ * ts_dtype `dtype` with cols and row_stride multiples of 8 and a 16-byte
+ * aligned base.  Followed by ts_sum_slots it is the bias gradient of the
+ * output-gate projection (gates.py:34-40, summed over every token). */
+int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_t row_stride, float* parts,
+                int32_t slices, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

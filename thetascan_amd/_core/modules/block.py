@@ -365,17 +365,16 @@ class ThetaScan(nn.Module):
         cfg = self.cfg
         B, T, _ = x.shape
         H, d, m = cfg.n_heads, cfg.head_dim, cfg.mem_hidden
-        qkv = linear(x, self.proj_qkv.weight).view(B, T, 3, H, d)
         in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
         feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
         kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
         spec = fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot, cfg.rope_base,
                                  1.0 / math.sqrt(cfg.depth), cfg.eps)
         (W1, W2, _), = self._weights()
-        g = None
-        if self.ogate is not None:
-            g = linear(x, self.ogate.g.lin.weight, self.ogate.g.lin.bias)
-        y = fused.kernel_memory(qkv, W1, W2, self.kernel_relu2_threshold, g, spec, cfg.read_norm)
+        gate = self.ogate is not None
+        proj = fused.in_projection(x, self.proj_qkv.weight, self.ogate.g.lin.weight if gate else None,
+                                   self.ogate.g.lin.bias if gate else None)
+        y = fused.kernel_memory(proj, W1, W2, self.kernel_relu2_threshold, spec, cfg.read_norm, H, gate)
         return linear(y, self.proj_out.weight)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

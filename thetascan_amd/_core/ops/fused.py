@@ -8,6 +8,9 @@ projection and the output projection of a kernel-memory mixer:
     num, mass = scan(phi_q, phi_k, v)  ts_scan_fwd      (key-mass column)
     y = (resid + s*num/(mass+eps)) * silu(g)            ts_read_fwd
 
+with q, k, v and the gate logits g read from one input projection
+(``in_projection``: the qkv and output-gate weights stacked into one GEMM)
+
 and its backward (ts_read_bwd -> three scans -> ts_feature_bwd, then plain
 GEMMs for the W1/W2 gradients).  Reference chain:
 src/thetascan/_core/modules/block.py:593-724 and
@@ -22,7 +25,7 @@ import torch
 
 from ... import _lib
 from . import scan_hip
-from .linear import split_k_outer
+from .linear import column_sum, split_k_outer, weight_grad
 
 
 def _rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -78,7 +81,7 @@ def feature_fwd(spec: FeatureSpec, x, w1, w2, tau, want_resid: bool):
     io = _lib.FeatureIO(_lib.strided(x), _lib.ptr(w1), _lib.ptr(w2), _lib.ptr(tau), _lib.ptr(ic),
                         _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(phi), _lib.strided(resid))
     desc = spec.desc(x, tau is not None)
-    with _lib.timed("ts_feature_fwd", _lib.nbytes(x, phi, resid)):
+    with _lib.timed("ts_feature_fwd", lambda: _lib.nbytes(x, phi, resid)):
         status = lib.ts_feature_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
     _lib.check(status, "ts_feature_fwd")
     return phi, resid
@@ -90,28 +93,42 @@ def _head_major(B, H, T, w, dtype, device):
     return buf.transpose(0, 1), buf.view(H, B * T, w)
 
 
-def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_weights=True):
+class Slots:
+    """Partial weight-gradient slots [P, ...] (fp32) written by one fused backward."""
+
+    def __init__(self, parts: torch.Tensor):
+        self.parts = parts
+
+
+def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_weights=True, w1t=None, w2t=None):
     """Backward of one stream; dx is written in place.
 
-    Returns fp32 ``(dw1 [H,m,d], dw2 [H,d,m], dtau [H])`` -- this stream's
+    Returns ``(dw1 [H,m,d], dw2 [H,d,m], dtau [H])`` -- this stream's
     contributions to the gradients of W1, W2 (queries only) and the threshold
-    tau (None where not applicable or not wanted).  The weight gradients are
-    contracted inside the kernel into per-workgroup partial slots and summed
-    here; shapes without a fused kernel fall back to per-token tiles and
-    split-K GEMMs.
+    tau, each a :class:`Slots` of per-workgroup partial sums contracted inside
+    the kernel (sum them with :func:`sum_grads`), or, for shapes without a
+    fused kernel, an fp32 tensor from per-token tiles and split-K GEMMs
+    (None where not applicable or not wanted).  ``w1t`` / ``w2t`` are the
+    [H,d,m] / [H,m,d] transposes when the caller already has them.
     """
     lib = _lib.load()
     B, H, T, d = x.shape
     m = spec.m
     dev = x.device
-    w1t = w1.transpose(1, 2).contiguous()
-    w2t = w2.transpose(1, 2).contiguous() if (dresid is not None) else None
+    if w1t is None:
+        w1t = w1.transpose(1, 2).contiguous()
+    if dresid is not None and w2t is None:
+        w2t = w2.transpose(1, 2).contiguous()
     desc = spec.desc(x, tau is not None)
-    parts = ctypes.c_int32(0)
+    P = 0
     if want_weights:
-        _lib.check(lib.ts_feature_bwd_parts(ctypes.byref(desc), int(dresid is not None), ctypes.byref(parts)),
-                   "ts_feature_bwd_parts")
-    P = parts.value
+        key = (B, H, T, d, m, x.dtype, spec.kind, dresid is not None)
+        P = _PARTS.get(key, -1)
+        if P < 0:
+            parts = ctypes.c_int32(0)
+            _lib.check(lib.ts_feature_bwd_parts(ctypes.byref(desc), int(dresid is not None), ctypes.byref(parts)),
+                       "ts_feature_bwd_parts")
+            P = _PARTS[key] = parts.value
     da = xn = h = da_v = xn_v = h_v = dtau_tok = None
     dw1p = dw2p = dtaup = None
     if want_weights and P > 0:
@@ -134,18 +151,45 @@ def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_w
         _lib.strided(dx), _lib.strided(da_v), _lib.strided(xn_v), _lib.strided(h_v), _lib.strided(dtau_tok),
         _lib.ptr(dw1p), _lib.ptr(dw2p), _lib.ptr(dtaup),
     )
-    traffic = _lib.nbytes(x, dphi, dresid, dx, da, xn, h, dtau_tok, dw1p, dw2p, dtaup)
-    with _lib.timed("ts_feature_bwd", traffic):
+    with _lib.timed("ts_feature_bwd", lambda: _lib.nbytes(x, dphi, dresid, dx, da, xn, h, dtau_tok, dw1p, dw2p,
+                                                          dtaup)):
         status = lib.ts_feature_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(dev))
     _lib.check(status, "ts_feature_bwd")
     if not want_weights:
         return None, None, None
     if P > 0:
-        return (dw1p.sum(0), None if dw2p is None else dw2p.sum(0), None if dtaup is None else dtaup.sum(0))
+        return Slots(dw1p), None if dw2p is None else Slots(dw2p), None if dtaup is None else Slots(dtaup)
     dw1 = split_k_outer(da, xn)
     dw2 = None if h is None else split_k_outer(_head_major_of(dresid), h) * spec.resid_scale
     dtau = None if dtau_tok is None else dtau_tok.sum(dim=(0, 2))
     return dw1, dw2, dtau
+
+
+_PARTS: dict = {}
+
+
+def sum_grads(a, b, dtype: torch.dtype, shape):
+    """Gradient of ``shape`` in ``dtype`` from one or two stream contributions
+    (:class:`Slots` are summed by one ts_sum_slots launch)."""
+    items = [x for x in (a, b) if x is not None]
+    if not items:
+        return None
+    if all(isinstance(x, Slots) for x in items) and dtype in (torch.bfloat16, torch.float32):
+        lib = _lib.load()
+        first = items[0].parts
+        n = first[0].numel()
+        second = items[1].parts if len(items) > 1 else None
+        out = torch.empty(shape, dtype=dtype, device=first.device)
+        _lib.check(lib.ts_sum_slots(first.data_ptr(), first.shape[0], _lib.ptr(second),
+                                    0 if second is None else second.shape[0], n, out.data_ptr(),
+                                    _lib.dtype_code(dtype), 1.0, _lib.stream_handle(first.device)),
+                   "ts_sum_slots")
+        return out
+    total = None
+    for x in items:
+        val = x.parts.sum(0) if isinstance(x, Slots) else x
+        total = val if total is None else total + val
+    return total.view(shape).to(dtype)
 
 
 def _head_major_of(t: torch.Tensor) -> torch.Tensor:
@@ -164,25 +208,28 @@ def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6):
                          float(scale), float(eps))
     io = _lib.ReadIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
                      _lib.strided(y))
-    with _lib.timed("ts_read_fwd", _lib.nbytes(num, mass, resid, g, y)):
+    with _lib.timed("ts_read_fwd", lambda: _lib.nbytes(num, mass, resid, g, y)):
         status = lib.ts_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
     _lib.check(status, "ts_read_fwd")
     return y
 
 
-def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6):
+def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None):
+    """Backward of :func:`read_fwd`; ``dg`` optionally names the [B,H,T,d]
+    view the gate gradient is written to."""
     lib = _lib.load()
     B, H, T, d = num.shape
     dnum = torch.empty_like(num)
     dmass = torch.empty(B, H, T, dtype=torch.float32, device=num.device) if mass is not None else None
     dresid, dresid_hm = _head_major(B, H, T, d, num.dtype, num.device)
-    dg = torch.empty(B, T, H, d, dtype=num.dtype, device=num.device).transpose(1, 2) if g is not None else None
+    if g is not None and dg is None:
+        dg = torch.empty(B, T, H, d, dtype=num.dtype, device=num.device).transpose(1, 2)
     desc = _lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None), int(g is not None),
                          float(scale), float(eps))
     io = _lib.ReadBwdIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
                         _lib.strided(dy), _lib.strided(dnum), _lib.strided(dmass), _lib.strided(dresid),
                         _lib.strided(dg))
-    with _lib.timed("ts_read_bwd", _lib.nbytes(num, mass, resid, g, dy, dnum, dmass, dresid, dg)):
+    with _lib.timed("ts_read_bwd", lambda: _lib.nbytes(num, mass, resid, g, dy, dnum, dmass, dresid, dg)):
         status = lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
     _lib.check(status, "ts_read_bwd")
     return dnum, dmass, (dresid, dresid_hm), dg
@@ -211,23 +258,85 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
             kind = _lib.RET_STATIC
             la = retention.detach().to(torch.float32).reshape(H).contiguous()
     desc = _lib.WcumsumDesc(B, H, T, F, kind, int(reverse))
-    with _lib.timed("ts_wcumsum", _lib.nbytes(xf, out, dec)):
+    with _lib.timed("ts_wcumsum", lambda: _lib.nbytes(xf, out, dec)):
         status = lib.ts_wcumsum(ctypes.byref(desc), _lib.strided(xf), _lib.strided(out), _lib.ptr(la),
                                 _lib.strided(dec), _lib.stream_handle(x.device))
     _lib.check(status, "ts_wcumsum")
     return out
 
 
-class _KernelMemory(torch.autograd.Function):
-    """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g) for a depth-1 kernel memory."""
+def _stacked(w_qkv, w_g, b_g, dtype):
+    """[W_qkv; W_g] and [0; b_g] (rebuilt every call: parameters may change
+    in place in ways no version counter records, e.g. through ``.data``)."""
+    weight = torch.cat([w_qkv.detach(), w_g.detach().to(w_qkv.dtype)], dim=0)
+    bias = torch.cat([w_qkv.new_zeros(w_qkv.shape[0], dtype=dtype), b_g.detach().to(dtype)])
+    return weight, bias
+
+
+class _InProjection(torch.autograd.Function):
+    """proj = x [W_qkv; W_g]^T + [0; b_g]: the qkv projection and the output-gate
+    projection as one GEMM (block.py:593-594 and gates.py:34-40 read the same
+    x), with one gradient GEMM for x and one split-K GEMM for the stacked
+    weights."""
 
     @staticmethod
-    def forward(ctx, qkv, w1, w2, tau, g, spec: FeatureSpec, normalize: bool, seg_chunks: int):
-        B, T, three, H, d = qkv.shape
+    def forward(ctx, x, w_qkv, w_g, b_g):
+        n_qkv = w_qkv.shape[0]
+        if w_g is None:
+            weight, bias = w_qkv, None
+        else:
+            weight, bias = _stacked(w_qkv, w_g, b_g, x.dtype)
+        ctx.save_for_backward(x, weight)
+        ctx.n_qkv = n_qkv
+        ctx.has_g = w_g is not None
+        ctx.dtypes = (w_qkv.dtype, None if w_g is None else w_g.dtype, None if b_g is None else b_g.dtype)
+        return torch.nn.functional.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, dproj):
+        x, weight = ctx.saved_tensors
+        n_out, n_in = weight.shape
+        d2 = dproj.reshape(-1, n_out)
+        dx = dw_qkv = dw_g = db_g = None
+        if ctx.needs_input_grad[0]:
+            dx = (d2 @ weight).view(x.shape)
+        if ctx.needs_input_grad[1] or (ctx.has_g and ctx.needs_input_grad[2]):
+            same = not ctx.has_g or ctx.dtypes[0] == ctx.dtypes[1]
+            dw = weight_grad(d2, x.reshape(-1, n_in), ctx.dtypes[0] if same else torch.float32)
+            dw_qkv = dw[:ctx.n_qkv].to(ctx.dtypes[0])
+            if ctx.has_g:
+                dw_g = dw[ctx.n_qkv:].to(ctx.dtypes[1])
+        if ctx.has_g and ctx.needs_input_grad[3]:
+            db_g = column_sum(d2[:, ctx.n_qkv:], ctx.dtypes[2])
+        return dx, dw_qkv, dw_g, db_g
+
+
+def in_projection(x, w_qkv, w_g=None, b_g=None):
+    """[B,T,3*H*d (+H*d)] projection for :func:`kernel_memory`."""
+    if not x.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    return _InProjection.apply(x, w_qkv, w_g, b_g)
+
+
+class _KernelMemory(torch.autograd.Function):
+    """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g) for a depth-1 kernel memory.
+
+    ``proj`` is the [B,T,3*H*d (+H*d)] input projection: q, k, v heads, then
+    the output-gate logits when ``has_gate``.  The gradient of ``proj`` is one
+    tensor, written in place by the kernels.
+    """
+
+    @staticmethod
+    def forward(ctx, proj, w1, w2, tau, spec: FeatureSpec, normalize: bool, seg_chunks: int, heads: int,
+                has_gate: bool):
+        B, T, P = proj.shape
+        H = heads
+        d = P // (4 * H) if has_gate else P // (3 * H)
+        qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
         q = qkv[:, :, 0].transpose(1, 2)
         k = qkv[:, :, 1].transpose(1, 2)
         v = qkv[:, :, 2].transpose(1, 2)
-        dt = qkv.dtype
+        dt = proj.dtype
         w1c = w1.to(dt).contiguous()
         w2c = w2.to(dt).contiguous()
         tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
@@ -237,63 +346,71 @@ class _KernelMemory(torch.autograd.Function):
             phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
             seg_chunks=seg_chunks,
         )
-        gv = None if g is None else g.view(B, T, H, d).transpose(1, 2)
-        y = torch.empty(B, T, H, d, dtype=dt, device=qkv.device)
+        gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
+        y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
         read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps)
         ctx.spec, ctx.normalize, ctx.seg_chunks = spec, normalize, seg_chunks
-        ctx.has_tau, ctx.has_g = tau is not None, g is not None
+        ctx.heads, ctx.d, ctx.has_gate = H, d, has_gate
+        ctx.has_tau = tau is not None
         ctx.tau_dtype = None if tau is None else tau.dtype
         ctx.w_dtypes = (w1.dtype, w2.dtype)
-        ctx.save_for_backward(qkv, w1c, w2c, tauf, g, phi_q, phi_k, num, mass, resid)
+        ctx.save_for_backward(proj, w1c, w2c, tauf, phi_q, phi_k, num, mass, resid)
         return y.view(B, T, H * d)
 
     @staticmethod
     def backward(ctx, dy):
-        qkv, w1c, w2c, tauf, g, phi_q, phi_k, num, mass, resid = ctx.saved_tensors
+        proj, w1c, w2c, tauf, phi_q, phi_k, num, mass, resid = ctx.saved_tensors
         spec = ctx.spec
-        B, T, three, H, d = qkv.shape
-        dt = qkv.dtype
+        B, T, P = proj.shape
+        H, d = ctx.heads, ctx.d
+        dt = proj.dtype
+        qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
         q = qkv[:, :, 0].transpose(1, 2)
         k = qkv[:, :, 1].transpose(1, 2)
         v = qkv[:, :, 2].transpose(1, 2)
+        dproj = torch.empty_like(proj)
+        dqkv = dproj[..., :3 * H * d].view(B, T, 3, H, d)
+        dq = dqkv[:, :, 0].transpose(1, 2)
+        dk = dqkv[:, :, 1].transpose(1, 2)
+        dv = dqkv[:, :, 2].transpose(1, 2)
+        gv = dgv = None
+        if ctx.has_gate:
+            gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
+            dgv = dproj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
         dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
-        gv = None if g is None else g.view(B, T, H, d).transpose(1, 2)
-        dnum, dmass, (dresid, dresid_hm), dg = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps)
+        dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv)
         norm = ctx.normalize
         q_ext = dmass if norm else None
         dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
                                             seg_chunks=ctx.seg_chunks)
         dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
                                             k_ext=q_ext, seg_chunks=ctx.seg_chunks)
-        dqkv = torch.empty_like(qkv)
-        dq = dqkv[:, :, 0].transpose(1, 2)
-        dk = dqkv[:, :, 1].transpose(1, 2)
-        dv = dqkv[:, :, 2].transpose(1, 2)
         scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=ctx.seg_chunks)
         need_w1 = ctx.needs_input_grad[1]
         need_w2 = ctx.needs_input_grad[2]
         need_tau = ctx.has_tau and ctx.needs_input_grad[3]
         want_k = need_w1 or need_tau
         want_q = need_w1 or need_w2 or need_tau
-        dw1_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=want_k)
-        dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c, want_weights=want_q)
+        w1t = w1c.transpose(1, 2).contiguous()
+        w2t = w2c.transpose(1, 2).contiguous()
+        dw1_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=want_k, w1t=w1t)
+        dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c, want_weights=want_q,
+                                           w1t=w1t, w2t=w2t)
         dw1 = dw2 = dtau = None
         if need_w1:
-            dw1 = (dw1_k + dw1_q).to(ctx.w_dtypes[0])
+            dw1 = sum_grads(dw1_k, dw1_q, ctx.w_dtypes[0], w1c.shape)
         if need_w2:
-            dw2 = dw2_q.to(ctx.w_dtypes[1])
+            dw2 = sum_grads(dw2_q, None, ctx.w_dtypes[1], w2c.shape)
         if need_tau:
-            dtau = (dtau_k + dtau_q).to(ctx.tau_dtype)
-        dgo = None
-        if ctx.has_g:
-            dgo = dg.transpose(1, 2).reshape(B, T, H * d)
-        return dqkv, dw1, dw2, dtau, dgo, None, None, None
+            dtau = sum_grads(dtau_k, dtau_q, ctx.tau_dtype, (H,))
+        return dproj, dw1, dw2, dtau, None, None, None, None, None
 
 
-def kernel_memory(qkv, w1, w2, tau, g, spec: FeatureSpec, normalize: bool, seg_chunks: int = 0):
-    """Fused kernel-memory read; qkv is the [B,T,3,H,d] projection output."""
-    if not qkv.is_cuda:
+def kernel_memory(proj, w1, w2, tau, spec: FeatureSpec, normalize: bool, heads: int, has_gate: bool,
+                  seg_chunks: int = 0):
+    """Fused kernel-memory read of the [B,T,3*H*d (+H*d)] input projection."""
+    if not proj.is_cuda:
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
-    if not qkv.is_contiguous():
-        qkv = qkv.contiguous()
-    return _KernelMemory.apply(qkv, w1, w2, tau, g, spec, normalize, seg_chunks)
+    if not proj.is_contiguous():
+        proj = proj.contiguous()
+    return _KernelMemory.apply(proj, w1, w2, tau, spec, normalize, seg_chunks, heads, has_gate)

@@ -10,8 +10,12 @@ library GEMMs.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn.functional as F
+
+from ... import _lib
 
 
 def _slices(rows: int, target: int = 2048, max_slices: int = 16) -> int:
@@ -34,6 +38,45 @@ def split_k_outer(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return out.view(G, s, A, -1).sum(1)
 
 
+def slot_sum(parts: torch.Tensor, dtype: torch.dtype, shape) -> torch.Tensor:
+    """sum over the leading (slot) axis of fp32 ``parts`` -> ``shape`` in ``dtype``
+    (one ts_sum_slots launch on the GPU)."""
+    if not parts.is_cuda or dtype not in (torch.bfloat16, torch.float32):
+        return parts.sum(0).view(shape).to(dtype)
+    parts = parts.contiguous()
+    out = torch.empty(shape, dtype=dtype, device=parts.device)
+    lib = _lib.load()
+    _lib.check(lib.ts_sum_slots(parts.data_ptr(), parts.shape[0], None, 0, parts[0].numel(), out.data_ptr(),
+                                _lib.dtype_code(dtype), 1.0, _lib.stream_handle(parts.device)), "ts_sum_slots")
+    return out
+
+
+def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """dy2^T x2 over all rows -> [n_out, n_in] in ``dtype`` (split-K GEMM + slot sum)."""
+    rows = dy2.shape[0]
+    s = _slices(rows)
+    if not (dy2.is_cuda and dy2.dtype in (torch.bfloat16, torch.float16)):
+        return split_k_outer(dy2.unsqueeze(0), x2.unsqueeze(0))[0].to(dtype)
+    parts = torch.bmm(dy2.reshape(s, rows // s, -1).transpose(1, 2), x2.reshape(s, rows // s, -1),
+                      out_dtype=torch.float32)
+    return slot_sum(parts, dtype, (dy2.shape[1], x2.shape[1]))
+
+
+def column_sum(x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Sum of the rows of a [rows, cols] matrix (any row stride) -> [cols] in ``dtype``."""
+    rows, cols = x2.shape
+    ok = (x2.is_cuda and x2.dtype in (torch.bfloat16, torch.float32) and x2.stride(1) == 1 and cols % 8 == 0
+          and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0)
+    if not ok:
+        return x2.float().sum(0).to(dtype)
+    slices = max(1, min(256, rows // 64))
+    parts = torch.empty(slices, cols, dtype=torch.float32, device=x2.device)
+    lib = _lib.load()
+    _lib.check(lib.ts_col_sums(x2.data_ptr(), _lib.dtype_code(x2.dtype), rows, cols, x2.stride(0),
+                               parts.data_ptr(), slices, _lib.stream_handle(x2.device)), "ts_col_sums")
+    return slot_sum(parts, dtype, (cols,))
+
+
 class _Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias):
@@ -50,12 +93,9 @@ class _Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = (dy2 @ weight).view(x.shape)
         if ctx.needs_input_grad[1]:
-            x2 = x.reshape(-1, n_in)
-            dw = split_k_outer(dy2.unsqueeze(0), x2.unsqueeze(0))[0].to(weight.dtype)
+            dw = weight_grad(dy2, x.reshape(-1, n_in), weight.dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            rows = dy2.shape[0]
-            s = _slices(rows, 256, 64)
-            db = dy2.view(s, rows // s, n_out).sum(1, dtype=torch.float32).sum(0).to(dy.dtype)
+            db = column_sum(dy2, dy.dtype)
         return dx, dw, db
 
 

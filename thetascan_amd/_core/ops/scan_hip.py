@@ -206,15 +206,20 @@ def _scan_once(
     ke_mode, ke = _ext_arg(k_ext)
     ve_mode, ve = _ext_arg(v_ext)
 
-    desc = _lib.ScanDesc(
-        B, H, T, dkw, dvw, code, retention, int(reverse), qe_mode, ke_mode, ve_mode,
-        out_mode, float(out_scale), int(seg_chunks), int(want_final),
-    )
-    c_dkp, c_dvp, c_nseg = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    _lib.check(lib.ts_scan_layout(ctypes.byref(desc), ctypes.byref(c_dkp), ctypes.byref(c_dvp),
-                                  ctypes.byref(c_nseg)), "scan layout")
-    ws_bytes = ctypes.c_size_t()
-    _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(ws_bytes)), "scan workspace")
+    fields = (B, H, T, dkw, dvw, code, retention, int(reverse), qe_mode, ke_mode, ve_mode,
+              out_mode, float(out_scale), int(seg_chunks), int(want_final))
+    desc = _lib.ScanDesc(*fields)
+    plan = _PLANS.get(fields)
+    if plan is None:
+        c_dkp, c_dvp, c_nseg = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        _lib.check(lib.ts_scan_layout(ctypes.byref(desc), ctypes.byref(c_dkp), ctypes.byref(c_dvp),
+                                      ctypes.byref(c_nseg)), "scan layout")
+        c_ws = ctypes.c_size_t()
+        _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan workspace")
+        if len(_PLANS) > 256:
+            _PLANS.clear()
+        plan = _PLANS[fields] = (c_dkp.value, c_dvp.value, c_ws.value)
+    dk_pad, dv_pad, ws_bytes = plan
 
     out_dtype = dtype if out_mode == _lib.OUT_STORE else torch.float32
     if out is None:
@@ -231,10 +236,10 @@ def _scan_once(
         ext_out = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
     final = None
     if want_final:
-        final = torch.zeros(B * H, c_dkp.value, c_dvp.value, dtype=torch.float32, device=q.device)
+        final = torch.zeros(B * H, dk_pad, dv_pad, dtype=torch.float32, device=q.device)
     workspace = None
-    if ws_bytes.value:
-        workspace = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
+    if ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
 
     la = None
     if retention == _lib.RET_STATIC:
@@ -252,20 +257,26 @@ def _scan_once(
         _lib.strided(ext_out if want_ext_out else None),
         final.data_ptr() if final is not None else None,
     )
-    out_bytes = B * H * T * dv * out_buf.element_size() * (2 if out_mode == _lib.OUT_ACCUM_F32 else 1)
-    traffic = (_lib.nbytes(q, k, v, qe, ke, ve, dec) + out_bytes
-               + (_lib.nbytes(ext_out) * (2 if out_mode == _lib.OUT_ACCUM_F32 else 1) if want_ext_out else 0))
+    def traffic():
+        rw = 2 if out_mode == _lib.OUT_ACCUM_F32 else 1
+        out_bytes = B * H * T * dv * out_buf.element_size() * rw
+        return (_lib.nbytes(q, k, v, qe, ke, ve, dec) + out_bytes
+                + (_lib.nbytes(ext_out) * rw if want_ext_out else 0))
+
     with _lib.timed("ts_scan_fwd", traffic):
         status = lib.ts_scan_fwd(
             ctypes.byref(desc), ctypes.byref(io),
             workspace.data_ptr() if workspace is not None else None,
-            ws_bytes.value, _lib.stream_handle(q.device),
+            ws_bytes, _lib.stream_handle(q.device),
         )
     _lib.check(status, "ts_scan_fwd")
     result = out_buf if out is not None else out_buf[..., :dv]
     if final is not None:
-        final = final.view(B, H, c_dkp.value, c_dvp.value)
+        final = final.view(B, H, dk_pad, dv_pad)
     return result, ext_out, final
+
+
+_PLANS: dict = {}
 
 
 # ------------------------------------------------------------------ retentions

@@ -230,6 +230,11 @@ def load() -> ctypes.CDLL:
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
+        lib.ts_col_sums.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
+                                    ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+        lib.ts_sum_slots.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                     ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32, ctypes.c_float,
+                                     ctypes.c_void_p]
         if lib.ts_abi_version() != 1:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
@@ -259,7 +264,14 @@ def ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The caller's current HIP stream on ``device`` (kernels launch on it)."""
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -282,17 +294,47 @@ def record_launches():
         _RECORDS = previous
 
 
-@contextlib.contextmanager
-def timed(name: str, nbytes: int):
-    """Bracket one entry-point call with events when launches are recorded."""
+def recording() -> bool:
+    """Whether entry-point launches are being recorded."""
+    return _RECORDS is not None
+
+
+class _Untimed:
+    __slots__ = ()
+
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_UNTIMED = _Untimed()
+
+
+class _Timed:
+    __slots__ = ("name", "nbytes", "start", "end")
+
+    def __init__(self, name, nbytes):
+        self.name, self.nbytes = name, nbytes
+
+    def __enter__(self):
+        self.start, self.end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        self.start.record()
+
+    def __exit__(self, *exc):
+        self.end.record()
+        nb = self.nbytes() if callable(self.nbytes) else self.nbytes
+        _RECORDS.append((self.name, self.start, self.end, int(nb)))
+        return False
+
+
+def timed(name: str, nbytes):
+    """Bracket one entry-point call with events when launches are recorded.
+    ``nbytes`` (an int or a callable returning one) is evaluated only then."""
     if _RECORDS is None:
-        yield
-        return
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    yield
-    end.record()
-    _RECORDS.append((name, start, end, int(nbytes)))
+        return _UNTIMED
+    return _Timed(name, nbytes)
 
 
 def nbytes(*tensors) -> int:

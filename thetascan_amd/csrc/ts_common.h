@@ -9,6 +9,10 @@ namespace ts {
 // Record a message for ts_last_error() and return `code` (host side).
 int fail(int code, const char* fmt, ...);
 
+// Raise a kernel's dynamic-LDS limit to `bytes` once per process (later
+// launches, including launches recorded into a graph, skip the call).
+hipError_t ensure_lds_limit(const void* fn, int bytes);
+
 typedef __bf16 bf16;
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -166,6 +166,61 @@ __global__ __launch_bounds__(256) void wcumsum_kernel(int B, int H, int T, int F
   }
 }
 
+// out[i] = scale * (sum_s a[s][i] + sum_s b[s][i]): the partial weight-gradient
+// slots of one or two ts_feature_bwd calls, one element per thread (coalesced
+// over i for every slot).
+__global__ __launch_bounds__(256) void sum_slots_kernel(const float* a, int na, const float* b, int nb, int64_t n,
+                                                        void* out, int out_bf16, float scale) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float acc0 = 0.0f, acc1 = 0.0f;
+  int s = 0;
+  for (; s + 1 < na; s += 2) {
+    acc0 += a[(int64_t)s * n + i];
+    acc1 += a[(int64_t)(s + 1) * n + i];
+  }
+  if (s < na) acc0 += a[(int64_t)s * n + i];
+  for (s = 0; s + 1 < nb; s += 2) {
+    acc0 += b[(int64_t)s * n + i];
+    acc1 += b[(int64_t)(s + 1) * n + i];
+  }
+  if (s < nb) acc0 += b[(int64_t)s * n + i];
+  const float v = scale * (acc0 + acc1);
+  if (out_bf16)
+    ((bf16*)out)[i] = (bf16)v;
+  else
+    ((float*)out)[i] = v;
+}
+
+// parts[s][c] = sum over rows r of slice s of x[r * stride + c]; eight
+// consecutive columns per thread (one 16-byte load of bf16, two of fp32).
+template <typename E>
+__global__ __launch_bounds__(256) void col_sums_kernel(const E* x, int64_t rows, int cols, int64_t stride,
+                                                       float* parts, int slices) {
+  const int groups = cols / 8;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)groups * slices) return;
+  const int s = (int)(gid / groups);
+  const int c = (int)(gid - (int64_t)s * groups) * 8;
+  const int64_t per = (rows + slices - 1) / slices;
+  const int64_t r0 = (int64_t)s * per;
+  const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t r = r0; r < r1; ++r) {
+    const E* p = x + r * stride + c;
+#pragma unroll
+    for (int h = 0; h < 8 / Vec16<E>::N; ++h) {
+      Vec16<E> v;
+      v.raw = *(const uint4*)(p + h * Vec16<E>::N);
+#pragma unroll
+      for (int e = 0; e < Vec16<E>::N; ++e) acc[h * Vec16<E>::N + e] += tof(v.e[e]);
+    }
+  }
+  float* out = parts + (int64_t)s * cols + c;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = acc[e];
+}
+
 }  // namespace ts
 
 namespace {
@@ -245,6 +300,37 @@ int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t str
   else
     hipLaunchKernelGGL(ts::read_bwd_kernel<float>, grid, dim3(256), 0, stream, p, p2);
   return finish("read bwd");
+}
+
+int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t n, void* out, int32_t out_dtype,
+                 float scale, hipStream_t stream) {
+  if (n < 0 || na < 0 || nb < 0) return fail(TS_ERR_VALUE, "sum_slots: bad sizes");
+  if ((na && !a) || (nb && !b) || !out) return fail(TS_ERR_VALUE, "sum_slots: missing buffers");
+  if (out_dtype != TS_BF16 && out_dtype != TS_F32) return fail(TS_ERR_VALUE, "sum_slots: unknown dtype");
+  if (n == 0) return TS_OK;
+  hipLaunchKernelGGL(ts::sum_slots_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, na, b, nb, n,
+                     out, out_dtype == TS_BF16 ? 1 : 0, scale);
+  return finish("sum_slots");
+}
+
+int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_t row_stride, float* parts,
+                int32_t slices, hipStream_t stream) {
+  if (!x || !parts || rows < 0 || cols < 0 || slices < 1) return fail(TS_ERR_VALUE, "col_sums: bad arguments");
+  if (dtype != TS_BF16 && dtype != TS_F32) return fail(TS_ERR_VALUE, "col_sums: unknown dtype");
+  const int esize = dtype == TS_BF16 ? 2 : 4;
+  if (cols % 8 || row_stride % 8 || ((uintptr_t)x & 15u))
+    return fail(TS_ERR_VALUE, "col_sums: columns and rows must be 8-element aligned");
+  (void)esize;
+  const int64_t n = (int64_t)(cols / 8) * slices;
+  if (n == 0) return TS_OK;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (dtype == TS_BF16)
+    hipLaunchKernelGGL(ts::col_sums_kernel<ts::bf16>, grid, dim3(256), 0, stream, (const ts::bf16*)x, rows, cols,
+                       row_stride, parts, slices);
+  else
+    hipLaunchKernelGGL(ts::col_sums_kernel<float>, grid, dim3(256), 0, stream, (const float*)x, rows, cols,
+                       row_stride, parts, slices);
+  return finish("col_sums");
 }
 
 int ts_wcumsum(const ts_wcumsum_desc* d, ts_strided x, ts_strided out, const float* log_alpha,

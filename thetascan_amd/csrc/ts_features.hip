@@ -871,7 +871,7 @@ int plan_feature(const ts_feature_desc* d, bool fwd, bool resid, bool want_wgrad
 int launch_feature(FeatFn fn, const Plan& P, hipStream_t stream, ts::FeatP& p) {
   p.groups = P.groups;
   if (P.lds > 65536) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)P.lds);
+    hipError_t e = ts::ensure_lds_limit((const void*)fn, (int)P.lds);
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "feature: LDS request failed: %s", hipGetErrorString(e));
   }
   hipLaunchKernelGGL(fn, P.grid, dim3(256), P.lds, stream, p);

@@ -39,6 +39,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+#include <unordered_map>
+
 namespace ts {
 
 constexpr int C = 64;  // tokens per tile
@@ -752,6 +755,17 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+hipError_t ensure_lds_limit(const void* fn, int bytes) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, int> limits;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = limits.find(fn);
+  if (it != limits.end() && it->second >= bytes) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) limits[fn] = bytes;
+  return e;
+}
+
 }  // namespace ts
 
 namespace {
@@ -871,7 +885,7 @@ int check_stream(const char* name, const ts_strided& s, int vec, bool required) 
 int launch(KernelFn fn, dim3 grid, size_t lds, hipStream_t stream, const ts::ScanP& p) {
   if (!fn) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: no kernel for this shape");
   if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = ts::ensure_lds_limit((const void*)fn, (int)lds);
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: LDS request failed: %s", hipGetErrorString(e));
   }
   hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, p);

@@ -254,8 +254,8 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
 
 /* parts[s][c] = sum of x[r * row_stride + c] over the rows r of slice s
  * (rows split into `slices` equal runs), for a [rows, cols] matrix of
- * ts_dtype `dtype` with cols and row_stride multiples of 8 and a 16-byte
- * aligned base.  Followed by ts_sum_slots it is the bias gradient of the
+ * ts_dtype `dtype` with cols (at most 2048) and row_stride multiples of 8
+ * and a 16-byte aligned base.  Followed by ts_sum_slots it is the bias gradient of the
  * output-gate projection (gates.py:34-40, summed over every token). */
 int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_t row_stride, float* parts,
                 int32_t slices, hipStream_t stream);

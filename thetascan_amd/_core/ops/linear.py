@@ -69,7 +69,7 @@ def column_sum(x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
           and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0)
     if not ok:
         return x2.float().sum(0).to(dtype)
-    slices = max(1, min(256, rows // 64))
+    slices = max(1, min(256, rows // 128))
     parts = torch.empty(slices, cols, dtype=torch.float32, device=x2.device)
     lib = _lib.load()
     _lib.check(lib.ts_col_sums(x2.data_ptr(), _lib.dtype_code(x2.dtype), rows, cols, x2.stride(0),

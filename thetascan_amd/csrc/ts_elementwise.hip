@@ -167,58 +167,94 @@ __global__ __launch_bounds__(256) void wcumsum_kernel(int B, int H, int T, int F
 }
 
 // out[i] = scale * (sum_s a[s][i] + sum_s b[s][i]): the partial weight-gradient
-// slots of one or two ts_feature_bwd calls, one element per thread (coalesced
-// over i for every slot).
+// slots of one or two ts_feature_bwd calls.  A block covers `opb` consecutive
+// outputs; its 256 / opb thread rows split the slots between them (four
+// independent loads in flight per thread) and combine through LDS.
 __global__ __launch_bounds__(256) void sum_slots_kernel(const float* a, int na, const float* b, int nb, int64_t n,
-                                                        void* out, int out_bf16, float scale) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float acc0 = 0.0f, acc1 = 0.0f;
-  int s = 0;
-  for (; s + 1 < na; s += 2) {
-    acc0 += a[(int64_t)s * n + i];
-    acc1 += a[(int64_t)(s + 1) * n + i];
+                                                        void* out, int out_bf16, float scale, int opb) {
+  __shared__ float red[256];
+  const int tid = threadIdx.x;
+  const int c = tid % opb, j = tid / opb, sub = 256 / opb;
+  const int64_t i = (int64_t)blockIdx.x * opb + c;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (i < n) {
+    const int total = na + nb;
+    int s = j;
+    for (; s + 3 * sub < total; s += 4 * sub) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = s + u * sub;
+        acc[u] += t < na ? a[(int64_t)t * n + i] : b[(int64_t)(t - na) * n + i];
+      }
+    }
+    for (; s < total; s += sub) acc[0] += s < na ? a[(int64_t)s * n + i] : b[(int64_t)(s - na) * n + i];
   }
-  if (s < na) acc0 += a[(int64_t)s * n + i];
-  for (s = 0; s + 1 < nb; s += 2) {
-    acc0 += b[(int64_t)s * n + i];
-    acc1 += b[(int64_t)(s + 1) * n + i];
+  red[tid] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (j == 0 && i < n) {
+    float v = 0.f;
+    for (int r = 0; r < sub; ++r) v += red[r * opb + c];
+    v *= scale;
+    if (out_bf16)
+      ((bf16*)out)[i] = (bf16)v;
+    else
+      ((float*)out)[i] = v;
   }
-  if (s < nb) acc0 += b[(int64_t)s * n + i];
-  const float v = scale * (acc0 + acc1);
-  if (out_bf16)
-    ((bf16*)out)[i] = (bf16)v;
-  else
-    ((float*)out)[i] = v;
 }
 
-// parts[s][c] = sum over rows r of slice s of x[r * stride + c]; eight
-// consecutive columns per thread (one 16-byte load of bf16, two of fp32).
+// parts[blk][c] = sum of x[r * stride + c] over the `rows_per_block` rows of
+// block blk.  A block is 256 / (cols / 8) row lanes x (cols / 8) column
+// groups of eight (one 16-byte load of bf16, two of fp32); row lanes step by
+// their count with four loads in flight and combine through LDS.
 template <typename E>
 __global__ __launch_bounds__(256) void col_sums_kernel(const E* x, int64_t rows, int cols, int64_t stride,
-                                                       float* parts, int slices) {
+                                                       float* parts, int rows_per_block) {
+  __shared__ float red[256 * 8];
   const int groups = cols / 8;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)groups * slices) return;
-  const int s = (int)(gid / groups);
-  const int c = (int)(gid - (int64_t)s * groups) * 8;
-  const int64_t per = (rows + slices - 1) / slices;
-  const int64_t r0 = (int64_t)s * per;
-  const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+  const int tid = threadIdx.x;
+  const int cg = tid % groups, rl = tid / groups, lanes = 256 / groups;
+  const int c = cg * 8;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int64_t r = r0; r < r1; ++r) {
-    const E* p = x + r * stride + c;
+  if (rl < lanes) {
+    int64_t r = r0 + rl;
+    for (; r + 3 * lanes < r1; r += 4 * lanes) {
+      Vec16<E> v[4][8 / Vec16<E>::N];
 #pragma unroll
-    for (int h = 0; h < 8 / Vec16<E>::N; ++h) {
-      Vec16<E> v;
-      v.raw = *(const uint4*)(p + h * Vec16<E>::N);
+      for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int e = 0; e < Vec16<E>::N; ++e) acc[h * Vec16<E>::N + e] += tof(v.e[e]);
+        for (int h = 0; h < 8 / Vec16<E>::N; ++h)
+          v[u][h].raw = *(const uint4*)(x + (r + u * lanes) * stride + c + h * Vec16<E>::N);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int h = 0; h < 8 / Vec16<E>::N; ++h)
+#pragma unroll
+          for (int e = 0; e < Vec16<E>::N; ++e) acc[h * Vec16<E>::N + e] += tof(v[u][h].e[e]);
+    }
+    for (; r < r1; r += lanes) {
+#pragma unroll
+      for (int h = 0; h < 8 / Vec16<E>::N; ++h) {
+        Vec16<E> v;
+        v.raw = *(const uint4*)(x + r * stride + c + h * Vec16<E>::N);
+#pragma unroll
+        for (int e = 0; e < Vec16<E>::N; ++e) acc[h * Vec16<E>::N + e] += tof(v.e[e]);
+      }
     }
   }
-  float* out = parts + (int64_t)s * cols + c;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) out[e] = acc[e];
+  for (int e = 0; e < 8; ++e) red[tid * 8 + e] = acc[e];
+  __syncthreads();
+  if (rl == 0) {
+    float* out = parts + (int64_t)blockIdx.x * cols + c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = 0.f;
+      for (int l = 0; l < lanes; ++l) v += red[(l * groups + cg) * 8 + e];
+      out[e] = v;
+    }
+  }
 }
 
 }  // namespace ts
@@ -308,8 +344,11 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
   if ((na && !a) || (nb && !b) || !out) return fail(TS_ERR_VALUE, "sum_slots: missing buffers");
   if (out_dtype != TS_BF16 && out_dtype != TS_F32) return fail(TS_ERR_VALUE, "sum_slots: unknown dtype");
   if (n == 0) return TS_OK;
-  hipLaunchKernelGGL(ts::sum_slots_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, na, b, nb, n,
-                     out, out_dtype == TS_BF16 ? 1 : 0, scale);
+  // outputs per block: as many as keep >= 512 blocks, at least 4 slot rows per output
+  int opb = 64;
+  while (opb > 4 && (n + opb - 1) / opb < 512) opb >>= 1;
+  hipLaunchKernelGGL(ts::sum_slots_kernel, dim3((unsigned)((n + opb - 1) / opb)), dim3(256), 0, stream, a, na, b, nb,
+                     n, out, out_dtype == TS_BF16 ? 1 : 0, scale, opb);
   return finish("sum_slots");
 }
 
@@ -317,19 +356,17 @@ int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_
                 int32_t slices, hipStream_t stream) {
   if (!x || !parts || rows < 0 || cols < 0 || slices < 1) return fail(TS_ERR_VALUE, "col_sums: bad arguments");
   if (dtype != TS_BF16 && dtype != TS_F32) return fail(TS_ERR_VALUE, "col_sums: unknown dtype");
-  const int esize = dtype == TS_BF16 ? 2 : 4;
   if (cols % 8 || row_stride % 8 || ((uintptr_t)x & 15u))
     return fail(TS_ERR_VALUE, "col_sums: columns and rows must be 8-element aligned");
-  (void)esize;
-  const int64_t n = (int64_t)(cols / 8) * slices;
-  if (n == 0) return TS_OK;
-  const dim3 grid((unsigned)((n + 255) / 256));
+  if (cols / 8 > 256) return fail(TS_ERR_NOT_IMPLEMENTED, "col_sums: more than 2048 columns");
+  if (cols == 0) return TS_OK;
+  const int rows_per_block = (int)((rows + slices - 1) / slices);
   if (dtype == TS_BF16)
-    hipLaunchKernelGGL(ts::col_sums_kernel<ts::bf16>, grid, dim3(256), 0, stream, (const ts::bf16*)x, rows, cols,
-                       row_stride, parts, slices);
+    hipLaunchKernelGGL(ts::col_sums_kernel<ts::bf16>, dim3((unsigned)slices), dim3(256), 0, stream,
+                       (const ts::bf16*)x, rows, cols, row_stride, parts, rows_per_block);
   else
-    hipLaunchKernelGGL(ts::col_sums_kernel<float>, grid, dim3(256), 0, stream, (const float*)x, rows, cols,
-                       row_stride, parts, slices);
+    hipLaunchKernelGGL(ts::col_sums_kernel<float>, dim3((unsigned)slices), dim3(256), 0, stream, (const float*)x,
+                       rows, cols, row_stride, parts, rows_per_block);
   return finish("col_sums");
 }
 

@@ -55,6 +55,8 @@ def weight_grad(dy2: torch.Tensor, x2: torch.Tensor, dtype: torch.dtype) -> torc
     """dy2^T x2 over all rows -> [n_out, n_in] in ``dtype`` (split-K GEMM + slot sum)."""
     rows = dy2.shape[0]
     s = _slices(rows)
+    while s > 1 and s * dy2.shape[1] * x2.shape[1] > (8 << 20):  # partial slots stay within 32 MiB
+        s //= 2
     if not (dy2.is_cuda and dy2.dtype in (torch.bfloat16, torch.float16)):
         return split_k_outer(dy2.unsqueeze(0), x2.unsqueeze(0))[0].to(dtype)
     parts = torch.bmm(dy2.reshape(s, rows // s, -1).transpose(1, 2), x2.reshape(s, rows // s, -1),

@@ -72,15 +72,35 @@ __device__ __forceinline__ Rows<E> rows_of(const Str& s, int b, int h) {
 
 __device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// Values of lanes l ^ 16 and l ^ 32 by the gfx950 row-swap instructions
+// v_permlane16_swap / v_permlane32_swap: swapping a VGPR with a copy of itself
+// leaves lanes l and l ^ 16 (l ^ 32) in the two registers, so the per-token
+// reductions over the four lane groups need no LDS round trip.  Written as
+// inline asm because the compiler's builtins for these instructions return
+// the same register for both halves of the swapped pair.  The s_nop covers
+// the wait states between a VALU write of a VGPR and a permlane read of it.
+struct LanePair {
+  float a, b;
+};
+__device__ __forceinline__ LanePair xor16_pair(float v) {
+  LanePair p{v, v};
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(p.a), "+v"(p.b));
+  return p;
+}
+__device__ __forceinline__ LanePair xor32_pair(float v) {
+  LanePair p{v, v};
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(p.a), "+v"(p.b));
+  return p;
+}
 __device__ __forceinline__ float sum_g(float v) {  // over the 4 lane groups of a token
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  LanePair p = xor16_pair(v);
+  p = xor32_pair(p.a + p.b);
+  return p.a + p.b;
 }
 __device__ __forceinline__ float max_g(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  LanePair p = xor16_pair(v);
+  p = xor32_pair(fmaxf(p.a, p.b));
+  return fmaxf(p.a, p.b);
 }
 
 // Four consecutive elements <-> floats.
@@ -467,8 +487,10 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
 template <int D, int MB>
 constexpr int wgrad_blocks() { return ((MB + 3) / 4) * (D / 16); }
 
+// Two resident waves per SIMD for the common bf16 widths: the allocator then
+// fits the backward in 256 registers without spilling.
 template <typename E, int D, int MB, bool WG, bool RESID>
-__global__ __launch_bounds__(256) void feature_bwd_kernel(FeatP p) {
+__global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)) void feature_bwd_kernel(FeatP p) {
   typedef LdsIO<E> IO;
   typedef TokFrag<E> TF;
   constexpr bool WL = weights_in_lds<E, D, MB, false, WG>();

@@ -228,6 +228,62 @@ typedef struct ts_read_bwd_io {
 
 int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t stream);
 
+/* ------------------------------------------------------ B-spline features */
+
+/* Projected open-uniform B-spline feature map
+ * (src/thetascan/_core/ops/kernel_features.py:138-230):
+ *   c = clamp(scale_h * pre[b,h,t,p], -bound, nextafter(bound, -inf))
+ *   out[b,h,t, p*n_basis + j] = N_j(c) / sum_i N_i(c) / P
+ * N_j are the n_basis Cox-de Boor functions of `degree` on the clamped knot
+ * vector (degree+1 copies of -bound and of +bound around n_basis-degree-1
+ * uniform interior knots).  n_basis <= 32, degree <= 7.  scale_h is an fp32
+ * [H] array (learned per-head scale) or NULL for the constant `scale`. */
+typedef struct ts_bspline_desc {
+  int32_t B, H, T, P;   /* pre [B,H,T,P]; out [B,H,T,P*n_basis]               */
+  int32_t n_basis, degree;
+  int32_t dtype;        /* of pre, out, dout and dpre                          */
+  float bound;
+  float scale;          /* used when scale_h is NULL                           */
+} ts_bspline_desc;
+
+int ts_bspline_fwd(const ts_bspline_desc* desc, ts_strided pre, const float* scale_h, ts_strided out,
+                   hipStream_t stream);
+
+/* Number of fp32 partial sums per head that ts_bspline_bwd writes to
+ * dscale_part ([H][nparts]; their sum over the last axis is dL/dscale_h). */
+int ts_bspline_parts(const ts_bspline_desc* desc, int32_t* nparts);
+
+/* dpre = (d out / d pre)^T dout, and when scale_h is set the partial sums of
+ * (d out / d scale_h)^T dout.  Differentiates the clamp, the recursion, the
+ * clamp at zero and the renormalisation exactly as written above. */
+int ts_bspline_bwd(const ts_bspline_desc* desc, ts_strided pre, const float* scale_h, ts_strided dout,
+                   ts_strided dpre, float* dscale_part, hipStream_t stream);
+
+/* ------------------------------------------------------------ bank blend */
+
+/* Temporal-bank blend of n_in (<= 8) read views (block.py:667-718):
+ *   y[b,h,t,:] = sum_i coef[i*H + h] * in_i[b,h,t,:]
+ * Fast bank:  coef = (1 - sum_j eta_j, eta_1 .. eta_J) over (R_0, R_1 .. R_J);
+ * stale bank: coef = (1, -eta_1 .. -eta_J, sum_j eta_j) over
+ * (R_0, R_stale_1 .. R_stale_J, R_null). */
+typedef struct ts_blend_desc {
+  int32_t B, H, T, d;
+  int32_t n_in;
+  int32_t dtype;        /* of every input, y, dy and din                       */
+} ts_blend_desc;
+
+int ts_blend_fwd(const ts_blend_desc* desc, const ts_strided* in, const float* coef, ts_strided y,
+                 hipStream_t stream);
+
+/* Number of fp32 partial sums per (input, head) that ts_blend_bwd writes to
+ * dcoef_part ([n_in][H][nparts]). */
+int ts_blend_parts(const ts_blend_desc* desc, int32_t* nparts);
+
+/* din_i = coef[i*H + h] * dy (din entries may be NULL to skip an input) and
+ * partial sums of dL/dcoef[i*H + h] = sum dy * in_i. */
+int ts_blend_bwd(const ts_blend_desc* desc, const ts_strided* in, const float* coef, ts_strided dy,
+                 const ts_strided* din, float* dcoef_part, hipStream_t stream);
+
 /* --------------------------------------------------------------- prefixes */
 
 /* Decayed prefix sum along T of an fp32 [B,H,T,F] stream:

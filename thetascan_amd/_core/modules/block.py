@@ -23,7 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
-from ..ops import engine, fused
+from ..ops import engine, fused, maps
 from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
@@ -460,12 +460,9 @@ class ThetaScan(nn.Module):
         y = reads[0]
         if cfg.read_fade:
             if cfg.read_fade_mode == "fast":
-                for out_fast, eta in zip(reads[1:], etas):
-                    y = y + eta.to(y.dtype) * (out_fast - reads[0])
+                y = maps.bank_blend(reads, maps.fast_coefficients(etas))
             else:
-                base = reads[-1]
-                for out_stale, eta in zip(reads[1:-1], etas):
-                    y = y - eta.to(y.dtype) * (out_stale - base)
+                y = maps.bank_blend(reads, maps.stale_coefficients(etas))
         if self.ogate is not None:
             y = y * self.ogate(x)
         y = y.transpose(1, 2).reshape(B, T, H * d)

@@ -1,16 +1,19 @@
 """Positive feature maps of the kernel memory (GPU tensor form).
 
 Same maps and numerical safeguards as src/thetascan/_core/ops/kernel_features.py:
-softmax partition with optional relative-to-max sparsity (73-113, 43-70),
-ReLU^2 ridge with uniform fallback (116-135) and the clamped open-uniform cubic
-B-spline basis (138-230).  The depth-1 kernel-memory hot path evaluates the
-softmax/ReLU^2 maps inside the fused HIP write kernel (ts_feature_fwd); these
-tensor forms serve the configurations that kernel does not cover (B-spline,
-sparse softmax, score biases, learned sharpness, GN reads).
+softmax partition with optional relative-to-max sparsity (73-113, 43-70) and
+ReLU^2 ridge with uniform fallback (116-135).  The clamped open-uniform
+B-spline map (138-230) runs in its own HIP kernel (ts_bspline_fwd/bwd).  The
+depth-1 kernel-memory hot path evaluates the softmax/ReLU^2 maps inside the
+fused HIP write kernel (ts_feature_fwd); these tensor forms serve the
+configurations that kernel does not cover (sparse softmax, score biases,
+learned sharpness, GN reads).
 """
 from __future__ import annotations
 
 import torch
+
+from . import maps
 
 
 def head_parameter(value: torch.Tensor, reference: torch.Tensor) -> torch.Tensor:
@@ -82,39 +85,10 @@ def relu2_ridge_features(pre, *, score_bias, relu2_threshold=None, eps: float):
     return torch.where(mass > eps, features / mass.clamp_min(eps), uniform)
 
 
-def open_uniform_bspline_basis(coordinates, *, n_basis: int, degree: int = 3, bound: float = 3.0):
-    if degree < 0:
-        raise ValueError("B-spline degree must be non-negative")
-    if n_basis <= degree:
-        raise ValueError("B-spline basis count must exceed its degree")
-    if bound <= 0.0:
-        raise ValueError("B-spline bound must be positive")
-    dtype, device = coordinates.dtype, coordinates.device
-    low = torch.tensor(-bound, dtype=dtype, device=device)
-    high = torch.tensor(bound, dtype=dtype, device=device)
-    n_inner = n_basis - degree - 1
-    interior = (torch.linspace(-bound, bound, n_inner + 2, dtype=dtype, device=device)[1:-1]
-                if n_inner else coordinates.new_empty(0))
-    knots = torch.cat([low.repeat(degree + 1), interior, high.repeat(degree + 1)])
-    x = torch.minimum(coordinates.clamp(min=-bound, max=bound), torch.nextafter(high, low)).unsqueeze(-1)
-    basis = ((x >= knots[:-1]) & (x < knots[1:])).to(dtype)
-    tiny = torch.finfo(dtype).tiny
-    for order in range(1, degree + 1):
-        count = knots.numel() - order - 1
-        left_den = knots[order:order + count] - knots[:count]
-        right_den = knots[order + 1:order + 1 + count] - knots[1:1 + count]
-        left = torch.where(left_den > 0, (x - knots[:count]) / left_den.clamp_min(tiny), torch.zeros_like(left_den))
-        right = torch.where(right_den > 0, (knots[order + 1:order + 1 + count] - x) / right_den.clamp_min(tiny),
-                            torch.zeros_like(right_den))
-        basis = left * basis[..., :count] + right * basis[..., 1:count + 1]
-    basis = basis.clamp_min(0.0)
-    return basis / basis.sum(dim=-1, keepdim=True).clamp_min(tiny)
-
-
 def projected_bspline_features(pre, *, n_basis: int, degree: int, bound: float, scale, fallback_scale: float):
-    coordinates = pre * _gain(scale, fallback_scale, pre)
-    basis = open_uniform_bspline_basis(coordinates, n_basis=n_basis, degree=degree, bound=bound)
-    return basis.flatten(-2) / float(pre.shape[-1])
+    """The projected B-spline map on the GPU (ts_bspline_fwd / ts_bspline_bwd)."""
+    return maps.bspline_features(pre, n_basis=n_basis, degree=degree, bound=bound,
+                                 scale=fallback_scale if scale is None else scale)
 
 
 def feature_map(pre, cfg, *, softmax_gain=None, spline_scale=None, score_bias=None, relu2_threshold=None,

@@ -1,0 +1,185 @@
+"""HIP B-spline feature map and temporal-bank blend (autograd wrappers).
+
+``bspline_features`` replaces the tensor form of
+src/thetascan/_core/ops/kernel_features.py:138-230 (open-uniform basis and
+the projected feature map) with ``ts_bspline_fwd`` / ``ts_bspline_bwd``.
+``bank_blend`` replaces the fast / stale fade blends of
+src/thetascan/_core/modules/block.py:667-718 with ``ts_blend_fwd`` /
+``ts_blend_bwd``.  Both run on the caller's current stream; a CPU tensor or a
+missing library raises (no fallback).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ... import _lib
+
+_KERNEL_DTYPES = (torch.bfloat16, torch.float32)
+
+
+def _on_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """A view whose last axis is contiguous and whose rows start on 16 bytes
+    where the storage allows (otherwise the kernels take the scalar path)."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _as4d(t: torch.Tensor) -> torch.Tensor:
+    if t.ndim == 4:
+        return t
+    if t.ndim < 1:
+        raise ValueError("expected at least one axis")
+    return t.reshape(1, 1, -1, t.shape[-1])
+
+
+# ------------------------------------------------------------------ B-spline
+
+
+def _spline_desc(pre4, n_basis, degree, bound, scale):
+    B, H, T, P = pre4.shape
+    return _lib.BsplineDesc(B, H, T, P, int(n_basis), int(degree), _lib.dtype_code(pre4.dtype), float(bound),
+                            float(scale))
+
+
+class _BSpline(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pre, scale_h, n_basis, degree, bound, scale):
+        lib = _lib.load()
+        shape = pre.shape
+        pre4 = _rows(_as4d(pre))
+        desc = _spline_desc(pre4, n_basis, degree, bound, scale)
+        out = torch.empty(*pre4.shape[:3], pre4.shape[3] * n_basis, dtype=pre.dtype, device=pre.device)
+        sh = None if scale_h is None else scale_h.detach().to(torch.float32).contiguous()
+        with _lib.timed("ts_bspline_fwd", lambda: _lib.nbytes(pre4, out)):
+            status = lib.ts_bspline_fwd(ctypes.byref(desc), _lib.strided(pre4), _lib.ptr(sh), _lib.strided(out),
+                                        _lib.stream_handle(pre.device))
+        _lib.check(status, "ts_bspline_fwd")
+        ctx.save_for_backward(pre4, sh)
+        ctx.meta = (shape, n_basis, degree, bound, scale, scale_h is not None)
+        return out.reshape(*shape[:-1], shape[-1] * n_basis)
+
+    @staticmethod
+    def backward(ctx, dout):
+        pre4, sh = ctx.saved_tensors
+        shape, n_basis, degree, bound, scale, has_scale = ctx.meta
+        lib = _lib.load()
+        desc = _spline_desc(pre4, n_basis, degree, bound, scale)
+        d4 = _rows(dout.to(pre4.dtype).reshape(*pre4.shape[:3], pre4.shape[3] * n_basis))
+        dpre = torch.empty_like(pre4)
+        parts = None
+        if has_scale:
+            n = ctypes.c_int32()
+            _lib.check(lib.ts_bspline_parts(ctypes.byref(desc), ctypes.byref(n)), "ts_bspline_parts")
+            parts = torch.empty(pre4.shape[1], n.value, dtype=torch.float32, device=pre4.device)
+        with _lib.timed("ts_bspline_bwd", lambda: _lib.nbytes(pre4, d4, dpre)):
+            status = lib.ts_bspline_bwd(ctypes.byref(desc), _lib.strided(pre4), _lib.ptr(sh), _lib.strided(d4),
+                                        _lib.strided(dpre), _lib.ptr(parts), _lib.stream_handle(pre4.device))
+        _lib.check(status, "ts_bspline_bwd")
+        dscale = parts.sum(-1) if has_scale and ctx.needs_input_grad[1] else None
+        return dpre.reshape(shape), dscale, None, None, None, None
+
+
+def bspline_features(pre: torch.Tensor, *, n_basis: int, degree: int, bound: float, scale) -> torch.Tensor:
+    """``basis(pre * scale).flatten(-2) / P`` (kernel_features.py:208-230).
+
+    ``scale`` is a float (fixed scale) or a per-head tensor ``[H]`` for a
+    head-major ``[B,H,T,P]`` input (the learned per-head scale).
+    """
+    _on_gpu(pre)
+    if pre.dtype not in _KERNEL_DTYPES:
+        raise NotImplementedError(f"hip B-spline features support bf16 and fp32, got {pre.dtype}")
+    if degree < 0:
+        raise ValueError("B-spline degree must be non-negative")
+    if n_basis <= degree:
+        raise ValueError("B-spline basis count must exceed its degree")
+    if bound <= 0.0:
+        raise ValueError("B-spline bound must be positive")
+    if torch.is_tensor(scale):
+        if pre.ndim != 4 or scale.ndim != 1 or scale.shape[0] != pre.shape[1]:
+            raise ValueError(
+                "kernel control must have shape [n_heads] or [n_heads, n_features], "
+                f"got {tuple(scale.shape)} for reference {tuple(pre.shape)}"
+            )
+        _on_gpu(scale)
+        return _BSpline.apply(pre, scale, n_basis, degree, bound, 1.0)
+    return _BSpline.apply(pre, None, n_basis, degree, bound, float(scale))
+
+
+# ---------------------------------------------------------------- bank blend
+
+
+def _blend_desc(first, n_in):
+    B, H, T, d = first.shape
+    return _lib.BlendDesc(B, H, T, d, n_in, _lib.dtype_code(first.dtype))
+
+
+class _Blend(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, coef, *inputs):
+        lib = _lib.load()
+        ins = [_rows(t) for t in inputs]
+        desc = _blend_desc(ins[0], len(ins))
+        cf = coef.detach().to(torch.float32).contiguous()
+        y = torch.empty(ins[0].shape, dtype=ins[0].dtype, device=ins[0].device)
+        arr = (_lib.Strided * len(ins))(*[_lib.strided(t) for t in ins])
+        with _lib.timed("ts_blend_fwd", lambda: _lib.nbytes(*ins, y)):
+            status = lib.ts_blend_fwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(y),
+                                      _lib.stream_handle(y.device))
+        _lib.check(status, "ts_blend_fwd")
+        ctx.save_for_backward(cf, *ins)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        cf, *ins = ctx.saved_tensors
+        lib = _lib.load()
+        n = len(ins)
+        desc = _blend_desc(ins[0], n)
+        g = _rows(dy.to(ins[0].dtype))
+        dins = [torch.empty_like(t) if ctx.needs_input_grad[1 + i] else None for i, t in enumerate(ins)]
+        count = ctypes.c_int32()
+        _lib.check(lib.ts_blend_parts(ctypes.byref(desc), ctypes.byref(count)), "ts_blend_parts")
+        parts = torch.empty(n, ins[0].shape[1], count.value, dtype=torch.float32, device=g.device)
+        arr = (_lib.Strided * n)(*[_lib.strided(t) for t in ins])
+        darr = (_lib.Strided * n)(*[_lib.strided(t) for t in dins])
+        with _lib.timed("ts_blend_bwd", lambda: _lib.nbytes(*ins, g, *dins)):
+            status = lib.ts_blend_bwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(g), darr, _lib.ptr(parts),
+                                      _lib.stream_handle(g.device))
+        _lib.check(status, "ts_blend_bwd")
+        dcoef = parts.sum(-1) if ctx.needs_input_grad[0] else None
+        return (dcoef, *dins)
+
+
+def bank_blend(inputs, coef: torch.Tensor) -> torch.Tensor:
+    """``sum_i coef[i, h] * inputs[i]`` over ``[B,H,T,d]`` views (1 to 8 of them)."""
+    if not 1 <= len(inputs) <= 8:
+        raise ValueError("bank blend takes 1 to 8 views")
+    _on_gpu(coef, *inputs)
+    first = inputs[0]
+    if first.dtype not in _KERNEL_DTYPES or first.ndim != 4:
+        raise NotImplementedError("hip bank blend takes bf16 or fp32 [B,H,T,d] views")
+    for t in inputs:
+        if t.shape != first.shape or t.dtype != first.dtype:
+            raise ValueError("bank blend views must share shape and dtype")
+    if coef.shape != (len(inputs), first.shape[1]):
+        raise ValueError(f"bank blend coefficients must be [{len(inputs)}, {first.shape[1]}]")
+    return _Blend.apply(coef, *inputs)
+
+
+def fast_coefficients(etas) -> torch.Tensor:
+    """(1 - sum_j eta_j, eta_1 .. eta_J) over (R_0, R_1 .. R_J) (block.py:683-695)."""
+    eta = torch.stack([e.reshape(-1) for e in etas]).to(torch.float32)
+    return torch.cat([(1.0 - eta.sum(0)).unsqueeze(0), eta])
+
+
+def stale_coefficients(etas) -> torch.Tensor:
+    """(1, -eta_1 .. -eta_J, sum_j eta_j) over (R_0, R_stale_1 .. R_stale_J, R_null) (block.py:697-717)."""
+    eta = torch.stack([e.reshape(-1) for e in etas]).to(torch.float32)
+    return torch.cat([torch.ones_like(eta[:1]), -eta, eta.sum(0, keepdim=True)])

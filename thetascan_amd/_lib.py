@@ -181,6 +181,31 @@ class WcumsumDesc(ctypes.Structure):
     ]
 
 
+class BsplineDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("P", ctypes.c_int32),
+        ("n_basis", ctypes.c_int32),
+        ("degree", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("bound", ctypes.c_float),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class BlendDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("n_in", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 FEAT_RELU2 = 0
 FEAT_SOFTMAX = 1
 
@@ -235,6 +260,14 @@ def load() -> ctypes.CDLL:
         lib.ts_sum_slots.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                      ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32, ctypes.c_float,
                                      ctypes.c_void_p]
+        lib.ts_bspline_fwd.argtypes = [P(BsplineDesc), Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
+        lib.ts_bspline_parts.argtypes = [P(BsplineDesc), P(ctypes.c_int32)]
+        lib.ts_bspline_bwd.argtypes = [P(BsplineDesc), Strided, ctypes.c_void_p, Strided, Strided, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+        lib.ts_blend_fwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, ctypes.c_void_p]
+        lib.ts_blend_parts.argtypes = [P(BlendDesc), P(ctypes.c_int32)]
+        lib.ts_blend_bwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, P(Strided),
+                                     ctypes.c_void_p, ctypes.c_void_p]
         if lib.ts_abi_version() != 1:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 1
+#define TS_ABI_VERSION 2
 
 enum ts_status {
   TS_OK = 0,
@@ -72,6 +72,8 @@ typedef struct ts_scan_desc {
   float out_scale;      /* scale for the fp32 output modes                   */
   int32_t seg_chunks;   /* 64-token tiles per workgroup segment; 0 = auto    */
   int32_t want_final;   /* 1: write the final [dk_pad, dv_pad] state          */
+  int32_t value_split;  /* value columns per workgroup (16, 32, 64 or 128,
+                           dividing dv_pad); 0 = the whole width             */
 } ts_scan_desc;
 
 typedef struct ts_scan_io {

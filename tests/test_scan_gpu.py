@@ -96,6 +96,30 @@ def test_segmented_decomposition_is_exact(cuda, seg_chunks, kind):
     assert rel_err(out, expected) < 1e-4
 
 
+@pytest.mark.parametrize("split,Dv", [(16, 64), (32, 64), (64, 64), (16, 40), (0, 72)])
+@pytest.mark.parametrize("seg_chunks", [0, 1, 3])
+@pytest.mark.parametrize("kind", ["none", "stream"])
+def test_value_slices_are_exact(cuda, split, Dv, seg_chunks, kind):
+    """Workgroups that carry only a slice of the value columns (and, with
+    segments, their slice of the segment summaries) give the same scan, the
+    key-mass column of slice 0 included; the last slice may be ragged."""
+    from thetascan_amd._core.ops import scan_hip
+    from thetascan_amd import _lib
+
+    B, H, T, Dk = 2, 3, 333, 64
+    q, k, v = _streams(B, H, T, Dk, Dv, dtype=torch.float32, seed=11)
+    ret = _retention(kind, B, H, T)
+    vc = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1)
+    expected = oracle.linattn_naive(q.double(), k.double(), vc.double(), _oracle_decay(ret, q.double()))
+    kw = {"retention": _lib.RET_STREAM if kind == "stream" else _lib.RET_NONE}
+    if kind == "stream":
+        kw["decay"] = ret.to(cuda, torch.float32)
+    out, mass, _ = scan_hip.scan_launch(q.to(cuda), k.to(cuda), v.to(cuda), v_ext="ones", want_ext_out=True,
+                                        seg_chunks=seg_chunks, value_split=split, **kw)
+    assert rel_err(out, expected[..., :Dv]) < 1e-4, (split, Dv, seg_chunks, kind)
+    assert rel_err(mass, expected[..., Dv]) < 1e-4, (split, Dv, seg_chunks, kind)
+
+
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
 def test_reverse_scan_is_the_time_reversed_scan(cuda, kind):
     """The anti-causal mode used by the backward equals flipping time."""

@@ -102,6 +102,7 @@ def scan_launch(
     ext_out: torch.Tensor | None = None,
     want_final: bool = False,
     seg_chunks: int = 0,
+    value_split: int = 0,
 ):
     """One scan (several kernel launches when a width exceeds ``MAX_WIDTH``).
 
@@ -114,10 +115,11 @@ def scan_launch(
         return _scan_once(q, k, v, retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse,
                           q_ext=q_ext, k_ext=k_ext, v_ext=v_ext, out=out, out_mode=out_mode, out_scale=out_scale,
                           want_ext_out=want_ext_out, ext_out=ext_out, want_final=want_final,
-                          seg_chunks=seg_chunks)
+                          seg_chunks=seg_chunks, value_split=value_split)
     if want_final:
         raise NotImplementedError(f"hip scan: final state of widths dk={dk} dv={dv} above {MAX_WIDTH}")
-    kw = dict(retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse, seg_chunks=seg_chunks)
+    kw = dict(retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse, seg_chunks=seg_chunks,
+              value_split=value_split)
     B, H, T = q.shape[:3]
     if dv > MAX_WIDTH:
         pieces, ext_res = [], ext_out
@@ -175,6 +177,7 @@ def _scan_once(
     ext_out: torch.Tensor | None = None,
     want_final: bool = False,
     seg_chunks: int = 0,
+    value_split: int = 0,
 ):
     """One kernel launch.  Returns ``(out, ext_out, final_state)``.
 
@@ -207,7 +210,7 @@ def _scan_once(
     ve_mode, ve = _ext_arg(v_ext)
 
     fields = (B, H, T, dkw, dvw, code, retention, int(reverse), qe_mode, ke_mode, ve_mode,
-              out_mode, float(out_scale), int(seg_chunks), int(want_final))
+              out_mode, float(out_scale), int(seg_chunks), int(want_final), int(value_split))
     desc = _lib.ScanDesc(*fields)
     plan = _PLANS.get(fields)
     if plan is None:

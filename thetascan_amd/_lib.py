@@ -62,6 +62,7 @@ class ScanDesc(ctypes.Structure):
         ("out_scale", ctypes.c_float),
         ("seg_chunks", ctypes.c_int32),
         ("want_final", ctypes.c_int32),
+        ("value_split", ctypes.c_int32),
     ]
 
 
@@ -268,7 +269,7 @@ def load() -> ctypes.CDLL:
         lib.ts_blend_parts.argtypes = [P(BlendDesc), P(ctypes.c_int32)]
         lib.ts_blend_bwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, P(Strided),
                                      ctypes.c_void_p, ctypes.c_void_p]
-        if lib.ts_abi_version() != 1:
+        if lib.ts_abi_version() != 2:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

@@ -80,7 +80,8 @@ __device__ __forceinline__ void bstf(rsrc_t r, uint32_t off, float v) {
 }
 
 struct ScanP {
-  int B, H, T, dk, dv, dvp;
+  int B, H, T, dk, dv, dvp;  // dvp: padded value width of the whole scan
+  int vs;                    // padded value columns per workgroup (blockIdx.z selects the slice)
   int nchunks, seg_chunks, nseg, nsum, nelem;
   int ret, reverse;
   int q_ext, k_ext, v_ext;
@@ -90,7 +91,7 @@ struct ScanP {
   // bytes spanned by one (batch, head) slice of each tensor
   uint32_t q_rec, k_rec, v_rec, qe_rec, ke_rec, ve_rec, dec_rec, out_rec, oe_rec;
   const float* log_alpha;
-  float* seg;     // [BH][nseg][nelem]: S [DK][dvp], u [dvp], D [DK]
+  float* seg;     // [BH][nseg][nelem]: S [DK][dvp], u [dvp], D [DK] (every slice's columns)
   float* segdec;  // [BH][nseg]
 };
 
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   const int k_ext = GEN ? p.k_ext : TS_EXT_NONE;
   const int v_ext = GEN ? p.v_ext : TS_EXT_NONE;
   const bool kx = q_ext != TS_EXT_NONE && k_ext != TS_EXT_NONE;  // key-side rank-1 term
-  const bool vx = v_ext != TS_EXT_NONE;
+  const bool vx = v_ext != TS_EXT_NONE && blockIdx.z == 0;
   const int out_mode = GEN ? p.out_mode : TS_OUT_STORE;
   const bool has_oe = GEN && p.oe.ptr != nullptr;
 
@@ -274,33 +275,38 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
-  const int dvp = p.dvp;
-  const int nvb = dvp >> 4;
+  // value slice of this workgroup: padded columns col0 .. col0 + vs, of which
+  // dvz are real.  Slices of one (segment, b, h) share the q / k tiles through
+  // L2; the value-side ext column belongs to slice 0.
+  const int col0 = blockIdx.z * p.vs;
+  const int vs = p.vs;
+  const int dvz = min(p.vs, p.dv - col0);
+  const int nvb = vs >> 4;
   const int sgn = p.reverse ? -1 : 1;
   const int wave_first = __builtin_amdgcn_readfirstlane(tid & ~63);
 
   // ---- LDS carve-up
-  const ScanLayout L = scan_layout(ES, DK, dvp, MAIN);
+  const ScanLayout L = scan_layout(ES, DK, vs, MAIN);
   extern __shared__ __align__(16) unsigned char smem[];
   E* ebase = (E*)smem;
   E* st_base = ebase + STAGES * L.stage;
   float* fb = (float*)smem + L.fbase;
   float* s_ext = fb;                              // [stage][ke C | ve C]
-  float* s_u = s_ext + STAGES * 2 * C;            // [2][dvp]
-  float* s_d = s_u + 2 * dvp;                     // [2][DK]
+  float* s_u = s_ext + STAGES * 2 * C;            // [2][vs]
+  float* s_d = s_u + 2 * vs;                      // [2][DK]
   float* s_pw = s_d + 2 * DK;                     // alpha^d, d = 0..64 (static)
   float* my_lloc = s_pw + 68 + w * C;             // per-wave tile log-decay (stream)
 
   // ---- per-(b, h) addressing
   const int64_t bh_q = (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
   const int64_t bh_k = (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
-  const int64_t bh_v = (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
+  const int64_t bh_v = (int64_t)b * p.v.sb + (int64_t)h * p.v.sh + col0;
   const int q_st_b = (int)p.q.st * ES;
   const int k_st_b = (int)p.k.st * ES;
   const int v_st_b = (int)p.v.st * ES;
   const int dec_st_b = (int)p.decay.st * 4;
   auto k_rsrc = [&]() { return make_rsrc((const E*)p.k.ptr + bh_k, p.k_rec); };
-  auto v_rsrc = [&]() { return make_rsrc((const E*)p.v.ptr + bh_v, p.v_rec); };
+  auto v_rsrc = [&]() { return make_rsrc((const E*)p.v.ptr + bh_v, p.v_rec - (uint32_t)(col0 * ES)); };
   auto q_rsrc = [&]() { return make_rsrc((const E*)p.q.ptr + bh_q, p.q_rec); };
 
   // a(s), the decay applied when stepping into logical position s: a reversed
@@ -352,7 +358,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
           IO::st4(st + (vb * 16 + l16) * L.kp + kb * 16 + 4 * g, S[r][kb][0], S[r][kb][1], S[r][kb][2], S[r][kb][3]);
-        if (kx && g == 0) s_u[bi * dvp + vb * 16 + l16] = us[r][0];
+        if (kx && g == 0) s_u[bi * vs + vb * 16 + l16] = us[r][0];
       }
     }
     if (vx && g == 0) {
@@ -374,8 +380,8 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) S[r][kb][i] = src[(kb * 16 + 4 * g + i) * dvp + vb * 16 + l16];
-        const float u = src[DK * dvp + vb * 16 + l16];
+          for (int i = 0; i < 4; ++i) S[r][kb][i] = src[(kb * 16 + 4 * g + i) * p.dvp + col0 + vb * 16 + l16];
+        const float u = src[DK * p.dvp + col0 + vb * 16 + l16];
         us[r] = floatx4{u, u, u, u};
       }
     }
@@ -383,7 +389,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
     for (int r = 0; r < NKO; ++r) {
       const int kb = w + 4 * r;
       if (kb < NKB) {
-        const float d = src[DK * dvp + dvp + kb * 16 + l16];
+        const float d = src[DK * p.dvp + p.dvp + kb * 16 + l16];
         dst_[r] = floatx4{d, d, d, d};
       }
     }
@@ -391,11 +397,11 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 
   // ---- tile loading
   const int nk_vec = C * (DK / VEC);
-  const int nv_vec = C * (dvp / VEC);
+  const int nv_vec = C * (vs / VEC);
   TileLoader<E, SLOTS_K> ldk;
   TileLoader<E, SLOTS_V> ldv;
   ldk.setup(p, DK / VEC, p.dk, L.kp, k_st_b, tid);
-  ldv.setup(p, dvp / VEC, p.dv, L.vp, v_st_b, tid);
+  ldv.setup(p, vs / VEC, dvz, L.vp, v_st_b, tid);
   float ext_r = 0.0f;  // this thread's ke (wave 0) / ve (wave 1) of the fetched tile
   auto fetch = [&](int t0) {
     ldk.fetch(k_rsrc(), t0, sgn, k_st_b, wave_first, nk_vec);
@@ -433,7 +439,8 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 
   // ---- output addressing
   const int osz = out_mode == TS_OUT_STORE ? ES : 4;
-  const void* out_base = bh_base(p.out, b, h, osz);
+  const void* out_base = (const char*)bh_base(p.out, b, h, osz) + col0 * osz;
+  const uint32_t out_rec = p.out_rec - (uint32_t)(col0 * osz);
   const int out_st_b = (int)p.out.st * osz;
   const int oe_st_b = (int)p.oe.st * 4;
 
@@ -526,12 +533,12 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
       const F8 p0 = IO::from_acc(sc[0], sc[1]);
       const F8 p1 = IO::from_acc(sc[2], sc[3]);
       const E* st = st_base + (c & (L.nst - 1)) * L.st;
-      const float* u_in = s_u + (c & (L.nst - 1)) * dvp;
+      const float* u_in = s_u + (c & (L.nst - 1)) * vs;
       const float* d_in = s_d + (c & (L.nst - 1)) * DK;
 
       // ---- outputs O^T[v][query] = cw (S^T Q^T)[v] + (V^T P^T)[v], every value block
       const uint32_t ro = row_off(p, t0, query, out_st_b);
-      const rsrc_t out_rs = make_rsrc(out_base, p.out_rec);
+      const rsrc_t out_rs = make_rsrc(out_base, out_rec);
 #pragma unroll
       for (int vb = 0; vb < 4 * NVW; ++vb) {
         if (vb >= nvb) break;
@@ -555,7 +562,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
         if (w >= 2) acc = mma32(TK::col8(Vs, L.vp, vb * 16, 1, lane), p1, acc);
 
         const int ocol = vb * 16 + 4 * g;
-        const uint32_t ooff = ocol < p.dv ? ro + (uint32_t)(ocol * osz) : kOOB;
+        const uint32_t ooff = ocol < dvz ? ro + (uint32_t)(ocol * osz) : kOOB;
         if (out_mode == TS_OUT_STORE) {
           if constexpr (ES == 2) {
             bf16x4 o;
@@ -688,18 +695,18 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * dvp + vb * 16 + l16] = S[r][kb][i];
-        if (g == 0) dst[DK * dvp + vb * 16 + l16] = us[r][0];
+          for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * p.dvp + col0 + vb * 16 + l16] = S[r][kb][i];
+        if (g == 0) dst[DK * p.dvp + col0 + vb * 16 + l16] = us[r][0];
       }
     }
-    if (g == 0) {
+    if (g == 0 && blockIdx.z == 0) {
 #pragma unroll
       for (int r = 0; r < NKO; ++r) {
         const int kb = w + 4 * r;
-        if (kb < NKB) dst[DK * dvp + dvp + kb * 16 + l16] = dst_[r][0];
+        if (kb < NKB) dst[DK * p.dvp + p.dvp + kb * 16 + l16] = dst_[r][0];
       }
     }
-    if (tid == 0) p.segdec[(size_t)bh * p.nseg + seg] = seg_log;
+    if (tid == 0 && blockIdx.z == 0) p.segdec[(size_t)bh * p.nseg + seg] = seg_log;
   }
 }
 
@@ -781,7 +788,7 @@ int pick_dkp(int need) {
 }
 
 struct Layout {
-  int dkp, dvp, nvw, nchunks, seg_chunks, nseg, nsum, nelem;
+  int dkp, dvp, vs, nvs, nvw, nchunks, seg_chunks, nseg, nsum, nelem;
   bool kx, vx;
   size_t ws_bytes;
 };
@@ -807,14 +814,30 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   if (L->dkp < 0) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: key width %d exceeds 128", d->dk);
   L->dvp = (d->dv + 15) / 16 * 16;
   if (L->dvp > 128) return fail(TS_ERR_NOT_IMPLEMENTED, "scan: value width %d exceeds 128", d->dv);
-  L->nvw = L->dvp <= 64 ? 1 : 2;
   L->nchunks = (d->T + ts::C - 1) / ts::C;
   const int bh = d->B * d->H;
+  // Value slices: each workgroup carries the state of `vs` value columns, so
+  // B*H*nvs scans run side by side (the slices of one (b, h) re-read its q / k
+  // tiles from L2).  Auto: one slice of the whole width -- at the benchmark
+  // shape time segments beat slices (46 us against 49 us for two slices and
+  // 68 us for four; a slice's 64-token steps are bound by the in-CU
+  // dependency chain, not by memory).
+  if (d->value_split > 0) {
+    const int v = d->value_split;
+    if ((v != 16 && v != 32 && v != 64 && v != 128) || L->dvp % v)
+      return fail(TS_ERR_VALUE, "scan: value_split %d must be 16, 32, 64 or 128 and divide %d", v, L->dvp);
+    L->vs = v;
+  } else {
+    L->vs = L->dvp;
+  }
+  L->nvs = L->dvp / L->vs;
+  L->nvw = L->vs <= 64 ? 1 : 2;
   if (d->seg_chunks > 0) {
     L->seg_chunks = d->seg_chunks;
   } else {
-    // Two resident workgroups per CU on 256 CUs.
-    int want = 512 / (bh > 0 ? bh : 1);
+    // Segments of the time axis up to about two workgroups per CU (256 CUs).
+    const int lanes = bh * L->nvs;
+    int want = 512 / (lanes > 0 ? lanes : 1);
     if (want < 1) want = 1;
     L->seg_chunks = (L->nchunks + want - 1) / want;
     if (L->seg_chunks < 1) L->seg_chunks = 1;
@@ -949,7 +972,7 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
 
   ts::ScanP p;
   memset(&p, 0, sizeof(p));
-  p.B = d->B; p.H = d->H; p.T = d->T; p.dk = d->dk; p.dv = d->dv; p.dvp = L.dvp;
+  p.B = d->B; p.H = d->H; p.T = d->T; p.dk = d->dk; p.dv = d->dv; p.dvp = L.dvp; p.vs = L.vs;
   p.nchunks = L.nchunks; p.seg_chunks = L.seg_chunks; p.nseg = L.nseg; p.nsum = L.nsum; p.nelem = L.nelem;
   p.ret = d->retention; p.reverse = d->reverse;
   p.q_ext = L.kx ? d->q_ext : TS_EXT_NONE;
@@ -980,14 +1003,14 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
                        io->out_ext.ptr != nullptr;
   KernelFn fsum = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, false, general);
   KernelFn fmain = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, true, general);
-  const size_t lds_sum = (size_t)ts::scan_layout(esize, L.dkp, L.dvp, false).bytes;
-  const size_t lds_main = (size_t)ts::scan_layout(esize, L.dkp, L.dvp, true).bytes;
+  const size_t lds_sum = (size_t)ts::scan_layout(esize, L.dkp, L.vs, false).bytes;
+  const size_t lds_main = (size_t)ts::scan_layout(esize, L.dkp, L.vs, true).bytes;
   if (lds_main > 160 * 1024)
-    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: tile of %lld bytes exceeds LDS (dk_pad=%d dv_pad=%d)",
-                (long long)lds_main, L.dkp, L.dvp);
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: tile of %lld bytes exceeds LDS (dk_pad=%d slice=%d)",
+                (long long)lds_main, L.dkp, L.vs);
 
   if (L.nsum > 0) {
-    if ((rc = launch(fsum, dim3(L.nsum, bh), lds_sum, stream, p))) return rc;
+    if ((rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p))) return rc;
     ts::FinalP F{d->want_final ? io->final_state : nullptr, L.dkp, L.dvp, d->dk, d->dv, L.kx ? 1 : 0,
                  L.vx ? 1 : 0};
     hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
@@ -995,7 +1018,7 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: prefix launch failed: %s", hipGetErrorString(e));
   }
-  return launch(fmain, dim3(L.nseg, bh), lds_main, stream, p);
+  return launch(fmain, dim3(L.nseg, bh, L.nvs), lds_main, stream, p);
 }
 
 }  // extern "C"

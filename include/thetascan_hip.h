@@ -230,6 +230,57 @@ typedef struct ts_read_bwd_io {
 
 int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t stream);
 
+/* -------------------------------------------------------- GN write payloads */
+
+/* Damped Gauss-Newton write of a one-hidden-layer ReLU^2 fast network
+ * (engine.py:117-158 _block_forward, 180-195 _g_from_lambda, 215-255
+ * _lambda_solve and the write streams of 260-340), per token x (key) and v:
+ *   a = W1 x;  pre = a rsqrt(mean a^2 + eps) - tau;  h = relu(pre)^2
+ *   r = v - x - s W2 h
+ *   lam = r / ((|h|^2 + |x|^2 (W2 o W2)(2 relu(pre) rinv)^2) * inv_depth + eps)
+ *   g = s 2 relu(pre) (W2^T lam) rinv
+ * Outputs h [.,m] (LA2 keys), s*lam [.,d] (LA2 values), g [.,m] (LA1 values).
+ * Depth-1 memories (s = inv_depth = 1) with relu2 or relu2_threshold. */
+typedef struct ts_gn_desc {
+  int32_t B, H, T;
+  int32_t d;            /* head width: 16, 32, 64 or 128                        */
+  int32_t m;            /* hidden width: a multiple of 16 up to 128, or 256     */
+  int32_t dtype;        /* ts_dtype of every stream and weight                  */
+  int32_t has_tau;      /* relu2_threshold: subtract tau [H, m]                 */
+  float s;              /* 1/sqrt(depth)                                        */
+  float inv_depth;      /* 1/depth: the Jacobi diagonal averages the levels     */
+  float eps;            /* 1e-6 in the reference (also the damping)             */
+} ts_gn_desc;
+
+typedef struct ts_gn_io {
+  ts_strided x, v;      /* [B,H,T,d] keys (as written) and values               */
+  const void* w1;       /* [H,m,d]                                              */
+  const void* w2;       /* [H,d,m]                                              */
+  const void* w2t;      /* [H,m,d] transposed copy of w2                        */
+  const float* tau;     /* [H,m] or NULL                                        */
+  ts_strided h, lam, g; /* out: h [.,m], s*lam [.,d], g [.,m]                   */
+} ts_gn_io;
+
+int ts_gn_write_fwd(const ts_gn_desc* desc, const ts_gn_io* io, hipStream_t stream);
+
+typedef struct ts_gn_bwd_io {
+  ts_strided x, v;
+  const void* w1, *w2;
+  const void* w1t;      /* [H,d,m] transposed copy of w1                        */
+  const void* w2t;
+  const float* tau;
+  ts_strided dh, dlam, dg; /* gradients of the three outputs (NULL = zero)     */
+  ts_strided dx_in;     /* added into dx (NULL = zero)                          */
+  ts_strided dx, dv;    /* out [B,H,T,d]                                        */
+  void* tiles_m;        /* out [H, 4 (+1 with tau), B*T, m]: dz, h, da, s2 (, dpre) */
+  void* tiles_d;        /* out [H, 4, B*T, d]: lam, du, x, drq                  */
+} ts_gn_bwd_io;
+
+/* Backward of ts_gn_write_fwd: dx, dv, and the token tiles whose contractions
+ * give the weight gradients: dW1 = da^T x, dW2 = lam^T dz + du^T h
+ * + 2 W2 o (drq^T s2), dtau = -sum_tokens dpre. */
+int ts_gn_write_bwd(const ts_gn_desc* desc, const ts_gn_bwd_io* io, hipStream_t stream);
+
 /* ------------------------------------------------------ B-spline features */
 
 /* Projected open-uniform B-spline feature map

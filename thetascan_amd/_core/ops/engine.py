@@ -4,8 +4,9 @@ Host-side mirror of src/thetascan/_core/ops/engine.py:117-553 for every
 configuration the public API accepts (both families, any depth, one or two
 Jacobian steps, all read normalizations, value anchors).  Every scan goes
 through ``interface.scan_views`` / ``scan_views_mass`` (the HIP chunked scan),
-and key masses through the HIP decayed prefix sum.  The depth-1 kernel-memory
-hot path bypasses this module entirely (see ``fused.kernel_memory``).
+and key masses through the HIP decayed prefix sum.  Depth-1 ReLU^2 GN writes
+run in the HIP GN kernel (``gn.write``); the depth-1 kernel-memory hot path
+bypasses this module entirely (see ``fused.kernel_memory``).
 """
 from __future__ import annotations
 
@@ -15,7 +16,7 @@ from dataclasses import dataclass, field
 import torch
 import torch.nn.functional as F
 
-from . import interface, kernel_features
+from . import gn, interface, kernel_features
 from ..modules.norms import rmsnorm
 
 
@@ -167,8 +168,20 @@ def _lambda_solve(weights, cfg, ctxs, r):
 
 
 def write_streams(weights, cfg, k, v, hrot=None, softmax_gain=None, kernel_controls=None):
-    """Per-token write streams (engine.py:260-340) -> (Streams, ctxs, o)."""
+    """Per-token write streams (engine.py:260-340) -> (Streams, ctxs, o).
+
+    Depth-1 ReLU^2 GN memories run the whole write in the HIP GN kernel
+    (``gn.write``); ``ctxs`` and ``o`` are then ``None`` (no caller reads them).
+    """
     s = 1.0 / math.sqrt(cfg.depth)
+    if gn.eligible(cfg, weights, k, v):
+        W1, W2, Wg = weights[0]
+        tau = Wg[..., 0] if cfg.learn_thresh else None
+        h, lam_hat, g = gn.write(k, v, W1, W2, tau, s=s, inv_depth=1.0 / cfg.depth, eps=cfg.eps)
+        streams = Streams()
+        streams.la1.append((k, g) if cfg.fast_w1 else None)
+        streams.la2.append((hrot_stream(h, hrot), lam_hat))
+        return streams, None, None
     m = weights[0][1].shape[-1]
     o, ctxs = _forward_theta0(weights, cfg, k, softmax_gain=softmax_gain, kernel_controls=kernel_controls)
     hks = [hrot_stream(c.h, hrot) for c in ctxs] if hrot is not None else None

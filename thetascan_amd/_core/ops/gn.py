@@ -1,0 +1,128 @@
+"""GN-family write payloads on the GPU (ts_gn_write_fwd / ts_gn_write_bwd).
+
+Replaces, for depth-1 ReLU^2 (and ReLU^2-threshold) GN memories with one
+Jacobian step, the torch chain of src/thetascan/_core/ops/engine.py:117-158
+(_block_forward), 180-195 (_g_from_lambda), 215-255 (_lambda_solve) and the
+stream assembly of 260-340: one kernel produces the LA2 keys h, the LA2
+values s*lam and the LA1 values g per token.  The backward kernel recomputes
+the forward, writes dx and dv, and leaves head-major token tiles that batched
+GEMMs contract into dW1, dW2 and dtau.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ... import _lib
+
+GN_HEAD_DIMS = (16, 32, 64, 128)
+
+
+def supported_width(m: int) -> bool:
+    return m == 256 or (16 <= m <= 128 and m % 16 == 0)
+
+
+def eligible(cfg, weights, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether the HIP GN write covers this configuration and these streams."""
+    if cfg.write_rule != "gn" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.nonlin != "relu2":
+        return False
+    if cfg.value_centers:
+        return False
+    if not (k.is_cuda and v.is_cuda) or k.dtype not in (torch.bfloat16, torch.float32) or v.dtype != k.dtype:
+        return False
+    W1, W2, _ = weights[0]
+    d, m = k.shape[-1], W1.shape[-2]
+    return d in GN_HEAD_DIMS and supported_width(m) and v.shape[-1] == d and W2.shape[-1] == m
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """A [B,H,T,w] view whose rows the kernel can read: contiguous last axis,
+    16-byte aligned rows (else a contiguous copy)."""
+    vec = 16 // t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % vec == 0 for s in t.stride()[:3])
+    return t if ok else t.contiguous()
+
+
+def _desc(x, m, has_tau, s, inv_depth, eps):
+    B, H, T, d = x.shape
+    return _lib.GnDesc(B, H, T, d, m, _lib.dtype_code(x.dtype), int(has_tau), float(s), float(inv_depth),
+                       float(eps))
+
+
+class _GnWrite(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, v, w1, w2, tau, s, inv_depth, eps):
+        lib = _lib.load()
+        xk, vk = _rows(x), _rows(v)
+        B, H, T, d = xk.shape
+        m = w1.shape[1]
+        dt = x.dtype
+        w1c = w1.detach().to(dt).contiguous()
+        w2c = w2.detach().to(dt).contiguous()
+        w2t = w2c.transpose(1, 2).contiguous()
+        tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
+        h = torch.empty(B, H, T, m, dtype=dt, device=x.device)
+        lam = torch.empty(B, H, T, d, dtype=dt, device=x.device)
+        g = torch.empty(B, H, T, m, dtype=dt, device=x.device)
+        desc = _desc(xk, m, tc is not None, s, inv_depth, eps)
+        io = _lib.GnIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w2t.data_ptr(),
+                       _lib.ptr(tc), _lib.strided(h), _lib.strided(lam), _lib.strided(g))
+        with _lib.timed("ts_gn_write_fwd", lambda: _lib.nbytes(xk, vk, h, lam, g)):
+            status = lib.ts_gn_write_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
+        _lib.check(status, "ts_gn_write_fwd")
+        ctx.save_for_backward(xk, vk, w1c, w2c, w2t, tc)
+        ctx.meta = (s, inv_depth, eps, tau is not None, w1.dtype, w2.dtype, None if tau is None else tau.dtype)
+        return h, lam, g
+
+    @staticmethod
+    def backward(ctx, dh, dlam, dg):
+        xk, vk, w1c, w2c, w2t, tc = ctx.saved_tensors
+        s, inv_depth, eps, has_tau, w1_dtype, w2_dtype, tau_dtype = ctx.meta
+        lib = _lib.load()
+        B, H, T, d = xk.shape
+        m = w1c.shape[1]
+        dt = xk.dtype
+        N = B * T
+
+        def grad(t):
+            return None if t is None else _rows(t.to(dt))
+
+        dh, dlam, dg = grad(dh), grad(dlam), grad(dg)
+        w1t = w1c.transpose(1, 2).contiguous()
+        dx = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
+        dv = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
+        nsm = 5 if has_tau else 4
+        tm = torch.empty(H, nsm, N, m, dtype=dt, device=xk.device)
+        td = torch.empty(H, 4, N, d, dtype=dt, device=xk.device)
+        desc = _desc(xk, m, has_tau, s, inv_depth, eps)
+        io = _lib.GnBwdIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w1t.data_ptr(),
+                          w2t.data_ptr(), _lib.ptr(tc), _lib.strided(dh), _lib.strided(dlam), _lib.strided(dg),
+                          _lib.strided(None), _lib.strided(dx), _lib.strided(dv), tm.data_ptr(), td.data_ptr())
+        with _lib.timed("ts_gn_write_bwd", lambda: _lib.nbytes(xk, vk, dh, dlam, dg, dx, dv, tm, td)):
+            status = lib.ts_gn_write_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(xk.device))
+        _lib.check(status, "ts_gn_write_bwd")
+        # dW1 = da^T x;  dW2 = lam^T dz + du^T h + 2 W2 o (drq^T s2);  dtau = -sum dpre
+        dw1 = torch.bmm(tm[:, 2].transpose(1, 2), td[:, 2])
+        dw2 = torch.bmm(td[:, 0:2].reshape(H, 2 * N, d).transpose(1, 2), tm[:, 0:2].reshape(H, 2 * N, m))
+        dw2 = dw2 + 2.0 * w2c * torch.bmm(td[:, 3].transpose(1, 2), tm[:, 3])
+        dtau = None
+        if has_tau and ctx.needs_input_grad[4]:
+            dtau = (-tm[:, 4].to(torch.float32).sum(1)).to(tau_dtype)
+        return dx, dv, dw1.to(w1_dtype), dw2.to(w2_dtype), dtau, None, None, None
+
+
+def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps: float = 1e-6):
+    """GN write payloads ``(h, s*lam, g)`` of keys ``x`` and values ``v``
+    ([B,H,T,d]) for per-head weights ``w1`` [H,m,d], ``w2`` [H,d,m] (a leading
+    1 broadcasts over heads) and an optional threshold ``tau`` [H,m]."""
+    if not (x.is_cuda and v.is_cuda):
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    H = x.shape[1]
+    if w1.shape[0] != H:
+        w1 = w1.expand(H, -1, -1)
+    if w2.shape[0] != H:
+        w2 = w2.expand(H, -1, -1)
+    if tau is not None and tau.shape != (H, w1.shape[1]):
+        tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
+    return _GnWrite.apply(x, v, w1, w2, tau, s, inv_depth, eps)

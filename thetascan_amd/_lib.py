@@ -196,6 +196,55 @@ class BsplineDesc(ctypes.Structure):
     ]
 
 
+class GnDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("m", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("has_tau", ctypes.c_int32),
+        ("s", ctypes.c_float),
+        ("inv_depth", ctypes.c_float),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class GnIO(ctypes.Structure):
+    _fields_ = [
+        ("x", Strided),
+        ("v", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("w2t", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("h", Strided),
+        ("lam", Strided),
+        ("g", Strided),
+    ]
+
+
+class GnBwdIO(ctypes.Structure):
+    _fields_ = [
+        ("x", Strided),
+        ("v", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("w1t", ctypes.c_void_p),
+        ("w2t", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("dh", Strided),
+        ("dlam", Strided),
+        ("dg", Strided),
+        ("dx_in", Strided),
+        ("dx", Strided),
+        ("dv", Strided),
+        ("tiles_m", ctypes.c_void_p),
+        ("tiles_d", ctypes.c_void_p),
+    ]
+
+
 class BlendDesc(ctypes.Structure):
     _fields_ = [
         ("B", ctypes.c_int32),
@@ -269,6 +318,8 @@ def load() -> ctypes.CDLL:
         lib.ts_blend_parts.argtypes = [P(BlendDesc), P(ctypes.c_int32)]
         lib.ts_blend_bwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, P(Strided),
                                      ctypes.c_void_p, ctypes.c_void_p]
+        lib.ts_gn_write_fwd.argtypes = [P(GnDesc), P(GnIO), ctypes.c_void_p]
+        lib.ts_gn_write_bwd.argtypes = [P(GnDesc), P(GnBwdIO), ctypes.c_void_p]
         if lib.ts_abi_version() != 2:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib

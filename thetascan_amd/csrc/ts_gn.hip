@@ -1,0 +1,592 @@
+// GN-family write payloads for gfx950: the damped Gauss-Newton fast-weight
+// update of a one-hidden-layer ReLU^2 memory (forward and backward).
+//
+// Per token x (key, [d]) and v (value, [d]), with per-head W1 [m, d],
+// W2 [d, m] and an optional per-feature threshold tau [m]
+// (engine.py:117-158, 180-195, 215-255; depth L, s = 1/sqrt(L)):
+//
+//   a = W1 x,   rinv = (mean(a^2) + eps)^-1/2,   pre = a rinv - tau
+//   h = relu(pre)^2,   sp = 2 relu(pre)                (relu2 and its slope)
+//   u = W2 h,   r = v - (x + s u)                       (residual of theta0)
+//   den = (|h|^2 + |x|^2 (W2 o W2)(sp rinv)^2) / L + eps   (Jacobi diagonal)
+//   lam = r / den,   g = s sp (W2^T lam) rinv
+//
+// Outputs: h (the LA2 keys), s lam (LA2 values) and g (LA1 values).  The
+// backward recomputes the forward from x and v, writes dx and dv, and emits
+// head-major weight-gradient tiles ([H, slot, B*T, w]) that batched GEMMs
+// contract over tokens: dW1 = da^T x, dW2 = lam^T dz + du^T h + 2 W2 o
+// (drq^T s2), dtau = -sum dpre.
+//
+// Layout and MFMA usage follow the feature kernels (ts_tokens.h): lane =
+// token, the contraction over d or m runs on 16x16x32 MFMAs whose operands
+// are LDS weight rows and accumulator fragments of the previous product.
+
+#include "ts_common.h"
+#include "ts_tokens.h"
+#include "thetascan_hip.h"
+
+#include <string.h>
+
+namespace ts {
+
+struct GnP {
+  int B, H, T, groups, has_tau;
+  float s, inv_L, eps, inv_m;
+  Str x, v, h, lam, g;             // forward inputs / outputs
+  Str dh, dlam, dg, dxin, dx, dv;  // backward
+  const void* w1;                  // [H, m, d]
+  const void* w2;                  // [H, d, m]
+  const void* w1t;                 // [H, d, m]
+  const void* w2t;                 // [H, m, d]
+  const float* tau;                // [H, m]
+  void* tm;                        // [H, 4 (+1), B*T, m]: dz, h, da, s2 (, dpre with tau)
+  void* td;                        // [H, 4, B*T, d]: lam, du, x, drq
+};
+
+// LDS carve-up (elements of E): x tile, then the weights when they fit.
+struct GnLayout {
+  int xp, mp;
+  int xs, w1, w2, w1t, w2t;
+  int end;
+};
+__host__ __device__ constexpr GnLayout gn_layout(int esize, int d, int m, bool fwd, bool w_lds) {
+  const int vec = 16 / esize;
+  GnLayout L{};
+  L.xp = d + vec;
+  L.mp = m + vec;
+  int off = 0;
+  L.xs = off; off += TT * L.xp;
+  L.w1 = L.w2 = L.w1t = L.w2t = -1;
+  if (w_lds) {
+    L.w1 = off; off += m * L.xp;
+    L.w2 = off; off += d * L.mp;
+    L.w2t = off; off += m * L.xp;
+    if (!fwd) { L.w1t = off; off += d * L.mp; }
+  }
+  L.end = off;
+  return L;
+}
+constexpr int kGnLdsMax = 160 * 1024;
+template <typename E, int D, int MB, bool FWD>
+constexpr bool gn_weights_in_lds() {
+  return gn_layout((int)sizeof(E), D, MB * 16, FWD, true).end * (int)sizeof(E) <= kGnLdsMax;
+}
+
+// Four consecutive elements of row t (zero past T).
+template <typename E>
+__device__ __forceinline__ void ld4_row(const Str& s, int b, int h, int t, int c, bool valid, float* o) {
+  if (valid && s.ptr) {
+    ld4f<E>(rows_of<E>(s, b, h).at(t) + c, o);
+  } else {
+    o[0] = o[1] = o[2] = o[3] = 0.f;
+  }
+}
+template <typename E>
+__device__ __forceinline__ void st4_row(const Str& s, int b, int h, int t, int c, bool valid, const float* v) {
+  if (valid) st4f<E>(rows_of<E>(s, b, h).at(t) + c, v);
+}
+// Row n of a head-major tile [.., N, w].
+template <typename E>
+__device__ __forceinline__ void st4_tile(void* base, int64_t row, int w, int c, bool valid, const float* v) {
+  if (valid) st4f<E>((E*)base + row * w + c, v);
+}
+
+// out[db] = (Wt o Wt) reg: gemm_back with every weight squared on its way
+// into the MFMA (the reference squares W2 elementwise, engine.py:244).
+template <typename E, int D, int MB>
+__device__ __forceinline__ void gemm_back_sq(const E* wt, int wp, const floatx4* reg, int l16, int g, floatx4* out) {
+  typedef LdsIO<E> IO;
+  auto sq4 = [](typename Frag<E>::f4 v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float f = tof(v[i]);
+      v[i] = cvt<E>(f * f);
+    }
+    return v;
+  };
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    out[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const E* wrow = wt + (db * 16 + l16) * wp;
+#pragma unroll
+    for (int j = 0; j < MB / 2; ++j)
+      out[db] = mma32(IO::cat(sq4(IO::ld4(wrow + 32 * j + 4 * g)), sq4(IO::ld4(wrow + 32 * j + 16 + 4 * g))),
+                      IO::from_acc(reg[2 * j], reg[2 * j + 1]), out[db]);
+    if (MB & 1)
+      out[db] = mma16(sq4(IO::ld4(wrow + 16 * (MB - 1) + 4 * g)), IO::from_acc4(reg[MB - 1]), out[db]);
+  }
+}
+
+// The forward chain of one token (lane = token, four features per block).
+template <typename E, int D, int MB>
+struct GnToken {
+  float xr[D / 16][4];  // x (dims 16db+4g+i)
+  float vr[D / 16][4];  // v
+  floatx4 a[MB];        // W1 x
+  floatx4 rq[D / 16];   // (W2 o W2) (sp rinv)^2
+  floatx4 lam[D / 16];  // lambda
+  floatx4 den[D / 16];
+  float rinv, xx, hh;
+};
+
+template <typename E, int D, int MB>
+__device__ __forceinline__ void gn_forward_token(const GnP& p, int b, int h, int t, bool valid, int l16, int g,
+                                                 const E* xrow, const E* xs_w, int xp, const E* w1, int wp1,
+                                                 const E* w2, int wp2, const float* tau, GnToken<E, D, MB>& k,
+                                                 floatx4* hv, floatx4* s2v) {
+  float xx = 0.f;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    ld4f<E>(xrow + db * 16 + 4 * g, k.xr[db]);
+    ld4_row<E>(p.v, b, h, t, db * 16 + 4 * g, valid, k.vr[db]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xx += k.xr[db][i] * k.xr[db][i];
+  }
+  k.xx = sum_g(xx);
+  gemm_a<E, D, MB>(w1, wp1, xs_w, xp, l16, g, MB, k.a);
+  float ss = 0.f;
+#pragma unroll
+  for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += k.a[fb][i] * k.a[fb][i];
+  k.rinv = rsqrtf(sum_g(ss) * p.inv_m + p.eps);
+  float hh = 0.f;
+#pragma unroll
+  for (int fb = 0; fb < MB; ++fb) {
+    float tv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.has_tau) {
+      const floatx4 t4 = *(const floatx4*)(tau + fb * 16 + 4 * g);
+      tv[0] = t4[0]; tv[1] = t4[1]; tv[2] = t4[2]; tv[3] = t4[3];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float rp = fmaxf(k.a[fb][i] * k.rinv - tv[i], 0.f);
+      hv[fb][i] = rp * rp;
+      const float sv = 2.f * rp * k.rinv;
+      s2v[fb][i] = sv * sv;
+      hh += hv[fb][i] * hv[fb][i];
+    }
+  }
+  k.hh = sum_g(hh);
+  floatx4 u[D / 16];
+  gemm_back<E, D, MB>(w2, wp2, hv, l16, g, MB, u);
+  gemm_back_sq<E, D, MB>(w2, wp2, s2v, l16, g, k.rq);
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float r = k.vr[db][i] - k.xr[db][i] - p.s * u[db][i];
+      const float dn = (k.hh + k.xx * k.rq[db][i]) * p.inv_L + p.eps;
+      k.den[db][i] = dn;
+      k.lam[db][i] = r / dn;
+    }
+}
+
+template <typename E, int D, int MB>
+__global__ __launch_bounds__(256) void gn_write_fwd_kernel(GnP p) {
+  constexpr int M = MB * 16;
+  constexpr bool WL = gn_weights_in_lds<E, D, MB, true>();
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnLayout L = gn_layout((int)sizeof(E), D, M, true, WL);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  const E* w1 = (const E*)p.w1 + h * M * D;
+  const E* w2 = (const E*)p.w2 + h * D * M;
+  const E* w2t = (const E*)p.w2t + h * M * D;
+  int wp1 = D, wp2 = M;
+  if constexpr (WL) {
+    stage_matrix<E>(w1, M, D, base + L.w1, L.xp, tid);
+    stage_matrix<E>(w2, D, M, base + L.w2, L.mp, tid);
+    stage_matrix<E>(w2t, M, D, base + L.w2t, L.xp, tid);
+    w1 = base + L.w1;
+    w2 = base + L.w2;
+    w2t = base + L.w2t;
+    wp1 = L.xp;
+    wp2 = L.mp;
+  }
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  RowTile<E, D> ldx;
+  ldx.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();       // weights staged; previous group consumed
+    ldx.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldx.fetch(xsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    GnToken<E, D, MB> k;
+    floatx4 hv[MB], s2v[MB];
+    gn_forward_token<E, D, MB>(p, b, h, t, valid, l16, g, xs + row * L.xp, xs + w * 16 * L.xp, L.xp, w1, wp1, w2,
+                               wp2, tau, k, hv, s2v);
+    floatx4 z[MB];
+    gemm_back<E, M, D / 16>(w2t, wp1, k.lam, l16, g, D / 16, z);
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+      float hvv[4], gv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        hvv[i] = hv[fb][i];
+        const float sp = 2.f * sqrtf(hv[fb][i]);  // 2 relu(pre) = 2 sqrt(h)
+        gv[i] = p.s * sp * z[fb][i] * k.rinv;
+      }
+      st4_row<E>(p.h, b, h, t, fb * 16 + 4 * g, valid, hvv);
+      st4_row<E>(p.g, b, h, t, fb * 16 + 4 * g, valid, gv);
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float lv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lv[i] = p.s * k.lam[db][i];
+      st4_row<E>(p.lam, b, h, t, db * 16 + 4 * g, valid, lv);
+    }
+  }
+}
+
+template <typename E, int D, int MB>
+__global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
+  constexpr int M = MB * 16;
+  constexpr bool WL = gn_weights_in_lds<E, D, MB, false>();
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnLayout L = gn_layout((int)sizeof(E), D, M, false, WL);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  const E* w1 = (const E*)p.w1 + h * M * D;
+  const E* w2 = (const E*)p.w2 + h * D * M;
+  const E* w2t = (const E*)p.w2t + h * M * D;
+  const E* w1t = (const E*)p.w1t + h * D * M;
+  int wpd = D, wpm = M;  // pitches of [.][D] and [.][M] weight rows
+  if constexpr (WL) {
+    stage_matrix<E>(w1, M, D, base + L.w1, L.xp, tid);
+    stage_matrix<E>(w2, D, M, base + L.w2, L.mp, tid);
+    stage_matrix<E>(w2t, M, D, base + L.w2t, L.xp, tid);
+    stage_matrix<E>(w1t, D, M, base + L.w1t, L.mp, tid);
+    w1 = base + L.w1;
+    w2 = base + L.w2;
+    w2t = base + L.w2t;
+    w1t = base + L.w1t;
+    wpd = L.xp;
+    wpm = L.mp;
+  }
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const int64_t N = (int64_t)p.B * p.T;
+  const int nsm = p.has_tau ? 5 : 4;
+  E* tm = (E*)p.tm + (int64_t)h * nsm * N * M;  // dz, h, da, s2 (, dpre)
+  E* td = (E*)p.td + (int64_t)h * 4 * N * D;  // lam, du, x, drq
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  RowTile<E, D> ldx;
+  ldx.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();
+    ldx.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldx.fetch(xsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const int64_t n = (int64_t)b * p.T + t;
+    GnToken<E, D, MB> k;
+    floatx4 hv[MB], s2v[MB];
+    gn_forward_token<E, D, MB>(p, b, h, t, valid, l16, g, xs + row * L.xp, xs + w * 16 * L.xp, L.xp, w1, wpd, w2,
+                               wpm, tau, k, hv, s2v);
+    // tiles known after the forward: h, s2, lam, x
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+      float o[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
+      st4_tile<E>(tm + 1 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+      float o2[4] = {s2v[fb][0], s2v[fb][1], s2v[fb][2], s2v[fb][3]};
+      st4_tile<E>(tm + 3 * N * M, n, M, fb * 16 + 4 * g, valid, o2);
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float o[4] = {k.lam[db][0], k.lam[db][1], k.lam[db][2], k.lam[db][3]};
+      st4_tile<E>(td + 0 * N * D, n, D, db * 16 + 4 * g, valid, o);
+      st4_tile<E>(td + 2 * N * D, n, D, db * 16 + 4 * g, valid, k.xr[db]);
+    }
+    // ---- g = s sp z rinv, z = W2^T lam
+    floatx4 dz[MB], dsp[MB];
+    float drinv = 0.f;
+    {
+      floatx4 z[MB];
+      gemm_back<E, M, D / 16>(w2t, wpd, k.lam, l16, g, D / 16, z);
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb) {
+        float dgv[4];
+        ld4_row<E>(p.dg, b, h, t, fb * 16 + 4 * g, valid, dgv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sp = 2.f * sqrtf(hv[fb][i]);
+          const float sdg = p.s * dgv[i];
+          dz[fb][i] = sdg * sp * k.rinv;
+          dsp[fb][i] = sdg * z[fb][i] * k.rinv;
+          drinv += sdg * sp * z[fb][i];
+        }
+        float o[4] = {dz[fb][0], dz[fb][1], dz[fb][2], dz[fb][3]};
+        st4_tile<E>(tm + 0 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+      }
+    }
+    // ---- lam -> r, den -> (hh, xx, rq)
+    floatx4 dr[D / 16], drq[D / 16];
+    float dhh = 0.f, dxx = 0.f;
+    {
+      floatx4 wdz[D / 16];
+      gemm_back<E, D, MB>(w2, wpm, dz, l16, g, MB, wdz);
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float dlv[4];
+        ld4_row<E>(p.dlam, b, h, t, db * 16 + 4 * g, valid, dlv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dl = p.s * dlv[i] + wdz[db][i];
+          dr[db][i] = dl / k.den[db][i];
+          const float dD = -dl * k.lam[db][i] / k.den[db][i] * p.inv_L;
+          dhh += dD;
+          dxx += dD * k.rq[db][i];
+          drq[db][i] = dD;  // times xx below (after the group sum)
+        }
+      }
+      dhh = sum_g(dhh);
+      dxx = sum_g(dxx);
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) drq[db][i] *= k.xx;
+        float o[4] = {drq[db][0], drq[db][1], drq[db][2], drq[db][3]};
+        st4_tile<E>(td + 3 * N * D, n, D, db * 16 + 4 * g, valid, o);
+      }
+    }
+    // ---- rq = (W2 o W2) s2, s2 = (sp rinv)^2
+    {
+      floatx4 ds2[MB];
+      gemm_back_sq<E, M, D / 16>(w2t, wpd, drq, l16, g, ds2);
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sp = 2.f * sqrtf(hv[fb][i]);
+          const float dsv = 2.f * sp * k.rinv * ds2[fb][i];
+          dsp[fb][i] += dsv * k.rinv;
+          drinv += dsv * sp;
+        }
+    }
+    // ---- r = v - x - s W2 h
+    floatx4 du[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float dvv[4], duv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dvv[i] = dr[db][i];
+        du[db][i] = -p.s * dr[db][i];
+        duv[i] = du[db][i];
+      }
+      st4_row<E>(p.dv, b, h, t, db * 16 + 4 * g, valid, dvv);
+      st4_tile<E>(td + 1 * N * D, n, D, db * 16 + 4 * g, valid, duv);
+    }
+    floatx4 da[MB];
+    {
+      floatx4 dhu[MB];
+      gemm_back<E, M, D / 16>(w2t, wpd, du, l16, g, D / 16, dhu);
+      float ra = 0.f;
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb) {
+        float dhv[4];
+        ld4_row<E>(p.dh, b, h, t, fb * 16 + 4 * g, valid, dhv);
+        float tv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.has_tau) {
+          const floatx4 t4 = *(const floatx4*)(tau + fb * 16 + 4 * g);
+          tv[0] = t4[0]; tv[1] = t4[1]; tv[2] = t4[2]; tv[3] = t4[3];
+        }
+        float dpv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pre = k.a[fb][i] * k.rinv - tv[i];
+          const float rp = fmaxf(pre, 0.f);
+          const float dht = dhv[i] + dhu[fb][i] + 2.f * hv[fb][i] * dhh;
+          const float dpre = (valid && pre > 0.f) ? 2.f * rp * dht + 2.f * dsp[fb][i] : 0.f;
+          dpv[i] = dpre;
+          da[fb][i] = dpre;  // completed below once drinv is known
+          ra += dpre * k.a[fb][i];
+        }
+        if (p.has_tau) st4_tile<E>(tm + 4 * N * M, n, M, fb * 16 + 4 * g, valid, dpv);
+      }
+      drinv = sum_g(drinv + ra);
+    }
+    const float c3 = drinv * k.rinv * k.rinv * k.rinv * p.inv_m;
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) da[fb][i] = da[fb][i] * k.rinv - c3 * k.a[fb][i];
+      float o[4] = {da[fb][0], da[fb][1], da[fb][2], da[fb][3]};
+      st4_tile<E>(tm + 2 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+    }
+    floatx4 wda[D / 16];
+    gemm_back<E, D, MB>(w1t, wpm, da, l16, g, MB, wda);
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float dxi[4], o[4];
+      ld4_row<E>(p.dxin, b, h, t, db * 16 + 4 * g, valid, dxi);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = dxi[i] - dr[db][i] + 2.f * k.xr[db][i] * dxx + wda[db][i];
+      st4_row<E>(p.dx, b, h, t, db * 16 + 4 * g, valid, o);
+    }
+  }
+}
+
+}  // namespace ts
+
+namespace {
+
+using ts::fail;
+
+int check_gn(const ts_gn_desc* d) {
+  if (!d) return fail(TS_ERR_VALUE, "gn: null descriptor");
+  if (d->B < 1 || d->H < 1 || d->T < 0) return fail(TS_ERR_VALUE, "gn: bad shape");
+  if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "gn: unknown dtype");
+  if (d->d != 16 && d->d != 32 && d->d != 64 && d->d != 128)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "gn: head width %d (16, 32, 64 or 128)", d->d);
+  if (d->m < 16 || d->m % 16 || (d->m > 128 && d->m != 256))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "gn: hidden width %d (a multiple of 16 up to 128, or 256)", d->m);
+  if (d->H > 65535 || d->B > 65535) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: grid too large");
+  return TS_OK;
+}
+
+bool gn_stream_ok(const ts_strided& s, int vec) {
+  return s.ptr == nullptr || (((uintptr_t)s.ptr & 15u) == 0 && s.sb % vec == 0 && s.sh % vec == 0 && s.st % vec == 0 &&
+                              s.st <= 0x7fffffff);
+}
+
+ts::Str gn_str(const ts_strided& s) { return ts::Str{const_cast<void*>(s.ptr), s.sb, s.sh, (int)s.st}; }
+
+typedef void (*GnKernel)(ts::GnP);
+
+template <typename E, bool FWD, int D>
+GnKernel gn_pick_m(int m) {
+#define TS_GN(MB) \
+  return FWD ? (GnKernel)ts::gn_write_fwd_kernel<E, D, MB> : (GnKernel)ts::gn_write_bwd_kernel<E, D, MB>;
+  switch (m) {
+    case 16: TS_GN(1)
+    case 32: TS_GN(2)
+    case 48: TS_GN(3)
+    case 64: TS_GN(4)
+    case 80: TS_GN(5)
+    case 96: TS_GN(6)
+    case 112: TS_GN(7)
+    case 128: TS_GN(8)
+    case 256: TS_GN(16)
+  }
+#undef TS_GN
+  return nullptr;
+}
+
+template <typename E, bool FWD>
+GnKernel gn_pick(int d, int m) {
+  switch (d) {
+    case 16: return gn_pick_m<E, FWD, 16>(m);
+    case 32: return gn_pick_m<E, FWD, 32>(m);
+    case 64: return gn_pick_m<E, FWD, 64>(m);
+    case 128: return gn_pick_m<E, FWD, 128>(m);
+  }
+  return nullptr;
+}
+
+int gn_lds_bytes(const ts_gn_desc* d, bool fwd) {
+  const int es = d->dtype == TS_BF16 ? 2 : 4;
+  const ts::GnLayout full = ts::gn_layout(es, d->d, d->m, fwd, true);
+  const bool wl = full.end * es <= ts::kGnLdsMax;
+  return ts::gn_layout(es, d->d, d->m, fwd, wl).end * es;
+}
+
+// Groups of 64 tokens per workgroup: enough workgroups to fill 256 CUs.
+int gn_groups(const ts_gn_desc* d) {
+  const int ngroups = (d->T + ts::TT - 1) / ts::TT;
+  const int64_t slices = (int64_t)d->B * d->H;
+  int per = 1;
+  while (per < ngroups && slices * ((ngroups + 2 * per - 1) / (2 * per)) >= 512) per *= 2;
+  return per;
+}
+
+void gn_fill(const ts_gn_desc* d, ts::GnP& p) {
+  memset(&p, 0, sizeof(p));
+  p.B = d->B; p.H = d->H; p.T = d->T;
+  p.groups = gn_groups(d);
+  p.has_tau = d->has_tau;
+  p.s = d->s; p.inv_L = d->inv_depth; p.eps = d->eps;
+  p.inv_m = 1.0f / (float)d->m;
+}
+
+int gn_launch(const ts_gn_desc* d, const ts::GnP& p, bool fwd, hipStream_t stream) {
+  GnKernel k = d->dtype == TS_BF16 ? (fwd ? gn_pick<ts::bf16, true>(d->d, d->m) : gn_pick<ts::bf16, false>(d->d, d->m))
+                                   : (fwd ? gn_pick<float, true>(d->d, d->m) : gn_pick<float, false>(d->d, d->m));
+  if (!k) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: no kernel for d=%d m=%d", d->d, d->m);
+  const int lds = gn_lds_bytes(d, fwd);
+  if (lds > ts::kGnLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: tile of %d bytes exceeds LDS", lds);
+  if (lds > 65536) {
+    hipError_t e = ts::ensure_lds_limit((const void*)k, lds);
+    if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "gn: LDS request failed: %s", hipGetErrorString(e));
+  }
+  const int ngroups = (d->T + ts::TT - 1) / ts::TT;
+  const dim3 grid((unsigned)((ngroups + p.groups - 1) / p.groups), (unsigned)d->H, (unsigned)d->B);
+  hipLaunchKernelGGL(k, grid, dim3(256), lds, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "gn: launch failed: %s", hipGetErrorString(e));
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ts_gn_write_fwd(const ts_gn_desc* d, const ts_gn_io* io, hipStream_t stream) {
+  int rc = check_gn(d);
+  if (rc) return rc;
+  if (!io || !io->x.ptr || !io->v.ptr || !io->w1 || !io->w2 || !io->w2t || !io->h.ptr || !io->lam.ptr || !io->g.ptr)
+    return fail(TS_ERR_VALUE, "gn: missing tensors");
+  if (d->has_tau && !io->tau) return fail(TS_ERR_VALUE, "gn: missing tau");
+  const int vec = d->dtype == TS_BF16 ? 8 : 4;
+  for (const ts_strided* s : {&io->x, &io->v, &io->h, &io->lam, &io->g})
+    if (!gn_stream_ok(*s, vec)) return fail(TS_ERR_VALUE, "gn: streams need 16-byte aligned rows");
+  if (d->T == 0) return TS_OK;
+  ts::GnP p;
+  gn_fill(d, p);
+  p.x = gn_str(io->x); p.v = gn_str(io->v);
+  p.h = gn_str(io->h); p.lam = gn_str(io->lam); p.g = gn_str(io->g);
+  p.w1 = io->w1; p.w2 = io->w2; p.w2t = io->w2t; p.tau = io->tau;
+  return gn_launch(d, p, true, stream);
+}
+
+int ts_gn_write_bwd(const ts_gn_desc* d, const ts_gn_bwd_io* io, hipStream_t stream) {
+  int rc = check_gn(d);
+  if (rc) return rc;
+  if (!io || !io->x.ptr || !io->v.ptr || !io->w1 || !io->w2 || !io->w1t || !io->w2t || !io->dx.ptr || !io->dv.ptr ||
+      !io->tiles_m || !io->tiles_d)
+    return fail(TS_ERR_VALUE, "gn bwd: missing tensors");
+  if (d->has_tau && !io->tau) return fail(TS_ERR_VALUE, "gn bwd: missing tau");
+  const int vec = d->dtype == TS_BF16 ? 8 : 4;
+  for (const ts_strided* s : {&io->x, &io->v, &io->dh, &io->dlam, &io->dg, &io->dx_in, &io->dx, &io->dv})
+    if (!gn_stream_ok(*s, vec)) return fail(TS_ERR_VALUE, "gn bwd: streams need 16-byte aligned rows");
+  if (d->T == 0) return TS_OK;
+  ts::GnP p;
+  gn_fill(d, p);
+  p.x = gn_str(io->x); p.v = gn_str(io->v);
+  p.dh = gn_str(io->dh); p.dlam = gn_str(io->dlam); p.dg = gn_str(io->dg); p.dxin = gn_str(io->dx_in);
+  p.dx = gn_str(io->dx); p.dv = gn_str(io->dv);
+  p.w1 = io->w1; p.w2 = io->w2; p.w1t = io->w1t; p.w2t = io->w2t; p.tau = io->tau;
+  p.tm = io->tiles_m; p.td = io->tiles_d;
+  return gn_launch(d, p, false, stream);
+}
+
+}  // extern "C"

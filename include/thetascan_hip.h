@@ -281,6 +281,56 @@ typedef struct ts_gn_bwd_io {
  * + 2 W2 o (drq^T s2), dtau = -sum_tokens dpre. */
 int ts_gn_write_bwd(const ts_gn_desc* desc, const ts_gn_bwd_io* io, hipStream_t stream);
 
+/* One stage of the GN read (engine.py:467-506), per query q [.,d]:
+ *   a = W1 q + c,  c = 0 | num | num / (mass + eps)      (corr = 0 | 1 | 2)
+ *   h = relu(a rsqrt(mean a^2 + eps) - tau)^2            -> h [.,m]
+ *   resid = q + s W2 h                                   -> resid [.,d]
+ * Stage 1 of the two-stage normalized read is corr 0 without resid (the
+ * queries of the feature-mass scan, engine.py:475-480); stage 2 adds the
+ * normalized stage-1 read (corr 2, engine.py:481-487) and gives the queries of
+ * the memory scan and the residual of y = q + s (W2 h + mem).  corr 1 is the
+ * unnormalized LA1 correction of engine.py:488-500. */
+typedef struct ts_gn_read_desc {
+  int32_t B, H, T, d, m;
+  int32_t dtype;
+  int32_t has_tau;      /* subtract tau [H, m]                                  */
+  int32_t corr;         /* 0, 1 or 2 as above                                   */
+  int32_t want_resid;
+  float s;              /* 1/sqrt(depth)                                        */
+  float eps;
+} ts_gn_read_desc;
+
+typedef struct ts_gn_read_io {
+  ts_strided q;
+  const void* w1;       /* [H,m,d]                                              */
+  const void* w2;       /* [H,d,m] (want_resid)                                 */
+  const float* tau;     /* [H,m] or NULL                                        */
+  ts_strided num;       /* [B,H,T,m] (corr 1, 2)                                */
+  ts_strided mass;      /* fp32 [B,H,T] (corr 2)                                */
+  ts_strided h, resid;  /* out                                                  */
+} ts_gn_read_io;
+
+int ts_gn_read_fwd(const ts_gn_read_desc* desc, const ts_gn_read_io* io, hipStream_t stream);
+
+typedef struct ts_gn_read_bwd_io {
+  ts_strided q;
+  const void* w1;
+  const void* w1t;      /* [H,d,m] transposed copy of w1                        */
+  const void* w2t;      /* [H,m,d] transposed copy of w2 (want_resid)           */
+  const float* tau;
+  ts_strided num, mass;
+  ts_strided dh, dresid;   /* gradients of h and resid (NULL = zero)           */
+  ts_strided dq;        /* out [.,d]                                            */
+  ts_strided dnum;      /* out [.,m] (corr 1, 2)                                */
+  float* dmass;         /* out fp32, laid out like mass (corr 2)                */
+  void* tiles_m;        /* out [H, 2 (+1 with tau), B*T, m]: da, h (, dpre)     */
+  void* tiles_d;        /* out [H, 2, B*T, d]: q, s*dresid                      */
+} ts_gn_read_bwd_io;
+
+/* Backward of ts_gn_read_fwd: dq, dnum, dmass and the token tiles of
+ * dW1 = da^T q, dW2 = (s dresid)^T h, dtau = -sum_tokens dpre. */
+int ts_gn_read_bwd(const ts_gn_read_desc* desc, const ts_gn_read_bwd_io* io, hipStream_t stream);
+
 /* ------------------------------------------------------ B-spline features */
 
 /* Projected open-uniform B-spline feature map

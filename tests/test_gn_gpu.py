@@ -81,3 +81,92 @@ def test_gn_write_rejects_unsupported_widths(cuda):
     w2 = torch.zeros(1, 24, 32, device=cuda)
     with pytest.raises(NotImplementedError):
         gn.write(x, x, w1, w2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d,m,learn_thresh,T", [(16, 48, True, 70), (64, 128, False, 130), (32, 96, False, 64)])
+def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T):
+    """Stage without a correction: h and q + s W2 h are the oracle's
+    block_forward (engine.py:117-158) of the query, gradients included."""
+    from thetascan_amd._core.ops import gn
+
+    B, H = 2, 3
+    q, _, w1, w2, wg = _case(B, H, T, d, m, learn_thresh, 7 * d + m + T, dtype)
+    c = _cfg(learn_thresh)
+    rq, rw1, rw2 = (t.clone().requires_grad_(True) for t in (q, w1, w2))
+    rwg = wg.clone().requires_grad_(True) if learn_thresh else None
+    u, ctx = mixer.block_forward(rw1, rw2, rwg, c, rq, {})
+    h_ref, resid_ref = ctx["h"], rq + u
+    gen = torch.Generator().manual_seed(3)
+    dh = torch.randn(h_ref.shape, generator=gen, dtype=torch.float64)
+    dr = torch.randn(resid_ref.shape, generator=gen, dtype=torch.float64)
+    torch.autograd.backward([h_ref, resid_ref], [dh, dr])
+
+    dev = lambda t: t.to(cuda, dtype).requires_grad_(True)  # noqa: E731
+    q_, w1_, w2_ = dev(q), dev(w1), dev(w2)
+    tau_ = dev(wg[..., 0].contiguous()) if learn_thresh else None
+    h, resid = gn.read_stage(q_, w1_, w2_, tau_, want_resid=True)
+    torch.autograd.backward([h, resid], [dh.to(cuda, dtype), dr.to(cuda, dtype)])
+    tol = 2e-3 if dtype == torch.float32 else 3e-2
+    assert rel_err(h, h_ref) < tol and rel_err(resid, resid_ref) < tol
+    gtol = 5e-3 if dtype == torch.float32 else 6e-2
+    pairs = [("dq", q_.grad, rq.grad), ("dW1", w1_.grad, rw1.grad), ("dW2", w2_.grad, rw2.grad)]
+    if learn_thresh:
+        pairs.append(("dtau", tau_.grad, rwg.grad[..., 0]))
+    for name, a, e in pairs:
+        assert rel_err(a, e) < gtol, (name, rel_err(a, e))
+
+
+@pytest.mark.parametrize("corr", [1, 2])
+def test_gn_read_stage_correction_gradients(cuda, corr):
+    """Stage with the LA1 correction (plain, or divided by its mass): the HIP
+    backward agrees with fp64 autograd of rmsnorm(W1 q + c) composed from the
+    oracle's rmsnorm, for q, num, mass, W1, W2 and tau (fp32)."""
+    from thetascan_amd._core.ops import gn
+
+    B, H, T, d, m = 2, 2, 75, 32, 64
+    q, _, w1, w2, wg = _case(B, H, T, d, m, True, 11 + corr, torch.float32)
+    gen = torch.Generator().manual_seed(5)
+    num = torch.randn(B, H, T, m, generator=gen, dtype=torch.float64)
+    mass = torch.rand(B, H, T, generator=gen, dtype=torch.float64) + 0.5
+    leaves = [t.clone().requires_grad_(True) for t in (q, w1, w2, wg, num, mass)]
+    rq, rw1, rw2, rwg, rnum, rmass = leaves
+    cc = rnum / (rmass.unsqueeze(-1) + 1e-6) if corr == 2 else rnum
+    a = torch.einsum("hmd,bhtd->bhtm", rw1, rq) + cc
+    pre = mixer.rmsnorm(a)[0] - rwg[..., 0].unsqueeze(0).unsqueeze(2)
+    h_ref = torch.relu(pre) ** 2
+    resid_ref = rq + torch.einsum("hdm,bhtm->bhtd", rw2, h_ref)
+    dh = torch.randn(h_ref.shape, generator=gen, dtype=torch.float64)
+    dr = torch.randn(resid_ref.shape, generator=gen, dtype=torch.float64)
+    torch.autograd.backward([h_ref, resid_ref], [dh, dr])
+
+    dev = [t.to(cuda, torch.float32).requires_grad_(True) for t in (q, w1, w2, wg[..., 0].contiguous(), num, mass)]
+    q_, w1_, w2_, tau_, num_, mass_ = dev
+    h, resid = gn.read_stage(q_, w1_, w2_, tau_, num_, mass_ if corr == 2 else None, corr=corr, want_resid=True)
+    torch.autograd.backward([h, resid], [dh.to(cuda, torch.float32), dr.to(cuda, torch.float32)])
+    assert rel_err(h, h_ref) < 2e-3 and rel_err(resid, resid_ref) < 2e-3
+    pairs = [("dq", q_.grad, rq.grad), ("dW1", w1_.grad, rw1.grad), ("dW2", w2_.grad, rw2.grad),
+             ("dtau", tau_.grad, rwg.grad[..., 0]), ("dnum", num_.grad, rnum.grad)]
+    if corr == 2:
+        pairs.append(("dmass", mass_.grad, rmass.grad))
+    for name, a, e in pairs:
+        assert rel_err(a, e) < 5e-3, (name, rel_err(a, e))
+
+
+def test_normalized_read_matches_formula(cuda):
+    """The read epilogue y = resid + s num / (mass + eps) with its gradients."""
+    from thetascan_amd._core.ops import gn
+
+    g = torch.Generator().manual_seed(9)
+    num, resid = (torch.randn(2, 3, 40, 32, generator=g, dtype=torch.float64) for _ in range(2))
+    mass = torch.rand(2, 3, 40, generator=g, dtype=torch.float64) + 0.3
+    leaves = [t.clone().requires_grad_(True) for t in (num, mass, resid)]
+    y_ref = leaves[2] + 0.5 * leaves[0] / (leaves[1].unsqueeze(-1) + 1e-6)
+    dy = torch.randn(y_ref.shape, generator=g, dtype=torch.float64)
+    y_ref.backward(dy)
+    dev = [t.to(cuda, torch.float32).requires_grad_(True) for t in (num, mass, resid)]
+    y = gn.normalized_read(dev[0], dev[1], dev[2], s=0.5)
+    y.backward(dy.to(cuda, torch.float32))
+    assert rel_err(y, y_ref) < 1e-5
+    for a, e in zip(dev, leaves):
+        assert rel_err(a.grad, e.grad) < 1e-5

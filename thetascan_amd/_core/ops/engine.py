@@ -5,8 +5,9 @@ configuration the public API accepts (both families, any depth, one or two
 Jacobian steps, all read normalizations, value anchors).  Every scan goes
 through ``interface.scan_views`` / ``scan_views_mass`` (the HIP chunked scan),
 and key masses through the HIP decayed prefix sum.  Depth-1 ReLU^2 GN writes
-run in the HIP GN kernel (``gn.write``); the depth-1 kernel-memory hot path
-bypasses this module entirely (see ``fused.kernel_memory``).
+and reads run in the HIP GN kernels (``gn.write``, ``gn.read_stage``,
+``gn.normalized_read``); the depth-1 kernel-memory hot path bypasses this
+module entirely (see ``fused.kernel_memory``).
 """
 from __future__ import annotations
 
@@ -272,7 +273,39 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
             mems = [torch.einsum("hvd,bhtv->bhtd", Cve.to(mem.dtype), mem) for mem in mems]
         return mems
 
+    gn_read = gn.read_eligible(cfg, weights, q)
+
+    def gn_layer(group, l, x):
+        """Depth-1 ReLU^2 GN read on the HIP read stages (engine.py:467-544)."""
+        W1, W2, Wg = weights[l]
+        tau = Wg[..., 0] if cfg.learn_thresh else None
+        entry = streams.la1[l]
+        keys, vals = streams.la2[l]
+        if cfg.read_norm_w1:
+            if entry is None:
+                raise RuntimeError("read_norm_w1 requires an LA1 GN stream")
+            h0, _ = gn.read_stage(x, W1, tau=tau, eps=cfg.eps)
+            pairs = interface.scan_views_mass(group, hrot_stream(h0, hrot).to(keys.dtype), keys, entry[1], "m")
+            stage = [(num, mass, gn.READ_NORMALIZED) for num, mass in pairs]
+        elif entry is not None:
+            corrs = interface.scan_views(group, x, entry[0], entry[1], "d")
+            stage = [(corr[..., :m], None, gn.READ_PLAIN) for corr in corrs]
+        else:
+            stage = [(None, None, gn.READ_NONE)] * len(group)
+        outputs = []
+        for view, (num1, mass1, corr) in zip(group, stage):
+            h, resid = gn.read_stage(x, W1, W2, tau, num1, mass1, corr=corr, want_resid=True, s=s, eps=cfg.eps)
+            hq = hrot_stream(h, hrot).to(keys.dtype)
+            if cfg.read_norm:
+                (num2, mass2), = interface.scan_views_mass((view,), hq, keys, vals, "m")
+            else:
+                num2, mass2 = interface.scan_views((view,), hq, keys, vals, "m")[0], None
+            outputs.append(gn.normalized_read(num2, mass2, resid, s=s, eps=cfg.eps))
+        return outputs
+
     def layer(group, l, x):
+        if gn_read:
+            return gn_layer(group, l, x)
         W1, W2, Wg = weights[l]
         a = _ein_w(W1, x, "hmd,bhtd->bhtm")
         b = _ein_w(Wg, x, "hmd,bhtd->bhtm") if cfg.nonlin == "swiglu" else None

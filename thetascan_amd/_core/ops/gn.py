@@ -126,3 +126,141 @@ def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps
     if tau is not None and tau.shape != (H, w1.shape[1]):
         tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
     return _GnWrite.apply(x, v, w1, w2, tau, s, inv_depth, eps)
+
+
+# ------------------------------------------------------------------ GN read
+
+READ_NONE, READ_PLAIN, READ_NORMALIZED = 0, 1, 2
+
+
+def _read_desc(q, m, has_tau, corr, want_resid, s, eps):
+    B, H, T, d = q.shape
+    return _lib.GnReadDesc(B, H, T, d, m, _lib.dtype_code(q.dtype), int(has_tau), int(corr), int(want_resid),
+                           float(s), float(eps))
+
+
+class _GnRead(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, w1, w2, tau, num, mass, corr, want_resid, s, eps):
+        lib = _lib.load()
+        qk = _rows(q)
+        B, H, T, d = qk.shape
+        m = w1.shape[1]
+        dt = q.dtype
+        w1c = w1.detach().to(dt).contiguous()
+        w2c = w2.detach().to(dt).contiguous() if want_resid else None
+        tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
+        nk = None if num is None else _rows(num.to(dt))
+        mk = None if mass is None else mass.detach().to(torch.float32)
+        h = torch.empty(B, H, T, m, dtype=dt, device=q.device)
+        resid = torch.empty(B, H, T, d, dtype=dt, device=q.device) if want_resid else None
+        desc = _read_desc(qk, m, tc is not None, corr, want_resid, s, eps)
+        io = _lib.GnReadIO(_lib.strided(qk), w1c.data_ptr(), _lib.ptr(w2c), _lib.ptr(tc), _lib.strided(nk),
+                           _lib.strided(mk), _lib.strided(h), _lib.strided(resid))
+        with _lib.timed("ts_gn_read_fwd", lambda: _lib.nbytes(qk, nk, mk, h, resid)):
+            status = lib.ts_gn_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(q.device))
+        _lib.check(status, "ts_gn_read_fwd")
+        ctx.save_for_backward(qk, w1c, w2c, tc, nk, mk)
+        ctx.meta = (corr, want_resid, s, eps, w1.dtype, None if w2 is None else w2.dtype,
+                    None if tau is None else tau.dtype, None if num is None else num.dtype)
+        if want_resid:
+            return h, resid
+        return h, None
+
+    @staticmethod
+    def backward(ctx, dh, dresid):
+        qk, w1c, w2c, tc, nk, mk = ctx.saved_tensors
+        corr, want_resid, s, eps, w1_dtype, w2_dtype, tau_dtype, num_dtype = ctx.meta
+        lib = _lib.load()
+        B, H, T, d = qk.shape
+        m = w1c.shape[1]
+        dt = qk.dtype
+        N = B * T
+        dh = None if dh is None else _rows(dh.to(dt))
+        dresid = None if (dresid is None or not want_resid) else _rows(dresid.to(dt))
+        w1t = w1c.transpose(1, 2).contiguous()
+        w2t = w2c.transpose(1, 2).contiguous() if want_resid else None
+        dq = torch.empty(B, H, T, d, dtype=dt, device=qk.device)
+        dnum = torch.empty(B, H, T, m, dtype=dt, device=qk.device) if corr else None
+        dmass = torch.empty(B, H, T, dtype=torch.float32, device=qk.device) if corr == READ_NORMALIZED else None
+        has_tau = tc is not None
+        tm = torch.empty(H, 3 if has_tau else 2, N, m, dtype=dt, device=qk.device)
+        td = torch.empty(H, 2, N, d, dtype=dt, device=qk.device)
+        desc = _read_desc(qk, m, has_tau, corr, want_resid, s, eps)
+        io = _lib.GnReadBwdIO(_lib.strided(qk), w1c.data_ptr(), w1t.data_ptr(), _lib.ptr(w2t), _lib.ptr(tc),
+                              _lib.strided(nk), _lib.strided(mk), _lib.strided(dh), _lib.strided(dresid),
+                              _lib.strided(dq), _lib.strided(dnum), _lib.ptr(dmass), tm.data_ptr(), td.data_ptr())
+        with _lib.timed("ts_gn_read_bwd", lambda: _lib.nbytes(qk, nk, mk, dh, dresid, dq, dnum, dmass, tm, td)):
+            status = lib.ts_gn_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(qk.device))
+        _lib.check(status, "ts_gn_read_bwd")
+        dw1 = torch.bmm(tm[:, 0].transpose(1, 2), td[:, 0]).to(w1_dtype)
+        dw2 = torch.bmm(td[:, 1].transpose(1, 2), tm[:, 1]).to(w2_dtype) if want_resid else None
+        dtau = None
+        if has_tau and ctx.needs_input_grad[3]:
+            dtau = (-tm[:, 2].to(torch.float32).sum(1)).to(tau_dtype)
+        if dnum is not None:
+            dnum = dnum.to(num_dtype)
+        return dq, dw1, dw2, dtau, dnum, dmass, None, None, None, None
+
+
+def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = READ_NONE, want_resid: bool = False,
+               s: float = 1.0, eps: float = 1e-6):
+    """One GN read stage: ``h = relu2(rmsnorm(W1 q + c) - tau)`` with
+    ``c`` = 0, ``num`` or ``num / (mass + eps)`` and, with ``want_resid``,
+    ``resid = q + s W2 h``.  Returns ``(h, resid or None)``."""
+    if not q.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    H = q.shape[1]
+    if w1.shape[0] != H:
+        w1 = w1.expand(H, -1, -1)
+    if w2 is not None and w2.shape[0] != H:
+        w2 = w2.expand(H, -1, -1)
+    if tau is not None and tau.shape != (H, w1.shape[1]):
+        tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
+    return _GnRead.apply(q, w1, w2, tau, num, mass, corr, want_resid, s, eps)
+
+
+class _NormalizedRead(torch.autograd.Function):
+    """y = resid + s * num / (mass + eps)  (or + s * num without mass):
+    the read epilogue of engine.py:440-442, 538-544 on ts_read_fwd/bwd."""
+
+    @staticmethod
+    def forward(ctx, num, mass, resid, s, eps):
+        from . import fused
+
+        nk, rk = _rows(num), _rows(resid.to(num.dtype))
+        mk = None if mass is None else mass.detach().to(torch.float32)
+        y = torch.empty_like(nk)
+        fused.read_fwd(nk, mk, rk, None, y, s, eps)
+        ctx.save_for_backward(nk, mk, rk)
+        ctx.meta = (s, eps, resid.dtype, None if mass is None else mass.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        from . import fused
+
+        nk, mk, rk = ctx.saved_tensors
+        s, eps, resid_dtype, mass_dtype = ctx.meta
+        dnum, dmass, (dresid, _), _ = fused.read_bwd(nk, mk, rk, None, _rows(dy.to(nk.dtype)), s, eps)
+        if dmass is not None:
+            dmass = dmass.to(mass_dtype)
+        return dnum, dmass, dresid.to(resid_dtype), None, None
+
+
+def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6):
+    """Read epilogue of one view on the GPU (ts_read_fwd / ts_read_bwd)."""
+    return _NormalizedRead.apply(num, mass, resid, s, eps)
+
+
+def read_eligible(cfg, weights, q: torch.Tensor) -> bool:
+    """Whether the HIP GN read stages cover this configuration (depth-1
+    ReLU^2 GN memories with one Jacobian step, no value anchors)."""
+    if cfg.write_rule != "gn" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.nonlin != "relu2":
+        return False
+    if cfg.value_centers or not q.is_cuda or q.dtype not in (torch.bfloat16, torch.float32):
+        return False
+    if cfg.read_norm and cfg.read_norm_mode != "key_mass":
+        return False
+    W1, W2, _ = weights[0]
+    return q.shape[-1] in GN_HEAD_DIMS and supported_width(W1.shape[-2])

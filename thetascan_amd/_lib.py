@@ -245,6 +245,54 @@ class GnBwdIO(ctypes.Structure):
     ]
 
 
+class GnReadDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("d", ctypes.c_int32),
+        ("m", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("has_tau", ctypes.c_int32),
+        ("corr", ctypes.c_int32),
+        ("want_resid", ctypes.c_int32),
+        ("s", ctypes.c_float),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class GnReadIO(ctypes.Structure):
+    _fields_ = [
+        ("q", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("num", Strided),
+        ("mass", Strided),
+        ("h", Strided),
+        ("resid", Strided),
+    ]
+
+
+class GnReadBwdIO(ctypes.Structure):
+    _fields_ = [
+        ("q", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w1t", ctypes.c_void_p),
+        ("w2t", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("num", Strided),
+        ("mass", Strided),
+        ("dh", Strided),
+        ("dresid", Strided),
+        ("dq", Strided),
+        ("dnum", Strided),
+        ("dmass", ctypes.c_void_p),
+        ("tiles_m", ctypes.c_void_p),
+        ("tiles_d", ctypes.c_void_p),
+    ]
+
+
 class BlendDesc(ctypes.Structure):
     _fields_ = [
         ("B", ctypes.c_int32),
@@ -320,6 +368,8 @@ def load() -> ctypes.CDLL:
                                      ctypes.c_void_p, ctypes.c_void_p]
         lib.ts_gn_write_fwd.argtypes = [P(GnDesc), P(GnIO), ctypes.c_void_p]
         lib.ts_gn_write_bwd.argtypes = [P(GnDesc), P(GnBwdIO), ctypes.c_void_p]
+        lib.ts_gn_read_fwd.argtypes = [P(GnReadDesc), P(GnReadIO), ctypes.c_void_p]
+        lib.ts_gn_read_bwd.argtypes = [P(GnReadDesc), P(GnReadBwdIO), ctypes.c_void_p]
         if lib.ts_abi_version() != 2:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib

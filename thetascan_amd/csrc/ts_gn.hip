@@ -446,6 +446,262 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
   }
 }
 
+// ------------------------------------------------------------ GN read stage
+//
+// One stage of the GN read (engine.py:467-506): per query q,
+//   a = W1 q + c,  c = 0 | num | num / (mass + eps)   (corr = 0 | 1 | 2)
+//   pre = a rsqrt(mean a^2 + eps) - tau,  h = relu(pre)^2
+//   resid = q + s W2 h                                  (want_resid)
+// Stage 1 of the normalized two-stage read is corr = 0 without resid (its h
+// are the queries of the feature-mass scan); stage 2 adds the normalized
+// stage-1 read (corr = 2) and produces the queries of the memory scan and the
+// residual the read epilogue adds the memory to.  The backward emits dq, the
+// gradients of num and mass, and head-major tiles for dW1 = da^T q,
+// dW2 = (s dresid)^T h and dtau = -sum dpre.
+struct GnReadP {
+  int B, H, T, groups, has_tau, corr, want_resid;
+  float s, eps, inv_m;
+  Str q, num, h, resid, dh, dresid, dq, dnum;
+  const float* mass;  // fp32 [B,H,T] with element strides msb, msh, mst
+  float* dmass;
+  int64_t msb, msh, mst;
+  const void* w1;   // [H, m, d]
+  const void* w2;   // [H, d, m]
+  const void* w1t;  // [H, d, m]
+  const void* w2t;  // [H, m, d]
+  const float* tau;
+  void* tm;  // [H, 2 (+1), B*T, m]: da, h (, dpre with tau)
+  void* td;  // [H, 2, B*T, d]: q, s dresid
+};
+
+template <typename E, int D, int MB>
+__device__ __forceinline__ float gn_read_preact(const GnReadP& p, int b, int h, int t, bool valid, int l16, int g,
+                                                const E* xs_w, int xp, const E* w1, int wp1, floatx4* a,
+                                                float& cinv) {
+  gemm_a<E, D, MB>(w1, wp1, xs_w, xp, l16, g, MB, a);
+  cinv = 1.f;
+  if (p.corr) {
+    if (p.corr == 2) cinv = valid ? 1.f / (p.mass[b * p.msb + h * p.msh + (int64_t)t * p.mst] + p.eps) : 0.f;
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+      float c[4];
+      ld4_row<E>(p.num, b, h, t, fb * 16 + 4 * g, valid, c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[fb][i] += c[i] * cinv;
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += a[fb][i] * a[fb][i];
+  return rsqrtf(sum_g(ss) * p.inv_m + p.eps);
+}
+
+template <int MB>
+__device__ __forceinline__ void tau_of(const float* tau, int fb, int g, bool on, float* tv) {
+  tv[0] = tv[1] = tv[2] = tv[3] = 0.f;
+  if (on) {
+    const floatx4 t4 = *(const floatx4*)(tau + fb * 16 + 4 * g);
+    tv[0] = t4[0]; tv[1] = t4[1]; tv[2] = t4[2]; tv[3] = t4[3];
+  }
+}
+
+template <typename E, int D, int MB>
+__global__ __launch_bounds__(256) void gn_read_fwd_kernel(GnReadP p) {
+  constexpr int M = MB * 16;
+  constexpr bool WL = gn_weights_in_lds<E, D, MB, true>();
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnLayout L = gn_layout((int)sizeof(E), D, M, true, WL);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  const E* w1 = (const E*)p.w1 + h * M * D;
+  const E* w2 = p.want_resid ? (const E*)p.w2 + h * D * M : nullptr;
+  int wp1 = D, wp2 = M;
+  if constexpr (WL) {
+    stage_matrix<E>(w1, M, D, base + L.w1, L.xp, tid);
+    if (p.want_resid) stage_matrix<E>(w2, D, M, base + L.w2, L.mp, tid);
+    w1 = base + L.w1;
+    w2 = base + L.w2;
+    wp1 = L.xp;
+    wp2 = L.mp;
+  }
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const Rows<E> qsrc = rows_of<E>(p.q, b, h);
+  RowTile<E, D> ldq;
+  ldq.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldq.fetch(qsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();
+    ldq.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldq.fetch(qsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    floatx4 a[MB], hv[MB];
+    float cinv;
+    const float rinv = gn_read_preact<E, D, MB>(p, b, h, t, valid, l16, g, xs + w * 16 * L.xp, L.xp, w1, wp1, a,
+                                                cinv);
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+      float tv[4], o[4];
+      tau_of<MB>(tau, fb, g, p.has_tau, tv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float rp = fmaxf(a[fb][i] * rinv - tv[i], 0.f);
+        hv[fb][i] = rp * rp;
+        o[i] = hv[fb][i];
+      }
+      st4_row<E>(p.h, b, h, t, fb * 16 + 4 * g, valid, o);
+    }
+    if (p.want_resid) {
+      floatx4 u[D / 16];
+      gemm_back<E, D, MB>(w2, wp2, hv, l16, g, MB, u);
+      const E* qrow = xs + row * L.xp;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float qv[4];
+        ld4f<E>(qrow + db * 16 + 4 * g, qv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] += p.s * u[db][i];
+        st4_row<E>(p.resid, b, h, t, db * 16 + 4 * g, valid, qv);
+      }
+    }
+  }
+}
+
+template <typename E, int D, int MB>
+__global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
+  constexpr int M = MB * 16;
+  constexpr bool WL = gn_weights_in_lds<E, D, MB, false>();
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnLayout L = gn_layout((int)sizeof(E), D, M, false, WL);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  const E* w1 = (const E*)p.w1 + h * M * D;
+  const E* w1t = (const E*)p.w1t + h * D * M;
+  const E* w2t = p.want_resid ? (const E*)p.w2t + h * M * D : nullptr;
+  int wpd = D, wpm = M;
+  if constexpr (WL) {
+    stage_matrix<E>(w1, M, D, base + L.w1, L.xp, tid);
+    stage_matrix<E>(w1t, D, M, base + L.w1t, L.mp, tid);
+    if (p.want_resid) stage_matrix<E>(w2t, M, D, base + L.w2t, L.xp, tid);
+    w1 = base + L.w1;
+    w1t = base + L.w1t;
+    w2t = base + L.w2t;
+    wpd = L.xp;
+    wpm = L.mp;
+  }
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const int64_t N = (int64_t)p.B * p.T;
+  const int nsm = p.has_tau ? 3 : 2;
+  E* tm = (E*)p.tm + (int64_t)h * nsm * N * M;  // da, h (, dpre)
+  E* td = (E*)p.td + (int64_t)h * 2 * N * D;    // q, s dresid
+  const Rows<E> qsrc = rows_of<E>(p.q, b, h);
+  RowTile<E, D> ldq;
+  ldq.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldq.fetch(qsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();
+    ldq.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldq.fetch(qsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const int64_t n = (int64_t)b * p.T + t;
+    floatx4 a[MB];
+    float cinv;
+    const float rinv = gn_read_preact<E, D, MB>(p, b, h, t, valid, l16, g, xs + w * 16 * L.xp, L.xp, w1, wpd, a,
+                                                cinv);
+    float dres[D / 16][4], qv[D / 16][4];
+    floatx4 dres4[D / 16];
+    const E* qrow = xs + row * L.xp;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      ld4f<E>(qrow + db * 16 + 4 * g, qv[db]);
+      ld4_row<E>(p.dresid, b, h, t, db * 16 + 4 * g, valid && p.want_resid, dres[db]);
+      float sd[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dres4[db][i] = dres[db][i];
+        sd[i] = p.s * dres[db][i];
+      }
+      st4_tile<E>(td + 0 * N * D, n, D, db * 16 + 4 * g, valid, qv[db]);
+      st4_tile<E>(td + 1 * N * D, n, D, db * 16 + 4 * g, valid, sd);
+    }
+    floatx4 dhr[MB];
+    if (p.want_resid) {
+      gemm_back<E, M, D / 16>(w2t, wpd, dres4, l16, g, D / 16, dhr);
+    } else {
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb) dhr[fb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    floatx4 da[MB];
+    float ra = 0.f;
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+      float tv[4], dhv[4], hvv[4], dpv[4];
+      tau_of<MB>(tau, fb, g, p.has_tau, tv);
+      ld4_row<E>(p.dh, b, h, t, fb * 16 + 4 * g, valid, dhv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pre = a[fb][i] * rinv - tv[i];
+        const float rp = fmaxf(pre, 0.f);
+        hvv[i] = rp * rp;
+        const float dpre = (valid && pre > 0.f) ? 2.f * rp * (dhv[i] + p.s * dhr[fb][i]) : 0.f;
+        dpv[i] = dpre;
+        da[fb][i] = dpre;
+        ra += dpre * a[fb][i];
+      }
+      st4_tile<E>(tm + 1 * N * M, n, M, fb * 16 + 4 * g, valid, hvv);
+      if (p.has_tau) st4_tile<E>(tm + 2 * N * M, n, M, fb * 16 + 4 * g, valid, dpv);
+    }
+    ra = sum_g(ra);
+    const float c3 = ra * rinv * rinv * rinv * p.inv_m;
+    float dm = 0.f;
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb) {
+      float o[4], dn[4];
+      float c[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.corr == 2) ld4_row<E>(p.num, b, h, t, fb * 16 + 4 * g, valid, c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        da[fb][i] = da[fb][i] * rinv - c3 * a[fb][i];
+        o[i] = da[fb][i];
+        dn[i] = da[fb][i] * cinv;
+        dm += da[fb][i] * c[i];
+      }
+      st4_tile<E>(tm + 0 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+      if (p.corr) st4_row<E>(p.dnum, b, h, t, fb * 16 + 4 * g, valid, dn);
+    }
+    if (p.corr == 2) {
+      dm = sum_g(dm);
+      if (g == 0 && valid) p.dmass[b * p.msb + h * p.msh + (int64_t)t * p.mst] = -dm * cinv * cinv;
+    }
+    floatx4 wda[D / 16];
+    gemm_back<E, D, MB>(w1t, wpm, da, l16, g, MB, wda);
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = dres[db][i] + wda[db][i];
+      st4_row<E>(p.dq, b, h, t, db * 16 + 4 * g, valid, o);
+    }
+  }
+}
+
 }  // namespace ts
 
 namespace {
@@ -546,6 +802,76 @@ int gn_launch(const ts_gn_desc* d, const ts::GnP& p, bool fwd, hipStream_t strea
   return TS_OK;
 }
 
+typedef void (*GnReadKernel)(ts::GnReadP);
+
+template <typename E, bool FWD, int D>
+GnReadKernel gn_read_pick_m(int m) {
+#define TS_GNR(MB) \
+  return FWD ? (GnReadKernel)ts::gn_read_fwd_kernel<E, D, MB> : (GnReadKernel)ts::gn_read_bwd_kernel<E, D, MB>;
+  switch (m) {
+    case 16: TS_GNR(1)
+    case 32: TS_GNR(2)
+    case 48: TS_GNR(3)
+    case 64: TS_GNR(4)
+    case 80: TS_GNR(5)
+    case 96: TS_GNR(6)
+    case 112: TS_GNR(7)
+    case 128: TS_GNR(8)
+    case 256: TS_GNR(16)
+  }
+#undef TS_GNR
+  return nullptr;
+}
+
+template <typename E, bool FWD>
+GnReadKernel gn_read_pick(int d, int m) {
+  switch (d) {
+    case 16: return gn_read_pick_m<E, FWD, 16>(m);
+    case 32: return gn_read_pick_m<E, FWD, 32>(m);
+    case 64: return gn_read_pick_m<E, FWD, 64>(m);
+    case 128: return gn_read_pick_m<E, FWD, 128>(m);
+  }
+  return nullptr;
+}
+
+int check_gn_read(const ts_gn_read_desc* r, ts_gn_desc* d) {
+  if (!r) return fail(TS_ERR_VALUE, "gn read: null descriptor");
+  if (r->corr < 0 || r->corr > 2) return fail(TS_ERR_VALUE, "gn read: corr must be 0, 1 or 2");
+  memset(d, 0, sizeof(*d));
+  d->B = r->B; d->H = r->H; d->T = r->T; d->d = r->d; d->m = r->m; d->dtype = r->dtype; d->has_tau = r->has_tau;
+  d->s = r->s; d->inv_depth = 1.f; d->eps = r->eps;
+  return check_gn(d);
+}
+
+void gn_read_fill(const ts_gn_read_desc* r, const ts_gn_desc* d, ts::GnReadP& p, const ts_strided& mass) {
+  memset(&p, 0, sizeof(p));
+  p.B = r->B; p.H = r->H; p.T = r->T;
+  p.groups = gn_groups(d);
+  p.has_tau = r->has_tau; p.corr = r->corr; p.want_resid = r->want_resid;
+  p.s = r->s; p.eps = r->eps; p.inv_m = 1.0f / (float)r->m;
+  p.mass = (const float*)mass.ptr;
+  p.msb = mass.sb; p.msh = mass.sh; p.mst = mass.st;
+}
+
+int gn_read_launch(const ts_gn_desc* d, const ts::GnReadP& p, bool fwd, hipStream_t stream) {
+  GnReadKernel k = d->dtype == TS_BF16
+                       ? (fwd ? gn_read_pick<ts::bf16, true>(d->d, d->m) : gn_read_pick<ts::bf16, false>(d->d, d->m))
+                       : (fwd ? gn_read_pick<float, true>(d->d, d->m) : gn_read_pick<float, false>(d->d, d->m));
+  if (!k) return fail(TS_ERR_NOT_IMPLEMENTED, "gn read: no kernel for d=%d m=%d", d->d, d->m);
+  const int lds = gn_lds_bytes(d, fwd);
+  if (lds > ts::kGnLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "gn read: tile of %d bytes exceeds LDS", lds);
+  if (lds > 65536) {
+    hipError_t e = ts::ensure_lds_limit((const void*)k, lds);
+    if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "gn read: LDS request failed: %s", hipGetErrorString(e));
+  }
+  const int ngroups = (d->T + ts::TT - 1) / ts::TT;
+  const dim3 grid((unsigned)((ngroups + p.groups - 1) / p.groups), (unsigned)d->H, (unsigned)d->B);
+  hipLaunchKernelGGL(k, grid, dim3(256), lds, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "gn read: launch failed: %s", hipGetErrorString(e));
+  return TS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -587,6 +913,51 @@ int ts_gn_write_bwd(const ts_gn_desc* d, const ts_gn_bwd_io* io, hipStream_t str
   p.w1 = io->w1; p.w2 = io->w2; p.w1t = io->w1t; p.w2t = io->w2t; p.tau = io->tau;
   p.tm = io->tiles_m; p.td = io->tiles_d;
   return gn_launch(d, p, false, stream);
+}
+
+
+int ts_gn_read_fwd(const ts_gn_read_desc* r, const ts_gn_read_io* io, hipStream_t stream) {
+  ts_gn_desc d;
+  int rc = check_gn_read(r, &d);
+  if (rc) return rc;
+  if (!io || !io->q.ptr || !io->w1 || !io->h.ptr) return fail(TS_ERR_VALUE, "gn read: missing tensors");
+  if (r->want_resid && (!io->w2 || !io->resid.ptr)) return fail(TS_ERR_VALUE, "gn read: missing W2 or resid");
+  if (r->corr && !io->num.ptr) return fail(TS_ERR_VALUE, "gn read: missing num");
+  if (r->corr == 2 && !io->mass.ptr) return fail(TS_ERR_VALUE, "gn read: missing mass");
+  if (r->has_tau && !io->tau) return fail(TS_ERR_VALUE, "gn read: missing tau");
+  const int vec = r->dtype == TS_BF16 ? 8 : 4;
+  for (const ts_strided* s : {&io->q, &io->num, &io->h, &io->resid})
+    if (!gn_stream_ok(*s, vec)) return fail(TS_ERR_VALUE, "gn read: streams need 16-byte aligned rows");
+  if (r->T == 0) return TS_OK;
+  ts::GnReadP p;
+  gn_read_fill(r, &d, p, io->mass);
+  p.q = gn_str(io->q); p.num = gn_str(io->num); p.h = gn_str(io->h); p.resid = gn_str(io->resid);
+  p.w1 = io->w1; p.w2 = io->w2; p.tau = io->tau;
+  return gn_read_launch(&d, p, true, stream);
+}
+
+int ts_gn_read_bwd(const ts_gn_read_desc* r, const ts_gn_read_bwd_io* io, hipStream_t stream) {
+  ts_gn_desc d;
+  int rc = check_gn_read(r, &d);
+  if (rc) return rc;
+  if (!io || !io->q.ptr || !io->w1 || !io->w1t || !io->dq.ptr || !io->tiles_m || !io->tiles_d)
+    return fail(TS_ERR_VALUE, "gn read bwd: missing tensors");
+  if (r->want_resid && !io->w2t) return fail(TS_ERR_VALUE, "gn read bwd: missing W2^T");
+  if (r->corr && (!io->num.ptr || !io->dnum.ptr)) return fail(TS_ERR_VALUE, "gn read bwd: missing num");
+  if (r->corr == 2 && (!io->mass.ptr || !io->dmass)) return fail(TS_ERR_VALUE, "gn read bwd: missing mass");
+  if (r->has_tau && !io->tau) return fail(TS_ERR_VALUE, "gn read bwd: missing tau");
+  const int vec = r->dtype == TS_BF16 ? 8 : 4;
+  for (const ts_strided* s : {&io->q, &io->num, &io->dh, &io->dresid, &io->dq, &io->dnum})
+    if (!gn_stream_ok(*s, vec)) return fail(TS_ERR_VALUE, "gn read bwd: streams need 16-byte aligned rows");
+  if (r->T == 0) return TS_OK;
+  ts::GnReadP p;
+  gn_read_fill(r, &d, p, io->mass);
+  p.q = gn_str(io->q); p.num = gn_str(io->num);
+  p.dh = gn_str(io->dh); p.dresid = gn_str(io->dresid); p.dq = gn_str(io->dq); p.dnum = gn_str(io->dnum);
+  p.dmass = io->dmass;
+  p.w1 = io->w1; p.w1t = io->w1t; p.w2t = io->w2t; p.tau = io->tau;
+  p.tm = io->tiles_m; p.td = io->tiles_d;
+  return gn_read_launch(&d, p, false, stream);
 }
 
 }  // extern "C"

@@ -79,7 +79,7 @@ def seeded_module(config, seed: int):
     return module
 
 
-def time_steps(module, x, dy, steps: int, warmup: int, graphed=None):
+def time_steps(module, x, dy, steps: int, warmup: int, graphed=None, train: bool = True):
     """Mean ms per fwd+bwd step over exactly ``steps`` steps after ``warmup``.
 
     With ``graphed`` (a ``torch.cuda.make_graphed_callables`` wrapper of the
@@ -90,6 +90,10 @@ def time_steps(module, x, dy, steps: int, warmup: int, graphed=None):
     fwd = module if graphed is None else graphed
 
     def step():
+        if not train:
+            with torch.no_grad():
+                fwd(x)
+            return
         module.zero_grad(set_to_none=True)
         y = fwd(x)
         y.backward(dy)
@@ -125,7 +129,7 @@ def graphed_step_ms(module, x, dy, steps: int, warmup: int):
     return time_steps(twin, x, dy, steps, warmup, graphed)
 
 
-def pass_profile(module, x, dy, steps: int = 5):
+def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
     """Per-entry-point timing inside real fwd+bwd steps.
 
     Every HIP entry point called during ``steps`` steps is bracketed by events
@@ -137,8 +141,12 @@ def pass_profile(module, x, dy, steps: int = 5):
     from thetascan_amd import _lib
 
     def step():
-        module.zero_grad(set_to_none=True)
-        module(x).backward(dy)
+        if train:
+            module.zero_grad(set_to_none=True)
+            module(x).backward(dy)
+        else:
+            with torch.no_grad():
+                module(x)
 
     step()
     torch.cuda.synchronize()
@@ -256,9 +264,73 @@ def cpu_baseline(budget_s: float = 12.0):
     }
 
 
+# The other two workloads the path serves, measured with ``--workload``:
+#   gn            damped Gauss-Newton memory, fast net 64 -> 128 -> 64 (ReLU^2),
+#                 two-stage feature-mass read normalization, B8 T2048 H8 d64,
+#                 bf16, fwd+bwd;
+#   bspline_bank  kernel memory with the cubic B-spline map (8 basis functions,
+#                 m = 128), key-mass read, two-rate recency bank (fast blend,
+#                 retentions 0.9 / 0.999), B2 T32768 H8 d64, 128-token tiles,
+#                 bf16, forward only.
+OTHER = {
+    "gn": dict(B=8, T=2048, train=True, metric="GN mixer tokens/s fwd+bwd (B8 T2048 H8 d64 m128 bf16)"),
+    "bspline_bank": dict(B=2, T=32768, train=False,
+                         metric="B-spline bank mixer tokens/s fwd (B2 T32768 H8 d64 m128 bf16)"),
+}
+
+
+def other_config(name: str):
+    import thetascan_amd as ts
+
+    if name == "gn":
+        return ts.ThetaScanConfig(
+            d_model=D_MODEL, n_heads=H, memory_multiplier=2, family="gn",
+            gn=ts.GNConfig(nonlinearity="relu2", jacobian_steps=1, read_normalization="both_feature_mass"),
+            temporal=ts.TemporalConfig(mode="sum"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64),
+        )
+    return ts.ThetaScanConfig(
+        d_model=D_MODEL, n_heads=H, memory_multiplier=2, family="kernel",
+        kernel=ts.KernelConfig(feature_map="projected_bspline", read_normalization="key_mass"),
+        temporal=ts.TemporalConfig(mode="bank", bank_mode="fast", recency_branches=2, retention_inits=(0.9, 0.999)),
+        runtime=ts.RuntimeConfig(backend="hip", scan_chunk=128),
+    )
+
+
+def run_other(name: str, args) -> dict:
+    """One JSON line for a non-headline workload (no CPU baseline)."""
+    import torch
+
+    spec = OTHER[name]
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    module = __import__("thetascan_amd").ThetaScan(other_config(name))
+    g = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        for pname, p in sorted(module.named_parameters()):
+            if "fade_eta" in pname or (p.ndim >= 2 and float(p.abs().max()) == 0.0):
+                p.copy_(torch.randn(p.shape, generator=g) * (0.3 if "fade_eta" in pname else 0.02))
+    module = module.to(dev, torch.bfloat16)
+    x = torch.randn(spec["B"], spec["T"], D_MODEL, generator=g).to(dev, torch.bfloat16)
+    dy = (torch.randn(spec["B"], spec["T"], D_MODEL, generator=g) * 1e-2).to(dev, torch.bfloat16)
+    ms = time_steps(module, x, dy, args.steps, args.warmup, train=spec["train"])
+    passes = pass_profile(module, x, dy, train=spec["train"])
+    return {
+        "metric": spec["metric"], "value": round(spec["B"] * spec["T"] / (ms * 1e-3), 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (x ~ N(0,1), seeded weights)", "execution": "eager",
+        "path": module._core.last_path,
+        "config": {"workload": name, "batch": spec["B"], "seq_len": spec["T"], "heads": H, "head_dim": D_HEAD,
+                   "d_model": D_MODEL, "parallelism": "single GPU"},
+        "roofline": roofline_of(passes, {}), "passes": passes,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=("headline", *OTHER), default="headline",
+                    help="headline (default) or one of the other two workloads of the path")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -280,6 +352,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.workload != "headline":
+        print(json.dumps(run_other(args.workload, args)), flush=True)
+        return 0
     dev = torch.device("cuda", 0)
     g = torch.Generator().manual_seed(1234)
     x = torch.randn(B, T, D_MODEL, generator=g).to(dev, torch.bfloat16)

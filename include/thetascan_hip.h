@@ -272,8 +272,8 @@ typedef struct ts_gn_bwd_io {
   ts_strided dh, dlam, dg; /* gradients of the three outputs (NULL = zero)     */
   ts_strided dx_in;     /* added into dx (NULL = zero)                          */
   ts_strided dx, dv;    /* out [B,H,T,d]                                        */
-  void* tiles_m;        /* out [H, 4 (+1 with tau), B*T, m]: dz, h, da, s2 (, dpre) */
-  void* tiles_d;        /* out [H, 4, B*T, d]: lam, du, x, drq                  */
+  void* tiles_m;        /* out [4 (+1 with tau), H, B*T, m]: dz, h, da, s2 (, dpre) */
+  void* tiles_d;        /* out [4, H, B*T, d]: lam, du, x, drq                  */
 } ts_gn_bwd_io;
 
 /* Backward of ts_gn_write_fwd: dx, dv, and the token tiles whose contractions
@@ -323,8 +323,8 @@ typedef struct ts_gn_read_bwd_io {
   ts_strided dq;        /* out [.,d]                                            */
   ts_strided dnum;      /* out [.,m] (corr 1, 2)                                */
   float* dmass;         /* out fp32, laid out like mass (corr 2)                */
-  void* tiles_m;        /* out [H, 2 (+1 with tau), B*T, m]: da, h (, dpre)     */
-  void* tiles_d;        /* out [H, 2, B*T, d]: q, s*dresid                      */
+  void* tiles_m;        /* out [2 (+1 with tau), H, B*T, m]: da, h (, dpre)     */
+  void* tiles_d;        /* out [2, H, B*T, d]: q, s*dresid                      */
 } ts_gn_read_bwd_io;
 
 /* Backward of ts_gn_read_fwd: dq, dnum, dmass and the token tiles of

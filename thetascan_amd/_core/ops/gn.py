@@ -5,8 +5,8 @@ Jacobian step, the torch chain of src/thetascan/_core/ops/engine.py:117-158
 (_block_forward), 180-195 (_g_from_lambda), 215-255 (_lambda_solve) and the
 stream assembly of 260-340: one kernel produces the LA2 keys h, the LA2
 values s*lam and the LA1 values g per token.  The backward kernel recomputes
-the forward, writes dx and dv, and leaves head-major token tiles that batched
-GEMMs contract into dW1, dW2 and dtau.
+the forward, writes dx and dv, and leaves slot-major token tiles
+([slot, H, B*T, w]) that split-K batched GEMMs contract into dW1, dW2 and dtau.
 """
 from __future__ import annotations
 
@@ -48,6 +48,20 @@ def _desc(x, m, has_tau, s, inv_depth, eps):
     B, H, T, d = x.shape
     return _lib.GnDesc(B, H, T, d, m, _lib.dtype_code(x.dtype), int(has_tau), float(s), float(inv_depth),
                        float(eps))
+
+
+def contract_tokens(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """sum_n a[h, n, :]^T b[h, n, :] -> fp32 [H, p, q] for head-major token
+    tiles a [H, N, p], b [H, N, q].  The token axis is split into slices that
+    run as separate GEMM batches (split-K), so a handful of heads still fill
+    the GPU; the slice partials are summed in fp32."""
+    H, N, p = a.shape
+    q = b.shape[-1]
+    S = 1
+    while S < 64 and H * S < 512 and N % (2 * S) == 0 and N // (2 * S) >= 256:
+        S *= 2
+    parts = torch.bmm(a.reshape(H * S, N // S, p).transpose(1, 2), b.reshape(H * S, N // S, q))
+    return parts.view(H, S, p, q).sum(1, dtype=torch.float32)
 
 
 class _GnWrite(torch.autograd.Function):
@@ -93,8 +107,8 @@ class _GnWrite(torch.autograd.Function):
         dx = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
         dv = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
         nsm = 5 if has_tau else 4
-        tm = torch.empty(H, nsm, N, m, dtype=dt, device=xk.device)
-        td = torch.empty(H, 4, N, d, dtype=dt, device=xk.device)
+        tm = torch.empty(nsm, H, N, m, dtype=dt, device=xk.device)
+        td = torch.empty(4, H, N, d, dtype=dt, device=xk.device)
         desc = _desc(xk, m, has_tau, s, inv_depth, eps)
         io = _lib.GnBwdIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w1t.data_ptr(),
                           w2t.data_ptr(), _lib.ptr(tc), _lib.strided(dh), _lib.strided(dlam), _lib.strided(dg),
@@ -103,12 +117,12 @@ class _GnWrite(torch.autograd.Function):
             status = lib.ts_gn_write_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(xk.device))
         _lib.check(status, "ts_gn_write_bwd")
         # dW1 = da^T x;  dW2 = lam^T dz + du^T h + 2 W2 o (drq^T s2);  dtau = -sum dpre
-        dw1 = torch.bmm(tm[:, 2].transpose(1, 2), td[:, 2])
-        dw2 = torch.bmm(td[:, 0:2].reshape(H, 2 * N, d).transpose(1, 2), tm[:, 0:2].reshape(H, 2 * N, m))
-        dw2 = dw2 + 2.0 * w2c * torch.bmm(td[:, 3].transpose(1, 2), tm[:, 3])
+        dw1 = contract_tokens(tm[2], td[2])
+        dw2 = contract_tokens(td[0], tm[0]) + contract_tokens(td[1], tm[1])
+        dw2 = dw2 + 2.0 * w2c.to(torch.float32) * contract_tokens(td[3], tm[3])
         dtau = None
         if has_tau and ctx.needs_input_grad[4]:
-            dtau = (-tm[:, 4].to(torch.float32).sum(1)).to(tau_dtype)
+            dtau = (-tm[4].sum(1, dtype=torch.float32)).to(tau_dtype)
         return dx, dv, dw1.to(w1_dtype), dw2.to(w2_dtype), dtau, None, None, None
 
 
@@ -184,8 +198,8 @@ class _GnRead(torch.autograd.Function):
         dnum = torch.empty(B, H, T, m, dtype=dt, device=qk.device) if corr else None
         dmass = torch.empty(B, H, T, dtype=torch.float32, device=qk.device) if corr == READ_NORMALIZED else None
         has_tau = tc is not None
-        tm = torch.empty(H, 3 if has_tau else 2, N, m, dtype=dt, device=qk.device)
-        td = torch.empty(H, 2, N, d, dtype=dt, device=qk.device)
+        tm = torch.empty(3 if has_tau else 2, H, N, m, dtype=dt, device=qk.device)
+        td = torch.empty(2, H, N, d, dtype=dt, device=qk.device)
         desc = _read_desc(qk, m, has_tau, corr, want_resid, s, eps)
         io = _lib.GnReadBwdIO(_lib.strided(qk), w1c.data_ptr(), w1t.data_ptr(), _lib.ptr(w2t), _lib.ptr(tc),
                               _lib.strided(nk), _lib.strided(mk), _lib.strided(dh), _lib.strided(dresid),
@@ -193,11 +207,11 @@ class _GnRead(torch.autograd.Function):
         with _lib.timed("ts_gn_read_bwd", lambda: _lib.nbytes(qk, nk, mk, dh, dresid, dq, dnum, dmass, tm, td)):
             status = lib.ts_gn_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(qk.device))
         _lib.check(status, "ts_gn_read_bwd")
-        dw1 = torch.bmm(tm[:, 0].transpose(1, 2), td[:, 0]).to(w1_dtype)
-        dw2 = torch.bmm(td[:, 1].transpose(1, 2), tm[:, 1]).to(w2_dtype) if want_resid else None
+        dw1 = contract_tokens(tm[0], td[0]).to(w1_dtype)
+        dw2 = contract_tokens(td[1], tm[1]).to(w2_dtype) if want_resid else None
         dtau = None
         if has_tau and ctx.needs_input_grad[3]:
-            dtau = (-tm[:, 2].to(torch.float32).sum(1)).to(tau_dtype)
+            dtau = (-tm[2].sum(1, dtype=torch.float32)).to(tau_dtype)
         if dnum is not None:
             dnum = dnum.to(num_dtype)
         return dq, dw1, dw2, dtau, dnum, dmass, None, None, None, None

@@ -13,7 +13,7 @@
 //
 // Outputs: h (the LA2 keys), s lam (LA2 values) and g (LA1 values).  The
 // backward recomputes the forward from x and v, writes dx and dv, and emits
-// head-major weight-gradient tiles ([H, slot, B*T, w]) that batched GEMMs
+// head-major weight-gradient tiles ([slot, H, B*T, w]) that batched GEMMs
 // contract over tokens: dW1 = da^T x, dW2 = lam^T dz + du^T h + 2 W2 o
 // (drq^T s2), dtau = -sum dpre.
 //
@@ -39,8 +39,8 @@ struct GnP {
   const void* w1t;                 // [H, d, m]
   const void* w2t;                 // [H, m, d]
   const float* tau;                // [H, m]
-  void* tm;                        // [H, 4 (+1), B*T, m]: dz, h, da, s2 (, dpre with tau)
-  void* td;                        // [H, 4, B*T, d]: lam, du, x, drq
+  void* tm;                        // [4 (+1), H, B*T, m]: dz, h, da, s2 (, dpre with tau)
+  void* td;                        // [4, H, B*T, d]: lam, du, x, drq
 };
 
 // LDS carve-up (elements of E): x tile, then the weights when they fit.
@@ -279,9 +279,10 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
   }
   const float* tau = p.has_tau ? p.tau + h * M : nullptr;
   const int64_t N = (int64_t)p.B * p.T;
-  const int nsm = p.has_tau ? 5 : 4;
-  E* tm = (E*)p.tm + (int64_t)h * nsm * N * M;  // dz, h, da, s2 (, dpre)
-  E* td = (E*)p.td + (int64_t)h * 4 * N * D;  // lam, du, x, drq
+  // slot-major tiles: slot k of head h starts at k * H * N * w + h * N * w
+  E* tm = (E*)p.tm + (int64_t)h * N * M;  // dz, h, da, s2 (, dpre)
+  E* td = (E*)p.td + (int64_t)h * N * D;  // lam, du, x, drq
+  const int64_t HNM = (int64_t)p.H * N * M, HND = (int64_t)p.H * N * D;
   const Rows<E> xsrc = rows_of<E>(p.x, b, h);
   RowTile<E, D> ldx;
   ldx.init(D, tid);
@@ -306,15 +307,15 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb) {
       float o[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
-      st4_tile<E>(tm + 1 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+      st4_tile<E>(tm + 1 * HNM, n, M, fb * 16 + 4 * g, valid, o);
       float o2[4] = {s2v[fb][0], s2v[fb][1], s2v[fb][2], s2v[fb][3]};
-      st4_tile<E>(tm + 3 * N * M, n, M, fb * 16 + 4 * g, valid, o2);
+      st4_tile<E>(tm + 3 * HNM, n, M, fb * 16 + 4 * g, valid, o2);
     }
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
       float o[4] = {k.lam[db][0], k.lam[db][1], k.lam[db][2], k.lam[db][3]};
-      st4_tile<E>(td + 0 * N * D, n, D, db * 16 + 4 * g, valid, o);
-      st4_tile<E>(td + 2 * N * D, n, D, db * 16 + 4 * g, valid, k.xr[db]);
+      st4_tile<E>(td + 0 * HND, n, D, db * 16 + 4 * g, valid, o);
+      st4_tile<E>(td + 2 * HND, n, D, db * 16 + 4 * g, valid, k.xr[db]);
     }
     // ---- g = s sp z rinv, z = W2^T lam
     floatx4 dz[MB], dsp[MB];
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
           drinv += sdg * sp * z[fb][i];
         }
         float o[4] = {dz[fb][0], dz[fb][1], dz[fb][2], dz[fb][3]};
-        st4_tile<E>(tm + 0 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+        st4_tile<E>(tm + 0 * HNM, n, M, fb * 16 + 4 * g, valid, o);
       }
     }
     // ---- lam -> r, den -> (hh, xx, rq)
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) drq[db][i] *= k.xx;
         float o[4] = {drq[db][0], drq[db][1], drq[db][2], drq[db][3]};
-        st4_tile<E>(td + 3 * N * D, n, D, db * 16 + 4 * g, valid, o);
+        st4_tile<E>(td + 3 * HND, n, D, db * 16 + 4 * g, valid, o);
       }
     }
     // ---- rq = (W2 o W2) s2, s2 = (sp rinv)^2
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
         duv[i] = du[db][i];
       }
       st4_row<E>(p.dv, b, h, t, db * 16 + 4 * g, valid, dvv);
-      st4_tile<E>(td + 1 * N * D, n, D, db * 16 + 4 * g, valid, duv);
+      st4_tile<E>(td + 1 * HND, n, D, db * 16 + 4 * g, valid, duv);
     }
     floatx4 da[MB];
     {
@@ -421,7 +422,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
           da[fb][i] = dpre;  // completed below once drinv is known
           ra += dpre * k.a[fb][i];
         }
-        if (p.has_tau) st4_tile<E>(tm + 4 * N * M, n, M, fb * 16 + 4 * g, valid, dpv);
+        if (p.has_tau) st4_tile<E>(tm + 4 * HNM, n, M, fb * 16 + 4 * g, valid, dpv);
       }
       drinv = sum_g(drinv + ra);
     }
@@ -431,7 +432,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) da[fb][i] = da[fb][i] * k.rinv - c3 * k.a[fb][i];
       float o[4] = {da[fb][0], da[fb][1], da[fb][2], da[fb][3]};
-      st4_tile<E>(tm + 2 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+      st4_tile<E>(tm + 2 * HNM, n, M, fb * 16 + 4 * g, valid, o);
     }
     floatx4 wda[D / 16];
     gemm_back<E, D, MB>(w1t, wpm, da, l16, g, MB, wda);
@@ -470,8 +471,8 @@ struct GnReadP {
   const void* w1t;  // [H, d, m]
   const void* w2t;  // [H, m, d]
   const float* tau;
-  void* tm;  // [H, 2 (+1), B*T, m]: da, h (, dpre with tau)
-  void* td;  // [H, 2, B*T, d]: q, s dresid
+  void* tm;  // [2 (+1), H, B*T, m]: da, h (, dpre with tau)
+  void* td;  // [2, H, B*T, d]: q, s dresid
 };
 
 template <typename E, int D, int MB>
@@ -602,9 +603,10 @@ __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
   }
   const float* tau = p.has_tau ? p.tau + h * M : nullptr;
   const int64_t N = (int64_t)p.B * p.T;
-  const int nsm = p.has_tau ? 3 : 2;
-  E* tm = (E*)p.tm + (int64_t)h * nsm * N * M;  // da, h (, dpre)
-  E* td = (E*)p.td + (int64_t)h * 2 * N * D;    // q, s dresid
+  // slot-major tiles: slot k of head h starts at k * H * N * w + h * N * w
+  E* tm = (E*)p.tm + (int64_t)h * N * M;  // da, h (, dpre)
+  E* td = (E*)p.td + (int64_t)h * N * D;  // q, s dresid
+  const int64_t HNM = (int64_t)p.H * N * M, HND = (int64_t)p.H * N * D;
   const Rows<E> qsrc = rows_of<E>(p.q, b, h);
   RowTile<E, D> ldq;
   ldq.init(D, tid);
@@ -638,8 +640,8 @@ __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
         dres4[db][i] = dres[db][i];
         sd[i] = p.s * dres[db][i];
       }
-      st4_tile<E>(td + 0 * N * D, n, D, db * 16 + 4 * g, valid, qv[db]);
-      st4_tile<E>(td + 1 * N * D, n, D, db * 16 + 4 * g, valid, sd);
+      st4_tile<E>(td + 0 * HND, n, D, db * 16 + 4 * g, valid, qv[db]);
+      st4_tile<E>(td + 1 * HND, n, D, db * 16 + 4 * g, valid, sd);
     }
     floatx4 dhr[MB];
     if (p.want_resid) {
@@ -665,8 +667,8 @@ __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
         da[fb][i] = dpre;
         ra += dpre * a[fb][i];
       }
-      st4_tile<E>(tm + 1 * N * M, n, M, fb * 16 + 4 * g, valid, hvv);
-      if (p.has_tau) st4_tile<E>(tm + 2 * N * M, n, M, fb * 16 + 4 * g, valid, dpv);
+      st4_tile<E>(tm + 1 * HNM, n, M, fb * 16 + 4 * g, valid, hvv);
+      if (p.has_tau) st4_tile<E>(tm + 2 * HNM, n, M, fb * 16 + 4 * g, valid, dpv);
     }
     ra = sum_g(ra);
     const float c3 = ra * rinv * rinv * rinv * p.inv_m;
@@ -683,7 +685,7 @@ __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
         dn[i] = da[fb][i] * cinv;
         dm += da[fb][i] * c[i];
       }
-      st4_tile<E>(tm + 0 * N * M, n, M, fb * 16 + 4 * g, valid, o);
+      st4_tile<E>(tm + 0 * HNM, n, M, fb * 16 + 4 * g, valid, o);
       if (p.corr) st4_row<E>(p.dnum, b, h, t, fb * 16 + 4 * g, valid, dn);
     }
     if (p.corr == 2) {

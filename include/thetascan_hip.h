@@ -74,6 +74,12 @@ typedef struct ts_scan_desc {
   int32_t want_final;   /* 1: write the final [dk_pad, dv_pad] state          */
   int32_t value_split;  /* value columns per workgroup (16, 32, 64 or 128,
                            dividing dv_pad); 0 = the whole width             */
+  int32_t states_in;    /* 0: compute the segment states; 1: the workspace
+                           already holds them (from an earlier call of this
+                           scan's keys and values); 2: it holds those of the
+                           swapped scan (keys and values exchanged, same
+                           segments and retention), read transposed.  Skips the
+                           summary and prefix passes.  No ext columns.       */
 } ts_scan_desc;
 
 typedef struct ts_scan_io {

@@ -121,6 +121,39 @@ def test_value_slices_are_exact(cuda, split, Dv, seg_chunks, kind):
 
 
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
+@pytest.mark.parametrize("reverse", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kept_segment_states_are_exact(cuda, kind, reverse, dtype):
+    """A scan that reads the segment states an earlier scan left in its
+    workspace (states_in=1), or those of the swapped scan read transposed
+    (states_in=2: keys and values exchanged), equals the scan computed from
+    scratch.  This is how the backward's dq (dv) scan reuses the forward's
+    (dk's) states."""
+    from thetascan_amd._core.ops import scan_hip
+    from thetascan_amd import _lib
+
+    B, H, T, D = 2, 3, 700, 64
+    q, k, v, w = (x.to(cuda, dtype) for x in _streams(B, H, T, D, D, seed=21) + (_streams(B, H, T, D, D, seed=22)[0],))
+    ret = _retention(kind, B, H, T)
+    kw = {"retention": {"none": _lib.RET_NONE, "static": _lib.RET_STATIC, "stream": _lib.RET_STREAM}[kind],
+          "reverse": reverse, "seg_chunks": 3}
+    if kind == "static":
+        kw["log_alpha"] = ret.to(cuda, torch.float32)
+    if kind == "stream":
+        kw["decay"] = ret.to(cuda, torch.float32)
+    # forward-like scan scan(q, k, v) keeps its states
+    ws = scan_hip.workspace_for(q, k, v, seg_chunks=3, retention=kw["retention"], reverse=reverse)
+    assert ws is not None
+    out, _, _ = scan_hip.scan_launch(q, k, v, workspace=ws, **kw)
+    again, _, _ = scan_hip.scan_launch(q, k, v, workspace=ws, states_in=1, **kw)
+    assert torch.equal(again, out)
+    # swapped scan scan(w, v, k): keys v, values k -- its states are the transpose
+    ref, _, _ = scan_hip.scan_launch(w, v, k, **kw)
+    got, _, _ = scan_hip.scan_launch(w, v, k, workspace=ws, states_in=2, **kw)
+    assert rel_err(got, ref) < (1e-5 if dtype == torch.float32 else 1e-2), (kind, reverse)
+
+
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
 def test_reverse_scan_is_the_time_reversed_scan(cuda, kind):
     """The anti-causal mode used by the backward equals flipping time."""
     from thetascan_amd._core.ops import scan_hip

@@ -342,9 +342,13 @@ class _KernelMemory(torch.autograd.Function):
         tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
         phi_k, _ = feature_fwd(spec, k, w1c, None, tauf, False)
         phi_q, resid = feature_fwd(spec, q, w1c, w2c, tauf, True)
+        # Without the mass column the dq scan's segment states are the transpose
+        # of this scan's (sum_i v_i phi_k_i^T), so the forward keeps them.
+        share = not normalize and phi_k.shape[-1] == d
+        ws = scan_hip.workspace_for(phi_q, phi_k, v, seg_chunks=seg_chunks) if share else None
         num, mass, _ = scan_hip.scan_launch(
             phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
-            seg_chunks=seg_chunks,
+            seg_chunks=seg_chunks, workspace=ws,
         )
         gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
         y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
@@ -354,6 +358,7 @@ class _KernelMemory(torch.autograd.Function):
         ctx.has_tau = tau is not None
         ctx.tau_dtype = None if tau is None else tau.dtype
         ctx.w_dtypes = (w1.dtype, w2.dtype)
+        ctx.ws = ws
         ctx.save_for_backward(proj, w1c, w2c, tauf, phi_q, phi_k, num, mass, resid)
         return y.view(B, T, H * d)
 
@@ -381,11 +386,19 @@ class _KernelMemory(torch.autograd.Function):
         dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv)
         norm = ctx.normalize
         q_ext = dmass if norm else None
+        ws_f, ctx.ws = ctx.ws, None
+        # dq = scan(dnum, v, phi_k): its segment states are the forward's, transposed
         dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
-                                            seg_chunks=ctx.seg_chunks)
+                                            seg_chunks=ctx.seg_chunks, workspace=ws_f,
+                                            states_in=2 if ws_f is not None else 0)
+        # dk = reverse scan(v, dnum, phi_q) and dv = reverse scan(phi_k, phi_q, dnum) share
+        # their segment states up to a transpose (sum_i dnum_i phi_q_i^T)
+        ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=ctx.seg_chunks, reverse=True) \
+            if ws_f is not None else None
         dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
-                                            k_ext=q_ext, seg_chunks=ctx.seg_chunks)
-        scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=ctx.seg_chunks)
+                                            k_ext=q_ext, seg_chunks=ctx.seg_chunks, workspace=ws_r)
+        scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=ctx.seg_chunks,
+                             workspace=ws_r, states_in=2 if ws_r is not None else 0)
         need_w1 = ctx.needs_input_grad[1]
         need_w2 = ctx.needs_input_grad[2]
         need_tau = ctx.has_tau and ctx.needs_input_grad[3]

@@ -103,19 +103,30 @@ def scan_launch(
     want_final: bool = False,
     seg_chunks: int = 0,
     value_split: int = 0,
+    workspace: torch.Tensor | None = None,
+    states_in: int = 0,
 ):
     """One scan (several kernel launches when a width exceeds ``MAX_WIDTH``).
 
     Returns ``(out, ext_out, final_state)`` as :func:`_scan_once`.  The scan
     is linear in each operand, so wide values split into independent value
     chunks and wide keys into key chunks whose results add up.
+
+    ``workspace`` (from :func:`workspace_for`) keeps the segment states of
+    this scan after the call; ``states_in`` = 1 (2) reads the states an
+    earlier call of the same (swapped) keys and values left there instead of
+    recomputing them -- single-launch widths only.
     """
     dk, dv = q.shape[-1], v.shape[-1]
+    if workspace is not None or states_in:
+        if dk > MAX_WIDTH or dv > MAX_WIDTH:
+            raise NotImplementedError("hip scan: kept segment states need widths up to 128")
     if dk <= MAX_WIDTH and dv <= MAX_WIDTH:
         return _scan_once(q, k, v, retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse,
                           q_ext=q_ext, k_ext=k_ext, v_ext=v_ext, out=out, out_mode=out_mode, out_scale=out_scale,
                           want_ext_out=want_ext_out, ext_out=ext_out, want_final=want_final,
-                          seg_chunks=seg_chunks, value_split=value_split)
+                          seg_chunks=seg_chunks, value_split=value_split, workspace=workspace,
+                          states_in=states_in)
     if want_final:
         raise NotImplementedError(f"hip scan: final state of widths dk={dk} dv={dv} above {MAX_WIDTH}")
     kw = dict(retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse, seg_chunks=seg_chunks,
@@ -178,6 +189,8 @@ def _scan_once(
     want_final: bool = False,
     seg_chunks: int = 0,
     value_split: int = 0,
+    workspace: torch.Tensor | None = None,
+    states_in: int = 0,
 ):
     """One kernel launch.  Returns ``(out, ext_out, final_state)``.
 
@@ -210,7 +223,7 @@ def _scan_once(
     ve_mode, ve = _ext_arg(v_ext)
 
     fields = (B, H, T, dkw, dvw, code, retention, int(reverse), qe_mode, ke_mode, ve_mode,
-              out_mode, float(out_scale), int(seg_chunks), int(want_final), int(value_split))
+              out_mode, float(out_scale), int(seg_chunks), int(want_final), int(value_split), int(states_in))
     desc = _lib.ScanDesc(*fields)
     plan = _PLANS.get(fields)
     if plan is None:
@@ -240,8 +253,10 @@ def _scan_once(
     final = None
     if want_final:
         final = torch.zeros(B * H, dk_pad, dv_pad, dtype=torch.float32, device=q.device)
-    workspace = None
-    if ws_bytes:
+    if workspace is not None:
+        if workspace.numel() * workspace.element_size() < ws_bytes:
+            raise ValueError("hip scan: workspace too small")
+    elif ws_bytes:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
 
     la = None
@@ -280,6 +295,23 @@ def _scan_once(
 
 
 _PLANS: dict = {}
+
+
+def workspace_for(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, seg_chunks: int = 0,
+                  retention: int = _lib.RET_NONE, reverse: bool = False) -> torch.Tensor | None:
+    """A workspace that keeps the segment states of ``scan_launch(q, k, v, ...)``
+    for a later call with ``states_in`` (None when the scan has one segment)."""
+    lib = _lib.load()
+    vec = _vec(q.dtype)
+    B, H, T, dk = q.shape
+    dv = v.shape[-1]
+    desc = _lib.ScanDesc(B, H, T, -(-dk // vec) * vec, -(-dv // vec) * vec, _lib.dtype_code(q.dtype), retention,
+                         int(reverse), 0, 0, 0, _lib.OUT_STORE, 1.0, int(seg_chunks), 0, 0, 0)
+    c_ws = ctypes.c_size_t()
+    _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan workspace")
+    if not c_ws.value:
+        return None
+    return torch.empty(c_ws.value, dtype=torch.uint8, device=q.device)
 
 
 # ------------------------------------------------------------------ retentions

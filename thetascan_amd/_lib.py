@@ -63,6 +63,7 @@ class ScanDesc(ctypes.Structure):
         ("seg_chunks", ctypes.c_int32),
         ("want_final", ctypes.c_int32),
         ("value_split", ctypes.c_int32),
+        ("states_in", ctypes.c_int32),
     ]
 
 

@@ -82,6 +82,7 @@ __device__ __forceinline__ void bstf(rsrc_t r, uint32_t off, float v) {
 struct ScanP {
   int B, H, T, dk, dv, dvp;  // dvp: padded value width of the whole scan
   int vs;                    // padded value columns per workgroup (blockIdx.z selects the slice)
+  int states_t;              // segment states read transposed (those of the swapped scan)
   int nchunks, seg_chunks, nseg, nsum, nelem;
   int ret, reverse;
   int q_ext, k_ext, v_ext;
@@ -377,10 +378,20 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
     for (int r = 0; r < NVW; ++r) {
       const int vb = w + 4 * r;
       if (vb < nvb) {
+        if (p.states_t) {
+          // the swapped scan's state [value][key] is this scan's [key][value]
+          const float* row = src + (size_t)(col0 + vb * 16 + l16) * DK;
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+          for (int kb = 0; kb < NKB; ++kb) {
+            const floatx4 v4 = *(const floatx4*)(row + kb * 16 + 4 * g);
+            S[r][kb] = v4;
+          }
+        } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) S[r][kb][i] = src[(kb * 16 + 4 * g + i) * p.dvp + col0 + vb * 16 + l16];
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[r][kb][i] = src[(kb * 16 + 4 * g + i) * p.dvp + col0 + vb * 16 + l16];
+        }
         const float u = src[DK * p.dvp + col0 + vb * 16 + l16];
         us[r] = floatx4{u, u, u, u};
       }
@@ -845,6 +856,14 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   L->nseg = L->nchunks > 0 ? (L->nchunks + L->seg_chunks - 1) / L->seg_chunks : 0;
   L->nsum = d->want_final ? L->nseg : (L->nseg > 0 ? L->nseg - 1 : 0);
   L->nelem = L->dkp * L->dvp + L->dvp + L->dkp;
+  if (d->states_in < 0 || d->states_in > 2) return fail(TS_ERR_VALUE, "scan: states_in must be 0, 1 or 2");
+  if (d->states_in) {
+    if (L->kx || L->vx || d->want_final || L->nvs != 1)
+      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment states need no ext columns, no final state "
+                                          "and the whole value width per workgroup");
+    if (d->states_in == 2 && (d->dk != d->dv || L->dkp != L->dvp))
+      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: transposed segment states need dk == dv (a padded width)");
+  }
   L->ws_bytes = 0;
   if (L->nsum > 0)
     L->ws_bytes = (size_t)bh * L->nseg * (size_t)L->nelem * sizeof(float) + (size_t)bh * L->nseg * sizeof(float) + 256;
@@ -1009,7 +1028,8 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
     return fail(TS_ERR_NOT_IMPLEMENTED, "scan: tile of %lld bytes exceeds LDS (dk_pad=%d slice=%d)",
                 (long long)lds_main, L.dkp, L.vs);
 
-  if (L.nsum > 0) {
+  p.states_t = d->states_in == 2;
+  if (L.nsum > 0 && d->states_in == 0) {
     if ((rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p))) return rc;
     ts::FinalP F{d->want_final ? io->final_state : nullptr, L.dkp, L.dvp, d->dk, d->dv, L.kx ? 1 : 0,
                  L.vx ? 1 : 0};

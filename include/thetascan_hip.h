@@ -78,8 +78,10 @@ typedef struct ts_scan_desc {
                            already holds them (from an earlier call of this
                            scan's keys and values); 2: it holds those of the
                            swapped scan (keys and values exchanged, same
-                           segments and retention), read transposed.  Skips the
-                           summary and prefix passes.  No ext columns.       */
+                           segments and retention), read transposed; a key-side
+                           ext row u is then the swapped scan's value-side ext
+                           state.  Skips the summary and prefix passes.  No
+                           value-side ext column (nor key-side with 1).      */
 } ts_scan_desc;
 
 typedef struct ts_scan_io {

@@ -153,6 +153,26 @@ def test_kept_segment_states_are_exact(cuda, kind, reverse, dtype):
     assert rel_err(got, ref) < (1e-5 if dtype == torch.float32 else 1e-2), (kind, reverse)
 
 
+@pytest.mark.parametrize("reverse", [False, True])
+def test_kept_segment_states_with_mass_columns(cuda, reverse):
+    """The normalized read's pair: scan(q, k, v | ones) keeps its states, and
+    the swapped scan(w, v, k) with a q ext array and unit k ext column reads
+    them transposed, its key-side row u being the first scan's value-side
+    sum of keys."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, D = 2, 3, 650, 64
+    q, k, v = (x.to(cuda, torch.float32) for x in _streams(B, H, T, D, D, seed=31))
+    w = _streams(B, H, T, D, D, seed=32)[0].to(cuda, torch.float32)
+    we = torch.randn(B, H, T, generator=torch.Generator().manual_seed(4)).to(cuda)
+    ws = scan_hip.workspace_for(q, k, v, seg_chunks=3, reverse=reverse, v_ext=True)
+    scan_hip.scan_launch(q, k, v, v_ext="ones", want_ext_out=True, seg_chunks=3, reverse=reverse, workspace=ws)
+    ref, _, _ = scan_hip.scan_launch(w, v, k, q_ext=we, k_ext="ones", seg_chunks=3, reverse=reverse)
+    got, _, _ = scan_hip.scan_launch(w, v, k, q_ext=we, k_ext="ones", seg_chunks=3, reverse=reverse, workspace=ws,
+                                     states_in=2)
+    assert rel_err(got, ref) < 1e-5
+
+
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
 def test_reverse_scan_is_the_time_reversed_scan(cuda, kind):
     """The anti-causal mode used by the backward equals flipping time."""

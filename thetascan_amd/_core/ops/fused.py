@@ -342,10 +342,13 @@ class _KernelMemory(torch.autograd.Function):
         tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
         phi_k, _ = feature_fwd(spec, k, w1c, None, tauf, False)
         phi_q, resid = feature_fwd(spec, q, w1c, w2c, tauf, True)
-        # Without the mass column the dq scan's segment states are the transpose
-        # of this scan's (sum_i v_i phi_k_i^T), so the forward keeps them.
-        share = not normalize and phi_k.shape[-1] == d
-        ws = scan_hip.workspace_for(phi_q, phi_k, v, seg_chunks=seg_chunks) if share else None
+        # The dq scan's segment states are the transpose of this scan's
+        # (sum_i v_i phi_k_i^T; with the mass column its key-side row is this
+        # scan's value-side sum_i phi_k_i), so the forward keeps them.
+        share = phi_k.shape[-1] == d
+        ws = None
+        if share:
+            ws = scan_hip.workspace_for(phi_q, phi_k, v, seg_chunks=seg_chunks, v_ext=normalize)
         num, mass, _ = scan_hip.scan_launch(
             phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
             seg_chunks=seg_chunks, workspace=ws,
@@ -393,7 +396,7 @@ class _KernelMemory(torch.autograd.Function):
                                             states_in=2 if ws_f is not None else 0)
         # dk = reverse scan(v, dnum, phi_q) and dv = reverse scan(phi_k, phi_q, dnum) share
         # their segment states up to a transpose (sum_i dnum_i phi_q_i^T)
-        ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=ctx.seg_chunks, reverse=True) \
+        ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=ctx.seg_chunks, reverse=True, kx=norm) \
             if ws_f is not None else None
         dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
                                             k_ext=q_ext, seg_chunks=ctx.seg_chunks, workspace=ws_r)

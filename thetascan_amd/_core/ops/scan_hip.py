@@ -298,15 +298,19 @@ _PLANS: dict = {}
 
 
 def workspace_for(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, seg_chunks: int = 0,
-                  retention: int = _lib.RET_NONE, reverse: bool = False) -> torch.Tensor | None:
+                  retention: int = _lib.RET_NONE, reverse: bool = False, v_ext: bool = False,
+                  kx: bool = False) -> torch.Tensor | None:
     """A workspace that keeps the segment states of ``scan_launch(q, k, v, ...)``
-    for a later call with ``states_in`` (None when the scan has one segment)."""
+    for a later call with ``states_in`` (None when the scan has one segment).
+    ``v_ext`` / ``kx`` describe the scan's value-side / key-side ext columns."""
     lib = _lib.load()
     vec = _vec(q.dtype)
     B, H, T, dk = q.shape
     dv = v.shape[-1]
+    ext = _lib.EXT_ONES
     desc = _lib.ScanDesc(B, H, T, -(-dk // vec) * vec, -(-dv // vec) * vec, _lib.dtype_code(q.dtype), retention,
-                         int(reverse), 0, 0, 0, _lib.OUT_STORE, 1.0, int(seg_chunks), 0, 0, 0)
+                         int(reverse), ext if kx else 0, ext if kx else 0, ext if v_ext else 0, _lib.OUT_STORE, 1.0,
+                         int(seg_chunks), 0, 0, 0)
     c_ws = ctypes.c_size_t()
     _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan workspace")
     if not c_ws.value:

@@ -378,21 +378,26 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
     for (int r = 0; r < NVW; ++r) {
       const int vb = w + 4 * r;
       if (vb < nvb) {
+        float u;
         if (p.states_t) {
-          // the swapped scan's state [value][key] is this scan's [key][value]
-          const float* row = src + (size_t)(col0 + vb * 16 + l16) * DK;
+          // the swapped scan's state [value][key] is this scan's [key][value],
+          // and its value-side ext state D (sum of its keys times its ext
+          // value) is this scan's key-side ext row u
+          const int c = col0 + vb * 16 + l16;
+          const float* row = src + (size_t)c * DK;
 #pragma unroll
           for (int kb = 0; kb < NKB; ++kb) {
             const floatx4 v4 = *(const floatx4*)(row + kb * 16 + 4 * g);
             S[r][kb] = v4;
           }
+          u = src[DK * DK + DK + c];
         } else {
 #pragma unroll
           for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) S[r][kb][i] = src[(kb * 16 + 4 * g + i) * p.dvp + col0 + vb * 16 + l16];
+          u = src[DK * p.dvp + col0 + vb * 16 + l16];
         }
-        const float u = src[DK * p.dvp + col0 + vb * 16 + l16];
         us[r] = floatx4{u, u, u, u};
       }
     }
@@ -858,9 +863,9 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   L->nelem = L->dkp * L->dvp + L->dvp + L->dkp;
   if (d->states_in < 0 || d->states_in > 2) return fail(TS_ERR_VALUE, "scan: states_in must be 0, 1 or 2");
   if (d->states_in) {
-    if (L->kx || L->vx || d->want_final || L->nvs != 1)
-      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment states need no ext columns, no final state "
-                                          "and the whole value width per workgroup");
+    if ((L->kx && d->states_in == 1) || L->vx || d->want_final || L->nvs != 1)
+      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment states need no value-side ext column, no "
+                                          "final state and the whole value width per workgroup");
     if (d->states_in == 2 && (d->dk != d->dv || L->dkp != L->dvp))
       return fail(TS_ERR_NOT_IMPLEMENTED, "scan: transposed segment states need dk == dv (a padded width)");
   }

@@ -168,8 +168,8 @@ int ts_feature_fwd(const ts_feature_desc* desc, const ts_feature_io* io, hipStre
 typedef struct ts_feature_bwd_io {
   ts_strided x;                    /* [B,H,T,d] forward input                  */
   const void* w1;                  /* [H,m,d]                                  */
-  const void* w1t;                 /* [H,d,m] (W1 transposed)                  */
-  const void* w2t;                 /* [H,m,d] (W2 transposed; resid only)      */
+  const void* w1t;                 /* [H,d,m] (W1 transposed), or NULL         */
+  const void* w2t;                 /* [H,m,d] (W2 transposed; resid), or NULL  */
   const float* tau;
   const float* in_cos;
   const float* in_sin;
@@ -185,7 +185,14 @@ typedef struct ts_feature_bwd_io {
   float* dw1_part;                 /* out fp32 [P,H,m,d]: partial sums of da^T xn        */
   float* dw2_part;                 /* out fp32 [P,H,d,m]: partial sums of s dresid^T h   */
   float* dtau_part;                /* out fp32 [P,H]: partial sums of -sum_j dpre_j      */
+  const void* w2;                  /* [H,d,m] (resid; read when w2t is NULL)   */
 } ts_feature_bwd_io;
+
+/* Whether ts_feature_bwd needs the transposed weights w1t / w2t for `desc`
+ * (weights too large to stage in LDS).  Otherwise they may be NULL: the
+ * kernel transposes W1 (and W2 from `w2`) while staging them. */
+int ts_feature_bwd_transposed(const ts_feature_desc* desc, int32_t has_dresid, int32_t fused_wgrad,
+                              int32_t* needed);
 
 /* Backward of ts_feature_fwd (recomputes the forward tile in registers/LDS).
  * Two ways to obtain the weight gradients of W1, W2 and tau:
@@ -220,9 +227,10 @@ typedef struct ts_read_io {
   ts_strided resid;                /* [B,H,T,d] xn + s*W2 h                    */
   ts_strided g;                    /* gate pre-activation, [B,H,T,d] view      */
   ts_strided y;                    /* out [B,H,T,d] view (e.g. of [B,T,H*d])   */
+  const float* g_bias;             /* fp32 [H,d] added to g before silu (NULL) */
 } ts_read_io;
 
-/* Normalized read epilogue:  y = (resid + s * num / (mass + eps)) * silu(g).
+/* Normalized read epilogue:  y = (resid + s * num / (mass + eps)) * silu(g + g_bias).
  * Replaces engine.py:440-442, 526-528 and the output gate of
  * block.py:721-722 (gates.py:34-40). */
 int ts_read_fwd(const ts_read_desc* desc, const ts_read_io* io, hipStream_t stream);
@@ -234,6 +242,7 @@ typedef struct ts_read_bwd_io {
   ts_strided dmass;                /* out fp32 [B,H,T] (normalize)             */
   ts_strided dresid;               /* out [B,H,T,d] (desc dtype; NULL ok)      */
   ts_strided dg;                   /* out [B,H,T,d] (gate)                     */
+  const float* g_bias;             /* as in ts_read_io                         */
 } ts_read_bwd_io;
 
 int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t stream);

@@ -339,9 +339,17 @@ class ThetaScan(nn.Module):
 
     def fused_eligible(self, x: torch.Tensor) -> bool:
         """Whether the three-kernel hot path covers this configuration and input."""
-        cfg = self.cfg
         if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
             return False
+        # The answer depends on the (immutable) configuration and on which
+        # optional parameters exist, never on parameter values.
+        hit = self.__dict__.get("_fused_ok")
+        if hit is None:
+            hit = self.__dict__["_fused_ok"] = self._config_fused_eligible()
+        return hit
+
+    def _config_fused_eligible(self) -> bool:
+        cfg = self.cfg
         if cfg.write_rule != "kernel" or cfg.depth != 1 or cfg.value_centers or cfg.value_mlp_mult > 0:
             return False
         if cfg.read_fade or cfg.accumulation != "sum" or cfg.share_kq or cfg.key_value_heads is not None:
@@ -361,20 +369,27 @@ class ThetaScan(nn.Module):
                     and self.kernel_score_bias is None)
         return False
 
+    def _feature_spec(self):
+        spec = self.__dict__.get("_spec")
+        if spec is None:
+            cfg = self.cfg
+            d, m = cfg.head_dim, cfg.mem_hidden
+            in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
+            feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
+            kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
+            spec = self.__dict__["_spec"] = fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot,
+                                                              cfg.rope_base, 1.0 / math.sqrt(cfg.depth), cfg.eps)
+        return spec
+
     def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
         cfg = self.cfg
-        B, T, _ = x.shape
-        H, d, m = cfg.n_heads, cfg.head_dim, cfg.mem_hidden
-        in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
-        feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
-        kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
-        spec = fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot, cfg.rope_base,
-                                 1.0 / math.sqrt(cfg.depth), cfg.eps)
+        H = cfg.n_heads
+        spec = self._feature_spec()
         (W1, W2, _), = self._weights()
         gate = self.ogate is not None
-        proj = fused.in_projection(x, self.proj_qkv.weight, self.ogate.g.lin.weight if gate else None,
-                                   self.ogate.g.lin.bias if gate else None)
-        y = fused.kernel_memory(proj, W1, W2, self.kernel_relu2_threshold, spec, cfg.read_norm, H, gate)
+        proj = fused.in_projection(x, self.proj_qkv.weight, self.ogate.g.lin.weight if gate else None)
+        y = fused.kernel_memory(proj, W1, W2, self.kernel_relu2_threshold, spec, cfg.read_norm, H, gate,
+                                gate_bias=self.ogate.g.lin.bias if gate else None)
         return linear(y, self.proj_out.weight)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -109,26 +109,31 @@ def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_w
     the kernel (sum them with :func:`sum_grads`), or, for shapes without a
     fused kernel, an fp32 tensor from per-token tiles and split-K GEMMs
     (None where not applicable or not wanted).  ``w1t`` / ``w2t`` are the
-    [H,d,m] / [H,m,d] transposes when the caller already has them.
+    [H,d,m] / [H,m,d] transposes; they are only formed when the weights are too
+    large for the kernel to transpose while staging them in LDS.
     """
     lib = _lib.load()
     B, H, T, d = x.shape
     m = spec.m
     dev = x.device
-    if w1t is None:
-        w1t = w1.transpose(1, 2).contiguous()
-    if dresid is not None and w2t is None:
-        w2t = w2.transpose(1, 2).contiguous()
     desc = spec.desc(x, tau is not None)
-    P = 0
-    if want_weights:
-        key = (B, H, T, d, m, x.dtype, spec.kind, dresid is not None)
-        P = _PARTS.get(key, -1)
-        if P < 0:
-            parts = ctypes.c_int32(0)
+    key = (B, H, T, d, m, x.dtype, spec.kind, dresid is not None, bool(want_weights))
+    plan = _PARTS.get(key)
+    if plan is None:
+        parts, needed = ctypes.c_int32(0), ctypes.c_int32(1)
+        if want_weights:
             _lib.check(lib.ts_feature_bwd_parts(ctypes.byref(desc), int(dresid is not None), ctypes.byref(parts)),
                        "ts_feature_bwd_parts")
-            P = _PARTS[key] = parts.value
+        _lib.check(lib.ts_feature_bwd_transposed(ctypes.byref(desc), int(dresid is not None),
+                                                 int(parts.value > 0), ctypes.byref(needed)),
+                   "ts_feature_bwd_transposed")
+        plan = _PARTS[key] = (parts.value, bool(needed.value))
+    P, need_t = plan
+    if need_t:
+        if w1t is None:
+            w1t = w1.transpose(1, 2).contiguous()
+        if dresid is not None and w2t is None:
+            w2t = w2.transpose(1, 2).contiguous()
     da = xn = h = da_v = xn_v = h_v = dtau_tok = None
     dw1p = dw2p = dtaup = None
     if want_weights and P > 0:
@@ -149,7 +154,7 @@ def feature_bwd(spec: FeatureSpec, x, w1, tau, dphi, dresid, dx, w2=None, want_w
         _lib.strided(x), _lib.ptr(w1), _lib.ptr(w1t), _lib.ptr(w2t), _lib.ptr(tau), _lib.ptr(ic),
         _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs), _lib.strided(dphi), _lib.strided(dresid),
         _lib.strided(dx), _lib.strided(da_v), _lib.strided(xn_v), _lib.strided(h_v), _lib.strided(dtau_tok),
-        _lib.ptr(dw1p), _lib.ptr(dw2p), _lib.ptr(dtaup),
+        _lib.ptr(dw1p), _lib.ptr(dw2p), _lib.ptr(dtaup), _lib.ptr(w2 if dresid is not None else None),
     )
     with _lib.timed("ts_feature_bwd", lambda: _lib.nbytes(x, dphi, dresid, dx, da, xn, h, dtau_tok, dw1p, dw2p,
                                                           dtaup)):
@@ -201,20 +206,20 @@ def _head_major_of(t: torch.Tensor) -> torch.Tensor:
     return hm.view(H, B * T, w)
 
 
-def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6):
+def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6, gbias=None):
     lib = _lib.load()
     B, H, T, d = num.shape
     desc = _lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None), int(g is not None),
                          float(scale), float(eps))
     io = _lib.ReadIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
-                     _lib.strided(y))
+                     _lib.strided(y), _lib.ptr(gbias))
     with _lib.timed("ts_read_fwd", lambda: _lib.nbytes(num, mass, resid, g, y)):
         status = lib.ts_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
     _lib.check(status, "ts_read_fwd")
     return y
 
 
-def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None):
+def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None, gbias=None):
     """Backward of :func:`read_fwd`; ``dg`` optionally names the [B,H,T,d]
     view the gate gradient is written to."""
     lib = _lib.load()
@@ -228,7 +233,7 @@ def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None):
                          float(scale), float(eps))
     io = _lib.ReadBwdIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
                         _lib.strided(dy), _lib.strided(dnum), _lib.strided(dmass), _lib.strided(dresid),
-                        _lib.strided(dg))
+                        _lib.strided(dg), _lib.ptr(gbias))
     with _lib.timed("ts_read_bwd", lambda: _lib.nbytes(num, mass, resid, g, dy, dnum, dmass, dresid, dg)):
         status = lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
     _lib.check(status, "ts_read_bwd")
@@ -265,39 +270,34 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
     return out
 
 
-def _stacked(w_qkv, w_g, b_g, dtype):
-    """[W_qkv; W_g] and [0; b_g] (rebuilt every call: parameters may change
-    in place in ways no version counter records, e.g. through ``.data``)."""
-    weight = torch.cat([w_qkv.detach(), w_g.detach().to(w_qkv.dtype)], dim=0)
-    bias = torch.cat([w_qkv.new_zeros(w_qkv.shape[0], dtype=dtype), b_g.detach().to(dtype)])
-    return weight, bias
+def _stacked(w_qkv, w_g):
+    """[W_qkv; W_g] (rebuilt every call: parameters may change in place in ways
+    no version counter records, e.g. through ``.data``)."""
+    return torch.cat([w_qkv.detach(), w_g.detach().to(w_qkv.dtype)], dim=0)
 
 
 class _InProjection(torch.autograd.Function):
-    """proj = x [W_qkv; W_g]^T + [0; b_g]: the qkv projection and the output-gate
+    """proj = x [W_qkv; W_g]^T: the qkv projection and the output gate's
     projection as one GEMM (block.py:593-594 and gates.py:34-40 read the same
-    x), with one gradient GEMM for x and one split-K GEMM for the stacked
-    weights."""
+    x; the gate bias is added inside the read kernel), with one gradient GEMM
+    for x and one split-K GEMM for the stacked weights."""
 
     @staticmethod
-    def forward(ctx, x, w_qkv, w_g, b_g):
+    def forward(ctx, x, w_qkv, w_g):
         n_qkv = w_qkv.shape[0]
-        if w_g is None:
-            weight, bias = w_qkv, None
-        else:
-            weight, bias = _stacked(w_qkv, w_g, b_g, x.dtype)
+        weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
         ctx.save_for_backward(x, weight)
         ctx.n_qkv = n_qkv
         ctx.has_g = w_g is not None
-        ctx.dtypes = (w_qkv.dtype, None if w_g is None else w_g.dtype, None if b_g is None else b_g.dtype)
-        return torch.nn.functional.linear(x, weight, bias)
+        ctx.dtypes = (w_qkv.dtype, None if w_g is None else w_g.dtype)
+        return torch.nn.functional.linear(x, weight)
 
     @staticmethod
     def backward(ctx, dproj):
         x, weight = ctx.saved_tensors
         n_out, n_in = weight.shape
         d2 = dproj.reshape(-1, n_out)
-        dx = dw_qkv = dw_g = db_g = None
+        dx = dw_qkv = dw_g = None
         if ctx.needs_input_grad[0]:
             dx = (d2 @ weight).view(x.shape)
         if ctx.needs_input_grad[1] or (ctx.has_g and ctx.needs_input_grad[2]):
@@ -306,16 +306,14 @@ class _InProjection(torch.autograd.Function):
             dw_qkv = dw[:ctx.n_qkv].to(ctx.dtypes[0])
             if ctx.has_g:
                 dw_g = dw[ctx.n_qkv:].to(ctx.dtypes[1])
-        if ctx.has_g and ctx.needs_input_grad[3]:
-            db_g = column_sum(d2[:, ctx.n_qkv:], ctx.dtypes[2])
-        return dx, dw_qkv, dw_g, db_g
+        return dx, dw_qkv, dw_g
 
 
-def in_projection(x, w_qkv, w_g=None, b_g=None):
-    """[B,T,3*H*d (+H*d)] projection for :func:`kernel_memory`."""
+def in_projection(x, w_qkv, w_g=None):
+    """The stacked qkv (+ output-gate) projection of ``x`` [B,T,d_model]."""
     if not x.is_cuda:
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
-    return _InProjection.apply(x, w_qkv, w_g, b_g)
+    return _InProjection.apply(x, w_qkv, w_g)
 
 
 class _KernelMemory(torch.autograd.Function):
@@ -327,7 +325,7 @@ class _KernelMemory(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, proj, w1, w2, tau, spec: FeatureSpec, normalize: bool, seg_chunks: int, heads: int,
+    def forward(ctx, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int, heads: int,
                 has_gate: bool):
         B, T, P = proj.shape
         H = heads
@@ -354,20 +352,22 @@ class _KernelMemory(torch.autograd.Function):
             seg_chunks=seg_chunks, workspace=ws,
         )
         gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
+        gb = None if b_g is None else b_g.detach().to(torch.float32).contiguous()
         y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
-        read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps)
+        read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=gb)
         ctx.spec, ctx.normalize, ctx.seg_chunks = spec, normalize, seg_chunks
         ctx.heads, ctx.d, ctx.has_gate = H, d, has_gate
         ctx.has_tau = tau is not None
         ctx.tau_dtype = None if tau is None else tau.dtype
         ctx.w_dtypes = (w1.dtype, w2.dtype)
+        ctx.b_dtype = None if b_g is None else b_g.dtype
         ctx.ws = ws
-        ctx.save_for_backward(proj, w1c, w2c, tauf, phi_q, phi_k, num, mass, resid)
+        ctx.save_for_backward(proj, w1c, w2c, tauf, gb, phi_q, phi_k, num, mass, resid)
         return y.view(B, T, H * d)
 
     @staticmethod
     def backward(ctx, dy):
-        proj, w1c, w2c, tauf, phi_q, phi_k, num, mass, resid = ctx.saved_tensors
+        proj, w1c, w2c, tauf, gb, phi_q, phi_k, num, mass, resid = ctx.saved_tensors
         spec = ctx.spec
         B, T, P = proj.shape
         H, d = ctx.heads, ctx.d
@@ -386,7 +386,8 @@ class _KernelMemory(torch.autograd.Function):
             gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
             dgv = dproj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
         dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
-        dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv)
+        dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv,
+                                               gbias=gb)
         norm = ctx.normalize
         q_ext = dmass if norm else None
         ws_f, ctx.ws = ctx.ws, None
@@ -405,13 +406,13 @@ class _KernelMemory(torch.autograd.Function):
         need_w1 = ctx.needs_input_grad[1]
         need_w2 = ctx.needs_input_grad[2]
         need_tau = ctx.has_tau and ctx.needs_input_grad[3]
+        db_g = None
+        if gb is not None and ctx.needs_input_grad[4]:
+            db_g = column_sum(dproj.view(-1, P)[:, 3 * H * d:], ctx.b_dtype)
         want_k = need_w1 or need_tau
         want_q = need_w1 or need_w2 or need_tau
-        w1t = w1c.transpose(1, 2).contiguous()
-        w2t = w2c.transpose(1, 2).contiguous()
-        dw1_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=want_k, w1t=w1t)
-        dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c, want_weights=want_q,
-                                           w1t=w1t, w2t=w2t)
+        dw1_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=want_k)
+        dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c, want_weights=want_q)
         dw1 = dw2 = dtau = None
         if need_w1:
             dw1 = sum_grads(dw1_k, dw1_q, ctx.w_dtypes[0], w1c.shape)
@@ -419,14 +420,14 @@ class _KernelMemory(torch.autograd.Function):
             dw2 = sum_grads(dw2_q, None, ctx.w_dtypes[1], w2c.shape)
         if need_tau:
             dtau = sum_grads(dtau_k, dtau_q, ctx.tau_dtype, (H,))
-        return dproj, dw1, dw2, dtau, None, None, None, None, None
+        return dproj, dw1, dw2, dtau, db_g, None, None, None, None, None
 
 
 def kernel_memory(proj, w1, w2, tau, spec: FeatureSpec, normalize: bool, heads: int, has_gate: bool,
-                  seg_chunks: int = 0):
+                  seg_chunks: int = 0, gate_bias=None):
     """Fused kernel-memory read of the [B,T,3*H*d (+H*d)] input projection."""
     if not proj.is_cuda:
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
     if not proj.is_contiguous():
         proj = proj.contiguous()
-    return _KernelMemory.apply(proj, w1, w2, tau, spec, normalize, seg_chunks, heads, has_gate)
+    return _KernelMemory.apply(proj, w1, w2, tau, gate_bias, spec, normalize, seg_chunks, heads, has_gate)

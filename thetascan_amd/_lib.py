@@ -137,6 +137,7 @@ class FeatureBwdIO(ctypes.Structure):
         ("dw1_part", ctypes.c_void_p),
         ("dw2_part", ctypes.c_void_p),
         ("dtau_part", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
     ]
 
 
@@ -155,7 +156,8 @@ class ReadDesc(ctypes.Structure):
 
 
 class ReadIO(ctypes.Structure):
-    _fields_ = [("num", Strided), ("mass", Strided), ("resid", Strided), ("g", Strided), ("y", Strided)]
+    _fields_ = [("num", Strided), ("mass", Strided), ("resid", Strided), ("g", Strided), ("y", Strided),
+                ("g_bias", ctypes.c_void_p)]
 
 
 class ReadBwdIO(ctypes.Structure):
@@ -169,6 +171,7 @@ class ReadBwdIO(ctypes.Structure):
         ("dmass", Strided),
         ("dresid", Strided),
         ("dg", Strided),
+        ("g_bias", ctypes.c_void_p),
     ]
 
 
@@ -351,6 +354,7 @@ def load() -> ctypes.CDLL:
         lib.ts_feature_fwd.argtypes = [P(FeatureDesc), P(FeatureIO), ctypes.c_void_p]
         lib.ts_feature_bwd.argtypes = [P(FeatureDesc), P(FeatureBwdIO), ctypes.c_void_p]
         lib.ts_feature_bwd_parts.argtypes = [P(FeatureDesc), ctypes.c_int32, P(ctypes.c_int32)]
+        lib.ts_feature_bwd_transposed.argtypes = [P(FeatureDesc), ctypes.c_int32, ctypes.c_int32, P(ctypes.c_int32)]
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]

@@ -12,6 +12,7 @@ struct ReadP {
   int B, H, T, d, normalize, gate;
   float s, eps;
   ts_strided num, mass, resid, g, y, dy, dnum, dmass, dresid, dg;
+  const float* gbias;  // [H, d] added to the gate pre-activation (or null)
 };
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -84,7 +85,12 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(ReadP p, int p2) {
   float nv[N], rv[N], gv[N], out[N];
   ld_vec<E>(rowp<E>(p.num, b, h, t) + c, nv);
   if (p.resid.ptr) ld_vec<E>(rowp<E>(p.resid, b, h, t) + c, rv);
-  if (p.gate) ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
+  if (p.gate) {
+    ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
+    if (p.gbias)
+#pragma unroll
+      for (int e = 0; e < N; ++e) gv[e] += p.gbias[h * p.d + c + e];
+  }
 #pragma unroll
   for (int e = 0; e < N; ++e) {
     const float v = (p.resid.ptr ? rv[e] : 0.0f) + scale * nv[e];
@@ -113,7 +119,12 @@ __global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p, int p2) {
     ld_vec<E>(rowp<E>(p.num, b, h, t) + c, nv);
     ld_vec<E>(rowp<E>(p.dy, b, h, t) + c, dv);
     if (p.resid.ptr) ld_vec<E>(rowp<E>(p.resid, b, h, t) + c, rv);
-    if (p.gate) ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
+    if (p.gate) {
+      ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
+      if (p.gbias)
+#pragma unroll
+        for (int e = 0; e < N; ++e) gv[e] += p.gbias[h * p.d + c + e];
+    }
 #pragma unroll
     for (int e = 0; e < N; ++e) {
       float dpre = dv[e];
@@ -308,6 +319,7 @@ int ts_read_fwd(const ts_read_desc* d, const ts_read_io* io, hipStream_t stream)
   ts::ReadP p;
   fill_read(d, p);
   p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.y = io->y;
+  p.gbias = io->g_bias;
   const int p2 = lanes_per_row(d);
   const dim3 grid((unsigned)((rows * p2 + 255) / 256));
   if (d->dtype == TS_BF16)
@@ -329,6 +341,7 @@ int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t str
   fill_read(d, p);
   p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.dy = io->dy;
   p.dnum = io->dnum; p.dmass = io->dmass; p.dresid = io->dresid; p.dg = io->dg;
+  p.gbias = io->g_bias;
   const int p2 = lanes_per_row(d);
   const dim3 grid((unsigned)((rows * p2 + 255) / 256));
   if (d->dtype == TS_BF16)

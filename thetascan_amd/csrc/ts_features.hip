@@ -294,8 +294,12 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
   int wpa = D, wpt = m;
   if constexpr (WL) {
     stage_matrix<E>(w1, m, D, base + L.w1, L.xp, tid);
-    stage_matrix<E>(w1t, D, m, base + L.w1t, L.mp, tid);
-    if (has_resid) stage_matrix<E>(w2t, m, D, base + L.w2, L.xp, tid);
+    if (p.w1t) stage_matrix<E>(w1t, D, m, base + L.w1t, L.mp, tid);
+    else stage_transposed<E>(w1, m, D, base + L.w1t, L.mp, tid);
+    if (has_resid) {
+      if (p.w2t) stage_matrix<E>(w2t, m, D, base + L.w2, L.xp, tid);
+      else stage_transposed<E>((const E*)p.w2 + h * D * m, D, m, base + L.w2, L.xp, tid);
+    }
     w1 = base + L.w1;
     w1t = base + L.w1t;
     w2t = base + L.w2;
@@ -722,12 +726,21 @@ int ts_feature_bwd_parts(const ts_feature_desc* d, int32_t has_dresid, int32_t* 
   return TS_OK;
 }
 
+int ts_feature_bwd_transposed(const ts_feature_desc* d, int32_t has_dresid, int32_t fused_wgrad, int32_t* needed) {
+  int rc = check_feature_desc(d);
+  if (rc) return rc;
+  Plan P;
+  if ((rc = plan_feature(d, false, has_dresid != 0, fused_wgrad != 0, &P))) return rc;
+  if (needed) *needed = kernel_wl(d->dtype == TS_BF16 ? 2 : 4, d->d, d->m, false, P.wgrad) ? 0 : 1;
+  return TS_OK;
+}
+
 int ts_feature_bwd(const ts_feature_desc* d, const ts_feature_bwd_io* io, hipStream_t stream) {
   int rc = check_feature_desc(d);
   if (rc) return rc;
-  if (!io || !io->x.ptr || !io->w1 || !io->w1t || !io->dphi.ptr || !io->dx.ptr)
+  if (!io || !io->x.ptr || !io->w1 || !io->dphi.ptr || !io->dx.ptr)
     return fail(TS_ERR_VALUE, "feature bwd: missing tensors");
-  if (io->dresid.ptr && !io->w2t) return fail(TS_ERR_VALUE, "feature bwd: dresid needs w2t");
+  if (io->dresid.ptr && !io->w2t && !io->w2) return fail(TS_ERR_VALUE, "feature bwd: dresid needs w2 or w2t");
   if (d->has_tau && !io->tau) return fail(TS_ERR_VALUE, "feature bwd: missing tau");
   if ((d->in_rot && (!io->in_cos || !io->in_sin)) || (d->feat_rot && (!io->f_cos || !io->f_sin)))
     return fail(TS_ERR_VALUE, "feature bwd: missing rope tables");
@@ -751,8 +764,10 @@ int ts_feature_bwd(const ts_feature_desc* d, const ts_feature_bwd_io* io, hipStr
     return fail(TS_ERR_VALUE, "feature bwd: fused weight gradients with dresid need dw2_part");
   if (want_wgrad && d->has_tau && !io->dtau_part)
     return fail(TS_ERR_VALUE, "feature bwd: fused weight gradients with tau need dtau_part");
+  if (!kernel_wl(es, d->d, d->m, false, P.wgrad) && (!io->w1t || (io->dresid.ptr && !io->w2t)))
+    return fail(TS_ERR_VALUE, "feature bwd: weights too large for LDS need w1t (and w2t)");
   if (d->T == 0) return TS_OK;
-  p.w1 = io->w1; p.w1t = io->w1t; p.w2t = io->w2t; p.tau = io->tau;
+  p.w1 = io->w1; p.w1t = io->w1t; p.w2t = io->w2t; p.w2 = io->w2; p.tau = io->tau;
   p.in_cos = io->in_cos; p.in_sin = io->in_sin; p.f_cos = io->f_cos; p.f_sin = io->f_sin;
   if (want_wgrad) {
     p.dw1_part = io->dw1_part; p.dw2_part = io->dw2_part; p.dtau_part = io->dtau_part;

@@ -232,4 +232,14 @@ __device__ __forceinline__ void stage_matrix(const E* src, int rows, int cols, E
   }
 }
 
+// Copy a [rows x cols] row-major global matrix transposed into LDS: row c of
+// the destination (pitch `pitch`) is column c of the source.
+template <typename E>
+__device__ __forceinline__ void stage_transposed(const E* src, int rows, int cols, E* dst, int pitch, int tid) {
+  for (int idx = tid; idx < rows * cols; idx += 256) {
+    const int r = idx / cols, c = idx - r * cols;
+    dst[c * pitch + r] = src[idx];
+  }
+}
+
 }  // namespace ts

@@ -6,7 +6,7 @@ between the two unchanged (including the 40-byte expansion fingerprint and
 its strict-load check).  ``forward`` (block.py:573-724) runs in one of two
 ways, both on the GPU:
 
-* the fused hot path (``fused.kernel_memory``) for a depth-1 kernel memory
+* the fused hot path (``fused.kernel_mixer``) for a depth-1 kernel memory
   with a ReLU^2-ridge or fixed-gain softmax-partition map, raw values, plain
   or key-mass read and the plain temporal sum: three HIP kernels (write,
   scan, read) between the two projection GEMMs;
@@ -24,7 +24,6 @@ import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
 from ..ops import engine, fused, maps
-from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
 from .norms import l2norm
@@ -387,10 +386,9 @@ class ThetaScan(nn.Module):
         spec = self._feature_spec()
         (W1, W2, _), = self._weights()
         gate = self.ogate is not None
-        proj = fused.in_projection(x, self.proj_qkv.weight, self.ogate.g.lin.weight if gate else None)
-        y = fused.kernel_memory(proj, W1, W2, self.kernel_relu2_threshold, spec, cfg.read_norm, H, gate,
-                                gate_bias=self.ogate.g.lin.bias if gate else None)
-        return linear(y, self.proj_out.weight)
+        return fused.kernel_mixer(x, self.proj_qkv.weight, self.ogate.g.lin.weight if gate else None,
+                                  self.ogate.g.lin.bias if gate else None, W1, W2, self.kernel_relu2_threshold,
+                                  self.proj_out.weight, spec, cfg.read_norm, H)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         cfg = self.cfg

@@ -7,7 +7,7 @@ through ``interface.scan_views`` / ``scan_views_mass`` (the HIP chunked scan),
 and key masses through the HIP decayed prefix sum.  Depth-1 ReLU^2 GN writes
 and reads run in the HIP GN kernels (``gn.write``, ``gn.read_stage``,
 ``gn.normalized_read``); the depth-1 kernel-memory hot path bypasses this
-module entirely (see ``fused.kernel_memory``).
+module entirely (see ``fused.kernel_mixer``).
 """
 from __future__ import annotations
 

@@ -316,8 +316,110 @@ def in_projection(x, w_qkv, w_g=None):
     return _InProjection.apply(x, w_qkv, w_g)
 
 
+class _State:
+    """What the kernel-memory backward needs from its forward."""
+
+    __slots__ = ("spec", "normalize", "seg_chunks", "heads", "d", "has_gate", "has_tau", "tau_dtype", "w_dtypes",
+                 "b_dtype", "ws", "proj", "w1c", "w2c", "tauf", "gb", "phi_q", "phi_k", "num", "mass", "resid")
+
+
+def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int,
+                    heads: int, has_gate: bool):
+    """Forward of the depth-1 kernel memory; fills ``st`` for the backward."""
+    B, T, P = proj.shape
+    H = heads
+    d = P // (4 * H) if has_gate else P // (3 * H)
+    qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
+    q = qkv[:, :, 0].transpose(1, 2)
+    k = qkv[:, :, 1].transpose(1, 2)
+    v = qkv[:, :, 2].transpose(1, 2)
+    dt = proj.dtype
+    w1c = w1.to(dt).contiguous()
+    w2c = w2.to(dt).contiguous()
+    tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    phi_k, _ = feature_fwd(spec, k, w1c, None, tauf, False)
+    phi_q, resid = feature_fwd(spec, q, w1c, w2c, tauf, True)
+    # The dq scan's segment states are the transpose of this scan's
+    # (sum_i v_i phi_k_i^T; with the mass column its key-side row is this
+    # scan's value-side sum_i phi_k_i), so the forward keeps them.
+    ws = None
+    if phi_k.shape[-1] == d:
+        ws = scan_hip.workspace_for(phi_q, phi_k, v, seg_chunks=seg_chunks, v_ext=normalize)
+    num, mass, _ = scan_hip.scan_launch(
+        phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
+        seg_chunks=seg_chunks, workspace=ws,
+    )
+    gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
+    gb = None if b_g is None else b_g.detach().to(torch.float32).contiguous()
+    y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
+    read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=gb)
+    st.spec, st.normalize, st.seg_chunks, st.heads, st.d, st.has_gate = spec, normalize, seg_chunks, H, d, has_gate
+    st.has_tau, st.tau_dtype = tau is not None, None if tau is None else tau.dtype
+    st.w_dtypes, st.b_dtype = (w1.dtype, w2.dtype), None if b_g is None else b_g.dtype
+    st.ws, st.proj, st.w1c, st.w2c, st.tauf, st.gb = ws, proj, w1c, w2c, tauf, gb
+    st.phi_q, st.phi_k, st.num, st.mass, st.resid = phi_q, phi_k, num, mass, resid
+    return y.view(B, T, H * d)
+
+
+def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: bool, need_b: bool):
+    """Backward of :func:`_memory_forward` -> (dproj, dW1, dW2, dtau, db_g)."""
+    spec, proj = st.spec, st.proj
+    B, T, P = proj.shape
+    H, d = st.heads, st.d
+    dt = proj.dtype
+    num, mass, resid, phi_q, phi_k = st.num, st.mass, st.resid, st.phi_q, st.phi_k
+    qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
+    q = qkv[:, :, 0].transpose(1, 2)
+    k = qkv[:, :, 1].transpose(1, 2)
+    v = qkv[:, :, 2].transpose(1, 2)
+    dproj = torch.empty_like(proj)
+    dqkv = dproj[..., :3 * H * d].view(B, T, 3, H, d)
+    dq = dqkv[:, :, 0].transpose(1, 2)
+    dk = dqkv[:, :, 1].transpose(1, 2)
+    dv = dqkv[:, :, 2].transpose(1, 2)
+    gv = dgv = None
+    if st.has_gate:
+        gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
+        dgv = dproj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
+    dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
+    dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv,
+                                           gbias=st.gb)
+    norm = st.normalize
+    q_ext = dmass if norm else None
+    ws_f, st.ws = st.ws, None
+    # dq = scan(dnum, v, phi_k): its segment states are the forward's, transposed
+    dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
+                                        seg_chunks=st.seg_chunks, workspace=ws_f,
+                                        states_in=2 if ws_f is not None else 0)
+    # dk = reverse scan(v, dnum, phi_q) and dv = reverse scan(phi_k, phi_q, dnum) share
+    # their segment states up to a transpose (sum_i dnum_i phi_q_i^T)
+    ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=st.seg_chunks, reverse=True, kx=norm) \
+        if ws_f is not None else None
+    dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
+                                        k_ext=q_ext, seg_chunks=st.seg_chunks, workspace=ws_r)
+    scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=st.seg_chunks,
+                         workspace=ws_r, states_in=2 if ws_r is not None else 0)
+    need_tau = st.has_tau and need_tau
+    db_g = None
+    if st.gb is not None and need_b:
+        db_g = column_sum(dproj.view(-1, P)[:, 3 * H * d:], st.b_dtype)
+    want_k = need_w1 or need_tau
+    want_q = need_w1 or need_w2 or need_tau
+    dw1_k, _, dtau_k = feature_bwd(spec, k, st.w1c, st.tauf, dphi_k, None, dk, want_weights=want_k)
+    dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, st.w1c, st.tauf, dphi_q, dresid, dq, w2=st.w2c,
+                                       want_weights=want_q)
+    dw1 = dw2 = dtau = None
+    if need_w1:
+        dw1 = sum_grads(dw1_k, dw1_q, st.w_dtypes[0], st.w1c.shape)
+    if need_w2:
+        dw2 = sum_grads(dw2_q, None, st.w_dtypes[1], st.w2c.shape)
+    if need_tau:
+        dtau = sum_grads(dtau_k, dtau_q, st.tau_dtype, (H,))
+    return dproj, dw1, dw2, dtau, db_g
+
+
 class _KernelMemory(torch.autograd.Function):
-    """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g) for a depth-1 kernel memory.
+    """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g + b_g) for a depth-1 kernel memory.
 
     ``proj`` is the [B,T,3*H*d (+H*d)] input projection: q, k, v heads, then
     the output-gate logits when ``has_gate``.  The gradient of ``proj`` is one
@@ -327,100 +429,64 @@ class _KernelMemory(torch.autograd.Function):
     @staticmethod
     def forward(ctx, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int, heads: int,
                 has_gate: bool):
-        B, T, P = proj.shape
-        H = heads
-        d = P // (4 * H) if has_gate else P // (3 * H)
-        qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
-        q = qkv[:, :, 0].transpose(1, 2)
-        k = qkv[:, :, 1].transpose(1, 2)
-        v = qkv[:, :, 2].transpose(1, 2)
-        dt = proj.dtype
-        w1c = w1.to(dt).contiguous()
-        w2c = w2.to(dt).contiguous()
-        tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
-        phi_k, _ = feature_fwd(spec, k, w1c, None, tauf, False)
-        phi_q, resid = feature_fwd(spec, q, w1c, w2c, tauf, True)
-        # The dq scan's segment states are the transpose of this scan's
-        # (sum_i v_i phi_k_i^T; with the mass column its key-side row is this
-        # scan's value-side sum_i phi_k_i), so the forward keeps them.
-        share = phi_k.shape[-1] == d
-        ws = None
-        if share:
-            ws = scan_hip.workspace_for(phi_q, phi_k, v, seg_chunks=seg_chunks, v_ext=normalize)
-        num, mass, _ = scan_hip.scan_launch(
-            phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
-            seg_chunks=seg_chunks, workspace=ws,
-        )
-        gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
-        gb = None if b_g is None else b_g.detach().to(torch.float32).contiguous()
-        y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
-        read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=gb)
-        ctx.spec, ctx.normalize, ctx.seg_chunks = spec, normalize, seg_chunks
-        ctx.heads, ctx.d, ctx.has_gate = H, d, has_gate
-        ctx.has_tau = tau is not None
-        ctx.tau_dtype = None if tau is None else tau.dtype
-        ctx.w_dtypes = (w1.dtype, w2.dtype)
-        ctx.b_dtype = None if b_g is None else b_g.dtype
-        ctx.ws = ws
-        ctx.save_for_backward(proj, w1c, w2c, tauf, gb, phi_q, phi_k, num, mass, resid)
-        return y.view(B, T, H * d)
+        ctx.st = _State()
+        return _memory_forward(ctx.st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
 
     @staticmethod
     def backward(ctx, dy):
-        proj, w1c, w2c, tauf, gb, phi_q, phi_k, num, mass, resid = ctx.saved_tensors
-        spec = ctx.spec
-        B, T, P = proj.shape
-        H, d = ctx.heads, ctx.d
-        dt = proj.dtype
-        qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
-        q = qkv[:, :, 0].transpose(1, 2)
-        k = qkv[:, :, 1].transpose(1, 2)
-        v = qkv[:, :, 2].transpose(1, 2)
-        dproj = torch.empty_like(proj)
-        dqkv = dproj[..., :3 * H * d].view(B, T, 3, H, d)
-        dq = dqkv[:, :, 0].transpose(1, 2)
-        dk = dqkv[:, :, 1].transpose(1, 2)
-        dv = dqkv[:, :, 2].transpose(1, 2)
-        gv = dgv = None
-        if ctx.has_gate:
-            gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
-            dgv = dproj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
-        dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
-        dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv,
-                                               gbias=gb)
-        norm = ctx.normalize
-        q_ext = dmass if norm else None
-        ws_f, ctx.ws = ctx.ws, None
-        # dq = scan(dnum, v, phi_k): its segment states are the forward's, transposed
-        dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
-                                            seg_chunks=ctx.seg_chunks, workspace=ws_f,
-                                            states_in=2 if ws_f is not None else 0)
-        # dk = reverse scan(v, dnum, phi_q) and dv = reverse scan(phi_k, phi_q, dnum) share
-        # their segment states up to a transpose (sum_i dnum_i phi_q_i^T)
-        ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=ctx.seg_chunks, reverse=True, kx=norm) \
-            if ws_f is not None else None
-        dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
-                                            k_ext=q_ext, seg_chunks=ctx.seg_chunks, workspace=ws_r)
-        scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=ctx.seg_chunks,
-                             workspace=ws_r, states_in=2 if ws_r is not None else 0)
-        need_w1 = ctx.needs_input_grad[1]
-        need_w2 = ctx.needs_input_grad[2]
-        need_tau = ctx.has_tau and ctx.needs_input_grad[3]
-        db_g = None
-        if gb is not None and ctx.needs_input_grad[4]:
-            db_g = column_sum(dproj.view(-1, P)[:, 3 * H * d:], ctx.b_dtype)
-        want_k = need_w1 or need_tau
-        want_q = need_w1 or need_w2 or need_tau
-        dw1_k, _, dtau_k = feature_bwd(spec, k, w1c, tauf, dphi_k, None, dk, want_weights=want_k)
-        dw1_q, dw2_q, dtau_q = feature_bwd(spec, q, w1c, tauf, dphi_q, dresid, dq, w2=w2c, want_weights=want_q)
-        dw1 = dw2 = dtau = None
-        if need_w1:
-            dw1 = sum_grads(dw1_k, dw1_q, ctx.w_dtypes[0], w1c.shape)
-        if need_w2:
-            dw2 = sum_grads(dw2_q, None, ctx.w_dtypes[1], w2c.shape)
-        if need_tau:
-            dtau = sum_grads(dtau_k, dtau_q, ctx.tau_dtype, (H,))
+        n = ctx.needs_input_grad
+        dproj, dw1, dw2, dtau, db_g = _memory_backward(ctx.st, dy, n[1], n[2], n[3], n[4])
         return dproj, dw1, dw2, dtau, db_g, None, None, None, None, None
+
+
+class _KernelMixer(torch.autograd.Function):
+    """The whole depth-1 kernel-memory mixer as one autograd node: the stacked
+    qkv / gate projection GEMM, the kernel memory and the output projection
+    (block.py:593-599, 721-724 around engine.py's read); backward in the same
+    node (split-K weight-gradient GEMMs)."""
+
+    @staticmethod
+    def forward(ctx, x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec: FeatureSpec, normalize: bool, seg_chunks: int,
+                heads: int):
+        has_gate = w_g is not None
+        weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
+        proj = torch.nn.functional.linear(x, weight)
+        ctx.st = _State()
+        y = _memory_forward(ctx.st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
+        ctx.save_for_backward(x, weight, y, w_out)
+        ctx.n_qkv = w_qkv.shape[0]
+        ctx.dtypes = (w_qkv.dtype, None if w_g is None else w_g.dtype, w_out.dtype)
+        return torch.nn.functional.linear(y, w_out)
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, weight, y, w_out = ctx.saved_tensors
+        n = ctx.needs_input_grad
+        d2 = dout.reshape(-1, w_out.shape[0])
+        dw_out = weight_grad(d2, y.reshape(-1, y.shape[-1]), ctx.dtypes[2]) if n[7] else None
+        dy = (d2 @ w_out).view(y.shape)
+        dproj, dw1, dw2, dtau, db_g = _memory_backward(ctx.st, dy, n[4], n[5], n[6], n[3])
+        P = weight.shape[0]
+        dp2 = dproj.view(-1, P)
+        dx = (dp2 @ weight).view(x.shape) if n[0] else None
+        dw_qkv = dw_g = None
+        if n[1] or n[2]:
+            same = ctx.dtypes[1] is None or ctx.dtypes[0] == ctx.dtypes[1]
+            dw = weight_grad(dp2, x.reshape(-1, x.shape[-1]), ctx.dtypes[0] if same else torch.float32)
+            dw_qkv = dw[:ctx.n_qkv].to(ctx.dtypes[0])
+            if ctx.dtypes[1] is not None:
+                dw_g = dw[ctx.n_qkv:].to(ctx.dtypes[1])
+        return dx, dw_qkv, dw_g, db_g, dw1, dw2, dtau, dw_out, None, None, None, None
+
+
+def kernel_mixer(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec: FeatureSpec, normalize: bool, heads: int,
+                 seg_chunks: int = 0):
+    """out = proj_out(kernel_memory(x [W_qkv; W_g]^T)) for the depth-1 kernel memory, one autograd node."""
+    if not x.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    if not x.is_contiguous():
+        x = x.contiguous()
+    return _KernelMixer.apply(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec, normalize, seg_chunks, heads)
 
 
 def kernel_memory(proj, w1, w2, tau, spec: FeatureSpec, normalize: bool, heads: int, has_gate: bool,

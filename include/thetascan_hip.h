@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 2
+#define TS_ABI_VERSION 3
 
 enum ts_status {
   TS_OK = 0,
@@ -435,6 +435,69 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
  * output-gate projection (gates.py:34-40, summed over every token). */
 int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_t row_stride, float* parts,
                 int32_t slices, hipStream_t stream);
+
+/* ------------------------------------------------ depth-1 kernel memory */
+
+/* Everything between the input and the output projection of a depth-1
+ * kernel-memory mixer, forward and backward, each as one call (the host
+ * submits one call instead of four to eight):
+ *   phi_k = feature(k);  phi_q, resid = feature(q)          ts_feature_fwd x2
+ *   num [, mass] = scan(phi_q, phi_k, v [, ones])            ts_scan_fwd
+ *   y = (resid + s num / (mass + eps)) * silu(g + g_bias)    ts_read_fwd
+ * and the backward ts_read_bwd -> three scans -> ts_feature_bwd x2 -> slot
+ * sums (weight gradients of W1, W2, tau and the gate bias).  Replaces
+ * block.py:593-724 between proj_qkv and proj_out (block.py:598-599 q/k/v
+ * split, gates.py:34-40 the gate) and engine.py:260-544 for a depth-1
+ * kernel memory with a plain temporal sum.  Shapes whose feature backward has
+ * no fused weight-gradient kernel, or whose weights are too wide to stage
+ * in LDS, are reported as TS_ERR_NOT_IMPLEMENTED by ts_memory_bytes. */
+typedef struct ts_memory_desc {
+  ts_feature_desc feat;  /* B, H, T, head width d, feature width m, dtype, map */
+  int32_t normalize;     /* key-mass read (the scan's value-side ones column)  */
+  int32_t gate;          /* output gate g                                       */
+  int32_t has_g_bias;    /* gate bias (gate only)                               */
+  int32_t seg_chunks;    /* scan segments (0 = auto)                            */
+  int32_t param_dtype;   /* ts_dtype of tau and g_bias as given, and of the
+                            weight gradients written by ts_memory_bwd          */
+} ts_memory_desc;
+
+typedef struct ts_memory_io {
+  ts_strided q, k, v, g;  /* [B,H,T,d] views of the input projection (desc dtype;
+                             g NULL without gate)                              */
+  const void* w1;         /* [H,m,d] effective W1 (desc dtype)                 */
+  const void* w2;         /* [H,d,m] effective W2 (desc dtype)                 */
+  const void* tau;        /* [H] threshold (param dtype; feat.has_tau)         */
+  const void* g_bias;     /* [H*d] gate bias (param dtype; has_g_bias)         */
+  const float* in_cos;    /* rope tables as for ts_feature_fwd                 */
+  const float* in_sin;
+  const float* f_cos;
+  const float* f_sin;
+} ts_memory_io;
+
+/* Bytes of the `saved` buffer (written by the forward, read by the
+ * backward: features, residual, numerator, mass, fp32 parameters and the
+ * forward scan's segment states) and of the backward's `scratch` buffer. */
+int ts_memory_bytes(const ts_memory_desc* desc, size_t* saved_bytes, size_t* scratch_bytes);
+
+/* Forward: y [B,H,T,d] view (e.g. of [B,T,H*d]). */
+int ts_memory_fwd(const ts_memory_desc* desc, const ts_memory_io* io, ts_strided y, void* saved,
+                  size_t saved_bytes, hipStream_t stream);
+
+typedef struct ts_memory_grads {
+  ts_strided dy;          /* [B,H,T,d] grad of y                               */
+  ts_strided dq, dk, dv;  /* out [B,H,T,d] views of the projection's gradient  */
+  ts_strided dg;          /* out [B,H,T,d] (gate)                              */
+  void* dw1;              /* out [H,m,d] param dtype, or NULL                  */
+  void* dw2;              /* out [H,d,m] param dtype, or NULL                  */
+  void* dtau;             /* out [H] param dtype, or NULL                      */
+  void* dg_bias;          /* out [H*d] param dtype, or NULL; needs dg rows of
+                             one [B*T, H*d] matrix (row stride dg.st)          */
+} ts_memory_grads;
+
+/* Backward of ts_memory_fwd with the same desc, io and saved buffer. */
+int ts_memory_bwd(const ts_memory_desc* desc, const ts_memory_io* io, const ts_memory_grads* grads,
+                  const void* saved, size_t saved_bytes, void* scratch, size_t scratch_bytes,
+                  hipStream_t stream);
 
 #ifdef __cplusplus
 }

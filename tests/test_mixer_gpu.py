@@ -156,3 +156,43 @@ def test_cpu_input_raises_instead_of_falling_back(cuda):
     module = ts.ThetaScan(ts.ThetaScanConfig(d_model=64, n_heads=2, family="kernel"))
     with pytest.raises(RuntimeError, match="GPU"):
         module(torch.randn(1, 8, 64))
+
+
+@pytest.mark.parametrize("variant", [("feature", "none"), ("input", "key_mass")])
+@pytest.mark.parametrize("feature_map", ["relu2_ridge", "softmax_partition"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_one_call_memory_matches_per_entry_calls(cuda, variant, feature_map, dtype, monkeypatch):
+    """ts_memory_fwd / ts_memory_bwd run the same kernels as the per-entry-point
+    calls (used while launches are recorded): outputs and every gradient are
+    bit-identical, and the one-call path is the one a plain step takes."""
+    from thetascan_amd import _lib
+    from thetascan_amd._core.ops import fused
+
+    placement, normalization = variant
+    pub = _headline_config(placement, normalization, feature_map, d_model=256, heads=4)
+    module = build_module(pub, cuda, dtype)
+    _seeded(module, 5)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 300, 256, generator=g).to(cuda, dtype)
+    dy = torch.randn(2, 300, 256, generator=g).to(cuda, dtype)
+    native = []
+    real = fused._native_forward
+    monkeypatch.setattr(fused, "_native_forward", lambda *a, **k: (native.append(1), real(*a, **k))[1])
+    results = []
+    for per_entry in (False, True):
+        module.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        if per_entry:
+            with _lib.record_launches():
+                y = module(xi)
+                y.backward(dy)
+                torch.cuda.synchronize()
+        else:
+            y = module(xi)
+            y.backward(dy)
+        assert module._core.last_path == "fused"
+        results.append([y.detach(), xi.grad] + [p.grad for p in module.parameters() if p.grad is not None])
+    assert native == [1], "the plain step must take the one-call path"
+    assert len(results[0]) == len(results[1])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)

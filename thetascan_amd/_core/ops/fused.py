@@ -320,7 +320,48 @@ class _State:
     """What the kernel-memory backward needs from its forward."""
 
     __slots__ = ("spec", "normalize", "seg_chunks", "heads", "d", "has_gate", "has_tau", "tau_dtype", "w_dtypes",
-                 "b_dtype", "ws", "proj", "w1c", "w2c", "tauf", "gb", "phi_q", "phi_k", "num", "mass", "resid")
+                 "b_dtype", "ws", "proj", "w1c", "w2c", "tauf", "gb", "phi_q", "phi_k", "num", "mass", "resid",
+                 "native", "io", "saved", "tau", "b_g")
+
+
+_MEMORY: dict = {}
+
+
+def _memory_plan(spec: FeatureSpec, B, H, T, d, dtype, tau, b_g, w1, w2, normalize, has_gate, seg_chunks):
+    """(desc, saved bytes, scratch bytes) of the one-call kernel memory
+    (ts_memory_fwd / ts_memory_bwd), or None where it does not apply."""
+    pdt = w1.dtype
+    if pdt not in (torch.bfloat16, torch.float32) or w2.dtype != pdt:
+        return None
+    if tau is not None and (tau.dtype != pdt or tau.numel() != H or not tau.is_contiguous()):
+        return None
+    if b_g is not None and (b_g.dtype != pdt or b_g.numel() != H * d or not b_g.is_contiguous()):
+        return None
+    key = (B, H, T, d, spec.m, dtype, spec.kind, spec.in_rot, spec.feat_rot, spec.gain, spec.resid_scale, spec.eps,
+           tau is not None, b_g is not None, bool(normalize), bool(has_gate), int(seg_chunks), pdt)
+    hit = _MEMORY.get(key)
+    if hit is None:
+        lib = _lib.load()
+        feat = _lib.FeatureDesc(B, H, T, d, spec.m, _lib.dtype_code(dtype), spec.kind, spec.in_rot, spec.feat_rot,
+                                int(tau is not None), float(spec.gain), float(spec.resid_scale), float(spec.eps))
+        desc = _lib.MemoryDesc(feat, int(normalize), int(has_gate), int(b_g is not None), int(seg_chunks),
+                               _lib.dtype_code(pdt))
+        sb, cb = ctypes.c_size_t(), ctypes.c_size_t()
+        status = lib.ts_memory_bytes(ctypes.byref(desc), ctypes.byref(sb), ctypes.byref(cb))
+        if status == _lib.TS_ERR_NOT_IMPLEMENTED:
+            hit = False
+        else:
+            _lib.check(status, "ts_memory_bytes")
+            hit = (desc, sb.value, cb.value)
+        if len(_MEMORY) > 64:
+            _MEMORY.clear()
+        _MEMORY[key] = hit
+    return hit or None
+
+
+def _proj_view(base: int, es: int, col: int, T: int, P: int, d: int) -> _lib.Strided:
+    """[B,H,T,d] view at column ``col`` of a [B,T,P] buffer at address ``base``."""
+    return _lib.Strided(base + col * es, T * P, d, P)
 
 
 def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int,
@@ -329,6 +370,14 @@ def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, norma
     B, T, P = proj.shape
     H = heads
     d = P // (4 * H) if has_gate else P // (3 * H)
+    st.spec, st.normalize, st.seg_chunks, st.heads, st.d, st.has_gate = spec, normalize, seg_chunks, H, d, has_gate
+    st.has_tau, st.tau_dtype = tau is not None, None if tau is None else tau.dtype
+    st.w_dtypes, st.b_dtype = (w1.dtype, w2.dtype), None if b_g is None else b_g.dtype
+    st.native = None
+    if not _lib.recording() and proj.is_contiguous():
+        plan = _memory_plan(spec, B, H, T, d, proj.dtype, tau, b_g, w1, w2, normalize, has_gate, seg_chunks)
+        if plan is not None:
+            return _native_forward(st, plan, proj, w1, w2, tau, b_g, spec, H, d, has_gate)
     qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
     q = qkv[:, :, 0].transpose(1, 2)
     k = qkv[:, :, 1].transpose(1, 2)
@@ -353,16 +402,78 @@ def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, norma
     gb = None if b_g is None else b_g.detach().to(torch.float32).contiguous()
     y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
     read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=gb)
-    st.spec, st.normalize, st.seg_chunks, st.heads, st.d, st.has_gate = spec, normalize, seg_chunks, H, d, has_gate
-    st.has_tau, st.tau_dtype = tau is not None, None if tau is None else tau.dtype
-    st.w_dtypes, st.b_dtype = (w1.dtype, w2.dtype), None if b_g is None else b_g.dtype
     st.ws, st.proj, st.w1c, st.w2c, st.tauf, st.gb = ws, proj, w1c, w2c, tauf, gb
     st.phi_q, st.phi_k, st.num, st.mass, st.resid = phi_q, phi_k, num, mass, resid
     return y.view(B, T, H * d)
 
 
+def _native_forward(st: _State, plan, proj, w1, w2, tau, b_g, spec: FeatureSpec, H: int, d: int, has_gate: bool):
+    """The forward as one ts_memory_fwd call; intermediates stay in one
+    ``saved`` buffer that only the library reads."""
+    desc, saved_bytes, _ = plan
+    B, T, P = proj.shape
+    dt = proj.dtype
+    dev = proj.device
+    lib = _lib.load()
+    w1c = w1.detach().to(dt).contiguous()
+    w2c = w2.detach().to(dt).contiguous()
+    tau_ = None if tau is None else tau.detach()
+    bg_ = None if b_g is None else b_g.detach()
+    ic, is_, fc, fs = spec.tables(T, dev)
+    base, es, Hd = proj.data_ptr(), proj.element_size(), H * d
+    io = _lib.MemoryIO(_proj_view(base, es, 0, T, P, d), _proj_view(base, es, Hd, T, P, d),
+                       _proj_view(base, es, 2 * Hd, T, P, d),
+                       _proj_view(base, es, 3 * Hd, T, P, d) if has_gate else _lib.Strided(None, 0, 0, 0),
+                       w1c.data_ptr(), w2c.data_ptr(), _lib.ptr(tau_), _lib.ptr(bg_), _lib.ptr(ic), _lib.ptr(is_),
+                       _lib.ptr(fc), _lib.ptr(fs))
+    saved = torch.empty(saved_bytes, dtype=torch.uint8, device=dev)
+    y = torch.empty(B, T, Hd, dtype=dt, device=dev)
+    status = lib.ts_memory_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.Strided(y.data_ptr(), T * Hd, d, Hd),
+                               saved.data_ptr(), saved_bytes, _lib.stream_handle(dev))
+    _lib.check(status, "ts_memory_fwd")
+    # the io holds raw addresses: keep every tensor it names alive
+    st.native, st.io, st.saved = plan, io, saved
+    st.proj, st.w1c, st.w2c, st.tau, st.b_g = proj, w1c, w2c, tau_, bg_
+    return y
+
+
+def _native_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: bool, need_b: bool):
+    desc, saved_bytes, scratch_bytes = st.native
+    proj = st.proj
+    B, T, P = proj.shape
+    H, d = st.heads, st.d
+    Hd = H * d
+    dev = proj.device
+    lib = _lib.load()
+    dy = dy.to(proj.dtype)
+    if not dy.is_contiguous():
+        dy = dy.contiguous()
+    dproj = torch.empty_like(proj)
+    scratch = torch.empty(scratch_bytes, dtype=torch.uint8, device=dev)
+    pdt = st.w_dtypes[0]
+    dw1 = torch.empty(st.w1c.shape, dtype=pdt, device=dev) if need_w1 else None
+    dw2 = torch.empty(st.w2c.shape, dtype=pdt, device=dev) if need_w2 else None
+    dtau = torch.empty(H, dtype=pdt, device=dev) if (need_tau and st.has_tau) else None
+    db = torch.empty(Hd, dtype=pdt, device=dev) if (need_b and st.b_dtype is not None) else None
+    base, es = dproj.data_ptr(), dproj.element_size()
+    grads = _lib.MemoryGrads(_lib.Strided(dy.data_ptr(), T * Hd, d, Hd), _proj_view(base, es, 0, T, P, d),
+                             _proj_view(base, es, Hd, T, P, d), _proj_view(base, es, 2 * Hd, T, P, d),
+                             _proj_view(base, es, 3 * Hd, T, P, d) if st.has_gate else _lib.Strided(None, 0, 0, 0),
+                             _lib.ptr(dw1), _lib.ptr(dw2), _lib.ptr(dtau), _lib.ptr(db))
+    status = lib.ts_memory_bwd(ctypes.byref(desc), ctypes.byref(st.io), ctypes.byref(grads), st.saved.data_ptr(),
+                               saved_bytes, scratch.data_ptr(), scratch_bytes, _lib.stream_handle(dev))
+    _lib.check(status, "ts_memory_bwd")
+    if dtau is not None and st.tau is not None:
+        dtau = dtau.view(st.tau.shape)
+    if db is not None and st.b_g is not None:
+        db = db.view(st.b_g.shape)
+    return dproj, dw1, dw2, dtau, db
+
+
 def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: bool, need_b: bool):
     """Backward of :func:`_memory_forward` -> (dproj, dW1, dW2, dtau, db_g)."""
+    if st.native is not None:
+        return _native_backward(st, dy, need_w1, need_w2, need_tau, need_b)
     spec, proj = st.spec, st.proj
     B, T, P = proj.shape
     H, d = st.heads, st.d

@@ -308,6 +308,48 @@ class BlendDesc(ctypes.Structure):
     ]
 
 
+class MemoryDesc(ctypes.Structure):
+    _fields_ = [
+        ("feat", FeatureDesc),
+        ("normalize", ctypes.c_int32),
+        ("gate", ctypes.c_int32),
+        ("has_g_bias", ctypes.c_int32),
+        ("seg_chunks", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+    ]
+
+
+class MemoryIO(ctypes.Structure):
+    _fields_ = [
+        ("q", Strided),
+        ("k", Strided),
+        ("v", Strided),
+        ("g", Strided),
+        ("w1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("g_bias", ctypes.c_void_p),
+        ("in_cos", ctypes.c_void_p),
+        ("in_sin", ctypes.c_void_p),
+        ("f_cos", ctypes.c_void_p),
+        ("f_sin", ctypes.c_void_p),
+    ]
+
+
+class MemoryGrads(ctypes.Structure):
+    _fields_ = [
+        ("dy", Strided),
+        ("dq", Strided),
+        ("dk", Strided),
+        ("dv", Strided),
+        ("dg", Strided),
+        ("dw1", ctypes.c_void_p),
+        ("dw2", ctypes.c_void_p),
+        ("dtau", ctypes.c_void_p),
+        ("dg_bias", ctypes.c_void_p),
+    ]
+
+
 FEAT_RELU2 = 0
 FEAT_SOFTMAX = 1
 
@@ -375,7 +417,12 @@ def load() -> ctypes.CDLL:
         lib.ts_gn_write_bwd.argtypes = [P(GnDesc), P(GnBwdIO), ctypes.c_void_p]
         lib.ts_gn_read_fwd.argtypes = [P(GnReadDesc), P(GnReadIO), ctypes.c_void_p]
         lib.ts_gn_read_bwd.argtypes = [P(GnReadDesc), P(GnReadBwdIO), ctypes.c_void_p]
-        if lib.ts_abi_version() != 2:
+        lib.ts_memory_bytes.argtypes = [P(MemoryDesc), P(ctypes.c_size_t), P(ctypes.c_size_t)]
+        lib.ts_memory_fwd.argtypes = [P(MemoryDesc), P(MemoryIO), Strided, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p]
+        lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        if lib.ts_abi_version() != 3:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

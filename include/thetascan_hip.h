@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 3
+#define TS_ABI_VERSION 4
 
 enum ts_status {
   TS_OK = 0,
@@ -243,9 +243,20 @@ typedef struct ts_read_bwd_io {
   ts_strided dresid;               /* out [B,H,T,d] (desc dtype; NULL ok)      */
   ts_strided dg;                   /* out [B,H,T,d] (gate)                     */
   const float* g_bias;             /* as in ts_read_io                         */
+  float* dg_bias_part;             /* out fp32 [P, H*d] per-workgroup sums of dg
+                                      over tokens (gate, d <= 256; NULL ok): the
+                                      gate-bias gradient is their sum over P,
+                                      P from ts_read_bwd_parts (ts_sum_slots)  */
 } ts_read_bwd_io;
 
+/* Backward of ts_read_fwd: dnum, dmass, dresid, dg and optionally the
+ * gate-bias gradient partials.  Replaces the autograd backward of the same
+ * chain (engine.py:440-442, 526-528; gates.py:34-40, with the bias gradient
+ * summed over every token). */
 int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t stream);
+
+/* Number P of gate-bias partial rows ts_read_bwd writes for `desc`. */
+int ts_read_bwd_parts(const ts_read_desc* desc, int32_t* parts);
 
 /* -------------------------------------------------------- GN write payloads */
 

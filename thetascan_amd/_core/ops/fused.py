@@ -25,7 +25,7 @@ import torch
 
 from ... import _lib
 from . import scan_hip
-from .linear import column_sum, split_k_outer, weight_grad
+from .linear import slot_sum, split_k_outer, weight_grad
 
 
 def _rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -219,9 +219,13 @@ def read_fwd(num, mass, resid, g, y, scale: float, eps: float = 1e-6, gbias=None
     return y
 
 
-def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None, gbias=None):
+def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None, gbias=None, gbias_grad=None):
     """Backward of :func:`read_fwd`; ``dg`` optionally names the [B,H,T,d]
-    view the gate gradient is written to."""
+    view the gate gradient is written to.  With ``gbias_grad`` (a dtype) the
+    gate-bias gradient [H*d] is also formed, from per-workgroup column sums
+    the kernel writes beside dg.
+
+    Returns ``(dnum, dmass, (dresid, dresid_head_major), dg, dgbias)``."""
     lib = _lib.load()
     B, H, T, d = num.shape
     dnum = torch.empty_like(num)
@@ -231,13 +235,19 @@ def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None, 
         dg = torch.empty(B, T, H, d, dtype=num.dtype, device=num.device).transpose(1, 2)
     desc = _lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None), int(g is not None),
                          float(scale), float(eps))
+    parts = None
+    if gbias_grad is not None and g is not None:
+        n = ctypes.c_int32()
+        _lib.check(lib.ts_read_bwd_parts(ctypes.byref(desc), ctypes.byref(n)), "ts_read_bwd_parts")
+        parts = torch.empty(n.value, H * d, dtype=torch.float32, device=num.device)
     io = _lib.ReadBwdIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
                         _lib.strided(dy), _lib.strided(dnum), _lib.strided(dmass), _lib.strided(dresid),
-                        _lib.strided(dg), _lib.ptr(gbias))
+                        _lib.strided(dg), _lib.ptr(gbias), _lib.ptr(parts))
     with _lib.timed("ts_read_bwd", lambda: _lib.nbytes(num, mass, resid, g, dy, dnum, dmass, dresid, dg)):
         status = lib.ts_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
     _lib.check(status, "ts_read_bwd")
-    return dnum, dmass, (dresid, dresid_hm), dg
+    dgbias = None if parts is None else slot_sum(parts, gbias_grad, (H * d,))
+    return dnum, dmass, (dresid, dresid_hm), dg, dgbias
 
 
 def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Tensor:
@@ -493,8 +503,9 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
         gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
         dgv = dproj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
     dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
-    dnum, dmass, (dresid, _), _ = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv,
-                                           gbias=st.gb)
+    want_gb = st.gb is not None and need_b
+    dnum, dmass, (dresid, _), _, db_g = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv,
+                                                 gbias=st.gb, gbias_grad=st.b_dtype if want_gb else None)
     norm = st.normalize
     q_ext = dmass if norm else None
     ws_f, st.ws = st.ws, None
@@ -511,9 +522,6 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
     scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=st.seg_chunks,
                          workspace=ws_r, states_in=2 if ws_r is not None else 0)
     need_tau = st.has_tau and need_tau
-    db_g = None
-    if st.gb is not None and need_b:
-        db_g = column_sum(dproj.view(-1, P)[:, 3 * H * d:], st.b_dtype)
     want_k = need_w1 or need_tau
     want_q = need_w1 or need_w2 or need_tau
     dw1_k, _, dtau_k = feature_bwd(spec, k, st.w1c, st.tauf, dphi_k, None, dk, want_weights=want_k)

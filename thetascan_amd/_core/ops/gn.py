@@ -256,7 +256,7 @@ class _NormalizedRead(torch.autograd.Function):
 
         nk, mk, rk = ctx.saved_tensors
         s, eps, resid_dtype, mass_dtype = ctx.meta
-        dnum, dmass, (dresid, _), _ = fused.read_bwd(nk, mk, rk, None, _rows(dy.to(nk.dtype)), s, eps)
+        dnum, dmass, (dresid, _), _, _ = fused.read_bwd(nk, mk, rk, None, _rows(dy.to(nk.dtype)), s, eps)
         if dmass is not None:
             dmass = dmass.to(mass_dtype)
         return dnum, dmass, dresid.to(resid_dtype), None, None

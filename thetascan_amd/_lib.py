@@ -172,6 +172,7 @@ class ReadBwdIO(ctypes.Structure):
         ("dresid", Strided),
         ("dg", Strided),
         ("g_bias", ctypes.c_void_p),
+        ("dg_bias_part", ctypes.c_void_p),
     ]
 
 
@@ -399,6 +400,7 @@ def load() -> ctypes.CDLL:
         lib.ts_feature_bwd_transposed.argtypes = [P(FeatureDesc), ctypes.c_int32, ctypes.c_int32, P(ctypes.c_int32)]
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
+        lib.ts_read_bwd_parts.argtypes = [P(ReadDesc), P(ctypes.c_int32)]
         lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
         lib.ts_col_sums.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
@@ -422,7 +424,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 3:
+        if lib.ts_abi_version() != 4:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

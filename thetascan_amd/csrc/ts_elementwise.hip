@@ -15,135 +15,195 @@ struct ReadP {
   const float* gbias;  // [H, d] added to the gate pre-activation (or null)
 };
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
-__device__ __forceinline__ float dsilu(float x) {
-  const float sg = 1.0f / (1.0f + expf(-x));
-  return sg * (1.0f + x * (1.0f - sg));
-}
+
+// Work mapping of the read kernels: block (x, y) covers rows
+// x * RPB .. x * RPB + RPB - 1 of the (b, h) = y slice.  A row (one token) is
+// CPR 16-byte chunks held by CPR consecutive lanes, so a pass of 256 threads
+// covers 256 / CPR consecutive rows of one head, a contiguous run of a
+// head-major [B, H, T, d] stream (measured faster than spreading a pass over
+// every head of a few tokens, which breaks head-major streams into short runs
+// half a MiB apart).  A thread makes RPT passes (its loads are all issued
+// before any arithmetic) and keeps the same chunk in each; a row reduction is
+// a log2(CPR)-step butterfly.  CPR is the row's chunk count rounded up to a
+// power of two; lanes past the row's last chunk only join the butterfly.
+constexpr int kReadRPT = 4;
+
+template <int CPR>
+__host__ __device__ constexpr int read_rows_per_block() { return kReadRPT * (256 / CPR); }
 
 template <typename E>
-__device__ __forceinline__ const E* rowp(const ts_strided& s, int b, int h, int t) {
-  return (const E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
-}
-template <typename E>
-__device__ __forceinline__ E* rowp_w(const ts_strided& s, int b, int h, int t) {
-  return (E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
+__device__ __forceinline__ const E* slice_of(const ts_strided& s, int b, int h) {
+  return (const E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh;
 }
 
-template <typename E>
-__device__ __forceinline__ void ld_vec(const E* p, float* out) {
+template <typename E, int N>
+__device__ __forceinline__ void unpack(const uint4& raw, float* out) {
   Vec16<E> v;
-  v.raw = *(const uint4*)p;
+  v.raw = raw;
 #pragma unroll
-  for (int e = 0; e < Vec16<E>::N; ++e) out[e] = tof(v.e[e]);
+  for (int e = 0; e < N; ++e) out[e] = tof(v.e[e]);
 }
-template <typename E>
-__device__ __forceinline__ void st_vec(E* p, const float* in) {
+template <typename E, int N>
+__device__ __forceinline__ uint4 pack(const float* in) {
   Vec16<E> v;
 #pragma unroll
-  for (int e = 0; e < Vec16<E>::N; ++e) v.e[e] = cvt<E>(in[e]);
-  *(uint4*)p = v.raw;
+  for (int e = 0; e < N; ++e) v.e[e] = cvt<E>(in[e]);
+  return v.raw;
 }
 
-// Work mapping of the read kernels: a row (one (b, h, t)) is split into
-// 16-byte chunks; `p2` consecutive lanes (a power of two >= chunks per row)
-// own one row, so every load and store instruction covers whole contiguous
-// row segments, and a row reduction is a log2(p2)-step butterfly.
-struct RowMap {
-  int64_t row;
-  int chunk;
-  bool active;
-};
-
-__device__ __forceinline__ RowMap row_map(int64_t nrows, int nchunk, int p2) {
-  const int64_t gtid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  RowMap r;
-  r.row = gtid / p2;
-  r.chunk = (int)(gtid % p2);
-  r.active = r.row < nrows && r.chunk < nchunk;
-  return r;
+// sigma(x) from the hardware exp2 and reciprocal (a relative error of a few
+// ulp of fp32, far below the bf16 rounding of the outputs)
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
-__device__ __forceinline__ float row_sum(float v, int p2) {
-  for (int o = 1; o < p2; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-// y = (resid + s * num / (mass + eps)) * silu(g)     (engine.py:440-442, 526-528; gates.py:34-40)
-template <typename E>
-__global__ __launch_bounds__(256) void read_fwd_kernel(ReadP p, int p2) {
+// y = (resid + s * num / (mass + eps)) * silu(g + g_bias)     (engine.py:440-442, 526-528; gates.py:34-40)
+template <typename E, int CPR>
+__global__ __launch_bounds__(256) void read_fwd_kernel(ReadP p) {
   constexpr int N = Vec16<E>::N;
-  const int64_t nrows = (int64_t)p.B * p.H * p.T;
-  const RowMap rm = row_map(nrows, p.d / N, p2);
-  if (!rm.active) return;
-  const int t = (int)(rm.row % p.T);
-  const int h = (int)((rm.row / p.T) % p.H);
-  const int b = (int)(rm.row / ((int64_t)p.T * p.H));
-  const int c = rm.chunk * N;
-  float scale = p.s;
-  if (p.normalize) scale = p.s / (rowp<float>(p.mass, b, h, t)[0] + p.eps);
-  float nv[N], rv[N], gv[N], out[N];
-  ld_vec<E>(rowp<E>(p.num, b, h, t) + c, nv);
-  if (p.resid.ptr) ld_vec<E>(rowp<E>(p.resid, b, h, t) + c, rv);
-  if (p.gate) {
-    ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
-    if (p.gbias)
+  constexpr int RP = 256 / CPR;  // rows per pass
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+  const int c = ((int)threadIdx.x % CPR) * N;
+  const bool colok = c < p.d;
+  const int r0 = blockIdx.x * read_rows_per_block<CPR>() + (int)threadIdx.x / CPR;
+  const E* num = slice_of<E>(p.num, b, h) + c;
+  const E* res = p.resid.ptr ? slice_of<E>(p.resid, b, h) + c : nullptr;
+  const E* gp = p.gate ? slice_of<E>(p.g, b, h) + c : nullptr;
+  const float* mass = p.normalize ? slice_of<float>(p.mass, b, h) : nullptr;
+  E* y = (E*)slice_of<E>(p.y, b, h) + c;
+  uint4 rn[kReadRPT], rr[kReadRPT], rg[kReadRPT];
+  float ms[kReadRPT];
 #pragma unroll
-      for (int e = 0; e < N; ++e) gv[e] += p.gbias[h * p.d + c + e];
-  }
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    const float v = (p.resid.ptr ? rv[e] : 0.0f) + scale * nv[e];
-    out[e] = p.gate ? v * silu(gv[e]) : v;
-  }
-  st_vec<E>(rowp_w<E>(p.y, b, h, t) + c, out);
-}
-
-template <typename E>
-__global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p, int p2) {
-  constexpr int N = Vec16<E>::N;
-  const int64_t nrows = (int64_t)p.B * p.H * p.T;
-  const RowMap rm = row_map(nrows, p.d / N, p2);
-  // inactive lanes still take part in the row butterfly with zeros
-  const int64_t row = rm.row < nrows ? rm.row : nrows - 1;
-  const int t = (int)(row % p.T);
-  const int h = (int)((row / p.T) % p.H);
-  const int b = (int)(row / ((int64_t)p.T * p.H));
-  const int c = rm.chunk * N;
-  float denom = 1.0f;
-  if (p.normalize) denom = rowp<float>(p.mass, b, h, t)[0] + p.eps;
-  const float scale = p.s / denom;
-  float dot = 0.0f;
-  if (rm.active) {
-    float nv[N], rv[N], gv[N], dv[N], o_dnum[N], o_dg[N], o_dres[N];
-    ld_vec<E>(rowp<E>(p.num, b, h, t) + c, nv);
-    ld_vec<E>(rowp<E>(p.dy, b, h, t) + c, dv);
-    if (p.resid.ptr) ld_vec<E>(rowp<E>(p.resid, b, h, t) + c, rv);
-    if (p.gate) {
-      ld_vec<E>(rowp<E>(p.g, b, h, t) + c, gv);
-      if (p.gbias)
-#pragma unroll
-        for (int e = 0; e < N; ++e) gv[e] += p.gbias[h * p.d + c + e];
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    if (t < p.T && colok) {
+      rn[i] = *(const uint4*)(num + (int64_t)t * p.num.st);
+      if (res) rr[i] = *(const uint4*)(res + (int64_t)t * p.resid.st);
+      if (gp) rg[i] = *(const uint4*)(gp + (int64_t)t * p.g.st);
+      if (mass) ms[i] = mass[(int64_t)t * p.mass.st];
     }
+  }
+  float gb[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) gb[e] = p.gbias && colok ? p.gbias[h * p.d + c + e] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    if (t >= p.T || !colok) continue;
+    const float scale = mass ? p.s * __builtin_amdgcn_rcpf(ms[i] + p.eps) : p.s;
+    float nv[N], rv[N], gv[N], out[N];
+    unpack<E, N>(rn[i], nv);
+    if (res) unpack<E, N>(rr[i], rv);
+    if (gp) unpack<E, N>(rg[i], gv);
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      float dpre = dv[e];
-      if (p.gate) {
-        const float ypre = (p.resid.ptr ? rv[e] : 0.0f) + scale * nv[e];
-        o_dg[e] = dv[e] * ypre * dsilu(gv[e]);
-        dpre = dv[e] * silu(gv[e]);
+      const float v = (res ? rv[e] : 0.0f) + scale * nv[e];
+      if (gp) {
+        const float x = gv[e] + gb[e];
+        out[e] = v * x * fast_sigmoid(x);
+      } else {
+        out[e] = v;
       }
-      o_dnum[e] = scale * dpre;
-      o_dres[e] = dpre;
-      dot += dpre * nv[e];
     }
-    st_vec<E>(rowp_w<E>(p.dnum, b, h, t) + c, o_dnum);
-    if (p.dresid.ptr) st_vec<E>(rowp_w<E>(p.dresid, b, h, t) + c, o_dres);
-    if (p.gate) st_vec<E>(rowp_w<E>(p.dg, b, h, t) + c, o_dg);
+    *(uint4*)(y + (int64_t)t * p.y.st) = pack<E, N>(out);
   }
-  if (p.normalize) {
-    dot = row_sum(dot, p2);
-    if (rm.active && rm.chunk == 0) rowp_w<float>(p.dmass, b, h, t)[0] = -p.s * dot / (denom * denom);
+}
+
+// Backward of read_fwd; with `dgb_part` also the per-block sums of dg over
+// tokens (the gate-bias gradient before the sum over blocks):
+// parts[b * gridDim.x + blockIdx.x][h * d + col].  Each thread sums its own
+// rows in registers, then each column adds the 256 / CPR row lanes in lane
+// order through LDS: the result is reproducible bit for bit.
+template <typename E, int CPR>
+__global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p, float* dgb_part) {
+  constexpr int N = Vec16<E>::N;
+  constexpr int RP = 256 / CPR;
+  __shared__ float red[256 * N];
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+  const int c = ((int)threadIdx.x % CPR) * N;
+  const bool colok = c < p.d;
+  const int r0 = blockIdx.x * read_rows_per_block<CPR>() + (int)threadIdx.x / CPR;
+  const E* num = slice_of<E>(p.num, b, h) + c;
+  const E* dyp = slice_of<E>(p.dy, b, h) + c;
+  const E* res = p.resid.ptr ? slice_of<E>(p.resid, b, h) + c : nullptr;
+  const E* gp = p.gate ? slice_of<E>(p.g, b, h) + c : nullptr;
+  const float* mass = p.normalize ? slice_of<float>(p.mass, b, h) : nullptr;
+  E* dnum = (E*)slice_of<E>(p.dnum, b, h) + c;
+  E* dres = p.dresid.ptr ? (E*)slice_of<E>(p.dresid, b, h) + c : nullptr;
+  E* dg = p.gate ? (E*)slice_of<E>(p.dg, b, h) + c : nullptr;
+  float* dmass = p.normalize ? (float*)slice_of<float>(p.dmass, b, h) : nullptr;
+  uint4 rn[kReadRPT], rd[kReadRPT], rr[kReadRPT], rg[kReadRPT];
+  float ms[kReadRPT];
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    if (t < p.T && mass) ms[i] = mass[(int64_t)t * p.mass.st];
+    if (t < p.T && colok) {
+      rn[i] = *(const uint4*)(num + (int64_t)t * p.num.st);
+      rd[i] = *(const uint4*)(dyp + (int64_t)t * p.dy.st);
+      if (res) rr[i] = *(const uint4*)(res + (int64_t)t * p.resid.st);
+      if (gp) rg[i] = *(const uint4*)(gp + (int64_t)t * p.g.st);
+    }
+  }
+  float gb[N], colsum[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    gb[e] = p.gbias && colok ? p.gbias[h * p.d + c + e] : 0.0f;
+    colsum[e] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    const bool live = t < p.T;  // dead rows and columns still join the row butterfly (with zeros)
+    const float denom = mass && live ? ms[i] + p.eps : 1.0f;
+    const float inv = __builtin_amdgcn_rcpf(denom);
+    const float scale = mass ? p.s * inv : p.s;
+    float dot = 0.0f;
+    if (live && colok) {
+      float nv[N], dv[N], rv[N], gv[N], o_dnum[N], o_dg[N], o_dres[N];
+      unpack<E, N>(rn[i], nv);
+      unpack<E, N>(rd[i], dv);
+      if (res) unpack<E, N>(rr[i], rv);
+      if (gp) unpack<E, N>(rg[i], gv);
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        float dpre = dv[e];
+        if (gp) {
+          const float x = gv[e] + gb[e];
+          const float sg = fast_sigmoid(x);
+          const float ypre = (res ? rv[e] : 0.0f) + scale * nv[e];
+          o_dg[e] = dv[e] * ypre * (sg * (1.0f + x * (1.0f - sg)));
+          colsum[e] += o_dg[e];
+          dpre = dv[e] * x * sg;
+        }
+        o_dnum[e] = scale * dpre;
+        o_dres[e] = dpre;
+        dot += dpre * nv[e];
+      }
+      *(uint4*)(dnum + (int64_t)t * p.dnum.st) = pack<E, N>(o_dnum);
+      if (dres) *(uint4*)(dres + (int64_t)t * p.dresid.st) = pack<E, N>(o_dres);
+      if (dg) *(uint4*)(dg + (int64_t)t * p.dg.st) = pack<E, N>(o_dg);
+    }
+    if (mass) {
+#pragma unroll
+      for (int o = 1; o < CPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
+      if (live && threadIdx.x % CPR == 0) dmass[(int64_t)t * p.dmass.st] = -p.s * dot * inv * inv;
+    }
+  }
+  if (dgb_part) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) red[threadIdx.x * N + e] = colsum[e];
+    __syncthreads();
+    // one output column per thread (the host checks d <= 256)
+    const int j = threadIdx.x;
+    if (j < p.d) {
+      const int chunk = j / N, e = j - chunk * N;
+      float v = 0.0f;
+      for (int l = 0; l < RP; ++l) v += red[(l * CPR + chunk) * N + e];
+      dgb_part[((int64_t)b * gridDim.x + blockIdx.x) * (p.H * p.d) + h * p.d + j] = v;
+    }
   }
 }
 
@@ -284,12 +344,49 @@ int check_read(const ts_read_desc* d) {
   return TS_OK;
 }
 
-// Lanes per row: chunks of 16 bytes rounded up to a power of two (<= 64).
-int lanes_per_row(const ts_read_desc* d) {
+// Chunks of 16 bytes per row rounded up to a power of two (<= 64).
+int chunks_p2(const ts_read_desc* d) {
   const int chunks = d->d / (d->dtype == TS_BF16 ? 8 : 4);
   int p2 = 1;
   while (p2 < chunks) p2 <<= 1;
   return p2;
+}
+
+int rows_per_block(int cpr) { return ts::kReadRPT * (256 / cpr); }
+
+// (T blocks, B*H) grid of the read kernels; false when it cannot be launched
+bool read_grid(const ts_read_desc* d, dim3* grid) {
+  const int rpb = rows_per_block(chunks_p2(d));
+  *grid = dim3((unsigned)((d->T + rpb - 1) / rpb), (unsigned)(d->B * d->H));
+  return (int64_t)d->B * d->H <= 65535;
+}
+
+template <typename E, int CPR>
+void launch_read_fwd(dim3 grid, hipStream_t stream, const ts::ReadP& p) {
+  hipLaunchKernelGGL((ts::read_fwd_kernel<E, CPR>), grid, dim3(256), 0, stream, p);
+}
+template <typename E, int CPR>
+void launch_read_bwd(dim3 grid, hipStream_t stream, const ts::ReadP& p, float* parts) {
+  hipLaunchKernelGGL((ts::read_bwd_kernel<E, CPR>), grid, dim3(256), 0, stream, p, parts);
+}
+
+template <typename E>
+void dispatch_read(int cpr, dim3 grid, hipStream_t stream, const ts::ReadP& p, bool bwd, float* parts) {
+  switch (cpr) {
+#define TS_CASE(K)                                                              \
+  case K:                                                                       \
+    if (bwd) launch_read_bwd<E, K>(grid, stream, p, parts);                     \
+    else launch_read_fwd<E, K>(grid, stream, p);                                \
+    break;
+    TS_CASE(1)
+    TS_CASE(2)
+    TS_CASE(4)
+    TS_CASE(8)
+    TS_CASE(16)
+    TS_CASE(32)
+    TS_CASE(64)
+#undef TS_CASE
+  }
 }
 
 void fill_read(const ts_read_desc* d, ts::ReadP& p) {
@@ -314,19 +411,25 @@ int ts_read_fwd(const ts_read_desc* d, const ts_read_io* io, hipStream_t stream)
   if (!io || !io->num.ptr || !io->y.ptr) return fail(TS_ERR_VALUE, "read: missing tensors");
   if (d->normalize && !io->mass.ptr) return fail(TS_ERR_VALUE, "read: missing mass");
   if (d->gate && !io->g.ptr) return fail(TS_ERR_VALUE, "read: missing gate");
-  const int64_t rows = (int64_t)d->B * d->H * d->T;
-  if (rows == 0) return TS_OK;
+  if ((int64_t)d->B * d->H * d->T == 0) return TS_OK;
+  dim3 grid;
+  if (!read_grid(d, &grid)) return fail(TS_ERR_NOT_IMPLEMENTED, "read: more than 65535 (batch, head) slices");
   ts::ReadP p;
   fill_read(d, p);
   p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.y = io->y;
   p.gbias = io->g_bias;
-  const int p2 = lanes_per_row(d);
-  const dim3 grid((unsigned)((rows * p2 + 255) / 256));
-  if (d->dtype == TS_BF16)
-    hipLaunchKernelGGL(ts::read_fwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p, p2);
-  else
-    hipLaunchKernelGGL(ts::read_fwd_kernel<float>, grid, dim3(256), 0, stream, p, p2);
+  if (d->dtype == TS_BF16) dispatch_read<ts::bf16>(chunks_p2(d), grid, stream, p, false, nullptr);
+  else dispatch_read<float>(chunks_p2(d), grid, stream, p, false, nullptr);
   return finish("read");
+}
+
+int ts_read_bwd_parts(const ts_read_desc* d, int32_t* parts) {
+  int rc = check_read(d);
+  if (rc) return rc;
+  dim3 grid;
+  read_grid(d, &grid);
+  if (parts) *parts = (int32_t)(d->B * (int)grid.x);
+  return TS_OK;
 }
 
 int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t stream) {
@@ -335,19 +438,18 @@ int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t str
   if (!io || !io->num.ptr || !io->dy.ptr || !io->dnum.ptr) return fail(TS_ERR_VALUE, "read bwd: missing tensors");
   if (d->normalize && (!io->mass.ptr || !io->dmass.ptr)) return fail(TS_ERR_VALUE, "read bwd: missing mass");
   if (d->gate && (!io->g.ptr || !io->dg.ptr)) return fail(TS_ERR_VALUE, "read bwd: missing gate");
-  const int64_t rows = (int64_t)d->B * d->H * d->T;
-  if (rows == 0) return TS_OK;
+  if (io->dg_bias_part && (!d->gate || d->d > 256))
+    return fail(TS_ERR_VALUE, "read bwd: gate-bias partials need the gate and a width of at most 256");
+  if ((int64_t)d->B * d->H * d->T == 0) return TS_OK;
+  dim3 grid;
+  if (!read_grid(d, &grid)) return fail(TS_ERR_NOT_IMPLEMENTED, "read bwd: more than 65535 (batch, head) slices");
   ts::ReadP p;
   fill_read(d, p);
   p.num = io->num; p.mass = io->mass; p.resid = io->resid; p.g = io->g; p.dy = io->dy;
   p.dnum = io->dnum; p.dmass = io->dmass; p.dresid = io->dresid; p.dg = io->dg;
   p.gbias = io->g_bias;
-  const int p2 = lanes_per_row(d);
-  const dim3 grid((unsigned)((rows * p2 + 255) / 256));
-  if (d->dtype == TS_BF16)
-    hipLaunchKernelGGL(ts::read_bwd_kernel<ts::bf16>, grid, dim3(256), 0, stream, p, p2);
-  else
-    hipLaunchKernelGGL(ts::read_bwd_kernel<float>, grid, dim3(256), 0, stream, p, p2);
+  if (d->dtype == TS_BF16) dispatch_read<ts::bf16>(chunks_p2(d), grid, stream, p, true, io->dg_bias_part);
+  else dispatch_read<float>(chunks_p2(d), grid, stream, p, true, io->dg_bias_part);
   return finish("read bwd");
 }
 

@@ -121,12 +121,14 @@ int plan_memory(const ts_memory_desc* d, MemPlan* P) {
   P->saved = o;
 
   const int hd = f.H * f.d;
-  const long rows = (long)f.B * f.T;
   P->col_slices = 0;
   if (d->has_g_bias) {
-    if (hd % 8 || hd > 2048) return fail(TS_ERR_NOT_IMPLEMENTED, "memory: gate-bias gradient of %d columns", hd);
-    long s = rows / 128;
-    P->col_slices = (int)(s < 1 ? 1 : (s > 256 ? 256 : s));
+    // gate-bias gradient: per-workgroup column partials written by the read backward
+    if (f.d > 256) return fail(TS_ERR_NOT_IMPLEMENTED, "memory: gate-bias gradient of head width %d", f.d);
+    ts_read_desc rd = {f.B, f.H, f.T, f.d, f.dtype, d->normalize ? 1 : 0, 1, f.resid_scale, f.eps};
+    int32_t parts = 0;
+    if ((rc = ts_read_bwd_parts(&rd, &parts))) return rc;
+    P->col_slices = parts;
   }
   o = 0;
   P->o_dnum = o; o = align_up(o + P->n_bhtd * es);
@@ -235,8 +237,6 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
     return fail(TS_ERR_VALUE, "memory: scratch buffer needs %zu bytes, 256-byte aligned", P.scratch);
   if ((gr->dtau && !f.has_tau) || (gr->dg_bias && !d->has_g_bias))
     return fail(TS_ERR_VALUE, "memory: gradient of an absent parameter");
-  if (gr->dg_bias && (gr->dg.sb != (int64_t)f.T * gr->dg.st || gr->dg.sh != f.d))
-    return fail(TS_ERR_VALUE, "memory: gate-bias gradient needs gate rows of one [B*T, H*d] matrix");
   if (f.T == 0) return TS_OK;
   const char* sv = (const char*)saved;
   char* sc = (char*)scratch;
@@ -251,8 +251,9 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
 
   // read backward
   ts_read_desc rd = {f.B, f.H, f.T, f.d, f.dtype, d->normalize ? 1 : 0, d->gate ? 1 : 0, f.resid_scale, f.eps};
+  float* gb_parts = gr->dg_bias ? (float*)(sc + P.o_col) : nullptr;
   ts_read_bwd_io rb = {num, mass, res, d->gate ? io->g : none(), gr->dy, dnum, dmass, dres,
-                       d->gate ? gr->dg : none(), gb32};
+                       d->gate ? gr->dg : none(), gb32, gb_parts};
   if ((rc = ts_read_bwd(&rd, &rb, stream))) return rc;
 
   // dphi_q = scan(dnum, v, phi_k): its segment states are the forward's, transposed
@@ -272,13 +273,10 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
   s.q = phk; s.k = phq; s.v = dnum; s.out = gr->dv;
   if ((rc = ts_scan_fwd(&P.sdv, &s, wsb, P.ws_b, stream))) return rc;
 
-  if (gr->dg_bias) {
-    float* parts = (float*)(sc + P.o_col);
-    const int hd = f.H * f.d;
-    if ((rc = ts_col_sums(gr->dg.ptr, f.dtype, (int64_t)f.B * f.T, hd, gr->dg.st, parts, P.col_slices, stream)) ||
-        (rc = ts_sum_slots(parts, P.col_slices, nullptr, 0, hd, gr->dg_bias, d->param_dtype, 1.0f, stream)))
-      return rc;
-  }
+  if (gb_parts &&
+      (rc = ts_sum_slots(gb_parts, P.col_slices, nullptr, 0, (int64_t)f.H * f.d, gr->dg_bias, d->param_dtype,
+                         1.0f, stream)))
+    return rc;
 
   // feature backwards with per-workgroup weight-gradient slots
   const bool want_k = gr->dw1 || gr->dtau;

@@ -240,9 +240,15 @@ __host__ __device__ inline ScanLayout scan_layout(int esize, int DK, int dvp, bo
   return L;
 }
 
-// GEN = false compiles the common case only: no retention, no ext columns,
-// plain stores (the host picks it whenever a call allows).
-template <typename E, int DK, int NVW, bool MAIN, bool GEN>
+// MODE selects what the kernel supports, so the common cases carry no code
+// for the others (the host picks the narrowest mode a call allows):
+//   kPlain   no retention, no ext columns, plain stores;
+//   kKeyExt  as kPlain plus the key-side ext column pair (q_ext, k_ext);
+//   kValExt  as kPlain plus the value-side ext column (v_ext, out_ext);
+//   kGeneral every retention, ext column and output mode, read at run time.
+constexpr int kPlain = 0, kGeneral = 1, kKeyExt = 2, kValExt = 3;
+
+template <typename E, int DK, int NVW, bool MAIN, int MODE>
 __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   typedef typename Frag<E>::f8 F8;
   typedef typename Frag<E>::f4 F4;
@@ -258,14 +264,16 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   constexpr int SLOTS_K = (C * DK / VEC + 255) / 256;
   constexpr int SLOTS_V = (C * 64 * NVW / VEC + 255) / 256;
 
+  constexpr bool GEN = MODE == kGeneral;
   const int ret = GEN ? p.ret : TS_RET_NONE;
-  const int q_ext = GEN ? p.q_ext : TS_EXT_NONE;
-  const int k_ext = GEN ? p.k_ext : TS_EXT_NONE;
-  const int v_ext = GEN ? p.v_ext : TS_EXT_NONE;
-  const bool kx = q_ext != TS_EXT_NONE && k_ext != TS_EXT_NONE;  // key-side rank-1 term
-  const bool vx = v_ext != TS_EXT_NONE && blockIdx.z == 0;
+  const int q_ext = GEN || MODE == kKeyExt ? p.q_ext : TS_EXT_NONE;
+  const int k_ext = GEN || MODE == kKeyExt ? p.k_ext : TS_EXT_NONE;
+  const int v_ext = GEN || MODE == kValExt ? p.v_ext : TS_EXT_NONE;
+  // key-side rank-1 term (kKeyExt: the host guarantees both columns)
+  const bool kx = MODE == kKeyExt || (GEN && q_ext != TS_EXT_NONE && k_ext != TS_EXT_NONE);
+  const bool vx = (MODE == kValExt || (GEN && v_ext != TS_EXT_NONE)) && blockIdx.z == 0;
   const int out_mode = GEN ? p.out_mode : TS_OUT_STORE;
-  const bool has_oe = GEN && p.oe.ptr != nullptr;
+  const bool has_oe = (GEN || MODE == kValExt) && p.oe.ptr != nullptr;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -877,13 +885,13 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
 
 typedef void (*KernelFn)(ts::ScanP);
 
-template <typename E, int NVW, bool GEN>
+template <typename E, int NVW, int MODE>
 KernelFn pick_kernel_v(int dkp, bool main_kernel) {
   switch (dkp) {
 #define TS_CASE(D)                                                                    \
   case D:                                                                             \
-    return main_kernel ? (KernelFn)ts::scan_kernel<E, D, NVW, true, GEN>              \
-                       : (KernelFn)ts::scan_kernel<E, D, NVW, false, GEN>;
+    return main_kernel ? (KernelFn)ts::scan_kernel<E, D, NVW, true, MODE>             \
+                       : (KernelFn)ts::scan_kernel<E, D, NVW, false, MODE>;
     TS_CASE(16)
     TS_CASE(32)
     TS_CASE(64)
@@ -893,16 +901,23 @@ KernelFn pick_kernel_v(int dkp, bool main_kernel) {
   return nullptr;
 }
 
-// bf16 kernels are specialised by whether the call needs the general features
-// (retention, ext columns, fp32 outputs); the fp32 parity kernels are general.
-KernelFn pick_kernel(bool bf16, int dkp, int nvw, bool main_kernel, bool general) {
+template <typename E, int NVW>
+KernelFn pick_kernel_m(int dkp, bool main_kernel, int mode) {
+  switch (mode) {
+    case ts::kPlain: return pick_kernel_v<E, NVW, ts::kPlain>(dkp, main_kernel);
+    case ts::kKeyExt: return pick_kernel_v<E, NVW, ts::kKeyExt>(dkp, main_kernel);
+    case ts::kValExt: return pick_kernel_v<E, NVW, ts::kValExt>(dkp, main_kernel);
+  }
+  return pick_kernel_v<E, NVW, ts::kGeneral>(dkp, main_kernel);
+}
+
+// bf16 kernels are specialised by mode; the fp32 parity kernels are general.
+KernelFn pick_kernel(bool bf16, int dkp, int nvw, bool main_kernel, int mode) {
   if (!bf16)
-    return nvw == 1 ? pick_kernel_v<float, 1, true>(dkp, main_kernel) : pick_kernel_v<float, 2, true>(dkp, main_kernel);
-  if (nvw == 1)
-    return general ? pick_kernel_v<ts::bf16, 1, true>(dkp, main_kernel)
-                   : pick_kernel_v<ts::bf16, 1, false>(dkp, main_kernel);
-  return general ? pick_kernel_v<ts::bf16, 2, true>(dkp, main_kernel)
-                 : pick_kernel_v<ts::bf16, 2, false>(dkp, main_kernel);
+    return nvw == 1 ? pick_kernel_v<float, 1, ts::kGeneral>(dkp, main_kernel)
+                    : pick_kernel_v<float, 2, ts::kGeneral>(dkp, main_kernel);
+  return nvw == 1 ? pick_kernel_m<ts::bf16, 1>(dkp, main_kernel, mode)
+                  : pick_kernel_m<ts::bf16, 2>(dkp, main_kernel, mode);
 }
 
 // Bytes spanned by one (batch, head) slice of a [.., T, width] stream, or an
@@ -1023,10 +1038,12 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   }
 
   const int bh = d->B * d->H;
-  const bool general = d->retention != TS_RET_NONE || L.kx || L.vx || d->out_mode != TS_OUT_STORE ||
-                       io->out_ext.ptr != nullptr;
-  KernelFn fsum = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, false, general);
-  KernelFn fmain = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, true, general);
+  int mode = ts::kPlain;
+  if (d->retention != TS_RET_NONE || d->out_mode != TS_OUT_STORE) mode = ts::kGeneral;
+  else if (L.kx) mode = ts::kKeyExt;
+  else if (L.vx) mode = ts::kValExt;
+  KernelFn fsum = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, false, mode);
+  KernelFn fmain = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, true, mode);
   const size_t lds_sum = (size_t)ts::scan_layout(esize, L.dkp, L.vs, false).bytes;
   const size_t lds_main = (size_t)ts::scan_layout(esize, L.dkp, L.vs, true).bytes;
   if (lds_main > 160 * 1024)

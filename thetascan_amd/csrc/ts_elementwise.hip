@@ -273,6 +273,51 @@ __global__ __launch_bounds__(256) void sum_slots_kernel(const float* a, int na, 
   }
 }
 
+// The same sum over 16-byte columns: a block is (256 / R) columns of four
+// outputs x R slot rows; row r adds slots r, r + R, ... (two loads in flight
+// per step), and the R rows of a column combine through LDS in row order, so
+// the result does not depend on timing.  R grows with the slot count when
+// there are few columns, so a wide sum and a tall one both fill the chip.
+template <int R>
+__global__ __launch_bounds__(256) void sum_slots_vec_kernel(const float* a, int na, const float* b, int nb,
+                                                            int64_t nv, void* out, int out_bf16, float scale) {
+  constexpr int CPB = 256 / R;
+  __shared__ floatx4 red[256];
+  const int tid = threadIdx.x;
+  const int cl = tid % CPB, r = tid / CPB;
+  const int64_t v = (int64_t)blockIdx.x * CPB + cl;
+  const int total = na + nb;
+  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  if (v < nv) {
+    const floatx4* av = (const floatx4*)a;
+    const floatx4* bv = (const floatx4*)b;
+    auto slot = [&](int t) -> floatx4 { return t < na ? av[(int64_t)t * nv + v] : bv[(int64_t)(t - na) * nv + v]; };
+    int t = r;
+    for (; t + R < total; t += 2 * R) {
+      const floatx4 x0 = slot(t), x1 = slot(t + R);
+      acc0 += x0;
+      acc1 += x1;
+    }
+    if (t < total) acc0 += slot(t);
+  }
+  red[tid] = acc0 + acc1;
+  __syncthreads();
+  if (r == 0 && v < nv) {
+    floatx4 sum = red[cl];
+#pragma unroll
+    for (int k = 1; k < R; ++k) sum += red[k * CPB + cl];
+    sum *= scale;
+    if (out_bf16) {
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (bf16)sum[e];
+      ((bf16x4*)out)[v] = o;
+    } else {
+      ((floatx4*)out)[v] = sum;
+    }
+  }
+}
+
 // parts[blk][c] = sum of x[r * stride + c] over the `rows_per_block` rows of
 // block blk.  A block is 256 / (cols / 8) row lanes x (cols / 8) column
 // groups of eight (one 16-byte load of bf16, two of fp32); row lanes step by
@@ -459,6 +504,26 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
   if ((na && !a) || (nb && !b) || !out) return fail(TS_ERR_VALUE, "sum_slots: missing buffers");
   if (out_dtype != TS_BF16 && out_dtype != TS_F32) return fail(TS_ERR_VALUE, "sum_slots: unknown dtype");
   if (n == 0) return TS_OK;
+  const int total = na + nb;
+  const bool vec = n % 4 == 0 && !((uintptr_t)a & 15u) && !((uintptr_t)b & 15u) &&
+                   !((uintptr_t)out & (out_dtype == TS_BF16 ? 7u : 15u));
+  if (vec && total > 0) {
+    // slot rows per column: enough threads to fill the chip, at most one slot per row step
+    const int64_t nv = n / 4;
+    int R = 1;
+    while (R < 16 && R < total && nv * R < 65536) R <<= 1;
+    const int cpb = 256 / R;
+    const dim3 grid((unsigned)((nv + cpb - 1) / cpb));
+    const int ob = out_dtype == TS_BF16 ? 1 : 0;
+    switch (R) {
+      case 1: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<1>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      case 2: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<2>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      case 4: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<4>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      case 8: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<8>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      default: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<16>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+    }
+    return finish("sum_slots");
+  }
   // outputs per block: as many as keep >= 512 blocks, at least 4 slot rows per output
   int opb = 64;
   while (opb > 4 && (n + opb - 1) / opb < 512) opb >>= 1;

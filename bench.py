@@ -133,7 +133,8 @@ def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
     """Per-entry-point timing inside real fwd+bwd steps.
 
     Every HIP entry point called during ``steps`` steps is bracketed by events
-    on the stream it launches on (``_lib.record_launches``).  Returns, per entry
+    on the stream it launches on (``_lib.record_launches``), with the GPU kept
+    behind the host so that no event pair includes host submission time.  Returns, per entry
     point, launches per step, mean duration per launch and achieved GB/s of its
     algorithmic bytes (inputs read once, outputs written once).
     """
@@ -150,8 +151,27 @@ def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
 
     step()
     torch.cuda.synchronize()
+    # The recorded step submits one entry point at a time from Python, slower
+    # than the GPU runs them; a start event would then also time the host's
+    # submission of its launch.  A device-side sleep queued ahead of each step
+    # (longer than the host takes to submit the whole step) keeps the GPU
+    # behind the host, so every event pair brackets GPU work only.
+    with _lib.record_launches():
+        t0 = time.perf_counter()
+        step()
+        host_s = time.perf_counter() - t0
+        torch.cuda.synchronize()
+    probe_cycles = 1 << 20
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    torch.cuda._sleep(probe_cycles)
+    b.record()
+    torch.cuda.synchronize()
+    cycles_per_s = probe_cycles / max(a.elapsed_time(b) * 1e-3, 1e-6)
+    sleep_cycles = int(cycles_per_s * (2.0 * host_s + 1e-3))
     with _lib.record_launches() as recs:
         for _ in range(steps):
+            torch.cuda._sleep(sleep_cycles)
             step()
         torch.cuda.synchronize()
         rows = [(name, a.elapsed_time(b), nb) for name, a, b, nb in recs]

@@ -351,8 +351,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", choices=("headline", *OTHER), default="headline",
                     help="headline (default) or one of the other two workloads of the path")
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", choices=("eager", "graph"), default="eager",
                     help="time eager execution (default) or graph replays of the captured step")

@@ -240,13 +240,13 @@ __host__ __device__ inline ScanLayout scan_layout(int esize, int DK, int dvp, bo
   return L;
 }
 
-// MODE selects what the kernel supports, so the common cases carry no code
-// for the others (the host picks the narrowest mode a call allows):
-//   kPlain   no retention, no ext columns, plain stores;
-//   kKeyExt  as kPlain plus the key-side ext column pair (q_ext, k_ext);
-//   kValExt  as kPlain plus the value-side ext column (v_ext, out_ext);
-//   kGeneral every retention, ext column and output mode, read at run time.
-constexpr int kPlain = 0, kGeneral = 1, kKeyExt = 2, kValExt = 3;
+// MODE selects what the kernel supports, so a call carries no code for what
+// it does not use.  Bits: kStatic (static [H] retention), kKeyExt (the
+// key-side ext column pair q_ext, k_ext), kValExt (the value-side ext column
+// v_ext, out_ext), kF32Out (fp32 outputs, stored or accumulated); kGeneral
+// alone reads every retention, ext column and output mode at run time.  The
+// host picks an instantiated mode that covers the call, else kGeneral.
+constexpr int kPlain = 0, kStatic = 1, kKeyExt = 2, kValExt = 4, kF32Out = 8, kGeneral = 16;
 
 template <typename E, int DK, int NVW, bool MAIN, int MODE>
 __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
@@ -265,15 +265,16 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   constexpr int SLOTS_V = (C * 64 * NVW / VEC + 255) / 256;
 
   constexpr bool GEN = MODE == kGeneral;
-  const int ret = GEN ? p.ret : TS_RET_NONE;
-  const int q_ext = GEN || MODE == kKeyExt ? p.q_ext : TS_EXT_NONE;
-  const int k_ext = GEN || MODE == kKeyExt ? p.k_ext : TS_EXT_NONE;
-  const int v_ext = GEN || MODE == kValExt ? p.v_ext : TS_EXT_NONE;
+  constexpr bool M_KX = (MODE & kKeyExt) != 0, M_VX = (MODE & kValExt) != 0;
+  const int ret = GEN ? p.ret : ((MODE & kStatic) ? TS_RET_STATIC : TS_RET_NONE);
+  const int q_ext = GEN || M_KX ? p.q_ext : TS_EXT_NONE;
+  const int k_ext = GEN || M_KX ? p.k_ext : TS_EXT_NONE;
+  const int v_ext = GEN || M_VX ? p.v_ext : TS_EXT_NONE;
   // key-side rank-1 term (kKeyExt: the host guarantees both columns)
-  const bool kx = MODE == kKeyExt || (GEN && q_ext != TS_EXT_NONE && k_ext != TS_EXT_NONE);
-  const bool vx = (MODE == kValExt || (GEN && v_ext != TS_EXT_NONE)) && blockIdx.z == 0;
-  const int out_mode = GEN ? p.out_mode : TS_OUT_STORE;
-  const bool has_oe = (GEN || MODE == kValExt) && p.oe.ptr != nullptr;
+  const bool kx = M_KX || (GEN && q_ext != TS_EXT_NONE && k_ext != TS_EXT_NONE);
+  const bool vx = (M_VX || (GEN && v_ext != TS_EXT_NONE)) && blockIdx.z == 0;
+  const int out_mode = GEN || (MODE & kF32Out) ? p.out_mode : TS_OUT_STORE;
+  const bool has_oe = (GEN || M_VX) && p.oe.ptr != nullptr;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -901,14 +902,28 @@ KernelFn pick_kernel_v(int dkp, bool main_kernel) {
   return nullptr;
 }
 
+// The bf16 modes compiled: the kernel memory's scans (plain, key-side and
+// value-side ext columns), the temporal bank's static views (with or without
+// the key-mass column) and the composed backward's fp32 gradient scans (with
+// or without the key-side column and a static retention).
 template <typename E, int NVW>
 KernelFn pick_kernel_m(int dkp, bool main_kernel, int mode) {
+  using namespace ts;
   switch (mode) {
-    case ts::kPlain: return pick_kernel_v<E, NVW, ts::kPlain>(dkp, main_kernel);
-    case ts::kKeyExt: return pick_kernel_v<E, NVW, ts::kKeyExt>(dkp, main_kernel);
-    case ts::kValExt: return pick_kernel_v<E, NVW, ts::kValExt>(dkp, main_kernel);
+#define TS_MODE(M) \
+  case M: return pick_kernel_v<E, NVW, M>(dkp, main_kernel);
+    TS_MODE(kPlain)
+    TS_MODE(kKeyExt)
+    TS_MODE(kValExt)
+    TS_MODE(kStatic)
+    TS_MODE(kStatic | kValExt)
+    TS_MODE(kF32Out)
+    TS_MODE(kF32Out | kKeyExt)
+    TS_MODE(kF32Out | kStatic)
+    TS_MODE(kF32Out | kStatic | kKeyExt)
+#undef TS_MODE
   }
-  return pick_kernel_v<E, NVW, ts::kGeneral>(dkp, main_kernel);
+  return pick_kernel_v<E, NVW, kGeneral>(dkp, main_kernel);
 }
 
 // bf16 kernels are specialised by mode; the fp32 parity kernels are general.
@@ -1038,10 +1053,13 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   }
 
   const int bh = d->B * d->H;
-  int mode = ts::kPlain;
-  if (d->retention != TS_RET_NONE || d->out_mode != TS_OUT_STORE) mode = ts::kGeneral;
-  else if (L.kx) mode = ts::kKeyExt;
-  else if (L.vx) mode = ts::kValExt;
+  int mode = ts::kGeneral;
+  if (d->retention != TS_RET_STREAM) {
+    mode = (d->retention == TS_RET_STATIC ? ts::kStatic : 0) | (L.kx ? ts::kKeyExt : 0) | (L.vx ? ts::kValExt : 0) |
+           (d->out_mode != TS_OUT_STORE ? ts::kF32Out : 0);
+    // an fp32 output with a value-side ext column (its fp32 ext output) is general
+    if ((mode & ts::kF32Out) && (mode & ts::kValExt)) mode = ts::kGeneral;
+  }
   KernelFn fsum = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, false, mode);
   KernelFn fmain = pick_kernel(d->dtype == TS_BF16, L.dkp, L.nvw, true, mode);
   const size_t lds_sum = (size_t)ts::scan_layout(esize, L.dkp, L.vs, false).bytes;

@@ -258,6 +258,26 @@ int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t 
 /* Number P of gate-bias partial rows ts_read_bwd writes for `desc`. */
 int ts_read_bwd_parts(const ts_read_desc* desc, int32_t* parts);
 
+/* ------------------------------------------------- query/key prologue */
+
+typedef struct ts_qknorm_desc {
+  int32_t B, H, T, d;
+  int32_t dtype;        /* of x, y, dy, dx                                     */
+  int32_t rot;          /* RoPE width (even, <= d; 0 = none)                   */
+  float eps;
+} ts_qknorm_desc;
+
+/* y = rope(x) / max(|rope(x)|, eps) per [B,H,T,d] row, RoPE on pairs
+ * (2i, 2i+1), i < rot / 2, with fp32 angles from rope_cos/rope_sin [T, rot/2].
+ * Replaces the input RoPE and the query/key L2 norm of the mixer prologue
+ * (block.py:595-599; rope.py:41-49; norms.py:11-12). */
+int ts_qknorm_fwd(const ts_qknorm_desc* desc, ts_strided x, ts_strided y, const float* rope_cos,
+                  const float* rope_sin, hipStream_t stream);
+
+/* Backward of ts_qknorm_fwd: dx from x and dy. */
+int ts_qknorm_bwd(const ts_qknorm_desc* desc, ts_strided x, ts_strided dy, ts_strided dx, const float* rope_cos,
+                  const float* rope_sin, hipStream_t stream);
+
 /* -------------------------------------------------------- GN write payloads */
 
 /* Damped Gauss-Newton write of a one-hidden-layer ReLU^2 fast network

@@ -23,7 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
-from ..ops import engine, fused, maps
+from ..ops import engine, fused, maps, prologue
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
 from .norms import l2norm
@@ -426,11 +426,20 @@ class ThetaScan(nn.Module):
         B, T, _ = x.shape
         H, d = cfg.n_heads, cfg.head_dim
         q, k, v = self._project(x)
-        if cfg.rope_placement == "input":
-            q = apply_rope(q, cfg.rope, cfg.rope_frac, cfg.rope_base)
-            k = apply_rope(k, cfg.rope, cfg.rope_frac, cfg.rope_base)
+        rot_in = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
+        qn = kn = None
         if cfg.qk_norm:
-            q, k = l2norm(q, cfg.eps), l2norm(k, cfg.eps)
+            # input RoPE + L2 norm in one HIP kernel per stream (strided views in)
+            qn = prologue.qk_norm(q, rot_in, cfg.rope_base, cfg.eps)
+            kn = prologue.qk_norm(k, rot_in, cfg.rope_base, cfg.eps) if qn is not None else None
+        if qn is not None and kn is not None:
+            q, k = qn, kn
+        else:
+            if cfg.rope_placement == "input":
+                q = apply_rope(q, cfg.rope, cfg.rope_frac, cfg.rope_base)
+                k = apply_rope(k, cfg.rope, cfg.rope_frac, cfg.rope_base)
+            if cfg.qk_norm:
+                q, k = l2norm(q, cfg.eps), l2norm(k, cfg.eps)
         v_w = v
         if self.vmlp_in is not None:
             v_w = v_w + self.vmlp_out(F.silu(self.vmlp_in(v_w)))

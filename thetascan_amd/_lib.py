@@ -160,6 +160,11 @@ class ReadIO(ctypes.Structure):
                 ("g_bias", ctypes.c_void_p)]
 
 
+class QkNormDesc(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32), ("d", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("rot", ctypes.c_int32), ("eps", ctypes.c_float)]
+
+
 class ReadBwdIO(ctypes.Structure):
     _fields_ = [
         ("num", Strided),
@@ -401,6 +406,10 @@ def load() -> ctypes.CDLL:
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_read_bwd_parts.argtypes = [P(ReadDesc), P(ctypes.c_int32)]
+        lib.ts_qknorm_fwd.argtypes = [P(QkNormDesc), Strided, Strided, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p]
+        lib.ts_qknorm_bwd.argtypes = [P(QkNormDesc), Strided, Strided, Strided, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p]
         lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
         lib.ts_col_sums.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]

@@ -207,6 +207,130 @@ __global__ __launch_bounds__(256) void read_bwd_kernel(ReadP p, float* dgb_part)
   }
 }
 
+// ---- query/key prologue: y = rope(x) / max(|rope(x)|, eps) per row
+// (block.py:595-599 with rope.py:41-49 and norms.py:11-12), rows of strided
+// [B,H,T,d] views in, contiguous rows out; same work mapping as the read
+// kernels.  RoPE rotates pairs (2i, 2i+1) with i < rot / 2 by fp32 angles
+// from [T, rot / 2] tables; a pair never straddles a 16-byte chunk.
+struct NormP {
+  int B, H, T, d, rot;
+  float eps;
+  ts_strided x, dy, y, dx;
+  const float* cs;
+  const float* sn;
+};
+
+template <int N>
+__device__ __forceinline__ void rope_chunk(float* v, int c, int t, const NormP& p, bool inverse) {
+#pragma unroll
+  for (int e = 0; e < N; e += 2) {
+    if (c + e < p.rot) {
+      const int j = t * (p.rot >> 1) + ((c + e) >> 1);
+      const float cs = p.cs[j];
+      const float sn = inverse ? -p.sn[j] : p.sn[j];
+      const float a = v[e], b = v[e + 1];
+      v[e] = a * cs - b * sn;
+      v[e + 1] = a * sn + b * cs;
+    }
+  }
+}
+
+template <typename E, int CPR>
+__global__ __launch_bounds__(256) void qknorm_fwd_kernel(NormP p) {
+  constexpr int N = Vec16<E>::N;
+  constexpr int RP = 256 / CPR;
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+  const int c = ((int)threadIdx.x % CPR) * N;
+  const bool colok = c < p.d;
+  const int r0 = blockIdx.x * read_rows_per_block<CPR>() + (int)threadIdx.x / CPR;
+  const E* x = slice_of<E>(p.x, b, h) + c;
+  E* y = (E*)slice_of<E>(p.y, b, h) + c;
+  uint4 rx[kReadRPT];
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    if (t < p.T && colok) rx[i] = *(const uint4*)(x + (int64_t)t * p.x.st);
+  }
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    const bool live = t < p.T && colok;
+    float v[N];
+    float ss = 0.0f;
+    if (live) {
+      unpack<E, N>(rx[i], v);
+      if (p.rot > 0) rope_chunk<N>(v, c, t, p, false);
+#pragma unroll
+      for (int e = 0; e < N; ++e) ss += v[e] * v[e];
+    }
+#pragma unroll
+    for (int o = 1; o < CPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    if (live) {
+      const float inv = 1.0f / fmaxf(sqrtf(ss), p.eps);
+#pragma unroll
+      for (int e = 0; e < N; ++e) v[e] *= inv;
+      *(uint4*)(y + (int64_t)t * p.y.st) = pack<E, N>(v);
+    }
+  }
+}
+
+// dx = rope^T( n > eps ? (dy - y (y . dy)) / n : dy / eps ),  n = |rope(x)|
+template <typename E, int CPR>
+__global__ __launch_bounds__(256) void qknorm_bwd_kernel(NormP p) {
+  constexpr int N = Vec16<E>::N;
+  constexpr int RP = 256 / CPR;
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+  const int c = ((int)threadIdx.x % CPR) * N;
+  const bool colok = c < p.d;
+  const int r0 = blockIdx.x * read_rows_per_block<CPR>() + (int)threadIdx.x / CPR;
+  const E* x = slice_of<E>(p.x, b, h) + c;
+  const E* dyp = slice_of<E>(p.dy, b, h) + c;
+  E* dx = (E*)slice_of<E>(p.dx, b, h) + c;
+  uint4 rx[kReadRPT], rd[kReadRPT];
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    if (t < p.T && colok) {
+      rx[i] = *(const uint4*)(x + (int64_t)t * p.x.st);
+      rd[i] = *(const uint4*)(dyp + (int64_t)t * p.dy.st);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kReadRPT; ++i) {
+    const int t = r0 + i * RP;
+    const bool live = t < p.T && colok;
+    float v[N], g[N];
+    float ss = 0.0f, dot = 0.0f;
+    if (live) {
+      unpack<E, N>(rx[i], v);
+      unpack<E, N>(rd[i], g);
+      if (p.rot > 0) rope_chunk<N>(v, c, t, p, false);
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        ss += v[e] * v[e];
+        dot += v[e] * g[e];
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < CPR; o <<= 1) {
+      ss += __shfl_xor(ss, o, 64);
+      dot += __shfl_xor(dot, o, 64);
+    }
+    if (live) {
+      const float n = sqrtf(ss);
+      const bool big = n > p.eps;
+      const float inv = 1.0f / (big ? n : p.eps);
+      const float yd = dot * inv * inv;  // y . dy / n
+#pragma unroll
+      for (int e = 0; e < N; ++e) g[e] = big ? (g[e] - v[e] * yd) * inv : g[e] * inv;
+      if (p.rot > 0) rope_chunk<N>(g, c, t, p, true);
+      *(uint4*)(dx + (int64_t)t * p.dx.st) = pack<E, N>(g);
+    }
+  }
+}
+
 // z_t = a_t z_{t-1} + x_t  over T for every (b, h, feature).
 __global__ __launch_bounds__(256) void wcumsum_kernel(int B, int H, int T, int F, int ret, int reverse,
                                                       ts_strided x, ts_strided out, const float* log_alpha,
@@ -446,6 +570,53 @@ int finish(const char* what) {
   return TS_OK;
 }
 
+template <typename E, int CPR>
+void launch_qknorm(dim3 grid, hipStream_t stream, const ts::NormP& p, bool bwd) {
+  if (bwd) hipLaunchKernelGGL((ts::qknorm_bwd_kernel<E, CPR>), grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL((ts::qknorm_fwd_kernel<E, CPR>), grid, dim3(256), 0, stream, p);
+}
+
+template <typename E>
+void dispatch_qknorm(int cpr, dim3 grid, hipStream_t stream, const ts::NormP& p, bool bwd) {
+  switch (cpr) {
+    case 1: launch_qknorm<E, 1>(grid, stream, p, bwd); break;
+    case 2: launch_qknorm<E, 2>(grid, stream, p, bwd); break;
+    case 4: launch_qknorm<E, 4>(grid, stream, p, bwd); break;
+    case 8: launch_qknorm<E, 8>(grid, stream, p, bwd); break;
+    case 16: launch_qknorm<E, 16>(grid, stream, p, bwd); break;
+    case 32: launch_qknorm<E, 32>(grid, stream, p, bwd); break;
+    default: launch_qknorm<E, 64>(grid, stream, p, bwd); break;
+  }
+}
+
+int qknorm_launch(const ts_qknorm_desc* d, ts_strided x, ts_strided dy, ts_strided out, const float* cs,
+                  const float* sn, bool bwd, hipStream_t stream) {
+  if (!d) return fail(TS_ERR_VALUE, "qknorm: null descriptor");
+  if (d->B < 1 || d->H < 1 || d->T < 0 || d->d < 1) return fail(TS_ERR_VALUE, "qknorm: bad shape");
+  if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "qknorm: unknown dtype");
+  const int vec = d->dtype == TS_BF16 ? 8 : 4;
+  if (d->d % vec || d->d / vec > 64) return fail(TS_ERR_VALUE, "qknorm: width %d must be a multiple of 16 bytes, at most 64 of them", d->d);
+  if (d->rot < 0 || d->rot > d->d || d->rot % 2) return fail(TS_ERR_VALUE, "qknorm: rotated width %d", d->rot);
+  if (d->rot > 0 && (!cs || !sn)) return fail(TS_ERR_VALUE, "qknorm: missing RoPE tables");
+  if (!x.ptr || !out.ptr || (bwd && !dy.ptr)) return fail(TS_ERR_VALUE, "qknorm: missing tensors");
+  for (const ts_strided* t : {&x, &dy, &out})
+    if (t->ptr && (((uintptr_t)t->ptr & 15u) || t->st % vec || t->sh % vec || t->sb % vec))
+      return fail(TS_ERR_VALUE, "qknorm: rows must be 16-byte aligned");
+  if ((int64_t)d->B * d->H * d->T == 0) return TS_OK;
+  const ts_read_desc rd = {d->B, d->H, d->T, d->d, d->dtype, 0, 0, 1.0f, d->eps};
+  dim3 grid;
+  if (!read_grid(&rd, &grid)) return fail(TS_ERR_NOT_IMPLEMENTED, "qknorm: more than 65535 (batch, head) slices");
+  ts::NormP p;
+  memset(&p, 0, sizeof(p));
+  p.B = d->B; p.H = d->H; p.T = d->T; p.d = d->d; p.rot = d->rot; p.eps = d->eps;
+  p.x = x; p.dy = dy; p.cs = cs; p.sn = sn;
+  if (bwd) p.dx = out;
+  else p.y = out;
+  if (d->dtype == TS_BF16) dispatch_qknorm<ts::bf16>(chunks_p2(&rd), grid, stream, p, bwd);
+  else dispatch_qknorm<float>(chunks_p2(&rd), grid, stream, p, bwd);
+  return finish(bwd ? "qknorm bwd" : "qknorm");
+}
+
 }  // namespace
 
 extern "C" {
@@ -496,6 +667,16 @@ int ts_read_bwd(const ts_read_desc* d, const ts_read_bwd_io* io, hipStream_t str
   if (d->dtype == TS_BF16) dispatch_read<ts::bf16>(chunks_p2(d), grid, stream, p, true, io->dg_bias_part);
   else dispatch_read<float>(chunks_p2(d), grid, stream, p, true, io->dg_bias_part);
   return finish("read bwd");
+}
+
+int ts_qknorm_fwd(const ts_qknorm_desc* d, ts_strided x, ts_strided y, const float* rope_cos, const float* rope_sin,
+                  hipStream_t stream) {
+  return qknorm_launch(d, x, ts_strided{nullptr, 0, 0, 0}, y, rope_cos, rope_sin, false, stream);
+}
+
+int ts_qknorm_bwd(const ts_qknorm_desc* d, ts_strided x, ts_strided dy, ts_strided dx, const float* rope_cos,
+                  const float* rope_sin, hipStream_t stream) {
+  return qknorm_launch(d, x, dy, dx, rope_cos, rope_sin, true, stream);
 }
 
 int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t n, void* out, int32_t out_dtype,

@@ -467,6 +467,25 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
 int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_t row_stride, float* parts,
                 int32_t slices, hipStream_t stream);
 
+/* ------------------------------------------------- token contractions */
+
+typedef struct ts_contract_desc {
+  int32_t G, N;         /* groups (heads) and tokens                           */
+  int32_t p, q;         /* widths of a and b (multiples of 16, at most 128)    */
+  int32_t dtype;        /* of a and b                                          */
+} ts_contract_desc;
+
+/* Bytes of the fp32 partials ts_contract_tokens needs as its workspace. */
+int ts_contract_workspace_bytes(const ts_contract_desc* desc, size_t* bytes);
+
+/* out[g] = sum_n a[g, n, :]^T b[g, n, :] as fp32 [G, p, q], for token-major
+ * tiles a[g, n, i] at a + g * a_sg + n * a_sn + i (and b alike).  The weight
+ * gradients of the GN fast network (dW1, dW2) contracted over every token
+ * (the autograd reductions of engine.py:117-158, 180-255). */
+int ts_contract_tokens(const ts_contract_desc* desc, const void* a, int64_t a_sg, int64_t a_sn, const void* b,
+                       int64_t b_sg, int64_t b_sn, float* out, void* workspace, size_t ws_bytes,
+                       hipStream_t stream);
+
 /* ------------------------------------------------ depth-1 kernel memory */
 
 /* Everything between the input and the output projection of a depth-1

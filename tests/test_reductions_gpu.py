@@ -44,3 +44,22 @@ def test_two_slot_buffers_sum_together(cuda):
                                 _lib.stream_handle(a.device)), "sum")
     expected = 0.5 * (a.double().sum(0) + b.double().sum(0))
     assert rel_err(out, expected) < 1e-6
+
+
+@pytest.mark.parametrize("G,N,p,q", [(8, 2048, 128, 64), (2, 1000, 64, 128), (3, 37, 16, 32), (1, 4096, 128, 128),
+                                     (4, 64, 48, 80)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_token_contraction_matches_float64(cuda, G, N, p, q, dtype):
+    """ts_contract_tokens (the GN weight-gradient contractions) against a
+    float64 einsum on the same rounded inputs, including token counts that
+    leave a ragged last tile and operand views with a group stride."""
+    from thetascan_amd._core.ops.gn import contract_tokens
+
+    g = torch.Generator().manual_seed(G * 7 + N + p + q)
+    a = torch.randn(G, N, p, generator=g).to(dtype)
+    b_full = torch.randn(2, G, N, q, generator=g).to(dtype)
+    b = b_full[1]
+    expected = torch.einsum("gnp,gnq->gpq", a.double(), b.double())
+    out = contract_tokens(a.to(cuda), b_full.to(cuda)[1])
+    assert out.dtype == torch.float32 and out.shape == (G, p, q)
+    assert rel_err(out, expected) < 1e-5

@@ -24,6 +24,7 @@ import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
 from ..ops import engine, fused, maps, prologue
+from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
 from .norms import l2norm
@@ -408,17 +409,17 @@ class ThetaScan(nn.Module):
         H, d = cfg.n_heads, cfg.head_dim
         if cfg.key_value_heads is not None:
             G = cfg.key_value_heads
-            q = F.linear(x, self.proj_q.weight).view(B, T, H, d).transpose(1, 2)
-            k = F.linear(x, self.proj_k.weight).view(B, T, G, d).transpose(1, 2)
-            v = F.linear(x, self.proj_v.weight).view(B, T, G, d).transpose(1, 2)
+            q = linear(x, self.proj_q.weight).view(B, T, H, d).transpose(1, 2)
+            k = linear(x, self.proj_k.weight).view(B, T, G, d).transpose(1, 2)
+            v = linear(x, self.proj_v.weight).view(B, T, G, d).transpose(1, 2)
             return q, k.repeat_interleave(H // G, dim=1), v.repeat_interleave(H // G, dim=1)
         if cfg.share_kq:
             kqb = self.kq_bias.to(dtype=x.dtype)
-            q = F.linear(x, self.proj_q1.weight).unsqueeze(1) + kqb[0][None, :, None, :]
-            k = F.linear(x, self.proj_k1.weight).unsqueeze(1) + kqb[1][None, :, None, :]
-            v = F.linear(x, self.proj_v.weight).view(B, T, H, d).transpose(1, 2)
+            q = linear(x, self.proj_q1.weight).unsqueeze(1) + kqb[0][None, :, None, :]
+            k = linear(x, self.proj_k1.weight).unsqueeze(1) + kqb[1][None, :, None, :]
+            v = linear(x, self.proj_v.weight).view(B, T, H, d).transpose(1, 2)
             return q, k, v
-        q, k, v = F.linear(x, self.proj_qkv.weight).view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
+        q, k, v = linear(x, self.proj_qkv.weight).view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
         return q, k, v
 
     def _forward_composed(self, x: torch.Tensor) -> torch.Tensor:
@@ -488,4 +489,4 @@ class ThetaScan(nn.Module):
         if self.ogate is not None:
             y = y * self.ogate(x)
         y = y.transpose(1, 2).reshape(B, T, H * d)
-        return F.linear(y, self.proj_out.weight)
+        return linear(y, self.proj_out.weight)

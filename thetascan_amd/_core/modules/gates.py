@@ -6,6 +6,8 @@ from __future__ import annotations
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ..ops.linear import linear
+
 
 class _HeadLinear(nn.Module):
     def __init__(self, d_model: int, n_heads: int, out: int, bias_init: float):
@@ -17,7 +19,8 @@ class _HeadLinear(nn.Module):
 
     def forward(self, x):
         B, T, _ = x.shape
-        return self.lin(x).view(B, T, self.h, self.o).transpose(1, 2)
+        # split-K weight gradient and HIP bias column sums on the GPU
+        return linear(x, self.lin.weight, self.lin.bias).view(B, T, self.h, self.o).transpose(1, 2)
 
 
 class DecayGate(nn.Module):

@@ -52,11 +52,28 @@ def _desc(x, m, has_tau, s, inv_depth, eps):
 
 def contract_tokens(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """sum_n a[h, n, :]^T b[h, n, :] -> fp32 [H, p, q] for head-major token
-    tiles a [H, N, p], b [H, N, q].  The token axis is split into slices that
-    run as separate GEMM batches (split-K), so a handful of heads still fill
-    the GPU; the slice partials are summed in fp32."""
+    tiles a [H, N, p], b [H, N, q]: one ts_contract_tokens call (token
+    slices contracted on MFMA into fp32 partials, summed in slice order) for
+    widths that are multiples of 16 up to 128, else a split-K batched GEMM."""
     H, N, p = a.shape
     q = b.shape[-1]
+    if (a.is_cuda and a.dtype == b.dtype and a.dtype in (torch.bfloat16, torch.float32) and p % 16 == 0
+            and q % 16 == 0 and p <= 128 and q <= 128 and a.stride(-1) == 1 and b.stride(-1) == 1):
+        vec = 16 // a.element_size()
+        if (a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
+                and all(x % vec == 0 for x in (a.stride(0), a.stride(1), b.stride(0), b.stride(1)))):
+            lib = _lib.load()
+            desc = _lib.ContractDesc(H, N, p, q, _lib.dtype_code(a.dtype))
+            ws = ctypes.c_size_t()
+            _lib.check(lib.ts_contract_workspace_bytes(ctypes.byref(desc), ctypes.byref(ws)), "contract workspace")
+            work = torch.empty(ws.value, dtype=torch.uint8, device=a.device)
+            out = torch.empty(H, p, q, dtype=torch.float32, device=a.device)
+            with _lib.timed("ts_contract_tokens", lambda: _lib.nbytes(a, b, out)):
+                status = lib.ts_contract_tokens(ctypes.byref(desc), a.data_ptr(), a.stride(0), a.stride(1),
+                                                b.data_ptr(), b.stride(0), b.stride(1), out.data_ptr(),
+                                                work.data_ptr(), ws.value, _lib.stream_handle(a.device))
+            _lib.check(status, "ts_contract_tokens")
+            return out
     S = 1
     while S < 64 and H * S < 512 and N % (2 * S) == 0 and N // (2 * S) >= 256:
         S *= 2

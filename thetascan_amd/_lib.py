@@ -165,6 +165,11 @@ class QkNormDesc(ctypes.Structure):
                 ("dtype", ctypes.c_int32), ("rot", ctypes.c_int32), ("eps", ctypes.c_float)]
 
 
+class ContractDesc(ctypes.Structure):
+    _fields_ = [("G", ctypes.c_int32), ("N", ctypes.c_int32), ("p", ctypes.c_int32), ("q", ctypes.c_int32),
+                ("dtype", ctypes.c_int32)]
+
+
 class ReadBwdIO(ctypes.Structure):
     _fields_ = [
         ("num", Strided),
@@ -406,6 +411,10 @@ def load() -> ctypes.CDLL:
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_read_bwd_parts.argtypes = [P(ReadDesc), P(ctypes.c_int32)]
+        lib.ts_contract_workspace_bytes.argtypes = [P(ContractDesc), P(ctypes.c_size_t)]
+        lib.ts_contract_tokens.argtypes = [P(ContractDesc), ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                           ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_qknorm_fwd.argtypes = [P(QkNormDesc), Strided, Strided, ctypes.c_void_p, ctypes.c_void_p,
                                       ctypes.c_void_p]
         lib.ts_qknorm_bwd.argtypes = [P(QkNormDesc), Strided, Strided, Strided, ctypes.c_void_p, ctypes.c_void_p,

@@ -390,6 +390,26 @@ class _ScanViews(torch.autograd.Function):
         need_r = ctx.needs_input_grad[4:]
         B, H, T, dk = q.shape
         dv = v.shape[-1]
+        if n == 1 and not (retentions[0] is not None and need_r[0]) and (d_outs[0] is not None or d_mass[0] is not None):
+            # one view and no retention gradient: each gradient is one scan,
+            # stored in the input dtype (the same single rounding as an fp32
+            # accumulation cast at the end)
+            kind, r = ctx.kinds[0], retentions[0]
+            dO, dm = d_outs[0], d_mass[0]
+            if dO is None:
+                dO = torch.zeros(B, H, T, dv, dtype=q.dtype, device=q.device)
+            dO = dO.to(q.dtype)
+            rk = _ret_kwargs(kind, r)
+            q_ext = None if dm is None else dm.to(torch.float32)
+            gq = gk = gv = None
+            if need_q:
+                gq = scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if dm is not None else None)[0][..., :dk]
+            if need_k:
+                gk = scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if dm is not None else None,
+                                 k_ext=q_ext)[0][..., :dk]
+            if need_v:
+                gv = scan_launch(k, q, dO, **rk, reverse=True)[0][..., :dv]
+            return (gq, gk, gv, None, None)
         dq = torch.zeros(B, H, T, -(-dk // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
         dkk = torch.zeros_like(dq)
         dvv = torch.zeros(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)

@@ -334,6 +334,17 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
         if preacts is None:
             h, hq = features(a, b, Wg)
             base = _ein_w(W2, h, "hdm,bhtm->bhtd")
+            if (n_iter == 1 and not cfg.value_centers and x.is_cuda and x.dtype in (torch.bfloat16, torch.float32)
+                    and (not cfg.read_norm or cfg.read_norm_mode == "key_mass")):
+                # x + s (W2 h + num / (mass + eps)) per view on the HIP read
+                # kernel, the residual x + s W2 h formed once for every view
+                resid = torch.add(x, base, alpha=s)
+                keys, vals = streams.la2[l]
+                if cfg.read_norm:
+                    pairs = interface.scan_views_mass(group, hq.to(keys.dtype), keys, vals, "m")
+                else:
+                    pairs = [(num, None) for num in interface.scan_views(group, hq, keys, vals, "m")]
+                return [gn.normalized_read(num, mass, resid, s=s, eps=cfg.eps) for num, mass in pairs]
             return [x + s * (base + mem) for mem in memory(group, l, Wg, hq)]
         outputs = []
         for view, pre, one_b in zip(group, preacts, bs):

@@ -18,10 +18,18 @@ import torch
 import torch.nn.functional as F
 
 from . import gn, interface, kernel_features
+from .linear import head_matmul
 from ..modules.norms import rmsnorm
 
 
 def _ein_w(W, x, pat):
+    """Per-head GEMV of a [B,H,T,*] stream; the GPU forms run as batched GEMMs
+    (linear.head_matmul)."""
+    if x.is_cuda and x.ndim == 4 and W.ndim == 3 and W.shape[0] in (1, x.shape[1]):
+        if pat in ("hmd,bhtd->bhtm", "hdm,bhtm->bhtd"):
+            return head_matmul(x, W, True)
+        if pat == "hdm,bhtd->bhtm":
+            return head_matmul(x, W, False)
     if W.shape[0] == 1 and x.shape[1] != 1:
         W = W.expand(x.shape[1], -1, -1)
     return torch.einsum(pat, W, x)

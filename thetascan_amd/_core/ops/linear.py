@@ -106,3 +106,48 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     if not x.is_cuda:
         return F.linear(x, weight, bias)
     return _Linear.apply(x, weight, bias)
+
+
+class _HeadMatmul(torch.autograd.Function):
+    """y[b, h] = x[b, h] @ M[h] for a [B,H,T,K] stream and per-head (or shared)
+    matrices M [H or 1, K, N] (M = W^T or W): the fast-network GEMVs of the
+    composed path (engine.py:117-158, 180-195) as one batched GEMM per call,
+    without the permute copies of an einsum.  Both GEMMs take contiguous right
+    operands; the weight gradient is a token contraction per (batch, head)
+    (ts_contract_tokens) summed over the batch."""
+
+    @staticmethod
+    def forward(ctx, x, W, trans: bool):
+        B, H, T, K = x.shape
+        M = (W.transpose(-1, -2) if trans else W).to(x.dtype)
+        N = M.shape[-1]
+        Mb = M.expand(B, H, K, N).reshape(B * H, K, N).contiguous()
+        x3 = x.reshape(B * H, T, K)
+        if not x3.is_contiguous():
+            x3 = x3.contiguous()
+        y = torch.bmm(x3, Mb).view(B, H, T, N)
+        ctx.save_for_backward(x3, Mb)
+        ctx.meta = (B, H, T, K, N, W.shape[0], trans, W.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        from .gn import contract_tokens
+
+        x3, Mb = ctx.saved_tensors
+        B, H, T, K, N, Hw, trans, wdtype = ctx.meta
+        dy3 = dy.to(x3.dtype).reshape(B * H, T, N).contiguous()
+        dx = dW = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.bmm(dy3, Mb.transpose(1, 2).contiguous()).view(B, H, T, K)
+        if ctx.needs_input_grad[1]:
+            dM = contract_tokens(x3, dy3).view(B, H, K, N).sum(0)  # fp32 [H, K, N]
+            if Hw == 1:
+                dM = dM.sum(0, keepdim=True)
+            dW = (dM.transpose(-1, -2) if trans else dM).to(wdtype)
+        return dx, dW, None
+
+
+def head_matmul(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tensor:
+    """x [B,H,T,K] times W^T (``trans``, W [H|1, N, K]) or W (W [H|1, K, N]) per head."""
+    return _HeadMatmul.apply(x, W, trans)

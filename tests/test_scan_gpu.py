@@ -123,16 +123,17 @@ def test_value_slices_are_exact(cuda, split, Dv, seg_chunks, kind):
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
 @pytest.mark.parametrize("reverse", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_kept_segment_states_are_exact(cuda, kind, reverse, dtype):
+@pytest.mark.parametrize("D", [64, 128])
+def test_kept_segment_states_are_exact(cuda, kind, reverse, dtype, D):
     """A scan that reads the segment states an earlier scan left in its
     workspace (states_in=1), or those of the swapped scan read transposed
     (states_in=2: keys and values exchanged), equals the scan computed from
     scratch.  This is how the backward's dq (dv) scan reuses the forward's
-    (dk's) states."""
+    (dk's) states.  At D = 128 both scans run in two 64-column value slices."""
     from thetascan_amd._core.ops import scan_hip
     from thetascan_amd import _lib
 
-    B, H, T, D = 2, 3, 700, 64
+    B, H, T = 2, 3, 700
     q, k, v, w = (x.to(cuda, dtype) for x in _streams(B, H, T, D, D, seed=21) + (_streams(B, H, T, D, D, seed=22)[0],))
     ret = _retention(kind, B, H, T)
     kw = {"retention": {"none": _lib.RET_NONE, "static": _lib.RET_STATIC, "stream": _lib.RET_STREAM}[kind],

@@ -223,20 +223,35 @@ __host__ __device__ constexpr int scan_stages(int esize) { return esize == 2 ? 2
 
 // Float region after the E tiles (per stage: ke[C], ve[C]; then u[2][dvp],
 // D[2][DK], pw[68], lloc[4][C]).
-__host__ __device__ inline ScanLayout scan_layout(int esize, int DK, int dvp, bool main_kernel) {
+__host__ __device__ inline ScanLayout scan_layout_n(int esize, int DK, int dvp, int nst) {
   const int vec = 16 / esize;
   ScanLayout L{};
   L.kp = DK + vec;
   L.vp = dvp + vec;
   L.stage = C * L.kp + C * L.vp;
   L.stages = scan_stages(esize);
-  L.nst = main_kernel ? (esize == 2 ? 2 : 1) : 0;
+  L.nst = nst;
   L.st = dvp * L.kp;
   const int e_elems = L.stages * L.stage + L.nst * L.st;
   const int e_bytes = (e_elems * esize + 15) / 16 * 16;
   L.fbase = e_bytes / 4;
   const int floats = L.stages * 2 * C + 2 * dvp + 2 * DK + 68 + 4 * C;
   L.bytes = e_bytes + floats * 4;
+  return L;
+}
+
+// The main kernel double-buffers the published state (one barrier per tile)
+// unless that leaves a CU room for only one workgroup while a single copy
+// (one more barrier per tile) fits two: at 128-wide keys and 64 value
+// columns the two copies take 92 KB, one copy 75 KB of the CU's 160 KB.
+constexpr int kLdsPerCU = 160 * 1024;
+__host__ __device__ inline ScanLayout scan_layout(int esize, int DK, int dvp, bool main_kernel) {
+  if (!main_kernel) return scan_layout_n(esize, DK, dvp, 0);
+  ScanLayout L = scan_layout_n(esize, DK, dvp, esize == 2 ? 2 : 1);
+  if (L.nst == 2 && 2 * L.bytes > kLdsPerCU) {
+    const ScanLayout L1 = scan_layout_n(esize, DK, dvp, 1);
+    if (2 * L1.bytes <= kLdsPerCU) L = L1;
+  }
   return L;
 }
 
@@ -704,7 +719,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
     state_zero = false;
     if constexpr (MAIN) {
       if (c + 1 < c_end) {
-        if constexpr (STAGES == 1) __syncthreads();  // single state copy: readers of this tile are done
+        if (STAGES == 1 || L.nst == 1) __syncthreads();  // single state copy: readers of this tile are done
         publish((c + 1) & (L.nst - 1));
       }
     }
@@ -843,17 +858,21 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   const int bh = d->B * d->H;
   // Value slices: each workgroup carries the state of `vs` value columns, so
   // B*H*nvs scans run side by side (the slices of one (b, h) re-read its q / k
-  // tiles from L2).  Auto: one slice of the whole width -- at the benchmark
-  // shape time segments beat slices (46 us against 49 us for two slices and
+  // tiles from L2).  Auto: one slice of the whole width -- at 64-wide keys and
+  // values time segments beat slices (46 us against 49 us for two slices and
   // 68 us for four; a slice's 64-token steps are bound by the in-CU
-  // dependency chain, not by memory).
+  // dependency chain, not by memory) -- unless that tile leaves room for only
+  // one workgroup per CU: then 64-column slices (128-wide keys and values,
+  // B8 H8 T2048: 59 us against 82 us for one slice).
   if (d->value_split > 0) {
     const int v = d->value_split;
     if ((v != 16 && v != 32 && v != 64 && v != 128) || L->dvp % v)
       return fail(TS_ERR_VALUE, "scan: value_split %d must be 16, 32, 64 or 128 and divide %d", v, L->dvp);
     L->vs = v;
   } else {
+    const int esize = d->dtype == TS_BF16 ? 2 : 4;
     L->vs = L->dvp;
+    if (L->dvp == 128 && 2 * ts::scan_layout(esize, L->dkp, 128, true).bytes > ts::kLdsPerCU) L->vs = 64;
   }
   L->nvs = L->dvp / L->vs;
   L->nvw = L->vs <= 64 ? 1 : 2;
@@ -872,9 +891,9 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   L->nelem = L->dkp * L->dvp + L->dvp + L->dkp;
   if (d->states_in < 0 || d->states_in > 2) return fail(TS_ERR_VALUE, "scan: states_in must be 0, 1 or 2");
   if (d->states_in) {
-    if ((L->kx && d->states_in == 1) || L->vx || d->want_final || L->nvs != 1)
-      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment states need no value-side ext column, no "
-                                          "final state and the whole value width per workgroup");
+    if ((L->kx && d->states_in == 1) || L->vx || d->want_final)
+      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment states need no value-side ext column and no "
+                                          "final state");
     if (d->states_in == 2 && (d->dk != d->dv || L->dkp != L->dvp))
       return fail(TS_ERR_NOT_IMPLEMENTED, "scan: transposed segment states need dk == dv (a padded width)");
   }

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 4
+#define TS_ABI_VERSION 5
 
 enum ts_status {
   TS_OK = 0,
@@ -122,6 +122,42 @@ int ts_scan_workspace_bytes(const ts_scan_desc* desc, size_t* bytes);
  * denominator of the normalized read (src/thetascan/_core/ops/engine.py:419-442). */
 int ts_scan_fwd(const ts_scan_desc* desc, const ts_scan_io* io,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------ several retentions */
+
+#define TS_MAX_VIEWS 3
+
+typedef struct ts_scan_views_desc {
+  int32_t B, H, T;
+  int32_t dk, dv;       /* feature widths: dk <= 128, dv <= 64 (multiples of 8) */
+  int32_t dtype;        /* TS_BF16                                             */
+  int32_t n_views;      /* 2 .. TS_MAX_VIEWS                                   */
+  int32_t mass;         /* 1: v carries a unit ext column; each view also
+                           returns its key mass (out_ext)                      */
+  int32_t seg_chunks;   /* 64-token tiles per workgroup segment; 0 = auto      */
+} ts_scan_views_desc;
+
+typedef struct ts_scan_views_io {
+  ts_strided q, k, v;
+  const float* log_alpha[TS_MAX_VIEWS]; /* [H] static retention of view j;
+                                           NULL: no retention (plain sum)     */
+  ts_strided out[TS_MAX_VIEWS];         /* [B,H,T,dv] in the input dtype      */
+  ts_strided out_ext[TS_MAX_VIEWS];     /* fp32 [B,H,T] key mass (mass = 1)   */
+} ts_scan_views_io;
+
+/* Device workspace (bytes) ts_scan_views_fwd needs for `desc`. */
+int ts_scan_views_workspace_bytes(const ts_scan_views_desc* desc, size_t* bytes);
+
+/* The forward causal scans of n_views retentions (none or static [H]) over
+ * the same q, k, v in one pass: the multi-view call of
+ * scan_chunk.linattn_views (src/thetascan/_core/ops/scan_chunk.py:246-339,
+ * whose score tile S = Q K^T is shared by every view), as called by
+ * interface.scan_views for a temporal bank (interface.py:173-182).  q, k and
+ * v are read once per pass, the score tile is formed once per 64-token tile,
+ * and each view keeps its own fp32 state.  Results equal n_views calls of
+ * ts_scan_fwd with the same segmentation. */
+int ts_scan_views_fwd(const ts_scan_views_desc* desc, const ts_scan_views_io* io,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 
 /* ------------------------------------------------------------------ write */

@@ -37,4 +37,40 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared_functions() if not hasattr(lib, name)]
     assert not missing, missing
     lib.ts_abi_version.restype = ctypes.c_int
-    assert lib.ts_abi_version() == 4
+    assert lib.ts_abi_version() == 5
+
+
+def test_views_descriptor_validation_on_the_host():
+    """ts_scan_views_workspace_bytes checks the descriptor without touching a
+    GPU: unsupported view counts, dtypes and widths are refused with the
+    reference's error kinds, and the workspace holds one set of segment
+    summaries per view."""
+    import torch  # noqa: F401
+
+    from thetascan_amd import _lib
+
+    if not _lib.library_path().exists():
+        pytest.fail("libthetascan_hip.so is not built: run __graft_entry__.build()")
+    lib = _lib.load()
+
+    def ws(**kw):
+        fields = dict(B=2, H=8, T=32768, dk=128, dv=64, dtype=_lib.dtype_code(torch.bfloat16), n_views=3, mass=1,
+                      seg_chunks=0)
+        fields.update(kw)
+        desc = _lib.ScanViewsDesc(*fields.values())
+        out = ctypes.c_size_t()
+        return lib.ts_scan_views_workspace_bytes(ctypes.byref(desc), ctypes.byref(out)), out.value
+
+    rc, nbytes = ws()
+    assert rc == _lib.TS_OK
+    # 16 (batch, head) lanes, 512 tiles -> 32 segments of 16 tiles, 31 summaries kept;
+    # per segment: S [128][64] + u [64] + D [128] floats, plus one decay per segment
+    nseg, nelem = 32, 128 * 64 + 64 + 128
+    assert nbytes == 3 * (16 * nseg * nelem + 16 * nseg) * 4 + 256
+    assert ws(n_views=4)[0] == _lib.TS_ERR_NOT_IMPLEMENTED
+    assert ws(n_views=1)[0] == _lib.TS_ERR_NOT_IMPLEMENTED
+    assert ws(dtype=_lib.dtype_code(torch.float32))[0] == _lib.TS_ERR_NOT_IMPLEMENTED
+    assert ws(dv=72)[0] == _lib.TS_ERR_NOT_IMPLEMENTED
+    assert ws(dk=136)[0] == _lib.TS_ERR_NOT_IMPLEMENTED
+    assert ws(T=-1)[0] == _lib.TS_ERR_VALUE
+    assert ws(T=64) == (_lib.TS_OK, 0)  # one segment: no summaries

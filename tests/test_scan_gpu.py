@@ -242,6 +242,83 @@ def test_multi_view_matches_separate_views(cuda):
         assert rel_err(out, oracle.linattn_naive(q, k, v, _oracle_decay(ret, q))) < 1e-3
 
 
+VIEW_SHAPES = [
+    (2, 3, 700, 128, 64),  # the B-spline bank's widths, several segments, ragged last tile
+    (1, 2, 1100, 64, 64),  # 64-wide keys
+    (2, 2, 333, 40, 24),   # keys and values padded inside the tile
+    (1, 1, 64, 128, 64),   # exactly one tile
+    (1, 2, 5, 16, 8),      # a few tokens
+]
+
+
+@pytest.mark.parametrize("seg_chunks", [0, 3])
+@pytest.mark.parametrize("mass", [False, True])
+@pytest.mark.parametrize("n_views", [2, 3])
+@pytest.mark.parametrize("shape", VIEW_SHAPES)
+def test_views_scan_equals_one_view_scans(cuda, shape, n_views, mass, seg_chunks):
+    """ts_scan_views_fwd (one pass, the score tile shared by every retention)
+    gives each view exactly what ts_scan_fwd gives for that retention alone:
+    bit for bit, for the plain sum and static retentions, with and without
+    the key-mass column; and both match the float64 recurrence."""
+    from thetascan_amd._core.ops import scan_hip
+    from thetascan_amd import _lib
+
+    B, H, T, Dk, Dv = shape
+    q, k, v = (_rounded(x, torch.bfloat16) for x in _streams(B, H, T, Dk, Dv, seed=41))
+    if mass:
+        q, k = q.abs(), k.abs()
+    g = torch.Generator().manual_seed(5)
+    rets = [None] + [torch.log(torch.rand(H, generator=g, dtype=torch.float64) * 0.099 + 0.9)
+                     for _ in range(n_views - 1)]
+    rets_dev = [None if r is None else r.to(cuda, torch.float32) for r in rets]
+    qd, kd, vd = (x.to(cuda, torch.bfloat16) for x in (q, k, v))
+    outs, masses = scan_hip.scan_views_launch(qd, kd, vd, rets_dev, mass=mass, seg_chunks=seg_chunks)
+    assert (masses is not None) == mass
+    for j, (r, r_dev) in enumerate(zip(rets, rets_dev)):
+        kw = {"retention": _lib.RET_NONE} if r is None else {"retention": _lib.RET_STATIC, "log_alpha": r_dev}
+        one, one_mass, _ = scan_hip.scan_launch(qd, kd, vd, v_ext="ones" if mass else None, want_ext_out=mass,
+                                                seg_chunks=seg_chunks, **kw)
+        assert torch.equal(outs[j], one), (shape, n_views, j)
+        if mass:
+            assert torch.equal(masses[j], one_mass), (shape, n_views, j)
+        unit = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1) if mass else v
+        expected = oracle.linattn_naive(q, k, unit, _oracle_decay(r, q))
+        assert rel_err(outs[j], expected[..., :Dv]) < TOL[torch.bfloat16], (shape, j)
+        if mass:
+            assert rel_err(masses[j], expected[..., Dv]) < TOL[torch.bfloat16], (shape, j)
+
+
+def test_views_scan_serves_the_bank_views(cuda):
+    """linattn_views_mass with a plain and two static retentions (a two-rate
+    recency bank) takes the one-pass kernel and matches separate views."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dk, Dv = 1, 2, 300, 128, 64
+    q, k, v = (_rounded(x, torch.bfloat16).abs() for x in _streams(B, H, T, Dk, Dv, seed=43))
+    rets = (None, torch.log(torch.tensor([0.9, 0.95], dtype=torch.float64)),
+            torch.log(torch.tensor([0.999, 0.99], dtype=torch.float64)))
+    rets_dev = tuple(None if r is None else r.to(cuda, torch.float32) for r in rets)
+    qd, kd, vd = (x.to(cuda, torch.bfloat16) for x in (q, k, v))
+    calls = []
+    real = scan_hip.scan_views_launch
+
+    def spy(*a, **kw):
+        calls.append(1)
+        return real(*a, **kw)
+
+    scan_hip.scan_views_launch = spy
+    try:
+        pairs = scan_hip.linattn_views_mass(qd, kd, vd, rets_dev)
+    finally:
+        scan_hip.scan_views_launch = real
+    assert calls == [1]
+    unit = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1)
+    for (num, mass), r in zip(pairs, rets):
+        expected = oracle.linattn_naive(q, k, unit, _oracle_decay(r, q))
+        assert rel_err(num, expected[..., :Dv]) < TOL[torch.bfloat16]
+        assert rel_err(mass, expected[..., Dv]) < TOL[torch.bfloat16]
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_mass_column_matches_unit_value_column(cuda, dtype):
     """linattn_views_mass == scan against cat([v, 1]) (engine.py:430-442)."""

@@ -297,6 +297,59 @@ def _scan_once(
 _PLANS: dict = {}
 
 
+def views_eligible(q: torch.Tensor, v: torch.Tensor, kinds) -> bool:
+    """Whether ts_scan_views_fwd serves these views (bf16 on the GPU, 2..3
+    retentions that are none or static, dk <= 128, dv <= 64)."""
+    return (q.is_cuda and q.dtype == torch.bfloat16 and 2 <= len(kinds) <= _lib.MAX_VIEWS
+            and all(k in (_lib.RET_NONE, _lib.RET_STATIC) for k in kinds)
+            and q.shape[-1] <= 128 and v.shape[-1] <= 64)
+
+
+def scan_views_launch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, log_alphas, *, mass: bool,
+                      seg_chunks: int = 0):
+    """Forward causal scans of the same q, k, v under several retentions in one
+    pass (``log_alphas``: a per-head fp32 log-retention, or None for the plain
+    sum, per view).  Returns ``(outs, masses)`` (masses None without ``mass``);
+    each equals :func:`scan_launch` of that retention bit for bit."""
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    lib = _lib.load()
+    dtype = q.dtype
+    k = k.to(dtype)
+    v = v.to(dtype)
+    B, H, T, dk = q.shape
+    dv = v.shape[-1]
+    n = len(log_alphas)
+    vec = _vec(dtype)
+    dkw = -(-dk // vec) * vec
+    dvw = -(-dv // vec) * vec
+    qk, kk, vk = _kernel_view(q, dkw), _kernel_view(k, dkw), _kernel_view(v, dvw)
+    desc = _lib.ScanViewsDesc(B, H, T, dkw, dvw, _lib.dtype_code(dtype), n, int(mass), int(seg_chunks))
+    c_ws = ctypes.c_size_t()
+    _lib.check(lib.ts_scan_views_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan views workspace")
+    workspace = torch.empty(c_ws.value, dtype=torch.uint8, device=q.device) if c_ws.value else None
+    outs = [torch.empty(B, H, T, dvw, dtype=dtype, device=q.device) for _ in range(n)]
+    masses = [torch.empty(B, H, T, dtype=torch.float32, device=q.device) for _ in range(n)] if mass else None
+    las = [None if la is None else la.detach().to(device=q.device, dtype=torch.float32).reshape(H).contiguous()
+           for la in log_alphas]
+    io = _lib.ScanViewsIO()
+    io.q, io.k, io.v = _lib.strided(qk), _lib.strided(kk), _lib.strided(vk)
+    for j in range(n):
+        io.log_alpha[j] = las[j].data_ptr() if las[j] is not None else None
+        io.out[j] = _lib.strided(outs[j])
+        io.out_ext[j] = _lib.strided(masses[j] if mass else None)
+
+    def traffic():
+        return _lib.nbytes(q, k, v) + n * B * H * T * (dv * outs[0].element_size() + (4 if mass else 0))
+
+    with _lib.timed("ts_scan_views_fwd", traffic):
+        status = lib.ts_scan_views_fwd(ctypes.byref(desc), ctypes.byref(io),
+                                       workspace.data_ptr() if workspace is not None else None, c_ws.value,
+                                       _lib.stream_handle(q.device))
+    _lib.check(status, "ts_scan_views_fwd")
+    return [o[..., :dv] for o in outs], masses
+
+
 def workspace_for(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, seg_chunks: int = 0,
                   retention: int = _lib.RET_NONE, reverse: bool = False, v_ext: bool = False,
                   kx: bool = False) -> torch.Tensor | None:
@@ -365,15 +418,21 @@ class _ScanViews(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, with_mass, *retentions):
         kinds = [_classify(r, q) for r in retentions]
-        outs, masses = [], []
-        for kind, r in zip(kinds, retentions):
-            out, mass, _ = scan_launch(
-                q, k, v, **_ret_kwargs(kind, r),
-                v_ext="ones" if with_mass else None, want_ext_out=with_mass,
-            )
-            outs.append(out)
-            if with_mass:
-                masses.append(mass)
+        if views_eligible(q, v, kinds):
+            # one pass for every retention: the score tile is formed once
+            outs, masses = scan_views_launch(q, k, v, [r if kd == _lib.RET_STATIC else None
+                                                       for kd, r in zip(kinds, retentions)], mass=with_mass)
+            masses = masses or []
+        else:
+            outs, masses = [], []
+            for kind, r in zip(kinds, retentions):
+                out, mass, _ = scan_launch(
+                    q, k, v, **_ret_kwargs(kind, r),
+                    v_ext="ones" if with_mass else None, want_ext_out=with_mass,
+                )
+                outs.append(out)
+                if with_mass:
+                    masses.append(mass)
         ctx.kinds = kinds
         ctx.with_mass = with_mass
         ctx.n_views = len(retentions)

@@ -67,6 +67,34 @@ class ScanDesc(ctypes.Structure):
     ]
 
 
+MAX_VIEWS = 3
+
+
+class ScanViewsDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("dk", ctypes.c_int32),
+        ("dv", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("n_views", ctypes.c_int32),
+        ("mass", ctypes.c_int32),
+        ("seg_chunks", ctypes.c_int32),
+    ]
+
+
+class ScanViewsIO(ctypes.Structure):
+    _fields_ = [
+        ("q", Strided),
+        ("k", Strided),
+        ("v", Strided),
+        ("log_alpha", ctypes.c_void_p * MAX_VIEWS),
+        ("out", Strided * MAX_VIEWS),
+        ("out_ext", Strided * MAX_VIEWS),
+    ]
+
+
 class ScanIO(ctypes.Structure):
     _fields_ = [
         ("q", Strided),
@@ -404,6 +432,9 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         P = ctypes.POINTER
+        lib.ts_scan_views_workspace_bytes.argtypes = [P(ScanViewsDesc), P(ctypes.c_size_t)]
+        lib.ts_scan_views_fwd.argtypes = [P(ScanViewsDesc), P(ScanViewsIO), ctypes.c_void_p, ctypes.c_size_t,
+                                          ctypes.c_void_p]
         lib.ts_feature_fwd.argtypes = [P(FeatureDesc), P(FeatureIO), ctypes.c_void_p]
         lib.ts_feature_bwd.argtypes = [P(FeatureDesc), P(FeatureBwdIO), ctypes.c_void_p]
         lib.ts_feature_bwd_parts.argtypes = [P(FeatureDesc), ctypes.c_int32, P(ctypes.c_int32)]
@@ -442,7 +473,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 4:
+        if lib.ts_abi_version() != 5:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

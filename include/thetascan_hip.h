@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 5
+#define TS_ABI_VERSION 6
 
 enum ts_status {
   TS_OK = 0,
@@ -82,6 +82,14 @@ typedef struct ts_scan_desc {
                            ext row u is then the swapped scan's value-side ext
                            state.  Skips the summary and prefix passes.  No
                            value-side ext column (nor key-side with 1).      */
+  int32_t init_state;   /* 1: io->init_state holds the state entering the first
+                           token (a continued sequence; 0 = a zero state).
+                           The first token's decay applies to it, so a scan
+                           of x[T0:] from the final state of x[:T0] equals
+                           the tail of the scan of x (a reversed scan's first
+                           step carries no per-token decay: its caller
+                           applies the decay linking the pieces).  Not with
+                           states_in.                                        */
 } ts_scan_desc;
 
 typedef struct ts_scan_io {
@@ -92,6 +100,7 @@ typedef struct ts_scan_io {
   ts_strided out;                 /* [B,H,T,dv]                                */
   ts_strided out_ext;             /* fp32 [B,H,T]: result column dv (or NULL) */
   float* final_state;             /* fp32 [B*H, dk_pad, dv_pad] (or NULL)      */
+  const float* init_state;        /* fp32 [B*H, dk_pad, dv_pad] (init_state)   */
 } ts_scan_io;
 
 /* ABI version (TS_ABI_VERSION). */

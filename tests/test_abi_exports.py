@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared_functions() if not hasattr(lib, name)]
     assert not missing, missing
     lib.ts_abi_version.restype = ctypes.c_int
-    assert lib.ts_abi_version() == 5
+    assert lib.ts_abi_version() == 6
 
 
 def test_views_descriptor_validation_on_the_host():
@@ -74,3 +74,26 @@ def test_views_descriptor_validation_on_the_host():
     assert ws(dk=136)[0] == _lib.TS_ERR_NOT_IMPLEMENTED
     assert ws(T=-1)[0] == _lib.TS_ERR_VALUE
     assert ws(T=64) == (_lib.TS_OK, 0)  # one segment: no summaries
+
+
+def test_initial_state_rules_on_the_host():
+    """An initial state needs a workspace even for one segment, and is refused
+    together with kept segment states."""
+    import torch  # noqa: F401
+
+    from thetascan_amd import _lib
+
+    lib = _lib.load()
+
+    def ws(**kw):
+        f = dict(B=1, H=2, T=50, dk=64, dv=64, dtype=0, retention=0, reverse=0, q_ext=0, k_ext=0, v_ext=0,
+                 out_mode=0, out_scale=1.0, seg_chunks=0, want_final=0, value_split=0, states_in=0, init_state=0)
+        f.update(kw)
+        desc = _lib.ScanDesc(*f.values())
+        out = ctypes.c_size_t()
+        return lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(out)), out.value
+
+    assert ws() == (_lib.TS_OK, 0)  # one segment, nothing carried
+    rc, nbytes = ws(init_state=1)
+    assert rc == _lib.TS_OK and nbytes >= 2 * (64 * 64 + 64 + 64) * 4
+    assert ws(init_state=1, states_in=1)[0] == _lib.TS_ERR_NOT_IMPLEMENTED

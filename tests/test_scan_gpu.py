@@ -449,3 +449,91 @@ def test_errors_match_the_reference(cuda):
         scan_hip.linattn(q, k, v, log_alpha=torch.zeros(3, device=cuda))
     with pytest.raises(RuntimeError, match="GPU"):
         scan_hip.linattn(q.cpu(), k.cpu(), v.cpu())
+
+
+def _ret_for(kind, r, lo, hi, cuda):
+    """The retention of tokens lo:hi (static: all of it) on the GPU."""
+    if r is None:
+        return None
+    if r.ndim == 1:
+        return r.to(cuda, torch.float32)
+    return r[:, :, lo:hi].to(cuda, torch.float32).contiguous()
+
+
+@pytest.mark.parametrize("mass", [False, True])
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_scan_continues_from_a_carried_state(cuda, dtype, kind, mass):
+    """Streaming: scanning the pieces of a sequence in order, each from the
+    state the previous piece ended in (ragged pieces, a piece shorter than a
+    tile, single-token decode steps), gives the scan of the whole sequence
+    and its final state (the recurrence S_t = a_t S_{t-1} + k_t v_t^T)."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dk, Dv = 2, 3, 1000, 64, 48
+    q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, Dk, Dv, seed=51))
+    if mass:
+        q, k = q.abs(), k.abs()
+    ret = _retention(kind, B, H, T, seed=52)
+    cuts = [0, 517, 560, 995, 996, 997, 998, 999, 1000]
+    outs, masses, state = [], [], None
+    for lo, hi in zip(cuts[:-1], cuts[1:]):
+        out, m, state = scan_hip.linattn_state(q[:, :, lo:hi].to(cuda, dtype), k[:, :, lo:hi].to(cuda, dtype),
+                                               v[:, :, lo:hi].to(cuda, dtype), _ret_for(kind, ret, lo, hi, cuda),
+                                               state, mass=mass)
+        outs.append(out)
+        if mass:
+            masses.append(m)
+    got = torch.cat(outs, dim=2)
+    unit = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1) if mass else v
+    expected = oracle.linattn_naive(q, k, unit, _oracle_decay(ret, q))
+    assert rel_err(got, expected[..., :Dv]) < TOL[dtype], (kind, dtype)
+    if mass:
+        assert rel_err(torch.cat(masses, dim=2), expected[..., Dv]) < TOL[dtype], (kind, dtype)
+    # the final state: S_T = sum_i w(T-1, i) k_i v_i^T (+ the key-mass column sum_i w k_i)
+    decay = _oracle_decay(ret, q)
+    w = torch.ones(B, H, T, dtype=torch.float64) if decay is None else \
+        torch.exp(decay[..., 0].flip(-1).cumsum(-1).flip(-1) - decay[..., 0])
+    S = torch.einsum("bht,bhtk,bhtv->bhkv", w, k, unit)
+    assert state.shape == (B, H, Dk, Dv + (1 if mass else 0))
+    assert rel_err(state, S) < (1e-4 if dtype == torch.float32 else 1e-2), (kind, dtype)
+
+
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+def test_sequence_sharded_scan_equals_the_whole_scan(cuda, kind):
+    """The sequence-sharding design on one GPU: P shards scan their slices
+    from zero and report their final states; an exclusive combine of those
+    carries (each decayed by the later shards' retention) gives each shard its
+    incoming state; re-scanning every shard from it reproduces the whole
+    scan.  This is the step an all-gather of carries across GPUs would feed."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, D = 1, 2, 1200, 64
+    q, k, v = _streams(B, H, T, D, D, seed=61, dtype=torch.float32)
+    ret = _retention(kind, B, H, T, seed=62)
+    bounds = [0, 300, 650, 900, 1200]
+    # 1. every shard from zero: its carry U_p and its total log-decay
+    carries, logs = [], []
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        _, _, fin = scan_hip.linattn_state(q[:, :, lo:hi].to(cuda), k[:, :, lo:hi].to(cuda), v[:, :, lo:hi].to(cuda),
+                                           _ret_for(kind, ret, lo, hi, cuda), None)
+        carries.append(fin)
+        if ret is None:
+            logs.append(torch.zeros(B, H, device=cuda))
+        elif ret.ndim == 1:
+            logs.append((ret.to(cuda, torch.float32) * (hi - lo)).view(1, H).expand(B, H))
+        else:
+            logs.append(ret[:, :, lo:hi, 0].sum(-1).to(cuda, torch.float32))
+    # 2. exclusive combine: S_in(p) = exp(L_{p-1}) S_in(p-1) + U_{p-1}
+    s_in = [None]
+    for p in range(1, len(carries)):
+        prev = torch.zeros_like(carries[0]) if s_in[-1] is None else s_in[-1]
+        s_in.append(torch.exp(logs[p - 1]).view(B, H, 1, 1) * prev + carries[p - 1])
+    # 3. every shard from its incoming state
+    outs = []
+    for p, (lo, hi) in enumerate(zip(bounds[:-1], bounds[1:])):
+        out, _, _ = scan_hip.linattn_state(q[:, :, lo:hi].to(cuda), k[:, :, lo:hi].to(cuda), v[:, :, lo:hi].to(cuda),
+                                           _ret_for(kind, ret, lo, hi, cuda), s_in[p])
+        outs.append(out)
+    expected = oracle.linattn_naive(q.double(), k.double(), v.double(), _oracle_decay(ret, q.double()))
+    assert rel_err(torch.cat(outs, dim=2), expected) < 1e-4, kind

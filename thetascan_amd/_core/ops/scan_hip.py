@@ -105,6 +105,7 @@ def scan_launch(
     value_split: int = 0,
     workspace: torch.Tensor | None = None,
     states_in: int = 0,
+    init_state: torch.Tensor | None = None,
 ):
     """One scan (several kernel launches when a width exceeds ``MAX_WIDTH``).
 
@@ -118,15 +119,15 @@ def scan_launch(
     recomputing them -- single-launch widths only.
     """
     dk, dv = q.shape[-1], v.shape[-1]
-    if workspace is not None or states_in:
+    if workspace is not None or states_in or init_state is not None:
         if dk > MAX_WIDTH or dv > MAX_WIDTH:
-            raise NotImplementedError("hip scan: kept segment states need widths up to 128")
+            raise NotImplementedError("hip scan: kept segment states and initial states need widths up to 128")
     if dk <= MAX_WIDTH and dv <= MAX_WIDTH:
         return _scan_once(q, k, v, retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse,
                           q_ext=q_ext, k_ext=k_ext, v_ext=v_ext, out=out, out_mode=out_mode, out_scale=out_scale,
                           want_ext_out=want_ext_out, ext_out=ext_out, want_final=want_final,
                           seg_chunks=seg_chunks, value_split=value_split, workspace=workspace,
-                          states_in=states_in)
+                          states_in=states_in, init_state=init_state)
     if want_final:
         raise NotImplementedError(f"hip scan: final state of widths dk={dk} dv={dv} above {MAX_WIDTH}")
     kw = dict(retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse, seg_chunks=seg_chunks,
@@ -191,6 +192,7 @@ def _scan_once(
     value_split: int = 0,
     workspace: torch.Tensor | None = None,
     states_in: int = 0,
+    init_state: torch.Tensor | None = None,
 ):
     """One kernel launch.  Returns ``(out, ext_out, final_state)``.
 
@@ -223,7 +225,8 @@ def _scan_once(
     ve_mode, ve = _ext_arg(v_ext)
 
     fields = (B, H, T, dkw, dvw, code, retention, int(reverse), qe_mode, ke_mode, ve_mode,
-              out_mode, float(out_scale), int(seg_chunks), int(want_final), int(value_split), int(states_in))
+              out_mode, float(out_scale), int(seg_chunks), int(want_final), int(value_split), int(states_in),
+              int(init_state is not None))
     desc = _lib.ScanDesc(*fields)
     plan = _PLANS.get(fields)
     if plan is None:
@@ -253,6 +256,12 @@ def _scan_once(
     final = None
     if want_final:
         final = torch.zeros(B * H, dk_pad, dv_pad, dtype=torch.float32, device=q.device)
+    init = None
+    if init_state is not None:
+        if tuple(init_state.shape[-2:]) != (dk_pad, dv_pad) or init_state.numel() != B * H * dk_pad * dv_pad:
+            raise ValueError(f"hip scan: initial state of shape {tuple(init_state.shape)}, "
+                             f"expected [{B}, {H}, {dk_pad}, {dv_pad}]")
+        init = init_state.detach().to(device=q.device, dtype=torch.float32).contiguous()
     if workspace is not None:
         if workspace.numel() * workspace.element_size() < ws_bytes:
             raise ValueError("hip scan: workspace too small")
@@ -274,6 +283,7 @@ def _scan_once(
         _lib.strided(out_buf),
         _lib.strided(ext_out if want_ext_out else None),
         final.data_ptr() if final is not None else None,
+        init.data_ptr() if init is not None else None,
     )
     def traffic():
         rw = 2 if out_mode == _lib.OUT_ACCUM_F32 else 1
@@ -590,3 +600,25 @@ def final_state(
     if with_mass:
         state = torch.cat([state, fin[:, :, :dk, dvw:dvw + 1]], dim=-1)
     return state
+
+
+def linattn_state(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, retention=None, state=None, *,
+                  mass: bool = False):
+    """Continue a causal scan from a carried state (forward only, for streaming).
+
+    ``state`` is the fp32 ``[B, H, dk(+1), dv(+1)]`` state after the tokens
+    already seen (None: a fresh sequence); ``retention`` is None, a static
+    ``[H]`` log-retention or a per-token ``[B, H, T, 1]`` one for these tokens.
+    With ``mass`` the value stream carries the unit column of the key-mass read
+    (its row sums come back as ``mass`` and its column rides in the state).
+    Returns ``(out, mass or None, new_state)``; feeding the pieces of a
+    sequence through this in order gives exactly the scan of the whole
+    sequence (``scan_naive.py:5-18``: S_t = a_t S_{t-1} + k_t v_t^T), so a
+    decode step is a call with T = 1.
+    """
+    kind = _classify(retention, q)
+    with torch.no_grad():
+        out, ext, final = scan_launch(q, k, v, **_ret_kwargs(kind, retention), v_ext="ones" if mass else None,
+                                      want_ext_out=mass, want_final=True, init_state=state)
+    return out, ext, final
+

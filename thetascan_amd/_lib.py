@@ -64,6 +64,7 @@ class ScanDesc(ctypes.Structure):
         ("want_final", ctypes.c_int32),
         ("value_split", ctypes.c_int32),
         ("states_in", ctypes.c_int32),
+        ("init_state", ctypes.c_int32),
     ]
 
 
@@ -108,6 +109,7 @@ class ScanIO(ctypes.Structure):
         ("out", Strided),
         ("out_ext", Strided),
         ("final_state", ctypes.c_void_p),
+        ("init_state", ctypes.c_void_p),
     ]
 
 
@@ -473,7 +475,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 5:
+        if lib.ts_abi_version() != 6:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

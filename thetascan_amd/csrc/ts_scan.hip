@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
     }
   };
 
-  if (MAIN && seg > 0) {
+  if (MAIN && (seg > 0 || p.has_init)) {
     state_zero = false;
     const float* src = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)p.nelem;
 #pragma unroll
@@ -591,29 +591,37 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 // [dk + kx][dv + vx] layout (ext row / column last).
 struct FinalP {
   float* fin;
+  const float* init;  // the state entering the first token, same layout as fin (or null)
   int DK, dvp, dk, dv, kx, vx;
 };
+
+// Element e of the segment-state layout ([DK][dvp] S, [dvp] u, [DK] D) in the
+// exact [dk + kx][dv + vx] layout of a final / initial state, or -1.
+__device__ __forceinline__ int exact_index(const FinalP& F, int e) {
+  const int cols = F.dv + F.vx;
+  const int ns = F.DK * F.dvp;
+  if (e < ns) {
+    const int f = e / F.dvp, v = e - f * F.dvp;
+    return f < F.dk && v < F.dv ? f * cols + v : -1;
+  }
+  if (e < ns + F.dvp) {
+    const int v = e - ns;
+    return F.kx && v < F.dv ? F.dk * cols + v : -1;
+  }
+  const int f = e - ns - F.dvp;
+  return F.vx && f < F.dk ? f * cols + F.dv : -1;
+}
 
 __global__ void scan_prefix_kernel(float* seg, const float* segdec, FinalP F, int nseg, int nsum, int nelem) {
   const int bh = blockIdx.y;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= nelem) return;
-  const float carry = segment_prefix(seg + (size_t)bh * nseg * nelem + e, segdec + (size_t)bh * nseg, nseg, nsum, nelem);
-  if (F.fin) {
-    const int rows = F.dk + F.kx, cols = F.dv + F.vx;
-    float* out = F.fin + (size_t)bh * rows * cols;
-    const int ns = F.DK * F.dvp;
-    if (e < ns) {
-      const int f = e / F.dvp, v = e - f * F.dvp;
-      if (f < F.dk && v < F.dv) out[f * cols + v] = carry;
-    } else if (e < ns + F.dvp) {
-      const int v = e - ns;
-      if (F.kx && v < F.dv) out[F.dk * cols + v] = carry;
-    } else {
-      const int f = e - ns - F.dvp;
-      if (F.vx && f < F.dk) out[f * cols + F.dv] = carry;
-    }
-  }
+  const size_t state = (size_t)bh * (F.dk + F.kx) * (F.dv + F.vx);
+  const int x = exact_index(F, e);
+  const float carry0 = F.init && x >= 0 ? F.init[state + x] : 0.0f;
+  const float carry = segment_prefix(seg + (size_t)bh * nseg * nelem + e, segdec + (size_t)bh * nseg, nseg, nsum,
+                                     nelem, carry0);
+  if (F.fin && x >= 0) F.fin[state + x] = carry;
 }
 
 }  // namespace ts
@@ -726,8 +734,10 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
     if (d->states_in == 2 && (d->dk != d->dv || L->dkp != L->dvp))
       return fail(TS_ERR_NOT_IMPLEMENTED, "scan: transposed segment states need dk == dv (a padded width)");
   }
+  if (d->init_state && d->states_in)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: an initial state with given segment states");
   L->ws_bytes = 0;
-  if (L->nsum > 0)
+  if (L->nsum > 0 || d->init_state)
     L->ws_bytes = (size_t)bh * L->nseg * (size_t)L->nelem * sizeof(float) + (size_t)bh * L->nseg * sizeof(float) + 256;
   return TS_OK;
 }
@@ -868,6 +878,7 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   if (d->retention == TS_RET_STATIC && !io->log_alpha) return fail(TS_ERR_VALUE, "scan: missing log_alpha");
   if (d->retention == TS_RET_STREAM && !io->decay.ptr) return fail(TS_ERR_VALUE, "scan: missing decay stream");
   if (d->want_final && !io->final_state) return fail(TS_ERR_VALUE, "scan: missing final_state buffer");
+  if (d->init_state && !io->init_state) return fail(TS_ERR_VALUE, "scan: missing init_state buffer");
   if (L.ws_bytes > 0 && (!workspace || ws_bytes < L.ws_bytes))
     return fail(TS_ERR_VALUE, "scan: workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
                 (long long)L.ws_bytes);
@@ -917,10 +928,11 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
                 (long long)lds_main, L.dkp, L.vs);
 
   p.states_t = d->states_in == 2;
-  if (L.nsum > 0 && d->states_in == 0) {
-    if ((rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p))) return rc;
-    ts::FinalP F{d->want_final ? io->final_state : nullptr, L.dkp, L.dvp, d->dk, d->dv, L.kx ? 1 : 0,
-                 L.vx ? 1 : 0};
+  p.has_init = d->init_state ? 1 : 0;
+  if ((L.nsum > 0 || d->init_state) && d->states_in == 0) {
+    if (L.nsum > 0 && (rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p))) return rc;
+    ts::FinalP F{d->want_final ? io->final_state : nullptr, d->init_state ? io->init_state : nullptr, L.dkp, L.dvp,
+                 d->dk, d->dv, L.kx ? 1 : 0, L.vx ? 1 : 0};
     hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
                        p.segdec, F, L.nseg, L.nsum, L.nelem);
     hipError_t e = hipGetLastError();

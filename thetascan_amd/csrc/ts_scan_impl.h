@@ -47,6 +47,7 @@ struct ScanP {
   int B, H, T, dk, dv, dvp;  // dvp: padded value width of the whole scan
   int vs;                    // padded value columns per workgroup (blockIdx.z selects the slice)
   int states_t;              // segment states read transposed (those of the swapped scan)
+  int has_init;              // segment 0 also starts from a given state (the prefix wrote it)
   int nchunks, seg_chunks, nseg, nsum, nelem;
   int ret, reverse;
   int q_ext, k_ext, v_ext;
@@ -175,10 +176,12 @@ struct TileLoader {
 // Exclusive scan of one element of the segment summaries of one (batch, head)
 // (`base` points at that element of segment 0, summaries `nelem` apart):
 // segment p receives the state entering it, sum over q < p of U_q times the
-// decay of segments q+1 .. p-1 (exp of the per-segment log decays `dec`).
-// Returns the state after the last summarised segment.
-__device__ __forceinline__ float segment_prefix(float* base, const float* dec, int nseg, int nsum, int nelem) {
-  float carry = 0.0f;
+// decay of segments q+1 .. p-1 (exp of the per-segment log decays `dec`),
+// plus `carry0` (the state entering segment 0) times the decay of segments
+// 0 .. p-1.  Returns the state after the last summarised segment.
+__device__ __forceinline__ float segment_prefix(float* base, const float* dec, int nseg, int nsum, int nelem,
+                                                float carry0 = 0.0f) {
+  float carry = carry0;
   for (int s = 0; s < nseg; ++s) {
     float u = 0.0f;
     if (s < nsum) u = base[(size_t)s * nelem];

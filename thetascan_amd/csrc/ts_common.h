@@ -13,6 +13,23 @@ int fail(int code, const char* fmt, ...);
 // launches, including launches recorded into a graph, skip the call).
 hipError_t ensure_lds_limit(const void* fn, int bytes);
 
+// One ts_sum_slots call's arguments (host side).
+struct SlotSum {
+  const float* a;
+  int32_t na;
+  const float* b;
+  int32_t nb;
+  int64_t n;
+  void* out;
+  int32_t out_dtype;
+  float scale;
+};
+constexpr int kMaxSlotJobs = 4;
+
+// Several independent slot sums in one launch (each result equal to its own
+// ts_sum_slots call); falls back to separate calls when one cannot be batched.
+int sum_slots_batch(const SlotSum* jobs, int njobs, hipStream_t stream);
+
 typedef __bf16 bf16;
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

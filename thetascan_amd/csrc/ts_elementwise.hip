@@ -403,13 +403,12 @@ __global__ __launch_bounds__(256) void sum_slots_kernel(const float* a, int na, 
 // the result does not depend on timing.  R grows with the slot count when
 // there are few columns, so a wide sum and a tall one both fill the chip.
 template <int R>
-__global__ __launch_bounds__(256) void sum_slots_vec_kernel(const float* a, int na, const float* b, int nb,
-                                                            int64_t nv, void* out, int out_bf16, float scale) {
+__device__ __forceinline__ void sum_slots_block(const float* a, int na, const float* b, int nb, int64_t nv, void* out,
+                                                int out_bf16, float scale, int64_t blk, floatx4* red) {
   constexpr int CPB = 256 / R;
-  __shared__ floatx4 red[256];
   const int tid = threadIdx.x;
   const int cl = tid % CPB, r = tid / CPB;
-  const int64_t v = (int64_t)blockIdx.x * CPB + cl;
+  const int64_t v = blk * CPB + cl;
   const int total = na + nb;
   floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   if (v < nv) {
@@ -439,6 +438,41 @@ __global__ __launch_bounds__(256) void sum_slots_vec_kernel(const float* a, int 
     } else {
       ((floatx4*)out)[v] = sum;
     }
+  }
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void sum_slots_vec_kernel(const float* a, int na, const float* b, int nb,
+                                                            int64_t nv, void* out, int out_bf16, float scale) {
+  __shared__ floatx4 red[256];
+  sum_slots_block<R>(a, na, b, nb, nv, out, out_bf16, scale, blockIdx.x, red);
+}
+
+// Several slot sums in one launch: block ranges [first[j], first[j+1]) belong
+// to job j, which runs the one-launch kernel's code with its own R, so each
+// result equals that of a separate ts_sum_slots call bit for bit.
+struct SlotJobs {
+  const float* a[kMaxSlotJobs];
+  const float* b[kMaxSlotJobs];
+  void* out[kMaxSlotJobs];
+  int64_t nv[kMaxSlotJobs];
+  int na[kMaxSlotJobs], nb[kMaxSlotJobs], R[kMaxSlotJobs], ob[kMaxSlotJobs];
+  float scale[kMaxSlotJobs];
+  int first[kMaxSlotJobs + 1];
+  int n;
+};
+
+__global__ __launch_bounds__(256) void sum_slots_multi_kernel(SlotJobs J) {
+  __shared__ floatx4 red[256];
+  int j = 0;
+  while (j + 1 < J.n && (int)blockIdx.x >= J.first[j + 1]) ++j;  // uniform per block
+  const int64_t blk = (int64_t)blockIdx.x - J.first[j];
+  switch (J.R[j]) {
+    case 1: sum_slots_block<1>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    case 2: sum_slots_block<2>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    case 4: sum_slots_block<4>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    case 8: sum_slots_block<8>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    default: sum_slots_block<16>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
   }
 }
 
@@ -619,6 +653,60 @@ int qknorm_launch(const ts_qknorm_desc* d, ts_strided x, ts_strided dy, ts_strid
 
 }  // namespace
 
+namespace ts {
+
+// Slot rows per column of the vectorised sum: enough threads to fill the chip,
+// at most one slot per row step.
+static int slot_rows(int64_t nv, int total) {
+  int R = 1;
+  while (R < 16 && R < total && nv * R < 65536) R <<= 1;
+  return R;
+}
+
+static bool slot_vec_ok(const float* a, const float* b, int64_t n, const void* out, int32_t out_dtype) {
+  return n % 4 == 0 && !((uintptr_t)a & 15u) && !((uintptr_t)b & 15u) &&
+         !((uintptr_t)out & (out_dtype == TS_BF16 ? 7u : 15u));
+}
+
+int sum_slots_batch(const SlotSum* jobs, int njobs, hipStream_t stream) {
+  SlotJobs J;
+  memset(&J, 0, sizeof(J));
+  bool batch = njobs <= kMaxSlotJobs;
+  for (int i = 0; i < njobs && batch; ++i) {
+    const SlotSum& s = jobs[i];
+    batch = s.n > 0 && s.na + s.nb > 0 && (s.na == 0 || s.a) && (s.nb == 0 || s.b) && s.out &&
+            (s.out_dtype == TS_BF16 || s.out_dtype == TS_F32) && slot_vec_ok(s.a, s.b, s.n, s.out, s.out_dtype);
+  }
+  if (!batch) {
+    for (int i = 0; i < njobs; ++i) {
+      const SlotSum& s = jobs[i];
+      const int rc = ts_sum_slots(s.a, s.na, s.b, s.nb, s.n, s.out, s.out_dtype, s.scale, stream);
+      if (rc) return rc;
+    }
+    return TS_OK;
+  }
+  int blocks = 0;
+  for (int i = 0; i < njobs; ++i) {
+    const SlotSum& s = jobs[i];
+    J.a[i] = s.a; J.b[i] = s.b; J.out[i] = s.out; J.na[i] = s.na; J.nb[i] = s.nb;
+    J.nv[i] = s.n / 4;
+    J.R[i] = slot_rows(J.nv[i], s.na + s.nb);
+    J.ob[i] = s.out_dtype == TS_BF16 ? 1 : 0;
+    J.scale[i] = s.scale;
+    J.first[i] = blocks;
+    blocks += (int)((J.nv[i] + 256 / J.R[i] - 1) / (256 / J.R[i]));
+  }
+  J.first[njobs] = blocks;
+  J.n = njobs;
+  if (blocks == 0) return TS_OK;
+  hipLaunchKernelGGL(sum_slots_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, J);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "sum_slots: launch failed: %s", hipGetErrorString(e));
+  return TS_OK;
+}
+
+}  // namespace ts
+
 extern "C" {
 
 int ts_read_fwd(const ts_read_desc* d, const ts_read_io* io, hipStream_t stream) {
@@ -686,13 +774,11 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
   if (out_dtype != TS_BF16 && out_dtype != TS_F32) return fail(TS_ERR_VALUE, "sum_slots: unknown dtype");
   if (n == 0) return TS_OK;
   const int total = na + nb;
-  const bool vec = n % 4 == 0 && !((uintptr_t)a & 15u) && !((uintptr_t)b & 15u) &&
-                   !((uintptr_t)out & (out_dtype == TS_BF16 ? 7u : 15u));
+  const bool vec = ts::slot_vec_ok(a, b, n, out, out_dtype);
   if (vec && total > 0) {
     // slot rows per column: enough threads to fill the chip, at most one slot per row step
     const int64_t nv = n / 4;
-    int R = 1;
-    while (R < 16 && R < total && nv * R < 65536) R <<= 1;
+    const int R = ts::slot_rows(nv, total);
     const int cpb = 256 / R;
     const dim3 grid((unsigned)((nv + cpb - 1) / cpb));
     const int ob = out_dtype == TS_BF16 ? 1 : 0;

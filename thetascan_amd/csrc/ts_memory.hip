@@ -273,10 +273,6 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
   s.q = phk; s.k = phq; s.v = dnum; s.out = gr->dv;
   if ((rc = ts_scan_fwd(&P.sdv, &s, wsb, P.ws_b, stream))) return rc;
 
-  if (gb_parts &&
-      (rc = ts_sum_slots(gb_parts, P.col_slices, nullptr, 0, (int64_t)f.H * f.d, gr->dg_bias, d->param_dtype,
-                         1.0f, stream)))
-    return rc;
 
   // feature backwards with per-workgroup weight-gradient slots
   const bool want_k = gr->dw1 || gr->dtau;
@@ -299,11 +295,15 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
   if (want_q) { bq.dw1_part = w1q; bq.dw2_part = w2q; bq.dtau_part = tq; }
   if ((rc = ts_feature_bwd(&f, &bq, stream))) return rc;
 
+  // every weight-gradient sum (gate bias, W1, W2, tau) in one launch
   const int64_t hmd = (int64_t)f.H * f.m * f.d;
-  if (gr->dw1 && (rc = ts_sum_slots(w1k, P.pk, w1q, P.pq, hmd, gr->dw1, d->param_dtype, 1.0f, stream))) return rc;
-  if (gr->dw2 && (rc = ts_sum_slots(w2q, P.pq, nullptr, 0, hmd, gr->dw2, d->param_dtype, 1.0f, stream))) return rc;
-  if (gr->dtau && (rc = ts_sum_slots(tk, P.pk, tq, P.pq, f.H, gr->dtau, d->param_dtype, 1.0f, stream))) return rc;
-  return TS_OK;
+  ts::SlotSum jobs[ts::kMaxSlotJobs];
+  int njobs = 0;
+  if (gb_parts) jobs[njobs++] = {gb_parts, P.col_slices, nullptr, 0, (int64_t)f.H * f.d, gr->dg_bias, d->param_dtype, 1.0f};
+  if (gr->dw1) jobs[njobs++] = {w1k, P.pk, w1q, P.pq, hmd, gr->dw1, d->param_dtype, 1.0f};
+  if (gr->dw2) jobs[njobs++] = {w2q, P.pq, nullptr, 0, hmd, gr->dw2, d->param_dtype, 1.0f};
+  if (gr->dtau) jobs[njobs++] = {tk, P.pk, tq, P.pq, f.H, gr->dtau, d->param_dtype, 1.0f};
+  return ts::sum_slots_batch(jobs, njobs, stream);
 }
 
 }  // extern "C"

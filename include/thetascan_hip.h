@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 6
+#define TS_ABI_VERSION 7
 
 enum ts_status {
   TS_OK = 0,
@@ -131,6 +131,26 @@ int ts_scan_workspace_bytes(const ts_scan_desc* desc, size_t* bytes);
  * denominator of the normalized read (src/thetascan/_core/ops/engine.py:419-442). */
 int ts_scan_fwd(const ts_scan_desc* desc, const ts_scan_io* io,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Two plain scans over the same keys and values up to a swap, in one pass:
+ *
+ *   out_a_t = sum_{i<=t} <qa_t, k_i> v_i,   out_b_t = sum_{i<=t} <qb_t, v_i> k_i
+ *
+ * (anti-causal with desc->reverse).  These are the backward's dk and dv scans
+ * of a kernel memory (scan_hip._ScanViews.backward; the reference's autograd
+ * of scan_chunk.linattn_views, scan_chunk.py:246-339): k = dnum, v = phi(q),
+ * qa = v, qb = phi(k).  K and V are read once and the state is updated once
+ * per tile; each output equals its own ts_scan_fwd call.  desc describes
+ * scan A (q = qa): bf16, no retention, no ext columns, TS_OUT_STORE,
+ * dk == dv == 64; workspace from ts_scan_workspace_bytes(desc). */
+typedef struct ts_scan_pair_io {
+  ts_strided qa, k, v, qb;
+  ts_strided out_a;               /* [B,H,T,dv]                                */
+  ts_strided out_b;               /* [B,H,T,dk]                                */
+} ts_scan_pair_io;
+
+int ts_scan_pair_fwd(const ts_scan_desc* desc, const ts_scan_pair_io* io,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------ several retentions */
 

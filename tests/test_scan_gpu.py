@@ -537,3 +537,48 @@ def test_sequence_sharded_scan_equals_the_whole_scan(cuda, kind):
         outs.append(out)
     expected = oracle.linattn_naive(q.double(), k.double(), v.double(), _oracle_decay(ret, q.double()))
     assert rel_err(torch.cat(outs, dim=2), expected) < 1e-4, kind
+
+
+@pytest.mark.parametrize("reverse", [True, False])
+@pytest.mark.parametrize("seg_chunks", [0, 1, 3])
+@pytest.mark.parametrize("T", [700, 64, 5, 4096])
+def test_pair_scan_equals_its_two_scans(cuda, T, seg_chunks, reverse):
+    """ts_scan_pair_fwd (the backward's dk and dv scans in one pass: K and V
+    read once, one state) gives scan(qa, k, v) and scan(qb, v, k) bit for bit
+    as two ts_scan_fwd calls do, and both match the float64 recurrence."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, D = 2, 3, 64
+    g = torch.Generator().manual_seed(71 + T)
+    qa, k, v, qb = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64).to(torch.bfloat16).to(torch.float64)
+                    for _ in range(4))
+    dev = [x.to(cuda, torch.bfloat16) for x in (qa, k, v, qb)]
+    a, b = scan_hip.scan_pair_launch(*dev, reverse=reverse, seg_chunks=seg_chunks)
+    ref_a, _, _ = scan_hip.scan_launch(dev[0], dev[1], dev[2], reverse=reverse, seg_chunks=seg_chunks)
+    ref_b, _, _ = scan_hip.scan_launch(dev[3], dev[2], dev[1], reverse=reverse, seg_chunks=seg_chunks)
+    assert torch.equal(a, ref_a) and torch.equal(b, ref_b), (T, seg_chunks, reverse)
+
+    def naive(q, kk, vv):
+        if reverse:
+            return oracle.linattn_naive(q.flip(2), kk.flip(2), vv.flip(2)).flip(2)
+        return oracle.linattn_naive(q, kk, vv)
+
+    if T <= 700:
+        assert rel_err(a, naive(qa, k, v)) < TOL[torch.bfloat16]
+        assert rel_err(b, naive(qb, v, k)) < TOL[torch.bfloat16]
+
+
+def test_pair_scan_writes_strided_outputs(cuda):
+    """The dv output goes straight into a strided view of the qkv gradient."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, D = 2, 4, 300, 64
+    g = torch.Generator().manual_seed(77)
+    qa, k, v, qb = (torch.randn(B, H, T, D, generator=g).to(cuda, torch.bfloat16) for _ in range(4))
+    big = torch.zeros(B, T, 3, H, D, dtype=torch.bfloat16, device=cuda)
+    view = big[:, :, 2].transpose(1, 2)
+    _, b = scan_hip.scan_pair_launch(qa, k, v, qb, reverse=True, out_b=view)
+    ref_b, _, _ = scan_hip.scan_launch(qb, v, k, reverse=True)
+    assert b.data_ptr() == view.data_ptr()
+    assert torch.equal(view, ref_b)
+    assert not big[:, :, :2].any()

@@ -515,12 +515,17 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
                                         states_in=2 if ws_f is not None else 0)
     # dk = reverse scan(v, dnum, phi_q) and dv = reverse scan(phi_k, phi_q, dnum) share
     # their segment states up to a transpose (sum_i dnum_i phi_q_i^T)
-    ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=st.seg_chunks, reverse=True, kx=norm) \
-        if ws_f is not None else None
-    dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
-                                        k_ext=q_ext, seg_chunks=st.seg_chunks, workspace=ws_r)
-    scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=st.seg_chunks,
-                         workspace=ws_r, states_in=2 if ws_r is not None else 0)
+    if not norm and scan_hip.pair_eligible(v, dnum, phi_q, phi_k):
+        # both in one pass over dnum and phi_q
+        dphi_k, _ = scan_hip.scan_pair_launch(v, dnum, phi_q, phi_k, reverse=True, seg_chunks=st.seg_chunks,
+                                              out_b=dv)
+    else:
+        ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=st.seg_chunks, reverse=True, kx=norm) \
+            if ws_f is not None else None
+        dphi_k, _, _ = scan_hip.scan_launch(v, dnum, phi_q, reverse=True, q_ext="ones" if norm else None,
+                                            k_ext=q_ext, seg_chunks=st.seg_chunks, workspace=ws_r)
+        scan_hip.scan_launch(phi_k, phi_q, dnum, reverse=True, out=dv, seg_chunks=st.seg_chunks,
+                             workspace=ws_r, states_in=2 if ws_r is not None else 0)
     need_tau = st.has_tau and need_tau
     want_k = need_w1 or need_tau
     want_q = need_w1 or need_w2 or need_tau

@@ -68,6 +68,10 @@ class ScanDesc(ctypes.Structure):
     ]
 
 
+class ScanPairIO(ctypes.Structure):
+    _fields_ = [(n, Strided) for n in ("qa", "k", "v", "qb", "out_a", "out_b")]
+
+
 MAX_VIEWS = 3
 
 
@@ -434,6 +438,7 @@ def load() -> ctypes.CDLL:
             ctypes.c_void_p,
         ]
         P = ctypes.POINTER
+        lib.ts_scan_pair_fwd.argtypes = [P(ScanDesc), P(ScanPairIO), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_scan_views_workspace_bytes.argtypes = [P(ScanViewsDesc), P(ctypes.c_size_t)]
         lib.ts_scan_views_fwd.argtypes = [P(ScanViewsDesc), P(ScanViewsIO), ctypes.c_void_p, ctypes.c_size_t,
                                           ctypes.c_void_p]
@@ -475,7 +480,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 6:
+        if lib.ts_abi_version() != 7:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

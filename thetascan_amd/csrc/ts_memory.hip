@@ -266,12 +266,18 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
   if (rc) return rc;
   // dphi_k = reverse scan(v, dnum, phi_q); dv = reverse scan(phi_k, phi_q, dnum)
   // reads its segment states transposed (sum_i dnum_i phi_q_i^T)
-  memset(&s, 0, sizeof(s));
-  s.q = io->v; s.k = dnum; s.v = phq; s.k_ext = dmass; s.out = dphk;
-  if ((rc = ts_scan_fwd(&P.sdk, &s, wsb, P.ws_b, stream))) return rc;
-  memset(&s, 0, sizeof(s));
-  s.q = phk; s.k = phq; s.v = dnum; s.out = gr->dv;
-  if ((rc = ts_scan_fwd(&P.sdv, &s, wsb, P.ws_b, stream))) return rc;
+  if (!d->normalize && f.d == 64 && f.m == 64 && f.dtype == TS_BF16) {
+    // both in one pass over dnum and phi_q (the state updated once per tile)
+    const ts_scan_pair_io pio = {io->v, dnum, phq, phk, dphk, gr->dv};
+    if ((rc = ts_scan_pair_fwd(&P.sdk, &pio, wsb, P.ws_b, stream))) return rc;
+  } else {
+    memset(&s, 0, sizeof(s));
+    s.q = io->v; s.k = dnum; s.v = phq; s.k_ext = dmass; s.out = dphk;
+    if ((rc = ts_scan_fwd(&P.sdk, &s, wsb, P.ws_b, stream))) return rc;
+    memset(&s, 0, sizeof(s));
+    s.q = phk; s.k = phq; s.v = dnum; s.out = gr->dv;
+    if ((rc = ts_scan_fwd(&P.sdv, &s, wsb, P.ws_b, stream))) return rc;
+  }
 
 
   // feature backwards with per-workgroup weight-gradient slots

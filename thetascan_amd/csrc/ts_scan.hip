@@ -586,6 +586,211 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
   }
 }
 
+// Two plain scans that share keys and values up to a swap, in one pass:
+//   A: out_a_t = sum_i <qa_t, k_i> v_i   (state S = sum_i k_i v_i^T)
+//   B: out_b_t = sum_i <qb_t, v_i> k_i   (state S^T)
+// with the same causal (or anti-causal) order.  These are the backward's dk
+// and dv scans of a kernel memory (keys dnum, values phi(q); queries v and
+// phi(k)).  K and V tiles are read once, S is updated once per tile, both
+// score blocks stay in accumulators, and scan B reads the published state
+// copy transposed (ds_read_b64_tr_b16) instead of carrying S^T.  Each output
+// is computed in the order its own one-scan kernel uses.  Plain retention,
+// no ext columns, bf16, dk = dv = DK; segment states come from scan A's
+// summary and prefix passes.
+struct PairP {
+  ScanP s;           // q = qa, k, v, out = out_a (and the segmentation)
+  ts_strided qb, ob;
+  uint32_t qb_rec, ob_rec;
+};
+
+template <int DK>
+__global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
+  typedef bf16 E;
+  typedef bf16x8 F8;
+  typedef LdsIO<E> IO;
+  typedef Tok<E> TK;
+  constexpr int ES = 2;
+  constexpr int VEC = 8;
+  constexpr int NK32 = DK / 32;
+  constexpr int NKB = DK / 16;
+  constexpr int SLOTS_K = (C * DK / VEC + 255) / 256;
+  const ScanP& p = pp.s;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int g = lane >> 4;
+  const int l16 = lane & 15;
+  const int seg = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int sgn = p.reverse ? -1 : 1;
+  const int wave_first = __builtin_amdgcn_readfirstlane(tid & ~63);
+  const int nvb = DK / 16;
+
+  const ScanLayout L = scan_layout(ES, DK, DK, true);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* ebase = (E*)smem;
+  E* st_base = ebase + L.stages * L.stage;
+
+  const int64_t bh_q = (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
+  const int64_t bh_b = (int64_t)b * pp.qb.sb + (int64_t)h * pp.qb.sh;
+  const int64_t bh_k = (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
+  const int64_t bh_v = (int64_t)b * p.v.sb + (int64_t)h * p.v.sh;
+  const int q_st_b = (int)p.q.st * ES;
+  const int b_st_b = (int)pp.qb.st * ES;
+  const int k_st_b = (int)p.k.st * ES;
+  const int v_st_b = (int)p.v.st * ES;
+  auto k_rsrc = [&]() { return make_rsrc((const E*)p.k.ptr + bh_k, p.k_rec); };
+  auto v_rsrc = [&]() { return make_rsrc((const E*)p.v.ptr + bh_v, p.v_rec); };
+
+  // state: value block w of S, every key block
+  floatx4 S[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) S[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int c_begin = seg * p.seg_chunks;
+  const int c_end = min(c_begin + p.seg_chunks, p.nchunks);
+  bool state_zero = true;
+  if (seg > 0) {
+    state_zero = false;
+    const float* src = p.seg + ((size_t)bh * p.nseg + seg) * (size_t)p.nelem;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[kb][i] = src[(kb * 16 + 4 * g + i) * p.dvp + w * 16 + l16];
+  }
+  auto publish = [&](int bi) {
+    E* st = st_base + bi * L.st;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      IO::st4(st + (w * 16 + l16) * L.kp + kb * 16 + 4 * g, S[kb][0], S[kb][1], S[kb][2], S[kb][3]);
+  };
+
+  const int nk_vec = C * (DK / VEC);
+  TileLoader<E, SLOTS_K> ldk;
+  TileLoader<E, SLOTS_K> ldv;
+  ldk.setup(p, DK / VEC, p.dk, L.kp, k_st_b, tid);
+  ldv.setup(p, DK / VEC, p.dv, L.vp, v_st_b, tid);
+  auto fetch = [&](int t0) {
+    ldk.fetch(k_rsrc(), t0, sgn, k_st_b, wave_first, nk_vec);
+    ldv.fetch(v_rsrc(), t0, sgn, v_st_b, wave_first, nk_vec);
+  };
+  auto store = [&](int stg) {
+    E* base = ebase + stg * L.stage;
+    ldk.store(base, wave_first, nk_vec);
+    ldv.store(base + C * L.kp, wave_first, nk_vec);
+  };
+
+  // queries of this wave's block, for both scans
+  F8 qa[NK32], qb[NK32];
+  auto qload = [&](int t0) {
+    const int row = w * 16 + l16;
+    const rsrc_t ra = make_rsrc((const E*)p.q.ptr + bh_q, p.q_rec);
+    const rsrc_t rb = make_rsrc((const E*)pp.qb.ptr + bh_b, pp.qb_rec);
+    const uint32_t oa = row_off(p, t0, row, q_st_b), ob = row_off(p, t0, row, b_st_b);
+    auto part = [&](rsrc_t r, uint32_t ro, int c) -> bf16x4 {
+      return __builtin_bit_cast(bf16x4, bld8(r, ro + (uint32_t)(c * ES)));
+    };
+#pragma unroll
+    for (int j = 0; j < NK32; ++j) {
+      qa[j] = IO::cat(part(ra, oa, 32 * j + 4 * g), part(ra, oa, 32 * j + 16 + 4 * g));
+      qb[j] = IO::cat(part(rb, ob, 32 * j + 4 * g), part(rb, ob, 32 * j + 16 + 4 * g));
+    }
+  };
+
+  const void* oa_base = bh_base(p.out, b, h, ES);
+  const void* ob_base = bh_base(pp.ob, b, h, ES);
+  const int oa_st_b = (int)p.out.st * ES;
+  const int ob_st_b = (int)pp.ob.st * ES;
+
+  fetch(c_begin * C);
+  store(c_begin & 1);
+  if (c_begin + 1 < c_end) fetch((c_begin + 1) * C);
+  qload(c_begin * C);
+  if (!state_zero) publish(c_begin & 1);
+  __syncthreads();
+
+  for (int c = c_begin; c < c_end; ++c) {
+    const int t0 = c * C;
+    if (c + 1 < c_end) store((c + 1) & 1);
+    if (c + 2 < c_end) fetch(t0 + 2 * C);
+    const E* Ks = ebase + (c & 1) * L.stage;
+    const E* Vs = Ks + C * L.kp;
+    const E* st = st_base + (c & 1) * L.st;
+    const int query = w * 16 + l16;
+
+    // causal score blocks of this wave's queries against keys k (A) and v (B)
+    floatx4 sa[4], sb[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      sa[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      sb[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (kb > w) continue;
+      const int krow = kb * 16 + l16;
+#pragma unroll
+      for (int j = 0; j < NK32; ++j) sa[kb] = mma32(frow8<E>(Ks, L.kp, krow, j, g), qa[j], sa[kb]);
+#pragma unroll
+      for (int j = 0; j < NK32; ++j) sb[kb] = mma32(frow8<E>(Vs, L.vp, krow, j, g), qb[j], sb[kb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb * 16 + 4 * g + i;
+        const bool keep = kb < w || key <= query;
+        sa[kb][i] = keep ? sa[kb][i] : 0.0f;
+        sb[kb][i] = keep ? sb[kb][i] : 0.0f;
+      }
+    }
+    const F8 pa0 = IO::from_acc(sa[0], sa[1]), pa1 = IO::from_acc(sa[2], sa[3]);
+    const F8 pb0 = IO::from_acc(sb[0], sb[1]), pb1 = IO::from_acc(sb[2], sb[3]);
+
+    const uint32_t roa = row_off(p, t0, query, oa_st_b);
+    const uint32_t rob = row_off(p, t0, query, ob_st_b);
+    const rsrc_t oa_rs = make_rsrc(oa_base, p.out_rec);
+    const rsrc_t ob_rs = make_rsrc(ob_base, pp.ob_rec);
+#pragma unroll
+    for (int vb = 0; vb < nvb; ++vb) {
+      // A: O^T[v][query] = (S^T qa^T)[v] + (V^T Pa^T)[v]
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (!state_zero) {
+#pragma unroll
+        for (int j = 0; j < NK32; ++j) acc = mma32(frow8<E>(st, L.kp, vb * 16 + l16, j, g), qa[j], acc);
+      }
+      acc = mma32(TK::col8(Vs, L.vp, vb * 16, 0, lane), pa0, acc);
+      if (w >= 2) acc = mma32(TK::col8(Vs, L.vp, vb * 16, 1, lane), pa1, acc);
+      // B: O^T[k][query] = (S qb^T)[k] (state copy read transposed) + (K^T Pb^T)[k]
+      floatx4 accb = {0.f, 0.f, 0.f, 0.f};
+      if (!state_zero) {
+#pragma unroll
+        for (int j = 0; j < NK32; ++j) accb = mma32(TK::col8(st, L.kp, vb * 16, j, lane), qb[j], accb);
+      }
+      accb = mma32(TK::col8(Ks, L.kp, vb * 16, 0, lane), pb0, accb);
+      if (w >= 2) accb = mma32(TK::col8(Ks, L.kp, vb * 16, 1, lane), pb1, accb);
+      const int ocol = vb * 16 + 4 * g;
+      bf16x4 oa, ob;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        oa[i] = (bf16)acc[i];
+        ob[i] = (bf16)accb[i];
+      }
+      bst8(oa_rs, ocol < p.dv ? roa + (uint32_t)(ocol * ES) : kOOB, __builtin_bit_cast(uint2, oa));
+      bst8(ob_rs, ocol < p.dk ? rob + (uint32_t)(ocol * ES) : kOOB, __builtin_bit_cast(uint2, ob));
+    }
+    if (c + 1 < c_end) qload(t0 + C);
+
+    // S += K^T V (value block w), once for both scans
+    F8 av[2];
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp) av[kp] = TK::col8(Vs, L.vp, w * 16, kp, lane);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) S[kb] = mma32(TK::col8(Ks, L.kp, kb * 16, kp, lane), av[kp], S[kb]);
+    state_zero = false;
+    if (c + 1 < c_end) publish((c + 1) & 1);
+    __syncthreads();
+  }
+}
+
 // Exclusive scan of the segment summaries:  seg[p] <- state entering segment p.
 // With `fin`, the state after the last token is also written in the exact
 // [dk + kx][dv + vx] layout (ext row / column last).
@@ -852,6 +1057,64 @@ int ts_scan_workspace_bytes(const ts_scan_desc* desc, size_t* bytes) {
   int rc = compute_layout(desc, &L);
   if (rc) return rc;
   if (bytes) *bytes = L.ws_bytes;
+  return TS_OK;
+}
+
+int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* workspace, size_t ws_bytes,
+                     hipStream_t stream) {
+  Layout L;
+  int rc = compute_layout(d, &L);
+  if (rc) return rc;
+  if (!io) return fail(TS_ERR_VALUE, "scan pair: null io");
+  if (d->dtype != TS_BF16 || d->retention != TS_RET_NONE || L.kx || L.vx || d->out_mode != TS_OUT_STORE ||
+      d->dk != 64 || d->dv != 64 || L.nvs != 1 || d->states_in || d->want_final || d->init_state)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan pair: bf16 plain scans of 64-wide keys and values only");
+  if (d->T == 0) return TS_OK;
+  int rc2;
+  if ((rc2 = check_stream("qa", io->qa, 8, true)) || (rc2 = check_stream("k", io->k, 8, true)) ||
+      (rc2 = check_stream("v", io->v, 8, true)) || (rc2 = check_stream("qb", io->qb, 8, true)))
+    return rc2;
+  for (const ts_strided* o : {&io->out_a, &io->out_b})
+    if (!o->ptr || ((uintptr_t)o->ptr & 7u) || o->st % 8 || o->sh % 8 || o->sb % 8)
+      return fail(TS_ERR_VALUE, "scan pair: outputs must be 16-byte aligned rows");
+  if (L.ws_bytes > 0 && (!workspace || ws_bytes < L.ws_bytes))
+    return fail(TS_ERR_VALUE, "scan pair: workspace too small (%zu < %zu bytes)", ws_bytes, L.ws_bytes);
+
+  ts::PairP pp;
+  memset(&pp, 0, sizeof(pp));
+  ts::ScanP& p = pp.s;
+  p.B = d->B; p.H = d->H; p.T = d->T; p.dk = d->dk; p.dv = d->dv; p.dvp = L.dvp; p.vs = L.vs;
+  p.nchunks = L.nchunks; p.seg_chunks = L.seg_chunks; p.nseg = L.nseg; p.nsum = L.nsum; p.nelem = L.nelem;
+  p.ret = TS_RET_NONE; p.reverse = d->reverse;
+  p.q_ext = p.k_ext = p.v_ext = TS_EXT_NONE;
+  p.out_mode = TS_OUT_STORE; p.out_scale = 1.0f;
+  p.q = io->qa; p.k = io->k; p.v = io->v; p.out = io->out_a;
+  pp.qb = io->qb; pp.ob = io->out_b;
+  if ((rc = slice_bytes("qa", p.q, d->T, d->dk, 2, &p.q_rec))) return rc;
+  if ((rc = slice_bytes("k", p.k, d->T, d->dk, 2, &p.k_rec))) return rc;
+  if ((rc = slice_bytes("v", p.v, d->T, d->dv, 2, &p.v_rec))) return rc;
+  if ((rc = slice_bytes("qb", pp.qb, d->T, d->dv, 2, &pp.qb_rec))) return rc;
+  if ((rc = slice_bytes("out_a", p.out, d->T, d->dv, 2, &p.out_rec))) return rc;
+  if ((rc = slice_bytes("out_b", pp.ob, d->T, d->dk, 2, &pp.ob_rec))) return rc;
+  if (L.ws_bytes > 0) {
+    p.seg = (float*)workspace;
+    p.segdec = p.seg + (size_t)d->B * d->H * L.nseg * (size_t)L.nelem;
+  }
+  const int bh = d->B * d->H;
+  const ts::ScanLayout SL = ts::scan_layout(2, 64, 64, true);
+  if (SL.nst != 2) return fail(TS_ERR_RUNTIME, "scan pair: unexpected state buffering");
+  if (L.nsum > 0) {
+    KernelFn fsum = pick_kernel(true, 64, 1, false, ts::kPlain);
+    if ((rc = launch(fsum, dim3(L.nsum, bh, 1), (size_t)ts::scan_layout(2, 64, 64, false).bytes, stream, p))) return rc;
+    ts::FinalP F{nullptr, nullptr, L.dkp, L.dvp, d->dk, d->dv, 0, 0};
+    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
+                       p.segdec, F, L.nseg, L.nsum, L.nelem);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: prefix launch failed: %s", hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(ts::pair_kernel<64>, dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: launch failed: %s", hipGetErrorString(e));
   return TS_OK;
 }
 

@@ -179,14 +179,31 @@ struct TileLoader {
 // decay of segments q+1 .. p-1 (exp of the per-segment log decays `dec`),
 // plus `carry0` (the state entering segment 0) times the decay of segments
 // 0 .. p-1.  Returns the state after the last summarised segment.
+// Segments are taken eight at a time with all their summaries and decays
+// loaded before any of their states is stored, so the loads of a block are in
+// flight together instead of each waiting behind the previous store.
 __device__ __forceinline__ float segment_prefix(float* base, const float* dec, int nseg, int nsum, int nelem,
                                                 float carry0 = 0.0f) {
+  // Loads past the last summary re-read summary nsum-1 (in bounds) and are
+  // discarded, which keeps the loads free of branches.
+  constexpr int K = 8;
   float carry = carry0;
-  for (int s = 0; s < nseg; ++s) {
-    float u = 0.0f;
-    if (s < nsum) u = base[(size_t)s * nelem];
-    base[(size_t)s * nelem] = carry;
-    if (s < nsum) carry = expf(dec[s]) * carry + u;
+  for (int s0 = 0; s0 < nseg; s0 += K) {
+    float u[K], e[K];
+    if (nsum > 0) {  // uniform
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const int sc = min(s0 + j, nsum - 1);
+        u[j] = base[(size_t)sc * nelem];
+        e[j] = dec[sc];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int s = s0 + j;
+      if (s < nseg) base[(size_t)s * nelem] = carry;
+      if (s < nsum) carry = expf(e[j]) * carry + u[j];
+    }
   }
   return carry;
 }

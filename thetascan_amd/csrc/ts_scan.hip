@@ -817,16 +817,27 @@ __device__ __forceinline__ int exact_index(const FinalP& F, int e) {
   return F.vx && f < F.dk ? f * cols + F.dv : -1;
 }
 
+// Four consecutive elements per thread (nelem is a multiple of 16).
 __global__ void scan_prefix_kernel(float* seg, const float* segdec, FinalP F, int nseg, int nsum, int nelem) {
   const int bh = blockIdx.y;
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= nelem) return;
+  const int e0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (e0 >= nelem) return;
   const size_t state = (size_t)bh * (F.dk + F.kx) * (F.dv + F.vx);
-  const int x = exact_index(F, e);
-  const float carry0 = F.init && x >= 0 ? F.init[state + x] : 0.0f;
-  const float carry = segment_prefix(seg + (size_t)bh * nseg * nelem + e, segdec + (size_t)bh * nseg, nseg, nsum,
-                                     nelem, carry0);
-  if (F.fin && x >= 0) F.fin[state + x] = carry;
+  int x[4];
+  float c0[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = exact_index(F, e0 + i);
+    c0[i] = F.init && x[i] >= 0 ? F.init[state + x[i]] : 0.0f;
+  }
+  const float4 carry = segment_prefix4(seg + (size_t)bh * nseg * nelem + e0, segdec + (size_t)bh * nseg, nseg, nsum,
+                                       nelem, make_float4(c0[0], c0[1], c0[2], c0[3]));
+  const float c[4] = {carry.x, carry.y, carry.z, carry.w};
+  if (F.fin) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (x[i] >= 0) F.fin[state + x[i]] = c[i];
+  }
 }
 
 }  // namespace ts
@@ -1079,6 +1090,7 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
       return fail(TS_ERR_VALUE, "scan pair: outputs must be 16-byte aligned rows");
   if (L.ws_bytes > 0 && (!workspace || ws_bytes < L.ws_bytes))
     return fail(TS_ERR_VALUE, "scan pair: workspace too small (%zu < %zu bytes)", ws_bytes, L.ws_bytes);
+  if (L.ws_bytes > 0 && !aligned16(workspace)) return fail(TS_ERR_VALUE, "scan pair: workspace is not 16-byte aligned");
 
   ts::PairP pp;
   memset(&pp, 0, sizeof(pp));
@@ -1107,7 +1119,7 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
     KernelFn fsum = pick_kernel(true, 64, 1, false, ts::kPlain);
     if ((rc = launch(fsum, dim3(L.nsum, bh, 1), (size_t)ts::scan_layout(2, 64, 64, false).bytes, stream, p))) return rc;
     ts::FinalP F{nullptr, nullptr, L.dkp, L.dvp, d->dk, d->dv, 0, 0};
-    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
+    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem / 4 + 255) / 256, bh), dim3(256), 0, stream, p.seg,
                        p.segdec, F, L.nseg, L.nsum, L.nelem);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: prefix launch failed: %s", hipGetErrorString(e));
@@ -1145,6 +1157,7 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   if (L.ws_bytes > 0 && (!workspace || ws_bytes < L.ws_bytes))
     return fail(TS_ERR_VALUE, "scan: workspace too small (%lld < %lld bytes)", (long long)ws_bytes,
                 (long long)L.ws_bytes);
+  if (L.ws_bytes > 0 && !aligned16(workspace)) return fail(TS_ERR_VALUE, "scan: workspace is not 16-byte aligned");
 
   ts::ScanP p;
   memset(&p, 0, sizeof(p));
@@ -1196,7 +1209,7 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
     if (L.nsum > 0 && (rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p))) return rc;
     ts::FinalP F{d->want_final ? io->final_state : nullptr, d->init_state ? io->init_state : nullptr, L.dkp, L.dvp,
                  d->dk, d->dv, L.kx ? 1 : 0, L.vx ? 1 : 0};
-    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem + 255) / 256, bh), dim3(256), 0, stream, p.seg,
+    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem / 4 + 255) / 256, bh), dim3(256), 0, stream, p.seg,
                        p.segdec, F, L.nseg, L.nsum, L.nelem);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: prefix launch failed: %s", hipGetErrorString(e));

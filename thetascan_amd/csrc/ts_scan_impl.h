@@ -173,6 +173,11 @@ struct TileLoader {
   }
 };
 
+// One segment of the prefix: the state entering the next segment.
+__device__ __forceinline__ float prefix_step(float carry, float log_dec, float u) {
+  return expf(log_dec) * carry + u;
+}
+
 // Exclusive scan of one element of the segment summaries of one (batch, head)
 // (`base` points at that element of segment 0, summaries `nelem` apart):
 // segment p receives the state entering it, sum over q < p of U_q times the
@@ -202,7 +207,39 @@ __device__ __forceinline__ float segment_prefix(float* base, const float* dec, i
     for (int j = 0; j < K; ++j) {
       const int s = s0 + j;
       if (s < nseg) base[(size_t)s * nelem] = carry;
-      if (s < nsum) carry = expf(e[j]) * carry + u[j];
+      if (s < nsum) carry = prefix_step(carry, e[j], u[j]);
+    }
+  }
+  return carry;
+}
+
+// segment_prefix over four consecutive elements with 16-byte accesses
+// (`base` 16-byte aligned, `nelem` a multiple of 4): per element the same
+// arithmetic in the same order, so results equal four scalar calls.
+__device__ __forceinline__ float4 segment_prefix4(float* base, const float* dec, int nseg, int nsum, int nelem,
+                                                  float4 carry) {
+  constexpr int K = 8;
+  for (int s0 = 0; s0 < nseg; s0 += K) {
+    float4 u[K];
+    float e[K];
+    if (nsum > 0) {  // uniform
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const int sc = min(s0 + j, nsum - 1);
+        u[j] = *(const float4*)(base + (size_t)sc * nelem);
+        e[j] = dec[sc];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int s = s0 + j;
+      if (s < nseg) *(float4*)(base + (size_t)s * nelem) = carry;
+      if (s < nsum) {
+        carry.x = prefix_step(carry.x, e[j], u[j].x);
+        carry.y = prefix_step(carry.y, e[j], u[j].y);
+        carry.z = prefix_step(carry.z, e[j], u[j].z);
+        carry.w = prefix_step(carry.w, e[j], u[j].w);
+      }
     }
   }
   return carry;

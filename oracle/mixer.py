@@ -288,7 +288,7 @@ class View:
         if self.decay is None:
             return keys.cumsum(2)
         ones = keys.new_ones(*keys.shape[:3], 1)
-        return scans.linattn_naive(ones, ones, keys, self.decay)
+        return self.linattn(ones, ones, keys, self.decay)
 
 
 # ---------------------------------------------------------------- engine
@@ -529,14 +529,17 @@ def project(c, params, x):
     return q, k, v
 
 
-SCANS = {"naive": scans.linattn_naive, "quad": scans.linattn_quad, "cumsum": scans.linattn_cumsum}
+SCANS = {"naive": scans.linattn_naive, "quad": scans.linattn_quad, "cumsum": scans.linattn_cumsum,
+         "chunk": scans.linattn_chunk}
 
 
 def forward(c, params, x, backend: str = "naive"):
     """ThetaScan forward x[B,T,D] -> y[B,T,D] (block.py:573-724).
 
     ``backend`` picks the oracle scan: the naive loop (parity target), the
-    quadratic form, or the prefix-sum form (the CPU baseline algorithm).
+    quadratic form, the prefix-sum form (the CPU baseline algorithm), or the
+    tiled form (64-token tiles; equal to the naive loop at 1e-12, linear in T,
+    for long sequences).
     """
     scan = SCANS[backend]
     B, T, _ = x.shape

@@ -27,13 +27,17 @@ def linattn_naive(q, k, v, decay=None):
     B, H, T, Dk = k.shape
     Dv = v.shape[-1]
     S = q.new_zeros(B, H, Dk, Dv)
-    out = q.new_zeros(B, H, T, Dv)
+    if T == 0:
+        return q.new_zeros(B, H, 0, Dv)
+    # rows are collected and stacked once: in-place row writes would make
+    # autograd's backward copy the whole output per step (O(T^2))
+    rows = []
     for t in range(T):
         if decay is not None:
             S = S * decay[:, :, t].exp().unsqueeze(-1)
         S = S + k[:, :, t].unsqueeze(-1) * v[:, :, t].unsqueeze(-2)
-        out[:, :, t] = torch.einsum("bhk,bhkv->bhv", q[:, :, t], S)
-    return out
+        rows.append(torch.einsum("bhk,bhkv->bhv", q[:, :, t], S))
+    return torch.stack(rows, dim=2)
 
 
 def final_state_naive(k, v, decay=None):
@@ -45,6 +49,61 @@ def final_state_naive(k, v, decay=None):
             S = S * decay[:, :, t].exp().unsqueeze(-1)
         S = S + k[:, :, t].unsqueeze(-1) * v[:, :, t].unsqueeze(-2)
     return S
+
+
+def linattn_chunk(q, k, v, decay=None, chunk=64):
+    """Tiled exact form of the recurrence (src/thetascan/_core/ops/scan_chunk.py:246-339).
+
+    Tiles of ``min(chunk, T)`` tokens, the last one zero-padded
+    (scan_chunk.py:158-167, 274-275).  Inside a tile the score block is
+    weighted by exp(min(L_i - L_j, 0)) with L the tile-local cumulative log of
+    ``decay`` (scan_chunk.py:122-155); across tiles the state entering tile n
+    is S_n = S_{n-1} exp(L_last) + U_{n-1}, U = sum_j exp(L_last - L_j) k_j v_j^T
+    (scan_chunk.py:170-212, 318-334); the entering state reaches position i
+    with weight exp(L_i).  A static [H] retention is passed as its [B,H,T,1]
+    stream (``as_stream``).  Same mathematics as ``linattn_naive`` with a cost
+    linear in T, so the float64 oracle reaches long sequences; pinned against
+    ``linattn_naive`` at 1e-12 for several chunks, retentions and ragged tiles
+    (tests/test_oracle_closed_forms.py), as the reference pins its chunk
+    backend (tests/test_scan_chunk.py:55-123).
+    """
+    B, H, T, Dk = q.shape
+    Dv = v.shape[-1]
+    if T == 0:
+        return q.new_zeros(B, H, 0, Dv)
+    if decay is not None and decay.shape[-1] != 1:
+        raise NotImplementedError("chunk backend: scalar decay only (v1)")
+    C = min(int(chunk), T)
+    NT = -(-T // C)
+    pad = NT * C - T
+
+    def tiles(x):
+        if pad:
+            x = torch.cat([x, x.new_zeros(*x.shape[:2], pad, *x.shape[3:])], dim=2)
+        return x.reshape(B, H, NT, C, x.shape[-1])
+
+    qt, kt, vt = tiles(q), tiles(k), tiles(v)
+    causal = torch.ones(C, C, dtype=torch.bool).tril()
+    if decay is None:
+        w = causal.to(q.dtype)
+        key_w = close = enter = None
+    else:
+        L = tiles(decay.to(q.dtype)).squeeze(-1).cumsum(-1)        # [B,H,NT,C]
+        w = (L.unsqueeze(-1) - L.unsqueeze(-2)).clamp(max=0.0).exp() * causal
+        key_w = (L[..., -1:] - L).exp()                            # weight of key j leaving the tile
+        close = L[..., -1].exp()                                   # whole-tile retention
+        enter = L.exp()                                            # entering state at position i
+    out = ((qt @ kt.transpose(-1, -2)) * w) @ vt                   # intra-tile part
+    keys = kt if key_w is None else kt * key_w.unsqueeze(-1)
+    U = keys.transpose(-1, -2) @ vt                                # [B,H,NT,Dk,Dv]
+    S = q.new_zeros(B, H, Dk, Dv)
+    states = []
+    for n in range(NT):
+        states.append(S)
+        S = (S if close is None else S * close[:, :, n, None, None]) + U[:, :, n]
+    cross = qt @ torch.stack(states, dim=2)
+    out = out + (cross if enter is None else cross * enter.unsqueeze(-1))
+    return out.reshape(B, H, NT * C, Dv)[:, :, :T]
 
 
 def linattn_quad(q, k, v, decay=None):
@@ -105,10 +164,12 @@ def ema_cumsum(x, log_alpha):
     """
     B, H, T = x.shape[:3]
     la = log_alpha.to(x.dtype).view(1, H, 1, 1) if x.dim() == 4 else log_alpha.to(x.dtype).view(1, H, 1)
-    out = torch.zeros_like(x)
+    if T == 0:
+        return torch.zeros_like(x)
     z = torch.zeros_like(x[:, :, 0])
     alpha = la.exp().squeeze(2)
+    rows = []
     for t in range(T):
         z = z * alpha + x[:, :, t]
-        out[:, :, t] = z
-    return out
+        rows.append(z)
+    return torch.stack(rows, dim=2)

@@ -196,3 +196,35 @@ def test_one_call_memory_matches_per_entry_calls(cuda, variant, feature_map, dty
     assert len(results[0]) == len(results[1])
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+def test_native_backward_survives_rope_table_eviction(cuda):
+    """The one-call backward reads the RoPE tables its forward named: they stay
+    alive with the autograd node when the table cache drops them between the
+    forward and the backward (sequences of many lengths), so the gradients
+    equal those of an undisturbed step bit for bit."""
+    from thetascan_amd._core.ops import fused
+
+    pub = _headline_config("feature", "none", d_model=256, heads=4)
+    module = build_module(pub, cuda, torch.bfloat16)
+    _seeded(module, 9)
+    g = torch.Generator().manual_seed(10)
+    T = 300
+    x = torch.randn(2, T, 256, generator=g).to(cuda, torch.bfloat16)
+    dy = torch.randn(2, T, 256, generator=g).to(cuda, torch.bfloat16)
+    runs = []
+    for evict in (False, True):
+        module.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        y = module(xi)
+        if evict:
+            for t in range(1, 80):
+                fused.rope_tables(1000 + t, 16, 10000.0, cuda)
+            assert not any(key[0] == T for key in fused._TABLES)
+            torch.cuda.empty_cache()
+            junk = torch.full((1 << 22,), float("nan"), device=cuda)
+            del junk
+        y.backward(dy)
+        runs.append([xi.grad] + [p.grad for p in module.parameters() if p.grad is not None])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)

@@ -113,3 +113,65 @@ def test_expansion_map_magnitudes():
     m = expansion.row_map((1, 24, 12), "k", "w1-expand-layer-0")
     assert torch.allclose(m.abs(), torch.full_like(m, 1.0 / math.sqrt(12)))
     assert not torch.equal(m, expansion.row_map((1, 24, 12), "k2", "w1-expand-layer-0"))
+
+
+def _streams(T=37, Dk=5, Dv=4, seed=20260725):
+    """B=2, H=3 streams and log-retentions [-0.05, -0.4, -2.0], the shapes of
+    the reference's scan fixture (tests/test_scan_chunk.py:15-24)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(2, 3, T, Dk, generator=g, dtype=torch.float64)
+    k = torch.randn(2, 3, T, Dk, generator=g, dtype=torch.float64)
+    v = torch.randn(2, 3, T, Dv, generator=g, dtype=torch.float64)
+    la = torch.tensor([-0.05, -0.4, -2.0], dtype=torch.float64)
+    stream = -torch.rand(2, 3, T, 1, generator=g, dtype=torch.float64)
+    return q, k, v, la, stream
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 8, 64, 128])
+@pytest.mark.parametrize("retention", ["none", "static", "stream"])
+def test_chunk_oracle_equals_naive(chunk, retention):
+    """The tiled oracle against the recurrence at 1e-12 for chunks that divide
+    T, leave a ragged last tile, or exceed T (tests/test_scan_chunk.py:55-123)."""
+    q, k, v, la, stream = _streams()
+    decay = {"none": None, "static": scans.as_stream(la, q), "stream": stream}[retention]
+    got = scans.linattn_chunk(q, k, v, decay, chunk=chunk)
+    ref = scans.linattn_naive(q, k, v, decay)
+    assert torch.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_chunk_oracle_gradients_equal_naive():
+    q, k, v, la, stream = _streams(T=29)
+    args = [t.clone().requires_grad_(True) for t in (q, k, v, stream)]
+    dy = torch.randn(2, 3, 29, 4, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    grads = []
+    for fn in (lambda *a: scans.linattn_chunk(*a, chunk=8), scans.linattn_naive):
+        for t in args:
+            t.grad = None
+        (fn(*args) * dy).sum().backward()
+        grads.append([t.grad.clone() for t in args])
+    for a, b in zip(*grads):
+        assert torch.allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
+def test_final_state_closed_form_and_one_hot_reads():
+    """final_state_naive equals N_T = sum_i w_i k_i v_i^T, w_i = prod_{i<j<=T-1} a_j,
+    and reading it with one-hot queries reproduces the last output row of the
+    recurrence (out_{T-1} = q_{T-1} S_{T-1})."""
+    q, k, v, la, stream = _streams(T=23)
+    for decay in (None, scans.as_stream(la, q), stream):
+        S = scans.final_state_naive(k, v, decay)
+        if decay is None:
+            w = torch.ones(2, 3, 23, dtype=torch.float64)
+        else:
+            L = decay[..., 0]
+            # weight of token i at the end: exp(sum_{j>i} log a_j)
+            w = (L.sum(-1, keepdim=True) - L.cumsum(-1)).exp()
+        closed = torch.einsum("bht,bhtk,bhtv->bhkv", w, k, v)
+        assert torch.allclose(S, closed, rtol=1e-12, atol=1e-12)
+        eye = torch.eye(5, dtype=torch.float64).expand(2, 3, 5, 5)
+        # queries e_j at the last step read row j of S_{T-1}
+        qq = torch.zeros(2, 3, 23, 5, dtype=torch.float64)
+        for j in range(5):
+            qq[:, :, -1] = eye[:, :, j]
+            out = scans.linattn_naive(qq, k, v, decay)
+            assert torch.allclose(out[:, :, -1], S[:, :, j], rtol=1e-12, atol=1e-12)

@@ -331,7 +331,7 @@ class _State:
 
     __slots__ = ("spec", "normalize", "seg_chunks", "heads", "d", "has_gate", "has_tau", "tau_dtype", "w_dtypes",
                  "b_dtype", "ws", "proj", "w1c", "w2c", "tauf", "gb", "phi_q", "phi_k", "num", "mass", "resid",
-                 "native", "io", "saved", "tau", "b_g")
+                 "native", "io", "saved", "tau", "b_g", "tables")
 
 
 _MEMORY: dict = {}
@@ -441,8 +441,10 @@ def _native_forward(st: _State, plan, proj, w1, w2, tau, b_g, spec: FeatureSpec,
     status = lib.ts_memory_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.Strided(y.data_ptr(), T * Hd, d, Hd),
                                saved.data_ptr(), saved_bytes, _lib.stream_handle(dev))
     _lib.check(status, "ts_memory_fwd")
-    # the io holds raw addresses: keep every tensor it names alive
-    st.native, st.io, st.saved = plan, io, saved
+    # the io holds raw addresses that ts_memory_bwd reads again: keep every
+    # tensor it names alive, the RoPE tables included (the table cache may
+    # drop its entry before this step's backward runs)
+    st.native, st.io, st.saved, st.tables = plan, io, saved, (ic, is_, fc, fs)
     st.proj, st.w1c, st.w2c, st.tau, st.b_g = proj, w1c, w2c, tau_, bg_
     return y
 

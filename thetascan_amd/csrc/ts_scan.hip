@@ -1136,7 +1136,21 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
   int rc = compute_layout(d, &L);
   if (rc) return rc;
   if (!io) return fail(TS_ERR_VALUE, "scan: null io");
-  if (d->T == 0) return TS_OK;
+  if (d->want_final && !io->final_state) return fail(TS_ERR_VALUE, "scan: missing final_state buffer");
+  if (d->init_state && !io->init_state) return fail(TS_ERR_VALUE, "scan: missing init_state buffer");
+  if (d->T == 0) {
+    // An empty piece leaves the carried state unchanged: the final state is
+    // the initial one (or zero).  The prefix kernel over zero segments
+    // writes exactly that.
+    if (!d->want_final) return TS_OK;
+    ts::FinalP F{io->final_state, d->init_state ? io->init_state : nullptr, L.dkp, L.dvp, d->dk, d->dv,
+                 L.kx ? 1 : 0, L.vx ? 1 : 0};
+    hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem / 4 + 255) / 256, d->B * d->H), dim3(256), 0, stream,
+                       (float*)nullptr, (const float*)nullptr, F, 0, 0, L.nelem);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: prefix launch failed: %s", hipGetErrorString(e));
+    return TS_OK;
+  }
   const int esize = d->dtype == TS_BF16 ? 2 : 4;
   const int vec = 16 / esize;
   if ((rc = check_stream("q", io->q, vec, true))) return rc;

@@ -27,7 +27,9 @@
 extern "C" {
 #endif
 
-#define TS_ABI_VERSION 7
+/* 8: the scan entry points require a 16-byte aligned workspace (a sub-
+ *    allocated workspace at an odd offset was accepted by version 7). */
+#define TS_ABI_VERSION 8
 
 enum ts_status {
   TS_OK = 0,
@@ -115,7 +117,10 @@ const char* ts_last_error(void);
 int ts_scan_layout(const ts_scan_desc* desc, int32_t* dk_pad, int32_t* dv_pad,
                    int32_t* n_segments);
 
-/* Device workspace (bytes) ts_scan_fwd needs for `desc`. */
+/* Device workspace (bytes) ts_scan_fwd and ts_scan_pair_fwd need for `desc`.
+ * The workspace base must be 16-byte aligned (the summaries are read and
+ * written as 16-byte vectors); a misaligned base is refused with
+ * TS_ERR_VALUE.  Its contents need no initialisation. */
 int ts_scan_workspace_bytes(const ts_scan_desc* desc, size_t* bytes);
 
 /* Causal (or anti-causal, desc->reverse) linear-attention scan of one view:
@@ -142,7 +147,8 @@ int ts_scan_fwd(const ts_scan_desc* desc, const ts_scan_io* io,
  * qa = v, qb = phi(k).  K and V are read once and the state is updated once
  * per tile; each output equals its own ts_scan_fwd call.  desc describes
  * scan A (q = qa): bf16, no retention, no ext columns, TS_OUT_STORE,
- * dk == dv == 64; workspace from ts_scan_workspace_bytes(desc). */
+ * dk == dv == 64; workspace from ts_scan_workspace_bytes(desc), 16-byte
+ * aligned. */
 typedef struct ts_scan_pair_io {
   ts_strided qa, k, v, qb;
   ts_strided out_a;               /* [B,H,T,dv]                                */
@@ -174,7 +180,8 @@ typedef struct ts_scan_views_io {
   ts_strided out_ext[TS_MAX_VIEWS];     /* fp32 [B,H,T] key mass (mass = 1)   */
 } ts_scan_views_io;
 
-/* Device workspace (bytes) ts_scan_views_fwd needs for `desc`. */
+/* Device workspace (bytes) ts_scan_views_fwd needs for `desc` (16-byte
+ * aligned base, contents need no initialisation). */
 int ts_scan_views_workspace_bytes(const ts_scan_views_desc* desc, size_t* bytes);
 
 /* The forward causal scans of n_views retentions (none or static [H]) over

@@ -96,13 +96,14 @@ def test_headline_mixer_at_T4096_matches_float64_oracle(cuda, variant):
     pub = _headline_config(placement, normalization)
     module = build_module(pub, cuda, torch.float32)
     _seeded(module, 7)
+    module = module.to(torch.bfloat16)
     g = torch.Generator().manual_seed(8)
     B, T, D = 2, 4096, 512
-    x = torch.randn(B, T, D, generator=g, dtype=torch.float64)
+    # identical inputs on both sides: the bf16 values of x and the weights
+    x = torch.randn(B, T, D, generator=g, dtype=torch.float64).to(torch.bfloat16).double()
     dy = torch.randn(B, T, D, generator=g, dtype=torch.float64) * 0.1
     y64, dx64, grads64 = _oracle_run(pub, module, x, dy)
 
-    module = module.to(torch.bfloat16)
     for reps in (1, 4):
         module.zero_grad(set_to_none=True)
         xb = x.repeat(reps, 1, 1).to(cuda, torch.bfloat16).requires_grad_(True)
@@ -166,18 +167,53 @@ def test_cpu_reference_workload_matches_oracle_fp32(cuda):
 
 # ------------------------------------------------------------------ bf16 bank and GN mixers
 
-def _bf16_against_oracle(cuda, pub, module, B, T, seed, tol=2e-2):
+class _Bf16Storage(torch.autograd.Function):
+    """Round a tensor and its gradient to bf16 (float64 otherwise)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.to(torch.bfloat16).double()
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).double()
+
+
+def _dx_with_bf16_projection(pub, module, x, dy, dx64, monkeypatch):
+    """rel error of the oracle's dx when only the qkv projection and its
+    gradient are stored in bf16 -- what any bf16 mixer, the reference's own
+    bf16 path included, carries at the least."""
+    real = oracle_mixer.project
+    monkeypatch.setattr(oracle_mixer, "project", lambda *a: tuple(_Bf16Storage.apply(t) for t in real(*a)))
+    try:
+        _, dx_r, _ = _oracle_run(pub, module, x, dy)
+    finally:
+        monkeypatch.setattr(oracle_mixer, "project", real)
+    return rel_err(dx_r, dx64)
+
+
+def _bf16_against_oracle(cuda, pub, module, B, T, seed, tol=2e-2, monkeypatch=None):
+    """bf16 module against the float64 oracle on identical inputs (the bf16
+    values of x and of every parameter).  With ``monkeypatch`` the bar of dx is
+    the larger of ``tol`` and the error that bf16 storage of the qkv projection
+    and its gradient alone gives the oracle (an ill-conditioned input gradient:
+    the q, k and v paths cancel)."""
     g = torch.Generator().manual_seed(seed)
     D = pub["d_model"]
-    x = torch.randn(B, T, D, generator=g, dtype=torch.float64)
+    module = module.to(torch.bfloat16)
+    x = torch.randn(B, T, D, generator=g, dtype=torch.float64).to(torch.bfloat16).double()
     dy = torch.randn(B, T, D, generator=g, dtype=torch.float64) * 0.1
     y64, dx64, grads64 = _oracle_run(pub, module, x, dy)
-    module = module.to(torch.bfloat16)
+    dx_tol = tol
+    if monkeypatch is not None:
+        floor = _dx_with_bf16_projection(pub, module, x, dy, dx64, monkeypatch)
+        print(f"dx bar: bf16 storage of the projection alone gives {floor:.4f}", flush=True)
+        dx_tol = max(tol, floor)
     xb = x.to(cuda, torch.bfloat16).requires_grad_(True)
     yb = module(xb)
     (yb.float() * dy.to(cuda, torch.float32)).sum().backward()
     assert rel_err(yb, y64) < tol
-    assert rel_err(xb.grad, dx64) < tol
+    assert rel_err(xb.grad, dx64) < dx_tol
     for name, p in module._core.named_parameters():
         if name in grads64 and grads64[name].abs().max() > 0:
             assert rel_err(p.grad, grads64[name]) < 3 * tol / 2, name
@@ -193,7 +229,7 @@ def test_bank_mixer_bf16_matches_oracle(cuda, bank_mode, branches):
     _bf16_against_oracle(cuda, pub, module, 2, 700, 23)
 
 
-def test_gn_mixer_bf16_matches_oracle(cuda):
+def test_gn_mixer_bf16_matches_oracle(cuda, monkeypatch):
     pub = json.loads(json.dumps(CASES["gn_relu2_plain_sum"]["config"]))
     pub.update(d_model=256, n_heads=4)
     pub["runtime"]["scan_chunk"] = 64
@@ -204,4 +240,4 @@ def test_gn_mixer_bf16_matches_oracle(cuda):
             if name.startswith("W2."):
                 p.copy_(torch.randn(p.shape, generator=g) * 0.02)
     print("gn bf16", flush=True)
-    _bf16_against_oracle(cuda, pub, module, 2, 600, 32)
+    _bf16_against_oracle(cuda, pub, module, 2, 600, 32, monkeypatch=monkeypatch)

@@ -230,8 +230,9 @@ def write_streams(weights, cfg, k, v, hrot=None, softmax_gain=None, kernel_contr
     return streams, ctxs, o
 
 
-def _normalized(num, mass, eps):
-    return num / (mass.unsqueeze(-1).to(num.dtype) + eps)
+def _normalized(num, mass, eps, dtype):
+    """num / (mass + eps) in fp32 (mass is an fp32 scan column), in ``dtype``."""
+    return (num.float() / (mass.unsqueeze(-1).float() + eps)).to(dtype)
 
 
 def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=None, kernel_controls=None):
@@ -269,7 +270,7 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
                 else:
                     pairs = [interface.scan_views_mass((view,), one.to(keys.dtype), keys, vals, "m")[0]
                              for view, one in zip(group, queries)]
-                mems = [_normalized(num, mass, cfg.eps) for num, mass in pairs]
+                mems = [_normalized(num, mass, cfg.eps, vals.dtype) for num, mass in pairs]
             else:
                 mems = []
                 for view, one in zip(group, queries):
@@ -326,7 +327,7 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
             if entry is None:
                 raise RuntimeError("read_norm_w1 requires an LA1 GN stream")
             pairs = interface.scan_views_mass(group, h0q.to(feature_keys.dtype), feature_keys, entry[1], "m")
-            preacts = [a + _normalized(num, mass, cfg.eps)[..., :m] for num, mass in pairs]
+            preacts = [a + _normalized(num, mass, cfg.eps, a.dtype)[..., :m] for num, mass in pairs]
             bs = [b] * len(group)
         else:
             for it in range(n_iter):

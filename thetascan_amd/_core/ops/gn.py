@@ -265,7 +265,9 @@ class _NormalizedRead(torch.autograd.Function):
         fused.read_fwd(nk, mk, rk, None, y, s, eps)
         ctx.save_for_backward(nk, mk, rk)
         ctx.meta = (s, eps, resid.dtype, None if mass is None else mass.dtype)
-        return y
+        # an fp32 numerator (a difference of views) is read in fp32, then
+        # rounded once to the stream dtype
+        return y.to(resid.dtype)
 
     @staticmethod
     def backward(ctx, dy):

@@ -150,11 +150,18 @@ def _combine(terms, slots, scanned, zeros):
     return tuple(outputs)
 
 
+def _subtracts(terms) -> bool:
+    """Whether some view is a difference of scans (a stale view)."""
+    return any(c < 0 for view_terms in terms for c, _ in view_terms)
+
+
 def scan_views(views, q, k, v, key_kind: str) -> tuple:
     """Scan one stream set through several temporal views (interface.py:120-195).
 
     Each distinct retention is scanned once by the hip backend and every view
-    is assembled as its signed combination of those scans.
+    is assembled as its signed combination of those scans.  A difference of
+    scans (a stale view: plain - fast, nearly equal over recent tokens) is
+    formed from fp32 scan outputs and rounded once.
     """
     terms, retentions, slots = _dedupe(views, key_kind)
 
@@ -165,13 +172,16 @@ def scan_views(views, q, k, v, key_kind: str) -> tuple:
         return tuple(zeros() for _ in views)
     contributing = next(view for view, view_terms in zip(views, terms) if view_terms)
     chunk = getattr(contributing, "chunk", scan_hip.DEFAULT_CHUNK)
-    scanned = scan_hip.linattn_views(q, k, v, tuple(retentions), chunk)
-    return _combine(terms, slots, scanned, zeros)
+    f32 = _subtracts(terms)
+    scanned = scan_hip.linattn_views(q, k, v, tuple(retentions), chunk, out_f32=f32)
+    out = _combine(terms, slots, scanned, zeros)
+    return tuple(o.to(q.dtype) for o in out) if f32 else out
 
 
 def scan_views_mass(views, q, k, v, key_kind: str) -> tuple:
     """Like :func:`scan_views` against ``cat([v, 1])``, returning ``(num, mass)``
-    per view without materialising the unit column (engine.py:430-442)."""
+    per view without materialising the unit column (engine.py:430-442).  A
+    difference of scans keeps its numerator in fp32 (masses are fp32)."""
     terms, retentions, slots = _dedupe(views, key_kind)
 
     def zeros():
@@ -184,7 +194,7 @@ def scan_views_mass(views, q, k, v, key_kind: str) -> tuple:
         return tuple((zeros(), zmass()) for _ in views)
     contributing = next(view for view, view_terms in zip(views, terms) if view_terms)
     chunk = getattr(contributing, "chunk", scan_hip.DEFAULT_CHUNK)
-    pairs = scan_hip.linattn_views_mass(q, k, v, tuple(retentions), chunk)
+    pairs = scan_hip.linattn_views_mass(q, k, v, tuple(retentions), chunk, out_f32=_subtracts(terms))
     nums = _combine(terms, slots, [p[0] for p in pairs], zeros)
     masses = _combine(terms, slots, [p[1] for p in pairs], zmass)
     return tuple(zip(nums, masses))
@@ -242,7 +252,9 @@ class FadeStale:
         return scan_views((self,), q, k, v, key_kind)[0]
 
     def mass_cum(self, keys: torch.Tensor) -> torch.Tensor:
-        return causal_prefix_sum(keys) - ema_cumsum(keys, self.log_alpha, self.chunk)
+        # the difference of two nearly equal prefixes is formed in fp32
+        k32 = keys.float()
+        return (causal_prefix_sum(k32) - ema_cumsum(k32, self.log_alpha, self.chunk)).to(keys.dtype)
 
 
 class FadeFast:

@@ -440,9 +440,12 @@ def _ret_kwargs(kind: int, retention):
 
 
 def _retention_grad(kind: int, retention: torch.Tensor, dL: torch.Tensor) -> torch.Tensor:
-    """Gradient of a retention from dL[B,H,T] = q.dq - k.dk (per view)."""
+    """Gradient of a retention from dL[B,H,T] = q.dq - k.dk (per view).
+
+    The sums cancel heavily (sum_t dL_t = 0), so they accumulate in float64."""
+    dL = dL.double()
     if kind == _lib.RET_STATIC:
-        t = torch.arange(dL.shape[2], device=dL.device, dtype=torch.float32)
+        t = torch.arange(dL.shape[2], device=dL.device, dtype=torch.float64)
         grad = (dL * t).sum(dim=(0, 2))
         return grad.to(retention.dtype).view_as(retention)
     # d a_j = sum_{t>=j} dL_t for j >= 1; position 0 never multiplies a stored term.
@@ -529,11 +532,20 @@ class _ScanViews(torch.autograd.Function):
             q_ext = dm.to(torch.float32) if mass_ext else None
             want_r = r is not None and need_r[j]
             if want_r:
-                dq_j, _, _ = scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
+                # dL_t = q_t.dq_t - k_t.dk_t sums to zero over t, and the
+                # retention gradient (sum_t t dL_t, or a suffix sum of dL) is a
+                # small difference of large terms: bf16 rounding of the score
+                # tiles inside the scans would be amplified by about T / (the
+                # retention's window).  These two scans therefore run on fp32
+                # operands (the bf16 values are exact in fp32).
+                qs, ks, vs, dOs = q, k, v, dO
+                if q.dtype != torch.float32:
+                    qs, ks, vs, dOs = q.float(), k.float(), v.float(), dO.float()
+                dq_j, _, _ = scan_launch(dOs, vs, ks, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
                                          out_mode=_lib.OUT_STORE_F32)
-                dk_j, _, _ = scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
+                dk_j, _, _ = scan_launch(vs, dOs, qs, **rk, reverse=True, q_ext="ones" if mass_ext else None,
                                          k_ext=q_ext, out_mode=_lib.OUT_STORE_F32)
-                dL = (q.float() * dq_j[..., :dk]).sum(-1) - (k.float() * dk_j[..., :dk]).sum(-1)
+                dL = (qs * dq_j[..., :dk]).sum(-1) - (ks * dk_j[..., :dk]).sum(-1)
                 r_grads.append(_retention_grad(kind, r, dL))
                 dq[..., : dq_j.shape[-1]] += dq_j
                 dkk[..., : dk_j.shape[-1]] += dk_j
@@ -553,13 +565,20 @@ class _ScanViews(torch.autograd.Function):
         return (gq, gk, gv, None, *r_grads)
 
 
-def _run_views(q, k, v, retentions, chunk, with_mass):
+def _run_views(q, k, v, retentions, chunk, with_mass, out_f32=False):
     if chunk < 1:
         raise ValueError("chunk backend: chunk must be >= 1")
     if not retentions:
         return ()
     for r in retentions:
         _classify(r, q)
+    if out_f32 and q.dtype != torch.float32:
+        # A caller that subtracts views (a stale view is plain - fast, nearly
+        # equal over recent tokens) gets scans on fp32 operands, forward and
+        # backward: bf16 rounding inside each scan would be amplified by the
+        # cancellation.  The bf16 values are exact in fp32; autograd casts the
+        # gradients back.
+        q, k, v = q.float(), k.float(), v.float()
     return _ScanViews.apply(q, k, v, with_mass, *retentions)
 
 
@@ -569,9 +588,15 @@ def linattn_views(
     v: torch.Tensor,
     retentions: tuple,
     chunk: int = DEFAULT_CHUNK,
+    *,
+    out_f32: bool = False,
 ) -> tuple:
-    """Scan one stream set through several temporal views (scan_chunk.py:246-339)."""
-    return tuple(_run_views(q, k, v, tuple(retentions), chunk, False))
+    """Scan one stream set through several temporal views (scan_chunk.py:246-339).
+
+    ``out_f32`` scans fp32 copies of the operands and returns fp32 outputs (for
+    callers that combine views by subtraction); otherwise outputs are in the
+    query dtype."""
+    return tuple(_run_views(q, k, v, tuple(retentions), chunk, False, out_f32))
 
 
 def linattn_views_mass(
@@ -580,6 +605,8 @@ def linattn_views_mass(
     v: torch.Tensor,
     retentions: tuple,
     chunk: int = DEFAULT_CHUNK,
+    *,
+    out_f32: bool = False,
 ) -> tuple:
     """Like :func:`linattn_views` with an implicit unit value column.
 
@@ -588,7 +615,7 @@ def linattn_views_mass(
     reference obtains from ``cat([v, ones])`` (``engine.py:430``), without
     materialising the augmented tensor.
     """
-    res = _run_views(q, k, v, tuple(retentions), chunk, True)
+    res = _run_views(q, k, v, tuple(retentions), chunk, True, out_f32)
     n = len(retentions)
     return tuple((res[j], res[n + j]) for j in range(n))
 

@@ -480,7 +480,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 7:
+        if lib.ts_abi_version() != 8:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

@@ -137,6 +137,20 @@ int ts_scan_workspace_bytes(const ts_scan_desc* desc, size_t* bytes);
 int ts_scan_fwd(const ts_scan_desc* desc, const ts_scan_io* io,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ts_scan_fwd without a workspace argument and without any device allocation
+ * (no counterpart in the reference: for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The segment summaries live in a library-owned device
+ * buffer of TS_SCAN_NOALLOC_MAX_WORKSPACE bytes, one per GPU, held until the
+ * process ends; a scan whose ts_scan_workspace_bytes() exceeds it returns
+ * TS_ERR_VALUE, and states_in (kept segment states) is refused.  Every call on
+ * one GPU shares that buffer: calls that overlap on one GPU (several streams,
+ * several host threads) race and must be serialised by the caller.  Results
+ * equal ts_scan_fwd's with the same desc and io. */
+#define TS_SCAN_NOALLOC_MAX_WORKSPACE (32u * 1024u * 1024u)
+
+int ts_scan_fwd_noalloc(const ts_scan_desc* desc, const ts_scan_io* io, hipStream_t stream);
+
 /* Two plain scans over the same keys and values up to a swap, in one pass:
  *
  *   out_a_t = sum_{i<=t} <qa_t, k_i> v_i,   out_b_t = sum_{i<=t} <qb_t, v_i> k_i

@@ -439,6 +439,7 @@ def load() -> ctypes.CDLL:
         ]
         P = ctypes.POINTER
         lib.ts_scan_pair_fwd.argtypes = [P(ScanDesc), P(ScanPairIO), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.ts_scan_fwd_noalloc.argtypes = [P(ScanDesc), P(ScanIO), ctypes.c_void_p]
         lib.ts_scan_views_workspace_bytes.argtypes = [P(ScanViewsDesc), P(ctypes.c_size_t)]
         lib.ts_scan_views_fwd.argtypes = [P(ScanViewsDesc), P(ScanViewsIO), ctypes.c_void_p, ctypes.c_size_t,
                                           ctypes.c_void_p]

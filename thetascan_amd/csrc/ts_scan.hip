@@ -1047,6 +1047,42 @@ int launch(KernelFn fn, dim3 grid, size_t lds, hipStream_t stream, const ts::Sca
 
 }  // namespace
 
+// Workspace of ts_scan_fwd_noalloc: one copy on every GPU the library runs
+// on, held until the process ends (the code object's device globals are
+// placed when the library's kernels are loaded on a device).  Host code never
+// passes `scratch` itself to a kernel or a copy -- on the host the name is a
+// stand-in, not a device address -- but the per-device address that
+// hipGetSymbolAddress returns (device_scratch).
+static __device__ __align__(256) unsigned char scratch[TS_SCAN_NOALLOC_MAX_WORKSPACE];
+
+namespace {
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices];  // per device, set on the first call made with that device current
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.
+int device_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(TS_ERR_RUNTIME, "scan noalloc: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TS_ERR_RUNTIME, "scan noalloc: no device address for the scratch buffer on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TS_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int ts_abi_version(void) { return TS_ABI_VERSION; }
@@ -1130,8 +1166,8 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   return TS_OK;
 }
 
-int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, size_t ws_bytes,
-                hipStream_t stream) {
+static int scan_fwd_impl(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, size_t ws_bytes,
+                         hipStream_t stream) {
   Layout L;
   int rc = compute_layout(d, &L);
   if (rc) return rc;
@@ -1229,6 +1265,27 @@ int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, si
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: prefix launch failed: %s", hipGetErrorString(e));
   }
   return launch(fmain, dim3(L.nseg, bh, L.nvs), lds_main, stream, p);
+}
+
+int ts_scan_fwd(const ts_scan_desc* d, const ts_scan_io* io, void* workspace, size_t ws_bytes,
+                hipStream_t stream) {
+  return scan_fwd_impl(d, io, workspace, ws_bytes, stream);
+}
+
+int ts_scan_fwd_noalloc(const ts_scan_desc* d, const ts_scan_io* io, hipStream_t stream) {
+  Layout L;
+  int rc = compute_layout(d, &L);
+  if (rc) return rc;
+  if (d->states_in)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan noalloc: kept segment states (states_in) need a workspace the "
+                                        "caller owns across calls; use ts_scan_fwd");
+  if (L.ws_bytes > (size_t)TS_SCAN_NOALLOC_MAX_WORKSPACE)
+    return fail(TS_ERR_VALUE, "scan noalloc: this scan needs %zu bytes of workspace, above the %zu-byte scratch "
+                              "buffer of ts_scan_fwd_noalloc; use ts_scan_fwd with a workspace",
+                L.ws_bytes, (size_t)TS_SCAN_NOALLOC_MAX_WORKSPACE);
+  void* ws = nullptr;
+  if (L.ws_bytes > 0 && (rc = device_scratch(&ws))) return rc;
+  return scan_fwd_impl(d, io, ws, L.ws_bytes, stream);
 }
 
 }  // extern "C"

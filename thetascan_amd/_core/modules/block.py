@@ -203,7 +203,11 @@ class ThetaScan(nn.Module):
         else:
             self.fade_alpha = None
             self.fade_eta = None
-        self._backend = None
+        # The fused path depends only on the (immutable) configuration and on
+        # which optional parameters exist, so both are settled here and
+        # forward() reads them without writing module state.
+        self._fused_cfg = self._config_fused_eligible()
+        self._spec = self._make_feature_spec()
         self.last_path = None
 
     # ------------------------------------------------------------ checkpoints
@@ -341,12 +345,7 @@ class ThetaScan(nn.Module):
         """Whether the three-kernel hot path covers this configuration and input."""
         if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
             return False
-        # The answer depends on the (immutable) configuration and on which
-        # optional parameters exist, never on parameter values.
-        hit = self.__dict__.get("_fused_ok")
-        if hit is None:
-            hit = self.__dict__["_fused_ok"] = self._config_fused_eligible()
-        return hit
+        return self._fused_cfg
 
     def _config_fused_eligible(self) -> bool:
         cfg = self.cfg
@@ -369,22 +368,19 @@ class ThetaScan(nn.Module):
                     and self.kernel_score_bias is None)
         return False
 
-    def _feature_spec(self):
-        spec = self.__dict__.get("_spec")
-        if spec is None:
-            cfg = self.cfg
-            d, m = cfg.head_dim, cfg.mem_hidden
-            in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
-            feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
-            kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
-            spec = self.__dict__["_spec"] = fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot,
-                                                              cfg.rope_base, 1.0 / math.sqrt(cfg.depth), cfg.eps)
-        return spec
+    def _make_feature_spec(self):
+        cfg = self.cfg
+        d, m = cfg.head_dim, cfg.mem_hidden
+        in_rot = rotated_width(d, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
+        feat_rot = rotated_width(m, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
+        kind = fused._lib.FEAT_RELU2 if cfg.kernel_kind == "relu2_ridge" else fused._lib.FEAT_SOFTMAX
+        return fused.FeatureSpec(kind, m, cfg.softmax_gain, in_rot, feat_rot, cfg.rope_base,
+                                 1.0 / math.sqrt(cfg.depth), cfg.eps)
 
     def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
         cfg = self.cfg
         H = cfg.n_heads
-        spec = self._feature_spec()
+        spec = self._spec
         (W1, W2, _), = self._weights()
         gate = self.ogate is not None
         return fused.kernel_mixer(x, self.proj_qkv.weight, self.ogate.g.lin.weight if gate else None,
@@ -393,15 +389,17 @@ class ThetaScan(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         cfg = self.cfg
-        self._backend = resolve_backend(cfg.backend, cfg.decay_gate, cfg.accumulation, device=x.device,
-                                        require_scalar_decay=cfg.read_fade)
+        backend = resolve_backend(cfg.backend, cfg.decay_gate, cfg.accumulation, device=x.device,
+                                  require_scalar_decay=cfg.read_fade)
         if not x.is_cuda:
             raise RuntimeError("the hip backend runs on the GPU only (no CPU fallback)")
-        if self.fused_eligible(x):
-            self.last_path = "fused"
+        fused_path = self.fused_eligible(x)
+        if not torch.compiler.is_compiling():
+            # a record for eager callers; a traced forward writes no module state
+            self.last_path = "fused" if fused_path else "composed"
+        if fused_path:
             return self._forward_fused(x)
-        self.last_path = "composed"
-        return self._forward_composed(x)
+        return self._forward_composed(x, backend)
 
     def _project(self, x):
         cfg = self.cfg
@@ -422,7 +420,7 @@ class ThetaScan(nn.Module):
         q, k, v = linear(x, self.proj_qkv.weight).view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
         return q, k, v
 
-    def _forward_composed(self, x: torch.Tensor) -> torch.Tensor:
+    def _forward_composed(self, x: torch.Tensor, backend: str = "hip") -> torch.Tensor:
         cfg = self.cfg
         B, T, _ = x.shape
         H, d = cfg.n_heads, cfg.head_dim
@@ -453,7 +451,7 @@ class ThetaScan(nn.Module):
         decay_d = decay_m = None
         if self.decay is not None:
             decay_d, decay_m = self.decay(x)
-        acc = Accumulator(self._backend, decay_d=decay_d, decay_m=decay_m, eps=cfg.eps, chunk=cfg.scan_chunk)
+        acc = Accumulator(backend, decay_d=decay_d, decay_m=decay_m, eps=cfg.eps, chunk=cfg.scan_chunk)
         weights = self._weights()
         sharp = self.kernel_sharpness()
         controls = self.kernel_controls()
@@ -469,7 +467,7 @@ class ThetaScan(nn.Module):
             for branch in range(cfg.fade_branches):
                 log_alpha = (-F.softplus(-alpha_raw[branch])).to(dtype=x.dtype)
                 la_s = log_alpha.view(1, H, 1, 1).expand(B, H, T, 1)
-                fast = Accumulator(self._backend, decay_d=la_s, decay_m=la_s, eps=cfg.eps, chunk=cfg.scan_chunk,
+                fast = Accumulator(backend, decay_d=la_s, decay_m=la_s, eps=cfg.eps, chunk=cfg.scan_chunk,
                                    static_log_alpha=log_alpha)
                 if cfg.read_fade_mode == "fast":
                     views.append(FadeFast(fast, log_alpha, chunk=cfg.scan_chunk))

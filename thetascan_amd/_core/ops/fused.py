@@ -1,17 +1,16 @@
 """Fused HIP hot path of the kernel-family mixer (write -> scan -> read).
 
-``kernel_memory`` is one autograd node covering everything between the qkv
-projection and the output projection of a kernel-memory mixer:
+``kernel_mixer`` is one autograd node (a pair of torch.library custom ops)
+covering a depth-1 kernel-memory mixer: the stacked qkv / output-gate
+projection GEMM, then
 
     phi_k = feature(k)                 ts_feature_fwd   (keys)
     phi_q, resid = feature(q)          ts_feature_fwd   (queries, + W2 base)
     num, mass = scan(phi_q, phi_k, v)  ts_scan_fwd      (key-mass column)
     y = (resid + s*num/(mass+eps)) * silu(g)            ts_read_fwd
 
-with q, k, v and the gate logits g read from one input projection
-(``in_projection``: the qkv and output-gate weights stacked into one GEMM)
-
-and its backward (ts_read_bwd -> three scans -> ts_feature_bwd, then plain
+with q, k, v and the gate logits g read from that one projection, then the
+output projection; and its backward (ts_read_bwd -> three scans -> ts_feature_bwd, then plain
 GEMMs for the W1/W2 gradients).  Reference chain:
 src/thetascan/_core/modules/block.py:593-724 and
 src/thetascan/_core/ops/engine.py:260-544 for a depth-1 kernel memory.
@@ -286,49 +285,12 @@ def _stacked(w_qkv, w_g):
     return torch.cat([w_qkv.detach(), w_g.detach().to(w_qkv.dtype)], dim=0)
 
 
-class _InProjection(torch.autograd.Function):
-    """proj = x [W_qkv; W_g]^T: the qkv projection and the output gate's
-    projection as one GEMM (block.py:593-594 and gates.py:34-40 read the same
-    x; the gate bias is added inside the read kernel), with one gradient GEMM
-    for x and one split-K GEMM for the stacked weights."""
-
-    @staticmethod
-    def forward(ctx, x, w_qkv, w_g):
-        n_qkv = w_qkv.shape[0]
-        weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
-        ctx.save_for_backward(x, weight)
-        ctx.n_qkv = n_qkv
-        ctx.has_g = w_g is not None
-        ctx.dtypes = (w_qkv.dtype, None if w_g is None else w_g.dtype)
-        return torch.nn.functional.linear(x, weight)
-
-    @staticmethod
-    def backward(ctx, dproj):
-        x, weight = ctx.saved_tensors
-        n_out, n_in = weight.shape
-        d2 = dproj.reshape(-1, n_out)
-        dx = dw_qkv = dw_g = None
-        if ctx.needs_input_grad[0]:
-            dx = (d2 @ weight).view(x.shape)
-        if ctx.needs_input_grad[1] or (ctx.has_g and ctx.needs_input_grad[2]):
-            same = not ctx.has_g or ctx.dtypes[0] == ctx.dtypes[1]
-            dw = weight_grad(d2, x.reshape(-1, n_in), ctx.dtypes[0] if same else torch.float32)
-            dw_qkv = dw[:ctx.n_qkv].to(ctx.dtypes[0])
-            if ctx.has_g:
-                dw_g = dw[ctx.n_qkv:].to(ctx.dtypes[1])
-        return dx, dw_qkv, dw_g
-
-
-def in_projection(x, w_qkv, w_g=None):
-    """The stacked qkv (+ output-gate) projection of ``x`` [B,T,d_model]."""
-    if not x.is_cuda:
-        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
-    return _InProjection.apply(x, w_qkv, w_g)
-
-
 class _State:
-    """What the kernel-memory backward needs from its forward."""
+    """What the kernel-memory backward needs from its forward.  The tensors of
+    ``SAVED`` travel between the forward and backward ops; everything else is
+    rebuilt from the op inputs (:func:`_restore`)."""
 
+    SAVED = ("saved", "ws", "phi_q", "phi_k", "num", "mass", "resid")
     __slots__ = ("spec", "normalize", "seg_chunks", "heads", "d", "has_gate", "has_tau", "tau_dtype", "w_dtypes",
                  "b_dtype", "ws", "proj", "w1c", "w2c", "tauf", "gb", "phi_q", "phi_k", "num", "mass", "resid",
                  "native", "io", "saved", "tau", "b_g", "tables")
@@ -339,13 +301,14 @@ _MEMORY: dict = {}
 
 def _memory_plan(spec: FeatureSpec, B, H, T, d, dtype, tau, b_g, w1, w2, normalize, has_gate, seg_chunks):
     """(desc, saved bytes, scratch bytes) of the one-call kernel memory
-    (ts_memory_fwd / ts_memory_bwd), or None where it does not apply."""
+    (ts_memory_fwd / ts_memory_bwd), or None where it does not apply (a host
+    query: no device work)."""
     pdt = w1.dtype
     if pdt not in (torch.bfloat16, torch.float32) or w2.dtype != pdt:
         return None
-    if tau is not None and (tau.dtype != pdt or tau.numel() != H or not tau.is_contiguous()):
+    if tau is not None and (tau.dtype != pdt or tau.numel() != H):
         return None
-    if b_g is not None and (b_g.dtype != pdt or b_g.numel() != H * d or not b_g.is_contiguous()):
+    if b_g is not None and (b_g.dtype != pdt or b_g.numel() != H * d):
         return None
     key = (B, H, T, d, spec.m, dtype, spec.kind, spec.in_rot, spec.feat_rot, spec.gain, spec.resid_scale, spec.eps,
            tau is not None, b_g is not None, bool(normalize), bool(has_gate), int(seg_chunks), pdt)
@@ -369,9 +332,24 @@ def _memory_plan(spec: FeatureSpec, B, H, T, d, dtype, tau, b_g, w1, w2, normali
     return hit or None
 
 
+def _use_native(proj, tau, b_g) -> bool:
+    """The one-call path runs unless launches are recorded per entry point or a
+    parameter is not a contiguous vector."""
+    return (not _lib.recording() and proj.is_contiguous() and (tau is None or tau.is_contiguous())
+            and (b_g is None or b_g.is_contiguous()))
+
+
 def _proj_view(base: int, es: int, col: int, T: int, P: int, d: int) -> _lib.Strided:
     """[B,H,T,d] view at column ``col`` of a [B,T,P] buffer at address ``base``."""
     return _lib.Strided(base + col * es, T * P, d, P)
+
+
+def _split_proj(proj, H: int, d: int, has_gate: bool):
+    """q, k, v (and the gate logits) as [B,H,T,d] views of the projection."""
+    B, T, P = proj.shape
+    qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
+    gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
+    return qkv[:, :, 0].transpose(1, 2), qkv[:, :, 1].transpose(1, 2), qkv[:, :, 2].transpose(1, 2), gv
 
 
 def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int,
@@ -380,24 +358,16 @@ def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, norma
     B, T, P = proj.shape
     H = heads
     d = P // (4 * H) if has_gate else P // (3 * H)
-    st.spec, st.normalize, st.seg_chunks, st.heads, st.d, st.has_gate = spec, normalize, seg_chunks, H, d, has_gate
-    st.has_tau, st.tau_dtype = tau is not None, None if tau is None else tau.dtype
-    st.w_dtypes, st.b_dtype = (w1.dtype, w2.dtype), None if b_g is None else b_g.dtype
-    st.native = None
-    if not _lib.recording() and proj.is_contiguous():
+    _describe(st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, H, d, has_gate)
+    if _use_native(proj, tau, b_g):
         plan = _memory_plan(spec, B, H, T, d, proj.dtype, tau, b_g, w1, w2, normalize, has_gate, seg_chunks)
         if plan is not None:
             return _native_forward(st, plan, proj, w1, w2, tau, b_g, spec, H, d, has_gate)
-    qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
-    q = qkv[:, :, 0].transpose(1, 2)
-    k = qkv[:, :, 1].transpose(1, 2)
-    v = qkv[:, :, 2].transpose(1, 2)
+    q, k, v, gv = _split_proj(proj, H, d, has_gate)
     dt = proj.dtype
-    w1c = w1.to(dt).contiguous()
-    w2c = w2.to(dt).contiguous()
-    tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
-    phi_k, _ = feature_fwd(spec, k, w1c, None, tauf, False)
-    phi_q, resid = feature_fwd(spec, q, w1c, w2c, tauf, True)
+    _weights_for(st, proj, w1, w2, tau, b_g)
+    phi_k, _ = feature_fwd(spec, k, st.w1c, None, st.tauf, False)
+    phi_q, resid = feature_fwd(spec, q, st.w1c, st.w2c, st.tauf, True)
     # The dq scan's segment states are the transpose of this scan's
     # (sum_i v_i phi_k_i^T; with the mass column its key-side row is this
     # scan's value-side sum_i phi_k_i), so the forward keeps them.
@@ -408,13 +378,46 @@ def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, norma
         phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
         seg_chunks=seg_chunks, workspace=ws,
     )
-    gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2) if has_gate else None
-    gb = None if b_g is None else b_g.detach().to(torch.float32).contiguous()
     y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
-    read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=gb)
-    st.ws, st.proj, st.w1c, st.w2c, st.tauf, st.gb = ws, proj, w1c, w2c, tauf, gb
-    st.phi_q, st.phi_k, st.num, st.mass, st.resid = phi_q, phi_k, num, mass, resid
+    read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=st.gb)
+    st.ws, st.phi_q, st.phi_k, st.num, st.mass, st.resid = ws, phi_q, phi_k, num, mass, resid
     return y.view(B, T, H * d)
+
+
+def _describe(st: _State, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, H, d, has_gate):
+    st.spec, st.normalize, st.seg_chunks, st.heads, st.d, st.has_gate = spec, normalize, seg_chunks, H, d, has_gate
+    st.has_tau, st.tau_dtype = tau is not None, None if tau is None else tau.dtype
+    st.w_dtypes, st.b_dtype = (w1.dtype, w2.dtype), None if b_g is None else b_g.dtype
+    st.proj, st.tau, st.b_g = proj, None if tau is None else tau.detach(), None if b_g is None else b_g.detach()
+    st.native = st.saved = st.ws = st.phi_q = st.phi_k = st.num = st.mass = st.resid = None
+
+
+def _weights_for(st: _State, proj, w1, w2, tau, b_g):
+    """Kernel-dtype copies of the memory weights (the per-entry-point path)."""
+    dt = proj.dtype
+    st.w1c = w1.detach().to(dt).contiguous()
+    st.w2c = w2.detach().to(dt).contiguous()
+    st.tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    st.gb = None if b_g is None else b_g.detach().to(torch.float32).contiguous()
+
+
+def _native_io(st: _State, proj, w1, w2, spec: FeatureSpec, H: int, d: int, has_gate: bool):
+    """The ts_memory_io of ``proj``; every tensor it names is kept on ``st``."""
+    B, T, P = proj.shape
+    dt = proj.dtype
+    st.w1c = w1.detach().to(dt).contiguous()
+    st.w2c = w2.detach().to(dt).contiguous()
+    # the io holds raw addresses that ts_memory_bwd reads again: the RoPE
+    # tables stay referenced here even if the table cache drops them
+    st.tables = spec.tables(T, proj.device)
+    ic, is_, fc, fs = st.tables
+    base, es, Hd = proj.data_ptr(), proj.element_size(), H * d
+    st.io = _lib.MemoryIO(_proj_view(base, es, 0, T, P, d), _proj_view(base, es, Hd, T, P, d),
+                          _proj_view(base, es, 2 * Hd, T, P, d),
+                          _proj_view(base, es, 3 * Hd, T, P, d) if has_gate else _lib.Strided(None, 0, 0, 0),
+                          st.w1c.data_ptr(), st.w2c.data_ptr(), _lib.ptr(st.tau), _lib.ptr(st.b_g), _lib.ptr(ic),
+                          _lib.ptr(is_), _lib.ptr(fc), _lib.ptr(fs))
+    return st.io
 
 
 def _native_forward(st: _State, plan, proj, w1, w2, tau, b_g, spec: FeatureSpec, H: int, d: int, has_gate: bool):
@@ -422,31 +425,38 @@ def _native_forward(st: _State, plan, proj, w1, w2, tau, b_g, spec: FeatureSpec,
     ``saved`` buffer that only the library reads."""
     desc, saved_bytes, _ = plan
     B, T, P = proj.shape
-    dt = proj.dtype
     dev = proj.device
     lib = _lib.load()
-    w1c = w1.detach().to(dt).contiguous()
-    w2c = w2.detach().to(dt).contiguous()
-    tau_ = None if tau is None else tau.detach()
-    bg_ = None if b_g is None else b_g.detach()
-    ic, is_, fc, fs = spec.tables(T, dev)
-    base, es, Hd = proj.data_ptr(), proj.element_size(), H * d
-    io = _lib.MemoryIO(_proj_view(base, es, 0, T, P, d), _proj_view(base, es, Hd, T, P, d),
-                       _proj_view(base, es, 2 * Hd, T, P, d),
-                       _proj_view(base, es, 3 * Hd, T, P, d) if has_gate else _lib.Strided(None, 0, 0, 0),
-                       w1c.data_ptr(), w2c.data_ptr(), _lib.ptr(tau_), _lib.ptr(bg_), _lib.ptr(ic), _lib.ptr(is_),
-                       _lib.ptr(fc), _lib.ptr(fs))
+    io = _native_io(st, proj, w1, w2, spec, H, d, has_gate)
     saved = torch.empty(saved_bytes, dtype=torch.uint8, device=dev)
-    y = torch.empty(B, T, Hd, dtype=dt, device=dev)
+    Hd = H * d
+    y = torch.empty(B, T, Hd, dtype=proj.dtype, device=dev)
     status = lib.ts_memory_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.Strided(y.data_ptr(), T * Hd, d, Hd),
                                saved.data_ptr(), saved_bytes, _lib.stream_handle(dev))
     _lib.check(status, "ts_memory_fwd")
-    # the io holds raw addresses that ts_memory_bwd reads again: keep every
-    # tensor it names alive, the RoPE tables included (the table cache may
-    # drop its entry before this step's backward runs)
-    st.native, st.io, st.saved, st.tables = plan, io, saved, (ic, is_, fc, fs)
-    st.proj, st.w1c, st.w2c, st.tau, st.b_g = proj, w1c, w2c, tau_, bg_
+    st.native, st.saved = plan, saved
     return y
+
+
+def _restore(saved_tensors, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int, H: int,
+             has_gate: bool) -> _State:
+    """The forward's :class:`_State` from the op inputs and its saved tensors."""
+    st = _State()
+    B, T, P = proj.shape
+    d = P // (4 * H) if has_gate else P // (3 * H)
+    _describe(st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, H, d, has_gate)
+    vals = dict(zip(_State.SAVED, (None if t is None or (t.ndim == 1 and t.numel() == 0 and name != "saved")
+                                   else t for name, t in zip(_State.SAVED, saved_tensors))))
+    if vals["saved"] is not None and vals["saved"].numel() > 0:
+        st.native = _memory_plan(spec, B, H, T, d, proj.dtype, st.tau, st.b_g, w1, w2, normalize, has_gate,
+                                 seg_chunks)
+        st.saved = vals["saved"]
+        _native_io(st, proj, w1, w2, spec, H, d, has_gate)
+        return st
+    _weights_for(st, proj, w1, w2, tau, b_g)
+    for name in _State.SAVED[1:]:
+        setattr(st, name, vals[name])
+    return st
 
 
 def _native_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: bool, need_b: bool):
@@ -491,26 +501,16 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
     H, d = st.heads, st.d
     dt = proj.dtype
     num, mass, resid, phi_q, phi_k = st.num, st.mass, st.resid, st.phi_q, st.phi_k
-    qkv = proj[..., :3 * H * d].view(B, T, 3, H, d)
-    q = qkv[:, :, 0].transpose(1, 2)
-    k = qkv[:, :, 1].transpose(1, 2)
-    v = qkv[:, :, 2].transpose(1, 2)
+    q, k, v, gv = _split_proj(proj, H, d, st.has_gate)
     dproj = torch.empty_like(proj)
-    dqkv = dproj[..., :3 * H * d].view(B, T, 3, H, d)
-    dq = dqkv[:, :, 0].transpose(1, 2)
-    dk = dqkv[:, :, 1].transpose(1, 2)
-    dv = dqkv[:, :, 2].transpose(1, 2)
-    gv = dgv = None
-    if st.has_gate:
-        gv = proj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
-        dgv = dproj[..., 3 * H * d:].view(B, T, H, d).transpose(1, 2)
+    dq, dk, dv, dgv = _split_proj(dproj, H, d, st.has_gate)
     dyv = dy.to(dt).view(B, T, H, d).transpose(1, 2)
     want_gb = st.gb is not None and need_b
     dnum, dmass, (dresid, _), _, db_g = read_bwd(num, mass, resid, gv, dyv, spec.resid_scale, spec.eps, dg=dgv,
                                                  gbias=st.gb, gbias_grad=st.b_dtype if want_gb else None)
     norm = st.normalize
     q_ext = dmass if norm else None
-    ws_f, st.ws = st.ws, None
+    ws_f = st.ws
     # dq = scan(dnum, v, phi_k): its segment states are the forward's, transposed
     dphi_q, _, _ = scan_hip.scan_launch(dnum, v, phi_k, q_ext=q_ext, k_ext="ones" if norm else None,
                                         seg_chunks=st.seg_chunks, workspace=ws_f,
@@ -544,65 +544,112 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
     return dproj, dw1, dw2, dtau, db_g
 
 
-class _KernelMemory(torch.autograd.Function):
-    """y[B,T,H*d] = read(scan(feature(q), feature(k), v)) * silu(g + b_g) for a depth-1 kernel memory.
+# The depth-1 kernel-memory mixer as torch.library custom ops: one forward op
+# (the stacked qkv / gate projection GEMM, the kernel memory, the output
+# projection: block.py:593-599, 721-724 around engine.py's read) and one
+# backward op (split-K weight-gradient GEMMs around the memory backward).
+# TorchDynamo records each as one opaque call; the tensors the backward needs
+# are outputs of the forward op, placeholders (empty tensors) where absent.
 
-    ``proj`` is the [B,T,3*H*d (+H*d)] input projection: q, k, v heads, then
-    the output-gate logits when ``has_gate``.  The gradient of ``proj`` is one
-    tensor, written in place by the kernels.
-    """
-
-    @staticmethod
-    def forward(ctx, proj, w1, w2, tau, b_g, spec: FeatureSpec, normalize: bool, seg_chunks: int, heads: int,
-                has_gate: bool):
-        ctx.st = _State()
-        return _memory_forward(ctx.st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
-
-    @staticmethod
-    def backward(ctx, dy):
-        n = ctx.needs_input_grad
-        dproj, dw1, dw2, dtau, db_g = _memory_backward(ctx.st, dy, n[1], n[2], n[3], n[4])
-        return dproj, dw1, dw2, dtau, db_g, None, None, None, None, None
+def _spec_args(spec: FeatureSpec):
+    return (int(spec.kind), int(spec.m), float(spec.gain), int(spec.in_rot), int(spec.feat_rot),
+            float(spec.rope_base), float(spec.resid_scale), float(spec.eps))
 
 
-class _KernelMixer(torch.autograd.Function):
-    """The whole depth-1 kernel-memory mixer as one autograd node: the stacked
-    qkv / gate projection GEMM, the kernel memory and the output projection
-    (block.py:593-599, 721-724 around engine.py's read); backward in the same
-    node (split-K weight-gradient GEMMs)."""
+@torch.library.custom_op("thetascan_hip::kernel_mixer", mutates_args=())
+def _kernel_mixer_op(x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None, b_g: torch.Tensor | None,
+                     w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None, w_out: torch.Tensor, kind: int,
+                     m: int, gain: float, in_rot: int, feat_rot: int, rope_base: float, resid_scale: float,
+                     eps: float, normalize: bool, seg_chunks: int, heads: int) -> list[torch.Tensor]:
+    spec = FeatureSpec(kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps)
+    weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
+    proj = torch.nn.functional.linear(x, weight)
+    st = _State()
+    y = _memory_forward(st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, w_g is not None)
+    out = torch.nn.functional.linear(y, w_out)
+    return [out, proj, y] + [x.new_empty(0) if getattr(st, n) is None else getattr(st, n) for n in _State.SAVED]
 
-    @staticmethod
-    def forward(ctx, x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec: FeatureSpec, normalize: bool, seg_chunks: int,
-                heads: int):
-        has_gate = w_g is not None
-        weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
-        proj = torch.nn.functional.linear(x, weight)
-        ctx.st = _State()
-        y = _memory_forward(ctx.st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
-        ctx.save_for_backward(x, weight, y, w_out)
-        ctx.n_qkv = w_qkv.shape[0]
-        ctx.dtypes = (w_qkv.dtype, None if w_g is None else w_g.dtype, w_out.dtype)
-        return torch.nn.functional.linear(y, w_out)
 
-    @staticmethod
-    def backward(ctx, dout):
-        x, weight, y, w_out = ctx.saved_tensors
-        n = ctx.needs_input_grad
-        d2 = dout.reshape(-1, w_out.shape[0])
-        dw_out = weight_grad(d2, y.reshape(-1, y.shape[-1]), ctx.dtypes[2]) if n[7] else None
-        dy = (d2 @ w_out).view(y.shape)
-        dproj, dw1, dw2, dtau, db_g = _memory_backward(ctx.st, dy, n[4], n[5], n[6], n[3])
-        P = weight.shape[0]
-        dp2 = dproj.view(-1, P)
-        dx = (dp2 @ weight).view(x.shape) if n[0] else None
-        dw_qkv = dw_g = None
-        if n[1] or n[2]:
-            same = ctx.dtypes[1] is None or ctx.dtypes[0] == ctx.dtypes[1]
-            dw = weight_grad(dp2, x.reshape(-1, x.shape[-1]), ctx.dtypes[0] if same else torch.float32)
-            dw_qkv = dw[:ctx.n_qkv].to(ctx.dtypes[0])
-            if ctx.dtypes[1] is not None:
-                dw_g = dw[ctx.n_qkv:].to(ctx.dtypes[1])
-        return dx, dw_qkv, dw_g, db_g, dw1, dw2, dtau, dw_out, None, None, None, None
+@_kernel_mixer_op.register_fake
+def _(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps,
+      normalize, seg_chunks, heads):
+    spec = FeatureSpec(kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps)
+    B, T, _ = x.shape
+    H = heads
+    P = w_qkv.shape[0] + (0 if w_g is None else w_g.shape[0])
+    d = w_qkv.shape[0] // (3 * H)
+    dev, dt = x.device, x.dtype
+    out = x.new_empty(B, T, w_out.shape[0])
+    proj = x.new_empty(B, T, P)
+    y = x.new_empty(B, T, H * d)
+    plan = _memory_plan(spec, B, H, T, d, dt, tau, b_g, w1, w2, normalize, w_g is not None, seg_chunks) \
+        if _use_native(proj, tau, b_g) else None
+    if plan is not None:
+        return [out, proj, y, torch.empty(plan[1], dtype=torch.uint8, device=dev)] + \
+            [x.new_empty(0) for _ in range(6)]
+    ws = x.new_empty(0)
+    if m == d:
+        nbytes = scan_hip.workspace_bytes(B, H, T, m, d, dt, seg_chunks=seg_chunks, v_ext=normalize)
+        if nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    mass = torch.empty(B, H, T, dtype=torch.float32, device=dev) if normalize else x.new_empty(0)
+    return [out, proj, y, x.new_empty(0), ws, x.new_empty(B, H, T, m), x.new_empty(B, H, T, m),
+            x.new_empty(B, H, T, d), mass, x.new_empty(B, H, T, d)]
+
+
+@torch.library.custom_op("thetascan_hip::kernel_mixer_backward", mutates_args=())
+def _kernel_mixer_bwd_op(dout: torch.Tensor, x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None,
+                         b_g: torch.Tensor | None, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None,
+                         w_out: torch.Tensor, proj: torch.Tensor, y: torch.Tensor, saved: list[torch.Tensor],
+                         kind: int, m: int, gain: float, in_rot: int, feat_rot: int, rope_base: float,
+                         resid_scale: float, eps: float, normalize: bool, seg_chunks: int, heads: int,
+                         need: list[bool]) -> list[torch.Tensor]:
+    spec = FeatureSpec(kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps)
+    has_gate = w_g is not None
+    st = _restore(saved, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
+    d2 = dout.reshape(-1, w_out.shape[0])
+    dw_out = weight_grad(d2, y.reshape(-1, y.shape[-1]), w_out.dtype) if need[7] else None
+    dy = (d2 @ w_out).view(y.shape)
+    dproj, dw1, dw2, dtau, db_g = _memory_backward(st, dy, need[4], need[5], need[6], need[3])
+    weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
+    P = weight.shape[0]
+    dp2 = dproj.view(-1, P)
+    dx = (dp2 @ weight).view(x.shape) if need[0] else None
+    dw_qkv = dw_g = None
+    if need[1] or (has_gate and need[2]):
+        same = not has_gate or w_qkv.dtype == w_g.dtype
+        dw = weight_grad(dp2, x.reshape(-1, x.shape[-1]), w_qkv.dtype if same else torch.float32)
+        dw_qkv = dw[:w_qkv.shape[0]].to(w_qkv.dtype)
+        if has_gate:
+            # its own storage: an op's outputs may not share one
+            dw_g = dw[w_qkv.shape[0]:].to(w_g.dtype, copy=True)
+    grads = [dx, dw_qkv, dw_g, db_g, dw1, dw2, dtau, dw_out]
+    return [x.new_empty(0) if g is None else g for g in grads]
+
+
+@_kernel_mixer_bwd_op.register_fake
+def _(dout, x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, saved, kind, m, gain, in_rot, feat_rot, rope_base,
+      resid_scale, eps, normalize, seg_chunks, heads, need):
+    like = [x, w_qkv, w_g, b_g, w1, w2, tau, w_out]
+    return [t.new_empty(t.shape) if (t is not None and w) else x.new_empty(0) for t, w in zip(like, need)]
+
+
+def _kernel_mixer_setup(ctx, inputs, output):
+    x, w_qkv, w_g, b_g, w1, w2, tau, w_out, *args = inputs
+    ctx.args = args
+    tensors = [x, w_qkv, w_g, b_g, w1, w2, tau, w_out]
+    ctx.need = [t is not None and t.requires_grad for t in tensors]
+    ctx.save_for_backward(*tensors, *output[1:])
+
+
+def _kernel_mixer_backward(ctx, grads):
+    x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, *saved = ctx.saved_tensors
+    res = _kernel_mixer_bwd_op(grads[0], x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, list(saved), *ctx.args,
+                               ctx.need)
+    return (*[g if w else None for g, w in zip(res, ctx.need)], *([None] * len(ctx.args)))
+
+
+_kernel_mixer_op.register_autograd(_kernel_mixer_backward, setup_context=_kernel_mixer_setup)
 
 
 def kernel_mixer(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec: FeatureSpec, normalize: bool, heads: int,
@@ -612,14 +659,5 @@ def kernel_mixer(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec: FeatureSpec, norm
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
     if not x.is_contiguous():
         x = x.contiguous()
-    return _KernelMixer.apply(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec, normalize, seg_chunks, heads)
-
-
-def kernel_memory(proj, w1, w2, tau, spec: FeatureSpec, normalize: bool, heads: int, has_gate: bool,
-                  seg_chunks: int = 0, gate_bias=None):
-    """Fused kernel-memory read of the [B,T,3*H*d (+H*d)] input projection."""
-    if not proj.is_cuda:
-        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
-    if not proj.is_contiguous():
-        proj = proj.contiguous()
-    return _KernelMemory.apply(proj, w1, w2, tau, gate_bias, spec, normalize, seg_chunks, heads, has_gate)
+    return _kernel_mixer_op(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, *_spec_args(spec), bool(normalize),
+                            int(seg_chunks), int(heads))[0]

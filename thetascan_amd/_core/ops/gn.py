@@ -81,66 +81,101 @@ def contract_tokens(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return parts.view(H, S, p, q).sum(1, dtype=torch.float32)
 
 
-class _GnWrite(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, v, w1, w2, tau, s, inv_depth, eps):
-        lib = _lib.load()
-        xk, vk = _rows(x), _rows(v)
-        B, H, T, d = xk.shape
-        m = w1.shape[1]
-        dt = x.dtype
-        w1c = w1.detach().to(dt).contiguous()
-        w2c = w2.detach().to(dt).contiguous()
-        w2t = w2c.transpose(1, 2).contiguous()
-        tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
-        h = torch.empty(B, H, T, m, dtype=dt, device=x.device)
-        lam = torch.empty(B, H, T, d, dtype=dt, device=x.device)
-        g = torch.empty(B, H, T, m, dtype=dt, device=x.device)
-        desc = _desc(xk, m, tc is not None, s, inv_depth, eps)
-        io = _lib.GnIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w2t.data_ptr(),
-                       _lib.ptr(tc), _lib.strided(h), _lib.strided(lam), _lib.strided(g))
-        with _lib.timed("ts_gn_write_fwd", lambda: _lib.nbytes(xk, vk, h, lam, g)):
-            status = lib.ts_gn_write_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
-        _lib.check(status, "ts_gn_write_fwd")
-        ctx.save_for_backward(xk, vk, w1c, w2c, w2t, tc)
-        ctx.meta = (s, inv_depth, eps, tau is not None, w1.dtype, w2.dtype, None if tau is None else tau.dtype)
-        return h, lam, g
+@torch.library.custom_op("thetascan_hip::gn_write", mutates_args=())
+def _gn_write_op(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None,
+                 s: float, inv_depth: float, eps: float) -> list[torch.Tensor]:
+    lib = _lib.load()
+    xk, vk = _rows(x), _rows(v)
+    B, H, T, d = xk.shape
+    m = w1.shape[1]
+    dt = x.dtype
+    w1c = w1.detach().to(dt).contiguous()
+    w2c = w2.detach().to(dt).contiguous()
+    w2t = w2c.transpose(1, 2).contiguous()
+    tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    h = torch.empty(B, H, T, m, dtype=dt, device=x.device)
+    lam = torch.empty(B, H, T, d, dtype=dt, device=x.device)
+    g = torch.empty(B, H, T, m, dtype=dt, device=x.device)
+    desc = _desc(xk, m, tc is not None, s, inv_depth, eps)
+    io = _lib.GnIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w2t.data_ptr(),
+                   _lib.ptr(tc), _lib.strided(h), _lib.strided(lam), _lib.strided(g))
+    with _lib.timed("ts_gn_write_fwd", lambda: _lib.nbytes(xk, vk, h, lam, g)):
+        status = lib.ts_gn_write_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(x.device))
+    _lib.check(status, "ts_gn_write_fwd")
+    return [h, lam, g]
 
-    @staticmethod
-    def backward(ctx, dh, dlam, dg):
-        xk, vk, w1c, w2c, w2t, tc = ctx.saved_tensors
-        s, inv_depth, eps, has_tau, w1_dtype, w2_dtype, tau_dtype = ctx.meta
-        lib = _lib.load()
-        B, H, T, d = xk.shape
-        m = w1c.shape[1]
-        dt = xk.dtype
-        N = B * T
 
-        def grad(t):
-            return None if t is None else _rows(t.to(dt))
+@_gn_write_op.register_fake
+def _(x, v, w1, w2, tau, s, inv_depth, eps):
+    B, H, T, d = x.shape
+    m = w1.shape[1]
+    return [x.new_empty(B, H, T, m), x.new_empty(B, H, T, d), x.new_empty(B, H, T, m)]
 
-        dh, dlam, dg = grad(dh), grad(dlam), grad(dg)
-        w1t = w1c.transpose(1, 2).contiguous()
-        dx = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
-        dv = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
-        nsm = 5 if has_tau else 4
-        tm = torch.empty(nsm, H, N, m, dtype=dt, device=xk.device)
-        td = torch.empty(4, H, N, d, dtype=dt, device=xk.device)
-        desc = _desc(xk, m, has_tau, s, inv_depth, eps)
-        io = _lib.GnBwdIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w1t.data_ptr(),
-                          w2t.data_ptr(), _lib.ptr(tc), _lib.strided(dh), _lib.strided(dlam), _lib.strided(dg),
-                          _lib.strided(None), _lib.strided(dx), _lib.strided(dv), tm.data_ptr(), td.data_ptr())
-        with _lib.timed("ts_gn_write_bwd", lambda: _lib.nbytes(xk, vk, dh, dlam, dg, dx, dv, tm, td)):
-            status = lib.ts_gn_write_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(xk.device))
-        _lib.check(status, "ts_gn_write_bwd")
-        # dW1 = da^T x;  dW2 = lam^T dz + du^T h + 2 W2 o (drq^T s2);  dtau = -sum dpre
-        dw1 = contract_tokens(tm[2], td[2])
-        dw2 = contract_tokens(td[0], tm[0]) + contract_tokens(td[1], tm[1])
-        dw2 = dw2 + 2.0 * w2c.to(torch.float32) * contract_tokens(td[3], tm[3])
-        dtau = None
-        if has_tau and ctx.needs_input_grad[4]:
-            dtau = (-tm[4].sum(1, dtype=torch.float32)).to(tau_dtype)
-        return dx, dv, dw1.to(w1_dtype), dw2.to(w2_dtype), dtau, None, None, None
+
+@torch.library.custom_op("thetascan_hip::gn_write_backward", mutates_args=())
+def _gn_write_bwd_op(dh: torch.Tensor | None, dlam: torch.Tensor | None, dg: torch.Tensor | None, x: torch.Tensor,
+                     v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None, s: float,
+                     inv_depth: float, eps: float, need_tau: bool) -> list[torch.Tensor]:
+    lib = _lib.load()
+    xk, vk = _rows(x), _rows(v)
+    B, H, T, d = xk.shape
+    m = w1.shape[1]
+    dt = xk.dtype
+    N = B * T
+    w1c = w1.detach().to(dt).contiguous()
+    w2c = w2.detach().to(dt).contiguous()
+    w2t = w2c.transpose(1, 2).contiguous()
+    w1t = w1c.transpose(1, 2).contiguous()
+    tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    has_tau = tc is not None
+
+    def grad(t):
+        return None if t is None else _rows(t.to(dt))
+
+    dh, dlam, dg = grad(dh), grad(dlam), grad(dg)
+    dx = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
+    dv = torch.empty(B, H, T, d, dtype=dt, device=xk.device)
+    nsm = 5 if has_tau else 4
+    tm = torch.empty(nsm, H, N, m, dtype=dt, device=xk.device)
+    td = torch.empty(4, H, N, d, dtype=dt, device=xk.device)
+    desc = _desc(xk, m, has_tau, s, inv_depth, eps)
+    io = _lib.GnBwdIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w1t.data_ptr(),
+                      w2t.data_ptr(), _lib.ptr(tc), _lib.strided(dh), _lib.strided(dlam), _lib.strided(dg),
+                      _lib.strided(None), _lib.strided(dx), _lib.strided(dv), tm.data_ptr(), td.data_ptr())
+    with _lib.timed("ts_gn_write_bwd", lambda: _lib.nbytes(xk, vk, dh, dlam, dg, dx, dv, tm, td)):
+        status = lib.ts_gn_write_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(xk.device))
+    _lib.check(status, "ts_gn_write_bwd")
+    # dW1 = da^T x;  dW2 = lam^T dz + du^T h + 2 W2 o (drq^T s2);  dtau = -sum dpre
+    dw1 = contract_tokens(tm[2], td[2])
+    dw2 = contract_tokens(td[0], tm[0]) + contract_tokens(td[1], tm[1])
+    dw2 = dw2 + 2.0 * w2c.to(torch.float32) * contract_tokens(td[3], tm[3])
+    dtau = x.new_empty(0)
+    if has_tau and need_tau:
+        dtau = (-tm[4].sum(1, dtype=torch.float32)).to(tau.dtype)
+    return [dx, dv, dw1.to(w1.dtype), dw2.to(w2.dtype), dtau]
+
+
+@_gn_write_bwd_op.register_fake
+def _(dh, dlam, dg, x, v, w1, w2, tau, s, inv_depth, eps, need_tau):
+    dtau = x.new_empty(0) if (tau is None or not need_tau) else tau.new_empty(tau.shape)
+    return [x.new_empty(x.shape), x.new_empty(x.shape), w1.new_empty(w1.shape), w2.new_empty(w2.shape), dtau]
+
+
+def _gn_write_setup(ctx, inputs, output):
+    x, v, w1, w2, tau, s, inv_depth, eps = inputs
+    ctx.args = (s, inv_depth, eps)
+    ctx.need_tau = tau is not None and tau.requires_grad
+    ctx.save_for_backward(x, v, w1, w2, tau)
+
+
+def _gn_write_backward(ctx, grads):
+    x, v, w1, w2, tau = ctx.saved_tensors
+    dh, dlam, dg = grads
+    dx, dv, dw1, dw2, dtau = _gn_write_bwd_op(dh, dlam, dg, x, v, w1, w2, tau, *ctx.args, ctx.need_tau)
+    return dx, dv, dw1, dw2, (dtau if ctx.need_tau else None), None, None, None
+
+
+_gn_write_op.register_autograd(_gn_write_backward, setup_context=_gn_write_setup)
 
 
 def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps: float = 1e-6):
@@ -156,7 +191,8 @@ def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps
         w2 = w2.expand(H, -1, -1)
     if tau is not None and tau.shape != (H, w1.shape[1]):
         tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
-    return _GnWrite.apply(x, v, w1, w2, tau, s, inv_depth, eps)
+    h, lam, g = _gn_write_op(x, v, w1, w2, tau, float(s), float(inv_depth), float(eps))
+    return h, lam, g
 
 
 # ------------------------------------------------------------------ GN read
@@ -170,68 +206,103 @@ def _read_desc(q, m, has_tau, corr, want_resid, s, eps):
                            float(s), float(eps))
 
 
-class _GnRead(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, w1, w2, tau, num, mass, corr, want_resid, s, eps):
-        lib = _lib.load()
-        qk = _rows(q)
-        B, H, T, d = qk.shape
-        m = w1.shape[1]
-        dt = q.dtype
-        w1c = w1.detach().to(dt).contiguous()
-        w2c = w2.detach().to(dt).contiguous() if want_resid else None
-        tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
-        nk = None if num is None else _rows(num.to(dt))
-        mk = None if mass is None else mass.detach().to(torch.float32)
-        h = torch.empty(B, H, T, m, dtype=dt, device=q.device)
-        resid = torch.empty(B, H, T, d, dtype=dt, device=q.device) if want_resid else None
-        desc = _read_desc(qk, m, tc is not None, corr, want_resid, s, eps)
-        io = _lib.GnReadIO(_lib.strided(qk), w1c.data_ptr(), _lib.ptr(w2c), _lib.ptr(tc), _lib.strided(nk),
-                           _lib.strided(mk), _lib.strided(h), _lib.strided(resid))
-        with _lib.timed("ts_gn_read_fwd", lambda: _lib.nbytes(qk, nk, mk, h, resid)):
-            status = lib.ts_gn_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(q.device))
-        _lib.check(status, "ts_gn_read_fwd")
-        ctx.save_for_backward(qk, w1c, w2c, tc, nk, mk)
-        ctx.meta = (corr, want_resid, s, eps, w1.dtype, None if w2 is None else w2.dtype,
-                    None if tau is None else tau.dtype, None if num is None else num.dtype)
-        if want_resid:
-            return h, resid
-        return h, None
+@torch.library.custom_op("thetascan_hip::gn_read", mutates_args=())
+def _gn_read_op(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None, tau: torch.Tensor | None,
+                num: torch.Tensor | None, mass: torch.Tensor | None, corr: int, want_resid: bool, s: float,
+                eps: float) -> list[torch.Tensor]:
+    lib = _lib.load()
+    qk = _rows(q)
+    B, H, T, d = qk.shape
+    m = w1.shape[1]
+    dt = q.dtype
+    w1c = w1.detach().to(dt).contiguous()
+    w2c = w2.detach().to(dt).contiguous() if want_resid else None
+    tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    nk = None if num is None else _rows(num.to(dt))
+    mk = None if mass is None else mass.detach().to(torch.float32)
+    h = torch.empty(B, H, T, m, dtype=dt, device=q.device)
+    resid = torch.empty(B, H, T, d, dtype=dt, device=q.device) if want_resid else q.new_empty(0)
+    desc = _read_desc(qk, m, tc is not None, corr, want_resid, s, eps)
+    io = _lib.GnReadIO(_lib.strided(qk), w1c.data_ptr(), _lib.ptr(w2c), _lib.ptr(tc), _lib.strided(nk),
+                       _lib.strided(mk), _lib.strided(h), _lib.strided(resid if want_resid else None))
+    with _lib.timed("ts_gn_read_fwd", lambda: _lib.nbytes(qk, nk, mk, h, resid)):
+        status = lib.ts_gn_read_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(q.device))
+    _lib.check(status, "ts_gn_read_fwd")
+    return [h, resid]
 
-    @staticmethod
-    def backward(ctx, dh, dresid):
-        qk, w1c, w2c, tc, nk, mk = ctx.saved_tensors
-        corr, want_resid, s, eps, w1_dtype, w2_dtype, tau_dtype, num_dtype = ctx.meta
-        lib = _lib.load()
-        B, H, T, d = qk.shape
-        m = w1c.shape[1]
-        dt = qk.dtype
-        N = B * T
-        dh = None if dh is None else _rows(dh.to(dt))
-        dresid = None if (dresid is None or not want_resid) else _rows(dresid.to(dt))
-        w1t = w1c.transpose(1, 2).contiguous()
-        w2t = w2c.transpose(1, 2).contiguous() if want_resid else None
-        dq = torch.empty(B, H, T, d, dtype=dt, device=qk.device)
-        dnum = torch.empty(B, H, T, m, dtype=dt, device=qk.device) if corr else None
-        dmass = torch.empty(B, H, T, dtype=torch.float32, device=qk.device) if corr == READ_NORMALIZED else None
-        has_tau = tc is not None
-        tm = torch.empty(3 if has_tau else 2, H, N, m, dtype=dt, device=qk.device)
-        td = torch.empty(2, H, N, d, dtype=dt, device=qk.device)
-        desc = _read_desc(qk, m, has_tau, corr, want_resid, s, eps)
-        io = _lib.GnReadBwdIO(_lib.strided(qk), w1c.data_ptr(), w1t.data_ptr(), _lib.ptr(w2t), _lib.ptr(tc),
-                              _lib.strided(nk), _lib.strided(mk), _lib.strided(dh), _lib.strided(dresid),
-                              _lib.strided(dq), _lib.strided(dnum), _lib.ptr(dmass), tm.data_ptr(), td.data_ptr())
-        with _lib.timed("ts_gn_read_bwd", lambda: _lib.nbytes(qk, nk, mk, dh, dresid, dq, dnum, dmass, tm, td)):
-            status = lib.ts_gn_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(qk.device))
-        _lib.check(status, "ts_gn_read_bwd")
-        dw1 = contract_tokens(tm[0], td[0]).to(w1_dtype)
-        dw2 = contract_tokens(td[1], tm[1]).to(w2_dtype) if want_resid else None
-        dtau = None
-        if has_tau and ctx.needs_input_grad[3]:
-            dtau = (-tm[2].sum(1, dtype=torch.float32)).to(tau_dtype)
-        if dnum is not None:
-            dnum = dnum.to(num_dtype)
-        return dq, dw1, dw2, dtau, dnum, dmass, None, None, None, None
+
+@_gn_read_op.register_fake
+def _(q, w1, w2, tau, num, mass, corr, want_resid, s, eps):
+    B, H, T, d = q.shape
+    return [q.new_empty(B, H, T, w1.shape[1]), q.new_empty(B, H, T, d) if want_resid else q.new_empty(0)]
+
+
+@torch.library.custom_op("thetascan_hip::gn_read_backward", mutates_args=())
+def _gn_read_bwd_op(dh: torch.Tensor | None, dresid: torch.Tensor | None, q: torch.Tensor, w1: torch.Tensor,
+                    w2: torch.Tensor | None, tau: torch.Tensor | None, num: torch.Tensor | None,
+                    mass: torch.Tensor | None, corr: int, want_resid: bool, s: float, eps: float, need_tau: bool
+                    ) -> list[torch.Tensor]:
+    lib = _lib.load()
+    qk = _rows(q)
+    B, H, T, d = qk.shape
+    m = w1.shape[1]
+    dt = qk.dtype
+    N = B * T
+    w1c = w1.detach().to(dt).contiguous()
+    w1t = w1c.transpose(1, 2).contiguous()
+    w2t = w2.detach().to(dt).transpose(1, 2).contiguous() if want_resid else None
+    tc = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    nk = None if num is None else _rows(num.to(dt))
+    mk = None if mass is None else mass.detach().to(torch.float32)
+    dh = None if dh is None else _rows(dh.to(dt))
+    dresid = None if (dresid is None or not want_resid) else _rows(dresid.to(dt))
+    dq = torch.empty(B, H, T, d, dtype=dt, device=qk.device)
+    dnum = torch.empty(B, H, T, m, dtype=dt, device=qk.device) if corr else None
+    dmass = torch.empty(B, H, T, dtype=torch.float32, device=qk.device) if corr == READ_NORMALIZED else None
+    has_tau = tc is not None
+    tm = torch.empty(3 if has_tau else 2, H, N, m, dtype=dt, device=qk.device)
+    td = torch.empty(2, H, N, d, dtype=dt, device=qk.device)
+    desc = _read_desc(qk, m, has_tau, corr, want_resid, s, eps)
+    io = _lib.GnReadBwdIO(_lib.strided(qk), w1c.data_ptr(), w1t.data_ptr(), _lib.ptr(w2t), _lib.ptr(tc),
+                          _lib.strided(nk), _lib.strided(mk), _lib.strided(dh), _lib.strided(dresid),
+                          _lib.strided(dq), _lib.strided(dnum), _lib.ptr(dmass), tm.data_ptr(), td.data_ptr())
+    with _lib.timed("ts_gn_read_bwd", lambda: _lib.nbytes(qk, nk, mk, dh, dresid, dq, dnum, dmass, tm, td)):
+        status = lib.ts_gn_read_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(qk.device))
+    _lib.check(status, "ts_gn_read_bwd")
+    dw1 = contract_tokens(tm[0], td[0]).to(w1.dtype)
+    dw2 = contract_tokens(td[1], tm[1]).to(w2.dtype) if want_resid else q.new_empty(0)
+    dtau = (-tm[2].sum(1, dtype=torch.float32)).to(tau.dtype) if (has_tau and need_tau) else q.new_empty(0)
+    dnum = q.new_empty(0) if dnum is None else dnum.to(num.dtype)
+    dmass = q.new_empty(0) if dmass is None else dmass.to(mass.dtype)
+    return [dq, dw1, dw2, dtau, dnum, dmass]
+
+
+@_gn_read_bwd_op.register_fake
+def _(dh, dresid, q, w1, w2, tau, num, mass, corr, want_resid, s, eps, need_tau):
+    return [q.new_empty(q.shape), w1.new_empty(w1.shape), w2.new_empty(w2.shape) if want_resid else q.new_empty(0),
+            tau.new_empty(tau.shape) if (tau is not None and need_tau) else q.new_empty(0),
+            num.new_empty(num.shape) if corr else q.new_empty(0),
+            mass.new_empty(mass.shape) if corr == READ_NORMALIZED else q.new_empty(0)]
+
+
+def _gn_read_setup(ctx, inputs, output):
+    q, w1, w2, tau, num, mass, corr, want_resid, s, eps = inputs
+    ctx.args = (corr, want_resid, s, eps)
+    ctx.need_tau = tau is not None and tau.requires_grad
+    ctx.save_for_backward(q, w1, w2, tau, num, mass)
+
+
+def _gn_read_backward(ctx, grads):
+    q, w1, w2, tau, num, mass = ctx.saved_tensors
+    corr, want_resid, s, eps = ctx.args
+    dh, dresid = grads
+    dq, dw1, dw2, dtau, dnum, dmass = _gn_read_bwd_op(dh, dresid if want_resid else None, q, w1, w2, tau, num,
+                                                      mass, corr, want_resid, s, eps, ctx.need_tau)
+    return (dq, dw1, dw2 if want_resid else None, dtau if ctx.need_tau else None,
+            dnum if corr else None, dmass if corr == READ_NORMALIZED else None, None, None, None, None)
+
+
+_gn_read_op.register_autograd(_gn_read_backward, setup_context=_gn_read_setup)
 
 
 def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = READ_NONE, want_resid: bool = False,
@@ -248,42 +319,67 @@ def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = REA
         w2 = w2.expand(H, -1, -1)
     if tau is not None and tau.shape != (H, w1.shape[1]):
         tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
-    return _GnRead.apply(q, w1, w2, tau, num, mass, corr, want_resid, s, eps)
+    h, resid = _gn_read_op(q, w1, w2, tau, num, mass, int(corr), bool(want_resid), float(s), float(eps))
+    return h, (resid if want_resid else None)
 
 
-class _NormalizedRead(torch.autograd.Function):
-    """y = resid + s * num / (mass + eps)  (or + s * num without mass):
-    the read epilogue of engine.py:440-442, 538-544 on ts_read_fwd/bwd."""
+@torch.library.custom_op("thetascan_hip::normalized_read", mutates_args=())
+def _normalized_read_op(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor, s: float, eps: float
+                        ) -> torch.Tensor:
+    """y = resid + s * num / (mass + eps)  (or + s * num without mass): the read
+    epilogue of engine.py:440-442, 538-544 on ts_read_fwd.  An fp32 numerator
+    (a difference of views) is read in fp32, then rounded once to the dtype of
+    ``resid``."""
+    from . import fused
 
-    @staticmethod
-    def forward(ctx, num, mass, resid, s, eps):
-        from . import fused
+    nk, rk = _rows(num), _rows(resid.to(num.dtype))
+    mk = None if mass is None else mass.detach().to(torch.float32)
+    y = torch.empty_like(nk)
+    fused.read_fwd(nk, mk, rk, None, y, s, eps)
+    return y.to(resid.dtype)
 
-        nk, rk = _rows(num), _rows(resid.to(num.dtype))
-        mk = None if mass is None else mass.detach().to(torch.float32)
-        y = torch.empty_like(nk)
-        fused.read_fwd(nk, mk, rk, None, y, s, eps)
-        ctx.save_for_backward(nk, mk, rk)
-        ctx.meta = (s, eps, resid.dtype, None if mass is None else mass.dtype)
-        # an fp32 numerator (a difference of views) is read in fp32, then
-        # rounded once to the stream dtype
-        return y.to(resid.dtype)
 
-    @staticmethod
-    def backward(ctx, dy):
-        from . import fused
+@_normalized_read_op.register_fake
+def _(num, mass, resid, s, eps):
+    return resid.new_empty(num.shape)
 
-        nk, mk, rk = ctx.saved_tensors
-        s, eps, resid_dtype, mass_dtype = ctx.meta
-        dnum, dmass, (dresid, _), _, _ = fused.read_bwd(nk, mk, rk, None, _rows(dy.to(nk.dtype)), s, eps)
-        if dmass is not None:
-            dmass = dmass.to(mass_dtype)
-        return dnum, dmass, dresid.to(resid_dtype), None, None
+
+@torch.library.custom_op("thetascan_hip::normalized_read_backward", mutates_args=())
+def _normalized_read_bwd_op(dy: torch.Tensor, num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor,
+                            s: float, eps: float) -> list[torch.Tensor]:
+    from . import fused
+
+    nk, rk = _rows(num), _rows(resid.to(num.dtype))
+    mk = None if mass is None else mass.detach().to(torch.float32)
+    dnum, dmass, (dresid, _), _, _ = fused.read_bwd(nk, mk, rk, None, _rows(dy.to(nk.dtype)), s, eps)
+    dmass = num.new_empty(0) if dmass is None else dmass.to(mass.dtype)
+    return [dnum, dmass, dresid.to(resid.dtype)]
+
+
+@_normalized_read_bwd_op.register_fake
+def _(dy, num, mass, resid, s, eps):
+    return [num.new_empty(num.shape), num.new_empty(0) if mass is None else mass.new_empty(mass.shape),
+            resid.new_empty(resid.shape)]
+
+
+def _normalized_read_setup(ctx, inputs, output):
+    num, mass, resid, s, eps = inputs
+    ctx.args = (s, eps)
+    ctx.save_for_backward(num, mass, resid)
+
+
+def _normalized_read_backward(ctx, dy):
+    num, mass, resid = ctx.saved_tensors
+    dnum, dmass, dresid = _normalized_read_bwd_op(dy, num, mass, resid, *ctx.args)
+    return dnum, (None if mass is None else dmass), dresid, None, None
+
+
+_normalized_read_op.register_autograd(_normalized_read_backward, setup_context=_normalized_read_setup)
 
 
 def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6):
     """Read epilogue of one view on the GPU (ts_read_fwd / ts_read_bwd)."""
-    return _NormalizedRead.apply(num, mass, resid, s, eps)
+    return _normalized_read_op(num, mass, resid, float(s), float(eps))
 
 
 def read_eligible(cfg, weights, q: torch.Tensor) -> bool:

@@ -48,65 +48,85 @@ def _fn(backend: str, chunk: int = scan_hip.DEFAULT_CHUNK):
 
 def ema_cumsum(x: torch.Tensor, log_alpha: torch.Tensor, chunk: int = 64) -> torch.Tensor:
     """z_t = sum_{i<=t} alpha^(t-i) x_i with static alpha[H] (interface.py:58-93)."""
-    return _WCumsum.apply(x, log_alpha, False)
+    return _wcumsum_op(x, log_alpha, False).to(x.dtype)
 
 
 def causal_prefix_sum(x: torch.Tensor) -> torch.Tensor:
     """Prefix sum along T (interface.py:96-107)."""
-    return _WCumsum.apply(x, None, False)
+    return _wcumsum_op(x, None, False).to(x.dtype)
 
 
 def decayed_prefix(x: torch.Tensor, decay: torch.Tensor) -> torch.Tensor:
     """z_t = sum_{i<=t} prod_{i<j<=t} a_j x_i for a [B,H,T,1] log-decay stream
     (the unit query/key scan of interface.py:229-230)."""
-    return _WCumsum.apply(x, decay, False)
+    return _wcumsum_op(x, decay, False).to(x.dtype)
 
 
-class _WCumsum(torch.autograd.Function):
-    """Decayed prefix along T with its transposed (anti-causal) backward."""
+# The decayed prefix as a torch.library custom op (opaque to TorchDynamo) with
+# its transposed (anti-causal) backward.  The op returns the fp32 prefix; the
+# caller casts.
 
-    @staticmethod
-    def forward(ctx, x, retention, reverse):
-        ctx.has_ret = retention is not None
-        ctx.reverse = reverse
-        ctx.x_dtype = x.dtype
-        out = fused.wcumsum(x, retention, reverse)
-        if retention is not None:
-            ctx.save_for_backward(retention, out)
-        else:
-            ctx.save_for_backward(out)
-        return out.to(x.dtype)
+@torch.library.custom_op("thetascan_hip::wcumsum", mutates_args=())
+def _wcumsum_op(x: torch.Tensor, retention: torch.Tensor | None, reverse: bool) -> torch.Tensor:
+    return fused.wcumsum(x, retention, reverse)
 
-    @staticmethod
-    def backward(ctx, grad):
-        saved = ctx.saved_tensors
-        retention = saved[0] if ctx.has_ret else None
-        out = saved[-1]
-        gx = fused.wcumsum(grad, retention, not ctx.reverse)
-        gret = None
-        if retention is not None and ctx.needs_input_grad[1]:
-            # z_t = a_t z_{t-1} + x_t  =>  dL/dlog a_t = gx_t * a_t z_{t-1}
-            z_prev = torch.zeros_like(out)
-            if ctx.reverse:
-                z_prev[:, :, :-1] = out[:, :, 1:]
-            else:
-                z_prev[:, :, 1:] = out[:, :, :-1]
-            if retention.ndim == 4:
-                a = retention.to(torch.float32).exp()
-                if ctx.reverse:
-                    a_shift = torch.zeros_like(a)
-                    a_shift[:, :, :-1] = a[:, :, 1:]
-                    a = a_shift
-                gl = (gx * z_prev).sum(-1, keepdim=True) * a
-                if ctx.reverse:
-                    shifted = torch.zeros_like(gl)
-                    shifted[:, :, 1:] = gl[:, :, :-1]
-                    gl = shifted
-                gret = gl.to(retention.dtype)
-            else:
-                a = retention.to(torch.float32).exp().view(1, -1, 1, 1)
-                gret = ((gx * z_prev).sum(dim=(0, 2, 3)) * a.view(-1)).to(retention.dtype).view_as(retention)
-        return gx.to(ctx.x_dtype), gret, None
+
+@_wcumsum_op.register_fake
+def _(x, retention, reverse):
+    return x.new_empty(x.shape, dtype=torch.float32)
+
+
+@torch.library.custom_op("thetascan_hip::wcumsum_backward", mutates_args=())
+def _wcumsum_bwd_op(grad: torch.Tensor, retention: torch.Tensor | None, out: torch.Tensor, reverse: bool,
+                    need_retention: bool) -> list[torch.Tensor]:
+    gx = fused.wcumsum(grad, retention, not reverse)
+    if retention is None or not need_retention:
+        return [gx, gx.new_empty(0)]
+    # z_t = a_t z_{t-1} + x_t  =>  dL/dlog a_t = gx_t * a_t z_{t-1}
+    z_prev = torch.zeros_like(out)
+    if reverse:
+        z_prev[:, :, :-1] = out[:, :, 1:]
+    else:
+        z_prev[:, :, 1:] = out[:, :, :-1]
+    if retention.ndim == 4:
+        a = retention.to(torch.float32).exp()
+        if reverse:
+            a_shift = torch.zeros_like(a)
+            a_shift[:, :, :-1] = a[:, :, 1:]
+            a = a_shift
+        gl = (gx * z_prev).sum(-1, keepdim=True) * a
+        if reverse:
+            shifted = torch.zeros_like(gl)
+            shifted[:, :, 1:] = gl[:, :, :-1]
+            gl = shifted
+        return [gx, gl.to(retention.dtype)]
+    a = retention.to(torch.float32).exp().view(1, -1, 1, 1)
+    gret = ((gx * z_prev).sum(dim=(0, 2, 3)) * a.view(-1)).to(retention.dtype).view_as(retention)
+    return [gx, gret]
+
+
+@_wcumsum_bwd_op.register_fake
+def _(grad, retention, out, reverse, need_retention):
+    if retention is None or not need_retention:
+        return [torch.empty_like(grad, dtype=torch.float32), grad.new_empty(0)]
+    return [torch.empty_like(grad, dtype=torch.float32), torch.empty_like(retention)]
+
+
+def _wcumsum_setup(ctx, inputs, output):
+    x, retention, reverse = inputs
+    ctx.reverse = reverse
+    ctx.x_dtype = x.dtype
+    ctx.need_retention = retention is not None and retention.requires_grad
+    ctx.save_for_backward(retention, output)
+
+
+def _wcumsum_backward(ctx, grad):
+    retention, out = ctx.saved_tensors
+    gx, gret = _wcumsum_bwd_op(grad.float(), retention, out, ctx.reverse, ctx.need_retention)
+    return gx.to(ctx.x_dtype), (gret if ctx.need_retention else None), None
+
+
+_wcumsum_op.register_autograd(_wcumsum_backward, setup_context=_wcumsum_setup)
 
 
 def _retention_stream(retention, like: torch.Tensor):

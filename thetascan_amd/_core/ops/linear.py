@@ -79,75 +79,130 @@ def column_sum(x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return slot_sum(parts, dtype, (cols,))
 
 
-class _Linear(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, weight, bias):
-        ctx.save_for_backward(x, weight)
-        ctx.has_bias = bias is not None
-        return F.linear(x, weight, bias)
+# F.linear whose backward forms the weight gradient as a split-K GEMM, and the
+# per-head GEMMs of the composed path, as torch.library custom ops: TorchDynamo
+# records them as opaque calls (their backward reaches the HIP reductions
+# through ctypes, which a traced graph cannot contain).
 
-    @staticmethod
-    def backward(ctx, dy):
-        x, weight = ctx.saved_tensors
-        n_out, n_in = weight.shape
-        dy2 = dy.reshape(-1, n_out)
-        dx = dw = db = None
-        if ctx.needs_input_grad[0]:
-            dx = (dy2 @ weight).view(x.shape)
-        if ctx.needs_input_grad[1]:
-            dw = weight_grad(dy2, x.reshape(-1, n_in), weight.dtype)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = column_sum(dy2, dy.dtype)
-        return dx, dw, db
+@torch.library.custom_op("thetascan_hip::linear", mutates_args=())
+def _linear_op(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    return F.linear(x, weight, bias)
+
+
+@_linear_op.register_fake
+def _(x, weight, bias):
+    return x.new_empty(*x.shape[:-1], weight.shape[0])
+
+
+@torch.library.custom_op("thetascan_hip::linear_backward", mutates_args=())
+def _linear_bwd_op(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, need: list[bool]) -> list[torch.Tensor]:
+    n_out, n_in = weight.shape
+    dy2 = dy.reshape(-1, n_out)
+    dx = (dy2 @ weight).view(x.shape) if need[0] else dy.new_empty(0)
+    dw = weight_grad(dy2, x.reshape(-1, n_in), weight.dtype) if need[1] else dy.new_empty(0)
+    db = column_sum(dy2, dy.dtype) if need[2] else dy.new_empty(0)
+    return [dx, dw, db]
+
+
+@_linear_bwd_op.register_fake
+def _(dy, x, weight, need):
+    return [x.new_empty(x.shape) if need[0] else dy.new_empty(0),
+            weight.new_empty(weight.shape) if need[1] else dy.new_empty(0),
+            dy.new_empty(weight.shape[0]) if need[2] else dy.new_empty(0)]
+
+
+def _linear_setup(ctx, inputs, output):
+    x, weight, bias = inputs
+    ctx.need = [x.requires_grad, weight.requires_grad, bias is not None and bias.requires_grad]
+    ctx.save_for_backward(x, weight)
+
+
+def _linear_backward(ctx, dy):
+    x, weight = ctx.saved_tensors
+    dx, dw, db = _linear_bwd_op(dy, x, weight, ctx.need)
+    return (dx if ctx.need[0] else None, dw if ctx.need[1] else None, db if ctx.need[2] else None)
+
+
+_linear_op.register_autograd(_linear_backward, setup_context=_linear_setup)
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """``F.linear`` whose weight gradient is a split-K batched GEMM."""
     if not x.is_cuda:
         return F.linear(x, weight, bias)
-    return _Linear.apply(x, weight, bias)
+    return _linear_op(x, weight, bias)
 
 
-class _HeadMatmul(torch.autograd.Function):
-    """y[b, h] = x[b, h] @ M[h] for a [B,H,T,K] stream and per-head (or shared)
-    matrices M [H or 1, K, N] (M = W^T or W): the fast-network GEMVs of the
-    composed path (engine.py:117-158, 180-195) as one batched GEMM per call,
-    without the permute copies of an einsum.  Both GEMMs take contiguous right
-    operands; the weight gradient is a token contraction per (batch, head)
-    (ts_contract_tokens) summed over the batch."""
+def _head_operand(W: torch.Tensor, B: int, H: int, K: int, trans: bool, dtype) -> torch.Tensor:
+    M = (W.transpose(-1, -2) if trans else W).to(dtype)
+    return M.expand(B, H, K, M.shape[-1]).reshape(B * H, K, M.shape[-1]).contiguous()
 
-    @staticmethod
-    def forward(ctx, x, W, trans: bool):
-        B, H, T, K = x.shape
-        M = (W.transpose(-1, -2) if trans else W).to(x.dtype)
-        N = M.shape[-1]
-        Mb = M.expand(B, H, K, N).reshape(B * H, K, N).contiguous()
-        x3 = x.reshape(B * H, T, K)
-        if not x3.is_contiguous():
-            x3 = x3.contiguous()
-        y = torch.bmm(x3, Mb).view(B, H, T, N)
-        ctx.save_for_backward(x3, Mb)
-        ctx.meta = (B, H, T, K, N, W.shape[0], trans, W.dtype)
-        return y
 
-    @staticmethod
-    def backward(ctx, dy):
-        from .gn import contract_tokens
+@torch.library.custom_op("thetascan_hip::head_matmul", mutates_args=())
+def _head_matmul_op(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tensor:
+    B, H, T, K = x.shape
+    Mb = _head_operand(W, B, H, K, trans, x.dtype)
+    x3 = x.reshape(B * H, T, K)
+    if not x3.is_contiguous():
+        x3 = x3.contiguous()
+    return torch.bmm(x3, Mb).view(B, H, T, Mb.shape[-1])
 
-        x3, Mb = ctx.saved_tensors
-        B, H, T, K, N, Hw, trans, wdtype = ctx.meta
-        dy3 = dy.to(x3.dtype).reshape(B * H, T, N).contiguous()
-        dx = dW = None
-        if ctx.needs_input_grad[0]:
-            dx = torch.bmm(dy3, Mb.transpose(1, 2).contiguous()).view(B, H, T, K)
-        if ctx.needs_input_grad[1]:
-            dM = contract_tokens(x3, dy3).view(B, H, K, N).sum(0)  # fp32 [H, K, N]
-            if Hw == 1:
-                dM = dM.sum(0, keepdim=True)
-            dW = (dM.transpose(-1, -2) if trans else dM).to(wdtype)
-        return dx, dW, None
+
+@_head_matmul_op.register_fake
+def _(x, W, trans):
+    N = W.shape[-2] if trans else W.shape[-1]
+    return x.new_empty(*x.shape[:3], N)
+
+
+@torch.library.custom_op("thetascan_hip::head_matmul_backward", mutates_args=())
+def _head_matmul_bwd_op(dy: torch.Tensor, x: torch.Tensor, W: torch.Tensor, trans: bool, need: list[bool]
+                        ) -> list[torch.Tensor]:
+    from .gn import contract_tokens
+
+    B, H, T, K = x.shape
+    Mb = _head_operand(W, B, H, K, trans, x.dtype)
+    N = Mb.shape[-1]
+    x3 = x.reshape(B * H, T, K)
+    if not x3.is_contiguous():
+        x3 = x3.contiguous()
+    dy3 = dy.to(x.dtype).reshape(B * H, T, N).contiguous()
+    dx, dW = dy.new_empty(0), dy.new_empty(0)
+    if need[0]:
+        dx = torch.bmm(dy3, Mb.transpose(1, 2).contiguous()).view(B, H, T, K)
+    if need[1]:
+        dM = contract_tokens(x3, dy3).view(B, H, K, N).sum(0)  # fp32 [H, K, N]
+        if W.shape[0] == 1:
+            dM = dM.sum(0, keepdim=True)
+        dW = (dM.transpose(-1, -2) if trans else dM).to(W.dtype).contiguous()
+    return [dx, dW]
+
+
+@_head_matmul_bwd_op.register_fake
+def _(dy, x, W, trans, need):
+    return [x.new_empty(x.shape) if need[0] else dy.new_empty(0), W.new_empty(W.shape) if need[1] else dy.new_empty(0)]
+
+
+def _head_matmul_setup(ctx, inputs, output):
+    x, W, trans = inputs
+    ctx.trans = trans
+    ctx.need = [x.requires_grad, W.requires_grad]
+    ctx.save_for_backward(x, W)
+
+
+def _head_matmul_backward(ctx, dy):
+    x, W = ctx.saved_tensors
+    dx, dW = _head_matmul_bwd_op(dy, x, W, ctx.trans, ctx.need)
+    return (dx if ctx.need[0] else None, dW if ctx.need[1] else None, None)
+
+
+_head_matmul_op.register_autograd(_head_matmul_backward, setup_context=_head_matmul_setup)
 
 
 def head_matmul(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tensor:
-    """x [B,H,T,K] times W^T (``trans``, W [H|1, N, K]) or W (W [H|1, K, N]) per head."""
-    return _HeadMatmul.apply(x, W, trans)
+    """x [B,H,T,K] times W^T (``trans``, W [H|1, N, K]) or W (W [H|1, K, N]) per
+    head: the fast-network GEMVs of the composed path (engine.py:117-158,
+    180-195) as one batched GEMM per call, without the permute copies of an
+    einsum.  Both GEMMs take contiguous right operands; the weight gradient is
+    a token contraction per (batch, head) (ts_contract_tokens) summed over the
+    batch."""
+    return _head_matmul_op(x, W, bool(trans))

@@ -48,42 +48,68 @@ def _spline_desc(pre4, n_basis, degree, bound, scale):
                             float(scale))
 
 
-class _BSpline(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, pre, scale_h, n_basis, degree, bound, scale):
-        lib = _lib.load()
-        shape = pre.shape
-        pre4 = _rows(_as4d(pre))
-        desc = _spline_desc(pre4, n_basis, degree, bound, scale)
-        out = torch.empty(*pre4.shape[:3], pre4.shape[3] * n_basis, dtype=pre.dtype, device=pre.device)
-        sh = None if scale_h is None else scale_h.detach().to(torch.float32).contiguous()
-        with _lib.timed("ts_bspline_fwd", lambda: _lib.nbytes(pre4, out)):
-            status = lib.ts_bspline_fwd(ctypes.byref(desc), _lib.strided(pre4), _lib.ptr(sh), _lib.strided(out),
-                                        _lib.stream_handle(pre.device))
-        _lib.check(status, "ts_bspline_fwd")
-        ctx.save_for_backward(pre4, sh)
-        ctx.meta = (shape, n_basis, degree, bound, scale, scale_h is not None)
-        return out.reshape(*shape[:-1], shape[-1] * n_basis)
+@torch.library.custom_op("thetascan_hip::bspline", mutates_args=())
+def _bspline_op(pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, degree: int, bound: float,
+                scale: float) -> torch.Tensor:
+    lib = _lib.load()
+    shape = pre.shape
+    pre4 = _rows(_as4d(pre))
+    desc = _spline_desc(pre4, n_basis, degree, bound, scale)
+    out = torch.empty(*pre4.shape[:3], pre4.shape[3] * n_basis, dtype=pre.dtype, device=pre.device)
+    sh = None if scale_h is None else scale_h.detach().to(torch.float32).contiguous()
+    with _lib.timed("ts_bspline_fwd", lambda: _lib.nbytes(pre4, out)):
+        status = lib.ts_bspline_fwd(ctypes.byref(desc), _lib.strided(pre4), _lib.ptr(sh), _lib.strided(out),
+                                    _lib.stream_handle(pre.device))
+    _lib.check(status, "ts_bspline_fwd")
+    return out.reshape(*shape[:-1], shape[-1] * n_basis)
 
-    @staticmethod
-    def backward(ctx, dout):
-        pre4, sh = ctx.saved_tensors
-        shape, n_basis, degree, bound, scale, has_scale = ctx.meta
-        lib = _lib.load()
-        desc = _spline_desc(pre4, n_basis, degree, bound, scale)
-        d4 = _rows(dout.to(pre4.dtype).reshape(*pre4.shape[:3], pre4.shape[3] * n_basis))
-        dpre = torch.empty_like(pre4)
-        parts = None
-        if has_scale:
-            n = ctypes.c_int32()
-            _lib.check(lib.ts_bspline_parts(ctypes.byref(desc), ctypes.byref(n)), "ts_bspline_parts")
-            parts = torch.empty(pre4.shape[1], n.value, dtype=torch.float32, device=pre4.device)
-        with _lib.timed("ts_bspline_bwd", lambda: _lib.nbytes(pre4, d4, dpre)):
-            status = lib.ts_bspline_bwd(ctypes.byref(desc), _lib.strided(pre4), _lib.ptr(sh), _lib.strided(d4),
-                                        _lib.strided(dpre), _lib.ptr(parts), _lib.stream_handle(pre4.device))
-        _lib.check(status, "ts_bspline_bwd")
-        dscale = parts.sum(-1) if has_scale and ctx.needs_input_grad[1] else None
-        return dpre.reshape(shape), dscale, None, None, None, None
+
+@_bspline_op.register_fake
+def _(pre, scale_h, n_basis, degree, bound, scale):
+    return pre.new_empty(*pre.shape[:-1], pre.shape[-1] * n_basis)
+
+
+@torch.library.custom_op("thetascan_hip::bspline_backward", mutates_args=())
+def _bspline_bwd_op(dout: torch.Tensor, pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, degree: int,
+                    bound: float, scale: float) -> list[torch.Tensor]:
+    lib = _lib.load()
+    shape = pre.shape
+    pre4 = _rows(_as4d(pre))
+    desc = _spline_desc(pre4, n_basis, degree, bound, scale)
+    sh = None if scale_h is None else scale_h.detach().to(torch.float32).contiguous()
+    d4 = _rows(dout.to(pre4.dtype).reshape(*pre4.shape[:3], pre4.shape[3] * n_basis))
+    dpre = torch.empty_like(pre4)
+    parts = None
+    if sh is not None:
+        n = ctypes.c_int32()
+        _lib.check(lib.ts_bspline_parts(ctypes.byref(desc), ctypes.byref(n)), "ts_bspline_parts")
+        parts = torch.empty(pre4.shape[1], n.value, dtype=torch.float32, device=pre4.device)
+    with _lib.timed("ts_bspline_bwd", lambda: _lib.nbytes(pre4, d4, dpre)):
+        status = lib.ts_bspline_bwd(ctypes.byref(desc), _lib.strided(pre4), _lib.ptr(sh), _lib.strided(d4),
+                                    _lib.strided(dpre), _lib.ptr(parts), _lib.stream_handle(pre4.device))
+    _lib.check(status, "ts_bspline_bwd")
+    dscale = dout.new_empty(0) if parts is None else parts.sum(-1).to(scale_h.dtype)
+    return [dpre.reshape(shape), dscale]
+
+
+@_bspline_bwd_op.register_fake
+def _(dout, pre, scale_h, n_basis, degree, bound, scale):
+    return [pre.new_empty(pre.shape), dout.new_empty(0) if scale_h is None else scale_h.new_empty(scale_h.shape)]
+
+
+def _bspline_setup(ctx, inputs, output):
+    pre, scale_h, n_basis, degree, bound, scale = inputs
+    ctx.args = (n_basis, degree, bound, scale)
+    ctx.save_for_backward(pre, scale_h)
+
+
+def _bspline_backward(ctx, dout):
+    pre, scale_h = ctx.saved_tensors
+    dpre, dscale = _bspline_bwd_op(dout, pre, scale_h, *ctx.args)
+    return dpre, (dscale if scale_h is not None else None), None, None, None, None
+
+
+_bspline_op.register_autograd(_bspline_backward, setup_context=_bspline_setup)
 
 
 def bspline_features(pre: torch.Tensor, *, n_basis: int, degree: int, bound: float, scale) -> torch.Tensor:
@@ -108,8 +134,8 @@ def bspline_features(pre: torch.Tensor, *, n_basis: int, degree: int, bound: flo
                 f"got {tuple(scale.shape)} for reference {tuple(pre.shape)}"
             )
         _on_gpu(scale)
-        return _BSpline.apply(pre, scale, n_basis, degree, bound, 1.0)
-    return _BSpline.apply(pre, None, n_basis, degree, bound, float(scale))
+        return _bspline_op(pre, scale, int(n_basis), int(degree), float(bound), 1.0)
+    return _bspline_op(pre, None, int(n_basis), int(degree), float(bound), float(scale))
 
 
 # ---------------------------------------------------------------- bank blend
@@ -120,41 +146,70 @@ def _blend_desc(first, n_in):
     return _lib.BlendDesc(B, H, T, d, n_in, _lib.dtype_code(first.dtype))
 
 
-class _Blend(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, coef, *inputs):
-        lib = _lib.load()
-        ins = [_rows(t) for t in inputs]
-        desc = _blend_desc(ins[0], len(ins))
-        cf = coef.detach().to(torch.float32).contiguous()
-        y = torch.empty(ins[0].shape, dtype=ins[0].dtype, device=ins[0].device)
-        arr = (_lib.Strided * len(ins))(*[_lib.strided(t) for t in ins])
-        with _lib.timed("ts_blend_fwd", lambda: _lib.nbytes(*ins, y)):
-            status = lib.ts_blend_fwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(y),
-                                      _lib.stream_handle(y.device))
-        _lib.check(status, "ts_blend_fwd")
-        ctx.save_for_backward(cf, *ins)
-        return y
+@torch.library.custom_op("thetascan_hip::blend", mutates_args=())
+def _blend_op(coef: torch.Tensor, inputs: list[torch.Tensor]) -> torch.Tensor:
+    lib = _lib.load()
+    ins = [_rows(t) for t in inputs]
+    desc = _blend_desc(ins[0], len(ins))
+    cf = coef.detach().to(torch.float32).contiguous()
+    y = torch.empty(ins[0].shape, dtype=ins[0].dtype, device=ins[0].device)
+    arr = (_lib.Strided * len(ins))(*[_lib.strided(t) for t in ins])
+    with _lib.timed("ts_blend_fwd", lambda: _lib.nbytes(*ins, y)):
+        status = lib.ts_blend_fwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(y),
+                                  _lib.stream_handle(y.device))
+    _lib.check(status, "ts_blend_fwd")
+    return y
 
-    @staticmethod
-    def backward(ctx, dy):
-        cf, *ins = ctx.saved_tensors
-        lib = _lib.load()
-        n = len(ins)
-        desc = _blend_desc(ins[0], n)
-        g = _rows(dy.to(ins[0].dtype))
-        dins = [torch.empty_like(t) if ctx.needs_input_grad[1 + i] else None for i, t in enumerate(ins)]
-        count = ctypes.c_int32()
-        _lib.check(lib.ts_blend_parts(ctypes.byref(desc), ctypes.byref(count)), "ts_blend_parts")
-        parts = torch.empty(n, ins[0].shape[1], count.value, dtype=torch.float32, device=g.device)
-        arr = (_lib.Strided * n)(*[_lib.strided(t) for t in ins])
-        darr = (_lib.Strided * n)(*[_lib.strided(t) for t in dins])
-        with _lib.timed("ts_blend_bwd", lambda: _lib.nbytes(*ins, g, *dins)):
-            status = lib.ts_blend_bwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(g), darr, _lib.ptr(parts),
-                                      _lib.stream_handle(g.device))
-        _lib.check(status, "ts_blend_bwd")
-        dcoef = parts.sum(-1) if ctx.needs_input_grad[0] else None
-        return (dcoef, *dins)
+
+@_blend_op.register_fake
+def _(coef, inputs):
+    return inputs[0].new_empty(inputs[0].shape)
+
+
+@torch.library.custom_op("thetascan_hip::blend_backward", mutates_args=())
+def _blend_bwd_op(dy: torch.Tensor, coef: torch.Tensor, inputs: list[torch.Tensor], need: list[bool]
+                  ) -> list[torch.Tensor]:
+    lib = _lib.load()
+    ins = [_rows(t) for t in inputs]
+    n = len(ins)
+    desc = _blend_desc(ins[0], n)
+    cf = coef.detach().to(torch.float32).contiguous()
+    g = _rows(dy.to(ins[0].dtype))
+    dins = [torch.empty_like(t) if need[1 + i] else None for i, t in enumerate(ins)]
+    count = ctypes.c_int32()
+    _lib.check(lib.ts_blend_parts(ctypes.byref(desc), ctypes.byref(count)), "ts_blend_parts")
+    parts = torch.empty(n, ins[0].shape[1], count.value, dtype=torch.float32, device=g.device)
+    arr = (_lib.Strided * n)(*[_lib.strided(t) for t in ins])
+    darr = (_lib.Strided * n)(*[_lib.strided(t) for t in dins])
+    with _lib.timed("ts_blend_bwd", lambda: _lib.nbytes(*ins, g, *dins)):
+        status = lib.ts_blend_bwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(g), darr, _lib.ptr(parts),
+                                  _lib.stream_handle(g.device))
+    _lib.check(status, "ts_blend_bwd")
+    dcoef = parts.sum(-1).to(coef.dtype) if need[0] else dy.new_empty(0)
+    return [dcoef] + [dy.new_empty(0) if t is None else t for t in dins]
+
+
+@_blend_bwd_op.register_fake
+def _(dy, coef, inputs, need):
+    empty = dy.new_empty(0)
+    return [coef.new_empty(coef.shape) if need[0] else empty] + \
+        [t.new_empty(t.shape) if w else empty for t, w in zip(inputs, need[1:])]
+
+
+def _blend_setup(ctx, inputs, output):
+    coef, ins = inputs
+    ctx.need = [coef.requires_grad] + [t.requires_grad for t in ins]
+    ctx.save_for_backward(coef, *ins)
+
+
+def _blend_backward(ctx, dy):
+    coef, *ins = ctx.saved_tensors
+    res = _blend_bwd_op(dy, coef, list(ins), ctx.need)
+    grads = [g if w else None for g, w in zip(res, ctx.need)]
+    return grads[0], grads[1:]
+
+
+_blend_op.register_autograd(_blend_backward, setup_context=_blend_setup)
 
 
 def bank_blend(inputs, coef: torch.Tensor) -> torch.Tensor:
@@ -170,7 +225,7 @@ def bank_blend(inputs, coef: torch.Tensor) -> torch.Tensor:
             raise ValueError("bank blend views must share shape and dtype")
     if coef.shape != (len(inputs), first.shape[1]):
         raise ValueError(f"bank blend coefficients must be [{len(inputs)}, {first.shape[1]}]")
-    return _Blend.apply(coef, *inputs)
+    return _blend_op(coef, list(inputs))
 
 
 def fast_coefficients(etas) -> torch.Tensor:

@@ -17,55 +17,87 @@ from .fused import rope_tables
 
 
 def _eligible(x: torch.Tensor) -> bool:
+    """Shape and dtype the kernel covers (layout is fixed up inside the op)."""
     if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32) or x.ndim != 4:
         return False
     vec = 16 // x.element_size()
     d = x.shape[-1]
-    return (x.stride(-1) == 1 and d % vec == 0 and d // vec <= 64 and x.data_ptr() % 16 == 0
-            and all(s % vec == 0 for s in x.stride()[:3]))
+    return d % vec == 0 and d // vec <= 64
 
 
-class _QkNorm(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, rot: int, base: float, eps: float):
-        B, H, T, d = x.shape
-        lib = _lib.load()
-        desc = _lib.QkNormDesc(B, H, T, d, _lib.dtype_code(x.dtype), int(rot), float(eps))
-        cs = sn = None
-        if rot:
-            cs, sn = rope_tables(T, rot, base, x.device)
-        y = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device)
-        with _lib.timed("ts_qknorm_fwd", lambda: _lib.nbytes(x, y)):
-            status = lib.ts_qknorm_fwd(ctypes.byref(desc), _lib.strided(x), _lib.strided(y), _lib.ptr(cs),
-                                       _lib.ptr(sn), _lib.stream_handle(x.device))
-        _lib.check(status, "ts_qknorm_fwd")
-        ctx.save_for_backward(x)
-        ctx.rot, ctx.base, ctx.eps = rot, base, eps
-        return y
+def _readable(x: torch.Tensor) -> torch.Tensor:
+    """x itself when its rows are 16-byte aligned with a contiguous feature
+    axis, else an aligned copy."""
+    vec = 16 // x.element_size()
+    if x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % vec == 0 for s in x.stride()[:3]):
+        return x
+    return x.clone(memory_format=torch.contiguous_format)
 
-    @staticmethod
-    def backward(ctx, dy):
-        (x,) = ctx.saved_tensors
-        B, H, T, d = x.shape
-        lib = _lib.load()
-        dy = dy.to(x.dtype)
-        if not _eligible(dy):
-            dy = dy.contiguous()
-        desc = _lib.QkNormDesc(B, H, T, d, _lib.dtype_code(x.dtype), int(ctx.rot), float(ctx.eps))
-        cs = sn = None
-        if ctx.rot:
-            cs, sn = rope_tables(T, ctx.rot, ctx.base, x.device)
-        dx = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device)
-        with _lib.timed("ts_qknorm_bwd", lambda: _lib.nbytes(x, dy, dx)):
-            status = lib.ts_qknorm_bwd(ctypes.byref(desc), _lib.strided(x), _lib.strided(dy), _lib.strided(dx),
-                                       _lib.ptr(cs), _lib.ptr(sn), _lib.stream_handle(x.device))
-        _lib.check(status, "ts_qknorm_bwd")
-        return dx, None, None, None
+
+def _tables(T: int, rot: int, base: float, device):
+    if not rot:
+        return None, None
+    return rope_tables(T, rot, base, device)
+
+
+@torch.library.custom_op("thetascan_hip::qknorm", mutates_args=())
+def _qknorm_op(x: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor:
+    B, H, T, d = x.shape
+    x = _readable(x)
+    lib = _lib.load()
+    desc = _lib.QkNormDesc(B, H, T, d, _lib.dtype_code(x.dtype), int(rot), float(eps))
+    cs, sn = _tables(T, rot, base, x.device)
+    y = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device)
+    with _lib.timed("ts_qknorm_fwd", lambda: _lib.nbytes(x, y)):
+        status = lib.ts_qknorm_fwd(ctypes.byref(desc), _lib.strided(x), _lib.strided(y), _lib.ptr(cs),
+                                   _lib.ptr(sn), _lib.stream_handle(x.device))
+    _lib.check(status, "ts_qknorm_fwd")
+    return y
+
+
+@_qknorm_op.register_fake
+def _(x, rot, base, eps):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("thetascan_hip::qknorm_backward", mutates_args=())
+def _qknorm_bwd_op(x: torch.Tensor, dy: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor:
+    B, H, T, d = x.shape
+    x = _readable(x)
+    lib = _lib.load()
+    dy = _readable(dy.to(x.dtype))
+    desc = _lib.QkNormDesc(B, H, T, d, _lib.dtype_code(x.dtype), int(rot), float(eps))
+    cs, sn = _tables(T, rot, base, x.device)
+    dx = torch.empty(B, H, T, d, dtype=x.dtype, device=x.device)
+    with _lib.timed("ts_qknorm_bwd", lambda: _lib.nbytes(x, dy, dx)):
+        status = lib.ts_qknorm_bwd(ctypes.byref(desc), _lib.strided(x), _lib.strided(dy), _lib.strided(dx),
+                                   _lib.ptr(cs), _lib.ptr(sn), _lib.stream_handle(x.device))
+    _lib.check(status, "ts_qknorm_bwd")
+    return dx
+
+
+@_qknorm_bwd_op.register_fake
+def _(x, dy, rot, base, eps):
+    return x.new_empty(x.shape)
+
+
+def _qknorm_setup(ctx, inputs, output):
+    x, rot, base, eps = inputs
+    ctx.args = (rot, base, eps)
+    ctx.save_for_backward(x)
+
+
+def _qknorm_backward(ctx, dy):
+    (x,) = ctx.saved_tensors
+    return _qknorm_bwd_op(x, dy, *ctx.args), None, None, None
+
+
+_qknorm_op.register_autograd(_qknorm_backward, setup_context=_qknorm_setup)
 
 
 def qk_norm(x: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor | None:
     """rope(x) / max(|rope(x)|, eps) over the last axis of a [B,H,T,d] view,
-    or None when the view cannot be read by the kernel (unaligned rows)."""
+    or None for a width or dtype the kernel does not cover."""
     if not _eligible(x):
         return None
-    return _QkNorm.apply(x, rot, base, eps)
+    return _qknorm_op(x, int(rot), float(base), float(eps))

@@ -397,19 +397,27 @@ def workspace_for(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, seg_chun
     """A workspace that keeps the segment states of ``scan_launch(q, k, v, ...)``
     for a later call with ``states_in`` (None when the scan has one segment).
     ``v_ext`` / ``kx`` describe the scan's value-side / key-side ext columns."""
-    lib = _lib.load()
-    vec = _vec(q.dtype)
     B, H, T, dk = q.shape
-    dv = v.shape[-1]
+    nbytes = workspace_bytes(B, H, T, dk, v.shape[-1], q.dtype, seg_chunks=seg_chunks, retention=retention,
+                             reverse=reverse, v_ext=v_ext, kx=kx)
+    if not nbytes:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+
+
+def workspace_bytes(B: int, H: int, T: int, dk: int, dv: int, dtype: torch.dtype, *, seg_chunks: int = 0,
+                    retention: int = _lib.RET_NONE, reverse: bool = False, v_ext: bool = False,
+                    kx: bool = False) -> int:
+    """Bytes of the segment-state workspace of such a scan (a host query)."""
+    lib = _lib.load()
+    vec = _vec(dtype)
     ext = _lib.EXT_ONES
-    desc = _lib.ScanDesc(B, H, T, -(-dk // vec) * vec, -(-dv // vec) * vec, _lib.dtype_code(q.dtype), retention,
+    desc = _lib.ScanDesc(B, H, T, -(-dk // vec) * vec, -(-dv // vec) * vec, _lib.dtype_code(dtype), retention,
                          int(reverse), ext if kx else 0, ext if kx else 0, ext if v_ext else 0, _lib.OUT_STORE, 1.0,
                          int(seg_chunks), 0, 0, 0)
     c_ws = ctypes.c_size_t()
     _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan workspace")
-    if not c_ws.value:
-        return None
-    return torch.empty(c_ws.value, dtype=torch.uint8, device=q.device)
+    return c_ws.value
 
 
 # ------------------------------------------------------------------ retentions
@@ -456,113 +464,168 @@ def _retention_grad(kind: int, retention: torch.Tensor, dL: torch.Tensor) -> tor
 
 # ------------------------------------------------------------------ autograd
 
-class _ScanViews(torch.autograd.Function):
-    """Forward: one kernel scan per retention.  Backward: three scans per view."""
+def _views_forward(q, k, v, with_mass: bool, retentions):
+    """Forward scans of every retention -> (outs, masses)."""
+    kinds = [_classify(r, q) for r in retentions]
+    if views_eligible(q, v, kinds):
+        # one pass for every retention: the score tile is formed once
+        outs, masses = scan_views_launch(q, k, v, [r if kd == _lib.RET_STATIC else None
+                                                   for kd, r in zip(kinds, retentions)], mass=with_mass)
+        return list(outs), list(masses or [])
+    outs, masses = [], []
+    for kind, r in zip(kinds, retentions):
+        out, mass, _ = scan_launch(q, k, v, **_ret_kwargs(kind, r), v_ext="ones" if with_mass else None,
+                                   want_ext_out=with_mass)
+        outs.append(out)
+        if with_mass:
+            masses.append(mass)
+    return outs, masses
 
-    @staticmethod
-    def forward(ctx, q, k, v, with_mass, *retentions):
-        kinds = [_classify(r, q) for r in retentions]
-        if views_eligible(q, v, kinds):
-            # one pass for every retention: the score tile is formed once
-            outs, masses = scan_views_launch(q, k, v, [r if kd == _lib.RET_STATIC else None
-                                                       for kd, r in zip(kinds, retentions)], mass=with_mass)
-            masses = masses or []
+
+def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: bool, need_v: bool, need_r):
+    """Backward of :func:`_views_forward`: three scans per view (None entries
+    of ``d_outs`` / ``d_mass`` are zero gradients) -> (gq, gk, gv, r_grads)."""
+    n = len(retentions)
+    kinds = [_classify(r, q) for r in retentions]
+    B, H, T, dk = q.shape
+    dv = v.shape[-1]
+    if n == 1 and not (retentions[0] is not None and need_r[0]) and (d_outs[0] is not None or d_mass[0] is not None):
+        # one view and no retention gradient: each gradient is one scan,
+        # stored in the input dtype (the same single rounding as an fp32
+        # accumulation cast at the end)
+        kind, r = kinds[0], retentions[0]
+        dO, dm = d_outs[0], d_mass[0]
+        if dO is None:
+            dO = torch.zeros(B, H, T, dv, dtype=q.dtype, device=q.device)
+        dO = dO.to(q.dtype)
+        rk = _ret_kwargs(kind, r)
+        q_ext = None if dm is None else dm.to(torch.float32)
+        gq = gk = gv = None
+        if need_q:
+            gq = scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if dm is not None else None)[0][..., :dk]
+        if need_k:
+            gk = scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if dm is not None else None,
+                             k_ext=q_ext)[0][..., :dk]
+        if need_v:
+            gv = scan_launch(k, q, dO, **rk, reverse=True)[0][..., :dv]
+        return gq, gk, gv, [None]
+    dq = torch.zeros(B, H, T, -(-dk // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+    dkk = torch.zeros_like(dq)
+    dvv = torch.zeros(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+    r_grads = []
+    for j in range(n):
+        kind, r = kinds[j], retentions[j]
+        dO = d_outs[j]
+        dm = d_mass[j]
+        if dO is None and dm is None:
+            r_grads.append(None)
+            continue
+        if dO is None:
+            dO = torch.zeros(B, H, T, dv, dtype=q.dtype, device=q.device)
+        dO = dO.to(q.dtype)
+        rk = _ret_kwargs(kind, r)
+        mass_ext = dm is not None
+        q_ext = dm.to(torch.float32) if mass_ext else None
+        want_r = r is not None and need_r[j]
+        if want_r:
+            # dL_t = q_t.dq_t - k_t.dk_t sums to zero over t, and the
+            # retention gradient (sum_t t dL_t, or a suffix sum of dL) is a
+            # small difference of large terms: bf16 rounding of the score
+            # tiles inside the scans would be amplified by about T / (the
+            # retention's window).  These two scans therefore run on fp32
+            # operands (the bf16 values are exact in fp32).
+            qs, ks, vs, dOs = q, k, v, dO
+            if q.dtype != torch.float32:
+                qs, ks, vs, dOs = q.float(), k.float(), v.float(), dO.float()
+            dq_j, _, _ = scan_launch(dOs, vs, ks, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
+                                     out_mode=_lib.OUT_STORE_F32)
+            dk_j, _, _ = scan_launch(vs, dOs, qs, **rk, reverse=True, q_ext="ones" if mass_ext else None,
+                                     k_ext=q_ext, out_mode=_lib.OUT_STORE_F32)
+            dL = (qs * dq_j[..., :dk]).sum(-1) - (ks * dk_j[..., :dk]).sum(-1)
+            r_grads.append(_retention_grad(kind, r, dL))
+            dq[..., : dq_j.shape[-1]] += dq_j
+            dkk[..., : dk_j.shape[-1]] += dk_j
         else:
-            outs, masses = [], []
-            for kind, r in zip(kinds, retentions):
-                out, mass, _ = scan_launch(
-                    q, k, v, **_ret_kwargs(kind, r),
-                    v_ext="ones" if with_mass else None, want_ext_out=with_mass,
-                )
-                outs.append(out)
-                if with_mass:
-                    masses.append(mass)
-        ctx.kinds = kinds
-        ctx.with_mass = with_mass
-        ctx.n_views = len(retentions)
-        ctx.save_for_backward(q, k, v, *[r if r is not None else None for r in retentions])
-        return (*outs, *masses)
-
-    @staticmethod
-    def backward(ctx, *grads):
-        q, k, v, *retentions = ctx.saved_tensors
-        n = ctx.n_views
-        d_outs = grads[:n]
-        d_mass = grads[n:] if ctx.with_mass else [None] * n
-        need_q, need_k, need_v = ctx.needs_input_grad[0:3]
-        need_r = ctx.needs_input_grad[4:]
-        B, H, T, dk = q.shape
-        dv = v.shape[-1]
-        if n == 1 and not (retentions[0] is not None and need_r[0]) and (d_outs[0] is not None or d_mass[0] is not None):
-            # one view and no retention gradient: each gradient is one scan,
-            # stored in the input dtype (the same single rounding as an fp32
-            # accumulation cast at the end)
-            kind, r = ctx.kinds[0], retentions[0]
-            dO, dm = d_outs[0], d_mass[0]
-            if dO is None:
-                dO = torch.zeros(B, H, T, dv, dtype=q.dtype, device=q.device)
-            dO = dO.to(q.dtype)
-            rk = _ret_kwargs(kind, r)
-            q_ext = None if dm is None else dm.to(torch.float32)
-            gq = gk = gv = None
+            r_grads.append(None)
             if need_q:
-                gq = scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if dm is not None else None)[0][..., :dk]
+                scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
+                            out=dq, out_mode=_lib.OUT_ACCUM_F32)
             if need_k:
-                gk = scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if dm is not None else None,
-                                 k_ext=q_ext)[0][..., :dk]
-            if need_v:
-                gv = scan_launch(k, q, dO, **rk, reverse=True)[0][..., :dv]
-            return (gq, gk, gv, None, None)
-        dq = torch.zeros(B, H, T, -(-dk // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
-        dkk = torch.zeros_like(dq)
-        dvv = torch.zeros(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
-        r_grads = []
-        for j in range(n):
-            kind, r = ctx.kinds[j], retentions[j]
-            dO = d_outs[j]
-            dm = d_mass[j]
-            if dO is None and dm is None:
-                r_grads.append(None)
-                continue
-            if dO is None:
-                dO = torch.zeros(B, H, T, dv, dtype=q.dtype, device=q.device)
-            dO = dO.to(q.dtype)
-            rk = _ret_kwargs(kind, r)
-            mass_ext = dm is not None
-            q_ext = dm.to(torch.float32) if mass_ext else None
-            want_r = r is not None and need_r[j]
-            if want_r:
-                # dL_t = q_t.dq_t - k_t.dk_t sums to zero over t, and the
-                # retention gradient (sum_t t dL_t, or a suffix sum of dL) is a
-                # small difference of large terms: bf16 rounding of the score
-                # tiles inside the scans would be amplified by about T / (the
-                # retention's window).  These two scans therefore run on fp32
-                # operands (the bf16 values are exact in fp32).
-                qs, ks, vs, dOs = q, k, v, dO
-                if q.dtype != torch.float32:
-                    qs, ks, vs, dOs = q.float(), k.float(), v.float(), dO.float()
-                dq_j, _, _ = scan_launch(dOs, vs, ks, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
-                                         out_mode=_lib.OUT_STORE_F32)
-                dk_j, _, _ = scan_launch(vs, dOs, qs, **rk, reverse=True, q_ext="ones" if mass_ext else None,
-                                         k_ext=q_ext, out_mode=_lib.OUT_STORE_F32)
-                dL = (qs * dq_j[..., :dk]).sum(-1) - (ks * dk_j[..., :dk]).sum(-1)
-                r_grads.append(_retention_grad(kind, r, dL))
-                dq[..., : dq_j.shape[-1]] += dq_j
-                dkk[..., : dk_j.shape[-1]] += dk_j
-            else:
-                r_grads.append(None)
-                if need_q:
-                    scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
-                                out=dq, out_mode=_lib.OUT_ACCUM_F32)
-                if need_k:
-                    scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
-                                k_ext=q_ext, out=dkk, out_mode=_lib.OUT_ACCUM_F32)
-            if need_v and dO is not None:
-                scan_launch(k, q, dO, **rk, reverse=True, out=dvv, out_mode=_lib.OUT_ACCUM_F32)
-        gq = dq[..., :dk].to(q.dtype) if need_q else None
-        gk = dkk[..., :dk].to(k.dtype) if need_k else None
-        gv = dvv[..., :dv].to(v.dtype) if need_v else None
-        return (gq, gk, gv, None, *r_grads)
+                scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
+                            k_ext=q_ext, out=dkk, out_mode=_lib.OUT_ACCUM_F32)
+        if need_v:
+            scan_launch(k, q, dO, **rk, reverse=True, out=dvv, out_mode=_lib.OUT_ACCUM_F32)
+    gq = dq[..., :dk].to(q.dtype) if need_q else None
+    gk = dkk[..., :dk].to(k.dtype) if need_k else None
+    gv = dvv[..., :dv].to(v.dtype) if need_v else None
+    return gq, gk, gv, r_grads
+
+
+# The scan as torch.library custom ops: opaque to TorchDynamo (the ctypes
+# launches never enter a traced graph), with a fake implementation for shape
+# propagation and an autograd formula that calls the backward op.  Absent
+# retentions and absent gradients travel as empty placeholders.
+
+def _placeholder(like: torch.Tensor) -> torch.Tensor:
+    return like.new_empty(0)
+
+
+def _or_none(t: torch.Tensor):
+    return None if t.numel() == 0 and t.ndim == 1 else t
+
+
+@torch.library.custom_op("thetascan_hip::scan_views", mutates_args=())
+def _scan_views_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: list[torch.Tensor], with_mass: bool
+                   ) -> list[torch.Tensor]:
+    outs, masses = _views_forward(q, k, v, with_mass, [_or_none(r) for r in rets])
+    return outs + masses
+
+
+@_scan_views_op.register_fake
+def _(q, k, v, rets, with_mass):
+    B, H, T = q.shape[:3]
+    outs = [q.new_empty(B, H, T, v.shape[-1]) for _ in rets]
+    masses = [q.new_empty(B, H, T, dtype=torch.float32) for _ in rets] if with_mass else []
+    return outs + masses
+
+
+@torch.library.custom_op("thetascan_hip::scan_views_backward", mutates_args=())
+def _scan_views_bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: list[torch.Tensor],
+                       d_outs: list[torch.Tensor], d_mass: list[torch.Tensor], need: list[bool]
+                       ) -> list[torch.Tensor]:
+    retentions = [_or_none(r) for r in rets]
+    gq, gk, gv, r_grads = _views_backward(q, k, v, retentions, [_or_none(g) for g in d_outs],
+                                          [_or_none(g) for g in d_mass], need[0], need[1], need[2], need[3:])
+    grads = [gq, gk, gv] + list(r_grads) + [None] * (len(rets) - len(r_grads))
+    like = [q, k, v] + list(rets)
+    return [_placeholder(x) if g is None else g for g, x in zip(grads, like)]
+
+
+@_scan_views_bwd_op.register_fake
+def _(q, k, v, rets, d_outs, d_mass, need):
+    like = [q, k, v] + list(rets)
+    return [torch.empty_like(x) if (w and _or_none(x) is not None) else _placeholder(x) for x, w in zip(like, need)]
+
+
+def _scan_views_setup(ctx, inputs, output):
+    q, k, v, rets, with_mass = inputs
+    ctx.with_mass = with_mass
+    ctx.need = [q.requires_grad, k.requires_grad, v.requires_grad] + [r.requires_grad for r in rets]
+    ctx.save_for_backward(q, k, v, *rets)
+
+
+def _scan_views_backward(ctx, grads):
+    q, k, v, *rets = ctx.saved_tensors
+    n = len(rets)
+    d_outs = [_placeholder(q) if g is None else g for g in grads[:n]]
+    d_mass = [_placeholder(q) if g is None else g for g in grads[n:]] if ctx.with_mass else \
+        [_placeholder(q)] * n
+    res = _scan_views_bwd_op(q, k, v, list(rets), d_outs, d_mass, ctx.need)
+    out = [None if not w else _or_none(g) for g, w in zip(res, ctx.need)]
+    return out[0], out[1], out[2], out[3:], None
+
+
+_scan_views_op.register_autograd(_scan_views_backward, setup_context=_scan_views_setup)
 
 
 def _run_views(q, k, v, retentions, chunk, with_mass, out_f32=False):
@@ -579,7 +642,8 @@ def _run_views(q, k, v, retentions, chunk, with_mass, out_f32=False):
         # cancellation.  The bf16 values are exact in fp32; autograd casts the
         # gradients back.
         q, k, v = q.float(), k.float(), v.float()
-    return _ScanViews.apply(q, k, v, with_mass, *retentions)
+    rets = [_placeholder(q) if r is None else r for r in retentions]
+    return _scan_views_op(q, k, v, rets, bool(with_mass))
 
 
 def linattn_views(

@@ -23,6 +23,7 @@ import math
 import torch
 
 from ... import _lib
+from .dispatch import HipOp
 from . import scan_hip
 from .linear import slot_sum, split_k_outer, weight_grad
 
@@ -544,20 +545,19 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
     return dproj, dw1, dw2, dtau, db_g
 
 
-# The depth-1 kernel-memory mixer as torch.library custom ops: one forward op
-# (the stacked qkv / gate projection GEMM, the kernel memory, the output
-# projection: block.py:593-599, 721-724 around engine.py's read) and one
-# backward op (split-K weight-gradient GEMMs around the memory backward).
-# TorchDynamo records each as one opaque call; the tensors the backward needs
-# are outputs of the forward op, placeholders (empty tensors) where absent.
+# The depth-1 kernel-memory mixer as one autograd node (dispatch.HipOp): the
+# forward is the stacked qkv / gate projection GEMM, the kernel memory and the
+# output projection (block.py:593-599, 721-724 around engine.py's read); the
+# backward the split-K weight-gradient GEMMs around the memory backward.  The
+# tensors the backward needs are outputs of the forward, placeholders (empty
+# tensors) where absent.
 
 def _spec_args(spec: FeatureSpec):
     return (int(spec.kind), int(spec.m), float(spec.gain), int(spec.in_rot), int(spec.feat_rot),
             float(spec.rope_base), float(spec.resid_scale), float(spec.eps))
 
 
-@torch.library.custom_op("thetascan_hip::kernel_mixer", mutates_args=())
-def _kernel_mixer_op(x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None, b_g: torch.Tensor | None,
+def _kernel_mixer_forward(x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None, b_g: torch.Tensor | None,
                      w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None, w_out: torch.Tensor, kind: int,
                      m: int, gain: float, in_rot: int, feat_rot: int, rope_base: float, resid_scale: float,
                      eps: float, normalize: bool, seg_chunks: int, heads: int) -> list[torch.Tensor]:
@@ -570,9 +570,8 @@ def _kernel_mixer_op(x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | N
     return [out, proj, y] + [x.new_empty(0) if getattr(st, n) is None else getattr(st, n) for n in _State.SAVED]
 
 
-@_kernel_mixer_op.register_fake
-def _(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps,
-      normalize, seg_chunks, heads):
+def _kernel_mixer_fake(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in_rot, feat_rot, rope_base,
+                       resid_scale, eps, normalize, seg_chunks, heads):
     spec = FeatureSpec(kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps)
     B, T, _ = x.shape
     H = heads
@@ -597,8 +596,7 @@ def _(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in_rot, feat_rot, r
             x.new_empty(B, H, T, d), mass, x.new_empty(B, H, T, d)]
 
 
-@torch.library.custom_op("thetascan_hip::kernel_mixer_backward", mutates_args=())
-def _kernel_mixer_bwd_op(dout: torch.Tensor, x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None,
+def _kernel_mixer_backward_impl(dout: torch.Tensor, x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None,
                          b_g: torch.Tensor | None, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None,
                          w_out: torch.Tensor, proj: torch.Tensor, y: torch.Tensor, saved: list[torch.Tensor],
                          kind: int, m: int, gain: float, in_rot: int, feat_rot: int, rope_base: float,
@@ -627,9 +625,8 @@ def _kernel_mixer_bwd_op(dout: torch.Tensor, x: torch.Tensor, w_qkv: torch.Tenso
     return [x.new_empty(0) if g is None else g for g in grads]
 
 
-@_kernel_mixer_bwd_op.register_fake
-def _(dout, x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, saved, kind, m, gain, in_rot, feat_rot, rope_base,
-      resid_scale, eps, normalize, seg_chunks, heads, need):
+def _kernel_mixer_backward_fake(dout, x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, saved, kind, m, gain, in_rot,
+                                feat_rot, rope_base, resid_scale, eps, normalize, seg_chunks, heads, need):
     like = [x, w_qkv, w_g, b_g, w1, w2, tau, w_out]
     return [t.new_empty(t.shape) if (t is not None and w) else x.new_empty(0) for t, w in zip(like, need)]
 
@@ -642,14 +639,16 @@ def _kernel_mixer_setup(ctx, inputs, output):
     ctx.save_for_backward(*tensors, *output[1:])
 
 
-def _kernel_mixer_backward(ctx, grads):
+def _kernel_mixer_backward(ctx, grads, bwd):
     x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, *saved = ctx.saved_tensors
-    res = _kernel_mixer_bwd_op(grads[0], x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, list(saved), *ctx.args,
+    res = bwd(grads[0], x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, list(saved), *ctx.args,
                                ctx.need)
     return (*[g if w else None for g, w in zip(res, ctx.need)], *([None] * len(ctx.args)))
 
 
-_kernel_mixer_op.register_autograd(_kernel_mixer_backward, setup_context=_kernel_mixer_setup)
+_kernel_mixer_op = HipOp("kernel_mixer", forward=_kernel_mixer_forward, forward_fake=_kernel_mixer_fake,
+                         backward_impl=_kernel_mixer_backward_impl, backward_fake=_kernel_mixer_backward_fake,
+                         setup=_kernel_mixer_setup, backward=_kernel_mixer_backward)
 
 
 def kernel_mixer(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, spec: FeatureSpec, normalize: bool, heads: int,

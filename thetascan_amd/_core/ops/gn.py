@@ -15,6 +15,7 @@ import ctypes
 import torch
 
 from ... import _lib
+from .dispatch import HipOp
 
 GN_HEAD_DIMS = (16, 32, 64, 128)
 
@@ -81,8 +82,7 @@ def contract_tokens(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return parts.view(H, S, p, q).sum(1, dtype=torch.float32)
 
 
-@torch.library.custom_op("thetascan_hip::gn_write", mutates_args=())
-def _gn_write_op(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None,
+def _gn_write_forward(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None,
                  s: float, inv_depth: float, eps: float) -> list[torch.Tensor]:
     lib = _lib.load()
     xk, vk = _rows(x), _rows(v)
@@ -105,15 +105,13 @@ def _gn_write_op(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: torch.T
     return [h, lam, g]
 
 
-@_gn_write_op.register_fake
-def _(x, v, w1, w2, tau, s, inv_depth, eps):
+def _gn_write_fake(x, v, w1, w2, tau, s, inv_depth, eps):
     B, H, T, d = x.shape
     m = w1.shape[1]
     return [x.new_empty(B, H, T, m), x.new_empty(B, H, T, d), x.new_empty(B, H, T, m)]
 
 
-@torch.library.custom_op("thetascan_hip::gn_write_backward", mutates_args=())
-def _gn_write_bwd_op(dh: torch.Tensor | None, dlam: torch.Tensor | None, dg: torch.Tensor | None, x: torch.Tensor,
+def _gn_write_backward_impl(dh: torch.Tensor | None, dlam: torch.Tensor | None, dg: torch.Tensor | None, x: torch.Tensor,
                      v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None, s: float,
                      inv_depth: float, eps: float, need_tau: bool) -> list[torch.Tensor]:
     lib = _lib.load()
@@ -155,8 +153,7 @@ def _gn_write_bwd_op(dh: torch.Tensor | None, dlam: torch.Tensor | None, dg: tor
     return [dx, dv, dw1.to(w1.dtype), dw2.to(w2.dtype), dtau]
 
 
-@_gn_write_bwd_op.register_fake
-def _(dh, dlam, dg, x, v, w1, w2, tau, s, inv_depth, eps, need_tau):
+def _gn_write_backward_fake(dh, dlam, dg, x, v, w1, w2, tau, s, inv_depth, eps, need_tau):
     dtau = x.new_empty(0) if (tau is None or not need_tau) else tau.new_empty(tau.shape)
     return [x.new_empty(x.shape), x.new_empty(x.shape), w1.new_empty(w1.shape), w2.new_empty(w2.shape), dtau]
 
@@ -168,14 +165,16 @@ def _gn_write_setup(ctx, inputs, output):
     ctx.save_for_backward(x, v, w1, w2, tau)
 
 
-def _gn_write_backward(ctx, grads):
+def _gn_write_backward(ctx, grads, bwd):
     x, v, w1, w2, tau = ctx.saved_tensors
     dh, dlam, dg = grads
-    dx, dv, dw1, dw2, dtau = _gn_write_bwd_op(dh, dlam, dg, x, v, w1, w2, tau, *ctx.args, ctx.need_tau)
+    dx, dv, dw1, dw2, dtau = bwd(dh, dlam, dg, x, v, w1, w2, tau, *ctx.args, ctx.need_tau)
     return dx, dv, dw1, dw2, (dtau if ctx.need_tau else None), None, None, None
 
 
-_gn_write_op.register_autograd(_gn_write_backward, setup_context=_gn_write_setup)
+_gn_write_op = HipOp("gn_write", forward=_gn_write_forward, forward_fake=_gn_write_fake,
+                     backward_impl=_gn_write_backward_impl, backward_fake=_gn_write_backward_fake,
+                     setup=_gn_write_setup, backward=_gn_write_backward)
 
 
 def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps: float = 1e-6):
@@ -206,8 +205,7 @@ def _read_desc(q, m, has_tau, corr, want_resid, s, eps):
                            float(s), float(eps))
 
 
-@torch.library.custom_op("thetascan_hip::gn_read", mutates_args=())
-def _gn_read_op(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None, tau: torch.Tensor | None,
+def _gn_read_forward(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None, tau: torch.Tensor | None,
                 num: torch.Tensor | None, mass: torch.Tensor | None, corr: int, want_resid: bool, s: float,
                 eps: float) -> list[torch.Tensor]:
     lib = _lib.load()
@@ -231,14 +229,12 @@ def _gn_read_op(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None, tau:
     return [h, resid]
 
 
-@_gn_read_op.register_fake
-def _(q, w1, w2, tau, num, mass, corr, want_resid, s, eps):
+def _gn_read_fake(q, w1, w2, tau, num, mass, corr, want_resid, s, eps):
     B, H, T, d = q.shape
     return [q.new_empty(B, H, T, w1.shape[1]), q.new_empty(B, H, T, d) if want_resid else q.new_empty(0)]
 
 
-@torch.library.custom_op("thetascan_hip::gn_read_backward", mutates_args=())
-def _gn_read_bwd_op(dh: torch.Tensor | None, dresid: torch.Tensor | None, q: torch.Tensor, w1: torch.Tensor,
+def _gn_read_backward_impl(dh: torch.Tensor | None, dresid: torch.Tensor | None, q: torch.Tensor, w1: torch.Tensor,
                     w2: torch.Tensor | None, tau: torch.Tensor | None, num: torch.Tensor | None,
                     mass: torch.Tensor | None, corr: int, want_resid: bool, s: float, eps: float, need_tau: bool
                     ) -> list[torch.Tensor]:
@@ -277,8 +273,7 @@ def _gn_read_bwd_op(dh: torch.Tensor | None, dresid: torch.Tensor | None, q: tor
     return [dq, dw1, dw2, dtau, dnum, dmass]
 
 
-@_gn_read_bwd_op.register_fake
-def _(dh, dresid, q, w1, w2, tau, num, mass, corr, want_resid, s, eps, need_tau):
+def _gn_read_backward_fake(dh, dresid, q, w1, w2, tau, num, mass, corr, want_resid, s, eps, need_tau):
     return [q.new_empty(q.shape), w1.new_empty(w1.shape), w2.new_empty(w2.shape) if want_resid else q.new_empty(0),
             tau.new_empty(tau.shape) if (tau is not None and need_tau) else q.new_empty(0),
             num.new_empty(num.shape) if corr else q.new_empty(0),
@@ -292,17 +287,19 @@ def _gn_read_setup(ctx, inputs, output):
     ctx.save_for_backward(q, w1, w2, tau, num, mass)
 
 
-def _gn_read_backward(ctx, grads):
+def _gn_read_backward(ctx, grads, bwd):
     q, w1, w2, tau, num, mass = ctx.saved_tensors
     corr, want_resid, s, eps = ctx.args
     dh, dresid = grads
-    dq, dw1, dw2, dtau, dnum, dmass = _gn_read_bwd_op(dh, dresid if want_resid else None, q, w1, w2, tau, num,
+    dq, dw1, dw2, dtau, dnum, dmass = bwd(dh, dresid if want_resid else None, q, w1, w2, tau, num,
                                                       mass, corr, want_resid, s, eps, ctx.need_tau)
     return (dq, dw1, dw2 if want_resid else None, dtau if ctx.need_tau else None,
             dnum if corr else None, dmass if corr == READ_NORMALIZED else None, None, None, None, None)
 
 
-_gn_read_op.register_autograd(_gn_read_backward, setup_context=_gn_read_setup)
+_gn_read_op = HipOp("gn_read", forward=_gn_read_forward, forward_fake=_gn_read_fake,
+                    backward_impl=_gn_read_backward_impl, backward_fake=_gn_read_backward_fake,
+                    setup=_gn_read_setup, backward=_gn_read_backward)
 
 
 def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = READ_NONE, want_resid: bool = False,
@@ -323,8 +320,7 @@ def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = REA
     return h, (resid if want_resid else None)
 
 
-@torch.library.custom_op("thetascan_hip::normalized_read", mutates_args=())
-def _normalized_read_op(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor, s: float, eps: float
+def _normalized_read_forward(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor, s: float, eps: float
                         ) -> torch.Tensor:
     """y = resid + s * num / (mass + eps)  (or + s * num without mass): the read
     epilogue of engine.py:440-442, 538-544 on ts_read_fwd.  An fp32 numerator
@@ -339,13 +335,11 @@ def _normalized_read_op(num: torch.Tensor, mass: torch.Tensor | None, resid: tor
     return y.to(resid.dtype)
 
 
-@_normalized_read_op.register_fake
-def _(num, mass, resid, s, eps):
+def _normalized_read_fake(num, mass, resid, s, eps):
     return resid.new_empty(num.shape)
 
 
-@torch.library.custom_op("thetascan_hip::normalized_read_backward", mutates_args=())
-def _normalized_read_bwd_op(dy: torch.Tensor, num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor,
+def _normalized_read_backward_impl(dy: torch.Tensor, num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor,
                             s: float, eps: float) -> list[torch.Tensor]:
     from . import fused
 
@@ -356,8 +350,7 @@ def _normalized_read_bwd_op(dy: torch.Tensor, num: torch.Tensor, mass: torch.Ten
     return [dnum, dmass, dresid.to(resid.dtype)]
 
 
-@_normalized_read_bwd_op.register_fake
-def _(dy, num, mass, resid, s, eps):
+def _normalized_read_backward_fake(dy, num, mass, resid, s, eps):
     return [num.new_empty(num.shape), num.new_empty(0) if mass is None else mass.new_empty(mass.shape),
             resid.new_empty(resid.shape)]
 
@@ -368,13 +361,16 @@ def _normalized_read_setup(ctx, inputs, output):
     ctx.save_for_backward(num, mass, resid)
 
 
-def _normalized_read_backward(ctx, dy):
+def _normalized_read_backward(ctx, dy, bwd):
     num, mass, resid = ctx.saved_tensors
-    dnum, dmass, dresid = _normalized_read_bwd_op(dy, num, mass, resid, *ctx.args)
+    dnum, dmass, dresid = bwd(dy, num, mass, resid, *ctx.args)
     return dnum, (None if mass is None else dmass), dresid, None, None
 
 
-_normalized_read_op.register_autograd(_normalized_read_backward, setup_context=_normalized_read_setup)
+_normalized_read_op = HipOp("normalized_read", forward=_normalized_read_forward,
+                            forward_fake=_normalized_read_fake, backward_impl=_normalized_read_backward_impl,
+                            backward_fake=_normalized_read_backward_fake, setup=_normalized_read_setup,
+                            backward=_normalized_read_backward)
 
 
 def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6):

@@ -15,6 +15,7 @@ from functools import partial
 import torch
 
 from . import fused, scan_hip
+from .dispatch import HipOp
 
 _REGISTRY = {"hip": scan_hip.linattn}
 PORTABLE = ("naive", "quad", "chunk", "cumsum", "fla")
@@ -62,23 +63,20 @@ def decayed_prefix(x: torch.Tensor, decay: torch.Tensor) -> torch.Tensor:
     return _wcumsum_op(x, decay, False).to(x.dtype)
 
 
-# The decayed prefix as a torch.library custom op (opaque to TorchDynamo) with
-# its transposed (anti-causal) backward.  The op returns the fp32 prefix; the
-# caller casts.
+# The decayed prefix as an autograd node (dispatch.HipOp) with its transposed
+# (anti-causal) backward.  The forward returns the fp32 prefix; the caller
+# casts.
 
-@torch.library.custom_op("thetascan_hip::wcumsum", mutates_args=())
-def _wcumsum_op(x: torch.Tensor, retention: torch.Tensor | None, reverse: bool) -> torch.Tensor:
+def _wcumsum_forward(x: torch.Tensor, retention: torch.Tensor | None, reverse: bool) -> torch.Tensor:
     return fused.wcumsum(x, retention, reverse)
 
 
-@_wcumsum_op.register_fake
-def _(x, retention, reverse):
+def _wcumsum_fake(x, retention, reverse):
     return x.new_empty(x.shape, dtype=torch.float32)
 
 
-@torch.library.custom_op("thetascan_hip::wcumsum_backward", mutates_args=())
-def _wcumsum_bwd_op(grad: torch.Tensor, retention: torch.Tensor | None, out: torch.Tensor, reverse: bool,
-                    need_retention: bool) -> list[torch.Tensor]:
+def _wcumsum_backward_impl(grad: torch.Tensor, retention: torch.Tensor | None, out: torch.Tensor, reverse: bool,
+                           need_retention: bool) -> list[torch.Tensor]:
     gx = fused.wcumsum(grad, retention, not reverse)
     if retention is None or not need_retention:
         return [gx, gx.new_empty(0)]
@@ -105,8 +103,7 @@ def _wcumsum_bwd_op(grad: torch.Tensor, retention: torch.Tensor | None, out: tor
     return [gx, gret]
 
 
-@_wcumsum_bwd_op.register_fake
-def _(grad, retention, out, reverse, need_retention):
+def _wcumsum_backward_fake(grad, retention, out, reverse, need_retention):
     if retention is None or not need_retention:
         return [torch.empty_like(grad, dtype=torch.float32), grad.new_empty(0)]
     return [torch.empty_like(grad, dtype=torch.float32), torch.empty_like(retention)]
@@ -120,13 +117,15 @@ def _wcumsum_setup(ctx, inputs, output):
     ctx.save_for_backward(retention, output)
 
 
-def _wcumsum_backward(ctx, grad):
+def _wcumsum_backward(ctx, grad, bwd):
     retention, out = ctx.saved_tensors
-    gx, gret = _wcumsum_bwd_op(grad.float(), retention, out, ctx.reverse, ctx.need_retention)
+    gx, gret = bwd(grad.float(), retention, out, ctx.reverse, ctx.need_retention)
     return gx.to(ctx.x_dtype), (gret if ctx.need_retention else None), None
 
 
-_wcumsum_op.register_autograd(_wcumsum_backward, setup_context=_wcumsum_setup)
+_wcumsum_op = HipOp("wcumsum", forward=_wcumsum_forward, forward_fake=_wcumsum_fake,
+                    backward_impl=_wcumsum_backward_impl, backward_fake=_wcumsum_backward_fake,
+                    setup=_wcumsum_setup, backward=_wcumsum_backward)
 
 
 def _retention_stream(retention, like: torch.Tensor):

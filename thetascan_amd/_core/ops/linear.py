@@ -16,6 +16,7 @@ import torch
 import torch.nn.functional as F
 
 from ... import _lib
+from .dispatch import HipOp
 
 
 def _slices(rows: int, target: int = 2048, max_slices: int = 16) -> int:
@@ -80,22 +81,21 @@ def column_sum(x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 
 # F.linear whose backward forms the weight gradient as a split-K GEMM, and the
-# per-head GEMMs of the composed path, as torch.library custom ops: TorchDynamo
-# records them as opaque calls (their backward reaches the HIP reductions
-# through ctypes, which a traced graph cannot contain).
+# per-head GEMMs of the composed path, as autograd nodes (dispatch.HipOp: a
+# torch.library custom op under torch.compile -- their backward reaches the
+# HIP reductions through ctypes, which a traced graph cannot contain -- and an
+# autograd.Function in eager mode).
 
-@torch.library.custom_op("thetascan_hip::linear", mutates_args=())
-def _linear_op(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+def _linear_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
     return F.linear(x, weight, bias)
 
 
-@_linear_op.register_fake
-def _(x, weight, bias):
+def _linear_fake(x, weight, bias):
     return x.new_empty(*x.shape[:-1], weight.shape[0])
 
 
-@torch.library.custom_op("thetascan_hip::linear_backward", mutates_args=())
-def _linear_bwd_op(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, need: list[bool]) -> list[torch.Tensor]:
+def _linear_backward_impl(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, need: list[bool]
+                          ) -> list[torch.Tensor]:
     n_out, n_in = weight.shape
     dy2 = dy.reshape(-1, n_out)
     dx = (dy2 @ weight).view(x.shape) if need[0] else dy.new_empty(0)
@@ -104,8 +104,7 @@ def _linear_bwd_op(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, need
     return [dx, dw, db]
 
 
-@_linear_bwd_op.register_fake
-def _(dy, x, weight, need):
+def _linear_backward_fake(dy, x, weight, need):
     return [x.new_empty(x.shape) if need[0] else dy.new_empty(0),
             weight.new_empty(weight.shape) if need[1] else dy.new_empty(0),
             dy.new_empty(weight.shape[0]) if need[2] else dy.new_empty(0)]
@@ -117,13 +116,15 @@ def _linear_setup(ctx, inputs, output):
     ctx.save_for_backward(x, weight)
 
 
-def _linear_backward(ctx, dy):
+def _linear_backward(ctx, dy, bwd):
     x, weight = ctx.saved_tensors
-    dx, dw, db = _linear_bwd_op(dy, x, weight, ctx.need)
+    dx, dw, db = bwd(dy, x, weight, ctx.need)
     return (dx if ctx.need[0] else None, dw if ctx.need[1] else None, db if ctx.need[2] else None)
 
 
-_linear_op.register_autograd(_linear_backward, setup_context=_linear_setup)
+_linear_op = HipOp("linear", forward=_linear_forward, forward_fake=_linear_fake,
+                   backward_impl=_linear_backward_impl, backward_fake=_linear_backward_fake,
+                   setup=_linear_setup, backward=_linear_backward)
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
@@ -138,8 +139,7 @@ def _head_operand(W: torch.Tensor, B: int, H: int, K: int, trans: bool, dtype) -
     return M.expand(B, H, K, M.shape[-1]).reshape(B * H, K, M.shape[-1]).contiguous()
 
 
-@torch.library.custom_op("thetascan_hip::head_matmul", mutates_args=())
-def _head_matmul_op(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tensor:
+def _head_matmul_forward(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tensor:
     B, H, T, K = x.shape
     Mb = _head_operand(W, B, H, K, trans, x.dtype)
     x3 = x.reshape(B * H, T, K)
@@ -148,15 +148,13 @@ def _head_matmul_op(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tens
     return torch.bmm(x3, Mb).view(B, H, T, Mb.shape[-1])
 
 
-@_head_matmul_op.register_fake
-def _(x, W, trans):
+def _head_matmul_fake(x, W, trans):
     N = W.shape[-2] if trans else W.shape[-1]
     return x.new_empty(*x.shape[:3], N)
 
 
-@torch.library.custom_op("thetascan_hip::head_matmul_backward", mutates_args=())
-def _head_matmul_bwd_op(dy: torch.Tensor, x: torch.Tensor, W: torch.Tensor, trans: bool, need: list[bool]
-                        ) -> list[torch.Tensor]:
+def _head_matmul_backward_impl(dy: torch.Tensor, x: torch.Tensor, W: torch.Tensor, trans: bool, need: list[bool]
+                               ) -> list[torch.Tensor]:
     from .gn import contract_tokens
 
     B, H, T, K = x.shape
@@ -177,8 +175,7 @@ def _head_matmul_bwd_op(dy: torch.Tensor, x: torch.Tensor, W: torch.Tensor, tran
     return [dx, dW]
 
 
-@_head_matmul_bwd_op.register_fake
-def _(dy, x, W, trans, need):
+def _head_matmul_backward_fake(dy, x, W, trans, need):
     return [x.new_empty(x.shape) if need[0] else dy.new_empty(0), W.new_empty(W.shape) if need[1] else dy.new_empty(0)]
 
 
@@ -189,13 +186,15 @@ def _head_matmul_setup(ctx, inputs, output):
     ctx.save_for_backward(x, W)
 
 
-def _head_matmul_backward(ctx, dy):
+def _head_matmul_backward(ctx, dy, bwd):
     x, W = ctx.saved_tensors
-    dx, dW = _head_matmul_bwd_op(dy, x, W, ctx.trans, ctx.need)
+    dx, dW = bwd(dy, x, W, ctx.trans, ctx.need)
     return (dx if ctx.need[0] else None, dW if ctx.need[1] else None, None)
 
 
-_head_matmul_op.register_autograd(_head_matmul_backward, setup_context=_head_matmul_setup)
+_head_matmul_op = HipOp("head_matmul", forward=_head_matmul_forward, forward_fake=_head_matmul_fake,
+                        backward_impl=_head_matmul_backward_impl, backward_fake=_head_matmul_backward_fake,
+                        setup=_head_matmul_setup, backward=_head_matmul_backward)
 
 
 def head_matmul(x: torch.Tensor, W: torch.Tensor, trans: bool) -> torch.Tensor:

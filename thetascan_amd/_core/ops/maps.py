@@ -15,6 +15,7 @@ import ctypes
 import torch
 
 from ... import _lib
+from .dispatch import HipOp
 
 _KERNEL_DTYPES = (torch.bfloat16, torch.float32)
 
@@ -48,8 +49,7 @@ def _spline_desc(pre4, n_basis, degree, bound, scale):
                             float(scale))
 
 
-@torch.library.custom_op("thetascan_hip::bspline", mutates_args=())
-def _bspline_op(pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, degree: int, bound: float,
+def _bspline_forward(pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, degree: int, bound: float,
                 scale: float) -> torch.Tensor:
     lib = _lib.load()
     shape = pre.shape
@@ -64,13 +64,11 @@ def _bspline_op(pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, d
     return out.reshape(*shape[:-1], shape[-1] * n_basis)
 
 
-@_bspline_op.register_fake
-def _(pre, scale_h, n_basis, degree, bound, scale):
+def _bspline_fake(pre, scale_h, n_basis, degree, bound, scale):
     return pre.new_empty(*pre.shape[:-1], pre.shape[-1] * n_basis)
 
 
-@torch.library.custom_op("thetascan_hip::bspline_backward", mutates_args=())
-def _bspline_bwd_op(dout: torch.Tensor, pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, degree: int,
+def _bspline_backward_impl(dout: torch.Tensor, pre: torch.Tensor, scale_h: torch.Tensor | None, n_basis: int, degree: int,
                     bound: float, scale: float) -> list[torch.Tensor]:
     lib = _lib.load()
     shape = pre.shape
@@ -92,8 +90,7 @@ def _bspline_bwd_op(dout: torch.Tensor, pre: torch.Tensor, scale_h: torch.Tensor
     return [dpre.reshape(shape), dscale]
 
 
-@_bspline_bwd_op.register_fake
-def _(dout, pre, scale_h, n_basis, degree, bound, scale):
+def _bspline_backward_fake(dout, pre, scale_h, n_basis, degree, bound, scale):
     return [pre.new_empty(pre.shape), dout.new_empty(0) if scale_h is None else scale_h.new_empty(scale_h.shape)]
 
 
@@ -103,13 +100,15 @@ def _bspline_setup(ctx, inputs, output):
     ctx.save_for_backward(pre, scale_h)
 
 
-def _bspline_backward(ctx, dout):
+def _bspline_backward(ctx, dout, bwd):
     pre, scale_h = ctx.saved_tensors
-    dpre, dscale = _bspline_bwd_op(dout, pre, scale_h, *ctx.args)
+    dpre, dscale = bwd(dout, pre, scale_h, *ctx.args)
     return dpre, (dscale if scale_h is not None else None), None, None, None, None
 
 
-_bspline_op.register_autograd(_bspline_backward, setup_context=_bspline_setup)
+_bspline_op = HipOp("bspline", forward=_bspline_forward, forward_fake=_bspline_fake,
+                    backward_impl=_bspline_backward_impl, backward_fake=_bspline_backward_fake,
+                    setup=_bspline_setup, backward=_bspline_backward)
 
 
 def bspline_features(pre: torch.Tensor, *, n_basis: int, degree: int, bound: float, scale) -> torch.Tensor:
@@ -146,8 +145,7 @@ def _blend_desc(first, n_in):
     return _lib.BlendDesc(B, H, T, d, n_in, _lib.dtype_code(first.dtype))
 
 
-@torch.library.custom_op("thetascan_hip::blend", mutates_args=())
-def _blend_op(coef: torch.Tensor, inputs: list[torch.Tensor]) -> torch.Tensor:
+def _blend_forward(coef: torch.Tensor, inputs: list[torch.Tensor]) -> torch.Tensor:
     lib = _lib.load()
     ins = [_rows(t) for t in inputs]
     desc = _blend_desc(ins[0], len(ins))
@@ -161,13 +159,11 @@ def _blend_op(coef: torch.Tensor, inputs: list[torch.Tensor]) -> torch.Tensor:
     return y
 
 
-@_blend_op.register_fake
-def _(coef, inputs):
+def _blend_fake(coef, inputs):
     return inputs[0].new_empty(inputs[0].shape)
 
 
-@torch.library.custom_op("thetascan_hip::blend_backward", mutates_args=())
-def _blend_bwd_op(dy: torch.Tensor, coef: torch.Tensor, inputs: list[torch.Tensor], need: list[bool]
+def _blend_backward_impl(dy: torch.Tensor, coef: torch.Tensor, inputs: list[torch.Tensor], need: list[bool]
                   ) -> list[torch.Tensor]:
     lib = _lib.load()
     ins = [_rows(t) for t in inputs]
@@ -189,8 +185,7 @@ def _blend_bwd_op(dy: torch.Tensor, coef: torch.Tensor, inputs: list[torch.Tenso
     return [dcoef] + [dy.new_empty(0) if t is None else t for t in dins]
 
 
-@_blend_bwd_op.register_fake
-def _(dy, coef, inputs, need):
+def _blend_backward_fake(dy, coef, inputs, need):
     empty = dy.new_empty(0)
     return [coef.new_empty(coef.shape) if need[0] else empty] + \
         [t.new_empty(t.shape) if w else empty for t, w in zip(inputs, need[1:])]
@@ -202,14 +197,15 @@ def _blend_setup(ctx, inputs, output):
     ctx.save_for_backward(coef, *ins)
 
 
-def _blend_backward(ctx, dy):
+def _blend_backward(ctx, dy, bwd):
     coef, *ins = ctx.saved_tensors
-    res = _blend_bwd_op(dy, coef, list(ins), ctx.need)
+    res = bwd(dy, coef, list(ins), ctx.need)
     grads = [g if w else None for g, w in zip(res, ctx.need)]
     return grads[0], grads[1:]
 
 
-_blend_op.register_autograd(_blend_backward, setup_context=_blend_setup)
+_blend_op = HipOp("blend", forward=_blend_forward, forward_fake=_blend_fake, backward_impl=_blend_backward_impl,
+                  backward_fake=_blend_backward_fake, setup=_blend_setup, backward=_blend_backward)
 
 
 def bank_blend(inputs, coef: torch.Tensor) -> torch.Tensor:

@@ -13,6 +13,7 @@ import ctypes
 import torch
 
 from ... import _lib
+from .dispatch import HipOp
 from .fused import rope_tables
 
 
@@ -40,8 +41,7 @@ def _tables(T: int, rot: int, base: float, device):
     return rope_tables(T, rot, base, device)
 
 
-@torch.library.custom_op("thetascan_hip::qknorm", mutates_args=())
-def _qknorm_op(x: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor:
+def _qknorm_forward(x: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor:
     B, H, T, d = x.shape
     x = _readable(x)
     lib = _lib.load()
@@ -55,13 +55,11 @@ def _qknorm_op(x: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tens
     return y
 
 
-@_qknorm_op.register_fake
-def _(x, rot, base, eps):
+def _qknorm_fake(x, rot, base, eps):
     return x.new_empty(x.shape)
 
 
-@torch.library.custom_op("thetascan_hip::qknorm_backward", mutates_args=())
-def _qknorm_bwd_op(x: torch.Tensor, dy: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor:
+def _qknorm_backward_impl(x: torch.Tensor, dy: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor:
     B, H, T, d = x.shape
     x = _readable(x)
     lib = _lib.load()
@@ -76,8 +74,7 @@ def _qknorm_bwd_op(x: torch.Tensor, dy: torch.Tensor, rot: int, base: float, eps
     return dx
 
 
-@_qknorm_bwd_op.register_fake
-def _(x, dy, rot, base, eps):
+def _qknorm_backward_fake(x, dy, rot, base, eps):
     return x.new_empty(x.shape)
 
 
@@ -87,12 +84,14 @@ def _qknorm_setup(ctx, inputs, output):
     ctx.save_for_backward(x)
 
 
-def _qknorm_backward(ctx, dy):
+def _qknorm_backward(ctx, dy, bwd):
     (x,) = ctx.saved_tensors
-    return _qknorm_bwd_op(x, dy, *ctx.args), None, None, None
+    return bwd(x, dy, *ctx.args), None, None, None
 
 
-_qknorm_op.register_autograd(_qknorm_backward, setup_context=_qknorm_setup)
+_qknorm_op = HipOp("qknorm", forward=_qknorm_forward, forward_fake=_qknorm_fake,
+                   backward_impl=_qknorm_backward_impl, backward_fake=_qknorm_backward_fake,
+                   setup=_qknorm_setup, backward=_qknorm_backward)
 
 
 def qk_norm(x: torch.Tensor, rot: int, base: float, eps: float) -> torch.Tensor | None:

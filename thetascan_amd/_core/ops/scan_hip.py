@@ -41,6 +41,7 @@ import ctypes
 import torch
 
 from ... import _lib
+from .dispatch import HipOp
 
 DEFAULT_CHUNK = 512   # reference default (scan_chunk.DEFAULT_CHUNK); validated only
 TILE = 64             # the kernel's tile
@@ -561,10 +562,9 @@ def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: b
     return gq, gk, gv, r_grads
 
 
-# The scan as torch.library custom ops: opaque to TorchDynamo (the ctypes
-# launches never enter a traced graph), with a fake implementation for shape
-# propagation and an autograd formula that calls the backward op.  Absent
-# retentions and absent gradients travel as empty placeholders.
+# The scan as an autograd node (dispatch.HipOp: a torch.library custom op
+# under torch.compile, an autograd.Function in eager mode).  Absent retentions
+# and absent gradients travel as empty placeholders.
 
 def _placeholder(like: torch.Tensor) -> torch.Tensor:
     return like.new_empty(0)
@@ -574,25 +574,22 @@ def _or_none(t: torch.Tensor):
     return None if t.numel() == 0 and t.ndim == 1 else t
 
 
-@torch.library.custom_op("thetascan_hip::scan_views", mutates_args=())
-def _scan_views_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: list[torch.Tensor], with_mass: bool
-                   ) -> list[torch.Tensor]:
+def _scan_views_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: list[torch.Tensor],
+                        with_mass: bool) -> list[torch.Tensor]:
     outs, masses = _views_forward(q, k, v, with_mass, [_or_none(r) for r in rets])
     return outs + masses
 
 
-@_scan_views_op.register_fake
-def _(q, k, v, rets, with_mass):
+def _scan_views_fake(q, k, v, rets, with_mass):
     B, H, T = q.shape[:3]
     outs = [q.new_empty(B, H, T, v.shape[-1]) for _ in rets]
     masses = [q.new_empty(B, H, T, dtype=torch.float32) for _ in rets] if with_mass else []
     return outs + masses
 
 
-@torch.library.custom_op("thetascan_hip::scan_views_backward", mutates_args=())
-def _scan_views_bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: list[torch.Tensor],
-                       d_outs: list[torch.Tensor], d_mass: list[torch.Tensor], need: list[bool]
-                       ) -> list[torch.Tensor]:
+def _scan_views_backward_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: list[torch.Tensor],
+                              d_outs: list[torch.Tensor], d_mass: list[torch.Tensor], need: list[bool]
+                              ) -> list[torch.Tensor]:
     retentions = [_or_none(r) for r in rets]
     gq, gk, gv, r_grads = _views_backward(q, k, v, retentions, [_or_none(g) for g in d_outs],
                                           [_or_none(g) for g in d_mass], need[0], need[1], need[2], need[3:])
@@ -601,8 +598,7 @@ def _scan_views_bwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rets: 
     return [_placeholder(x) if g is None else g for g, x in zip(grads, like)]
 
 
-@_scan_views_bwd_op.register_fake
-def _(q, k, v, rets, d_outs, d_mass, need):
+def _scan_views_backward_fake(q, k, v, rets, d_outs, d_mass, need):
     like = [q, k, v] + list(rets)
     return [torch.empty_like(x) if (w and _or_none(x) is not None) else _placeholder(x) for x, w in zip(like, need)]
 
@@ -614,18 +610,20 @@ def _scan_views_setup(ctx, inputs, output):
     ctx.save_for_backward(q, k, v, *rets)
 
 
-def _scan_views_backward(ctx, grads):
+def _scan_views_backward(ctx, grads, bwd):
     q, k, v, *rets = ctx.saved_tensors
     n = len(rets)
     d_outs = [_placeholder(q) if g is None else g for g in grads[:n]]
     d_mass = [_placeholder(q) if g is None else g for g in grads[n:]] if ctx.with_mass else \
-        [_placeholder(q)] * n
-    res = _scan_views_bwd_op(q, k, v, list(rets), d_outs, d_mass, ctx.need)
+        [_placeholder(q) for _ in range(n)]
+    res = bwd(q, k, v, list(rets), d_outs, d_mass, ctx.need)
     out = [None if not w else _or_none(g) for g, w in zip(res, ctx.need)]
     return out[0], out[1], out[2], out[3:], None
 
 
-_scan_views_op.register_autograd(_scan_views_backward, setup_context=_scan_views_setup)
+_scan_views_op = HipOp("scan_views", forward=_scan_views_forward, forward_fake=_scan_views_fake,
+                       backward_impl=_scan_views_backward_impl, backward_fake=_scan_views_backward_fake,
+                       setup=_scan_views_setup, backward=_scan_views_backward)
 
 
 def _run_views(q, k, v, retentions, chunk, with_mass, out_f32=False):

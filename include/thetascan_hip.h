@@ -28,8 +28,9 @@ extern "C" {
 #endif
 
 /* 8: the scan entry points require a 16-byte aligned workspace (a sub-
- *    allocated workspace at an odd offset was accepted by version 7). */
-#define TS_ABI_VERSION 8
+ *    allocated workspace at an odd offset was accepted by version 7).
+ * 9: ts_wcumsum takes a workspace (ts_wcumsum_workspace_bytes). */
+#define TS_ABI_VERSION 9
 
 enum ts_status {
   TS_OK = 0,
@@ -526,6 +527,10 @@ int ts_blend_bwd(const ts_blend_desc* desc, const ts_strided* in, const float* c
 /* Decayed prefix sum along T of an fp32 [B,H,T,F] stream:
  *   z_t = a_t z_{t-1} + x_t   (a = exp(log_alpha[h]) static, or exp(decay[b,h,t]),
  *   or 1 for the plain prefix), optionally anti-causal (reverse).
+ * Parallel over time: segments of the time axis scan from a zero state, then
+ * each adds the decayed state entering it (two launches).  The workspace
+ * (ts_wcumsum_workspace_bytes, 16-byte aligned, no initialisation) holds one
+ * state and one decay product per segment.
  * Replaces interface.ema_cumsum / causal_prefix_sum / Accumulator.mass_cum
  * (src/thetascan/_core/ops/interface.py:58-107, 216-230). */
 typedef struct ts_wcumsum_desc {
@@ -534,8 +539,10 @@ typedef struct ts_wcumsum_desc {
   int32_t reverse;
 } ts_wcumsum_desc;
 
+int ts_wcumsum_workspace_bytes(const ts_wcumsum_desc* desc, size_t* bytes);
+
 int ts_wcumsum(const ts_wcumsum_desc* desc, ts_strided x, ts_strided out, const float* log_alpha,
-               ts_strided decay, hipStream_t stream);
+               ts_strided decay, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* out[i] = scale * (sum_{s<na} a[s*n + i] + sum_{s<nb} b[s*n + i]) for i < n,
  * written as ts_dtype out_dtype: sums the partial weight-gradient slots of

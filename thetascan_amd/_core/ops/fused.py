@@ -273,9 +273,12 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
             kind = _lib.RET_STATIC
             la = retention.detach().to(torch.float32).reshape(H).contiguous()
     desc = _lib.WcumsumDesc(B, H, T, F, kind, int(reverse))
+    nbytes = ctypes.c_size_t()
+    _lib.check(lib.ts_wcumsum_workspace_bytes(ctypes.byref(desc), ctypes.byref(nbytes)), "ts_wcumsum_workspace_bytes")
+    work = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=x.device)
     with _lib.timed("ts_wcumsum", lambda: _lib.nbytes(xf, out, dec)):
         status = lib.ts_wcumsum(ctypes.byref(desc), _lib.strided(xf), _lib.strided(out), _lib.ptr(la),
-                                _lib.strided(dec), _lib.stream_handle(x.device))
+                                _lib.strided(dec), work.data_ptr(), nbytes.value, _lib.stream_handle(x.device))
     _lib.check(status, "ts_wcumsum")
     return out
 

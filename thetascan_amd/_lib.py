@@ -458,7 +458,9 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_qknorm_bwd.argtypes = [P(QkNormDesc), Strided, Strided, Strided, ctypes.c_void_p, ctypes.c_void_p,
                                       ctypes.c_void_p]
-        lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
+        lib.ts_wcumsum_workspace_bytes.argtypes = [P(WcumsumDesc), P(ctypes.c_size_t)]
+        lib.ts_wcumsum.argtypes = [P(WcumsumDesc), Strided, Strided, ctypes.c_void_p, Strided, ctypes.c_void_p,
+                                   ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_col_sums.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
         lib.ts_sum_slots.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
@@ -481,7 +483,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 8:
+        if lib.ts_abi_version() != 9:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

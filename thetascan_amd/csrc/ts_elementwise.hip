@@ -332,32 +332,91 @@ __global__ __launch_bounds__(256) void qknorm_bwd_kernel(NormP p) {
 }
 
 // z_t = a_t z_{t-1} + x_t  over T for every (b, h, feature).
-__global__ __launch_bounds__(256) void wcumsum_kernel(int B, int H, int T, int F, int ret, int reverse,
-                                                      ts_strided x, ts_strided out, const float* log_alpha,
-                                                      ts_strided decay) {
+// Decayed prefix z_u = a_u z_{u-1} + x_u along the scan order u (t = u, or
+// t = T-1-u for an anti-causal scan), parallel over time: the order is cut
+// into S segments of L steps.
+//   wcumsum_local_kernel : each thread scans one (b, h, segment, feature) from
+//                          a zero state, stores the local prefix l_u, the
+//                          segment's last value and (feature 0) its decay
+//                          product P = prod a_u;
+//   wcumsum_carry_kernel : each thread of segment j >= 1 folds the earlier
+//                          segments' (P, last) into the entering state C_j
+//                          (C_{j+1} = P_j C_j + last_j, in segment order) and
+//                          adds A_u C_j to its outputs, A_u = prod of a over
+//                          the segment up to u.
+// Consecutive threads take consecutive features, so every access is a
+// coalesced row.  Step decays: static exp(log_alpha[h]); a stream's a_u is
+// exp(decay[t]) causally and exp(decay[t+1]) anti-causally (the decay of the
+// token the state steps out of), 1 past the end.
+struct WcumsumP {
+  int B, H, T, F, S, L, ret, reverse;
+  ts_strided x, out, decay;
+  const float* log_alpha;
+  float* tot;   // [B*H, S, F] last local value of each segment
+  float* prod;  // [B*H, S]    decay product of each segment
+};
+
+__device__ __forceinline__ float wcumsum_step(const WcumsumP& p, const float* db, float a_static, int u) {
+  if (p.ret == TS_RET_STATIC) return a_static;
+  if (p.ret != TS_RET_STREAM) return 1.0f;
+  const int tp = p.reverse ? p.T - 1 - u : u;
+  const int src = p.reverse ? tp + 1 : tp;
+  return src < p.T ? expf(db[(int64_t)src * p.decay.st]) : 1.0f;
+}
+
+__global__ __launch_bounds__(256) void wcumsum_local_kernel(WcumsumP p) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)B * H * F) return;
-  const int f = (int)(idx % F);
-  const int h = (int)((idx / F) % H);
-  const int b = (int)(idx / ((int64_t)F * H));
-  const float* xb = (const float*)x.ptr + (int64_t)b * x.sb + (int64_t)h * x.sh + f;
-  float* ob = (float*)out.ptr + (int64_t)b * out.sb + (int64_t)h * out.sh + f;
-  const float a_static = ret == TS_RET_STATIC ? expf(log_alpha[h]) : 1.0f;
-  const float* db = ret == TS_RET_STREAM
-                        ? (const float*)decay.ptr + (int64_t)b * decay.sb + (int64_t)h * decay.sh
+  if (idx >= (int64_t)p.B * p.H * p.S * p.F) return;
+  const int f = (int)(idx % p.F);
+  const int64_t r = idx / p.F;
+  const int seg = (int)(r % p.S);
+  const int bh = (int)(r / p.S);
+  const int b = bh / p.H, h = bh % p.H;
+  const float* xb = (const float*)p.x.ptr + (int64_t)b * p.x.sb + (int64_t)h * p.x.sh + f;
+  float* ob = (float*)p.out.ptr + (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + f;
+  const float* db = p.ret == TS_RET_STREAM
+                        ? (const float*)p.decay.ptr + (int64_t)b * p.decay.sb + (int64_t)h * p.decay.sh
                         : nullptr;
-  float z = 0.0f;
-  for (int s = 0; s < T; ++s) {
-    const int tp = reverse ? T - 1 - s : s;
-    float a = a_static;
-    if (db) {
-      // a_t multiplies the state when stepping into t; anti-causal scans
-      // step from t+1 into t and use the decay of t+1.
-      const int src = reverse ? tp + 1 : tp;
-      a = src < T ? expf(db[(int64_t)src * decay.st]) : 1.0f;
-    }
-    z = (s == 0 ? 0.0f : a * z) + xb[(int64_t)tp * x.st];
-    ob[(int64_t)tp * out.st] = z;
+  const float a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.0f;
+  const int u0 = seg * p.L;
+  const int u1 = min(u0 + p.L, p.T);
+  float z = 0.0f, P = 1.0f;
+  for (int u = u0; u < u1; ++u) {
+    const int tp = p.reverse ? p.T - 1 - u : u;
+    const float a = wcumsum_step(p, db, a_static, u);
+    z = (u == u0 ? 0.0f : a * z) + xb[(int64_t)tp * p.x.st];
+    P *= a;
+    ob[(int64_t)tp * p.out.st] = z;
+  }
+  p.tot[r * p.F + f] = z;
+  if (f == 0) p.prod[r] = P;
+}
+
+__global__ __launch_bounds__(256) void wcumsum_carry_kernel(WcumsumP p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)p.B * p.H * p.S * p.F) return;
+  const int f = (int)(idx % p.F);
+  const int64_t r = idx / p.F;
+  const int seg = (int)(r % p.S);
+  if (seg == 0) return;
+  const int bh = (int)(r / p.S);
+  const int b = bh / p.H, h = bh % p.H;
+  const int64_t row0 = (int64_t)bh * p.S;
+  float C = 0.0f;
+  for (int j = 0; j < seg; ++j) C = p.prod[row0 + j] * C + p.tot[(row0 + j) * p.F + f];
+  float* ob = (float*)p.out.ptr + (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + f;
+  const float* db = p.ret == TS_RET_STREAM
+                        ? (const float*)p.decay.ptr + (int64_t)b * p.decay.sb + (int64_t)h * p.decay.sh
+                        : nullptr;
+  const float a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.0f;
+  const int u0 = seg * p.L;
+  const int u1 = min(u0 + p.L, p.T);
+  float A = 1.0f;
+  for (int u = u0; u < u1; ++u) {
+    const int tp = p.reverse ? p.T - 1 - u : u;
+    A *= wcumsum_step(p, db, a_static, u);
+    float* o = ob + (int64_t)tp * p.out.st;
+    *o += A * C;
   }
 }
 
@@ -817,17 +876,54 @@ int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_
   return finish("col_sums");
 }
 
-int ts_wcumsum(const ts_wcumsum_desc* d, ts_strided x, ts_strided out, const float* log_alpha,
-               ts_strided decay, hipStream_t stream) {
+// Segments of the scan order: enough (b, h, segment, feature) threads to
+// fill the chip (about 2^19), at least 16 steps per segment.
+static void wcumsum_segments(const ts_wcumsum_desc* d, int* S, int* L) {
+  const int64_t lanes = (int64_t)d->B * d->H * d->F;
+  int64_t want = ((int64_t)1 << 19) / (lanes > 0 ? lanes : 1);
+  const int64_t most = (d->T + 15) / 16;
+  if (want > most) want = most;
+  if (want < 1) want = 1;
+  *L = (int)((d->T + want - 1) / want);
+  if (*L < 1) *L = 1;
+  *S = (d->T + *L - 1) / *L;
+}
+
+int ts_wcumsum_workspace_bytes(const ts_wcumsum_desc* d, size_t* bytes) {
   if (!d || d->B < 1 || d->H < 1 || d->T < 0 || d->F < 1) return fail(TS_ERR_VALUE, "wcumsum: bad shape");
+  int S = 0, L = 0;
+  wcumsum_segments(d, &S, &L);
+  if (bytes) *bytes = d->T == 0 ? 0 : (size_t)d->B * d->H * S * ((size_t)d->F + 1) * sizeof(float) + 256;
+  return TS_OK;
+}
+
+int ts_wcumsum(const ts_wcumsum_desc* d, ts_strided x, ts_strided out, const float* log_alpha,
+               ts_strided decay, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!d || d->B < 1 || d->H < 1 || d->T < 0 || d->F < 1) return fail(TS_ERR_VALUE, "wcumsum: bad shape");
+  if (d->retention < TS_RET_NONE || d->retention > TS_RET_STREAM) return fail(TS_ERR_VALUE, "wcumsum: bad retention");
+  if (d->T == 0) return TS_OK;
   if (!x.ptr || !out.ptr) return fail(TS_ERR_VALUE, "wcumsum: missing tensors");
   if (d->retention == TS_RET_STATIC && !log_alpha) return fail(TS_ERR_VALUE, "wcumsum: missing log_alpha");
   if (d->retention == TS_RET_STREAM && !decay.ptr) return fail(TS_ERR_VALUE, "wcumsum: missing decay");
-  const int64_t n = (int64_t)d->B * d->H * d->F;
-  if (d->T == 0) return TS_OK;
-  hipLaunchKernelGGL(ts::wcumsum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, d->B, d->H, d->T,
-                     d->F, d->retention, d->reverse, x, out, log_alpha, decay);
-  return finish("wcumsum");
+  size_t need = 0;
+  int rc = ts_wcumsum_workspace_bytes(d, &need);
+  if (rc) return rc;
+  if (!workspace || workspace_bytes < need)
+    return fail(TS_ERR_VALUE, "wcumsum: workspace too small (%zu < %zu bytes)", workspace_bytes, need);
+  if ((uintptr_t)workspace & 15u) return fail(TS_ERR_VALUE, "wcumsum: workspace is not 16-byte aligned");
+  ts::WcumsumP p;
+  p.B = d->B; p.H = d->H; p.T = d->T; p.F = d->F;
+  wcumsum_segments(d, &p.S, &p.L);
+  p.ret = d->retention; p.reverse = d->reverse;
+  p.x = x; p.out = out; p.decay = decay; p.log_alpha = log_alpha;
+  p.tot = (float*)workspace;
+  p.prod = p.tot + (size_t)d->B * d->H * p.S * d->F;
+  const int64_t n = (int64_t)d->B * d->H * p.S * d->F;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  hipLaunchKernelGGL(ts::wcumsum_local_kernel, grid, dim3(256), 0, stream, p);
+  if ((rc = finish("wcumsum"))) return rc;
+  if (p.S > 1) hipLaunchKernelGGL(ts::wcumsum_carry_kernel, grid, dim3(256), 0, stream, p);
+  return finish("wcumsum carry");
 }
 
 }  // extern "C"

@@ -285,49 +285,60 @@ def cpu_baseline(budget_s: float = 12.0):
 
 
 # The other two workloads the path serves, measured with ``--workload``:
-#   gn            damped Gauss-Newton memory, fast net 64 -> 128 -> 64 (ReLU^2),
-#                 two-stage feature-mass read normalization, B8 T2048 H8 d64,
-#                 bf16, fwd+bwd;
+#   gn            damped Gauss-Newton memory, fast net 64 -> 128 -> 64 with tanh
+#                 and damping 1e-2 (this build's extension of the core config:
+#                 the public config, like the reference's, offers relu2/silu),
+#                 two-stage read normalization (signed mass), B8 T2048 H8 d64,
+#                 slow reference weights W1, W2 ~ N(0, 0.02), bf16, fwd+bwd;
 #   bspline_bank  kernel memory with the cubic B-spline map (8 basis functions,
 #                 m = 128), key-mass read, two-rate recency bank (fast blend,
 #                 retentions 0.9 / 0.999), B2 T32768 H8 d64, 128-token tiles,
 #                 bf16, forward only.
 OTHER = {
-    "gn": dict(B=8, T=2048, train=True, metric="GN mixer tokens/s fwd+bwd (B8 T2048 H8 d64 m128 bf16)"),
+    "gn": dict(B=8, T=2048, train=True,
+               metric="GN mixer tokens/s fwd+bwd (B8 T2048 H8 d64 m128 tanh, damping 1e-2, bf16)"),
     "bspline_bank": dict(B=2, T=32768, train=False,
                          metric="B-spline bank mixer tokens/s fwd (B2 T32768 H8 d64 m128 bf16)"),
 }
 
 
 def other_config(name: str):
+    """The core (flat) configuration of a secondary workload."""
+    import dataclasses
+
     import thetascan_amd as ts
 
     if name == "gn":
-        return ts.ThetaScanConfig(
+        public = ts.ThetaScanConfig(
             d_model=D_MODEL, n_heads=H, memory_multiplier=2, family="gn",
             gn=ts.GNConfig(nonlinearity="relu2", jacobian_steps=1, read_normalization="both_feature_mass"),
             temporal=ts.TemporalConfig(mode="sum"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64),
         )
+        return dataclasses.replace(public._to_core_config(), nonlin="tanh", gn_damping=1e-2)
     return ts.ThetaScanConfig(
         d_model=D_MODEL, n_heads=H, memory_multiplier=2, family="kernel",
         kernel=ts.KernelConfig(feature_map="projected_bspline", read_normalization="key_mass"),
         temporal=ts.TemporalConfig(mode="bank", bank_mode="fast", recency_branches=2, retention_inits=(0.9, 0.999)),
         runtime=ts.RuntimeConfig(backend="hip", scan_chunk=128),
-    )
+    )._to_core_config()
 
 
 def run_other(name: str, args) -> dict:
     """One JSON line for a non-headline workload (no CPU baseline)."""
     import torch
 
+    from thetascan_amd._core.modules.block import ThetaScan as CoreMixer
+
     spec = OTHER[name]
     dev = torch.device("cuda", 0)
     torch.manual_seed(0)
-    module = __import__("thetascan_amd").ThetaScan(other_config(name))
+    module = CoreMixer(other_config(name))
     g = torch.Generator().manual_seed(1)
     with torch.no_grad():
         for pname, p in sorted(module.named_parameters()):
-            if "fade_eta" in pname or (p.ndim >= 2 and float(p.abs().max()) == 0.0):
+            if name == "gn" and pname.startswith(("W1.", "W2.")):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+            elif "fade_eta" in pname or (p.ndim >= 2 and float(p.abs().max()) == 0.0):
                 p.copy_(torch.randn(p.shape, generator=g) * (0.3 if "fade_eta" in pname else 0.02))
     module = module.to(dev, torch.bfloat16)
     x = torch.randn(spec["B"], spec["T"], D_MODEL, generator=g).to(dev, torch.bfloat16)
@@ -339,7 +350,7 @@ def run_other(name: str, args) -> dict:
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (x ~ N(0,1), seeded weights)", "execution": "eager",
-        "path": module._core.last_path,
+        "path": module.last_path,
         "config": {"workload": name, "batch": spec["B"], "seq_len": spec["T"], "heads": H, "head_dim": D_HEAD,
                    "d_model": D_MODEL, "parallelism": "single GPU"},
         "roofline": roofline_of(passes, {}), "passes": passes,

@@ -29,8 +29,10 @@ extern "C" {
 
 /* 8: the scan entry points require a 16-byte aligned workspace (a sub-
  *    allocated workspace at an odd offset was accepted by version 7).
- * 9: ts_wcumsum takes a workspace (ts_wcumsum_workspace_bytes). */
-#define TS_ABI_VERSION 9
+ * 9: ts_wcumsum takes a workspace (ts_wcumsum_workspace_bytes).
+ * 10: the GN descriptors carry the hidden nonlinearity (and the write its
+ *     damping). */
+#define TS_ABI_VERSION 10
 
 enum ts_status {
   TS_OK = 0,
@@ -367,15 +369,23 @@ int ts_qknorm_bwd(const ts_qknorm_desc* desc, ts_strided x, ts_strided dy, ts_st
 
 /* -------------------------------------------------------- GN write payloads */
 
-/* Damped Gauss-Newton write of a one-hidden-layer ReLU^2 fast network
+/* Hidden nonlinearity sigma of a GN fast network. */
+enum ts_gn_act {
+  TS_GN_RELU2 = 0,  /* sigma = relu(pre)^2, sigma' = 2 relu(pre)   (engine.py nonlin relu2) */
+  TS_GN_TANH = 1,   /* sigma = tanh(pre), sigma' = 1 - tanh(pre)^2 (no counterpart in the
+                       reference, whose nonlinearities are relu2 and silu, nonlin.py:28-31) */
+};
+
+/* Damped Gauss-Newton write of a one-hidden-layer fast network
  * (engine.py:117-158 _block_forward, 180-195 _g_from_lambda, 215-255
  * _lambda_solve and the write streams of 260-340), per token x (key) and v:
- *   a = W1 x;  pre = a rsqrt(mean a^2 + eps) - tau;  h = relu(pre)^2
+ *   a = W1 x;  pre = a rsqrt(mean a^2 + eps) - tau;  h = sigma(pre)
  *   r = v - x - s W2 h
- *   lam = r / ((|h|^2 + |x|^2 (W2 o W2)(2 relu(pre) rinv)^2) * inv_depth + eps)
- *   g = s 2 relu(pre) (W2^T lam) rinv
+ *   lam = r / ((|h|^2 + |x|^2 (W2 o W2)(sigma'(pre) rinv)^2) * inv_depth + damping)
+ *   g = s sigma'(pre) (W2^T lam) rinv
  * Outputs h [.,m] (LA2 keys), s*lam [.,d] (LA2 values), g [.,m] (LA1 values).
- * Depth-1 memories (s = inv_depth = 1) with relu2 or relu2_threshold. */
+ * Depth-1 memories (s = inv_depth = 1) with relu2, relu2_threshold or tanh.
+ * The reference's damping is eps (engine.py:255). */
 typedef struct ts_gn_desc {
   int32_t B, H, T;
   int32_t d;            /* head width: 16, 32, 64 or 128                        */
@@ -384,7 +394,9 @@ typedef struct ts_gn_desc {
   int32_t has_tau;      /* relu2_threshold: subtract tau [H, m]                 */
   float s;              /* 1/sqrt(depth)                                        */
   float inv_depth;      /* 1/depth: the Jacobi diagonal averages the levels     */
-  float eps;            /* 1e-6 in the reference (also the damping)             */
+  float eps;            /* 1e-6 in the reference (RMSNorm)                      */
+  int32_t act;          /* ts_gn_act                                            */
+  float damping;        /* > 0: the Jacobi diagonal's damping (the reference: eps) */
 } ts_gn_desc;
 
 typedef struct ts_gn_io {
@@ -418,7 +430,7 @@ int ts_gn_write_bwd(const ts_gn_desc* desc, const ts_gn_bwd_io* io, hipStream_t 
 
 /* One stage of the GN read (engine.py:467-506), per query q [.,d]:
  *   a = W1 q + c,  c = 0 | num | num / (mass + eps)      (corr = 0 | 1 | 2)
- *   h = relu(a rsqrt(mean a^2 + eps) - tau)^2            -> h [.,m]
+ *   h = sigma(a rsqrt(mean a^2 + eps) - tau)             -> h [.,m]
  *   resid = q + s W2 h                                   -> resid [.,d]
  * Stage 1 of the two-stage normalized read is corr 0 without resid (the
  * queries of the feature-mass scan, engine.py:475-480); stage 2 adds the
@@ -433,6 +445,7 @@ typedef struct ts_gn_read_desc {
   int32_t want_resid;
   float s;              /* 1/sqrt(depth)                                        */
   float eps;
+  int32_t act;          /* ts_gn_act of h (stage 1 of the two-stage read: relu2) */
 } ts_gn_read_desc;
 
 typedef struct ts_gn_read_io {

@@ -237,7 +237,33 @@ def dsilu(pre):
     return s * (1 + pre * (1 - s))
 
 
-ACT = {"relu2": (relu2, drelu2), "silu": (F.silu, dsilu)}
+def dtanh(pre):
+    return 1.0 - torch.tanh(pre).square()
+
+
+# tanh (sigma' = 1 - tanh^2) is this build's extension of the reference's
+# relu2 / silu table (nonlin.py:28-31); the write and read formulas around it
+# are the reference's, with the damping of the Jacobi diagonal and the key
+# mass of signed features below.
+ACT = {"relu2": (relu2, drelu2), "silu": (F.silu, dsilu), "tanh": (torch.tanh, dtanh)}
+
+
+def damping(c) -> float:
+    """The Jacobi diagonal's damping; the reference's is eps (engine.py:255)."""
+    return EPS if c.get("gn_damping") is None else float(c["gn_damping"])
+
+
+def key_mass(view, qf, keys, unit_mass, c):
+    """The mass a normalized read divides by, num / (mass + eps)
+    (engine.py:440-442, 503-506).  For the reference's nonnegative features it
+    is the scan's unit column, sum_i w_i qf . k_i.  tanh features are signed,
+    so those products cancel and the mass can cross zero; the mass is then
+    that of the absolute features, sum_i w_i |qf| . |k_i| = |qf| . (the view's
+    decayed prefix of |k|), which equals the unit column for nonnegative
+    features and bounds the read: |num| / mass <= max |value|."""
+    if c["nonlin"] == "tanh":
+        return (qf.abs() * view.mass_cum(keys.abs())).sum(-1, keepdim=True)
+    return unit_mass
 
 
 def ein(W, x, pat):
@@ -358,7 +384,7 @@ def lambda_solve(weights, c, ctxs, r):
             s = ACT[c["nonlin"]][1](ctx["pre"]) * ctx["inv_a"]
             s2 = s * s
         diag = diag + hh + xx * ein(W2 * W2, s2, "hdm,bhtm->bhtd")
-    return r / (diag / c["depth"] + EPS)
+    return r / (diag / c["depth"] + damping(c))
 
 
 def write_streams(weights, c, k, v, hrot, ctl):
@@ -436,7 +462,7 @@ def read_view(weights, c, q, streams, view, hrot, ctl):
             fkeys = streams["la2"][l][0]
             gvals = streams["la1"][l][1]
             corr1 = view.scan(h0q, fkeys, torch.cat([gvals, gvals.new_ones(*gvals.shape[:3], 1)], -1))
-            a = a + corr1[..., :m] / (corr1[..., -1:] + EPS)
+            a = a + corr1[..., :m] / (key_mass(view, h0q, fkeys, corr1[..., -1:], c) + EPS)
         else:
             for it in range(c["write_iters"]):
                 entry = streams["la1"][it * L + l]
@@ -457,7 +483,7 @@ def read_view(weights, c, q, streams, view, hrot, ctl):
             keys, vals = streams["la2"][l]
             if c["read_norm_mode"] == "key_mass":
                 corr = view.scan(hq, keys, torch.cat([vals, vals.new_ones(*vals.shape[:3], 1)], -1))
-                mem = corr[..., :-1] / (corr[..., -1:] + EPS)
+                mem = corr[..., :-1] / (key_mass(view, hq, keys, corr[..., -1:], c) + EPS)
             else:
                 kcum = view.mass_cum(keys)
                 mem = view.scan(hq / (kcum + EPS), keys, vals)

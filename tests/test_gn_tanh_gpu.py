@@ -1,0 +1,162 @@
+"""The GN kernels with a tanh hidden layer and a separate damping (GPU tests).
+
+The ThetaScan-GN workload's fast network is 64 -> 128 -> 64 with tanh and a
+damping lambda = 1e-2 separate from eps (an extension of this build: the
+reference's GN nonlinearities are relu2, silu and swiglu, and its damping is
+eps).  tanh features are signed, so the normalized reads divide by the mass
+of the absolute features, sum_i w_i |q| . |k_i|.  Checked against the float64
+oracle (pinned by the Gauss-Newton and brute-force constructions of
+tests/test_oracle_gn_extensions.py):
+* the write payloads h, s*lam, g and every gradient;
+* the read stages with tanh features, every correction kind;
+* the whole GN mixer (two-stage normalized read; plain sum, the ema stream
+  and a fast bank), fp32 at rel 1e-3 and bf16 at rel 2e-2.
+"""
+from __future__ import annotations
+
+import dataclasses
+import json
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import mixer as oracle_mixer
+from tests.conftest import rel_err
+from tests.test_gn_gpu import _case
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+CASES = json.loads((GOLDEN / "mixer_cases.json").read_text())
+DAMP = 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d,m,learn_thresh,T", [(64, 128, False, 150), (32, 96, True, 64), (16, 48, False, 70)])
+def test_tanh_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T):
+    from thetascan_amd._core.ops import gn
+
+    B, H = 2, 3
+    k, v, w1, w2, wg = _case(B, H, T, d, m, learn_thresh, 31 * d + m + T, dtype)
+    c = {"write_rule": "gn", "nonlin": "tanh", "depth": 1, "fast_w1": True, "write_iters": 1,
+         "learn_thresh": learn_thresh, "value_centers": 0, "gn_damping": DAMP}
+    rk, rv, rw1, rw2 = (t.clone().requires_grad_(True) for t in (k, v, w1, w2))
+    rwg = wg.clone().requires_grad_(True) if learn_thresh else None
+    st = oracle_mixer.write_streams([(rw1, rw2, rwg)], c, rk, rv, None, {})
+    (_, g_ref), = st["la1"]
+    (h_ref, lam_ref), = st["la2"]
+    gen = torch.Generator().manual_seed(8)
+    dh = torch.randn(h_ref.shape, generator=gen, dtype=torch.float64)
+    dl = torch.randn(lam_ref.shape, generator=gen, dtype=torch.float64)
+    dg = torch.randn(g_ref.shape, generator=gen, dtype=torch.float64) * 0.1
+    torch.autograd.backward([h_ref, lam_ref, g_ref], [dh, dl, dg])
+
+    dev = lambda t: None if t is None else t.to(cuda, dtype).requires_grad_(True)  # noqa: E731
+    x_, v_, w1_, w2_ = dev(k), dev(v), dev(w1), dev(w2)
+    tau_ = dev(wg[..., 0].contiguous()) if learn_thresh else None
+    h, lam, g = gn.write(x_, v_, w1_, w2_, tau_, nonlin="tanh", damping=DAMP)
+    torch.autograd.backward([h, lam, g], [dh.to(cuda, dtype), dl.to(cuda, dtype), dg.to(cuda, dtype)])
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
+    for name, a, e in (("h", h, h_ref), ("lam", lam, lam_ref), ("g", g, g_ref)):
+        assert rel_err(a, e) < tol, (name, rel_err(a, e))
+    gtol = 2e-3 if dtype == torch.float32 else 4e-2
+    grads = [("dx", x_.grad, rk.grad), ("dv", v_.grad, rv.grad), ("dW1", w1_.grad, rw1.grad),
+             ("dW2", w2_.grad, rw2.grad)]
+    if learn_thresh:
+        grads.append(("dtau", tau_.grad, rwg.grad[..., 0]))
+    for name, a, e in grads:
+        assert rel_err(a, e) < gtol, (name, rel_err(a, e))
+
+
+@pytest.mark.parametrize("corr", [0, 1, 2])
+def test_tanh_read_stage(cuda, corr):
+    """Stage 2 of the GN read with tanh features: h = tanh(rmsnorm(W1 q + c) - tau),
+    c = 0, num or num / (mass + eps), and resid = q + s W2 h, with every
+    gradient (fp32, float64 autograd)."""
+    from thetascan_amd._core.ops import gn
+
+    B, H, T, d, m = 2, 2, 75, 32, 64
+    q, _, w1, w2, wg = _case(B, H, T, d, m, True, 17 + corr, torch.float32)
+    gen = torch.Generator().manual_seed(6)
+    num = torch.randn(B, H, T, m, generator=gen, dtype=torch.float64)
+    mass = torch.rand(B, H, T, generator=gen, dtype=torch.float64) * 4 + 0.05
+    leaves = [t.clone().requires_grad_(True) for t in (q, w1, w2, wg, num, mass)]
+    rq, rw1, rw2, rwg, rnum, rmass = leaves
+    if corr == 2:
+        cc = rnum / (rmass.unsqueeze(-1) + 1e-6)
+    elif corr == 1:
+        cc = rnum
+    else:
+        cc = 0.0
+    a = torch.einsum("hmd,bhtd->bhtm", rw1, rq) + cc
+    pre = oracle_mixer.rmsnorm(a)[0] - rwg[..., 0].unsqueeze(0).unsqueeze(2)
+    h_ref = torch.tanh(pre)
+    resid_ref = rq + 0.5 * torch.einsum("hdm,bhtm->bhtd", rw2, h_ref)
+    dh = torch.randn(h_ref.shape, generator=gen, dtype=torch.float64)
+    dr = torch.randn(resid_ref.shape, generator=gen, dtype=torch.float64)
+    torch.autograd.backward([h_ref, resid_ref], [dh, dr])
+
+    dev = [t.to(cuda, torch.float32).requires_grad_(True) for t in (q, w1, w2, wg[..., 0].contiguous(), num, mass)]
+    q_, w1_, w2_, tau_, num_, mass_ = dev
+    h, resid = gn.read_stage(q_, w1_, w2_, tau_, num_ if corr else None, mass_ if corr == 2 else None, corr=corr,
+                             want_resid=True, s=0.5, nonlin="tanh")
+    torch.autograd.backward([h, resid], [dh.to(cuda, torch.float32), dr.to(cuda, torch.float32)])
+    assert rel_err(h, h_ref) < 1e-3 and rel_err(resid, resid_ref) < 1e-3
+    pairs = [("dq", q_.grad, rq.grad), ("dW1", w1_.grad, rw1.grad), ("dW2", w2_.grad, rw2.grad),
+             ("dtau", tau_.grad, rwg.grad[..., 0])]
+    if corr:
+        pairs.append(("dnum", num_.grad, rnum.grad))
+    if corr == 2:
+        pairs.append(("dmass", mass_.grad, rmass.grad))
+    for name, a, e in pairs:
+        assert rel_err(a, e) < 2e-3, (name, rel_err(a, e))
+
+
+def tanh_gn_module(cuda, d_model, heads, temporal="sum", dtype=torch.float32, seed=0):
+    """The ThetaScan-GN mixer with a tanh fast network and damping 1e-2 (core
+    config: the public one, like the reference's, has no tanh), and the
+    oracle's flat config of the same mixer."""
+    import thetascan_amd as ts
+    from thetascan_amd._core.modules.block import ThetaScan as CoreMixer
+
+    pub = json.loads(json.dumps(CASES["gn_reference_v0_1"]["config"]))
+    pub.update(d_model=d_model, n_heads=heads, memory_multiplier=2, share_key_query=False)
+    pub["runtime"].update(backend="hip", scan_chunk=64)
+    if temporal != "bank":
+        pub["temporal"].update(mode=temporal)
+    cfg = dataclasses.replace(ts.ThetaScanConfig.from_dict(pub)._to_core_config(), nonlin="tanh", gn_damping=DAMP)
+    torch.manual_seed(seed)
+    module = CoreMixer(cfg)
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            if name.startswith(("W1.", "W2.")):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+            elif name == "fade_eta":
+                p.copy_(torch.rand(p.shape, generator=g) - 0.5)
+    core = dict(oracle_mixer.core_config(pub), nonlin="tanh", gn_damping=DAMP)
+    return module.to(cuda, dtype), core
+
+
+@pytest.mark.parametrize("temporal", ["sum", "ema", "bank"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_tanh_gn_mixer_matches_oracle(cuda, temporal, dtype):
+    module, core = tanh_gn_module(cuda, 256, 4, temporal, dtype, seed=5)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 300, 256, generator=g, dtype=torch.float64).to(dtype).double()
+    dy = torch.randn(2, 300, 256, generator=g, dtype=torch.float64) * 0.1
+    params = {k: v.detach().double().cpu().clone().requires_grad_(True) for k, v in module.named_parameters()}
+    x64 = x.clone().requires_grad_(True)
+    y64 = oracle_mixer.forward(core, params, x64, backend="chunk")
+    (y64 * dy).sum().backward()
+    xd = x.to(cuda, dtype).requires_grad_(True)
+    y = module(xd)
+    (y.float() * dy.to(cuda, torch.float32)).sum().backward()
+    print(f"tanh gn mixer {temporal} {dtype}: path={module.last_path}", flush=True)
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
+    assert rel_err(y, y64) < tol
+    assert rel_err(xd.grad, x64.grad) < 2 * tol
+    for name, p in module.named_parameters():
+        if params[name].grad is not None and params[name].grad.abs().max() > 0:
+            assert rel_err(p.grad, params[name].grad) < 3 * tol, name

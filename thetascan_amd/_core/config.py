@@ -5,7 +5,9 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-NONLINS = ("relu2", "silu", "swiglu", "softmax_hidden")
+# tanh is an extension of this build (the reference's GN nonlinearities are
+# relu2, silu and swiglu): sigma' = 1 - tanh^2, signed features
+NONLINS = ("relu2", "silu", "swiglu", "softmax_hidden", "tanh")
 FADE_MODES = ("stale", "fast")
 FADE_BLEND_MODES = ("free", "tanh")
 ACCUMS = ("sum", "ema_gate")
@@ -81,6 +83,10 @@ class ThetaScanConfig:
     value_mlp_ortho: float = 0.0
     eps: float = 1e-6
     scan_chunk: int = 512
+    # Extension of this build: the damping of the GN Jacobi diagonal (and of
+    # the signed-mass read normalization of a tanh memory).  None keeps the
+    # reference's damping, eps (engine.py:255).
+    gn_damping: float | None = None
 
     def __post_init__(self):
         if self.head_dim is None:
@@ -187,13 +193,16 @@ class ThetaScanConfig:
             raise ValueError("rope_frac in (0,1]")
         if self.softmax_gain <= 0:
             raise ValueError("softmax_gain must be > 0")
+        if self.gn_damping is not None and not self.gn_damping > 0.0:
+            raise ValueError("gn_damping must be > 0")
         if self.read_norm:
             if self.rope != "none" and self.rope_placement == "feature":
                 raise ValueError("feature-space RoPE makes the read_norm denominator signed")
-            if self.write_rule == "gn" and self.nonlin != "relu2":
-                raise ValueError("GN read_norm requires nonlin='relu2'")
+            if self.write_rule == "gn" and self.nonlin not in ("relu2", "tanh"):
+                raise ValueError("GN read_norm requires nonlin='relu2' (or this build's signed-mass tanh)")
         elif self.read_norm_mode != "key_mass":
             raise ValueError("read_norm_mode is active only when read_norm=True")
         if self.read_norm_w1:
-            if not self.read_norm or self.write_rule != "gn" or not self.fast_w1 or self.nonlin != "relu2":
-                raise ValueError("read_norm_w1 requires read_norm, GN, fast W1 and relu2")
+            if (not self.read_norm or self.write_rule != "gn" or not self.fast_w1
+                    or self.nonlin not in ("relu2", "tanh")):
+                raise ValueError("read_norm_w1 requires read_norm, GN, fast W1 and relu2 (or tanh)")

@@ -56,7 +56,31 @@ def dsilu(pre, h=None):
     return s * (1 + pre * (1 - s))
 
 
-ELEMENTWISE = {"relu2": (relu2, drelu2), "silu": (F.silu, dsilu)}
+def dtanh(pre, h):
+    return 1.0 - h * h
+
+
+# sigma and sigma'(pre, h) of the GN hidden layer (nonlin.py:28-31; tanh has no
+# counterpart in the reference)
+ELEMENTWISE = {"relu2": (relu2, drelu2), "silu": (F.silu, dsilu), "tanh": (torch.tanh, dtanh)}
+
+
+def damping(cfg) -> float:
+    """The Jacobi diagonal's damping: the reference's is eps (engine.py:255)."""
+    return cfg.eps if cfg.gn_damping is None else float(cfg.gn_damping)
+
+
+def key_mass(cfg, view, qf, keys, mass):
+    """The mass a normalized read divides by, num / (mass + eps)
+    (engine.py:440-442, 503-506): the scan's unit column ``mass`` for the
+    reference's nonnegative features.  tanh features are signed, so their
+    products cancel and that column can cross zero; the mass is then the one
+    of the absolute features, sum_i w_i |qf| . |k_i| = |qf| . (the view's
+    decayed prefix of |k|) in fp32 [B,H,T], equal to the unit column for
+    nonnegative features, and |num| / mass <= max |value|."""
+    if cfg.nonlin != "tanh":
+        return mass
+    return (qf.abs().float() * view.mass_cum(keys.abs().float())).sum(-1)
 
 
 def hrot_stream(h, hrot):
@@ -173,7 +197,7 @@ def _lambda_solve(weights, cfg, ctxs, r):
             rowsq = _ein_w(W2 * W2, s2, "hdm,bhtm->bhtd")
         term = hh + xx * rowsq
         diag = term if diag is None else diag + term
-    return r / (diag / cfg.depth + cfg.eps)
+    return r / (diag / cfg.depth + damping(cfg))
 
 
 def write_streams(weights, cfg, k, v, hrot=None, softmax_gain=None, kernel_controls=None):
@@ -186,7 +210,8 @@ def write_streams(weights, cfg, k, v, hrot=None, softmax_gain=None, kernel_contr
     if gn.eligible(cfg, weights, k, v):
         W1, W2, Wg = weights[0]
         tau = Wg[..., 0] if cfg.learn_thresh else None
-        h, lam_hat, g = gn.write(k, v, W1, W2, tau, s=s, inv_depth=1.0 / cfg.depth, eps=cfg.eps)
+        h, lam_hat, g = gn.write(k, v, W1, W2, tau, s=s, inv_depth=1.0 / cfg.depth, eps=cfg.eps,
+                                 nonlin=cfg.nonlin, damping=damping(cfg))
         streams = Streams()
         streams.la1.append((k, g) if cfg.fast_w1 else None)
         streams.la2.append((hrot_stream(h, hrot), lam_hat))
@@ -270,7 +295,8 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
                 else:
                     pairs = [interface.scan_views_mass((view,), one.to(keys.dtype), keys, vals, "m")[0]
                              for view, one in zip(group, queries)]
-                mems = [_normalized(num, mass, cfg.eps, vals.dtype) for num, mass in pairs]
+                mems = [_normalized(num, key_mass(cfg, view, one, keys, mass), cfg.eps, vals.dtype)
+                        for view, one, (num, mass) in zip(group, queries, pairs)]
             else:
                 mems = []
                 for view, one in zip(group, queries):
@@ -294,8 +320,10 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
             if entry is None:
                 raise RuntimeError("read_norm_w1 requires an LA1 GN stream")
             h0, _ = gn.read_stage(x, W1, tau=tau, eps=cfg.eps)
-            pairs = interface.scan_views_mass(group, hrot_stream(h0, hrot).to(keys.dtype), keys, entry[1], "m")
-            stage = [(num, mass, gn.READ_NORMALIZED) for num, mass in pairs]
+            h0q = hrot_stream(h0, hrot).to(keys.dtype)
+            pairs = interface.scan_views_mass(group, h0q, keys, entry[1], "m")
+            stage = [(num, key_mass(cfg, view, h0q, keys, mass), gn.READ_NORMALIZED)
+                     for view, (num, mass) in zip(group, pairs)]
         elif entry is not None:
             corrs = interface.scan_views(group, x, entry[0], entry[1], "d")
             stage = [(corr[..., :m], None, gn.READ_PLAIN) for corr in corrs]
@@ -303,10 +331,12 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
             stage = [(None, None, gn.READ_NONE)] * len(group)
         outputs = []
         for view, (num1, mass1, corr) in zip(group, stage):
-            h, resid = gn.read_stage(x, W1, W2, tau, num1, mass1, corr=corr, want_resid=True, s=s, eps=cfg.eps)
+            h, resid = gn.read_stage(x, W1, W2, tau, num1, mass1, corr=corr, want_resid=True, s=s, eps=cfg.eps,
+                                     nonlin=cfg.nonlin)
             hq = hrot_stream(h, hrot).to(keys.dtype)
             if cfg.read_norm:
                 (num2, mass2), = interface.scan_views_mass((view,), hq, keys, vals, "m")
+                mass2 = key_mass(cfg, view, hq, keys, mass2)
             else:
                 num2, mass2 = interface.scan_views((view,), hq, keys, vals, "m")[0], None
             outputs.append(gn.normalized_read(num2, mass2, resid, s=s, eps=cfg.eps))
@@ -326,8 +356,10 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
             entry = streams.la1[l]
             if entry is None:
                 raise RuntimeError("read_norm_w1 requires an LA1 GN stream")
-            pairs = interface.scan_views_mass(group, h0q.to(feature_keys.dtype), feature_keys, entry[1], "m")
-            preacts = [a + _normalized(num, mass, cfg.eps, a.dtype)[..., :m] for num, mass in pairs]
+            h0q = h0q.to(feature_keys.dtype)
+            pairs = interface.scan_views_mass(group, h0q, feature_keys, entry[1], "m")
+            preacts = [a + _normalized(num, key_mass(cfg, view, h0q, feature_keys, mass), cfg.eps, a.dtype)[..., :m]
+                       for view, (num, mass) in zip(group, pairs)]
             bs = [b] * len(group)
         else:
             for it in range(n_iter):
@@ -350,7 +382,9 @@ def dual_read_views(weights, cfg, q, streams, views, hrot=None, softmax_gain=Non
                 resid = torch.add(x, base, alpha=s)
                 keys, vals = streams.la2[l]
                 if cfg.read_norm:
-                    pairs = interface.scan_views_mass(group, hq.to(keys.dtype), keys, vals, "m")
+                    hq = hq.to(keys.dtype)
+                    pairs = [(num, key_mass(cfg, view, hq, keys, mass))
+                             for view, (num, mass) in zip(group, interface.scan_views_mass(group, hq, keys, vals, "m"))]
                 else:
                     pairs = [(num, None) for num in interface.scan_views(group, hq, keys, vals, "m")]
                 return [gn.normalized_read(num, mass, resid, s=s, eps=cfg.eps) for num, mass in pairs]

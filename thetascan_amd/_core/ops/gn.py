@@ -18,6 +18,7 @@ from ... import _lib
 from .dispatch import HipOp
 
 GN_HEAD_DIMS = (16, 32, 64, 128)
+ACTS = {"relu2": _lib.GN_RELU2, "tanh": _lib.GN_TANH}  # hidden nonlinearities the kernels take
 
 
 def supported_width(m: int) -> bool:
@@ -26,7 +27,7 @@ def supported_width(m: int) -> bool:
 
 def eligible(cfg, weights, k: torch.Tensor, v: torch.Tensor) -> bool:
     """Whether the HIP GN write covers this configuration and these streams."""
-    if cfg.write_rule != "gn" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.nonlin != "relu2":
+    if cfg.write_rule != "gn" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.nonlin not in ACTS:
         return False
     if cfg.value_centers:
         return False
@@ -45,10 +46,10 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
-def _desc(x, m, has_tau, s, inv_depth, eps):
+def _desc(x, m, has_tau, s, inv_depth, eps, act, damping):
     B, H, T, d = x.shape
     return _lib.GnDesc(B, H, T, d, m, _lib.dtype_code(x.dtype), int(has_tau), float(s), float(inv_depth),
-                       float(eps))
+                       float(eps), int(act), float(damping))
 
 
 def contract_tokens(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -83,7 +84,7 @@ def contract_tokens(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def _gn_write_forward(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None,
-                 s: float, inv_depth: float, eps: float) -> list[torch.Tensor]:
+                 s: float, inv_depth: float, eps: float, act: int, damping: float) -> list[torch.Tensor]:
     lib = _lib.load()
     xk, vk = _rows(x), _rows(v)
     B, H, T, d = xk.shape
@@ -96,7 +97,7 @@ def _gn_write_forward(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: to
     h = torch.empty(B, H, T, m, dtype=dt, device=x.device)
     lam = torch.empty(B, H, T, d, dtype=dt, device=x.device)
     g = torch.empty(B, H, T, m, dtype=dt, device=x.device)
-    desc = _desc(xk, m, tc is not None, s, inv_depth, eps)
+    desc = _desc(xk, m, tc is not None, s, inv_depth, eps, act, damping)
     io = _lib.GnIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w2t.data_ptr(),
                    _lib.ptr(tc), _lib.strided(h), _lib.strided(lam), _lib.strided(g))
     with _lib.timed("ts_gn_write_fwd", lambda: _lib.nbytes(xk, vk, h, lam, g)):
@@ -105,7 +106,7 @@ def _gn_write_forward(x: torch.Tensor, v: torch.Tensor, w1: torch.Tensor, w2: to
     return [h, lam, g]
 
 
-def _gn_write_fake(x, v, w1, w2, tau, s, inv_depth, eps):
+def _gn_write_fake(x, v, w1, w2, tau, s, inv_depth, eps, act, damping):
     B, H, T, d = x.shape
     m = w1.shape[1]
     return [x.new_empty(B, H, T, m), x.new_empty(B, H, T, d), x.new_empty(B, H, T, m)]
@@ -113,7 +114,8 @@ def _gn_write_fake(x, v, w1, w2, tau, s, inv_depth, eps):
 
 def _gn_write_backward_impl(dh: torch.Tensor | None, dlam: torch.Tensor | None, dg: torch.Tensor | None, x: torch.Tensor,
                      v: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, tau: torch.Tensor | None, s: float,
-                     inv_depth: float, eps: float, need_tau: bool) -> list[torch.Tensor]:
+                     inv_depth: float, eps: float, act: int, damping: float, need_tau: bool
+                     ) -> list[torch.Tensor]:
     lib = _lib.load()
     xk, vk = _rows(x), _rows(v)
     B, H, T, d = xk.shape
@@ -136,7 +138,7 @@ def _gn_write_backward_impl(dh: torch.Tensor | None, dlam: torch.Tensor | None, 
     nsm = 5 if has_tau else 4
     tm = torch.empty(nsm, H, N, m, dtype=dt, device=xk.device)
     td = torch.empty(4, H, N, d, dtype=dt, device=xk.device)
-    desc = _desc(xk, m, has_tau, s, inv_depth, eps)
+    desc = _desc(xk, m, has_tau, s, inv_depth, eps, act, damping)
     io = _lib.GnBwdIO(_lib.strided(xk), _lib.strided(vk), w1c.data_ptr(), w2c.data_ptr(), w1t.data_ptr(),
                       w2t.data_ptr(), _lib.ptr(tc), _lib.strided(dh), _lib.strided(dlam), _lib.strided(dg),
                       _lib.strided(None), _lib.strided(dx), _lib.strided(dv), tm.data_ptr(), td.data_ptr())
@@ -153,14 +155,14 @@ def _gn_write_backward_impl(dh: torch.Tensor | None, dlam: torch.Tensor | None, 
     return [dx, dv, dw1.to(w1.dtype), dw2.to(w2.dtype), dtau]
 
 
-def _gn_write_backward_fake(dh, dlam, dg, x, v, w1, w2, tau, s, inv_depth, eps, need_tau):
+def _gn_write_backward_fake(dh, dlam, dg, x, v, w1, w2, tau, s, inv_depth, eps, act, damping, need_tau):
     dtau = x.new_empty(0) if (tau is None or not need_tau) else tau.new_empty(tau.shape)
     return [x.new_empty(x.shape), x.new_empty(x.shape), w1.new_empty(w1.shape), w2.new_empty(w2.shape), dtau]
 
 
 def _gn_write_setup(ctx, inputs, output):
-    x, v, w1, w2, tau, s, inv_depth, eps = inputs
-    ctx.args = (s, inv_depth, eps)
+    x, v, w1, w2, tau, s, inv_depth, eps, act, damping = inputs
+    ctx.args = (s, inv_depth, eps, act, damping)
     ctx.need_tau = tau is not None and tau.requires_grad
     ctx.save_for_backward(x, v, w1, w2, tau)
 
@@ -169,7 +171,7 @@ def _gn_write_backward(ctx, grads, bwd):
     x, v, w1, w2, tau = ctx.saved_tensors
     dh, dlam, dg = grads
     dx, dv, dw1, dw2, dtau = bwd(dh, dlam, dg, x, v, w1, w2, tau, *ctx.args, ctx.need_tau)
-    return dx, dv, dw1, dw2, (dtau if ctx.need_tau else None), None, None, None
+    return dx, dv, dw1, dw2, (dtau if ctx.need_tau else None), None, None, None, None, None
 
 
 _gn_write_op = HipOp("gn_write", forward=_gn_write_forward, forward_fake=_gn_write_fake,
@@ -177,10 +179,13 @@ _gn_write_op = HipOp("gn_write", forward=_gn_write_forward, forward_fake=_gn_wri
                      setup=_gn_write_setup, backward=_gn_write_backward)
 
 
-def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps: float = 1e-6):
+def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps: float = 1e-6,
+          nonlin: str = "relu2", damping: float | None = None):
     """GN write payloads ``(h, s*lam, g)`` of keys ``x`` and values ``v``
     ([B,H,T,d]) for per-head weights ``w1`` [H,m,d], ``w2`` [H,d,m] (a leading
-    1 broadcasts over heads) and an optional threshold ``tau`` [H,m]."""
+    1 broadcasts over heads) and an optional threshold ``tau`` [H,m].
+    ``nonlin`` is the hidden nonlinearity (relu2 or tanh); ``damping`` the
+    Jacobi diagonal's damping (None: ``eps``, as the reference)."""
     if not (x.is_cuda and v.is_cuda):
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
     H = x.shape[1]
@@ -190,7 +195,8 @@ def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps
         w2 = w2.expand(H, -1, -1)
     if tau is not None and tau.shape != (H, w1.shape[1]):
         tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
-    h, lam, g = _gn_write_op(x, v, w1, w2, tau, float(s), float(inv_depth), float(eps))
+    damp = float(eps if damping is None else damping)
+    h, lam, g = _gn_write_op(x, v, w1, w2, tau, float(s), float(inv_depth), float(eps), ACTS[nonlin], damp)
     return h, lam, g
 
 
@@ -199,15 +205,15 @@ def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps
 READ_NONE, READ_PLAIN, READ_NORMALIZED = 0, 1, 2
 
 
-def _read_desc(q, m, has_tau, corr, want_resid, s, eps):
+def _read_desc(q, m, has_tau, corr, want_resid, s, eps, act):
     B, H, T, d = q.shape
     return _lib.GnReadDesc(B, H, T, d, m, _lib.dtype_code(q.dtype), int(has_tau), int(corr), int(want_resid),
-                           float(s), float(eps))
+                           float(s), float(eps), int(act))
 
 
 def _gn_read_forward(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None, tau: torch.Tensor | None,
                 num: torch.Tensor | None, mass: torch.Tensor | None, corr: int, want_resid: bool, s: float,
-                eps: float) -> list[torch.Tensor]:
+                eps: float, act: int) -> list[torch.Tensor]:
     lib = _lib.load()
     qk = _rows(q)
     B, H, T, d = qk.shape
@@ -220,7 +226,7 @@ def _gn_read_forward(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None,
     mk = None if mass is None else mass.detach().to(torch.float32)
     h = torch.empty(B, H, T, m, dtype=dt, device=q.device)
     resid = torch.empty(B, H, T, d, dtype=dt, device=q.device) if want_resid else q.new_empty(0)
-    desc = _read_desc(qk, m, tc is not None, corr, want_resid, s, eps)
+    desc = _read_desc(qk, m, tc is not None, corr, want_resid, s, eps, act)
     io = _lib.GnReadIO(_lib.strided(qk), w1c.data_ptr(), _lib.ptr(w2c), _lib.ptr(tc), _lib.strided(nk),
                        _lib.strided(mk), _lib.strided(h), _lib.strided(resid if want_resid else None))
     with _lib.timed("ts_gn_read_fwd", lambda: _lib.nbytes(qk, nk, mk, h, resid)):
@@ -229,15 +235,15 @@ def _gn_read_forward(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor | None,
     return [h, resid]
 
 
-def _gn_read_fake(q, w1, w2, tau, num, mass, corr, want_resid, s, eps):
+def _gn_read_fake(q, w1, w2, tau, num, mass, corr, want_resid, s, eps, act):
     B, H, T, d = q.shape
     return [q.new_empty(B, H, T, w1.shape[1]), q.new_empty(B, H, T, d) if want_resid else q.new_empty(0)]
 
 
 def _gn_read_backward_impl(dh: torch.Tensor | None, dresid: torch.Tensor | None, q: torch.Tensor, w1: torch.Tensor,
                     w2: torch.Tensor | None, tau: torch.Tensor | None, num: torch.Tensor | None,
-                    mass: torch.Tensor | None, corr: int, want_resid: bool, s: float, eps: float, need_tau: bool
-                    ) -> list[torch.Tensor]:
+                    mass: torch.Tensor | None, corr: int, want_resid: bool, s: float, eps: float, act: int,
+                    need_tau: bool) -> list[torch.Tensor]:
     lib = _lib.load()
     qk = _rows(q)
     B, H, T, d = qk.shape
@@ -258,7 +264,7 @@ def _gn_read_backward_impl(dh: torch.Tensor | None, dresid: torch.Tensor | None,
     has_tau = tc is not None
     tm = torch.empty(3 if has_tau else 2, H, N, m, dtype=dt, device=qk.device)
     td = torch.empty(2, H, N, d, dtype=dt, device=qk.device)
-    desc = _read_desc(qk, m, has_tau, corr, want_resid, s, eps)
+    desc = _read_desc(qk, m, has_tau, corr, want_resid, s, eps, act)
     io = _lib.GnReadBwdIO(_lib.strided(qk), w1c.data_ptr(), w1t.data_ptr(), _lib.ptr(w2t), _lib.ptr(tc),
                           _lib.strided(nk), _lib.strided(mk), _lib.strided(dh), _lib.strided(dresid),
                           _lib.strided(dq), _lib.strided(dnum), _lib.ptr(dmass), tm.data_ptr(), td.data_ptr())
@@ -273,7 +279,7 @@ def _gn_read_backward_impl(dh: torch.Tensor | None, dresid: torch.Tensor | None,
     return [dq, dw1, dw2, dtau, dnum, dmass]
 
 
-def _gn_read_backward_fake(dh, dresid, q, w1, w2, tau, num, mass, corr, want_resid, s, eps, need_tau):
+def _gn_read_backward_fake(dh, dresid, q, w1, w2, tau, num, mass, corr, want_resid, s, eps, act, need_tau):
     return [q.new_empty(q.shape), w1.new_empty(w1.shape), w2.new_empty(w2.shape) if want_resid else q.new_empty(0),
             tau.new_empty(tau.shape) if (tau is not None and need_tau) else q.new_empty(0),
             num.new_empty(num.shape) if corr else q.new_empty(0),
@@ -281,20 +287,20 @@ def _gn_read_backward_fake(dh, dresid, q, w1, w2, tau, num, mass, corr, want_res
 
 
 def _gn_read_setup(ctx, inputs, output):
-    q, w1, w2, tau, num, mass, corr, want_resid, s, eps = inputs
-    ctx.args = (corr, want_resid, s, eps)
+    q, w1, w2, tau, num, mass, corr, want_resid, s, eps, act = inputs
+    ctx.args = (corr, want_resid, s, eps, act)
     ctx.need_tau = tau is not None and tau.requires_grad
     ctx.save_for_backward(q, w1, w2, tau, num, mass)
 
 
 def _gn_read_backward(ctx, grads, bwd):
     q, w1, w2, tau, num, mass = ctx.saved_tensors
-    corr, want_resid, s, eps = ctx.args
+    corr, want_resid, s, eps, act = ctx.args
     dh, dresid = grads
-    dq, dw1, dw2, dtau, dnum, dmass = bwd(dh, dresid if want_resid else None, q, w1, w2, tau, num,
-                                                      mass, corr, want_resid, s, eps, ctx.need_tau)
+    dq, dw1, dw2, dtau, dnum, dmass = bwd(dh, dresid if want_resid else None, q, w1, w2, tau, num, mass, corr,
+                                          want_resid, s, eps, act, ctx.need_tau)
     return (dq, dw1, dw2 if want_resid else None, dtau if ctx.need_tau else None,
-            dnum if corr else None, dmass if corr == READ_NORMALIZED else None, None, None, None, None)
+            dnum if corr else None, dmass if corr == READ_NORMALIZED else None, None, None, None, None, None)
 
 
 _gn_read_op = HipOp("gn_read", forward=_gn_read_forward, forward_fake=_gn_read_fake,
@@ -303,10 +309,10 @@ _gn_read_op = HipOp("gn_read", forward=_gn_read_forward, forward_fake=_gn_read_f
 
 
 def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = READ_NONE, want_resid: bool = False,
-               s: float = 1.0, eps: float = 1e-6):
-    """One GN read stage: ``h = relu2(rmsnorm(W1 q + c) - tau)`` with
-    ``c`` = 0, ``num`` or ``num / (mass + eps)`` and, with ``want_resid``,
-    ``resid = q + s W2 h``.  Returns ``(h, resid or None)``."""
+               s: float = 1.0, eps: float = 1e-6, nonlin: str = "relu2"):
+    """One GN read stage: ``h = sigma(rmsnorm(W1 q + c) - tau)`` (sigma relu2
+    or tanh) with ``c`` = 0, ``num`` or ``num / (mass + eps)`` and, with
+    ``want_resid``, ``resid = q + s W2 h``.  Returns ``(h, resid or None)``."""
     if not q.is_cuda:
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
     H = q.shape[1]
@@ -316,15 +322,16 @@ def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = REA
         w2 = w2.expand(H, -1, -1)
     if tau is not None and tau.shape != (H, w1.shape[1]):
         tau = tau.reshape(-1, w1.shape[1]).expand(H, -1)
-    h, resid = _gn_read_op(q, w1, w2, tau, num, mass, int(corr), bool(want_resid), float(s), float(eps))
+    h, resid = _gn_read_op(q, w1, w2, tau, num, mass, int(corr), bool(want_resid), float(s), float(eps),
+                           ACTS[nonlin])
     return h, (resid if want_resid else None)
 
 
-def _normalized_read_forward(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor, s: float, eps: float
-                        ) -> torch.Tensor:
+def _normalized_read_forward(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor, s: float,
+                             eps: float) -> torch.Tensor:
     """y = resid + s * num / (mass + eps)  (or + s * num without mass): the read
-    epilogue of engine.py:440-442, 538-544 on ts_read_fwd.  An fp32 numerator
-    (a difference of views) is read in fp32, then rounded once to the dtype of
+    epilogue of engine.py:440-442, 538-544 on ts_read_fwd.  An fp32 numerator (a
+    difference of views) is read in fp32, then rounded once to the dtype of
     ``resid``."""
     from . import fused
 
@@ -339,8 +346,8 @@ def _normalized_read_fake(num, mass, resid, s, eps):
     return resid.new_empty(num.shape)
 
 
-def _normalized_read_backward_impl(dy: torch.Tensor, num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor,
-                            s: float, eps: float) -> list[torch.Tensor]:
+def _normalized_read_backward_impl(dy: torch.Tensor, num: torch.Tensor, mass: torch.Tensor | None,
+                                   resid: torch.Tensor, s: float, eps: float) -> list[torch.Tensor]:
     from . import fused
 
     nk, rk = _rows(num), _rows(resid.to(num.dtype))
@@ -381,7 +388,7 @@ def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6):
 def read_eligible(cfg, weights, q: torch.Tensor) -> bool:
     """Whether the HIP GN read stages cover this configuration (depth-1
     ReLU^2 GN memories with one Jacobian step, no value anchors)."""
-    if cfg.write_rule != "gn" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.nonlin != "relu2":
+    if cfg.write_rule != "gn" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.nonlin not in ACTS:
         return False
     if cfg.value_centers or not q.is_cuda or q.dtype not in (torch.bfloat16, torch.float32):
         return False

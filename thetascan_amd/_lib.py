@@ -31,6 +31,9 @@ EXT_NONE = 0
 EXT_ONES = 1
 EXT_ARRAY = 2
 
+GN_RELU2 = 0
+GN_TANH = 1
+
 OUT_STORE = 0
 OUT_STORE_F32 = 1
 OUT_ACCUM_F32 = 2
@@ -257,6 +260,8 @@ class GnDesc(ctypes.Structure):
         ("s", ctypes.c_float),
         ("inv_depth", ctypes.c_float),
         ("eps", ctypes.c_float),
+        ("act", ctypes.c_int32),
+        ("damping", ctypes.c_float),
     ]
 
 
@@ -307,6 +312,7 @@ class GnReadDesc(ctypes.Structure):
         ("want_resid", ctypes.c_int32),
         ("s", ctypes.c_float),
         ("eps", ctypes.c_float),
+        ("act", ctypes.c_int32),
     ]
 
 
@@ -483,7 +489,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 9:
+        if lib.ts_abi_version() != 10:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

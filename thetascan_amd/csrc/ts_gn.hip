@@ -1,14 +1,17 @@
 // GN-family write payloads for gfx950: the damped Gauss-Newton fast-weight
-// update of a one-hidden-layer ReLU^2 memory (forward and backward).
+// update of a one-hidden-layer memory with a ReLU^2 or tanh hidden layer
+// (forward and backward).
 //
 // Per token x (key, [d]) and v (value, [d]), with per-head W1 [m, d],
 // W2 [d, m] and an optional per-feature threshold tau [m]
 // (engine.py:117-158, 180-195, 215-255; depth L, s = 1/sqrt(L)):
 //
 //   a = W1 x,   rinv = (mean(a^2) + eps)^-1/2,   pre = a rinv - tau
-//   h = relu(pre)^2,   sp = 2 relu(pre)                (relu2 and its slope)
+//   h = sigma(pre),   sp = sigma'(pre)    (relu2: relu(pre)^2, 2 relu(pre);
+//                                          tanh: tanh(pre), 1 - h^2)
 //   u = W2 h,   r = v - (x + s u)                       (residual of theta0)
-//   den = (|h|^2 + |x|^2 (W2 o W2)(sp rinv)^2) / L + eps   (Jacobi diagonal)
+//   den = (|h|^2 + |x|^2 (W2 o W2)(sp rinv)^2) / L + damping  (Jacobi diagonal;
+//         the reference's damping is eps)
 //   lam = r / den,   g = s sp (W2^T lam) rinv
 //
 // Outputs: h (the LA2 keys), s lam (LA2 values) and g (LA1 values).  The
@@ -30,8 +33,8 @@
 namespace ts {
 
 struct GnP {
-  int B, H, T, groups, has_tau;
-  float s, inv_L, eps, inv_m;
+  int B, H, T, groups, has_tau, act;
+  float s, inv_L, eps, inv_m, damp;
   Str x, v, h, lam, g;             // forward inputs / outputs
   Str dh, dlam, dg, dxin, dx, dv;  // backward
   const void* w1;                  // [H, m, d]
@@ -70,6 +73,27 @@ constexpr int kGnLdsMax = 160 * 1024;
 template <typename E, int D, int MB, bool FWD>
 constexpr bool gn_weights_in_lds() {
   return gn_layout((int)sizeof(E), D, MB * 16, FWD, true).end * (int)sizeof(E) <= kGnLdsMax;
+}
+
+// The hidden nonlinearity sigma and its slope sp = sigma'(pre), written as a
+// function of h = sigma(pre) (relu2: 2 sqrt(h) = 2 relu(pre); tanh: 1 - h^2).
+__device__ __forceinline__ float gn_act(int act, float pre) {
+  if (act == TS_GN_TANH) return tanhf(pre);
+  const float rp = fmaxf(pre, 0.f);
+  return rp * rp;
+}
+__device__ __forceinline__ float gn_slope(int act, float hval) {
+  return act == TS_GN_TANH ? 1.f - hval * hval : 2.f * sqrtf(hval);
+}
+// d pre of a term dh * h + dsp * sp: sigma'(pre) dh + sigma''(pre) dsp
+// (relu2: 2 relu(pre) dh + 2 dsp for pre > 0, else 0;
+//  tanh: (1 - h^2) dh - 2 h (1 - h^2) dsp).
+__device__ __forceinline__ float gn_dpre(int act, float pre, float hval, float dh, float dsp) {
+  if (act == TS_GN_TANH) {
+    const float d1 = 1.f - hval * hval;
+    return d1 * dh - 2.f * hval * d1 * dsp;
+  }
+  return pre > 0.f ? 2.f * fmaxf(pre, 0.f) * dh + 2.f * dsp : 0.f;
 }
 
 // Four consecutive elements of row t (zero past T).
@@ -160,11 +184,11 @@ __device__ __forceinline__ void gn_forward_token(const GnP& p, int b, int h, int
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float rp = fmaxf(k.a[fb][i] * k.rinv - tv[i], 0.f);
-      hv[fb][i] = rp * rp;
-      const float sv = 2.f * rp * k.rinv;
+      const float hval = gn_act(p.act, k.a[fb][i] * k.rinv - tv[i]);
+      hv[fb][i] = hval;
+      const float sv = gn_slope(p.act, hval) * k.rinv;
       s2v[fb][i] = sv * sv;
-      hh += hv[fb][i] * hv[fb][i];
+      hh += hval * hval;
     }
   }
   k.hh = sum_g(hh);
@@ -176,7 +200,7 @@ __device__ __forceinline__ void gn_forward_token(const GnP& p, int b, int h, int
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float r = k.vr[db][i] - k.xr[db][i] - p.s * u[db][i];
-      const float dn = (k.hh + k.xx * k.rq[db][i]) * p.inv_L + p.eps;
+      const float dn = (k.hh + k.xx * k.rq[db][i]) * p.inv_L + p.damp;
       k.den[db][i] = dn;
       k.lam[db][i] = r / dn;
     }
@@ -234,7 +258,7 @@ __global__ __launch_bounds__(256) void gn_write_fwd_kernel(GnP p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         hvv[i] = hv[fb][i];
-        const float sp = 2.f * sqrtf(hv[fb][i]);  // 2 relu(pre) = 2 sqrt(h)
+        const float sp = gn_slope(p.act, hv[fb][i]);
         gv[i] = p.s * sp * z[fb][i] * k.rinv;
       }
       st4_row<E>(p.h, b, h, t, fb * 16 + 4 * g, valid, hvv);
@@ -329,7 +353,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
         ld4_row<E>(p.dg, b, h, t, fb * 16 + 4 * g, valid, dgv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float sp = 2.f * sqrtf(hv[fb][i]);
+          const float sp = gn_slope(p.act, hv[fb][i]);
           const float sdg = p.s * dgv[i];
           dz[fb][i] = sdg * sp * k.rinv;
           dsp[fb][i] = sdg * z[fb][i] * k.rinv;
@@ -377,7 +401,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
       for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float sp = 2.f * sqrtf(hv[fb][i]);
+          const float sp = gn_slope(p.act, hv[fb][i]);
           const float dsv = 2.f * sp * k.rinv * ds2[fb][i];
           dsp[fb][i] += dsv * k.rinv;
           drinv += dsv * sp;
@@ -415,9 +439,8 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float pre = k.a[fb][i] * k.rinv - tv[i];
-          const float rp = fmaxf(pre, 0.f);
           const float dht = dhv[i] + dhu[fb][i] + 2.f * hv[fb][i] * dhh;
-          const float dpre = (valid && pre > 0.f) ? 2.f * rp * dht + 2.f * dsp[fb][i] : 0.f;
+          const float dpre = valid ? gn_dpre(p.act, pre, hv[fb][i], dht, dsp[fb][i]) : 0.f;
           dpv[i] = dpre;
           da[fb][i] = dpre;  // completed below once drinv is known
           ra += dpre * k.a[fb][i];
@@ -451,7 +474,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
 //
 // One stage of the GN read (engine.py:467-506): per query q,
 //   a = W1 q + c,  c = 0 | num | num / (mass + eps)   (corr = 0 | 1 | 2)
-//   pre = a rsqrt(mean a^2 + eps) - tau,  h = relu(pre)^2
+//   pre = a rsqrt(mean a^2 + eps) - tau,  h = sigma(pre) (relu2 or tanh)
 //   resid = q + s W2 h                                  (want_resid)
 // Stage 1 of the normalized two-stage read is corr = 0 without resid (its h
 // are the queries of the feature-mass scan); stage 2 adds the normalized
@@ -460,7 +483,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
 // gradients of num and mass, and head-major tiles for dW1 = da^T q,
 // dW2 = (s dresid)^T h and dtau = -sum dpre.
 struct GnReadP {
-  int B, H, T, groups, has_tau, corr, want_resid;
+  int B, H, T, groups, has_tau, corr, want_resid, act;
   float s, eps, inv_m;
   Str q, num, h, resid, dh, dresid, dq, dnum;
   const float* mass;  // fp32 [B,H,T] with element strides msb, msh, mst
@@ -555,8 +578,7 @@ __global__ __launch_bounds__(256) void gn_read_fwd_kernel(GnReadP p) {
       tau_of<MB>(tau, fb, g, p.has_tau, tv);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float rp = fmaxf(a[fb][i] * rinv - tv[i], 0.f);
-        hv[fb][i] = rp * rp;
+        hv[fb][i] = gn_act(p.act, a[fb][i] * rinv - tv[i]);
         o[i] = hv[fb][i];
       }
       st4_row<E>(p.h, b, h, t, fb * 16 + 4 * g, valid, o);
@@ -660,9 +682,8 @@ __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float pre = a[fb][i] * rinv - tv[i];
-        const float rp = fmaxf(pre, 0.f);
-        hvv[i] = rp * rp;
-        const float dpre = (valid && pre > 0.f) ? 2.f * rp * (dhv[i] + p.s * dhr[fb][i]) : 0.f;
+        hvv[i] = gn_act(p.act, pre);
+        const float dpre = valid ? gn_dpre(p.act, pre, hvv[i], dhv[i] + p.s * dhr[fb][i], 0.f) : 0.f;
         dpv[i] = dpre;
         da[fb][i] = dpre;
         ra += dpre * a[fb][i];
@@ -719,6 +740,8 @@ int check_gn(const ts_gn_desc* d) {
   if (d->m < 16 || d->m % 16 || (d->m > 128 && d->m != 256))
     return fail(TS_ERR_NOT_IMPLEMENTED, "gn: hidden width %d (a multiple of 16 up to 128, or 256)", d->m);
   if (d->H > 65535 || d->B > 65535) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: grid too large");
+  if (d->act != TS_GN_RELU2 && d->act != TS_GN_TANH) return fail(TS_ERR_VALUE, "gn: unknown nonlinearity %d", d->act);
+  if (!(d->damping > 0.f)) return fail(TS_ERR_VALUE, "gn: damping must be > 0");
   return TS_OK;
 }
 
@@ -782,7 +805,7 @@ void gn_fill(const ts_gn_desc* d, ts::GnP& p) {
   p.B = d->B; p.H = d->H; p.T = d->T;
   p.groups = gn_groups(d);
   p.has_tau = d->has_tau;
-  p.s = d->s; p.inv_L = d->inv_depth; p.eps = d->eps;
+  p.s = d->s; p.inv_L = d->inv_depth; p.eps = d->eps; p.act = d->act; p.damp = d->damping;
   p.inv_m = 1.0f / (float)d->m;
 }
 
@@ -841,7 +864,8 @@ int check_gn_read(const ts_gn_read_desc* r, ts_gn_desc* d) {
   if (r->corr < 0 || r->corr > 2) return fail(TS_ERR_VALUE, "gn read: corr must be 0, 1 or 2");
   memset(d, 0, sizeof(*d));
   d->B = r->B; d->H = r->H; d->T = r->T; d->d = r->d; d->m = r->m; d->dtype = r->dtype; d->has_tau = r->has_tau;
-  d->s = r->s; d->inv_depth = 1.f; d->eps = r->eps;
+  d->s = r->s; d->inv_depth = 1.f; d->eps = r->eps; d->act = r->act;
+  d->damping = 1.f;  // the read stage has no Jacobi diagonal
   return check_gn(d);
 }
 
@@ -850,7 +874,7 @@ void gn_read_fill(const ts_gn_read_desc* r, const ts_gn_desc* d, ts::GnReadP& p,
   p.B = r->B; p.H = r->H; p.T = r->T;
   p.groups = gn_groups(d);
   p.has_tau = r->has_tau; p.corr = r->corr; p.want_resid = r->want_resid;
-  p.s = r->s; p.eps = r->eps; p.inv_m = 1.0f / (float)r->m;
+  p.s = r->s; p.eps = r->eps; p.inv_m = 1.0f / (float)r->m; p.act = r->act;
   p.mass = (const float*)mass.ptr;
   p.msb = mass.sb; p.msh = mass.sh; p.mst = mass.st;
 }

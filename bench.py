@@ -288,17 +288,22 @@ def cpu_baseline(budget_s: float = 12.0):
 #   gn            damped Gauss-Newton memory, fast net 64 -> 128 -> 64 with tanh
 #                 and damping 1e-2 (this build's extension of the core config:
 #                 the public config, like the reference's, offers relu2/silu),
-#                 two-stage read normalization (signed mass), B8 T2048 H8 d64,
-#                 slow reference weights W1, W2 ~ N(0, 0.02), bf16, fwd+bwd;
-#   bspline_bank  kernel memory with the cubic B-spline map (8 basis functions,
-#                 m = 128), key-mass read, two-rate recency bank (fast blend,
-#                 retentions 0.9 / 0.999), B2 T32768 H8 d64, 128-token tiles,
-#                 bf16, forward only.
+#                 two-stage read normalization (tanh features: the mass of the
+#                 absolute features), B8 T2048 H8 d64, slow reference weights
+#                 W1, W2 ~ N(0, 0.02), bf16, fwd+bwd;
+#   bspline_bank  kernel memory with the cubic B-spline map (8 basis functions)
+#                 expanded 2x on its projection rows by fixed key-derived sign
+#                 maps (8 trainable projections -> 16 -> m = 128 features),
+#                 key-mass read, a bank of four recency rates {0.9, 0.99,
+#                 0.999, 0.9999} (fast blend), B2 T32768 H8 d64, bf16, forward
+#                 only (both extensions of the core config: the public config,
+#                 like the reference's, stops at two rates and expands only
+#                 the ReLU^2 map).
 OTHER = {
     "gn": dict(B=8, T=2048, train=True,
                metric="GN mixer tokens/s fwd+bwd (B8 T2048 H8 d64 m128 tanh, damping 1e-2, bf16)"),
     "bspline_bank": dict(B=2, T=32768, train=False,
-                         metric="B-spline bank mixer tokens/s fwd (B2 T32768 H8 d64 m128 bf16)"),
+                         metric="B-spline 4-rate bank mixer tokens/s fwd (B2 T32768 H8 d64 m128 2x expanded, bf16)"),
 }
 
 
@@ -315,12 +320,14 @@ def other_config(name: str):
             temporal=ts.TemporalConfig(mode="sum"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64),
         )
         return dataclasses.replace(public._to_core_config(), nonlin="tanh", gn_damping=1e-2)
-    return ts.ThetaScanConfig(
+    public = ts.ThetaScanConfig(
         d_model=D_MODEL, n_heads=H, memory_multiplier=2, family="kernel",
         kernel=ts.KernelConfig(feature_map="projected_bspline", read_normalization="key_mass"),
         temporal=ts.TemporalConfig(mode="bank", bank_mode="fast", recency_branches=2, retention_inits=(0.9, 0.999)),
         runtime=ts.RuntimeConfig(backend="hip", scan_chunk=128),
-    )._to_core_config()
+    )
+    return dataclasses.replace(public._to_core_config(), feature_expansion=2, fade_branches=4,
+                               fade_alpha_inits=(0.9, 0.99, 0.999, 0.9999))
 
 
 def run_other(name: str, args) -> dict:

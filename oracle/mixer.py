@@ -505,7 +505,11 @@ def effective_weights(c, params):
         if c["feature_expansion"] > 1:
             m = c["mem_hidden"]
             b = m // c["feature_expansion"]
-            E1 = expansion.row_map((1, m, b), c["expansion_key"], f"w1-expand-layer-{l}").to(W1.dtype)
+            # W1's rows are features, or the projections of a B-spline map
+            # (hidden / basis count, block.py:214-222); expanding the latter is
+            # an extension of this build
+            nb = c["bspline_basis_count"] if c["kernel_kind"] == "projected_bspline" else 1
+            E1 = expansion.row_map((1, m // nb, b // nb), c["expansion_key"], f"w1-expand-layer-{l}").to(W1.dtype)
             E2 = expansion.row_map((1, b, m), c["expansion_key"], f"w2-expand-layer-{l}").to(W2.dtype)
             W1 = torch.matmul(E1, W1)
             W2 = torch.matmul(W2, E2)

@@ -23,6 +23,9 @@ KERNEL_SPARSITY_MODES = ("none", "relative_soft", "relative_st", "relative_st_bl
 KERNEL_RELU2_THRESHOLD_MODES = ("none", "learned_per_head")
 READ_NORM_MODES = ("key_mass", "feature_mass")
 BSPLINE_SCALE_MODES = ("fixed", "learned_per_head")
+# recency branches of a bank: the reference allows 1 or 2; this build's core
+# config up to 6 (a stale bank blends J + 2 views, the blend kernel up to 8)
+MAX_FADE_BRANCHES = 6
 
 
 @dataclass
@@ -83,9 +86,8 @@ class ThetaScanConfig:
     value_mlp_ortho: float = 0.0
     eps: float = 1e-6
     scan_chunk: int = 512
-    # Extension of this build: the damping of the GN Jacobi diagonal (and of
-    # the signed-mass read normalization of a tanh memory).  None keeps the
-    # reference's damping, eps (engine.py:255).
+    # Extension of this build: the damping of the GN Jacobi diagonal.  None
+    # keeps the reference's damping, eps (engine.py:255).
     gn_damping: float | None = None
 
     def __post_init__(self):
@@ -162,8 +164,8 @@ class ThetaScanConfig:
             one_of(self.fade_blend_mode, FADE_BLEND_MODES, "fade_blend_mode")
             if self.accumulation != "sum":
                 raise ValueError("read_fade requires accumulation='sum'")
-            if self.fade_branches not in (1, 2):
-                raise ValueError("fade_branches must be 1 or 2")
+            if type(self.fade_branches) is not int or not 1 <= self.fade_branches <= MAX_FADE_BRANCHES:
+                raise ValueError(f"fade_branches must be between 1 and {MAX_FADE_BRANCHES}")
             alphas = self.resolved_fade_alphas
             if len(alphas) != self.fade_branches:
                 raise ValueError("fade_alpha_inits must contain exactly fade_branches values")
@@ -171,6 +173,8 @@ class ThetaScanConfig:
                 raise ValueError("all fade alpha initializers must be in (0, 1)")
             if self.fade_branches == 2 and alphas[0] == alphas[1]:
                 raise ValueError("two fade branches require distinct initial timescales")
+            if len(set(alphas)) != len(alphas):
+                raise ValueError("fade branches require distinct initial timescales")
         if type(self.feature_expansion) is not int or self.feature_expansion < 1:
             raise ValueError("feature_expansion must be an integer >= 1")
         if self.feature_expansion > 1:
@@ -178,8 +182,13 @@ class ThetaScanConfig:
                 raise ValueError("feature_expansion must divide the effective memory width")
             if self.nonlin != "relu2":
                 raise ValueError("feature_expansion requires nonlin='relu2'")
-            if self.write_rule == "kernel" and self.kernel_kind != "relu2_ridge":
-                raise ValueError("kernel feature_expansion requires kernel_kind='relu2_ridge'")
+            if self.write_rule == "kernel" and self.kernel_kind not in ("relu2_ridge", "projected_bspline"):
+                raise ValueError("kernel feature_expansion requires kernel_kind='relu2_ridge' "
+                                 "(or this build's projected_bspline, expanded on projection rows)")
+            if (self.write_rule == "kernel" and self.kernel_kind == "projected_bspline"
+                    and (self.mem_hidden // self.feature_expansion) % self.bspline_basis_count):
+                raise ValueError("projected_bspline feature_expansion requires mem_hidden / feature_expansion "
+                                 "divisible by bspline_basis_count")
         if self.key_value_heads is not None:
             if not 1 <= self.key_value_heads <= self.n_heads or self.n_heads % self.key_value_heads:
                 raise ValueError("key_value_heads must divide n_heads")

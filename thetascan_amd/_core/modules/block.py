@@ -76,17 +76,23 @@ def _fixed_row_map(shape, *, key: str, role: str, row_norm: float = 1.0, center_
     return matrix * (float(row_norm) / matrix.norm(dim=-1, keepdim=True))
 
 
-def _expansion_fingerprint(*, key: str, effective_hidden: int, feature_expansion: int, depth: int):
-    """``TSXF || u32 schema || sha256`` identity of the expansion maps (block.py:77-114)."""
+def _expansion_fingerprint(*, key: str, effective_hidden: int, feature_expansion: int, depth: int,
+                           w1_rows: tuple | None = None):
+    """``TSXF || u32 schema || sha256`` identity of the expansion maps (block.py:77-114).
+
+    ``w1_rows`` = (effective, base) rows of the W1 map when they differ from
+    the hidden widths: a projected B-spline memory expands its projection rows
+    (hidden / basis count), an extension of this build."""
     if feature_expansion <= 1:
         raise ValueError("an expansion fingerprint requires feature_expansion > 1")
     base_hidden = effective_hidden // feature_expansion
+    rows_eff, rows_base = w1_rows if w1_rows is not None else (effective_hidden, base_hidden)
     digest = hashlib.sha256()
     digest.update(b"thetascan-expansion-checkpoint\0")
     digest.update(_EXPANSION_MAP_DOMAIN.encode("ascii"))
     for layer in range(depth):
         for desc in (
-            _sign_domain((1, effective_hidden, base_hidden), key=key, role=f"w1-expand-layer-{layer}"),
+            _sign_domain((1, rows_eff, rows_base), key=key, role=f"w1-expand-layer-{layer}"),
             _sign_domain((1, base_hidden, effective_hidden), key=key, role=f"w2-expand-layer-{layer}"),
         ):
             digest.update(len(desc).to_bytes(8, "big"))
@@ -150,7 +156,13 @@ class ThetaScan(nn.Module):
             return nn.Parameter(torch.randn(*shape) / math.sqrt(fan))
 
         width = m // cfg.feature_expansion
-        proj_rows = width // cfg.bspline_basis_count if cfg.kernel_kind == "projected_bspline" else width
+        bspline = cfg.kernel_kind == "projected_bspline"
+        # W1 rows: one per feature, or one per projection of a B-spline map
+        # (hidden / basis count, block.py:214-222); an expansion widens these
+        # rows by feature_expansion (for the B-spline map an extension of this
+        # build: 8 trainable projections -> 16 -> 16 x 8 basis = 128 features)
+        proj_rows = width // cfg.bspline_basis_count if bspline else width
+        rows_eff = m // cfg.bspline_basis_count if bspline else m
         self.W1 = nn.ParameterList([w(H, proj_rows, d, fan=d) for _ in range(L)])
         self.W2 = nn.ParameterList([nn.Parameter(torch.zeros(H, d, width)) for _ in range(L)])
         if cfg.nonlin == "swiglu":
@@ -169,7 +181,7 @@ class ThetaScan(nn.Module):
             w1_names, w2_names = [], []
             for layer in range(L):
                 w1_name, w2_name = f"_expand_w1_{layer}", f"_expand_w2_{layer}"
-                self.register_buffer(w1_name, _fixed_row_map((1, m, width), key=cfg.expansion_key,
+                self.register_buffer(w1_name, _fixed_row_map((1, rows_eff, proj_rows), key=cfg.expansion_key,
                                                              role=f"w1-expand-layer-{layer}", center_rows=False),
                                      persistent=False)
                 self.register_buffer(w2_name, _fixed_row_map((1, width, m), key=cfg.expansion_key,
@@ -180,7 +192,8 @@ class ThetaScan(nn.Module):
             self._w1_expansion_buffer_names = tuple(w1_names)
             self._w2_expansion_buffer_names = tuple(w2_names)
             self._expansion_fingerprint = _expansion_fingerprint(
-                key=cfg.expansion_key, effective_hidden=m, feature_expansion=cfg.feature_expansion, depth=L)
+                key=cfg.expansion_key, effective_hidden=m, feature_expansion=cfg.feature_expansion, depth=L,
+                w1_rows=(rows_eff, proj_rows))
 
         self.decay = DecayGate(D, H) if cfg.decay_gate != "off" else None
         self.vmlp_in = self.vmlp_out = None

@@ -465,14 +465,35 @@ def _retention_grad(kind: int, retention: torch.Tensor, dL: torch.Tensor) -> tor
 
 # ------------------------------------------------------------------ autograd
 
+def _view_groups(n: int) -> list[range]:
+    """Consecutive groups of at most MAX_VIEWS retentions, as even as possible
+    (5 -> 3 + 2): one multi-view pass each."""
+    count = -(-n // _lib.MAX_VIEWS)
+    bounds = [n * i // count for i in range(count + 1)]
+    return [range(a, b) for a, b in zip(bounds, bounds[1:])]
+
+
 def _views_forward(q, k, v, with_mass: bool, retentions):
     """Forward scans of every retention -> (outs, masses)."""
     kinds = [_classify(r, q) for r in retentions]
-    if views_eligible(q, v, kinds):
-        # one pass for every retention: the score tile is formed once
-        outs, masses = scan_views_launch(q, k, v, [r if kd == _lib.RET_STATIC else None
-                                                   for kd, r in zip(kinds, retentions)], mass=with_mass)
-        return list(outs), list(masses or [])
+    if len(kinds) >= 2 and views_eligible(q, v, kinds[:2]) and all(
+            kd in (_lib.RET_NONE, _lib.RET_STATIC) for kd in kinds):
+        # one pass per group of retentions: the score tile is formed once per
+        # group (a bank of four rates and the plain sum: two passes)
+        outs, masses = [], []
+        for group in _view_groups(len(kinds)):
+            if len(group) == 1:
+                j = group[0]
+                out, mass, _ = scan_launch(q, k, v, **_ret_kwargs(kinds[j], retentions[j]),
+                                           v_ext="ones" if with_mass else None, want_ext_out=with_mass)
+                outs.append(out)
+                masses.extend([mass] if with_mass else [])
+                continue
+            g_outs, g_masses = scan_views_launch(q, k, v, [retentions[j] if kinds[j] == _lib.RET_STATIC else None
+                                                           for j in group], mass=with_mass)
+            outs.extend(g_outs)
+            masses.extend(g_masses or [])
+        return outs, masses
     outs, masses = [], []
     for kind, r in zip(kinds, retentions):
         out, mass, _ = scan_launch(q, k, v, **_ret_kwargs(kind, r), v_ext="ones" if with_mass else None,

@@ -23,7 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
-from ..ops import engine, fused, maps, prologue
+from ..ops import engine, features, fused, gn, interface, maps, prologue
 from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
@@ -219,7 +219,8 @@ class ThetaScan(nn.Module):
         # The fused path depends only on the (immutable) configuration and on
         # which optional parameters exist, so both are settled here and
         # forward() reads them without writing module state.
-        self._fused_cfg = self._config_fused_eligible()
+        self._views_cfg = self._config_views_eligible()
+        self._fused_cfg = self._views_cfg and self._config_fused_eligible()
         self._spec = self._make_feature_spec()
         self.last_path = None
 
@@ -355,16 +356,22 @@ class ThetaScan(nn.Module):
     # ------------------------------------------------------------ forward
 
     def fused_eligible(self, x: torch.Tensor) -> bool:
-        """Whether the three-kernel hot path covers this configuration and input."""
+        """Whether the HIP feature kernels carry this configuration and input
+        (the one-call sum path or the multi-view path)."""
         if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
             return False
-        return self._fused_cfg
+        return self._views_cfg
 
-    def _config_fused_eligible(self) -> bool:
+    def _config_views_eligible(self) -> bool:
+        """The kernel memory that ts_feature_fwd / ts_feature_bwd compute: depth
+        1, one write, L2-normed keys and queries, the ReLU^2 ridge (with or
+        without the per-head threshold) or the fixed-gain dense softmax
+        partition, widths the kernels take, and a plain or key-mass read;
+        any projection layout, value MLP and temporal mode."""
         cfg = self.cfg
-        if cfg.write_rule != "kernel" or cfg.depth != 1 or cfg.value_centers or cfg.value_mlp_mult > 0:
+        if cfg.write_rule != "kernel" or cfg.depth != 1 or cfg.write_iters != 1 or cfg.value_centers:
             return False
-        if cfg.read_fade or cfg.accumulation != "sum" or cfg.share_kq or cfg.key_value_heads is not None:
+        if not cfg.qk_norm:
             return False
         if cfg.read_norm and cfg.read_norm_mode != "key_mass":
             return False
@@ -380,6 +387,14 @@ class ThetaScan(nn.Module):
             return (cfg.softmax_gain_mode == "fixed" and cfg.kernel_sparsity == "none"
                     and self.kernel_score_bias is None)
         return False
+
+    def _config_fused_eligible(self) -> bool:
+        """The one-call sum path (ts_memory_fwd / ts_memory_bwd between the
+        stacked projection and the output projection): a views-eligible memory
+        with the plain sum and the stacked qkv projection."""
+        cfg = self.cfg
+        return not (cfg.read_fade or cfg.accumulation != "sum" or cfg.share_kq or cfg.key_value_heads is not None
+                    or cfg.value_mlp_mult > 0)
 
     def _make_feature_spec(self):
         cfg = self.cfg
@@ -411,7 +426,7 @@ class ThetaScan(nn.Module):
             # a record for eager callers; a traced forward writes no module state
             self.last_path = "fused" if fused_path else "composed"
         if fused_path:
-            return self._forward_fused(x)
+            return self._forward_fused(x) if self._fused_cfg else self._forward_views(x, backend)
         return self._forward_composed(x, backend)
 
     def _project(self, x):
@@ -461,15 +476,27 @@ class ThetaScan(nn.Module):
             if rot:
                 hcos, hsin = rope_cache(T, rot, cfg.rope_base, x.device, x.dtype)
                 hrot = (hcos, hsin, rot)
-        decay_d = decay_m = None
-        if self.decay is not None:
-            decay_d, decay_m = self.decay(x)
-        acc = Accumulator(backend, decay_d=decay_d, decay_m=decay_m, eps=cfg.eps, chunk=cfg.scan_chunk)
+        views, etas = self._temporal_views(x, backend)
         weights = self._weights()
         sharp = self.kernel_sharpness()
         controls = self.kernel_controls()
         streams, _, _ = engine.write_streams(weights, cfg, k, v_w, hrot=hrot, softmax_gain=sharp,
                                              kernel_controls=controls)
+        reads = engine.dual_read_views(weights, cfg, q, streams, tuple(views), hrot=hrot, softmax_gain=sharp,
+                                       kernel_controls=controls)
+        return self._blend_and_project(x, reads, etas)
+
+    def _temporal_views(self, x: torch.Tensor, backend: str):
+        """The memory's temporal views (interface.py:198-327): the accumulator
+        (plain sum or the ema stream) and, for a bank, one fast or stale view
+        per recency branch (block.py:647-681), with the branches' blends."""
+        cfg = self.cfg
+        B, T, _ = x.shape
+        H = cfg.n_heads
+        decay_d = decay_m = None
+        if self.decay is not None:
+            decay_d, decay_m = self.decay(x)
+        acc = Accumulator(backend, decay_d=decay_d, decay_m=decay_m, eps=cfg.eps, chunk=cfg.scan_chunk)
         views = [acc]
         etas = []
         if cfg.read_fade:
@@ -489,8 +516,12 @@ class ThetaScan(nn.Module):
                 etas.append(eta[branch].view(1, -1, 1, 1))
             if cfg.read_fade_mode == "stale":
                 views.append(NullAccumulator())
-        reads = engine.dual_read_views(weights, cfg, q, streams, tuple(views), hrot=hrot, softmax_gain=sharp,
-                                       kernel_controls=controls)
+        return views, etas
+
+    def _blend_and_project(self, x: torch.Tensor, reads, etas) -> torch.Tensor:
+        """Bank blend (block.py:683-717), output gate and projection (block.py:721-724)."""
+        cfg = self.cfg
+        B, T, _ = x.shape
         y = reads[0]
         if cfg.read_fade:
             if cfg.read_fade_mode == "fast":
@@ -499,5 +530,30 @@ class ThetaScan(nn.Module):
                 y = maps.bank_blend(reads, maps.stale_coefficients(etas))
         if self.ogate is not None:
             y = y * self.ogate(x)
-        y = y.transpose(1, 2).reshape(B, T, H * d)
+        y = y.transpose(1, 2).reshape(B, T, cfg.n_heads * cfg.head_dim)
         return linear(y, self.proj_out.weight)
+
+    def _forward_views(self, x: torch.Tensor, backend: str = "hip") -> torch.Tensor:
+        """The kernel memory on the HIP feature kernels for any projection
+        layout and temporal mode: the raw key and query streams go through
+        ts_feature_fwd (input RoPE, L2 norm, W1, RMSNorm, threshold, feature
+        map, feature RoPE, and the query's residual xn + s W2 h), every view
+        is scanned by the multi-view scan and read by ts_read_fwd
+        (engine.py:345-544 for depth 1, write_iters 1)."""
+        cfg = self.cfg
+        q, k, v = self._project(x)
+        v_w = v
+        if self.vmlp_in is not None:
+            v_w = v_w + self.vmlp_out(F.silu(self.vmlp_in(v_w)))
+        (W1, W2, _), = self._weights()
+        tau = self.kernel_relu2_threshold
+        phi_k, _ = features.kernel_features(k, W1, None, tau, self._spec, False)
+        phi_q, resid = features.kernel_features(q, W1, W2, tau, self._spec, True)
+        views, etas = self._temporal_views(x, backend)
+        s = 1.0 / math.sqrt(cfg.depth)
+        if cfg.read_norm:
+            pairs = interface.scan_views_mass(tuple(views), phi_q, phi_k, v_w, "m")
+        else:
+            pairs = [(num, None) for num in interface.scan_views(tuple(views), phi_q, phi_k, v_w, "m")]
+        reads = [gn.normalized_read(num, mass, resid, s=s, eps=cfg.eps) for num, mass in pairs]
+        return self._blend_and_project(x, reads, etas)

@@ -1,0 +1,113 @@
+"""Streaming continuation: one causal sequence fed to the mixer in pieces,
+each call starting from the state the previous one returned (GPU tests).
+
+For every family, temporal view, read normalization, RoPE placement and
+expansion setting of the golden reference cases (and the benchmark layout):
+the concatenated outputs of pieces of 1, 63, 64 and 65 tokens, empty pieces
+and one-token decode steps match the float64 oracle of the whole sequence as
+closely as the full-sequence forward does (fp32, rel 1e-4; they differ from it
+only in the scans' tilings).  The state's size does not grow with T,
+survives a save/load round trip, and is refused by another configuration,
+batch size or an autograd-recording call.
+"""
+from __future__ import annotations
+
+import io
+import json
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import mixer as oracle_mixer
+from tests.conftest import rel_err
+from tests.test_mixer_gpu import _headline_config, _seeded, build_module
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+CASES = json.loads((GOLDEN / "mixer_cases.json").read_text())
+CUTS = [0, 1, 64, 64, 129, 130, 193, 194, 195, 200]
+
+
+def _module(name, cuda):
+    if name.startswith("headline"):
+        placement, norm = ("feature", "none") if name == "headline_2a" else ("input", "key_mass")
+        pub = _headline_config(placement, norm, d_model=256, heads=4)
+    else:
+        pub = json.loads(json.dumps(CASES[name]["config"]))
+    module = build_module(pub, cuda)
+    _seeded(module, 3, w2_std=0.2)
+    g = torch.Generator().manual_seed(4)
+    with torch.no_grad():
+        for pname, p in module._core.named_parameters():
+            if pname in ("fade_eta", "kernel_relu2_threshold") or pname.startswith("W2."):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.3)
+    return module, pub
+
+
+def _oracle(module, pub, x):
+    params = {k: v.detach().double().cpu() for k, v in module._core.named_parameters()}
+    return oracle_mixer.forward(oracle_mixer.core_config(pub), params, x.double().cpu(), backend="chunk")
+
+
+@pytest.mark.parametrize("name", ["headline_2a", "headline_2b"] + sorted(CASES))
+def test_pieces_continue_the_whole_sequence(cuda, name):
+    module, pub = _module(name, cuda)
+    D = pub["d_model"]
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 200, D, generator=g).to(cuda)
+    with torch.no_grad():
+        full = module(x)
+        state = module.initial_state()
+        outs = []
+        for a, b in zip(CUTS, CUTS[1:]):
+            y, state = module(x[:, a:b], state=state)
+            outs.append(y)
+        sizes = state.nbytes
+        # one-token decode after the sequence: equals the longer sequence's last rows
+        x2 = torch.randn(2, 5, D, generator=g).to(cuda)
+        longer = module(torch.cat([x, x2], 1))
+        steps = []
+        for t in range(5):
+            y, state = module(x2[:, t:t + 1], state=state)
+            steps.append(y)
+    print(f"{name}: path={module._core.last_path} state {sizes} bytes", flush=True)
+    assert state.position == 205 and state.nbytes == sizes
+    ref = _oracle(module, pub, torch.cat([x, x2], 1))
+    assert rel_err(full, ref[:, :200]) < 1e-4, name
+    assert rel_err(torch.cat(outs, 1), ref[:, :200]) < 1e-4, name
+    assert rel_err(torch.cat(steps, 1), ref[:, 200:]) < 1e-4, name
+    assert rel_err(torch.cat(outs, 1), full) < 1e-4, name
+
+
+def test_state_semantics(cuda):
+    import thetascan_amd as ts
+
+    module, pub = _module("kernel_softmax_bank_fast", cuda)
+    D = pub["d_model"]
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 90, D, generator=g).to(cuda)
+    with torch.no_grad():
+        _, st = module(x[:, :50], state=module.initial_state())
+        # save / load round trip and clones continue identically
+        buf = io.BytesIO()
+        torch.save(st.state_dict(), buf)
+        buf.seek(0)
+        loaded = ts.ThetaScanState.from_state_dict(torch.load(buf, weights_only=True))
+        copy = st.clone()
+        y1, after = module(x[:, 50:], state=st)
+        y2, _ = module(x[:, 50:], state=loaded)
+        y3, _ = module(x[:, 50:], state=copy)
+        assert torch.equal(y1, y2) and torch.equal(y1, y3)
+        assert after.position == 90 and st.position == 50
+        # a different batch size, configuration or device is refused
+        with pytest.raises(ValueError, match="sequences"):
+            module(x[:1, 50:], state=st)
+        other, _ = _module("kernel_softmax_sparse_st_blend_stale", cuda)
+        with pytest.raises(ValueError, match="configuration"):
+            other(x[:, 50:], state=st)
+        with pytest.raises(ValueError, match="lives on"):
+            module(x[:, 50:], state=st.to("cpu"))
+    with pytest.raises(RuntimeError, match="autograd"):
+        module(x[:, 50:], state=st)

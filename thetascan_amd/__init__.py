@@ -1,6 +1,7 @@
 """ThetaScan on MI355X: the public API of the reference package with a
 hand-written gfx950 ``hip`` scan backend underneath."""
 from .api import ThetaScan
+from .state import ThetaScanState
 from .config import (
     Backend,
     BankMode,
@@ -34,5 +35,5 @@ __all__ = [
     "KernelBSplineScaleMode", "KernelConfig", "KernelFeatureMap", "KernelReLU2ThresholdMode",
     "KernelReadNormalization", "KernelSharpnessMode", "KernelSparsity", "KernelValueRepresentation",
     "RegularizationConfig", "RoPEConfig", "RoPEMode", "RoPEPlacement", "RuntimeConfig", "TemporalConfig",
-    "TemporalMode", "ThetaScan", "ThetaScanConfig",
+    "TemporalMode", "ThetaScan", "ThetaScanConfig", "ThetaScanState",
 ]

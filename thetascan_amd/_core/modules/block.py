@@ -23,7 +23,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
-from ..ops import engine, features, fused, gn, interface, maps, prologue
+from ...state import ThetaScanState, config_fingerprint
+from ..ops import engine, features, fused, gn, interface, maps, prologue, stream
 from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
@@ -415,12 +416,20 @@ class ThetaScan(nn.Module):
                                   self.ogate.g.lin.bias if gate else None, W1, W2, self.kernel_relu2_threshold,
                                   self.proj_out.weight, spec, cfg.read_norm, H)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def initial_state(self) -> ThetaScanState:
+        """The state of a sequence with no tokens yet (streaming continuation)."""
+        return ThetaScanState(fingerprint=config_fingerprint(self.cfg))
+
+    def forward(self, x: torch.Tensor, state: ThetaScanState | None = None):
+        """``y`` for ``x`` [B,T,D]; with ``state``, the sequence continues from
+        it and ``(y, new_state)`` is returned (no autograd)."""
         cfg = self.cfg
         backend = resolve_backend(cfg.backend, cfg.decay_gate, cfg.accumulation, device=x.device,
                                   require_scalar_decay=cfg.read_fade)
         if not x.is_cuda:
             raise RuntimeError("the hip backend runs on the GPU only (no CPU fallback)")
+        if state is not None:
+            return self._forward_carried(x, state, backend)
         fused_path = self.fused_eligible(x)
         if not torch.compiler.is_compiling():
             # a record for eager callers; a traced forward writes no module state
@@ -428,6 +437,35 @@ class ThetaScan(nn.Module):
         if fused_path:
             return self._forward_fused(x) if self._fused_cfg else self._forward_views(x, backend)
         return self._forward_composed(x, backend)
+
+    def _forward_carried(self, x: torch.Tensor, state: ThetaScanState, backend: str):
+        """One call of a continued sequence: every scan and decayed prefix of
+        the forward starts from the state the previous call left (the
+        one-call sum path keeps no state, so the multi-view path serves it)."""
+        if state.fingerprint != config_fingerprint(self.cfg):
+            raise ValueError("this state belongs to a mixer of another configuration")
+        B = x.shape[0]
+        if state.carries and state.batch != B:
+            raise ValueError(f"the state holds {state.batch} sequences; the input has {B}")
+        for t in state._tensors():
+            if t.device != x.device:
+                raise ValueError(f"the state lives on {t.device}; the input on {x.device} (use state.to)")
+        if x.shape[1] == 0:
+            # no tokens: the memory is unchanged
+            with stream.carrying(stream.Carry()):
+                return x.new_empty(B, 0, self.proj_out.weight.shape[0]), state
+        carry = stream.Carry(state.carries, state.position)
+        with stream.carrying(carry):
+            if self.fused_eligible(x):
+                self.last_path = "fused"
+                y = self._forward_views(x, backend)
+            else:
+                self.last_path = "composed"
+                y = self._forward_composed(x, backend)
+        if state.carries and len(carry.out) != len(state.carries):
+            raise RuntimeError("the state does not match this forward's scans")
+        return y, ThetaScanState(fingerprint=state.fingerprint, position=state.position + x.shape[1], batch=B,
+                                 carries=tuple(carry.out))
 
     def _project(self, x):
         cfg = self.cfg

@@ -11,16 +11,27 @@ from functools import lru_cache
 import torch
 
 
-@lru_cache(maxsize=32)
-def _rope_cache_cached(T: int, rot_dim: int, base: float, device_type: str, device_index, dtype: torch.dtype):
-    device = torch.device(device_type) if device_index is None else torch.device(device_type, device_index)
+def _tables(T: int, rot_dim: int, base: float, device, dtype: torch.dtype, start: int = 0):
     phase_dtype = torch.float64 if dtype == torch.float64 else torch.float32
     inv = 1.0 / (base ** (torch.arange(0, rot_dim, 2, device=device, dtype=phase_dtype) / rot_dim))
-    f = torch.outer(torch.arange(T, device=device, dtype=phase_dtype), inv)
+    f = torch.outer(torch.arange(start, start + T, device=device, dtype=phase_dtype), inv)
     return f.cos().to(dtype=dtype), f.sin().to(dtype=dtype)
 
 
+@lru_cache(maxsize=32)
+def _rope_cache_cached(T: int, rot_dim: int, base: float, device_type: str, device_index, dtype: torch.dtype):
+    device = torch.device(device_type) if device_index is None else torch.device(device_type, device_index)
+    return _tables(T, rot_dim, base, device, dtype)
+
+
 def rope_cache(T: int, rot_dim: int, base: float, device, dtype):
+    """cos/sin of the current call's positions: 0 .. T-1, or, while a
+    sequence is continued across calls, from the number of tokens seen."""
+    from ..ops import stream
+
+    start = stream.position()
+    if start:
+        return _tables(T, rot_dim, base, torch.device(device), dtype, start)
     resolved = torch.device(device)
     index = resolved.index
     if resolved.type == "cuda" and index is None:

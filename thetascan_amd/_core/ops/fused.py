@@ -24,14 +24,15 @@ import torch
 
 from ... import _lib
 from .dispatch import HipOp
-from . import scan_hip
+from . import scan_hip, stream
 from .linear import slot_sum, split_k_outer, weight_grad
 
 
-def _rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """fp32 cos/sin [T, rot/2] (rope.py:7-38 phases, kept in fp32)."""
+def _rope_tables(T: int, rot: int, base: float, device, start: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos/sin [T, rot/2] of positions start .. start+T-1 (rope.py:7-38
+    phases, kept in fp32)."""
     inv = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
-    f = torch.outer(torch.arange(T, device=device, dtype=torch.float32), inv)
+    f = torch.outer(torch.arange(start, start + T, device=device, dtype=torch.float32), inv)
     return f.cos().contiguous(), f.sin().contiguous()
 
 
@@ -39,6 +40,11 @@ _TABLES: dict = {}
 
 
 def rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """The tables of the current call's positions: 0 .. T-1, or, while a
+    sequence is continued, from the number of tokens already seen."""
+    start = stream.position()
+    if start:
+        return _rope_tables(T, rot, base, device, start)
     key = (T, rot, float(base), str(device))
     hit = _TABLES.get(key)
     if hit is None:

@@ -14,7 +14,7 @@ from functools import partial
 
 import torch
 
-from . import fused, scan_hip
+from . import fused, scan_hip, stream
 from .dispatch import HipOp
 
 _REGISTRY = {"hip": scan_hip.linattn}
@@ -49,18 +49,43 @@ def _fn(backend: str, chunk: int = scan_hip.DEFAULT_CHUNK):
 
 def ema_cumsum(x: torch.Tensor, log_alpha: torch.Tensor, chunk: int = 64) -> torch.Tensor:
     """z_t = sum_{i<=t} alpha^(t-i) x_i with static alpha[H] (interface.py:58-93)."""
-    return _wcumsum_op(x, log_alpha, False).to(x.dtype)
+    return _prefix(x, log_alpha)
 
 
 def causal_prefix_sum(x: torch.Tensor) -> torch.Tensor:
     """Prefix sum along T (interface.py:96-107)."""
-    return _wcumsum_op(x, None, False).to(x.dtype)
+    return _prefix(x, None)
 
 
 def decayed_prefix(x: torch.Tensor, decay: torch.Tensor) -> torch.Tensor:
     """z_t = sum_{i<=t} prod_{i<j<=t} a_j x_i for a [B,H,T,1] log-decay stream
     (the unit query/key scan of interface.py:229-230)."""
-    return _wcumsum_op(x, decay, False).to(x.dtype)
+    return _prefix(x, decay)
+
+
+def _prefix(x: torch.Tensor, retention: torch.Tensor | None) -> torch.Tensor:
+    carry = stream.active()
+    if carry is None:
+        return _wcumsum_op(x, retention, False).to(x.dtype)
+    # continued from the previous call's last row c: z_t = local_t + w_t c,
+    # w_t = 1 (plain), alpha^(t+1) (static) or prod_{j<=t} a_j (stream)
+    z = fused.wcumsum(x, retention, False)
+    c = carry.take()
+    if c is not None:
+        T = x.shape[2]
+        if retention is None:
+            w = torch.ones(1, 1, T, 1, dtype=torch.float32, device=x.device)
+        elif retention.ndim == 4:
+            w = retention.float().cumsum(2).exp()
+        else:
+            t1 = torch.arange(1, T + 1, dtype=torch.float32, device=x.device)
+            w = (retention.float().view(1, -1, 1, 1) * t1.view(1, 1, T, 1)).exp()
+        z = z + w * c.unsqueeze(2)
+    if x.shape[2]:
+        carry.put(z[:, :, -1].clone())
+    else:
+        carry.put(c if c is not None else z.new_zeros(*x.shape[:2], x.shape[-1]))
+    return z.to(x.dtype)
 
 
 # The decayed prefix as an autograd node (dispatch.HipOp) with its transposed

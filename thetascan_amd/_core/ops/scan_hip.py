@@ -41,6 +41,7 @@ import ctypes
 import torch
 
 from ... import _lib
+from . import stream
 from .dispatch import HipOp
 
 DEFAULT_CHUNK = 512   # reference default (scan_chunk.DEFAULT_CHUNK); validated only
@@ -647,6 +648,55 @@ _scan_views_op = HipOp("scan_views", forward=_scan_views_forward, forward_fake=_
                        setup=_scan_views_setup, backward=_scan_views_backward)
 
 
+def _carried_scan(q, k, v, kind, r, with_mass: bool, init):
+    """One forward scan that starts from ``init`` (a list of fp32 state
+    blocks, None: zero) and returns ``(out, mass, blocks)``.  Keys and values
+    wider than one launch split into blocks of at most MAX_WIDTH columns; each
+    block of the state N [dk, dv] (the mass column rides with the first value
+    block) is carried by its own launch, and the outputs of key blocks add."""
+    dk, dv = q.shape[-1], v.shape[-1]
+    kcols = list(range(0, dk, MAX_WIDTH))
+    vcols = list(range(0, dv, MAX_WIDTH))
+    blocks = init if init is not None else [None] * (len(kcols) * len(vcols))
+    if len(blocks) != len(kcols) * len(vcols):
+        raise ValueError("streaming state does not match this scan's widths")
+    rk = _ret_kwargs(kind, r)
+    if len(blocks) == 1:
+        out, mass, fin = scan_launch(q, k, v, **rk, v_ext="ones" if with_mass else None, want_ext_out=with_mass,
+                                     want_final=True, init_state=blocks[0])
+        return out, mass, [fin]
+    acc = torch.zeros(*q.shape[:3], dv, dtype=torch.float32, device=q.device)
+    mass = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device) if with_mass else None
+    finals = []
+    i = 0
+    for k0 in kcols:
+        qs, ks = q[..., k0:k0 + MAX_WIDTH], k[..., k0:k0 + MAX_WIDTH]
+        for j, v0 in enumerate(vcols):
+            ext = with_mass and j == 0
+            o, e, fin = scan_launch(qs, ks, v[..., v0:v0 + MAX_WIDTH], **rk, v_ext="ones" if ext else None,
+                                    want_ext_out=ext, want_final=True, init_state=blocks[i])
+            acc[..., v0:v0 + o.shape[-1]] += o.float()
+            if ext:
+                mass += e
+            finals.append(fin)
+            i += 1
+    return acc.to(q.dtype), mass, finals
+
+
+def _views_carried(q, k, v, retentions, with_mass: bool, out_f32: bool, carry) -> list:
+    """The forward scans of every retention continued from ``carry``."""
+    if out_f32 and q.dtype != torch.float32:
+        q, k, v = q.float(), k.float(), v.float()
+    outs, masses = [], []
+    for r in retentions:
+        out, mass, finals = _carried_scan(q, k, v, _classify(r, q), r, with_mass, carry.take())
+        carry.put(finals)
+        outs.append(out)
+        if with_mass:
+            masses.append(mass)
+    return outs + masses
+
+
 def _run_views(q, k, v, retentions, chunk, with_mass, out_f32=False):
     if chunk < 1:
         raise ValueError("chunk backend: chunk must be >= 1")
@@ -654,6 +704,9 @@ def _run_views(q, k, v, retentions, chunk, with_mass, out_f32=False):
         return ()
     for r in retentions:
         _classify(r, q)
+    carry = stream.active()
+    if carry is not None:
+        return _views_carried(q, k, v, tuple(retentions), with_mass, out_f32, carry)
     if out_f32 and q.dtype != torch.float32:
         # A caller that subtracts views (a stale view is plain - fast, nearly
         # equal over recent tokens) gets scans on fp32 operands, forward and

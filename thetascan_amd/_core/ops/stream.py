@@ -1,0 +1,61 @@
+"""Continuation of one causal sequence across forward calls.
+
+A mixer forward is a fixed sequence of causal scans and decayed prefixes
+(every other operation is per token).  While a :class:`Carry` is active, each
+of them starts from the state the same scan left at the end of the previous
+call -- taken in call order -- and leaves its final state for the next one;
+RoPE phases start at the number of tokens already seen.  The carries are the
+fp32 scan states N = sum_i w_i k_i v_i^T (with the key-mass column where the
+read normalizes) and the fp32 last rows of the decayed prefixes, i.e. exactly
+what a recurrence S_t = a_t S_{t-1} + k_t v_t^T (scan_naive.py:5-18) keeps
+between tokens.  Continuation runs without autograd.
+"""
+from __future__ import annotations
+
+import contextlib
+import contextvars
+
+import torch
+
+_ACTIVE: contextvars.ContextVar = contextvars.ContextVar("thetascan_carry", default=None)
+
+
+class Carry:
+    """The states one forward call consumes (``inp``, in call order; empty
+    for a fresh sequence) and produces (``out``), and the position of its
+    first token."""
+
+    def __init__(self, carries=(), position: int = 0):
+        self.inp = list(carries)
+        self.out: list = []
+        self.position = int(position)
+
+    def take(self):
+        """The state the next scan or prefix starts from (None: zero)."""
+        i = len(self.out)
+        return self.inp[i] if i < len(self.inp) else None
+
+    def put(self, state) -> None:
+        self.out.append(state)
+
+
+def active() -> Carry | None:
+    return _ACTIVE.get()
+
+
+def position() -> int:
+    """Absolute position of the current call's first token (0 outside a carry)."""
+    carry = _ACTIVE.get()
+    return 0 if carry is None else carry.position
+
+
+@contextlib.contextmanager
+def carrying(carry: Carry):
+    if torch.is_grad_enabled():
+        raise RuntimeError("streaming continuation runs without autograd: call it under torch.no_grad() "
+                           "or torch.inference_mode()")
+    token = _ACTIVE.set(carry)
+    try:
+        yield carry
+    finally:
+        _ACTIVE.reset(token)

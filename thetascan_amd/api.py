@@ -7,6 +7,7 @@ import torch
 import torch.nn as nn
 
 from ._core.modules.block import ThetaScan as _CoreThetaScan
+from .state import ThetaScanState
 from .config import ThetaScanConfig
 
 
@@ -26,8 +27,16 @@ class ThetaScan(nn.Module):
             if not frozen:
                 raise RuntimeError("could not locate kernel feature parameters to freeze")
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self._core(x)
+    def forward(self, x: torch.Tensor, state: ThetaScanState | None = None):
+        """``y`` [B,T,D]; with ``state`` (see :mod:`thetascan_amd.state`) the
+        causal sequence continues from it and ``(y, new_state)`` is returned."""
+        if state is None:
+            return self._core(x)
+        return self._core(x, state)
+
+    def initial_state(self) -> ThetaScanState:
+        """The state of a sequence with no tokens yet."""
+        return self._core.initial_state()
 
     def zero_output_projection_(self) -> "ThetaScan":
         nn.init.zeros_(self._core.proj_out.weight)

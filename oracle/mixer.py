@@ -563,17 +563,11 @@ SCANS = {"naive": scans.linattn_naive, "quad": scans.linattn_quad, "cumsum": sca
          "chunk": scans.linattn_chunk}
 
 
-def forward(c, params, x, backend: str = "naive"):
-    """ThetaScan forward x[B,T,D] -> y[B,T,D] (block.py:573-724).
-
-    ``backend`` picks the oracle scan: the naive loop (parity target), the
-    quadratic form, the prefix-sum form (the CPU baseline algorithm), or the
-    tiled form (64-token tiles; equal to the naive loop at 1e-12, linear in T,
-    for long sequences).
-    """
-    scan = SCANS[backend]
+def _write_side(c, params, x):
+    """Projections, RoPE, L2 norm, value MLP, decay gate and the write
+    streams (block.py:573-665)."""
     B, T, _ = x.shape
-    H, d = c["n_heads"], c["head_dim"]
+    H = c["n_heads"]
     q, k, v = project(c, params, x)
     if c["rope_placement"] == "input":
         q = apply_rope(q, c["rope"], c["rope_frac"], c["rope_base"])
@@ -595,6 +589,50 @@ def forward(c, params, x, backend: str = "naive"):
     weights = effective_weights(c, params)
     ctl = kernel_controls(c, params)
     streams = write_streams(weights, c, k, v, hrot, ctl)
+    return q, streams, hrot, ctl, weights, decay
+
+
+def kernel_final_states(c, params, x):
+    """Memory of a depth-1 kernel mixer after the last token, per view, by the
+    closed form N_T = sum_i w_i phi(k_i) v_i^T and D_T = sum_i w_i phi(k_i)
+    (the brute-force DW2 / Smass of engine.py:669-703 at t = T-1): the plain
+    sum (w_i = 1, or the ema stream's prod_{i<j<T} a_j) first, then every
+    recency branch (w_i = alpha^(T-1-i)).  Returns [(N [B,H,m,d], D [B,H,m])]."""
+    _, streams, _, _, _, decay = _write_side(c, params, x)
+    keys, vals = streams["la2"][0]
+    T = keys.shape[2]
+    weights = []
+    if decay is None:
+        weights.append(keys.new_ones(1, 1, T))
+    else:
+        tail = decay[..., 0].flip(-1).cumsum(-1).flip(-1)  # sum_{j>=i} log a_j
+        weights.append(torch.cat([tail[..., 1:], tail.new_zeros(*tail.shape[:2], 1)], -1).exp())
+    if c["read_fade"]:
+        raw = params["fade_alpha"]
+        raw = raw.unsqueeze(0) if raw.ndim == 1 else raw
+        lags = torch.arange(T - 1, -1, -1, dtype=keys.dtype)
+        for j in range(c["fade_branches"]):
+            la = -F.softplus(-raw[j])
+            weights.append((la.view(1, -1, 1) * lags.view(1, 1, T)).exp())
+    out = []
+    for w in weights:
+        wk = keys * w.unsqueeze(-1)
+        out.append((torch.einsum("bhtm,bhtd->bhmd", wk, vals), wk.sum(2)))
+    return out
+
+
+def forward(c, params, x, backend: str = "naive"):
+    """ThetaScan forward x[B,T,D] -> y[B,T,D] (block.py:573-724).
+
+    ``backend`` picks the oracle scan: the naive loop (parity target), the
+    quadratic form, the prefix-sum form (the CPU baseline algorithm), or the
+    tiled form (64-token tiles; equal to the naive loop at 1e-12, linear in T,
+    for long sequences).
+    """
+    scan = SCANS[backend]
+    B, T, _ = x.shape
+    H, d = c["n_heads"], c["head_dim"]
+    q, streams, hrot, ctl, weights, decay = _write_side(c, params, x)
 
     def read(view):
         return read_view(weights, c, q, streams, view, hrot, ctl)

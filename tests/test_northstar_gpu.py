@@ -11,7 +11,9 @@
 * The ThetaScan-Kernel CPU-reference workload: B2 T1024 d512 H8, softmax
   partition, a fast recency bank with per-head retentions drawn from
   U[0.9, 0.999] (``fade_alpha = logit(alpha)``) and non-zero blends, fp32 at
-  rel 1e-3.
+  rel 1e-3, and its memory after the last token (the streaming state) against
+  the closed form N_T = sum_i w_i phi(k_i) v_i^T, D_T = sum_i w_i phi(k_i)
+  per view.
 * A temporal-bank mixer and a GN mixer in bf16 against the oracle (rel 2e-2).
 
 The oracle is ``oracle.mixer.forward`` with the tiled scan (``linattn_chunk``,
@@ -163,6 +165,18 @@ def test_cpu_reference_workload_matches_oracle_fp32(cuda):
     for name, p in module._core.named_parameters():
         if name in grads64 and grads64[name].abs().max() > 0:
             assert rel_err(p.grad, grads64[name]) < 5e-3, name
+    # the memory after the last token, per view: N_T = sum_i w_i phi(k_i) v_i^T
+    # and D_T = sum_i w_i phi(k_i) (plain sum, then the recency branch)
+    with torch.no_grad():
+        _, state = module(xf.detach(), state=module.initial_state())
+    params = {k: v.detach().double().cpu() for k, v in module._core.named_parameters()}
+    finals = oracle_mixer.kernel_final_states(oracle_mixer.core_config(pub), params, x)
+    assert len(state.carries) == len(finals) == 2
+    m = d = 64
+    for (blocks), (N, D) in zip(state.carries, finals):
+        fin = blocks[0]
+        assert rel_err(fin[:, :, :m, :d], N) < 1e-3
+        assert rel_err(fin[:, :, :m, d], D) < 1e-3
 
 
 # ------------------------------------------------------------------ bf16 bank and GN mixers

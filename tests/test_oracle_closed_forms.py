@@ -175,3 +175,32 @@ def test_final_state_closed_form_and_one_hot_reads():
             qq[:, :, -1] = eye[:, :, j]
             out = scans.linattn_naive(qq, k, v, decay)
             assert torch.allclose(out[:, :, -1], S[:, :, j], rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("case", ["kernel_softmax_bank_fast", "kernel_relu2_threshold_feature_mass_ema"])
+def test_kernel_final_states_equal_the_recurrence(case):
+    """oracle.mixer.kernel_final_states (closed form per view) equals the
+    naive recurrence's final state on the mixer's own write streams, view by
+    view (the plain sum or ema stream, then each recency branch)."""
+    import torch.nn.functional as F
+
+    from oracle import mixer
+    from tests.test_oracle_golden import load_case
+
+    pub, params, _, arrays = load_case(case)
+    c = mixer.core_config(pub)
+    x = arrays["x"]
+    finals = mixer.kernel_final_states(c, params, x)
+    _, streams, _, _, _, decay = mixer._write_side(c, params, x)
+    keys, vals = streams["la2"][0]
+    ones = torch.ones(*keys.shape[:3], 1, dtype=keys.dtype)
+    decays = [decay]
+    if c["read_fade"]:
+        raw = params["fade_alpha"]
+        raw = raw.unsqueeze(0) if raw.ndim == 1 else raw
+        decays += [scans.as_stream(-F.softplus(-raw[j]), keys) for j in range(c["fade_branches"])]
+    assert len(finals) == len(decays)
+    for (N, D), dec in zip(finals, decays):
+        S = scans.final_state_naive(keys, torch.cat([vals, ones], -1), dec)
+        assert torch.allclose(N, S[..., :-1], rtol=1e-10, atol=1e-12)
+        assert torch.allclose(D, S[..., -1], rtol=1e-10, atol=1e-12)

@@ -298,10 +298,18 @@ def cpu_baseline(budget_s: float = 12.0):
 #                 0.999, 0.9999} (fast blend), B2 T32768 H8 d64, bf16, forward
 #                 only (both extensions of the core config: the public config,
 #                 like the reference's, stops at two rates and expands only
-#                 the ReLU^2 map).
+#                 the ReLU^2 map);
+#   lm            the 17.06M-parameter hybrid language model (9 layers,
+#                 d_model 512, vocabulary 1024, attention in all layers but 4
+#                 and 5, which are ThetaScan-Kernel memories at m = 128 by 2x
+#                 expansion), B64 T1024 uniform random tokens, bf16, fwd+bwd;
+#                 the line also reports the eval loss change of the per-row
+#                 int8 round trip of its weights.
 OTHER = {
     "gn": dict(B=8, T=2048, train=True,
                metric="GN mixer tokens/s fwd+bwd (B8 T2048 H8 d64 m128 tanh, damping 1e-2, bf16)"),
+    "lm": dict(B=64, T=1024, train=True,
+               metric="hybrid LM tokens/s fwd+bwd (17.06M params, 2 ThetaScan layers, B64 T1024, bf16)"),
     "bspline_bank": dict(B=2, T=32768, train=False,
                          metric="B-spline 4-rate bank mixer tokens/s fwd (B2 T32768 H8 d64 m128 2x expanded, bf16)"),
 }
@@ -330,9 +338,56 @@ def other_config(name: str):
                                fade_alpha_inits=(0.9, 0.99, 0.999, 0.9999))
 
 
+def run_lm(args) -> dict:
+    """The hybrid language model's training step on uniform random tokens."""
+    import torch
+
+    from thetascan_amd import hybrid_lm as lm
+
+    spec = OTHER["lm"]
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    model = lm.HybridLM().to(dev, torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randint(0, lm.VOCAB, (spec["B"], spec["T"]), generator=g).to(dev)
+    y = torch.randint(0, lm.VOCAB, (spec["B"], spec["T"]), generator=g).to(dev)
+
+    def step():
+        model(x, y).backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    model.eval()
+    with torch.no_grad():
+        base = float(model(x[:8], y[:8]))
+        model.load_state_dict(lm.int8_round_trip(model))
+        quant = float(model(x[:8], y[:8]))
+    tokens = spec["B"] * spec["T"]
+    return {
+        "metric": spec["metric"], "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform random tokens, seeded init)", "execution": "eager",
+        "path": model.blocks[lm.THETA_LAYERS[0]].attn._core.last_path,
+        "config": {"workload": "lm", "batch": spec["B"], "seq_len": spec["T"], "params": lm.parameter_count(model),
+                   "layers": lm.LAYERS, "theta_layers": list(lm.THETA_LAYERS), "parallelism": "single GPU"},
+        "int8_round_trip": {"eval_loss": round(base, 6), "eval_loss_int8": round(quant, 6),
+                            "rel": round(abs(quant - base) / base, 8), "parity": "unpinned"},
+    }
+
+
 def run_other(name: str, args) -> dict:
     """One JSON line for a non-headline workload (no CPU baseline)."""
     import torch
+
+    if name == "lm":
+        return run_lm(args)
 
     from thetascan_amd._core.modules.block import ThetaScan as CoreMixer
 

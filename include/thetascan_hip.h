@@ -31,8 +31,9 @@ extern "C" {
  *    allocated workspace at an odd offset was accepted by version 7).
  * 9: ts_wcumsum takes a workspace (ts_wcumsum_workspace_bytes).
  * 10: the GN descriptors carry the hidden nonlinearity (and the write its
- *     damping). */
-#define TS_ABI_VERSION 10
+ *     damping);
+ * 11: ts_scan_pair_io carries scan A's key-side ext column (k_ext). */
+#define TS_ABI_VERSION 11
 
 enum ts_status {
   TS_OK = 0,
@@ -163,13 +164,17 @@ int ts_scan_fwd_noalloc(const ts_scan_desc* desc, const ts_scan_io* io, hipStrea
  * of scan_chunk.linattn_views, scan_chunk.py:246-339): k = dnum, v = phi(q),
  * qa = v, qb = phi(k).  K and V are read once and the state is updated once
  * per tile; each output equals its own ts_scan_fwd call.  desc describes
- * scan A (q = qa): bf16, no retention, no ext columns, TS_OUT_STORE,
- * dk == dv == 64; workspace from ts_scan_workspace_bytes(desc), 16-byte
- * aligned. */
+ * scan A (q = qa): bf16, no retention, TS_OUT_STORE, dk == dv == 64, no
+ * value-side ext column; with q_ext = TS_EXT_ONES and k_ext = TS_EXT_ARRAY
+ * scan A is the key-mass read's backward, out_a_t = sum_i (<qa_t, k_i> +
+ * k_ext_i) v_i (scan B has no ext column); workspace from
+ * ts_scan_workspace_bytes(desc), 16-byte aligned. */
 typedef struct ts_scan_pair_io {
   ts_strided qa, k, v, qb;
   ts_strided out_a;               /* [B,H,T,dv]                                */
   ts_strided out_b;               /* [B,H,T,dk]                                */
+  ts_strided k_ext;               /* fp32 [B,H,T] key-side ext of scan A (desc
+                                     q_ext ones, k_ext array), else NULL       */
 } ts_scan_pair_io;
 
 int ts_scan_pair_fwd(const ts_scan_desc* desc, const ts_scan_pair_io* io,

@@ -583,3 +583,33 @@ def test_pair_scan_writes_strided_outputs(cuda):
     assert b.data_ptr() == view.data_ptr()
     assert torch.equal(view, ref_b)
     assert not big[:, :, :2].any()
+
+
+@pytest.mark.parametrize("T,seg_chunks,reverse", [(1, 0, True), (200, 1, False), (700, 2, True), (4096, 0, True)])
+def test_pair_scan_with_key_ext_equals_its_two_scans(cuda, T, seg_chunks, reverse):
+    """With scan A's key-side ext pair (the key-mass read's backward: queries
+    carry a ones column, keys the fp32 dmass), ts_scan_pair_fwd gives
+    scan(qa, k, v; ones x dmass) and scan(qb, v, k) bit for bit as two
+    ts_scan_fwd calls do, and scan A matches the float64 recurrence with the
+    ext column appended."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, D = 2, 3, 64
+    g = torch.Generator().manual_seed(97 + T)
+    qa, k, v, qb = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64).to(torch.bfloat16).to(torch.float64)
+                    for _ in range(4))
+    ke = torch.randn(B, H, T, generator=g, dtype=torch.float64).to(torch.float32).to(torch.float64)
+    dev = [x.to(cuda, torch.bfloat16) for x in (qa, k, v, qb)]
+    ke_d = ke.to(cuda, torch.float32)
+    a, b = scan_hip.scan_pair_launch(*dev, reverse=reverse, seg_chunks=seg_chunks, k_ext=ke_d)
+    ref_a, _, _ = scan_hip.scan_launch(dev[0], dev[1], dev[2], reverse=reverse, seg_chunks=seg_chunks,
+                                       q_ext="ones", k_ext=ke_d)
+    ref_b, _, _ = scan_hip.scan_launch(dev[3], dev[2], dev[1], reverse=reverse, seg_chunks=seg_chunks)
+    assert torch.equal(a, ref_a) and torch.equal(b, ref_b), (T, seg_chunks, reverse)
+    ones = torch.ones(B, H, T, 1, dtype=torch.float64)
+    qx, kx = torch.cat([qa, ones], -1), torch.cat([k, ke.unsqueeze(-1)], -1)
+    if reverse:
+        want = oracle.linattn_chunk(qx.flip(2), kx.flip(2), v.flip(2)).flip(2)
+    else:
+        want = oracle.linattn_chunk(qx, kx, v)
+    assert rel_err(a, want) < TOL[torch.bfloat16]

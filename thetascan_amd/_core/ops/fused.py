@@ -527,10 +527,11 @@ def _memory_backward(st: _State, dy, need_w1: bool, need_w2: bool, need_tau: boo
                                         states_in=2 if ws_f is not None else 0)
     # dk = reverse scan(v, dnum, phi_q) and dv = reverse scan(phi_k, phi_q, dnum) share
     # their segment states up to a transpose (sum_i dnum_i phi_q_i^T)
-    if not norm and scan_hip.pair_eligible(v, dnum, phi_q, phi_k):
-        # both in one pass over dnum and phi_q
+    if scan_hip.pair_eligible(v, dnum, phi_q, phi_k):
+        # both in one pass over dnum and phi_q (the key-mass read's dmass
+        # joins the dk scan's scores)
         dphi_k, _ = scan_hip.scan_pair_launch(v, dnum, phi_q, phi_k, reverse=True, seg_chunks=st.seg_chunks,
-                                              out_b=dv)
+                                              out_b=dv, k_ext=q_ext)
     else:
         ws_r = scan_hip.workspace_for(v, dnum, phi_q, seg_chunks=st.seg_chunks, reverse=True, kx=norm) \
             if ws_f is not None else None

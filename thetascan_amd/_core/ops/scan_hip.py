@@ -316,9 +316,12 @@ def pair_eligible(qa: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qb: torch.
 
 
 def scan_pair_launch(qa: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qb: torch.Tensor, *, reverse: bool = False,
-                     seg_chunks: int = 0, out_a: torch.Tensor | None = None, out_b: torch.Tensor | None = None):
+                     seg_chunks: int = 0, out_a: torch.Tensor | None = None, out_b: torch.Tensor | None = None,
+                     k_ext: torch.Tensor | None = None):
     """scan(qa, k, v) and scan(qb, v, k) (plain, bf16, 64-wide) in one pass over
-    k and v; returns ``(out_a, out_b)``, each equal to its own scan_launch."""
+    k and v; returns ``(out_a, out_b)``, each equal to its own scan_launch.
+    ``k_ext`` (fp32 [B,H,T]) gives scan A the key-side ext pair of a
+    normalized read's backward: scan_launch(qa, k, v, q_ext="ones", k_ext=k_ext)."""
     lib = _lib.load()
     B, H, T, d = qa.shape
     views = [_kernel_view(t, 64) for t in (qa, k, v, qb)]
@@ -326,13 +329,16 @@ def scan_pair_launch(qa: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qb: tor
         out_a = torch.empty(B, H, T, 64, dtype=qa.dtype, device=qa.device)
     if out_b is None:
         out_b = torch.empty(B, H, T, 64, dtype=qa.dtype, device=qa.device)
-    desc = _lib.ScanDesc(B, H, T, 64, 64, _lib.dtype_code(qa.dtype), _lib.RET_NONE, int(reverse), 0, 0, 0,
+    ke = None if k_ext is None else k_ext.to(torch.float32).contiguous()
+    desc = _lib.ScanDesc(B, H, T, 64, 64, _lib.dtype_code(qa.dtype), _lib.RET_NONE, int(reverse),
+                         _lib.EXT_ONES if ke is not None else 0, _lib.EXT_ARRAY if ke is not None else 0, 0,
                          _lib.OUT_STORE, 1.0, int(seg_chunks), 0, 0, 0, 0)
     c_ws = ctypes.c_size_t()
     _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan workspace")
     workspace = torch.empty(c_ws.value, dtype=torch.uint8, device=qa.device) if c_ws.value else None
-    io = _lib.ScanPairIO(*[_lib.strided(t) for t in views], _lib.strided(out_a), _lib.strided(out_b))
-    with _lib.timed("ts_scan_pair_fwd", lambda: _lib.nbytes(*views, out_a, out_b)):
+    io = _lib.ScanPairIO(*[_lib.strided(t) for t in views], _lib.strided(out_a), _lib.strided(out_b),
+                         _lib.strided(ke))
+    with _lib.timed("ts_scan_pair_fwd", lambda: _lib.nbytes(*views, out_a, out_b, ke)):
         status = lib.ts_scan_pair_fwd(ctypes.byref(desc), ctypes.byref(io),
                                       workspace.data_ptr() if workspace is not None else None, c_ws.value,
                                       _lib.stream_handle(qa.device))

@@ -72,7 +72,7 @@ class ScanDesc(ctypes.Structure):
 
 
 class ScanPairIO(ctypes.Structure):
-    _fields_ = [(n, Strided) for n in ("qa", "k", "v", "qb", "out_a", "out_b")]
+    _fields_ = [(n, Strided) for n in ("qa", "k", "v", "qb", "out_a", "out_b", "k_ext")]
 
 
 MAX_VIEWS = 3
@@ -489,7 +489,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 10:
+        if lib.ts_abi_version() != 11:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

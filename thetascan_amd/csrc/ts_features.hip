@@ -74,8 +74,9 @@ __device__ __forceinline__ float load_xn(const FeatP& p, int t, bool valid, int 
 }
 
 // In-register feature map of a^T (lane = token).  Leaves h in `hv`; returns
-// the statistics the backward needs.
-template <int MB>
+// the statistics the backward needs.  KIND is the ts_feature_kind (a
+// compile-time constant, so neither map carries the other's code).
+template <int KIND, int MB>
 __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const floatx4* a, int nfb, floatx4* hv,
                                             float& rinv, float& mass) {
   float ss = 0.f;
@@ -85,7 +86,7 @@ __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const flo
 #pragma unroll
       for (int i = 0; i < 4; ++i) ss += a[fb][i] * a[fb][i];
   rinv = rsqrtf(sum_g(ss) * p.inv_m + p.eps);
-  if (p.kind == TS_FEAT_RELU2) {
+  if constexpr (KIND == TS_FEAT_RELU2) {
     float sf = 0.f;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb)
@@ -177,7 +178,7 @@ constexpr bool weights_in_lds() {
   return feat_layout((int)sizeof(E), D, MB * 16, FWD, true, WG, true).end * (int)sizeof(E) + 64 <= kLdsMax;
 }
 
-template <typename E, int D, int MB>
+template <typename E, int D, int MB, int KIND>
 __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
   constexpr bool WL = weights_in_lds<E, D, MB, true, false>();
   const int b = blockIdx.z, h = blockIdx.y;
@@ -208,12 +209,15 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
   ldx.init(D, tid);
   const int g0 = blockIdx.x * p.groups;
   ldx.fetch(xsrc, g0 * TT, p.T);
-  for (int grp = 0; grp < p.groups; ++grp) {
+  // groups this workgroup owns (>= 1: the grid covers the tiles exactly)
+  const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
+  for (int grp = 0; grp < ng; ++grp) {
     const int t0 = (g0 + grp) * TT;
-    if (t0 >= p.T) break;  // uniform over the workgroup
     __syncthreads();       // weights staged; previous group's rows written out
     ldx.store(xs, L.xp);
-    if (grp + 1 < p.groups) ldx.fetch(xsrc, t0 + TT, p.T);
+    // the next group's rows (none after the last group: a bound of 0 loads
+    // nothing, and the prefetch registers take one path through the loop)
+    ldx.fetch(xsrc, t0 + TT, grp + 1 < ng ? p.T : 0);
     __syncthreads();
 
     const int row = w * 16 + l16;
@@ -227,7 +231,7 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
     floatx4 a[MB], hv[MB];
     gemm_a<E, D, MB>(w1, wp1, xs + w * 16 * L.xp, L.xp, l16, g, nfb, a);
     float rinv, mass;
-    feature_map<MB>(p, tau, a, nfb, hv, rinv, mass);
+    feature_map<KIND, MB>(p, tau, a, nfb, hv, rinv, mass);
     {
       E* prow = ps + row * L.mp;
 #pragma unroll
@@ -267,7 +271,7 @@ constexpr int wgrad_blocks() { return ((MB + 3) / 4) * (D / 16); }
 
 // Two resident waves per SIMD for the common bf16 widths: the allocator then
 // fits the backward in 256 registers without spilling.
-template <typename E, int D, int MB, bool WG, bool RESID>
+template <typename E, int D, int MB, bool WG, bool RESID, int KIND>
 __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)) void feature_bwd_kernel(FeatP p) {
   typedef LdsIO<E> IO;
   typedef TokFrag<E> TF;
@@ -326,18 +330,18 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
   ldp.fetch(psrc, g0 * TT, p.T);
   if (has_resid) ldr.fetch(rsrc, g0 * TT, p.T);
 
-  for (int grp = 0; grp < p.groups; ++grp) {
+  const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
+  for (int grp = 0; grp < ng; ++grp) {
     const int t0 = (g0 + grp) * TT;
-    if (t0 >= p.T) break;  // uniform over the workgroup
     __syncthreads();       // weights staged; previous group fully consumed
     ldx.store(xs, L.xp);
     ldp.store(ps, L.mp);
     if (has_resid) ldr.store(rs, L.xp);
-    if (grp + 1 < p.groups) {
-      ldx.fetch(xsrc, t0 + TT, p.T);
-      ldp.fetch(psrc, t0 + TT, p.T);
-      if (has_resid) ldr.fetch(rsrc, t0 + TT, p.T);
-    }
+    // next group's rows; a bound of 0 after the last group loads nothing
+    const int next_T = grp + 1 < ng ? p.T : 0;
+    ldx.fetch(xsrc, t0 + TT, next_T);
+    ldp.fetch(psrc, t0 + TT, next_T);
+    if (has_resid) ldr.fetch(rsrc, t0 + TT, next_T);
     __syncthreads();
 
     const int row = w * 16 + l16;
@@ -351,7 +355,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
     floatx4 a[MB], hv[MB];
     gemm_a<E, D, MB>(w1, wpa, xs + w * 16 * L.xp, L.xp, l16, g, nfb, a);
     float rinv, mass;
-    feature_map<MB>(p, tau, a, nfb, hv, rinv, mass);
+    feature_map<KIND, MB>(p, tau, a, nfb, hv, rinv, mass);
 
     // dh = rotate^T(dphi) (+ s W2^T dresid); rows past T are zero in LDS
     floatx4 dh[MB];
@@ -390,8 +394,9 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
     }
     sdh = sum_g(sdh);
     // dpre -> da (RMSNorm backward); dh becomes da
-    const bool ok = p.kind != TS_FEAT_RELU2 || mass > p.eps;
-    const float minv = rcp(mass);
+    // relu2: h = f / sum f with f = relu(pre)^2 (the uniform fallback below
+    // eps has no gradient); softmax: h = softmax(gain pre)
+    const float scale = KIND == TS_FEAT_RELU2 ? (mass > p.eps ? 2.0f * rcp(mass) : 0.f) : p.gain;
     float sdp = 0.f, sda = 0.f;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb) {
@@ -399,12 +404,10 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
       for (int i = 0; i < 4; ++i) {
         float dp = 0.f;
         if (fb < nfb) {
-          if (p.kind == TS_FEAT_RELU2) {
-            const float pre = a[fb][i] * rinv - tau;
-            dp = ok ? (dh[fb][i] - sdh) * minv * 2.0f * fmaxf(pre, 0.f) : 0.f;
-          } else {
-            dp = p.gain * hv[fb][i] * (dh[fb][i] - sdh);
-          }
+          if constexpr (KIND == TS_FEAT_RELU2)
+            dp = (dh[fb][i] - sdh) * scale * fmaxf(a[fb][i] * rinv - tau, 0.f);
+          else
+            dp = scale * hv[fb][i] * (dh[fb][i] - sdh);
         }
         dh[fb][i] = dp;
         sdp += dp;
@@ -553,48 +556,54 @@ using ts::fail;
 
 typedef void (*FeatFn)(ts::FeatP);
 
-template <typename E, int D, int MB>
-FeatFn pick3(bool fwd, bool wgrad, bool resid) {
-  if (fwd) return (FeatFn)ts::feature_fwd_kernel<E, D, MB>;
+template <typename E, int D, int MB, int KIND>
+FeatFn pick4(bool fwd, bool wgrad, bool resid) {
+  if (fwd) return (FeatFn)ts::feature_fwd_kernel<E, D, MB, KIND>;
   if (wgrad) {
     if constexpr (ts::wgrad_blocks<D, MB>() <= 8)
-      return resid ? (FeatFn)ts::feature_bwd_kernel<E, D, MB, true, true>
-                   : (FeatFn)ts::feature_bwd_kernel<E, D, MB, true, false>;
+      return resid ? (FeatFn)ts::feature_bwd_kernel<E, D, MB, true, true, KIND>
+                   : (FeatFn)ts::feature_bwd_kernel<E, D, MB, true, false, KIND>;
     return nullptr;
   }
-  return resid ? (FeatFn)ts::feature_bwd_kernel<E, D, MB, false, true>
-               : (FeatFn)ts::feature_bwd_kernel<E, D, MB, false, false>;
+  return resid ? (FeatFn)ts::feature_bwd_kernel<E, D, MB, false, true, KIND>
+               : (FeatFn)ts::feature_bwd_kernel<E, D, MB, false, false, KIND>;
+}
+
+template <typename E, int D, int MB>
+FeatFn pick3(int kind, bool fwd, bool wgrad, bool resid) {
+  return kind == TS_FEAT_RELU2 ? pick4<E, D, MB, TS_FEAT_RELU2>(fwd, wgrad, resid)
+                               : pick4<E, D, MB, TS_FEAT_SOFTMAX>(fwd, wgrad, resid);
 }
 
 // Kernels exist for head widths d in {16, 32, 64, 128} and feature widths
 // m in {16, 32, 64, 128, 256} (the feature-block count is a compile-time
 // constant, so no per-block predicates remain in the kernels).
 template <typename E, int D>
-FeatFn pick_mb(int m, bool fwd, bool wgrad, bool resid) {
+FeatFn pick_mb(int m, int kind, bool fwd, bool wgrad, bool resid) {
   switch (m) {
-    case 16: return pick3<E, D, 1>(fwd, wgrad, resid);
-    case 32: return pick3<E, D, 2>(fwd, wgrad, resid);
-    case 64: return pick3<E, D, 4>(fwd, wgrad, resid);
-    case 128: return pick3<E, D, 8>(fwd, wgrad, resid);
-    case 256: return pick3<E, D, 16>(fwd, wgrad, resid);
+    case 16: return pick3<E, D, 1>(kind, fwd, wgrad, resid);
+    case 32: return pick3<E, D, 2>(kind, fwd, wgrad, resid);
+    case 64: return pick3<E, D, 4>(kind, fwd, wgrad, resid);
+    case 128: return pick3<E, D, 8>(kind, fwd, wgrad, resid);
+    case 256: return pick3<E, D, 16>(kind, fwd, wgrad, resid);
   }
   return nullptr;
 }
 
 template <typename E>
-FeatFn pick_feature(int d, int m, bool fwd, bool wgrad, bool resid) {
+FeatFn pick_feature(int d, int m, int kind, bool fwd, bool wgrad, bool resid) {
   switch (d) {
-    case 16: return pick_mb<E, 16>(m, fwd, wgrad, resid);
-    case 32: return pick_mb<E, 32>(m, fwd, wgrad, resid);
-    case 64: return pick_mb<E, 64>(m, fwd, wgrad, resid);
-    case 128: return pick_mb<E, 128>(m, fwd, wgrad, resid);
+    case 16: return pick_mb<E, 16>(m, kind, fwd, wgrad, resid);
+    case 32: return pick_mb<E, 32>(m, kind, fwd, wgrad, resid);
+    case 64: return pick_mb<E, 64>(m, kind, fwd, wgrad, resid);
+    case 128: return pick_mb<E, 128>(m, kind, fwd, wgrad, resid);
   }
   return nullptr;
 }
 
 FeatFn pick(const ts_feature_desc* d, bool fwd, bool wgrad, bool resid = false) {
-  return d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, fwd, wgrad, resid)
-                             : pick_feature<float>(d->d, d->m, fwd, wgrad, resid);
+  return d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, d->kind, fwd, wgrad, resid)
+                             : pick_feature<float>(d->d, d->m, d->kind, fwd, wgrad, resid);
 }
 
 int check_feature_desc(const ts_feature_desc* d) {

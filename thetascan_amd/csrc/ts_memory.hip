@@ -266,9 +266,10 @@ int ts_memory_bwd(const ts_memory_desc* d, const ts_memory_io* io, const ts_memo
   if (rc) return rc;
   // dphi_k = reverse scan(v, dnum, phi_q); dv = reverse scan(phi_k, phi_q, dnum)
   // reads its segment states transposed (sum_i dnum_i phi_q_i^T)
-  if (!d->normalize && f.d == 64 && f.m == 64 && f.dtype == TS_BF16) {
-    // both in one pass over dnum and phi_q (the state updated once per tile)
-    const ts_scan_pair_io pio = {io->v, dnum, phq, phk, dphk, gr->dv};
+  if (f.d == 64 && f.m == 64 && f.dtype == TS_BF16) {
+    // both in one pass over dnum and phi_q (the state updated once per tile;
+    // the key-mass read adds dmass to the dk scan's scores)
+    const ts_scan_pair_io pio = {io->v, dnum, phq, phk, dphk, gr->dv, dmass};
     if ((rc = ts_scan_pair_fwd(&P.sdk, &pio, wsb, P.ws_b, stream))) return rc;
   } else {
     memset(&s, 0, sizeof(s));

@@ -595,15 +595,17 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 // score blocks stay in accumulators, and scan B reads the published state
 // copy transposed (ds_read_b64_tr_b16) instead of carrying S^T.  Each output
 // is computed in the order its own one-scan kernel uses.  Plain retention,
-// no ext columns, bf16, dk = dv = DK; segment states come from scan A's
-// summary and prefix passes.
+// bf16, dk = dv = DK; segment states come from scan A's summary and prefix
+// passes.  With KX, scan A carries the key-side ext pair of a normalized
+// read's backward (q_ext = ones, k_ext = dmass): score_a += ke_t and its
+// state gains the row u = sum_t ke_t v_t; scan B is unchanged.
 struct PairP {
   ScanP s;           // q = qa, k, v, out = out_a (and the segmentation)
   ts_strided qb, ob;
   uint32_t qb_rec, ob_rec;
 };
 
-template <int DK>
+template <int DK, bool KX>
 __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
   typedef bf16 E;
   typedef bf16x8 F8;
@@ -633,6 +635,8 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
   extern __shared__ __align__(16) unsigned char smem[];
   E* ebase = (E*)smem;
   E* st_base = ebase + L.stages * L.stage;
+  float* s_ext = (float*)smem + L.fbase;          // [stage][ke C | (unused) C]
+  float* s_u = s_ext + L.stages * 2 * C;          // [2][DK]
 
   const int64_t bh_q = (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
   const int64_t bh_b = (int64_t)b * pp.qb.sb + (int64_t)h * pp.qb.sh;
@@ -645,8 +649,9 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
   auto k_rsrc = [&]() { return make_rsrc((const E*)p.k.ptr + bh_k, p.k_rec); };
   auto v_rsrc = [&]() { return make_rsrc((const E*)p.v.ptr + bh_v, p.v_rec); };
 
-  // state: value block w of S, every key block
+  // state: value block w of S, every key block (and u over its columns)
   floatx4 S[NKB];
+  floatx4 us = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) S[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
   const int c_begin = seg * p.seg_chunks;
@@ -659,12 +664,17 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) S[kb][i] = src[(kb * 16 + 4 * g + i) * p.dvp + w * 16 + l16];
+    if (KX) {
+      const float u = src[DK * p.dvp + w * 16 + l16];
+      us = floatx4{u, u, u, u};
+    }
   }
   auto publish = [&](int bi) {
     E* st = st_base + bi * L.st;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
       IO::st4(st + (w * 16 + l16) * L.kp + kb * 16 + 4 * g, S[kb][0], S[kb][1], S[kb][2], S[kb][3]);
+    if (KX && g == 0) s_u[bi * DK + w * 16 + l16] = us[0];
   };
 
   const int nk_vec = C * (DK / VEC);
@@ -672,14 +682,18 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
   TileLoader<E, SLOTS_K> ldv;
   ldk.setup(p, DK / VEC, p.dk, L.kp, k_st_b, tid);
   ldv.setup(p, DK / VEC, p.dv, L.vp, v_st_b, tid);
+  float ke_r = 0.0f;  // this thread's ke of the fetched tile (wave 0)
   auto fetch = [&](int t0) {
     ldk.fetch(k_rsrc(), t0, sgn, k_st_b, wave_first, nk_vec);
     ldv.fetch(v_rsrc(), t0, sgn, v_st_b, wave_first, nk_vec);
+    if (KX && w == 0)
+      ke_r = bldf(make_rsrc(bh_base(p.ke, b, h, 4), p.ke_rec), row_off(p, t0, lane, (int)p.ke.st * 4));
   };
   auto store = [&](int stg) {
     E* base = ebase + stg * L.stage;
     ldk.store(base, wave_first, nk_vec);
     ldv.store(base + C * L.kp, wave_first, nk_vec);
+    if (KX && w == 0) s_ext[stg * 2 * C + lane] = ke_r;
   };
 
   // queries of this wave's block, for both scans
@@ -718,7 +732,10 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
     const E* Ks = ebase + (c & 1) * L.stage;
     const E* Vs = Ks + C * L.kp;
     const E* st = st_base + (c & 1) * L.st;
+    const float* ke_s = s_ext + (c & 1) * 2 * C;
+    const float* u_in = s_u + (c & 1) * DK;
     const int query = w * 16 + l16;
+    const float qe = t0 + query < p.T ? 1.0f : 0.0f;  // the ones column of scan A's queries
 
     // causal score blocks of this wave's queries against keys k (A) and v (B)
     floatx4 sa[4], sb[4];
@@ -732,11 +749,15 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
       for (int j = 0; j < NK32; ++j) sa[kb] = mma32(frow8<E>(Ks, L.kp, krow, j, g), qa[j], sa[kb]);
 #pragma unroll
       for (int j = 0; j < NK32; ++j) sb[kb] = mma32(frow8<E>(Vs, L.vp, krow, j, g), qb[j], sb[kb]);
+      floatx4 kev;
+      if (KX) kev = *(const floatx4*)(ke_s + kb * 16 + 4 * g);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = kb * 16 + 4 * g + i;
         const bool keep = kb < w || key <= query;
-        sa[kb][i] = keep ? sa[kb][i] : 0.0f;
+        float sv = sa[kb][i];
+        if (KX) sv += qe * kev[i];
+        sa[kb][i] = keep ? sv : 0.0f;
         sb[kb][i] = keep ? sb[kb][i] : 0.0f;
       }
     }
@@ -754,6 +775,11 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
       if (!state_zero) {
 #pragma unroll
         for (int j = 0; j < NK32; ++j) acc = mma32(frow8<E>(st, L.kp, vb * 16 + l16, j, g), qa[j], acc);
+        if (KX) {
+          const floatx4 u4 = *(const floatx4*)(u_in + vb * 16 + 4 * g);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] += qe * u4[i];
+        }
       }
       acc = mma32(TK::col8(Vs, L.vp, vb * 16, 0, lane), pa0, acc);
       if (w >= 2) acc = mma32(TK::col8(Vs, L.vp, vb * 16, 1, lane), pa1, acc);
@@ -785,6 +811,10 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) S[kb] = mma32(TK::col8(Ks, L.kp, kb * 16, kp, lane), av[kp], S[kb]);
+    if (KX) {
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) us = mma32(bcast8<E>(ke_s, 32 * kp, g), av[kp], us);
+    }
     state_zero = false;
     if (c + 1 < c_end) publish((c + 1) & 1);
     __syncthreads();
@@ -1113,9 +1143,14 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   int rc = compute_layout(d, &L);
   if (rc) return rc;
   if (!io) return fail(TS_ERR_VALUE, "scan pair: null io");
-  if (d->dtype != TS_BF16 || d->retention != TS_RET_NONE || L.kx || L.vx || d->out_mode != TS_OUT_STORE ||
+  // scan A may carry the key-side ext pair of a normalized read's backward
+  const bool kx = L.kx;
+  if (kx && (d->q_ext != TS_EXT_ONES || d->k_ext != TS_EXT_ARRAY))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan pair: the key-side ext pair must be q_ext ones, k_ext array");
+  if (d->dtype != TS_BF16 || d->retention != TS_RET_NONE || L.vx || d->out_mode != TS_OUT_STORE ||
       d->dk != 64 || d->dv != 64 || L.nvs != 1 || d->states_in || d->want_final || d->init_state)
     return fail(TS_ERR_NOT_IMPLEMENTED, "scan pair: bf16 plain scans of 64-wide keys and values only");
+  if (kx && !io->k_ext.ptr) return fail(TS_ERR_VALUE, "scan pair: missing k ext column");
   if (d->T == 0) return TS_OK;
   int rc2;
   if ((rc2 = check_stream("qa", io->qa, 8, true)) || (rc2 = check_stream("k", io->k, 8, true)) ||
@@ -1135,9 +1170,11 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   p.nchunks = L.nchunks; p.seg_chunks = L.seg_chunks; p.nseg = L.nseg; p.nsum = L.nsum; p.nelem = L.nelem;
   p.ret = TS_RET_NONE; p.reverse = d->reverse;
   p.q_ext = p.k_ext = p.v_ext = TS_EXT_NONE;
+  if (kx) { p.q_ext = TS_EXT_ONES; p.k_ext = TS_EXT_ARRAY; p.ke = io->k_ext; }
   p.out_mode = TS_OUT_STORE; p.out_scale = 1.0f;
   p.q = io->qa; p.k = io->k; p.v = io->v; p.out = io->out_a;
   pp.qb = io->qb; pp.ob = io->out_b;
+  if (kx && (rc = slice_bytes("k_ext", p.ke, d->T, 1, 4, &p.ke_rec))) return rc;
   if ((rc = slice_bytes("qa", p.q, d->T, d->dk, 2, &p.q_rec))) return rc;
   if ((rc = slice_bytes("k", p.k, d->T, d->dk, 2, &p.k_rec))) return rc;
   if ((rc = slice_bytes("v", p.v, d->T, d->dv, 2, &p.v_rec))) return rc;
@@ -1152,7 +1189,7 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   const ts::ScanLayout SL = ts::scan_layout(2, 64, 64, true);
   if (SL.nst != 2) return fail(TS_ERR_RUNTIME, "scan pair: unexpected state buffering");
   if (L.nsum > 0) {
-    KernelFn fsum = pick_kernel(true, 64, 1, false, ts::kPlain);
+    KernelFn fsum = pick_kernel(true, 64, 1, false, kx ? ts::kKeyExt : ts::kPlain);
     if ((rc = launch(fsum, dim3(L.nsum, bh, 1), (size_t)ts::scan_layout(2, 64, 64, false).bytes, stream, p))) return rc;
     ts::FinalP F{nullptr, nullptr, L.dkp, L.dvp, d->dk, d->dv, 0, 0};
     hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem / 4 + 255) / 256, bh), dim3(256), 0, stream, p.seg,
@@ -1160,7 +1197,8 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: prefix launch failed: %s", hipGetErrorString(e));
   }
-  hipLaunchKernelGGL(ts::pair_kernel<64>, dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
+  if (kx) hipLaunchKernelGGL((ts::pair_kernel<64, true>), dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
+  else hipLaunchKernelGGL((ts::pair_kernel<64, false>), dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: launch failed: %s", hipGetErrorString(e));
   return TS_OK;

@@ -32,8 +32,9 @@ extern "C" {
  * 9: ts_wcumsum takes a workspace (ts_wcumsum_workspace_bytes).
  * 10: the GN descriptors carry the hidden nonlinearity (and the write its
  *     damping);
- * 11: ts_scan_pair_io carries scan A's key-side ext column (k_ext). */
-#define TS_ABI_VERSION 11
+ * 11: ts_scan_pair_io carries scan A's key-side ext column (k_ext);
+ * 12: ts_retention_grad. */
+#define TS_ABI_VERSION 12
 
 enum ts_status {
   TS_OK = 0,
@@ -179,6 +180,41 @@ typedef struct ts_scan_pair_io {
 
 int ts_scan_pair_fwd(const ts_scan_desc* desc, const ts_scan_pair_io* io,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------ retention gradient */
+
+/* dL/dlog_alpha[h] of one causal scan with a static per-head retention,
+ *   o_t = sum_{i<=t} alpha^(t-i) <q_t, k_i> v_i  (+ the key-mass column),
+ * for upstream gradients dout (and dmass of the mass column):
+ *   out[b][h] = sum_t sum_{i<=t} (t-i) alpha^(t-i) <q_t, k_i> (<dout_t, v_i> + dmass_t).
+ * Summed pair by pair (bf16 operands, fp32 accumulation), not as
+ * sum_t t (q_t.dq_t - k_t.dk_t), whose terms cancel.  Replaces the retention
+ * gradient autograd forms through scan_chunk.py:102-155 (_static_weights /
+ * _tile_weights) for a learned static retention (block.py:647-681, the
+ * bank's fade_alpha).  Parallel over segments of seg_tiles 64-token tiles
+ * (0: automatic) with a combine pass for pairs across segments. */
+typedef struct ts_retention_desc {
+  int32_t B, H, T;
+  int32_t dk;           /* multiple of 16, <= 128 (split wider keys: the sum is additive) */
+  int32_t dv;           /* multiple of 8; value blocks + mass block <= 8 x 16 */
+  int32_t dtype;        /* TS_BF16 */
+  int32_t has_mass;     /* dmass given: the read's key-mass column */
+  int32_t seg_tiles;
+} ts_retention_desc;
+
+typedef struct ts_retention_io {
+  ts_strided q, k;      /* [B,H,T,dk] */
+  ts_strided v, dout;   /* [B,H,T,dv] */
+  ts_strided dmass;     /* fp32 [B,H,T] or NULL */
+  const float* log_alpha;  /* fp32 [H] */
+} ts_retention_io;
+
+/* Device workspace ts_retention_grad needs (16-byte aligned). */
+int ts_retention_workspace_bytes(const ts_retention_desc* desc, size_t* bytes);
+
+/* out: fp32 [B][H]. */
+int ts_retention_grad(const ts_retention_desc* desc, const ts_retention_io* io, float* out, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------ several retentions */
 

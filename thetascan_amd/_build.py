@@ -23,6 +23,7 @@ LIB_PATH = PACKAGE_DIR / LIB_NAME
 ARCH = "gfx950"
 
 SOURCES = ("ts_scan.hip", "ts_scan_views.hip", "ts_features.hip", "ts_elementwise.hip", "ts_maps.hip", "ts_gn.hip", "ts_memory.hip",
+           "ts_retention.hip",
            "ts_contract.hip")
 
 HIPCC_FLAGS = (

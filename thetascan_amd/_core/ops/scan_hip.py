@@ -346,6 +346,52 @@ def scan_pair_launch(qa: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qb: tor
     return out_a, out_b
 
 
+def retention_grad(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dout: torch.Tensor,
+                   dmass: torch.Tensor | None, log_alpha: torch.Tensor, seg_tiles: int = 0) -> torch.Tensor:
+    """dL/dlog_alpha [B,H] (fp32) of scan(q, k, v) with the static retention
+    ``log_alpha`` [H] (and the key-mass column when ``dmass`` is given), summed
+    pair by pair by ts_retention_grad; keys wider than 128 and values wider
+    than one call split into independent calls whose sums add."""
+    lib = _lib.load()
+    B, H, T, dk = q.shape
+    dv = v.shape[-1]
+    la = log_alpha.detach().to(torch.float32).reshape(H).contiguous()
+    dm = None if dmass is None else dmass.detach().to(torch.float32).contiguous()
+    total = torch.zeros(B, H, dtype=torch.float32, device=q.device)
+    dkw = -(-dk // 16) * 16
+    qk = [_kernel_view(q, dkw), _kernel_view(k.to(q.dtype), dkw)]
+    vwidth = -(-dv // 8) * 8
+    vv = _kernel_view(v.to(q.dtype), vwidth)
+    do = _kernel_view(dout.to(q.dtype), vwidth)
+    for k0 in range(0, dkw, 128):
+        qs, ks = qk[0][..., k0:k0 + 128], qk[1][..., k0:k0 + 128]
+        first = True
+        v0 = 0
+        while v0 < vwidth:
+            mass = first and dm is not None
+            # value blocks one call stages in LDS with its key width
+            blocks = 8 if qs.shape[-1] <= 64 else 5
+            width = min(vwidth - v0, 16 * (blocks - 1) if mass else 16 * blocks)
+            vs, ds = vv[..., v0:v0 + width], do[..., v0:v0 + width]
+            desc = _lib.RetentionDesc(B, H, T, qs.shape[-1], width, _lib.dtype_code(q.dtype), int(mass),
+                                      int(seg_tiles))
+            nbytes = ctypes.c_size_t()
+            _lib.check(lib.ts_retention_workspace_bytes(ctypes.byref(desc), ctypes.byref(nbytes)),
+                       "ts_retention_workspace_bytes")
+            work = torch.empty(nbytes.value, dtype=torch.uint8, device=q.device)
+            out = torch.empty(B, H, dtype=torch.float32, device=q.device)
+            io = _lib.RetentionIO(_lib.strided(qs), _lib.strided(ks), _lib.strided(vs), _lib.strided(ds),
+                                  _lib.strided(dm if mass else None), la.data_ptr())
+            with _lib.timed("ts_retention_grad", lambda: _lib.nbytes(qs, ks, vs, ds)):
+                status = lib.ts_retention_grad(ctypes.byref(desc), ctypes.byref(io), out.data_ptr(), work.data_ptr(),
+                                               nbytes.value, _lib.stream_handle(q.device))
+            _lib.check(status, "ts_retention_grad")
+            total += out
+            first = False
+            v0 += width
+    return total
+
+
 def views_eligible(q: torch.Tensor, v: torch.Tensor, kinds) -> bool:
     """Whether ts_scan_views_fwd serves these views (bf16 on the GPU, 2..3
     retentions that are none or static, dk <= 128, dv <= 64)."""
@@ -556,7 +602,11 @@ def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: b
         mass_ext = dm is not None
         q_ext = dm.to(torch.float32) if mass_ext else None
         want_r = r is not None and need_r[j]
-        if want_r:
+        # a bf16 static retention's gradient is summed pair by pair
+        # (ts_retention_grad: no cancellation); the other retention gradients
+        # come from fp32 scans
+        pairwise = want_r and kind == _lib.RET_STATIC and q.dtype == torch.bfloat16
+        if want_r and not pairwise:
             # dL_t = q_t.dq_t - k_t.dk_t sums to zero over t, and the
             # retention gradient (sum_t t dL_t, or a suffix sum of dL) is a
             # small difference of large terms: bf16 rounding of the score
@@ -575,7 +625,7 @@ def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: b
             dq[..., : dq_j.shape[-1]] += dq_j
             dkk[..., : dk_j.shape[-1]] += dk_j
         else:
-            r_grads.append(None)
+            r_grads.append(retention_grad(q, k, v, dO, dm, r).sum(0).to(r.dtype).view_as(r) if pairwise else None)
             if need_q:
                 scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
                             out=dq, out_mode=_lib.OUT_ACCUM_F32)

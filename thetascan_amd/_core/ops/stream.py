@@ -40,12 +40,16 @@ class Carry:
 
 
 def active() -> Carry | None:
+    """The carry of the current call (None outside one, and in a traced
+    forward: continuation is an eager, no-autograd mode)."""
+    if torch.compiler.is_compiling():
+        return None
     return _ACTIVE.get()
 
 
 def position() -> int:
     """Absolute position of the current call's first token (0 outside a carry)."""
-    carry = _ACTIVE.get()
+    carry = active()
     return 0 if carry is None else carry.position
 
 

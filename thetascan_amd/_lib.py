@@ -401,6 +401,14 @@ class MemoryGrads(ctypes.Structure):
     ]
 
 
+class RetentionDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "dk", "dv", "dtype", "has_mass", "seg_tiles")]
+
+
+class RetentionIO(ctypes.Structure):
+    _fields_ = [(n, Strided) for n in ("q", "k", "v", "dout", "dmass")] + [("log_alpha", ctypes.c_void_p)]
+
+
 FEAT_RELU2 = 0
 FEAT_SOFTMAX = 1
 
@@ -489,7 +497,10 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_void_p]
         lib.ts_memory_bwd.argtypes = [P(MemoryDesc), P(MemoryIO), P(MemoryGrads), ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 11:
+        lib.ts_retention_workspace_bytes.argtypes = [P(RetentionDesc), P(ctypes.c_size_t)]
+        lib.ts_retention_grad.argtypes = [P(RetentionDesc), P(RetentionIO), ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_void_p]
+        if lib.ts_abi_version() != 12:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

@@ -3,8 +3,9 @@ GPU tests) against float64 autograd of the tiled oracle scan.
 
 dL/dlog_alpha = sum_t sum_{i<=t} (t-i) alpha^(t-i) (q_t.k_i)(dO_t.v_i + dm_t):
 checked for ragged and tile-multiple T, one and several segments, key widths
-that split (192 = 128 + 64), value widths with and without the key-mass
-column, against the oracle at rel 2e-3 per head (bf16 inputs; the kernel's
+with a 16-wide tail block (16, 48, 80) and without, key widths that split
+(192 = 128 + 64), value widths up to eight 16-column blocks per call and
+wider ones that split (200), with and without the key-mass column, against the oracle at rel 2e-3 per head (bf16 inputs; the kernel's
 own operands are hi/lo bf16 pairs), and through the bank
 mixer's backward at T=4096, where the former sum_t t (q.dq - k.dk) in bf16
 was 16% off.
@@ -35,6 +36,7 @@ def _oracle_grad(q, k, v, dO, dm, la):
 @pytest.mark.parametrize("T,dk,dv,mass,seg_tiles", [
     (1, 64, 64, False, 0), (63, 64, 64, True, 0), (64, 32, 16, True, 1), (65, 64, 64, True, 1),
     (300, 128, 64, True, 2), (300, 192, 80, False, 0), (1000, 64, 64, True, 0), (4096, 64, 64, True, 0),
+    (130, 48, 112, True, 1), (200, 16, 200, True, 0), (129, 128, 120, False, 1), (777, 80, 56, True, 3),
 ])
 def test_retention_grad_matches_float64_autograd(cuda, T, dk, dv, mass, seg_tiles):
     from thetascan_amd._core.ops import scan_hip

@@ -369,8 +369,8 @@ def retention_grad(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dout: torc
         v0 = 0
         while v0 < vwidth:
             mass = first and dm is not None
-            # value blocks one call stages in LDS with its key width
-            blocks = 8 if qs.shape[-1] <= 64 else 5
+            # one wave per 16 value columns, at most eight per call
+            blocks = 8
             width = min(vwidth - v0, 16 * (blocks - 1) if mass else 16 * blocks)
             vs, ds = vv[..., v0:v0 + width], do[..., v0:v0 + width]
             desc = _lib.RetentionDesc(B, H, T, qs.shape[-1], width, _lib.dtype_code(q.dtype), int(mass),

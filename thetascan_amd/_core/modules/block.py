@@ -37,6 +37,9 @@ _EXPANSION_FINGERPRINT_SCHEMA_VERSION = 1
 
 FUSED_HEAD_DIMS = (16, 32, 64, 128)
 FUSED_FEATURE_WIDTHS = (16, 32, 64, 128, 256)
+# widths the chunked feature kernels take: bf16 streams, head widths 32 and 64
+WIDE_FEATURE_WIDTHS = (192, 384)
+WIDE_HEAD_DIMS = (32, 64)
 
 
 def _inverse_softplus(value: float) -> float:
@@ -361,6 +364,8 @@ class ThetaScan(nn.Module):
         (the one-call sum path or the multi-view path)."""
         if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float32):
             return False
+        if self.cfg.mem_hidden in WIDE_FEATURE_WIDTHS and x.dtype != torch.bfloat16:
+            return False
         return self._views_cfg
 
     def _config_views_eligible(self) -> bool:
@@ -376,7 +381,8 @@ class ThetaScan(nn.Module):
             return False
         if cfg.read_norm and cfg.read_norm_mode != "key_mass":
             return False
-        if cfg.head_dim not in FUSED_HEAD_DIMS or cfg.mem_hidden not in FUSED_FEATURE_WIDTHS:
+        wide = cfg.mem_hidden in WIDE_FEATURE_WIDTHS and cfg.head_dim in WIDE_HEAD_DIMS
+        if cfg.head_dim not in FUSED_HEAD_DIMS or (cfg.mem_hidden not in FUSED_FEATURE_WIDTHS and not wide):
             return False
         rot_in = rotated_width(cfg.head_dim, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "input" else 0
         rot_feat = rotated_width(cfg.mem_hidden, cfg.rope, cfg.rope_frac) if cfg.rope_placement == "feature" else 0
@@ -392,10 +398,11 @@ class ThetaScan(nn.Module):
     def _config_fused_eligible(self) -> bool:
         """The one-call sum path (ts_memory_fwd / ts_memory_bwd between the
         stacked projection and the output projection): a views-eligible memory
-        with the plain sum and the stacked qkv projection."""
+        with the plain sum and the stacked qkv projection, at a feature width
+        with in-kernel weight-gradient partials."""
         cfg = self.cfg
         return not (cfg.read_fade or cfg.accumulation != "sum" or cfg.share_kq or cfg.key_value_heads is not None
-                    or cfg.value_mlp_mult > 0)
+                    or cfg.value_mlp_mult > 0 or cfg.mem_hidden in WIDE_FEATURE_WIDTHS)
 
     def _make_feature_spec(self):
         cfg = self.cfg

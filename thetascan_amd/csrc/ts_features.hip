@@ -547,6 +547,427 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
   }
 }
 
+
+// ------------------------------------------------------------------ wide maps
+//
+// Feature widths of 192 and 384 (bf16, head widths 32 and 64): the per-lane
+// feature arrays of the kernels above would not fit in registers, so these
+// walk the feature axis 64 features at a time, re-forming the chunk's
+// a^T = W1 xn^T on MFMA in every pass that needs it (RMSNorm sum, mass or
+// softmax max/sum, then h; in the backward dh . h, sum dp and dp . a, then
+// da).  W1 (and W2) are staged in LDS once per workgroup; W1^T and W2^T
+// operands are transposing LDS reads of the staged rows.  The backward
+// writes da, xn, h and dtau per token for the weight-gradient GEMMs (no
+// fused weight-gradient partials at these widths).
+
+struct WideLayout {
+  int xp, cp, mp;
+  int xs, cs, rs, os, w1, w2;  // element offsets
+  int end;
+};
+
+__host__ __device__ constexpr WideLayout wide_layout(int d, int m, bool fwd, bool resid) {
+  WideLayout L{};
+  L.xp = d + 8;
+  L.cp = 64 + 8;
+  L.mp = m + 8;
+  int off = 0;
+  L.xs = off; off += TT * L.xp;
+  L.cs = L.rs = L.os = -1;
+  if (fwd) {
+    L.cs = off; off += TT * L.cp;
+  } else {
+    if (resid) { L.rs = off; off += TT * L.xp; }
+    L.os = off; off += TT * L.xp;
+  }
+  L.w1 = off; off += m * L.xp;
+  L.w2 = -1;
+  if (resid) { L.w2 = off; off += d * L.mp; }
+  L.end = off;
+  return L;
+}
+
+// a^T of feature chunk c (blocks 4c..4c+3) for this wave's 16 tokens.
+template <int D>
+__device__ __forceinline__ void wide_a(const bf16* w1s, int xp, const bf16* xs_w, int c, int l16, int g, floatx4* a) {
+  gemm_a<bf16, D, 4>(w1s + c * 64 * xp, xp, xs_w, xp, l16, g, 4, a);
+}
+
+// Per-token statistics over the whole width: rinv (RMSNorm) and the
+// normalizer (ReLU^2 mass, or the softmax max mx and sum).
+template <int D, int KIND, int NC>
+__device__ __forceinline__ void wide_stats(const FeatP& p, float tau, const bf16* w1s, int xp, const bf16* xs_w,
+                                           int l16, int g, float& rinv, float& mass, float& mx) {
+  float ss = 0.f;
+#pragma unroll 1
+  for (int c = 0; c < NC; ++c) {
+    floatx4 a[4];
+    wide_a<D>(w1s, xp, xs_w, c, l16, g, a);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss += a[f][i] * a[f][i];
+  }
+  rinv = rsqrtf(sum_g(ss) * p.inv_m + p.eps);
+  mx = 0.f;
+  if constexpr (KIND == TS_FEAT_RELU2) {
+    float sf = 0.f;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4];
+      wide_a<D>(w1s, xp, xs_w, c, l16, g, a);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pre = fmaxf(a[f][i] * rinv - tau, 0.f);
+          sf += pre * pre;
+        }
+    }
+    mass = sum_g(sf);
+  } else {
+    float m_ = -INFINITY;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4];
+      wide_a<D>(w1s, xp, xs_w, c, l16, g, a);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m_ = fmaxf(m_, p.gain * (a[f][i] * rinv - tau));
+    }
+    mx = max_g(m_);
+    float se = 0.f;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4];
+      wide_a<D>(w1s, xp, xs_w, c, l16, g, a);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) se += __expf(p.gain * (a[f][i] * rinv - tau) - mx);
+    }
+    mass = sum_g(se);
+  }
+}
+
+// h of one chunk from its a and the statistics.
+template <int KIND>
+__device__ __forceinline__ void wide_h(const FeatP& p, float tau, const floatx4* a, float rinv, float mass, float mx,
+                                       floatx4* hc) {
+  if constexpr (KIND == TS_FEAT_RELU2) {
+    const bool ok = mass > p.eps;
+    const float inv = ok ? rcp(mass) : 0.f;
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pre = fmaxf(a[f][i] * rinv - tau, 0.f);
+        hc[f][i] = ok ? pre * pre * inv : p.inv_m;
+      }
+  } else {
+    const float inv = rcp(mass);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hc[f][i] = __expf(p.gain * (a[f][i] * rinv - tau) - mx) * inv;
+  }
+}
+
+template <int D, int MB, int KIND>
+__global__ __launch_bounds__(256) void feature_fwd_wide_kernel(FeatP p) {
+  typedef bf16 E;
+  typedef LdsIO<E> IO;
+  constexpr int NC = MB / 4;
+  constexpr int m = MB * 16;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const bool want_resid = p.resid.ptr != nullptr;
+  const WideLayout L = wide_layout(D, m, true, want_resid);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* cs = base + L.cs;
+  E* w1s = base + L.w1;
+  E* w2s = base + L.w2;
+  stage_matrix<E>((const E*)p.w1 + (size_t)h * m * D, m, D, w1s, L.xp, tid);
+  if (want_resid) stage_matrix<E>((const E*)p.w2 + (size_t)h * D * m, D, m, w2s, L.mp, tid);
+  const float tau = p.has_tau ? p.tau[h] : 0.f;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  const Rows<E> phi = rows_of<E>(p.phi, b, h);
+
+  RowTile<E, D> ldx;
+  ldx.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
+  for (int grp = 0; grp < ng; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    __syncthreads();  // weights staged; previous group's rows written out
+    ldx.store(xs, L.xp);
+    ldx.fetch(xsrc, t0 + TT, grp + 1 < ng ? p.T : 0);
+    __syncthreads();
+
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    E* xrow = xs + row * L.xp;
+    const E* xs_w = xs + w * 16 * L.xp;
+    float xr[D / 16][4];
+    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
+    __syncthreads();  // xn rows complete before they feed the MFMA
+
+    float rinv, mass, mx;
+    wide_stats<D, KIND, NC>(p, tau, w1s, L.xp, xs_w, l16, g, rinv, mass, mx);
+    floatx4 rb[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) rb[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], hc[4];
+      wide_a<D>(w1s, L.xp, xs_w, c, l16, g, a);
+      wide_h<KIND>(p, tau, a, rinv, mass, mx, hc);
+      if (want_resid) {
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+          const E* wrow = w2s + (db * 16 + l16) * L.mp + c * 64;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+            rb[db] = mma32(IO::cat(IO::ld4(wrow + 32 * jj + 4 * g), IO::ld4(wrow + 32 * jj + 16 + 4 * g)),
+                           IO::from_acc(hc[2 * jj], hc[2 * jj + 1]), rb[db]);
+        }
+      }
+      E* crow = cs + row * L.cp;
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float v[4] = {hc[f][0], hc[f][1], hc[f][2], hc[f][3]};
+        const int col = c * 64 + f * 16 + 4 * g;
+        if (p.feat_rot > 0) rope4(v, col, p.feat_rot, p.f_cos, p.f_sin, t, valid && col < p.feat_rot, false);
+        st4f<E>(crow + f * 16 + 4 * g, v);
+      }
+      __syncthreads();
+      write_rows<E>(cs, L.cp, Rows<E>{phi.base + c * 64, phi.st}, t0, p.T, 64, tid);
+      __syncthreads();
+    }
+    if (want_resid) {
+      const float inv = rcp(fmaxf(nrm, p.eps));
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = xr[db][i] * inv + p.s * rb[db][i];
+        st4f<E>(xrow + db * 16 + 4 * g, v);
+      }
+      __syncthreads();
+      write_rows<E>(xs, L.xp, rows_of<E>(p.resid, b, h), t0, p.T, D, tid);
+    }
+  }
+}
+
+template <int D, int MB, bool RESID, int KIND>
+__global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
+  typedef bf16 E;
+  typedef LdsIO<E> IO;
+  typedef TokFrag<E> TF;
+  constexpr int NC = MB / 4;
+  constexpr int m = MB * 16;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const WideLayout L = wide_layout(D, m, false, RESID);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* rs = base + L.rs;
+  E* os = base + L.os;
+  E* w1s = base + L.w1;
+  E* w2s = base + L.w2;
+  stage_matrix<E>((const E*)p.w1 + (size_t)h * m * D, m, D, w1s, L.xp, tid);
+  if (RESID) stage_matrix<E>((const E*)p.w2 + (size_t)h * D * m, D, m, w2s, L.mp, tid);
+  const float tau = p.has_tau ? p.tau[h] : 0.f;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  const Rows<E> rsrc = rows_of<E>(p.dresid, b, h);
+  const Rows<E> psrc = rows_of<E>(p.dphi, b, h);
+
+  RowTile<E, D> ldx, ldr;
+  ldx.init(D, tid);
+  ldr.init(RESID ? D : 0, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  if (RESID) ldr.fetch(rsrc, g0 * TT, p.T);
+  const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
+  for (int grp = 0; grp < ng; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    __syncthreads();  // weights staged; previous group fully consumed
+    ldx.store(xs, L.xp);
+    if (RESID) ldr.store(rs, L.xp);
+    const int next_T = grp + 1 < ng ? p.T : 0;
+    ldx.fetch(xsrc, t0 + TT, next_T);
+    if (RESID) ldr.fetch(rsrc, t0 + TT, next_T);
+    __syncthreads();
+
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const E* prow = psrc.at(valid ? t : 0);
+    E* xrow = xs + row * L.xp;
+    const E* xs_w = xs + w * 16 * L.xp;
+    float xr[D / 16][4];
+    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
+    __syncthreads();  // xn rows complete before they feed the MFMA
+
+    float rinv, mass, mx;
+    wide_stats<D, KIND, NC>(p, tau, w1s, L.xp, xs_w, l16, g, rinv, mass, mx);
+    const E* rrow = rs + row * L.xp;
+    // a, h and dh = rotate^T(dphi) + s W2^T dresid of chunk c
+    auto chunk = [&](int c, floatx4* a, floatx4* hc, floatx4* dh) {
+      uint2 dpr[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        dpr[f] = valid ? *(const uint2*)(prow + c * 64 + f * 16 + 4 * g) : make_uint2(0u, 0u);
+      wide_a<D>(w1s, L.xp, xs_w, c, l16, g, a);
+      wide_h<KIND>(p, tau, a, rinv, mass, mx, hc);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        dh[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (RESID) {
+#pragma unroll
+          for (int kk = 0; kk < D / 32; ++kk)
+            dh[f] = mma32(TF::get(w2s, L.mp, c * 64 + f * 16, kk, lane),
+                          IO::cat(IO::ld4(rrow + 32 * kk + 4 * g), IO::ld4(rrow + 32 * kk + 16 + 4 * g)), dh[f]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dh[f][i] *= p.s;
+        }
+        float v[4] = {__uint_as_float(dpr[f].x << 16), __uint_as_float(dpr[f].x & 0xffff0000u),
+                      __uint_as_float(dpr[f].y << 16), __uint_as_float(dpr[f].y & 0xffff0000u)};
+        const int col = c * 64 + f * 16 + 4 * g;
+        if (p.feat_rot > 0) rope4(v, col, p.feat_rot, p.f_cos, p.f_sin, t, valid && col < p.feat_rot, true);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dh[f][i] += v[i];
+      }
+    };
+    // pass 1: sdh = dh . h
+    float sdh = 0.f;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], hc[4], dh[4];
+      chunk(c, a, hc, dh);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sdh += dh[f][i] * hc[f][i];
+    }
+    sdh = sum_g(sdh);
+    const float scale = KIND == TS_FEAT_RELU2 ? (mass > p.eps ? 2.0f * rcp(mass) : 0.f) : p.gain;
+    // dp of a chunk (left in dh)
+    auto dp_of = [&](const floatx4* a, const floatx4* hc, floatx4* dh) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (KIND == TS_FEAT_RELU2)
+            dh[f][i] = (dh[f][i] - sdh) * scale * fmaxf(a[f][i] * rinv - tau, 0.f);
+          else
+            dh[f][i] = scale * hc[f][i] * (dh[f][i] - sdh);
+        }
+    };
+    // pass 2: sum dp, dp . a
+    float sdp = 0.f, sda = 0.f;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], hc[4], dh[4];
+      chunk(c, a, hc, dh);
+      dp_of(a, hc, dh);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sdp += dh[f][i];
+          sda += dh[f][i] * a[f][i];
+        }
+    }
+    sdp = sum_g(sdp);
+    sda = sum_g(sda);
+    if (g == 0 && valid && p.dtau.ptr) *rows_of<float>(p.dtau, b, h).at(t) = -sdp;
+    const float c3 = rinv * rinv * rinv * sda * p.inv_m;
+    // pass 3: da = rinv dp - c3 a per chunk -> dxn^T += W1^T da^T; da and h out
+    floatx4 dxn[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) dxn[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    E* da_out = valid && p.da.ptr ? rows_of<E>(p.da, b, h).at(t) : nullptr;
+    E* h_out = valid && p.h.ptr ? rows_of<E>(p.h, b, h).at(t) : nullptr;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], hc[4], da[4];
+      chunk(c, a, hc, da);
+      dp_of(a, hc, da);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) da[f][i] = rinv * da[f][i] - c3 * a[f][i];
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          dxn[db] = mma32(TF::get(w1s + c * 64 * L.xp, L.xp, db * 16, jj, lane),
+                          IO::from_acc(da[2 * jj], da[2 * jj + 1]), dxn[db]);
+      if (da_out) {
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          float v[4] = {da[f][0], da[f][1], da[f][2], da[f][3]};
+          st4f<E>(da_out + c * 64 + f * 16 + 4 * g, v);
+        }
+      }
+      if (h_out) {
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          float u[4] = {hc[f][0], hc[f][1], hc[f][2], hc[f][3]};
+          st4f<E>(h_out + c * 64 + f * 16 + 4 * g, u);
+        }
+      }
+    }
+    if (valid && p.xn.ptr) {
+      E* xn_out = rows_of<E>(p.xn, b, h).at(t);
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float v[4];
+        ld4f<E>(xrow + db * 16 + 4 * g, v);
+        st4f<E>(xn_out + db * 16 + 4 * g, v);
+      }
+    }
+    // residual path, L2-norm backward, input-RoPE backward at dims 16db+4g+i
+    const float inv = rcp(fmaxf(nrm, p.eps));
+    float dot = 0.f;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      if (RESID) {
+        float r[4];
+        ld4f<E>(rrow + db * 16 + 4 * g, r);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dxn[db][i] += r[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dot += dxn[db][i] * xr[db][i];
+    }
+    dot = sum_g(dot) * inv * inv;
+    {
+      const bool big = nrm > p.eps;
+      const float sc = big ? rcp(nrm) : rcp(p.eps);
+      E* orow = os + row * L.xp;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (big ? dxn[db][i] - xr[db][i] * dot : dxn[db][i]) * sc;
+        if (p.in_rot > 0)
+          rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, true);
+        st4f<E>(orow + db * 16 + 4 * g, v);
+      }
+    }
+    __syncthreads();  // dx rows of all four waves complete
+    write_rows<E>(os, L.xp, rows_of<E>(p.dx, b, h), t0, p.T, D, tid);
+  }
+}
+
 }  // namespace ts
 
 // ============================================================== host side
@@ -601,7 +1022,40 @@ FeatFn pick_feature(int d, int m, int kind, bool fwd, bool wgrad, bool resid) {
   return nullptr;
 }
 
+// Feature widths the wide kernels take (bf16, head widths 32 and 64).
+bool is_wide(const ts_feature_desc* d) { return d->m == 192 || d->m == 384; }
+
+template <int D, int MB, int KIND>
+FeatFn pick_wide4(bool fwd, bool resid) {
+  if (fwd) return (FeatFn)ts::feature_fwd_wide_kernel<D, MB, KIND>;
+  return resid ? (FeatFn)ts::feature_bwd_wide_kernel<D, MB, true, KIND>
+               : (FeatFn)ts::feature_bwd_wide_kernel<D, MB, false, KIND>;
+}
+
+template <int D, int MB>
+FeatFn pick_wide3(int kind, bool fwd, bool resid) {
+  return kind == TS_FEAT_RELU2 ? pick_wide4<D, MB, TS_FEAT_RELU2>(fwd, resid)
+                               : pick_wide4<D, MB, TS_FEAT_SOFTMAX>(fwd, resid);
+}
+
+template <int D>
+FeatFn pick_wide2(int m, int kind, bool fwd, bool resid) {
+  switch (m) {
+    case 192: return pick_wide3<D, 12>(kind, fwd, resid);
+    case 384: return pick_wide3<D, 24>(kind, fwd, resid);
+  }
+  return nullptr;
+}
+
 FeatFn pick(const ts_feature_desc* d, bool fwd, bool wgrad, bool resid = false) {
+  if (is_wide(d)) {
+    if (d->dtype != TS_BF16 || wgrad) return nullptr;
+    switch (d->d) {
+      case 32: return pick_wide2<32>(d->m, d->kind, fwd, resid);
+      case 64: return pick_wide2<64>(d->m, d->kind, fwd, resid);
+    }
+    return nullptr;
+  }
   return d->dtype == TS_BF16 ? pick_feature<ts::bf16>(d->d, d->m, d->kind, fwd, wgrad, resid)
                              : pick_feature<float>(d->d, d->m, d->kind, fwd, wgrad, resid);
 }
@@ -612,8 +1066,10 @@ int check_feature_desc(const ts_feature_desc* d) {
   if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "feature: unknown dtype");
   if (d->kind != TS_FEAT_RELU2 && d->kind != TS_FEAT_SOFTMAX)
     return fail(TS_ERR_NOT_IMPLEMENTED, "feature: kind %d has no fused kernel", d->kind);
-  if (d->m != 16 && d->m != 32 && d->m != 64 && d->m != 128 && d->m != 256)
+  if (d->m != 16 && d->m != 32 && d->m != 64 && d->m != 128 && d->m != 256 && !is_wide(d))
     return fail(TS_ERR_NOT_IMPLEMENTED, "feature: no fused kernel for feature width m=%d", d->m);
+  if (is_wide(d) && (d->dtype != TS_BF16 || (d->d != 32 && d->d != 64)))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature: width m=%d runs in bf16 with head width 32 or 64", d->m);
   if (d->in_rot < 0 || d->in_rot > d->d || d->in_rot % 4)
     return fail(TS_ERR_VALUE, "feature: input rotation must be a multiple of 4 within d");
   if (d->feat_rot < 0 || d->feat_rot > d->m || d->feat_rot % 4)
@@ -670,7 +1126,8 @@ int plan_feature(const ts_feature_desc* d, bool fwd, bool resid, bool want_wgrad
   const int es = d->dtype == TS_BF16 ? 2 : 4;
   P->wgrad = !fwd && want_wgrad && pick(d, false, true) != nullptr &&
              lds_bytes(es, d->d, d->m, fwd, resid, true) <= (size_t)ts::kLdsMax;
-  P->lds = lds_bytes(es, d->d, d->m, fwd, resid, P->wgrad);
+  P->lds = is_wide(d) ? (size_t)ts::wide_layout(d->d, d->m, fwd, resid).end * es
+                      : lds_bytes(es, d->d, d->m, fwd, resid, P->wgrad);
   if (P->lds > (size_t)ts::kLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "feature: tiles need %zu bytes of LDS", P->lds);
   const int tiles = (d->T + ts::TT - 1) / ts::TT;
   const long target = fwd ? 1024 : 512;
@@ -740,7 +1197,7 @@ int ts_feature_bwd_transposed(const ts_feature_desc* d, int32_t has_dresid, int3
   if (rc) return rc;
   Plan P;
   if ((rc = plan_feature(d, false, has_dresid != 0, fused_wgrad != 0, &P))) return rc;
-  if (needed) *needed = kernel_wl(d->dtype == TS_BF16 ? 2 : 4, d->d, d->m, false, P.wgrad) ? 0 : 1;
+  if (needed) *needed = is_wide(d) || kernel_wl(d->dtype == TS_BF16 ? 2 : 4, d->d, d->m, false, P.wgrad) ? 0 : 1;
   return TS_OK;
 }
 
@@ -773,8 +1230,11 @@ int ts_feature_bwd(const ts_feature_desc* d, const ts_feature_bwd_io* io, hipStr
     return fail(TS_ERR_VALUE, "feature bwd: fused weight gradients with dresid need dw2_part");
   if (want_wgrad && d->has_tau && !io->dtau_part)
     return fail(TS_ERR_VALUE, "feature bwd: fused weight gradients with tau need dtau_part");
-  if (!kernel_wl(es, d->d, d->m, false, P.wgrad) && (!io->w1t || (io->dresid.ptr && !io->w2t)))
+  if (is_wide(d)) {
+    if (io->dresid.ptr && !io->w2) return fail(TS_ERR_VALUE, "feature bwd: width m=%d with dresid needs w2", d->m);
+  } else if (!kernel_wl(es, d->d, d->m, false, P.wgrad) && (!io->w1t || (io->dresid.ptr && !io->w2t))) {
     return fail(TS_ERR_VALUE, "feature bwd: weights too large for LDS need w1t (and w2t)");
+  }
   if (d->T == 0) return TS_OK;
   p.w1 = io->w1; p.w1t = io->w1t; p.w2t = io->w2t; p.w2 = io->w2; p.tau = io->tau;
   p.in_cos = io->in_cos; p.in_sin = io->in_sin; p.f_cos = io->f_cos; p.f_sin = io->f_sin;

@@ -36,7 +36,7 @@ def _case(B, H, T, d, m, learn_thresh, seed, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("d,m,learn_thresh,T", [(16, 48, False, 70), (64, 128, False, 150), (32, 96, True, 64),
-                                               (16, 16, True, 33), (128, 64, False, 40)])
+                                               (16, 16, True, 33), (128, 64, False, 40), (64, 192, True, 90)])
 def test_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T):
     from thetascan_amd._core.ops import gn
 
@@ -84,7 +84,8 @@ def test_gn_write_rejects_unsupported_widths(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("d,m,learn_thresh,T", [(16, 48, True, 70), (64, 128, False, 130), (32, 96, False, 64)])
+@pytest.mark.parametrize("d,m,learn_thresh,T", [(16, 48, True, 70), (64, 128, False, 130), (32, 96, False, 64),
+                                               (64, 192, True, 90)])
 def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T):
     """Stage without a correction: h and q + s W2 h are the oracle's
     block_forward (engine.py:117-158) of the query, gradients included."""

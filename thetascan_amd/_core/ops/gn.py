@@ -22,7 +22,7 @@ ACTS = {"relu2": _lib.GN_RELU2, "tanh": _lib.GN_TANH}  # hidden nonlinearities t
 
 
 def supported_width(m: int) -> bool:
-    return m == 256 or (16 <= m <= 128 and m % 16 == 0)
+    return m in (192, 256) or (16 <= m <= 128 and m % 16 == 0)
 
 
 def eligible(cfg, weights, k: torch.Tensor, v: torch.Tensor) -> bool:

@@ -737,8 +737,8 @@ int check_gn(const ts_gn_desc* d) {
   if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "gn: unknown dtype");
   if (d->d != 16 && d->d != 32 && d->d != 64 && d->d != 128)
     return fail(TS_ERR_NOT_IMPLEMENTED, "gn: head width %d (16, 32, 64 or 128)", d->d);
-  if (d->m < 16 || d->m % 16 || (d->m > 128 && d->m != 256))
-    return fail(TS_ERR_NOT_IMPLEMENTED, "gn: hidden width %d (a multiple of 16 up to 128, or 256)", d->m);
+  if (d->m < 16 || d->m % 16 || (d->m > 128 && d->m != 192 && d->m != 256))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "gn: hidden width %d (a multiple of 16 up to 128, 192 or 256)", d->m);
   if (d->H > 65535 || d->B > 65535) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: grid too large");
   if (d->act != TS_GN_RELU2 && d->act != TS_GN_TANH) return fail(TS_ERR_VALUE, "gn: unknown nonlinearity %d", d->act);
   if (!(d->damping > 0.f)) return fail(TS_ERR_VALUE, "gn: damping must be > 0");
@@ -767,6 +767,7 @@ GnKernel gn_pick_m(int m) {
     case 96: TS_GN(6)
     case 112: TS_GN(7)
     case 128: TS_GN(8)
+    case 192: TS_GN(12)
     case 256: TS_GN(16)
   }
 #undef TS_GN
@@ -842,6 +843,7 @@ GnReadKernel gn_read_pick_m(int m) {
     case 96: TS_GNR(6)
     case 112: TS_GNR(7)
     case 128: TS_GNR(8)
+    case 192: TS_GNR(12)
     case 256: TS_GNR(16)
   }
 #undef TS_GNR

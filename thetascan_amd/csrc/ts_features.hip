@@ -58,7 +58,7 @@ __device__ __forceinline__ float load_xn(const FeatP& p, int t, bool valid, int 
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
     ld4f<E>(xrow + db * 16 + 4 * g, xr[db]);
-    if (p.in_rot > 0)
+    if (db * 16 < p.in_rot)  // uniform: blocks past the rotated dims skip the table reads
       rope4(xr[db], db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, false);
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss += xr[db][i] * xr[db][i];
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
       for (int fb = 0; fb < MB; ++fb) {
         if (fb < nfb) {
           float v[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
-          if (p.feat_rot > 0)
+          if (fb * 16 < p.feat_rot)
             rope4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, t, valid && fb * 16 + 4 * g < p.feat_rot,
                   false);
           st4f<E>(prow + fb * 16 + 4 * g, v);
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
         if (fb < nfb) {
           float v[4];
           ld4f<E>(prow + fb * 16 + 4 * g, v);
-          if (p.feat_rot > 0)
+          if (fb * 16 < p.feat_rot)
             rope4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, t, valid && fb * 16 + 4 * g < p.feat_rot, true);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (big ? dxn[db][i] - xr[db][i] * dot : dxn[db][i]) * scale;
-        if (p.in_rot > 0)
+        if (db * 16 < p.in_rot)
           rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, true);
         st4f<E>(orow + db * 16 + 4 * g, v);
       }
@@ -742,7 +742,8 @@ __global__ __launch_bounds__(256) void feature_fwd_wide_kernel(FeatP p) {
       for (int f = 0; f < 4; ++f) {
         float v[4] = {hc[f][0], hc[f][1], hc[f][2], hc[f][3]};
         const int col = c * 64 + f * 16 + 4 * g;
-        if (p.feat_rot > 0) rope4(v, col, p.feat_rot, p.f_cos, p.f_sin, t, valid && col < p.feat_rot, false);
+        if (c * 64 + f * 16 < p.feat_rot)
+          rope4(v, col, p.feat_rot, p.f_cos, p.f_sin, t, valid && col < p.feat_rot, false);
         st4f<E>(crow + f * 16 + 4 * g, v);
       }
       __syncthreads();
@@ -840,7 +841,8 @@ __global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
         float v[4] = {__uint_as_float(dpr[f].x << 16), __uint_as_float(dpr[f].x & 0xffff0000u),
                       __uint_as_float(dpr[f].y << 16), __uint_as_float(dpr[f].y & 0xffff0000u)};
         const int col = c * 64 + f * 16 + 4 * g;
-        if (p.feat_rot > 0) rope4(v, col, p.feat_rot, p.f_cos, p.f_sin, t, valid && col < p.feat_rot, true);
+        if (c * 64 + f * 16 < p.feat_rot)
+          rope4(v, col, p.feat_rot, p.f_cos, p.f_sin, t, valid && col < p.feat_rot, true);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dh[f][i] += v[i];
       }
@@ -958,7 +960,7 @@ __global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (big ? dxn[db][i] - xr[db][i] * dot : dxn[db][i]) * sc;
-        if (p.in_rot > 0)
+        if (db * 16 < p.in_rot)
           rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, true);
         st4f<E>(orow + db * 16 + 4 * g, v);
       }

@@ -21,7 +21,11 @@ GN_HEAD_DIMS = (16, 32, 64, 128)
 ACTS = {"relu2": _lib.GN_RELU2, "tanh": _lib.GN_TANH}  # hidden nonlinearities the kernels take
 
 
-def supported_width(m: int) -> bool:
+def supported_width(m: int, dtype: torch.dtype | None = None, d: int | None = None) -> bool:
+    """Hidden widths the GN kernels take: multiples of 16 up to 128, 192 and
+    256 in any dtype, and 384 in bf16 at head widths 32 and 64."""
+    if m == 384:
+        return dtype == torch.bfloat16 and d in (32, 64)
     return m in (192, 256) or (16 <= m <= 128 and m % 16 == 0)
 
 
@@ -35,7 +39,7 @@ def eligible(cfg, weights, k: torch.Tensor, v: torch.Tensor) -> bool:
         return False
     W1, W2, _ = weights[0]
     d, m = k.shape[-1], W1.shape[-2]
-    return d in GN_HEAD_DIMS and supported_width(m) and v.shape[-1] == d and W2.shape[-1] == m
+    return d in GN_HEAD_DIMS and supported_width(m, k.dtype, d) and v.shape[-1] == d and W2.shape[-1] == m
 
 
 def _rows(t: torch.Tensor) -> torch.Tensor:
@@ -395,4 +399,4 @@ def read_eligible(cfg, weights, q: torch.Tensor) -> bool:
     if cfg.read_norm and cfg.read_norm_mode != "key_mass":
         return False
     W1, W2, _ = weights[0]
-    return q.shape[-1] in GN_HEAD_DIMS and supported_width(W1.shape[-2])
+    return q.shape[-1] in GN_HEAD_DIMS and supported_width(W1.shape[-2], q.dtype, q.shape[-1])

@@ -725,11 +725,690 @@ __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
   }
 }
 
+// ------------------------------------------------------------ wide widths
+//
+// Hidden widths of 192 and 384 (bf16, head widths 32 and 64): the per-lane
+// m-vectors of the kernels above would not fit in registers (they spill to
+// scratch), so these walk the hidden axis 64 features at a time.  Each pass
+// over the chunks re-forms what it needs of a = W1 x (RMSNorm sum, then h,
+// s^2 and the W2 products; in the backward the products that feed drinv and
+// the per-chunk dpre) on MFMA, keeping only d-vectors and per-token scalars
+// across chunks.  W1 and W2 (or W2^T for the read backward) are staged in
+// LDS once per workgroup; W1^T and W2^T operands of the write kernels are
+// transposing LDS reads of the staged rows.
+
+struct GnWideLayout {
+  int xp, mp;
+  int xs, w1, w2;  // element offsets; w2 holds W2 [d][mp] or W2^T [m][xp]
+  int end;
+};
+// w2_rows: 0 (no W2), 1 (W2 as [d][m + 8]), 2 (W2^T as [m][d + 8])
+__host__ __device__ constexpr GnWideLayout gn_wide_layout(int d, int m, int w2_rows) {
+  GnWideLayout L{};
+  L.xp = d + 8;
+  L.mp = m + 8;
+  int off = 0;
+  L.xs = off; off += TT * L.xp;
+  L.w1 = off; off += m * L.xp;
+  L.w2 = -1;
+  if (w2_rows == 1) { L.w2 = off; off += d * L.mp; }
+  if (w2_rows == 2) { L.w2 = off; off += m * L.xp; }
+  L.end = off;
+  return L;
+}
+
+__device__ __forceinline__ bf16x8 sq8(bf16x8 v) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float f = tof(v[i]);
+    v[i] = (bf16)(f * f);
+  }
+  return v;
+}
+
+// a of chunk c (feature blocks 4c..4c+3) for this wave's 16 tokens
+template <int D>
+__device__ __forceinline__ void gnw_a(const bf16* w1s, int xp, const bf16* xs_w, int c, int l16, int g, floatx4* a) {
+  gemm_a<bf16, D, 4>(w1s + c * 64 * xp, xp, xs_w, xp, l16, g, 4, a);
+}
+// out[db] += (W2 or W2 o W2)[:, chunk c] reg  (W2 staged as [D][mp])
+template <int D, bool SQ>
+__device__ __forceinline__ void gnw_w2(const bf16* w2s, int mp, int c, const floatx4* reg, int l16, int g,
+                                       floatx4* out) {
+  typedef LdsIO<bf16> IO;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    const bf16* wrow = w2s + (db * 16 + l16) * mp + c * 64;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      bf16x8 wa = IO::cat(IO::ld4(wrow + 32 * jj + 4 * g), IO::ld4(wrow + 32 * jj + 16 + 4 * g));
+      if (SQ) wa = sq8(wa);
+      out[db] = mma32(wa, IO::from_acc(reg[2 * jj], reg[2 * jj + 1]), out[db]);
+    }
+  }
+}
+// out[f] = (W2 or W2 o W2)[:, chunk c]^T dvec  (transposing reads of W2 [D][mp])
+template <int D, bool SQ>
+__device__ __forceinline__ void gnw_w2t(const bf16* w2s, int mp, int c, const floatx4* dvec, int lane,
+                                        floatx4* out) {
+  typedef LdsIO<bf16> IO;
+  typedef TokFrag<bf16> TF;
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    out[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      bf16x8 wa = TF::get(w2s, mp, c * 64 + f * 16, kk, lane);
+      if (SQ) wa = sq8(wa);
+      out[f] = mma32(wa, IO::from_acc(dvec[2 * kk], dvec[2 * kk + 1]), out[f]);
+    }
+  }
+}
+// out[db] += W1[chunk c]^T reg  (transposing reads of W1 [m][xp])
+template <int D>
+__device__ __forceinline__ void gnw_w1t(const bf16* w1s, int xp, int c, const floatx4* reg, int lane,
+                                        floatx4* out) {
+  typedef LdsIO<bf16> IO;
+  typedef TokFrag<bf16> TF;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      out[db] = mma32(TF::get(w1s + c * 64 * xp, xp, db * 16, jj, lane), IO::from_acc(reg[2 * jj], reg[2 * jj + 1]),
+                      out[db]);
+}
+
+// The forward chain of one token over the chunks: rinv, hh, u = W2 h,
+// rq = (W2 o W2) s^2, then lam and den.  Per chunk it hands h and s^2 to
+// `sink` (the tiles of the backward, the h output of the forward).
+template <int D, int MB, typename Sink>
+__device__ __forceinline__ void gnw_forward(const GnP& p, const float* tau, const bf16* w1s, int xp, const bf16* w2s,
+                                            int mp, const bf16* xs_w, int l16, int g, const float (*xr)[4],
+                                            const float (*vr)[4], float xx, float& rinv, float& hh, floatx4* lam,
+                                            floatx4* den, floatx4* rq, Sink sink) {
+  constexpr int NC = MB / 4;
+  float ss = 0.f;
+#pragma unroll 1
+  for (int c = 0; c < NC; ++c) {
+    floatx4 a[4];
+    gnw_a<D>(w1s, xp, xs_w, c, l16, g, a);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss += a[f][i] * a[f][i];
+  }
+  rinv = rsqrtf(sum_g(ss) * p.inv_m + p.eps);
+  floatx4 u[D / 16];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) u[db] = rq[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float hsum = 0.f;
+#pragma unroll 1
+  for (int c = 0; c < NC; ++c) {
+    floatx4 a[4], hv[4], s2v[4];
+    gnw_a<D>(w1s, xp, xs_w, c, l16, g, a);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      float tv[4];
+      tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float hval = gn_act(p.act, a[f][i] * rinv - tv[i]);
+        hv[f][i] = hval;
+        const float sv = gn_slope(p.act, hval) * rinv;
+        s2v[f][i] = sv * sv;
+        hsum += hval * hval;
+      }
+    }
+    gnw_w2<D, false>(w2s, mp, c, hv, l16, g, u);
+    gnw_w2<D, true>(w2s, mp, c, s2v, l16, g, rq);
+    sink(c, hv, s2v);
+  }
+  hh = sum_g(hsum);
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float r = vr[db][i] - xr[db][i] - p.s * u[db][i];
+      const float dn = (hh + xx * rq[db][i]) * p.inv_L + p.damp;
+      den[db][i] = dn;
+      lam[db][i] = r / dn;
+    }
+}
+
+template <int D, int MB>
+__global__ __launch_bounds__(256) void gn_write_fwd_wide_kernel(GnP p) {
+  typedef bf16 E;
+  constexpr int M = MB * 16;
+  constexpr int NC = MB / 4;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnWideLayout L = gn_wide_layout(D, M, 1);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* w1s = base + L.w1;
+  E* w2s = base + L.w2;
+  stage_matrix<E>((const E*)p.w1 + (size_t)h * M * D, M, D, w1s, L.xp, tid);
+  stage_matrix<E>((const E*)p.w2 + (size_t)h * D * M, D, M, w2s, L.mp, tid);
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  RowTile<E, D> ldx;
+  ldx.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();       // weights staged; previous group consumed
+    ldx.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldx.fetch(xsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const E* xs_w = xs + w * 16 * L.xp;
+    float xr[D / 16][4], vr[D / 16][4];
+    float xx = 0.f;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      ld4f<E>(xs + row * L.xp + db * 16 + 4 * g, xr[db]);
+      ld4_row<E>(p.v, b, h, t, db * 16 + 4 * g, valid, vr[db]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xx += xr[db][i] * xr[db][i];
+    }
+    xx = sum_g(xx);
+    float rinv, hh;
+    floatx4 lam[D / 16], den[D / 16], rq[D / 16];
+    gnw_forward<D, MB>(p, tau, w1s, L.xp, w2s, L.mp, xs_w, l16, g, xr, vr, xx, rinv, hh, lam, den, rq,
+                       [&](int c, const floatx4* hv, const floatx4*) {
+#pragma unroll
+                         for (int f = 0; f < 4; ++f) {
+                           float o[4] = {hv[f][0], hv[f][1], hv[f][2], hv[f][3]};
+                           st4_row<E>(p.h, b, h, t, c * 64 + f * 16 + 4 * g, valid, o);
+                         }
+                       });
+    // g = s sp (W2^T lam) rinv per chunk
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], z[4];
+      gnw_a<D>(w1s, L.xp, xs_w, c, l16, g, a);
+      gnw_w2t<D, false>(w2s, L.mp, c, lam, lane, z);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float tv[4], gv[4];
+        tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float hval = gn_act(p.act, a[f][i] * rinv - tv[i]);
+          gv[i] = p.s * gn_slope(p.act, hval) * z[f][i] * rinv;
+        }
+        st4_row<E>(p.g, b, h, t, c * 64 + f * 16 + 4 * g, valid, gv);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float lv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lv[i] = p.s * lam[db][i];
+      st4_row<E>(p.lam, b, h, t, db * 16 + 4 * g, valid, lv);
+    }
+  }
+}
+
+template <int D, int MB>
+__global__ __launch_bounds__(256) void gn_write_bwd_wide_kernel(GnP p) {
+  typedef bf16 E;
+  constexpr int M = MB * 16;
+  constexpr int NC = MB / 4;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnWideLayout L = gn_wide_layout(D, M, 1);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* w1s = base + L.w1;
+  E* w2s = base + L.w2;
+  stage_matrix<E>((const E*)p.w1 + (size_t)h * M * D, M, D, w1s, L.xp, tid);
+  stage_matrix<E>((const E*)p.w2 + (size_t)h * D * M, D, M, w2s, L.mp, tid);
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const int64_t N = (int64_t)p.B * p.T;
+  // slot-major tiles: slot k of head h starts at k * H * N * w + h * N * w
+  E* tm = (E*)p.tm + (int64_t)h * N * M;  // dz, h, da, s2 (, dpre)
+  E* td = (E*)p.td + (int64_t)h * N * D;  // lam, du, x, drq
+  const int64_t HNM = (int64_t)p.H * N * M, HND = (int64_t)p.H * N * D;
+  const Rows<E> xsrc = rows_of<E>(p.x, b, h);
+  RowTile<E, D> ldx;
+  ldx.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldx.fetch(xsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();
+    ldx.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldx.fetch(xsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const int64_t n = (int64_t)b * p.T + t;
+    const E* xs_w = xs + w * 16 * L.xp;
+    float xr[D / 16][4], vr[D / 16][4];
+    float xx = 0.f;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      ld4f<E>(xs + row * L.xp + db * 16 + 4 * g, xr[db]);
+      ld4_row<E>(p.v, b, h, t, db * 16 + 4 * g, valid, vr[db]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xx += xr[db][i] * xr[db][i];
+    }
+    xx = sum_g(xx);
+    float rinv, hh;
+    floatx4 lam[D / 16], den[D / 16], rq[D / 16];
+    gnw_forward<D, MB>(p, tau, w1s, L.xp, w2s, L.mp, xs_w, l16, g, xr, vr, xx, rinv, hh, lam, den, rq,
+                       [&](int c, const floatx4* hv, const floatx4* s2v) {
+#pragma unroll
+                         for (int f = 0; f < 4; ++f) {
+                           float o[4] = {hv[f][0], hv[f][1], hv[f][2], hv[f][3]};
+                           st4_tile<E>(tm + 1 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, o);
+                           float o2[4] = {s2v[f][0], s2v[f][1], s2v[f][2], s2v[f][3]};
+                           st4_tile<E>(tm + 3 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, o2);
+                         }
+                       });
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float o[4] = {lam[db][0], lam[db][1], lam[db][2], lam[db][3]};
+      st4_tile<E>(td + 0 * HND, n, D, db * 16 + 4 * g, valid, o);
+      st4_tile<E>(td + 2 * HND, n, D, db * 16 + 4 * g, valid, xr[db]);
+    }
+    // ---- pass 1: g = s sp z rinv (z = W2^T lam) -> dz, and its share of drinv
+    float drinv = 0.f;
+    floatx4 wdz[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) wdz[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], z[4], dz[4];
+      gnw_a<D>(w1s, L.xp, xs_w, c, l16, g, a);
+      gnw_w2t<D, false>(w2s, L.mp, c, lam, lane, z);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float tv[4], dgv[4];
+        tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+        ld4_row<E>(p.dg, b, h, t, c * 64 + f * 16 + 4 * g, valid, dgv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sp = gn_slope(p.act, gn_act(p.act, a[f][i] * rinv - tv[i]));
+          const float sdg = p.s * dgv[i];
+          dz[f][i] = sdg * sp * rinv;
+          drinv += sdg * sp * z[f][i];
+        }
+        float o[4] = {dz[f][0], dz[f][1], dz[f][2], dz[f][3]};
+        st4_tile<E>(tm + 0 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, o);
+      }
+      gnw_w2<D, false>(w2s, L.mp, c, dz, l16, g, wdz);
+    }
+    // ---- lam -> r, den -> (hh, xx, rq)
+    floatx4 dr[D / 16], drq[D / 16], du[D / 16];
+    float dhh = 0.f, dxx = 0.f;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float dlv[4];
+      ld4_row<E>(p.dlam, b, h, t, db * 16 + 4 * g, valid, dlv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dl = p.s * dlv[i] + wdz[db][i];
+        dr[db][i] = dl / den[db][i];
+        const float dD = -dl * lam[db][i] / den[db][i] * p.inv_L;
+        dhh += dD;
+        dxx += dD * rq[db][i];
+        drq[db][i] = dD;
+      }
+    }
+    dhh = sum_g(dhh);
+    dxx = sum_g(dxx);
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float dvv[4], duv[4], o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        drq[db][i] *= xx;
+        o[i] = drq[db][i];
+        dvv[i] = dr[db][i];
+        du[db][i] = -p.s * dr[db][i];
+        duv[i] = du[db][i];
+      }
+      st4_tile<E>(td + 3 * HND, n, D, db * 16 + 4 * g, valid, o);
+      st4_row<E>(p.dv, b, h, t, db * 16 + 4 * g, valid, dvv);
+      st4_tile<E>(td + 1 * HND, n, D, db * 16 + 4 * g, valid, duv);
+    }
+    // dpre of chunk c (with its a): sigma' dht + sigma'' dsp, dht = dh + W2^T du + 2 h dhh,
+    // dsp = s dg z rinv + 2 sp rinv ((W2 o W2)^T drq) rinv; adds the chunk's share to drinv
+    auto dpre_chunk = [&](int c, floatx4* a, floatx4* dpre, float& drv) {
+      floatx4 z[4], ds2[4], dhu[4];
+      gnw_a<D>(w1s, L.xp, xs_w, c, l16, g, a);
+      gnw_w2t<D, false>(w2s, L.mp, c, lam, lane, z);
+      gnw_w2t<D, true>(w2s, L.mp, c, drq, lane, ds2);
+      gnw_w2t<D, false>(w2s, L.mp, c, du, lane, dhu);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float tv[4], dgv[4], dhv[4];
+        tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+        ld4_row<E>(p.dg, b, h, t, c * 64 + f * 16 + 4 * g, valid, dgv);
+        ld4_row<E>(p.dh, b, h, t, c * 64 + f * 16 + 4 * g, valid, dhv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pre = a[f][i] * rinv - tv[i];
+          const float hval = gn_act(p.act, pre);
+          const float sp = gn_slope(p.act, hval);
+          const float dsv = 2.f * sp * rinv * ds2[f][i];
+          const float dsp = p.s * dgv[i] * z[f][i] * rinv + dsv * rinv;
+          drv += dsv * sp;
+          const float dht = dhv[i] + dhu[f][i] + 2.f * hval * dhh;
+          dpre[f][i] = valid ? gn_dpre(p.act, pre, hval, dht, dsp) : 0.f;
+        }
+      }
+    };
+    // ---- pass 2: drinv from the s^2 path and from dpre . a
+    float ra = 0.f;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], dpre[4];
+      dpre_chunk(c, a, dpre, drinv);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra += dpre[f][i] * a[f][i];
+        if (p.has_tau) {
+          float o[4] = {dpre[f][0], dpre[f][1], dpre[f][2], dpre[f][3]};
+          st4_tile<E>(tm + 4 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, o);
+        }
+      }
+    }
+    drinv = sum_g(drinv + ra);
+    const float c3 = drinv * rinv * rinv * rinv * p.inv_m;
+    // ---- pass 3: da = dpre rinv - c3 a -> W1^T da
+    floatx4 wda[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) wda[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], da[4];
+      float unused = 0.f;
+      dpre_chunk(c, a, da, unused);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) da[f][i] = da[f][i] * rinv - c3 * a[f][i];
+        float o[4] = {da[f][0], da[f][1], da[f][2], da[f][3]};
+        st4_tile<E>(tm + 2 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, o);
+      }
+      gnw_w1t<D>(w1s, L.xp, c, da, lane, wda);
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float dxi[4], o[4];
+      ld4_row<E>(p.dxin, b, h, t, db * 16 + 4 * g, valid, dxi);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = dxi[i] - dr[db][i] + 2.f * xr[db][i] * dxx + wda[db][i];
+      st4_row<E>(p.dx, b, h, t, db * 16 + 4 * g, valid, o);
+    }
+  }
+}
+
+// a + correction of chunk c for the read stage (c = num or num / (mass + eps))
+template <int D>
+__device__ __forceinline__ void gnw_read_a(const GnReadP& p, int b, int h, int t, bool valid, const bf16* w1s, int xp,
+                                           const bf16* xs_w, int c, int l16, int g, float cinv, floatx4* a) {
+  gnw_a<D>(w1s, xp, xs_w, c, l16, g, a);
+  if (p.corr) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      float cv[4];
+      ld4_row<bf16>(p.num, b, h, t, c * 64 + f * 16 + 4 * g, valid, cv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[f][i] += cv[i] * cinv;
+    }
+  }
+}
+
+template <int D, int MB>
+__device__ __forceinline__ float gnw_read_rinv(const GnReadP& p, int b, int h, int t, bool valid, const bf16* w1s,
+                                               int xp, const bf16* xs_w, int l16, int g, float& cinv) {
+  cinv = 1.f;
+  if (p.corr == 2) cinv = valid ? 1.f / (p.mass[b * p.msb + h * p.msh + (int64_t)t * p.mst] + p.eps) : 0.f;
+  float ss = 0.f;
+#pragma unroll 1
+  for (int c = 0; c < MB / 4; ++c) {
+    floatx4 a[4];
+    gnw_read_a<D>(p, b, h, t, valid, w1s, xp, xs_w, c, l16, g, cinv, a);
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss += a[f][i] * a[f][i];
+  }
+  return rsqrtf(sum_g(ss) * p.inv_m + p.eps);
+}
+
+template <int D, int MB>
+__global__ __launch_bounds__(256) void gn_read_fwd_wide_kernel(GnReadP p) {
+  typedef bf16 E;
+  constexpr int M = MB * 16;
+  constexpr int NC = MB / 4;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnWideLayout L = gn_wide_layout(D, M, p.want_resid ? 1 : 0);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* w1s = base + L.w1;
+  E* w2s = base + L.w2;
+  stage_matrix<E>((const E*)p.w1 + (size_t)h * M * D, M, D, w1s, L.xp, tid);
+  if (p.want_resid) stage_matrix<E>((const E*)p.w2 + (size_t)h * D * M, D, M, w2s, L.mp, tid);
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const Rows<E> qsrc = rows_of<E>(p.q, b, h);
+  RowTile<E, D> ldq;
+  ldq.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldq.fetch(qsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();
+    ldq.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldq.fetch(qsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const E* xs_w = xs + w * 16 * L.xp;
+    float cinv;
+    const float rinv = gnw_read_rinv<D, MB>(p, b, h, t, valid, w1s, L.xp, xs_w, l16, g, cinv);
+    floatx4 u[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) u[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], hv[4];
+      gnw_read_a<D>(p, b, h, t, valid, w1s, L.xp, xs_w, c, l16, g, cinv, a);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float tv[4], o[4];
+        tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hv[f][i] = gn_act(p.act, a[f][i] * rinv - tv[i]);
+          o[i] = hv[f][i];
+        }
+        st4_row<E>(p.h, b, h, t, c * 64 + f * 16 + 4 * g, valid, o);
+      }
+      if (p.want_resid) gnw_w2<D, false>(w2s, L.mp, c, hv, l16, g, u);
+    }
+    if (p.want_resid) {
+      const E* qrow = xs + row * L.xp;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        float qv[4];
+        ld4f<E>(qrow + db * 16 + 4 * g, qv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] += p.s * u[db][i];
+        st4_row<E>(p.resid, b, h, t, db * 16 + 4 * g, valid, qv);
+      }
+    }
+  }
+}
+
+template <int D, int MB>
+__global__ __launch_bounds__(256) void gn_read_bwd_wide_kernel(GnReadP p) {
+  typedef bf16 E;
+  typedef LdsIO<E> IO;
+  constexpr int M = MB * 16;
+  constexpr int NC = MB / 4;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const GnWideLayout L = gn_wide_layout(D, M, p.want_resid ? 2 : 0);
+  extern __shared__ __align__(16) unsigned char smem[];
+  E* base = (E*)smem;
+  E* xs = base + L.xs;
+  E* w1s = base + L.w1;
+  E* w2ts = base + L.w2;  // W2^T [m][xp]
+  stage_matrix<E>((const E*)p.w1 + (size_t)h * M * D, M, D, w1s, L.xp, tid);
+  if (p.want_resid) stage_matrix<E>((const E*)p.w2t + (size_t)h * M * D, M, D, w2ts, L.xp, tid);
+  const float* tau = p.has_tau ? p.tau + h * M : nullptr;
+  const int64_t N = (int64_t)p.B * p.T;
+  E* tm = (E*)p.tm + (int64_t)h * N * M;  // da, h (, dpre)
+  E* td = (E*)p.td + (int64_t)h * N * D;  // q, s dresid
+  const int64_t HNM = (int64_t)p.H * N * M, HND = (int64_t)p.H * N * D;
+  const Rows<E> qsrc = rows_of<E>(p.q, b, h);
+  RowTile<E, D> ldq;
+  ldq.init(D, tid);
+  const int g0 = blockIdx.x * p.groups;
+  ldq.fetch(qsrc, g0 * TT, p.T);
+  for (int grp = 0; grp < p.groups; ++grp) {
+    const int t0 = (g0 + grp) * TT;
+    if (t0 >= p.T) break;  // uniform over the workgroup
+    __syncthreads();
+    ldq.store(xs, L.xp);
+    if (grp + 1 < p.groups) ldq.fetch(qsrc, t0 + TT, p.T);
+    __syncthreads();
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    const int64_t n = (int64_t)b * p.T + t;
+    const E* xs_w = xs + w * 16 * L.xp;
+    float cinv;
+    const float rinv = gnw_read_rinv<D, MB>(p, b, h, t, valid, w1s, L.xp, xs_w, l16, g, cinv);
+    float dres[D / 16][4];
+    floatx4 dres4[D / 16];
+    const E* qrow = xs + row * L.xp;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float qv[4], sd[4];
+      ld4f<E>(qrow + db * 16 + 4 * g, qv);
+      ld4_row<E>(p.dresid, b, h, t, db * 16 + 4 * g, valid && p.want_resid, dres[db]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dres4[db][i] = dres[db][i];
+        sd[i] = p.s * dres[db][i];
+      }
+      st4_tile<E>(td + 0 * HND, n, D, db * 16 + 4 * g, valid, qv);
+      st4_tile<E>(td + 1 * HND, n, D, db * 16 + 4 * g, valid, sd);
+    }
+    // dpre of chunk c: sigma'(pre) (dh + s W2^T dresid)
+    auto dpre_chunk = [&](int c, floatx4* a, floatx4* dpre) {
+      floatx4 dhr[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        dhr[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (p.want_resid) {
+          const E* wrow = w2ts + (c * 64 + f * 16 + l16) * L.xp;
+#pragma unroll
+          for (int kk = 0; kk < D / 32; ++kk)
+            dhr[f] = mma32(IO::cat(IO::ld4(wrow + 32 * kk + 4 * g), IO::ld4(wrow + 32 * kk + 16 + 4 * g)),
+                           IO::from_acc(dres4[2 * kk], dres4[2 * kk + 1]), dhr[f]);
+        }
+      }
+      gnw_read_a<D>(p, b, h, t, valid, w1s, L.xp, xs_w, c, l16, g, cinv, a);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float tv[4], dhv[4];
+        tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+        ld4_row<E>(p.dh, b, h, t, c * 64 + f * 16 + 4 * g, valid, dhv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pre = a[f][i] * rinv - tv[i];
+          const float hval = gn_act(p.act, pre);
+          dpre[f][i] = valid ? gn_dpre(p.act, pre, hval, dhv[i] + p.s * dhr[f][i], 0.f) : 0.f;
+        }
+      }
+    };
+    float ra = 0.f;
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], dpre[4];
+      dpre_chunk(c, a, dpre);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float tv[4], hvv[4], dpv[4];
+        tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hvv[i] = gn_act(p.act, a[f][i] * rinv - tv[i]);
+          dpv[i] = dpre[f][i];
+          ra += dpre[f][i] * a[f][i];
+        }
+        st4_tile<E>(tm + 1 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, hvv);
+        if (p.has_tau) st4_tile<E>(tm + 2 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, dpv);
+      }
+    }
+    ra = sum_g(ra);
+    const float c3 = ra * rinv * rinv * rinv * p.inv_m;
+    float dm = 0.f;
+    floatx4 wda[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) wda[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      floatx4 a[4], da[4];
+      dpre_chunk(c, a, da);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        float o[4], dn[4];
+        float cv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.corr == 2) ld4_row<E>(p.num, b, h, t, c * 64 + f * 16 + 4 * g, valid, cv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          da[f][i] = da[f][i] * rinv - c3 * a[f][i];
+          o[i] = da[f][i];
+          dn[i] = da[f][i] * cinv;
+          dm += da[f][i] * cv[i];
+        }
+        st4_tile<E>(tm + 0 * HNM, n, M, c * 64 + f * 16 + 4 * g, valid, o);
+        if (p.corr) st4_row<E>(p.dnum, b, h, t, c * 64 + f * 16 + 4 * g, valid, dn);
+      }
+      gnw_w1t<D>(w1s, L.xp, c, da, lane, wda);
+    }
+    if (p.corr == 2) {
+      dm = sum_g(dm);
+      if (g == 0 && valid) p.dmass[b * p.msb + h * p.msh + (int64_t)t * p.mst] = -dm * cinv * cinv;
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = dres[db][i] + wda[db][i];
+      st4_row<E>(p.dq, b, h, t, db * 16 + 4 * g, valid, o);
+    }
+  }
+}
+
 }  // namespace ts
 
 namespace {
 
 using ts::fail;
+
+bool gn_is_wide(const ts_gn_desc* d);
 
 int check_gn(const ts_gn_desc* d) {
   if (!d) return fail(TS_ERR_VALUE, "gn: null descriptor");
@@ -737,8 +1416,9 @@ int check_gn(const ts_gn_desc* d) {
   if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "gn: unknown dtype");
   if (d->d != 16 && d->d != 32 && d->d != 64 && d->d != 128)
     return fail(TS_ERR_NOT_IMPLEMENTED, "gn: head width %d (16, 32, 64 or 128)", d->d);
-  if (d->m < 16 || d->m % 16 || (d->m > 128 && d->m != 192 && d->m != 256))
-    return fail(TS_ERR_NOT_IMPLEMENTED, "gn: hidden width %d (a multiple of 16 up to 128, 192 or 256)", d->m);
+  if (d->m < 16 || d->m % 16 || (d->m > 128 && d->m != 192 && d->m != 256 && !gn_is_wide(d)))
+    return fail(TS_ERR_NOT_IMPLEMENTED,
+                "gn: hidden width %d (a multiple of 16 up to 128, 192 or 256; 384 in bf16 at head widths 32, 64)", d->m);
   if (d->H > 65535 || d->B > 65535) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: grid too large");
   if (d->act != TS_GN_RELU2 && d->act != TS_GN_TANH) return fail(TS_ERR_VALUE, "gn: unknown nonlinearity %d", d->act);
   if (!(d->damping > 0.f)) return fail(TS_ERR_VALUE, "gn: damping must be > 0");
@@ -785,6 +1465,23 @@ GnKernel gn_pick(int d, int m) {
   return nullptr;
 }
 
+// Hidden widths the chunked kernels take (bf16, head widths 32 and 64).
+bool gn_is_wide(const ts_gn_desc* d) {
+  return d->dtype == TS_BF16 && (d->d == 32 || d->d == 64) && (d->m == 192 || d->m == 384);
+}
+
+template <int D>
+GnKernel gn_wide_pick_d(int m, bool fwd) {
+  switch (m) {
+    case 192: return fwd ? (GnKernel)ts::gn_write_fwd_wide_kernel<D, 12> : (GnKernel)ts::gn_write_bwd_wide_kernel<D, 12>;
+    case 384: return fwd ? (GnKernel)ts::gn_write_fwd_wide_kernel<D, 24> : (GnKernel)ts::gn_write_bwd_wide_kernel<D, 24>;
+  }
+  return nullptr;
+}
+GnKernel gn_wide_pick(const ts_gn_desc* d, bool fwd) {
+  return d->d == 32 ? gn_wide_pick_d<32>(d->m, fwd) : gn_wide_pick_d<64>(d->m, fwd);
+}
+
 int gn_lds_bytes(const ts_gn_desc* d, bool fwd) {
   const int es = d->dtype == TS_BF16 ? 2 : 4;
   const ts::GnLayout full = ts::gn_layout(es, d->d, d->m, fwd, true);
@@ -811,10 +1508,12 @@ void gn_fill(const ts_gn_desc* d, ts::GnP& p) {
 }
 
 int gn_launch(const ts_gn_desc* d, const ts::GnP& p, bool fwd, hipStream_t stream) {
-  GnKernel k = d->dtype == TS_BF16 ? (fwd ? gn_pick<ts::bf16, true>(d->d, d->m) : gn_pick<ts::bf16, false>(d->d, d->m))
-                                   : (fwd ? gn_pick<float, true>(d->d, d->m) : gn_pick<float, false>(d->d, d->m));
+  const bool wide = gn_is_wide(d);
+  GnKernel k = wide ? gn_wide_pick(d, fwd)
+               : d->dtype == TS_BF16 ? (fwd ? gn_pick<ts::bf16, true>(d->d, d->m) : gn_pick<ts::bf16, false>(d->d, d->m))
+                                     : (fwd ? gn_pick<float, true>(d->d, d->m) : gn_pick<float, false>(d->d, d->m));
   if (!k) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: no kernel for d=%d m=%d", d->d, d->m);
-  const int lds = gn_lds_bytes(d, fwd);
+  const int lds = wide ? ts::gn_wide_layout(d->d, d->m, 1).end * 2 : gn_lds_bytes(d, fwd);
   if (lds > ts::kGnLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: tile of %d bytes exceeds LDS", lds);
   if (lds > 65536) {
     hipError_t e = ts::ensure_lds_limit((const void*)k, lds);
@@ -881,12 +1580,24 @@ void gn_read_fill(const ts_gn_read_desc* r, const ts_gn_desc* d, ts::GnReadP& p,
   p.msb = mass.sb; p.msh = mass.sh; p.mst = mass.st;
 }
 
+template <int D>
+GnReadKernel gn_read_wide_pick_d(int m, bool fwd) {
+  switch (m) {
+    case 192: return fwd ? (GnReadKernel)ts::gn_read_fwd_wide_kernel<D, 12> : (GnReadKernel)ts::gn_read_bwd_wide_kernel<D, 12>;
+    case 384: return fwd ? (GnReadKernel)ts::gn_read_fwd_wide_kernel<D, 24> : (GnReadKernel)ts::gn_read_bwd_wide_kernel<D, 24>;
+  }
+  return nullptr;
+}
+
 int gn_read_launch(const ts_gn_desc* d, const ts::GnReadP& p, bool fwd, hipStream_t stream) {
-  GnReadKernel k = d->dtype == TS_BF16
-                       ? (fwd ? gn_read_pick<ts::bf16, true>(d->d, d->m) : gn_read_pick<ts::bf16, false>(d->d, d->m))
-                       : (fwd ? gn_read_pick<float, true>(d->d, d->m) : gn_read_pick<float, false>(d->d, d->m));
+  const bool wide = gn_is_wide(d);
+  GnReadKernel k =
+      wide ? (d->d == 32 ? gn_read_wide_pick_d<32>(d->m, fwd) : gn_read_wide_pick_d<64>(d->m, fwd))
+      : d->dtype == TS_BF16 ? (fwd ? gn_read_pick<ts::bf16, true>(d->d, d->m) : gn_read_pick<ts::bf16, false>(d->d, d->m))
+                            : (fwd ? gn_read_pick<float, true>(d->d, d->m) : gn_read_pick<float, false>(d->d, d->m));
   if (!k) return fail(TS_ERR_NOT_IMPLEMENTED, "gn read: no kernel for d=%d m=%d", d->d, d->m);
-  const int lds = gn_lds_bytes(d, fwd);
+  const int lds = wide ? ts::gn_wide_layout(d->d, d->m, p.want_resid ? (fwd ? 1 : 2) : 0).end * 2
+                       : gn_lds_bytes(d, fwd);
   if (lds > ts::kGnLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "gn read: tile of %d bytes exceeds LDS", lds);
   if (lds > 65536) {
     hipError_t e = ts::ensure_lds_limit((const void*)k, lds);

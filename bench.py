@@ -284,7 +284,19 @@ def cpu_baseline(budget_s: float = 12.0):
     }
 
 
-# The other two workloads the path serves, measured with ``--workload``:
+# The other workloads the path serves, measured with ``--workload``:
+#   bank          the headline mixer with the key-mass read and input RoPE
+#                 and a fast bank of two recency rates {0.9, 0.99} (views
+#                 path: multi-view scan, retention gradients pair by pair),
+#                 B8 T4096 H8 d64, bf16, fwd+bwd;
+#   preset_kernel, preset_gn, preset_gn_expanded
+#                 the reference's three published presets
+#                 (kernel_expanded_reference_v0_1: m = 384, shared key/query,
+#                 learned ReLU^2 threshold, fast bank of two half-lives;
+#                 gn_reference_v0_1: GN m = 192; gn_expanded_reference_v0_1:
+#                 GN m = 384) at d_model 512, B8 T4096, bf16, fwd+bwd; these
+#                 lines also report the step's peak memory above the resident
+#                 parameters and inputs;
 #   gn            damped Gauss-Newton memory, fast net 64 -> 128 -> 64 with tanh
 #                 and damping 1e-2 (this build's extension of the core config:
 #                 the public config, like the reference's, offers relu2/silu),
@@ -308,6 +320,15 @@ def cpu_baseline(budget_s: float = 12.0):
 OTHER = {
     "gn": dict(B=8, T=2048, train=True,
                metric="GN mixer tokens/s fwd+bwd (B8 T2048 H8 d64 m128 tanh, damping 1e-2, bf16)"),
+    "bank": dict(B=8, T=4096, train=True,
+                 metric="bank mixer tokens/s fwd+bwd (B8 T4096 H8 d64 m64 ReLU^2, fast bank {0.9, 0.99}, "
+                        "key-mass read, bf16)"),
+    "preset_kernel": dict(B=8, T=4096, train=True, preset="kernel_expanded_reference_v0_1",
+                          metric="kernel_expanded_reference_v0_1 tokens/s fwd+bwd (B8 T4096 d_model 512, m=384, bf16)"),
+    "preset_gn": dict(B=8, T=4096, train=True, preset="gn_reference_v0_1",
+                      metric="gn_reference_v0_1 tokens/s fwd+bwd (B8 T4096 d_model 512, m=192, bf16)"),
+    "preset_gn_expanded": dict(B=8, T=4096, train=True, preset="gn_expanded_reference_v0_1",
+                               metric="gn_expanded_reference_v0_1 tokens/s fwd+bwd (B8 T4096 d_model 512, m=384, bf16)"),
     "lm": dict(B=64, T=1024, train=True,
                metric="hybrid LM tokens/s fwd+bwd (17.06M params, 2 ThetaScan layers, B64 T1024, bf16)"),
     "bspline_bank": dict(B=2, T=32768, train=False,
@@ -321,6 +342,19 @@ def other_config(name: str):
 
     import thetascan_amd as ts
 
+    if "preset" in OTHER[name]:
+        public = getattr(ts.ThetaScanConfig, OTHER[name]["preset"])(d_model=D_MODEL, n_heads=H)
+        public.runtime.backend = "hip"
+        return public._to_core_config()
+    if name == "bank":
+        public = ts.ThetaScanConfig(
+            d_model=D_MODEL, n_heads=H, memory_multiplier=1, family="kernel",
+            kernel=ts.KernelConfig(feature_map="relu2_ridge", read_normalization="key_mass"),
+            rope=ts.RoPEConfig(mode="partial", fraction=0.5, placement="input"),
+            temporal=ts.TemporalConfig(mode="bank", bank_mode="fast", recency_branches=2, retention_inits=(0.9, 0.99)),
+            runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64),
+        )
+        return public._to_core_config()
     if name == "gn":
         public = ts.ThetaScanConfig(
             d_model=D_MODEL, n_heads=H, memory_multiplier=2, family="gn",
@@ -405,7 +439,11 @@ def run_other(name: str, args) -> dict:
     module = module.to(dev, torch.bfloat16)
     x = torch.randn(spec["B"], spec["T"], D_MODEL, generator=g).to(dev, torch.bfloat16)
     dy = (torch.randn(spec["B"], spec["T"], D_MODEL, generator=g) * 1e-2).to(dev, torch.bfloat16)
+    torch.cuda.synchronize()
+    resident = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
     ms = time_steps(module, x, dy, args.steps, args.warmup, train=spec["train"])
+    peak = torch.cuda.max_memory_allocated() - resident
     passes = pass_profile(module, x, dy, train=spec["train"])
     return {
         "metric": spec["metric"], "value": round(spec["B"] * spec["T"] / (ms * 1e-3), 1), "unit": "tokens/s",
@@ -414,7 +452,8 @@ def run_other(name: str, args) -> dict:
         "data": "synthetic (x ~ N(0,1), seeded weights)", "execution": "eager",
         "path": module.last_path,
         "config": {"workload": name, "batch": spec["B"], "seq_len": spec["T"], "heads": H, "head_dim": D_HEAD,
-                   "d_model": D_MODEL, "parallelism": "single GPU"},
+                   "d_model": D_MODEL, "mem_hidden": module.cfg.mem_hidden, "parallelism": "single GPU"},
+        "peak_memory_bytes": peak,
         "roofline": roofline_of(passes, {}), "passes": passes,
     }
 
@@ -423,7 +462,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", choices=("headline", *OTHER), default="headline",
-                    help="headline (default) or one of the other two workloads of the path")
+                    help="headline (default) or one of the other workloads of the path")
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -50,27 +50,30 @@ struct FeatP {
 };
 
 // One token row of x from LDS in the accumulator layout (dims 16db+4g+i):
-// input RoPE, L2 norm.  Keeps the rotated x in xr, writes xn over the row,
-// returns ||x_rot||.
+// input RoPE (factors preloaded in ir), L2 norm.  Keeps the rotated x in xr,
+// writes xn over the row, returns 1 / max(||x_rot||, eps) and sets `big`
+// when ||x_rot|| > eps.
 template <typename E, int D>
-__device__ __forceinline__ float load_xn(const FeatP& p, int t, bool valid, int g, E* xrow, float (*xr)[4]) {
+__device__ __forceinline__ float load_xn(const FeatP& p, const RopeRegs<D / 16>& ir, int g, E* xrow,
+                                         float (*xr)[4], bool& big) {
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) ld4f<E>(xrow + db * 16 + 4 * g, xr[db]);
   float ss = 0.f;
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
-    ld4f<E>(xrow + db * 16 + 4 * g, xr[db]);
-    if (db * 16 < p.in_rot)  // uniform: blocks past the rotated dims skip the table reads
-      rope4(xr[db], db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, false);
+    if (db * 16 < p.in_rot) ir.apply(xr[db], db, p.in_rot, g, false);  // uniform per block
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss += xr[db][i] * xr[db][i];
   }
   const float nrm = sqrtf(sum_g(ss));
+  big = nrm > p.eps;
   const float inv = rcp(fmaxf(nrm, p.eps));
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
     float o[4] = {xr[db][0] * inv, xr[db][1] * inv, xr[db][2] * inv, xr[db][3] * inv};
     st4f<E>(xrow + db * 16 + 4 * g, o);
   }
-  return nrm;
+  return inv;
 }
 
 // In-register feature map of a^T (lane = token).  Leaves h in `hv`; returns
@@ -92,19 +95,19 @@ __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const flo
     for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pre = a[fb][i] * rinv - tau;
-        const float f = (fb < nfb && pre > 0.f) ? pre * pre : 0.f;
+        const float r = __builtin_amdgcn_fmed3f(fmaf(a[fb][i], rinv, -tau), 0.f, __FLT_MAX__);  // relu
+        const float f = fb < nfb ? r * r : 0.f;
         hv[fb][i] = f;
         sf += f;
       }
     mass = sum_g(sf);
     const bool ok = mass > p.eps;
     const float inv = ok ? rcp(mass) : 0.f;
-    const float uni = p.inv_m;
+    const float uni = ok ? 0.f : p.inv_m;  // the uniform fallback below eps
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) hv[fb][i] = ok ? hv[fb][i] * inv : uni;
+      for (int i = 0; i < 4; ++i) hv[fb][i] = fmaf(hv[fb][i], inv, uni);
   } else {
     float m_ = -INFINITY;
 #pragma unroll
@@ -208,25 +211,32 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
   RowTile<E, D> ldx;
   ldx.init(D, tid);
   const int g0 = blockIdx.x * p.groups;
-  ldx.fetch(xsrc, g0 * TT, p.T);
+  ldx.fetch_all(xsrc, g0 * TT, p.T);
   // groups this workgroup owns (>= 1: the grid covers the tiles exactly)
   const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
   for (int grp = 0; grp < ng; ++grp) {
     const int t0 = (g0 + grp) * TT;
     __syncthreads();       // weights staged; previous group's rows written out
-    ldx.store(xs, L.xp);
-    // the next group's rows (none after the last group: a bound of 0 loads
-    // nothing, and the prefetch registers take one path through the loop)
-    ldx.fetch(xsrc, t0 + TT, grp + 1 < ng ? p.T : 0);
-    __syncthreads();
-
+    ldx.store_valid(xs, L.xp, t0, p.T);
     const int row = w * 16 + l16;
     const int t = t0 + row;
     const bool valid = t < p.T;
+    // input-RoPE factors ahead of the prefetch (needed first); the feature
+    // rotation, applied after the map, reads its tables there (registers for
+    // both would cost this kernel a resident wave per SIMD)
+    RopeRegs<D / 16> ir;
+    ir.fetch(p.in_rot, p.in_cos, p.in_sin, t, valid, g);
+    // the next group's rows (after the last group, this group's own rows
+    // again: cached, never stored)
+    const int tmax = grp + 1 < ng ? p.T : min(p.T, t0 + TT);
+    ldx.fetch_all(xsrc, t0 + TT, tmax);
+    __syncthreads();
+
     E* xrow = xs + row * L.xp;
     float xr[D / 16][4];
-    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
-    __syncthreads();  // xn rows complete before they feed the MFMA
+    bool big;
+    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     floatx4 a[MB], hv[MB];
     gemm_a<E, D, MB>(w1, wp1, xs + w * 16 * L.xp, L.xp, l16, g, nfb, a);
@@ -248,7 +258,6 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
     if (want_resid) {
       floatx4 base_[D / 16];
       gemm_back<E, D, MB>(w2, wp2, hv, l16, g, nfb, base_);
-      const float inv = rcp(fmaxf(nrm, p.eps));
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
         float v[4];
@@ -326,105 +335,156 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
   ldr.init(has_resid ? D : 0, tid);
   ldp.init(m, tid);
   const int g0 = blockIdx.x * p.groups;
-  ldx.fetch(xsrc, g0 * TT, p.T);
-  ldp.fetch(psrc, g0 * TT, p.T);
-  if (has_resid) ldr.fetch(rsrc, g0 * TT, p.T);
+  ldx.fetch_all(xsrc, g0 * TT, p.T);
+  ldp.fetch_all(psrc, g0 * TT, p.T);
+  if (has_resid) ldr.fetch_all(rsrc, g0 * TT, p.T);
 
   const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
   for (int grp = 0; grp < ng; ++grp) {
     const int t0 = (g0 + grp) * TT;
     __syncthreads();       // weights staged; previous group fully consumed
-    ldx.store(xs, L.xp);
-    ldp.store(ps, L.mp);
-    if (has_resid) ldr.store(rs, L.xp);
-    // next group's rows; a bound of 0 after the last group loads nothing
-    const int next_T = grp + 1 < ng ? p.T : 0;
-    ldx.fetch(xsrc, t0 + TT, next_T);
-    ldp.fetch(psrc, t0 + TT, next_T);
-    if (has_resid) ldr.fetch(rsrc, t0 + TT, next_T);
-    __syncthreads();
-
+    ldx.store_valid(xs, L.xp, t0, p.T);
+    ldp.store_valid(ps, L.mp, t0, p.T);
+    if (has_resid) ldr.store_valid(rs, L.xp, t0, p.T);
     const int row = w * 16 + l16;
     const int t = t0 + row;
     const bool valid = t < p.T;
+    RopeRegs<D / 16> ir;
+    RopeRegs<MB> fr;
+    ir.fetch(p.in_rot, p.in_cos, p.in_sin, t, valid, g);
+    fr.fetch(p.feat_rot, p.f_cos, p.f_sin, t, valid, g);
+    // next group's rows (after the last group, this group's own rows again:
+    // cached, never stored)
+    const int tmax = grp + 1 < ng ? p.T : min(p.T, t0 + TT);
+    ldx.fetch_all(xsrc, t0 + TT, tmax);
+    ldp.fetch_all(psrc, t0 + TT, tmax);
+    if (has_resid) ldr.fetch_all(rsrc, t0 + TT, tmax);
+    __syncthreads();
+
     E* xrow = xs + row * L.xp;
     float xr[D / 16][4];
-    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
-    __syncthreads();  // xn rows complete before they feed the MFMA
+    bool big;
+    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
-    floatx4 a[MB], hv[MB];
+    floatx4 a[MB];
     gemm_a<E, D, MB>(w1, wpa, xs + w * 16 * L.xp, L.xp, l16, g, nfb, a);
-    float rinv, mass;
-    feature_map<KIND, MB>(p, tau, a, nfb, hv, rinv, mass);
+    float ssa = 0.f;
+#pragma unroll
+    for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ssa += a[fb][i] * a[fb][i];
+    const float rinv = rsqrtf(sum_g(ssa) * p.inv_m + p.eps);
 
     // dh = rotate^T(dphi) (+ s W2^T dresid); rows past T are zero in LDS
     floatx4 dh[MB];
     const E* rrow = rs + row * L.xp;
+    if constexpr (has_resid) {
 #pragma unroll
-    for (int fb = 0; fb < MB; ++fb) {
-      dh[fb] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (has_resid && fb < nfb) {
+      for (int fb = 0; fb < MB; ++fb) {
+        dh[fb] = floatx4{0.f, 0.f, 0.f, 0.f};
         const E* wrow = w2t + (fb * 16 + l16) * wpa;
 #pragma unroll
         for (int kk = 0; kk < D / 32; ++kk)
           dh[fb] = mma32(IO::ld8(wrow + kk * 32 + 8 * g), IO::ld8(rrow + kk * 32 + 8 * g), dh[fb]);
         if (D % 32)
           dh[fb] = mma16(IO::ld4(wrow + (D / 32) * 32 + 4 * g), IO::ld4(rrow + (D / 32) * 32 + 4 * g), dh[fb]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dh[fb][i] *= p.s;
       }
     }
-    float sdh = 0.f;
     {
       const E* prow = ps + row * L.mp;
+      float v[MB][4];
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb) ld4f<E>(prow + fb * 16 + 4 * g, v[fb]);
 #pragma unroll
       for (int fb = 0; fb < MB; ++fb) {
-        if (fb < nfb) {
-          float v[4];
-          ld4f<E>(prow + fb * 16 + 4 * g, v);
-          if (fb * 16 < p.feat_rot)
-            rope4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, t, valid && fb * 16 + 4 * g < p.feat_rot, true);
+        if (fb * 16 < p.feat_rot) fr.apply(v[fb], fb, p.feat_rot, g, true);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            dh[fb][i] += v[i];
-            sdh += dh[fb][i] * hv[fb][i];
-          }
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (has_resid) dh[fb][i] = fmaf(p.s, dh[fb][i], v[fb][i]);
+          else dh[fb][i] = v[fb][i];
         }
       }
     }
-    sdh = sum_g(sdh);
-    // dpre -> da (RMSNorm backward); dh becomes da
-    // relu2: h = f / sum f with f = relu(pre)^2 (the uniform fallback below
-    // eps has no gradient); softmax: h = softmax(gain pre)
-    const float scale = KIND == TS_FEAT_RELU2 ? (mass > p.eps ? 2.0f * rcp(mass) : 0.f) : p.gain;
-    float sdp = 0.f, sda = 0.f;
+
+    // The pre-activation gradient is dscale * dp (dp left in dh), with
+    // sdp = sum_i dp_i and sda = sum_i dp_i a_i; hv holds h where it is written.
+    // relu2: h = f / sum f, f = r^2, r = relu(pre) (the uniform 1/m below eps
+    //   has no gradient): dpre_i = (2/mass) r_i (dh_i - sum_j dh_j h_j), so
+    //   with u = dh r, dp = u - (sum_j u_j r_j / mass) r and dscale = 2/mass.
+    // softmax: h = softmax(gain pre): dp = h (dh - sum_j dh_j h_j), dscale = gain.
+    constexpr bool need_h = !WG || has_resid;
+    floatx4 hv[MB];
+    float dscale, sdp = 0.f, sda = 0.f;
+    if constexpr (KIND == TS_FEAT_RELU2) {
+      floatx4 r[MB];
+      float sf = 0.f;
 #pragma unroll
-    for (int fb = 0; fb < MB; ++fb) {
+      for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float dp = 0.f;
-        if (fb < nfb) {
-          if constexpr (KIND == TS_FEAT_RELU2)
-            dp = (dh[fb][i] - sdh) * scale * fmaxf(a[fb][i] * rinv - tau, 0.f);
-          else
-            dp = scale * hv[fb][i] * (dh[fb][i] - sdh);
+        for (int i = 0; i < 4; ++i) {
+          r[fb][i] = __builtin_amdgcn_fmed3f(fmaf(a[fb][i], rinv, -tau), 0.f, __FLT_MAX__);
+          sf = fmaf(r[fb][i], r[fb][i], sf);
         }
-        dh[fb][i] = dp;
-        sdp += dp;
-        sda += dp * a[fb][i];
+      const float mass = sum_g(sf);
+      const bool ok = mass > p.eps;
+      const float inv_mass = ok ? rcp(mass) : 0.f;
+      float su = 0.f;
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dh[fb][i] *= r[fb][i];
+          su = fmaf(dh[fb][i], r[fb][i], su);
+        }
+      const float sdh = sum_g(su) * inv_mass;
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dh[fb][i] = fmaf(-sdh, r[fb][i], dh[fb][i]);
+          sdp += dh[fb][i];
+          sda = fmaf(dh[fb][i], a[fb][i], sda);
+        }
+      dscale = 2.f * inv_mass;
+      if constexpr (need_h) {
+        const float uni = ok ? 0.f : p.inv_m;
+#pragma unroll
+        for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) hv[fb][i] = fmaf(r[fb][i] * r[fb][i], inv_mass, uni);
       }
+    } else {
+      float rinv_, mass;
+      feature_map<KIND, MB>(p, tau, a, nfb, hv, rinv_, mass);
+      float sdh = 0.f;
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sdh = fmaf(dh[fb][i], hv[fb][i], sdh);
+      sdh = sum_g(sdh);
+#pragma unroll
+      for (int fb = 0; fb < MB; ++fb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dh[fb][i] = hv[fb][i] * (dh[fb][i] - sdh);
+          sdp += dh[fb][i];
+          sda = fmaf(dh[fb][i], a[fb][i], sda);
+        }
+      dscale = p.gain;
     }
-    sdp = sum_g(sdp);
-    sda = sum_g(sda);
+    sdp = sum_g(sdp) * dscale;
+    sda = sum_g(sda) * dscale;
     if (g == 0 && valid) {
       if (WG) dtau_acc -= sdp;
       else if (p.dtau.ptr) *rows_of<float>(p.dtau, b, h).at(t) = -sdp;
     }
-    const float c3 = rinv * rinv * rinv * sda * p.inv_m;
+    // RMSNorm backward: da = rinv dpre - rinv^3 (sum_j dpre_j a_j / m) a
+    const float c1 = rinv * dscale, c3 = rinv * rinv * rinv * sda * p.inv_m;
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dh[fb][i] = rinv * dh[fb][i] - c3 * a[fb][i];
+      for (int i = 0; i < 4; ++i) dh[fb][i] = c1 * dh[fb][i] - c3 * a[fb][i];
 
     if constexpr (WG) {
       // da over this lane's dphi entries; h for the dW2 contraction
@@ -432,13 +492,11 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
       E* hrow = hs + row * L.mp;
 #pragma unroll
       for (int fb = 0; fb < MB; ++fb) {
-        if (fb < nfb) {
-          float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
-          st4f<E>(prow + fb * 16 + 4 * g, v);
-          if (has_resid) {
-            float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
-            st4f<E>(hrow + fb * 16 + 4 * g, u);
-          }
+        float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
+        st4f<E>(prow + fb * 16 + 4 * g, v);
+        if constexpr (has_resid) {
+          float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
+          st4f<E>(hrow + fb * 16 + 4 * g, u);
         }
       }
     } else if (valid) {
@@ -447,12 +505,10 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
       E* xn_out = p.xn.ptr ? rows_of<E>(p.xn, b, h).at(t) : nullptr;
 #pragma unroll
       for (int fb = 0; fb < MB; ++fb) {
-        if (fb < nfb) {
-          float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
-          if (da_out) st4f<E>(da_out + fb * 16 + 4 * g, v);
-          float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
-          if (h_out) st4f<E>(h_out + fb * 16 + 4 * g, u);
-        }
+        float v[4] = {dh[fb][0], dh[fb][1], dh[fb][2], dh[fb][3]};
+        if (da_out) st4f<E>(da_out + fb * 16 + 4 * g, v);
+        float u[4] = {hv[fb][0], hv[fb][1], hv[fb][2], hv[fb][3]};
+        if (h_out) st4f<E>(h_out + fb * 16 + 4 * g, u);
       }
       if (xn_out) {
 #pragma unroll
@@ -467,8 +523,8 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
     // dxn^T = W1^T da^T  (W1^T given as [D x m])
     floatx4 dxn[D / 16];
     gemm_back<E, D, MB>(w1t, wpt, dh, l16, g, nfb, dxn);
-    // residual path, L2-norm backward, input-RoPE backward at dims 16db+4g+i
-    const float inv = rcp(fmaxf(nrm, p.eps));
+    // residual path, L2-norm backward (x / max(||x||, eps): the projection
+    // term only where ||x|| > eps), input-RoPE backward at dims 16db+4g+i
     float dot = 0.f;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
@@ -481,18 +537,16 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dot += dxn[db][i] * xr[db][i];
     }
-    dot = sum_g(dot) * inv * inv;
+    dot = sum_g(dot);  // every lane takes part in the cross-lane sum
+    dot = big ? dot * inv * inv : 0.f;
     {
-      const bool big = nrm > p.eps;
-      const float scale = big ? rcp(nrm) : rcp(p.eps);
       E* orow = os + row * L.xp;
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (big ? dxn[db][i] - xr[db][i] * dot : dxn[db][i]) * scale;
-        if (db * 16 < p.in_rot)
-          rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, true);
+        for (int i = 0; i < 4; ++i) v[i] = (dxn[db][i] - xr[db][i] * dot) * inv;
+        if (db * 16 < p.in_rot) ir.apply(v, db, p.in_rot, g, true);
         st4f<E>(orow + db * 16 + 4 * g, v);
       }
     }
@@ -705,17 +759,20 @@ __global__ __launch_bounds__(256) void feature_fwd_wide_kernel(FeatP p) {
     const int t0 = (g0 + grp) * TT;
     __syncthreads();  // weights staged; previous group's rows written out
     ldx.store(xs, L.xp);
-    ldx.fetch(xsrc, t0 + TT, grp + 1 < ng ? p.T : 0);
-    __syncthreads();
-
     const int row = w * 16 + l16;
     const int t = t0 + row;
     const bool valid = t < p.T;
+    RopeRegs<D / 16> ir;
+    ir.fetch(p.in_rot, p.in_cos, p.in_sin, t, valid, g);
+    ldx.fetch(xsrc, t0 + TT, grp + 1 < ng ? p.T : 0);
+    __syncthreads();
+
     E* xrow = xs + row * L.xp;
     const E* xs_w = xs + w * 16 * L.xp;
     float xr[D / 16][4];
-    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
-    __syncthreads();  // xn rows complete before they feed the MFMA
+    bool big;
+    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     float rinv, mass, mx;
     wide_stats<D, KIND, NC>(p, tau, w1s, L.xp, xs_w, l16, g, rinv, mass, mx);
@@ -751,7 +808,6 @@ __global__ __launch_bounds__(256) void feature_fwd_wide_kernel(FeatP p) {
       __syncthreads();
     }
     if (want_resid) {
-      const float inv = rcp(fmaxf(nrm, p.eps));
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
         float v[4];
@@ -801,20 +857,23 @@ __global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
     __syncthreads();  // weights staged; previous group fully consumed
     ldx.store(xs, L.xp);
     if (RESID) ldr.store(rs, L.xp);
+    const int row = w * 16 + l16;
+    const int t = t0 + row;
+    const bool valid = t < p.T;
+    RopeRegs<D / 16> ir;
+    ir.fetch(p.in_rot, p.in_cos, p.in_sin, t, valid, g);
     const int next_T = grp + 1 < ng ? p.T : 0;
     ldx.fetch(xsrc, t0 + TT, next_T);
     if (RESID) ldr.fetch(rsrc, t0 + TT, next_T);
     __syncthreads();
 
-    const int row = w * 16 + l16;
-    const int t = t0 + row;
-    const bool valid = t < p.T;
     const E* prow = psrc.at(valid ? t : 0);
     E* xrow = xs + row * L.xp;
     const E* xs_w = xs + w * 16 * L.xp;
     float xr[D / 16][4];
-    const float nrm = load_xn<E, D>(p, t, valid, g, xrow, xr);
-    __syncthreads();  // xn rows complete before they feed the MFMA
+    bool big;
+    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     float rinv, mass, mx;
     wide_stats<D, KIND, NC>(p, tau, w1s, L.xp, xs_w, l16, g, rinv, mass, mx);
@@ -936,8 +995,8 @@ __global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
         st4f<E>(xn_out + db * 16 + 4 * g, v);
       }
     }
-    // residual path, L2-norm backward, input-RoPE backward at dims 16db+4g+i
-    const float inv = rcp(fmaxf(nrm, p.eps));
+    // residual path, L2-norm backward (x / max(||x||, eps): the projection
+    // term only where ||x|| > eps), input-RoPE backward at dims 16db+4g+i
     float dot = 0.f;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
@@ -950,18 +1009,16 @@ __global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) dot += dxn[db][i] * xr[db][i];
     }
-    dot = sum_g(dot) * inv * inv;
+    dot = sum_g(dot);  // every lane takes part in the cross-lane sum
+    dot = big ? dot * inv * inv : 0.f;
     {
-      const bool big = nrm > p.eps;
-      const float sc = big ? rcp(nrm) : rcp(p.eps);
       E* orow = os + row * L.xp;
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (big ? dxn[db][i] - xr[db][i] * dot : dxn[db][i]) * sc;
-        if (db * 16 < p.in_rot)
-          rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, true);
+        for (int i = 0; i < 4; ++i) v[i] = (dxn[db][i] - xr[db][i] * dot) * inv;
+        if (db * 16 < p.in_rot) ir.apply(v, db, p.in_rot, g, true);
         st4f<E>(orow + db * 16 + 4 * g, v);
       }
     }

@@ -64,6 +64,16 @@ __device__ __forceinline__ float max_g(float v) {
   return fmaxf(p.a, p.b);
 }
 
+// Orders this wave's LDS writes before its later LDS reads of rows that
+// other lanes of the same wave wrote: a wave's LDS operations execute in issue
+// order, so this only keeps the compiler from moving the reads above the
+// writes (no workgroup barrier where each wave reads back its own rows).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Four consecutive elements <-> floats.
 template <typename E>
 __device__ __forceinline__ void ld4f(const E* p, float* o) {
@@ -99,6 +109,45 @@ __device__ __forceinline__ void rope4(float* v, int c, int rot, const float* cs_
   v[3] = a1 * sn.y + b1 * cs.y;
 }
 
+// RoPE factors of one token for the four-feature groups 16 blk + 4g of its
+// first NB 16-wide blocks, loaded once per token group ahead of their use:
+// issued before the next group's row prefetch, a wait for them does not wait
+// for the prefetch, and all blocks' loads are in flight together.  Blocks at
+// or past `rot` load nothing; tokens past T read entry 0 (their rows are
+// zero, so any finite factor serves); a four-feature group at or past `rot`
+// inside a rotated block rotates by the identity.
+template <int NB>
+struct RopeRegs {
+  float2 cs[NB], sn[NB];
+
+  __device__ __forceinline__ void fetch(int rot, const float* cs_tab, const float* sn_tab, int t, bool valid, int g) {
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      if (blk * 16 < rot) {
+        const int c = blk * 16 + 4 * g;
+        const int idx = valid && c < rot ? t * (rot >> 1) + (c >> 1) : 0;
+        cs[blk] = *(const float2*)(cs_tab + idx);
+        sn[blk] = *(const float2*)(sn_tab + idx);
+      }
+    }
+  }
+  // Rotate v (features 16 blk + 4g .. +3) by the token's angles, or back.
+  __device__ __forceinline__ void apply(float* v, int blk, int rot, int g, bool inverse) const {
+    const bool on = blk * 16 + 4 * g < rot;
+    const float cx = on ? cs[blk].x : 1.f, cy = on ? cs[blk].y : 1.f;
+    float sx = on ? sn[blk].x : 0.f, sy = on ? sn[blk].y : 0.f;
+    if (inverse) {
+      sx = -sx;
+      sy = -sy;
+    }
+    const float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3];
+    v[0] = a0 * cx - b0 * sx;
+    v[1] = a0 * sx + b0 * cx;
+    v[2] = a1 * cy - b1 * sy;
+    v[3] = a1 * sy + b1 * cy;
+  }
+};
+
 // Register-staged copy of one [64 x width] token tile: 16-byte vectors,
 // row-major, vector idx = tid + i * 256.  Rows at or past T load as zero.
 template <typename E, int MAXW>
@@ -128,6 +177,24 @@ struct RowTile {
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i)
       if (rc[i] >= 0) *(uint4*)(dst + (rc[i] & 255) * pitch + (rc[i] >> 8)) = r[i];
+  }
+  // Branch-free fetch: every slot loads, rows clamped to tmax - 1 (1 <= tmax
+  // <= T) and unused slots reading column 0, so the loads issue as one
+  // straight-line sequence and the compiler's wait for a load issued before
+  // them need not wait for them.  store_valid() zeroes the rows at or past T.
+  __device__ __forceinline__ void fetch_all(const Rows<E>& src, int t0, int tmax) {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+      const int rcv = rc[i] < 0 ? 0 : rc[i];
+      r[i] = *(const uint4*)(src.at(min(t0 + (rcv & 255), tmax - 1)) + (rcv >> 8));
+    }
+  }
+  __device__ __forceinline__ void store_valid(E* dst, int pitch, int t0, int T) const {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i)
+      if (rc[i] >= 0)
+        *(uint4*)(dst + (rc[i] & 255) * pitch + (rc[i] >> 8)) =
+            t0 + (rc[i] & 255) < T ? r[i] : make_uint4(0u, 0u, 0u, 0u);
   }
 };
 

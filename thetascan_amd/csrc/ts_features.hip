@@ -50,18 +50,18 @@ struct FeatP {
 };
 
 // One token row of x from LDS in the accumulator layout (dims 16db+4g+i):
-// input RoPE (factors preloaded in ir), L2 norm.  Keeps the rotated x in xr,
-// writes xn over the row, returns 1 / max(||x_rot||, eps) and sets `big`
-// when ||x_rot|| > eps.
-template <typename E, int D>
-__device__ __forceinline__ float load_xn(const FeatP& p, const RopeRegs<D / 16>& ir, int g, E* xrow,
-                                         float (*xr)[4], bool& big) {
+// input RoPE (rotate_in(v, db) rotates block db), L2 norm.  Keeps the
+// rotated x in xr, writes xn over the row, returns 1 / max(||x_rot||, eps)
+// and sets `big` when ||x_rot|| > eps.
+template <typename E, int D, typename RotIn>
+__device__ __forceinline__ float load_xn(const FeatP& p, const RotIn& rotate_in, int g, E* xrow, float (*xr)[4],
+                                         bool& big) {
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) ld4f<E>(xrow + db * 16 + 4 * g, xr[db]);
   float ss = 0.f;
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
-    if (db * 16 < p.in_rot) ir.apply(xr[db], db, p.in_rot, g, false);  // uniform per block
+    if (db * 16 < p.in_rot) rotate_in(xr[db], db);  // uniform per block
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss += xr[db][i] * xr[db][i];
   }
@@ -75,6 +75,35 @@ __device__ __forceinline__ float load_xn(const FeatP& p, const RopeRegs<D / 16>&
   }
   return inv;
 }
+
+// RoPE factors of one token for a kernel that applies both rotations: the
+// first four 16-wide blocks of one rotation are preloaded (the input rotation
+// when there is one, else the feature rotation: one register set, not two);
+// any other block reads its tables where it is applied.
+struct TokRope {
+  RopeRegs<4> pre;
+  bool in_pre;  // uniform: the preloaded factors serve the input rotation
+
+  __device__ __forceinline__ void fetch(const FeatP& p, int t, bool valid, int g) {
+    in_pre = p.in_rot > 0;
+    pre.fetch(in_pre ? p.in_rot : p.feat_rot, in_pre ? p.in_cos : p.f_cos, in_pre ? p.in_sin : p.f_sin, t, valid,
+              g);
+  }
+  __device__ __forceinline__ void apply_in(const FeatP& p, float* v, int db, int t, bool valid, int g,
+                                           bool inverse) const {
+    if (db < 4 && in_pre)
+      pre.apply(v, db, p.in_rot, g, inverse);
+    else
+      rope4(v, db * 16 + 4 * g, p.in_rot, p.in_cos, p.in_sin, t, valid && db * 16 + 4 * g < p.in_rot, inverse);
+  }
+  __device__ __forceinline__ void apply_feat(const FeatP& p, float* v, int fb, int t, bool valid, int g,
+                                             bool inverse) const {
+    if (fb < 4 && !in_pre)
+      pre.apply(v, fb, p.feat_rot, g, inverse);
+    else
+      rope4(v, fb * 16 + 4 * g, p.feat_rot, p.f_cos, p.f_sin, t, valid && fb * 16 + 4 * g < p.feat_rot, inverse);
+  }
+};
 
 // In-register feature map of a^T (lane = token).  Leaves h in `hv`; returns
 // the statistics the backward needs.  KIND is the ts_feature_kind (a
@@ -235,7 +264,8 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
     E* xrow = xs + row * L.xp;
     float xr[D / 16][4];
     bool big;
-    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    const float inv =
+        load_xn<E, D>(p, [&](float* v, int db) { ir.apply(v, db, p.in_rot, g, false); }, g, xrow, xr, big);
     wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     floatx4 a[MB], hv[MB];
@@ -278,10 +308,12 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
 template <int D, int MB>
 constexpr int wgrad_blocks() { return ((MB + 3) / 4) * (D / 16); }
 
-// Two resident waves per SIMD for the common bf16 widths: the allocator then
-// fits the backward in 256 registers without spilling.
+// Resident waves per SIMD for the common bf16 widths: three for the ReLU^2
+// key side (168 registers; its tiles take 46 KB of LDS), two with the
+// residual stream or the softmax map.
 template <typename E, int D, int MB, bool WG, bool RESID, int KIND>
-__global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)) void feature_bwd_kernel(FeatP p) {
+__global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID || KIND != TS_FEAT_RELU2 ? 2 : 3) : 1))
+    void feature_bwd_kernel(FeatP p) {
   typedef LdsIO<E> IO;
   typedef TokFrag<E> TF;
   constexpr bool WL = weights_in_lds<E, D, MB, false, WG>();
@@ -349,10 +381,8 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
     const int row = w * 16 + l16;
     const int t = t0 + row;
     const bool valid = t < p.T;
-    RopeRegs<D / 16> ir;
-    RopeRegs<MB> fr;
-    ir.fetch(p.in_rot, p.in_cos, p.in_sin, t, valid, g);
-    fr.fetch(p.feat_rot, p.f_cos, p.f_sin, t, valid, g);
+    TokRope rope;
+    rope.fetch(p, t, valid, g);
     // next group's rows (after the last group, this group's own rows again:
     // cached, never stored)
     const int tmax = grp + 1 < ng ? p.T : min(p.T, t0 + TT);
@@ -364,7 +394,8 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
     E* xrow = xs + row * L.xp;
     float xr[D / 16][4];
     bool big;
-    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    const float inv = load_xn<E, D>(
+        p, [&](float* v, int db) { rope.apply_in(p, v, db, t, valid, g, false); }, g, xrow, xr, big);
     wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     floatx4 a[MB];
@@ -398,7 +429,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
       for (int fb = 0; fb < MB; ++fb) ld4f<E>(prow + fb * 16 + 4 * g, v[fb]);
 #pragma unroll
       for (int fb = 0; fb < MB; ++fb) {
-        if (fb * 16 < p.feat_rot) fr.apply(v[fb], fb, p.feat_rot, g, true);
+        if (fb * 16 < p.feat_rot) rope.apply_feat(p, v[fb], fb, t, valid, g, true);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if constexpr (has_resid) dh[fb][i] = fmaf(p.s, dh[fb][i], v[fb][i]);
@@ -546,7 +577,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? 2 : 1)
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (dxn[db][i] - xr[db][i] * dot) * inv;
-        if (db * 16 < p.in_rot) ir.apply(v, db, p.in_rot, g, true);
+        if (db * 16 < p.in_rot) rope.apply_in(p, v, db, t, valid, g, true);
         st4f<E>(orow + db * 16 + 4 * g, v);
       }
     }
@@ -771,7 +802,8 @@ __global__ __launch_bounds__(256) void feature_fwd_wide_kernel(FeatP p) {
     const E* xs_w = xs + w * 16 * L.xp;
     float xr[D / 16][4];
     bool big;
-    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    const float inv =
+        load_xn<E, D>(p, [&](float* v, int db) { ir.apply(v, db, p.in_rot, g, false); }, g, xrow, xr, big);
     wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     float rinv, mass, mx;
@@ -872,7 +904,8 @@ __global__ __launch_bounds__(256) void feature_bwd_wide_kernel(FeatP p) {
     const E* xs_w = xs + w * 16 * L.xp;
     float xr[D / 16][4];
     bool big;
-    const float inv = load_xn<E, D>(p, ir, g, xrow, xr, big);
+    const float inv =
+        load_xn<E, D>(p, [&](float* v, int db) { ir.apply(v, db, p.in_rot, g, false); }, g, xrow, xr, big);
     wave_lds_sync();  // this wave's xn rows complete before they feed its MFMAs
 
     float rinv, mass, mx;
@@ -1179,8 +1212,11 @@ size_t lds_bytes(int es, int d, int m, bool fwd, bool resid, bool wgrad) {
 }
 
 // Launch plan of one call: fused weight gradients when a kernel exists for
-// the shape and its tiles fit in LDS; enough 64-token groups per workgroup
-// to leave about two (backward) or four (forward) resident workgroups per CU.
+// the shape and its tiles fit in LDS.  Forward: enough 64-token groups per
+// workgroup to leave about four resident workgroups per CU.  Backward: the
+// groups of each (batch, head) split over as many workgroups as the device
+// holds at once (the occupancy calculator's count for the kernel), so that
+// one wave of workgroups covers the call.
 int plan_feature(const ts_feature_desc* d, bool fwd, bool resid, bool want_wgrad, Plan* P) {
   const int es = d->dtype == TS_BF16 ? 2 : 4;
   P->wgrad = !fwd && want_wgrad && pick(d, false, true) != nullptr &&
@@ -1189,9 +1225,16 @@ int plan_feature(const ts_feature_desc* d, bool fwd, bool resid, bool want_wgrad
                       : lds_bytes(es, d->d, d->m, fwd, resid, P->wgrad);
   if (P->lds > (size_t)ts::kLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "feature: tiles need %zu bytes of LDS", P->lds);
   const int tiles = (d->T + ts::TT - 1) / ts::TT;
-  const long target = fwd ? 1024 : 512;
   int groups = 1;
-  while (groups < 16 && (long)((tiles + 2 * groups - 1) / (2 * groups)) * d->H * d->B >= target) groups *= 2;
+  if (fwd) {
+    while (groups < 16 && (long)((tiles + 2 * groups - 1) / (2 * groups)) * d->H * d->B >= 1024) groups *= 2;
+  } else {
+    long slots = ts::resident_workgroups((const void*)pick(d, false, P->wgrad, resid), (int)P->lds);
+    if (slots <= 0) slots = 512;  // two per CU on 256 CUs
+    const long per_bh = slots / ((long)d->H * d->B) > 1 ? slots / ((long)d->H * d->B) : 1;
+    const long g = (tiles + per_bh - 1) / per_bh;
+    groups = (int)(g < 1 ? 1 : g > 16 ? 16 : g);
+  }
   P->groups = groups;
   P->grid = dim3((tiles + groups - 1) / groups, d->H, d->B);
   return TS_OK;

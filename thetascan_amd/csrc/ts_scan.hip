@@ -40,7 +40,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
+#include <tuple>
 #include <unordered_map>
 
 namespace ts {
@@ -894,6 +896,24 @@ hipError_t ensure_lds_limit(const void* fn, int bytes) {
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   if (e == hipSuccess) limits[fn] = bytes;
   return e;
+}
+
+long resident_workgroups(const void* fn, int lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int>, long> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(dev, fn, lds);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  long n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, (size_t)lds) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    n = (long)per_cu * cus;
+  cache[key] = n;
+  return n;
 }
 
 }  // namespace ts

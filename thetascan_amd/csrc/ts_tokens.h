@@ -190,6 +190,10 @@ struct RowTile {
     }
   }
   __device__ __forceinline__ void store_valid(E* dst, int pitch, int t0, int T) const {
+    if (t0 + TT <= T) {  // a whole group (uniform): every row is valid
+      store(dst, pitch);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i)
       if (rc[i] >= 0)

@@ -577,7 +577,10 @@ def _kernel_mixer_forward(x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tenso
     st = _State()
     y = _memory_forward(st, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, w_g is not None)
     out = torch.nn.functional.linear(y, w_out)
-    return [out, proj, y] + [x.new_empty(0) if getattr(st, n) is None else getattr(st, n) for n in _State.SAVED]
+    # the stacked [W_qkv; W_g] travels to the backward's input-gradient GEMM
+    stacked = weight if w_g is not None else x.new_empty(0)
+    return [out, proj, y] + [x.new_empty(0) if getattr(st, n) is None else getattr(st, n)
+                             for n in _State.SAVED] + [stacked]
 
 
 def _kernel_mixer_fake(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in_rot, feat_rot, rope_base,
@@ -593,9 +596,10 @@ def _kernel_mixer_fake(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in
     y = x.new_empty(B, T, H * d)
     plan = _memory_plan(spec, B, H, T, d, dt, tau, b_g, w1, w2, normalize, w_g is not None, seg_chunks) \
         if _use_native(proj, tau, b_g) else None
+    stacked = x.new_empty(P, x.shape[-1]) if w_g is not None else x.new_empty(0)
     if plan is not None:
         return [out, proj, y, torch.empty(plan[1], dtype=torch.uint8, device=dev)] + \
-            [x.new_empty(0) for _ in range(6)]
+            [x.new_empty(0) for _ in range(6)] + [stacked]
     ws = x.new_empty(0)
     if m == d:
         nbytes = scan_hip.workspace_bytes(B, H, T, m, d, dt, seg_chunks=seg_chunks, v_ext=normalize)
@@ -603,7 +607,7 @@ def _kernel_mixer_fake(x, w_qkv, w_g, b_g, w1, w2, tau, w_out, kind, m, gain, in
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     mass = torch.empty(B, H, T, dtype=torch.float32, device=dev) if normalize else x.new_empty(0)
     return [out, proj, y, x.new_empty(0), ws, x.new_empty(B, H, T, m), x.new_empty(B, H, T, m),
-            x.new_empty(B, H, T, d), mass, x.new_empty(B, H, T, d)]
+            x.new_empty(B, H, T, d), mass, x.new_empty(B, H, T, d), stacked]
 
 
 def _kernel_mixer_backward_impl(dout: torch.Tensor, x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tensor | None,
@@ -614,12 +618,13 @@ def _kernel_mixer_backward_impl(dout: torch.Tensor, x: torch.Tensor, w_qkv: torc
                          need: list[bool]) -> list[torch.Tensor]:
     spec = FeatureSpec(kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps)
     has_gate = w_g is not None
-    st = _restore(saved, proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
+    stacked = saved[-1]
+    st = _restore(saved[:-1], proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
     d2 = dout.reshape(-1, w_out.shape[0])
     dw_out = weight_grad(d2, y.reshape(-1, y.shape[-1]), w_out.dtype) if need[7] else None
     dy = (d2 @ w_out).view(y.shape)
     dproj, dw1, dw2, dtau, db_g = _memory_backward(st, dy, need[4], need[5], need[6], need[3])
-    weight = w_qkv if w_g is None else _stacked(w_qkv, w_g)
+    weight = w_qkv if w_g is None else stacked
     P = weight.shape[0]
     dp2 = dproj.view(-1, P)
     dx = (dp2 @ weight).view(x.shape) if need[0] else None

@@ -237,15 +237,19 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
   const float tau = p.has_tau ? p.tau[h] : 0.f;
   const Rows<E> xsrc = rows_of<E>(p.x, b, h);
 
-  RowTile<E, D> ldx;
-  ldx.init(D, tid);
+  // Each wave loads, computes and writes back its own 16 rows of every
+  // group, so the group loop needs no workgroup barrier (only the weights'
+  // staging does, once).
+  WaveRows<E, D> ldx;
+  ldx.init(D, w, lane);
   const int g0 = blockIdx.x * p.groups;
   ldx.fetch_all(xsrc, g0 * TT, p.T);
   // groups this workgroup owns (>= 1: the grid covers the tiles exactly)
   const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
+  __syncthreads();  // weights staged
   for (int grp = 0; grp < ng; ++grp) {
     const int t0 = (g0 + grp) * TT;
-    __syncthreads();       // weights staged; previous group's rows written out
+    wave_lds_sync();  // the previous group's rows written out
     ldx.store_valid(xs, L.xp, t0, p.T);
     const int row = w * 16 + l16;
     const int t = t0 + row;
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
     // again: cached, never stored)
     const int tmax = grp + 1 < ng ? p.T : min(p.T, t0 + TT);
     ldx.fetch_all(xsrc, t0 + TT, tmax);
-    __syncthreads();
+    wave_lds_sync();
 
     E* xrow = xs + row * L.xp;
     float xr[D / 16][4];
@@ -296,9 +300,9 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
         st4f<E>(xrow + db * 16 + 4 * g, v);  // resid over this lane's own xn entries
       }
     }
-    __syncthreads();
-    write_rows<E>(ps, L.mp, rows_of<E>(p.phi, b, h), t0, p.T, m, tid);
-    if (want_resid) write_rows<E>(xs, L.xp, rows_of<E>(p.resid, b, h), t0, p.T, D, tid);
+    wave_lds_sync();
+    write_rows_wave<E>(ps, L.mp, rows_of<E>(p.phi, b, h), t0, p.T, m, w, lane);
+    if (want_resid) write_rows_wave<E>(xs, L.xp, rows_of<E>(p.resid, b, h), t0, p.T, D, w, lane);
   }
 }
 
@@ -361,11 +365,14 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
   for (int k = 0; k < NB; ++k) acc1[k] = acc2[k] = floatx4{0.f, 0.f, 0.f, 0.f};
   float dtau_acc = 0.f;
 
-  RowTile<E, D> ldx, ldr;
-  RowTile<E, MB * 16> ldp;
-  ldx.init(D, tid);
-  ldr.init(has_resid ? D : 0, tid);
-  ldp.init(m, tid);
+  // Each wave loads its own 16 rows of every group (no barrier between the
+  // rows' store and their first use); the weight-gradient contraction reads
+  // all 64 rows, so the group still starts and ends on a workgroup barrier.
+  WaveRows<E, D> ldx, ldr;
+  WaveRows<E, MB * 16> ldp;
+  ldx.init(D, w, lane);
+  ldr.init(has_resid ? D : 0, w, lane);
+  ldp.init(m, w, lane);
   const int g0 = blockIdx.x * p.groups;
   ldx.fetch_all(xsrc, g0 * TT, p.T);
   ldp.fetch_all(psrc, g0 * TT, p.T);
@@ -389,7 +396,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
     ldx.fetch_all(xsrc, t0 + TT, tmax);
     ldp.fetch_all(psrc, t0 + TT, tmax);
     if (has_resid) ldr.fetch_all(rsrc, t0 + TT, tmax);
-    __syncthreads();
+    wave_lds_sync();
 
     E* xrow = xs + row * L.xp;
     float xr[D / 16][4];
@@ -581,8 +588,8 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
         st4f<E>(orow + db * 16 + 4 * g, v);
       }
     }
-    __syncthreads();  // da, h, xn, dx rows of all four waves complete
-    write_rows<E>(os, L.xp, rows_of<E>(p.dx, b, h), t0, p.T, D, tid);
+    __syncthreads();  // da, h, xn rows of all four waves complete (the contraction reads them all)
+    write_rows_wave<E>(os, L.xp, rows_of<E>(p.dx, b, h), t0, p.T, D, w, lane);
 
     if constexpr (WG) {
       // dW1[f][e] += sum_t da[t][f] xn[t][e];  dW2[e][f] += sum_t dresid[t][e] h[t][f]

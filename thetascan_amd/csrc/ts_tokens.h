@@ -202,6 +202,59 @@ struct RowTile {
   }
 };
 
+// The same for the 16 rows of a [64 x width] token tile that one wave
+// computes (rows 16w .. 16w+15, vector idx = lane + i * 64), so that a wave
+// that fills, reads and writes back only its own rows needs no workgroup
+// barrier for them.
+template <typename E, int MAXW>
+struct WaveRows {
+  static constexpr int VEC = 16 / (int)sizeof(E);
+  static constexpr int SLOTS = (16 * MAXW / VEC + 63) / 64;
+  uint4 r[SLOTS];
+  int rc[SLOTS];  // row | column << 8, or -1 for an unused slot
+
+  __device__ __forceinline__ void init(int width, int w, int lane) {
+    const int per_row = width / VEC;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+      const int idx = lane + i * 64;
+      const int row = per_row ? idx / per_row : 0;
+      rc[i] = idx < 16 * per_row ? (16 * w + row) | (((idx - row * per_row) * VEC) << 8) : -1;
+    }
+  }
+  // Every slot loads (rows clamped to tmax - 1, 1 <= tmax <= T; unused slots
+  // read the wave's first row), one straight-line sequence of loads.
+  __device__ __forceinline__ void fetch_all(const Rows<E>& src, int t0, int tmax) {
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+      const int rcv = rc[i] < 0 ? (rc[0] & 255) : rc[i];
+      r[i] = *(const uint4*)(src.at(min(t0 + (rcv & 255), tmax - 1)) + (rcv >> 8));
+    }
+  }
+  __device__ __forceinline__ void store_valid(E* dst, int pitch, int t0, int T) const {
+    const bool whole = t0 + TT <= T;  // uniform
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i)
+      if (rc[i] >= 0)
+        *(uint4*)(dst + (rc[i] & 255) * pitch + (rc[i] >> 8)) =
+            whole || t0 + (rc[i] & 255) < T ? r[i] : make_uint4(0u, 0u, 0u, 0u);
+  }
+};
+
+// LDS rows 16w .. 16w+15 of a [64 x width] tile -> global rows (rows past T
+// dropped); one wave.
+template <typename E>
+__device__ __forceinline__ void write_rows_wave(const E* src, int pitch, const Rows<E>& dst, int t0, int T, int width,
+                                                int w, int lane) {
+  constexpr int VEC = 16 / (int)sizeof(E);
+  const int per_row = width / VEC;
+  for (int idx = lane; idx < 16 * per_row; idx += 64) {
+    const int row = 16 * w + idx / per_row;
+    const int c = (idx - (idx / per_row) * per_row) * VEC;
+    if (t0 + row < T) *(uint4*)(dst.at(t0 + row) + c) = *(const uint4*)(src + row * pitch + c);
+  }
+}
+
 // LDS rows of a [64 x width] tile -> global rows t0.. (rows past T dropped).
 template <typename E>
 __device__ __forceinline__ void write_rows(const E* src, int pitch, const Rows<E>& dst, int t0, int T, int width,

@@ -460,7 +460,7 @@ __global__ __launch_bounds__(256) void sum_slots_kernel(const float* a, int na, 
 }
 
 // The same sum over 16-byte columns: a block is (256 / R) columns of four
-// outputs x R slot rows; row r adds slots r, r + R, ... (two loads in flight
+// outputs x R slot rows; row r adds slots r, r + R, ... (four loads in flight
 // per step), and the R rows of a column combine through LDS in row order, so
 // the result does not depend on timing.  R grows with the slot count when
 // there are few columns, so a wide sum and a tall one both fill the chip.
@@ -472,20 +472,22 @@ __device__ __forceinline__ void sum_slots_block(const float* a, int na, const fl
   const int cl = tid % CPB, r = tid / CPB;
   const int64_t v = blk * CPB + cl;
   const int total = na + nb;
-  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0, acc2 = acc0, acc3 = acc0;
   if (v < nv) {
     const floatx4* av = (const floatx4*)a;
     const floatx4* bv = (const floatx4*)b;
     auto slot = [&](int t) -> floatx4 { return t < na ? av[(int64_t)t * nv + v] : bv[(int64_t)(t - na) * nv + v]; };
     int t = r;
-    for (; t + R < total; t += 2 * R) {
-      const floatx4 x0 = slot(t), x1 = slot(t + R);
+    for (; t + 3 * R < total; t += 4 * R) {
+      const floatx4 x0 = slot(t), x1 = slot(t + R), x2 = slot(t + 2 * R), x3 = slot(t + 3 * R);
       acc0 += x0;
       acc1 += x1;
+      acc2 += x2;
+      acc3 += x3;
     }
-    if (t < total) acc0 += slot(t);
+    for (; t < total; t += R) acc0 += slot(t);
   }
-  red[tid] = acc0 + acc1;
+  red[tid] = (acc0 + acc1) + (acc2 + acc3);
   __syncthreads();
   if (r == 0 && v < nv) {
     floatx4 sum = red[cl];
@@ -534,7 +536,9 @@ __global__ __launch_bounds__(256) void sum_slots_multi_kernel(SlotJobs J) {
     case 2: sum_slots_block<2>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
     case 4: sum_slots_block<4>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
     case 8: sum_slots_block<8>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
-    default: sum_slots_block<16>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    case 16: sum_slots_block<16>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    case 32: sum_slots_block<32>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
+    default: sum_slots_block<64>(J.a[j], J.na[j], J.b[j], J.nb[j], J.nv[j], J.out[j], J.ob[j], J.scale[j], blk, red); break;
   }
 }
 
@@ -717,11 +721,11 @@ int qknorm_launch(const ts_qknorm_desc* d, ts_strided x, ts_strided dy, ts_strid
 
 namespace ts {
 
-// Slot rows per column of the vectorised sum: enough threads to fill the chip,
-// at most one slot per row step.
+// Slot rows per column of the vectorised sum: enough threads to fill the chip
+// (about 2^18 of them), at most one slot per row step.
 static int slot_rows(int64_t nv, int total) {
   int R = 1;
-  while (R < 16 && R < total && nv * R < 65536) R <<= 1;
+  while (R < 64 && R < total && nv * R < 262144) R <<= 1;
   return R;
 }
 
@@ -849,7 +853,9 @@ int ts_sum_slots(const float* a, int32_t na, const float* b, int32_t nb, int64_t
       case 2: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<2>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
       case 4: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<4>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
       case 8: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<8>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
-      default: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<16>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      case 16: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<16>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      case 32: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<32>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
+      default: hipLaunchKernelGGL(ts::sum_slots_vec_kernel<64>, grid, dim3(256), 0, stream, a, na, b, nb, nv, out, ob, scale); break;
     }
     return finish("sum_slots");
   }

@@ -338,19 +338,20 @@ __global__ __launch_bounds__(256) void qknorm_bwd_kernel(NormP p) {
 // Decayed prefix z_u = a_u z_{u-1} + x_u along the scan order u (t = u, or
 // t = T-1-u for an anti-causal scan), parallel over time: the order is cut
 // into S segments of L steps.
-//   wcumsum_local_kernel : each thread scans one (b, h, segment, feature) from
-//                          a zero state, stores the local prefix l_u, the
-//                          segment's last value and (feature 0) its decay
-//                          product P = prod a_u;
-//   wcumsum_carry_kernel : each thread of segment j >= 1 folds the earlier
-//                          segments' (P, last) into the entering state C_j
-//                          (C_{j+1} = P_j C_j + last_j, in segment order) and
-//                          adds A_u C_j to its outputs, A_u = prod of a over
-//                          the segment up to u.
-// Consecutive threads take consecutive features, so every access is a
-// coalesced row.  Step decays: static exp(log_alpha[h]); a stream's a_u is
-// exp(decay[t]) causally and exp(decay[t+1]) anti-causally (the decay of the
-// token the state steps out of), 1 past the end.
+//   wcumsum_summary_kernel : each thread folds one (b, h, segment, feature)
+//                            from a zero state and stores only the segment's
+//                            last value and (feature 0) its decay product
+//                            P = prod a_u;
+//   wcumsum_main_kernel    : each thread folds the earlier segments' (P, last)
+//                            into its entering state C_j (C_{j+1} = P_j C_j +
+//                            last_j, in segment order), then walks its
+//                            segment from C_j and stores every z_u once.
+// x is read twice and z written once (the local-then-correct form wrote z
+// twice and read it back once).  Consecutive threads take consecutive
+// features, so every access is a coalesced row.  Step decays: static
+// exp(log_alpha[h]); a stream's a_u is exp(decay[t]) causally and
+// exp(decay[t+1]) anti-causally (the decay of the token the state steps out
+// of), 1 past the end.
 struct WcumsumP {
   int B, H, T, F, S, L, ret, reverse;
   ts_strided x, out, decay;
@@ -367,59 +368,61 @@ __device__ __forceinline__ float wcumsum_step(const WcumsumP& p, const float* db
   return src < p.T ? expf(db[(int64_t)src * p.decay.st]) : 1.0f;
 }
 
-__global__ __launch_bounds__(256) void wcumsum_local_kernel(WcumsumP p) {
+struct WcumsumThread {
+  int f, seg, b, h;
+  int64_t r;
+  const float* xb;
+  const float* db;
+  float a_static;
+};
+
+__device__ __forceinline__ bool wcumsum_thread(const WcumsumP& p, WcumsumThread& w) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.H * p.S * p.F) return;
-  const int f = (int)(idx % p.F);
-  const int64_t r = idx / p.F;
-  const int seg = (int)(r % p.S);
-  const int bh = (int)(r / p.S);
-  const int b = bh / p.H, h = bh % p.H;
-  const float* xb = (const float*)p.x.ptr + (int64_t)b * p.x.sb + (int64_t)h * p.x.sh + f;
-  float* ob = (float*)p.out.ptr + (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + f;
-  const float* db = p.ret == TS_RET_STREAM
-                        ? (const float*)p.decay.ptr + (int64_t)b * p.decay.sb + (int64_t)h * p.decay.sh
-                        : nullptr;
-  const float a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.0f;
-  const int u0 = seg * p.L;
+  if (idx >= (int64_t)p.B * p.H * p.S * p.F) return false;
+  w.f = (int)(idx % p.F);
+  w.r = idx / p.F;
+  w.seg = (int)(w.r % p.S);
+  const int bh = (int)(w.r / p.S);
+  w.b = bh / p.H;
+  w.h = bh % p.H;
+  w.xb = (const float*)p.x.ptr + (int64_t)w.b * p.x.sb + (int64_t)w.h * p.x.sh + w.f;
+  w.db = p.ret == TS_RET_STREAM
+             ? (const float*)p.decay.ptr + (int64_t)w.b * p.decay.sb + (int64_t)w.h * p.decay.sh
+             : nullptr;
+  w.a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[w.h]) : 1.0f;
+  return true;
+}
+
+__global__ __launch_bounds__(256) void wcumsum_summary_kernel(WcumsumP p) {
+  WcumsumThread w;
+  if (!wcumsum_thread(p, w)) return;
+  const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
   float z = 0.0f, P = 1.0f;
   for (int u = u0; u < u1; ++u) {
     const int tp = p.reverse ? p.T - 1 - u : u;
-    const float a = wcumsum_step(p, db, a_static, u);
-    z = (u == u0 ? 0.0f : a * z) + xb[(int64_t)tp * p.x.st];
+    const float a = wcumsum_step(p, w.db, w.a_static, u);
+    z = (u == u0 ? 0.0f : a * z) + w.xb[(int64_t)tp * p.x.st];
     P *= a;
-    ob[(int64_t)tp * p.out.st] = z;
   }
-  p.tot[r * p.F + f] = z;
-  if (f == 0) p.prod[r] = P;
+  p.tot[w.r * p.F + w.f] = z;
+  if (w.f == 0) p.prod[w.r] = P;
 }
 
-__global__ __launch_bounds__(256) void wcumsum_carry_kernel(WcumsumP p) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.H * p.S * p.F) return;
-  const int f = (int)(idx % p.F);
-  const int64_t r = idx / p.F;
-  const int seg = (int)(r % p.S);
-  if (seg == 0) return;
-  const int bh = (int)(r / p.S);
-  const int b = bh / p.H, h = bh % p.H;
-  const int64_t row0 = (int64_t)bh * p.S;
-  float C = 0.0f;
-  for (int j = 0; j < seg; ++j) C = p.prod[row0 + j] * C + p.tot[(row0 + j) * p.F + f];
-  float* ob = (float*)p.out.ptr + (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + f;
-  const float* db = p.ret == TS_RET_STREAM
-                        ? (const float*)p.decay.ptr + (int64_t)b * p.decay.sb + (int64_t)h * p.decay.sh
-                        : nullptr;
-  const float a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.0f;
-  const int u0 = seg * p.L;
+__global__ __launch_bounds__(256) void wcumsum_main_kernel(WcumsumP p) {
+  WcumsumThread w;
+  if (!wcumsum_thread(p, w)) return;
+  const int64_t row0 = (w.r / p.S) * p.S;
+  float z = 0.0f;  // the state entering this segment
+  for (int j = 0; j < w.seg; ++j) z = p.prod[row0 + j] * z + p.tot[(row0 + j) * p.F + w.f];
+  float* ob = (float*)p.out.ptr + (int64_t)w.b * p.out.sb + (int64_t)w.h * p.out.sh + w.f;
+  const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
-  float A = 1.0f;
   for (int u = u0; u < u1; ++u) {
     const int tp = p.reverse ? p.T - 1 - u : u;
-    A *= wcumsum_step(p, db, a_static, u);
-    float* o = ob + (int64_t)tp * p.out.st;
-    *o += A * C;
+    const float a = wcumsum_step(p, w.db, w.a_static, u);
+    z = (u == 0 ? 0.0f : a * z) + w.xb[(int64_t)tp * p.x.st];
+    ob[(int64_t)tp * p.out.st] = z;
   }
 }
 
@@ -929,10 +932,12 @@ int ts_wcumsum(const ts_wcumsum_desc* d, ts_strided x, ts_strided out, const flo
   p.prod = p.tot + (size_t)d->B * d->H * p.S * d->F;
   const int64_t n = (int64_t)d->B * d->H * p.S * d->F;
   const dim3 grid((unsigned)((n + 255) / 256));
-  hipLaunchKernelGGL(ts::wcumsum_local_kernel, grid, dim3(256), 0, stream, p);
-  if ((rc = finish("wcumsum"))) return rc;
-  if (p.S > 1) hipLaunchKernelGGL(ts::wcumsum_carry_kernel, grid, dim3(256), 0, stream, p);
-  return finish("wcumsum carry");
+  if (p.S > 1) {
+    hipLaunchKernelGGL(ts::wcumsum_summary_kernel, grid, dim3(256), 0, stream, p);
+    if ((rc = finish("wcumsum summary"))) return rc;
+  }
+  hipLaunchKernelGGL(ts::wcumsum_main_kernel, grid, dim3(256), 0, stream, p);
+  return finish("wcumsum");
 }
 
 }  // extern "C"

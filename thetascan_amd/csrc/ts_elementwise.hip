@@ -399,6 +399,7 @@ __global__ __launch_bounds__(256) void wcumsum_summary_kernel(WcumsumP p) {
   const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
   float z = 0.0f, P = 1.0f;
+#pragma unroll 8
   for (int u = u0; u < u1; ++u) {
     const int tp = p.reverse ? p.T - 1 - u : u;
     const float a = wcumsum_step(p, w.db, w.a_static, u);
@@ -418,6 +419,7 @@ __global__ __launch_bounds__(256) void wcumsum_main_kernel(WcumsumP p) {
   float* ob = (float*)p.out.ptr + (int64_t)w.b * p.out.sb + (int64_t)w.h * p.out.sh + w.f;
   const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
+#pragma unroll 8
   for (int u = u0; u < u1; ++u) {
     const int tp = p.reverse ? p.T - 1 - u : u;
     const float a = wcumsum_step(p, w.db, w.a_static, u);

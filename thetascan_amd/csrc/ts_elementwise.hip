@@ -368,6 +368,21 @@ __device__ __forceinline__ float wcumsum_step(const WcumsumP& p, const float* db
   return src < p.T ? expf(db[(int64_t)src * p.decay.st]) : 1.0f;
 }
 
+// V consecutive features per thread (V = 4: 16-byte accesses where the rows
+// allow them).
+template <int V>
+struct WVec;
+template <>
+struct WVec<1> {
+  typedef float T;
+  static __device__ __forceinline__ T zero() { return 0.f; }
+};
+template <>
+struct WVec<4> {
+  typedef floatx4 T;
+  static __device__ __forceinline__ T zero() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+};
+
 struct WcumsumThread {
   int f, seg, b, h;
   int64_t r;
@@ -376,11 +391,13 @@ struct WcumsumThread {
   float a_static;
 };
 
+template <int V>
 __device__ __forceinline__ bool wcumsum_thread(const WcumsumP& p, WcumsumThread& w) {
+  const int FV = p.F / V;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.H * p.S * p.F) return false;
-  w.f = (int)(idx % p.F);
-  w.r = idx / p.F;
+  if (idx >= (int64_t)p.B * p.H * p.S * FV) return false;
+  w.f = (int)(idx % FV) * V;
+  w.r = idx / FV;
   w.seg = (int)(w.r % p.S);
   const int bh = (int)(w.r / p.S);
   w.b = bh / p.H;
@@ -393,29 +410,34 @@ __device__ __forceinline__ bool wcumsum_thread(const WcumsumP& p, WcumsumThread&
   return true;
 }
 
+template <int V>
 __global__ __launch_bounds__(256) void wcumsum_summary_kernel(WcumsumP p) {
+  typedef typename WVec<V>::T T;
   WcumsumThread w;
-  if (!wcumsum_thread(p, w)) return;
+  if (!wcumsum_thread<V>(p, w)) return;
   const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
-  float z = 0.0f, P = 1.0f;
+  T z = WVec<V>::zero();
+  float P = 1.0f;
 #pragma unroll 8
   for (int u = u0; u < u1; ++u) {
     const int tp = p.reverse ? p.T - 1 - u : u;
     const float a = wcumsum_step(p, w.db, w.a_static, u);
-    z = (u == u0 ? 0.0f : a * z) + w.xb[(int64_t)tp * p.x.st];
+    z = (u == u0 ? WVec<V>::zero() : a * z) + *(const T*)(w.xb + (int64_t)tp * p.x.st);
     P *= a;
   }
-  p.tot[w.r * p.F + w.f] = z;
+  *(T*)(p.tot + w.r * p.F + w.f) = z;
   if (w.f == 0) p.prod[w.r] = P;
 }
 
+template <int V>
 __global__ __launch_bounds__(256) void wcumsum_main_kernel(WcumsumP p) {
+  typedef typename WVec<V>::T T;
   WcumsumThread w;
-  if (!wcumsum_thread(p, w)) return;
+  if (!wcumsum_thread<V>(p, w)) return;
   const int64_t row0 = (w.r / p.S) * p.S;
-  float z = 0.0f;  // the state entering this segment
-  for (int j = 0; j < w.seg; ++j) z = p.prod[row0 + j] * z + p.tot[(row0 + j) * p.F + w.f];
+  T z = WVec<V>::zero();  // the state entering this segment
+  for (int j = 0; j < w.seg; ++j) z = p.prod[row0 + j] * z + *(const T*)(p.tot + (row0 + j) * p.F + w.f);
   float* ob = (float*)p.out.ptr + (int64_t)w.b * p.out.sb + (int64_t)w.h * p.out.sh + w.f;
   const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
@@ -423,8 +445,8 @@ __global__ __launch_bounds__(256) void wcumsum_main_kernel(WcumsumP p) {
   for (int u = u0; u < u1; ++u) {
     const int tp = p.reverse ? p.T - 1 - u : u;
     const float a = wcumsum_step(p, w.db, w.a_static, u);
-    z = (u == 0 ? 0.0f : a * z) + w.xb[(int64_t)tp * p.x.st];
-    ob[(int64_t)tp * p.out.st] = z;
+    z = (u == 0 ? WVec<V>::zero() : a * z) + *(const T*)(w.xb + (int64_t)tp * p.x.st);
+    *(T*)(ob + (int64_t)tp * p.out.st) = z;
   }
 }
 
@@ -932,13 +954,19 @@ int ts_wcumsum(const ts_wcumsum_desc* d, ts_strided x, ts_strided out, const flo
   p.x = x; p.out = out; p.decay = decay; p.log_alpha = log_alpha;
   p.tot = (float*)workspace;
   p.prod = p.tot + (size_t)d->B * d->H * p.S * d->F;
-  const int64_t n = (int64_t)d->B * d->H * p.S * d->F;
+  // four features per thread when every row start is 16-byte aligned
+  const bool v4 = d->F % 4 == 0 && !((uintptr_t)x.ptr & 15u) && !((uintptr_t)out.ptr & 15u) && x.sb % 4 == 0 &&
+                  x.sh % 4 == 0 && x.st % 4 == 0 && out.sb % 4 == 0 && out.sh % 4 == 0 && out.st % 4 == 0;
+  const int V = v4 ? 4 : 1;
+  const int64_t n = (int64_t)d->B * d->H * p.S * (d->F / V);
   const dim3 grid((unsigned)((n + 255) / 256));
   if (p.S > 1) {
-    hipLaunchKernelGGL(ts::wcumsum_summary_kernel, grid, dim3(256), 0, stream, p);
+    if (v4) hipLaunchKernelGGL(ts::wcumsum_summary_kernel<4>, grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(ts::wcumsum_summary_kernel<1>, grid, dim3(256), 0, stream, p);
     if ((rc = finish("wcumsum summary"))) return rc;
   }
-  hipLaunchKernelGGL(ts::wcumsum_main_kernel, grid, dim3(256), 0, stream, p);
+  if (v4) hipLaunchKernelGGL(ts::wcumsum_main_kernel<4>, grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL(ts::wcumsum_main_kernel<1>, grid, dim3(256), 0, stream, p);
   return finish("wcumsum");
 }
 

@@ -3,7 +3,8 @@
 The key-mass prefixes of the feature-mass read (src/thetascan/_core/ops/
 interface.py:58-107, 216-230): the plain prefix, the static-retention
 ``ema_cumsum`` and the per-token decayed stream, causal and anti-causal, at
-T = 80, 4096 and 32768 (one to thousands of time segments), plus the
+T = 80, 4096 and 32768 (one to thousands of time segments), with rows taken
+four features at a time and, for unaligned rows, one at a time, plus the
 gradients of the prefix input and of the retention through the autograd op.
 fp32 throughout; rel 1e-4 forward, rel 1e-3 for gradients.
 """
@@ -61,6 +62,31 @@ def test_decayed_prefix_matches_oracle(cuda, T, kind, reverse):
     got = fused.wcumsum(x.to(cuda, torch.float32), r_dev, reverse)
     print(f"wcumsum T={T} {kind} reverse={reverse}", flush=True)
     assert got.dtype == torch.float32 and got.shape == expected.shape
+    assert rel_err(got, expected) < 1e-4
+
+
+@pytest.mark.parametrize("layout", ["six_features", "unaligned_view"])
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+def test_decayed_prefix_one_feature_per_thread(cuda, kind, layout):
+    """Rows that are not 16-byte aligned (a feature count that is not a
+    multiple of four, or a view starting one float into its storage) take the
+    one-feature-per-thread kernels; same bar as above."""
+    from thetascan_amd._core.ops import fused
+
+    B, H, T = 2, 3, 4096
+    F = 6 if layout == "six_features" else 40
+    x, ret = _inputs(B, H, T, F, kind, seed=31)
+    expected = _oracle(x, ret, False)
+    r_dev = None if ret is None else ret.to(cuda, torch.float32)
+    if layout == "unaligned_view":
+        wide = torch.zeros(B, H, T, F + 1, device=cuda, dtype=torch.float32)
+        wide[..., 1:] = x.to(cuda, torch.float32)
+        xd = wide[..., 1:]
+        assert xd.data_ptr() % 16 != 0 and xd.stride(-1) == 1
+    else:
+        xd = x.to(cuda, torch.float32)
+    got = fused.wcumsum(xd, r_dev, False)
+    print(f"wcumsum {layout} {kind}", flush=True)
     assert rel_err(got, expected) < 1e-4
 
 

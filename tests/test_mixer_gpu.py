@@ -122,6 +122,38 @@ def test_fused_and_composed_paths_agree(cuda, variant, feature_map):
         assert rel_err(a, b) < 1e-3
 
 
+@pytest.mark.parametrize("case", ["input_full_d128", "feature_full_m128"])
+def test_fused_and_composed_agree_with_full_rotations(cuda, case):
+    """Rotations wider than 64 dims or features: the feature kernels preload
+    the factors of the first four 16-wide blocks and read the tables of the
+    others where they are applied; both parts against the composed path."""
+    if case == "input_full_d128":
+        pub = _headline_config("input", "key_mass", d_model=512, heads=4)  # head width 128, m = 128
+    else:
+        pub = _headline_config("feature", "none", d_model=256, heads=4, mult=2)  # head width 64, m = 128
+    pub["rope"]["fraction"] = 1.0
+    module = build_module(pub, cuda)
+    _seeded(module, 3)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 150, pub["d_model"], generator=g).to(cuda)
+    dy = torch.randn(2, 150, pub["d_model"], generator=g).to(cuda)
+    outs, grads = [], []
+    for force_composed in (False, True):
+        module.zero_grad()
+        xi = x.clone().requires_grad_(True)
+        if force_composed:
+            module._core.fused_eligible = lambda _x: False
+        y = module(xi)
+        print(f"full rotation {case}: path={module._core.last_path}", flush=True)
+        assert module._core.last_path == ("composed" if force_composed else "fused")
+        (y * dy).sum().backward()
+        outs.append(y.detach())
+        grads.append([xi.grad] + [p.grad.clone() for p in module.parameters()])
+    assert rel_err(outs[0], outs[1]) < 1e-4
+    for a, b in zip(grads[0], grads[1]):
+        assert rel_err(a, b) < 1e-3
+
+
 @pytest.mark.parametrize("variant", [("feature", "none"), ("input", "key_mass")])
 def test_headline_bf16_matches_float64_oracle(cuda, variant):
     """The benchmark mixer (kernel, ReLU^2 ridge, m=d=64, H=8, d_model=512) in

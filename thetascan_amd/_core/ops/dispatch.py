@@ -22,7 +22,17 @@ eager mode.  Outputs that receive no gradient arrive as None in both modes.
 """
 from __future__ import annotations
 
+import threading
+
 import torch
+
+_EAGER = threading.local()
+
+
+def eager_forward() -> bool:
+    """True inside a forward that the eager autograd.Function runs (its setup
+    follows on the same thread), False under the custom-op dispatcher."""
+    return getattr(_EAGER, "active", False)
 
 
 def _tensor_slots(args):
@@ -40,7 +50,11 @@ class _Eager(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hip_op, args, *tensors):
         ctx.set_materialize_grads(False)
-        out = hip_op.forward(*args)
+        _EAGER.active = True
+        try:
+            out = hip_op.forward(*args)
+        finally:
+            _EAGER.active = False
         hip_op.setup(ctx, args, out)
         ctx.hip_op = hip_op
         ctx.slots = _tensor_slots(args)

@@ -19,11 +19,12 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 
 import torch
 
 from ... import _lib
-from .dispatch import HipOp
+from .dispatch import HipOp, eager_forward
 from . import scan_hip, stream
 from .linear import slot_sum, split_k_outer, weight_grad
 
@@ -579,6 +580,8 @@ def _kernel_mixer_forward(x: torch.Tensor, w_qkv: torch.Tensor, w_g: torch.Tenso
     out = torch.nn.functional.linear(y, w_out)
     # the stacked [W_qkv; W_g] travels to the backward's input-gradient GEMM
     stacked = weight if w_g is not None else x.new_empty(0)
+    if eager_forward():
+        _HANDOFF.state = (out, st)
     return [out, proj, y] + [x.new_empty(0) if getattr(st, n) is None else getattr(st, n)
                              for n in _State.SAVED] + [stacked]
 
@@ -617,9 +620,13 @@ def _kernel_mixer_backward_impl(dout: torch.Tensor, x: torch.Tensor, w_qkv: torc
                          resid_scale: float, eps: float, normalize: bool, seg_chunks: int, heads: int,
                          need: list[bool]) -> list[torch.Tensor]:
     spec = FeatureSpec(kind, m, gain, in_rot, feat_rot, rope_base, resid_scale, eps)
+    st = _restore(saved[:-1], proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, w_g is not None)
+    return _kernel_mixer_grads(st, dout, x, w_qkv, w_g, w_out, y, saved[-1], need)
+
+
+def _kernel_mixer_grads(st: _State, dout, x, w_qkv, w_g, w_out, y, stacked, need: list[bool]) -> list[torch.Tensor]:
+    """The backward of the kernel-mixer op from its forward's state."""
     has_gate = w_g is not None
-    stacked = saved[-1]
-    st = _restore(saved[:-1], proj, w1, w2, tau, b_g, spec, normalize, seg_chunks, heads, has_gate)
     d2 = dout.reshape(-1, w_out.shape[0])
     dw_out = weight_grad(d2, y.reshape(-1, y.shape[-1]), w_out.dtype) if need[7] else None
     dy = (d2 @ w_out).view(y.shape)
@@ -646,18 +653,32 @@ def _kernel_mixer_backward_fake(dout, x, w_qkv, w_g, b_g, w1, w2, tau, w_out, pr
     return [t.new_empty(t.shape) if (t is not None and w) else x.new_empty(0) for t, w in zip(like, need)]
 
 
+# Eager execution hands the forward's _State to its backward on the autograd
+# context (the forward stores it here, keyed by its output, and the setup right
+# after it on the same thread takes it), so the backward need not rebuild it
+# from the saved tensors.  The compiled path's backward rebuilds it.
+_HANDOFF = threading.local()
+
+
 def _kernel_mixer_setup(ctx, inputs, output):
     x, w_qkv, w_g, b_g, w1, w2, tau, w_out, *args = inputs
     ctx.args = args
     tensors = [x, w_qkv, w_g, b_g, w1, w2, tau, w_out]
     ctx.need = [t is not None and t.requires_grad for t in tensors]
     ctx.save_for_backward(*tensors, *output[1:])
+    handed = getattr(_HANDOFF, "state", None)
+    _HANDOFF.state = None
+    ctx.state = handed[1] if handed is not None and handed[0] is output[0] else None
 
 
 def _kernel_mixer_backward(ctx, grads, bwd):
     x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, *saved = ctx.saved_tensors
-    res = bwd(grads[0], x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, list(saved), *ctx.args,
-                               ctx.need)
+    st = getattr(ctx, "state", None)
+    if st is not None:  # eager: the forward's own state (same launches as the rebuilt one)
+        ctx.state = None
+        res = _kernel_mixer_grads(st, grads[0], x, w_qkv, w_g, w_out, y, saved[-1], ctx.need)
+    else:
+        res = bwd(grads[0], x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, list(saved), *ctx.args, ctx.need)
     return (*[g if w else None for g, w in zip(res, ctx.need)], *([None] * len(ctx.args)))
 
 

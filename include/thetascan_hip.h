@@ -34,7 +34,7 @@ extern "C" {
  *     damping);
  * 11: ts_scan_pair_io carries scan A's key-side ext column (k_ext);
  * 12: ts_retention_grad. */
-#define TS_ABI_VERSION 12
+#define TS_ABI_VERSION 13
 
 enum ts_status {
   TS_OK = 0,
@@ -172,10 +172,13 @@ int ts_scan_fwd_noalloc(const ts_scan_desc* desc, const ts_scan_io* io, hipStrea
  * ts_scan_workspace_bytes(desc), 16-byte aligned. */
 typedef struct ts_scan_pair_io {
   ts_strided qa, k, v, qb;
-  ts_strided out_a;               /* [B,H,T,dv]                                */
-  ts_strided out_b;               /* [B,H,T,dk]                                */
+  ts_strided out_a;               /* [B,H,T,dv] (bf16, or fp32 in the fp32
+                                     output modes, stored or accumulated)     */
+  ts_strided out_b;               /* [B,H,T,dk] (same)                         */
   ts_strided k_ext;               /* fp32 [B,H,T] key-side ext of scan A (desc
                                      q_ext ones, k_ext array), else NULL       */
+  const float* log_alpha;         /* [H] static log-retention of both scans
+                                     (desc retention TS_RET_STATIC), else NULL */
 } ts_scan_pair_io;
 
 int ts_scan_pair_fwd(const ts_scan_desc* desc, const ts_scan_pair_io* io,

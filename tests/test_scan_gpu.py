@@ -613,3 +613,62 @@ def test_pair_scan_with_key_ext_equals_its_two_scans(cuda, T, seg_chunks, revers
     else:
         want = oracle.linattn_chunk(qx, kx, v)
     assert rel_err(a, want) < TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("T,seg_chunks,reverse,kx,static,out_mode", [
+    (700, 0, True, False, True, "store"),
+    (5, 0, False, False, True, "store"),
+    (4096, 3, True, True, True, "accum"),
+    (300, 1, False, True, True, "store_f32"),
+    (1, 0, True, True, True, "accum"),
+    (700, 2, True, False, False, "accum"),
+    (200, 0, False, True, False, "store_f32"),
+])
+def test_pair_scan_retention_and_fp32_outputs_equal_its_two_scans(cuda, T, seg_chunks, reverse, kx, static, out_mode):
+    """With a static per-head retention shared by both scans and fp32
+    outputs (stored, or accumulated with a scale into existing values),
+    ts_scan_pair_fwd gives scan A with the same bits as its ts_scan_fwd call
+    and scan B within bf16 rounding of its own (plain scans: the same bits).
+    The pair keeps one state, sum_i alpha^(t-i) v_i k_i^T, whose decay
+    weights round with v as scan A's own call rounds them; scan B's own call
+    weights (and rounds) k instead.  Retained scans match the float64
+    decayed recurrence."""
+    from thetascan_amd import _lib
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, D = 2, 3, 64
+    g = torch.Generator().manual_seed(131 + T)
+    qa, k, v, qb = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64).to(torch.bfloat16).to(torch.float64)
+                    for _ in range(4))
+    dev = [x.to(cuda, torch.bfloat16) for x in (qa, k, v, qb)]
+    la = torch.log(torch.tensor([0.9, 0.97, 0.995])) if static else None
+    ke = torch.randn(B, H, T, generator=g).to(cuda) if kx else None
+    mode = {"store": _lib.OUT_STORE, "store_f32": _lib.OUT_STORE_F32, "accum": _lib.OUT_ACCUM_F32}[out_mode]
+    scale = 0.75 if mode == _lib.OUT_ACCUM_F32 else 1.0
+    rk = dict(retention=_lib.RET_STATIC, log_alpha=la) if static else {}
+    base_a = torch.randn(B, H, T, D, generator=g).to(cuda)
+    base_b = torch.randn(B, H, T, D, generator=g).to(cuda)
+    pa = pb = ra = rb = None
+    if mode == _lib.OUT_ACCUM_F32:
+        pa, pb, ra, rb = base_a.clone(), base_b.clone(), base_a.clone(), base_b.clone()
+    a, b = scan_hip.scan_pair_launch(*dev, reverse=reverse, seg_chunks=seg_chunks, k_ext=ke, log_alpha=la,
+                                     out_mode=mode, out_scale=scale, out_a=pa, out_b=pb)
+    ref_a, _, _ = scan_hip.scan_launch(dev[0], dev[1], dev[2], **rk, reverse=reverse, seg_chunks=seg_chunks,
+                                       q_ext="ones" if kx else None, k_ext=ke, out=ra, out_mode=mode,
+                                       out_scale=scale)
+    ref_b, _, _ = scan_hip.scan_launch(dev[3], dev[2], dev[1], **rk, reverse=reverse, seg_chunks=seg_chunks,
+                                       out=rb, out_mode=mode, out_scale=scale)
+    assert torch.equal(a, ref_a[..., :D]), (T, seg_chunks, reverse, kx, out_mode)
+    if static:
+        acc = base_b if mode == _lib.OUT_ACCUM_F32 else 0
+        assert rel_err(b - acc, ref_b[..., :D] - acc) < 1e-2
+    else:
+        assert torch.equal(b, ref_b[..., :D]), (T, seg_chunks, reverse, kx, out_mode)
+    if static and not kx and mode != _lib.OUT_ACCUM_F32:
+        idx = torch.arange(T, dtype=torch.float64)
+        dist = (idx[:, None] - idx[None, :]) if not reverse else (idx[None, :] - idx[:, None])
+        w = torch.where(dist >= 0, torch.exp(la.double().view(H, 1, 1) * dist.clamp(min=0)), torch.zeros(()))
+        want_a = torch.einsum("bhts,bhsd->bhtd", torch.einsum("bhtd,bhsd->bhts", qa, k) * w, v)
+        want_b = torch.einsum("bhts,bhsd->bhtd", torch.einsum("bhtd,bhsd->bhts", qb, v) * w, k)
+        assert rel_err(a, want_a) < TOL[torch.bfloat16]
+        assert rel_err(b, want_b) < TOL[torch.bfloat16]

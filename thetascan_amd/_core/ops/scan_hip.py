@@ -317,27 +317,37 @@ def pair_eligible(qa: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qb: torch.
 
 def scan_pair_launch(qa: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qb: torch.Tensor, *, reverse: bool = False,
                      seg_chunks: int = 0, out_a: torch.Tensor | None = None, out_b: torch.Tensor | None = None,
-                     k_ext: torch.Tensor | None = None):
-    """scan(qa, k, v) and scan(qb, v, k) (plain, bf16, 64-wide) in one pass over
-    k and v; returns ``(out_a, out_b)``, each equal to its own scan_launch.
+                     k_ext: torch.Tensor | None = None, log_alpha: torch.Tensor | None = None,
+                     out_mode: int = _lib.OUT_STORE, out_scale: float = 1.0):
+    """scan(qa, k, v) and scan(qb, v, k) (bf16, 64-wide) in one pass over k
+    and v; returns ``(out_a, out_b)``, each equal to its own scan_launch.
     ``k_ext`` (fp32 [B,H,T]) gives scan A the key-side ext pair of a
-    normalized read's backward: scan_launch(qa, k, v, q_ext="ones", k_ext=k_ext)."""
+    normalized read's backward: scan_launch(qa, k, v, q_ext="ones", k_ext=k_ext).
+    ``log_alpha`` ([H]) is a static retention of both scans; ``out_mode``
+    OUT_STORE_F32 / OUT_ACCUM_F32 writes or adds ``out_scale`` x the results
+    into fp32 outputs (both given for accumulation)."""
     lib = _lib.load()
     B, H, T, d = qa.shape
     views = [_kernel_view(t, 64) for t in (qa, k, v, qb)]
+    odt = qa.dtype if out_mode == _lib.OUT_STORE else torch.float32
+    if out_mode == _lib.OUT_ACCUM_F32 and (out_a is None or out_b is None):
+        raise ValueError("scan pair: accumulation needs both outputs")
     if out_a is None:
-        out_a = torch.empty(B, H, T, 64, dtype=qa.dtype, device=qa.device)
+        out_a = torch.empty(B, H, T, 64, dtype=odt, device=qa.device)
     if out_b is None:
-        out_b = torch.empty(B, H, T, 64, dtype=qa.dtype, device=qa.device)
+        out_b = torch.empty(B, H, T, 64, dtype=odt, device=qa.device)
+    if out_a.dtype != odt or out_b.dtype != odt:
+        raise ValueError(f"scan pair: outputs must be {odt} for this output mode")
     ke = None if k_ext is None else k_ext.to(torch.float32).contiguous()
-    desc = _lib.ScanDesc(B, H, T, 64, 64, _lib.dtype_code(qa.dtype), _lib.RET_NONE, int(reverse),
-                         _lib.EXT_ONES if ke is not None else 0, _lib.EXT_ARRAY if ke is not None else 0, 0,
-                         _lib.OUT_STORE, 1.0, int(seg_chunks), 0, 0, 0, 0)
+    la = None if log_alpha is None else log_alpha.detach().to(device=qa.device, dtype=torch.float32).reshape(H).contiguous()
+    desc = _lib.ScanDesc(B, H, T, 64, 64, _lib.dtype_code(qa.dtype), _lib.RET_STATIC if la is not None else _lib.RET_NONE,
+                         int(reverse), _lib.EXT_ONES if ke is not None else 0, _lib.EXT_ARRAY if ke is not None else 0, 0,
+                         out_mode, float(out_scale), int(seg_chunks), 0, 0, 0, 0)
     c_ws = ctypes.c_size_t()
     _lib.check(lib.ts_scan_workspace_bytes(ctypes.byref(desc), ctypes.byref(c_ws)), "scan workspace")
     workspace = torch.empty(c_ws.value, dtype=torch.uint8, device=qa.device) if c_ws.value else None
     io = _lib.ScanPairIO(*[_lib.strided(t) for t in views], _lib.strided(out_a), _lib.strided(out_b),
-                         _lib.strided(ke))
+                         _lib.strided(ke), la.data_ptr() if la is not None else None)
     with _lib.timed("ts_scan_pair_fwd", lambda: _lib.nbytes(*views, out_a, out_b, ke)):
         status = lib.ts_scan_pair_fwd(ctypes.byref(desc), ctypes.byref(io),
                                       workspace.data_ptr() if workspace is not None else None, c_ws.value,
@@ -629,6 +639,11 @@ def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: b
             if need_q:
                 scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
                             out=dq, out_mode=_lib.OUT_ACCUM_F32)
+            if need_k and need_v and kind in (_lib.RET_NONE, _lib.RET_STATIC) and pair_eligible(v, dO, q, k):
+                # dk and dv share keys dO and values q: one pass over both
+                scan_pair_launch(v, dO, q, k, reverse=True, k_ext=q_ext, out_a=dkk, out_b=dvv,
+                                 log_alpha=r if kind == _lib.RET_STATIC else None, out_mode=_lib.OUT_ACCUM_F32)
+                continue
             if need_k:
                 scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
                             k_ext=q_ext, out=dkk, out_mode=_lib.OUT_ACCUM_F32)

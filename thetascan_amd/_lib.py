@@ -72,7 +72,8 @@ class ScanDesc(ctypes.Structure):
 
 
 class ScanPairIO(ctypes.Structure):
-    _fields_ = [(n, Strided) for n in ("qa", "k", "v", "qb", "out_a", "out_b", "k_ext")]
+    _fields_ = [(n, Strided) for n in ("qa", "k", "v", "qb", "out_a", "out_b", "k_ext")] + [
+        ("log_alpha", ctypes.c_void_p)]
 
 
 MAX_VIEWS = 3
@@ -500,7 +501,7 @@ def load() -> ctypes.CDLL:
         lib.ts_retention_workspace_bytes.argtypes = [P(RetentionDesc), P(ctypes.c_size_t)]
         lib.ts_retention_grad.argtypes = [P(RetentionDesc), P(RetentionIO), ctypes.c_void_p, ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 12:
+        if lib.ts_abi_version() != 13:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

@@ -596,19 +596,24 @@ __global__ __launch_bounds__(256) void scan_kernel(ScanP p) {
 // phi(k)).  K and V tiles are read once, S is updated once per tile, both
 // score blocks stay in accumulators, and scan B reads the published state
 // copy transposed (ds_read_b64_tr_b16) instead of carrying S^T.  Each output
-// is computed in the order its own one-scan kernel uses.  Plain retention,
-// bf16, dk = dv = DK; segment states come from scan A's summary and prefix
-// passes.  With KX, scan A carries the key-side ext pair of a normalized
-// read's backward (q_ext = ones, k_ext = dmass): score_a += ke_t and its
-// state gains the row u = sum_t ke_t v_t; scan B is unchanged.
+// is computed in the order its own one-scan kernel uses.  bf16, dk = dv = DK;
+// segment states come from scan A's summary and prefix passes.  With KX, scan
+// A carries the key-side ext pair of a normalized read's backward (q_ext =
+// ones, k_ext = dmass): score_a += ke_t and its state gains the row u =
+// sum_t ke_t v_t; scan B is unchanged.  MODE may add kStatic (one static
+// per-head retention for both scans: the same causal weights alpha^(t-i)) and
+// kF32Out (fp32 outputs, stored or accumulated with out_scale, as the one-view
+// kernel's fp32 output modes).
 struct PairP {
   ScanP s;           // q = qa, k, v, out = out_a (and the segmentation)
   ts_strided qb, ob;
   uint32_t qb_rec, ob_rec;
 };
 
-template <int DK, bool KX>
+template <int DK, bool KX, int MODE>
 __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
+  constexpr bool STATIC = (MODE & kStatic) != 0;
+  constexpr bool F32OUT = (MODE & kF32Out) != 0;
   typedef bf16 E;
   typedef bf16x8 F8;
   typedef LdsIO<E> IO;
@@ -639,6 +644,12 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
   E* st_base = ebase + L.stages * L.stage;
   float* s_ext = (float*)smem + L.fbase;          // [stage][ke C | (unused) C]
   float* s_u = s_ext + L.stages * 2 * C;          // [2][DK]
+  float* s_pw = s_u + 2 * DK + 2 * DK;            // alpha^d, d = 0..64 (static)
+  if (STATIC && w == 0) {
+    const float la = p.log_alpha[h];
+    s_pw[lane] = expf(la * (float)lane);
+    if (lane == 0) s_pw[64] = expf(la * 64.0f);
+  }
 
   const int64_t bh_q = (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
   const int64_t bh_b = (int64_t)b * pp.qb.sb + (int64_t)h * pp.qb.sh;
@@ -715,10 +726,12 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
     }
   };
 
-  const void* oa_base = bh_base(p.out, b, h, ES);
-  const void* ob_base = bh_base(pp.ob, b, h, ES);
-  const int oa_st_b = (int)p.out.st * ES;
-  const int ob_st_b = (int)pp.ob.st * ES;
+  constexpr int OSZ = F32OUT ? 4 : ES;
+  const int out_mode = F32OUT ? p.out_mode : TS_OUT_STORE;
+  const void* oa_base = bh_base(p.out, b, h, OSZ);
+  const void* ob_base = bh_base(pp.ob, b, h, OSZ);
+  const int oa_st_b = (int)p.out.st * OSZ;
+  const int ob_st_b = (int)pp.ob.st * OSZ;
 
   fetch(c_begin * C);
   store(c_begin & 1);
@@ -738,6 +751,8 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
     const float* u_in = s_u + (c & 1) * DK;
     const int query = w * 16 + l16;
     const float qe = t0 + query < p.T ? 1.0f : 0.0f;  // the ones column of scan A's queries
+    const int len = min(C, p.T - t0);
+    const float cw = STATIC ? s_pw[query + 1] : 1.0f;
 
     // causal score blocks of this wave's queries against keys k (A) and v (B)
     floatx4 sa[4], sb[4];
@@ -759,8 +774,14 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
         const bool keep = kb < w || key <= query;
         float sv = sa[kb][i];
         if (KX) sv += qe * kev[i];
-        sa[kb][i] = keep ? sv : 0.0f;
-        sb[kb][i] = keep ? sb[kb][i] : 0.0f;
+        if (STATIC) {
+          const float wt = s_pw[max(query - key, 0)];
+          sa[kb][i] = keep ? sv * wt : 0.0f;
+          sb[kb][i] = keep ? sb[kb][i] * wt : 0.0f;
+        } else {
+          sa[kb][i] = keep ? sv : 0.0f;
+          sb[kb][i] = keep ? sb[kb][i] : 0.0f;
+        }
       }
     }
     const F8 pa0 = IO::from_acc(sa[0], sa[1]), pa1 = IO::from_acc(sa[2], sa[3]);
@@ -782,6 +803,10 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += qe * u4[i];
         }
+        if (STATIC) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] *= cw;
+        }
       }
       acc = mma32(TK::col8(Vs, L.vp, vb * 16, 0, lane), pa0, acc);
       if (w >= 2) acc = mma32(TK::col8(Vs, L.vp, vb * 16, 1, lane), pa1, acc);
@@ -790,25 +815,70 @@ __global__ __launch_bounds__(256) void pair_kernel(PairP pp) {
       if (!state_zero) {
 #pragma unroll
         for (int j = 0; j < NK32; ++j) accb = mma32(TK::col8(st, L.kp, vb * 16, j, lane), qb[j], accb);
+        if (STATIC) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) accb[i] *= cw;
+        }
       }
       accb = mma32(TK::col8(Ks, L.kp, vb * 16, 0, lane), pb0, accb);
       if (w >= 2) accb = mma32(TK::col8(Ks, L.kp, vb * 16, 1, lane), pb1, accb);
       const int ocol = vb * 16 + 4 * g;
-      bf16x4 oa, ob;
+      const uint32_t offa = ocol < p.dv ? roa + (uint32_t)(ocol * OSZ) : kOOB;
+      const uint32_t offb = ocol < p.dk ? rob + (uint32_t)(ocol * OSZ) : kOOB;
+      if (out_mode == TS_OUT_STORE) {
+        bf16x4 oa, ob;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        oa[i] = (bf16)acc[i];
-        ob[i] = (bf16)accb[i];
+        for (int i = 0; i < 4; ++i) {
+          oa[i] = (bf16)acc[i];
+          ob[i] = (bf16)accb[i];
+        }
+        bst8(oa_rs, offa, __builtin_bit_cast(uint2, oa));
+        bst8(ob_rs, offb, __builtin_bit_cast(uint2, ob));
+      } else {
+        floatx4 oa, ob;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          oa[i] = p.out_scale * acc[i];
+          ob[i] = p.out_scale * accb[i];
+        }
+        if (out_mode == TS_OUT_ACCUM_F32) {
+          const floatx4 pa = __builtin_bit_cast(floatx4, bld16(oa_rs, offa));
+          const floatx4 pb = __builtin_bit_cast(floatx4, bld16(ob_rs, offb));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            oa[i] += pa[i];
+            ob[i] += pb[i];
+          }
+        }
+        bst16(oa_rs, offa, __builtin_bit_cast(uint4, oa));
+        bst16(ob_rs, offb, __builtin_bit_cast(uint4, ob));
       }
-      bst8(oa_rs, ocol < p.dv ? roa + (uint32_t)(ocol * ES) : kOOB, __builtin_bit_cast(uint2, oa));
-      bst8(ob_rs, ocol < p.dk ? rob + (uint32_t)(ocol * ES) : kOOB, __builtin_bit_cast(uint2, ob));
     }
     if (c + 1 < c_end) qload(t0 + C);
 
-    // S += K^T V (value block w), once for both scans
+    // S = decay(tile) S + K^T diag(wk) V (value block w), once for both scans
     F8 av[2];
 #pragma unroll
     for (int kp = 0; kp < 2; ++kp) av[kp] = TK::col8(Vs, L.vp, w * 16, kp, lane);
+    if (STATIC) {
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = 32 * kp + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+          const float wk = key < len ? s_pw[len - 1 - key] : 0.0f;
+          av[kp][e] = cvt<E>(tof(av[kp][e]) * wk);
+        }
+      if (!state_zero) {
+        const float cdec = s_pw[len];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S[kb][i] *= cdec;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) us[i] *= cdec;
+      }
+    }
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -1167,17 +1237,22 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   const bool kx = L.kx;
   if (kx && (d->q_ext != TS_EXT_ONES || d->k_ext != TS_EXT_ARRAY))
     return fail(TS_ERR_NOT_IMPLEMENTED, "scan pair: the key-side ext pair must be q_ext ones, k_ext array");
-  if (d->dtype != TS_BF16 || d->retention != TS_RET_NONE || L.vx || d->out_mode != TS_OUT_STORE ||
+  if (d->dtype != TS_BF16 || (d->retention != TS_RET_NONE && d->retention != TS_RET_STATIC) || L.vx ||
       d->dk != 64 || d->dv != 64 || L.nvs != 1 || d->states_in || d->want_final || d->init_state)
-    return fail(TS_ERR_NOT_IMPLEMENTED, "scan pair: bf16 plain scans of 64-wide keys and values only");
+    return fail(TS_ERR_NOT_IMPLEMENTED,
+                "scan pair: bf16 scans of 64-wide keys and values with no or a static retention only");
   if (kx && !io->k_ext.ptr) return fail(TS_ERR_VALUE, "scan pair: missing k ext column");
+  const bool stat = d->retention == TS_RET_STATIC;
+  if (stat && !io->log_alpha) return fail(TS_ERR_VALUE, "scan pair: missing log_alpha");
+  const bool f32 = d->out_mode != TS_OUT_STORE;
   if (d->T == 0) return TS_OK;
   int rc2;
   if ((rc2 = check_stream("qa", io->qa, 8, true)) || (rc2 = check_stream("k", io->k, 8, true)) ||
       (rc2 = check_stream("v", io->v, 8, true)) || (rc2 = check_stream("qb", io->qb, 8, true)))
     return rc2;
   for (const ts_strided* o : {&io->out_a, &io->out_b})
-    if (!o->ptr || ((uintptr_t)o->ptr & 7u) || o->st % 8 || o->sh % 8 || o->sb % 8)
+    if (!o->ptr || ((uintptr_t)o->ptr & (f32 ? 15u : 7u)) || o->st % (f32 ? 4 : 8) || o->sh % (f32 ? 4 : 8) ||
+        o->sb % (f32 ? 4 : 8))
       return fail(TS_ERR_VALUE, "scan pair: outputs must be 16-byte aligned rows");
   if (L.ws_bytes > 0 && (!workspace || ws_bytes < L.ws_bytes))
     return fail(TS_ERR_VALUE, "scan pair: workspace too small (%zu < %zu bytes)", ws_bytes, L.ws_bytes);
@@ -1188,10 +1263,11 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   ts::ScanP& p = pp.s;
   p.B = d->B; p.H = d->H; p.T = d->T; p.dk = d->dk; p.dv = d->dv; p.dvp = L.dvp; p.vs = L.vs;
   p.nchunks = L.nchunks; p.seg_chunks = L.seg_chunks; p.nseg = L.nseg; p.nsum = L.nsum; p.nelem = L.nelem;
-  p.ret = TS_RET_NONE; p.reverse = d->reverse;
+  p.ret = stat ? TS_RET_STATIC : TS_RET_NONE; p.reverse = d->reverse;
+  p.log_alpha = io->log_alpha;
   p.q_ext = p.k_ext = p.v_ext = TS_EXT_NONE;
   if (kx) { p.q_ext = TS_EXT_ONES; p.k_ext = TS_EXT_ARRAY; p.ke = io->k_ext; }
-  p.out_mode = TS_OUT_STORE; p.out_scale = 1.0f;
+  p.out_mode = d->out_mode; p.out_scale = f32 ? d->out_scale : 1.0f;
   p.q = io->qa; p.k = io->k; p.v = io->v; p.out = io->out_a;
   pp.qb = io->qb; pp.ob = io->out_b;
   if (kx && (rc = slice_bytes("k_ext", p.ke, d->T, 1, 4, &p.ke_rec))) return rc;
@@ -1199,8 +1275,8 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   if ((rc = slice_bytes("k", p.k, d->T, d->dk, 2, &p.k_rec))) return rc;
   if ((rc = slice_bytes("v", p.v, d->T, d->dv, 2, &p.v_rec))) return rc;
   if ((rc = slice_bytes("qb", pp.qb, d->T, d->dv, 2, &pp.qb_rec))) return rc;
-  if ((rc = slice_bytes("out_a", p.out, d->T, d->dv, 2, &p.out_rec))) return rc;
-  if ((rc = slice_bytes("out_b", pp.ob, d->T, d->dk, 2, &pp.ob_rec))) return rc;
+  if ((rc = slice_bytes("out_a", p.out, d->T, d->dv, f32 ? 4 : 2, &p.out_rec))) return rc;
+  if ((rc = slice_bytes("out_b", pp.ob, d->T, d->dk, f32 ? 4 : 2, &pp.ob_rec))) return rc;
   if (L.ws_bytes > 0) {
     p.seg = (float*)workspace;
     p.segdec = p.seg + (size_t)d->B * d->H * L.nseg * (size_t)L.nelem;
@@ -1209,7 +1285,11 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
   const ts::ScanLayout SL = ts::scan_layout(2, 64, 64, true);
   if (SL.nst != 2) return fail(TS_ERR_RUNTIME, "scan pair: unexpected state buffering");
   if (L.nsum > 0) {
-    KernelFn fsum = pick_kernel(true, 64, 1, false, kx ? ts::kKeyExt : ts::kPlain);
+    // The summary pass writes no outputs, so kF32Out only picks an
+    // instantiation that exists for a static key-ext scan.
+    const int smode = stat ? (kx ? ts::kStatic | ts::kKeyExt | ts::kF32Out : ts::kStatic)
+                           : (kx ? ts::kKeyExt : ts::kPlain);
+    KernelFn fsum = pick_kernel(true, 64, 1, false, smode);
     if ((rc = launch(fsum, dim3(L.nsum, bh, 1), (size_t)ts::scan_layout(2, 64, 64, false).bytes, stream, p))) return rc;
     ts::FinalP F{nullptr, nullptr, L.dkp, L.dvp, d->dk, d->dv, 0, 0};
     hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem / 4 + 255) / 256, bh), dim3(256), 0, stream, p.seg,
@@ -1217,8 +1297,19 @@ int ts_scan_pair_fwd(const ts_scan_desc* d, const ts_scan_pair_io* io, void* wor
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: prefix launch failed: %s", hipGetErrorString(e));
   }
-  if (kx) hipLaunchKernelGGL((ts::pair_kernel<64, true>), dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
-  else hipLaunchKernelGGL((ts::pair_kernel<64, false>), dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
+  typedef void (*PairFn)(ts::PairP);
+  const int pm = (stat ? ts::kStatic : 0) | (f32 ? ts::kF32Out : 0);
+  PairFn fn = nullptr;
+  switch (pm) {
+#define TS_PAIR(M) \
+  case M: fn = kx ? (PairFn)ts::pair_kernel<64, true, M> : (PairFn)ts::pair_kernel<64, false, M>; break;
+    TS_PAIR(ts::kPlain)
+    TS_PAIR(ts::kStatic)
+    TS_PAIR(ts::kF32Out)
+    TS_PAIR(ts::kStatic | ts::kF32Out)
+#undef TS_PAIR
+  }
+  hipLaunchKernelGGL(fn, dim3(L.nseg, bh), dim3(256), (size_t)SL.bytes, stream, pp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan pair: launch failed: %s", hipGetErrorString(e));
   return TS_OK;

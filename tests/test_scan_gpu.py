@@ -672,3 +672,52 @@ def test_pair_scan_retention_and_fp32_outputs_equal_its_two_scans(cuda, T, seg_c
         want_b = torch.einsum("bhts,bhsd->bhtd", torch.einsum("bhtd,bhsd->bhts", qb, v) * w, k)
         assert rel_err(a, want_a) < TOL[torch.bfloat16]
         assert rel_err(b, want_b) < TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("Dk,with_mass,used", [(64, True, (1, 2)), (64, False, (0, 1, 2)), (192, True, (0, 2)),
+                                               (64, True, (2,))])
+def test_bank_view_gradients_match_float64_autograd(cuda, Dk, with_mass, used):
+    """q, k, v and retention gradients of a bank's views (plain and two static
+    retentions), some views left out of the loss: the first scan into each
+    fp32 gradient stores, later ones accumulate (64-wide: the paired dk/dv
+    scan; 192-wide keys: key chunks), and a view with no upstream gradient
+    adds nothing."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T, Dv = 2, 2, 330, 64
+    q, k, v = (_rounded(x, torch.bfloat16) for x in _streams(B, H, T, Dk, Dv, seed=61))
+    rets = (None, torch.log(torch.tensor([0.9, 0.95], dtype=torch.float64)),
+            torch.log(torch.tensor([0.99, 0.97], dtype=torch.float64)))
+    g = torch.Generator().manual_seed(9)
+    dOs = [_rounded(torch.randn(B, H, T, Dv, generator=g, dtype=torch.float64), torch.bfloat16) for _ in rets]
+    dms = [torch.randn(B, H, T, generator=g, dtype=torch.float64) * 0.1 for _ in rets]
+
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    r_ref = [None if r is None else r.clone().requires_grad_(True) for r in rets]
+    loss = 0
+    for j in used:
+        unit = torch.cat([leaves[2], torch.ones_like(v[..., :1])], dim=-1) if with_mass else leaves[2]
+        full = oracle.linattn_quad(leaves[0], leaves[1], unit, _oracle_decay(r_ref[j], q))
+        loss = loss + (full[..., :Dv] * dOs[j]).sum() + ((full[..., -1] * dms[j]).sum() if with_mass else 0)
+    loss.backward()
+
+    dev = [t.to(cuda, torch.bfloat16).requires_grad_(True) for t in (q, k, v)]
+    r_dev = [None if r is None else r.to(cuda, torch.float32).requires_grad_(True) for r in rets]
+    if with_mass:
+        outs = scan_hip.linattn_views_mass(*dev, tuple(r_dev))
+    else:
+        outs = [(o, None) for o in scan_hip.linattn_views(*dev, tuple(r_dev))]
+    loss_dev = 0
+    for j in used:
+        num, mass = outs[j]
+        loss_dev = loss_dev + (num.float() * dOs[j].to(cuda, torch.float32)).sum()
+        if with_mass:
+            loss_dev = loss_dev + (mass * dms[j].to(cuda, torch.float32)).sum()
+    loss_dev.backward()
+    for a, e, name in zip(dev, leaves, "qkv"):
+        assert rel_err(a.grad, e.grad) < 2 * TOL[torch.bfloat16], name
+    for j in (1, 2):
+        if j in used:
+            assert rel_err(r_dev[j].grad, r_ref[j].grad) < 5e-2, j
+        else:
+            assert r_dev[j].grad is None or not r_dev[j].grad.any(), j

@@ -166,7 +166,9 @@ def scan_launch(
     if out_mode == _lib.OUT_ACCUM_F32:
         return out, ext_out, None
     if out_mode == _lib.OUT_STORE_F32:
-        result = acc if out is None else out.copy_(acc)
+        result = acc if out is None else out
+        if out is not None:
+            out[..., : acc.shape[-1]].copy_(acc)
     else:
         result = acc.to(q.dtype) if out is None else out.copy_(acc)
     return result, eacc, None
@@ -594,9 +596,18 @@ def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: b
         if need_v:
             gv = scan_launch(k, q, dO, **rk, reverse=True)[0][..., :dv]
         return gq, gk, gv, [None]
-    dq = torch.zeros(B, H, T, -(-dk // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
-    dkk = torch.zeros_like(dq)
-    dvv = torch.zeros(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+    # the first scan into each fp32 gradient stores, later ones accumulate;
+    # a gradient no scan wrote is zeroed at the end
+    dq = torch.empty(B, H, T, -(-dk // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+    dkk = torch.empty_like(dq)
+    dvv = torch.empty(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32, device=q.device)
+    written = {"q": False, "k": False, "v": False}
+
+    def mode(name):
+        m = _lib.OUT_ACCUM_F32 if written[name] else _lib.OUT_STORE_F32
+        written[name] = True
+        return m
+
     r_grads = []
     for j in range(n):
         kind, r = kinds[j], retentions[j]
@@ -632,23 +643,33 @@ def _views_backward(q, k, v, retentions, d_outs, d_mass, need_q: bool, need_k: b
                                      k_ext=q_ext, out_mode=_lib.OUT_STORE_F32)
             dL = (qs * dq_j[..., :dk]).sum(-1) - (ks * dk_j[..., :dk]).sum(-1)
             r_grads.append(_retention_grad(kind, r, dL))
-            dq[..., : dq_j.shape[-1]] += dq_j
-            dkk[..., : dk_j.shape[-1]] += dk_j
+            for name, buf, part in (("q", dq, dq_j), ("k", dkk, dk_j)):
+                if written[name]:
+                    buf[..., : part.shape[-1]] += part
+                else:
+                    buf.zero_()[..., : part.shape[-1]] = part
+                    written[name] = True
         else:
             r_grads.append(retention_grad(q, k, v, dO, dm, r).sum(0).to(r.dtype).view_as(r) if pairwise else None)
             if need_q:
                 scan_launch(dO, v, k, **rk, q_ext=q_ext, k_ext="ones" if mass_ext else None,
-                            out=dq, out_mode=_lib.OUT_ACCUM_F32)
-            if need_k and need_v and kind in (_lib.RET_NONE, _lib.RET_STATIC) and pair_eligible(v, dO, q, k):
+                            out=dq, out_mode=mode("q"))
+            if need_k and need_v and kind in (_lib.RET_NONE, _lib.RET_STATIC) and pair_eligible(v, dO, q, k) \
+                    and written["k"] == written["v"]:
                 # dk and dv share keys dO and values q: one pass over both
+                m = mode("k")
+                mode("v")
                 scan_pair_launch(v, dO, q, k, reverse=True, k_ext=q_ext, out_a=dkk, out_b=dvv,
-                                 log_alpha=r if kind == _lib.RET_STATIC else None, out_mode=_lib.OUT_ACCUM_F32)
+                                 log_alpha=r if kind == _lib.RET_STATIC else None, out_mode=m)
                 continue
             if need_k:
                 scan_launch(v, dO, q, **rk, reverse=True, q_ext="ones" if mass_ext else None,
-                            k_ext=q_ext, out=dkk, out_mode=_lib.OUT_ACCUM_F32)
+                            k_ext=q_ext, out=dkk, out_mode=mode("k"))
         if need_v:
-            scan_launch(k, q, dO, **rk, reverse=True, out=dvv, out_mode=_lib.OUT_ACCUM_F32)
+            scan_launch(k, q, dO, **rk, reverse=True, out=dvv, out_mode=mode("v"))
+    for name, buf in (("q", dq), ("k", dkk), ("v", dvv)):
+        if not written[name]:
+            buf.zero_()
     gq = dq[..., :dk].to(q.dtype) if need_q else None
     gk = dkk[..., :dk].to(k.dtype) if need_k else None
     gv = dvv[..., :dv].to(v.dtype) if need_v else None

@@ -148,29 +148,24 @@ def scan_launch(
                 ext_res = e
         result = out if out is not None else torch.cat(pieces, dim=-1)
         return result, ext_res, None
-    # dk > MAX_WIDTH: accumulate fp32 partial scans over key chunks
-    acc = None if out_mode == _lib.OUT_ACCUM_F32 else torch.zeros(B, H, T, dv, dtype=torch.float32,
-                                                                  device=q.device)
-    target = out if out_mode == _lib.OUT_ACCUM_F32 else acc
-    eacc = None
-    if want_ext_out:
-        eacc = ext_out if out_mode == _lib.OUT_ACCUM_F32 else torch.zeros(B, H, T, dtype=torch.float32,
-                                                                           device=q.device)
+    # dk > MAX_WIDTH: fp32 partial scans over key chunks, the first stored
+    # (or accumulated, for an accumulating call), the others accumulated
+    target, eacc = (None, None) if out_mode == _lib.OUT_STORE else (out, ext_out)
+    if target is None:
+        target = torch.empty(B, H, T, -(-dv // _vec(q.dtype)) * _vec(q.dtype), dtype=torch.float32,
+                             device=q.device)
     scale = out_scale if out_mode != _lib.OUT_STORE else 1.0
+    first_mode = _lib.OUT_ACCUM_F32 if out_mode == _lib.OUT_ACCUM_F32 else _lib.OUT_STORE_F32
     for i, c0 in enumerate(range(0, dk, MAX_WIDTH)):
         first = i == 0
-        _scan_once(q[..., c0:c0 + MAX_WIDTH], k[..., c0:c0 + MAX_WIDTH], v,
-                   q_ext=q_ext if first else None, k_ext=k_ext if first else None, v_ext=v_ext,
-                   out=target, out_mode=_lib.OUT_ACCUM_F32, out_scale=scale,
-                   want_ext_out=want_ext_out, ext_out=eacc, **kw)
-    if out_mode == _lib.OUT_ACCUM_F32:
-        return out, ext_out, None
-    if out_mode == _lib.OUT_STORE_F32:
-        result = acc if out is None else out
-        if out is not None:
-            out[..., : acc.shape[-1]].copy_(acc)
-    else:
-        result = acc.to(q.dtype) if out is None else out.copy_(acc)
+        target, e, _ = _scan_once(q[..., c0:c0 + MAX_WIDTH], k[..., c0:c0 + MAX_WIDTH], v,
+                                  q_ext=q_ext if first else None, k_ext=k_ext if first else None, v_ext=v_ext,
+                                  out=target, out_mode=first_mode if first else _lib.OUT_ACCUM_F32,
+                                  out_scale=scale, want_ext_out=want_ext_out, ext_out=eacc, **kw)
+        eacc = e if want_ext_out else None
+    if out_mode != _lib.OUT_STORE:
+        return (target if out is not None else target[..., :dv]), eacc, None
+    result = target[..., :dv].to(q.dtype) if out is None else out.copy_(target[..., : out.shape[-1]])
     return result, eacc, None
 
 

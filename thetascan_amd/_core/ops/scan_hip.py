@@ -136,18 +136,26 @@ def scan_launch(
               value_split=value_split)
     B, H, T = q.shape[:3]
     if dv > MAX_WIDTH:
-        pieces, ext_res = [], ext_out
+        ext_res = ext_out
+        full = out
+        if full is None:
+            if out_mode == _lib.OUT_ACCUM_F32:
+                raise ValueError("accumulating scan needs an output tensor")
+            # every value chunk writes its columns of one buffer (the last
+            # chunk's padded to the kernel's vector width)
+            vec = _vec(q.dtype)
+            odt = q.dtype if out_mode == _lib.OUT_STORE else torch.float32
+            full = torch.empty(B, H, T, -(-dv // vec) * vec, dtype=odt, device=q.device)
         for i, c0 in enumerate(range(0, dv, MAX_WIDTH)):
             vs = v[..., c0:c0 + MAX_WIDTH]
-            o_i = None if out is None else out[..., c0:c0 + vs.shape[-1]]
-            r, e, _ = scan_launch(q, k, vs, q_ext=q_ext, k_ext=k_ext, v_ext=v_ext if i == 0 else None,
+            o_i = full[..., c0:c0 + vs.shape[-1]] if out is not None else \
+                full[..., c0:c0 + -(-vs.shape[-1] // _vec(q.dtype)) * _vec(q.dtype)]
+            _, e, _ = scan_launch(q, k, vs, q_ext=q_ext, k_ext=k_ext, v_ext=v_ext if i == 0 else None,
                                   out=o_i, out_mode=out_mode, out_scale=out_scale,
                                   want_ext_out=want_ext_out and i == 0, ext_out=ext_out if i == 0 else None, **kw)
-            pieces.append(r)
             if i == 0:
                 ext_res = e
-        result = out if out is not None else torch.cat(pieces, dim=-1)
-        return result, ext_res, None
+        return (out if out is not None else full[..., :dv]), ext_res, None
     # dk > MAX_WIDTH: fp32 partial scans over key chunks, the first stored
     # (or accumulated, for an accumulating call), the others accumulated
     target, eacc = (None, None) if out_mode == _lib.OUT_STORE else (out, ext_out)

@@ -721,3 +721,40 @@ def test_bank_view_gradients_match_float64_autograd(cuda, Dk, with_mass, used):
             assert rel_err(r_dev[j].grad, r_ref[j].grad) < 5e-2, j
         else:
             assert r_dev[j].grad is None or not r_dev[j].grad.any(), j
+
+
+@pytest.mark.parametrize("out_mode", ["store", "store_f32", "accum"])
+@pytest.mark.parametrize("Dk,Dv", [(192, 64), (64, 200), (300, 136)])
+def test_wide_scans_in_every_output_mode(cuda, Dk, Dv, out_mode):
+    """Keys wider than one launch (fp32 partial scans over key chunks, the
+    first stored) and values wider than one launch (value chunks written into
+    one output, the last padded to the vector width), in the bf16 store, fp32
+    store and fp32 accumulate modes, against the float64 recurrence, with a
+    static retention and the key-mass column."""
+    from thetascan_amd import _lib
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H, T = 1, 2, 333
+    q, k, v = (_rounded(x, torch.bfloat16) for x in _streams(B, H, T, Dk, Dv, seed=83))
+    q, k = q.abs() / Dk ** 0.5, k.abs()
+    la = torch.log(torch.tensor([0.9, 0.99], dtype=torch.float64))
+    qd, kd, vd = (x.to(cuda, torch.bfloat16) for x in (q, k, v))
+    mode = {"store": _lib.OUT_STORE, "store_f32": _lib.OUT_STORE_F32, "accum": _lib.OUT_ACCUM_F32}[out_mode]
+    vec = 8
+    width = -(-Dv // vec) * vec
+    base = torch.randn(B, H, T, width, generator=torch.Generator().manual_seed(3)).to(cuda)
+    base_m = torch.randn(B, H, T, generator=torch.Generator().manual_seed(4)).to(cuda)
+    out = base.clone() if mode == _lib.OUT_ACCUM_F32 else None
+    ext = base_m.clone() if mode == _lib.OUT_ACCUM_F32 else None
+    scale = 0.5 if mode != _lib.OUT_STORE else 1.0
+    res, mass, _ = scan_hip.scan_launch(qd, kd, vd, retention=_lib.RET_STATIC, log_alpha=la.to(cuda, torch.float32),
+                                        v_ext="ones", want_ext_out=True, out=out, ext_out=ext, out_mode=mode,
+                                        out_scale=scale)
+    unit = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1)
+    want = oracle.linattn_naive(q, k, unit, _oracle_decay(la, q)) * scale
+    got, got_m = res[..., :Dv].double().cpu(), mass.double().cpu()
+    if mode == _lib.OUT_ACCUM_F32:
+        got, got_m = got - base[..., :Dv].double().cpu(), got_m - base_m.double().cpu()
+    assert res.dtype == (torch.bfloat16 if mode == _lib.OUT_STORE else torch.float32)
+    assert rel_err(got, want[..., :Dv]) < TOL[torch.bfloat16], (Dk, Dv, out_mode)
+    assert rel_err(got_m, want[..., Dv]) < TOL[torch.bfloat16], (Dk, Dv, out_mode)

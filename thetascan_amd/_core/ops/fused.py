@@ -624,8 +624,12 @@ def _kernel_mixer_backward_impl(dout: torch.Tensor, x: torch.Tensor, w_qkv: torc
     return _kernel_mixer_grads(st, dout, x, w_qkv, w_g, w_out, y, saved[-1], need)
 
 
-def _kernel_mixer_grads(st: _State, dout, x, w_qkv, w_g, w_out, y, stacked, need: list[bool]) -> list[torch.Tensor]:
-    """The backward of the kernel-mixer op from its forward's state."""
+def _kernel_mixer_grads(st: _State, dout, x, w_qkv, w_g, w_out, y, stacked, need: list[bool],
+                        own_storage: bool = True) -> list[torch.Tensor]:
+    """The backward of the kernel-mixer op from its forward's state.  With
+    ``own_storage`` False (an autograd function's backward) the W_qkv and W_g
+    gradients are two views of one stacked gradient; a custom op's outputs
+    must not share storage, so it gets a copy of the W_g rows."""
     has_gate = w_g is not None
     d2 = dout.reshape(-1, w_out.shape[0])
     dw_out = weight_grad(d2, y.reshape(-1, y.shape[-1]), w_out.dtype) if need[7] else None
@@ -641,8 +645,7 @@ def _kernel_mixer_grads(st: _State, dout, x, w_qkv, w_g, w_out, y, stacked, need
         dw = weight_grad(dp2, x.reshape(-1, x.shape[-1]), w_qkv.dtype if same else torch.float32)
         dw_qkv = dw[:w_qkv.shape[0]].to(w_qkv.dtype)
         if has_gate:
-            # its own storage: an op's outputs may not share one
-            dw_g = dw[w_qkv.shape[0]:].to(w_g.dtype, copy=True)
+            dw_g = dw[w_qkv.shape[0]:].to(w_g.dtype, copy=own_storage)
     grads = [dx, dw_qkv, dw_g, db_g, dw1, dw2, dtau, dw_out]
     return [x.new_empty(0) if g is None else g for g in grads]
 
@@ -676,7 +679,7 @@ def _kernel_mixer_backward(ctx, grads, bwd):
     st = getattr(ctx, "state", None)
     if st is not None:  # eager: the forward's own state (same launches as the rebuilt one)
         ctx.state = None
-        res = _kernel_mixer_grads(st, grads[0], x, w_qkv, w_g, w_out, y, saved[-1], ctx.need)
+        res = _kernel_mixer_grads(st, grads[0], x, w_qkv, w_g, w_out, y, saved[-1], ctx.need, own_storage=False)
     else:
         res = bwd(grads[0], x, w_qkv, w_g, b_g, w1, w2, tau, w_out, proj, y, list(saved), *ctx.args, ctx.need)
     return (*[g if w else None for g, w in zip(res, ctx.need)], *([None] * len(ctx.args)))

@@ -105,6 +105,25 @@ def _expansion_fingerprint(*, key: str, effective_hidden: int, feature_expansion
     return torch.tensor(tuple(encoded), dtype=torch.uint8)
 
 
+
+class _SplitQKV(torch.autograd.Function):
+    """q, k, v [B,H,T,d] views of a stacked [B,T,3,H,d] projection (block.py:594).
+    The backward writes the three stream gradients, whatever their strides,
+    into one [B,T,3,H,d] gradient in one pass, in the layout the projection's
+    backward GEMMs read (autograd's own unbind and permute backward stack
+    them head-major and then copy that into this layout)."""
+
+    @staticmethod
+    def forward(ctx, proj):
+        q, k, v = proj.permute(2, 0, 3, 1, 4).unbind(0)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        like = next(g for g in (dq, dk, dv) if g is not None)
+        parts = [torch.zeros_like(like) if g is None else g for g in (dq, dk, dv)]
+        return torch.stack([g.transpose(1, 2) for g in parts], dim=2)
+
 class ThetaScan(nn.Module):
     """Drop-in token mixer x[B,T,D] -> y[B,T,D] on MI355X."""
 
@@ -490,8 +509,7 @@ class ThetaScan(nn.Module):
             k = linear(x, self.proj_k1.weight).unsqueeze(1) + kqb[1][None, :, None, :]
             v = linear(x, self.proj_v.weight).view(B, T, H, d).transpose(1, 2)
             return q, k, v
-        q, k, v = linear(x, self.proj_qkv.weight).view(B, T, 3, H, d).permute(2, 0, 3, 1, 4)
-        return q, k, v
+        return _SplitQKV.apply(linear(x, self.proj_qkv.weight).view(B, T, 3, H, d))
 
     def _forward_composed(self, x: torch.Tensor, backend: str = "hip") -> torch.Tensor:
         cfg = self.cfg

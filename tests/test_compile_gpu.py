@@ -93,3 +93,40 @@ def test_fused_path_compiles_to_one_graph_equal_to_eager(cuda, dtype):
     for run in runs[1:]:
         for a, b in zip(runs[0], run):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("preset", ["kernel_expanded_reference_v0_1", "gn_reference_v0_1"])
+def test_stacked_qkv_under_aot_autograd_equals_eager(cuda, preset):
+    """The stacked qkv projection (share_key_query=False) and the custom ops'
+    autograd registrations through AOTAutograd (fullgraph, aot_eager): the
+    output and every parameter gradient equal the eager step's."""
+    import torch._dynamo as dynamo
+    from thetascan_amd import ThetaScan, ThetaScanConfig
+
+    config = ThetaScanConfig.from_dict({
+        "preset": preset, "d_model": 64, "n_heads": 2, "share_key_query": False,
+        "runtime": {"backend": "hip", "scan_chunk": 16},
+    })
+    torch.manual_seed(12)
+    mixer = ThetaScan(config).to(cuda)
+    with torch.no_grad():
+        for name, p in mixer.named_parameters():
+            if "W2" in name or "fade_eta" in name:
+                p.copy_(torch.randn_like(p) * 0.1)
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(2, 40, 64, generator=g).to(cuda)
+    dy = torch.randn(2, 40, 64, generator=g).to(cuda)
+    dynamo.reset()
+    compiled = torch.compile(mixer, backend="aot_eager", dynamic=False, fullgraph=True)
+    runs = []
+    for fn in (mixer, compiled):
+        mixer.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        y = fn(xi)
+        y.backward(dy)
+        runs.append([y.detach(), xi.grad] + [p.grad for p in mixer.parameters()])
+    print(f"aot_eager {preset}: path={mixer._core.last_path}", flush=True)
+    for a, b in zip(*runs):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-6)

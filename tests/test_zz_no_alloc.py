@@ -112,3 +112,43 @@ def test_noalloc_scan_refuses_what_it_cannot_hold(cuda):
     kept = _desc(2, 2, 1000, 64, 64, torch.bfloat16, states_in=1)
     assert lib.ts_scan_fwd_noalloc(ctypes.byref(kept), ctypes.byref(io),
                                    _lib.stream_handle(cuda)) == _lib.TS_ERR_NOT_IMPLEMENTED
+
+
+def test_noalloc_scan_replays_inside_a_graph(cuda):
+    """After one eager call on the device (which looks up the scratch address
+    and sets the kernels' LDS limits), a ts_scan_fwd_noalloc call captured in
+    a graph replays, twice, to exactly ts_scan_fwd's outputs and final states;
+    the inputs change between the replays, with eager work and a
+    synchronization in between."""
+    from thetascan_amd import _lib
+
+    lib = _lib.load()
+    B, H, T, D = 2, 4, 1300, 64
+    q, k, v, la, dec, desc = _case(cuda, B, H, T, D, torch.bfloat16, "static", 3)
+    _run(lib, cuda, desc, q, k, v, la, dec, noalloc=True)
+    out = torch.empty(B, H, T, D, dtype=q.dtype, device=cuda)
+    mass = torch.empty(B, H, T, dtype=torch.float32, device=cuda)
+    dk_pad, dv_pad = ctypes.c_int32(), ctypes.c_int32()
+    assert lib.ts_scan_layout(ctypes.byref(desc), ctypes.byref(dk_pad), ctypes.byref(dv_pad), None) == 0
+    final = torch.empty(B * H, dk_pad.value, dv_pad.value, dtype=torch.float32, device=cuda)
+    io = _lib.ScanIO(_lib.strided(q), _lib.strided(k), _lib.strided(v), _lib.strided(None), _lib.strided(None),
+                     _lib.strided(None), la.data_ptr(), _lib.strided(None),
+                     _lib.strided(out), _lib.strided(mass), final.data_ptr(), None)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = lib.ts_scan_fwd_noalloc(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(cuda))
+    assert rc == 0, lib.ts_last_error().decode()
+    g = torch.Generator().manual_seed(4)
+    for replay in range(2):
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=g).to(cuda, t.dtype))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _run(lib, cuda, desc, q, k, v, la, dec, noalloc=False)
+        print(f"noalloc graph replay {replay}", flush=True)
+        for a, b in zip((out, mass, final), ref):
+            assert torch.equal(a, b), replay

@@ -266,8 +266,10 @@ def cpu_baseline(budget_s: float = 12.0):
         y.backward(dy)
         return time.perf_counter() - t0
 
-    first = run()
-    reps = max(3, min(25, int(budget_s / max(first, 1e-3))))
+    # two untimed warmups, then the median of at least 5 timed steps (as many
+    # as fit the budget, at most 25)
+    first = min(run(), run())
+    reps = max(5, min(25, int(budget_s / max(first, 1e-3))))
     times = [run() for _ in range(reps)]
     t = statistics.median(times)
     model = ""
@@ -279,7 +281,7 @@ def cpu_baseline(budget_s: float = 12.0):
     return {
         "value": round(Bs * Ts / t, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
         "sample": f"B={Bs} T={Ts} (one of the {B} sequences of the workload), fp32, oracle mixer with the cumsum scan, "
-                  f"median of {reps} after 1 warmup",
+                  f"median of {reps} after 2 warmups",
         "cpu": model, "ms_per_step": round(t * 1e3, 1),
     }
 

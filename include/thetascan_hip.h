@@ -33,7 +33,11 @@ extern "C" {
  * 10: the GN descriptors carry the hidden nonlinearity (and the write its
  *     damping);
  * 11: ts_scan_pair_io carries scan A's key-side ext column (k_ext);
- * 12: ts_retention_grad. */
+ * 12: ts_retention_grad.
+ * 13: ts_scan_pair_io gains log_alpha (after k_ext): ts_scan_pair_fwd takes
+ *     a static retention and the fp32 store / accumulate output modes; a
+ *     ts_retention_grad slice that reaches 2 GiB is refused with
+ *     TS_ERR_NOT_IMPLEMENTED. */
 #define TS_ABI_VERSION 13
 
 enum ts_status {
@@ -151,7 +155,10 @@ int ts_scan_fwd(const ts_scan_desc* desc, const ts_scan_io* io,
  * TS_ERR_VALUE, and states_in (kept segment states) is refused.  Every call on
  * one GPU shares that buffer: calls that overlap on one GPU (several streams,
  * several host threads) race and must be serialised by the caller.  Results
- * equal ts_scan_fwd's with the same desc and io. */
+ * equal ts_scan_fwd's with the same desc and io.  The first call on a device
+ * looks up the buffer's address and sets the kernels' LDS limits: make one
+ * call on each device outside a stream capture before capturing calls into a
+ * graph (the captured calls then make no runtime query). */
 #define TS_SCAN_NOALLOC_MAX_WORKSPACE (32u * 1024u * 1024u)
 
 int ts_scan_fwd_noalloc(const ts_scan_desc* desc, const ts_scan_io* io, hipStream_t stream);

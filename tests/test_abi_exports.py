@@ -97,3 +97,31 @@ def test_initial_state_rules_on_the_host():
     rc, nbytes = ws(init_state=1)
     assert rc == _lib.TS_OK and nbytes >= 2 * (64 * 64 + 64 + 64) * 4
     assert ws(init_state=1, states_in=1)[0] == _lib.TS_ERR_NOT_IMPLEMENTED
+
+
+def test_retention_grad_refuses_slices_beyond_2_gib_on_the_host():
+    """ts_retention_grad computes its tile offsets in 32-bit integers, so a
+    (batch, head) slice that reaches 2 GiB or more is refused before any
+    launch or workspace check (no device memory is touched: the pointers here
+    are never dereferenced)."""
+    import torch  # noqa: F401
+
+    from thetascan_amd import _lib
+
+    lib = _lib.load()
+    desc = _lib.RetentionDesc(B=1, H=2, T=4096, dk=64, dv=64, dtype=_lib.dtype_code(torch.bfloat16), has_mass=0,
+                              seg_tiles=0)
+
+    def call(q_stride):
+        fake = 1 << 20  # 16-byte aligned, never dereferenced on this path
+        s = lambda st: _lib.Strided(fake, 0, 0, st)  # noqa: E731
+        io = _lib.RetentionIO(s(q_stride), s(64), s(64), s(64), _lib.Strided(None, 0, 0, 0), fake)
+        out = ctypes.c_void_p(fake)
+        return lib.ts_retention_grad(ctypes.byref(desc), ctypes.byref(io), out, None, 0, None)
+
+    # 4096 + 64 + 64 rows of 262144 bf16 elements: 2.2 GB of reach
+    assert call(262144) == _lib.TS_ERR_NOT_IMPLEMENTED
+    assert b"2 GiB" in lib.ts_last_error()
+    # an in-range slice passes the span check and stops at the missing workspace
+    assert call(64) == _lib.TS_ERR_VALUE
+    assert b"workspace" in lib.ts_last_error()

@@ -24,7 +24,7 @@ import torch.nn.functional as F
 
 from ..config import ThetaScanConfig
 from ...state import ThetaScanState, config_fingerprint
-from ..ops import engine, features, fused, gn, interface, maps, prologue, stream
+from ..ops import composed, features, fused, gn, interface, maps, prologue, stream
 from ..ops.linear import linear
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
@@ -543,10 +543,8 @@ class ThetaScan(nn.Module):
         weights = self._weights()
         sharp = self.kernel_sharpness()
         controls = self.kernel_controls()
-        streams, _, _ = engine.write_streams(weights, cfg, k, v_w, hrot=hrot, softmax_gain=sharp,
-                                             kernel_controls=controls)
-        reads = engine.dual_read_views(weights, cfg, q, streams, tuple(views), hrot=hrot, softmax_gain=sharp,
-                                       kernel_controls=controls)
+        reads = composed.memory_forward(weights, cfg, k, v_w, q, tuple(views), hrot=hrot, gain=sharp,
+                                        controls=controls)
         return self._blend_and_project(x, reads, etas)
 
     def _temporal_views(self, x: torch.Tensor, backend: str):

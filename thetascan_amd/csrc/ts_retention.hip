@@ -590,9 +590,20 @@ size_t ws_bytes(const RetPlan& P) {
   return (P.part_bytes + 255) / 256 * 256 + (P.sums_bytes + 255) / 256 * 256 + P.comb_bytes;
 }
 
-uint32_t span_bytes(const ts_strided& s, int T, int width, int es) {
-  if (!s.ptr || T == 0) return 0;
-  return (uint32_t)(((int64_t)(T - 1) * s.st + width) * es);
+// Bytes spanned by one (batch, head) slice of a [.., T, width] stream (the
+// range of its buffer loads), or an error if the rows the kernel addresses --
+// up to T rounded up to whole tiles, plus one tile -- could not be reached with
+// 31-bit offsets (the tile offsets are computed in 32-bit integers).
+int span_bytes(const char* name, const ts_strided& s, int T, int width, int es, uint32_t* out) {
+  *out = 0;
+  if (!s.ptr || T == 0) return TS_OK;
+  if (s.st < 0) return fail(TS_ERR_VALUE, "retention grad: negative time stride of %s", name);
+  const int64_t rows = ((int64_t)T + ts::C - 1) / ts::C * ts::C + ts::C;
+  const int64_t reach = rows * s.st * es + (int64_t)width * es;
+  if (reach >= ((int64_t)1 << 31))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "retention grad: one (batch, head) slice of %s spans more than 2 GiB", name);
+  *out = (uint32_t)(((int64_t)(T - 1) * s.st + width) * es);
+  return TS_OK;
 }
 
 }  // namespace
@@ -618,6 +629,13 @@ int ts_retention_grad(const ts_retention_desc* d, const ts_retention_io* io, flo
   for (const ts_strided* s : {&io->q, &io->k, &io->v, &io->dout})
     if (((uintptr_t)s->ptr & 15u) || s->st % 8 || s->sh % 8 || s->sb % 8)
       return fail(TS_ERR_VALUE, "retention grad: streams need 16-byte aligned rows");
+  // every slice must be addressable with 31-bit offsets (checked before any launch)
+  uint32_t rec[5];
+  if ((rc = span_bytes("q", io->q, d->T, d->dk, 2, &rec[0])) || (rc = span_bytes("k", io->k, d->T, d->dk, 2, &rec[1])) ||
+      (rc = span_bytes("v", io->v, d->T, d->dv, 2, &rec[2])) ||
+      (rc = span_bytes("dout", io->dout, d->T, d->dv, 2, &rec[3])) ||
+      (rc = span_bytes("dmass", io->dmass, d->T, 1, 4, &rec[4])))
+    return rc;
   const size_t need = ws_bytes(P);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15u))
     return fail(TS_ERR_VALUE, "retention grad: workspace needs %zu bytes, 16-byte aligned", need);
@@ -632,11 +650,7 @@ int ts_retention_grad(const ts_retention_desc* d, const ts_retention_io* io, flo
   p.B = d->B; p.H = d->H; p.T = d->T; p.dk = P.dkp; p.dv = d->dv; p.nvr = P.nvr; p.has_mass = d->has_mass;
   p.seg_tiles = P.seg_tiles; p.nseg = P.nseg; p.vw = P.vw; p.nw = P.nw;
   p.q = io->q; p.k = io->k; p.v = io->v; p.dout = io->dout; p.dm = io->dmass;
-  p.q_rec = span_bytes(io->q, d->T, d->dk, 2);
-  p.k_rec = span_bytes(io->k, d->T, d->dk, 2);
-  p.v_rec = span_bytes(io->v, d->T, d->dv, 2);
-  p.o_rec = span_bytes(io->dout, d->T, d->dv, 2);
-  p.dm_rec = span_bytes(io->dmass, d->T, 1, 4);
+  p.q_rec = rec[0]; p.k_rec = rec[1]; p.v_rec = rec[2]; p.o_rec = rec[3]; p.dm_rec = rec[4];
   p.log_alpha = io->log_alpha;
   p.part = (float*)workspace;
   p.sums = (float*)((char*)workspace + (P.part_bytes + 255) / 256 * 256);

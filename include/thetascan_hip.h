@@ -37,8 +37,10 @@ extern "C" {
  * 13: ts_scan_pair_io gains log_alpha (after k_ext): ts_scan_pair_fwd takes
  *     a static retention and the fp32 store / accumulate output modes; a
  *     ts_retention_grad slice that reaches 2 GiB is refused with
- *     TS_ERR_NOT_IMPLEMENTED. */
-#define TS_ABI_VERSION 13
+ *     TS_ERR_NOT_IMPLEMENTED.
+ * 14: ts_read_out_fwd / ts_read_out_bwd / ts_read_out_bwd_parts (the read
+ *     fused with the output projection); nothing earlier changed. */
+#define TS_ABI_VERSION 14
 
 enum ts_status {
   TS_OK = 0,
@@ -397,6 +399,54 @@ int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t 
 
 /* Number P of gate-bias partial rows ts_read_bwd writes for `desc`. */
 int ts_read_bwd_parts(const ts_read_desc* desc, int32_t* parts);
+
+/* ------------------------------------- read fused with the output projection */
+
+typedef struct ts_read_out_desc {
+  ts_read_desc read;    /* B, H, T, d (32, 64, 96, 128), bf16 only, normalize,
+                           gate, scale, eps -- as for ts_read_fwd            */
+  int32_t n;            /* output width N (d_model); N and H*d are multiples
+                           of 128, H*d at most 512 and N at most 1024        */
+} ts_read_out_desc;
+
+typedef struct ts_read_out_io {
+  ts_strided num, mass, resid, g;  /* as ts_read_io (resid may be NULL)      */
+  const float* g_bias;             /* fp32 [H*d] or NULL                     */
+  const void* w;                   /* [N, H*d] output projection weight      */
+  void* out;                       /* out rows b*T + t of N elements         */
+  int64_t out_ld;                  /* row stride of out (elements)           */
+  void* y;                         /* out rows b*T + t of H*d elements: the
+                                      read output y (NULL: not kept)         */
+  int64_t y_ld;
+} ts_read_out_io;
+
+/* out = y W^T with y = (resid + s * num / (mass + eps)) * silu(g + g_bias)
+ * formed in the GEMM's prologue (y is bit-identical to ts_read_fwd's and
+ * never read back from HBM).  Replaces block.py:721-724 (the output gate,
+ * the reshape and proj_out) together with what ts_read_fwd replaces.
+ * TS_ERR_NOT_IMPLEMENTED for shapes outside the descriptor's limits. */
+int ts_read_out_fwd(const ts_read_out_desc* desc, const ts_read_out_io* io, hipStream_t stream);
+
+typedef struct ts_read_out_bwd_io {
+  ts_strided num, mass, resid, g;  /* forward inputs                         */
+  const float* g_bias;
+  const void* w_t;                 /* [H*d, N]: the weight transposed        */
+  const void* dout;                /* rows b*T + t of N: grad of out         */
+  int64_t dout_ld;
+  ts_strided dnum, dmass, dresid, dg;  /* outputs as for ts_read_bwd          */
+  float* dg_bias_part;             /* out fp32 [P, H*d] gate-bias partials
+                                      (P from ts_read_out_bwd_parts; NULL ok) */
+} ts_read_out_bwd_io;
+
+/* Backward of ts_read_out_fwd except the weight gradient (dout^T y, which
+ * the caller contracts from the y the forward kept): dy = dout W is formed
+ * in registers and consumed by the read backward (dnum, dmass, dresid, dg).
+ * Replaces the input-gradient product of proj_out (block.py:724) and the
+ * autograd backward ts_read_bwd replaces.  Needs head widths 32, 64 or 128. */
+int ts_read_out_bwd(const ts_read_out_desc* desc, const ts_read_out_bwd_io* io, hipStream_t stream);
+
+/* Number P of gate-bias partial rows ts_read_out_bwd writes for `desc`. */
+int ts_read_out_bwd_parts(const ts_read_out_desc* desc, int32_t* parts);
 
 /* ------------------------------------------------- query/key prologue */
 

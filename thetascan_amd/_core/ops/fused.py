@@ -257,6 +257,77 @@ def read_bwd(num, mass, resid, g, dy, scale: float, eps: float = 1e-6, dg=None, 
     return dnum, dmass, (dresid, dresid_hm), dg, dgbias
 
 
+def _read_out_desc(num, mass, g, n: int, scale: float, eps: float) -> _lib.ReadOutDesc:
+    B, H, T, d = num.shape
+    return _lib.ReadOutDesc(_lib.ReadDesc(B, H, T, d, _lib.dtype_code(num.dtype), int(mass is not None),
+                                          int(g is not None), float(scale), float(eps)), int(n))
+
+
+_READ_OUT_OK: dict = {}
+
+
+def read_out_supported(B: int, H: int, T: int, d: int, n: int, dtype: torch.dtype) -> bool:
+    """Whether ts_read_out_fwd / ts_read_out_bwd take this shape (a host query)."""
+    key = (B, H, T, d, n, dtype)
+    hit = _READ_OUT_OK.get(key)
+    if hit is None:
+        if dtype != torch.bfloat16:
+            hit = False
+        else:
+            desc = _lib.ReadOutDesc(_lib.ReadDesc(B, H, T, d, _lib.TS_BF16, 0, 0, 1.0, 1e-6), int(n))
+            hit = _lib.load().ts_read_out_bwd_parts(ctypes.byref(desc), None) == _lib.TS_OK
+        if len(_READ_OUT_OK) > 256:
+            _READ_OUT_OK.clear()
+        _READ_OUT_OK[key] = hit
+    return hit
+
+
+def read_out_fwd(num, mass, resid, g, w_out, out, y, scale: float, eps: float = 1e-6, gbias=None):
+    """``out`` [B*T, N] = read(num, mass, resid, g) @ w_out^T, the read
+    formed in the GEMM's prologue; ``y`` [B*T, H*d] (or None) receives the
+    read output for the weight gradient."""
+    lib = _lib.load()
+    n = w_out.shape[0]
+    desc = _read_out_desc(num, mass, g, n, scale, eps)
+    io = _lib.ReadOutIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
+                        _lib.ptr(gbias), w_out.data_ptr(), out.data_ptr(), out.stride(0),
+                        _lib.ptr(y), 0 if y is None else y.stride(0))
+    with _lib.timed("ts_read_out_fwd", lambda: _lib.nbytes(num, mass, resid, g, out, y)):
+        status = lib.ts_read_out_fwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
+    _lib.check(status, "ts_read_out_fwd")
+    return out
+
+
+def read_out_bwd(num, mass, resid, g, w_out_t, dout, scale: float, eps: float = 1e-6, dg=None, gbias=None,
+                 gbias_grad=None):
+    """Backward of :func:`read_out_fwd` except the weight gradient: ``dout``
+    [B*T, N] times the weight (``w_out_t`` = its [H*d, N] transpose) feeds
+    the read backward in registers.  Returns what :func:`read_bwd` returns."""
+    lib = _lib.load()
+    B, H, T, d = num.shape
+    n = dout.shape[-1]
+    dnum = torch.empty_like(num)
+    dmass = torch.empty(B, H, T, dtype=torch.float32, device=num.device) if mass is not None else None
+    dresid, dresid_hm = _head_major(B, H, T, d, num.dtype, num.device)
+    if g is not None and dg is None:
+        dg = torch.empty(B, T, H, d, dtype=num.dtype, device=num.device).transpose(1, 2)
+    desc = _read_out_desc(num, mass, g, n, scale, eps)
+    parts = None
+    if gbias_grad is not None and g is not None:
+        cnt = ctypes.c_int32()
+        _lib.check(lib.ts_read_out_bwd_parts(ctypes.byref(desc), ctypes.byref(cnt)), "ts_read_out_bwd_parts")
+        parts = torch.empty(cnt.value, H * d, dtype=torch.float32, device=num.device)
+    io = _lib.ReadOutBwdIO(_lib.strided(num), _lib.strided(mass), _lib.strided(resid), _lib.strided(g),
+                           _lib.ptr(gbias), w_out_t.data_ptr(), dout.data_ptr(), dout.stride(0),
+                           _lib.strided(dnum), _lib.strided(dmass), _lib.strided(dresid), _lib.strided(dg),
+                           _lib.ptr(parts))
+    with _lib.timed("ts_read_out_bwd", lambda: _lib.nbytes(num, mass, resid, g, dout, dnum, dmass, dresid, dg)):
+        status = lib.ts_read_out_bwd(ctypes.byref(desc), ctypes.byref(io), _lib.stream_handle(num.device))
+    _lib.check(status, "ts_read_out_bwd")
+    dgbias = None if parts is None else slot_sum(parts, gbias_grad, (H * d,))
+    return dnum, dmass, (dresid, dresid_hm), dg, dgbias
+
+
 def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Tensor:
     """Decayed prefix sum along T of a [B,H,T,F] stream (fp32 result).
 

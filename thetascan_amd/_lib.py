@@ -224,6 +224,23 @@ class ReadBwdIO(ctypes.Structure):
     ]
 
 
+class ReadOutDesc(ctypes.Structure):
+    _fields_ = [("read", ReadDesc), ("n", ctypes.c_int32)]
+
+
+class ReadOutIO(ctypes.Structure):
+    _fields_ = [("num", Strided), ("mass", Strided), ("resid", Strided), ("g", Strided),
+                ("g_bias", ctypes.c_void_p), ("w", ctypes.c_void_p), ("out", ctypes.c_void_p),
+                ("out_ld", ctypes.c_int64), ("y", ctypes.c_void_p), ("y_ld", ctypes.c_int64)]
+
+
+class ReadOutBwdIO(ctypes.Structure):
+    _fields_ = [("num", Strided), ("mass", Strided), ("resid", Strided), ("g", Strided),
+                ("g_bias", ctypes.c_void_p), ("w_t", ctypes.c_void_p), ("dout", ctypes.c_void_p),
+                ("dout_ld", ctypes.c_int64), ("dnum", Strided), ("dmass", Strided), ("dresid", Strided),
+                ("dg", Strided), ("dg_bias_part", ctypes.c_void_p)]
+
+
 class WcumsumDesc(ctypes.Structure):
     _fields_ = [
         ("B", ctypes.c_int32),
@@ -465,6 +482,9 @@ def load() -> ctypes.CDLL:
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_read_bwd_parts.argtypes = [P(ReadDesc), P(ctypes.c_int32)]
+        lib.ts_read_out_fwd.argtypes = [P(ReadOutDesc), P(ReadOutIO), ctypes.c_void_p]
+        lib.ts_read_out_bwd.argtypes = [P(ReadOutDesc), P(ReadOutBwdIO), ctypes.c_void_p]
+        lib.ts_read_out_bwd_parts.argtypes = [P(ReadOutDesc), P(ctypes.c_int32)]
         lib.ts_contract_workspace_bytes.argtypes = [P(ContractDesc), P(ctypes.c_size_t)]
         lib.ts_contract_tokens.argtypes = [P(ContractDesc), ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
@@ -501,7 +521,7 @@ def load() -> ctypes.CDLL:
         lib.ts_retention_workspace_bytes.argtypes = [P(RetentionDesc), P(ctypes.c_size_t)]
         lib.ts_retention_grad.argtypes = [P(RetentionDesc), P(RetentionIO), ctypes.c_void_p, ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 13:
+        if lib.ts_abi_version() != 14:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

@@ -13,10 +13,11 @@ int fail(int code, const char* fmt, ...);
 // launches, including launches recorded into a graph, skip the call).
 hipError_t ensure_lds_limit(const void* fn, int bytes);
 
-// Workgroups of `fn` (256 threads, `lds` bytes of dynamic LDS) resident on the
-// current device at once: the occupancy calculator's workgroups per CU times
-// the CU count, cached per (device, kernel, LDS size); 0 if a query fails.
-long resident_workgroups(const void* fn, int lds);
+// Workgroups of `fn` (`threads` threads, `lds` bytes of dynamic LDS) resident
+// on the current device at once: the occupancy calculator's workgroups per CU
+// times the CU count, cached per (device, kernel, LDS size, threads); 0 if a
+// query fails.
+long resident_workgroups(const void* fn, int lds, int threads = 256);
 
 // One ts_sum_slots call's arguments (host side).
 struct SlotSum {

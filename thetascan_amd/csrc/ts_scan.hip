@@ -968,18 +968,18 @@ hipError_t ensure_lds_limit(const void* fn, int bytes) {
   return e;
 }
 
-long resident_workgroups(const void* fn, int lds) {
+long resident_workgroups(const void* fn, int lds, int threads) {
   static std::mutex mu;
-  static std::map<std::tuple<int, const void*, int>, long> cache;
+  static std::map<std::tuple<int, const void*, int, int>, long> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dev, fn, lds);
+  const auto key = std::make_tuple(dev, fn, lds, threads);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int per_cu = 0, cus = 0;
   long n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, (size_t)lds) == hipSuccess &&
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, (size_t)lds) == hipSuccess &&
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
     n = (long)per_cu * cus;
   cache[key] = n;

@@ -400,6 +400,34 @@ int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t 
 /* Number P of gate-bias partial rows ts_read_bwd writes for `desc`. */
 int ts_read_bwd_parts(const ts_read_desc* desc, int32_t* parts);
 
+/* ---------------------------------------------------- value-anchor deposit */
+
+typedef struct ts_anchor_desc {
+  int32_t B, H, T;
+  int32_t d;            /* value width: 16, 32, 64 or 128                      */
+  int32_t V;            /* anchors in the codebook: 2 .. 64                    */
+  int32_t c_heads;      /* codebook heads: 1 (shared by every head) or H       */
+  int32_t dtype;        /* ts_dtype of v, r, dr, dv and the dls rows           */
+  float gain;           /* softmax gain (the configured scalar sharpness)      */
+  float eps;            /* norm floor (1e-6 in the reference)                  */
+} ts_anchor_desc;
+
+/* Padded anchor width VP (16, 32 or 64) of the backward's dls rows. */
+int ts_anchor_width(const ts_anchor_desc* desc, int32_t* vp);
+
+/* r [B,H,T,V] = softmax(gain * C (v / max(||v||, eps))), C = codebook fp32
+ * [c_heads, V, d]: the value-anchor deposit of a kernel memory.  Replaces
+ * engine.py:284-296 (the value_centers branch of write_streams). */
+int ts_anchor_fwd(const ts_anchor_desc* desc, ts_strided v, const float* codebook, ts_strided r,
+                  hipStream_t stream);
+
+/* Backward of ts_anchor_fwd: dv [B,H,T,d] from dr [B,H,T,V], and dls
+ * [H, B*T, VP] (head-major rows, zero past V) = dlogits / max(||v||, eps),
+ * so that the codebook gradient is sum over tokens of dls^T v (per head; summed
+ * over heads for a shared codebook). */
+int ts_anchor_bwd(const ts_anchor_desc* desc, ts_strided v, const float* codebook, ts_strided dr,
+                  ts_strided dv, void* dls, hipStream_t stream);
+
 /* ------------------------------------- read fused with the output projection */
 
 typedef struct ts_read_out_desc {

@@ -20,6 +20,7 @@ organisation is this module's own:
 
 What runs where: every scan in ``interface.scan_views`` / ``scan_views_mass``
 (HIP chunked scans), every decayed key mass in the HIP prefix sum, the
+value-anchor deposit (``maps.anchor_code``), the
 depth-1 GN writes and reads of the HIP GN kernels (``gn.write``,
 ``gn.read_stage``), the normalized read epilogue in ``gn.normalized_read``
 (HIP) and the per-head GEMMs in ``linear.head_matmul``.  The remaining
@@ -33,7 +34,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from . import gn, interface, kernel_features
+from . import gn, interface, kernel_features, maps
 from .linear import head_matmul
 from ..modules.norms import rmsnorm
 
@@ -270,11 +271,10 @@ class FastNet:
     # ---- write
 
     def _anchor_code(self, v):
-        """The value-anchor deposit: softmax(gain C_v v / ||v||) over the value
-        codebook (engine.py:284-296)."""
+        """The value-anchor deposit softmax(gain C_v v / max(||v||, eps)) over
+        the value codebook (engine.py:284-296): ts_anchor_fwd / ts_anchor_bwd."""
         cfg = self.cfg
-        vn = v / v.norm(dim=-1, keepdim=True).clamp_min(cfg.eps)
-        return torch.softmax(cfg.softmax_gain * _per_head(vn, self.layers[0][2], True), -1).to(v.dtype)
+        return maps.anchor_code(v, self.layers[0][2], gain=cfg.softmax_gain, eps=cfg.eps)
 
     def deposits(self, k, v):
         """Per-token payload channels of the write -> ``steps[step][layer]``

@@ -234,3 +234,90 @@ def stale_coefficients(etas) -> torch.Tensor:
     """(1, -eta_1 .. -eta_J, sum_j eta_j) over (R_0, R_stale_1 .. R_stale_J, R_null) (block.py:697-717)."""
     eta = torch.stack([e.reshape(-1) for e in etas]).to(torch.float32)
     return torch.cat([torch.ones_like(eta[:1]), -eta, eta.sum(0, keepdim=True)])
+
+
+# ------------------------------------------------------------------ value anchors
+
+
+def _anchor_desc(v4, V, c_heads, gain, eps):
+    B, H, T, d = v4.shape
+    return _lib.AnchorDesc(B, H, T, d, int(V), int(c_heads), _lib.dtype_code(v4.dtype), float(gain), float(eps))
+
+
+def _anchor_forward(v: torch.Tensor, codebook: torch.Tensor, gain: float, eps: float) -> torch.Tensor:
+    lib = _lib.load()
+    v4 = _rows(v)
+    c = codebook.detach().to(torch.float32).contiguous()
+    desc = _anchor_desc(v4, c.shape[1], c.shape[0], gain, eps)
+    r = torch.empty(*v4.shape[:3], c.shape[1], dtype=v.dtype, device=v.device)
+    with _lib.timed("ts_anchor_fwd", lambda: _lib.nbytes(v4, r)):
+        status = lib.ts_anchor_fwd(ctypes.byref(desc), _lib.strided(v4), c.data_ptr(), _lib.strided(r),
+                                   _lib.stream_handle(v.device))
+    _lib.check(status, "ts_anchor_fwd")
+    return r
+
+
+def _anchor_fake(v, codebook, gain, eps):
+    return v.new_empty(*v.shape[:3], codebook.shape[1])
+
+
+def _anchor_backward_impl(dr: torch.Tensor, v: torch.Tensor, codebook: torch.Tensor, gain: float,
+                          eps: float) -> list[torch.Tensor]:
+    from .gn import contract_tokens
+
+    lib = _lib.load()
+    v4 = _rows(v)
+    B, H, T, d = v4.shape
+    c = codebook.detach().to(torch.float32).contiguous()
+    V = c.shape[1]
+    desc = _anchor_desc(v4, V, c.shape[0], gain, eps)
+    vp = ctypes.c_int32()
+    _lib.check(lib.ts_anchor_width(ctypes.byref(desc), ctypes.byref(vp)), "ts_anchor_width")
+    dr4 = dr.to(v.dtype)
+    dv = torch.empty(B, H, T, d, dtype=v.dtype, device=v.device)
+    dls = torch.empty(H, B * T, vp.value, dtype=v.dtype, device=v.device)
+    with _lib.timed("ts_anchor_bwd", lambda: _lib.nbytes(v4, dr4, dv, dls)):
+        status = lib.ts_anchor_bwd(ctypes.byref(desc), _lib.strided(v4), c.data_ptr(), _lib.strided(dr4),
+                                   _lib.strided(dv), dls.data_ptr(), _lib.stream_handle(v.device))
+    _lib.check(status, "ts_anchor_bwd")
+    # dC[h] = sum over tokens of dls^T v: the values as head-major token rows
+    vt = v4.transpose(0, 1)
+    if not (vt.stride(1) == T * vt.stride(2)):
+        vt = vt.contiguous()
+    dc = contract_tokens(dls, vt.reshape(H, B * T, d))[:, :V]
+    if c.shape[0] == 1:
+        dc = dc.sum(0, keepdim=True)
+    return [dv, dc.to(codebook.dtype)]
+
+
+def _anchor_backward_fake(dr, v, codebook, gain, eps):
+    return [v.new_empty(v.shape), codebook.new_empty(codebook.shape)]
+
+
+def _anchor_setup(ctx, inputs, output):
+    v, codebook, gain, eps = inputs
+    ctx.args = (gain, eps)
+    ctx.save_for_backward(v, codebook)
+
+
+def _anchor_backward(ctx, dr, bwd):
+    v, codebook = ctx.saved_tensors
+    dv, dc = bwd(dr, v, codebook, *ctx.args)
+    return dv, dc, None, None
+
+
+_anchor_op = HipOp("anchor_code", forward=_anchor_forward, forward_fake=_anchor_fake,
+                   backward_impl=_anchor_backward_impl, backward_fake=_anchor_backward_fake,
+                   setup=_anchor_setup, backward=_anchor_backward)
+
+
+def anchor_code(v: torch.Tensor, codebook: torch.Tensor, *, gain: float, eps: float) -> torch.Tensor:
+    """softmax(gain * C (v / max(||v||, eps))) over the anchors of a value
+    codebook ``codebook`` [1|H, V, d] for head-major values ``v`` [B,H,T,d]
+    (engine.py:284-296), in v's dtype."""
+    _on_gpu(v, codebook)
+    if v.dtype not in _KERNEL_DTYPES:
+        raise NotImplementedError(f"hip value anchors support bf16 and fp32, got {v.dtype}")
+    if v.ndim != 4 or codebook.ndim != 3 or codebook.shape[-1] != v.shape[-1]:
+        raise ValueError("value anchors need v [B,H,T,d] and a codebook [1|H,V,d]")
+    return _anchor_op(v, codebook, float(gain), float(eps))

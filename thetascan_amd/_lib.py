@@ -224,6 +224,11 @@ class ReadBwdIO(ctypes.Structure):
     ]
 
 
+class AnchorDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "d", "V", "c_heads", "dtype")] + \
+        [("gain", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
 class ReadOutDesc(ctypes.Structure):
     _fields_ = [("read", ReadDesc), ("n", ctypes.c_int32)]
 
@@ -482,6 +487,10 @@ def load() -> ctypes.CDLL:
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_read_bwd_parts.argtypes = [P(ReadDesc), P(ctypes.c_int32)]
+        lib.ts_anchor_width.argtypes = [P(AnchorDesc), P(ctypes.c_int32)]
+        lib.ts_anchor_fwd.argtypes = [P(AnchorDesc), Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
+        lib.ts_anchor_bwd.argtypes = [P(AnchorDesc), Strided, ctypes.c_void_p, Strided, Strided, ctypes.c_void_p,
+                                      ctypes.c_void_p]
         lib.ts_read_out_fwd.argtypes = [P(ReadOutDesc), P(ReadOutIO), ctypes.c_void_p]
         lib.ts_read_out_bwd.argtypes = [P(ReadOutDesc), P(ReadOutBwdIO), ctypes.c_void_p]
         lib.ts_read_out_bwd_parts.argtypes = [P(ReadOutDesc), P(ctypes.c_int32)]

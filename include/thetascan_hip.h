@@ -400,6 +400,60 @@ int ts_read_bwd(const ts_read_desc* desc, const ts_read_bwd_io* io, hipStream_t 
 /* Number P of gate-bias partial rows ts_read_bwd writes for `desc`. */
 int ts_read_bwd_parts(const ts_read_desc* desc, int32_t* parts);
 
+/* ------------------------------------ kernel feature maps with controls */
+
+enum ts_kmap_kind { TS_KMAP_SOFTMAX = 0, TS_KMAP_RELU2 = 1 };
+enum ts_kmap_sparsity { TS_SPARSE_NONE = 0, TS_SPARSE_SOFT = 1, TS_SPARSE_ST = 2, TS_SPARSE_ST_BLEND = 3 };
+
+typedef struct ts_kmap_desc {
+  int32_t B, H, T;
+  int32_t m;            /* feature width: 16, 32, 48 or 64                     */
+  int32_t dtype;        /* ts_dtype of a, phi, dphi, da                         */
+  int32_t kind;         /* ts_kmap_kind                                         */
+  int32_t rms;          /* 1: a is the raw W1 product and is RMS-normalized
+                           first; 0: a is the normalized pre-activation        */
+  int32_t gain_mode;    /* softmax gain: 0 the scalar `gain`, 1 per head [H],
+                           2 per feature [H, m] (positive values)              */
+  int32_t sparsity;     /* ts_kmap_sparsity (softmax only)                      */
+  float gain;
+  float temperature;    /* relative-threshold temperature                      */
+  float eps;
+} ts_kmap_desc;
+
+typedef struct ts_kmap_params {
+  const float* shift;   /* [H, m] added after the RMSNorm: score bias minus the
+                           learned thresholds (NULL: none)                      */
+  const float* gain;    /* [H] or [H, m] (gain_mode 1, 2)                        */
+  const float* rho;     /* [H] relative threshold in (0, 1) (sparsity)          */
+  const float* alpha;   /* [H] sparse blend in [0, 1] (TS_SPARSE_ST_BLEND)      */
+} ts_kmap_params;
+
+/* Number P of per-workgroup partial rows of the control gradients. */
+int ts_kmap_parts(const ts_kmap_desc* desc, const ts_kmap_params* params, int32_t* parts);
+
+/* phi [B,H,T,m] = map(rmsnorm(a) + shift) (or map(a + shift)), the softmax
+ * partition with its gain, score bias and relative-to-max sparsity (soft,
+ * straight-through, straight-through blend) or the ReLU^2 ridge.  Replaces
+ * kernel_features.py:43-135 (with the RMSNorm of engine.py:117-158). */
+int ts_kmap_fwd(const ts_kmap_desc* desc, const ts_kmap_params* params, ts_strided a, ts_strided phi,
+                hipStream_t stream);
+
+typedef struct ts_kmap_grads {
+  ts_strided da;        /* out [B,H,T,m]: grad of a                              */
+  float* dshift_part;   /* out fp32 [P, H, m] (NULL: not wanted)                 */
+  float* dgain_part;    /* out fp32 [P, H] or [P, H, m] (NULL: not wanted)       */
+  float* drho_part;     /* out fp32 [P, H] (NULL: not wanted)                    */
+  float* dalpha_part;   /* out fp32 [P, H] (NULL: not wanted)                    */
+} ts_kmap_grads;
+
+/* Backward of ts_kmap_fwd: da and partial sums (over each workgroup's tokens)
+ * of the gradients of shift, gain, rho and alpha; the straight-through gates
+ * differentiate through their sigmoid, the clamp of rho and the floor of the
+ * sparse sum pass no gradient, and the max's gradient is shared equally by
+ * the maximal logits (torch's amax rule). */
+int ts_kmap_bwd(const ts_kmap_desc* desc, const ts_kmap_params* params, ts_strided a, ts_strided dphi,
+                const ts_kmap_grads* grads, hipStream_t stream);
+
 /* ---------------------------------------------------- value-anchor deposit */
 
 typedef struct ts_anchor_desc {

@@ -178,13 +178,30 @@ class FastNet:
             return torch.softmax(z * g, dim=-1)
         return _NONLIN[cfg.nonlin][0](z)
 
+    def _fused_map(self, a) -> bool:
+        """Whether the kernel family's RMSNorm, threshold and feature map (with
+        every learned control) run as one ts_kmap launch on ``a`` = W1 x."""
+        return self.cfg.write_rule == "kernel" and kernel_features.kmap_eligible(a, self.cfg)
+
+    def _kmap(self, l, a):
+        c = self.controls
+        tau = self.layers[l][2][..., 0] if self.cfg.learn_thresh else None
+        return kernel_features.kmap(
+            a, self.cfg, rms=True, tau=tau, softmax_gain=self.gain, score_bias=c.get("score_bias"),
+            relu2_threshold=c.get("relu2_threshold"), relative_threshold=c.get("relative_threshold"),
+            sparse_blend_alpha=c.get("sparse_blend_alpha"))
+
     def act(self, l, x, main_shift=None, gate_shift=None):
         """Block ``l`` at inputs ``x``; ``main_shift`` / ``gate_shift`` add to
-        the raw pre-activations W1 x / Wg x before the RMSNorm."""
+        the raw pre-activations W1 x / Wg x before the RMSNorm.  A kernel
+        memory's features come from one ts_kmap launch (its pre-activation is
+        then not kept: only the GN family's Jacobian payloads read it)."""
         W1, _, Wg = self.layers[l]
         a = _per_head(x, W1, True)
         if main_shift is not None:
             a = a + main_shift
+        if not self.gated and self._fused_map(a):
+            return Act(x, None, None, self._kmap(l, a))
         z, rz = rmsnorm(a, self.cfg.eps)
         if self.gated:
             b = _per_head(x, Wg, True)
@@ -326,6 +343,8 @@ class FastNet:
         eps = self.cfg.eps
         if self.gated:
             h = F.silu(rmsnorm(gate, eps)[0]) * rmsnorm(main, eps)[0]
+        elif self._fused_map(main):
+            h = self._kmap(l, main)
         else:
             h = self.hidden(self._shift(rmsnorm(main, eps)[0], l))
         return h, self.rotate(h)

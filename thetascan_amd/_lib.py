@@ -224,6 +224,20 @@ class ReadBwdIO(ctypes.Structure):
     ]
 
 
+class KmapDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "m", "dtype", "kind", "rms", "gain_mode", "sparsity")] + \
+        [("gain", ctypes.c_float), ("temperature", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+class KmapParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("shift", "gain", "rho", "alpha")]
+
+
+class KmapGrads(ctypes.Structure):
+    _fields_ = [("da", Strided)] + [(n, ctypes.c_void_p) for n in ("dshift_part", "dgain_part", "drho_part",
+                                                                    "dalpha_part")]
+
+
 class AnchorDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "d", "V", "c_heads", "dtype")] + \
         [("gain", ctypes.c_float), ("eps", ctypes.c_float)]
@@ -487,6 +501,9 @@ def load() -> ctypes.CDLL:
         lib.ts_read_fwd.argtypes = [P(ReadDesc), P(ReadIO), ctypes.c_void_p]
         lib.ts_read_bwd.argtypes = [P(ReadDesc), P(ReadBwdIO), ctypes.c_void_p]
         lib.ts_read_bwd_parts.argtypes = [P(ReadDesc), P(ctypes.c_int32)]
+        lib.ts_kmap_parts.argtypes = [P(KmapDesc), P(KmapParams), P(ctypes.c_int32)]
+        lib.ts_kmap_fwd.argtypes = [P(KmapDesc), P(KmapParams), Strided, Strided, ctypes.c_void_p]
+        lib.ts_kmap_bwd.argtypes = [P(KmapDesc), P(KmapParams), Strided, Strided, P(KmapGrads), ctypes.c_void_p]
         lib.ts_anchor_width.argtypes = [P(AnchorDesc), P(ctypes.c_int32)]
         lib.ts_anchor_fwd.argtypes = [P(AnchorDesc), Strided, ctypes.c_void_p, Strided, ctypes.c_void_p]
         lib.ts_anchor_bwd.argtypes = [P(AnchorDesc), Strided, ctypes.c_void_p, Strided, Strided, ctypes.c_void_p,

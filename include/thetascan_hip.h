@@ -693,6 +693,22 @@ int ts_bspline_parts(const ts_bspline_desc* desc, int32_t* nparts);
 int ts_bspline_bwd(const ts_bspline_desc* desc, ts_strided pre, const float* scale_h, ts_strided dout,
                    ts_strided dpre, float* dscale_part, hipStream_t stream);
 
+/* The same map of z = rmsnorm(a) + shift, where a [B,H,T,P] is the raw W1
+ * product (the RMS over each token's P projections, eps inside the root, as
+ * the reference's RMSNorm) and shift an fp32 [H, P] array (minus the learned
+ * threshold; NULL: none).  P is a power of two up to 64.  Replaces the
+ * RMSNorm and threshold of engine.py:117-158 around kernel_features.py:208-230
+ * for a projected B-spline memory. */
+int ts_bspline_norm_fwd(const ts_bspline_desc* desc, ts_strided a, const float* shift, float eps,
+                        const float* scale_h, ts_strided out, hipStream_t stream);
+
+/* Backward of ts_bspline_norm_fwd: da, the scale partials as ts_bspline_bwd,
+ * and fp32 partial sums of dL/dshift [H][nparts][P] (nparts from
+ * ts_bspline_parts; NULL: not wanted). */
+int ts_bspline_norm_bwd(const ts_bspline_desc* desc, ts_strided a, const float* shift, float eps,
+                        const float* scale_h, ts_strided dout, ts_strided da, float* dscale_part,
+                        float* dshift_part, hipStream_t stream);
+
 /* ------------------------------------------------------------ bank blend */
 
 /* Temporal-bank blend of n_in (<= 8) read views (block.py:667-718):

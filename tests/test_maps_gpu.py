@@ -152,3 +152,45 @@ def test_bank_blend_strided_views(cuda):
     out = maps.bank_blend(views, coef)
     ref = sum(coef[i].view(1, -1, 1, 1).cpu().double() * base[i].transpose(1, 2).double() for i in range(3))
     assert rel_err(out, ref) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-3), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("P,n_basis,learned,shifted", [(16, 8, False, False), (16, 8, True, True), (4, 8, True, False),
+                                                       (2, 5, False, True), (64, 8, False, False)])
+def test_bspline_of_rmsnormed_inputs_matches_the_oracle(cuda, dtype, tol, P, n_basis, learned, shifted):
+    """ts_bspline_norm_fwd / _bwd: basis((rmsnorm(a) + shift) * scale) / P of the
+    raw W1 products against the float64 oracle (rmsnorm, bspline_features),
+    with the gradients of a, the per-head scale and the shift; ragged T."""
+    from oracle import mixer as om
+    from thetascan_amd._core.ops import maps
+
+    B, H, T = 2, 3, 301
+    g0 = torch.Generator().manual_seed(P * 7 + n_basis)
+    a = (torch.randn(B, H, T, P, generator=g0) * 1.5).to(dtype).double()
+    scale = torch.rand(H, generator=g0) + 0.5 if learned else 1.3
+    shift = torch.randn(H, P, generator=g0) * 0.4 if shifted else None
+    dout = torch.randn(B, H, T, P * n_basis, generator=g0)
+    c = {"bspline_basis_count": n_basis, "bspline_degree": 3, "bspline_bound": 3.0}
+
+    a64 = a.clone().requires_grad_(True)
+    s64 = scale.double().requires_grad_(True) if learned else scale
+    h64 = None if shift is None else shift.double().requires_grad_(True)
+    z, _ = om.rmsnorm(a64)
+    if h64 is not None:
+        z = z + h64.view(1, H, 1, P)
+    ref = om.bspline_features(z, s64, c)
+    ref.backward(dout.to(dtype).double())
+
+    ad = a.to(dtype).to(cuda).requires_grad_(True)
+    sd = scale.to(cuda).requires_grad_(True) if learned else scale
+    hd = None if shift is None else shift.to(cuda).requires_grad_(True)
+    out = maps.bspline_norm_features(ad, shift=hd, eps=1e-6, n_basis=n_basis, degree=3, bound=3.0, scale=sd)
+    out.backward(dout.to(dtype).to(cuda))
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, T, P * n_basis) and out.dtype == dtype
+    assert rel_err(out.float(), ref) < tol
+    assert rel_err(ad.grad.float(), a64.grad) < 2 * tol
+    if learned:
+        assert rel_err(sd.grad, s64.grad) < 2 * tol
+    if shifted:
+        assert rel_err(hd.grad, h64.grad) < 2 * tol

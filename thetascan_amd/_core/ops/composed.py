@@ -180,12 +180,26 @@ class FastNet:
 
     def _fused_map(self, a) -> bool:
         """Whether the kernel family's RMSNorm, threshold and feature map (with
-        every learned control) run as one ts_kmap launch on ``a`` = W1 x."""
-        return self.cfg.write_rule == "kernel" and kernel_features.kmap_eligible(a, self.cfg)
+        every learned control) run as one HIP launch on ``a`` = W1 x: ts_kmap
+        for the softmax partition and the ReLU^2 ridge, ts_bspline_norm for
+        the projected B-spline map."""
+        if self.cfg.write_rule != "kernel":
+            return False
+        if self.cfg.kernel_kind == "projected_bspline":
+            return maps.bspline_norm_supported(a)
+        return kernel_features.kmap_eligible(a, self.cfg)
 
     def _kmap(self, l, a):
         c = self.controls
         tau = self.layers[l][2][..., 0] if self.cfg.learn_thresh else None
+        if self.cfg.kernel_kind == "projected_bspline":
+            cfg = self.cfg
+            scale = c.get("spline_scale")
+            H, P = a.shape[1], a.shape[-1]
+            shift = None if tau is None else -tau.float().reshape(-1, P).expand(H, P)
+            return maps.bspline_norm_features(a, shift=shift, eps=cfg.eps, n_basis=cfg.bspline_basis_count,
+                                              degree=cfg.bspline_degree, bound=cfg.bspline_bound,
+                                              scale=cfg.bspline_scale if scale is None else scale)
         return kernel_features.kmap(
             a, self.cfg, rms=True, tau=tau, softmax_gain=self.gain, score_bias=c.get("score_bias"),
             relu2_threshold=c.get("relu2_threshold"), relative_threshold=c.get("relative_threshold"),

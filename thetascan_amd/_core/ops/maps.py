@@ -137,6 +137,99 @@ def bspline_features(pre: torch.Tensor, *, n_basis: int, degree: int, bound: flo
     return _bspline_op(pre, None, int(n_basis), int(degree), float(bound), float(scale))
 
 
+# ---------------------------------------------------- B-spline of RMS-normed inputs
+
+
+def _bspline_norm_forward(a: torch.Tensor, shift: torch.Tensor | None, scale_h: torch.Tensor | None, n_basis: int,
+                          degree: int, bound: float, scale: float, eps: float) -> torch.Tensor:
+    lib = _lib.load()
+    a4 = _rows(a)
+    desc = _spline_desc(a4, n_basis, degree, bound, scale)
+    out = torch.empty(*a4.shape[:3], a4.shape[3] * n_basis, dtype=a.dtype, device=a.device)
+    sh = None if scale_h is None else scale_h.detach().to(torch.float32).contiguous()
+    sf = None if shift is None else shift.detach().to(torch.float32).contiguous()
+    with _lib.timed("ts_bspline_norm_fwd", lambda: _lib.nbytes(a4, out)):
+        status = lib.ts_bspline_norm_fwd(ctypes.byref(desc), _lib.strided(a4), _lib.ptr(sf), float(eps), _lib.ptr(sh),
+                                         _lib.strided(out), _lib.stream_handle(a.device))
+    _lib.check(status, "ts_bspline_norm_fwd")
+    return out
+
+
+def _bspline_norm_fake(a, shift, scale_h, n_basis, degree, bound, scale, eps):
+    return a.new_empty(*a.shape[:-1], a.shape[-1] * n_basis)
+
+
+def _bspline_norm_backward_impl(dout: torch.Tensor, a: torch.Tensor, shift: torch.Tensor | None,
+                                scale_h: torch.Tensor | None, n_basis: int, degree: int, bound: float, scale: float,
+                                eps: float) -> list[torch.Tensor]:
+    lib = _lib.load()
+    a4 = _rows(a)
+    B, H, T, P = a4.shape
+    desc = _spline_desc(a4, n_basis, degree, bound, scale)
+    sh = None if scale_h is None else scale_h.detach().to(torch.float32).contiguous()
+    sf = None if shift is None else shift.detach().to(torch.float32).contiguous()
+    d4 = _rows(dout.to(a4.dtype).reshape(B, H, T, P * n_basis))
+    da = torch.empty_like(a4)
+    n = ctypes.c_int32()
+    _lib.check(lib.ts_bspline_parts(ctypes.byref(desc), ctypes.byref(n)), "ts_bspline_parts")
+    sparts = None if sh is None else torch.empty(H, n.value, dtype=torch.float32, device=a.device)
+    hparts = None if sf is None else torch.empty(H, n.value, P, dtype=torch.float32, device=a.device)
+    with _lib.timed("ts_bspline_norm_bwd", lambda: _lib.nbytes(a4, d4, da)):
+        status = lib.ts_bspline_norm_bwd(ctypes.byref(desc), _lib.strided(a4), _lib.ptr(sf), float(eps), _lib.ptr(sh),
+                                         _lib.strided(d4), _lib.strided(da), _lib.ptr(sparts), _lib.ptr(hparts),
+                                         _lib.stream_handle(a.device))
+    _lib.check(status, "ts_bspline_norm_bwd")
+    dshift = dout.new_empty(0) if hparts is None else hparts.sum(1).to(shift.dtype)
+    dscale = dout.new_empty(0) if sparts is None else sparts.sum(-1).to(scale_h.dtype)
+    return [da, dshift, dscale]
+
+
+def _bspline_norm_backward_fake(dout, a, shift, scale_h, n_basis, degree, bound, scale, eps):
+    like = lambda t: dout.new_empty(0) if t is None else t.new_empty(t.shape)  # noqa: E731
+    return [a.new_empty(a.shape), like(shift), like(scale_h)]
+
+
+def _bspline_norm_setup(ctx, inputs, output):
+    a, shift, scale_h, *args = inputs
+    ctx.args = args
+    ctx.save_for_backward(a, shift, scale_h)
+
+
+def _bspline_norm_backward(ctx, dout, bwd):
+    a, shift, scale_h = ctx.saved_tensors
+    da, dshift, dscale = bwd(dout, a, shift, scale_h, *ctx.args)
+    return (da, dshift if shift is not None else None, dscale if scale_h is not None else None,
+            *([None] * len(ctx.args)))
+
+
+_bspline_norm_op = HipOp("bspline_norm", forward=_bspline_norm_forward, forward_fake=_bspline_norm_fake,
+                         backward_impl=_bspline_norm_backward_impl, backward_fake=_bspline_norm_backward_fake,
+                         setup=_bspline_norm_setup, backward=_bspline_norm_backward)
+
+
+def bspline_norm_supported(a: torch.Tensor) -> bool:
+    """Whether ts_bspline_norm_* take this stream: P a power of two up to 64."""
+    P = a.shape[-1]
+    return a.is_cuda and a.ndim == 4 and a.dtype in _KERNEL_DTYPES and P <= 64 and (P & (P - 1)) == 0
+
+
+def bspline_norm_features(a: torch.Tensor, *, shift, eps: float, n_basis: int, degree: int, bound: float,
+                          scale) -> torch.Tensor:
+    """``basis((rmsnorm(a) + shift) * scale).flatten(-2) / P`` for the raw W1
+    products ``a`` [B,H,T,P] (engine.py:117-158 with kernel_features.py:208-230):
+    one ts_bspline_norm_fwd / _bwd pair.  ``shift`` is None or [H, P]."""
+    _on_gpu(a)
+    if degree < 0:
+        raise ValueError("B-spline degree must be non-negative")
+    if n_basis <= degree:
+        raise ValueError("B-spline basis count must exceed its degree")
+    if bound <= 0.0:
+        raise ValueError("B-spline bound must be positive")
+    if torch.is_tensor(scale):
+        return _bspline_norm_op(a, shift, scale, int(n_basis), int(degree), float(bound), 1.0, float(eps))
+    return _bspline_norm_op(a, shift, None, int(n_basis), int(degree), float(bound), float(scale), float(eps))
+
+
 # ---------------------------------------------------------------- bank blend
 
 

@@ -62,8 +62,34 @@ struct SplineP {
   const float* scale_h;
   ts_strided pre, out, dout, dpre;
   float* dscale_part;
+  // RMS-normalized input (the norm variants): pre is the raw W1 product,
+  // normalized over each token's P projections and shifted per projection
+  float eps;
+  const float* shift;   // [H, P] or null
+  float* dshift_part;   // [H][B * tiles][P] or null
   float tab[kSplineTab];
 };
+
+// The coordinate a thread maps: the raw value, or (RMS) its token's
+// RMS-normalized value plus the shift, with zn = a / rms and 1 / rms.  The
+// P coordinates of a token sit in P consecutive lanes (P a power of two
+// dividing 64; a block starts on a token), so the token's sum of squares is
+// an xor butterfly over P lanes; every lane takes part.
+template <typename E, bool RMS>
+__device__ __forceinline__ float spline_input(const SplineP& p, int b, int h, int64_t t, int c, bool valid,
+                                              float& zn, float& rinv) {
+  const float a = valid ? tof(at<const E>(p.pre, b, h, t)[c]) : 0.f;
+  zn = a;
+  rinv = 1.f;
+  if constexpr (RMS) {
+    float ss = a * a;
+    for (int o = 1; o < p.P; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    rinv = rsqrtf(ss / (float)p.P + p.eps);
+    zn = a * rinv;
+    return zn + (p.shift ? p.shift[h * p.P + c] : 0.f);
+  }
+  return a;
+}
 
 // Copies the table into LDS (block-wide; ends with a barrier).
 template <int NI, int DMAX>
@@ -101,7 +127,7 @@ __device__ __forceinline__ void spline_basis(const float* tab, int deg, float x,
   }
 }
 
-template <typename E, int NB, int DMAX>
+template <typename E, int NB, int DMAX, bool RMS>
 __global__ __launch_bounds__(256) void bspline_fwd_kernel(SplineP p) {
   constexpr int NI = NB + DMAX;
   __shared__ float tab[spline_tab_size(NI, DMAX)];
@@ -111,10 +137,12 @@ __global__ __launch_bounds__(256) void bspline_fwd_kernel(SplineP p) {
   const int64_t n = (int64_t)p.T * p.P;
   const int64_t q0 = (int64_t)blockIdx.x * kSplineTile;
   const int64_t q = q0 + threadIdx.x;
+  const int64_t t = q / p.P;
+  const int c = (int)(q - t * p.P);
+  float zn, rinv;
+  const float pre = spline_input<E, RMS>(p, b, h, t, c, q < n, zn, rinv);
   if (q < n) {
-    const int64_t t = q / p.P;
-    const int c = (int)(q - t * p.P);
-    const float x0 = tof(at<const E>(p.pre, b, h, t)[c]) * scale;
+    const float x0 = pre * scale;
     const float x = fminf(fminf(fmaxf(x0, -p.bound), p.bound), p.hi);
     float bs[NI], dbs[NI];
     spline_basis<NI, DMAX, false>(tab, p.deg, x, bs, dbs);
@@ -142,22 +170,24 @@ __global__ __launch_bounds__(256) void bspline_fwd_kernel(SplineP p) {
   }
 }
 
-template <typename E, int NB, int DMAX>
+template <typename E, int NB, int DMAX, bool RMS>
 __global__ __launch_bounds__(256) void bspline_bwd_kernel(SplineP p) {
   constexpr int NI = NB + DMAX;
   __shared__ float tab[spline_tab_size(NI, DMAX)];
-  __shared__ float red[4];
+  __shared__ float red[4 * 64];
   spline_table<NI, DMAX>(p, tab);
   const int bh = blockIdx.y, b = bh / p.H, h = bh - b * p.H;
   const float scale = p.scale_h ? p.scale_h[h] : p.scale;
   const int64_t n = (int64_t)p.T * p.P;
   const int64_t q0 = (int64_t)blockIdx.x * kSplineTile;
   const int64_t q = q0 + threadIdx.x;
+  const int64_t t = q / p.P;
+  const int c = (int)(q - t * p.P);
+  float zn, rinv;
+  const float pre = spline_input<E, RMS>(p, b, h, t, c, q < n, zn, rinv);
   float acc[1] = {0.f};
+  float dz = 0.f;  // gradient of the map's input (before the scale)
   if (q < n) {
-    const int64_t t = q / p.P;
-    const int c = (int)(q - t * p.P);
-    const float pre = tof(at<const E>(p.pre, b, h, t)[c]);
     const float x0 = pre * scale;
     const float x1 = fminf(fmaxf(x0, -p.bound), p.bound);
     const float x = fminf(x1, p.hi);
@@ -204,12 +234,33 @@ __global__ __launch_bounds__(256) void bspline_bwd_kernel(SplineP p) {
     if (!(x0 >= -p.bound && x0 <= p.bound)) dx = 0.f;
     if (x1 > p.hi) dx = 0.f;
     else if (x1 == p.hi) dx *= 0.5f;
-    at<E>(p.dpre, b, h, t)[c] = cvt<E>(dx * scale);
+    dz = dx * scale;
     acc[0] += dx * pre;
+  }
+  if constexpr (RMS) {
+    // RMSNorm backward over the token's P lanes: da = rinv (dz - (sum dz zn / P) zn)
+    float s = dz * zn;
+    for (int o = 1; o < p.P; o <<= 1) s += __shfl_xor(s, o, 64);
+    if (q < n) at<E>(p.dpre, b, h, t)[c] = cvt<E>(rinv * (dz - s / (float)p.P * zn));
+  } else {
+    if (q < n) at<E>(p.dpre, b, h, t)[c] = cvt<E>(dz);
   }
   if (p.dscale_part) {
     const float s = block_sums<1>(acc, red);
     if (threadIdx.x == 0) p.dscale_part[(int64_t)h * p.B * p.tiles + (int64_t)b * p.tiles + blockIdx.x] = s;
+  }
+  if (RMS && p.dshift_part) {
+    // per projection c: the lanes c, c + P, ... of each wave, then the waves
+    float v = dz;
+    for (int o = p.P; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane < p.P) red[wave * 64 + lane] = v;
+    __syncthreads();
+    if ((int)threadIdx.x < p.P) {
+      const float tot = red[threadIdx.x] + red[64 + threadIdx.x] + red[128 + threadIdx.x] + red[192 + threadIdx.x];
+      p.dshift_part[((int64_t)h * p.B * p.tiles + (int64_t)b * p.tiles + blockIdx.x) * p.P + threadIdx.x] = tot;
+    }
   }
 }
 
@@ -416,27 +467,33 @@ void fill_spline(const ts_bspline_desc* d, const float* scale_h, ts::SplineP& p)
 
 typedef void (*SplineKernel)(ts::SplineP);
 
-template <typename E, bool FWD>
+template <typename E, bool FWD, bool RMS>
 SplineKernel spline_kernel(int nb, int deg) {
   const int nbb = spline_nb_bucket(nb);
   const bool lo = spline_deg_bucket(deg) == 3;
   if (FWD) {
-    if (nbb == 8) return lo ? ts::bspline_fwd_kernel<E, 8, 3> : ts::bspline_fwd_kernel<E, 8, 7>;
-    if (nbb == 16) return lo ? ts::bspline_fwd_kernel<E, 16, 3> : ts::bspline_fwd_kernel<E, 16, 7>;
-    return lo ? ts::bspline_fwd_kernel<E, 32, 3> : ts::bspline_fwd_kernel<E, 32, 7>;
+    if (nbb == 8) return lo ? ts::bspline_fwd_kernel<E, 8, 3, RMS> : ts::bspline_fwd_kernel<E, 8, 7, RMS>;
+    if (nbb == 16) return lo ? ts::bspline_fwd_kernel<E, 16, 3, RMS> : ts::bspline_fwd_kernel<E, 16, 7, RMS>;
+    return lo ? ts::bspline_fwd_kernel<E, 32, 3, RMS> : ts::bspline_fwd_kernel<E, 32, 7, RMS>;
   }
-  if (nbb == 8) return lo ? ts::bspline_bwd_kernel<E, 8, 3> : ts::bspline_bwd_kernel<E, 8, 7>;
-  if (nbb == 16) return lo ? ts::bspline_bwd_kernel<E, 16, 3> : ts::bspline_bwd_kernel<E, 16, 7>;
-  return lo ? ts::bspline_bwd_kernel<E, 32, 3> : ts::bspline_bwd_kernel<E, 32, 7>;
+  if (nbb == 8) return lo ? ts::bspline_bwd_kernel<E, 8, 3, RMS> : ts::bspline_bwd_kernel<E, 8, 7, RMS>;
+  if (nbb == 16) return lo ? ts::bspline_bwd_kernel<E, 16, 3, RMS> : ts::bspline_bwd_kernel<E, 16, 7, RMS>;
+  return lo ? ts::bspline_bwd_kernel<E, 32, 3, RMS> : ts::bspline_bwd_kernel<E, 32, 7, RMS>;
 }
 
-int launch_spline(const ts_bspline_desc* d, ts::SplineP& p, bool fwd, hipStream_t stream) {
+template <bool RMS>
+SplineKernel pick_spline(const ts_bspline_desc* d, bool fwd) {
+  if (d->dtype == TS_BF16)
+    return fwd ? spline_kernel<ts::bf16, true, RMS>(d->n_basis, d->degree)
+               : spline_kernel<ts::bf16, false, RMS>(d->n_basis, d->degree);
+  return fwd ? spline_kernel<float, true, RMS>(d->n_basis, d->degree)
+             : spline_kernel<float, false, RMS>(d->n_basis, d->degree);
+}
+
+int launch_spline(const ts_bspline_desc* d, ts::SplineP& p, bool fwd, bool rms, hipStream_t stream) {
   if (d->T == 0) return TS_OK;
   const dim3 grid((unsigned)p.tiles, (unsigned)(d->B * d->H));
-  SplineKernel k = d->dtype == TS_BF16 ? (fwd ? spline_kernel<ts::bf16, true>(d->n_basis, d->degree)
-                                              : spline_kernel<ts::bf16, false>(d->n_basis, d->degree))
-                                       : (fwd ? spline_kernel<float, true>(d->n_basis, d->degree)
-                                              : spline_kernel<float, false>(d->n_basis, d->degree));
+  SplineKernel k = rms ? pick_spline<true>(d, fwd) : pick_spline<false>(d, fwd);
   hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, p);
   return finish(fwd ? "bspline" : "bspline bwd");
 }
@@ -490,7 +547,7 @@ int ts_bspline_fwd(const ts_bspline_desc* d, ts_strided pre, const float* scale_
   p.out = out;
   p.vec = vec_rows(out, d->P * d->n_basis, d->dtype == TS_BF16 ? 2 : 4) &&
           d->n_basis % (d->dtype == TS_BF16 ? 8 : 4) == 0;
-  return launch_spline(d, p, true, stream);
+  return launch_spline(d, p, true, false, stream);
 }
 
 int ts_bspline_bwd(const ts_bspline_desc* d, ts_strided pre, const float* scale_h, ts_strided dout,
@@ -507,13 +564,59 @@ int ts_bspline_bwd(const ts_bspline_desc* d, ts_strided pre, const float* scale_
   p.dscale_part = scale_h ? dscale_part : nullptr;
   p.vec = vec_rows(dout, d->P * d->n_basis, d->dtype == TS_BF16 ? 2 : 4) &&
           d->n_basis % (d->dtype == TS_BF16 ? 8 : 4) == 0;
-  return launch_spline(d, p, false, stream);
+  return launch_spline(d, p, false, false, stream);
 }
 
 int ts_blend_parts(const ts_blend_desc* d, int32_t* nparts) {
   if (!d || !nparts || d->B < 1 || d->T < 0 || d->d < 1) return fail(TS_ERR_VALUE, "blend: bad arguments");
   *nparts = d->B * blend_tiles(d);
   return TS_OK;
+}
+
+// The B-spline map of RMS-normalized inputs: P must be a power of two up to 64.
+static int check_spline_norm(const ts_bspline_desc* d, float eps) {
+  int rc = check_spline(d);
+  if (rc) return rc;
+  if (d->P > 64 || (d->P & (d->P - 1))) return fail(TS_ERR_NOT_IMPLEMENTED, "bspline norm: %d projections (a power of two up to 64)", d->P);
+  if (!(eps > 0.f)) return fail(TS_ERR_VALUE, "bspline norm: eps must be positive");
+  return TS_OK;
+}
+
+int ts_bspline_norm_fwd(const ts_bspline_desc* d, ts_strided a, const float* shift, float eps, const float* scale_h,
+                        ts_strided out, hipStream_t stream) {
+  int rc = check_spline_norm(d, eps);
+  if (rc) return rc;
+  if (!a.ptr || !out.ptr) return fail(TS_ERR_VALUE, "bspline norm: missing tensors");
+  ts::SplineP p;
+  fill_spline(d, scale_h, p);
+  p.pre = a;
+  p.out = out;
+  p.eps = eps;
+  p.shift = shift;
+  p.vec = vec_rows(out, d->P * d->n_basis, d->dtype == TS_BF16 ? 2 : 4) &&
+          d->n_basis % (d->dtype == TS_BF16 ? 8 : 4) == 0;
+  return launch_spline(d, p, true, true, stream);
+}
+
+int ts_bspline_norm_bwd(const ts_bspline_desc* d, ts_strided a, const float* shift, float eps, const float* scale_h,
+                        ts_strided dout, ts_strided da, float* dscale_part, float* dshift_part, hipStream_t stream) {
+  int rc = check_spline_norm(d, eps);
+  if (rc) return rc;
+  if (!a.ptr || !dout.ptr || !da.ptr) return fail(TS_ERR_VALUE, "bspline norm bwd: missing tensors");
+  if (scale_h && !dscale_part) return fail(TS_ERR_VALUE, "bspline norm bwd: missing scale partials");
+  if (dshift_part && !shift) return fail(TS_ERR_VALUE, "bspline norm bwd: gradient of an absent shift");
+  ts::SplineP p;
+  fill_spline(d, scale_h, p);
+  p.pre = a;
+  p.dout = dout;
+  p.dpre = da;
+  p.eps = eps;
+  p.shift = shift;
+  p.dscale_part = scale_h ? dscale_part : nullptr;
+  p.dshift_part = dshift_part;
+  p.vec = vec_rows(dout, d->P * d->n_basis, d->dtype == TS_BF16 ? 2 : 4) &&
+          d->n_basis % (d->dtype == TS_BF16 ? 8 : 4) == 0;
+  return launch_spline(d, p, false, true, stream);
 }
 
 int ts_blend_fwd(const ts_blend_desc* d, const ts_strided* in, const float* coef, ts_strided y,

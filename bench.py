@@ -471,6 +471,8 @@ def main() -> int:
     ap.add_argument("--mode", choices=("eager", "graph"), default="eager",
                     help="time eager execution (default) or graph replays of the captured step")
     ap.add_argument("--no-variant", action="store_true", help="skip the key-mass variant")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the configurations 3, 4 and 5 lines of the default run")
     ap.add_argument("--steps-only", action="store_true", help="time the steps only (for profilers)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (reference for PMC byte counters)")
@@ -543,10 +545,33 @@ def main() -> int:
                                               "ms_per_step": round(ms_b_eager, 4)} if execution == "graph" else None,
                                     "roofline": roofline_of(passes_b, {}), "passes": passes_b},
         }
+    if not args.no_workloads:
+        out["workloads"] = other_workloads(args)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
     return 0
+
+
+def other_workloads(args) -> dict:
+    """Configurations 3 (GN), 4 (B-spline bank) and 5 (hybrid LM) in the
+    default run, each with its own steps (at most 20 timed after 5 warmups):
+    the figures ``--workload`` reports in full, minus the per-pass table."""
+    sub = argparse.Namespace(**vars(args))
+    sub.steps, sub.warmup = min(args.steps, 20), min(args.warmup, 5)
+    res = {}
+    for name in ("gn", "bspline_bank", "lm"):
+        line = run_other(name, sub)
+        keep = {k: line[k] for k in ("metric", "value", "unit", "ms_per_step", "steps", "warmup", "path")
+                if k in line}
+        keep["config"] = line["config"]
+        if "roofline" in line:
+            keep["roofline"] = line["roofline"]
+        for k in ("peak_memory_bytes", "int8_round_trip"):
+            if k in line:
+                keep[k] = line[k]
+        res[name] = keep
+    return res
 
 
 if __name__ == "__main__":

@@ -39,7 +39,9 @@ extern "C" {
  *     ts_retention_grad slice that reaches 2 GiB is refused with
  *     TS_ERR_NOT_IMPLEMENTED.
  * 14: ts_read_out_fwd / ts_read_out_bwd / ts_read_out_bwd_parts (the read
- *     fused with the output projection); nothing earlier changed. */
+ *     fused with the output projection), ts_kmap_*, ts_anchor_*,
+ *     ts_bspline_norm_*, ts_feature_fwd_summary, and ts_scan_desc.states_in
+ *     = 3; nothing earlier changed. */
 #define TS_ABI_VERSION 14
 
 enum ts_status {
@@ -95,6 +97,11 @@ typedef struct ts_scan_desc {
                            ext row u is then the swapped scan's value-side ext
                            state.  Skips the summary and prefix passes.  No
                            value-side ext column (nor key-side with 1).      */
+                        /* 3: it holds this scan's segment summaries (as
+                           ts_feature_fwd_summary writes them): the summary
+                           pass is skipped, the prefix and main passes run.
+                           Plain sum, no key-side ext columns, no final
+                           state, one value slice.                           */
   int32_t init_state;   /* 1: io->init_state holds the state entering the first
                            token (a continued sequence; 0 = a zero state).
                            The first token's decay applies to it, so a scan
@@ -329,6 +336,17 @@ typedef struct ts_feature_bwd_io {
   float* dtau_part;                /* out fp32 [P,H]: partial sums of -sum_j dpre_j      */
   const void* w2;                  /* [H,d,m] (resid; read when w2t is NULL)   */
 } ts_feature_bwd_io;
+
+/* ts_feature_fwd for keys that also writes the segment summaries of the scan
+ * `scan` (plain sum, keys = these features, values = v [B,H,T,64], with or
+ * without its value-side ones column) into that scan's workspace, exactly as
+ * the scan's own summary pass computes them (same MFMA sequence): a
+ * following ts_scan_fwd of `scan` with states_in = 3 then skips the pass that
+ * would read the features and values a second time.  bf16, d = m = 64.
+ * No counterpart in the reference (a fusion of two of its steps). */
+int ts_feature_fwd_summary(const ts_feature_desc* desc, const ts_feature_io* io, ts_strided v,
+                           const ts_scan_desc* scan, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
 
 /* Whether ts_feature_bwd needs the transposed weights w1t / w2t for `desc`
  * (weights too large to stage in LDS).  Otherwise they may be NULL: the

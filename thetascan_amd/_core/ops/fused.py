@@ -94,6 +94,36 @@ def feature_fwd(spec: FeatureSpec, x, w1, w2, tau, want_resid: bool):
     return phi, resid
 
 
+def summary_eligible(spec: FeatureSpec, x: torch.Tensor, ws) -> bool:
+    """Whether a key feature forward also writes the segment summaries of the
+    memory's forward scan (:func:`feature_fwd_summary`): bf16, d = m = 64 and
+    a scan with kept segment states.  The one-call forward uses the same rule,
+    so both paths compute the summaries in the same kernel."""
+    return ws is not None and x.dtype == torch.bfloat16 and x.shape[-1] == 64 and spec.m == 64
+
+
+def feature_fwd_summary(spec: FeatureSpec, x, w1, tau, v, normalize: bool, seg_chunks: int, ws):
+    """Key features phi(x) that also write, into ``ws``, the segment summaries
+    of the plain scan ``sum_i <q_t, phi_i> v_i`` (with its ones column when
+    ``normalize``): a following :func:`scan_hip.scan_launch` with
+    ``states_in=3`` and the same workspace skips its summary pass."""
+    lib = _lib.load()
+    B, H, T, d = x.shape
+    phi = torch.empty(B, H, T, spec.m, dtype=x.dtype, device=x.device)
+    ic, is_, fc, fs = spec.tables(T, x.device)
+    io = _lib.FeatureIO(_lib.strided(x), _lib.ptr(w1), None, _lib.ptr(tau), _lib.ptr(ic), _lib.ptr(is_),
+                        _lib.ptr(fc), _lib.ptr(fs), _lib.strided(phi), _lib.strided(None))
+    desc = spec.desc(x, tau is not None)
+    sdesc = _lib.ScanDesc(B, H, T, spec.m, v.shape[-1], _lib.dtype_code(x.dtype), _lib.RET_NONE, 0, 0, 0,
+                          _lib.EXT_ONES if normalize else 0, _lib.OUT_STORE, 1.0, int(seg_chunks), 0, 0, 3, 0)
+    with _lib.timed("ts_feature_fwd", lambda: _lib.nbytes(x, phi, v)):
+        status = lib.ts_feature_fwd_summary(ctypes.byref(desc), ctypes.byref(io), _lib.strided(v),
+                                            ctypes.byref(sdesc), ws.data_ptr(), ws.numel(),
+                                            _lib.stream_handle(x.device))
+    _lib.check(status, "ts_feature_fwd_summary")
+    return phi
+
+
 def _head_major(B, H, T, w, dtype, device):
     """[B,H,T,w] view of a head-major [H,B*T,w] buffer (GEMM-ready for weight grads)."""
     buf = torch.empty(H, B, T, w, dtype=dtype, device=device)
@@ -448,17 +478,21 @@ def _memory_forward(st: _State, proj, w1, w2, tau, b_g, spec: FeatureSpec, norma
     q, k, v, gv = _split_proj(proj, H, d, has_gate)
     dt = proj.dtype
     _weights_for(st, proj, w1, w2, tau, b_g)
-    phi_k, _ = feature_fwd(spec, k, st.w1c, None, st.tauf, False)
-    phi_q, resid = feature_fwd(spec, q, st.w1c, st.w2c, st.tauf, True)
     # The dq scan's segment states are the transpose of this scan's
     # (sum_i v_i phi_k_i^T; with the mass column its key-side row is this
     # scan's value-side sum_i phi_k_i), so the forward keeps them.
     ws = None
-    if phi_k.shape[-1] == d:
-        ws = scan_hip.workspace_for(phi_q, phi_k, v, seg_chunks=seg_chunks, v_ext=normalize)
+    if spec.m == d:
+        ws = scan_hip.workspace_for(k, k, v, seg_chunks=seg_chunks, v_ext=normalize)
+    summ = summary_eligible(spec, k, ws)
+    if summ:
+        phi_k = feature_fwd_summary(spec, k, st.w1c, st.tauf, v, normalize, seg_chunks, ws)
+    else:
+        phi_k, _ = feature_fwd(spec, k, st.w1c, None, st.tauf, False)
+    phi_q, resid = feature_fwd(spec, q, st.w1c, st.w2c, st.tauf, True)
     num, mass, _ = scan_hip.scan_launch(
         phi_q, phi_k, v, v_ext="ones" if normalize else None, want_ext_out=normalize,
-        seg_chunks=seg_chunks, workspace=ws,
+        seg_chunks=seg_chunks, workspace=ws, states_in=3 if summ else 0,
     )
     y = torch.empty(B, T, H, d, dtype=dt, device=proj.device)
     read_fwd(num, mass, resid, gv, y.transpose(1, 2), spec.resid_scale, spec.eps, gbias=st.gb)

@@ -495,6 +495,8 @@ def load() -> ctypes.CDLL:
         lib.ts_scan_views_fwd.argtypes = [P(ScanViewsDesc), P(ScanViewsIO), ctypes.c_void_p, ctypes.c_size_t,
                                           ctypes.c_void_p]
         lib.ts_feature_fwd.argtypes = [P(FeatureDesc), P(FeatureIO), ctypes.c_void_p]
+        lib.ts_feature_fwd_summary.argtypes = [P(FeatureDesc), P(FeatureIO), Strided, P(ScanDesc), ctypes.c_void_p,
+                                               ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_feature_bwd.argtypes = [P(FeatureDesc), P(FeatureBwdIO), ctypes.c_void_p]
         lib.ts_feature_bwd_parts.argtypes = [P(FeatureDesc), ctypes.c_int32, P(ctypes.c_int32)]
         lib.ts_feature_bwd_transposed.argtypes = [P(FeatureDesc), ctypes.c_int32, ctypes.c_int32, P(ctypes.c_int32)]

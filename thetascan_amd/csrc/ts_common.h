@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "thetascan_hip.h"
+
 namespace ts {
 
 // Record a message for ts_last_error() and return `code` (host side).
@@ -18,6 +20,15 @@ hipError_t ensure_lds_limit(const void* fn, int bytes);
 // times the CU count, cached per (device, kernel, LDS size, threads); 0 if a
 // query fails.
 long resident_workgroups(const void* fn, int lds, int threads = 256);
+
+// Segmentation and workspace layout of a scan (host side): 64-token tiles
+// per segment, segments, summaries the prefix reads, floats per segment state,
+// padded widths and workspace bytes (0 when the scan needs none).
+struct ScanSegments {
+  int seg_chunks, nseg, nsum, nelem, dkp, dvp;
+  size_t ws_bytes;
+};
+int scan_segments(const ts_scan_desc* d, ScanSegments* out);
 
 // One ts_sum_slots call's arguments (host side).
 struct SlotSum {

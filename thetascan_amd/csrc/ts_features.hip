@@ -47,6 +47,13 @@ struct FeatP {
   float* dw1_part;   // [parts, H, m, D] (fused weight gradients)
   float* dw2_part;   // [parts, H, D, m]
   float* dtau_part;  // [parts, H]
+  // segment summaries of the plain-sum scan whose keys are this call's
+  // features and whose values are v (summary mode of the forward): the
+  // workspace layout of that scan, one workgroup per segment
+  Str v;
+  float* seg;        // [B*H][nseg][nelem]: S [m][dvp], u [dvp], D [m]
+  float* segdec;     // [B*H][nseg]
+  int nseg, nsum, nelem, dvp, v_ones;
 };
 
 // One token row of x from LDS in the accumulator layout (dims 16db+4g+i):
@@ -210,7 +217,13 @@ constexpr bool weights_in_lds() {
   return feat_layout((int)sizeof(E), D, MB * 16, FWD, true, WG, true).end * (int)sizeof(E) + 64 <= kLdsMax;
 }
 
-template <typename E, int D, int MB, int KIND>
+// SUMM (bf16, D = 64, m = 64, no resid): the workgroup's groups are one
+// segment of the scan that reads these features as keys and v as values; the
+// workgroup also folds the segment's writes into the scan's summary
+// S = sum_t phi_t v_t^T (and D = sum_t phi_t with the scan's ones column)
+// with the scan summary pass's own MFMA sequence (same operands, same
+// order), so the scan can skip that pass and read no features twice.
+template <typename E, int D, int MB, int KIND, bool SUMM = false>
 __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
   constexpr bool WL = weights_in_lds<E, D, MB, true, false>();
   const int b = blockIdx.z, h = blockIdx.y;
@@ -239,13 +252,34 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
 
   // Each wave loads, computes and writes back its own 16 rows of every
   // group, so the group loop needs no workgroup barrier (only the weights'
-  // staging does, once).
-  WaveRows<E, D> ldx;
-  ldx.init(D, w, lane);
+  // staging does, once; the summary mode adds two per group).  The rows of
+  // the next group are in flight while a group is computed.
   const int g0 = blockIdx.x * p.groups;
-  ldx.fetch_all(xsrc, g0 * TT, p.T);
   // groups this workgroup owns (>= 1: the grid covers the tiles exactly)
   const int ng = min(p.groups, (p.T + TT - 1) / TT - g0);
+  // rows of group g0 + gi, or (gi past the last group) the last group's own
+  // rows again: cached, never stored
+  auto fetch_group = [&](auto& rows, const Rows<E>& src, int gi) {
+    const int gl = min(gi, ng - 1);
+    rows.fetch_all(src, (g0 + gi) * TT, gi < ng ? p.T : min(p.T, (g0 + gl) * TT + TT));
+  };
+  WaveRows<E, D> ldx;
+  ldx.init(D, w, lane);
+  fetch_group(ldx, xsrc, 0);
+  // summary mode: the value rows, this wave's value block of S and D
+  constexpr int VP = 64 + 16 / (int)sizeof(E);  // pitch of the value tile
+  E* vs = base + L.end;
+  const bool summ = SUMM && (int)blockIdx.x < p.nsum;  // uniform
+  WaveRows<E, 64> ldv;
+  floatx4 S[MB], Dv = {0.f, 0.f, 0.f, 0.f};
+  Rows<E> vsrc{};
+  if constexpr (SUMM) {
+#pragma unroll
+    for (int kb = 0; kb < MB; ++kb) S[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    vsrc = rows_of<E>(p.v, b, h);
+    ldv.init(64, w, lane);
+    if (summ) fetch_group(ldv, vsrc, 0);
+  }
   __syncthreads();  // weights staged
   for (int grp = 0; grp < ng; ++grp) {
     const int t0 = (g0 + grp) * TT;
@@ -259,10 +293,7 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
     // both would cost this kernel a resident wave per SIMD)
     RopeRegs<D / 16> ir;
     ir.fetch(p.in_rot, p.in_cos, p.in_sin, t, valid, g);
-    // the next group's rows (after the last group, this group's own rows
-    // again: cached, never stored)
-    const int tmax = grp + 1 < ng ? p.T : min(p.T, t0 + TT);
-    ldx.fetch_all(xsrc, t0 + TT, tmax);
+    fetch_group(ldx, xsrc, grp + 1);
     wave_lds_sync();
 
     E* xrow = xs + row * L.xp;
@@ -303,6 +334,53 @@ __global__ __launch_bounds__(256) void feature_fwd_kernel(FeatP p) {
     wave_lds_sync();
     write_rows_wave<E>(ps, L.mp, rows_of<E>(p.phi, b, h), t0, p.T, m, w, lane);
     if (want_resid) write_rows_wave<E>(xs, L.xp, rows_of<E>(p.resid, b, h), t0, p.T, D, w, lane);
+    if constexpr (SUMM) {
+      if (summ) {
+        ldv.store_valid(vs, VP, t0, p.T);  // rows past T are zero
+        if (grp + 1 < ng) fetch_group(ldv, vsrc, grp + 1);
+        __syncthreads();  // every wave's feature and value rows
+        // S[key block kb][value block w] += phi^T v over the tile's 64 tokens
+        typedef TokFrag<E> TK;
+        const auto av0 = TK::get(vs, VP, w * 16, 0, lane);
+        const auto av1 = TK::get(vs, VP, w * 16, 1, lane);
+#pragma unroll
+        for (int kb = 0; kb < MB; ++kb) {
+          S[kb] = mma32(TK::get(ps, L.mp, kb * 16, 0, lane), av0, S[kb]);
+          S[kb] = mma32(TK::get(ps, L.mp, kb * 16, 1, lane), av1, S[kb]);
+        }
+        if (p.v_ones) {
+          // D over key block w: a broadcast row of the ones column (zero past T)
+#pragma unroll
+          for (int kp = 0; kp < 2; ++kp) {
+            bf16x8 one;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int key = 32 * kp + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+              one[e] = cvt<E>(t0 + key < p.T ? 1.0f : 0.0f);
+            }
+            Dv = mma32(one, TK::get(ps, L.mp, w * 16, kp, lane), Dv);
+          }
+        }
+        __syncthreads();  // the tiles are read before the next group's rows replace them
+      }
+    }
+  }
+  if constexpr (SUMM) {
+    if (summ) {
+      // the scan summary pass's store: S [key][value] (pitch dvp), u = 0, D, and
+      // the segment's log-decay 0 (plain sum)
+      const int bh = b * p.H + h;
+      float* dst = p.seg + ((size_t)bh * p.nseg + blockIdx.x) * (size_t)p.nelem;
+#pragma unroll
+      for (int kb = 0; kb < MB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(kb * 16 + 4 * g + i) * p.dvp + w * 16 + l16] = S[kb][i];
+      if (g == 0) {
+        dst[m * p.dvp + w * 16 + l16] = 0.0f;
+        dst[m * p.dvp + p.dvp + w * 16 + l16] = Dv[0];
+      }
+      if (tid == 0) p.segdec[(size_t)bh * p.nseg + blockIdx.x] = 0.0f;
+    }
   }
 }
 
@@ -1290,6 +1368,53 @@ int ts_feature_fwd(const ts_feature_desc* d, const ts_feature_io* io, hipStream_
   Plan P;
   if ((rc = plan_feature(d, true, io->resid.ptr != nullptr, false, &P))) return rc;
   return launch_feature(pick(d, true, false), P, stream, p);
+}
+
+int ts_feature_fwd_summary(const ts_feature_desc* d, const ts_feature_io* io, ts_strided v,
+                           const ts_scan_desc* scan, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  int rc = check_feature_desc(d);
+  if (rc) return rc;
+  if (!io || !io->x.ptr || !io->w1 || !io->phi.ptr || !v.ptr || !scan)
+    return fail(TS_ERR_VALUE, "feature summary: missing tensors");
+  if (io->resid.ptr) return fail(TS_ERR_VALUE, "feature summary: keys carry no residual");
+  if (d->has_tau && !io->tau) return fail(TS_ERR_VALUE, "feature: missing tau");
+  if ((d->in_rot && (!io->in_cos || !io->in_sin)) || (d->feat_rot && (!io->f_cos || !io->f_sin)))
+    return fail(TS_ERR_VALUE, "feature: missing rope tables");
+  if (d->dtype != TS_BF16 || d->d != 64 || d->m != 64)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature summary: bf16 with d = m = 64 only");
+  if (scan->B != d->B || scan->H != d->H || scan->T != d->T || scan->dk != d->m || scan->dv != 64 ||
+      scan->dtype != TS_BF16 || scan->retention != TS_RET_NONE || scan->reverse || scan->q_ext != TS_EXT_NONE ||
+      scan->k_ext != TS_EXT_NONE || (scan->v_ext != TS_EXT_NONE && scan->v_ext != TS_EXT_ONES) ||
+      scan->want_final || scan->init_state || scan->value_split)
+    return fail(TS_ERR_NOT_IMPLEMENTED, "feature summary: the scan must be a plain 64 x 64 bf16 sum over these "
+                                        "features (optionally with its ones column)");
+  ts::ScanSegments sg;
+  if ((rc = ts::scan_segments(scan, &sg))) return rc;
+  if (sg.dvp != 64 || sg.dkp != 64) return fail(TS_ERR_NOT_IMPLEMENTED, "feature summary: padded widths");
+  if (sg.ws_bytes > 0 && (!workspace || ws_bytes < sg.ws_bytes || ((uintptr_t)workspace & 15)))
+    return fail(TS_ERR_VALUE, "feature summary: workspace needs %zu bytes, 16-byte aligned", sg.ws_bytes);
+  const int es = 2;
+  ts::FeatP p;
+  fill_common(d, p);
+  if ((rc = to_str("x", io->x, es, d->T, &p.x)) || (rc = to_str("phi", io->phi, es, d->T, &p.phi)) ||
+      (rc = to_str("v", v, es, d->T, &p.v)))
+    return rc;
+  if (d->T == 0) return TS_OK;
+  p.w1 = io->w1; p.tau = io->tau;
+  p.in_cos = io->in_cos; p.in_sin = io->in_sin; p.f_cos = io->f_cos; p.f_sin = io->f_sin;
+  p.seg = (float*)workspace;
+  p.segdec = p.seg ? p.seg + (size_t)d->B * d->H * sg.nseg * (size_t)sg.nelem : nullptr;
+  p.nseg = sg.nseg; p.nsum = sg.ws_bytes > 0 ? sg.nsum : 0; p.nelem = sg.nelem; p.dvp = sg.dvp;
+  p.v_ones = scan->v_ext == TS_EXT_ONES ? 1 : 0;
+  Plan P;
+  if ((rc = plan_feature(d, true, false, false, &P))) return rc;
+  // one workgroup per segment of the scan
+  P.groups = sg.seg_chunks;
+  P.grid = dim3((unsigned)sg.nseg, d->H, d->B);
+  P.lds += (size_t)ts::TT * (64 + 8) * es;
+  FeatFn fn = d->kind == TS_FEAT_RELU2 ? (FeatFn)ts::feature_fwd_kernel<ts::bf16, 64, 4, TS_FEAT_RELU2, true>
+                                       : (FeatFn)ts::feature_fwd_kernel<ts::bf16, 64, 4, TS_FEAT_SOFTMAX, true>;
+  return launch_feature(fn, P, stream, p);
 }
 
 int ts_feature_bwd_parts(const ts_feature_desc* d, int32_t has_dresid, int32_t* parts) {

@@ -148,6 +148,13 @@ int plan_memory(const ts_memory_desc* d, MemPlan* P) {
   return TS_OK;
 }
 
+// Whether the forward scan's segment summaries come from the key feature
+// kernel (ts_feature_fwd_summary): bf16, d = m = 64, and a scan with kept
+// segment states (more than one segment).
+bool summaries_from_features(const ts_feature_desc& f, const MemPlan& P) {
+  return f.dtype == TS_BF16 && f.d == 64 && f.m == 64 && P.ws_f > 0;
+}
+
 // Contiguous [B,H,T,w] stream at byte offset `off` of `base`.
 ts_strided bhtw(const void* base, size_t off, const ts_feature_desc& f, int w) {
   return ts_strided{(const char*)base + off, (int64_t)f.H * f.T * w, (int64_t)f.T * w, (int64_t)w};
@@ -203,15 +210,24 @@ int ts_memory_fwd(const ts_memory_desc* d, const ts_memory_io* io, ts_strided y,
   const ts_strided res = bhtw(sv, P.o_res, f, f.d), num = bhtw(sv, P.o_num, f, f.d);
   const ts_strided mass = d->normalize ? bhtw(sv, P.o_mass, f, 1) : none();
 
+  // The key features' kernel also writes the forward scan's segment
+  // summaries (64-wide bf16 features with kept segment states), so the scan
+  // runs its prefix and main passes only.
+  void* wsf = P.ws_f ? sv + P.o_wsf : nullptr;
+  const bool summ = summaries_from_features(f, P);
   ts_feature_io fk = {io->k, io->w1, nullptr, tau32, io->in_cos, io->in_sin, io->f_cos, io->f_sin, phk, none()};
-  if ((rc = ts_feature_fwd(&f, &fk, stream))) return rc;
+  if (summ) rc = ts_feature_fwd_summary(&f, &fk, io->v, &P.sf, wsf, P.ws_f, stream);
+  else rc = ts_feature_fwd(&f, &fk, stream);
+  if (rc) return rc;
   ts_feature_io fq = {io->q, io->w1, io->w2, tau32, io->in_cos, io->in_sin, io->f_cos, io->f_sin, phq, res};
   if ((rc = ts_feature_fwd(&f, &fq, stream))) return rc;
 
   ts_scan_io s;
   memset(&s, 0, sizeof(s));
   s.q = phq; s.k = phk; s.v = io->v; s.out = num; s.out_ext = mass;
-  if ((rc = ts_scan_fwd(&P.sf, &s, P.ws_f ? sv + P.o_wsf : nullptr, P.ws_f, stream))) return rc;
+  ts_scan_desc sf = P.sf;
+  if (summ) sf.states_in = 3;
+  if ((rc = ts_scan_fwd(&sf, &s, wsf, P.ws_f, stream))) return rc;
 
   ts_read_desc rd = {f.B, f.H, f.T, f.d, f.dtype, d->normalize ? 1 : 0, d->gate ? 1 : 0, f.resid_scale, f.eps};
   ts_read_io ri = {num, mass, res, d->gate ? io->g : none(), y, gb32};

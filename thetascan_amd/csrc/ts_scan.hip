@@ -1062,8 +1062,12 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   L->nseg = L->nchunks > 0 ? (L->nchunks + L->seg_chunks - 1) / L->seg_chunks : 0;
   L->nsum = d->want_final ? L->nseg : (L->nseg > 0 ? L->nseg - 1 : 0);
   L->nelem = L->dkp * L->dvp + L->dvp + L->dkp;
-  if (d->states_in < 0 || d->states_in > 2) return fail(TS_ERR_VALUE, "scan: states_in must be 0, 1 or 2");
-  if (d->states_in) {
+  if (d->states_in < 0 || d->states_in > 3) return fail(TS_ERR_VALUE, "scan: states_in must be 0, 1, 2 or 3");
+  if (d->states_in == 3) {
+    if (d->want_final || L->kx || d->retention != TS_RET_NONE)
+      return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment summaries need a plain sum without a final state "
+                                          "or key-side ext columns");
+  } else if (d->states_in) {
     if ((L->kx && d->states_in == 1) || L->vx || d->want_final)
       return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment states need no value-side ext column and no "
                                           "final state");
@@ -1072,11 +1076,26 @@ int compute_layout(const ts_scan_desc* d, Layout* L) {
   }
   if (d->init_state && d->states_in)
     return fail(TS_ERR_NOT_IMPLEMENTED, "scan: an initial state with given segment states");
+  if (d->states_in == 3 && L->nsum > 0 && !(d->value_split == 0 && L->nvs == 1))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "scan: given segment summaries need one value slice");
   L->ws_bytes = 0;
   if (L->nsum > 0 || d->init_state)
     L->ws_bytes = (size_t)bh * L->nseg * (size_t)L->nelem * sizeof(float) + (size_t)bh * L->nseg * sizeof(float) + 256;
   return TS_OK;
 }
+
+}  // namespace
+
+int ts::scan_segments(const ts_scan_desc* d, ts::ScanSegments* out) {
+  Layout L;
+  int rc = compute_layout(d, &L);
+  if (rc) return rc;
+  out->seg_chunks = L.seg_chunks; out->nseg = L.nseg; out->nsum = L.nsum; out->nelem = L.nelem;
+  out->dkp = L.dkp; out->dvp = L.dvp; out->ws_bytes = L.ws_bytes;
+  return TS_OK;
+}
+
+namespace {
 
 typedef void (*KernelFn)(ts::ScanP);
 
@@ -1404,8 +1423,10 @@ static int scan_fwd_impl(const ts_scan_desc* d, const ts_scan_io* io, void* work
 
   p.states_t = d->states_in == 2;
   p.has_init = d->init_state ? 1 : 0;
-  if ((L.nsum > 0 || d->init_state) && d->states_in == 0) {
-    if (L.nsum > 0 && (rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p))) return rc;
+  if ((L.nsum > 0 || d->init_state) && (d->states_in == 0 || d->states_in == 3)) {
+    // states_in 3: the workspace already holds the summaries (the prefix runs)
+    if (d->states_in == 0 && L.nsum > 0 && (rc = launch(fsum, dim3(L.nsum, bh, L.nvs), lds_sum, stream, p)))
+      return rc;
     ts::FinalP F{d->want_final ? io->final_state : nullptr, d->init_state ? io->init_state : nullptr, L.dkp, L.dvp,
                  d->dk, d->dv, L.kx ? 1 : 0, L.vx ? 1 : 0};
     hipLaunchKernelGGL(ts::scan_prefix_kernel, dim3((L.nelem / 4 + 255) / 256, bh), dim3(256), 0, stream, p.seg,

@@ -40,8 +40,8 @@ extern "C" {
  *     TS_ERR_NOT_IMPLEMENTED.
  * 14: ts_read_out_fwd / ts_read_out_bwd / ts_read_out_bwd_parts (the read
  *     fused with the output projection), ts_kmap_*, ts_anchor_*,
- *     ts_bspline_norm_*, ts_feature_fwd_summary, and ts_scan_desc.states_in
- *     = 3; nothing earlier changed. */
+ *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3
+ *     and TS_GN_SILU; nothing earlier changed. */
 #define TS_ABI_VERSION 14
 
 enum ts_status {
@@ -575,6 +575,8 @@ enum ts_gn_act {
   TS_GN_RELU2 = 0,  /* sigma = relu(pre)^2, sigma' = 2 relu(pre)   (engine.py nonlin relu2) */
   TS_GN_TANH = 1,   /* sigma = tanh(pre), sigma' = 1 - tanh(pre)^2 (no counterpart in the
                        reference, whose nonlinearities are relu2 and silu, nonlin.py:28-31) */
+  TS_GN_SILU = 2,   /* sigma = pre sigmoid(pre), sigma' = sg (1 + pre (1 - sg))
+                       (engine.py nonlin silu, nonlin.py:18-24)                          */
 };
 
 /* Damped Gauss-Newton write of a one-hidden-layer fast network
@@ -585,7 +587,7 @@ enum ts_gn_act {
  *   lam = r / ((|h|^2 + |x|^2 (W2 o W2)(sigma'(pre) rinv)^2) * inv_depth + damping)
  *   g = s sigma'(pre) (W2^T lam) rinv
  * Outputs h [.,m] (LA2 keys), s*lam [.,d] (LA2 values), g [.,m] (LA1 values).
- * Depth-1 memories (s = inv_depth = 1) with relu2, relu2_threshold or tanh.
+ * Depth-1 memories (s = inv_depth = 1) with relu2, relu2_threshold, silu or tanh.
  * The reference's damping is eps (engine.py:255). */
 typedef struct ts_gn_desc {
   int32_t B, H, T;

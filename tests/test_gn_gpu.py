@@ -4,7 +4,9 @@ The oracle's write_streams (a restatement of engine.py:117-340, pinned by the
 reference's GN mixer vectors in tests/golden) gives h, s*lam and g for a
 depth-1 ReLU^2 memory; its autograd gives every gradient the HIP backward
 must reproduce: dx (through h, lam and g), dv, dW1, dW2 and the per-feature
-threshold.
+threshold.  Both hidden nonlinearities of the reference are covered: ReLU^2
+and SiLU (nonlin.py:18-31; the SiLU slope needs the pre-activation and its
+backward silu'').
 """
 from __future__ import annotations
 
@@ -17,8 +19,8 @@ from tests.conftest import rel_err
 pytestmark = pytest.mark.gpu
 
 
-def _cfg(learn_thresh):
-    return {"write_rule": "gn", "nonlin": "relu2", "depth": 1, "fast_w1": True, "write_iters": 1,
+def _cfg(learn_thresh, nonlin="relu2"):
+    return {"write_rule": "gn", "nonlin": nonlin, "depth": 1, "fast_w1": True, "write_iters": 1,
             "learn_thresh": learn_thresh, "value_centers": 0}
 
 
@@ -41,16 +43,17 @@ WIDE = [pytest.param(BF, 64, 192, True, 90, id="bf16-wide-d64-m192"),
         pytest.param(BF, 64, 384, False, 100, id="bf16-wide-d64-m384")]
 
 
+@pytest.mark.parametrize("nonlin", ["relu2", "silu"])
 @pytest.mark.parametrize("dtype,d,m,learn_thresh,T", [
     (dt, *case) for dt in (torch.float32, BF)
     for case in [(16, 48, False, 70), (64, 128, False, 150), (32, 96, True, 64), (16, 16, True, 33),
                  (128, 64, False, 40)]] + [(torch.float32, 64, 192, True, 90)] + WIDE)
-def test_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T):
+def test_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T, nonlin):
     from thetascan_amd._core.ops import gn
 
     B, H = 2, 3
     k, v, w1, w2, wg = _case(B, H, T, d, m, learn_thresh, 100 * d + m + T, dtype)
-    c = _cfg(learn_thresh)
+    c = _cfg(learn_thresh, nonlin)
     # oracle forward + backward (fp64)
     rk, rv, rw1, rw2 = (t.clone().requires_grad_(True) for t in (k, v, w1, w2))
     rwg = wg.clone().requires_grad_(True) if learn_thresh else None
@@ -66,7 +69,7 @@ def test_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T):
     dev = lambda t: None if t is None else t.to(cuda, dtype).requires_grad_(True)  # noqa: E731
     x_, v_, w1_, w2_ = dev(k), dev(v), dev(w1), dev(w2)
     tau_ = dev(wg[..., 0].contiguous()) if learn_thresh else None
-    h, lam, g = gn.write(x_, v_, w1_, w2_, tau_)
+    h, lam, g = gn.write(x_, v_, w1_, w2_, tau_, nonlin=nonlin)
     torch.autograd.backward([h, lam, g], [dh.to(cuda, dtype), dl.to(cuda, dtype), dg.to(cuda, dtype)])
 
     tol = 2e-3 if dtype == torch.float32 else 3e-2
@@ -91,18 +94,19 @@ def test_gn_write_rejects_unsupported_widths(cuda):
         gn.write(x, x, w1, w2)
 
 
+@pytest.mark.parametrize("nonlin", ["relu2", "silu"])
 @pytest.mark.parametrize("dtype,d,m,learn_thresh,T", [
     (dt, *case) for dt in (torch.float32, BF)
     for case in [(16, 48, True, 70), (64, 128, False, 130), (32, 96, False, 64)]] +
     [(torch.float32, 64, 192, True, 90)] + WIDE)
-def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T):
+def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T, nonlin):
     """Stage without a correction: h and q + s W2 h are the oracle's
     block_forward (engine.py:117-158) of the query, gradients included."""
     from thetascan_amd._core.ops import gn
 
     B, H = 2, 3
     q, _, w1, w2, wg = _case(B, H, T, d, m, learn_thresh, 7 * d + m + T, dtype)
-    c = _cfg(learn_thresh)
+    c = _cfg(learn_thresh, nonlin)
     rq, rw1, rw2 = (t.clone().requires_grad_(True) for t in (q, w1, w2))
     rwg = wg.clone().requires_grad_(True) if learn_thresh else None
     u, ctx = mixer.block_forward(rw1, rw2, rwg, c, rq, {})
@@ -115,7 +119,7 @@ def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T)
     dev = lambda t: t.to(cuda, dtype).requires_grad_(True)  # noqa: E731
     q_, w1_, w2_ = dev(q), dev(w1), dev(w2)
     tau_ = dev(wg[..., 0].contiguous()) if learn_thresh else None
-    h, resid = gn.read_stage(q_, w1_, w2_, tau_, want_resid=True)
+    h, resid = gn.read_stage(q_, w1_, w2_, tau_, want_resid=True, nonlin=nonlin)
     torch.autograd.backward([h, resid], [dh.to(cuda, dtype), dr.to(cuda, dtype)])
     tol = 2e-3 if dtype == torch.float32 else 3e-2
     assert rel_err(h, h_ref) < tol and rel_err(resid, resid_ref) < tol

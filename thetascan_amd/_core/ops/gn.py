@@ -1,6 +1,6 @@
 """GN-family write payloads on the GPU (ts_gn_write_fwd / ts_gn_write_bwd).
 
-Replaces, for depth-1 ReLU^2 (and ReLU^2-threshold) GN memories with one
+Replaces, for depth-1 ReLU^2 (and ReLU^2-threshold), SiLU or tanh GN memories with one
 Jacobian step, the torch chain of src/thetascan/_core/ops/engine.py:117-158
 (_block_forward), 180-195 (_g_from_lambda), 215-255 (_lambda_solve) and the
 stream assembly of 260-340: one kernel produces the LA2 keys h, the LA2
@@ -18,7 +18,7 @@ from ... import _lib
 from .dispatch import HipOp
 
 GN_HEAD_DIMS = (16, 32, 64, 128)
-ACTS = {"relu2": _lib.GN_RELU2, "tanh": _lib.GN_TANH}  # hidden nonlinearities the kernels take
+ACTS = {"relu2": _lib.GN_RELU2, "tanh": _lib.GN_TANH, "silu": _lib.GN_SILU}  # hidden nonlinearities the kernels take
 
 
 def supported_width(m: int, dtype: torch.dtype | None = None, d: int | None = None) -> bool:
@@ -188,7 +188,7 @@ def write(x, v, w1, w2, tau=None, *, s: float = 1.0, inv_depth: float = 1.0, eps
     """GN write payloads ``(h, s*lam, g)`` of keys ``x`` and values ``v``
     ([B,H,T,d]) for per-head weights ``w1`` [H,m,d], ``w2`` [H,d,m] (a leading
     1 broadcasts over heads) and an optional threshold ``tau`` [H,m].
-    ``nonlin`` is the hidden nonlinearity (relu2 or tanh); ``damping`` the
+    ``nonlin`` is the hidden nonlinearity (relu2, silu or tanh); ``damping`` the
     Jacobi diagonal's damping (None: ``eps``, as the reference)."""
     if not (x.is_cuda and v.is_cuda):
         raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")

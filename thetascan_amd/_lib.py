@@ -33,6 +33,7 @@ EXT_ARRAY = 2
 
 GN_RELU2 = 0
 GN_TANH = 1
+GN_SILU = 2
 
 OUT_STORE = 0
 OUT_STORE_F32 = 1

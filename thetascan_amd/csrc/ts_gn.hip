@@ -77,23 +77,47 @@ constexpr bool gn_weights_in_lds() {
 
 // The hidden nonlinearity sigma and its slope sp = sigma'(pre), written as a
 // function of h = sigma(pre) (relu2: 2 sqrt(h) = 2 relu(pre); tanh: 1 - h^2).
+__device__ __forceinline__ float gn_sigmoid(float pre) { return 1.f / (1.f + __expf(-pre)); }
 __device__ __forceinline__ float gn_act(int act, float pre) {
   if (act == TS_GN_TANH) return tanhf(pre);
+  if (act == TS_GN_SILU) return pre * gn_sigmoid(pre);
   const float rp = fmaxf(pre, 0.f);
   return rp * rp;
 }
-__device__ __forceinline__ float gn_slope(int act, float hval) {
+// sigma'(pre): from h for relu2 and tanh, from pre for SiLU
+// (silu' = sg (1 + pre (1 - sg)), sg = sigmoid(pre)).
+__device__ __forceinline__ float gn_slope(int act, float pre, float hval) {
+  if (act == TS_GN_SILU) {
+    const float sg = gn_sigmoid(pre);
+    return sg * (1.f + pre * (1.f - sg));
+  }
   return act == TS_GN_TANH ? 1.f - hval * hval : 2.f * sqrtf(hval);
 }
 // d pre of a term dh * h + dsp * sp: sigma'(pre) dh + sigma''(pre) dsp
 // (relu2: 2 relu(pre) dh + 2 dsp for pre > 0, else 0;
-//  tanh: (1 - h^2) dh - 2 h (1 - h^2) dsp).
+//  tanh: (1 - h^2) dh - 2 h (1 - h^2) dsp;
+//  silu: silu'' = sg (1 - sg) (2 + pre (1 - 2 sg))).
 __device__ __forceinline__ float gn_dpre(int act, float pre, float hval, float dh, float dsp) {
   if (act == TS_GN_TANH) {
     const float d1 = 1.f - hval * hval;
     return d1 * dh - 2.f * hval * d1 * dsp;
   }
+  if (act == TS_GN_SILU) {
+    const float sg = gn_sigmoid(pre);
+    const float d1 = sg * (1.f + pre * (1.f - sg));
+    const float d2 = sg * (1.f - sg) * (2.f + pre * (1.f - 2.f * sg));
+    return d1 * dh + d2 * dsp;
+  }
   return pre > 0.f ? 2.f * fmaxf(pre, 0.f) * dh + 2.f * dsp : 0.f;
+}
+// The four thresholds of features fb*16 + 4g .. +3 (zeros without tau).
+__device__ __forceinline__ void tau4(const float* tau, bool has_tau, int fb, int g, float* tv) {
+  if (has_tau) {
+    const floatx4 t4 = *(const floatx4*)(tau + fb * 16 + 4 * g);
+    tv[0] = t4[0]; tv[1] = t4[1]; tv[2] = t4[2]; tv[3] = t4[3];
+  } else {
+    tv[0] = tv[1] = tv[2] = tv[3] = 0.f;
+  }
 }
 
 // Four consecutive elements of row t (zero past T).
@@ -184,9 +208,10 @@ __device__ __forceinline__ void gn_forward_token(const GnP& p, int b, int h, int
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float hval = gn_act(p.act, k.a[fb][i] * k.rinv - tv[i]);
+      const float pre = k.a[fb][i] * k.rinv - tv[i];
+      const float hval = gn_act(p.act, pre);
       hv[fb][i] = hval;
-      const float sv = gn_slope(p.act, hval) * k.rinv;
+      const float sv = gn_slope(p.act, pre, hval) * k.rinv;
       s2v[fb][i] = sv * sv;
       hh += hval * hval;
     }
@@ -254,11 +279,12 @@ __global__ __launch_bounds__(256) void gn_write_fwd_kernel(GnP p) {
     gemm_back<E, M, D / 16>(w2t, wp1, k.lam, l16, g, D / 16, z);
 #pragma unroll
     for (int fb = 0; fb < MB; ++fb) {
-      float hvv[4], gv[4];
+      float hvv[4], gv[4], tv[4];
+      tau4(tau, p.has_tau, fb, g, tv);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         hvv[i] = hv[fb][i];
-        const float sp = gn_slope(p.act, hv[fb][i]);
+        const float sp = gn_slope(p.act, k.a[fb][i] * k.rinv - tv[i], hv[fb][i]);
         gv[i] = p.s * sp * z[fb][i] * k.rinv;
       }
       st4_row<E>(p.h, b, h, t, fb * 16 + 4 * g, valid, hvv);
@@ -349,11 +375,12 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
       gemm_back<E, M, D / 16>(w2t, wpd, k.lam, l16, g, D / 16, z);
 #pragma unroll
       for (int fb = 0; fb < MB; ++fb) {
-        float dgv[4];
+        float dgv[4], tv[4];
         ld4_row<E>(p.dg, b, h, t, fb * 16 + 4 * g, valid, dgv);
+        tau4(tau, p.has_tau, fb, g, tv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float sp = gn_slope(p.act, hv[fb][i]);
+          const float sp = gn_slope(p.act, k.a[fb][i] * k.rinv - tv[i], hv[fb][i]);
           const float sdg = p.s * dgv[i];
           dz[fb][i] = sdg * sp * k.rinv;
           dsp[fb][i] = sdg * z[fb][i] * k.rinv;
@@ -398,14 +425,17 @@ __global__ __launch_bounds__(256) void gn_write_bwd_kernel(GnP p) {
       floatx4 ds2[MB];
       gemm_back_sq<E, M, D / 16>(w2t, wpd, drq, l16, g, ds2);
 #pragma unroll
-      for (int fb = 0; fb < MB; ++fb)
+      for (int fb = 0; fb < MB; ++fb) {
+        float tv[4];
+        tau4(tau, p.has_tau, fb, g, tv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float sp = gn_slope(p.act, hv[fb][i]);
+          const float sp = gn_slope(p.act, k.a[fb][i] * k.rinv - tv[i], hv[fb][i]);
           const float dsv = 2.f * sp * k.rinv * ds2[fb][i];
           dsp[fb][i] += dsv * k.rinv;
           drinv += dsv * sp;
         }
+      }
     }
     // ---- r = v - x - s W2 h
     floatx4 du[D / 16];
@@ -852,9 +882,10 @@ __device__ __forceinline__ void gnw_forward(const GnP& p, const float* tau, cons
       tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float hval = gn_act(p.act, a[f][i] * rinv - tv[i]);
+        const float pre = a[f][i] * rinv - tv[i];
+        const float hval = gn_act(p.act, pre);
         hv[f][i] = hval;
-        const float sv = gn_slope(p.act, hval) * rinv;
+        const float sv = gn_slope(p.act, pre, hval) * rinv;
         s2v[f][i] = sv * sv;
         hsum += hval * hval;
       }
@@ -939,8 +970,8 @@ __global__ __launch_bounds__(256) void gn_write_fwd_wide_kernel(GnP p) {
         tau_of<MB>(tau, 4 * c + f, g, p.has_tau, tv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float hval = gn_act(p.act, a[f][i] * rinv - tv[i]);
-          gv[i] = p.s * gn_slope(p.act, hval) * z[f][i] * rinv;
+          const float pre = a[f][i] * rinv - tv[i];
+          gv[i] = p.s * gn_slope(p.act, pre, gn_act(p.act, pre)) * z[f][i] * rinv;
         }
         st4_row<E>(p.g, b, h, t, c * 64 + f * 16 + 4 * g, valid, gv);
       }
@@ -1038,7 +1069,8 @@ __global__ __launch_bounds__(256) void gn_write_bwd_wide_kernel(GnP p) {
         ld4_row<E>(p.dg, b, h, t, c * 64 + f * 16 + 4 * g, valid, dgv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float sp = gn_slope(p.act, gn_act(p.act, a[f][i] * rinv - tv[i]));
+          const float pre = a[f][i] * rinv - tv[i];
+          const float sp = gn_slope(p.act, pre, gn_act(p.act, pre));
           const float sdg = p.s * dgv[i];
           dz[f][i] = sdg * sp * rinv;
           drinv += sdg * sp * z[f][i];
@@ -1100,7 +1132,7 @@ __global__ __launch_bounds__(256) void gn_write_bwd_wide_kernel(GnP p) {
         for (int i = 0; i < 4; ++i) {
           const float pre = a[f][i] * rinv - tv[i];
           const float hval = gn_act(p.act, pre);
-          const float sp = gn_slope(p.act, hval);
+          const float sp = gn_slope(p.act, pre, hval);
           const float dsv = 2.f * sp * rinv * ds2[f][i];
           const float dsp = p.s * dgv[i] * z[f][i] * rinv + dsv * rinv;
           drv += dsv * sp;
@@ -1420,7 +1452,8 @@ int check_gn(const ts_gn_desc* d) {
     return fail(TS_ERR_NOT_IMPLEMENTED,
                 "gn: hidden width %d (a multiple of 16 up to 128, 192 or 256; 384 in bf16 at head widths 32, 64)", d->m);
   if (d->H > 65535 || d->B > 65535) return fail(TS_ERR_NOT_IMPLEMENTED, "gn: grid too large");
-  if (d->act != TS_GN_RELU2 && d->act != TS_GN_TANH) return fail(TS_ERR_VALUE, "gn: unknown nonlinearity %d", d->act);
+  if (d->act != TS_GN_RELU2 && d->act != TS_GN_TANH && d->act != TS_GN_SILU)
+    return fail(TS_ERR_VALUE, "gn: unknown nonlinearity %d", d->act);
   if (!(d->damping > 0.f)) return fail(TS_ERR_VALUE, "gn: damping must be > 0");
   return TS_OK;
 }

@@ -40,8 +40,8 @@ extern "C" {
  *     TS_ERR_NOT_IMPLEMENTED.
  * 14: ts_read_out_fwd / ts_read_out_bwd / ts_read_out_bwd_parts (the read
  *     fused with the output projection), ts_kmap_*, ts_anchor_*,
- *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3
- *     and TS_GN_SILU; nothing earlier changed. */
+ *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3,
+ *     TS_GN_SILU and ts_gn_act_*; nothing earlier changed. */
 #define TS_ABI_VERSION 14
 
 enum ts_status {
@@ -681,6 +681,38 @@ typedef struct ts_gn_read_bwd_io {
 /* Backward of ts_gn_read_fwd: dq, dnum, dmass and the token tiles of
  * dW1 = da^T q, dW2 = (s dresid)^T h, dtau = -sum_tokens dpre. */
 int ts_gn_read_bwd(const ts_gn_read_desc* desc, const ts_gn_read_bwd_io* io, hipStream_t stream);
+
+/* Per-row GN hidden activation with its Jacobian scales, the nonlinear core
+ * of any GN block (engine.py:117-158 _block_forward, with the per-feature
+ * scales that _g_from_lambda / _w2s / _lambda_solve multiply W2 by,
+ * engine.py:180-255): for a = W1 x (and the SwiGLU gate pre-activation
+ * b = Wg x) of one token,
+ *   elementwise act:  z = a ra - tau, h = sigma(z), sa = sigma'(z) ra
+ *   TS_GN_SWIGLU:     za = a ra, zb = b rb, h = silu(zb) za,
+ *                     sa = silu(zb) ra, sb = za silu'(zb) rb
+ * with ra, rb the inverse RMS of a, b.  The GEMMs around it (W1 x, W2 h,
+ * W2^T lam, (W2 o W2) sa^2) stay with the caller, which is what lets one
+ * kernel serve any depth and both Gauss-Newton steps. */
+enum { TS_GN_SWIGLU = 3 };
+typedef struct ts_gn_act_desc {
+  int32_t B, H, T;
+  int32_t m;            /* hidden width, a multiple of 8 (bf16) or 4 (fp32)     */
+  int32_t dtype;        /* of every row                                         */
+  int32_t act;          /* ts_gn_act or TS_GN_SWIGLU                            */
+  int32_t has_tau;      /* elementwise acts: subtract tau [H, m] (fp32)         */
+  float eps;            /* RMSNorm eps (1e-6 in the reference)                  */
+} ts_gn_act_desc;
+
+/* h, and when their pointers are set sa (and sb for SwiGLU); rows [B,H,T,m]
+ * with 16-byte aligned rows; b only for SwiGLU. */
+int ts_gn_act_fwd(const ts_gn_act_desc* desc, ts_strided a, ts_strided b, const float* tau, ts_strided h,
+                  ts_strided sa, ts_strided sb, hipStream_t stream);
+
+/* Backward of ts_gn_act_fwd: da (and db) from dh, dsa, dsb (a null pointer
+ * reads as zeros); dz, when set, receives dz = d(a ra - tau) per row, whose
+ * negated token sum is dtau. */
+int ts_gn_act_bwd(const ts_gn_act_desc* desc, ts_strided a, ts_strided b, const float* tau, ts_strided dh,
+                  ts_strided dsa, ts_strided dsb, ts_strided da, ts_strided db, ts_strided dz, hipStream_t stream);
 
 /* ------------------------------------------------------ B-spline features */
 

@@ -53,10 +53,20 @@ def test_mixer_matches_reference_golden(cuda, name):
     module.load_state_dict({k: v.to(torch.float32) if v.is_floating_point() else v for k, v in state.items()},
                            strict=True)
     x = arr["x"].to(cuda, torch.float32).requires_grad_(True)
-    y = module(x)
+    from thetascan_amd import _lib
+
+    with _lib.record_launches() as launches:
+        y = module(x)
+        (y * arr["dy"].to(cuda, torch.float32)).sum().backward()
+        torch.cuda.synchronize()
     print(f"{name}: path={module._core.last_path}", flush=True)
     assert rel_err(y, arr["y"]) < 1e-3, name
-    (y * arr["dy"].to(cuda, torch.float32)).sum().backward()
+    if CASES[name]["config"]["family"] == "gn":
+        # every GN write runs its nonlinear core in a HIP kernel: the fused
+        # depth-1 write, or the per-row activation (any depth, two steps, SwiGLU)
+        names = {r[0] for r in launches}
+        assert names & {"ts_gn_write_fwd", "ts_gn_act_fwd"}, (name, sorted(names))
+        assert names & {"ts_gn_write_bwd", "ts_gn_act_bwd"}, (name, sorted(names))
     assert rel_err(x.grad, arr["grad:x"]) < 2e-3, name
     params = dict(module.named_parameters())
     for pname, g in grads.items():

@@ -20,11 +20,15 @@ organisation is this module's own:
 
 What runs where: every scan in ``interface.scan_views`` / ``scan_views_mass``
 (HIP chunked scans), every decayed key mass in the HIP prefix sum, the
-value-anchor deposit (``maps.anchor_code``), the
+value-anchor deposit (``maps.anchor_code``), the kernel feature maps
+(``kernel_features.kmap``, ``maps.bspline_norm_features``), the
 depth-1 GN writes and reads of the HIP GN kernels (``gn.write``,
-``gn.read_stage``), the normalized read epilogue in ``gn.normalized_read``
-(HIP) and the per-head GEMMs in ``linear.head_matmul``.  The remaining
-elementwise work is torch on the GPU.
+``gn.read_stage``), every other GN block's RMSNorm, nonlinearity and Jacobian
+scales (``gn.act_rows``: any depth, both Gauss-Newton steps, SwiGLU), the
+normalized read epilogue in ``gn.normalized_read`` (HIP) and the per-head
+GEMMs in ``linear.head_matmul``.  The remaining elementwise work (the
+products of the scales with the GEMM outputs, the Jacobi division) is torch
+on the GPU.
 """
 from __future__ import annotations
 
@@ -101,13 +105,18 @@ def _divide(num, mass, eps, dtype):
 class Act:
     """One block evaluated on a stream of block inputs ``inp``: ``z`` the
     RMS-normed (and thresholded) main pre-activation with ``rz`` = 1/rms,
-    ``h`` the hidden features, and for SwiGLU the gate branch ``zg``, ``rzg``."""
+    ``h`` the hidden features, and for SwiGLU the gate branch ``zg``, ``rzg``.
+    A GN block whose activation ran in ts_gn_act carries its Jacobian scales
+    instead: ``sa`` = sigma'(z) rz (SwiGLU: silu(zg) rz) and, for SwiGLU,
+    ``sb`` = z silu'(zg) rzg."""
     inp: torch.Tensor
-    z: torch.Tensor
-    rz: torch.Tensor
+    z: torch.Tensor | None
+    rz: torch.Tensor | None
     h: torch.Tensor
     zg: torch.Tensor | None = None
     rzg: torch.Tensor | None = None
+    sa: torch.Tensor | None = None
+    sb: torch.Tensor | None = None
 
 
 @dataclass(frozen=True)
@@ -205,22 +214,36 @@ class FastNet:
             relu2_threshold=c.get("relu2_threshold"), relative_threshold=c.get("relative_threshold"),
             sparse_blend_alpha=c.get("sparse_blend_alpha"))
 
+    def _gn_rows(self, a) -> bool:
+        """Whether a GN block's RMSNorm, nonlinearity and Jacobian scales run
+        as one ts_gn_act launch on ``a`` = W1 x (relu2, silu, tanh, SwiGLU)."""
+        return self.cfg.write_rule == "gn" and gn.act_rows_eligible(a, self.cfg.nonlin)
+
+    def _tau(self, l):
+        return self.layers[l][2][..., 0] if self.cfg.learn_thresh and not self.gated else None
+
     def act(self, l, x, main_shift=None, gate_shift=None):
         """Block ``l`` at inputs ``x``; ``main_shift`` / ``gate_shift`` add to
         the raw pre-activations W1 x / Wg x before the RMSNorm.  A kernel
         memory's features come from one ts_kmap launch (its pre-activation is
-        then not kept: only the GN family's Jacobian payloads read it)."""
+        then not kept: only the GN family's Jacobian payloads read it); a GN
+        block's features and Jacobian scales from one ts_gn_act launch."""
         W1, _, Wg = self.layers[l]
         a = _per_head(x, W1, True)
         if main_shift is not None:
             a = a + main_shift
         if not self.gated and self._fused_map(a):
             return Act(x, None, None, self._kmap(l, a))
-        z, rz = rmsnorm(a, self.cfg.eps)
+        b = None
         if self.gated:
             b = _per_head(x, Wg, True)
             if gate_shift is not None:
                 b = b + gate_shift
+        if self._gn_rows(a):
+            h, sa, sb = gn.act_rows(a, b, self._tau(l), nonlin=self.cfg.nonlin, eps=self.cfg.eps)
+            return Act(x, None, None, h, sa=sa, sb=sb)
+        z, rz = rmsnorm(a, self.cfg.eps)
+        if self.gated:
             zg, rzg = rmsnorm(b, self.cfg.eps)
             return Act(x, z, rz, F.silu(zg) * z, zg, rzg)
         z = self._shift(z, l)
@@ -233,7 +256,15 @@ class FastNet:
     def _slope(self, act):
         """dh/da as a per-feature scale for the elementwise nets (1/rms
         included: RMSNorm enters through its scalar factor only)."""
+        if act.sa is not None:
+            return act.sa
         return _NONLIN[self.cfg.nonlin][1](act.z, act.h) * act.rz
+
+    def _gate_scales(self, act):
+        """SwiGLU's two per-feature scales (main branch, gate branch)."""
+        if act.sa is not None:
+            return act.sa, act.sb
+        return F.silu(act.zg) * act.rz, act.z * _silu_slope(act.zg) * act.rzg
 
     def jac_payload(self, l, act, lam):
         """S^T (W2^T lam): the LA1 values of block ``l`` (engine.py:180-195)."""
@@ -243,7 +274,8 @@ class FastNet:
             hu = act.h * u
             return (hu - act.h * hu.sum(-1, keepdim=True)) * (act.rz * cfg.softmax_gain)
         if self.gated:
-            return torch.cat([F.silu(act.zg) * u * act.rz, act.z * _silu_slope(act.zg) * u * act.rzg], dim=-1)
+            sa, sb = self._gate_scales(act)
+            return torch.cat([sa * u, sb * u], dim=-1)
         return self._slope(act) * u
 
     def gram_share(self, l, act):
@@ -262,8 +294,7 @@ class FastNet:
             rowsq = (act.rz * cfg.softmax_gain).square() * (A - 2.0 * c * Bv + c * c * p2.sum(-1, keepdim=True))
         else:
             if self.gated:
-                sa = F.silu(act.zg) * act.rz
-                sb = act.z * _silu_slope(act.zg) * act.rzg
+                sa, sb = self._gate_scales(act)
                 sq = sa * sa + sb * sb
             else:
                 sq = self._slope(act).square()
@@ -355,7 +386,9 @@ class FastNet:
     def _features_at(self, l, main, gate):
         """Hidden features of raw pre-activations -> (h, rotated h)."""
         eps = self.cfg.eps
-        if self.gated:
+        if self._gn_rows(main):
+            h = gn.act_rows(main, gate, self._tau(l), nonlin=self.cfg.nonlin, eps=eps, want_scales=False)[0]
+        elif self.gated:
             h = F.silu(rmsnorm(gate, eps)[0]) * rmsnorm(main, eps)[0]
         elif self._fused_map(main):
             h = self._kmap(l, main)
@@ -419,7 +452,11 @@ class FastNet:
             first = steps[0][l]
             if first.jac is None:
                 raise RuntimeError("read_norm_w1 requires an LA1 GN stream")
-            probe = self.rotate(_relu_sq(self._shift(rmsnorm(main, cfg.eps)[0], l))).to(first.feat.dtype)
+            if gn.act_rows_eligible(main, "relu2"):
+                h0 = gn.act_rows(main, None, self._tau(l), nonlin="relu2", eps=cfg.eps, want_scales=False)[0]
+            else:
+                h0 = _relu_sq(self._shift(rmsnorm(main, cfg.eps)[0], l))
+            probe = self.rotate(h0).to(first.feat.dtype)
             pairs = interface.scan_views_mass(group, probe, first.feat, first.jac, "m")
             mains = [main + _divide(num, key_mass(cfg, view, probe, first.feat, mass), cfg.eps, main.dtype)[..., :m]
                      for view, (num, mass) in zip(group, pairs)]

@@ -400,3 +400,117 @@ def read_eligible(cfg, weights, q: torch.Tensor) -> bool:
         return False
     W1, W2, _ = weights[0]
     return q.shape[-1] in GN_HEAD_DIMS and supported_width(W1.shape[-2], q.dtype, q.shape[-1])
+
+
+# ------------------------------------------------------------------ per-row activation
+
+ACT_ROWS = dict(ACTS, swiglu=_lib.GN_SWIGLU)  # ts_gn_act_* nonlinearities
+
+
+def act_rows_eligible(a: torch.Tensor, nonlin: str) -> bool:
+    """Whether ts_gn_act takes these pre-activations: [B,H,T,m] rows in bf16
+    (m a multiple of 8) or fp32 (of 4) on the GPU, an elementwise nonlinearity
+    or SwiGLU."""
+    vec = 8 if a.dtype == torch.bfloat16 else 4
+    return (nonlin in ACT_ROWS and a.is_cuda and a.ndim == 4 and a.dtype in (torch.bfloat16, torch.float32)
+            and a.shape[-1] % vec == 0)
+
+
+def _act_desc(a, act, has_tau, eps):
+    B, H, T, m = a.shape
+    return _lib.GnActDesc(B, H, T, m, _lib.dtype_code(a.dtype), int(act), int(has_tau), float(eps))
+
+
+def _act_forward(a: torch.Tensor, b: torch.Tensor | None, tau: torch.Tensor | None, act: int, eps: float,
+                 want_scales: bool) -> list[torch.Tensor]:
+    lib = _lib.load()
+    a4 = _rows(a)
+    b4 = None if b is None else _rows(b.to(a.dtype))
+    tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    glu = act == _lib.GN_SWIGLU
+    h = torch.empty(a4.shape, dtype=a.dtype, device=a.device)
+    sa = torch.empty_like(h) if want_scales else None
+    sb = torch.empty_like(h) if want_scales and glu else None
+    desc = _act_desc(a4, act, tau is not None, eps)
+    with _lib.timed("ts_gn_act_fwd", lambda: _lib.nbytes(a4, b4, h, sa, sb)):
+        status = lib.ts_gn_act_fwd(ctypes.byref(desc), _lib.strided(a4), _lib.strided(b4), _lib.ptr(tauf),
+                                   _lib.strided(h), _lib.strided(sa), _lib.strided(sb), _lib.stream_handle(a.device))
+    _lib.check(status, "ts_gn_act_fwd")
+    empty = a.new_empty(0)
+    return [h, empty if sa is None else sa, empty if sb is None else sb]
+
+
+def _act_fake(a, b, tau, act, eps, want_scales):
+    glu = act == _lib.GN_SWIGLU
+    return [a.new_empty(a.shape), a.new_empty(a.shape) if want_scales else a.new_empty(0),
+            a.new_empty(a.shape) if want_scales and glu else a.new_empty(0)]
+
+
+def _act_backward_impl(dh: torch.Tensor | None, dsa: torch.Tensor | None, dsb: torch.Tensor | None, a: torch.Tensor,
+                       b: torch.Tensor | None, tau: torch.Tensor | None, act: int, eps: float,
+                       need_tau: bool) -> list[torch.Tensor]:
+    lib = _lib.load()
+    a4 = _rows(a)
+    b4 = None if b is None else _rows(b.to(a.dtype))
+    tauf = None if tau is None else tau.detach().to(torch.float32).contiguous()
+    glu = act == _lib.GN_SWIGLU
+    g = lambda t: None if t is None or t.numel() == 0 else _rows(t.to(a.dtype))  # noqa: E731
+    dh4, dsa4, dsb4 = g(dh), g(dsa), g(dsb)
+    da = torch.empty(a4.shape, dtype=a.dtype, device=a.device)
+    db = torch.empty_like(da) if glu else None
+    dz = torch.empty_like(da) if need_tau and tau is not None else None
+    desc = _act_desc(a4, act, tau is not None, eps)
+    with _lib.timed("ts_gn_act_bwd", lambda: _lib.nbytes(a4, b4, dh4, dsa4, dsb4, da, db, dz)):
+        status = lib.ts_gn_act_bwd(ctypes.byref(desc), _lib.strided(a4), _lib.strided(b4), _lib.ptr(tauf),
+                                   _lib.strided(dh4), _lib.strided(dsa4), _lib.strided(dsb4), _lib.strided(da),
+                                   _lib.strided(db), _lib.strided(dz), _lib.stream_handle(a.device))
+    _lib.check(status, "ts_gn_act_bwd")
+    empty = a.new_empty(0)
+    dtau = empty if dz is None else (-dz.float().sum(dim=(0, 2))).to(tau.dtype)
+    return [da, empty if db is None else db.to(b.dtype), dtau]
+
+
+def _act_backward_fake(dh, dsa, dsb, a, b, tau, act, eps, need_tau):
+    return [a.new_empty(a.shape), a.new_empty(0) if b is None else b.new_empty(b.shape),
+            tau.new_empty(tau.shape) if need_tau and tau is not None else a.new_empty(0)]
+
+
+def _act_setup(ctx, inputs, output):
+    a, b, tau, act, eps, _want = inputs
+    ctx.act, ctx.eps = act, eps
+    ctx.need_tau = tau is not None and tau.requires_grad
+    ctx.save_for_backward(a, b, tau)
+
+
+def _act_backward(ctx, grads, bwd):
+    dh, dsa, dsb = grads
+    a, b, tau = ctx.saved_tensors
+    da, db, dtau = bwd(dh, dsa, dsb, a, b, tau, ctx.act, ctx.eps, ctx.need_tau)
+    return (da, db if b is not None else None, dtau if ctx.need_tau else None, None, None, None)
+
+
+_act_op = HipOp("gn_act", forward=_act_forward, forward_fake=_act_fake, backward_impl=_act_backward_impl,
+                backward_fake=_act_backward_fake, setup=_act_setup, backward=_act_backward)
+
+
+def act_rows(a, b=None, tau=None, *, nonlin: str = "relu2", eps: float = 1e-6, want_scales: bool = True):
+    """The GN block's hidden features and Jacobian scales of pre-activations
+    ``a`` = W1 x ([B,H,T,m]; ``b`` = Wg x for SwiGLU) on the GPU
+    (ts_gn_act_fwd / ts_gn_act_bwd):
+
+    * elementwise nonlinearity: z = rmsnorm(a) - tau, h = sigma(z),
+      sa = sigma'(z) / rms(a)  (engine.py:117-158, 180-255);
+    * SwiGLU: h = silu(rmsnorm(b)) rmsnorm(a), sa = silu(rmsnorm(b)) / rms(a),
+      sb = rmsnorm(a) silu'(rmsnorm(b)) / rms(b).
+
+    Returns ``(h, sa, sb)`` (sa / sb None when not wanted or not SwiGLU)."""
+    if not a.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    act = ACT_ROWS[nonlin]
+    if (act == _lib.GN_SWIGLU) != (b is not None):
+        raise ValueError("gn act: SwiGLU needs the gate pre-activation b, the other nonlinearities none")
+    if tau is not None:
+        H, m = a.shape[1], a.shape[-1]
+        tau = tau.reshape(-1, m).expand(H, m) if tau.shape != (H, m) else tau
+    h, sa, sb = _act_op(a, b, tau, int(act), float(eps), bool(want_scales))
+    return h, (sa if want_scales else None), (sb if want_scales and b is not None else None)

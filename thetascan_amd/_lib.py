@@ -34,6 +34,7 @@ EXT_ARRAY = 2
 GN_RELU2 = 0
 GN_TANH = 1
 GN_SILU = 2
+GN_SWIGLU = 3
 
 OUT_STORE = 0
 OUT_STORE_F32 = 1
@@ -284,6 +285,11 @@ class BsplineDesc(ctypes.Structure):
         ("bound", ctypes.c_float),
         ("scale", ctypes.c_float),
     ]
+
+
+class GnActDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "m", "dtype", "act", "has_tau")] + [
+        ("eps", ctypes.c_float)]
 
 
 class GnDesc(ctypes.Structure):
@@ -546,6 +552,10 @@ def load() -> ctypes.CDLL:
         lib.ts_gn_write_bwd.argtypes = [P(GnDesc), P(GnBwdIO), ctypes.c_void_p]
         lib.ts_gn_read_fwd.argtypes = [P(GnReadDesc), P(GnReadIO), ctypes.c_void_p]
         lib.ts_gn_read_bwd.argtypes = [P(GnReadDesc), P(GnReadBwdIO), ctypes.c_void_p]
+        lib.ts_gn_act_fwd.argtypes = [P(GnActDesc), Strided, Strided, ctypes.c_void_p, Strided, Strided, Strided,
+                                      ctypes.c_void_p]
+        lib.ts_gn_act_bwd.argtypes = [P(GnActDesc), Strided, Strided, ctypes.c_void_p] + [Strided] * 6 + [
+            ctypes.c_void_p]
         lib.ts_memory_bytes.argtypes = [P(MemoryDesc), P(ctypes.c_size_t), P(ctypes.c_size_t)]
         lib.ts_memory_fwd.argtypes = [P(MemoryDesc), P(MemoryIO), Strided, ctypes.c_void_p, ctypes.c_size_t,
                                       ctypes.c_void_p]

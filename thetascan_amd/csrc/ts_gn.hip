@@ -25,6 +25,7 @@
 // are LDS weight rows and accumulator fragments of the previous product.
 
 #include "ts_common.h"
+#include "ts_gn_act.h"
 #include "ts_tokens.h"
 #include "thetascan_hip.h"
 
@@ -75,41 +76,6 @@ constexpr bool gn_weights_in_lds() {
   return gn_layout((int)sizeof(E), D, MB * 16, FWD, true).end * (int)sizeof(E) <= kGnLdsMax;
 }
 
-// The hidden nonlinearity sigma and its slope sp = sigma'(pre), written as a
-// function of h = sigma(pre) (relu2: 2 sqrt(h) = 2 relu(pre); tanh: 1 - h^2).
-__device__ __forceinline__ float gn_sigmoid(float pre) { return 1.f / (1.f + __expf(-pre)); }
-__device__ __forceinline__ float gn_act(int act, float pre) {
-  if (act == TS_GN_TANH) return tanhf(pre);
-  if (act == TS_GN_SILU) return pre * gn_sigmoid(pre);
-  const float rp = fmaxf(pre, 0.f);
-  return rp * rp;
-}
-// sigma'(pre): from h for relu2 and tanh, from pre for SiLU
-// (silu' = sg (1 + pre (1 - sg)), sg = sigmoid(pre)).
-__device__ __forceinline__ float gn_slope(int act, float pre, float hval) {
-  if (act == TS_GN_SILU) {
-    const float sg = gn_sigmoid(pre);
-    return sg * (1.f + pre * (1.f - sg));
-  }
-  return act == TS_GN_TANH ? 1.f - hval * hval : 2.f * sqrtf(hval);
-}
-// d pre of a term dh * h + dsp * sp: sigma'(pre) dh + sigma''(pre) dsp
-// (relu2: 2 relu(pre) dh + 2 dsp for pre > 0, else 0;
-//  tanh: (1 - h^2) dh - 2 h (1 - h^2) dsp;
-//  silu: silu'' = sg (1 - sg) (2 + pre (1 - 2 sg))).
-__device__ __forceinline__ float gn_dpre(int act, float pre, float hval, float dh, float dsp) {
-  if (act == TS_GN_TANH) {
-    const float d1 = 1.f - hval * hval;
-    return d1 * dh - 2.f * hval * d1 * dsp;
-  }
-  if (act == TS_GN_SILU) {
-    const float sg = gn_sigmoid(pre);
-    const float d1 = sg * (1.f + pre * (1.f - sg));
-    const float d2 = sg * (1.f - sg) * (2.f + pre * (1.f - 2.f * sg));
-    return d1 * dh + d2 * dsp;
-  }
-  return pre > 0.f ? 2.f * fmaxf(pre, 0.f) * dh + 2.f * dsp : 0.f;
-}
 // The four thresholds of features fb*16 + 4g .. +3 (zeros without tau).
 __device__ __forceinline__ void tau4(const float* tau, bool has_tau, int fb, int g, float* tv) {
   if (has_tau) {

@@ -11,7 +11,10 @@ synthetic: x ~ N(0,1), upstream gradient ~ N(0, (1e-2)^2), weights seeded
 
 One step = forward + backward of the whole mixer (projections included).
 The timed region brackets exactly ``--steps`` steps with a device
-synchronisation on both sides, inputs already resident in HBM.
+synchronisation on both sides, inputs already resident in HBM.  The
+projection GEMMs run the library solutions measured for these shapes
+(thetascan_amd.gemm_solutions; ``--library-gemm-heuristics`` times the
+libraries' own choice instead); ``gemm_solutions`` on the line says which.
 
 Extra objects on the JSON line:
   roofline      -- the HIP entry point with the most time per step against
@@ -476,6 +479,9 @@ def main() -> int:
     ap.add_argument("--steps-only", action="store_true", help="time the steps only (for profilers)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (reference for PMC byte counters)")
+    ap.add_argument("--library-gemm-heuristics", action="store_true",
+                    help="time the headline with the libraries' own GEMM solution choice instead of the "
+                         "measured table (thetascan_amd.gemm_solutions)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -491,11 +497,15 @@ def main() -> int:
     if args.workload != "headline":
         print(json.dumps(run_other(args.workload, args)), flush=True)
         return 0
+    from thetascan_amd import gemm_solutions
+
     dev = torch.device("cuda", 0)
     g = torch.Generator().manual_seed(1234)
     x = torch.randn(B, T, D_MODEL, generator=g).to(dev, torch.bfloat16)
     dy = (torch.randn(B, T, D_MODEL, generator=g) * 1e-2).to(dev, torch.bfloat16)
 
+    # the projection GEMMs replay the solutions measured for these shapes
+    measured = gemm_solutions.use_measured_gemms(not args.library_gemm_heuristics)
     module = seeded_module(headline_config("feature_rope"), 0).to(dev, torch.bfloat16)
     ms_eager = time_steps(module, x, dy, args.steps, args.warmup)
     assert module._core.last_path == "fused"
@@ -526,6 +536,9 @@ def main() -> int:
                                "unnormalized read",
                    "batch": B, "seq_len": T, "heads": H, "head_dim": D_HEAD, "d_model": D_MODEL,
                    "parallelism": "single GPU"},
+        "gemm_solutions": ("measured table (" + gemm_solutions.TABLE.name + ", "
+                           + str(len(gemm_solutions.read_table()[1])) + " shapes)") if measured
+        else "library heuristics",
     }
     traffic = load_traffic()
     passes = pass_profile(module, x, dy)
@@ -545,6 +558,8 @@ def main() -> int:
                                               "ms_per_step": round(ms_b_eager, 4)} if execution == "graph" else None,
                                     "roofline": roofline_of(passes_b, {}), "passes": passes_b},
         }
+    # the other workloads keep the libraries' own choice (their shapes are not in the table)
+    gemm_solutions.use_measured_gemms(False)
     if not args.no_workloads:
         out["workloads"] = other_workloads(args)
     if not args.no_cpu_baseline:

@@ -41,7 +41,7 @@ extern "C" {
  * 14: ts_read_out_fwd / ts_read_out_bwd / ts_read_out_bwd_parts (the read
  *     fused with the output projection), ts_kmap_*, ts_anchor_*,
  *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3,
- *     TS_GN_SILU and ts_gn_act_*; nothing earlier changed. */
+ *     TS_GN_SILU, ts_gn_act_* and ts_abs_mass_*; nothing earlier changed. */
 #define TS_ABI_VERSION 14
 
 enum ts_status {
@@ -807,6 +807,35 @@ int ts_wcumsum_workspace_bytes(const ts_wcumsum_desc* desc, size_t* bytes);
 
 int ts_wcumsum(const ts_wcumsum_desc* desc, ts_strided x, ts_strided out, const float* log_alpha,
                ts_strided decay, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Mass of absolute features: the normalizer num / (mass + eps) of a read whose
+ * features can be negative (a tanh GN fast network), so that |num| / mass <=
+ * max |value|:
+ *   mass_t = sum_j |q_tj| C_tj,   C_t = a_t C_{t-1} + |k_t|   (C_-1 = 0)
+ * for q, k [B,H,T,F] (ts_dtype `dtype`, F = 4, 8, 16, ... 256, rows aligned to
+ * four features) and the view's retention (as ts_wcumsum: none, static
+ * exp(log_alpha[h]) or exp(decay[b,h,t])); mass is fp32 [B,H,T] (element
+ * strides in ts_strided, the feature stride unused).  The backward forms
+ * dq = dmass sign(q) C and dk = sign(k) R, R the anti-causal decayed prefix of
+ * dmass |q| (either output may be NULL).  Neither stores the [B,H,T,F]
+ * prefix.  Replaces the composed path's absolute-feature key mass (a torch
+ * chain of abs, casts, a decayed prefix, product and row sum); the
+ * reference's features are nonnegative, so its unit column
+ * (engine.py:440-442) is this mass for them. */
+typedef struct ts_abs_mass_desc {
+  int32_t B, H, T, F;
+  int32_t dtype;        /* of q, k, dq, dk                                     */
+  int32_t retention;    /* ts_retention                                        */
+} ts_abs_mass_desc;
+
+int ts_abs_mass_workspace_bytes(const ts_abs_mass_desc* desc, size_t* bytes);
+
+int ts_abs_mass_fwd(const ts_abs_mass_desc* desc, ts_strided q, ts_strided k, const float* log_alpha,
+                    ts_strided decay, ts_strided mass, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+int ts_abs_mass_bwd(const ts_abs_mass_desc* desc, ts_strided q, ts_strided k, ts_strided dmass,
+                    const float* log_alpha, ts_strided decay, ts_strided dq, ts_strided dk, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
 
 /* out[i] = scale * (sum_{s<na} a[s*n + i] + sum_{s<nb} b[s*n + i]) for i < n,
  * written as ts_dtype out_dtype: sums the partial weight-gradient slots of

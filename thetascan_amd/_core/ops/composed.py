@@ -88,9 +88,13 @@ def key_mass(cfg, view, query, keys, unit_mass):
     that column, which can then cross zero; their mass is the one of the
     absolute features, |query| . (the view's decayed prefix of |keys|), in
     fp32 -- equal to the unit column for nonnegative features -- so that
-    |num| / mass <= max |value|."""
+    |num| / mass <= max |value| (one ts_abs_mass launch per direction where
+    the view allows it, else torch around the HIP prefix sum)."""
     if cfg.nonlin != "tanh":
         return unit_mass
+    mass = view.abs_mass(query, keys) if hasattr(view, "abs_mass") else None
+    if mass is not None:
+        return mass
     return (query.abs().float() * view.mass_cum(keys.abs().float())).sum(-1)
 
 

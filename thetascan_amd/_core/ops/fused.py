@@ -391,6 +391,102 @@ def wcumsum(x: torch.Tensor, retention=None, reverse: bool = False) -> torch.Ten
     return out
 
 
+def _retention_args(retention, B: int, H: int, T: int):
+    """(ts_retention, static log-retention [H] or None, per-token log-retention [B,H,T] or None)."""
+    if retention is None:
+        return _lib.RET_NONE, None, None
+    if retention.ndim == 4:
+        return _lib.RET_STREAM, None, retention.detach().to(torch.float32).reshape(B, H, T)
+    return _lib.RET_STATIC, retention.detach().to(torch.float32).reshape(H).contiguous(), None
+
+
+def abs_mass_eligible(q: torch.Tensor, k: torch.Tensor, retention=None) -> bool:
+    """Whether ts_abs_mass takes these features: the same dtype (bf16 / fp32)
+    on the GPU, F = 4, 8, ... 256, and a retention that needs no gradient."""
+    F = q.shape[-1]
+    return (q.is_cuda and q.ndim == 4 and k.shape == q.shape and q.dtype == k.dtype
+            and q.dtype in (torch.bfloat16, torch.float32) and F % 4 == 0 and (F // 4) & (F // 4 - 1) == 0
+            and F // 4 <= 64 and (retention is None or not retention.requires_grad))
+
+
+def _am_rows(t: torch.Tensor) -> torch.Tensor:
+    ok = t.stride(-1) == 1 and t.data_ptr() % (4 * t.element_size()) == 0 and all(s % 4 == 0 for s in t.stride()[:3])
+    return t if ok else t.contiguous()
+
+
+def _am_desc(q, retention):
+    B, H, T, F = q.shape
+    kind, la, dec = _retention_args(retention, B, H, T)
+    desc = _lib.AbsMassDesc(B, H, T, F, _lib.dtype_code(q.dtype), kind)
+    lib = _lib.load()
+    nbytes = ctypes.c_size_t()
+    _lib.check(lib.ts_abs_mass_workspace_bytes(ctypes.byref(desc), ctypes.byref(nbytes)), "ts_abs_mass_workspace_bytes")
+    work = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=q.device)
+    return lib, desc, la, dec, work, nbytes.value
+
+
+def _abs_mass_forward(q: torch.Tensor, k: torch.Tensor, retention: torch.Tensor | None) -> torch.Tensor:
+    q4, k4 = _am_rows(q), _am_rows(k)
+    B, H, T, F = q4.shape
+    lib, desc, la, dec, work, nb = _am_desc(q4, retention)
+    mass = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
+    with _lib.timed("ts_abs_mass_fwd", lambda: _lib.nbytes(q4, k4, mass)):
+        status = lib.ts_abs_mass_fwd(ctypes.byref(desc), _lib.strided(q4), _lib.strided(k4), _lib.ptr(la),
+                                     _lib.strided(dec), _lib.strided(mass), work.data_ptr(), nb,
+                                     _lib.stream_handle(q.device))
+    _lib.check(status, "ts_abs_mass_fwd")
+    return mass
+
+
+def _abs_mass_fake(q, k, retention):
+    return q.new_empty(q.shape[:3], dtype=torch.float32)
+
+
+def _abs_mass_backward_impl(dmass: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                            retention: torch.Tensor | None) -> list[torch.Tensor]:
+    q4, k4 = _am_rows(q), _am_rows(k)
+    lib, desc, la, dec, work, nb = _am_desc(q4, retention)
+    dm = dmass.to(torch.float32).contiguous()
+    dq = torch.empty(q4.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k4.shape, dtype=k.dtype, device=k.device)
+    with _lib.timed("ts_abs_mass_bwd", lambda: _lib.nbytes(q4, k4, dm, dm, q4, k4, dq, dk)):
+        status = lib.ts_abs_mass_bwd(ctypes.byref(desc), _lib.strided(q4), _lib.strided(k4), _lib.strided(dm),
+                                     _lib.ptr(la), _lib.strided(dec), _lib.strided(dq), _lib.strided(dk),
+                                     work.data_ptr(), nb, _lib.stream_handle(q.device))
+    _lib.check(status, "ts_abs_mass_bwd")
+    return [dq, dk]
+
+
+def _abs_mass_backward_fake(dmass, q, k, retention):
+    return [q.new_empty(q.shape), k.new_empty(k.shape)]
+
+
+def _abs_mass_setup(ctx, inputs, output):
+    q, k, retention = inputs
+    ctx.save_for_backward(q, k, retention)
+
+
+def _abs_mass_backward(ctx, dmass, bwd):
+    q, k, retention = ctx.saved_tensors
+    dq, dk = bwd(dmass, q, k, retention)
+    return dq, dk, None
+
+
+_abs_mass_op = HipOp("abs_mass", forward=_abs_mass_forward, forward_fake=_abs_mass_fake,
+                     backward_impl=_abs_mass_backward_impl, backward_fake=_abs_mass_backward_fake,
+                     setup=_abs_mass_setup, backward=_abs_mass_backward)
+
+
+def abs_mass(q: torch.Tensor, k: torch.Tensor, retention=None) -> torch.Tensor:
+    """mass_t = sum_j |q_tj| C_tj with C the decayed prefix of |k| along T
+    (``retention``: None, a static [H] or a per-token [B,H,T,1] log-retention;
+    it receives no gradient): fp32 [B,H,T], one ts_abs_mass_fwd call, and
+    ts_abs_mass_bwd for dq and dk."""
+    if not q.is_cuda:
+        raise RuntimeError("hip backend: tensors must live on the GPU (no CPU fallback)")
+    return _abs_mass_op(q, k, None if retention is None else retention.detach())
+
+
 def _stacked(w_qkv, w_g):
     """[W_qkv; W_g] (rebuilt every call: parameters may change in place in ways
     no version counter records, e.g. through ``.data``)."""

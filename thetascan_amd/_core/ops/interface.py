@@ -263,6 +263,21 @@ class Accumulator:
             return ema_cumsum(keys, self.static_log_alpha, self.chunk)
         return decayed_prefix(keys, decay)
 
+    def retention_m(self):
+        """The retention of this view's key prefix: None, static [H] or per-token [B,H,T,1]."""
+        if self.decay["m"] is None:
+            return None
+        return self.static_log_alpha if self.static_log_alpha is not None else self.decay["m"]
+
+    def abs_mass(self, query: torch.Tensor, keys: torch.Tensor):
+        """sum_j |query_j| (this view's decayed prefix of |keys|)_j in fp32 on
+        one HIP launch per direction, or None where that op does not apply
+        (continuation, a retention that takes a gradient, other widths)."""
+        ret = self.retention_m()
+        if stream.active() is not None or not fused.abs_mass_eligible(query, keys, ret):
+            return None
+        return fused.abs_mass(query, keys, ret)
+
     def scan_terms(self, key_kind: str):
         decay = self.decay[key_kind]
         if decay is None:
@@ -300,6 +315,12 @@ class FadeStale:
         k32 = keys.float()
         return (causal_prefix_sum(k32) - ema_cumsum(k32, self.log_alpha, self.chunk)).to(keys.dtype)
 
+    def abs_mass(self, query: torch.Tensor, keys: torch.Tensor):
+        if (stream.active() is not None or not fused.abs_mass_eligible(query, keys, None)
+                or not fused.abs_mass_eligible(query, keys, self.log_alpha)):
+            return None
+        return fused.abs_mass(query, keys, None) - fused.abs_mass(query, keys, self.log_alpha)
+
 
 class FadeFast:
     """Recency view (interface.py:282-307)."""
@@ -321,6 +342,11 @@ class FadeFast:
 
     def mass_cum(self, keys: torch.Tensor) -> torch.Tensor:
         return ema_cumsum(keys, self.log_alpha, self.chunk)
+
+    def abs_mass(self, query: torch.Tensor, keys: torch.Tensor):
+        if stream.active() is not None or not fused.abs_mass_eligible(query, keys, self.log_alpha):
+            return None
+        return fused.abs_mass(query, keys, self.log_alpha)
 
 
 class NullAccumulator:

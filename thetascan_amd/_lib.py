@@ -287,6 +287,10 @@ class BsplineDesc(ctypes.Structure):
     ]
 
 
+class AbsMassDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "F", "dtype", "retention")]
+
+
 class GnActDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "m", "dtype", "act", "has_tau")] + [
         ("eps", ctypes.c_float)]
@@ -552,6 +556,11 @@ def load() -> ctypes.CDLL:
         lib.ts_gn_write_bwd.argtypes = [P(GnDesc), P(GnBwdIO), ctypes.c_void_p]
         lib.ts_gn_read_fwd.argtypes = [P(GnReadDesc), P(GnReadIO), ctypes.c_void_p]
         lib.ts_gn_read_bwd.argtypes = [P(GnReadDesc), P(GnReadBwdIO), ctypes.c_void_p]
+        lib.ts_abs_mass_workspace_bytes.argtypes = [P(AbsMassDesc), P(ctypes.c_size_t)]
+        lib.ts_abs_mass_fwd.argtypes = [P(AbsMassDesc), Strided, Strided, ctypes.c_void_p, Strided, Strided,
+                                        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.ts_abs_mass_bwd.argtypes = [P(AbsMassDesc), Strided, Strided, Strided, ctypes.c_void_p, Strided, Strided,
+                                        Strided, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_gn_act_fwd.argtypes = [P(GnActDesc), Strided, Strided, ctypes.c_void_p, Strided, Strided, Strided,
                                       ctypes.c_void_p]
         lib.ts_gn_act_bwd.argtypes = [P(GnActDesc), Strided, Strided, ctypes.c_void_p] + [Strided] * 6 + [

@@ -8,8 +8,8 @@ that multiply W2 in its Jacobian payload and Gauss-Newton diagonal in torch
 golden mixer vectors); float64 autograd of them gives every gradient: da, db
 and the threshold's.  Every nonlinearity (relu2, silu, tanh and SwiGLU), with
 and without a threshold, bf16 and fp32, widths 16 to 256, ragged T.
-Tolerances: rel 1e-3 (fp32) and 2e-2 (bf16) on the values, twice that on the
-gradients; max-abs error over max-abs reference.
+Tolerances: rel 1e-3 (fp32) and 2e-2 (bf16) on the values and the gradients
+(measured at most 6.7e-7 and 3.7e-3); max-abs error over max-abs reference.
 """
 from __future__ import annotations
 
@@ -73,10 +73,10 @@ def test_gn_act_matches_the_oracle(cuda, dtype, tol, m, nonlin, has_tau):
     assert rel_err(sa.float(), sa_ref) < tol
     if glu:
         assert rel_err(sb.float(), sb_ref) < tol
-        assert rel_err(bd.grad.float(), rb_.grad) < 2 * tol
-    assert rel_err(ad.grad.float(), ra_.grad) < 2 * tol
+        assert rel_err(bd.grad.float(), rb_.grad) < tol
+    assert rel_err(ad.grad.float(), ra_.grad) < tol
     if has_tau:
-        assert rel_err(td.grad, rt_.grad) < 2 * tol
+        assert rel_err(td.grad, rt_.grad) < tol
 
 
 @pytest.mark.parametrize("nonlin", ["silu", "swiglu"])
@@ -100,9 +100,9 @@ def test_gn_act_features_only(cuda, nonlin):
     assert sa is None and sb is None
     h.backward(dh.float().to(cuda))
     assert rel_err(h, h_ref) < 1e-3
-    assert rel_err(ad.grad, ra_.grad) < 2e-3
+    assert rel_err(ad.grad, ra_.grad) < 1e-3
     if glu:
-        assert rel_err(bd.grad, rb_.grad) < 2e-3
+        assert rel_err(bd.grad, rb_.grad) < 1e-3
 
 
 def test_gn_act_rejects_bad_calls(cuda):

@@ -72,14 +72,17 @@ def test_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T, nonlin):
     h, lam, g = gn.write(x_, v_, w1_, w2_, tau_, nonlin=nonlin)
     torch.autograd.backward([h, lam, g], [dh.to(cuda, dtype), dl.to(cuda, dtype), dg.to(cuda, dtype)])
 
-    tol = 2e-3 if dtype == torch.float32 else 3e-2
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
     for name, a, e in (("h", h, h_ref), ("lam", lam, lam_ref), ("g", g, g_ref)):
-        assert rel_err(a, e) < tol, (name, d, m, learn_thresh)
-    gtol = 5e-3 if dtype == torch.float32 else 6e-2
+        assert rel_err(a, e) < tol, (name, d, m, learn_thresh, rel_err(a, e))
+    gtol = tol
     grads = [("dx", x_.grad, rk.grad), ("dv", v_.grad, rv.grad), ("dW1", w1_.grad, rw1.grad),
              ("dW2", w2_.grad, rw2.grad)]
     if learn_thresh:
         grads.append(("dtau", tau_.grad, rwg.grad[..., 0]))
+    errs = {name: rel_err(a, e) for name, a, e in grads}
+    print(f"errors gn write {nonlin} {dtype} d{d} m{m}: " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()),
+          flush=True)
     for name, a, e in grads:
         assert rel_err(a, e) < gtol, (name, d, m, learn_thresh, rel_err(a, e))
 
@@ -121,10 +124,12 @@ def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T,
     tau_ = dev(wg[..., 0].contiguous()) if learn_thresh else None
     h, resid = gn.read_stage(q_, w1_, w2_, tau_, want_resid=True, nonlin=nonlin)
     torch.autograd.backward([h, resid], [dh.to(cuda, dtype), dr.to(cuda, dtype)])
-    tol = 2e-3 if dtype == torch.float32 else 3e-2
-    assert rel_err(h, h_ref) < tol and rel_err(resid, resid_ref) < tol
-    gtol = 5e-3 if dtype == torch.float32 else 6e-2
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
     pairs = [("dq", q_.grad, rq.grad), ("dW1", w1_.grad, rw1.grad), ("dW2", w2_.grad, rw2.grad)]
+    print(f"errors gn read {nonlin} {dtype} d{d} m{m}: h {rel_err(h, h_ref):.2e} resid {rel_err(resid, resid_ref):.2e} "
+          + " ".join(f"{n} {rel_err(a, e):.2e}" for n, a, e in pairs), flush=True)
+    assert rel_err(h, h_ref) < tol and rel_err(resid, resid_ref) < tol
+    gtol = tol
     if learn_thresh:
         pairs.append(("dtau", tau_.grad, rwg.grad[..., 0]))
     for name, a, e in pairs:
@@ -136,8 +141,8 @@ def test_gn_read_stage_matches_block_forward(cuda, dtype, d, m, learn_thresh, T,
 def test_gn_read_stage_correction_gradients(cuda, corr, dtype, d, m):
     """Stage with the LA1 correction (plain, or divided by its mass): the HIP
     backward agrees with fp64 autograd of rmsnorm(W1 q + c) composed from the
-    oracle's rmsnorm, for q, num, mass, W1, W2 and tau (fp32 at rel 2e-3 / 5e-3;
-    the chunked bf16 widths at 3e-2 / 6e-2)."""
+    oracle's rmsnorm, for q, num, mass, W1, W2 and tau (fp32 at rel 1e-3, bf16
+    at 2e-2; measured at most 3.1e-6 and 5.1e-3)."""
     from thetascan_amd._core.ops import gn
 
     B, H, T = 2, 2, 75
@@ -162,12 +167,14 @@ def test_gn_read_stage_correction_gradients(cuda, corr, dtype, d, m):
     q_, w1_, w2_, tau_, num_, mass_ = dev
     h, resid = gn.read_stage(q_, w1_, w2_, tau_, num_, mass_ if corr == 2 else None, corr=corr, want_resid=True)
     torch.autograd.backward([h, resid], [dh.to(cuda, dtype), dr.to(cuda, dtype)])
-    tol, gtol = (2e-3, 5e-3) if dtype == torch.float32 else (3e-2, 6e-2)
-    assert rel_err(h, h_ref) < tol and rel_err(resid, resid_ref) < tol
+    tol = gtol = 1e-3 if dtype == torch.float32 else 2e-2
     pairs = [("dq", q_.grad, rq.grad), ("dW1", w1_.grad, rw1.grad), ("dW2", w2_.grad, rw2.grad),
              ("dtau", tau_.grad, rwg.grad[..., 0]), ("dnum", num_.grad, rnum.grad)]
     if corr == 2:
         pairs.append(("dmass", mass_.grad, rmass.grad))
+    print(f"errors gn read corr {corr} {dtype} d{d} m{m}: h {rel_err(h, h_ref):.2e} resid "
+          f"{rel_err(resid, resid_ref):.2e} " + " ".join(f"{n} {rel_err(a, e):.2e}" for n, a, e in pairs), flush=True)
+    assert rel_err(h, h_ref) < tol and rel_err(resid, resid_ref) < tol
     for name, a, e in pairs:
         assert rel_err(a, e) < gtol, (name, rel_err(a, e))
 

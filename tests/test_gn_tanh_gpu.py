@@ -10,7 +10,10 @@ tests/test_oracle_gn_extensions.py):
 * the write payloads h, s*lam, g and every gradient;
 * the read stages with tanh features, every correction kind;
 * the whole GN mixer (two-stage normalized read; plain sum, the ema stream
-  and a fast bank), fp32 at rel 1e-3 and bf16 at rel 2e-2.
+  and a fast bank), fp32 at rel 1e-3 and bf16 at rel 2e-2 on outputs, dx and
+  every parameter gradient, except the bf16 bank's blend gradient (eta) at
+  6e-2: it sums bf16 reads of every token (measured 4.1e-2 in bf16, 3e-6 in
+  fp32; every other bf16 figure at most 1.2e-2).
 """
 from __future__ import annotations
 
@@ -60,7 +63,7 @@ def test_tanh_gn_write_matches_oracle(cuda, dtype, d, m, learn_thresh, T):
     tol = 1e-3 if dtype == torch.float32 else 2e-2
     for name, a, e in (("h", h, h_ref), ("lam", lam, lam_ref), ("g", g, g_ref)):
         assert rel_err(a, e) < tol, (name, rel_err(a, e))
-    gtol = 2e-3 if dtype == torch.float32 else 4e-2
+    gtol = tol
     grads = [("dx", x_.grad, rk.grad), ("dv", v_.grad, rv.grad), ("dW1", w1_.grad, rw1.grad),
              ("dW2", w2_.grad, rw2.grad)]
     if learn_thresh:
@@ -110,7 +113,7 @@ def test_tanh_read_stage(cuda, corr):
     if corr == 2:
         pairs.append(("dmass", mass_.grad, rmass.grad))
     for name, a, e in pairs:
-        assert rel_err(a, e) < 2e-3, (name, rel_err(a, e))
+        assert rel_err(a, e) < 1e-3, (name, rel_err(a, e))
 
 
 def tanh_gn_module(cuda, d_model, heads, temporal="sum", dtype=torch.float32, seed=0):
@@ -155,8 +158,15 @@ def test_tanh_gn_mixer_matches_oracle(cuda, temporal, dtype):
     (y.float() * dy.to(cuda, torch.float32)).sum().backward()
     print(f"tanh gn mixer {temporal} {dtype}: path={module.last_path}", flush=True)
     tol = 1e-3 if dtype == torch.float32 else 2e-2
+    worst = max((rel_err(p.grad, params[n].grad), n) for n, p in module.named_parameters()
+                if params[n].grad is not None and params[n].grad.abs().max() > 0)
+    print(f"errors tanh gn {temporal} {dtype}: y {rel_err(y, y64):.2e} dx {rel_err(xd.grad, x64.grad):.2e} "
+          f"worst parameter gradient {worst[0]:.2e} ({worst[1]})", flush=True)
     assert rel_err(y, y64) < tol
-    assert rel_err(xd.grad, x64.grad) < 2 * tol
+    assert rel_err(xd.grad, x64.grad) < tol
     for name, p in module.named_parameters():
         if params[name].grad is not None and params[name].grad.abs().max() > 0:
-            assert rel_err(p.grad, params[name].grad) < 3 * tol, name
+            # the bank blend's eta gradient sums bf16 reads of every token: measured
+            # 4.1e-2 in bf16 (3e-6 in fp32), so it alone takes 3x the bf16 bar
+            bar = 3 * tol if name == "fade_eta" and dtype == torch.bfloat16 else tol
+            assert rel_err(p.grad, params[name].grad) < bar, name

@@ -7,7 +7,8 @@ oracle (oracle/mixer.py: rmsnorm, softmax_partition, relu2_ridge, restated
 from kernel_features.py:43-135 and pinned by the golden feature-map vectors).
 Forward and the gradients of a, tau, the score bias, the gain, rho and alpha;
 ragged T, feature widths 16 / 32 / 48 / 64, bf16 and fp32.  Tolerances: rel
-1e-3 (fp32), 2e-2 (bf16); max-abs error over max-abs reference.
+1e-3 (fp32), 2e-2 (bf16) on the map and every gradient (measured at most 2.6e-5
+and 3.7e-3); max-abs error over max-abs reference.
 """
 from __future__ import annotations
 
@@ -86,8 +87,8 @@ def test_kmap_matches_the_oracle(cuda, dtype, tol, m, case):
     torch.cuda.synchronize()
     assert phi.dtype == dtype
     assert rel_err(phi.float(), ref) < tol
-    assert rel_err(ad.grad.float(), a64.grad) < 2 * tol
+    assert rel_err(ad.grad.float(), a64.grad) < tol
     for name, leaf in ref_leaves.items():
         if leaf is None:
             continue
-        assert rel_err(dev[name].grad, leaf.grad) < 3 * tol, name
+        assert rel_err(dev[name].grad, leaf.grad) < tol, name

@@ -1,8 +1,10 @@
 """Mixer parity on the GPU (hip backend) against the reference.
 
 * Every golden case (written from the reference, float64) is loaded into the
-  MI355X module by state dict and run in fp32 on the GPU: outputs and every
-  parameter gradient must match the reference within rel 1e-3 (fp32 bar).
+  MI355X module by state dict and run in fp32 on the GPU: outputs, the input
+  gradient and every parameter gradient must match the reference within rel
+  1e-3 (fp32 bar; measured at most 2.3e-5, 2.8e-4 and 3.2e-4, all in the
+  sparse straight-through blend case).
 * The fused three-kernel path and the composed path agree with each other.
 * bf16 runs at benchmark-like widths match the float64 CPU oracle within rel
   2e-2 (the bf16 bar), forward and backward.
@@ -67,11 +69,14 @@ def test_mixer_matches_reference_golden(cuda, name):
         names = {r[0] for r in launches}
         assert names & {"ts_gn_write_fwd", "ts_gn_act_fwd"}, (name, sorted(names))
         assert names & {"ts_gn_write_bwd", "ts_gn_act_bwd"}, (name, sorted(names))
-    assert rel_err(x.grad, arr["grad:x"]) < 2e-3, name
     params = dict(module.named_parameters())
+    worst = max((rel_err(params[p].grad, g), p) for p, g in grads.items() if params[p].grad is not None)
+    print(f"errors {name}: y {rel_err(y, arr['y']):.2e} dx {rel_err(x.grad, arr['grad:x']):.2e} "
+          f"worst parameter gradient {worst[0]:.2e} ({worst[1]})", flush=True)
+    assert rel_err(x.grad, arr["grad:x"]) < 1e-3, name
     for pname, g in grads.items():
         assert params[pname].grad is not None, (name, pname)
-        assert rel_err(params[pname].grad, g) < 5e-3, (name, pname)
+        assert rel_err(params[pname].grad, g) < 1e-3, (name, pname)
 
 
 def _headline_config(placement: str, normalization: str, feature_map="relu2_ridge", d_model=512, heads=8,

@@ -77,7 +77,7 @@ def test_scan_at_T4096_matches_float64_oracle(cuda, dtype, kind):
     for a, b in zip(dev, leaves):
         assert rel_err(a.grad, b.grad) < tol
     if r_dev is not None:
-        assert rel_err(r_dev.grad, r64.grad) < (3e-2 if dtype == torch.bfloat16 else 2e-3)
+        assert rel_err(r_dev.grad, r64.grad) < tol
 
 
 # ------------------------------------------------------------------ headline mixer
@@ -160,11 +160,15 @@ def test_cpu_reference_workload_matches_oracle_fp32(cuda):
     y = module(xf)
     (y * dy.to(cuda, torch.float32)).sum().backward()
     print(f"cpu-reference workload path={module._core.last_path}", flush=True)
+    worst = max((rel_err(p.grad, grads64[n]), n) for n, p in module._core.named_parameters()
+                if n in grads64 and grads64[n].abs().max() > 0)
+    print(f"errors config 1 fp32: y {rel_err(y, y64):.2e} dx {rel_err(xf.grad, dx64):.2e} "
+          f"worst parameter gradient {worst[0]:.2e} ({worst[1]})", flush=True)
     assert rel_err(y, y64) < 1e-3
-    assert rel_err(xf.grad, dx64) < 2e-3
+    assert rel_err(xf.grad, dx64) < 1e-3
     for name, p in module._core.named_parameters():
         if name in grads64 and grads64[name].abs().max() > 0:
-            assert rel_err(p.grad, grads64[name]) < 5e-3, name
+            assert rel_err(p.grad, grads64[name]) < 1e-3, name
     # the memory after the last token, per view: N_T = sum_i w_i phi(k_i) v_i^T
     # and D_T = sum_i w_i phi(k_i) (plain sum, then the recency branch)
     with torch.no_grad():
@@ -219,17 +223,22 @@ def _bf16_against_oracle(cuda, pub, module, B, T, seed, tol=2e-2, monkeypatch=No
     y64, dx64, grads64 = _oracle_run(pub, module, x, dy)
     dx_tol = tol
     if monkeypatch is not None:
+        # for reference: the reference algorithm run in bf16 has an input-gradient
+        # error of its own (printed); the HIP path is held to the bf16 bar regardless
         floor = _dx_of_reference_in_bf16(pub, module, x, dy, dx64, monkeypatch)
-        print(f"dx bar: the reference algorithm in bf16 gives {floor:.4f}", flush=True)
-        dx_tol = max(tol, 1.25 * floor)
+        print(f"dx of the reference algorithm in bf16: {floor:.4f}", flush=True)
     xb = x.to(cuda, torch.bfloat16).requires_grad_(True)
     yb = module(xb)
     (yb.float() * dy.to(cuda, torch.float32)).sum().backward()
+    worst = max((rel_err(p.grad, grads64[n]), n) for n, p in module._core.named_parameters()
+                if n in grads64 and grads64[n].abs().max() > 0)
+    print(f"errors bf16: y {rel_err(yb, y64):.2e} dx {rel_err(xb.grad, dx64):.2e} (bar {dx_tol:.2e}) "
+          f"worst parameter gradient {worst[0]:.2e} ({worst[1]})", flush=True)
     assert rel_err(yb, y64) < tol
     assert rel_err(xb.grad, dx64) < dx_tol
     for name, p in module._core.named_parameters():
         if name in grads64 and grads64[name].abs().max() > 0:
-            assert rel_err(p.grad, grads64[name]) < 3 * tol / 2, name
+            assert rel_err(p.grad, grads64[name]) < tol, name
 
 
 @pytest.mark.parametrize("bank_mode,branches", [("fast", 2), ("stale", 1)])

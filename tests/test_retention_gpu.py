@@ -5,8 +5,8 @@ dL/dlog_alpha = sum_t sum_{i<=t} (t-i) alpha^(t-i) (q_t.k_i)(dO_t.v_i + dm_t):
 checked for ragged and tile-multiple T, one and several segments, key widths
 with a 16-wide tail block (16, 48, 80) and without, key widths that split
 (192 = 128 + 64), value widths up to eight 16-column blocks per call and
-wider ones that split (200), with and without the key-mass column, against the oracle at rel 2e-3 per head (bf16 inputs; the kernel's
-own operands are hi/lo bf16 pairs), and through the bank
+wider ones that split (200), with and without the key-mass column, against the oracle at rel 1e-3 per head (bf16 inputs; the kernel's
+own operands are hi/lo bf16 pairs; measured at most 5.1e-5), and through the bank
 mixer's backward at T=4096, where the former sum_t t (q.dq - k.dk) in bf16
 was 16% off.
 """
@@ -57,7 +57,7 @@ def test_retention_grad_matches_float64_autograd(cuda, T, dk, dv, mass, seg_tile
     print(f"retention grad T={T} dk={dk} dv={dv} mass={mass}: {got.tolist()} vs {want.tolist()}", flush=True)
     # every head on its own (the heads' gradients differ by orders of magnitude)
     for h in range(H):
-        assert rel_err(got[h], want[h]) < 2e-3, (h, got.tolist(), want.tolist())
+        assert rel_err(got[h], want[h]) < 1e-3, (h, got.tolist(), want.tolist())
 
 
 def test_bank_retention_gradient_at_T4096_in_bf16(cuda):
@@ -78,4 +78,4 @@ def test_bank_retention_gradient_at_T4096_in_bf16(cuda):
     sum((o.float() * dO.to(cuda, torch.float32)).sum() for o, dO in zip(outs, dOs)).backward()
     for r, want in zip(rets[1:], wants):
         for h in range(H):
-            assert rel_err(r.grad[h], want[h]) < 2e-3, (h, r.grad.tolist(), want.tolist())
+            assert rel_err(r.grad[h], want[h]) < 1e-3, (h, r.grad.tolist(), want.tolist())

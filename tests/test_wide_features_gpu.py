@@ -7,11 +7,13 @@ bf16 (the feature axis walked 64 features at a time).  Each mixer below runs
 them on the multi-view path and is checked against the float64 oracle, across
 both feature maps, input and feature RoPE, the learned ReLU^2 threshold,
 shared key/query, banks, the ema stream and the plain sum, with a ragged last
-tile.  ReLU^2 mixers take the bf16 bar (outputs and dx rel 2e-2, parameter
-gradients 3e-2).  The softmax partition at sharpness 8 multiplies the bf16
-rounding of its pre-activations by 8: on the same configurations the 64- and
-128-wide feature kernels reach 2.4-2.5 % in dx and the composed bf16 path
-5-7 %, so the softmax mixers take 3e-2 (outputs, dx) and 4e-2 (parameters).
+tile.  ReLU^2 mixers take the bf16 bar, rel 2e-2, on outputs, dx and every
+parameter gradient (measured at most 1.6e-2).  The softmax partition at
+sharpness 8 multiplies the bf16 rounding of its pre-activations by 8: on the
+same configurations the 64- and 128-wide feature kernels reach 2.4-2.5 % in dx
+and the composed bf16 path 5-7 %, so the softmax mixers take 3e-2 (outputs,
+dx) and 4e-2 (parameters); measured at most 2.9e-2 (m = 192) and 3.3e-2
+(m = 384).
 """
 from __future__ import annotations
 
@@ -76,7 +78,7 @@ def test_wide_feature_mixer_matches_float64_oracle(cuda, name):
     print(f"wide {name}: m={core['mem_hidden']} path={module._core.last_path}", flush=True)
     assert module._core.last_path == "fused"
     (yb.float() * dy.to(cuda, torch.float32)).sum().backward()
-    tol, ptol = (3e-2, 4e-2) if "softmax" in name else (2e-2, 3e-2)
+    tol, ptol = (3e-2, 4e-2) if "softmax" in name else (2e-2, 2e-2)
     assert rel_err(yb, y64) < tol
     assert rel_err(xb.grad, x64.grad) < tol
     for pname, p in module._core.named_parameters():

@@ -174,7 +174,7 @@ __device__ __forceinline__ void feature_map(const FeatP& p, float tau, const flo
 // tile; pitches are the tile width plus one 16-byte vector).
 struct FeatLayout {
   int xp, mp;                    // row pitches of d-wide and m-wide tiles
-  int xs, ps, rs, hs, os;        // tiles: x/xn(/resid), phi|dphi/da, dresid, h, dx
+  int xs, ps, rs, hs;            // tiles: x/xn(/resid), phi | dphi then da, dresid, h
   int w1, w1t, w2;               // weights: W1 [m][xp], W1^T [d][mp], W2 [d][mp] or W2^T [m][xp]
   int end;                       // total elements
 };
@@ -188,19 +188,18 @@ __host__ __device__ constexpr FeatLayout feat_layout(int esize, int d, int m, bo
   int off = 0;
   L.xs = off; off += TT * L.xp;
   L.ps = off; off += TT * L.mp;
-  L.rs = L.hs = L.os = -1;
-  if (!fwd) {
-    if (resid) { L.rs = off; off += TT * L.xp; }
-    if (wgrad && resid) { L.hs = off; off += TT * L.mp; }
-    L.os = off; off += TT * L.xp;
-  }
+  L.rs = L.hs = -1;
+  if (!fwd && resid) { L.rs = off; off += TT * L.xp; }
+  if (!fwd && resid && wgrad) { L.hs = off; off += TT * L.mp; }
   L.w1 = L.w1t = L.w2 = -1;
   if (w_lds) {
     L.w1 = off; off += m * L.xp;
     if (fwd) {
       if (resid) { L.w2 = off; off += d * L.mp; }
     } else {
-      L.w1t = off; off += d * L.mp;
+      // W1^T: transposing reads of the staged W1 where the feature blocks
+      // pair up into 32-wide MFMA steps (m a multiple of 32), else a copy
+      if ((m / 16) % 2) { L.w1t = off; off += d * L.mp; }
       if (resid) { L.w2 = off; off += m * L.xp; }
     }
   }
@@ -412,8 +411,9 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
   E* ps = base + L.ps;  // dphi, then da
   E* rs = base + L.rs;  // dresid
   E* hs = base + L.hs;  // h
-  E* os = base + L.os;  // dx
   float* red = (float*)(base + L.end);  // [4] wave partial sums
+  // W1^T operands: transposing reads of the staged W1 (pairs of feature blocks)
+  constexpr bool W1T_READ = WL && MB % 2 == 0;
 
   const E* w1 = (const E*)p.w1 + h * m * D;
   const E* w1t = (const E*)p.w1t + h * D * m;
@@ -421,8 +421,10 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
   int wpa = D, wpt = m;
   if constexpr (WL) {
     stage_matrix<E>(w1, m, D, base + L.w1, L.xp, tid);
-    if (p.w1t) stage_matrix<E>(w1t, D, m, base + L.w1t, L.mp, tid);
-    else stage_transposed<E>(w1, m, D, base + L.w1t, L.mp, tid);
+    if constexpr (!W1T_READ) {
+      if (p.w1t) stage_matrix<E>(w1t, D, m, base + L.w1t, L.mp, tid);
+      else stage_transposed<E>(w1, m, D, base + L.w1t, L.mp, tid);
+    }
     if (has_resid) {
       if (p.w2t) stage_matrix<E>(w2t, m, D, base + L.w2, L.xp, tid);
       else stage_transposed<E>((const E*)p.w2 + h * D * m, D, m, base + L.w2, L.xp, tid);
@@ -602,6 +604,7 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
 #pragma unroll
       for (int i = 0; i < 4; ++i) dh[fb][i] = c1 * dh[fb][i] - c3 * a[fb][i];
 
+
     if constexpr (WG) {
       // da over this lane's dphi entries; h for the dW2 contraction
       E* prow = ps + row * L.mp;
@@ -636,9 +639,19 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
       }
     }
 
-    // dxn^T = W1^T da^T  (W1^T given as [D x m])
+    // dxn^T = W1^T da^T  (W1^T as transposing reads of the staged W1, or given as [D x m])
     floatx4 dxn[D / 16];
-    gemm_back<E, D, MB>(w1t, wpt, dh, l16, g, nfb, dxn);
+    if constexpr (W1T_READ) {
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        dxn[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < MB / 2; ++j)
+          dxn[db] = mma32(TF::get(w1, wpa, db * 16, j, lane), IO::from_acc(dh[2 * j], dh[2 * j + 1]), dxn[db]);
+      }
+    } else {
+      gemm_back<E, D, MB>(w1t, wpt, dh, l16, g, nfb, dxn);
+    }
     // residual path, L2-norm backward (x / max(||x||, eps): the projection
     // term only where ||x|| > eps), input-RoPE backward at dims 16db+4g+i
     float dot = 0.f;
@@ -656,18 +669,18 @@ __global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 4 ? (RESID
     dot = sum_g(dot);  // every lane takes part in the cross-lane sum
     dot = big ? dot * inv * inv : 0.f;
     {
-      E* orow = os + row * L.xp;
+      // dx straight from registers: four consecutive dims per lane
+      E* dxrow = valid ? rows_of<E>(p.dx, b, h).at(t) : nullptr;
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (dxn[db][i] - xr[db][i] * dot) * inv;
         if (db * 16 < p.in_rot) rope.apply_in(p, v, db, t, valid, g, true);
-        st4f<E>(orow + db * 16 + 4 * g, v);
+        if (valid) st4f<E>(dxrow + db * 16 + 4 * g, v);
       }
     }
     __syncthreads();  // da, h, xn rows of all four waves complete (the contraction reads them all)
-    write_rows_wave<E>(os, L.xp, rows_of<E>(p.dx, b, h), t0, p.T, D, w, lane);
 
     if constexpr (WG) {
       // dW1[f][e] += sum_t da[t][f] xn[t][e];  dW2[e][f] += sum_t dresid[t][e] h[t][f]

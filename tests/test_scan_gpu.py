@@ -500,6 +500,74 @@ def test_scan_continues_from_a_carried_state(cuda, dtype, kind, mass):
     assert rel_err(state, S) < (1e-4 if dtype == torch.float32 else 1e-2), (kind, dtype)
 
 
+@pytest.mark.parametrize("mass", [False, True])
+@pytest.mark.parametrize("kind", ["none", "static", "stream"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("Dk,Dv", [(5, 4), (16, 16), (32, 64), (48, 40), (64, 64), (128, 128), (100, 24)])
+def test_short_continuations_walk_the_recurrence(cuda, dtype, kind, mass, Dk, Dv):
+    """Continuations of at most eight tokens (decode steps) take a
+    token-by-token launch over the register-resident state; a fresh sequence
+    that short, then pieces of 1..8 tokens after a long one, give the whole
+    sequence's scan and final state (S_t = a_t S_{t-1} + k_t v_t^T, with the
+    key-mass column D_t = a_t D_{t-1} + k_t when ``mass``)."""
+    from thetascan_amd._core.ops import scan_hip
+
+    B, H = 2, 3
+    cuts = [0, 3, 70, 71, 73, 76, 80, 85, 91, 98, 106, 107]
+    T = cuts[-1]
+    q, k, v = (_rounded(x, dtype) for x in _streams(B, H, T, Dk, Dv, seed=53 + Dk))
+    if mass:
+        q, k = q.abs(), k.abs()
+    ret = _retention(kind, B, H, T, seed=54)
+    outs, masses, state = [], [], None
+    for lo, hi in zip(cuts[:-1], cuts[1:]):
+        out, m, state = scan_hip.linattn_state(q[:, :, lo:hi].to(cuda, dtype), k[:, :, lo:hi].to(cuda, dtype),
+                                               v[:, :, lo:hi].to(cuda, dtype), _ret_for(kind, ret, lo, hi, cuda),
+                                               state, mass=mass)
+        assert out.dtype == dtype and out.shape == (B, H, hi - lo, Dv)
+        outs.append(out)
+        if mass:
+            masses.append(m)
+    unit = torch.cat([v, torch.ones_like(v[..., :1])], dim=-1) if mass else v
+    decay = _oracle_decay(ret, q)
+    expected = oracle.linattn_naive(q, k, unit, decay)
+    got = torch.cat(outs, dim=2)
+    errs = {"out": rel_err(got, expected[..., :Dv])}
+    if mass:
+        errs["mass"] = rel_err(torch.cat(masses, dim=2), expected[..., Dv])
+    w = torch.ones(B, H, T, dtype=torch.float64) if decay is None else \
+        torch.exp(decay[..., 0].flip(-1).cumsum(-1).flip(-1) - decay[..., 0])
+    S = torch.einsum("bht,bhtk,bhtv->bhkv", w, k, unit)
+    # widths round up to whole 16-byte vectors; the padding rows and columns stay zero
+    vec = 8 if dtype == torch.bfloat16 else 4
+    dkw, dvw = -(-Dk // vec) * vec, -(-Dv // vec) * vec
+    assert state.shape == (B, H, dkw, dvw + (1 if mass else 0))
+    cols = list(range(Dv)) + ([dvw] if mass else [])
+    kept = state[:, :, :Dk][..., cols]
+    rest = state.clone()
+    rest[:, :, :Dk, cols] = 0
+    assert not rest.any()
+    errs["state"] = rel_err(kept, S)
+    print(f"short continuations {Dk}x{Dv} {kind} {dtype} mass={mass}: {errs}", flush=True)
+    for name, e in errs.items():
+        assert e < (TOL[dtype] if name != "state" else (1e-4 if dtype == torch.float32 else 1e-2)), (name, e)
+
+
+def test_short_continuation_equals_the_tiled_path(cuda):
+    """A one-token step gives what the tiled passes give for the same token
+    appended to a tile-aligned prefix, to fp32 rounding."""
+    from thetascan_amd._core.ops import scan_hip
+
+    q, k, v = (x.float() for x in _streams(1, 4, 73, 64, 64, seed=55))
+    ret = -torch.rand(1, 4, 73, 1, generator=torch.Generator().manual_seed(56)) * 0.1
+    dev = [x.to(cuda) for x in (q, k, v, ret)]
+    whole, _, fin_whole = scan_hip.linattn_state(*dev)
+    _, _, st = scan_hip.linattn_state(*(x[:, :, :72] for x in dev))
+    step, _, fin_step = scan_hip.linattn_state(*(x[:, :, 72:] for x in dev), st)
+    assert rel_err(step, whole[:, :, 72:]) < 1e-5
+    assert rel_err(fin_step, fin_whole) < 1e-5
+
+
 @pytest.mark.parametrize("kind", ["none", "static", "stream"])
 def test_sequence_sharded_scan_equals_the_whole_scan(cuda, kind):
     """The sequence-sharding design on one GPU: P shards scan their slices

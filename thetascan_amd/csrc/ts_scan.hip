@@ -919,6 +919,102 @@ __device__ __forceinline__ int exact_index(const FinalP& F, int e) {
   return F.vx && f < F.dk ? f * cols + F.dv : -1;
 }
 
+// Short continuations (a decode step): T <= kStepMaxT tokens after a carried
+// state.  One workgroup per (b, h) walks the recurrence token by token,
+//   S_t = a_t S_{t-1} + k_t v_t^T,  out_t = S_t^T q_t,
+//   D_t = a_t D_{t-1} + k_t,        out_ext_t = <q_t, D_t>   (the ones column),
+// with the fp32 state in registers: thread (row group rg, column j) holds
+// S[rg * DKP/2 .. rg * DKP/2 + DKP/2)[j] and threads below dk hold D.  One
+// launch replaces the summary, prefix and main passes (and their workspace).
+constexpr int kStepMaxT = 8;
+
+struct StepP {
+  int H, T, dk, dv, vx, ret, out_f32, has_init;
+  float out_scale;
+  ts_strided q, k, v, decay, out, oe;
+  const float* log_alpha;
+  const float* init;  // [B*H][dk][dv + vx] fp32 (or null)
+  float* fin;         // same layout (or null)
+};
+
+template <typename E>
+__device__ __forceinline__ float step_ld(const ts_strided& s, int b, int h, int t, int c) {
+  return tof(*((const E*)s.ptr + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st + c));
+}
+
+template <typename E, int DKP>
+__global__ __launch_bounds__(256) void scan_step_kernel(StepP p) {
+  constexpr int RPT = DKP / 2;
+  __shared__ float sq[128], sk[128], sv[128], sd[128];
+  __shared__ float red[2][128];
+  const int tid = threadIdx.x, j = tid & 127, rg = tid >> 7, lane = tid & 63;
+  const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
+  const int cols = p.dv + p.vx;
+  const size_t state = (size_t)bh * p.dk * cols;
+  float S[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    S[r] = p.has_init && i < p.dk && j < p.dv ? p.init[state + (size_t)i * cols + j] : 0.f;
+  }
+  float D = p.vx && p.has_init && tid < p.dk ? p.init[state + (size_t)tid * cols + p.dv] : 0.f;
+  const float a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.f;
+  for (int t = 0; t < p.T; ++t) {
+    if (tid < p.dk) {
+      sq[tid] = step_ld<E>(p.q, b, h, t, tid);
+      sk[tid] = step_ld<E>(p.k, b, h, t, tid);
+    }
+    if (tid < p.dv) sv[tid] = step_ld<E>(p.v, b, h, t, tid);
+    const float a = p.ret == TS_RET_STREAM ? expf(step_ld<float>(p.decay, b, h, t, 0)) : a_static;
+    __syncthreads();
+    float part = 0.f;
+    if (j < p.dv) {
+      const float vj = sv[j];
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const int i = rg * RPT + r;
+        if (i < p.dk) {
+          S[r] = a * S[r] + sk[i] * vj;
+          part += sq[i] * S[r];
+        }
+      }
+    }
+    red[rg][j] = part;
+    if (tid < 128) {
+      float md = 0.f;
+      if (p.vx && tid < p.dk) {
+        D = a * D + sk[tid];
+        md = sq[tid] * D;
+      }
+      sd[tid] = md;
+    }
+    __syncthreads();
+    if (tid < p.dv) {
+      const float o = red[0][tid] + red[1][tid];
+      const int64_t off = (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + (int64_t)t * p.out.st + tid;
+      if (p.out_f32) ((float*)p.out.ptr)[off] = p.out_scale * o;
+      else ((E*)p.out.ptr)[off] = cvt<E>(o);
+    }
+    if (p.vx && p.oe.ptr && tid < 64) {
+      float m = sd[lane] + sd[lane + 64];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) m += __shfl_xor(m, o, 64);
+      if (lane == 0)
+        ((float*)p.oe.ptr)[(int64_t)b * p.oe.sb + (int64_t)h * p.oe.sh + (int64_t)t * p.oe.st] =
+            p.out_f32 ? p.out_scale * m : m;
+    }
+    __syncthreads();  // the token's rows and sums are read before the next token's replace them
+  }
+  if (p.fin) {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int i = rg * RPT + r;
+      if (i < p.dk && j < p.dv) p.fin[state + (size_t)i * cols + j] = S[r];
+    }
+    if (p.vx && tid < p.dk) p.fin[state + (size_t)tid * cols + p.dv] = D;
+  }
+}
+
 // Four consecutive elements per thread (nelem is a multiple of 16).
 __global__ void scan_prefix_kernel(float* seg, const float* segdec, FinalP F, int nseg, int nsum, int nelem) {
   const int bh = blockIdx.y;
@@ -1406,6 +1502,35 @@ static int scan_fwd_impl(const ts_scan_desc* d, const ts_scan_io* io, void* work
   }
 
   const int bh = d->B * d->H;
+  // a short continuation of a carried state: one token-by-token launch
+  if (d->T <= ts::kStepMaxT && (d->init_state || d->want_final) && !d->reverse && !L.kx &&
+      (d->v_ext == TS_EXT_NONE || d->v_ext == TS_EXT_ONES) &&
+      (d->out_mode == TS_OUT_STORE || d->out_mode == TS_OUT_STORE_F32) && d->value_split == 0 &&
+      d->states_in == 0 && L.dkp <= 128 && d->dv <= 128) {
+    ts::StepP sp;
+    memset(&sp, 0, sizeof(sp));
+    sp.H = d->H; sp.T = d->T; sp.dk = d->dk; sp.dv = d->dv; sp.vx = L.vx ? 1 : 0; sp.ret = d->retention;
+    sp.out_f32 = d->out_mode == TS_OUT_STORE ? 0 : 1; sp.has_init = d->init_state ? 1 : 0;
+    sp.out_scale = d->out_scale;
+    sp.q = io->q; sp.k = io->k; sp.v = io->v; sp.decay = io->decay; sp.out = io->out; sp.oe = io->out_ext;
+    sp.log_alpha = io->log_alpha;
+    sp.init = d->init_state ? io->init_state : nullptr;
+    sp.fin = d->want_final ? io->final_state : nullptr;
+    const bool bf = d->dtype == TS_BF16;
+#define TS_STEP_CASE(DK)                                                                               \
+  if (bf) hipLaunchKernelGGL((ts::scan_step_kernel<ts::bf16, DK>), dim3(bh), dim3(256), 0, stream, sp); \
+  else hipLaunchKernelGGL((ts::scan_step_kernel<float, DK>), dim3(bh), dim3(256), 0, stream, sp);
+    switch (L.dkp) {
+      case 16: { TS_STEP_CASE(16) } break;
+      case 32: { TS_STEP_CASE(32) } break;
+      case 64: { TS_STEP_CASE(64) } break;
+      default: { TS_STEP_CASE(128) } break;
+    }
+#undef TS_STEP_CASE
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(TS_ERR_RUNTIME, "scan: step launch failed: %s", hipGetErrorString(e));
+    return TS_OK;
+  }
   int mode = ts::kGeneral;
   if (d->retention != TS_RET_STREAM) {
     mode = (d->retention == TS_RET_STATIC ? ts::kStatic : 0) | (L.kx ? ts::kKeyExt : 0) | (L.vx ? ts::kValExt : 0) |

@@ -27,6 +27,8 @@ Extra objects on the JSON line:
   scan_mfma     -- the scan's tile contractions against the dense bf16 MFMA peak
   cpu_baseline  -- the CPU oracle's prefix-sum (``cumsum``) mixer, fp32,
                    fwd+bwd on a bounded sample, on this host's cores
+  decode        -- one-token decode latency of the headline mixer after its
+                   4096-token prompt (B8), eager and as HIP-graph replays
 """
 from __future__ import annotations
 
@@ -476,6 +478,7 @@ def main() -> int:
     ap.add_argument("--no-variant", action="store_true", help="skip the key-mass variant")
     ap.add_argument("--no-workloads", action="store_true",
                     help="skip the configurations 3, 4 and 5 lines of the default run")
+    ap.add_argument("--no-decode", action="store_true", help="skip the one-token decode latency")
     ap.add_argument("--steps-only", action="store_true", help="time the steps only (for profilers)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (reference for PMC byte counters)")
@@ -562,10 +565,56 @@ def main() -> int:
     gemm_solutions.use_measured_gemms(False)
     if not args.no_workloads:
         out["workloads"] = other_workloads(args)
+    if not args.no_decode:
+        out["decode"] = decode_latency(x)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
     return 0
+
+
+def decode_latency(x, steps: int = 200, warmup: int = 20) -> dict:
+    """One-token decode of the headline mixer (feature RoPE, bf16) for the B
+    sequences of ``x`` after their T-token prompt: the prompt is run into the
+    streaming state once (``prefill_ms``), then each step feeds one token per
+    sequence -- eagerly (``mixer(x_t, state=s)``) and as replays of the
+    captured step (thetascan_amd.DecodeGraph).  Latency is the wall time per
+    step over ``steps`` steps after ``warmup``, with a device synchronisation
+    on both sides; ``tokens_per_s`` counts B tokens per graph step."""
+    import torch
+    from thetascan_amd import DecodeGraph
+
+    module = seeded_module(headline_config("feature_rope"), 0).to(x.device, torch.bfloat16)
+    tok = x[:, -1:].contiguous()
+    with torch.no_grad():
+        module(x, state=module.initial_state())
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _, state = module(x, state=module.initial_state())
+        torch.cuda.synchronize()
+        prefill_ms = (time.perf_counter() - t0) * 1e3
+        s = state
+        for _ in range(warmup):
+            _, s = module(tok, state=s)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            _, s = module(tok, state=s)
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t0) / steps * 1e6
+        dec = DecodeGraph(module, state)
+        for _ in range(warmup):
+            dec.step(tok)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dec.step(tok)
+        torch.cuda.synchronize()
+        graph_us = (time.perf_counter() - t0) / steps * 1e6
+    return {"batch": x.shape[0], "prompt_tokens": x.shape[1], "prefill_ms": round(prefill_ms, 3),
+            "steps": steps, "eager_us_per_step": round(eager_us, 1), "graph_us_per_step": round(graph_us, 1),
+            "tokens_per_s": round(x.shape[0] / (graph_us * 1e-6), 1),
+            "state_bytes": state.nbytes}
 
 
 def other_workloads(args) -> dict:

@@ -442,9 +442,20 @@ class ThetaScan(nn.Module):
                                   self.ogate.g.lin.bias if gate else None, W1, W2, self.kernel_relu2_threshold,
                                   self.proj_out.weight, spec, cfg.read_norm, H)
 
+    def _fingerprint(self) -> str:
+        """config_fingerprint(self.cfg), recomputed only when a field changes
+        (the configuration's fields are flat values: a shallow snapshot sees
+        every change)."""
+        snap = tuple(self.cfg.__dict__.items())
+        memo = self.__dict__.get("_fingerprint_memo")
+        if memo is None or memo[0] is not self.cfg or memo[1] != snap:
+            memo = (self.cfg, snap, config_fingerprint(self.cfg))
+            self.__dict__["_fingerprint_memo"] = memo
+        return memo[2]
+
     def initial_state(self) -> ThetaScanState:
         """The state of a sequence with no tokens yet (streaming continuation)."""
-        return ThetaScanState(fingerprint=config_fingerprint(self.cfg))
+        return ThetaScanState(fingerprint=self._fingerprint())
 
     def forward(self, x: torch.Tensor, state: ThetaScanState | None = None):
         """``y`` for ``x`` [B,T,D]; with ``state``, the sequence continues from
@@ -468,7 +479,7 @@ class ThetaScan(nn.Module):
         """One call of a continued sequence: every scan and decayed prefix of
         the forward starts from the state the previous call left (the
         one-call sum path keeps no state, so the multi-view path serves it)."""
-        if state.fingerprint != config_fingerprint(self.cfg):
+        if state.fingerprint != self._fingerprint():
             raise ValueError("this state belongs to a mixer of another configuration")
         B = x.shape[0]
         if state.carries and state.batch != B:

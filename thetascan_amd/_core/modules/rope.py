@@ -11,10 +11,16 @@ from functools import lru_cache
 import torch
 
 
-def _tables(T: int, rot_dim: int, base: float, device, dtype: torch.dtype, start: int = 0):
+def _tables(T: int, rot_dim: int, base: float, device, dtype: torch.dtype, start=0):
+    """cos/sin [T, rot_dim/2] of positions start .. start+T-1; ``start`` may
+    be an int64 device tensor (a captured decode step)."""
     phase_dtype = torch.float64 if dtype == torch.float64 else torch.float32
     inv = 1.0 / (base ** (torch.arange(0, rot_dim, 2, device=device, dtype=phase_dtype) / rot_dim))
-    f = torch.outer(torch.arange(start, start + T, device=device, dtype=phase_dtype), inv)
+    if isinstance(start, torch.Tensor):
+        pos = (start + torch.arange(T, device=device, dtype=torch.int64)).to(phase_dtype)
+    else:
+        pos = torch.arange(start, start + T, device=device, dtype=phase_dtype)
+    f = torch.outer(pos, inv)
     return f.cos().to(dtype=dtype), f.sin().to(dtype=dtype)
 
 
@@ -24,18 +30,41 @@ def _rope_cache_cached(T: int, rot_dim: int, base: float, device_type: str, devi
     return _tables(T, rot_dim, base, device, dtype)
 
 
+POSITION_BLOCK = 1024
+
+
+@lru_cache(maxsize=32)
+def _rope_block_cached(start: int, rot_dim: int, base: float, device_type: str, device_index, dtype: torch.dtype):
+    device = torch.device(device_type) if device_index is None else torch.device(device_type, device_index)
+    return _tables(POSITION_BLOCK, rot_dim, base, device, dtype, start)
+
+
 def rope_cache(T: int, rot_dim: int, base: float, device, dtype):
     """cos/sin of the current call's positions: 0 .. T-1, or, while a
     sequence is continued across calls, from the number of tokens seen."""
     from ..ops import stream
 
+    dev_pos = stream.device_position()
+    if dev_pos is not None:
+        # a captured decode step: rows formed on the device once per call
+        memo = stream.active().memo
+        key = ("rope", T, rot_dim, float(base), str(device), dtype)
+        if key not in memo:
+            memo[key] = _tables(T, rot_dim, base, torch.device(device), dtype, dev_pos)
+        return memo[key]
     start = stream.position()
-    if start:
-        return _tables(T, rot_dim, base, torch.device(device), dtype, start)
     resolved = torch.device(device)
     index = resolved.index
     if resolved.type == "cuda" and index is None:
         index = torch.cuda.current_device()
+    if start:
+        # rows of a cached block of positions (bit-equal to forming them
+        # directly while positions are exact fp32 integers, below 2^24)
+        b0 = start - start % POSITION_BLOCK
+        if start + T > b0 + POSITION_BLOCK or b0 + POSITION_BLOCK > 1 << 24:
+            return _tables(T, rot_dim, base, resolved, dtype, start)
+        cos, sin = _rope_block_cached(b0, rot_dim, float(base), resolved.type, index, dtype)
+        return cos[start - b0:start - b0 + T], sin[start - b0:start - b0 + T]
     return _rope_cache_cached(T, rot_dim, float(base), resolved.type, index, dtype)
 
 

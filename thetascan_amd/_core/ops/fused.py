@@ -29,23 +29,57 @@ from . import scan_hip, stream
 from .linear import slot_sum, split_k_outer, weight_grad
 
 
-def _rope_tables(T: int, rot: int, base: float, device, start: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+_INV: dict = {}
+
+
+def _rope_tables(T: int, rot: int, base: float, device, start=0) -> tuple[torch.Tensor, torch.Tensor]:
     """fp32 cos/sin [T, rot/2] of positions start .. start+T-1 (rope.py:7-38
-    phases, kept in fp32)."""
-    inv = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
-    f = torch.outer(torch.arange(start, start + T, device=device, dtype=torch.float32), inv)
+    phases, kept in fp32).  ``start`` may be an int64 device tensor (a
+    captured decode step): the positions are the same exact fp32 integers."""
+    if isinstance(start, torch.Tensor):
+        # kept for the life of the process: a captured step reads it in place
+        key = (rot, float(base), str(device))
+        inv = _INV.get(key)
+        if inv is None:
+            inv = _INV[key] = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
+        pos = (start + torch.arange(T, device=device, dtype=torch.int64)).to(torch.float32)
+    else:
+        inv = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
+        pos = torch.arange(start, start + T, device=device, dtype=torch.float32)
+    f = torch.outer(pos, inv)
     return f.cos().contiguous(), f.sin().contiguous()
 
 
 _TABLES: dict = {}
+# Continued sequences (decode steps) read their rows from tables of whole
+# blocks of positions; rows of a block equal the directly formed ones bit for
+# bit while positions are exact fp32 integers (below 2^24).
+POSITION_BLOCK = 1024
 
 
 def rope_tables(T: int, rot: int, base: float, device) -> tuple[torch.Tensor, torch.Tensor]:
     """The tables of the current call's positions: 0 .. T-1, or, while a
     sequence is continued, from the number of tokens already seen."""
+    dev_pos = stream.device_position()
+    if dev_pos is not None:
+        # a captured decode step: rows formed on the device once per call
+        memo = stream.active().memo
+        key = ("rope", T, rot, float(base), str(device))
+        if key not in memo:
+            memo[key] = _rope_tables(T, rot, base, device, dev_pos)
+        return memo[key]
     start = stream.position()
     if start:
-        return _rope_tables(T, rot, base, device, start)
+        b0 = start - start % POSITION_BLOCK
+        if start + T > b0 + POSITION_BLOCK or b0 + POSITION_BLOCK > 1 << 24:
+            return _rope_tables(T, rot, base, device, start)
+        key = ("block", b0, rot, float(base), str(device))
+        hit = _TABLES.get(key)
+        if hit is None:
+            if len(_TABLES) > 64:
+                _TABLES.clear()
+            hit = _TABLES[key] = _rope_tables(POSITION_BLOCK, rot, base, device, b0)
+        return hit[0][start - b0:start - b0 + T], hit[1][start - b0:start - b0 + T]
     key = (T, rot, float(base), str(device))
     hit = _TABLES.get(key)
     if hit is None:

@@ -262,7 +262,11 @@ def _scan_once(
         ext_out = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
     final = None
     if want_final:
-        final = torch.zeros(B * H, dk_pad, dv_pad, dtype=torch.float32, device=q.device)
+        # every entry of the [dk(+1)][dv(+1)] layout is written except the
+        # corner of a key ext row meeting a value ext column
+        corner = qe_mode != _lib.EXT_NONE and ke_mode != _lib.EXT_NONE and ve_mode != _lib.EXT_NONE
+        final = (torch.zeros if corner else torch.empty)(B * H, dk_pad, dv_pad, dtype=torch.float32,
+                                                          device=q.device)
     init = None
     if init_state is not None:
         if tuple(init_state.shape[-2:]) != (dk_pad, dv_pad) or init_state.numel() != B * H * dk_pad * dv_pad:

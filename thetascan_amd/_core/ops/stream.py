@@ -29,6 +29,7 @@ class Carry:
         self.inp = list(carries)
         self.out: list = []
         self.position = int(position)
+        self.memo: dict = {}  # per-call values shared by the call's scans (RoPE rows)
 
     def take(self):
         """The state the next scan or prefix starts from (None: zero)."""
@@ -51,6 +52,28 @@ def position() -> int:
     """Absolute position of the current call's first token (0 outside a carry)."""
     carry = active()
     return 0 if carry is None else carry.position
+
+
+_DEVICE_POSITION: contextvars.ContextVar = contextvars.ContextVar("thetascan_device_position", default=None)
+
+
+def device_position() -> torch.Tensor | None:
+    """The int64 device tensor holding the position of the current call's
+    first token while a captured decode step is recorded (None otherwise):
+    RoPE phases are then formed on the device from it, so one recorded step
+    serves every position."""
+    if active() is None:
+        return None
+    return _DEVICE_POSITION.get()
+
+
+@contextlib.contextmanager
+def positions_on_device(pos: torch.Tensor):
+    token = _DEVICE_POSITION.set(pos)
+    try:
+        yield pos
+    finally:
+        _DEVICE_POSITION.reset(token)
 
 
 @contextlib.contextmanager

@@ -945,12 +945,27 @@ __device__ __forceinline__ float step_ld(const ts_strided& s, int b, int h, int 
 template <typename E, int DKP>
 __global__ __launch_bounds__(256) void scan_step_kernel(StepP p) {
   constexpr int RPT = DKP / 2;
-  __shared__ float sq[128], sk[128], sv[128], sd[128];
-  __shared__ float red[2][128];
+  // every token's rows are staged up front, so the state loads and the
+  // token loads are in flight together; the per-token sums alternate
+  // between two buffers (one barrier per token)
+  __shared__ float sq[kStepMaxT][128], sk[kStepMaxT][128], sv[kStepMaxT][128];
+  __shared__ float sa[kStepMaxT];
+  __shared__ float red[2][2][128], sd[2][128];
   const int tid = threadIdx.x, j = tid & 127, rg = tid >> 7, lane = tid & 63;
   const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
   const int cols = p.dv + p.vx;
   const size_t state = (size_t)bh * p.dk * cols;
+  for (int e = tid; e < p.T * 128; e += 256) {
+    const int t = e >> 7, c = e & 127;
+    if (c < p.dk) {
+      sq[t][c] = step_ld<E>(p.q, b, h, t, c);
+      sk[t][c] = step_ld<E>(p.k, b, h, t, c);
+    }
+    if (c < p.dv) sv[t][c] = step_ld<E>(p.v, b, h, t, c);
+  }
+  if (tid < p.T)
+    sa[tid] = p.ret == TS_RET_STREAM ? expf(step_ld<float>(p.decay, b, h, tid, 0))
+                                     : (p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.f);
   float S[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
@@ -958,52 +973,48 @@ __global__ __launch_bounds__(256) void scan_step_kernel(StepP p) {
     S[r] = p.has_init && i < p.dk && j < p.dv ? p.init[state + (size_t)i * cols + j] : 0.f;
   }
   float D = p.vx && p.has_init && tid < p.dk ? p.init[state + (size_t)tid * cols + p.dv] : 0.f;
-  const float a_static = p.ret == TS_RET_STATIC ? expf(p.log_alpha[h]) : 1.f;
+  __syncthreads();
   for (int t = 0; t < p.T; ++t) {
-    if (tid < p.dk) {
-      sq[tid] = step_ld<E>(p.q, b, h, t, tid);
-      sk[tid] = step_ld<E>(p.k, b, h, t, tid);
-    }
-    if (tid < p.dv) sv[tid] = step_ld<E>(p.v, b, h, t, tid);
-    const float a = p.ret == TS_RET_STREAM ? expf(step_ld<float>(p.decay, b, h, t, 0)) : a_static;
-    __syncthreads();
+    const int buf = t & 1;
+    const float a = sa[t];
     float part = 0.f;
     if (j < p.dv) {
-      const float vj = sv[j];
+      const float vj = sv[t][j];
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
         const int i = rg * RPT + r;
         if (i < p.dk) {
-          S[r] = a * S[r] + sk[i] * vj;
-          part += sq[i] * S[r];
+          S[r] = a * S[r] + sk[t][i] * vj;
+          part += sq[t][i] * S[r];
         }
       }
     }
-    red[rg][j] = part;
+    red[buf][rg][j] = part;
     if (tid < 128) {
       float md = 0.f;
       if (p.vx && tid < p.dk) {
-        D = a * D + sk[tid];
-        md = sq[tid] * D;
+        D = a * D + sk[t][tid];
+        md = sq[t][tid] * D;
       }
-      sd[tid] = md;
+      sd[buf][tid] = md;
     }
+    // a slow thread still reading buffer `buf` of token t has passed this
+    // barrier before any thread writes it again (token t + 2)
     __syncthreads();
     if (tid < p.dv) {
-      const float o = red[0][tid] + red[1][tid];
+      const float o = red[buf][0][tid] + red[buf][1][tid];
       const int64_t off = (int64_t)b * p.out.sb + (int64_t)h * p.out.sh + (int64_t)t * p.out.st + tid;
       if (p.out_f32) ((float*)p.out.ptr)[off] = p.out_scale * o;
       else ((E*)p.out.ptr)[off] = cvt<E>(o);
     }
-    if (p.vx && p.oe.ptr && tid < 64) {
-      float m = sd[lane] + sd[lane + 64];
+    if (p.vx && p.oe.ptr && tid >= 128 && tid < 192) {
+      float m = sd[buf][lane] + sd[buf][lane + 64];
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) m += __shfl_xor(m, o, 64);
       if (lane == 0)
         ((float*)p.oe.ptr)[(int64_t)b * p.oe.sb + (int64_t)h * p.oe.sh + (int64_t)t * p.oe.st] =
             p.out_f32 ? p.out_scale * m : m;
     }
-    __syncthreads();  // the token's rows and sums are read before the next token's replace them
   }
   if (p.fin) {
 #pragma unroll

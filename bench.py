@@ -11,7 +11,10 @@ synthetic: x ~ N(0,1), upstream gradient ~ N(0, (1e-2)^2), weights seeded
 
 One step = forward + backward of the whole mixer (projections included).
 The timed region brackets exactly ``--steps`` steps with a device
-synchronisation on both sides, inputs already resident in HBM.  The
+synchronisation on both sides, inputs already resident in HBM; Python's
+cyclic garbage collector is paused over it (after a full collection), so a
+collection of the interpreter's heap -- tens of milliseconds of host time --
+cannot land in a timed step.  The
 projection GEMMs run the library solutions measured for these shapes
 (thetascan_amd.gemm_solutions; ``--library-gemm-heuristics`` times the
 libraries' own choice instead); ``gemm_solutions`` on the line says which.
@@ -33,6 +36,8 @@ Extra objects on the JSON line:
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import statistics
@@ -84,6 +89,26 @@ def seeded_module(config, seed: int):
     return module
 
 
+@contextlib.contextmanager
+def paused_gc():
+    """Python's cyclic garbage collector paused over a timed region, after one
+    full collection whose survivors are frozen out of later ones.  A full
+    collection walks the interpreter's whole heap (about 65 ms of host time in
+    these processes); left running it lands in a random timed step and adds
+    its length to that step (the GPU idles behind the host meanwhile), which
+    is host noise, not the workload."""
+    was = gc.isenabled()
+    gc.collect()
+    gc.freeze()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+        gc.unfreeze()
+
+
 def time_steps(module, x, dy, steps: int, warmup: int, graphed=None, train: bool = True):
     """Mean ms per fwd+bwd step over exactly ``steps`` steps after ``warmup``.
 
@@ -107,11 +132,12 @@ def time_steps(module, x, dy, steps: int, warmup: int, graphed=None, train: bool
         step()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        step()
-    stop.record()
-    torch.cuda.synchronize()
+    with paused_gc():
+        start.record()
+        for _ in range(steps):
+            step()
+        stop.record()
+        torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
 
 
@@ -174,7 +200,7 @@ def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
     torch.cuda.synchronize()
     cycles_per_s = probe_cycles / max(a.elapsed_time(b) * 1e-3, 1e-6)
     sleep_cycles = int(cycles_per_s * (2.0 * host_s + 1e-3))
-    with _lib.record_launches() as recs:
+    with _lib.record_launches() as recs, paused_gc():
         for _ in range(steps):
             torch.cuda._sleep(sleep_cycles)
             step()
@@ -399,11 +425,12 @@ def run_lm(args) -> dict:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    with paused_gc():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / args.steps * 1e3
     model.eval()
     with torch.no_grad():
         base = float(model(x[:8], y[:8]))
@@ -597,20 +624,22 @@ def decode_latency(x, steps: int = 200, warmup: int = 20) -> dict:
         for _ in range(warmup):
             _, s = module(tok, state=s)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            _, s = module(tok, state=s)
-        torch.cuda.synchronize()
-        eager_us = (time.perf_counter() - t0) / steps * 1e6
+        with paused_gc():
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                _, s = module(tok, state=s)
+            torch.cuda.synchronize()
+            eager_us = (time.perf_counter() - t0) / steps * 1e6
         dec = DecodeGraph(module, state)
         for _ in range(warmup):
             dec.step(tok)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            dec.step(tok)
-        torch.cuda.synchronize()
-        graph_us = (time.perf_counter() - t0) / steps * 1e6
+        with paused_gc():
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                dec.step(tok)
+            torch.cuda.synchronize()
+            graph_us = (time.perf_counter() - t0) / steps * 1e6
     return {"batch": x.shape[0], "prompt_tokens": x.shape[1], "prefill_ms": round(prefill_ms, 3),
             "steps": steps, "eager_us_per_step": round(eager_us, 1), "graph_us_per_step": round(graph_us, 1),
             "tokens_per_s": round(x.shape[0] / (graph_us * 1e-6), 1),

@@ -12,9 +12,10 @@ synthetic: x ~ N(0,1), upstream gradient ~ N(0, (1e-2)^2), weights seeded
 One step = forward + backward of the whole mixer (projections included).
 The timed region brackets exactly ``--steps`` steps with a device
 synchronisation on both sides, inputs already resident in HBM; Python's
-cyclic garbage collector is paused over it (after a full collection), so a
-collection of the interpreter's heap -- tens of milliseconds of host time --
-cannot land in a timed step.  The
+cyclic garbage collector is paused over the warmup and the timed steps
+(after a full collection before the warmup), so a collection of the
+interpreter's heap -- tens of milliseconds of host time -- cannot land in a
+timed step.  The
 projection GEMMs run the library solutions measured for these shapes
 (thetascan_amd.gemm_solutions; ``--library-gemm-heuristics`` times the
 libraries' own choice instead); ``gemm_solutions`` on the line says which.
@@ -91,12 +92,14 @@ def seeded_module(config, seed: int):
 
 @contextlib.contextmanager
 def paused_gc():
-    """Python's cyclic garbage collector paused over a timed region, after one
-    full collection whose survivors are frozen out of later ones.  A full
-    collection walks the interpreter's whole heap (about 65 ms of host time in
-    these processes); left running it lands in a random timed step and adds
-    its length to that step (the GPU idles behind the host meanwhile), which
-    is host noise, not the workload."""
+    """Python's cyclic garbage collector paused over a warmup and the timed
+    steps after it, after one full collection whose survivors are frozen out
+    of later ones.  A full collection walks the interpreter's whole heap
+    (about 65 ms of host time in these processes); left running it lands in a
+    random timed step and adds its length to that step (the GPU idles behind
+    the host meanwhile), which is host noise, not the workload.  The
+    collection runs before the warmup: steps right after one ran 2-4 %
+    slower in measurement, a transient the warmup absorbs."""
     was = gc.isenabled()
     gc.collect()
     gc.freeze()
@@ -128,11 +131,11 @@ def time_steps(module, x, dy, steps: int, warmup: int, graphed=None, train: bool
         y = fwd(x)
         y.backward(dy)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with paused_gc():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
         start.record()
         for _ in range(steps):
             step()
@@ -170,7 +173,6 @@ def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
     algorithmic bytes (inputs read once, outputs written once).
     """
     import torch
-    from thetascan_amd import _lib
 
     def step():
         if train:
@@ -179,6 +181,14 @@ def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
         else:
             with torch.no_grad():
                 module(x)
+
+    with paused_gc():
+        return _pass_profile(module, x, dy, steps, step)
+
+
+def _pass_profile(module, x, dy, steps, step):
+    import torch
+    from thetascan_amd import _lib
 
     step()
     torch.cuda.synchronize()
@@ -200,7 +210,7 @@ def pass_profile(module, x, dy, steps: int = 5, train: bool = True):
     torch.cuda.synchronize()
     cycles_per_s = probe_cycles / max(a.elapsed_time(b) * 1e-3, 1e-6)
     sleep_cycles = int(cycles_per_s * (2.0 * host_s + 1e-3))
-    with _lib.record_launches() as recs, paused_gc():
+    with _lib.record_launches() as recs:
         for _ in range(steps):
             torch.cuda._sleep(sleep_cycles)
             step()
@@ -422,10 +432,10 @@ def run_lm(args) -> dict:
     def step():
         model(x, y).backward()
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
     with paused_gc():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
@@ -621,20 +631,20 @@ def decode_latency(x, steps: int = 200, warmup: int = 20) -> dict:
         torch.cuda.synchronize()
         prefill_ms = (time.perf_counter() - t0) * 1e3
         s = state
-        for _ in range(warmup):
-            _, s = module(tok, state=s)
-        torch.cuda.synchronize()
         with paused_gc():
+            for _ in range(warmup):
+                _, s = module(tok, state=s)
+            torch.cuda.synchronize()
             t0 = time.perf_counter()
             for _ in range(steps):
                 _, s = module(tok, state=s)
             torch.cuda.synchronize()
             eager_us = (time.perf_counter() - t0) / steps * 1e6
         dec = DecodeGraph(module, state)
-        for _ in range(warmup):
-            dec.step(tok)
-        torch.cuda.synchronize()
         with paused_gc():
+            for _ in range(warmup):
+                dec.step(tok)
+            torch.cuda.synchronize()
             t0 = time.perf_counter()
             for _ in range(steps):
                 dec.step(tok)

@@ -553,6 +553,30 @@ def test_short_continuations_walk_the_recurrence(cuda, dtype, kind, mass, Dk, Dv
         assert e < (TOL[dtype] if name != "state" else (1e-4 if dtype == torch.float32 else 1e-2)), (name, e)
 
 
+@pytest.mark.parametrize("T", [1, 8, 200])
+@pytest.mark.parametrize("mass", [False, True])
+def test_final_state_written_in_place(cuda, T, mass):
+    """A continuation may write its final state over the state it starts
+    from (the captured decode step does): the result equals the out-of-place
+    call bit for bit, for the token-by-token launch and the tiled passes."""
+    from thetascan_amd._core.ops import scan_hip
+
+    q, k, v = (x.to(cuda, torch.bfloat16) for x in _streams(2, 3, T, 64, 64, seed=57, dtype=torch.float32))
+    if mass:
+        q, k = q.abs(), k.abs()
+    la = torch.log(torch.rand(3, generator=torch.Generator().manual_seed(58)) * 0.09 + 0.9).to(cuda)
+    _, _, st = scan_hip.linattn_state(q[:, :, :5], k[:, :, :5], v[:, :, :5], la, mass=mass)
+    ref_out, ref_mass, ref_fin = scan_hip.linattn_state(q, k, v, la, st, mass=mass)
+    buf = st.clone()
+    kind = scan_hip._classify(la, q)
+    out, m, fin = scan_hip.scan_launch(q, k, v, **scan_hip._ret_kwargs(kind, la), v_ext="ones" if mass else None,
+                                       want_ext_out=mass, want_final=True, init_state=buf, final_out=buf)
+    assert fin.data_ptr() == buf.data_ptr()
+    assert torch.equal(out, ref_out) and torch.equal(buf, ref_fin)
+    if mass:
+        assert torch.equal(m, ref_mass)
+
+
 def test_short_continuation_equals_the_tiled_path(cuda):
     """A one-token step gives what the tiled passes give for the same token
     appended to a tile-aligned prefix, to fp32 rounding."""

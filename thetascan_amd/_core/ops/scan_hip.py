@@ -108,6 +108,7 @@ def scan_launch(
     workspace: torch.Tensor | None = None,
     states_in: int = 0,
     init_state: torch.Tensor | None = None,
+    final_out: torch.Tensor | None = None,
 ):
     """One scan (several kernel launches when a width exceeds ``MAX_WIDTH``).
 
@@ -118,10 +119,13 @@ def scan_launch(
     ``workspace`` (from :func:`workspace_for`) keeps the segment states of
     this scan after the call; ``states_in`` = 1 (2) reads the states an
     earlier call of the same (swapped) keys and values left there instead of
-    recomputing them -- single-launch widths only.
+    recomputing them -- single-launch widths only.  ``final_out`` (fp32, the
+    final state's shape) receives the final state; it may be ``init_state``
+    itself (an in-place update: every entry is read before the same thread
+    writes it).
     """
     dk, dv = q.shape[-1], v.shape[-1]
-    if workspace is not None or states_in or init_state is not None:
+    if workspace is not None or states_in or init_state is not None or final_out is not None:
         if dk > MAX_WIDTH or dv > MAX_WIDTH:
             raise NotImplementedError("hip scan: kept segment states and initial states need widths up to 128")
     if dk <= MAX_WIDTH and dv <= MAX_WIDTH:
@@ -129,7 +133,7 @@ def scan_launch(
                           q_ext=q_ext, k_ext=k_ext, v_ext=v_ext, out=out, out_mode=out_mode, out_scale=out_scale,
                           want_ext_out=want_ext_out, ext_out=ext_out, want_final=want_final,
                           seg_chunks=seg_chunks, value_split=value_split, workspace=workspace,
-                          states_in=states_in, init_state=init_state)
+                          states_in=states_in, init_state=init_state, final_out=final_out)
     if want_final:
         raise NotImplementedError(f"hip scan: final state of widths dk={dk} dv={dv} above {MAX_WIDTH}")
     kw = dict(retention=retention, log_alpha=log_alpha, decay=decay, reverse=reverse, seg_chunks=seg_chunks,
@@ -200,6 +204,7 @@ def _scan_once(
     workspace: torch.Tensor | None = None,
     states_in: int = 0,
     init_state: torch.Tensor | None = None,
+    final_out: torch.Tensor | None = None,
 ):
     """One kernel launch.  Returns ``(out, ext_out, final_state)``.
 
@@ -260,19 +265,30 @@ def _scan_once(
         if out_mode == _lib.OUT_ACCUM_F32:
             raise ValueError("accumulating scan needs an ext output tensor")
         ext_out = torch.empty(B, H, T, dtype=torch.float32, device=q.device)
-    final = None
-    if want_final:
-        # every entry of the [dk(+1)][dv(+1)] layout is written except the
-        # corner of a key ext row meeting a value ext column
-        corner = qe_mode != _lib.EXT_NONE and ke_mode != _lib.EXT_NONE and ve_mode != _lib.EXT_NONE
-        final = (torch.zeros if corner else torch.empty)(B * H, dk_pad, dv_pad, dtype=torch.float32,
-                                                          device=q.device)
     init = None
     if init_state is not None:
         if tuple(init_state.shape[-2:]) != (dk_pad, dv_pad) or init_state.numel() != B * H * dk_pad * dv_pad:
             raise ValueError(f"hip scan: initial state of shape {tuple(init_state.shape)}, "
                              f"expected [{B}, {H}, {dk_pad}, {dv_pad}]")
         init = init_state.detach().to(device=q.device, dtype=torch.float32).contiguous()
+    final = None
+    if want_final:
+        # every entry of the [dk(+1)][dv(+1)] layout is written except the
+        # corner of a key ext row meeting a value ext column
+        corner = qe_mode != _lib.EXT_NONE and ke_mode != _lib.EXT_NONE and ve_mode != _lib.EXT_NONE
+        if final_out is not None:
+            if (final_out.dtype != torch.float32 or not final_out.is_contiguous() or final_out.device != q.device
+                    or tuple(final_out.shape[-2:]) != (dk_pad, dv_pad)
+                    or final_out.numel() != B * H * dk_pad * dv_pad):
+                raise ValueError("hip scan: final_out must be a contiguous fp32 tensor of the final state's shape")
+            final = final_out.view(B * H, dk_pad, dv_pad)
+            if corner and (init is None or init.data_ptr() != final.data_ptr()):
+                final.zero_()
+        else:
+            final = (torch.zeros if corner else torch.empty)(B * H, dk_pad, dv_pad, dtype=torch.float32,
+                                                              device=q.device)
+    elif final_out is not None:
+        raise ValueError("hip scan: final_out without want_final")
     if workspace is not None:
         if workspace.numel() * workspace.element_size() < ws_bytes:
             raise ValueError("hip scan: workspace too small")
@@ -760,9 +776,11 @@ def _carried_scan(q, k, v, kind, r, with_mass: bool, init):
     if len(blocks) != len(kcols) * len(vcols):
         raise ValueError("streaming state does not match this scan's widths")
     rk = _ret_kwargs(kind, r)
+    in_place = stream.updates_in_place()
     if len(blocks) == 1:
         out, mass, fin = scan_launch(q, k, v, **rk, v_ext="ones" if with_mass else None, want_ext_out=with_mass,
-                                     want_final=True, init_state=blocks[0])
+                                     want_final=True, init_state=blocks[0],
+                                     final_out=blocks[0] if in_place else None)
         return out, mass, [fin]
     acc = torch.zeros(*q.shape[:3], dv, dtype=torch.float32, device=q.device)
     mass = torch.zeros(q.shape[:3], dtype=torch.float32, device=q.device) if with_mass else None
@@ -773,7 +791,8 @@ def _carried_scan(q, k, v, kind, r, with_mass: bool, init):
         for j, v0 in enumerate(vcols):
             ext = with_mass and j == 0
             o, e, fin = scan_launch(qs, ks, v[..., v0:v0 + MAX_WIDTH], **rk, v_ext="ones" if ext else None,
-                                    want_ext_out=ext, want_final=True, init_state=blocks[i])
+                                    want_ext_out=ext, want_final=True, init_state=blocks[i],
+                                    final_out=blocks[i] if in_place else None)
             acc[..., v0:v0 + o.shape[-1]] += o.float()
             if ext:
                 mass += e

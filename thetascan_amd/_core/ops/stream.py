@@ -67,6 +67,25 @@ def device_position() -> torch.Tensor | None:
     return _DEVICE_POSITION.get()
 
 
+_IN_PLACE: contextvars.ContextVar = contextvars.ContextVar("thetascan_in_place", default=False)
+
+
+def updates_in_place() -> bool:
+    """Whether the current call's scans write their final states into the
+    carried state tensors they start from (a captured decode step owns its
+    state buffers; an ordinary call never mutates the state it is given)."""
+    return active() is not None and _IN_PLACE.get()
+
+
+@contextlib.contextmanager
+def in_place_updates():
+    token = _IN_PLACE.set(True)
+    try:
+        yield
+    finally:
+        _IN_PLACE.reset(token)
+
+
 @contextlib.contextmanager
 def positions_on_device(pos: torch.Tensor):
     token = _DEVICE_POSITION.set(pos)

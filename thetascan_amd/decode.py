@@ -69,10 +69,13 @@ class DecodeGraph:
             torch.cuda.current_stream(device).wait_stream(side)
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph):
-                with stream.positions_on_device(self._pos):
+                # the scans update their state blocks in place; any other
+                # carried row is copied back into its buffer
+                with stream.positions_on_device(self._pos), stream.in_place_updates():
                     y, new = mixer(self.x, state=self._state)
                 for dst, src in zip(self._state._tensors(), new._tensors()):
-                    dst.copy_(src)
+                    if dst.data_ptr() != src.data_ptr():
+                        dst.copy_(src)
                 self._pos.add_(self.tokens)
         self.y = y
 

@@ -100,3 +100,12 @@ def test_decode_graph_rejects_bad_use(cuda):
         dec = ts.DecodeGraph(module, st)
         with pytest.raises(ValueError, match="shape"):
             dec.step(x)
+        # an in-place parameter update is seen by the next replay; a replaced
+        # parameter is refused before any replay
+        w = module._core.proj_out.weight
+        w.mul_(2.0)
+        y_eager, _ = module(x[:, :1], state=dec.state())
+        assert torch.equal(dec.step(x[:, :1]), y_eager)
+        w.data = w.data.clone()
+        with pytest.raises(RuntimeError, match="replaced"):
+            dec.step(x[:, :1])

@@ -17,10 +17,11 @@ a device counter -- and replays it::
 
 Each replay computes what ``mixer(x_t, state=state)`` computes (the same
 kernels on the same buffers; RoPE phases formed from the same exact fp32
-integer positions).  The recorded step is tied to the mixer's parameters as
-they were at capture (the graph reads the parameter tensors in place, so
-in-place updates are seen; replaced tensors are not) and to the batch size
-and tokens per step given.  Nothing is allocated per step.
+integer positions).  The recorded step reads the mixer's parameters in
+place: in-place updates (an optimizer step) are seen, while a parameter whose
+storage was replaced (``.to()``, assignment to ``.data``) makes the next step
+raise instead of reading memory the graph no longer owns.  The batch size and
+tokens per step are fixed at capture.  Nothing is allocated per step.
 """
 from __future__ import annotations
 
@@ -57,6 +58,9 @@ class DecodeGraph:
         self.x = torch.zeros(self.batch, self.tokens, core.cfg.d_model, device=device, dtype=weight.dtype)
         self._state = state.clone()
         self._pos = torch.full((), self.position, dtype=torch.int64, device=device)
+        # the storage every recorded launch reads (checked before each replay)
+        self._tensors = [t for t in list(core.parameters()) + list(core.buffers())]
+        self._ptrs = [t.data_ptr() for t in self._tensors]
 
         with torch.no_grad():
             # warm-up calls on a side stream set up library handles, plans and
@@ -84,6 +88,10 @@ class DecodeGraph:
         output, a fixed buffer that the next step overwrites."""
         if tuple(x.shape) != tuple(self.x.shape):
             raise ValueError(f"this decode graph takes inputs of shape {tuple(self.x.shape)}; got {tuple(x.shape)}")
+        for t, ptr in zip(self._tensors, self._ptrs):
+            if t.data_ptr() != ptr:
+                raise RuntimeError("a parameter of the mixer was replaced after this decode step was recorded "
+                                   "(moved, cast or reassigned); record a new DecodeGraph")
         self.x.copy_(x)
         self.graph.replay()
         self.position += self.tokens

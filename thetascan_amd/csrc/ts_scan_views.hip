@@ -36,11 +36,21 @@ struct ViewsP {
 };
 
 // LDS: K [C][kp], V [C][vp] (one stage), `nst` state copies [64][kp], then
-// fp32: D [NV][DK], alpha^d [NV][68].
+// fp32: D [NV][DK], alpha^d [NV][68], and the masked powers [NV][4][kPwx]:
+// copy s of view r holds f(j + s - 64) at j, f(d) = alpha_r^d for 0 <= d <= 64
+// and 0 for d < 0, so the four powers f(d0 .. d0+3) of any window are one
+// aligned 16-byte read (copy (d0 + 64) & 3 at j = d0 + 64 - that copy) and
+// the causal / tile-length masks are in the table.
+// The tables are kept where they leave the two workgroups per CU that the
+// registers allow (at most 80 KB each); 128-wide keys with three views keep
+// the per-element reads of alpha^d instead.
+constexpr int kPwx = 128;
+constexpr int kViewsLdsPerWg = 80 * 1024;
 struct ViewsLayout {
   int kp, vp, st, nst, fbase, bytes;
+  bool pwx;
 };
-__host__ __device__ inline ViewsLayout views_layout(int DK, int NV, bool main_kernel) {
+__host__ __device__ constexpr ViewsLayout views_layout(int DK, int NV, bool main_kernel) {
   ViewsLayout L{};
   L.kp = DK + 8;
   L.vp = 64 + 8;
@@ -48,8 +58,17 @@ __host__ __device__ inline ViewsLayout views_layout(int DK, int NV, bool main_ke
   L.nst = main_kernel ? NV : 0;
   const int e_bytes = ((C * L.kp + C * L.vp + L.nst * L.st) * 2 + 15) / 16 * 16;
   L.fbase = e_bytes / 4;
-  L.bytes = e_bytes + (NV * DK + NV * 68) * 4;
+  const int base = e_bytes + (NV * DK + NV * 68) * 4;
+  L.pwx = base + NV * 4 * kPwx * 4 <= kViewsLdsPerWg;
+  L.bytes = base + (L.pwx ? NV * 4 * kPwx * 4 : 0);
   return L;
+}
+
+// f(d0 .. d0 + 3) of one view's masked-power copies (-64 <= d0, d0 + 3 <= 67)
+__device__ __forceinline__ floatx4 pow_window(const float* pwx, int d0) {
+  const int j = d0 + 64;
+  const int sft = j & 3;
+  return *(const floatx4*)(pwx + sft * kPwx + (j - sft));
 }
 
 // One [64 x 8*PER_ROW] bf16 tile section (K or V rows), fetched into
@@ -102,13 +121,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int h = bh - b * p.H;
   const int wave_first = __builtin_amdgcn_readfirstlane(tid & ~63);
 
-  const ViewsLayout L = views_layout(DK, NV, MAIN);
+  constexpr ViewsLayout L = views_layout(DK, NV, MAIN);
+  constexpr bool PWX = L.pwx;
   extern __shared__ __align__(16) unsigned char smem[];
   E* Ks = (E*)smem;
   E* Vs = Ks + C * L.kp;
   E* st_base = Vs + C * L.vp;
   float* s_d = (float*)smem + L.fbase;  // [NV][DK]
   float* s_pw = s_d + NV * DK;           // [NV][68]: alpha_r^d, d = 0..64
+  float* s_pwx = s_pw + NV * 68;         // [NV][4][kPwx]: masked powers, shifted copies
 
   const int64_t bh_q = (int64_t)b * p.q.sb + (int64_t)h * p.q.sh;
   const int64_t bh_k = (int64_t)b * p.k.sb + (int64_t)h * p.k.sh;
@@ -128,6 +149,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int r = 0; r < NV; ++r) {
       s_pw[r * 68 + lane] = expf(la[r] * (float)lane);
       if (lane == 0) s_pw[r * 68 + 64] = expf(la[r] * 64.0f);
+    }
+  }
+  // masked powers: the same expf values (d = 0..64), zero below d = 0 and
+  // above 64 (indices past 64 are never read by a window that matters)
+  if constexpr (PWX) {
+    for (int e = tid; e < NV * 4 * kPwx; e += 256) {
+      const int r = e / (4 * kPwx), rem = e - r * 4 * kPwx;
+      const int sft = rem / kPwx, j = rem - sft * kPwx;
+      const int d = j + sft - 64;
+      s_pwx[e] = d >= 0 && d <= 64 ? expf(la[r] * (float)d) : 0.0f;
     }
   }
 
@@ -237,14 +268,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll 1
       for (int r = 0; r < NV; ++r) {
         const float* pw = s_pw + r * 68;
+        const float* pwx = s_pwx + r * 4 * kPwx;
         floatx4 pr[4];
+        if constexpr (PWX) {
+          // key kb*16+4g+i sits query - key = c - i before the query: the
+          // window f(c-3 .. c) holds its weight at element 3 - i (zero for a
+          // key after the query, which also covers the blocks kb > w)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+          for (int kb = 0; kb < 4; ++kb) {
+            const floatx4 wv = pow_window(pwx, query - kb * 16 - 4 * g - 3);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kb * 16 + 4 * g + i;
-            pr[kb][i] = (kb < w || (kb == w && key <= query)) ? sc[kb][i] * pw[max(query - key, 0)] : 0.0f;
+            for (int i = 0; i < 4; ++i) pr[kb][i] = sc[kb][i] * wv[3 - i];
           }
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = kb * 16 + 4 * g + i;
+              pr[kb][i] = (kb < w || (kb == w && key <= query)) ? sc[kb][i] * pw[max(query - key, 0)] : 0.0f;
+            }
+        }
         const F8 p0 = IO::from_acc(pr[0], pr[1]);
         const F8 p1 = IO::from_acc(pr[2], pr[3]);
         const float cw = pw[query + 1];
@@ -291,11 +335,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     F8 av[2];
 #pragma unroll
     for (int kp = 0; kp < 2; ++kp) av[kp] = TK::col8(Vs, L.vp, w * 16, kp, lane);
-    // weight of this lane's key e of contraction block kp in view r
-    auto key_weight = [&](int r, int kp, int e) -> float {
-      const int key = 32 * kp + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
-      const float wv = s_pw[r * 68 + max(len - 1 - key, 0)];  // loaded unconditionally: no branch
-      return key < len ? wv : 0.0f;
+    // weights of this lane's keys of contraction block kp in view r: keys
+    // 32kp+4g+e (e < 4) and 32kp+16+4g+(e-4) sit len-1-key before the tile's
+    // end; the window f(c-3 .. c) holds key e's weight at element 3 - (e & 3)
+    // (zero for a key past the tile's length)
+    auto key_weights = [&](int r, int kp, float* wk) {
+      if constexpr (PWX) {
+        const float* pwx = s_pwx + r * 4 * kPwx;
+        const int c0 = len - 1 - 32 * kp - 4 * g;
+        const floatx4 lo = pow_window(pwx, c0 - 3), hi = pow_window(pwx, c0 - 16 - 3);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wk[e] = lo[3 - e];
+          wk[4 + e] = hi[3 - e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = 32 * kp + (e < 4 ? 4 * g + e : 12 + 4 * g + e);
+          const float wv = s_pw[r * 68 + max(len - 1 - key, 0)];  // loaded unconditionally: no branch
+          wk[e] = key < len ? wv : 0.0f;
+        }
+      }
     };
     // one view at a time (K fragments re-read from LDS per view: fewer live
     // registers than sharing them across the views' states)
@@ -305,9 +366,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float cdec = s_pw[r * 68 + len];
       F8 avw[2];
 #pragma unroll
-      for (int kp = 0; kp < 2; ++kp)
+      for (int kp = 0; kp < 2; ++kp) {
+        float wk[8];
+        key_weights(r, kp, wk);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) avw[kp][e] = (E)(tof(av[kp][e]) * key_weight(r, kp, e));
+        for (int e = 0; e < 8; ++e) avw[kp][e] = (E)(tof(av[kp][e]) * wk[e]);
+      }
       if (!(MAIN && state_zero)) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
@@ -335,8 +399,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int kp = 0; kp < 2; ++kp) {
         F8 a;
+        float wk[8];
+        key_weights(min(l16, NV - 1), kp, wk);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = (E)(l16 < NV ? key_weight(l16, kp, e) : 0.0f);
+        for (int e = 0; e < 8; ++e) a[e] = (E)(l16 < NV ? wk[e] : 0.0f);
 #pragma unroll
         for (int j = 0; j < NKO; ++j) Dall[j] = mma32(a, TK::col8(Ks, L.kp, (w + 4 * j) * 16, kp, lane), Dall[j]);
       }

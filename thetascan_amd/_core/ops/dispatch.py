@@ -13,8 +13,9 @@ a pair two ways:
   dispatcher costs about 0.1 ms of host time per forward and backward, which
   a GPU-bound training step would otherwise pay per operation.
 
-Both run the same forward and backward functions, so their results are
-bit-identical.  ``setup`` and ``backward`` follow the ``register_autograd``
+Where autograd records nothing (grad mode off, or no input that requires
+grad) the forward function runs alone, with no node around it.  All paths run
+the same forward and backward functions, so their results are bit-identical.  ``setup`` and ``backward`` follow the ``register_autograd``
 convention (``setup(ctx, inputs, output)``; ``backward(ctx, grads, bwd)``
 returns one gradient per input, a list for a list input), where ``bwd`` is
 the backward custom op under compilation and the plain backward function in
@@ -89,5 +90,9 @@ class HipOp:
         if torch.compiler.is_compiling():
             return self.op(*args)
         tensors = [args[i] if j is None else args[i][j] for i, j in _tensor_slots(args)]
+        if not torch.is_grad_enabled() or not any(t.requires_grad for t in tensors):
+            # nothing to record (inference, streaming continuation): the
+            # forward alone, without an autograd node around it
+            return self.forward(*args)
         out = _Eager.apply(self, args, *tensors)
         return list(out) if isinstance(out, tuple) else out

@@ -121,6 +121,11 @@ __device__ __forceinline__ floatx4 am_input(const AbsMassP& p, const AmThread& w
   }
 }
 
+// Steps are taken eight at a time: the loads of all eight are issued before
+// the first is folded (the step chain itself is sequential, its loads are
+// not), with the tail's surplus loads clamped to the segment's last step.
+constexpr int kAmUnroll = 8;
+
 template <typename E, int MODE>
 __global__ __launch_bounds__(256) void absmass_summary_kernel(AbsMassP p) {
   AmThread w;
@@ -129,15 +134,25 @@ __global__ __launch_bounds__(256) void absmass_summary_kernel(AbsMassP p) {
   const int u1 = min(u0 + p.L, p.T);
   floatx4 z = {0.f, 0.f, 0.f, 0.f};
   float P = 1.0f;
-#pragma unroll 8
-  for (int u = u0; u < u1; ++u) {
-    const int tp = MODE == AM_DK ? p.T - 1 - u : u;
-    const float a = am_step<MODE>(p, w, u);
-    const floatx4 x = am_input<E, MODE>(p, w, tp);
-    const float c = u == u0 ? 0.f : a;
+  for (int u = u0; u < u1; u += kAmUnroll) {
+    floatx4 x[kAmUnroll];
+    float a[kAmUnroll];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) z[i] = c * z[i] + x[i];
-    P *= a;
+    for (int i = 0; i < kAmUnroll; ++i) {
+      const int uu = min(u + i, u1 - 1);
+      const int tp = MODE == AM_DK ? p.T - 1 - uu : uu;
+      a[i] = am_step<MODE>(p, w, uu);
+      x[i] = am_input<E, MODE>(p, w, tp);
+    }
+#pragma unroll
+    for (int i = 0; i < kAmUnroll; ++i) {
+      if (u + i < u1) {
+        const float c = u + i == u0 ? 0.f : a[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[e] = c * z[e] + x[i][e];
+        P *= a[i];
+      }
+    }
   }
   *(floatx4*)(p.tot + w.r * p.F + w.f) = z;
   if (w.f == 0) p.prod[w.r] = P;
@@ -150,41 +165,65 @@ __global__ __launch_bounds__(256) void absmass_main_kernel(AbsMassP p) {
   const int FV = p.F / 4;  // a power of two <= 64: the row's threads are adjacent, aligned lanes
   const int64_t row0 = (w.r / p.S) * p.S;
   floatx4 z = {0.f, 0.f, 0.f, 0.f};  // the state entering this segment
-  for (int j = 0; j < w.seg; ++j) {
-    const float P = p.prod[row0 + j];
-    const floatx4 t4 = *(const floatx4*)(p.tot + (row0 + j) * p.F + w.f);
+  for (int j0 = 0; j0 < w.seg; j0 += kAmUnroll) {
+    float P[kAmUnroll];
+    floatx4 t4[kAmUnroll];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) z[i] = P * z[i] + t4[i];
+    for (int i = 0; i < kAmUnroll; ++i) {
+      const int j = min(j0 + i, w.seg - 1);
+      P[i] = p.prod[row0 + j];
+      t4[i] = *(const floatx4*)(p.tot + (row0 + j) * p.F + w.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kAmUnroll; ++i) {
+      if (j0 + i < w.seg) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[e] = P[i] * z[e] + t4[i][e];
+      }
+    }
   }
   const int u0 = w.seg * p.L;
   const int u1 = min(u0 + p.L, p.T);
-#pragma unroll 8
-  for (int u = u0; u < u1; ++u) {
-    const int tp = MODE == AM_DK ? p.T - 1 - u : u;
-    const float a = am_step<MODE>(p, w, u);
-    const floatx4 x = am_input<E, MODE>(p, w, tp);
-    const float c = u == 0 ? 0.f : a;
+  for (int u = u0; u < u1; u += kAmUnroll) {
+    floatx4 x[kAmUnroll], y[kAmUnroll];
+    float a[kAmUnroll], dm[kAmUnroll];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) z[i] = c * z[i] + x[i];
-    if constexpr (MODE == AM_MASS) {
-      const floatx4 aq = am_abs(am_ld4<E>(am_row<E>(p.q, w.b, w.h, tp) + w.f));
-      float s = aq[0] * z[0] + aq[1] * z[1] + aq[2] * z[2] + aq[3] * z[3];
-      for (int o = 1; o < FV; o <<= 1) s += __shfl_xor(s, o, 64);
-      if (w.f == 0)
-        *((float*)p.mass.ptr + (int64_t)w.b * p.mass.sb + (int64_t)w.h * p.mass.sh + (int64_t)tp * p.mass.st) = s;
-    } else if constexpr (MODE == AM_DQ) {
-      const float dm = am_scalar(p.dmass, w.b, w.h, tp);
-      const floatx4 qv = am_ld4<E>(am_row<E>(p.q, w.b, w.h, tp) + w.f);
-      floatx4 o;
+    for (int i = 0; i < kAmUnroll; ++i) {
+      const int uu = min(u + i, u1 - 1);
+      const int tp = MODE == AM_DK ? p.T - 1 - uu : uu;
+      a[i] = am_step<MODE>(p, w, uu);
+      x[i] = am_input<E, MODE>(p, w, tp);
+      // the row the step's output reads besides the prefix: q (mass, dq) or k (dk)
+      y[i] = am_ld4<E>(am_row<E>(MODE == AM_DK ? p.k : p.q, w.b, w.h, tp) + w.f);
+      dm[i] = MODE == AM_DQ ? am_scalar(p.dmass, w.b, w.h, tp) : 0.f;
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = dm * am_sign(qv[i]) * z[i];
-      am_st4<E>(const_cast<E*>(am_row<E>(p.out, w.b, w.h, tp)) + w.f, o);
-    } else {
-      const floatx4 kv = am_ld4<E>(am_row<E>(p.k, w.b, w.h, tp) + w.f);
-      floatx4 o;
+    for (int i = 0; i < kAmUnroll; ++i) {
+      // uniform over a row's lanes (one segment), so the row's shuffles below
+      // run with every partner lane active
+      if (u + i < u1) {
+        const int tp = MODE == AM_DK ? p.T - 1 - (u + i) : u + i;
+        const float c = u + i == 0 ? 0.f : a[i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = am_sign(kv[i]) * z[i];
-      am_st4<E>(const_cast<E*>(am_row<E>(p.out, w.b, w.h, tp)) + w.f, o);
+        for (int e = 0; e < 4; ++e) z[e] = c * z[e] + x[i][e];
+        if constexpr (MODE == AM_MASS) {
+          const floatx4 aq = am_abs(y[i]);
+          float s = aq[0] * z[0] + aq[1] * z[1] + aq[2] * z[2] + aq[3] * z[3];
+          for (int o = 1; o < FV; o <<= 1) s += __shfl_xor(s, o, 64);
+          if (w.f == 0)
+            *((float*)p.mass.ptr + (int64_t)w.b * p.mass.sb + (int64_t)w.h * p.mass.sh + (int64_t)tp * p.mass.st) = s;
+        } else if constexpr (MODE == AM_DQ) {
+          floatx4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = dm[i] * am_sign(y[i][e]) * z[e];
+          am_st4<E>(const_cast<E*>(am_row<E>(p.out, w.b, w.h, tp)) + w.f, o);
+        } else {
+          floatx4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = am_sign(y[i][e]) * z[e];
+          am_st4<E>(const_cast<E*>(am_row<E>(p.out, w.b, w.h, tp)) + w.f, o);
+        }
+      }
     }
   }
 }
@@ -195,11 +234,14 @@ namespace {
 
 using ts::fail;
 
-// Segments of the scan order: about 2^19 features in flight, at least 16
-// steps per segment.
+// Segments of the scan order: about 2^TS_AM_INFLIGHT_LOG2 features in
+// flight, at least 16 steps per segment.
+#ifndef TS_AM_INFLIGHT_LOG2
+#define TS_AM_INFLIGHT_LOG2 19
+#endif
 void am_segments(const ts_abs_mass_desc* d, int* S, int* L) {
   const int64_t lanes = (int64_t)d->B * d->H * d->F;
-  int64_t want = ((int64_t)1 << 19) / (lanes > 0 ? lanes : 1);
+  int64_t want = ((int64_t)1 << TS_AM_INFLIGHT_LOG2) / (lanes > 0 ? lanes : 1);
   const int64_t most = (d->T + 15) / 16;
   if (want > most) want = most;
   if (want < 1) want = 1;

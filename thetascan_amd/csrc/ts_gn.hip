@@ -197,8 +197,12 @@ __device__ __forceinline__ void gn_forward_token(const GnP& p, int b, int h, int
     }
 }
 
+// Two waves per SIMD for the bf16 forward up to 64-wide tokens and 128 hidden
+// features: at 128 hidden features that spills 44 registers and still runs
+// 25 % faster than one wave without spills (B8 T2048 H8: 135 -> 101 us).
+// (The backward at that width would spill 229 and measured 33 % slower.)
 template <typename E, int D, int MB>
-__global__ __launch_bounds__(256) void gn_write_fwd_kernel(GnP p) {
+__global__ __launch_bounds__(256, (sizeof(E) == 2 && D <= 64 && MB <= 8 ? 2 : 1)) void gn_write_fwd_kernel(GnP p) {
   constexpr int M = MB * 16;
   constexpr bool WL = gn_weights_in_lds<E, D, MB, true>();
   const int b = blockIdx.z, h = blockIdx.y;

@@ -70,10 +70,37 @@ __host__ __device__ constexpr GnLayout gn_layout(int esize, int d, int m, bool f
   L.end = off;
   return L;
 }
+// The read stage's own carve-up: the forward stages W1 and W2, the backward
+// W1, W1^T and W2^T (the write layout's other matrices would only cost
+// resident workgroups).
+__host__ __device__ constexpr GnLayout gn_read_layout(int esize, int d, int m, bool fwd, bool w_lds) {
+  const int vec = 16 / esize;
+  GnLayout L{};
+  L.xp = d + vec;
+  L.mp = m + vec;
+  int off = 0;
+  L.xs = off; off += TT * L.xp;
+  L.w1 = L.w2 = L.w1t = L.w2t = -1;
+  if (w_lds) {
+    L.w1 = off; off += m * L.xp;
+    if (fwd) {
+      L.w2 = off; off += d * L.mp;
+    } else {
+      L.w1t = off; off += d * L.mp;
+      L.w2t = off; off += m * L.xp;
+    }
+  }
+  L.end = off;
+  return L;
+}
 constexpr int kGnLdsMax = 160 * 1024;
 template <typename E, int D, int MB, bool FWD>
 constexpr bool gn_weights_in_lds() {
   return gn_layout((int)sizeof(E), D, MB * 16, FWD, true).end * (int)sizeof(E) <= kGnLdsMax;
+}
+template <typename E, int D, int MB, bool FWD>
+constexpr bool gn_read_weights_in_lds() {
+  return gn_read_layout((int)sizeof(E), D, MB * 16, FWD, true).end * (int)sizeof(E) <= kGnLdsMax;
 }
 
 // The four thresholds of features fb*16 + 4g .. +3 (zeros without tau).
@@ -534,10 +561,10 @@ __device__ __forceinline__ void tau_of(const float* tau, int fb, int g, bool on,
 template <typename E, int D, int MB>
 __global__ __launch_bounds__(256) void gn_read_fwd_kernel(GnReadP p) {
   constexpr int M = MB * 16;
-  constexpr bool WL = gn_weights_in_lds<E, D, MB, true>();
+  constexpr bool WL = gn_read_weights_in_lds<E, D, MB, true>();
   const int b = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
-  const GnLayout L = gn_layout((int)sizeof(E), D, M, true, WL);
+  const GnLayout L = gn_read_layout((int)sizeof(E), D, M, true, WL);
   extern __shared__ __align__(16) unsigned char smem[];
   E* base = (E*)smem;
   E* xs = base + L.xs;
@@ -602,10 +629,10 @@ __global__ __launch_bounds__(256) void gn_read_fwd_kernel(GnReadP p) {
 template <typename E, int D, int MB>
 __global__ __launch_bounds__(256) void gn_read_bwd_kernel(GnReadP p) {
   constexpr int M = MB * 16;
-  constexpr bool WL = gn_weights_in_lds<E, D, MB, false>();
+  constexpr bool WL = gn_read_weights_in_lds<E, D, MB, false>();
   const int b = blockIdx.z, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, g = lane >> 4;
-  const GnLayout L = gn_layout((int)sizeof(E), D, M, false, WL);
+  const GnLayout L = gn_read_layout((int)sizeof(E), D, M, false, WL);
   extern __shared__ __align__(16) unsigned char smem[];
   E* base = (E*)smem;
   E* xs = base + L.xs;
@@ -1492,6 +1519,13 @@ int gn_lds_bytes(const ts_gn_desc* d, bool fwd) {
   return ts::gn_layout(es, d->d, d->m, fwd, wl).end * es;
 }
 
+int gn_read_lds_bytes(const ts_gn_desc* d, bool fwd) {
+  const int es = d->dtype == TS_BF16 ? 2 : 4;
+  const ts::GnLayout full = ts::gn_read_layout(es, d->d, d->m, fwd, true);
+  const bool wl = full.end * es <= ts::kGnLdsMax;
+  return ts::gn_read_layout(es, d->d, d->m, fwd, wl).end * es;
+}
+
 // Groups of 64 tokens per workgroup: enough workgroups to fill 256 CUs.
 int gn_groups(const ts_gn_desc* d) {
   const int ngroups = (d->T + ts::TT - 1) / ts::TT;
@@ -1600,7 +1634,7 @@ int gn_read_launch(const ts_gn_desc* d, const ts::GnReadP& p, bool fwd, hipStrea
                             : (fwd ? gn_read_pick<float, true>(d->d, d->m) : gn_read_pick<float, false>(d->d, d->m));
   if (!k) return fail(TS_ERR_NOT_IMPLEMENTED, "gn read: no kernel for d=%d m=%d", d->d, d->m);
   const int lds = wide ? ts::gn_wide_layout(d->d, d->m, p.want_resid ? (fwd ? 1 : 2) : 0).end * 2
-                       : gn_lds_bytes(d, fwd);
+                       : gn_read_lds_bytes(d, fwd);
   if (lds > ts::kGnLdsMax) return fail(TS_ERR_NOT_IMPLEMENTED, "gn read: tile of %d bytes exceeds LDS", lds);
   if (lds > 65536) {
     hipError_t e = ts::ensure_lds_limit((const void*)k, lds);

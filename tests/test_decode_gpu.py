@@ -88,6 +88,37 @@ def test_decode_graph_spans_rope_blocks_and_several_tokens(cuda):
     assert dec.state().position == 1029
 
 
+@pytest.mark.parametrize("name", ["headline_2b", "kernel_softmax_bank_fast"])
+def test_decode_graph_with_tiled_steps(cuda, name):
+    """Steps of sixteen tokens take the tiled scan passes (summary, prefix and
+    main) under capture, their final states written in place: fp32 replays
+    equal the eager continuation bit for bit."""
+    import thetascan_amd as ts
+
+    module, pub = _module(name, cuda)
+    D = pub["d_model"]
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 100, D, generator=g).to(cuda)
+    xs = torch.randn(2, 48, D, generator=g).to(cuda)
+    with torch.no_grad():
+        _, st = module(x, state=module.initial_state())
+        s, expected = st.clone(), []
+        for t in range(0, 48, 16):
+            y, s = module(xs[:, t:t + 16], state=s)
+            expected.append(y)
+        dec = ts.DecodeGraph(module, st, tokens=16)
+        got = []
+        for t in range(0, 48, 16):
+            got.append(dec.step(xs[:, t:t + 16]).clone())
+            torch.cuda.synchronize()
+        fin = dec.state()
+    for a, b in zip(got, expected):
+        assert torch.equal(a, b), name
+    for a, b in zip(fin._tensors(), s._tensors()):
+        assert torch.equal(a, b), name
+    assert fin.position == 148
+
+
 def test_decode_graph_rejects_bad_use(cuda):
     import thetascan_amd as ts
 

@@ -41,8 +41,9 @@ extern "C" {
  * 14: ts_read_out_fwd / ts_read_out_bwd / ts_read_out_bwd_parts (the read
  *     fused with the output projection), ts_kmap_*, ts_anchor_*,
  *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3,
- *     TS_GN_SILU, ts_gn_act_* and ts_abs_mass_*; nothing earlier changed. */
-#define TS_ABI_VERSION 14
+ *     TS_GN_SILU, ts_gn_act_* and ts_abs_mass_*; nothing earlier changed.
+ * 15: ts_rownorm_fwd / ts_rownorm_bwd; nothing earlier changed. */
+#define TS_ABI_VERSION 15
 
 enum ts_status {
   TS_OK = 0,
@@ -836,6 +837,35 @@ int ts_abs_mass_fwd(const ts_abs_mass_desc* desc, ts_strided q, ts_strided k, co
 int ts_abs_mass_bwd(const ts_abs_mass_desc* desc, ts_strided q, ts_strided k, ts_strided dmass,
                     const float* log_alpha, ts_strided decay, ts_strided dq, ts_strided dk, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------- row norm of the host LM */
+
+/* RMS-normed rows with an optional half-split rotary turn and per-head gain,
+ * for the hybrid language model around the ThetaScan layers (config 5's
+ * attention prologue q, k = rotate(rms_norm(q)) * gain and its residual-stream
+ * norms, written with F.rms_norm and torch elementwise ops in the upstream
+ * training script, which this build does not have):
+ *   r = (mean(x^2) + eps)^-1/2,  y = gain[h] * R_t(x r)
+ * R_t turns the halves (n1, n2) of a row to (n1 c + n2 s, n2 c - n1 s) with
+ * c = cos[t], s = sin[t] (fp32 [T, W/2]) when desc->rope, else is the
+ * identity; gain (fp32 [H]) may be NULL.  x is a [B,H,T,W] view (rows 16-byte
+ * aligned), y a contiguous [B,H,T,W] tensor of the same dtype, rstd fp32
+ * [B*H*T] (kept for the backward).  W = 8, 16, 32, ... 512 (16 or more with
+ * the turn).  The backward writes dx (contiguous [B,H,T,W]) and, when dg_row
+ * is given, each row's <dy, R_t(x r)> (fp32 [B*H*T]; the gain's gradient is
+ * their sum over a head's rows).  fp32 arithmetic, one rounding per output. */
+typedef struct ts_rownorm_desc {
+  int32_t B, H, T, W;
+  int32_t dtype;        /* of x, y, dy, dx                                     */
+  int32_t rope;         /* 1: apply the rotary turn                            */
+  float eps;
+} ts_rownorm_desc;
+
+int ts_rownorm_fwd(const ts_rownorm_desc* desc, ts_strided x, const float* cos, const float* sin,
+                   const float* gain, void* y, float* rstd, hipStream_t stream);
+
+int ts_rownorm_bwd(const ts_rownorm_desc* desc, ts_strided x, ts_strided dy, const float* cos, const float* sin,
+                   const float* gain, const float* rstd, void* dx, float* dg_row, hipStream_t stream);
 
 /* out[i] = scale * (sum_{s<na} a[s*n + i] + sum_{s<nb} b[s*n + i]) for i < n,
  * written as ts_dtype out_dtype: sums the partial weight-gradient slots of

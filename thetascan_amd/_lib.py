@@ -291,6 +291,10 @@ class AbsMassDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "F", "dtype", "retention")]
 
 
+class RowNormDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "W", "dtype", "rope")] + [("eps", ctypes.c_float)]
+
+
 class GnActDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "m", "dtype", "act", "has_tau")] + [
         ("eps", ctypes.c_float)]
@@ -561,6 +565,11 @@ def load() -> ctypes.CDLL:
                                         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_abs_mass_bwd.argtypes = [P(AbsMassDesc), Strided, Strided, Strided, ctypes.c_void_p, Strided, Strided,
                                         Strided, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.ts_rownorm_fwd.argtypes = [P(RowNormDesc), Strided, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.ts_rownorm_bwd.argtypes = [P(RowNormDesc), Strided, Strided, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p]
         lib.ts_gn_act_fwd.argtypes = [P(GnActDesc), Strided, Strided, ctypes.c_void_p, Strided, Strided, Strided,
                                       ctypes.c_void_p]
         lib.ts_gn_act_bwd.argtypes = [P(GnActDesc), Strided, Strided, ctypes.c_void_p] + [Strided] * 6 + [
@@ -573,7 +582,7 @@ def load() -> ctypes.CDLL:
         lib.ts_retention_workspace_bytes.argtypes = [P(RetentionDesc), P(ctypes.c_size_t)]
         lib.ts_retention_grad.argtypes = [P(RetentionDesc), P(RetentionIO), ctypes.c_void_p, ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 14:
+        if lib.ts_abi_version() != 15:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

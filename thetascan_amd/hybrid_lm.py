@@ -28,6 +28,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ._core.ops import rownorm
 from .api import ThetaScan
 from .config import ThetaScanConfig
 
@@ -56,6 +57,10 @@ def theta_config() -> ThetaScanConfig:
 
 
 def _rms(x: torch.Tensor) -> torch.Tensor:
+    """RMS norm of the last axis (F.rms_norm's eps): one ts_rownorm launch per
+    direction for [B,T,D] activations on the GPU."""
+    if x.ndim == 3 and rownorm.supported(x.unsqueeze(1)):
+        return rownorm.rms_rows(x.unsqueeze(1)).squeeze(1)
     return F.rms_norm(x, (x.shape[-1],))
 
 
@@ -96,8 +101,13 @@ class CausalSelfAttention(nn.Module):
         k = self.c_k(x).view(B, T, self.kv_heads, self.hd).transpose(1, 2)
         v = self.c_v(x).view(B, T, self.kv_heads, self.hd).transpose(1, 2)
         cos, sin = self.rotary(T, x.device)
-        q, k = _rotate(_rms(q), cos, sin), _rotate(_rms(k), cos, sin)
-        q = q * self.q_gain.to(q.dtype)[None, :, None, None]
+        if rownorm.supported(q, rope=True) and rownorm.supported(k, rope=True):
+            # norm, rotary turn and query gain in one launch per stream
+            q = rownorm.rms_rows(q, cos, sin, self.q_gain)
+            k = rownorm.rms_rows(k, cos, sin)
+        else:
+            q, k = _rotate(_rms(q), cos, sin), _rotate(_rms(k), cos, sin)
+            q = q * self.q_gain.to(q.dtype)[None, :, None, None]
         rep = self.heads // self.kv_heads
         k = k.repeat_interleave(rep, dim=1).contiguous()
         v = v.repeat_interleave(rep, dim=1).contiguous()

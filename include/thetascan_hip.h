@@ -42,8 +42,9 @@ extern "C" {
  *     fused with the output projection), ts_kmap_*, ts_anchor_*,
  *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3,
  *     TS_GN_SILU, ts_gn_act_* and ts_abs_mass_*; nothing earlier changed.
- * 15: ts_rownorm_fwd / ts_rownorm_bwd; nothing earlier changed. */
-#define TS_ABI_VERSION 15
+ * 15: ts_rownorm_fwd / ts_rownorm_bwd; nothing earlier changed.
+ * 16: ts_stack_heads; nothing earlier changed. */
+#define TS_ABI_VERSION 16
 
 enum ts_status {
   TS_OK = 0,
@@ -866,6 +867,22 @@ int ts_rownorm_fwd(const ts_rownorm_desc* desc, ts_strided x, const float* cos, 
 
 int ts_rownorm_bwd(const ts_rownorm_desc* desc, ts_strided x, ts_strided dy, const float* cos, const float* sin,
                    const float* gain, const float* rstd, void* dx, float* dg_row, hipStream_t stream);
+
+/* ------------------------------------------ stacked projection gradient */
+
+/* dst[b, t, s, h, :] = src[s][b, h, t, :] for s < n (1 <= n <= 4); a source
+ * whose ptr is NULL contributes zeros.  dst is a contiguous [B, T, n, H, d]
+ * tensor of ts_dtype `dtype`; each source is a [B,H,T,d] view (unit feature
+ * stride) whose rows and base are 16-byte aligned.  This is the backward of
+ * the split of a stacked q/k/v projection (block.py:593-594: one GEMM for the
+ * three streams): the three stream gradients gathered into the layout that
+ * the projection's input- and weight-gradient GEMMs read, in one pass. */
+typedef struct ts_stack_desc {
+  int32_t B, H, T, d, n;
+  int32_t dtype;
+} ts_stack_desc;
+
+int ts_stack_heads(const ts_stack_desc* desc, const ts_strided* src, void* dst, hipStream_t stream);
 
 /* out[i] = scale * (sum_{s<na} a[s*n + i] + sum_{s<nb} b[s*n + i]) for i < n,
  * written as ts_dtype out_dtype: sums the partial weight-gradient slots of

@@ -196,3 +196,98 @@ def test_normalized_read_matches_formula(cuda):
     assert rel_err(y, y_ref) < 1e-5
     for a, e in zip(dev, leaves):
         assert rel_err(a.grad, e.grad) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (BF, 2e-2)])
+def test_gated_read_matches_formula(cuda, dtype, tol):
+    """The read epilogue with the output gate, y = (resid + s num / (mass +
+    eps)) * silu(gate + bias), written token-major, against float64 autograd:
+    y, dnum, dmass, dresid, dgate and the bias gradient (fp32 at 1e-5, bf16
+    within one rounding)."""
+    from thetascan_amd._core.ops import gn
+
+    g = torch.Generator().manual_seed(11)
+    B, H, T, d = 2, 3, 70, 32
+    num, resid, gate = (torch.randn(B, H, T, d, generator=g, dtype=torch.float64) for _ in range(3))
+    mass = torch.rand(B, H, T, generator=g, dtype=torch.float64) + 0.3
+    bias = torch.randn(H * d, generator=g, dtype=torch.float64)
+    num, resid, gate = (t.to(dtype).double() for t in (num, resid, gate))
+    leaves = [t.clone().requires_grad_(True) for t in (num, mass, resid, gate, bias)]
+    n, m, r, gt, b = leaves
+    y_ref = (r + 0.5 * n / (m.unsqueeze(-1) + 1e-6)) * torch.nn.functional.silu(gt + b.view(H, 1, d))
+    dy = torch.randn(B, T, H, d, generator=g, dtype=torch.float64).transpose(1, 2)
+    y_ref.backward(dy)
+
+    dev = [t.detach().to(cuda, dtype if i != 1 else torch.float32).requires_grad_(True)
+           for i, t in enumerate((num, mass, resid, gate, bias))]
+    # the gate as the projection gives it: a [B,H,T,d] view of [B,T,H*d]
+    gate_tok = dev[3].detach().transpose(1, 2).contiguous().transpose(1, 2).requires_grad_(True)
+    y = gn.normalized_read(dev[0], dev[1], dev[2], s=0.5, gate=gate_tok, gate_bias=dev[4])
+    assert y.shape == (B, H, T, d) and y.transpose(1, 2).is_contiguous()
+    y.backward(dy.to(cuda, dtype))
+    torch.cuda.synchronize()
+    errs = {"y": rel_err(y.float(), y_ref), "dnum": rel_err(dev[0].grad.float(), n.grad),
+            "dmass": rel_err(dev[1].grad, m.grad), "dresid": rel_err(dev[2].grad.float(), r.grad),
+            "dgate": rel_err(gate_tok.grad.float(), gt.grad), "dbias": rel_err(dev[4].grad.float(), b.grad)}
+    print(f"gated read {dtype}: {errs}", flush=True)
+    for k, e in errs.items():
+        assert e < tol, (k, e)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (BF, 3e-2)])
+def test_gn_mixer_gate_in_the_read_epilogue(cuda, dtype, tol, monkeypatch):
+    """A single-view GN mixer with the output gate (the tanh GN workload's
+    layout at a small shape) applies the gate inside the HIP read epilogue;
+    its output and every gradient agree with the same mixer whose gate is a
+    separate product after the read (bf16: one rounding step apart)."""
+    import dataclasses
+
+    import thetascan_amd as ts
+    from thetascan_amd import _lib
+    from thetascan_amd._core.modules import block as block_mod
+
+    public = ts.ThetaScanConfig(
+        d_model=128, n_heads=2, memory_multiplier=2, family="gn",
+        gn=ts.GNConfig(nonlinearity="relu2", jacobian_steps=1, read_normalization="both_feature_mass"),
+        temporal=ts.TemporalConfig(mode="sum"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64))
+    cfg = dataclasses.replace(public._to_core_config(), nonlin="tanh", gn_damping=1e-2)
+    torch.manual_seed(0)
+    module = block_mod.ThetaScan(cfg)
+    g = torch.Generator().manual_seed(2)
+    with torch.no_grad():
+        for _, p in sorted(module.named_parameters()):
+            p.add_(torch.randn(p.shape, generator=g) * 0.05)
+    module = module.to(cuda, dtype)
+    x = torch.randn(2, 150, 128, generator=g).to(cuda, dtype)
+    dy = torch.randn(2, 150, 128, generator=g).to(cuda, dtype)
+
+    def run():
+        module.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        with _lib.record_launches() as recs:
+            y = module(xx)
+            y.backward(dy)
+            torch.cuda.synchronize()
+        grads = {n: p.grad.float().clone() for n, p in module.named_parameters() if p.grad is not None}
+        return y.float(), xx.grad.float(), grads, recs
+
+    requests = []
+    plain_gate = block_mod.ThetaScan._read_gate
+
+    def spy(self, *args):
+        requests.append(plain_gate(self, *args))
+        return requests[-1]
+
+    monkeypatch.setattr(block_mod.ThetaScan, "_read_gate", spy)
+    y1, dx1, g1, recs = run()
+    assert requests and requests[0] is not None and requests[0].applied, "the read epilogue did not take the gate"
+    assert any(r[0] == "ts_read_fwd" for r in recs)
+    monkeypatch.setattr(block_mod.ThetaScan, "_read_gate", lambda self, *a: None)
+    y0, dx0, g0, _ = run()
+    assert set(g1) == set(g0)
+    errs = {"y": rel_err(y1, y0), "dx": rel_err(dx1, dx0)}
+    errs.update({n: rel_err(g1[n], g0[n]) for n in g0})
+    worst = max(errs, key=errs.get)
+    print(f"gate in read {dtype}: worst {worst} {errs[worst]:.3g}", flush=True)
+    for k, e in errs.items():
+        assert e < tol, (k, e)

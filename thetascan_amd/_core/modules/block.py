@@ -25,7 +25,7 @@ import torch.nn.functional as F
 from ..config import ThetaScanConfig
 from ...state import ThetaScanState, config_fingerprint
 from ..ops import composed, features, fused, gn, interface, maps, prologue, stream
-from ..ops.linear import linear
+from ..ops.linear import linear, stack_heads
 from ..ops.interface import Accumulator, FadeFast, FadeStale, NullAccumulator, resolve_backend
 from .gates import DecayGate, OutGate
 from .norms import l2norm
@@ -109,9 +109,9 @@ def _expansion_fingerprint(*, key: str, effective_hidden: int, feature_expansion
 class _SplitQKV(torch.autograd.Function):
     """q, k, v [B,H,T,d] views of a stacked [B,T,3,H,d] projection (block.py:594).
     The backward writes the three stream gradients, whatever their strides,
-    into one [B,T,3,H,d] gradient in one pass, in the layout the projection's
-    backward GEMMs read (autograd's own unbind and permute backward stack
-    them head-major and then copy that into this layout)."""
+    into one [B,T,3,H,d] gradient in one pass (ts_stack_heads), in the layout
+    the projection's backward GEMMs read (autograd's own unbind and permute
+    backward stack them head-major and then copy that into this layout)."""
 
     @staticmethod
     def forward(ctx, proj):
@@ -120,9 +120,7 @@ class _SplitQKV(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dq, dk, dv):
-        like = next(g for g in (dq, dk, dv) if g is not None)
-        parts = [torch.zeros_like(like) if g is None else g for g in (dq, dk, dv)]
-        return torch.stack([g.transpose(1, 2) for g in parts], dim=2)
+        return stack_heads([dq, dk, dv])
 
 class ThetaScan(nn.Module):
     """Drop-in token mixer x[B,T,D] -> y[B,T,D] on MI355X."""
@@ -554,9 +552,26 @@ class ThetaScan(nn.Module):
         weights = self._weights()
         sharp = self.kernel_sharpness()
         controls = self.kernel_controls()
+        gate = self._read_gate(x, views, weights, q)
         reads = composed.memory_forward(weights, cfg, k, v_w, q, tuple(views), hrot=hrot, gain=sharp,
-                                        controls=controls)
+                                        controls=controls, out_gate=gate)
+        if gate is not None and gate.applied:
+            # the read epilogue applied the output gate and wrote its output
+            # token-major: the projection reads it as [B,T,H*d] in place
+            return linear(reads[0].transpose(1, 2).reshape(B, T, H * d), self.proj_out.weight)
         return self._blend_and_project(x, reads, etas)
+
+    def _read_gate(self, x: torch.Tensor, views, weights, q: torch.Tensor):
+        """The output gate (block.py:721-722) as a request that the HIP read
+        epilogue of a single-view GN memory applies (composed.GateRequest), or
+        None where the gate stays a product after the read."""
+        cfg = self.cfg
+        if self.ogate is None or cfg.read_fade or len(views) != 1 or not gn.read_eligible(cfg, weights, q):
+            return None
+        B, T, _ = x.shape
+        lin = self.ogate.g.lin
+        pre = linear(x, lin.weight).view(B, T, cfg.n_heads, cfg.head_dim).transpose(1, 2)
+        return composed.GateRequest(pre, lin.bias)
 
     def _temporal_views(self, x: torch.Tensor, backend: str):
         """The memory's temporal views (interface.py:198-327): the accumulator

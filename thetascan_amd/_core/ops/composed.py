@@ -25,8 +25,9 @@ value-anchor deposit (``maps.anchor_code``), the kernel feature maps
 depth-1 GN writes and reads of the HIP GN kernels (``gn.write``,
 ``gn.read_stage``), every other GN block's RMSNorm, nonlinearity and Jacobian
 scales (``gn.act_rows``: any depth, both Gauss-Newton steps, SwiGLU), the
-normalized read epilogue in ``gn.normalized_read`` (HIP) and the per-head
-GEMMs in ``linear.head_matmul``.  The remaining elementwise work (the
+normalized read epilogue in ``gn.normalized_read`` (HIP; with one view it
+also applies the output gate, see ``GateRequest``) and the per-head GEMMs in
+``linear.head_matmul``.  The remaining elementwise work (the
 products of the scales with the GEMM outputs, the Jacobi division) is torch
 on the GPU.
 """
@@ -41,6 +42,22 @@ import torch.nn.functional as F
 from . import gn, interface, kernel_features, maps
 from .linear import head_matmul
 from ..modules.norms import rmsnorm
+
+
+# ------------------------------------------------------------------ output gate
+
+class GateRequest:
+    """An output gate the read epilogue may apply: ``pre`` is the [B,H,T,d]
+    view of the gate's pre-activation x W_g^T (without its bias), ``bias`` the
+    gate bias [H*d].  A depth-1 GN read of a single view applies
+    silu(pre + bias) inside its HIP epilogue and writes its output token-major
+    (``gn.normalized_read``), then sets ``applied``; otherwise the caller
+    applies the gate itself."""
+
+    def __init__(self, pre: torch.Tensor, bias: torch.Tensor | None):
+        self.pre = pre
+        self.bias = bias
+        self.applied = False
 
 
 # ------------------------------------------------------------------ per-head products
@@ -146,12 +163,13 @@ class FastNet:
     ``gain``: the learned softmax sharpness or None; ``controls``: the kernel
     feature map's learned controls."""
 
-    def __init__(self, layers, cfg, hrot=None, gain=None, controls=None):
+    def __init__(self, layers, cfg, hrot=None, gain=None, controls=None, out_gate=None):
         self.layers = layers
         self.cfg = cfg
         self.hrot = hrot
         self.gain = gain
         self.controls = controls or {}
+        self.out_gate = out_gate
         self.s = 1.0 / math.sqrt(cfg.depth)
         self.width = layers[0][1].shape[-1]
         self.gated = cfg.nonlin == "swiglu"
@@ -380,11 +398,13 @@ class FastNet:
     def recall(self, q, steps, views):
         """f_theta_t(q_t) for every temporal view (engine.py:345-544)."""
         outs = [q] * len(views)
+        gate = self.out_gate if len(views) == 1 else None
         for l in range(len(self.layers)):
+            last = gate if l == len(self.layers) - 1 else None
             if all(x is outs[0] for x in outs):
-                outs = self._read_layer(list(views), l, outs[0], steps)
+                outs = self._read_layer(list(views), l, outs[0], steps, last)
             else:
-                outs = [self._read_layer([view], l, x, steps)[0] for view, x in zip(views, outs)]
+                outs = [self._read_layer([view], l, x, steps, last)[0] for view, x in zip(views, outs)]
         return tuple(outs)
 
     def _features_at(self, l, main, gate):
@@ -439,11 +459,12 @@ class FastNet:
             mems = [_per_head(mem, book.to(mem.dtype), False) for mem in mems]
         return mems
 
-    def _read_layer(self, group, l, x, steps):
-        """One depth level for the views of ``group``, which share the input ``x``."""
+    def _read_layer(self, group, l, x, steps, gate=None):
+        """One depth level for the views of ``group``, which share the input
+        ``x``; ``gate`` is a ``GateRequest`` the last level may apply."""
         cfg = self.cfg
         if gn.read_eligible(cfg, self.layers, x):
-            return self._read_layer_gn(group, l, x, steps)
+            return self._read_layer_gn(group, l, x, steps, gate)
         W1, W2, Wg = self.layers[l]
         m = self.width
         main = _per_head(x, W1, True)
@@ -502,10 +523,11 @@ class FastNet:
             pairs = [(num, None) for num in interface.scan_views(group, hq, dep.feat, dep.pay, "m")]
         return [gn.normalized_read(num, mass, resid, s=self.s, eps=cfg.eps) for num, mass in pairs]
 
-    def _read_layer_gn(self, group, l, x, steps):
+    def _read_layer_gn(self, group, l, x, steps, gate=None):
         """A depth-1 GN read on the HIP read stages (engine.py:467-544): stage
         one corrects the pre-activation, stage two reads LA2 with the
-        corrected features."""
+        corrected features; the epilogue of a single view applies ``gate``
+        where it fits."""
         cfg = self.cfg
         W1, W2, Wg = self.layers[l]
         tau = Wg[..., 0] if cfg.learn_thresh else None
@@ -533,7 +555,12 @@ class FastNet:
                 mass2 = key_mass(cfg, view, hq, dep.feat, mass2)
             else:
                 num2, mass2 = interface.scan_views((view,), hq, dep.feat, dep.pay, "m")[0], None
-            outs.append(gn.normalized_read(num2, mass2, resid, s=self.s, eps=cfg.eps))
+            if gate is not None and len(group) == 1 and gn.gate_fits(num2, resid, gate.pre):
+                outs.append(gn.normalized_read(num2, mass2, resid, s=self.s, eps=cfg.eps, gate=gate.pre,
+                                               gate_bias=gate.bias))
+                gate.applied = True
+            else:
+                outs.append(gn.normalized_read(num2, mass2, resid, s=self.s, eps=cfg.eps))
         return outs
 
 
@@ -544,8 +571,9 @@ class _Written(Deposit):
     h0: torch.Tensor | None = None
 
 
-def memory_forward(layers, cfg, k, v, q, views, hrot=None, gain=None, controls=None):
+def memory_forward(layers, cfg, k, v, q, views, hrot=None, gain=None, controls=None, out_gate=None):
     """The memory read f_theta_t(q_t) of every temporal view after writing
-    keys ``k`` and values ``v`` (engine.py:260-553)."""
-    net = FastNet(layers, cfg, hrot=hrot, gain=gain, controls=controls)
+    keys ``k`` and values ``v`` (engine.py:260-553).  ``out_gate`` is an
+    optional ``GateRequest`` (its ``applied`` tells whether the read took it)."""
+    net = FastNet(layers, cfg, hrot=hrot, gain=gain, controls=controls, out_gate=out_gate)
     return net.recall(q, net.deposits(k, v), views)

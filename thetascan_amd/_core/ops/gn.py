@@ -331,51 +331,76 @@ def read_stage(q, w1, w2=None, tau=None, num=None, mass=None, *, corr: int = REA
     return h, (resid if want_resid else None)
 
 
-def _normalized_read_forward(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor, s: float,
+def _normalized_read_forward(num: torch.Tensor, mass: torch.Tensor | None, resid: torch.Tensor,
+                             gate: torch.Tensor | None, gate_bias: torch.Tensor | None, s: float,
                              eps: float) -> torch.Tensor:
     """y = resid + s * num / (mass + eps)  (or + s * num without mass): the read
     epilogue of engine.py:440-442, 538-544 on ts_read_fwd.  An fp32 numerator (a
     difference of views) is read in fp32, then rounded once to the dtype of
-    ``resid``."""
+    ``resid``.  With ``gate`` (the [B,H,T,d] view of the output gate's
+    pre-activation x W_g^T, same dtype as num) y is also multiplied by
+    silu(gate + gate_bias) (block.py:721-722, gates.py:34-40) and written
+    token-major: a [B,H,T,d] view of [B,T,H,d] memory, which the output
+    projection reads as [B,T,H*d] without a copy."""
     from . import fused
 
     nk, rk = _rows(num), _rows(resid.to(num.dtype))
     mk = None if mass is None else mass.detach().to(torch.float32)
-    y = torch.empty_like(nk)
-    fused.read_fwd(nk, mk, rk, None, y, s, eps)
-    return y.to(resid.dtype)
+    if gate is None:
+        y = torch.empty_like(nk)
+        fused.read_fwd(nk, mk, rk, None, y, s, eps)
+        return y.to(resid.dtype)
+    B, H, T, d = nk.shape
+    y = torch.empty(B, T, H, d, dtype=nk.dtype, device=nk.device).transpose(1, 2)
+    gb = None if gate_bias is None else gate_bias.detach().to(torch.float32).contiguous()
+    fused.read_fwd(nk, mk, rk, _rows(gate), y, s, eps, gbias=gb)
+    return y
 
 
-def _normalized_read_fake(num, mass, resid, s, eps):
-    return resid.new_empty(num.shape)
+def _normalized_read_fake(num, mass, resid, gate, gate_bias, s, eps):
+    if gate is None:
+        return resid.new_empty(num.shape)
+    B, H, T, d = num.shape
+    return num.new_empty(B, T, H, d).transpose(1, 2)
 
 
 def _normalized_read_backward_impl(dy: torch.Tensor, num: torch.Tensor, mass: torch.Tensor | None,
-                                   resid: torch.Tensor, s: float, eps: float) -> list[torch.Tensor]:
+                                   resid: torch.Tensor, gate: torch.Tensor | None, gate_bias: torch.Tensor | None,
+                                   s: float, eps: float) -> list[torch.Tensor]:
     from . import fused
 
     nk, rk = _rows(num), _rows(resid.to(num.dtype))
     mk = None if mass is None else mass.detach().to(torch.float32)
-    dnum, dmass, (dresid, _), _, _ = fused.read_bwd(nk, mk, rk, None, _rows(dy.to(nk.dtype)), s, eps)
+    gk = None if gate is None else _rows(gate)
+    gb = None if gate_bias is None else gate_bias.detach().to(torch.float32).contiguous()
+    dnum, dmass, (dresid, _), dg, dgb = fused.read_bwd(
+        nk, mk, rk, gk, _rows(dy.to(nk.dtype)), s, eps, gbias=gb,
+        gbias_grad=None if gate_bias is None else gate_bias.dtype)
     dmass = num.new_empty(0) if dmass is None else dmass.to(mass.dtype)
-    return [dnum, dmass, dresid.to(resid.dtype)]
+    return [dnum, dmass, dresid.to(resid.dtype), num.new_empty(0) if dg is None else dg,
+            num.new_empty(0) if dgb is None else dgb]
 
 
-def _normalized_read_backward_fake(dy, num, mass, resid, s, eps):
+def _normalized_read_backward_fake(dy, num, mass, resid, gate, gate_bias, s, eps):
+    B, H, T, d = num.shape
     return [num.new_empty(num.shape), num.new_empty(0) if mass is None else mass.new_empty(mass.shape),
-            resid.new_empty(resid.shape)]
+            resid.new_empty(resid.shape),
+            num.new_empty(0) if gate is None else num.new_empty(B, T, H, d).transpose(1, 2),
+            num.new_empty(0) if gate_bias is None else gate_bias.new_empty(gate_bias.shape)]
 
 
 def _normalized_read_setup(ctx, inputs, output):
-    num, mass, resid, s, eps = inputs
+    num, mass, resid, gate, gate_bias, s, eps = inputs
     ctx.args = (s, eps)
-    ctx.save_for_backward(num, mass, resid)
+    ctx.need_bias = gate_bias is not None and gate_bias.requires_grad
+    ctx.save_for_backward(num, mass, resid, gate, gate_bias)
 
 
 def _normalized_read_backward(ctx, dy, bwd):
-    num, mass, resid = ctx.saved_tensors
-    dnum, dmass, dresid = bwd(dy, num, mass, resid, *ctx.args)
-    return dnum, (None if mass is None else dmass), dresid, None, None
+    num, mass, resid, gate, gate_bias = ctx.saved_tensors
+    dnum, dmass, dresid, dg, dgb = bwd(dy, num, mass, resid, gate, gate_bias, *ctx.args)
+    return (dnum, None if mass is None else dmass, dresid, None if gate is None else dg,
+            dgb if ctx.need_bias else None, None, None)
 
 
 _normalized_read_op = HipOp("normalized_read", forward=_normalized_read_forward,
@@ -384,9 +409,17 @@ _normalized_read_op = HipOp("normalized_read", forward=_normalized_read_forward,
                             backward=_normalized_read_backward)
 
 
-def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6):
-    """Read epilogue of one view on the GPU (ts_read_fwd / ts_read_bwd)."""
-    return _normalized_read_op(num, mass, resid, float(s), float(eps))
+def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6, gate=None, gate_bias=None):
+    """Read epilogue of one view on the GPU (ts_read_fwd / ts_read_bwd),
+    optionally with the output gate (see :func:`_normalized_read_forward`)."""
+    return _normalized_read_op(num, mass, resid, gate, gate_bias, float(s), float(eps))
+
+
+def gate_fits(num: torch.Tensor, resid: torch.Tensor, gate: torch.Tensor) -> bool:
+    """Whether :func:`normalized_read` can apply the output gate to this read:
+    numerator, residual and gate of one dtype and shape (a host query)."""
+    return (num.is_cuda and num.dtype in (torch.bfloat16, torch.float32) and resid.dtype == num.dtype
+            and gate.dtype == num.dtype and gate.shape == num.shape and resid.shape == num.shape)
 
 
 def read_eligible(cfg, weights, q: torch.Tensor) -> bool:

@@ -80,6 +80,35 @@ def column_sum(x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return slot_sum(parts, dtype, (cols,))
 
 
+def stack_heads(grads) -> torch.Tensor:
+    """[B,T,n,H,d] from n stream gradients [B,H,T,d] (None: zeros), the
+    layout of a stacked projection's output gradient: one ts_stack_heads
+    launch on the GPU for bf16 / fp32 rows that are 16-byte aligned, else (and
+    while torch.compile traces, which cannot enter a ctypes call) the torch
+    stack of the transposed streams."""
+    like = next(g for g in grads if g is not None)
+    es = like.element_size()
+    vec = 16 // es
+
+    def fits(g):
+        return g is None or (g.is_cuda and g.dtype == like.dtype and g.shape == like.shape and g.stride(-1) == 1
+                             and g.data_ptr() % 16 == 0 and all(st % vec == 0 for st in g.stride()[:3]))
+
+    B, H, T, d = like.shape
+    if (torch.compiler.is_compiling() or not (like.dtype in (torch.bfloat16, torch.float32) and d % vec == 0
+                                              and len(grads) <= 4 and all(fits(g) for g in grads))):
+        parts = [torch.zeros_like(like) if g is None else g for g in grads]
+        return torch.stack([g.transpose(1, 2) for g in parts], dim=2)
+    out = torch.empty(B, T, len(grads), H, d, dtype=like.dtype, device=like.device)
+    src = (_lib.Strided * len(grads))(*[_lib.strided(g) for g in grads])
+    desc = _lib.StackDesc(B, H, T, d, len(grads), _lib.dtype_code(like.dtype))
+    lib = _lib.load()
+    with _lib.timed("ts_stack_heads", lambda: 2 * out.numel() * es):
+        status = lib.ts_stack_heads(ctypes.byref(desc), src, out.data_ptr(), _lib.stream_handle(like.device))
+    _lib.check(status, "ts_stack_heads")
+    return out
+
+
 # F.linear whose backward forms the weight gradient as a split-K GEMM, and the
 # per-head GEMMs of the composed path, as autograd nodes (dispatch.HipOp: a
 # torch.library custom op under torch.compile -- their backward reaches the

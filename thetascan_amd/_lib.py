@@ -295,6 +295,10 @@ class RowNormDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "W", "dtype", "rope")] + [("eps", ctypes.c_float)]
 
 
+class StackDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "d", "n", "dtype")]
+
+
 class GnActDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "m", "dtype", "act", "has_tau")] + [
         ("eps", ctypes.c_float)]
@@ -582,7 +586,8 @@ def load() -> ctypes.CDLL:
         lib.ts_retention_workspace_bytes.argtypes = [P(RetentionDesc), P(ctypes.c_size_t)]
         lib.ts_retention_grad.argtypes = [P(RetentionDesc), P(RetentionIO), ctypes.c_void_p, ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_void_p]
-        if lib.ts_abi_version() != 15:
+        lib.ts_stack_heads.argtypes = [P(StackDesc), P(Strided), ctypes.c_void_p, ctypes.c_void_p]
+        if lib.ts_abi_version() != 16:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

@@ -624,6 +624,37 @@ __global__ __launch_bounds__(256) void col_sums_kernel(const E* x, int64_t rows,
   }
 }
 
+// dst[b][t][s][h][:] = src_s[b][h][t][:]: grid x walks the [T][H][d/VEC]
+// vectors of one (stream s = blockIdx.y, batch b = blockIdx.z), so the
+// source descriptor is uniform per block; each thread moves 16 bytes.  Reads
+// are whole source rows (d * sizeof(E) contiguous bytes), writes one
+// contiguous [H*d] run per token.
+struct StackP {
+  int B, H, T, d, n;
+  ts_strided src[4];
+  void* dst;
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void stack_heads_kernel(StackP p) {
+  constexpr int VEC = 16 / (int)sizeof(E);
+  const int s = blockIdx.y, b = blockIdx.z;
+  const int dv = p.d / VEC;
+  const int64_t per = (int64_t)p.T * p.H * dv;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= per) return;
+  const int c = (int)(i % dv);
+  const int64_t r = i / dv;
+  const int h = (int)(r % p.H);
+  const int t = (int)(r / p.H);
+  const ts_strided src = p.src[s];
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (src.ptr)
+    v = *(const uint4*)((const E*)src.ptr + (int64_t)b * src.sb + (int64_t)h * src.sh + (int64_t)t * src.st + c * VEC);
+  E* dst = (E*)p.dst + (((int64_t)b * p.T + t) * p.n + s) * (int64_t)p.H * p.d + (int64_t)h * p.d + c * VEC;
+  *(uint4*)dst = v;
+}
+
 }  // namespace ts
 
 namespace {
@@ -910,6 +941,32 @@ int ts_col_sums(const void* x, int32_t dtype, int64_t rows, int32_t cols, int64_
     hipLaunchKernelGGL(ts::col_sums_kernel<float>, dim3((unsigned)slices), dim3(256), 0, stream, (const float*)x,
                        rows, cols, row_stride, parts, rows_per_block);
   return finish("col_sums");
+}
+
+int ts_stack_heads(const ts_stack_desc* d, const ts_strided* src, void* dst, hipStream_t stream) {
+  if (!d || !src || !dst || d->B < 0 || d->H < 1 || d->T < 0 || d->d < 1 || d->n < 1 || d->n > 4)
+    return fail(TS_ERR_VALUE, "stack_heads: bad arguments");
+  if (d->dtype != TS_BF16 && d->dtype != TS_F32) return fail(TS_ERR_VALUE, "stack_heads: unknown dtype");
+  const int vec = d->dtype == TS_BF16 ? 8 : 4;
+  if (d->d % vec || ((uintptr_t)dst & 15u)) return fail(TS_ERR_VALUE, "stack_heads: rows must be 16-byte aligned");
+  ts::StackP p;
+  memset(&p, 0, sizeof(p));
+  p.B = d->B; p.H = d->H; p.T = d->T; p.d = d->d; p.n = d->n; p.dst = dst;
+  for (int s = 0; s < d->n; ++s) {
+    const ts_strided& x = src[s];
+    if (x.ptr && (((uintptr_t)x.ptr & 15u) || x.sb % vec || x.sh % vec || x.st % vec))
+      return fail(TS_ERR_VALUE, "stack_heads: source %d rows must be 16-byte aligned", s);
+    p.src[s] = x;
+  }
+  const int64_t per = (int64_t)d->T * d->H * (d->d / vec);
+  if (d->B == 0 || per == 0) return TS_OK;
+  if ((per + 255) / 256 > 0x7fffffff || d->B > 65535) return fail(TS_ERR_NOT_IMPLEMENTED, "stack_heads: too large");
+  const dim3 grid((unsigned)((per + 255) / 256), (unsigned)d->n, (unsigned)d->B);
+  if (d->dtype == TS_BF16)
+    hipLaunchKernelGGL(ts::stack_heads_kernel<ts::bf16>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(ts::stack_heads_kernel<float>, grid, dim3(256), 0, stream, p);
+  return finish("stack_heads");
 }
 
 // Segments of the scan order: enough (b, h, segment, feature) threads to

@@ -234,23 +234,36 @@ def test_gated_read_matches_formula(cuda, dtype, tol):
         assert e < tol, (k, e)
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (BF, 3e-2)])
-def test_gn_mixer_gate_in_the_read_epilogue(cuda, dtype, tol, monkeypatch):
-    """A single-view GN mixer with the output gate (the tanh GN workload's
-    layout at a small shape) applies the gate inside the HIP read epilogue;
-    its output and every gradient agree with the same mixer whose gate is a
-    separate product after the read (bf16: one rounding step apart)."""
+def _gated_config(kind):
     import dataclasses
 
     import thetascan_amd as ts
+
+    if kind == "gn_tanh":
+        public = ts.ThetaScanConfig(
+            d_model=128, n_heads=2, memory_multiplier=2, family="gn",
+            gn=ts.GNConfig(nonlinearity="relu2", jacobian_steps=1, read_normalization="both_feature_mass"),
+            temporal=ts.TemporalConfig(mode="sum"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64))
+        return dataclasses.replace(public._to_core_config(), nonlin="tanh", gn_damping=1e-2)
+    public = ts.ThetaScanConfig(
+        d_model=128, n_heads=2, memory_multiplier=2, family="kernel",
+        kernel=ts.KernelConfig(feature_map="projected_bspline", read_normalization="key_mass"),
+        temporal=ts.TemporalConfig(mode="ema"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64))
+    return public._to_core_config()
+
+
+@pytest.mark.parametrize("kind", ["gn_tanh", "kernel_bspline_ema"])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (BF, 3e-2)])
+def test_mixer_gate_in_the_read_epilogue(cuda, dtype, tol, kind, monkeypatch):
+    """A single-view mixer on the composed path with the output gate (the
+    tanh GN workload's layout, and a B-spline kernel memory with an EMA view,
+    at small shapes) applies the gate inside the HIP read epilogue; its
+    output and every gradient agree with the same mixer whose gate is a
+    separate product after the read (bf16: one rounding step apart)."""
     from thetascan_amd import _lib
     from thetascan_amd._core.modules import block as block_mod
 
-    public = ts.ThetaScanConfig(
-        d_model=128, n_heads=2, memory_multiplier=2, family="gn",
-        gn=ts.GNConfig(nonlinearity="relu2", jacobian_steps=1, read_normalization="both_feature_mass"),
-        temporal=ts.TemporalConfig(mode="sum"), runtime=ts.RuntimeConfig(backend="hip", scan_chunk=64))
-    cfg = dataclasses.replace(public._to_core_config(), nonlin="tanh", gn_damping=1e-2)
+    cfg = _gated_config(kind)
     torch.manual_seed(0)
     module = block_mod.ThetaScan(cfg)
     g = torch.Generator().manual_seed(2)
@@ -288,6 +301,6 @@ def test_gn_mixer_gate_in_the_read_epilogue(cuda, dtype, tol, monkeypatch):
     errs = {"y": rel_err(y1, y0), "dx": rel_err(dx1, dx0)}
     errs.update({n: rel_err(g1[n], g0[n]) for n in g0})
     worst = max(errs, key=errs.get)
-    print(f"gate in read {dtype}: worst {worst} {errs[worst]:.3g}", flush=True)
+    print(f"gate in read {kind} {dtype}: worst {worst} {errs[worst]:.3g}", flush=True)
     for k, e in errs.items():
         assert e < tol, (k, e)

@@ -552,7 +552,7 @@ class ThetaScan(nn.Module):
         weights = self._weights()
         sharp = self.kernel_sharpness()
         controls = self.kernel_controls()
-        gate = self._read_gate(x, views, weights, q)
+        gate = self._read_gate(x, views)
         reads = composed.memory_forward(weights, cfg, k, v_w, q, tuple(views), hrot=hrot, gain=sharp,
                                         controls=controls, out_gate=gate)
         if gate is not None and gate.applied:
@@ -561,17 +561,16 @@ class ThetaScan(nn.Module):
             return linear(reads[0].transpose(1, 2).reshape(B, T, H * d), self.proj_out.weight)
         return self._blend_and_project(x, reads, etas)
 
-    def _read_gate(self, x: torch.Tensor, views, weights, q: torch.Tensor):
+    def _read_gate(self, x: torch.Tensor, views):
         """The output gate (block.py:721-722) as a request that the HIP read
-        epilogue of a single-view GN memory applies (composed.GateRequest), or
-        None where the gate stays a product after the read."""
+        epilogue of a single view may apply (composed.GateRequest), or None
+        where the gate stays a product after the read (banks: after the
+        blend)."""
         cfg = self.cfg
-        if self.ogate is None or cfg.read_fade or len(views) != 1 or not gn.read_eligible(cfg, weights, q):
+        if self.ogate is None or cfg.read_fade or len(views) != 1 or not x.is_cuda:
             return None
-        B, T, _ = x.shape
         lin = self.ogate.g.lin
-        pre = linear(x, lin.weight).view(B, T, cfg.n_heads, cfg.head_dim).transpose(1, 2)
-        return composed.GateRequest(pre, lin.bias)
+        return composed.GateRequest(x, lin.weight, lin.bias, cfg.n_heads, cfg.head_dim)
 
     def _temporal_views(self, x: torch.Tensor, backend: str):
         """The memory's temporal views (interface.py:198-327): the accumulator

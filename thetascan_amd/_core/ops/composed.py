@@ -47,17 +47,40 @@ from ..modules.norms import rmsnorm
 # ------------------------------------------------------------------ output gate
 
 class GateRequest:
-    """An output gate the read epilogue may apply: ``pre`` is the [B,H,T,d]
-    view of the gate's pre-activation x W_g^T (without its bias), ``bias`` the
-    gate bias [H*d].  A depth-1 GN read of a single view applies
-    silu(pre + bias) inside its HIP epilogue and writes its output token-major
-    (``gn.normalized_read``), then sets ``applied``; otherwise the caller
+    """An output gate silu(x W_g^T + b) (block.py:721-722) that the read
+    epilogue of a single view may apply.  ``pre`` is the [B,H,T,d] view of
+    the pre-activation x W_g^T without the bias, formed on first use (so a
+    read that does not take the gate costs no GEMM).  A read that applies
+    silu(pre + bias) inside its HIP epilogue writes its output token-major
+    (``gn.normalized_read``) and sets ``applied``; otherwise the caller
     applies the gate itself."""
 
-    def __init__(self, pre: torch.Tensor, bias: torch.Tensor | None):
-        self.pre = pre
-        self.bias = bias
+    def __init__(self, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, heads: int, width: int):
+        self.x, self.weight, self.bias = x, weight, bias
+        self.heads, self.width = heads, width
         self.applied = False
+        self._pre = None
+
+    @property
+    def pre(self) -> torch.Tensor:
+        if self._pre is None:
+            from .linear import linear
+
+            B, T, _ = self.x.shape
+            self._pre = linear(self.x, self.weight).view(B, T, self.heads, self.width).transpose(1, 2)
+        return self._pre
+
+    def fits(self, num: torch.Tensor, resid: torch.Tensor) -> bool:
+        """Whether the HIP read epilogue can apply the gate to this read."""
+        B, T, _ = self.x.shape
+        return (num.is_cuda and num.dtype in (torch.bfloat16, torch.float32) and resid.dtype == num.dtype
+                and self.x.dtype == num.dtype and self.weight.dtype == num.dtype
+                and tuple(num.shape) == (B, self.heads, T, self.width) and resid.shape == num.shape)
+
+    def read(self, num, mass, resid, s: float, eps: float) -> torch.Tensor:
+        """The gated read epilogue (marks the gate applied)."""
+        self.applied = True
+        return gn.normalized_read(num, mass, resid, s=s, eps=eps, gate=self.pre, gate_bias=self.bias)
 
 
 # ------------------------------------------------------------------ per-head products
@@ -173,6 +196,11 @@ class FastNet:
         self.s = 1.0 / math.sqrt(cfg.depth)
         self.width = layers[0][1].shape[-1]
         self.gated = cfg.nonlin == "swiglu"
+
+    def _scaled(self, t: torch.Tensor) -> torch.Tensor:
+        """s * t for the depth scale s = 1 / sqrt(depth): t itself at depth 1
+        (the product by 1.0 is the identity, bit for bit)."""
+        return t if self.s == 1.0 else self.s * t
 
     # ---- pieces of one block
 
@@ -344,7 +372,7 @@ class FastNet:
             if own is not None:
                 u = u + own[l].pay * (own[l].h0 * act.h).sum(-1, keepdim=True)
             acts.append(act)
-            x = x + self.s * u
+            x = x + self._scaled(u)
         return acts, x
 
     def solve(self, acts, residual):
@@ -384,12 +412,12 @@ class FastNet:
         step = []
         for l, act in enumerate(acts):
             feat = self.rotate(act.h)
-            pay = self.s * lam
+            pay = self._scaled(lam)
             if cast:
                 feat = feat.to(pay.dtype)
             dep = _Written(feat, pay)
             if self.cfg.fast_w1:
-                dep = _Written(feat, pay, act.inp, self.s * self.jac_payload(l, act, lam), act.h)
+                dep = _Written(feat, pay, act.inp, self._scaled(self.jac_payload(l, act, lam)), act.h)
             step.append(dep)
         return step
 
@@ -459,12 +487,12 @@ class FastNet:
             mems = [_per_head(mem, book.to(mem.dtype), False) for mem in mems]
         return mems
 
-    def _read_layer(self, group, l, x, steps, gate=None):
+    def _read_layer(self, group, l, x, steps, out_gate=None):
         """One depth level for the views of ``group``, which share the input
-        ``x``; ``gate`` is a ``GateRequest`` the last level may apply."""
+        ``x``; ``out_gate`` is a ``GateRequest`` the last level may apply."""
         cfg = self.cfg
         if gn.read_eligible(cfg, self.layers, x):
-            return self._read_layer_gn(group, l, x, steps, gate)
+            return self._read_layer_gn(group, l, x, steps, out_gate)
         W1, W2, Wg = self.layers[l]
         m = self.width
         main = _per_head(x, W1, True)
@@ -504,15 +532,15 @@ class FastNet:
                     and (not cfg.read_norm or cfg.read_norm_mode == "key_mass")):
                 # x + s (W2 h + num / (mass + eps)) per view in the HIP read
                 # epilogue, the residual x + s W2 h formed once for all views
-                return self._normalized_reads(group, l, hq, torch.add(x, base, alpha=self.s), steps)
-            return [x + self.s * (base + mem) for mem in self._memory(group, l, hq, steps)]
+                return self._normalized_reads(group, l, hq, torch.add(x, base, alpha=self.s), steps, out_gate)
+            return [x + self._scaled(base + mem) for mem in self._memory(group, l, hq, steps)]
         outs = []
         for view, a, b in zip(group, mains, gates):
             h, hq = self._features_at(l, a, b)
-            outs.append(x + self.s * (self.out(l, h) + self._memory([view], l, hq, steps)[0]))
+            outs.append(x + self._scaled(self.out(l, h) + self._memory([view], l, hq, steps)[0]))
         return outs
 
-    def _normalized_reads(self, group, l, hq, resid, steps):
+    def _normalized_reads(self, group, l, hq, resid, steps, out_gate=None):
         cfg = self.cfg
         dep = steps[0][l]
         if cfg.read_norm:
@@ -521,13 +549,15 @@ class FastNet:
                      for view, (num, mass) in zip(group, interface.scan_views_mass(group, hq, dep.feat, dep.pay, "m"))]
         else:
             pairs = [(num, None) for num in interface.scan_views(group, hq, dep.feat, dep.pay, "m")]
+        if out_gate is not None and len(pairs) == 1 and out_gate.fits(pairs[0][0], resid):
+            return [out_gate.read(pairs[0][0], pairs[0][1], resid, self.s, cfg.eps)]
         return [gn.normalized_read(num, mass, resid, s=self.s, eps=cfg.eps) for num, mass in pairs]
 
-    def _read_layer_gn(self, group, l, x, steps, gate=None):
+    def _read_layer_gn(self, group, l, x, steps, out_gate=None):
         """A depth-1 GN read on the HIP read stages (engine.py:467-544): stage
         one corrects the pre-activation, stage two reads LA2 with the
-        corrected features; the epilogue of a single view applies ``gate``
-        where it fits."""
+        corrected features; the epilogue of a single view applies
+        ``out_gate`` where it fits."""
         cfg = self.cfg
         W1, W2, Wg = self.layers[l]
         tau = Wg[..., 0] if cfg.learn_thresh else None
@@ -555,10 +585,8 @@ class FastNet:
                 mass2 = key_mass(cfg, view, hq, dep.feat, mass2)
             else:
                 num2, mass2 = interface.scan_views((view,), hq, dep.feat, dep.pay, "m")[0], None
-            if gate is not None and len(group) == 1 and gn.gate_fits(num2, resid, gate.pre):
-                outs.append(gn.normalized_read(num2, mass2, resid, s=self.s, eps=cfg.eps, gate=gate.pre,
-                                               gate_bias=gate.bias))
-                gate.applied = True
+            if out_gate is not None and len(group) == 1 and out_gate.fits(num2, resid):
+                outs.append(out_gate.read(num2, mass2, resid, self.s, cfg.eps))
             else:
                 outs.append(gn.normalized_read(num2, mass2, resid, s=self.s, eps=cfg.eps))
         return outs

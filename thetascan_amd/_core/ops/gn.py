@@ -415,13 +415,6 @@ def normalized_read(num, mass, resid, *, s: float = 1.0, eps: float = 1e-6, gate
     return _normalized_read_op(num, mass, resid, gate, gate_bias, float(s), float(eps))
 
 
-def gate_fits(num: torch.Tensor, resid: torch.Tensor, gate: torch.Tensor) -> bool:
-    """Whether :func:`normalized_read` can apply the output gate to this read:
-    numerator, residual and gate of one dtype and shape (a host query)."""
-    return (num.is_cuda and num.dtype in (torch.bfloat16, torch.float32) and resid.dtype == num.dtype
-            and gate.dtype == num.dtype and gate.shape == num.shape and resid.shape == num.shape)
-
-
 def read_eligible(cfg, weights, q: torch.Tensor) -> bool:
     """Whether the HIP GN read stages cover this configuration (depth-1
     ReLU^2 GN memories with one Jacobian step, no value anchors)."""

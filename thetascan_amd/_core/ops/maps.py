@@ -243,7 +243,10 @@ def _blend_forward(coef: torch.Tensor, inputs: list[torch.Tensor]) -> torch.Tens
     ins = [_rows(t) for t in inputs]
     desc = _blend_desc(ins[0], len(ins))
     cf = coef.detach().to(torch.float32).contiguous()
-    y = torch.empty(ins[0].shape, dtype=ins[0].dtype, device=ins[0].device)
+    # token-major: the output gate and the projection read it as [B,T,H*d]
+    # without a transposing copy
+    B, H, T, d = ins[0].shape
+    y = torch.empty(B, T, H, d, dtype=ins[0].dtype, device=ins[0].device).transpose(1, 2)
     arr = (_lib.Strided * len(ins))(*[_lib.strided(t) for t in ins])
     with _lib.timed("ts_blend_fwd", lambda: _lib.nbytes(*ins, y)):
         status = lib.ts_blend_fwd(ctypes.byref(desc), arr, _lib.ptr(cf), _lib.strided(y),
@@ -253,7 +256,8 @@ def _blend_forward(coef: torch.Tensor, inputs: list[torch.Tensor]) -> torch.Tens
 
 
 def _blend_fake(coef, inputs):
-    return inputs[0].new_empty(inputs[0].shape)
+    B, H, T, d = inputs[0].shape
+    return inputs[0].new_empty(B, T, H, d).transpose(1, 2)
 
 
 def _blend_backward_impl(dy: torch.Tensor, coef: torch.Tensor, inputs: list[torch.Tensor], need: list[bool]
@@ -302,7 +306,8 @@ _blend_op = HipOp("blend", forward=_blend_forward, forward_fake=_blend_fake, bac
 
 
 def bank_blend(inputs, coef: torch.Tensor) -> torch.Tensor:
-    """``sum_i coef[i, h] * inputs[i]`` over ``[B,H,T,d]`` views (1 to 8 of them)."""
+    """``sum_i coef[i, h] * inputs[i]`` over ``[B,H,T,d]`` views (1 to 8 of
+    them), returned as a [B,H,T,d] view of token-major [B,T,H,d] memory."""
     if not 1 <= len(inputs) <= 8:
         raise ValueError("bank blend takes 1 to 8 views")
     _on_gpu(coef, *inputs)

@@ -430,6 +430,7 @@ def run_lm(args) -> dict:
     y = torch.randint(0, lm.VOCAB, (spec["B"], spec["T"]), generator=g).to(dev)
 
     def step():
+        model.zero_grad(set_to_none=True)
         model(x, y).backward()
 
     with paused_gc():

@@ -43,8 +43,10 @@ extern "C" {
  *     ts_bspline_norm_*, ts_feature_fwd_summary, ts_scan_desc.states_in = 3,
  *     TS_GN_SILU, ts_gn_act_* and ts_abs_mass_*; nothing earlier changed.
  * 15: ts_rownorm_fwd / ts_rownorm_bwd; nothing earlier changed.
- * 16: ts_stack_heads; nothing earlier changed. */
-#define TS_ABI_VERSION 16
+ * 16: ts_stack_heads; nothing earlier changed.
+ * 17: ts_scale_add_fwd / ts_scale_add_bwd / ts_scale_add_parts, ts_relu2_fwd /
+ *     ts_relu2_bwd; nothing earlier changed. */
+#define TS_ABI_VERSION 17
 
 enum ts_status {
   TS_OK = 0,
@@ -867,6 +869,39 @@ int ts_rownorm_fwd(const ts_rownorm_desc* desc, ts_strided x, const float* cos, 
 
 int ts_rownorm_bwd(const ts_rownorm_desc* desc, ts_strided x, ts_strided dy, const float* cos, const float* sin,
                    const float* gain, const float* rstd, void* dx, float* dg_row, hipStream_t stream);
+
+/* ------------------------------------------------ host LM row glue */
+
+/* Contiguous [rows, W] tensors of ts_dtype `dtype` (W a multiple of 8, every
+ * pointer 16-byte aligned). */
+typedef struct ts_rows_desc {
+  int64_t rows;
+  int32_t W, dtype;
+} ts_rows_desc;
+
+/* y = a (.) x + b (.) u with fp32 per-column factors a, b [W] (NULL: 1), in
+ * fp32 with one rounding: the residual-stream mixes and scaled residual adds
+ * of the hybrid language model's blocks (x = mix0 x + mix1 x0 and
+ * x + scale (.) f(x), written with torch elementwise ops in the upstream
+ * training script, which this build does not have). */
+int ts_scale_add_fwd(const ts_rows_desc* desc, const void* x, const void* u, const float* a, const float* b,
+                     void* y, hipStream_t stream);
+
+/* Number P of fp32 column-sum partials [P][W] that ts_scale_add_bwd writes
+ * (W at most 2048). */
+int ts_scale_add_parts(const ts_rows_desc* desc, int32_t* parts);
+
+/* Backward of ts_scale_add_fwd for the output gradient g: dx = a (.) g and
+ * du = b (.) g (NULL: not wanted), and partials [P][W] of the column sums
+ * sum_rows g (.) x (da_part) and g (.) u (db_part) (NULL: not wanted), whose
+ * sum over P (ts_sum_slots) is the gradient of a and of b. */
+int ts_scale_add_bwd(const ts_rows_desc* desc, const void* g, const void* x, const void* u, const float* a,
+                     const float* b, void* dx, void* du, float* da_part, float* db_part, hipStream_t stream);
+
+/* h = relu(z)^2 and its backward dz = 2 relu(z) g: the MLP activation of the
+ * hybrid language model's blocks (relu(fc(x)).square()). */
+int ts_relu2_fwd(const ts_rows_desc* desc, const void* z, void* h, hipStream_t stream);
+int ts_relu2_bwd(const ts_rows_desc* desc, const void* z, const void* g, void* dz, hipStream_t stream);
 
 /* ------------------------------------------ stacked projection gradient */
 

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared_functions() if not hasattr(lib, name)]
     assert not missing, missing
     lib.ts_abi_version.restype = ctypes.c_int
-    assert lib.ts_abi_version() == 16
+    assert lib.ts_abi_version() == 17
 
 
 def test_views_descriptor_validation_on_the_host():

@@ -25,7 +25,7 @@ ARCH = "gfx950"
 SOURCES = ("ts_scan.hip", "ts_scan_views.hip", "ts_features.hip", "ts_elementwise.hip", "ts_maps.hip", "ts_gn.hip", "ts_memory.hip",
            "ts_retention.hip",
            "ts_contract.hip", "ts_readout.hip", "ts_anchor.hip", "ts_kmap.hip", "ts_gnact.hip", "ts_absmass.hip",
-           "ts_rownorm.hip")
+           "ts_rownorm.hip", "ts_rowglue.hip")
 
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",

@@ -299,6 +299,10 @@ class StackDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "d", "n", "dtype")]
 
 
+class RowsDesc(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_int64), ("W", ctypes.c_int32), ("dtype", ctypes.c_int32)]
+
+
 class GnActDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("B", "H", "T", "m", "dtype", "act", "has_tau")] + [
         ("eps", ctypes.c_float)]
@@ -587,7 +591,12 @@ def load() -> ctypes.CDLL:
         lib.ts_retention_grad.argtypes = [P(RetentionDesc), P(RetentionIO), ctypes.c_void_p, ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_void_p]
         lib.ts_stack_heads.argtypes = [P(StackDesc), P(Strided), ctypes.c_void_p, ctypes.c_void_p]
-        if lib.ts_abi_version() != 16:
+        lib.ts_scale_add_fwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 6
+        lib.ts_scale_add_parts.argtypes = [P(RowsDesc), P(ctypes.c_int32)]
+        lib.ts_scale_add_bwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 10
+        lib.ts_relu2_fwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 3
+        lib.ts_relu2_bwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 4
+        if lib.ts_abi_version() != 17:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib
         return lib

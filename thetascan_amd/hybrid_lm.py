@@ -28,7 +28,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ._core.ops import rownorm
+from ._core.ops import rowglue, rownorm
 from .api import ThetaScan
 from .config import ThetaScanConfig
 
@@ -136,7 +136,7 @@ class MLP(nn.Module):
         nn.init.zeros_(self.proj.weight)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.proj(torch.relu(self.fc(x)).square())
+        return self.proj(rowglue.relu2(self.fc(x)))
 
 
 class Block(nn.Module):
@@ -154,10 +154,11 @@ class Block(nn.Module):
         self.resid_mix = nn.Parameter(torch.stack((torch.ones(D_MODEL), torch.zeros(D_MODEL))))
 
     def forward(self, x: torch.Tensor, x0: torch.Tensor) -> torch.Tensor:
-        mix = self.resid_mix.to(x.dtype)
-        x = mix[0] * x + mix[1] * x0
-        x = x + self.attn_scale.to(x.dtype) * self.attn(_rms(x))
-        return x + self.mlp_scale.to(x.dtype) * self.mlp(_rms(x))
+        # mix0 x + mix1 x0, then x + scale * f(x) per sublayer: one row-glue
+        # launch each on the GPU
+        x = rowglue.scale_add(x, x0, self.resid_mix[0], self.resid_mix[1])
+        x = rowglue.scale_add(x, self.attn(_rms(x)), None, self.attn_scale)
+        return rowglue.scale_add(x, self.mlp(_rms(x)), None, self.mlp_scale)
 
 
 class HybridLM(nn.Module):
@@ -177,7 +178,7 @@ class HybridLM(nn.Module):
         skips = []
         for i, block in enumerate(self.blocks):
             if i >= self.n_enc and skips:
-                x = x + self.skip_weights[i - self.n_enc].to(x.dtype) * skips.pop()
+                x = rowglue.scale_add(x, skips.pop(), None, self.skip_weights[i - self.n_enc])
             x = block(x, x0)
             if i < self.n_enc:
                 skips.append(x)

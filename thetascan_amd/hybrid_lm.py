@@ -108,22 +108,25 @@ class CausalSelfAttention(nn.Module):
         else:
             q, k = _rotate(_rms(q), cos, sin), _rotate(_rms(k), cos, sin)
             q = q * self.q_gain.to(q.dtype)[None, :, None, None]
-        rep = self.heads // self.kv_heads
-        k = k.repeat_interleave(rep, dim=1).contiguous()
-        v = v.repeat_interleave(rep, dim=1).contiguous()
-        y = attention(q.contiguous(), k, v)
+        y = attention(q.contiguous(), k.contiguous(), v.contiguous())
         return self.proj(y.transpose(1, 2).reshape(B, T, D))
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-    """Causal softmax attention: the fused (flash / memory-efficient) kernels
-    for bf16 on the GPU, the math form in fp32 elsewhere (the bf16 math form
+    """Causal softmax attention of q [B,H,T,d] against k, v [B,Hkv,T,d]
+    (Hkv divides H: grouped key/value heads): the fused (flash /
+    memory-efficient) kernels for bf16 on the GPU, which read the grouped
+    heads in place, the math form in fp32 elsewhere (the bf16 math form
     multiplies by a transposed operand)."""
+    grouped = k.shape[1] != q.shape[1]
     if q.is_cuda and q.dtype == torch.bfloat16:
         from torch.nn.attention import SDPBackend, sdpa_kernel
 
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-            return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=grouped)
+    if grouped:
+        rep = q.shape[1] // k.shape[1]
+        k, v = k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1)
     out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
     return out.to(q.dtype)
 

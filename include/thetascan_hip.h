@@ -879,12 +879,13 @@ typedef struct ts_rows_desc {
   int32_t W, dtype;
 } ts_rows_desc;
 
-/* y = a (.) x + b (.) u with fp32 per-column factors a, b [W] (NULL: 1), in
- * fp32 with one rounding: the residual-stream mixes and scaled residual adds
+/* y = a (.) x + b (.) u with per-column factors a, b [W] of ts_dtype `dtype`
+ * (NULL: 1), in fp32 with one rounding: the residual-stream mixes and scaled
+ * residual adds
  * of the hybrid language model's blocks (x = mix0 x + mix1 x0 and
  * x + scale (.) f(x), written with torch elementwise ops in the upstream
  * training script, which this build does not have). */
-int ts_scale_add_fwd(const ts_rows_desc* desc, const void* x, const void* u, const float* a, const float* b,
+int ts_scale_add_fwd(const ts_rows_desc* desc, const void* x, const void* u, const void* a, const void* b,
                      void* y, hipStream_t stream);
 
 /* Number P of fp32 column-sum partials [P][W] that ts_scale_add_bwd writes
@@ -895,8 +896,8 @@ int ts_scale_add_parts(const ts_rows_desc* desc, int32_t* parts);
  * du = b (.) g (NULL: not wanted), and partials [P][W] of the column sums
  * sum_rows g (.) x (da_part) and g (.) u (db_part) (NULL: not wanted), whose
  * sum over P (ts_sum_slots) is the gradient of a and of b. */
-int ts_scale_add_bwd(const ts_rows_desc* desc, const void* g, const void* x, const void* u, const float* a,
-                     const float* b, void* dx, void* du, float* da_part, float* db_part, hipStream_t stream);
+int ts_scale_add_bwd(const ts_rows_desc* desc, const void* g, const void* x, const void* u, const void* a,
+                     const void* b, void* dx, void* du, float* da_part, float* db_part, hipStream_t stream);
 
 /* h = relu(z)^2 and its backward dz = 2 relu(z) g: the MLP activation of the
  * hybrid language model's blocks (relu(fc(x)).square()). */

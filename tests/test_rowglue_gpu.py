@@ -68,8 +68,8 @@ def test_relu2_equals_the_torch_chain(cuda, dtype):
 def test_hybrid_lm_blocks_use_the_row_glue(cuda):
     """The LM's residual mixes, scaled adds and MLP activation run the row
     glue, and one training step's loss and gradients agree with the torch
-    expressions (bf16 model; the glue rounds once where torch rounds after
-    each product, so the bar is bf16's)."""
+    expressions within 2e-2 (bf16 model; the glue rounds once where torch
+    rounds after each product; measured worst 7.1e-3)."""
     from thetascan_amd import _lib, hybrid_lm as lm
     from thetascan_amd._core.ops import rowglue
 
@@ -104,4 +104,4 @@ def test_hybrid_lm_blocks_use_the_row_glue(cuda):
     errs = {n: rel_err(g1[n], g0[n]) for n in g0 if float(g0[n].abs().max()) > 0}
     worst = max(errs, key=errs.get)
     print(f"LM row glue: loss {l1:.5f} vs {l0:.5f}, worst gradient {worst} {errs[worst]:.3g}", flush=True)
-    assert errs[worst] < 5e-2
+    assert errs[worst] < 2e-2

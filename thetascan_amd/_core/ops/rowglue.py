@@ -5,7 +5,8 @@ the embedding (``mix0 * x + mix1 * x0``), adds each sublayer's output with a
 learned per-channel scale (``x + scale * f(x)``) and squares the ReLU of its
 MLP's hidden layer (the upstream training script's torch elementwise chain).
 :func:`scale_add` is one HIP launch per direction for the first two
-(``ts_scale_add_*``: fp32 arithmetic, one rounding; the factors' gradients
+(``ts_scale_add_*``: fp32 arithmetic, one rounding, the factors read in the
+rows' dtype; the factors' gradients
 from per-workgroup column partials summed in slot order), :func:`relu2` one
 for the third (``ts_relu2_*``).
 """
@@ -24,8 +25,15 @@ def _desc(t: torch.Tensor) -> _lib.RowsDesc:
     return _lib.RowsDesc(t.numel() // t.shape[-1], t.shape[-1], _lib.dtype_code(t.dtype))
 
 
-def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
-    return None if t is None else t.detach().to(torch.float32).contiguous()
+def _factor(t: torch.Tensor | None, like: torch.Tensor) -> torch.Tensor | None:
+    """A per-channel factor in the rows' dtype (no conversion launch when it
+    already is: the parameters of a model in that dtype)."""
+    if t is None:
+        return None
+    t = t.detach()
+    if t.dtype != like.dtype:
+        t = t.to(like.dtype)
+    return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
 
 
 def supported(*tensors: torch.Tensor) -> bool:
@@ -44,7 +52,7 @@ def _scale_add_forward(x: torch.Tensor, u: torch.Tensor, a: torch.Tensor | None,
                        b: torch.Tensor | None) -> torch.Tensor:
     lib = _lib.load()
     y = torch.empty_like(x)
-    fa, fb = _f32(a), _f32(b)
+    fa, fb = _factor(a, x), _factor(b, x)
     with _lib.timed("ts_scale_add_fwd", lambda: _lib.nbytes(x, u, y)):
         status = lib.ts_scale_add_fwd(ctypes.byref(_desc(x)), x.data_ptr(), u.data_ptr(), _lib.ptr(fa), _lib.ptr(fb),
                                       y.data_ptr(), _lib.stream_handle(x.device))
@@ -68,7 +76,7 @@ def _scale_add_backward_impl(g: torch.Tensor, x: torch.Tensor, u: torch.Tensor, 
     du = torch.empty_like(u) if need[1] else None
     pa = torch.empty(n.value, W, dtype=torch.float32, device=x.device) if need[2] else None
     pb = torch.empty(n.value, W, dtype=torch.float32, device=x.device) if need[3] else None
-    fa, fb = _f32(a), _f32(b)
+    fa, fb = _factor(a, x), _factor(b, x)
     with _lib.timed("ts_scale_add_bwd", lambda: _lib.nbytes(g, x if need[2] else None, u if need[3] else None,
                                                             dx, du)):
         status = lib.ts_scale_add_bwd(ctypes.byref(desc), g.data_ptr(), x.data_ptr(), u.data_ptr(), _lib.ptr(fa),

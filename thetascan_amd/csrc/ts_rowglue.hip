@@ -1,8 +1,8 @@
 // Row-wise elementwise glue of the hybrid language model's blocks (gfx950):
 // the residual mixes and scaled residual adds, and the ReLU^2 of the MLP.
 //
-//   scale-add:  y = a (.) x + b (.) u        a, b: fp32 per-column factors [W]
-//                                            (NULL: 1), rows of width W
+//   scale-add:  y = a (.) x + b (.) u        a, b: per-column factors [W] of the
+//                                            rows' dtype (NULL: 1), rows of width W
 //     backward: dx = a (.) g,  du = b (.) g,
 //               da = sum_rows g (.) x,  db = sum_rows g (.) u
 //   ReLU^2:     h = relu(z)^2,  dz = 2 relu(z) g
@@ -50,14 +50,11 @@ __device__ __forceinline__ void rg_st8(E* p, const float* v) {
   }
 }
 
-__device__ __forceinline__ void rg_factors(const float* f, int c, float* v) {
+// Eight per-column factors (of the rows' dtype) from column c, or ones.
+template <typename E>
+__device__ __forceinline__ void rg_factors(const E* f, int c, float* v) {
   if (f) {
-    const floatx4 a = *(const floatx4*)(f + c), b = *(const floatx4*)(f + c + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = a[e];
-      v[4 + e] = b[e];
-    }
+    rg_ld8<E>(f + c, v);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = 1.0f;
@@ -70,8 +67,8 @@ struct GlueP {
   const void* x;
   const void* u;
   const void* g;
-  const float* a;
-  const float* b;
+  const void* a;  // per-column factors [W] of the rows' dtype (NULL: 1)
+  const void* b;
   void* y;   // forward output, or dx
   void* du;
   float* da_part;  // [P][W]
@@ -89,8 +86,8 @@ __global__ __launch_bounds__(256) void scale_add_fwd_kernel(GlueP p) {
     float x[8], u[8], a[8], b[8];
     rg_ld8<E>((const E*)p.x + off, x);
     rg_ld8<E>((const E*)p.u + off, u);
-    rg_factors(p.a, c, a);
-    rg_factors(p.b, c, b);
+    rg_factors<E>((const E*)p.a, c, a);
+    rg_factors<E>((const E*)p.b, c, b);
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = fmaf(a[e], x[e], b[e] * u[e]);
     rg_st8<E>((E*)p.y + off, x);
@@ -109,8 +106,8 @@ __global__ __launch_bounds__(256) void scale_add_bwd_kernel(GlueP p) {
   const int64_t r0 = (int64_t)blockIdx.x * p.rows_per_block;
   const int64_t r1 = min(r0 + p.rows_per_block, p.rows);
   float a[8], b[8], sa[8], sb[8];
-  rg_factors(p.a, c, a);
-  rg_factors(p.b, c, b);
+  rg_factors<E>((const E*)p.a, c, a);
+  rg_factors<E>((const E*)p.b, c, b);
 #pragma unroll
   for (int e = 0; e < 8; ++e) sa[e] = sb[e] = 0.f;
   if (rl < lanes) {
@@ -224,7 +221,7 @@ unsigned walk_grid(const ts_rows_desc* d) {
 
 extern "C" {
 
-int ts_scale_add_fwd(const ts_rows_desc* d, const void* x, const void* u, const float* a, const float* b, void* y,
+int ts_scale_add_fwd(const ts_rows_desc* d, const void* x, const void* u, const void* a, const void* b, void* y,
                      hipStream_t stream) {
   int rc = check_rows(d, "scale_add");
   if (rc) return rc;
@@ -251,8 +248,8 @@ int ts_scale_add_parts(const ts_rows_desc* d, int32_t* parts) {
   return TS_OK;
 }
 
-int ts_scale_add_bwd(const ts_rows_desc* d, const void* g, const void* x, const void* u, const float* a,
-                     const float* b, void* dx, void* du, float* da_part, float* db_part, hipStream_t stream) {
+int ts_scale_add_bwd(const ts_rows_desc* d, const void* g, const void* x, const void* u, const void* a,
+                     const void* b, void* dx, void* du, float* da_part, float* db_part, hipStream_t stream) {
   int32_t parts = 0;
   int rc = ts_scale_add_parts(d, &parts);
   if (rc) return rc;

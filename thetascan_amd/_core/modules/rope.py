@@ -10,16 +10,30 @@ from functools import lru_cache
 
 import torch
 
+# Tables of captured decode steps, keyed by shape, base, device and dtype
+_DEVICE_TABLES: dict = {}
+
 
 def _tables(T: int, rot_dim: int, base: float, device, dtype: torch.dtype, start=0):
     """cos/sin [T, rot_dim/2] of positions start .. start+T-1; ``start`` may
     be an int64 device tensor (a captured decode step)."""
     phase_dtype = torch.float64 if dtype == torch.float64 else torch.float32
-    inv = 1.0 / (base ** (torch.arange(0, rot_dim, 2, device=device, dtype=phase_dtype) / rot_dim))
     if isinstance(start, torch.Tensor):
-        pos = (start + torch.arange(T, device=device, dtype=torch.int64)).to(phase_dtype)
-    else:
-        pos = torch.arange(start, start + T, device=device, dtype=phase_dtype)
+        # a captured step: frequencies and offsets kept for the life of the
+        # process (the graph reads them in place), the positions in one launch
+        # (integers below 2^24 are exact in fp32: the values of
+        # (start + arange(T)) converted)
+        key = (T, rot_dim, float(base), str(device), phase_dtype)
+        hit = _DEVICE_TABLES.get(key)
+        if hit is None:
+            hit = _DEVICE_TABLES[key] = (
+                1.0 / (base ** (torch.arange(0, rot_dim, 2, device=device, dtype=phase_dtype) / rot_dim)),
+                torch.arange(T, device=device, dtype=phase_dtype))
+        inv, offsets = hit
+        f = torch.outer(offsets + start, inv)
+        return f.cos().to(dtype=dtype), f.sin().to(dtype=dtype)
+    inv = 1.0 / (base ** (torch.arange(0, rot_dim, 2, device=device, dtype=phase_dtype) / rot_dim))
+    pos = torch.arange(start, start + T, device=device, dtype=phase_dtype)
     f = torch.outer(pos, inv)
     return f.cos().to(dtype=dtype), f.sin().to(dtype=dtype)
 

@@ -37,12 +37,18 @@ def _rope_tables(T: int, rot: int, base: float, device, start=0) -> tuple[torch.
     phases, kept in fp32).  ``start`` may be an int64 device tensor (a
     captured decode step): the positions are the same exact fp32 integers."""
     if isinstance(start, torch.Tensor):
-        # kept for the life of the process: a captured step reads it in place
+        # kept for the life of the process: a captured step reads them in place
         key = (rot, float(base), str(device))
         inv = _INV.get(key)
         if inv is None:
             inv = _INV[key] = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
-        pos = (start + torch.arange(T, device=device, dtype=torch.int64)).to(torch.float32)
+        akey = ("offsets", T, str(device))
+        offsets = _INV.get(akey)
+        if offsets is None:
+            offsets = _INV[akey] = torch.arange(T, device=device, dtype=torch.float32)
+        # one launch: fp32 integers below 2^24 are exact, so these are the
+        # values (start + arange(T)).float() would give
+        pos = offsets + start
     else:
         inv = 1.0 / (base ** (torch.arange(0, rot, 2, device=device, dtype=torch.float32) / rot))
         pos = torch.arange(start, start + T, device=device, dtype=torch.float32)

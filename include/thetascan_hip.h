@@ -45,7 +45,8 @@ extern "C" {
  * 15: ts_rownorm_fwd / ts_rownorm_bwd; nothing earlier changed.
  * 16: ts_stack_heads; nothing earlier changed.
  * 17: ts_scale_add_fwd / ts_scale_add_bwd / ts_scale_add_parts, ts_relu2_fwd /
- *     ts_relu2_bwd; nothing earlier changed. */
+ *     ts_relu2_bwd, ts_softcap_xent_fwd / ts_softcap_xent_bwd; nothing earlier
+ *     changed. */
 #define TS_ABI_VERSION 17
 
 enum ts_status {
@@ -903,6 +904,20 @@ int ts_scale_add_bwd(const ts_rows_desc* desc, const void* g, const void* x, con
  * hybrid language model's blocks (relu(fc(x)).square()). */
 int ts_relu2_fwd(const ts_rows_desc* desc, const void* z, void* h, hipStream_t stream);
 int ts_relu2_bwd(const ts_rows_desc* desc, const void* z, const void* g, void* dz, hipStream_t stream);
+
+/* Softcapped cross entropy of the host LM's logits z [rows, W] (W at most
+ * 512, or a multiple of 512 up to 4096) against int64 targets in [0, W):
+ *   c = cap tanh(z / cap),  lse_r = log sum_j exp(c_rj),  loss_r = lse_r - c_r,target
+ * (fp32 loss and lse [rows]); the backward writes
+ *   dz = g g_scale (softmax(c_r) - onehot(target_r)) (1 - (c / cap)^2)
+ * for the scalar gradient *g (device fp32) of sum_r loss_r g_scale (g_scale =
+ * 1 / rows for the mean), recomputing c from z and lse.  The logit soft-cap
+ * and cross entropy of the upstream training script (torch's tanh and
+ * F.cross_entropy over fp32 logits). */
+int ts_softcap_xent_fwd(const ts_rows_desc* desc, const void* z, const int64_t* target, float cap, float* loss,
+                        float* lse, hipStream_t stream);
+int ts_softcap_xent_bwd(const ts_rows_desc* desc, const void* z, const int64_t* target, float cap, const float* lse,
+                        const float* g, float g_scale, void* dz, hipStream_t stream);
 
 /* ------------------------------------------ stacked projection gradient */
 

@@ -105,3 +105,31 @@ def test_hybrid_lm_blocks_use_the_row_glue(cuda):
     worst = max(errs, key=errs.get)
     print(f"LM row glue: loss {l1:.5f} vs {l0:.5f}, worst gradient {worst} {errs[worst]:.3g}", flush=True)
     assert errs[worst] < 2e-2
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("rows,W,cap", [(300, 1024, 30.0), (77, 64, 2.0), (5, 2048, 5.0), (33, 8, 1.5)])
+def test_softcap_cross_entropy_matches_float64(cuda, dtype, tol, rows, W, cap):
+    """mean_r cross_entropy(cap tanh(z / cap), target) and its gradient in z
+    against float64 autograd (the loss within 1e-5 relative for both dtypes,
+    since it is an fp32 reduction of the given logits; dz fp32 1e-5, bf16 one
+    rounding)."""
+    from thetascan_amd import _lib
+    from thetascan_amd._core.ops import rowglue
+
+    g = torch.Generator().manual_seed(rows + W)
+    z = (torch.randn(rows, W, generator=g) * 4).to(dtype)
+    target = torch.randint(0, W, (rows,), generator=g)
+    z64 = z.double().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(cap * torch.tanh(z64 / cap), target)
+    ref.backward(torch.tensor(0.7, dtype=torch.float64))
+    zd = z.to(cuda).requires_grad_(True)
+    with _lib.record_launches() as recs:
+        loss = rowglue.softcap_cross_entropy(zd, target.to(cuda), cap)
+        loss.backward(torch.tensor(0.7, device=cuda))
+        torch.cuda.synchronize()
+    assert {"ts_softcap_xent_fwd", "ts_softcap_xent_bwd"} <= {r[0] for r in recs}
+    e_loss = abs(float(loss) - float(ref)) / abs(float(ref))
+    e_dz = rel_err(zd.grad.float(), z64.grad)
+    print(f"softcap xent rows {rows} W {W} cap {cap} {dtype}: loss {e_loss:.3g} dz {e_dz:.3g}", flush=True)
+    assert e_loss < 1e-5 and e_dz < tol

@@ -176,3 +176,74 @@ def relu2(z: torch.Tensor) -> torch.Tensor:
     if supported(z):
         return _relu2_op(z)
     return torch.relu(z).square()
+
+
+# ---------------------------------------------------------------- softcapped cross entropy
+
+def _xent_forward(z: torch.Tensor, target: torch.Tensor, cap: float) -> list[torch.Tensor]:
+    lib = _lib.load()
+    rows = z.shape[0]
+    loss = torch.empty(rows, dtype=torch.float32, device=z.device)
+    lse = torch.empty(rows, dtype=torch.float32, device=z.device)
+    with _lib.timed("ts_softcap_xent_fwd", lambda: _lib.nbytes(z, target, loss, lse)):
+        status = lib.ts_softcap_xent_fwd(ctypes.byref(_desc(z)), z.data_ptr(), target.data_ptr(), float(cap),
+                                         loss.data_ptr(), lse.data_ptr(), _lib.stream_handle(z.device))
+    _lib.check(status, "ts_softcap_xent_fwd")
+    return [loss.mean(), lse]
+
+
+def _xent_fake(z, target, cap):
+    return [z.new_empty((), dtype=torch.float32), z.new_empty(z.shape[0], dtype=torch.float32)]
+
+
+def _xent_backward_impl(g: torch.Tensor, z: torch.Tensor, target: torch.Tensor, lse: torch.Tensor,
+                        cap: float) -> torch.Tensor:
+    lib = _lib.load()
+    dz = torch.empty_like(z)
+    g32 = g.detach().to(torch.float32).reshape(1).contiguous()
+    with _lib.timed("ts_softcap_xent_bwd", lambda: _lib.nbytes(z, target, lse, dz)):
+        status = lib.ts_softcap_xent_bwd(ctypes.byref(_desc(z)), z.data_ptr(), target.data_ptr(), float(cap),
+                                         lse.data_ptr(), g32.data_ptr(), 1.0 / max(z.shape[0], 1), dz.data_ptr(),
+                                         _lib.stream_handle(z.device))
+    _lib.check(status, "ts_softcap_xent_bwd")
+    return dz
+
+
+def _xent_backward_fake(g, z, target, lse, cap):
+    return torch.empty_like(z)
+
+
+def _xent_setup(ctx, inputs, output):
+    z, target, cap = inputs
+    ctx.cap = cap
+    ctx.save_for_backward(z, target, output[1])
+
+
+def _xent_backward(ctx, grads, bwd):
+    z, target, lse = ctx.saved_tensors
+    g = grads[0]
+    return (None if g is None else bwd(g, z, target, lse, ctx.cap)), None, None
+
+
+_xent_op = HipOp("softcap_xent", forward=_xent_forward, forward_fake=_xent_fake, backward_impl=_xent_backward_impl,
+                 backward_fake=_xent_backward_fake, setup=_xent_setup, backward=_xent_backward)
+
+
+def xent_supported(z: torch.Tensor, target: torch.Tensor) -> bool:
+    """Whether :func:`softcap_cross_entropy` runs the HIP kernels (a host
+    query): [rows, W] bf16 / fp32 logits (W at most 512 and a multiple of 8,
+    or a multiple of 512 up to 4096) and int64 targets on the GPU."""
+    W = z.shape[-1]
+    return (z.ndim == 2 and supported(z) and target.is_cuda and target.dtype == torch.int64
+            and target.shape == z.shape[:1] and target.is_contiguous() and (W <= 512 or (W % 512 == 0 and W <= 4096)))
+
+
+def softcap_cross_entropy(z: torch.Tensor, target: torch.Tensor, cap: float) -> torch.Tensor:
+    """Mean over rows of ``cross_entropy(cap * tanh(z / cap), target)`` for
+    logits z [rows, W] (targets in [0, W), no ignored index) in one HIP
+    launch per direction; torch's fp32 chain where the tensors are not
+    :func:`xent_supported`."""
+    if xent_supported(z, target):
+        return _xent_op(z, target, float(cap))[0]
+    c = cap * torch.tanh(z.float() / cap)
+    return torch.nn.functional.cross_entropy(c, target)

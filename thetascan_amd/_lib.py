@@ -596,6 +596,11 @@ def load() -> ctypes.CDLL:
         lib.ts_scale_add_bwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 10
         lib.ts_relu2_fwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 3
         lib.ts_relu2_bwd.argtypes = [P(RowsDesc)] + [ctypes.c_void_p] * 4
+        lib.ts_softcap_xent_fwd.argtypes = [P(RowsDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.ts_softcap_xent_bwd.argtypes = [P(RowsDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+                                            ctypes.c_void_p]
         if lib.ts_abi_version() != 17:
             raise RuntimeError("libthetascan_hip.so ABI version mismatch")
         _lib = lib

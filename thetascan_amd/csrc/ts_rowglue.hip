@@ -187,6 +187,80 @@ __global__ __launch_bounds__(256) void relu2_kernel(GlueP p) {
   }
 }
 
+// Softcapped cross entropy: one wave per row of V logits (V / 64 per lane,
+// in runs of eight), c = cap tanh(z / cap) in fp32, the row's max and
+// exp-sum by xor butterflies.  The backward recomputes c from z and the
+// forward's log-sum-exp, so no [rows, V] fp32 tensor is ever stored.
+template <typename E, bool BWD>
+__global__ __launch_bounds__(256) void softcap_xent_kernel(GlueP p, const int64_t* target, float cap, float* loss,
+                                                           float* lse, const float* g, float g_scale) {
+  constexpr int kMaxRun = 8;  // runs of eight logits per lane: V <= 4096
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;  // uniform per wave
+  const int runs = p.W / 512 > 0 ? p.W / 512 : 1;  // eight-logit runs per lane (W a multiple of 512, or 8..504)
+  const E* zr = (const E*)p.x + row * p.W;
+  const float inv_cap = 1.0f / cap;
+  float c[kMaxRun][8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kMaxRun; ++k) {
+    const int col = (k * 64 + lane) * 8;
+    if (k < runs && col < p.W) {
+      rg_ld8<E>(zr + col, c[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        c[k][e] = cap * tanhf(c[k][e] * inv_cap);
+        mx = fmaxf(mx, c[k][e]);
+      }
+    }
+  }
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  const int64_t y = target[row];
+  float l;
+  if constexpr (!BWD) {
+    float se = 0.f, cy = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxRun; ++k) {
+      const int col = (k * 64 + lane) * 8;
+      if (k < runs && col < p.W) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          se += __expf(c[k][e] - mx);
+          if (col + e == y) cy = c[k][e];
+        }
+      }
+    }
+    for (int o = 1; o < 64; o <<= 1) {
+      se += __shfl_xor(se, o, 64);
+      cy += __shfl_xor(cy, o, 64);
+    }
+    l = mx + __logf(se);
+    if (lane == 0) {
+      lse[row] = l;
+      loss[row] = l - cy;
+    }
+  } else {
+    l = lse[row];
+    const float gr = *g * g_scale;
+    E* dz = (E*)p.y + row * p.W;
+#pragma unroll
+    for (int k = 0; k < kMaxRun; ++k) {
+      const int col = (k * 64 + lane) * 8;
+      if (k < runs && col < p.W) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float t = c[k][e] * inv_cap;  // tanh(z / cap)
+          const float pr = __expf(c[k][e] - l) - (col + e == y ? 1.0f : 0.0f);
+          o[e] = gr * pr * (1.0f - t * t);
+        }
+        rg_st8<E>(dz + col, o);
+      }
+    }
+  }
+}
+
 }  // namespace ts
 
 namespace {
@@ -300,6 +374,49 @@ int ts_relu2_bwd(const ts_rows_desc* d, const void* z, const void* g, void* dz, 
   else
     hipLaunchKernelGGL((ts::relu2_kernel<float, true>), dim3(walk_grid(d)), dim3(256), 0, stream, p);
   return glue_finish("relu2 bwd");
+}
+
+int ts_softcap_xent_fwd(const ts_rows_desc* d, const void* z, const int64_t* target, float cap, float* loss,
+                        float* lse, hipStream_t stream) {
+  int rc = check_rows(d, "softcap_xent");
+  if (rc) return rc;
+  if (d->W > 4096 || (d->W > 512 && d->W % 512)) return fail(TS_ERR_NOT_IMPLEMENTED, "softcap_xent: width %d", d->W);
+  if (!z || !target || !loss || !lse || !aligned(z) || !(cap > 0.f))
+    return fail(TS_ERR_VALUE, "softcap_xent: missing or unaligned arguments, or cap <= 0");
+  if (d->rows == 0) return TS_OK;
+  ts::GlueP p;
+  memset(&p, 0, sizeof(p));
+  p.rows = d->rows; p.W = d->W; p.x = z;
+  const dim3 grid((unsigned)((d->rows + 3) / 4));
+  if (d->dtype == TS_BF16)
+    hipLaunchKernelGGL((ts::softcap_xent_kernel<ts::bf16, false>), grid, dim3(256), 0, stream, p, target, cap, loss, lse,
+                       (const float*)nullptr, 0.f);
+  else
+    hipLaunchKernelGGL((ts::softcap_xent_kernel<float, false>), grid, dim3(256), 0, stream, p, target, cap, loss, lse,
+                       (const float*)nullptr, 0.f);
+  return glue_finish("softcap_xent");
+}
+
+int ts_softcap_xent_bwd(const ts_rows_desc* d, const void* z, const int64_t* target, float cap, const float* lse,
+                        const float* g, float g_scale, void* dz, hipStream_t stream) {
+  int rc = check_rows(d, "softcap_xent bwd");
+  if (rc) return rc;
+  if (d->W > 4096 || (d->W > 512 && d->W % 512))
+    return fail(TS_ERR_NOT_IMPLEMENTED, "softcap_xent bwd: width %d", d->W);
+  if (!z || !target || !lse || !g || !dz || !aligned(z) || !aligned(dz) || !(cap > 0.f))
+    return fail(TS_ERR_VALUE, "softcap_xent bwd: missing or unaligned arguments, or cap <= 0");
+  if (d->rows == 0) return TS_OK;
+  ts::GlueP p;
+  memset(&p, 0, sizeof(p));
+  p.rows = d->rows; p.W = d->W; p.x = z; p.y = dz;
+  const dim3 grid((unsigned)((d->rows + 3) / 4));
+  if (d->dtype == TS_BF16)
+    hipLaunchKernelGGL((ts::softcap_xent_kernel<ts::bf16, true>), grid, dim3(256), 0, stream, p, target, cap,
+                       (float*)nullptr, (float*)lse, g, g_scale);
+  else
+    hipLaunchKernelGGL((ts::softcap_xent_kernel<float, true>), grid, dim3(256), 0, stream, p, target, cap,
+                       (float*)nullptr, (float*)lse, g, g_scale);
+  return glue_finish("softcap_xent bwd");
 }
 
 }  // extern "C"

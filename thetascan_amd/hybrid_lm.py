@@ -186,11 +186,12 @@ class HybridLM(nn.Module):
             if i < self.n_enc:
                 skips.append(x)
         x = _rms(x)
-        logits = F.linear(x, self.tok_emb.weight.to(x.dtype)).float()
-        logits = LOGIT_SOFTCAP * torch.tanh(logits / LOGIT_SOFTCAP)
+        logits = F.linear(x, self.tok_emb.weight.to(x.dtype))
         if targets is None:
-            return logits
-        return F.cross_entropy(logits.view(-1, VOCAB), targets.reshape(-1))
+            return LOGIT_SOFTCAP * torch.tanh(logits.float() / LOGIT_SOFTCAP)
+        # the soft-capped logits' cross entropy: one HIP launch per direction
+        # on the GPU (the fp32 capped logits are never stored)
+        return rowglue.softcap_cross_entropy(logits.reshape(-1, VOCAB), targets.reshape(-1), LOGIT_SOFTCAP)
 
 
 # ---------------------------------------------------------------- int8 round trip

@@ -45,8 +45,8 @@ extern "C" {
  * 15: ts_rownorm_fwd / ts_rownorm_bwd; nothing earlier changed.
  * 16: ts_stack_heads; nothing earlier changed.
  * 17: ts_scale_add_fwd / ts_scale_add_bwd / ts_scale_add_parts, ts_relu2_fwd /
- *     ts_relu2_bwd, ts_softcap_xent_fwd / ts_softcap_xent_bwd; nothing earlier
- *     changed. */
+ *     ts_relu2_bwd, ts_softcap_xent_fwd / ts_softcap_xent_bwd, ts_blend_gated_fwd;
+ *     nothing earlier changed. */
 #define TS_ABI_VERSION 17
 
 enum ts_status {
@@ -781,6 +781,15 @@ typedef struct ts_blend_desc {
 
 int ts_blend_fwd(const ts_blend_desc* desc, const ts_strided* in, const float* coef, ts_strided y,
                  hipStream_t stream);
+
+/* ts_blend_fwd followed by the output gate (block.py:721-722, gates.py:34-40):
+ *   y = (sum_i coef[i*H + h] * in_i) * silu(g + g_bias)
+ * with g the gate's pre-activation x W_g^T as a [B,H,T,d] view (of the
+ * rows' dtype) and g_bias fp32 [H*d] (NULL: none); g.ptr NULL is
+ * ts_blend_fwd.  Forward only (inference): a training step keeps the gate as
+ * its own autograd product. */
+int ts_blend_gated_fwd(const ts_blend_desc* desc, const ts_strided* in, const float* coef, ts_strided g,
+                       const float* g_bias, ts_strided y, hipStream_t stream);
 
 /* Number of fp32 partial sums per (input, head) that ts_blend_bwd writes to
  * dcoef_part ([n_in][H][nparts]). */

@@ -194,3 +194,29 @@ def test_bspline_of_rmsnormed_inputs_matches_the_oracle(cuda, dtype, tol, P, n_b
         assert rel_err(sd.grad, s64.grad) < tol
     if shifted:
         assert rel_err(hd.grad, h64.grad) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-6), (torch.bfloat16, 1e-2)])
+def test_gated_blend_matches_blend_then_gate(cuda, dtype, tol):
+    """ts_blend_gated_fwd (inference) against float64 (sum_i coef_i in_i) *
+    silu(gate + bias) on views of token-major memory (fp32 1e-6, bf16 one
+    rounding)."""
+    from thetascan_amd._core.ops import maps
+
+    g = torch.Generator().manual_seed(21)
+    B, H, T, d, n = 2, 3, 130, 64, 4
+    ins = [torch.randn(B, H, T, d, generator=g).to(dtype) for _ in range(n)]
+    coef = torch.randn(n, H, generator=g)
+    gate = torch.randn(B, T, H, d, generator=g).to(dtype).transpose(1, 2)
+    bias = torch.randn(H * d, generator=g)
+    ref = sum(coef[i].double().view(1, H, 1, 1) * ins[i].double() for i in range(n))
+    ref = ref * torch.nn.functional.silu(gate.double() + bias.double().view(H, 1, d))
+    with torch.no_grad():
+        y = maps.bank_blend_gated([t.to(cuda) for t in ins], coef.to(cuda), gate.to(cuda), bias.to(cuda))
+    torch.cuda.synchronize()
+    assert y.shape == (B, H, T, d) and y.transpose(1, 2).is_contiguous()
+    err = rel_err(y.double().cpu(), ref)
+    print(f"gated blend {dtype}: {err:.3g}", flush=True)
+    assert err < tol
+    with pytest.raises(RuntimeError, match="forward-only"):
+        maps.bank_blend_gated([t.to(cuda) for t in ins], coef.to(cuda), gate.to(cuda), bias.to(cuda))

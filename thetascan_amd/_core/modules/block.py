@@ -610,10 +610,16 @@ class ThetaScan(nn.Module):
         B, T, _ = x.shape
         y = reads[0]
         if cfg.read_fade:
-            if cfg.read_fade_mode == "fast":
-                y = maps.bank_blend(reads, maps.fast_coefficients(etas))
-            else:
-                y = maps.bank_blend(reads, maps.stale_coefficients(etas))
+            coef = maps.fast_coefficients(etas) if cfg.read_fade_mode == "fast" else maps.stale_coefficients(etas)
+            if (self.ogate is not None and not torch.is_grad_enabled() and x.is_cuda
+                    and all(r.dtype == x.dtype for r in reads) and self.ogate.g.lin.weight.dtype == x.dtype):
+                # inference: the output gate in the blend's epilogue (one
+                # launch, no gate or transposing copy of the blended read)
+                lin = self.ogate.g.lin
+                pre = linear(x, lin.weight).view(B, T, cfg.n_heads, cfg.head_dim).transpose(1, 2)
+                y = maps.bank_blend_gated(reads, coef, pre, lin.bias)
+                return linear(y.transpose(1, 2).reshape(B, T, cfg.n_heads * cfg.head_dim), self.proj_out.weight)
+            y = maps.bank_blend(reads, coef)
         if self.ogate is not None:
             y = y * self.ogate(x)
         y = y.transpose(1, 2).reshape(B, T, cfg.n_heads * cfg.head_dim)

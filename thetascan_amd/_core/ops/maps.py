@@ -322,6 +322,34 @@ def bank_blend(inputs, coef: torch.Tensor) -> torch.Tensor:
     return _blend_op(coef, list(inputs))
 
 
+def bank_blend_gated(inputs, coef: torch.Tensor, gate: torch.Tensor, gate_bias: torch.Tensor | None) -> torch.Tensor:
+    """``bank_blend(inputs, coef) * silu(gate + gate_bias)`` in one launch
+    (ts_blend_gated_fwd), written token-major like :func:`bank_blend`.
+    Inference only: nothing here records autograd (the caller runs it with
+    grad disabled); ``gate`` is the [B,H,T,d] view of the output gate's
+    pre-activation x W_g^T in the inputs' dtype, ``gate_bias`` [H*d]."""
+    if torch.is_grad_enabled():
+        raise RuntimeError("bank_blend_gated is a forward-only epilogue: call it with grad disabled")
+    first = inputs[0]
+    if not (1 <= len(inputs) <= 8 and first.is_cuda and first.dtype in _KERNEL_DTYPES and first.ndim == 4
+            and gate.shape == first.shape and gate.dtype == first.dtype
+            and all(t.shape == first.shape and t.dtype == first.dtype for t in inputs)):
+        raise NotImplementedError("bank_blend_gated: views and gate must share shape and a kernel dtype")
+    lib = _lib.load()
+    ins = [_rows(t) for t in inputs]
+    g = _rows(gate)
+    B, H, T, d = first.shape
+    y = torch.empty(B, T, H, d, dtype=first.dtype, device=first.device).transpose(1, 2)
+    cf = coef.detach().to(torch.float32).contiguous()
+    gb = None if gate_bias is None else gate_bias.detach().to(torch.float32).contiguous()
+    arr = (_lib.Strided * len(ins))(*[_lib.strided(t) for t in ins])
+    with _lib.timed("ts_blend_fwd", lambda: _lib.nbytes(*ins, g, y)):
+        status = lib.ts_blend_gated_fwd(ctypes.byref(_blend_desc(ins[0], len(ins))), arr, _lib.ptr(cf),
+                                        _lib.strided(g), _lib.ptr(gb), _lib.strided(y), _lib.stream_handle(y.device))
+    _lib.check(status, "ts_blend_gated_fwd")
+    return y
+
+
 def fast_coefficients(etas) -> torch.Tensor:
     """(1 - sum_j eta_j, eta_1 .. eta_J) over (R_0, R_1 .. R_J) (block.py:683-695)."""
     eta = torch.stack([e.reshape(-1) for e in etas]).to(torch.float32)

@@ -561,6 +561,8 @@ def load() -> ctypes.CDLL:
         lib.ts_bspline_norm_bwd.argtypes = [P(BsplineDesc), Strided, ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
                                              Strided, Strided, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         lib.ts_blend_fwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, ctypes.c_void_p]
+        lib.ts_blend_gated_fwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, ctypes.c_void_p, Strided,
+                                           ctypes.c_void_p]
         lib.ts_blend_parts.argtypes = [P(BlendDesc), P(ctypes.c_int32)]
         lib.ts_blend_bwd.argtypes = [P(BlendDesc), P(Strided), ctypes.c_void_p, Strided, P(Strided),
                                      ctypes.c_void_p, ctypes.c_void_p]

@@ -281,6 +281,8 @@ struct BlendP {
   ts_strided y, dy;
   ts_strided din[kBlendMax];
   float* dpart;
+  ts_strided g;      // output-gate pre-activation (forward only; NULL: no gate)
+  const float* gb;   // gate bias [H*d] (NULL: none)
 };
 
 // Chunk c of the (b, h) slice: row t = c / per_row, columns W*(c % per_row)..
@@ -314,6 +316,24 @@ __global__ __launch_bounds__(256) void blend_fwd_kernel(BlendP p) {
         } else {
           acc[0] += coef[i] * tof(src[0]);
         }
+      }
+    }
+    if (p.g.ptr) {
+      // output gate: y *= silu(g + bias), in fp32 before the one rounding
+      const E* gs = at<const E>(p.g, b, h, t) + col;
+      float gv[W];
+      if (V) {
+        Vec16<E> v;
+        v.raw = *(const uint4*)gs;
+#pragma unroll
+        for (int e = 0; e < W; ++e) gv[e] = tof(v.e[e]);
+      } else {
+        gv[0] = tof(gs[0]);
+      }
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        const float z = gv[e] + (p.gb ? p.gb[h * p.d + col + e] : 0.f);
+        acc[e] *= z / (1.0f + __expf(-z));
       }
     }
     E* dst = at<E>(p.y, b, h, t) + col;
@@ -619,8 +639,8 @@ int ts_bspline_norm_bwd(const ts_bspline_desc* d, ts_strided a, const float* shi
   return launch_spline(d, p, false, true, stream);
 }
 
-int ts_blend_fwd(const ts_blend_desc* d, const ts_strided* in, const float* coef, ts_strided y,
-                 hipStream_t stream) {
+int ts_blend_gated_fwd(const ts_blend_desc* d, const ts_strided* in, const float* coef, ts_strided g,
+                       const float* g_bias, ts_strided y, hipStream_t stream) {
   int rc = check_blend(d, in);
   if (rc) return rc;
   if (!coef || !y.ptr) return fail(TS_ERR_VALUE, "blend: missing coefficients or output");
@@ -631,7 +651,10 @@ int ts_blend_fwd(const ts_blend_desc* d, const ts_strided* in, const float* coef
   p.coef = coef;
   for (int i = 0; i < d->n_in; ++i) p.in[i] = in[i];
   p.y = y;
-  const bool vec = blend_vec(d, in, &y, 1);
+  p.g = g;
+  p.gb = g.ptr ? g_bias : nullptr;
+  const ts_strided outs[2] = {y, g};
+  const bool vec = blend_vec(d, in, outs, 2);
   p.tiles = blend_tiles(d);
   p.rows = ts::blend_rows(d->d);
   const dim3 grid((unsigned)p.tiles, (unsigned)(d->B * d->H));
@@ -643,6 +666,12 @@ int ts_blend_fwd(const ts_blend_desc* d, const ts_strided* in, const float* coef
     else hipLaunchKernelGGL((ts::blend_fwd_kernel<float, false>), grid, dim3(256), 0, stream, p);
   }
   return finish("blend");
+}
+
+int ts_blend_fwd(const ts_blend_desc* d, const ts_strided* in, const float* coef, ts_strided y,
+                 hipStream_t stream) {
+  const ts_strided none = {nullptr, 0, 0, 0};
+  return ts_blend_gated_fwd(d, in, coef, none, nullptr, y, stream);
 }
 
 int ts_blend_bwd(const ts_blend_desc* d, const ts_strided* in, const float* coef, ts_strided dy,

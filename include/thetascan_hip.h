@@ -917,7 +917,8 @@ int ts_relu2_bwd(const ts_rows_desc* desc, const void* z, const void* g, void* d
 /* Softcapped cross entropy of the host LM's logits z [rows, W] (W at most
  * 512, or a multiple of 512 up to 4096) against int64 targets in [0, W):
  *   c = cap tanh(z / cap),  lse_r = log sum_j exp(c_rj),  loss_r = lse_r - c_r,target
- * (fp32 loss and lse [rows]); the backward writes
+ * (fp32 loss and lse [rows]; a target outside [0, W) gives a NaN loss and
+ * gradient row); the backward writes
  *   dz = g g_scale (softmax(c_r) - onehot(target_r)) (1 - (c / cap)^2)
  * for the scalar gradient *g (device fp32) of sum_r loss_r g_scale (g_scale =
  * 1 / rows for the mean), recomputing c from z and lse.  The logit soft-cap

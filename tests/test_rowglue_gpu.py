@@ -133,3 +133,26 @@ def test_softcap_cross_entropy_matches_float64(cuda, dtype, tol, rows, W, cap):
     e_dz = rel_err(zd.grad.float(), z64.grad)
     print(f"softcap xent rows {rows} W {W} cap {cap} {dtype}: loss {e_loss:.3g} dz {e_dz:.3g}", flush=True)
     assert e_loss < 1e-5 and e_dz < tol
+
+
+def test_softcap_cross_entropy_flags_targets_out_of_range(cuda):
+    """A target outside [0, W) has no logit: its row's loss is NaN (the
+    kernels have no ignored index), the other rows are unaffected."""
+    from thetascan_amd import _lib
+    from thetascan_amd._core.ops import rowglue
+
+    z = torch.randn(4, 64, device=cuda)
+    target = torch.tensor([1, 64, 3, -100], device=cuda)
+    desc = _lib.RowsDesc(4, 64, _lib.TS_F32)
+    loss = torch.empty(4, device=cuda)
+    lse = torch.empty(4, device=cuda)
+    lib = _lib.load()
+    import ctypes
+    assert lib.ts_softcap_xent_fwd(ctypes.byref(desc), z.data_ptr(), target.data_ptr(), 30.0, loss.data_ptr(),
+                                   lse.data_ptr(), _lib.stream_handle(z.device)) == 0
+    torch.cuda.synchronize()
+    assert torch.isnan(loss[1]) and torch.isnan(loss[3])
+    ref = torch.nn.functional.cross_entropy(30 * torch.tanh(z.double() / 30), torch.tensor([1, 0, 3, 0], device=cuda),
+                                            reduction="none")
+    assert torch.allclose(loss[[0, 2]].double(), ref[[0, 2]], rtol=1e-5)
+    assert rowglue.xent_supported(z, target)

@@ -238,11 +238,12 @@ __global__ __launch_bounds__(256) void softcap_xent_kernel(GlueP p, const int64_
     l = mx + __logf(se);
     if (lane == 0) {
       lse[row] = l;
-      loss[row] = l - cy;
+      // a target outside [0, W) has no logit: NaN rather than a wrong loss
+      loss[row] = (y >= 0 && y < p.W) ? l - cy : __builtin_nanf("");
     }
   } else {
     l = lse[row];
-    const float gr = *g * g_scale;
+    const float gr = (y >= 0 && y < p.W) ? *g * g_scale : __builtin_nanf("");
     E* dz = (E*)p.y + row * p.W;
 #pragma unroll
     for (int k = 0; k < kMaxRun; ++k) {
